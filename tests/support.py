@@ -1,0 +1,108 @@
+"""Shared helpers for the test-suite: LAMMPS data files, brute-force graphs.
+
+The graphs follow the reference's conventions:
+  * SR: full directed list, receiver-major (LAMMPS full list, ilist order),
+    v = x_receiver - x_sender  (lammps_neighbor_adapter.cpp:58-101);
+  * LR: unique half pairs (LAMMPS newton-on half list), d = x_j - x_i with
+    i the sender and j the receiver (kokkos_physical_long_range.cpp:147-170).
+Periodic images use the minimum-image convention; every periodic box used in
+the tests is wider than twice the largest cutoff, so each pair has at most one
+image inside the cutoff.
+"""
+import os
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(REPO, "tests", "golden")
+MODEL = os.path.join(REPO, "models", "so3lr.so3lr")
+
+SYMBOLS = ["", "H", "He", "Li", "Be", "B", "C", "N", "O", "F", "Ne", "Na", "Mg", "Al",
+           "Si", "P", "S", "Cl", "Ar", "K", "Ca"]
+
+
+def z_of(symbol):
+    return SYMBOLS.index(symbol)
+
+
+def read_lammps_data(path):
+    """Return (positions[n,3], types[n], lo[3], hi[3]) sorted by atom id."""
+    lines = open(path).read().split("\n")
+    lo = np.zeros(3)
+    hi = np.zeros(3)
+    natoms = 0
+    atoms = []
+    i = 0
+    while i < len(lines):
+        s = lines[i].split("#")[0].strip()
+        parts = s.split()
+        if len(parts) == 2 and parts[1] == "atoms":
+            natoms = int(parts[0])
+        for a, (l, h) in enumerate((("xlo", "xhi"), ("ylo", "yhi"), ("zlo", "zhi"))):
+            if len(parts) == 4 and parts[2] == l and parts[3] == h:
+                lo[a], hi[a] = float(parts[0]), float(parts[1])
+        if s.startswith("Atoms"):
+            i += 1
+            while i < len(lines) and not lines[i].split("#")[0].strip():
+                i += 1
+            while i < len(lines) and len(atoms) < natoms:
+                p = lines[i].split("#")[0].split()
+                if p:
+                    atoms.append((int(p[0]), int(p[1]), float(p[2]), float(p[3]), float(p[4])))
+                i += 1
+            break
+        i += 1
+    atoms.sort()
+    pos = np.array([[a[2], a[3], a[4]] for a in atoms])
+    types = np.array([a[1] for a in atoms])
+    return pos, types, lo, hi
+
+
+def build_graphs(pos, box=None, rc_sr=4.5, rc_lr=12.0):
+    """Brute-force SR full list and LR half list.
+
+    box: None (non-periodic) or a 3-vector of orthogonal periodic lengths.
+    Returns sr=(senders, receivers, vectors), lr=(pi, pj, vectors).
+    """
+    n = len(pos)
+    snd, rcv, vec = [], [], []
+    pi, pj, pv = [], [], []
+    chunk = 512
+    for start in range(0, n, chunk):
+        idx = np.arange(start, min(n, start + chunk))
+        d = pos[None, :, :] - pos[idx, None, :]  # d[a, j] = x_j - x_i
+        if box is not None:
+            d -= np.round(d / box) * box
+        r2 = (d * d).sum(-1)
+        for a, i in enumerate(idx):
+            # SR full list for receiver i: v = x_i - x_j
+            js = np.nonzero((r2[a] > 0.0) & (r2[a] < rc_sr * rc_sr))[0]
+            snd.append(js)
+            rcv.append(np.full(len(js), i))
+            vec.append(-d[a, js])
+            # LR half list: j > i
+            jl = np.nonzero((r2[a] > 0.0) & (r2[a] < rc_lr * rc_lr))[0]
+            jl = jl[jl > i]
+            pi.append(np.full(len(jl), i))
+            pj.append(jl)
+            pv.append(d[a, jl])
+    cat = lambda xs, shape=None: (np.concatenate(xs) if xs else np.zeros(0))
+    sr = (np.concatenate(snd).astype(np.int64), np.concatenate(rcv).astype(np.int64),
+          np.concatenate(vec).reshape(-1, 3))
+    lr = (np.concatenate(pi).astype(np.int64), np.concatenate(pj).astype(np.int64),
+          np.concatenate(pv).reshape(-1, 3))
+    return sr, lr
+
+
+def load_golden(name):
+    """Golden JSON reference plus its geometry: returns (ref, z, pos, box)."""
+    import json
+    ref = json.load(open(os.path.join(GOLDEN, "refs", "so3lr_%s.json" % name)))
+    data = os.path.basename(ref["data"])
+    pos, types, lo, hi = read_lammps_data(os.path.join(GOLDEN, "molecules", data))
+    z = np.array([z_of(ref["types"][t - 1]) for t in types], dtype=np.int64)
+    assert list(z) == list(ref["atomic_numbers"]), name
+    box = (hi - lo) if ref["periodic"] else None
+    if box is not None:
+        pos = lo + np.mod(pos - lo, box)
+    return ref, z, pos, box
