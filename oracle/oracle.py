@@ -223,3 +223,17 @@ class Oracle:
         outs["energy"] = o.e_total
         outs["eatom"] = outs["e_learned"] + outs["e_zbl"] + outs["e_lr"]
         return outs
+
+
+def spherical_harmonics(u):
+    """Y_{1..4}(u) for unit vectors u[n,3] (24 values each), via the C oracle."""
+    u = np.ascontiguousarray(u, dtype=np.float64).reshape(-1, 3)
+    out = np.zeros((len(u), 24))
+    f = lib().orc_spherical_harmonics
+    f.restype = None
+    buf = np.zeros(24)
+    for k in range(len(u)):
+        f(ctypes.c_double(u[k, 0]), ctypes.c_double(u[k, 1]), ctypes.c_double(u[k, 2]),
+          buf.ctypes.data_as(ctypes.c_void_p))
+        out[k] = buf
+    return out
