@@ -1,0 +1,201 @@
+#!/usr/bin/env python3
+"""SO3LR MD throughput on one MI355X: atom-steps/s at the 24,000-atom NaCl
+solution, fp64 E + F + virial every step.
+
+One step = velocity Verlet with a Berendsen thermostat at 300 K (0.5 fs),
+ghost-row update, neighbour-list rebuild when an atom moved more than half the
+1 A skin (LAMMPS `neigh_modify every 1 delay 0 check yes`), and one
+so3lr_compute_device call.  Positions, velocities and forces stay in HBM
+(torch tensors as plumbing); the rebuild runs the host LAMMPS stand-in and
+uploads the new lists, as the reference re-uploads its candidate graph.
+
+Prints one JSON line (the driver's contract), with the dominant kernel's
+roofline from HIP events recorded on its launch stream, and the CPU oracle
+timed on the same host on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+MODEL = os.path.join(REPO, "models", "so3lr.so3lr")
+A100_ATOM_STEPS = 69706.0  # 24k-atom water, 1 A100 (examples/scaling/README.md:56-60)
+HBM_PEAK_GBS = 8000.0
+FP64_PEAK_TFS = 78.6
+# algorithmic work of the dominant kernel, per active short-range pair and block
+# (filters: 2 x (32x128 + 128x128 + 4x32 + 32x128) MAC, forward)
+FILTER_FWD_FLOP_PER_PAIR = 2.0 * 2.0 * (32 * 128 + 128 * 128 + 4 * 32 + 32 * 128)
+# reverse: dgrad of W1 (128x128), E1 (128x32), W0 (128x32), E0 (32x4) plus the
+# layer-0 recompute (32x128 + 4x32), both filters
+FILTER_BWD_FLOP_PER_PAIR = 2.0 * 2.0 * (128 * 128 + 128 * 32 + 128 * 32 + 32 * 4 + 32 * 128 + 4 * 32)
+KB = 8.617333262e-5
+ACC = 9648.533212  # eV / (A amu) -> A / ps^2
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(z, x, box, seconds_budget):
+    """Oracle (CPU restatement of the reference math, OpenMP) on one E+F+virial
+    of a sub-box sample of the same system, scaled to atom-steps/s."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from oracle.oracle import Oracle, lib
+    import support
+    orc = Oracle(MODEL)
+    # sample: every atom of a 40 A cube cut from the system, treated as
+    # periodic with that side (wider than twice the 12 A LR cutoff)
+    side = 40.0
+    sel = np.all(x < side, axis=1)
+    zs, xs = z[sel], x[sel]
+    sr, lr = support.build_graphs(xs, np.full(3, side))
+    t0 = time.time()
+    orc.evaluate(zs, sr, lr)
+    dt = time.time() - t0
+    return {"value": len(zs) / dt, "unit": "atom-steps/s", "cores": int(lib().orc_num_threads()),
+            "kind": "port",
+            "sample": "one E+F+virial of %d atoms (a %.0f A periodic sub-cube of the config-3 system), %.1f s"
+                      % (len(zs), side, dt)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=30.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs one LAMMPS rank on one MI355X with no "
+              "GPU-to-GPU exchange (--gpus %d is not supported)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from so3lrxlammps_amd import Context, Lists, systems
+
+    log("generating config %d" % args.config)
+    z, x, box, Q, M, desc = systems.config(args.config)
+    n = len(z)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    # an explicit stream: handle 0 (torch's default) would leave the library on its own stream
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.set_stream(stream)
+    ctx = Context(MODEL, 0)
+    ctx.set_system(z, Q, M)
+    lo = np.zeros(3)
+    v0, m = systems.maxwell_boltzmann(z, 300.0)
+    xt = torch.tensor(x, dtype=torch.float64, device=dev)
+    vt = torch.tensor(v0, dtype=torch.float64, device=dev)
+    inv_m = torch.tensor(ACC / m, dtype=torch.float64, device=dev)[:, None]
+    mt = torch.tensor(m, dtype=torch.float64, device=dev)[:, None]
+    ft = torch.zeros((n, 3), dtype=torch.float64, device=dev)
+    boxt = torch.tensor(box, dtype=torch.float64, device=dev)
+    dt, skin, tau, T0 = 0.0005, 1.0, 0.1, 300.0
+    state = {"builds": 0, "build_s": 0.0}
+
+    def rebuild():
+        t0 = time.time()
+        torch.cuda.synchronize()
+        xh = xt.cpu().numpy()
+        xh = np.mod(xh, box)
+        xh = np.where(xh >= box, 0.0, xh)
+        xt.copy_(torch.from_numpy(xh))
+        L = Lists(xh, lo, box, (1, 1, 1), 4.5, 12.0, skin, 13.0, sr_full=True)
+        ctx.set_topology(L)
+        state["owner"] = torch.tensor(L.owner, dtype=torch.long, device=dev)
+        state["shift"] = torch.tensor(L.image * box, dtype=torch.float64, device=dev)
+        state["x_build"] = xt.clone()
+        state["xrows"] = torch.empty((L.rows, 3), dtype=torch.float64, device=dev)
+        state["builds"] += 1
+        state["build_s"] += time.time() - t0
+
+    def force():
+        torch.index_select(xt, 0, state["owner"], out=state["xrows"])
+        state["xrows"].add_(state["shift"])
+        e, w = ctx.compute_device(state["xrows"], ft, stream=stream.cuda_stream)
+        return e, w
+
+    rebuild()
+    e, w = force()
+
+    def step():
+        vt.addcmul_(ft, inv_m, value=0.5 * dt)
+        xt.add_(vt, alpha=dt)
+        disp = (xt - state["x_build"]).norm(dim=1).max().item()
+        if disp > 0.5 * skin:
+            rebuild()
+        e, w = force()
+        vt.addcmul_(ft, inv_m, value=0.5 * dt)
+        ke = 0.5 * (mt * vt * vt).sum() / ACC
+        temp = 2.0 * ke / (3.0 * n * KB)
+        lam = torch.sqrt(1.0 + dt / tau * (T0 / temp - 1.0))
+        vt.mul_(lam)
+        return e, w
+
+    log("warmup %d steps" % args.warmup)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    builds0, build_s0 = state["builds"], state["build_s"]
+    ctx.kernel_timing(True)
+    log("timing %d steps" % args.steps)
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        e, w = step()
+        if (k + 1) % 25 == 0:
+            log("  step %d E=%.6f eV" % (k + 1, e))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = n * args.steps / elapsed
+
+    # dominant kernel: the pair filters (forward + reverse) carry ~90% of the FLOPs
+    timing = {}
+    for name in ("filter_fwd", "filter_bwd", "attn_fwd", "attn_bwd", "long_range"):
+        try:
+            timing[name] = ctx.kernel_timing_read(name)
+        except Exception:  # kernel not launched
+            pass
+    ms_f, launches_f, pairs_f = timing["filter_bwd"]
+    avg_ms = ms_f / launches_f
+    flop = FILTER_BWD_FLOP_PER_PAIR * pairs_f / launches_f
+    achieved = flop / (avg_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": "k_filter_bwd", "achieved": achieved, "peak": FP64_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFS, "traffic": None,
+                "avg_launch_ms": avg_ms, "pairs_per_launch": pairs_f / launches_f}
+    kernels = {k: {"avg_ms": v[0] / v[1], "launches": v[1]} for k, v in timing.items()}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(z, x, box, args.cpu_budget)
+
+    sr_active, sr_cand, lr_cand = ctx.graph_stats()
+    out = {
+        "metric": "atom-steps/s/GPU (fp64 E+F+virial) at 24k-atom water; max atoms per GPU",
+        "value": value, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": value / A100_ATOM_STEPS, "dtype": "f64", "data": "synthetic (seeded, config 3)",
+        "config": {"workload": "config 3: " + desc, "atoms": n, "integrator": "velocity Verlet + Berendsen 300 K",
+                   "timestep_fs": 0.5, "skin_A": skin, "sr_pairs_active": sr_active,
+                   "sr_pair_candidates": sr_cand, "lr_pair_candidates": lr_cand,
+                   "neighbor_rebuilds_timed": state["builds"] - builds0,
+                   "rebuild_seconds_timed": state["build_s"] - build_s0,
+                   "ns_per_day": value / n * 0.5 * 86400 / 1e6,
+                   "device_bytes": ctx.device_bytes(), "kernels": kernels},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,180 @@
+/*
+ * so3lr_hip -- MI355X (gfx950) SO3LR force evaluator, C ABI.
+ *
+ * Drop-in replacement for the compute path behind
+ *   pair_style so3lr/native/mpi MODEL [Q [M]]  /  pair_coeff * * E1 ... En
+ * running as one LAMMPS rank on one GPU.  Ghost rows come from LAMMPS's own
+ * communication and are collapsed onto their owners, so no GPU-to-GPU
+ * exchange exists.  Each entry point names the reference interface it
+ * replaces (paths under source/so3lr-lammps-native/).
+ *
+ * Threading: one context per rank; a context is not thread-safe.  All host
+ * pointers are caller-owned and only read or written during the call.  All
+ * device memory belongs to the context; capacities are retained across calls.
+ * Every function returns SO3LR_OK (0) or a nonzero status; the message of the
+ * last failure is available from so3lr_last_error().
+ */
+#ifndef SO3LR_HIP_H
+#define SO3LR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SO3LR_HIP_ABI_VERSION 1
+
+/* status codes */
+#define SO3LR_OK 0
+#define SO3LR_ERR_ARGUMENT 1    /* bad pointer, size or flag */
+#define SO3LR_ERR_MODEL 2       /* unreadable, corrupt or unsupported .so3lr */
+#define SO3LR_ERR_SYSTEM 3      /* (charge, multiplicity) or element problem */
+#define SO3LR_ERR_TOPOLOGY 4    /* neighbour lists inconsistent with the rows */
+#define SO3LR_ERR_DEVICE 5      /* HIP runtime failure */
+#define SO3LR_ERR_STATE 6       /* call made before its prerequisites */
+#define SO3LR_ERR_UNSUPPORTED 7 /* request the path does not implement */
+
+/* compute flags: LAMMPS eflag_global / eflag_atom / vflag_global / vflag_atom */
+#define SO3LR_ENERGY 1
+#define SO3LR_EATOM 2
+#define SO3LR_VIRIAL 4
+#define SO3LR_VATOM 8 /* refused, as in pair_so3lr_native_mpi.cpp:1248-1251 */
+
+/* neighbour-list kinds accepted for the short-range list */
+#define SO3LR_LIST_FULL 0 /* LAMMPS full list (the reference's SR request) */
+#define SO3LR_LIST_HALF 1 /* LAMMPS newton-on half list */
+
+typedef struct so3lr_ctx so3lr_ctx;
+
+/*
+ * Read and validate a .so3lr model, negotiate capabilities, upload weights to
+ * HIP device `device`.  Replaces PairSO3LRNativeMPI::settings model loading
+ * (plugins/lammps/pair_so3lr_native_mpi.cpp:1097-1137) and NativeModel::load
+ * (src/native_model.cpp:325-406).
+ */
+int so3lr_create(const char *model_path, int device, so3lr_ctx **out);
+
+/* Release all device and host resources. */
+void so3lr_destroy(so3lr_ctx *ctx);
+
+/* Message of the last failure on this context (or of the last failed
+ * so3lr_create when ctx is NULL). */
+const char *so3lr_last_error(const so3lr_ctx *ctx);
+
+/* Short-range (which = 0) or long-range (which = 1) model cutoff in Angstrom;
+ * PairSO3LRNativeMPI::init_one returns the SR cutoff (:1162-1172). */
+double so3lr_cutoff(const so3lr_ctx *ctx, int which);
+
+/* Element token (symbol in any case, or atomic number) -> Z in 1..99, 0 when
+ * unknown.  Same rule as plugins/lammps/so3lr_element_map.h:15-49. */
+int so3lr_atomic_number(const char *token);
+
+/*
+ * Owned atoms of the system: atomic numbers and the global (Q, M).  Validates
+ * (Q, M) against the composition and builds the charge/spin embedding table.
+ * Replaces PairSO3LRNativeMPI::setup_charge_spin (:1196-1235) and
+ * charge_spin_offset_table / charge_multiplicity_problem
+ * (src/so3lr_charge_spin.cpp:100-141).
+ */
+int so3lr_set_system(so3lr_ctx *ctx, int64_t n_owned, const int32_t *z,
+                     double total_charge, double multiplicity);
+
+/*
+ * Packed independent images (turbo semantics,
+ * src/kokkos_packed_so3lr_evaluator.cpp:180-286): owned atoms are grouped in
+ * n_images contiguous ranges image_offsets[0..n_images] (image_offsets[0] = 0,
+ * image_offsets[n_images] = n_owned); each image has its own total charge and
+ * multiplicity, its own charge correction and its own charge/spin table
+ * (src/kokkos_turbo_replica_bridge.cpp:122-145).  Call instead of
+ * so3lr_set_system.  No periodic images may connect two images.
+ */
+int so3lr_set_images(so3lr_ctx *ctx, int64_t n_owned, const int32_t *z,
+                     int64_t n_images, const int64_t *image_offsets,
+                     const double *charges, const double *multiplicities);
+
+/*
+ * Candidate neighbour lists, given at every LAMMPS reneighbor (cut-off plus
+ * skin).  Rows are LAMMPS atom rows: rows [0, n_owned) are owned, the rest are
+ * ghosts; owner_of_row maps every row to its owned atom (tag collapse, the
+ * one-rank periodic-image collapse of plugins/lammps/pair_so3lr_native.cpp:74-146).
+ * Each list is CSR over receivers: ilist[k] is an owned row, its neighbours are
+ * neigh[offsets[k] .. offsets[k+1]).
+ *   SR list: full (SO3LR_LIST_FULL, the reference's request id 0) or newton-on
+ *            half list; every directed edge of a full list must have its
+ *            reverse.
+ *   LR list: newton-on half list (the reference's request id 1).
+ * Replaces snapshot_neighbor_list + build_lammps_native_candidate_topologies +
+ * upload_device_candidate_graph (pair_so3lr_native_mpi.cpp:76-105,1297-1334;
+ * src/lammps_neighbor_adapter.cpp:190-280).  A pair of an atom with its own
+ * periodic image is refused, as the one-rank collapse refuses it.
+ */
+int so3lr_set_topology(so3lr_ctx *ctx, int64_t n_rows, const int32_t *owner_of_row,
+                       int sr_kind, int64_t sr_inum, const int32_t *sr_ilist,
+                       const int64_t *sr_offsets, const int32_t *sr_neigh,
+                       int64_t lr_inum, const int32_t *lr_ilist,
+                       const int64_t *lr_offsets, const int32_t *lr_neigh);
+
+/*
+ * One force evaluation.  x_rows: n_rows*3 host positions (owned + ghost rows,
+ * LAMMPS atom->x).  Writes (overwrites) f_owned[n_owned*3] with the total force,
+ * eatom[n_owned] when SO3LR_EATOM (may be NULL otherwise), *energy when
+ * SO3LR_ENERGY and virial[6] (xx yy zz xy xz yz, the LAMMPS order) when
+ * SO3LR_VIRIAL.  The caller adds them to atom->f, eatom, eng_vdwl and
+ * virial as PairSO3LRNativeMPI::compute does (:1867-1878).
+ * Replaces PairSO3LRNativeMPI::compute (:1246-1978).
+ */
+int so3lr_compute(so3lr_ctx *ctx, const double *x_rows, int flags, double *f_owned,
+                  double *eatom, double *energy, double *virial);
+
+/*
+ * As so3lr_compute, with x_rows, f_owned and eatom in device memory (HBM
+ * resident; no host copies of positions or forces).  energy and virial stay
+ * host pointers.  Work is ordered on the context's stream (so3lr_set_stream).
+ */
+int so3lr_compute_device(so3lr_ctx *ctx, const double *x_rows_dev, int flags,
+                         double *f_owned_dev, double *eatom_dev, double *energy,
+                         double *virial);
+
+/* Order all device work on `stream` (a hipStream_t; NULL = the context's own
+ * stream).  The stream must have default priority. */
+int so3lr_set_stream(so3lr_ctx *ctx, void *stream);
+
+/*
+ * Per-atom decomposition of the last evaluation, in owned-atom order; any
+ * pointer may be NULL.  The analogue of SO3LR_NATIVE_DEBUG_DUMP
+ * (pair_so3lr_native_mpi.cpp:1816-1865): learned energy (with the per-element
+ * shift), ZBL energy, long-range energy, partial charges, Hirshfeld ratios;
+ * totals[0] electrostatic and totals[1] dispersion energy.  image_energy
+ * receives per-image totals in packed mode.
+ */
+int so3lr_last_terms(so3lr_ctx *ctx, double *learned, double *zbl, double *long_range,
+                     double *charges, double *hirshfeld, double *totals,
+                     double *image_energy);
+
+/* Number of short-range pairs inside the cutoff at the last evaluation, and
+ * the candidate counts of the current topology (SR pairs, LR pairs). */
+int so3lr_graph_stats(const so3lr_ctx *ctx, int64_t *sr_active, int64_t *sr_candidates,
+                      int64_t *lr_candidates);
+
+/*
+ * Measurement hook (no counterpart in the reference, which times phases with
+ * fenced host clocks, pair_so3lr_native_mpi.cpp:1681-1762): when enabled,
+ * HIP events are recorded on the launch stream around the kernels
+ * "filter_fwd", "filter_bwd", "attn_fwd", "attn_bwd" and "long_range".
+ * Enabling clears the totals.  _read returns the summed duration, the number
+ * of launches and the units processed (active pairs for the filter kernels,
+ * owned atoms otherwise).
+ */
+int so3lr_kernel_timing(so3lr_ctx *ctx, int enable);
+int so3lr_kernel_timing_read(so3lr_ctx *ctx, const char *kernel, double *total_ms,
+                             int64_t *launches, int64_t *units);
+
+/* Device bytes held by the context (weights + retained workspaces). */
+int64_t so3lr_device_bytes(const so3lr_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SO3LR_HIP_H */

@@ -1,0 +1,219 @@
+// Device-side closed forms shared by the gfx950 kernels (fp64 throughout).
+//
+//   spherical harmonics l=1..4 and their input VJP
+//       src/kokkos_learned_energy_forces.cpp:14-139
+//   PhysNet cutoff, Bernstein basis    src/kokkos_integrated_block0.cpp:138-163
+//   exp-bump switch                    src/kokkos_physical_long_range.cpp:11-39
+//   ZBL per directed edge              src/kokkos_physical_zbl.cpp:81-177
+//   Coulomb + QDO dispersion pair      src/kokkos_physical_long_range.cpp:147-370
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace so3lr_amd {
+
+struct LrParams {
+  double ke, sigma, cutoff, cuton_el, fine_factor, bohr, hartree, disp_scale, cuton_disp, full_scale;
+  double shift, fshift;  // shifted-force constants at the cutoff
+  int n_ref;
+};
+
+struct ZblParams {
+  double ke, rc, switch_off, p, d, a[4], c[4];
+};
+
+__device__ __forceinline__ double silu(double x) { return x / (1.0 + exp(-x)); }
+__device__ __forceinline__ double silu_prime(double x) {
+  const double s = 1.0 / (1.0 + exp(-x));
+  return s * (1.0 + x * (1.0 - s));
+}
+
+// degree slot (0..3 for l = 1..4) of equivariant channel m in 0..23
+__device__ __forceinline__ int degree_slot(int m) { return m < 3 ? 0 : (m < 8 ? 1 : (m < 15 ? 2 : 3)); }
+// (-1)^l for the slot: the parity of Y_l under v -> -v
+__device__ __forceinline__ double slot_parity(int slot) { return (slot & 1) ? 1.0 : -1.0; }
+
+constexpr double kPi = 3.141592653589793238462643383279502884;
+
+// One real harmonic Y_m(u), m in 0..23 (l=1: y z x; then l=2,3,4 in m=-l..l).
+__device__ __forceinline__ double sh_component(int m, double x, double y, double z) {
+  switch (m) {
+    case 0: return 0.48860251190291992159 * y;   // sqrt(3/(4pi))
+    case 1: return 0.48860251190291992159 * z;
+    case 2: return 0.48860251190291992159 * x;
+    case 3: return 1.09254843059207907054 * x * y;  // 0.5 sqrt(15/pi)
+    case 4: return 1.09254843059207907054 * y * z;
+    case 5: return 0.31539156525252000603 * (3.0 * z * z - 1.0);  // 0.25 sqrt(5/pi)
+    case 6: return 1.09254843059207907054 * x * z;
+    case 7: return 0.54627421529603953527 * (x * x - y * y);  // 0.25 sqrt(15/pi)
+    case 8: return 0.59004358992664351035 * y * (3.0 * x * x - y * y);  // 0.25 sqrt(35/(2pi))
+    case 9: return 2.89061144264055405538 * x * y * z;  // 0.5 sqrt(105/pi)
+    case 10: return 0.45704579946446573616 * y * (5.0 * z * z - 1.0);  // 0.25 sqrt(21/(2pi))
+    case 11: return 0.37317633259011539141 * (5.0 * z * z * z - 3.0 * z);  // 0.25 sqrt(7/pi)
+    case 12: return 0.45704579946446573616 * x * (5.0 * z * z - 1.0);
+    case 13: return 1.44530572132027702769 * (x * x - y * y) * z;  // 0.25 sqrt(105/pi)
+    case 14: return 0.59004358992664351035 * x * (x * x - 3.0 * y * y);
+    case 15: return 2.50334294179670453836 * x * y * (x * x - y * y);  // 0.75 sqrt(35/pi)
+    case 16: return 1.77013076977993053104 * y * (3.0 * x * x - y * y) * z;  // 0.75 sqrt(35/(2pi))
+    case 17: return 0.94617469575756001809 * x * y * (7.0 * z * z - 1.0);  // 0.75 sqrt(5/pi)
+    case 18: return 0.66904654355728916795 * y * (7.0 * z * z * z - 3.0 * z);  // 0.75 sqrt(5/(2pi))
+    case 19: return 0.10578554691520430380 * (35.0 * z * z * z * z - 30.0 * z * z + 3.0);  // 0.1875 sqrt(1/pi)
+    case 20: return 0.66904654355728916795 * x * (7.0 * z * z * z - 3.0 * z);
+    case 21: return 0.47308734787878000905 * (x * x - y * y) * (7.0 * z * z - 1.0);  // 0.375 sqrt(5/pi)
+    case 22: return 1.77013076977993053104 * x * (x * x - 3.0 * y * y) * z;
+    default: return 0.62583573544917613459 * (x * x * (x * x - 3.0 * y * y) - y * y * (3.0 * x * x - y * y));  // 0.1875 sqrt(35/pi)
+  }
+}
+
+// d Y_m / d(x, y, z), u treated as a free 3-vector.
+__device__ __forceinline__ void sh_component_grad(int m, double x, double y, double z, double &gx,
+                                                  double &gy, double &gz) {
+  gx = gy = gz = 0.0;
+  switch (m) {
+    case 0: gy = 0.48860251190291992159; break;
+    case 1: gz = 0.48860251190291992159; break;
+    case 2: gx = 0.48860251190291992159; break;
+    case 3: { const double k = 1.09254843059207907054; gx = k * y; gy = k * x; break; }
+    case 4: { const double k = 1.09254843059207907054; gy = k * z; gz = k * y; break; }
+    case 5: gz = 0.31539156525252000603 * 6.0 * z; break;
+    case 6: { const double k = 1.09254843059207907054; gx = k * z; gz = k * x; break; }
+    case 7: { const double k = 0.54627421529603953527; gx = 2.0 * k * x; gy = -2.0 * k * y; break; }
+    case 8: { const double k = 0.59004358992664351035; gx = 6.0 * k * x * y; gy = 3.0 * k * (x * x - y * y); break; }
+    case 9: { const double k = 2.89061144264055405538; gx = k * y * z; gy = k * x * z; gz = k * x * y; break; }
+    case 10: { const double k = 0.45704579946446573616; gy = k * (5.0 * z * z - 1.0); gz = 10.0 * k * y * z; break; }
+    case 11: gz = 0.37317633259011539141 * (15.0 * z * z - 3.0); break;
+    case 12: { const double k = 0.45704579946446573616; gx = k * (5.0 * z * z - 1.0); gz = 10.0 * k * x * z; break; }
+    case 13: { const double k = 1.44530572132027702769; gx = 2.0 * k * x * z; gy = -2.0 * k * y * z; gz = k * (x * x - y * y); break; }
+    case 14: { const double k = 0.59004358992664351035; gx = 3.0 * k * (x * x - y * y); gy = -6.0 * k * x * y; break; }
+    case 15: { const double k = 2.50334294179670453836; gx = k * y * (3.0 * x * x - y * y); gy = k * x * (x * x - 3.0 * y * y); break; }
+    case 16: { const double k = 1.77013076977993053104; gx = 6.0 * k * x * y * z; gy = 3.0 * k * (x * x - y * y) * z; gz = k * y * (3.0 * x * x - y * y); break; }
+    case 17: { const double k = 0.94617469575756001809; gx = k * y * (7.0 * z * z - 1.0); gy = k * x * (7.0 * z * z - 1.0); gz = 14.0 * k * x * y * z; break; }
+    case 18: { const double k = 0.66904654355728916795; gy = k * (7.0 * z * z * z - 3.0 * z); gz = k * y * (21.0 * z * z - 3.0); break; }
+    case 19: gz = 0.10578554691520430380 * (140.0 * z * z * z - 60.0 * z); break;
+    case 20: { const double k = 0.66904654355728916795; gx = k * (7.0 * z * z * z - 3.0 * z); gz = k * x * (21.0 * z * z - 3.0); break; }
+    case 21: { const double k = 0.47308734787878000905; gx = 2.0 * k * x * (7.0 * z * z - 1.0); gy = -2.0 * k * y * (7.0 * z * z - 1.0); gz = 14.0 * k * z * (x * x - y * y); break; }
+    case 22: { const double k = 1.77013076977993053104; gx = 3.0 * k * (x * x - y * y) * z; gy = -6.0 * k * x * y * z; gz = k * x * (x * x - 3.0 * y * y); break; }
+    default: { const double k = 0.62583573544917613459; gx = 4.0 * k * x * (x * x - 3.0 * y * y); gy = 4.0 * k * y * (y * y - 3.0 * x * x); break; }
+  }
+}
+
+// exp-bump switch: 1 at cuton, 0 at cutoff, value and d/dr
+__device__ __forceinline__ void bump_switch(double r, double on, double off, double &val, double &der) {
+  if (r >= off) { val = 0.0; der = 0.0; return; }
+  const double w = off - on;
+  const double c = (r - on) / w;
+  const double left = 1.0 - c, right = c;
+  const double sl = left > 1e-12 ? left : 1e-12, sr = right > 1e-12 ? right : 1e-12;
+  const double el = left > 0.0 ? exp(-1.0 / sl) : 0.0;
+  const double er = right > 0.0 ? exp(-1.0 / sr) : 0.0;
+  const double den = el + er + 1e-12;
+  val = el / den;
+  const double dl = left > 0.0 ? -el / (sl * sl) : 0.0;
+  const double dr = right > 0.0 ? er / (sr * sr) : 0.0;
+  der = ((dl * den - el * (dl + dr)) / (den * den)) / w;
+}
+
+// ZBL energy and d/dr of ONE directed edge (the value is symmetric in i, j).
+__device__ __forceinline__ void zbl_directed(const ZblParams &P, double zi, double zj, double r,
+                                             double &energy, double &grad) {
+  energy = 0.0;
+  grad = 0.0;
+  if (!(r > 0.0) || r > P.rc * (1.0 + 1e-12)) return;
+  const double xn = r / P.rc, x2 = xn * xn, x3 = x2 * xn;
+  const double fc = r < P.rc ? 1.0 - 10.0 * x3 + 15.0 * x3 * xn - 6.0 * x3 * x2 : 0.0;
+  const double dfc = r < P.rc ? (-30.0 * x2 + 60.0 * x3 - 30.0 * x3 * xn) / P.rc : 0.0;
+  double sw, dsw;
+  bump_switch(r, 0.0, P.switch_off, sw, dsw);
+  const double zz = zi * zj;
+  const double rs = r > 1e-6 ? r : 1e-6;
+  const double inv = 1.0 / rs, dinv = r > 1e-6 ? -1.0 / (r * r) : 0.0;
+  const double X = P.ke * fc * zz * inv;
+  const double dX = P.ke * zz * (dfc * inv + fc * dinv);
+  const double rate = (pow(zi, P.p) + pow(zj, P.p)) * P.d;
+  double Yv = 0.0, dY = 0.0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const double ex = exp(-P.a[k] * r * rate);
+    Yv += P.c[k] * ex;
+    dY -= P.c[k] * P.a[k] * rate * ex;
+  }
+  energy = 0.5 * sw * X * Yv;
+  grad = 0.5 * (dsw * X * Yv + sw * dX * Yv + sw * X * dY);
+}
+
+struct LrPairTerms {
+  double e_el, e_disp, pref, dh_self, radial;
+};
+
+// Coulomb + QDO dispersion for one unique pair seen from atom "i" (self).
+// dh_self = dE/dh_i; pref * q_j = dE/dq_i.  Returns false outside the cutoff.
+__device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *__restrict__ aref,
+                                              const double *__restrict__ cref, int zi_, int zj_,
+                                              double qi, double qj, double hi, double hj, double r,
+                                              LrPairTerms &o) {
+  if (!(r > 1e-12) || r >= P.cutoff) return false;
+  const double inv_sqrt_pi = 0.56418958354775628695;
+  double esw, desw;
+  bump_switch(r, P.cuton_el, P.cutoff, esw, desw);
+  const double ratio = r / P.sigma;
+  const double erft = erf(ratio), expt = exp(-ratio * ratio);
+  const double pot = erft / r;
+  const double dpot = (2.0 * r * expt * inv_sqrt_pi / P.sigma - erft) / (r * r);
+  const double disp = r - P.cutoff;
+  const double shifted = pot - P.shift - P.fshift * disp;
+  const double kern = esw * (pot - P.shift) + (1.0 - esw) * shifted;
+  const double dkern = dpot - (1.0 - esw) * P.fshift + desw * P.fshift * disp;
+  o.e_el = P.full_scale * P.ke * qi * qj * kern;
+  o.pref = P.full_scale * P.ke * kern;
+  o.radial = P.full_scale * P.ke * qi * qj * dkern;
+  o.e_disp = 0.0;
+  o.dh_self = 0.0;
+  const int zi = zi_ - 1, zj = zj_ - 1;
+  if (zi < 0 || zj < 0 || zi >= P.n_ref || zj >= P.n_ref) return true;
+  const double ai0 = aref[zi], aj0 = aref[zj], ci0 = cref[zi], cj0 = cref[zj];
+  const double ai = ai0 * hi, aj = aj0 * hj;
+  const double c6i = ci0 * hi * hi, c6j = cj0 * hj * hj;
+  const double alpha = 0.5 * (ai + aj);
+  const double num = 2.0 * c6i * c6j * aj * ai;
+  const double den = ai * ai * c6j + aj * aj * c6i;
+  if (!(alpha > 0.0 && den > 1e-30)) return true;
+  const double c6 = num / den;
+  const double idd = 1.0 / (den * den);
+  const double dc6i = 2.0 * ci0 * hi;
+  const double dn_dhi = 2.0 * (dc6i * c6j * aj * ai + c6i * c6j * aj * ai0);
+  const double dd_dhi = 2.0 * ai * ai0 * c6j + aj * aj * dc6i;
+  const double dc6_dhi = (dn_dhi * den - num * dd_dhi) * idd;
+  const double b0 = -0.00433008, b1 = 0.24428889, b2 = 0.04125273, b3 = -0.00078893;
+  const double a7 = pow(alpha, 1.0 / 7.0);
+  const double rvdw = P.fine_factor * a7;
+  const double sfit = b3 * rvdw * rvdw * rvdw + b2 * rvdw * rvdw + b1 * rvdw + b0;
+  const double gam = 0.5 / (sfit * sfit);
+  const double drvdw = rvdw / (7.0 * alpha);
+  const double dsfit = (3.0 * b3 * rvdw * rvdw + 2.0 * b2 * rvdw + b1) * drvdw;
+  const double dgam = -2.0 * gam * dsfit / sfit;
+  const double c8 = 5.0 * c6 / gam, c10 = 245.0 * c6 / (8.0 * gam * gam);
+  const double damp = P.disp_scale * 2.0 * 2.54 * a7;
+  const double ddamp = damp / (7.0 * alpha);
+  const double ra = r / P.bohr;
+  const double r2 = ra * ra, r4 = r2 * r2, r6 = r4 * r2, r8 = r4 * r4, r10 = r8 * r2;
+  const double p2 = damp * damp, p4 = p2 * p2, p6 = p4 * p2, p8 = p4 * p4, p10 = p8 * p2;
+  const double d6 = r6 + p6, d8 = r8 + p8, d10 = r10 + p10;
+  const double qdo = -c6 / d6 - c8 / d8 - c10 / d10;
+  const double rad_au = 6.0 * c6 * r4 * ra / (d6 * d6) + 8.0 * c8 * r6 * ra / (d8 * d8) +
+                        10.0 * c10 * r8 * ra / (d10 * d10);
+  const double dc8 = -c8 * dgam / gam, dc10 = -2.0 * c10 * dgam / gam;
+  const double dd6 = 6.0 * p4 * damp * ddamp, dd8 = 8.0 * p6 * damp * ddamp,
+               dd10 = 10.0 * p8 * damp * ddamp;
+  const double dqdo_da = c6 * dd6 / (d6 * d6) - dc8 / d8 + c8 * dd8 / (d8 * d8) - dc10 / d10 +
+                         c10 * dd10 / (d10 * d10);
+  const double dqdo_dc6 = -1.0 / d6 - (5.0 / gam) / d8 - (245.0 / (8.0 * gam * gam)) / d10;
+  const double dpi = dqdo_dc6 * dc6_dhi + dqdo_da * 0.5 * ai0;
+  double dsw, ddsw;
+  bump_switch(r, P.cuton_disp, P.cutoff, dsw, ddsw);
+  o.e_disp = P.full_scale * P.hartree * qdo * dsw;
+  o.radial += P.full_scale * P.hartree * (rad_au * dsw / P.bohr + qdo * ddsw);
+  o.dh_self = P.full_scale * P.hartree * dsw * dpi;
+  return true;
+}
+
+}  // namespace so3lr_amd

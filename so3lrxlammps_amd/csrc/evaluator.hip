@@ -1,0 +1,1494 @@
+// SO3LR E + F + virial on one gfx950 GPU: kernels and per-step orchestration.
+//
+// Data layout in HBM (N owned atoms, P candidate short-range pairs):
+//   node state per block b:  x[b] N x 128, ev[b] N x 24, qkv[b] N x 640
+//                            (q | k | v | q_ev | k_ev, head-major inside each)
+//   pair state (active pairs compacted to the front each step):
+//     nodes (a, b), v = x_a - x_b, r, Y(v/r) (24), fc, ZBL (e, de/dr)
+//     per block: s (4 equivariant invariants), f (128 inv | 128 ev filters),
+//     alpha (2 directions x (4 inv + 4 ev) attention coefficients)
+//   reverse: df (256), dfc, ds (4), dr, dY (24), g = dE/dv (3)
+// The directed edge "b -> a" (receiver a) uses Y(v/r); "a -> b" uses
+// (-1)^l Y(v/r).  Node sums are gathers over a CSR incidence list.
+#include "evaluator.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+namespace so3lr_amd {
+
+#define HIP_CHECK(expr)                                                                   \
+  do {                                                                                    \
+    hipError_t err_ = (expr);                                                             \
+    if (err_ != hipSuccess)                                                               \
+      throw std::runtime_error(std::string("HIP error in ") + #expr + ": " +             \
+                               hipGetErrorString(err_));                                  \
+  } while (0)
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kCompactPerBlock = 1024;  // candidates per compaction block (256 threads x 4)
+
+__device__ __forceinline__ double half_sum(double v) {
+  // sum over the 32-lane half of the wavefront this lane belongs to
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 8, kWave);
+  v += __shfl_xor(v, 4, kWave);
+  v += __shfl_xor(v, 2, kWave);
+  v += __shfl_xor(v, 1, kWave);
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+  v += __shfl_xor(v, 32, kWave);
+  return half_sum(v);
+}
+__device__ __forceinline__ double pick4(int s, double a, double b, double c, double d) {
+  return s == 0 ? a : (s == 1 ? b : (s == 2 ? c : d));
+}
+
+__global__ void k_fill(double *p, std::size_t n, double v) {
+  const std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// ---------------------------------------------------------------- compaction
+// Active short-range pairs are those with 0 < r^2 < rc^2, kept in candidate
+// order (pair_so3lr_native_mpi.cpp:258-291,306-373 count + stable scan).
+__device__ __forceinline__ bool sr_active(const int *rows, const double *x, int c, double rc2,
+                                          double &dx, double &dy, double &dz) {
+  const int ra = rows[2 * c], rb = rows[2 * c + 1];
+  dx = x[3 * ra] - x[3 * rb];
+  dy = x[3 * ra + 1] - x[3 * rb + 1];
+  dz = x[3 * ra + 2] - x[3 * rb + 2];
+  const double r2 = dx * dx + dy * dy + dz * dz;
+  return r2 > 0.0 && r2 < rc2;
+}
+
+__global__ __launch_bounds__(256) void k_sr_count(int P, const int *rows, const double *x, double rc2,
+                                                  int *blk_count) {
+  __shared__ int part[256];
+  const int base = blockIdx.x * kCompactPerBlock + threadIdx.x * 4;
+  int cnt = 0;
+  for (int j = 0; j < 4; ++j) {
+    const int c = base + j;
+    double dx, dy, dz;
+    if (c < P && sr_active(rows, x, c, rc2, dx, dy, dz)) ++cnt;
+  }
+  part[threadIdx.x] = cnt;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (int(threadIdx.x) < s) part[threadIdx.x] += part[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) blk_count[blockIdx.x] = part[0];
+}
+
+// exclusive scan of per-block counts in place; total to *n_active
+__global__ __launch_bounds__(1024) void k_scan_counts(int nblk, int *cnt, int *n_active) {
+  __shared__ int buf[1024];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int start = 0; start < nblk; start += 1024) {
+    const int i = start + threadIdx.x;
+    const int v = i < nblk ? cnt[i] : 0;
+    buf[threadIdx.x] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int t = int(threadIdx.x) >= off ? buf[threadIdx.x - off] : 0;
+      __syncthreads();
+      buf[threadIdx.x] += t;
+      __syncthreads();
+    }
+    if (i < nblk) cnt[i] = carry + buf[threadIdx.x] - v;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry += buf[1023];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *n_active = carry;
+}
+
+__global__ __launch_bounds__(256) void k_sr_compact(
+    int P, const int *rows, const int *nodes, const double *x, double rc2, const int *blk_off,
+    const int *z, ZblParams zp, int *cand2act, int *pa, double *pv, double *pr, double *pY,
+    double *pfc, double *pzbl) {
+  __shared__ int part[256];
+  const int base = blockIdx.x * kCompactPerBlock + threadIdx.x * 4;
+  int flags = 0, cnt = 0;
+  for (int j = 0; j < 4; ++j) {
+    const int c = base + j;
+    double dx, dy, dz;
+    if (c < P && sr_active(rows, x, c, rc2, dx, dy, dz)) { flags |= 1 << j; ++cnt; }
+  }
+  part[threadIdx.x] = cnt;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int t = int(threadIdx.x) >= off ? part[threadIdx.x - off] : 0;
+    __syncthreads();
+    part[threadIdx.x] += t;
+    __syncthreads();
+  }
+  int pos = blk_off[blockIdx.x] + part[threadIdx.x] - cnt;
+  const double rc = sqrt(rc2);
+  for (int j = 0; j < 4; ++j) {
+    const int c = base + j;
+    if (c >= P) break;
+    if (!(flags & (1 << j))) { cand2act[c] = -1; continue; }
+    double dx, dy, dz;
+    sr_active(rows, x, c, rc2, dx, dy, dz);
+    const int p = pos++;
+    cand2act[c] = p;
+    const int na = nodes[2 * c], nb = nodes[2 * c + 1];
+    pa[2 * p] = na;
+    pa[2 * p + 1] = nb;
+    pv[3 * p] = dx; pv[3 * p + 1] = dy; pv[3 * p + 2] = dz;
+    const double r = sqrt(dx * dx + dy * dy + dz * dz);
+    pr[p] = r;
+    const double inv = r > 1e-14 ? 1.0 / r : 0.0;
+    const double ux = dx * inv, uy = dy * inv, uz = dz * inv;
+    for (int m = 0; m < kE; ++m) pY[kE * p + m] = sh_component(m, ux, uy, uz);
+    const double t = r / rc, t3 = t * t * t;
+    pfc[p] = r < rc ? 1.0 - 10.0 * t3 + 15.0 * t3 * t - 6.0 * t3 * t * t : 0.0;
+    double e, g;
+    zbl_directed(zp, double(z[na]), double(z[nb]), r, e, g);
+    pzbl[2 * p] = e;
+    pzbl[2 * p + 1] = g;
+  }
+}
+
+// ---------------------------------------------------------------- node GEMMs
+// out[r][o] = sum_k in[r][k] * WT[k][o] + bias[o], 16 rows x 64 columns per
+// block; MODE 0 plain, 1 keeps the pre-activation in out and silu in out2,
+// 2 adds aux[r][o], 3 multiplies by silu'(aux[r][o]).
+constexpr int kLinRows = 16;
+constexpr int kLinMaxK = 352;
+template <int MODE>
+__global__ __launch_bounds__(64) void k_linear(int rows, int K, int O, const double *in, int ldin,
+                                               const double *WT, const double *bias, double *out,
+                                               int ldout, double *out2, const double *aux, int ldaux) {
+  __shared__ double tile[kLinRows * kLinMaxK];
+  const int r0 = blockIdx.y * kLinRows;
+  for (int i = threadIdx.x; i < kLinRows * K; i += 64) {
+    const int rr = i / K, kk = i - rr * K;
+    tile[i] = r0 + rr < rows ? in[std::size_t(r0 + rr) * ldin + kk] : 0.0;
+  }
+  __syncthreads();
+  const int o = blockIdx.x * 64 + threadIdx.x;
+  if (o >= O) return;
+  double acc[kLinRows];
+#pragma unroll
+  for (int rr = 0; rr < kLinRows; ++rr) acc[rr] = 0.0;
+  for (int k = 0; k < K; ++k) {
+    const double w = WT[std::size_t(k) * O + o];
+#pragma unroll
+    for (int rr = 0; rr < kLinRows; ++rr) acc[rr] += tile[rr * K + k] * w;
+  }
+  const double b = bias ? bias[o] : 0.0;
+  for (int rr = 0; rr < kLinRows; ++rr) {
+    const int row = r0 + rr;
+    if (row >= rows) break;
+    const double v = acc[rr] + b;
+    const std::size_t io = std::size_t(row) * ldout + o;
+    if (MODE == 0) out[io] = v;
+    if (MODE == 1) { out[io] = v; out2[io] = silu(v); }
+    if (MODE == 2) out[io] = v + aux[std::size_t(row) * ldaux + o];
+    if (MODE == 3) out[io] = v * silu_prime(aux[std::size_t(row) * ldaux + o]);
+  }
+}
+
+// q, k, v, q_ev, k_ev: out[n][w][h*32+o] = sum_k x[n][h*32+k] W[w][h][k][o]
+__global__ __launch_bounds__(128) void k_qkv(int N, const double *x, const double *W, double *qkv) {
+  __shared__ double tile[16 * kF];
+  const int n0 = blockIdx.x * 16;
+  for (int i = threadIdx.x; i < 16 * kF; i += 128) {
+    const int rr = i / kF;
+    tile[i] = n0 + rr < N ? x[std::size_t(n0) * kF + i] : 0.0;
+  }
+  __syncthreads();
+  const int c = threadIdx.x;  // output channel within a projection
+  const int h = c / kHW, o = c % kHW;
+  for (int w = 0; w < 5; ++w) {
+    double acc[16];
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) acc[rr] = 0.0;
+    const double *Wh = W + (std::size_t(w) * kHeads + h) * kHW * kHW;
+    for (int k = 0; k < kHW; ++k) {
+      const double wv = Wh[k * kHW + o];
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) acc[rr] += tile[rr * kF + h * kHW + k] * wv;
+    }
+    for (int rr = 0; rr < 16; ++rr)
+      if (n0 + rr < N) qkv[std::size_t(n0 + rr) * 640 + w * kF + c] = acc[rr];
+  }
+}
+
+// dx[n][h*32+k] = base[n][.] + sum_{w,o} W[w][h][k][o] g[n][w][h*32+o]
+__global__ __launch_bounds__(128) void k_qkv_bwd(int N, const double *g, const double *W,
+                                                 const double *base, double *dx) {
+  __shared__ double tile[8 * 640];
+  const int n0 = blockIdx.x * 8;
+  for (int i = threadIdx.x; i < 8 * 640; i += 128) {
+    const int rr = i / 640;
+    tile[i] = n0 + rr < N ? g[std::size_t(n0) * 640 + i] : 0.0;
+  }
+  __syncthreads();
+  const int c = threadIdx.x;
+  const int h = c / kHW, k = c % kHW;
+  double acc[8];
+  for (int rr = 0; rr < 8; ++rr) acc[rr] = 0.0;
+  for (int w = 0; w < 5; ++w) {
+    const double *Wh = W + ((std::size_t(w) * kHeads + h) * kHW + k) * kHW;
+    for (int o = 0; o < kHW; ++o) {
+      const double wv = Wh[o];
+      for (int rr = 0; rr < 8; ++rr) acc[rr] += tile[rr * 640 + w * kF + h * kHW + o] * wv;
+    }
+  }
+  for (int rr = 0; rr < 8; ++rr)
+    if (n0 + rr < N) dx[std::size_t(n0 + rr) * kF + c] = base[std::size_t(n0 + rr) * kF + c] + acc[rr];
+}
+
+// ---------------------------------------------------------------- filters
+// Per active pair: Bernstein basis and PhysNet cutoff of r, the equivariant
+// invariant s_l = sum_{m in l} (ev_a - ev_b)^2 cg, and both filters
+//   f = W1 silu(W0 rbf + b0) + b1 + E1 silu(E0 s + e0) + e1
+// (kokkos_integrated_block0.cpp:138-255).  One 128-thread block per pair.
+struct FilterArgs {
+  const double *fw0[2], *fb0[2], *fw1t[2], *fb1[2], *fe0[2], *feb0[2], *fe1t[2], *feb1[2];
+  const double *att_cg;
+  const double *rbf_b, *rbf_k, *rbf_kr;
+  double gamma;
+};
+
+__device__ __forceinline__ void bernstein(double r, double gamma, const double *b, const double *k,
+                                          const double *kr, int ch, double &val) {
+  double xb = exp(-gamma * r);
+  xb = xb < 1e-6 ? 1e-6 : (xb > 1.0 - 1e-6 ? 1.0 - 1e-6 : xb);
+  val = exp(b[ch] + k[ch] * log(xb) + kr[ch] * log(1.0 - xb));
+}
+
+__global__ __launch_bounds__(128) void k_filter_fwd(const int *n_active, const int *pa, const double *pr,
+                                                    const double *ev, FilterArgs A, double *ps,
+                                                    double *pf) {
+  const int p = blockIdx.x;
+  if (p >= *n_active) return;
+  __shared__ double rbf[kR], s[4], h[kF], h2[kFH];
+  const int c = threadIdx.x;
+  const double r = pr[p];
+  if (c < kR) bernstein(r, A.gamma, A.rbf_b, A.rbf_k, A.rbf_kr, c, rbf[c]);
+  if (c < 4) {
+    const int a = pa[2 * p], b = pa[2 * p + 1];
+    const int lo = c == 0 ? 0 : (c == 1 ? 3 : (c == 2 ? 8 : 15));
+    const int hi = c == 0 ? 3 : (c == 1 ? 8 : (c == 2 ? 15 : 24));
+    double acc = 0.0;
+    for (int m = lo; m < hi; ++m) {
+      const double d = ev[std::size_t(a) * kE + m] - ev[std::size_t(b) * kE + m];
+      acc += d * d * A.att_cg[m];
+    }
+    s[c] = acc;
+    ps[4 * std::size_t(p) + c] = acc;
+  }
+  __syncthreads();
+  for (int which = 0; which < 2; ++which) {
+    double acc = A.fb0[which][c];
+    const double *w0 = A.fw0[which] + c * kR;
+    for (int k = 0; k < kR; ++k) acc += w0[k] * rbf[k];
+    h[c] = silu(acc);
+    if (c < kFH) {
+      const double *e0 = A.fe0[which] + c * 4;
+      h2[c] = silu(A.feb0[which][c] + e0[0] * s[0] + e0[1] * s[1] + e0[2] * s[2] + e0[3] * s[3]);
+    }
+    __syncthreads();
+    double f = A.fb1[which][c] + A.feb1[which][c];
+    const double *w1t = A.fw1t[which];
+    for (int k = 0; k < kF; ++k) f += w1t[k * kF + c] * h[k];
+    const double *e1t = A.fe1t[which];
+    for (int j = 0; j < kFH; ++j) f += e1t[j * kF + c] * h2[j];
+    pf[256 * std::size_t(p) + which * kF + c] = f;
+    __syncthreads();
+  }
+}
+
+// Reverse of the filters and of the radial basis / cutoff
+// (kokkos_block2_attention_input_reverse.cpp:198-240,301-336).
+__global__ __launch_bounds__(128) void k_filter_bwd(const int *n_active, const double *pr,
+                                                    const double *pfc_unused, const double *ps,
+                                                    const double *df, const double *dfc, FilterArgs A,
+                                                    double rc, double *ds, double *dr) {
+  const int p = blockIdx.x;
+  if (p >= *n_active) return;
+  __shared__ double rbf[kR], s[4], g[2 * kF], dh[kF], dh2[kFH], drbf[kR], dsv[4];
+  const int c = threadIdx.x;
+  const double r = pr[p];
+  if (c < kR) { bernstein(r, A.gamma, A.rbf_b, A.rbf_k, A.rbf_kr, c, rbf[c]); drbf[c] = 0.0; }
+  if (c < 4) { s[c] = ps[4 * std::size_t(p) + c]; dsv[c] = 0.0; }
+  g[c] = df[256 * std::size_t(p) + c];
+  g[kF + c] = df[256 * std::size_t(p) + kF + c];
+  __syncthreads();
+  for (int which = 0; which < 2; ++which) {
+    const double *gf = g + which * kF;
+    double pre = A.fb0[which][c];
+    const double *w0 = A.fw0[which] + c * kR;
+    for (int k = 0; k < kR; ++k) pre += w0[k] * rbf[k];
+    double acc = 0.0;
+    const double *w1 = A.fw1t[which];  // (in, out): column c of W1 is row c here
+    for (int o = 0; o < kF; ++o) acc += w1[c * kF + o] * gf[o];
+    dh[c] = acc * silu_prime(pre);
+    if (c < kFH) {
+      const double *e0 = A.fe0[which] + c * 4;
+      const double pre2 = A.feb0[which][c] + e0[0] * s[0] + e0[1] * s[1] + e0[2] * s[2] + e0[3] * s[3];
+      const double *e1t = A.fe1t[which];
+      double a2 = 0.0;
+      for (int o = 0; o < kF; ++o) a2 += e1t[c * kF + o] * gf[o];
+      dh2[c] = a2 * silu_prime(pre2);
+    }
+    __syncthreads();
+    if (c < kR) {
+      double a = 0.0;
+      for (int q = 0; q < kF; ++q) a += A.fw0[which][q * kR + c] * dh[q];
+      drbf[c] += a;
+    }
+    if (c < 4) {
+      double a = 0.0;
+      for (int j = 0; j < kFH; ++j) a += A.fe0[which][j * 4 + c] * dh2[j];
+      dsv[c] += a;
+    }
+    __syncthreads();
+  }
+  if (c == 0) {
+    for (int l = 0; l < 4; ++l) ds[4 * std::size_t(p) + l] = dsv[l];
+    double grad = 0.0;
+    if (r < rc) {
+      const double t = r / rc;
+      grad += dfc[p] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
+    }
+    const double xb = exp(-A.gamma * r);
+    if (xb > 1e-6 && xb < 1.0 - 1e-6)
+      for (int k = 0; k < kR; ++k)
+        grad += drbf[k] * rbf[k] * (-A.gamma * A.rbf_k[k] + A.gamma * A.rbf_kr[k] * xb / (1.0 - xb));
+    dr[p] += grad;
+  }
+}
+
+// ---------------------------------------------------------------- attention
+// Node-major: one wavefront per node n, lane l holds channels l and l+64
+// (heads l/32 and 2+l/32) and equivariant channel l < 24.
+__global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, const int *inc,
+                                                  const int *cand2act, const int *pa,
+                                                  const double *x, const double *ev,
+                                                  const double *qkv, const double *pf,
+                                                  const double *pY, const double *pfc,
+                                                  double inv_avg, double *palpha, double *ainv,
+                                                  double *aev) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const double *qn = qkv + std::size_t(n) * 640;
+  const double q0 = qn[lane], q1 = qn[64 + lane], qe0 = qn[384 + lane], qe1 = qn[448 + lane];
+  const int slot = lane < kE ? degree_slot(lane) : 0;
+  double acc0 = 0.0, acc1 = 0.0, acce = 0.0;
+  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
+    const int e = inc[k];
+    const int p = cand2act[e >> 1];
+    if (p < 0) continue;
+    const int side = e & 1;
+    const int o = pa[2 * p + 1 - side];
+    const double *ko = qkv + std::size_t(o) * 640;
+    const double *fp = pf + 256 * std::size_t(p);
+    const double ai_lo = half_sum(q0 * ko[128 + lane] * fp[lane]) * inv_avg;
+    const double ai_hi = half_sum(q1 * ko[192 + lane] * fp[64 + lane]) * inv_avg;
+    const double ae_lo = half_sum(qe0 * ko[512 + lane] * fp[128 + lane]) * inv_avg;
+    const double ae_hi = half_sum(qe1 * ko[576 + lane] * fp[192 + lane]) * inv_avg;
+    const double fc = pfc[p];
+    acc0 += fc * ai_lo * ko[256 + lane];
+    acc1 += fc * ai_hi * ko[320 + lane];
+    const double e0 = __shfl(ae_lo, 0, kWave), e1 = __shfl(ae_lo, 32, kWave);
+    const double e2 = __shfl(ae_hi, 0, kWave), e3 = __shfl(ae_hi, 32, kWave);
+    if (lane < kE) {
+      const double y = pY[kE * std::size_t(p) + lane] * (side == 0 ? 1.0 : slot_parity(slot));
+      acce += fc * pick4(slot, e0, e1, e2, e3) * y;
+    }
+    const double i0 = __shfl(ai_lo, 0, kWave), i1 = __shfl(ai_lo, 32, kWave);
+    const double i2 = __shfl(ai_hi, 0, kWave), i3 = __shfl(ai_hi, 32, kWave);
+    if (lane < 8) {
+      const double v = lane < 4 ? pick4(lane, i0, i1, i2, i3) : pick4(lane - 4, e0, e1, e2, e3);
+      palpha[16 * std::size_t(p) + 8 * side + lane] = v;
+    }
+  }
+  const std::size_t i = std::size_t(n) * kF;
+  ainv[i + lane] = x[i + lane] + acc0;
+  ainv[i + 64 + lane] = x[i + 64 + lane] + acc1;
+  if (lane < kE) aev[std::size_t(n) * kE + lane] = ev[std::size_t(n) * kE + lane] + acce;
+}
+
+// LayerNorm over 128 channels held two per lane (biased variance).
+__device__ __forceinline__ void wave_layer_norm(double v0, double v1, const double *w, const double *b,
+                                                double eps, int lane, double &y0, double &y1,
+                                                double &h0, double &h1, double &is) {
+  const double mean = wave_sum(v0 + v1) / kF;
+  const double d0 = v0 - mean, d1 = v1 - mean;
+  const double var = wave_sum(d0 * d0 + d1 * d1) / kF;
+  is = 1.0 / sqrt(var + eps);
+  h0 = d0 * is;
+  h1 = d1 * is;
+  y0 = h0 * w[lane] + b[lane];
+  y1 = h1 * w[64 + lane] + b[64 + lane];
+}
+__device__ __forceinline__ void wave_layer_norm_bwd(double g0, double g1, const double *w, double h0,
+                                                    double h1, double is, int lane, double &d0,
+                                                    double &d1) {
+  const double gh0 = g0 * w[lane], gh1 = g1 * w[64 + lane];
+  const double mg = wave_sum(gh0 + gh1) / kF;
+  const double mgx = wave_sum(gh0 * h0 + gh1 * h1) / kF;
+  d0 = is * (gh0 - mg - h0 * mgx);
+  d1 = is * (gh1 - mg - h1 * mgx);
+}
+
+// LN1 of the attention residual, and silu of it for the MLP input
+__global__ __launch_bounds__(256) void k_post1(int N, const double *ainv, const double *w, const double *b,
+                                               double eps, double *n1, double *n1hat, double *n1is,
+                                               double *act) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const std::size_t i = std::size_t(n) * kF;
+  double y0, y1, h0, h1, is;
+  wave_layer_norm(ainv[i + lane], ainv[i + 64 + lane], w, b, eps, lane, y0, y1, h0, h1, is);
+  n1[i + lane] = y0; n1[i + 64 + lane] = y1;
+  n1hat[i + lane] = h0; n1hat[i + 64 + lane] = h1;
+  if (lane == 0) n1is[n] = is;
+  act[i + lane] = silu(y0);
+  act[i + 64 + lane] = silu(y1);
+}
+
+// cat = [p, sum_{m in l} a_ev^2 cg]  (kokkos_post_attention_block0.cpp:223-266)
+__global__ __launch_bounds__(256) void k_concat(int N, const double *p, const double *aev, const double *cg,
+                                                double *cat) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  cat[std::size_t(n) * kNI + lane] = p[std::size_t(n) * kF + lane];
+  cat[std::size_t(n) * kNI + 64 + lane] = p[std::size_t(n) * kF + 64 + lane];
+  double v = 0.0;
+  if (lane < kE) { const double a = aev[std::size_t(n) * kE + lane]; v = a * a * cg[lane]; }
+  const int slot = lane < kE ? degree_slot(lane) : 7;
+  for (int l = 0; l < 4; ++l) {
+    const double s = wave_sum(slot == l ? v : 0.0);
+    if (lane == 0) cat[std::size_t(n) * kNI + kF + l] = s;
+  }
+}
+
+// pre2 = p + t[:128], ev_out = a_ev (1 + t[128+l]), x_out = LN2(pre2)
+__global__ __launch_bounds__(256) void k_post2(int N, const double *p, const double *t, const double *aev,
+                                               const double *w, const double *b, double eps,
+                                               double *xout, double *evout, double *pre2hat,
+                                               double *pre2is) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const std::size_t i = std::size_t(n) * kF, it = std::size_t(n) * kNI;
+  double y0, y1, h0, h1, is;
+  wave_layer_norm(p[i + lane] + t[it + lane], p[i + 64 + lane] + t[it + 64 + lane], w, b, eps, lane,
+                  y0, y1, h0, h1, is);
+  xout[i + lane] = y0; xout[i + 64 + lane] = y1;
+  pre2hat[i + lane] = h0; pre2hat[i + 64 + lane] = h1;
+  if (lane == 0) pre2is[n] = is;
+  if (lane < kE)
+    evout[std::size_t(n) * kE + lane] = aev[std::size_t(n) * kE + lane] * (1.0 + t[it + kF + degree_slot(lane)]);
+}
+
+// ---------------------------------------------------------------- heads
+struct HeadArgs {
+  const double *ew2, *qw2, *escale, *eshift, *qemb, *hw2, *hb2, *hqemb, *hvshift;
+  double eb2, qb2;
+};
+
+// energy, raw charge, Hirshfeld key and ratio (kokkos_output_heads.cpp:137-176,341-451)
+__global__ __launch_bounds__(256) void k_heads(int N, const int *z, const double *act, HeadArgs H,
+                                               double *eatom, double *qraw, double *hkey,
+                                               double *heff, double *hir) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const double *a = act + std::size_t(n) * 320;
+  const int zz = z[n];
+  const double e = wave_sum(H.ew2[lane] * a[lane] + H.ew2[64 + lane] * a[64 + lane]);
+  const double q = wave_sum(H.qw2[lane] * a[128 + lane] + H.qw2[64 + lane] * a[192 + lane]);
+  double key = H.hb2[lane];
+  for (int i = 0; i < kHH; ++i) key += H.hw2[lane * kHH + i] * a[256 + i];
+  hkey[std::size_t(n) * kHH + lane] = key;
+  const double qk = wave_sum(H.hqemb[zz * kHH + lane] * key);
+  if (lane == 0) {
+    eatom[n] = (e + H.eb2) * H.escale[zz - 1] + H.eshift[zz - 1];
+    qraw[n] = q + H.qb2 + H.qemb[zz];
+    const double ef = H.hvshift[zz] + qk / 8.0;  // sqrt(64)
+    heff[n] = ef;
+    hir[n] = fabs(ef);
+  }
+}
+
+// per-image mean removal: out = in + (target - sum_image(in)) / count  (sign = +1)
+// or out = in - mean_image(in) (target ignored, sign = -1).  One block per image.
+__global__ __launch_bounds__(1024) void k_image_center(const std::int64_t *img_off, const double *target,
+                                                       const double *in, double *out, int mode) {
+  __shared__ double part[1024];
+  const std::int64_t lo = img_off[blockIdx.x], hi = img_off[blockIdx.x + 1];
+  double s = 0.0;
+  for (std::int64_t i = lo + threadIdx.x; i < hi; i += 1024) s += in[i];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int st = 512; st > 0; st >>= 1) {
+    if (int(threadIdx.x) < st) part[threadIdx.x] += part[threadIdx.x + st];
+    __syncthreads();
+  }
+  const double cnt = double(hi - lo);
+  const double shift = mode == 0 ? (target[blockIdx.x] - part[0]) / cnt : -part[0] / cnt;
+  for (std::int64_t i = lo + threadIdx.x; i < hi; i += 1024) out[i] = in[i] + shift;
+}
+
+// seeds -> d/d(x_final): energy 1, charge (dE/dq - mean), Hirshfeld dE/dh
+__global__ __launch_bounds__(256) void k_heads_bwd(int N, const int *z, const double *pre, const double *qseed,
+                                                   const double *dh, const double *heff, HeadArgs H,
+                                                   double *ghead) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const double *pr = pre + std::size_t(n) * 320;
+  double *g = ghead + std::size_t(n) * 320;
+  const int zz = z[n];
+  const double sc = H.escale[zz - 1];
+  g[lane] = sc * H.ew2[lane] * silu_prime(pr[lane]);
+  g[64 + lane] = sc * H.ew2[64 + lane] * silu_prime(pr[64 + lane]);
+  const double qs = qseed[n];
+  g[128 + lane] = qs * H.qw2[lane] * silu_prime(pr[128 + lane]);
+  g[192 + lane] = qs * H.qw2[64 + lane] * silu_prime(pr[192 + lane]);
+  const double ef = heff[n];
+  const double sg = ef > 0.0 ? 1.0 : (ef < 0.0 ? -1.0 : 0.0);
+  const double hs = dh[n] * sg / 8.0;
+  // ghh[i] = sum_j hw2[j][i] gk[j], gk[j] = hs * hqemb[z][j]
+  double acc = 0.0;
+  for (int j = 0; j < kHH; ++j) acc += H.hw2[j * kHH + lane] * hs * H.hqemb[zz * kHH + j];
+  g[256 + lane] = acc * silu_prime(pr[256 + lane]);
+}
+
+// ---------------------------------------------------------------- long range
+// Node-major over the LR incidence: every lane takes one pair of node n.
+// d = x_n - x_other; F_n = -dE/dr d/r; half of every pair energy and of its
+// virial goes to each endpoint.
+__global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int *inc, const int *rows,
+                                            const int *nodes, const double *x, const int *z,
+                                            const double *q, const double *hir, LrParams P,
+                                            const double *aref, const double *cref, double *elr,
+                                            double *dq, double *dhv, double *flr, double *vlr,
+                                            double *parts) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int zn = z[n];
+  const double qn = q[n], hn = hir[n];
+  double e_el = 0, e_d = 0, sdq = 0, sdh = 0, f0 = 0, f1 = 0, f2 = 0;
+  double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
+  for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
+    const int e = inc[k];
+    const int c = e >> 1, side = e & 1;
+    const int ra = rows[2 * c], rb = rows[2 * c + 1];
+    const double sgn = side == 0 ? 1.0 : -1.0;
+    const double dx = sgn * (x[3 * ra] - x[3 * rb]);
+    const double dy = sgn * (x[3 * ra + 1] - x[3 * rb + 1]);
+    const double dz = sgn * (x[3 * ra + 2] - x[3 * rb + 2]);
+    const double r = sqrt(dx * dx + dy * dy + dz * dz);
+    const int o = nodes[2 * c + 1 - side];
+    LrPairTerms t;
+    if (!lr_pair_terms(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
+    e_el += 0.5 * t.e_el;
+    e_d += 0.5 * t.e_disp;
+    sdq += t.pref * q[o];
+    sdh += t.dh_self;
+    const double s = t.radial / r;
+    f0 -= s * dx; f1 -= s * dy; f2 -= s * dz;
+    // W = -sum_pairs d (x) f_pair, f_pair = radial d / r; half per endpoint
+    w0 -= 0.5 * s * dx * dx; w1 -= 0.5 * s * dy * dy; w2 -= 0.5 * s * dz * dz;
+    w3 -= 0.5 * s * dx * dy; w4 -= 0.5 * s * dx * dz; w5 -= 0.5 * s * dy * dz;
+  }
+  e_el = wave_sum(e_el); e_d = wave_sum(e_d); sdq = wave_sum(sdq); sdh = wave_sum(sdh);
+  f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2);
+  w0 = wave_sum(w0); w1 = wave_sum(w1); w2 = wave_sum(w2);
+  w3 = wave_sum(w3); w4 = wave_sum(w4); w5 = wave_sum(w5);
+  if (lane == 0) {
+    elr[n] = e_el + e_d;
+    dq[n] = sdq;
+    dhv[n] = sdh;
+    flr[3 * n] = f0; flr[3 * n + 1] = f1; flr[3 * n + 2] = f2;
+    double *v = vlr + 6 * std::size_t(n);
+    v[0] = w0; v[1] = w1; v[2] = w2; v[3] = w3; v[4] = w4; v[5] = w5;
+    parts[2 * n] = e_el;
+    parts[2 * n + 1] = e_d;
+  }
+}
+
+// ---------------------------------------------------------------- block reverse
+// LN2 reverse, gate adjoint, start of the interaction reverse
+__global__ __launch_bounds__(256) void k_post2_bwd(int N, const double *gx, const double *gev, const double *t,
+                                                   const double *aev, const double *w, const double *hat,
+                                                   const double *is, double *gp, double *gt, double *gaev) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const std::size_t i = std::size_t(n) * kF, it = std::size_t(n) * kNI;
+  double d0, d1;
+  wave_layer_norm_bwd(gx[i + lane], gx[i + 64 + lane], w, hat[i + lane], hat[i + 64 + lane], is[n], lane,
+                      d0, d1);
+  gp[i + lane] = d0; gp[i + 64 + lane] = d1;
+  gt[it + lane] = d0; gt[it + 64 + lane] = d1;
+  const int slot = lane < kE ? degree_slot(lane) : 7;
+  double ge = 0.0, a = 0.0;
+  if (lane < kE) {
+    ge = gev[std::size_t(n) * kE + lane];
+    a = aev[std::size_t(n) * kE + lane];
+    gaev[std::size_t(n) * kE + lane] = ge * (1.0 + t[it + kF + slot]);
+  }
+  for (int l = 0; l < 4; ++l) {
+    const double s = wave_sum(slot == l ? ge * a : 0.0);
+    if (lane == 0) gt[it + kF + l] = s;
+  }
+}
+
+// gp += gcat[:128]; g_aev += gcat[128 + l] 2 a_ev cg
+__global__ __launch_bounds__(256) void k_post_mid_bwd(int N, const double *gcat, const double *aev,
+                                                      const double *cg, double *gp, double *gaev) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const std::size_t i = std::size_t(n) * kF, it = std::size_t(n) * kNI;
+  gp[i + lane] += gcat[it + lane];
+  gp[i + 64 + lane] += gcat[it + 64 + lane];
+  if (lane < kE) {
+    const std::size_t j = std::size_t(n) * kE + lane;
+    gaev[j] += gcat[it + kF + degree_slot(lane)] * 2.0 * aev[j] * cg[lane];
+  }
+}
+
+// g_n1 = gp + gact silu'(n1); LN1 reverse -> d/d(x + d_inv)
+__global__ __launch_bounds__(256) void k_ln1_bwd(int N, const double *gp, const double *gact, const double *n1,
+                                                 const double *w, const double *hat, const double *is,
+                                                 double *gainv) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const std::size_t i = std::size_t(n) * kF;
+  const double g0 = gp[i + lane] + gact[i + lane] * silu_prime(n1[i + lane]);
+  const double g1 = gp[i + 64 + lane] + gact[i + 64 + lane] * silu_prime(n1[i + 64 + lane]);
+  double d0, d1;
+  wave_layer_norm_bwd(g0, g1, w, hat[i + lane], hat[i + 64 + lane], is[n], lane, d0, d1);
+  gainv[i + lane] = d0;
+  gainv[i + 64 + lane] = d1;
+}
+
+// Attention reverse, node-major (kokkos_attention_scatter_reverse.cpp:280-500).
+// For node n and each pair p = {n, o}: the incoming edge o -> n gives dq_n,
+// the outgoing edge n -> o gives dk_n, dv_n (sender-side terms, gathered here
+// instead of scattered).  The endpoint with side 0 also writes the per-pair
+// adjoints df (both directions), dfc and accumulates dY.
+__global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, const int *inc,
+                                                  const int *cand2act, const int *pa, const double *qkv,
+                                                  const double *pf, const double *pY, const double *pfc,
+                                                  const double *palpha, const double *gainv,
+                                                  const double *gaev, double inv_avg, double *gqkv,
+                                                  double *df, double *dfc, double *dY) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const double *me = qkv + std::size_t(n) * 640;
+  const double mq0 = me[lane], mq1 = me[64 + lane], mk0 = me[128 + lane], mk1 = me[192 + lane];
+  const double mv0 = me[256 + lane], mv1 = me[320 + lane], mqe0 = me[384 + lane], mqe1 = me[448 + lane];
+  const double mke0 = me[512 + lane], mke1 = me[576 + lane];
+  const double mg0 = gainv[std::size_t(n) * kF + lane], mg1 = gainv[std::size_t(n) * kF + 64 + lane];
+  const int slot = lane < kE ? degree_slot(lane) : 7;
+  const double mge = lane < kE ? gaev[std::size_t(n) * kE + lane] : 0.0;
+  double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
+  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
+    const int e = inc[k];
+    const int p = cand2act[e >> 1];
+    if (p < 0) continue;
+    const int side = e & 1;
+    const int o = pa[2 * p + 1 - side];
+    const double *ot = qkv + std::size_t(o) * 640;
+    const double oq0 = ot[lane], oq1 = ot[64 + lane], ok0 = ot[128 + lane], ok1 = ot[192 + lane];
+    const double ov0 = ot[256 + lane], ov1 = ot[320 + lane], oqe0 = ot[384 + lane], oqe1 = ot[448 + lane];
+    const double oke0 = ot[512 + lane], oke1 = ot[576 + lane];
+    const double og0 = gainv[std::size_t(o) * kF + lane], og1 = gainv[std::size_t(o) * kF + 64 + lane];
+    const double oge = lane < kE ? gaev[std::size_t(o) * kE + lane] : 0.0;
+    const double *fp = pf + 256 * std::size_t(p);
+    const double fi0 = fp[lane], fi1 = fp[64 + lane], fe0 = fp[128 + lane], fe1 = fp[192 + lane];
+    const double fc = pfc[p];
+    const double y = lane < kE ? pY[kE * std::size_t(p) + lane] : 0.0;
+    const double par = slot_parity(slot < 4 ? slot : 0);
+    const double y_n = side == 0 ? y : par * y;   // harmonics of edge o -> n
+    const double y_o = side == 0 ? par * y : y;   // harmonics of edge n -> o
+    const double *al = palpha + 16 * std::size_t(p);
+    // incoming o -> n
+    const double ci_lo = half_sum(mg0 * ov0), ci_hi = half_sum(mg1 * ov1);  // sum g v per head
+    const double ce_m = lane < kE ? mge * y_n : 0.0;
+    double ce[4];
+    for (int l = 0; l < 4; ++l) ce[l] = wave_sum(slot == l ? ce_m : 0.0);
+    // outgoing n -> o
+    const double co_lo = half_sum(og0 * mv0), co_hi = half_sum(og1 * mv1);
+    const double cem = lane < kE ? oge * y_o : 0.0;
+    double coe[4];
+    for (int l = 0; l < 4; ++l) coe[l] = wave_sum(slot == l ? cem : 0.0);
+    const int hlo = lane >> 5, hhi = 2 + (lane >> 5);
+    const double *ain = al + 8 * side, *aout = al + 8 * (1 - side);
+    // d alpha / norm for each direction, per lane's heads
+    const double sin_lo = fc * ci_lo * inv_avg, sin_hi = fc * ci_hi * inv_avg;
+    const double sout_lo = fc * co_lo * inv_avg, sout_hi = fc * co_hi * inv_avg;
+    const double sine_lo = fc * ce[hlo] * inv_avg, sine_hi = fc * ce[hhi] * inv_avg;
+    const double soute_lo = fc * coe[hlo] * inv_avg, soute_hi = fc * coe[hhi] * inv_avg;
+    dq0 += sin_lo * ok0 * fi0; dq1 += sin_hi * ok1 * fi1;
+    dqe0 += sine_lo * oke0 * fe0; dqe1 += sine_hi * oke1 * fe1;
+    dk0 += sout_lo * oq0 * fi0; dk1 += sout_hi * oq1 * fi1;
+    dke0 += soute_lo * oqe0 * fe0; dke1 += soute_hi * oqe1 * fe1;
+    dv0 += fc * aout[hlo] * og0; dv1 += fc * aout[hhi] * og1;
+    if (side == 0) {
+      double *d = df + 256 * std::size_t(p);
+      d[lane] = sin_lo * mq0 * ok0 + sout_lo * oq0 * mk0;
+      d[64 + lane] = sin_hi * mq1 * ok1 + sout_hi * oq1 * mk1;
+      d[128 + lane] = sine_lo * mqe0 * oke0 + soute_lo * oqe0 * mke0;
+      d[192 + lane] = sine_hi * mqe1 * oke1 + soute_hi * oqe1 * mke1;
+      double fcg = 0.0;
+      for (int h = 0; h < 4; ++h) fcg += ain[4 + h] * ce[h] + aout[4 + h] * coe[h];
+      // invariant part: heads 0,1 from ci_lo lanes 0/32, heads 2,3 from ci_hi
+      const double c0 = __shfl(ci_lo, 0, kWave), c1 = __shfl(ci_lo, 32, kWave);
+      const double c2 = __shfl(ci_hi, 0, kWave), c3 = __shfl(ci_hi, 32, kWave);
+      const double o0 = __shfl(co_lo, 0, kWave), o1 = __shfl(co_lo, 32, kWave);
+      const double o2 = __shfl(co_hi, 0, kWave), o3 = __shfl(co_hi, 32, kWave);
+      fcg += ain[0] * c0 + ain[1] * c1 + ain[2] * c2 + ain[3] * c3;
+      fcg += aout[0] * o0 + aout[1] * o1 + aout[2] * o2 + aout[3] * o3;
+      if (lane == 0) dfc[p] = fcg;
+      if (lane < kE) {
+        // dE/dY_p: edge o->n contributes via y_n, edge n->o via y_o (parity)
+        const double gin = fc * ain[4 + slot] * mge, gout = fc * aout[4 + slot] * oge;
+        dY[kE * std::size_t(p) + lane] += gin + par * gout;
+      }
+    }
+  }
+  double *g = gqkv + std::size_t(n) * 640;
+  g[lane] = dq0; g[64 + lane] = dq1;
+  g[128 + lane] = dk0; g[192 + lane] = dk1;
+  g[256 + lane] = dv0; g[320 + lane] = dv1;
+  g[384 + lane] = dqe0; g[448 + lane] = dqe1;
+  g[512 + lane] = dke0; g[576 + lane] = dke1;
+}
+
+// g_ev_in = g_aev + sum_pairs 2 (ev_n - ev_o) cg ds[slot]
+__global__ __launch_bounds__(256) void k_ev_bwd(int N, const int *inc_off, const int *inc, const int *cand2act,
+                                                const int *pa, const double *ev, const double *cg,
+                                                const double *ds, const double *gaev, double *gev) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N || lane >= kE) return;
+  const int slot = degree_slot(lane);
+  const double en = ev[std::size_t(n) * kE + lane];
+  double acc = gaev[std::size_t(n) * kE + lane];
+  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
+    const int e = inc[k];
+    const int p = cand2act[e >> 1];
+    if (p < 0) continue;
+    const int o = pa[2 * p + 1 - (e & 1)];
+    acc += 2.0 * (en - ev[std::size_t(o) * kE + lane]) * cg[lane] * ds[4 * std::size_t(p) + slot];
+  }
+  gev[std::size_t(n) * kE + lane] = acc;
+}
+
+// ---------------------------------------------------------------- geometry
+// g = dE/dv for v = x_a - x_b (kokkos_learned_energy_forces.cpp:241-306)
+__global__ __launch_bounds__(256) void k_geom_bwd(const int *n_active, const double *pv, const double *pr,
+                                                  const double *dr, const double *pzbl, const double *dY,
+                                                  double *pg) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= *n_active) return;
+  const double r = pr[p];
+  if (r <= 1e-14) { pg[3 * p] = pg[3 * p + 1] = pg[3 * p + 2] = 0.0; return; }
+  const double ux = pv[3 * p] / r, uy = pv[3 * p + 1] / r, uz = pv[3 * p + 2] / r;
+  double gx = 0, gy = 0, gz = 0;
+  for (int m = 0; m < kE; ++m) {
+    double ax, ay, az;
+    sh_component_grad(m, ux, uy, uz, ax, ay, az);
+    const double w = dY[kE * std::size_t(p) + m];
+    gx += w * ax; gy += w * ay; gz += w * az;
+  }
+  const double rad = ux * gx + uy * gy + uz * gz;
+  // the ZBL energy is carried by both directed edges of the pair
+  const double d = dr[p] + 2.0 * pzbl[2 * p + 1];
+  pg[3 * p] = d * ux + (gx - ux * rad) / r;
+  pg[3 * p + 1] = d * uy + (gy - uy * rad) / r;
+  pg[3 * p + 2] = d * uz + (gz - uz * rad) / r;
+}
+
+// forces and per-atom energies: F_a = -g, F_b = +g; each endpoint receives the
+// ZBL energy of the directed edge it receives
+__global__ __launch_bounds__(256) void k_forces(int N, const int *inc_off, const int *inc, const int *cand2act,
+                                                const double *pg, const double *pzbl, const double *flr,
+                                                const double *eatom, const double *elr, double *f,
+                                                double *ezbl, double *etot) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  double f0 = 0, f1 = 0, f2 = 0, ez = 0;
+  for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
+    const int e = inc[k];
+    const int p = cand2act[e >> 1];
+    if (p < 0) continue;
+    const double s = (e & 1) ? 1.0 : -1.0;
+    f0 += s * pg[3 * p]; f1 += s * pg[3 * p + 1]; f2 += s * pg[3 * p + 2];
+    ez += pzbl[2 * p];
+  }
+  f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2); ez = wave_sum(ez);
+  if (lane == 0) {
+    f[3 * n] = f0 + flr[3 * n];
+    f[3 * n + 1] = f1 + flr[3 * n + 1];
+    f[3 * n + 2] = f2 + flr[3 * n + 2];
+    ezbl[n] = ez;
+    etot[n] = eatom[n] + ez + elr[n];
+  }
+}
+
+// energy, virial (SR pairs + LR per-node halves), electrostatic and dispersion
+// totals: red[0] E, red[1..6] W, red[7] E_el, red[8] E_disp.  One block.
+__global__ __launch_bounds__(1024) void k_reduce(int N, const int *n_active, const double *etot,
+                                                 const double *pv, const double *pg, const double *vlr,
+                                                 const double *parts, double *red) {
+  __shared__ double part[1024];
+  double acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = threadIdx.x; i < N; i += 1024) {
+    acc[0] += etot[i];
+    for (int c = 0; c < 6; ++c) acc[1 + c] += vlr[6 * std::size_t(i) + c];
+    acc[7] += parts[2 * i];
+    acc[8] += parts[2 * i + 1];
+  }
+  const int P = *n_active;
+  for (int p = threadIdx.x; p < P; p += 1024) {
+    const double *v = pv + 3 * std::size_t(p), *g = pg + 3 * std::size_t(p);
+    acc[1] -= v[0] * g[0]; acc[2] -= v[1] * g[1]; acc[3] -= v[2] * g[2];
+    acc[4] -= 0.5 * (v[0] * g[1] + v[1] * g[0]);
+    acc[5] -= 0.5 * (v[0] * g[2] + v[2] * g[0]);
+    acc[6] -= 0.5 * (v[1] * g[2] + v[2] * g[1]);
+  }
+  for (int c = 0; c < 9; ++c) {
+    part[threadIdx.x] = acc[c];
+    __syncthreads();
+    for (int st = 512; st > 0; st >>= 1) {
+      if (int(threadIdx.x) < st) part[threadIdx.x] += part[threadIdx.x + st];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) red[c] = part[0];
+    __syncthreads();
+  }
+}
+
+int ceil_div(std::int64_t a, std::int64_t b) { return int((a + b - 1) / b); }
+
+}  // namespace
+
+// ====================================================================== host
+Evaluator::Buffer *Evaluator::buf(const char *) {
+  buffers_.push_back(new Buffer());
+  return buffers_.back();
+}
+
+template <class T>
+T *Evaluator::ensure(Buffer *b, std::size_t count) {
+  const std::size_t need = std::max<std::size_t>(count, 1) * sizeof(T);
+  if (b->bytes < need) {
+    if (b->p) { HIP_CHECK(hipFree(b->p)); bytes_ -= b->bytes; }
+    b->p = nullptr;
+    const std::size_t cap = need + need / 8;  // retained capacity with slack
+    HIP_CHECK(hipMalloc(&b->p, cap));
+    b->bytes = cap;
+    bytes_ += cap;
+  }
+  return static_cast<T *>(b->p);
+}
+
+void Evaluator::release_all() {
+  for (Buffer *b : buffers_) {
+    if (b->p) (void)hipFree(b->p);
+    delete b;
+  }
+  buffers_.clear();
+  for (void *p : weight_allocs_) (void)hipFree(p);
+  weight_allocs_.clear();
+}
+
+Evaluator::~Evaluator() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  release_all();
+  if (own_stream_) (void)hipStreamDestroy(own_stream_);
+}
+
+namespace {
+std::vector<double> transpose(const std::vector<double> &w, std::size_t rows, std::size_t cols) {
+  std::vector<double> t(w.size());
+  for (std::size_t r = 0; r < rows; ++r)
+    for (std::size_t c = 0; c < cols; ++c) t[c * rows + r] = w[r * cols + c];
+  return t;
+}
+}  // namespace
+
+Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::move(model)), device_(device) {
+  int count = 0;
+  HIP_CHECK(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) throw std::runtime_error("SO3LR: HIP device index out of range");
+  HIP_CHECK(hipSetDevice(device));
+  HIP_CHECK(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking));
+  stream_ = own_stream_;
+  const Model &m = *model_;
+  const Architecture &a = m.arch();
+  layers_ = a.layers;
+  gamma_ = a.gamma;
+  rc_ = a.sr_cutoff;
+  avg_ = a.attention_norm;
+  ln_eps_ = a.ln_eps;
+  auto up = [&](const std::vector<double> &v) -> const double * {
+    void *p = nullptr;
+    HIP_CHECK(hipMalloc(&p, v.size() * sizeof(double)));
+    HIP_CHECK(hipMemcpy(p, v.data(), v.size() * sizeof(double), hipMemcpyHostToDevice));
+    weight_allocs_.push_back(p);
+    bytes_ += std::int64_t(v.size() * sizeof(double));
+    return static_cast<const double *>(p);
+  };
+  const std::size_t F = kF, R = kR, FH = kFH, NI = kNI, HW = kHW;
+  for (int b = 0; b < layers_; ++b) {
+    const std::string p = "model.euclidean_transformers." + std::to_string(b) + ".";
+    const std::string at = p + "euclidean_attention_block.";
+    BlockWeights &B = bw_[b];
+    std::vector<double> qkv;
+    for (const char *nm : {"W_q_inv", "W_k_inv", "W_v_inv", "W_q_ev", "W_k_ev"}) {
+      const auto w = m.f64(at + nm, {4, HW, HW});
+      qkv.insert(qkv.end(), w.begin(), w.end());
+    }
+    B.wqkv = up(qkv);
+    for (int k = 0; k < 2; ++k) {
+      // the reference evaluates the transformer-level filter nets
+      // (kokkos_integrated_block0.cpp:507-512)
+      const std::string f = p + (k == 0 ? "filter_net_inv." : "filter_net_ev.");
+      B.fw0[k] = up(m.f64(f + "mlp_rbf.0.weight", {F, R}));
+      B.fb0[k] = up(m.f64(f + "mlp_rbf.0.bias", {F}));
+      const auto w1 = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.weight", {F, F});
+      B.fw1[k] = up(w1);
+      B.fw1t[k] = up(transpose(w1, F, F));
+      B.fb1[k] = up(m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F}));
+      B.fe0[k] = up(m.f64(f + "mlp_ev.0.weight", {FH, 4}));
+      B.feb0[k] = up(m.f64(f + "mlp_ev.0.bias", {FH}));
+      const auto e1 = m.f64(f + "mlp_ev.mlp_ev_layer_1.0.weight", {F, FH});
+      B.fe1[k] = up(e1);
+      B.fe1t[k] = up(transpose(e1, F, FH));
+      B.feb1[k] = up(m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F}));
+    }
+    B.att_cg = up(m.f64(at + "so3_conv_invariants.cg_rep", {24}));
+    B.int_cg = up(m.f64(p + "interaction_block.so3_conv_invariants.cg_rep", {24}));
+    B.ln1w = up(m.f64(p + "layer_norm_inv_1.weight", {F}));
+    B.ln1b = up(m.f64(p + "layer_norm_inv_1.bias", {F}));
+    B.ln2w = up(m.f64(p + "layer_norm_inv_2.weight", {F}));
+    B.ln2b = up(m.f64(p + "layer_norm_inv_2.bias", {F}));
+    const auto m1 = m.f64(p + "mlp_1.1.weight", {F, F}), m2 = m.f64(p + "mlp_1.3.weight", {F, F});
+    B.m1w = up(m1); B.m1t = up(transpose(m1, F, F));
+    B.m2w = up(m2); B.m2t = up(transpose(m2, F, F));
+    B.m1b = up(m.f64(p + "mlp_1.1.bias", {F}));
+    B.m2b = up(m.f64(p + "mlp_1.3.bias", {F}));
+    const auto iw = m.f64(p + "interaction_block.linear_layer.weight", {NI, NI});
+    B.intw = up(iw); B.intt = up(transpose(iw, NI, NI));
+    B.intb = up(m.f64(p + "interaction_block.linear_layer.bias", {NI}));
+  }
+  {
+    const std::string e = "model.atomic_energy_output_block.", q = "model.partial_charges_output_block.",
+                      h = "model.hirshfeld_output_block.";
+    std::vector<double> w1 = m.f64(e + "layers.0.weight", {F, F});
+    const auto qw1 = m.f64(q + "transform_inv_features.0.weight", {F, F});
+    const auto hw1 = m.f64(h + "transform_features.0.weight", {std::size_t(kHH), F});
+    w1.insert(w1.end(), qw1.begin(), qw1.end());
+    w1.insert(w1.end(), hw1.begin(), hw1.end());
+    hw_.w1 = up(w1);
+    hw_.w1t = up(transpose(w1, 320, F));
+    std::vector<double> b1 = m.f64(e + "layers.0.bias", {F});
+    const auto qb1 = m.f64(q + "transform_inv_features.0.bias", {F});
+    const auto hb1 = m.f64(h + "transform_features.0.bias", {std::size_t(kHH)});
+    b1.insert(b1.end(), qb1.begin(), qb1.end());
+    b1.insert(b1.end(), hb1.begin(), hb1.end());
+    hw_.b1 = up(b1);
+    hw_.ew2 = up(m.f64(e + "final_layer.weight", {1, F}));
+    hw_.eb2 = m.f64(e + "final_layer.bias", {1})[0];
+    hw_.escale = up(m.f64(e + "energy_scales.weight", {1, 118}));
+    hw_.eshift = up(m.f64(e + "energy_shifts", {118}));
+    hw_.qw2 = up(m.f64(q + "transform_inv_features.2.weight", {1, F}));
+    hw_.qb2 = m.f64(q + "transform_inv_features.2.bias", {1})[0];
+    hw_.qemb = up(m.f64(q + "atomic_embedding.weight", {100, 1}));
+    hw_.hw2 = up(m.f64(h + "transform_features.2.weight", {std::size_t(kHH), std::size_t(kHH)}));
+    hw_.hb2 = up(m.f64(h + "transform_features.2.bias", {std::size_t(kHH)}));
+    hw_.hqemb = up(m.f64(h + "q_embedding.weight", {100, std::size_t(kHH)}));
+    hw_.hvshift = up(m.f64(h + "v_shift_embedding.weight", {100, 1}));
+    const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
+    const auto kk = m.i64("model.radial_embedding.radial_basis_fn.k", {R});
+    const auto kr = m.i64("model.radial_embedding.radial_basis_fn.k_rev", {R});
+    hw_.rbf_b = up(bb);
+    hw_.rbf_k = up(std::vector<double>(kk.begin(), kk.end()));
+    hw_.rbf_kr = up(std::vector<double>(kr.begin(), kr.end()));
+    const auto &al = m.tensor("physical.reference_alphas");
+    if (al.shape.size() != 1 || al.shape[0] < 8) throw std::runtime_error("SO3LR physical reference-table contract changed");
+    hw_.n_ref = int(al.shape[0]);
+    hw_.alpha_ref = up(m.f64("physical.reference_alphas", al.shape));
+    hw_.c6_ref = up(m.f64("physical.reference_c6", al.shape));
+  }
+  emb_w_ = m.f64("model.inv_feature_embedding.embedding.weight", {F, 118});
+  charge_spin_.load(m);
+  zbl_.ke = a.zbl_ke; zbl_.rc = a.sr_cutoff; zbl_.switch_off = a.zbl_switch_off;
+  zbl_.p = a.zbl_p; zbl_.d = a.zbl_d;
+  for (int k = 0; k < 4; ++k) { zbl_.a[k] = a.zbl_a[k]; zbl_.c[k] = a.zbl_c[k]; }
+  lr_.ke = a.lr_ke; lr_.sigma = a.lr_sigma; lr_.cutoff = a.lr_cutoff; lr_.cuton_el = a.lr_cuton_el;
+  lr_.fine_factor = std::pow(a.lr_fine, -4.0 / 21.0);
+  lr_.bohr = a.lr_bohr; lr_.hartree = a.lr_hartree; lr_.disp_scale = a.lr_disp_scale;
+  lr_.cuton_disp = a.lr_cuton_disp; lr_.full_scale = 2.0 * a.lr_pair_scale;
+  {
+    const double cr = lr_.cutoff / lr_.sigma;
+    const double cerf = std::erf(cr), cexp = std::exp(-cr * cr);
+    lr_.shift = cerf / lr_.cutoff;
+    lr_.fshift = (2.0 * lr_.cutoff * cexp * 0.56418958354775628695 / lr_.sigma - cerf) / (lr_.cutoff * lr_.cutoff);
+  }
+  lr_.n_ref = hw_.n_ref;
+
+  z_ = buf("z"); x0_ = buf("x0"); img_of_node_ = buf("img"); img_off_ = buf("img_off"); img_q_ = buf("img_q");
+  xs_ = buf("xs"); evs_ = buf("evs"); qkv_ = buf("qkv"); aev_ = buf("aev"); n1_ = buf("n1");
+  n1hat_ = buf("n1hat"); n1is_ = buf("n1is"); hpre_ = buf("hpre"); tout_ = buf("tout");
+  pre2hat_ = buf("pre2hat"); pre2is_ = buf("pre2is"); ainv_ = buf("ainv"); act_ = buf("act");
+  hid_ = buf("hid"); pbuf_ = buf("p"); cat_ = buf("cat"); hhead_ = buf("hhead"); hkey_ = buf("hkey");
+  heff_ = buf("heff"); eatom_ = buf("eatom"); qraw_ = buf("qraw"); q_ = buf("q"); hir_ = buf("hir");
+  qseed_ = buf("qseed"); elr_ = buf("elr"); dq_ = buf("dq"); dh_ = buf("dh"); flr_ = buf("flr");
+  vlr_ = buf("vlr"); elr_parts_ = buf("elr_parts"); ezbl_ = buf("ezbl"); gx_ = buf("gx");
+  gev_ = buf("gev"); gp_ = buf("gp"); gt_ = buf("gt"); gcat_ = buf("gcat"); ghid_ = buf("ghid");
+  gact_ = buf("gact"); gainv_ = buf("gainv"); gaev_ = buf("gaev"); gqkv_ = buf("gqkv");
+  ghead_ = buf("ghead"); fout_ = buf("fout"); etot_ = buf("etot"); red_ = buf("red");
+  owner_ = buf("owner"); sr_rows_ = buf("sr_rows"); sr_nodes_ = buf("sr_nodes");
+  sr_inc_off_ = buf("sr_inc_off"); sr_inc_ = buf("sr_inc"); lr_rows_ = buf("lr_rows");
+  lr_nodes_ = buf("lr_nodes"); lr_inc_off_ = buf("lr_inc_off"); lr_inc_ = buf("lr_inc");
+  blk_count_ = buf("blk"); n_active_ = buf("nact"); cand2act_ = buf("c2a"); pa_ = buf("pa");
+  pv_ = buf("pv"); pr_ = buf("pr"); pY_ = buf("pY"); pfc_ = buf("pfc"); pzbl_ = buf("pzbl");
+  ps_ = buf("ps"); pf_ = buf("pf"); palpha_ = buf("palpha"); df_ = buf("df"); dfc_ = buf("dfc");
+  ds_ = buf("ds"); dr_ = buf("dr"); dY_ = buf("dY"); pg_ = buf("pg"); xrows_ = buf("xrows");
+  fhost_ = buf("fhost");
+}
+
+void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector<std::int64_t> &image_offsets,
+                           const std::vector<double> &charges, const std::vector<double> &multiplicities) {
+  const std::int64_t n = std::int64_t(z.size());
+  if (n <= 0) throw std::invalid_argument("SO3LR: the system has no atoms");
+  for (auto zz : z)
+    if (zz < 1 || zz > 99) throw std::invalid_argument("SO3LR: atomic numbers must lie in 1..99");
+  const std::int64_t ni = std::int64_t(charges.size());
+  if (ni < 1 || std::int64_t(multiplicities.size()) != ni || std::int64_t(image_offsets.size()) != ni + 1 ||
+      image_offsets.front() != 0 || image_offsets.back() != n)
+    throw std::invalid_argument("SO3LR: inconsistent image description");
+  std::vector<double> x0(std::size_t(n) * kF);
+  std::vector<int> img(n);
+  for (std::int64_t k = 0; k < ni; ++k) {
+    const std::int64_t lo = image_offsets[k], hi = image_offsets[k + 1];
+    if (hi <= lo) throw std::invalid_argument("SO3LR: every image needs at least one atom");
+    std::int64_t counts[119] = {0};
+    for (std::int64_t i = lo; i < hi; ++i) ++counts[z[i]];
+    const std::string why = charge_multiplicity_problem(counts, charges[k], multiplicities[k]);
+    if (!why.empty())
+      throw std::domain_error("charge " + std::to_string(charges[k]) + " with multiplicity " +
+                              std::to_string(multiplicities[k]) + ": " + why);
+    const std::vector<double> tab = charge_spin_.table(counts, charges[k], multiplicities[k] - 1.0);
+    const double inv = 1.0 / model_->arch().embedding_scale;
+    for (std::int64_t i = lo; i < hi; ++i) {
+      img[i] = int(k);
+      for (int c = 0; c < kF; ++c)
+        x0[std::size_t(i) * kF + c] = (emb_w_[c * 118 + (z[i] - 1)] + tab[(z[i] - 1) * kF + c]) * inv;
+    }
+  }
+  n_ = n;
+  n_images_ = ni;
+  image_offsets_ = image_offsets;
+  HIP_CHECK(hipMemcpyAsync(ensure<int>(z_, n), z.data(), n * sizeof(int), hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(ensure<double>(x0_, x0.size()), x0.data(), x0.size() * sizeof(double),
+                           hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(ensure<std::int64_t>(img_off_, ni + 1), image_offsets.data(),
+                           (ni + 1) * sizeof(std::int64_t), hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipMemcpyAsync(ensure<double>(img_q_, ni), charges.data(), ni * sizeof(double),
+                           hipMemcpyHostToDevice, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  system_ready_ = true;
+  topology_ready_ = false;
+  evaluated_ = false;
+}
+
+namespace {
+// half pairs -> node-major incidence CSR (stable: pairs in increasing order)
+void incidence(std::int64_t n, const std::vector<int> &nodes, std::vector<int> &off, std::vector<int> &inc) {
+  const std::int64_t P = std::int64_t(nodes.size() / 2);
+  if (2 * P >= (std::int64_t(1) << 31)) throw std::length_error("SO3LR: neighbour list exceeds 2^30 pairs");
+  off.assign(n + 1, 0);
+  for (std::int64_t p = 0; p < P; ++p) { ++off[nodes[2 * p] + 1]; ++off[nodes[2 * p + 1] + 1]; }
+  for (std::int64_t i = 0; i < n; ++i) off[i + 1] += off[i];
+  inc.resize(2 * P);
+  std::vector<int> fill(off.begin(), off.end() - 1);
+  for (std::int64_t p = 0; p < P; ++p) {
+    inc[fill[nodes[2 * p]]++] = int(2 * p);
+    inc[fill[nodes[2 * p + 1]]++] = int(2 * p + 1);
+  }
+}
+}  // namespace
+
+void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int sr_kind, std::int64_t sr_inum,
+                             const std::int32_t *sr_ilist, const std::int64_t *sr_off,
+                             const std::int32_t *sr_neigh, std::int64_t lr_inum,
+                             const std::int32_t *lr_ilist, const std::int64_t *lr_off,
+                             const std::int32_t *lr_neigh) {
+  if (!system_ready_) throw std::logic_error("SO3LR: set the system before the topology");
+  const std::int64_t n = n_;
+  if (n_rows < n || !owner) throw std::invalid_argument("SO3LR: fewer rows than owned atoms");
+  for (std::int64_t r = 0; r < n_rows; ++r) {
+    const std::int32_t o = owner[r];
+    if (o < 0 || o >= n || (r < n && o != r))
+      throw std::invalid_argument("SO3LR: owner_of_row must be the identity on owned rows and map ghosts to owned atoms");
+  }
+  auto collect = [&](const char *what, bool full, std::int64_t inum, const std::int32_t *ilist,
+                     const std::int64_t *off, const std::int32_t *neigh, std::vector<int> &rows,
+                     std::vector<int> &nodes) {
+    if (inum < 0 || (inum > 0 && (!ilist || !off || !neigh)))
+      throw std::invalid_argument(std::string("SO3LR: invalid ") + what + " neighbour list");
+    if (inum > 0 && off[0] != 0) throw std::invalid_argument(std::string("SO3LR: ") + what + " offsets must start at 0");
+    std::int64_t kept = 0, dropped = 0;
+    rows.clear();
+    nodes.clear();
+    for (std::int64_t k = 0; k < inum; ++k) {
+      const std::int32_t i = ilist[k];
+      if (i < 0 || i >= n) throw std::invalid_argument(std::string("SO3LR: ") + what + " receiver is not an owned row");
+      if (off[k + 1] < off[k]) throw std::invalid_argument(std::string("SO3LR: decreasing ") + what + " offsets");
+      for (std::int64_t e = off[k]; e < off[k + 1]; ++e) {
+        const std::int32_t j = neigh[e];
+        if (j < 0 || j >= n_rows) throw std::invalid_argument(std::string("SO3LR: ") + what + " neighbour row out of range");
+        if (j == i) continue;
+        const std::int32_t oj = owner[j];
+        if (oj == i)
+          throw std::invalid_argument(std::string("SO3LR: ") + what +
+                                      " list pairs an atom with its own periodic image; the box is too small for the cutoff");
+        if (full && oj < i) { ++dropped; continue; }
+        ++kept;
+        rows.push_back(i); rows.push_back(j);
+        nodes.push_back(i); nodes.push_back(oj);
+      }
+    }
+    if (full && kept != dropped)
+      throw std::invalid_argument("SO3LR: the full short-range list is not symmetric (an edge lacks its reverse)");
+  };
+  std::vector<int> sr_rows, sr_nodes, lr_rows, lr_nodes;
+  collect("short-range", sr_kind == 0, sr_inum, sr_ilist, sr_off, sr_neigh, sr_rows, sr_nodes);
+  collect("long-range", false, lr_inum, lr_ilist, lr_off, lr_neigh, lr_rows, lr_nodes);
+  std::vector<int> sr_off_v, sr_inc, lr_off_v, lr_inc;
+  incidence(n, sr_nodes, sr_off_v, sr_inc);
+  incidence(n, lr_nodes, lr_off_v, lr_inc);
+  p_sr_ = std::int64_t(sr_nodes.size() / 2);
+  p_lr_ = std::int64_t(lr_nodes.size() / 2);
+  n_rows_ = n_rows;
+  auto put = [&](Buffer *b, const std::vector<int> &v) {
+    HIP_CHECK(hipMemcpyAsync(ensure<int>(b, v.size()), v.data(), v.size() * sizeof(int), hipMemcpyHostToDevice, stream_));
+  };
+  put(sr_rows_, sr_rows); put(sr_nodes_, sr_nodes); put(sr_inc_off_, sr_off_v); put(sr_inc_, sr_inc);
+  put(lr_rows_, lr_rows); put(lr_nodes_, lr_nodes); put(lr_inc_off_, lr_off_v); put(lr_inc_, lr_inc);
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  topology_ready_ = true;
+  evaluated_ = false;
+}
+
+void Evaluator::compute_host(const double *x_rows, int flags, double *f, double *eatom, double *energy,
+                             double *virial) {
+  if (!topology_ready_) throw std::logic_error("SO3LR: compute called before set_topology");
+  double *xd = ensure<double>(xrows_, std::size_t(n_rows_) * 3);
+  HIP_CHECK(hipMemcpyAsync(xd, x_rows, std::size_t(n_rows_) * 3 * sizeof(double), hipMemcpyHostToDevice, stream_));
+  double *fd = ensure<double>(fhost_, std::size_t(n_) * 4);
+  compute_device(xd, flags, fd, (flags & 2) ? fd + 3 * n_ : nullptr, energy, virial);
+  if (f) HIP_CHECK(hipMemcpyAsync(f, fd, std::size_t(n_) * 3 * sizeof(double), hipMemcpyDeviceToHost, stream_));
+  if (eatom && (flags & 2))
+    HIP_CHECK(hipMemcpyAsync(eatom, fd + 3 * n_, std::size_t(n_) * sizeof(double), hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+void Evaluator::compute_device(const double *x, int flags, double *f_out, double *eatom_out, double *energy,
+                               double *virial) {
+  if (!topology_ready_) throw std::logic_error("SO3LR: compute called before set_topology");
+  const std::int64_t N = n_, P = p_sr_, L = layers_;
+  const std::size_t Nz = std::size_t(N), Pz = std::size_t(std::max<std::int64_t>(P, 1));
+  hipStream_t s = stream_;
+  // --- buffers (retained capacity) ---
+  const int *z = ensure<int>(z_, Nz);
+  double *xs = ensure<double>(xs_, (L + 1) * Nz * kF);
+  double *evs = ensure<double>(evs_, (L + 1) * Nz * kE);
+  double *qkv = ensure<double>(qkv_, L * Nz * 640);
+  double *aev = ensure<double>(aev_, L * Nz * kE);
+  double *n1 = ensure<double>(n1_, L * Nz * kF);
+  double *n1hat = ensure<double>(n1hat_, L * Nz * kF);
+  double *n1is = ensure<double>(n1is_, L * Nz);
+  double *hpre = ensure<double>(hpre_, L * Nz * kF);
+  double *tout = ensure<double>(tout_, L * Nz * kNI);
+  double *pre2hat = ensure<double>(pre2hat_, L * Nz * kF);
+  double *pre2is = ensure<double>(pre2is_, L * Nz);
+  double *ainv = ensure<double>(ainv_, Nz * kF);
+  double *act = ensure<double>(act_, Nz * 320);  // MLP input (128 wide) and head activations (320)
+  double *hid = ensure<double>(hid_, Nz * kF);
+  double *pb = ensure<double>(pbuf_, Nz * kF);
+  double *cat = ensure<double>(cat_, Nz * kNI);
+  double *hhead = ensure<double>(hhead_, Nz * 320);
+  double *hact = act;
+  double *hkey = ensure<double>(hkey_, Nz * kHH);
+  double *heff = ensure<double>(heff_, Nz);
+  double *eatom = ensure<double>(eatom_, Nz);
+  double *qraw = ensure<double>(qraw_, Nz);
+  double *q = ensure<double>(q_, Nz);
+  double *hir = ensure<double>(hir_, Nz);
+  double *qseed = ensure<double>(qseed_, Nz);
+  double *elr = ensure<double>(elr_, Nz);
+  double *dq = ensure<double>(dq_, Nz);
+  double *dh = ensure<double>(dh_, Nz);
+  double *flr = ensure<double>(flr_, Nz * 3);
+  double *vlr = ensure<double>(vlr_, Nz * 6);
+  double *parts = ensure<double>(elr_parts_, Nz * 2);
+  double *ezbl = ensure<double>(ezbl_, Nz);
+  double *gx = ensure<double>(gx_, Nz * kF);
+  double *gev = ensure<double>(gev_, Nz * kE);
+  double *gp = ensure<double>(gp_, Nz * kF);
+  double *gt = ensure<double>(gt_, Nz * kNI);
+  double *gcat = ensure<double>(gcat_, Nz * kNI);
+  double *ghid = ensure<double>(ghid_, Nz * kF);
+  double *gact = ensure<double>(gact_, Nz * kF);
+  double *gainv = ensure<double>(gainv_, Nz * kF);
+  double *gaev = ensure<double>(gaev_, Nz * kE);
+  double *gqkv = ensure<double>(gqkv_, Nz * 640);
+  double *ghead = ensure<double>(ghead_, Nz * 320);
+  double *fo = f_out ? f_out : ensure<double>(fout_, Nz * 3);
+  double *etot = eatom_out ? eatom_out : ensure<double>(etot_, Nz);
+  double *red = ensure<double>(red_, 16);
+  const int nblk = std::max(1, ceil_div(P, kCompactPerBlock));
+  int *blk = ensure<int>(blk_count_, nblk);
+  int *nact = ensure<int>(n_active_, 1);
+  int *c2a = ensure<int>(cand2act_, Pz);
+  int *pa = ensure<int>(pa_, 2 * Pz);
+  double *pv = ensure<double>(pv_, 3 * Pz);
+  double *pr = ensure<double>(pr_, Pz);
+  double *pY = ensure<double>(pY_, kE * Pz);
+  double *pfc = ensure<double>(pfc_, Pz);
+  double *pzbl = ensure<double>(pzbl_, 2 * Pz);
+  double *ps = ensure<double>(ps_, L * 4 * Pz);
+  double *pf = ensure<double>(pf_, L * 256 * Pz);
+  double *palpha = ensure<double>(palpha_, L * 16 * Pz);
+  double *df = ensure<double>(df_, 256 * Pz);
+  double *dfc = ensure<double>(dfc_, Pz);
+  double *ds = ensure<double>(ds_, 4 * Pz);
+  double *dr = ensure<double>(dr_, Pz);
+  double *dY = ensure<double>(dY_, kE * Pz);
+  double *pg = ensure<double>(pg_, 3 * Pz);
+  const int *sr_rows = static_cast<const int *>(sr_rows_->p);
+  const int *sr_nodes = static_cast<const int *>(sr_nodes_->p);
+  const int *sr_off = static_cast<const int *>(sr_inc_off_->p);
+  const int *sr_inc = static_cast<const int *>(sr_inc_->p);
+  const int *lr_rows = static_cast<const int *>(lr_rows_->p);
+  const int *lr_nodes = static_cast<const int *>(lr_nodes_->p);
+  const int *lr_off = static_cast<const int *>(lr_inc_off_->p);
+  const int *lr_inc = static_cast<const int *>(lr_inc_->p);
+  const std::int64_t *img_off = static_cast<const std::int64_t *>(img_off_->p);
+  const double *img_q = static_cast<const double *>(img_q_->p);
+
+  const int gN4 = ceil_div(N, 4);
+  // per-launch HIP events for the measured kernels; units: 0 = active pairs, 1 = nodes
+  struct Pending { const char *name; hipEvent_t a, b; int unit_kind; };
+  std::vector<Pending> pending;
+  auto timed = [&](const char *name, int unit_kind, auto &&launch) {
+    if (!timing_) { launch(); return; }
+    Pending pd{name, nullptr, nullptr, unit_kind};
+    HIP_CHECK(hipEventCreate(&pd.a));
+    HIP_CHECK(hipEventCreate(&pd.b));
+    HIP_CHECK(hipEventRecord(pd.a, s));
+    launch();
+    HIP_CHECK(hipEventRecord(pd.b, s));
+    pending.push_back(pd);
+  };
+  auto fill = [&](double *p, std::size_t cnt) {
+    if (cnt) hipLaunchKernelGGL(k_fill, dim3(unsigned((cnt + 255) / 256)), dim3(256), 0, s, p, cnt, 0.0);
+  };
+  auto linear = [&](int mode, int rows, int K, int O, const double *in, int ldin, const double *WT,
+                    const double *bias, double *out, int ldout, double *out2, const double *aux, int ldaux) {
+    const dim3 grid(unsigned(ceil_div(O, 64)), unsigned(ceil_div(rows, kLinRows)));
+    if (mode == 0) hipLaunchKernelGGL(k_linear<0>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
+    if (mode == 1) hipLaunchKernelGGL(k_linear<1>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
+    if (mode == 2) hipLaunchKernelGGL(k_linear<2>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
+    if (mode == 3) hipLaunchKernelGGL(k_linear<3>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
+  };
+
+  // --- active short-range pairs, geometry, ZBL ---
+  const double rc2 = rc_ * rc_;
+  if (P > 0) {
+    hipLaunchKernelGGL(k_sr_count, dim3(nblk), dim3(256), 0, s, int(P), sr_rows, x, rc2, blk);
+    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, blk, nact);
+    hipLaunchKernelGGL(k_sr_compact, dim3(nblk), dim3(256), 0, s, int(P), sr_rows, sr_nodes, x, rc2, blk, z,
+                       zbl_, c2a, pa, pv, pr, pY, pfc, pzbl);
+  } else {
+    HIP_CHECK(hipMemsetAsync(nact, 0, sizeof(int), s));
+  }
+  fill(dY, kE * Pz);
+  fill(dr, Pz);
+  HIP_CHECK(hipMemcpyAsync(xs, x0_->p, Nz * kF * sizeof(double), hipMemcpyDeviceToDevice, s));
+  fill(evs, Nz * kE);
+  const double inv_avg = 1.0 / avg_;
+  const unsigned gP = unsigned(std::max<std::int64_t>(P, 1));
+
+  // --- interaction blocks, forward ---
+  for (int b = 0; b < L; ++b) {
+    const BlockWeights &B = bw_[b];
+    double *xb = xs + b * Nz * kF, *evb = evs + b * Nz * kE;
+    double *qb = qkv + b * Nz * 640, *aevb = aev + b * Nz * kE;
+    double *n1b = n1 + b * Nz * kF, *n1hb = n1hat + b * Nz * kF, *n1ib = n1is + b * Nz;
+    double *hpb = hpre + b * Nz * kF, *tb = tout + b * Nz * kNI;
+    double *p2h = pre2hat + b * Nz * kF, *p2i = pre2is + b * Nz;
+    double *psb = ps + b * 4 * Pz, *pfb = pf + b * 256 * Pz, *pab = palpha + b * 16 * Pz;
+    FilterArgs A;
+    for (int k = 0; k < 2; ++k) {
+      A.fw0[k] = B.fw0[k]; A.fb0[k] = B.fb0[k]; A.fw1t[k] = B.fw1t[k]; A.fb1[k] = B.fb1[k];
+      A.fe0[k] = B.fe0[k]; A.feb0[k] = B.feb0[k]; A.fe1t[k] = B.fe1t[k]; A.feb1[k] = B.feb1[k];
+    }
+    A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
+    hipLaunchKernelGGL(k_qkv, dim3(ceil_div(N, 16)), dim3(128), 0, s, int(N), xb, B.wqkv, qb);
+    timed("filter_fwd", 0, [&] {
+      hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
+    });
+    timed("attn_fwd", 1, [&] {
+      hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, xb, evb, qb,
+                         pfb, pY, pfc, inv_avg, pab, ainv, aevb);
+    });
+    hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
+                       n1ib, act);
+    linear(1, int(N), kF, kF, act, kF, B.m1t, B.m1b, hpb, kF, hid, nullptr, 0);
+    // in-place: hid becomes silu(hpre); the MLP output goes to pb = n1 + W2 hid + b2
+    linear(2, int(N), kF, kF, hid, kF, B.m2t, B.m2b, pb, kF, nullptr, n1b, kF);
+    hipLaunchKernelGGL(k_concat, dim3(gN4), dim3(256), 0, s, int(N), pb, aevb, B.int_cg, cat);
+    linear(0, int(N), kNI, kNI, cat, kNI, B.intt, B.intb, tb, kNI, nullptr, nullptr, 0);
+    hipLaunchKernelGGL(k_post2, dim3(gN4), dim3(256), 0, s, int(N), pb, tb, aevb, B.ln2w, B.ln2b, ln_eps_,
+                       xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);
+  }
+
+  // --- heads, charge correction, long range ---
+  HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hw2, hw_.hb2, hw_.hqemb, hw_.hvshift,
+             hw_.eb2, hw_.qb2};
+  const double *xf = xs + L * Nz * kF;
+  linear(1, int(N), kF, 320, xf, kF, hw_.w1t, hw_.b1, hhead, 320, hact, nullptr, 0);
+  hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, hkey, heff, hir);
+  hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
+  timed("long_range", 1, [&] {
+    hipLaunchKernelGGL(k_lr, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x, z, q, hir,
+                       lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
+  });
+  hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
+  hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, H, ghead);
+  linear(0, int(N), 320, kF, ghead, 320, hw_.w1, nullptr, gx, kF, nullptr, nullptr, 0);
+  fill(gev, Nz * kE);
+
+  // --- interaction blocks, reverse ---
+  for (int b = L - 1; b >= 0; --b) {
+    const BlockWeights &B = bw_[b];
+    double *evb = evs + b * Nz * kE;
+    double *qb = qkv + b * Nz * 640, *aevb = aev + b * Nz * kE;
+    double *n1b = n1 + b * Nz * kF, *n1hb = n1hat + b * Nz * kF, *n1ib = n1is + b * Nz;
+    double *hpb = hpre + b * Nz * kF, *tb = tout + b * Nz * kNI;
+    double *p2h = pre2hat + b * Nz * kF, *p2i = pre2is + b * Nz;
+    double *psb = ps + b * 4 * Pz, *pfb = pf + b * 256 * Pz, *pab = palpha + b * 16 * Pz;
+    FilterArgs A;
+    for (int k = 0; k < 2; ++k) {
+      A.fw0[k] = B.fw0[k]; A.fb0[k] = B.fb0[k]; A.fw1t[k] = B.fw1t[k]; A.fb1[k] = B.fb1[k];
+      A.fe0[k] = B.fe0[k]; A.feb0[k] = B.feb0[k]; A.fe1t[k] = B.fe1t[k]; A.feb1[k] = B.feb1[k];
+    }
+    A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
+    hipLaunchKernelGGL(k_post2_bwd, dim3(gN4), dim3(256), 0, s, int(N), gx, gev, tb, aevb, B.ln2w, p2h, p2i, gp,
+                       gt, gaev);
+    linear(0, int(N), kNI, kNI, gt, kNI, B.intw, nullptr, gcat, kNI, nullptr, nullptr, 0);
+    hipLaunchKernelGGL(k_post_mid_bwd, dim3(gN4), dim3(256), 0, s, int(N), gcat, aevb, B.int_cg, gp, gaev);
+    linear(3, int(N), kF, kF, gp, kF, B.m2w, nullptr, ghid, kF, nullptr, hpb, kF);
+    linear(0, int(N), kF, kF, ghid, kF, B.m1w, nullptr, gact, kF, nullptr, nullptr, 0);
+    hipLaunchKernelGGL(k_ln1_bwd, dim3(gN4), dim3(256), 0, s, int(N), gp, gact, n1b, B.ln1w, n1hb, n1ib, gainv);
+    timed("attn_bwd", 1, [&] {
+      hipLaunchKernelGGL(k_attn_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, qb, pfb, pY, pfc,
+                         pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
+    });
+    timed("filter_bwd", 0, [&] {
+      hipLaunchKernelGGL(k_filter_bwd, dim3(gP), dim3(128), 0, s, nact, pr, pfc, psb, df, dfc, A, rc_, ds, dr);
+    });
+    hipLaunchKernelGGL(k_qkv_bwd, dim3(ceil_div(N, 8)), dim3(128), 0, s, int(N), gqkv, B.wqkv, gainv, gx);
+    hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, evb, B.att_cg, ds,
+                       gaev, gev);
+  }
+
+  // --- geometry reverse, forces, energies, virial ---
+  hipLaunchKernelGGL(k_geom_bwd, dim3(ceil_div(std::max<std::int64_t>(P, 1), 256)), dim3(256), 0, s, nact, pv, pr,
+                     dr, pzbl, dY, pg);
+  hipLaunchKernelGGL(k_forces, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pg, pzbl, flr, eatom, elr,
+                     fo, ezbl, etot);
+  hipLaunchKernelGGL(k_reduce, dim3(1), dim3(1024), 0, s, int(N), nact, etot, pv, pg, vlr, parts, red);
+  HIP_CHECK(hipGetLastError());
+  double host_red[9];
+  int host_nact = 0;
+  HIP_CHECK(hipMemcpyAsync(host_red, red, 9 * sizeof(double), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipMemcpyAsync(&host_nact, nact, sizeof(int), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipStreamSynchronize(s));
+  last_active_ = host_nact;
+  for (Pending &pd : pending) {
+    float ms = 0.f;
+    HIP_CHECK(hipEventElapsedTime(&ms, pd.a, pd.b));
+    Timing &t = timings_[pd.name];
+    t.ms += ms;
+    t.launches += 1;
+    t.units += pd.unit_kind == 0 ? host_nact : N;
+    (void)hipEventDestroy(pd.a);
+    (void)hipEventDestroy(pd.b);
+  }
+  if (energy) *energy = host_red[0];
+  if (virial) for (int c = 0; c < 6; ++c) virial[c] = host_red[1 + c];
+  totals_[0] = host_red[7];
+  totals_[1] = host_red[8];
+  last_etot_ = etot;
+  evaluated_ = true;
+  (void)flags;
+}
+
+bool Evaluator::timing_read(const std::string &kernel, double &total_ms, std::int64_t &launches,
+                            std::int64_t &units) const {
+  const auto it = timings_.find(kernel);
+  if (it == timings_.end()) return false;
+  total_ms = it->second.ms;
+  launches = it->second.launches;
+  units = it->second.units;
+  return true;
+}
+
+void Evaluator::last_terms(double *learned, double *zbl, double *lr, double *charges, double *hirshfeld,
+                           double *totals, double *image_energy) {
+  if (!evaluated_) throw std::logic_error("SO3LR: no evaluation yet");
+  const std::size_t Nz = std::size_t(n_);
+  auto get = [&](double *dst, Buffer *b) {
+    if (dst) HIP_CHECK(hipMemcpyAsync(dst, b->p, Nz * sizeof(double), hipMemcpyDeviceToHost, stream_));
+  };
+  get(learned, eatom_); get(zbl, ezbl_); get(lr, elr_); get(charges, q_); get(hirshfeld, hir_);
+  std::vector<double> et;
+  if (image_energy) {
+    et.resize(Nz);
+    HIP_CHECK(hipMemcpyAsync(et.data(), last_etot_, Nz * sizeof(double), hipMemcpyDeviceToHost, stream_));
+  }
+  HIP_CHECK(hipStreamSynchronize(stream_));
+  if (totals) { totals[0] = totals_[0]; totals[1] = totals_[1]; }
+  if (image_energy)
+    for (std::int64_t k = 0; k < n_images_; ++k) {
+      double s = 0.0;
+      for (std::int64_t i = image_offsets_[k]; i < image_offsets_[k + 1]; ++i) s += et[i];
+      image_energy[k] = s;
+    }
+}
+
+}  // namespace so3lr_amd

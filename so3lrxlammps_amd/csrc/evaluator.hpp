@@ -1,0 +1,143 @@
+// SO3LR E + F + virial evaluator on one gfx950 GPU (host side of the kernels).
+//
+// Pair-based, deterministic design.  The short-range graph is kept as unique
+// pairs {a, b} (the reference evaluates both directed edges of a pair
+// separately).  The filters depend on the pair only (distance and the
+// symmetric equivariant invariant), so they are evaluated once per pair and
+// shared by both directions; everything direction-dependent (attention
+// coefficients, harmonics parity) is carried per direction.  Node sums that
+// the reference forms with atomics are gathers over a node-major incidence
+// list (each node sees every pair it belongs to), so results do not depend on
+// thread timing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "device_math.hpp"
+#include "model.hpp"
+
+namespace so3lr_amd {
+
+// Device weight pointers for one interaction block.
+struct BlockWeights {
+  const double *wqkv;                   // (5, 4, 32, 32): q k v q_ev k_ev, (head, in, out)
+  const double *fw0[2], *fb0[2];        // filter {inv, ev} radial layer 0 (128, 32), (128)
+  const double *fw1[2], *fb1[2];        // radial layer 1 (128, 128), (128)
+  const double *fw1t[2];                // its transpose (in, out)
+  const double *fe0[2], *feb0[2];       // spherical layer 0 (32, 4), (32)
+  const double *fe1[2], *feb1[2];       // spherical layer 1 (128, 32), (128)
+  const double *fe1t[2];                // its transpose
+  const double *att_cg, *int_cg;        // (24)
+  const double *ln1w, *ln1b, *ln2w, *ln2b;
+  const double *m1t, *m1b, *m2t, *m2b;  // MLP weights transposed (in, out)
+  const double *m1w, *m2w;              // (out, in) for the reverse
+  const double *intt, *intb, *intw;     // interaction (132x132): transposed and (out, in)
+};
+
+struct HeadWeights {
+  const double *w1t;    // (128, 320): energy | charge | Hirshfeld first layers, transposed
+  const double *w1;     // (320, 128)
+  const double *b1;     // (320)
+  const double *ew2, *qw2;  // (128)
+  double eb2, qb2;
+  const double *escale, *eshift;  // (118)
+  const double *qemb;             // (100)
+  const double *hw2, *hb2;        // (64, 64), (64)
+  const double *hqemb, *hvshift;  // (100, 64), (100)
+  const double *rbf_b, *rbf_k, *rbf_kr;  // (32) each
+  const double *alpha_ref, *c6_ref;
+  int n_ref;
+};
+
+class Evaluator {
+ public:
+  Evaluator(std::shared_ptr<Model> model, int device);
+  ~Evaluator();
+
+  const Model &model() const { return *model_; }
+  void set_system(const std::vector<std::int32_t> &z, const std::vector<std::int64_t> &image_offsets,
+                  const std::vector<double> &charges, const std::vector<double> &multiplicities);
+  void set_topology(std::int64_t n_rows, const std::int32_t *owner_of_row, int sr_kind,
+                    std::int64_t sr_inum, const std::int32_t *sr_ilist, const std::int64_t *sr_off,
+                    const std::int32_t *sr_neigh, std::int64_t lr_inum, const std::int32_t *lr_ilist,
+                    const std::int64_t *lr_off, const std::int32_t *lr_neigh);
+  // x_rows_dev: device positions of all rows.  Forces/eatom to device
+  // buffers (may be null); energy/virial to host.
+  void compute_device(const double *x_rows_dev, int flags, double *f_dev, double *eatom_dev,
+                      double *energy, double *virial);
+  void compute_host(const double *x_rows, int flags, double *f, double *eatom, double *energy,
+                    double *virial);
+  void last_terms(double *learned, double *zbl, double *lr, double *charges, double *hirshfeld,
+                  double *totals, double *image_energy);
+  void set_stream(hipStream_t s) { stream_ = s ? s : own_stream_; }
+  std::int64_t n_owned() const { return n_; }
+  std::int64_t sr_active() const { return last_active_; }
+  std::int64_t sr_candidates() const { return p_sr_; }
+  std::int64_t lr_candidates() const { return p_lr_; }
+  std::int64_t device_bytes() const { return bytes_; }
+  // Kernel timing with HIP events on the launch stream (measurement hook).
+  void set_timing(bool on) { timing_ = on; timings_.clear(); }
+  bool timing_read(const std::string &kernel, double &total_ms, std::int64_t &launches,
+                   std::int64_t &units) const;
+
+ private:
+  std::shared_ptr<Model> model_;
+  int device_;
+  hipStream_t own_stream_ = nullptr, stream_ = nullptr;
+  std::int64_t bytes_ = 0;
+  std::vector<void *> weight_allocs_;
+  BlockWeights bw_[kMaxBlocks];
+  HeadWeights hw_{};
+  ZblParams zbl_{};
+  LrParams lr_{};
+  double gamma_ = 0, rc_ = 0, avg_ = 1, ln_eps_ = 1e-6;
+  int layers_ = 0;
+  ChargeSpin charge_spin_;
+  std::vector<double> emb_w_;  // (128, 118)
+
+  // system
+  std::int64_t n_ = 0, n_images_ = 0, n_rows_ = 0;
+  std::vector<std::int64_t> image_offsets_;
+  bool system_ready_ = false, topology_ready_ = false, evaluated_ = false;
+  std::int64_t p_sr_ = 0, p_lr_ = 0, last_active_ = 0;
+
+  struct Buffer {
+    void *p = nullptr;
+    std::size_t bytes = 0;
+  };
+  std::vector<Buffer *> buffers_;
+  Buffer *buf(const char *name);
+  template <class T> T *ensure(Buffer *b, std::size_t count);
+  void release_all();
+
+  // node-sized device buffers (named members so the kernels' arguments read clearly)
+  Buffer *z_, *x0_, *img_of_node_, *img_off_, *img_q_;
+  Buffer *xs_, *evs_, *qkv_, *aev_, *n1_, *n1hat_, *n1is_, *hpre_, *tout_, *pre2hat_, *pre2is_;
+  Buffer *ainv_, *act_, *hid_, *pbuf_, *cat_;
+  Buffer *hhead_, *hkey_, *heff_, *eatom_, *qraw_, *q_, *hir_, *qseed_;
+  Buffer *elr_, *dq_, *dh_, *flr_, *vlr_, *elr_parts_, *ezbl_;
+  Buffer *gx_, *gev_, *gp_, *gt_, *gcat_, *ghid_, *gact_, *gainv_, *gaev_, *gqkv_, *ghead_;
+  Buffer *fout_, *etot_, *red_;
+  // pair-sized buffers
+  Buffer *owner_, *sr_rows_, *sr_nodes_, *sr_inc_off_, *sr_inc_, *lr_rows_, *lr_nodes_,
+      *lr_inc_off_, *lr_inc_, *blk_count_, *n_active_, *cand2act_;
+  Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
+  Buffer *df_, *dfc_, *ds_, *dr_, *dY_, *pg_;
+  Buffer *xrows_, *fhost_;
+  double totals_[2] = {0.0, 0.0};
+  struct Timing {
+    double ms = 0;
+    std::int64_t launches = 0, units = 0;
+  };
+  bool timing_ = false;
+  std::map<std::string, Timing> timings_;
+  double *last_etot_ = nullptr;
+};
+
+}  // namespace so3lr_amd

@@ -1,0 +1,132 @@
+"""HIP path vs the CPU oracle, through the C ABI (libso3lr_hip.so).
+
+Tolerances are the ones BASELINE.json states for this path: energies within
+1e-10 relative, forces and virial within 1e-9 eV/A (virial components in eV,
+compared at 1e-9 relative to their scale).  The oracle's graph is built by
+brute force with the minimum-image convention (tests/support.py), the HIP
+path's by the LAMMPS stand-in (ghost rows, full SR + half LR lists with a
+1 A skin), so the neighbour handling is checked too.
+"""
+import numpy as np
+import pytest
+
+import support
+from oracle.oracle import Oracle
+
+pytestmark = pytest.mark.gpu
+
+MOLECULES = ["o2", "h2o_cation", "methyl", "methylammonium", "acetate", "alanine_cation", "alanine"]
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return Oracle(support.MODEL)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from so3lrxlammps_amd import Context
+    return Context(support.MODEL, 0)
+
+
+def _hip_single_point(ctx, z, pos, box, charge, mult):
+    from so3lrxlammps_amd import Lists
+    ctx.set_system(z, charge, mult)
+    if box is None:
+        lo, hi, per = pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0)
+    else:
+        lo, hi, per = np.zeros(3), box, (1, 1, 1)
+    lists = Lists(pos, lo, hi, per)
+    ctx.set_topology(lists)
+    e, f, ea, w = ctx.compute(lists.rows_positions(pos))
+    return e, f, ea, w, ctx.terms()
+
+
+def _check(out, e, f, ea, w, terms, ftol=1e-9):
+    assert abs(e - out["energy"]) <= 1e-10 * abs(out["energy"]), (e, out["energy"])
+    assert np.abs(f - out["forces"]).max() <= ftol
+    wscale = max(1.0, np.abs(out["virial"]).max())
+    assert np.abs(w - out["virial"]).max() <= 1e-9 * wscale
+    assert np.abs(ea - out["eatom"]).max() <= 1e-10 * max(1.0, np.abs(out["eatom"]).max())
+    assert np.abs(terms["charges"] - out["charges"]).max() <= 1e-12
+    assert np.abs(terms["hirshfeld"] - out["hirshfeld"]).max() <= 1e-12
+    assert np.abs(terms["learned"] - out["e_learned"]).max() <= 1e-9
+    assert np.abs(terms["zbl"] - out["e_zbl"]).max() <= 1e-11
+    assert np.abs(terms["long_range"] - out["e_lr"]).max() <= 1e-11
+
+
+@pytest.mark.parametrize("name", MOLECULES)
+def test_molecule_matches_oracle(ctx, orc, name):
+    ref, z, pos, box = support.load_golden(name)
+    q, m = ref.get("charge", 0), ref.get("multiplicity", 1)
+    print("case", name, flush=True)
+    e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, q, m)
+    sr, lr = support.build_graphs(pos, box)
+    out = orc.evaluate(z, sr, lr, charge=q, multiplicity=m)
+    _check(out, e, f, ea, w, terms)
+
+
+def test_molecule_matches_golden_reference(ctx):
+    """The HIP path against the reference's JAX vectors directly (float64 refs)."""
+    for name in ["acetate", "alanine_cation", "methylammonium"]:
+        ref, z, pos, box = support.load_golden(name)
+        e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, ref["charge"], ref["multiplicity"])
+        assert np.abs(f - np.asarray(ref["forces"])).max() <= 3e-10
+        assert abs(e - ref["energy_native_convention"]) <= 1e-11 * abs(ref["energy_native_convention"])
+
+
+def test_water3000_periodic(ctx, orc):
+    ref, z, pos, box = support.load_golden("water3000")
+    print("case water3000", flush=True)
+    e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, 0, 1)
+    sr, lr = support.build_graphs(pos, box)
+    out = orc.evaluate(z, sr, lr)
+    _check(out, e, f, ea, w, terms)
+    # the reference's own float32-parameter floor against JAX
+    assert np.abs(f - np.asarray(ref["forces"])).max() <= 3e-6
+
+
+def test_deterministic_bitwise(ctx):
+    ref, z, pos, box = support.load_golden("alanine_cation")
+    a = _hip_single_point(ctx, z, pos, box, 1, 2)
+    b = _hip_single_point(ctx, z, pos, box, 1, 2)
+    assert a[0] == b[0]
+    assert np.array_equal(a[1], b[1])
+    assert np.array_equal(a[3], b[3])
+
+
+def test_packed_images_match_oracle(orc):
+    from so3lrxlammps_amd import Context, Lists
+    names = [("acetate", -1, 1), ("methyl", 0, 2), ("h2o_cation", 1, 2), ("alanine", 0, 1)]
+    zs, ps, qs, ms, offs = [], [], [], [], [0]
+    for k, (name, q, m) in enumerate(names):
+        ref, z, pos, box = support.load_golden(name)
+        zs.append(z); ps.append(pos + np.array([40.0 * k, 0, 0])); qs.append(q); ms.append(m)
+        offs.append(offs[-1] + len(z))
+    z = np.concatenate(zs); pos = np.concatenate(ps)
+    c = Context(support.MODEL, 0)
+    c.set_images(z, offs, qs, ms)
+    lists = Lists(pos, pos.min(0) - 20, pos.max(0) + 20, (0, 0, 0))
+    c.set_topology(lists)
+    e, f, ea, w = c.compute(lists.rows_positions(pos))
+    t = c.terms()
+    img = np.repeat(np.arange(len(names)), np.diff(offs))
+    sr, lr = support.build_graphs(pos, None)
+    out = orc.evaluate(z, sr, lr, image=img, image_charge=np.array(qs, float), image_multiplicity=ms)
+    assert np.abs(f - out["forces"]).max() <= 1e-9
+    assert np.abs(t["image_energy"] - out["image_energy"]).max() <= 1e-10 * np.abs(out["image_energy"]).max()
+    for k in range(len(names)):
+        assert abs(t["charges"][offs[k]:offs[k + 1]].sum() - qs[k]) < 1e-12
+
+
+def test_refusals(ctx):
+    from so3lrxlammps_amd import _lib
+    ref, z, pos, box = support.load_golden("o2")
+    e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, 0, 3)
+    x = np.zeros(6)
+    fbuf = np.zeros(6)
+    rc = ctx.raw_compute(_lib.ptr(x), _lib.VATOM, _lib.ptr(fbuf), None, None, None)
+    assert rc == _lib.ERR_UNSUPPORTED
+    with pytest.raises(_lib.SO3LRError) as err:
+        ctx.set_system(z, 0, 2)  # O2 has 16 electrons: an even count needs an odd multiplicity
+    assert err.value.code == _lib.ERR_SYSTEM
