@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 
@@ -369,6 +370,249 @@ __global__ __launch_bounds__(128) void k_filter_bwd(const int *n_active, const d
       for (int k = 0; k < kR; ++k)
         grad += drbf[k] * rbf[k] * (-A.gamma * A.rbf_k[k] + A.gamma * A.rbf_kr[k] * xb / (1.0 - xb));
     dr[p] += grad;
+  }
+}
+
+
+// ---------------------------------------------------------------- MFMA filters
+// fp64 MFMA V_MFMA_F64_16X16X4F64: D(16x16) += A(16x4) B(4x16) with
+//   A[i][k] in lane i + 16k, B[k][j] in lane j + 16k,
+//   D[i][j] in lane j + 16 (i % 4), register i / 4          (probed on gfx950).
+// The filters run transposed: rows = features, columns = 16 pairs per
+// wavefront.  A D tile then holds, in lane group g = lane / 16 and register r,
+// feature 16 T + g + 4 r of pair lane % 16.  Taking the K index of the next
+// layer in the same order (k = 16 T + g + 4 v) makes every layer's B operand
+// the previous layer's D register, so activations never leave registers.
+// Weights are pre-permuted on the host into that operand order, four K values
+// per lane contiguous (permute_mfma).
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4d mfma(double a, double b, v4d c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4d wload(const double *P, int KT, int mt, int T, int lane) {
+  return reinterpret_cast<const v4d *>(P)[(mt * KT + T) * 64 + lane];
+}
+
+struct FilterMfma {
+  const double *w0p[2], *b0[2], *w1p[2], *b1[2], *e0p[2], *eb0[2], *e1p[2], *eb1[2];
+  const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];
+  const double *att_cg;
+  const double *rbf_b, *rbf_k, *rbf_kr;
+  double gamma;
+};
+
+// Bernstein basis of pair distance r at channels 16 T + g + 4 v (T < 2, v < 4).
+__device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, double *rb, double &xb) {
+  double x = exp(-A.gamma * r);
+  x = x < 1e-6 ? 1e-6 : (x > 1.0 - 1e-6 ? 1.0 - 1e-6 : x);
+  xb = x;
+  const double lx = log(x), l1x = log(1.0 - x);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
+    rb[t] = exp(A.rbf_b[ch] + A.rbf_k[ch] * lx + A.rbf_kr[ch] * l1x);
+  }
+}
+
+// 16 pairs per wavefront, 4 wavefronts per block.
+__global__ __launch_bounds__(256) void k_filter_fwd_mfma(const int *n_active, const int *pa, const double *pr,
+                                                         const double *ev, FilterMfma A, double *ps, double *pf) {
+  const int nact = *n_active;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int p = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + j;
+  if ((blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 >= nact) return;  // whole wavefront idle
+  const bool valid = p < nact;
+  const int pp = valid ? p : nact - 1;
+  double rb[8], xb;
+  rbf8(pr[pp], g, A, rb, xb);
+  // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
+  double sg = 0.0;
+  {
+    const int a = pa[2 * pp], b = pa[2 * pp + 1];
+    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
+    const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
+    for (int m = lo; m < hi; ++m) {
+      const double d = ev[std::size_t(a) * kE + m] - ev[std::size_t(b) * kE + m];
+      sg += d * d * A.att_cg[m];
+    }
+    if (valid) ps[4 * std::size_t(p) + g] = sg;
+  }
+  for (int which = 0; which < 2; ++which) {
+    v4d h[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) h[mt] = v4d{0, 0, 0, 0};
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const v4d w = wload(A.w0p[which], 2, mt, T, lane);
+        h[mt] = mfma(w[0], rb[4 * T + 0], h[mt]);
+        h[mt] = mfma(w[1], rb[4 * T + 1], h[mt]);
+        h[mt] = mfma(w[2], rb[4 * T + 2], h[mt]);
+        h[mt] = mfma(w[3], rb[4 * T + 3], h[mt]);
+      }
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) h[mt][r] = silu(h[mt][r] + A.b0[which][16 * mt + g + 4 * r]);
+    v4d o[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o[mt] = v4d{0, 0, 0, 0};
+#pragma unroll
+    for (int T = 0; T < 8; ++T)
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const v4d w = wload(A.w1p[which], 8, mt, T, lane);
+        o[mt] = mfma(w[0], h[T][0], o[mt]);
+        o[mt] = mfma(w[1], h[T][1], o[mt]);
+        o[mt] = mfma(w[2], h[T][2], o[mt]);
+        o[mt] = mfma(w[3], h[T][3], o[mt]);
+      }
+    // spherical branch: 4 -> 32 (silu) -> 128, added to the radial branch
+    v4d h2[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      h2[mt] = mfma(A.e0p[which][mt * 64 + lane], sg, v4d{0, 0, 0, 0});
+#pragma unroll
+      for (int r = 0; r < 4; ++r) h2[mt][r] = silu(h2[mt][r] + A.eb0[which][16 * mt + g + 4 * r]);
+    }
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const v4d w = wload(A.e1p[which], 2, mt, T, lane);
+        o[mt] = mfma(w[0], h2[T][0], o[mt]);
+        o[mt] = mfma(w[1], h2[T][1], o[mt]);
+        o[mt] = mfma(w[2], h2[T][2], o[mt]);
+        o[mt] = mfma(w[3], h2[T][3], o[mt]);
+      }
+    if (valid) {
+      double *dst = pf + 256 * std::size_t(p) + which * kF;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = 16 * mt + g + 4 * r;
+          dst[c] = o[mt][r] + A.b1[which][c] + A.eb1[which][c];
+        }
+    }
+  }
+}
+
+// Reverse of both filters, the Bernstein basis and the cutoff for 16 pairs per
+// wavefront: recompute the layer-0 pre-activations, d hidden = W1^T df (.)
+// silu', d rbf = W0^T d hidden, the same for the spherical branch down to ds,
+// and dE/dr.
+__global__ __launch_bounds__(256) void k_filter_bwd_mfma(const int *n_active, const double *pr, const double *ps,
+                                                         const double *df, const double *dfc, FilterMfma A, double rc,
+                                                         double *ds, double *dr) {
+  const int nact = *n_active;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int p = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + j;
+  if ((blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 >= nact) return;
+  const bool valid = p < nact;
+  const int pp = valid ? p : nact - 1;
+  const double r = pr[pp];
+  double rb[8], xb;
+  rbf8(r, g, A, rb, xb);
+  const double sg = ps[4 * std::size_t(pp) + g];
+  v4d drb[2] = {v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}};
+  v4d dsa = v4d{0, 0, 0, 0};
+  for (int which = 0; which < 2; ++which) {
+    const double *gf = df + 256 * std::size_t(pp) + which * kF;
+    v4d pre[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) pre[mt] = v4d{0, 0, 0, 0};
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const v4d w = wload(A.w0p[which], 2, mt, T, lane);
+        pre[mt] = mfma(w[0], rb[4 * T + 0], pre[mt]);
+        pre[mt] = mfma(w[1], rb[4 * T + 1], pre[mt]);
+        pre[mt] = mfma(w[2], rb[4 * T + 2], pre[mt]);
+        pre[mt] = mfma(w[3], rb[4 * T + 3], pre[mt]);
+      }
+    v4d pre2[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) pre2[mt] = mfma(A.e0p[which][mt * 64 + lane], sg, v4d{0, 0, 0, 0});
+    v4d dh[8], dh2[2];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) dh[mt] = v4d{0, 0, 0, 0};
+    dh2[0] = v4d{0, 0, 0, 0};
+    dh2[1] = v4d{0, 0, 0, 0};
+#pragma unroll
+    for (int T = 0; T < 8; ++T) {
+      double b[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) b[v] = gf[16 * T + g + 4 * v];
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const v4d w = wload(A.w1tp[which], 8, mt, T, lane);
+        dh[mt] = mfma(w[0], b[0], dh[mt]);
+        dh[mt] = mfma(w[1], b[1], dh[mt]);
+        dh[mt] = mfma(w[2], b[2], dh[mt]);
+        dh[mt] = mfma(w[3], b[3], dh[mt]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const v4d w = wload(A.e1tp[which], 8, mt, T, lane);
+        dh2[mt] = mfma(w[0], b[0], dh2[mt]);
+        dh2[mt] = mfma(w[1], b[1], dh2[mt]);
+        dh2[mt] = mfma(w[2], b[2], dh2[mt]);
+        dh2[mt] = mfma(w[3], b[3], dh2[mt]);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dh[mt][q] *= silu_prime(pre[mt][q] + A.b0[which][16 * mt + g + 4 * q]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime(pre2[mt][q] + A.eb0[which][16 * mt + g + 4 * q]);
+#pragma unroll
+    for (int T = 0; T < 8; ++T)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const v4d w = wload(A.w0tp[which], 8, mt, T, lane);
+        drb[mt] = mfma(w[0], dh[T][0], drb[mt]);
+        drb[mt] = mfma(w[1], dh[T][1], drb[mt]);
+        drb[mt] = mfma(w[2], dh[T][2], drb[mt]);
+        drb[mt] = mfma(w[3], dh[T][3], drb[mt]);
+      }
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      const v4d w = wload(A.e0tp[which], 2, 0, T, lane);
+      dsa = mfma(w[0], dh2[T][0], dsa);
+      dsa = mfma(w[1], dh2[T][1], dsa);
+      dsa = mfma(w[2], dh2[T][2], dsa);
+      dsa = mfma(w[3], dh2[T][3], dsa);
+    }
+  }
+  // dE/dr: Bernstein derivative (zero where the clamp is active) + cutoff
+  double part = 0.0;
+  if (xb > 1e-6 && xb < 1.0 - 1e-6) {
+    const double q = A.gamma * xb / (1.0 - xb);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
+      part += drb[t >> 2][t & 3] * rb[t] * (-A.gamma * A.rbf_k[ch] + A.rbf_kr[ch] * q);
+    }
+  }
+  part += __shfl_xor(part, 16, kWave);
+  part += __shfl_xor(part, 32, kWave);
+  if (valid) {
+    ds[4 * std::size_t(p) + g] = dsa[0];  // rows 0..3 of the padded tile: lane group g, register 0
+    if (g == 0) {
+      double grad = part;
+      if (r < rc) {
+        const double t = r / rc;
+        grad += dfc[p] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
+      }
+      dr[p] += grad;
+    }
   }
 }
 
@@ -934,6 +1178,34 @@ std::vector<double> transpose(const std::vector<double> &w, std::size_t rows, st
     for (std::size_t c = 0; c < cols; ++c) t[c * rows + r] = w[r * cols + c];
   return t;
 }
+
+// MFMA A-operand order of an (M x K) row-major matrix used as D = W X^T:
+// P[mt][T][lane][v] = W[16 mt + lane % 16][16 T + lane / 16 + 4 v] (K a
+// multiple of 16), or P[mt][lane] = W[16 mt + lane % 16][lane / 16] for K = 4.
+// Rows beyond M (padding to a multiple of 16) are zero.
+std::vector<double> permute_mfma(const std::vector<double> &w, std::size_t M, std::size_t K) {
+  const std::size_t MT = (M + 15) / 16;
+  if (K == 4) {
+    std::vector<double> p(MT * 64, 0.0);
+    for (std::size_t mt = 0; mt < MT; ++mt)
+      for (std::size_t lane = 0; lane < 64; ++lane) {
+        const std::size_t row = 16 * mt + lane % 16;
+        if (row < M) p[mt * 64 + lane] = w[row * K + lane / 16];
+      }
+    return p;
+  }
+  if (K % 16 != 0) throw std::logic_error("permute_mfma: K must be 4 or a multiple of 16");
+  const std::size_t KT = K / 16;
+  std::vector<double> p(MT * KT * 64 * 4, 0.0);
+  for (std::size_t mt = 0; mt < MT; ++mt)
+    for (std::size_t T = 0; T < KT; ++T)
+      for (std::size_t lane = 0; lane < 64; ++lane)
+        for (std::size_t v = 0; v < 4; ++v) {
+          const std::size_t row = 16 * mt + lane % 16, col = 16 * T + lane / 16 + 4 * v;
+          if (row < M) p[((mt * KT + T) * 64 + lane) * 4 + v] = w[row * K + col];
+        }
+  return p;
+}
 }  // namespace
 
 Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::move(model)), device_(device) {
@@ -942,6 +1214,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   if (device < 0 || device >= count) throw std::runtime_error("SO3LR: HIP device index out of range");
   HIP_CHECK(hipSetDevice(device));
   HIP_CHECK(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking));
+  if (const char *nv = std::getenv("SO3LR_NAIVE_FILTERS")) naive_filters_ = nv[0] == '1';
   stream_ = own_stream_;
   const Model &m = *model_;
   const Architecture &a = m.arch();
@@ -985,6 +1258,16 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
       B.fe1[k] = up(e1);
       B.fe1t[k] = up(transpose(e1, F, FH));
       B.feb1[k] = up(m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F}));
+      const auto w0 = m.f64(f + "mlp_rbf.0.weight", {F, R});
+      const auto e0 = m.f64(f + "mlp_ev.0.weight", {FH, 4});
+      B.w0p[k] = up(permute_mfma(w0, F, R));
+      B.w1p[k] = up(permute_mfma(w1, F, F));
+      B.e0p[k] = up(permute_mfma(e0, FH, 4));
+      B.e1p[k] = up(permute_mfma(e1, F, FH));
+      B.w1tp[k] = up(permute_mfma(transpose(w1, F, F), F, F));
+      B.w0tp[k] = up(permute_mfma(transpose(w0, F, R), R, F));
+      B.e1tp[k] = up(permute_mfma(transpose(e1, F, FH), FH, F));
+      B.e0tp[k] = up(permute_mfma(transpose(e0, FH, 4), 4, FH));
     }
     B.att_cg = up(m.f64(at + "so3_conv_invariants.cg_rep", {24}));
     B.int_cg = up(m.f64(p + "interaction_block.so3_conv_invariants.cg_rep", {24}));
@@ -1341,6 +1624,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   fill(evs, Nz * kE);
   const double inv_avg = 1.0 / avg_;
   const unsigned gP = unsigned(std::max<std::int64_t>(P, 1));
+  const unsigned gP64 = unsigned(std::max(1, ceil_div(P, 64)));  // 64 pairs per MFMA block
 
   // --- interaction blocks, forward ---
   for (int b = 0; b < L; ++b) {
@@ -1358,8 +1642,18 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     hipLaunchKernelGGL(k_qkv, dim3(ceil_div(N, 16)), dim3(128), 0, s, int(N), xb, B.wqkv, qb);
+    FilterMfma FM;
+    for (int k = 0; k < 2; ++k) {
+      FM.w0p[k] = B.w0p[k]; FM.b0[k] = B.fb0[k]; FM.w1p[k] = B.w1p[k]; FM.b1[k] = B.fb1[k];
+      FM.e0p[k] = B.e0p[k]; FM.eb0[k] = B.feb0[k]; FM.e1p[k] = B.e1p[k]; FM.eb1[k] = B.feb1[k];
+      FM.w1tp[k] = B.w1tp[k]; FM.w0tp[k] = B.w0tp[k]; FM.e1tp[k] = B.e1tp[k]; FM.e0tp[k] = B.e0tp[k];
+    }
+    FM.att_cg = B.att_cg; FM.rbf_b = hw_.rbf_b; FM.rbf_k = hw_.rbf_k; FM.rbf_kr = hw_.rbf_kr; FM.gamma = gamma_;
     timed("filter_fwd", 0, [&] {
-      hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
+      if (naive_filters_)
+        hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
+      else
+        hipLaunchKernelGGL(k_filter_fwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, FM, psb, pfb);
     });
     timed("attn_fwd", 1, [&] {
       hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, xb, evb, qb,
@@ -1418,8 +1712,18 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       hipLaunchKernelGGL(k_attn_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, qb, pfb, pY, pfc,
                          pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
     });
+    FilterMfma FM;
+    for (int k = 0; k < 2; ++k) {
+      FM.w0p[k] = B.w0p[k]; FM.b0[k] = B.fb0[k]; FM.w1p[k] = B.w1p[k]; FM.b1[k] = B.fb1[k];
+      FM.e0p[k] = B.e0p[k]; FM.eb0[k] = B.feb0[k]; FM.e1p[k] = B.e1p[k]; FM.eb1[k] = B.feb1[k];
+      FM.w1tp[k] = B.w1tp[k]; FM.w0tp[k] = B.w0tp[k]; FM.e1tp[k] = B.e1tp[k]; FM.e0tp[k] = B.e0tp[k];
+    }
+    FM.att_cg = B.att_cg; FM.rbf_b = hw_.rbf_b; FM.rbf_k = hw_.rbf_k; FM.rbf_kr = hw_.rbf_kr; FM.gamma = gamma_;
     timed("filter_bwd", 0, [&] {
-      hipLaunchKernelGGL(k_filter_bwd, dim3(gP), dim3(128), 0, s, nact, pr, pfc, psb, df, dfc, A, rc_, ds, dr);
+      if (naive_filters_)
+        hipLaunchKernelGGL(k_filter_bwd, dim3(gP), dim3(128), 0, s, nact, pr, pfc, psb, df, dfc, A, rc_, ds, dr);
+      else
+        hipLaunchKernelGGL(k_filter_bwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds, dr);
     });
     hipLaunchKernelGGL(k_qkv_bwd, dim3(ceil_div(N, 8)), dim3(128), 0, s, int(N), gqkv, B.wqkv, gainv, gx);
     hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, evb, B.att_cg, ds,

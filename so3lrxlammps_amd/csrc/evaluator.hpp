@@ -38,6 +38,9 @@ struct BlockWeights {
   const double *m1t, *m1b, *m2t, *m2b;  // MLP weights transposed (in, out)
   const double *m1w, *m2w;              // (out, in) for the reverse
   const double *intt, *intb, *intw;     // interaction (132x132): transposed and (out, in)
+  // MFMA operand order of the filter weights (see permute_mfma in evaluator.hip)
+  const double *w0p[2], *w1p[2], *e0p[2], *e1p[2];     // forward
+  const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];  // reverse (transposes)
 };
 
 struct HeadWeights {
@@ -136,6 +139,7 @@ class Evaluator {
     std::int64_t launches = 0, units = 0;
   };
   bool timing_ = false;
+  bool naive_filters_ = false;  // SO3LR_NAIVE_FILTERS=1: scalar filter kernels (cross-check)
   std::map<std::string, Timing> timings_;
   double *last_etot_ = nullptr;
 };
