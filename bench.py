@@ -6,8 +6,8 @@ One step = velocity Verlet with a Berendsen thermostat at 300 K (0.5 fs),
 ghost-row update, neighbour-list rebuild when an atom moved more than half the
 1 A skin (LAMMPS `neigh_modify every 1 delay 0 check yes`), and one
 so3lr_compute_device call.  Positions, velocities and forces stay in HBM
-(torch tensors as plumbing); the rebuild runs the host LAMMPS stand-in and
-uploads the new lists, as the reference re-uploads its candidate graph.
+(torch tensors as plumbing); the rebuild wraps the positions and builds the
+candidate lists on the GPU (so3lr_reneighbor_device).
 
 Prints one JSON line (the driver's contract), with the dominant kernel's
 roofline from HIP events recorded on its launch stream, and the CPU oracle
@@ -103,25 +103,16 @@ def main():
     state = {"builds": 0, "build_s": 0.0}
 
     def rebuild():
+        # HBM-resident reneighbor: wraps xt in place, builds the candidate
+        # lists on the GPU (no ghost rows, no host copies)
         t0 = time.time()
-        torch.cuda.synchronize()
-        xh = xt.cpu().numpy()
-        xh = np.mod(xh, box)
-        xh = np.where(xh >= box, 0.0, xh)
-        xt.copy_(torch.from_numpy(xh))
-        L = Lists(xh, lo, box, (1, 1, 1), 4.5, 12.0, skin, 13.0, sr_full=True)
-        ctx.set_topology(L)
-        state["owner"] = torch.tensor(L.owner, dtype=torch.long, device=dev)
-        state["shift"] = torch.tensor(L.image * box, dtype=torch.float64, device=dev)
+        ctx.reneighbor_device(xt, lo, box, (1, 1, 1), skin, stream=stream.cuda_stream)
         state["x_build"] = xt.clone()
-        state["xrows"] = torch.empty((L.rows, 3), dtype=torch.float64, device=dev)
         state["builds"] += 1
         state["build_s"] += time.time() - t0
 
     def force():
-        torch.index_select(xt, 0, state["owner"], out=state["xrows"])
-        state["xrows"].add_(state["shift"])
-        e, w = ctx.compute_device(state["xrows"], ft, stream=stream.cuda_stream)
+        e, w = ctx.compute_device(xt, ft, stream=stream.cuda_stream)
         return e, w
 
     rebuild()

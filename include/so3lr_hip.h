@@ -136,6 +136,22 @@ int so3lr_compute_device(so3lr_ctx *ctx, const double *x_rows_dev, int flags,
                          double *f_owned_dev, double *eatom_dev, double *energy,
                          double *virial);
 
+/*
+ * HBM-resident reneighbor (no counterpart in the reference, where LAMMPS
+ * builds the lists on the host): builds the same candidate sets -- every
+ * periodic image within cutoff + skin, SR and LR -- on the GPU from the owned
+ * positions x_owned_dev (n_owned*3, device), after wrapping them in place into
+ * the orthogonal box [lo, hi) along periodic axes (LAMMPS Domain::pbc).  Every
+ * periodic length must exceed twice the long-range cutoff.  Afterwards
+ * so3lr_compute_device takes owned positions (x_rows_dev = x_owned_dev, no
+ * ghost rows) until the next so3lr_set_topology.
+ */
+int so3lr_reneighbor_device(so3lr_ctx *ctx, double *x_owned_dev, const double *lo,
+                            const double *hi, const int *periodic, double skin);
+
+/* Box of the device reneighbor path between rebuilds (NPT); same axes. */
+int so3lr_set_box(so3lr_ctx *ctx, const double *lo, const double *hi);
+
 /* Order all device work on `stream` (a hipStream_t; NULL = the context's own
  * stream).  The stream must have default priority. */
 int so3lr_set_stream(so3lr_ctx *ctx, void *stream);

@@ -21,6 +21,7 @@ LIST_FULL, LIST_HALF = 0, 1
 HIP_SYMBOLS = ["so3lr_create", "so3lr_destroy", "so3lr_last_error", "so3lr_cutoff",
                "so3lr_atomic_number", "so3lr_set_system", "so3lr_set_images",
                "so3lr_set_topology", "so3lr_compute", "so3lr_compute_device",
+               "so3lr_reneighbor_device", "so3lr_set_box",
                "so3lr_set_stream", "so3lr_last_terms", "so3lr_graph_stats",
                "so3lr_kernel_timing", "so3lr_kernel_timing_read", "so3lr_device_bytes"]
 EMU_SYMBOLS = ["so3lr_emu_build", "so3lr_emu_error", "so3lr_emu_free", "so3lr_emu_rows",
@@ -48,9 +49,24 @@ _hip = None
 _emu = None
 
 
+def _bind_one_hip_runtime():
+    """Load torch's HIP runtime first when torch is installed.
+
+    torch ships its own libamdhip64 (SONAME libamdhip64.so.7) and reaches it by
+    file name; libso3lr_hip.so needs libamdhip64.so.7.  Loaded after torch, the
+    library binds to torch's already-loaded runtime; loaded before it, torch
+    would bring a second HIP runtime into the process and fail to initialise.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def hip():
     global _hip
     if _hip is None:
+        _bind_one_hip_runtime()
         lib = _load(HIP_LIB, "libso3lr_hip")
         lib.so3lr_create.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_P)]
         lib.so3lr_destroy.argtypes = [_P]
@@ -66,6 +82,8 @@ def hip():
         lib.so3lr_compute.argtypes = [_P, _P, ctypes.c_int, _P, _P, _P, _P]
         lib.so3lr_compute_device.argtypes = [_P, _P, ctypes.c_int, _P, _P, _P, _P]
         lib.so3lr_set_stream.argtypes = [_P, _P]
+        lib.so3lr_reneighbor_device.argtypes = [_P, _P, _P, _P, _P, _D]
+        lib.so3lr_set_box.argtypes = [_P, _P, _P]
         lib.so3lr_last_terms.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P]
         lib.so3lr_graph_stats.argtypes = [_P, _P, _P, _P]
         lib.so3lr_kernel_timing.argtypes = [_P, ctypes.c_int]
@@ -220,6 +238,21 @@ class Context:
         self._check(self._lib.so3lr_compute_device(self._h, ptr(x_rows_dev), flags, ptr(f_dev),
                                                    ptr(eatom_dev), ctypes.byref(e), ptr(w)))
         return e.value, w
+
+    def reneighbor_device(self, x_owned_dev, lo, hi, periodic, skin, stream=None):
+        """Device reneighbor; wraps x_owned_dev in place into [lo, hi)."""
+        if stream is not None:
+            self._check(self._lib.so3lr_set_stream(self._h, ctypes.c_void_p(stream)))
+        lo = np.ascontiguousarray(lo, dtype=np.float64)
+        hi = np.ascontiguousarray(hi, dtype=np.float64)
+        per = np.ascontiguousarray(periodic, dtype=np.int32)
+        self._check(self._lib.so3lr_reneighbor_device(self._h, ptr(x_owned_dev), ptr(lo), ptr(hi), ptr(per),
+                                                      float(skin)))
+
+    def set_box(self, lo, hi):
+        lo = np.ascontiguousarray(lo, dtype=np.float64)
+        hi = np.ascontiguousarray(hi, dtype=np.float64)
+        self._check(self._lib.so3lr_set_box(self._h, ptr(lo), ptr(hi)))
 
     def raw_compute(self, x_rows, flags, f, eatom, energy, virial):
         return self._lib.so3lr_compute(self._h, x_rows, flags, f, eatom, energy, virial)

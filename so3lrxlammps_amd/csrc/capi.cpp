@@ -167,6 +167,22 @@ int so3lr_compute_device(so3lr_ctx *ctx, const double *x_rows_dev, int flags, do
   });
 }
 
+int so3lr_reneighbor_device(so3lr_ctx *ctx, double *x_owned_dev, const double *lo, const double *hi,
+                            const int *periodic, double skin) {
+  return guarded(ctx, [&] {
+    if (!x_owned_dev || !lo || !hi || !periodic || !(skin >= 0.0))
+      throw std::invalid_argument("SO3LR: invalid device reneighbor arguments");
+    ctx->ev->build_topology_device(x_owned_dev, lo, hi, periodic, skin);
+  });
+}
+
+int so3lr_set_box(so3lr_ctx *ctx, const double *lo, const double *hi) {
+  return guarded(ctx, [&] {
+    if (!lo || !hi) throw std::invalid_argument("SO3LR: null box");
+    ctx->ev->set_box(lo, hi);
+  });
+}
+
 int so3lr_set_stream(so3lr_ctx *ctx, void *stream) {
   return guarded(ctx, [&] { ctx->ev->set_stream(static_cast<hipStream_t>(stream)); });
 }

@@ -58,25 +58,48 @@ __global__ void k_fill(double *p, std::size_t n, double v) {
 // ---------------------------------------------------------------- compaction
 // Active short-range pairs are those with 0 < r^2 < rc^2, kept in candidate
 // order (pair_so3lr_native_mpi.cpp:258-291,306-373 count + stable scan).
-__device__ __forceinline__ bool sr_active(const int *rows, const double *x, int c, double rc2,
-                                          double &dx, double &dy, double &dz) {
-  const int ra = rows[2 * c], rb = rows[2 * c + 1];
-  dx = x[3 * ra] - x[3 * rb];
-  dy = x[3 * ra + 1] - x[3 * rb + 1];
-  dz = x[3 * ra + 2] - x[3 * rb + 2];
+// Pair vector v = x_a - x_b of candidate c: LAMMPS rows (ghost rows carry
+// the image displacement) or owned positions plus an image code (device
+// reneighbor path; code c stands for ((c/9)-1, (c/3)%3-1, c%3-1) box lengths
+// added to b).
+struct RowsPos {
+  const double *x;
+  const int *rows;
+  __device__ __forceinline__ void vec(int c, double &dx, double &dy, double &dz) const {
+    const int ra = rows[2 * c], rb = rows[2 * c + 1];
+    dx = x[3 * ra] - x[3 * rb];
+    dy = x[3 * ra + 1] - x[3 * rb + 1];
+    dz = x[3 * ra + 2] - x[3 * rb + 2];
+  }
+};
+struct ShiftPos {
+  const double *x;
+  const int *nodes, *codes;
+  double lx, ly, lz;
+  __device__ __forceinline__ void vec(int c, double &dx, double &dy, double &dz) const {
+    const int a = nodes[2 * c], b = nodes[2 * c + 1], code = codes[c];
+    dx = x[3 * a] - x[3 * b] - (code / 9 - 1) * lx;
+    dy = x[3 * a + 1] - x[3 * b + 1] - ((code / 3) % 3 - 1) * ly;
+    dz = x[3 * a + 2] - x[3 * b + 2] - (code % 3 - 1) * lz;
+  }
+};
+
+template <class Pos>
+__device__ __forceinline__ bool sr_active(const Pos &pos, int c, double rc2, double &dx, double &dy, double &dz) {
+  pos.vec(c, dx, dy, dz);
   const double r2 = dx * dx + dy * dy + dz * dz;
   return r2 > 0.0 && r2 < rc2;
 }
 
-__global__ __launch_bounds__(256) void k_sr_count(int P, const int *rows, const double *x, double rc2,
-                                                  int *blk_count) {
+template <class Pos>
+__global__ __launch_bounds__(256) void k_sr_count(int P, Pos pos, double rc2, int *blk_count) {
   __shared__ int part[256];
   const int base = blockIdx.x * kCompactPerBlock + threadIdx.x * 4;
   int cnt = 0;
   for (int j = 0; j < 4; ++j) {
     const int c = base + j;
     double dx, dy, dz;
-    if (c < P && sr_active(rows, x, c, rc2, dx, dy, dz)) ++cnt;
+    if (c < P && sr_active(pos, c, rc2, dx, dy, dz)) ++cnt;
   }
   part[threadIdx.x] = cnt;
   __syncthreads();
@@ -112,8 +135,9 @@ __global__ __launch_bounds__(1024) void k_scan_counts(int nblk, int *cnt, int *n
   if (threadIdx.x == 0) *n_active = carry;
 }
 
+template <class Pos>
 __global__ __launch_bounds__(256) void k_sr_compact(
-    int P, const int *rows, const int *nodes, const double *x, double rc2, const int *blk_off,
+    int P, Pos pos, const int *nodes, double rc2, const int *blk_off,
     const int *z, ZblParams zp, int *cand2act, int *pa, double *pv, double *pr, double *pY,
     double *pfc, double *pzbl) {
   __shared__ int part[256];
@@ -122,7 +146,7 @@ __global__ __launch_bounds__(256) void k_sr_compact(
   for (int j = 0; j < 4; ++j) {
     const int c = base + j;
     double dx, dy, dz;
-    if (c < P && sr_active(rows, x, c, rc2, dx, dy, dz)) { flags |= 1 << j; ++cnt; }
+    if (c < P && sr_active(pos, c, rc2, dx, dy, dz)) { flags |= 1 << j; ++cnt; }
   }
   part[threadIdx.x] = cnt;
   __syncthreads();
@@ -132,15 +156,15 @@ __global__ __launch_bounds__(256) void k_sr_compact(
     part[threadIdx.x] += t;
     __syncthreads();
   }
-  int pos = blk_off[blockIdx.x] + part[threadIdx.x] - cnt;
+  int at = blk_off[blockIdx.x] + part[threadIdx.x] - cnt;
   const double rc = sqrt(rc2);
   for (int j = 0; j < 4; ++j) {
     const int c = base + j;
     if (c >= P) break;
     if (!(flags & (1 << j))) { cand2act[c] = -1; continue; }
     double dx, dy, dz;
-    sr_active(rows, x, c, rc2, dx, dy, dz);
-    const int p = pos++;
+    sr_active(pos, c, rc2, dx, dy, dz);
+    const int p = at++;
     cand2act[c] = p;
     const int na = nodes[2 * c], nb = nodes[2 * c + 1];
     pa[2 * p] = na;
@@ -872,6 +896,55 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
   }
 }
 
+// LR over the full node-major list of the device reneighbor: entry j * 32 +
+// image code, neighbour position x_j + shift(code) * box.
+__global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, const int *inc, const double *x,
+                                                 double lx, double ly, double lz, const int *z, const double *q,
+                                                 const double *hir, LrParams P, const double *aref,
+                                                 const double *cref, double *elr, double *dq, double *dhv,
+                                                 double *flr, double *vlr, double *parts) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int zn = z[n];
+  const double qn = q[n], hn = hir[n];
+  const double xn = x[3 * n], yn = x[3 * n + 1], zn_ = x[3 * n + 2];
+  double e_el = 0, e_d = 0, sdq = 0, sdh = 0, f0 = 0, f1 = 0, f2 = 0;
+  double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
+  for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
+    const int e = inc[k];
+    const int o = e >> 5, code = e & 31;
+    const double dx = xn - x[3 * o] - (code / 9 - 1) * lx;
+    const double dy = yn - x[3 * o + 1] - ((code / 3) % 3 - 1) * ly;
+    const double dz = zn_ - x[3 * o + 2] - (code % 3 - 1) * lz;
+    const double r = sqrt(dx * dx + dy * dy + dz * dz);
+    LrPairTerms t;
+    if (!lr_pair_terms(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
+    e_el += 0.5 * t.e_el;
+    e_d += 0.5 * t.e_disp;
+    sdq += t.pref * q[o];
+    sdh += t.dh_self;
+    const double s = t.radial / r;
+    f0 -= s * dx; f1 -= s * dy; f2 -= s * dz;
+    w0 -= 0.5 * s * dx * dx; w1 -= 0.5 * s * dy * dy; w2 -= 0.5 * s * dz * dz;
+    w3 -= 0.5 * s * dx * dy; w4 -= 0.5 * s * dx * dz; w5 -= 0.5 * s * dy * dz;
+  }
+  e_el = wave_sum(e_el); e_d = wave_sum(e_d); sdq = wave_sum(sdq); sdh = wave_sum(sdh);
+  f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2);
+  w0 = wave_sum(w0); w1 = wave_sum(w1); w2 = wave_sum(w2);
+  w3 = wave_sum(w3); w4 = wave_sum(w4); w5 = wave_sum(w5);
+  if (lane == 0) {
+    elr[n] = e_el + e_d;
+    dq[n] = sdq;
+    dhv[n] = sdh;
+    flr[3 * n] = f0; flr[3 * n + 1] = f1; flr[3 * n + 2] = f2;
+    double *v = vlr + 6 * std::size_t(n);
+    v[0] = w0; v[1] = w1; v[2] = w2; v[3] = w3; v[4] = w4; v[5] = w5;
+    parts[2 * n] = e_el;
+    parts[2 * n + 1] = e_d;
+  }
+}
+
 // ---------------------------------------------------------------- block reverse
 // LN2 reverse, gate adjoint, start of the interaction reverse
 __global__ __launch_bounds__(256) void k_post2_bwd(int N, const double *gx, const double *gev, const double *t,
@@ -1141,20 +1214,6 @@ Evaluator::Buffer *Evaluator::buf(const char *) {
   return buffers_.back();
 }
 
-template <class T>
-T *Evaluator::ensure(Buffer *b, std::size_t count) {
-  const std::size_t need = std::max<std::size_t>(count, 1) * sizeof(T);
-  if (b->bytes < need) {
-    if (b->p) { HIP_CHECK(hipFree(b->p)); bytes_ -= b->bytes; }
-    b->p = nullptr;
-    const std::size_t cap = need + need / 8;  // retained capacity with slack
-    HIP_CHECK(hipMalloc(&b->p, cap));
-    b->bytes = cap;
-    bytes_ += cap;
-  }
-  return static_cast<T *>(b->p);
-}
-
 void Evaluator::release_all() {
   for (Buffer *b : buffers_) {
     if (b->p) (void)hipFree(b->p);
@@ -1359,6 +1418,18 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   ps_ = buf("ps"); pf_ = buf("pf"); palpha_ = buf("palpha"); df_ = buf("df"); dfc_ = buf("dfc");
   ds_ = buf("ds"); dr_ = buf("dr"); dY_ = buf("dY"); pg_ = buf("pg"); xrows_ = buf("xrows");
   fhost_ = buf("fhost");
+  nb_key_ = buf("nb_key"); nb_idx_ = buf("nb_idx"); nb_skey_ = buf("nb_skey"); nb_sidx_ = buf("nb_sidx");
+  nb_cstart_ = buf("nb_cstart"); nb_tmp_ = buf("nb_tmp"); nb_srcnt_ = buf("nb_srcnt"); nb_lrcnt_ = buf("nb_lrcnt");
+  nb_err_ = buf("nb_err"); nb_srlist_ = buf("nb_srlist"); nb_poff_ = buf("nb_poff"); sr_code_ = buf("sr_code");
+}
+
+void Evaluator::set_box(const double lo[3], const double hi[3]) {
+  if (!shift_mode_) throw std::logic_error("SO3LR: the box is set by the device reneighbor path only");
+  for (int d = 0; d < 3; ++d) {
+    const double l = hi[d] - lo[d];
+    if (!(l > 2.0 * lr_.cutoff)) throw std::invalid_argument("SO3LR: box shorter than twice the long-range cutoff");
+    box_len_[d] = l;
+  }
 }
 
 void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector<std::int64_t> &image_offsets,
@@ -1475,6 +1546,7 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
   p_sr_ = std::int64_t(sr_nodes.size() / 2);
   p_lr_ = std::int64_t(lr_nodes.size() / 2);
   n_rows_ = n_rows;
+  shift_mode_ = false;
   auto put = [&](Buffer *b, const std::vector<int> &v) {
     HIP_CHECK(hipMemcpyAsync(ensure<int>(b, v.size()), v.data(), v.size() * sizeof(int), hipMemcpyHostToDevice, stream_));
   };
@@ -1488,6 +1560,9 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
 void Evaluator::compute_host(const double *x_rows, int flags, double *f, double *eatom, double *energy,
                              double *virial) {
   if (!topology_ready_) throw std::logic_error("SO3LR: compute called before set_topology");
+  if (shift_mode_)
+    throw std::logic_error("SO3LR: the topology came from so3lr_reneighbor_device; call so3lr_compute_device "
+                           "with owned positions");
   double *xd = ensure<double>(xrows_, std::size_t(n_rows_) * 3);
   HIP_CHECK(hipMemcpyAsync(xd, x_rows, std::size_t(n_rows_) * 3 * sizeof(double), hipMemcpyHostToDevice, stream_));
   double *fd = ensure<double>(fhost_, std::size_t(n_) * 4);
@@ -1610,10 +1685,17 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
 
   // --- active short-range pairs, geometry, ZBL ---
   const double rc2 = rc_ * rc_;
-  if (P > 0) {
-    hipLaunchKernelGGL(k_sr_count, dim3(nblk), dim3(256), 0, s, int(P), sr_rows, x, rc2, blk);
+  if (P > 0 && !shift_mode_) {
+    const RowsPos pos{x, sr_rows};
+    hipLaunchKernelGGL(k_sr_count<RowsPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, rc2, blk);
     hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, blk, nact);
-    hipLaunchKernelGGL(k_sr_compact, dim3(nblk), dim3(256), 0, s, int(P), sr_rows, sr_nodes, x, rc2, blk, z,
+    hipLaunchKernelGGL(k_sr_compact<RowsPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, sr_nodes, rc2, blk, z,
+                       zbl_, c2a, pa, pv, pr, pY, pfc, pzbl);
+  } else if (P > 0) {
+    const ShiftPos pos{x, sr_nodes, static_cast<const int *>(sr_code_->p), box_len_[0], box_len_[1], box_len_[2]};
+    hipLaunchKernelGGL(k_sr_count<ShiftPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, rc2, blk);
+    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, blk, nact);
+    hipLaunchKernelGGL(k_sr_compact<ShiftPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, sr_nodes, rc2, blk, z,
                        zbl_, c2a, pa, pv, pr, pY, pfc, pzbl);
   } else {
     HIP_CHECK(hipMemsetAsync(nact, 0, sizeof(int), s));
@@ -1678,8 +1760,12 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, hkey, heff, hir);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
   timed("long_range", 1, [&] {
-    hipLaunchKernelGGL(k_lr, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x, z, q, hir,
-                       lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
+    if (shift_mode_)
+      hipLaunchKernelGGL(k_lr_full, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, x, box_len_[0], box_len_[1],
+                         box_len_[2], z, q, hir, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
+    else
+      hipLaunchKernelGGL(k_lr, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x, z, q, hir,
+                         lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
   });
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
   hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, H, ghead);

@@ -16,6 +16,7 @@
 #include <cstdint>
 #include <map>
 #include <memory>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -78,6 +79,12 @@ class Evaluator {
                     double *virial);
   void last_terms(double *learned, double *zbl, double *lr, double *charges, double *hirshfeld,
                   double *totals, double *image_energy);
+  // HBM-resident reneighbor from owned positions (wrapped in place); after it,
+  // compute_device takes owned positions.  Orthogonal box [lo, hi).
+  void build_topology_device(double *x_owned, const double lo[3], const double hi[3], const int per[3],
+                             double skin);
+  void set_box(const double lo[3], const double hi[3]);
+  bool shift_mode() const { return shift_mode_; }
   void set_stream(hipStream_t s) { stream_ = s ? s : own_stream_; }
   std::int64_t n_owned() const { return n_; }
   std::int64_t sr_active() const { return last_active_; }
@@ -116,7 +123,23 @@ class Evaluator {
   };
   std::vector<Buffer *> buffers_;
   Buffer *buf(const char *name);
-  template <class T> T *ensure(Buffer *b, std::size_t count);
+  template <class T>
+  T *ensure(Buffer *b, std::size_t count) {
+    const std::size_t need = (count ? count : 1) * sizeof(T);
+    if (b->bytes < need) {
+      if (b->p) {
+        if (hipFree(b->p) != hipSuccess) throw std::runtime_error("HIP error in hipFree");
+        bytes_ -= std::int64_t(b->bytes);
+      }
+      b->p = nullptr;
+      const std::size_t cap = need + need / 8;  // retained capacity with slack
+      if (hipMalloc(&b->p, cap) != hipSuccess)
+        throw std::runtime_error("HIP error in hipMalloc: out of device memory (" + std::to_string(cap) + " bytes)");
+      b->bytes = cap;
+      bytes_ += std::int64_t(cap);
+    }
+    return static_cast<T *>(b->p);
+  }
   void release_all();
 
   // node-sized device buffers (named members so the kernels' arguments read clearly)
@@ -133,6 +156,12 @@ class Evaluator {
   Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
   Buffer *df_, *dfc_, *ds_, *dr_, *dY_, *pg_;
   Buffer *xrows_, *fhost_;
+  // device reneighbor
+  Buffer *nb_key_, *nb_idx_, *nb_skey_, *nb_sidx_, *nb_cstart_, *nb_tmp_, *nb_srcnt_, *nb_lrcnt_, *nb_err_,
+      *nb_srlist_, *nb_poff_, *sr_code_;
+  bool shift_mode_ = false;
+  std::int64_t lr_entries_ = 0;
+  double box_len_[3] = {0, 0, 0};
   double totals_[2] = {0.0, 0.0};
   struct Timing {
     double ms = 0;

@@ -1,0 +1,298 @@
+// Device-side reneighbor for the HBM-resident path (no ghost rows).
+//
+// LAMMPS builds the reference's neighbour lists on the host and the pair
+// style re-uploads them at every reneighbor (pair_so3lr_native_mpi.cpp:
+// 1297-1334).  Here the same candidate sets -- every periodic image within
+// cutoff + skin -- are built on the GPU from owned positions in an orthogonal
+// box:
+//   1. wrap positions into the box (LAMMPS Domain::pbc) and bin atoms into
+//      cells of edge >= LR cutoff + skin (stable radix sort, deterministic);
+//   2. one wavefront per atom walks the 27 neighbouring cells (periodic
+//      wrap with an image code per cell) and emits, in a fixed order
+//      (ballot prefix inside each 64-atom chunk), its full SR and LR lists;
+//   3. the SR full list becomes the half-pair table (canonical direction:
+//      smaller atom index first) and its own incidence list, the reverse
+//      entry finding its pair by scanning its partner's list; the LR full
+//      list is used as it is by the node-major LR kernel.
+// Image code c in 0..26 stands for the shift ((c/9)-1, (c/3)%3-1, c%3-1)
+// box lengths added to the neighbour's position.
+#include "evaluator.hpp"
+
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <cmath>
+#include <stdexcept>
+
+namespace so3lr_amd {
+
+#define NB_CHECK(expr)                                                                    \
+  do {                                                                                    \
+    hipError_t err_ = (expr);                                                             \
+    if (err_ != hipSuccess)                                                               \
+      throw std::runtime_error(std::string("HIP error in ") + #expr + ": " +             \
+                               hipGetErrorString(err_));                                  \
+  } while (0)
+
+namespace {
+
+struct Grid {
+  double lo[3], len[3];
+  int nc[3];
+  int per[3];
+};
+
+__global__ void k_wrap(int n, double *x, Grid G) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  for (int d = 0; d < 3; ++d) {
+    if (!G.per[d]) continue;
+    double v = x[3 * i + d] - G.lo[d];
+    v -= floor(v / G.len[d]) * G.len[d];
+    if (v >= G.len[d]) v -= G.len[d];
+    if (v < 0.0) v = 0.0;
+    x[3 * i + d] = G.lo[d] + v;
+  }
+}
+
+__device__ __forceinline__ int cell_coord(double v, double lo, double len, int nc) {
+  int c = int(floor((v - lo) / len * nc));
+  return c < 0 ? 0 : (c >= nc ? nc - 1 : c);
+}
+
+__global__ void k_cell_keys(int n, const double *x, Grid G, int *key, int *idx) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int cx = cell_coord(x[3 * i], G.lo[0], G.len[0], G.nc[0]);
+  const int cy = cell_coord(x[3 * i + 1], G.lo[1], G.len[1], G.nc[1]);
+  const int cz = cell_coord(x[3 * i + 2], G.lo[2], G.len[2], G.nc[2]);
+  key[i] = (cx * G.nc[1] + cy) * G.nc[2] + cz;
+  idx[i] = i;
+}
+
+// cell_start[c] = first position of cell c in the sorted order
+__global__ void k_cell_start(int n, int ncell, const int *skey, int *start) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i > n) return;
+  const int prev = i == 0 ? -1 : skey[i - 1];
+  const int cur = i == n ? ncell : skey[i];
+  for (int c = prev + 1; c <= cur; ++c) start[c] = i;
+}
+
+// One wavefront per atom: count (FILL = false) or emit (FILL = true) every
+// neighbour within the SR and LR radii, in stencil-cell order.
+template <bool FILL>
+__global__ __launch_bounds__(256) void k_nbr(int n, const double *x, Grid G, const int *cstart, const int *sidx,
+                                             double sr2, double lr2, int *sr_cnt, int *lr_cnt,
+                                             const int *sr_off, const int *lr_off, int *sr_list, int *lr_list,
+                                             int *err) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const double xi = x[3 * i], yi = x[3 * i + 1], zi = x[3 * i + 2];
+  const int ci[3] = {cell_coord(xi, G.lo[0], G.len[0], G.nc[0]), cell_coord(yi, G.lo[1], G.len[1], G.nc[1]),
+                     cell_coord(zi, G.lo[2], G.len[2], G.nc[2])};
+  int ns = 0, nl = 0;
+  int ws = FILL ? sr_off[i] : 0, wl = FILL ? lr_off[i] : 0;
+  for (int s = 0; s < 27; ++s) {
+    const int o[3] = {s / 9 - 1, (s / 3) % 3 - 1, s % 3 - 1};
+    int c[3], img[3];
+    bool ok = true;
+    for (int d = 0; d < 3; ++d) {
+      int cc = ci[d] + o[d];
+      img[d] = 0;
+      if (cc < 0) { if (!G.per[d]) { ok = false; break; } cc += G.nc[d]; img[d] = -1; }
+      if (cc >= G.nc[d]) { if (!G.per[d]) { ok = false; break; } cc -= G.nc[d]; img[d] = 1; }
+      c[d] = cc;
+    }
+    if (!ok) continue;
+    // with fewer than 3 cells along a periodic axis two offsets reach the same
+    // cell with different images; both are kept (distinct images)
+    const int code = (img[0] + 1) * 9 + (img[1] + 1) * 3 + (img[2] + 1);
+    const double sx = img[0] * G.len[0], sy = img[1] * G.len[1], sz = img[2] * G.len[2];
+    const int cell = (c[0] * G.nc[1] + c[1]) * G.nc[2] + c[2];
+    for (int k0 = cstart[cell]; k0 < cstart[cell + 1]; k0 += 64) {
+      const int k = k0 + lane;
+      bool in_sr = false, in_lr = false;
+      int j = -1;
+      if (k < cstart[cell + 1]) {
+        j = sidx[k];
+        const double dx = x[3 * j] + sx - xi, dy = x[3 * j + 1] + sy - yi, dz = x[3 * j + 2] + sz - zi;
+        const double r2 = dx * dx + dy * dy + dz * dz;
+        if (j == i && code == 13) {
+          // the atom itself
+        } else {
+          in_lr = r2 < lr2;
+          in_sr = r2 < sr2;
+          if (j == i && in_lr && err) *err = 1;  // own periodic image inside the cutoff
+        }
+      }
+      const unsigned long long bs = __ballot(in_sr), bl = __ballot(in_lr);
+      const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+      if (FILL) {
+        if (in_sr) sr_list[ws + __popcll(bs & below)] = j * 32 + code;
+        if (in_lr) lr_list[wl + __popcll(bl & below)] = j * 32 + code;
+        ws += __popcll(bs);
+        wl += __popcll(bl);
+      } else {
+        ns += __popcll(bs);
+        nl += __popcll(bl);
+      }
+    }
+  }
+  if (!FILL && lane == 0) {
+    sr_cnt[i] = ns;
+    lr_cnt[i] = nl;
+  }
+}
+
+// exclusive scan of counts[0..n) into off[0..n] (one block, deterministic)
+__global__ __launch_bounds__(1024) void k_scan_int(int n, const int *cnt, int *off) {
+  __shared__ int buf[1024];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int start = 0; start < n; start += 1024) {
+    const int i = start + threadIdx.x;
+    const int v = i < n ? cnt[i] : 0;
+    buf[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {
+      const int t = int(threadIdx.x) >= o ? buf[threadIdx.x - o] : 0;
+      __syncthreads();
+      buf[threadIdx.x] += t;
+      __syncthreads();
+    }
+    if (i < n) off[i] = carry + buf[threadIdx.x] - v;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry += buf[1023];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) off[n] = carry;
+}
+
+// canonical SR entries (i < j) per atom
+__global__ void k_canon_count(int n, const int *off, const int *list, int *cnt) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int c = 0;
+  for (int k = off[i]; k < off[i + 1]; ++k)
+    if ((list[k] >> 5) > i) ++c;
+  cnt[i] = c;
+}
+
+// pairs in atom-major order of their canonical entry; incidence entries
+// p * 2 + side in the same positions as the full list
+__global__ void k_pairs(int n, const int *off, const int *list, const int *poff, int *nodes, int *codes,
+                        int *inc, int *err) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int p = poff[i];
+  for (int k = off[i]; k < off[i + 1]; ++k) {
+    const int j = list[k] >> 5, code = list[k] & 31;
+    if (j > i) {
+      nodes[2 * p] = i;
+      nodes[2 * p + 1] = j;
+      codes[p] = code;
+      inc[k] = 2 * p;
+      ++p;
+    }
+  }
+  // reverse entries: find (i, -code) in j's list, whose canonical pair index
+  // is poff[j] + (number of canonical entries before it)
+  for (int k = off[i]; k < off[i + 1]; ++k) {
+    const int j = list[k] >> 5, code = list[k] & 31;
+    if (j > i) continue;
+    const int want = i * 32 + (26 - code);  // negated image
+    int q = poff[j], found = -1;
+    for (int m = off[j]; m < off[j + 1]; ++m) {
+      const int e = list[m];
+      if ((e >> 5) > j) {
+        if (e == want) { found = q; break; }
+        ++q;
+      }
+    }
+    if (found < 0) { if (err) *err = 2; inc[k] = 1; continue; }
+    inc[k] = 2 * found + 1;
+  }
+}
+
+}  // namespace
+
+void Evaluator::build_topology_device(double *x, const double lo[3], const double hi[3], const int per[3],
+                                      double skin) {
+  if (!system_ready_) throw std::logic_error("SO3LR: set the system before the topology");
+  hipStream_t s = stream_;
+  const int n = int(n_);
+  Grid G;
+  const double rmax = std::max(rc_, lr_.cutoff) + skin;
+  for (int d = 0; d < 3; ++d) {
+    G.lo[d] = lo[d];
+    G.len[d] = hi[d] - lo[d];
+    G.per[d] = per[d] ? 1 : 0;
+    if (!(G.len[d] > 0)) throw std::invalid_argument("SO3LR: degenerate box");
+    if (G.per[d] && G.len[d] <= 2.0 * (lr_.cutoff + 0.0))
+      throw std::invalid_argument("SO3LR: periodic box shorter than twice the long-range cutoff");
+    G.nc[d] = std::max(1, int(std::floor(G.len[d] / rmax)));
+  }
+  const int ncell = G.nc[0] * G.nc[1] * G.nc[2];
+  if (std::int64_t(ncell) > (std::int64_t(1) << 26)) throw std::invalid_argument("SO3LR: box too large for the cell grid");
+  hipLaunchKernelGGL(k_wrap, dim3((n + 255) / 256), dim3(256), 0, s, n, x, G);
+  int *key = ensure<int>(nb_key_, n), *idx = ensure<int>(nb_idx_, n);
+  int *skey = ensure<int>(nb_skey_, n), *sidx = ensure<int>(nb_sidx_, n);
+  int *cstart = ensure<int>(nb_cstart_, ncell + 1);
+  hipLaunchKernelGGL(k_cell_keys, dim3((n + 255) / 256), dim3(256), 0, s, n, x, G, key, idx);
+  std::size_t tmp_bytes = 0;
+  int bits = 1;
+  while ((1 << bits) < ncell + 1) ++bits;
+  NB_CHECK(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, key, skey, idx, sidx, n, 0, bits, s));
+  void *tmp = ensure<char>(nb_tmp_, tmp_bytes);
+  NB_CHECK(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, skey, idx, sidx, n, 0, bits, s));
+  hipLaunchKernelGGL(k_cell_start, dim3((n + 1 + 255) / 256), dim3(256), 0, s, n, ncell, skey, cstart);
+  int *sr_cnt = ensure<int>(nb_srcnt_, n), *lr_cnt = ensure<int>(nb_lrcnt_, n);
+  int *err = ensure<int>(nb_err_, 1);
+  NB_CHECK(hipMemsetAsync(err, 0, sizeof(int), s));
+  const double sr2 = (rc_ + skin) * (rc_ + skin), lr2 = (lr_.cutoff + skin) * (lr_.cutoff + skin);
+  const int gw = (n + 3) / 4;
+  hipLaunchKernelGGL(k_nbr<false>, dim3(gw), dim3(256), 0, s, n, x, G, cstart, sidx, sr2, lr2, sr_cnt, lr_cnt,
+                     nullptr, nullptr, nullptr, nullptr, err);
+  int *sr_off = ensure<int>(sr_inc_off_, n + 1), *lr_off = ensure<int>(lr_inc_off_, n + 1);
+  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, sr_cnt, sr_off);
+  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, lr_cnt, lr_off);
+  int totals[2];
+  NB_CHECK(hipMemcpyAsync(&totals[0], sr_off + n, sizeof(int), hipMemcpyDeviceToHost, s));
+  NB_CHECK(hipMemcpyAsync(&totals[1], lr_off + n, sizeof(int), hipMemcpyDeviceToHost, s));
+  NB_CHECK(hipStreamSynchronize(s));
+  if (std::int64_t(totals[0]) + totals[1] >= (std::int64_t(1) << 31) - 1)
+    throw std::length_error("SO3LR: neighbour lists exceed 2^31 entries");
+  int *sr_list = ensure<int>(nb_srlist_, totals[0]);
+  int *lr_list = ensure<int>(lr_inc_, totals[1]);
+  hipLaunchKernelGGL(k_nbr<true>, dim3(gw), dim3(256), 0, s, n, x, G, cstart, sidx, sr2, lr2, nullptr, nullptr,
+                     sr_off, lr_off, sr_list, lr_list, nullptr);
+  // half-pair table of the SR list
+  hipLaunchKernelGGL(k_canon_count, dim3((n + 255) / 256), dim3(256), 0, s, n, sr_off, sr_list, sr_cnt);
+  int *poff = ensure<int>(nb_poff_, n + 1);
+  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, sr_cnt, poff);
+  int npairs = 0, herr = 0;
+  NB_CHECK(hipMemcpyAsync(&npairs, poff + n, sizeof(int), hipMemcpyDeviceToHost, s));
+  NB_CHECK(hipStreamSynchronize(s));
+  int *nodes = ensure<int>(sr_nodes_, 2 * std::size_t(std::max(npairs, 1)));
+  int *codes = ensure<int>(sr_code_, std::max(npairs, 1));
+  int *inc = ensure<int>(sr_inc_, std::max(totals[0], 1));
+  hipLaunchKernelGGL(k_pairs, dim3((n + 255) / 256), dim3(256), 0, s, n, sr_off, sr_list, poff, nodes, codes, inc, err);
+  NB_CHECK(hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, s));
+  NB_CHECK(hipStreamSynchronize(s));
+  if (herr == 1)
+    throw std::invalid_argument("SO3LR: an atom sees its own periodic image within the cutoff; the box is too small");
+  if (herr == 2) throw std::logic_error("SO3LR: internal error, short-range list not symmetric");
+  if (2 * npairs != totals[0]) throw std::logic_error("SO3LR: internal error, short-range pair count");
+  p_sr_ = npairs;
+  p_lr_ = totals[1] / 2;
+  lr_entries_ = totals[1];
+  for (int d = 0; d < 3; ++d) box_len_[d] = G.len[d];
+  shift_mode_ = true;
+  topology_ready_ = true;
+  evaluated_ = false;
+}
+
+}  // namespace so3lr_amd

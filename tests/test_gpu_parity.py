@@ -130,3 +130,40 @@ def test_refusals(ctx):
     with pytest.raises(_lib.SO3LRError) as err:
         ctx.set_system(z, 0, 2)  # O2 has 16 electrons: an even count needs an odd multiplicity
     assert err.value.code == _lib.ERR_SYSTEM
+
+
+def test_device_reneighbor_matches_rows_path(orc):
+    """HBM-resident reneighbor (owned positions + image codes) against the
+    LAMMPS-rows path and the oracle, with atoms displaced outside the box."""
+    import torch
+    from so3lrxlammps_amd import Context, Lists
+    ref, z, pos, box = support.load_golden("water3000")
+    rng = np.random.default_rng(3)
+    moved = pos + rng.normal(scale=0.05, size=pos.shape)
+    moved[:50] += box  # some atoms one period away: the reneighbor wraps them
+    c = Context(support.MODEL, 0)
+    c.set_system(z, 0, 1)
+    lists = Lists(np.mod(moved, box), np.zeros(3), box, (1, 1, 1))
+    c.set_topology(lists)
+    e1, f1, ea1, w1 = c.compute(lists.rows_positions(np.mod(moved, box)))
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        xt = torch.tensor(moved, dtype=torch.float64, device=dev)
+        ft = torch.zeros_like(xt)
+        c.reneighbor_device(xt, np.zeros(3), box, (1, 1, 1), 1.0, stream=stream.cuda_stream)
+        e2, w2 = c.compute_device(xt, ft, stream=stream.cuda_stream)
+        stream.synchronize()
+        wrapped = xt.cpu().numpy()
+        f2 = ft.cpu().numpy()
+    assert np.all(wrapped >= 0) and np.all(wrapped < box)
+    assert np.abs(wrapped - np.mod(moved, box)).max() < 1e-12
+    assert abs(e1 - e2) <= 1e-12 * abs(e1)
+    assert np.abs(f1 - f2).max() <= 1e-11
+    assert np.abs(w1 - w2).max() <= 1e-10 * max(1.0, np.abs(w1).max())
+    sr_active, sr_cand, lr_cand = c.graph_stats()
+    assert sr_cand == len(lists.lists[0][2]) // 2 and lr_cand == len(lists.lists[1][2])
+    sr, lr = support.build_graphs(np.mod(moved, box), box)
+    out = orc.evaluate(z, sr, lr)
+    assert abs(e2 - out["energy"]) <= 1e-10 * abs(out["energy"])
+    assert np.abs(f2 - out["forces"]).max() <= 1e-9
