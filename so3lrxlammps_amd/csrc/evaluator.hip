@@ -184,97 +184,6 @@ __global__ __launch_bounds__(256) void k_sr_compact(
   }
 }
 
-// ---------------------------------------------------------------- node GEMMs
-// out[r][o] = sum_k in[r][k] * WT[k][o] + bias[o], 16 rows x 64 columns per
-// block; MODE 0 plain, 1 keeps the pre-activation in out and silu in out2,
-// 2 adds aux[r][o], 3 multiplies by silu'(aux[r][o]).
-constexpr int kLinRows = 16;
-constexpr int kLinMaxK = 352;
-template <int MODE>
-__global__ __launch_bounds__(64) void k_linear(int rows, int K, int O, const double *in, int ldin,
-                                               const double *WT, const double *bias, double *out,
-                                               int ldout, double *out2, const double *aux, int ldaux) {
-  __shared__ double tile[kLinRows * kLinMaxK];
-  const int r0 = blockIdx.y * kLinRows;
-  for (int i = threadIdx.x; i < kLinRows * K; i += 64) {
-    const int rr = i / K, kk = i - rr * K;
-    tile[i] = r0 + rr < rows ? in[std::size_t(r0 + rr) * ldin + kk] : 0.0;
-  }
-  __syncthreads();
-  const int o = blockIdx.x * 64 + threadIdx.x;
-  if (o >= O) return;
-  double acc[kLinRows];
-#pragma unroll
-  for (int rr = 0; rr < kLinRows; ++rr) acc[rr] = 0.0;
-  for (int k = 0; k < K; ++k) {
-    const double w = WT[std::size_t(k) * O + o];
-#pragma unroll
-    for (int rr = 0; rr < kLinRows; ++rr) acc[rr] += tile[rr * K + k] * w;
-  }
-  const double b = bias ? bias[o] : 0.0;
-  for (int rr = 0; rr < kLinRows; ++rr) {
-    const int row = r0 + rr;
-    if (row >= rows) break;
-    const double v = acc[rr] + b;
-    const std::size_t io = std::size_t(row) * ldout + o;
-    if (MODE == 0) out[io] = v;
-    if (MODE == 1) { out[io] = v; out2[io] = silu(v); }
-    if (MODE == 2) out[io] = v + aux[std::size_t(row) * ldaux + o];
-    if (MODE == 3) out[io] = v * silu_prime(aux[std::size_t(row) * ldaux + o]);
-  }
-}
-
-// q, k, v, q_ev, k_ev: out[n][w][h*32+o] = sum_k x[n][h*32+k] W[w][h][k][o]
-__global__ __launch_bounds__(128) void k_qkv(int N, const double *x, const double *W, double *qkv) {
-  __shared__ double tile[16 * kF];
-  const int n0 = blockIdx.x * 16;
-  for (int i = threadIdx.x; i < 16 * kF; i += 128) {
-    const int rr = i / kF;
-    tile[i] = n0 + rr < N ? x[std::size_t(n0) * kF + i] : 0.0;
-  }
-  __syncthreads();
-  const int c = threadIdx.x;  // output channel within a projection
-  const int h = c / kHW, o = c % kHW;
-  for (int w = 0; w < 5; ++w) {
-    double acc[16];
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) acc[rr] = 0.0;
-    const double *Wh = W + (std::size_t(w) * kHeads + h) * kHW * kHW;
-    for (int k = 0; k < kHW; ++k) {
-      const double wv = Wh[k * kHW + o];
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) acc[rr] += tile[rr * kF + h * kHW + k] * wv;
-    }
-    for (int rr = 0; rr < 16; ++rr)
-      if (n0 + rr < N) qkv[std::size_t(n0 + rr) * 640 + w * kF + c] = acc[rr];
-  }
-}
-
-// dx[n][h*32+k] = base[n][.] + sum_{w,o} W[w][h][k][o] g[n][w][h*32+o]
-__global__ __launch_bounds__(128) void k_qkv_bwd(int N, const double *g, const double *W,
-                                                 const double *base, double *dx) {
-  __shared__ double tile[8 * 640];
-  const int n0 = blockIdx.x * 8;
-  for (int i = threadIdx.x; i < 8 * 640; i += 128) {
-    const int rr = i / 640;
-    tile[i] = n0 + rr < N ? g[std::size_t(n0) * 640 + i] : 0.0;
-  }
-  __syncthreads();
-  const int c = threadIdx.x;
-  const int h = c / kHW, k = c % kHW;
-  double acc[8];
-  for (int rr = 0; rr < 8; ++rr) acc[rr] = 0.0;
-  for (int w = 0; w < 5; ++w) {
-    const double *Wh = W + ((std::size_t(w) * kHeads + h) * kHW + k) * kHW;
-    for (int o = 0; o < kHW; ++o) {
-      const double wv = Wh[o];
-      for (int rr = 0; rr < 8; ++rr) acc[rr] += tile[rr * 640 + w * kF + h * kHW + o] * wv;
-    }
-  }
-  for (int rr = 0; rr < 8; ++rr)
-    if (n0 + rr < N) dx[std::size_t(n0 + rr) * kF + c] = base[std::size_t(n0 + rr) * kF + c] + acc[rr];
-}
-
 // ---------------------------------------------------------------- filters
 // Per active pair: Bernstein basis and PhysNet cutoff of r, the equivariant
 // invariant s_l = sum_{m in l} (ev_a - ev_b)^2 cg, and both filters
@@ -640,9 +549,160 @@ __global__ __launch_bounds__(256) void k_filter_bwd_mfma(const int *n_active, co
   }
 }
 
+
+// ---------------------------------------------------------------- MFMA node GEMMs
+// out[n][o] = sum_k W[o][k] X[n][k] (+ epilogue), 16 nodes per wavefront as the
+// MFMA column block, output features as rows.  K is read from the node rows in
+// the permuted order k = 16 T + g + 4 v (zero beyond K); W is pre-permuted
+// (permute_mfma) and zero-padded to 16-row tiles and 16-column K chunks.
+// EPI 0: out = acc + bias; 1: out = pre, out2 = silu(pre); 2: out = acc + bias
+// + aux; 3: out = acc * silu'(aux).
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const double *X, int ldx,
+                                              const double *Wp, const double *bias, double *out, int ldo,
+                                              double *out2, const double *aux, int ldaux) {
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w * 16 >= rows) return;
+  const int n = w * 16 + j;
+  const bool valid = n < rows;
+  const int nn = valid ? n : rows - 1;
+  const int KT = (K + 15) / 16, MT = (O + 15) / 16;
+  const double *xr = X + std::size_t(nn) * ldx;
+  for (int mt0 = 0; mt0 < MT; mt0 += 4) {
+    const int mcount = MT - mt0 < 4 ? MT - mt0 : 4;
+    v4d acc[4] = {v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}};
+    for (int T = 0; T < KT; ++T) {
+      double b[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int k = 16 * T + g + 4 * v;
+        b[v] = k < K ? xr[k] : 0.0;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q >= mcount) break;
+        const v4d wv = wload(Wp, KT, mt0 + q, T, lane);
+        acc[q] = mfma(wv[0], b[0], acc[q]);
+        acc[q] = mfma(wv[1], b[1], acc[q]);
+        acc[q] = mfma(wv[2], b[2], acc[q]);
+        acc[q] = mfma(wv[3], b[3], acc[q]);
+      }
+    }
+    if (!valid) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q >= mcount) break;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 16 * (mt0 + q) + g + 4 * r;
+        if (o >= O) continue;
+        const std::size_t io = std::size_t(n) * ldo + o;
+        const double v = acc[q][r] + (bias ? bias[o] : 0.0);
+        if (EPI == 0) out[io] = v;
+        if (EPI == 1) { out[io] = v; out2[io] = silu(v); }
+        if (EPI == 2) out[io] = v + aux[std::size_t(n) * ldaux + o];
+        if (EPI == 3) out[io] = v * silu_prime(aux[std::size_t(n) * ldaux + o]);
+      }
+    }
+  }
+}
+
+// Block-diagonal projections: per head h, the 160 outputs (q k v q_ev k_ev,
+// 32 each) depend on x[h*32 .. h*32+32).  Wp holds, per head, the permuted
+// (160 x 32) matrix; out[n][w*128 + h*32 + o].
+__global__ __launch_bounds__(256) void k_qkv_mfma(int rows, const double *X, const double *Wp, double *out) {
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w * 16 >= rows) return;
+  const int n = w * 16 + j;
+  const bool valid = n < rows;
+  const double *xr = X + std::size_t(valid ? n : rows - 1) * kF;
+  for (int h = 0; h < kHeads; ++h) {
+    double b[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) b[t] = xr[h * kHW + 16 * (t >> 2) + g + 4 * (t & 3)];
+    const double *Wh = Wp + std::size_t(h) * 160 * kHW;
+    v4d acc[10];
+#pragma unroll
+    for (int mt = 0; mt < 10; ++mt) {
+      acc[mt] = v4d{0, 0, 0, 0};
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const v4d wv = wload(Wh, 2, mt, T, lane);
+        acc[mt] = mfma(wv[0], b[4 * T + 0], acc[mt]);
+        acc[mt] = mfma(wv[1], b[4 * T + 1], acc[mt]);
+        acc[mt] = mfma(wv[2], b[4 * T + 2], acc[mt]);
+        acc[mt] = mfma(wv[3], b[4 * T + 3], acc[mt]);
+      }
+    }
+    if (!valid) continue;
+#pragma unroll
+    for (int mt = 0; mt < 10; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = 16 * mt + g + 4 * r;  // 0..159 = projection * 32 + channel
+        out[std::size_t(n) * 640 + (o >> 5) * kF + h * kHW + (o & 31)] = acc[mt][r];
+      }
+  }
+}
+
+// dx[n][h*32 + k] = base[n][.] + sum_{w,o} W[w][h][k][o] g[n][w*128 + h*32 + o];
+// per head the permuted transpose (32 x 160), K read in the permuted order
+// from the 160 gradient entries of that head.
+__global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *G, const double *Wtp,
+                                                      const double *base, double *dx) {
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w * 16 >= rows) return;
+  const int n = w * 16 + j;
+  const bool valid = n < rows;
+  const double *gr = G + std::size_t(valid ? n : rows - 1) * 640;
+  for (int h = 0; h < kHeads; ++h) {
+    const double *Wh = Wtp + std::size_t(h) * kHW * 160;
+    v4d acc[2] = {v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}};
+#pragma unroll
+    for (int T = 0; T < 10; ++T) {
+      double b[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int k = 16 * T + g + 4 * v;  // projection * 32 + channel
+        b[v] = gr[(k >> 5) * kF + h * kHW + (k & 31)];
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const v4d wv = wload(Wh, 10, mt, T, lane);
+        acc[mt] = mfma(wv[0], b[0], acc[mt]);
+        acc[mt] = mfma(wv[1], b[1], acc[mt]);
+        acc[mt] = mfma(wv[2], b[2], acc[mt]);
+        acc[mt] = mfma(wv[3], b[3], acc[mt]);
+      }
+    }
+    if (!valid) continue;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = h * kHW + 16 * mt + g + 4 * r;
+        dx[std::size_t(n) * kF + c] = base[std::size_t(n) * kF + c] + acc[mt][r];
+      }
+  }
+}
+
 // ---------------------------------------------------------------- attention
-// Node-major: one wavefront per node n, lane l holds channels l and l+64
-// (heads l/32 and 2+l/32) and equivariant channel l < 24.
+// Node-major, one wavefront per node.  Lane l works for head h = l / 16: it
+// holds the invariant channels 32 h + t and 32 h + 16 + t (t = l % 16) and the
+// equivariant channel off[h] + t of degree h + 1 when t < 2 h + 3, so every
+// per-head sum is a 16-lane group reduction.
+__device__ __forceinline__ double group_sum(double v) {
+  v += __shfl_xor(v, 8, kWave);
+  v += __shfl_xor(v, 4, kWave);
+  v += __shfl_xor(v, 2, kWave);
+  v += __shfl_xor(v, 1, kWave);
+  return v;
+}
+__device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
+
 __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, const int *inc,
                                                   const int *cand2act, const int *pa,
                                                   const double *x, const double *ev,
@@ -653,9 +713,13 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
+  const int h = lane >> 4, t = lane & 15;
+  const int c0 = 32 * h + t, c1 = c0 + 16;
+  const bool evv = t < 2 * h + 3;
+  const int m = ev_offset(h) + t;
+  const double par = slot_parity(h);
   const double *qn = qkv + std::size_t(n) * 640;
-  const double q0 = qn[lane], q1 = qn[64 + lane], qe0 = qn[384 + lane], qe1 = qn[448 + lane];
-  const int slot = lane < kE ? degree_slot(lane) : 0;
+  const double q0 = qn[c0], q1 = qn[c1], qe0 = qn[384 + c0], qe1 = qn[384 + c1];
   double acc0 = 0.0, acc1 = 0.0, acce = 0.0;
   for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
     const int e = inc[k];
@@ -665,30 +729,21 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
     const int o = pa[2 * p + 1 - side];
     const double *ko = qkv + std::size_t(o) * 640;
     const double *fp = pf + 256 * std::size_t(p);
-    const double ai_lo = half_sum(q0 * ko[128 + lane] * fp[lane]) * inv_avg;
-    const double ai_hi = half_sum(q1 * ko[192 + lane] * fp[64 + lane]) * inv_avg;
-    const double ae_lo = half_sum(qe0 * ko[512 + lane] * fp[128 + lane]) * inv_avg;
-    const double ae_hi = half_sum(qe1 * ko[576 + lane] * fp[192 + lane]) * inv_avg;
+    const double ai = group_sum(q0 * ko[128 + c0] * fp[c0] + q1 * ko[128 + c1] * fp[c1]) * inv_avg;
+    const double ae = group_sum(qe0 * ko[512 + c0] * fp[128 + c0] + qe1 * ko[512 + c1] * fp[128 + c1]) * inv_avg;
     const double fc = pfc[p];
-    acc0 += fc * ai_lo * ko[256 + lane];
-    acc1 += fc * ai_hi * ko[320 + lane];
-    const double e0 = __shfl(ae_lo, 0, kWave), e1 = __shfl(ae_lo, 32, kWave);
-    const double e2 = __shfl(ae_hi, 0, kWave), e3 = __shfl(ae_hi, 32, kWave);
-    if (lane < kE) {
-      const double y = pY[kE * std::size_t(p) + lane] * (side == 0 ? 1.0 : slot_parity(slot));
-      acce += fc * pick4(slot, e0, e1, e2, e3) * y;
-    }
-    const double i0 = __shfl(ai_lo, 0, kWave), i1 = __shfl(ai_lo, 32, kWave);
-    const double i2 = __shfl(ai_hi, 0, kWave), i3 = __shfl(ai_hi, 32, kWave);
-    if (lane < 8) {
-      const double v = lane < 4 ? pick4(lane, i0, i1, i2, i3) : pick4(lane - 4, e0, e1, e2, e3);
-      palpha[16 * std::size_t(p) + 8 * side + lane] = v;
+    acc0 += fc * ai * ko[256 + c0];
+    acc1 += fc * ai * ko[256 + c1];
+    if (evv) acce += fc * ae * pY[kE * std::size_t(p) + m] * (side == 0 ? 1.0 : par);
+    if (t == 0) {
+      palpha[16 * std::size_t(p) + 8 * side + h] = ai;
+      palpha[16 * std::size_t(p) + 8 * side + 4 + h] = ae;
     }
   }
   const std::size_t i = std::size_t(n) * kF;
-  ainv[i + lane] = x[i + lane] + acc0;
-  ainv[i + 64 + lane] = x[i + 64 + lane] + acc1;
-  if (lane < kE) aev[std::size_t(n) * kE + lane] = ev[std::size_t(n) * kE + lane] + acce;
+  ainv[i + c0] = x[i + c0] + acc0;
+  ainv[i + c1] = x[i + c1] + acc1;
+  if (evv) aev[std::size_t(n) * kE + m] = ev[std::size_t(n) * kE + m] + acce;
 }
 
 // LayerNorm over 128 channels held two per lane (biased variance).
@@ -1007,7 +1062,8 @@ __global__ __launch_bounds__(256) void k_ln1_bwd(int N, const double *gp, const 
 // For node n and each pair p = {n, o}: the incoming edge o -> n gives dq_n,
 // the outgoing edge n -> o gives dk_n, dv_n (sender-side terms, gathered here
 // instead of scattered).  The endpoint with side 0 also writes the per-pair
-// adjoints df (both directions), dfc and accumulates dY.
+// adjoints df (both directions), dfc and accumulates dY.  Lane layout as in
+// k_attn_fwd.
 __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, const int *inc,
                                                   const int *cand2act, const int *pa, const double *qkv,
                                                   const double *pf, const double *pY, const double *pfc,
@@ -1017,13 +1073,17 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
+  const int h = lane >> 4, t = lane & 15;
+  const int c0 = 32 * h + t, c1 = c0 + 16;
+  const bool evv = t < 2 * h + 3;
+  const int m = ev_offset(h) + t;
+  const double par = slot_parity(h);
   const double *me = qkv + std::size_t(n) * 640;
-  const double mq0 = me[lane], mq1 = me[64 + lane], mk0 = me[128 + lane], mk1 = me[192 + lane];
-  const double mv0 = me[256 + lane], mv1 = me[320 + lane], mqe0 = me[384 + lane], mqe1 = me[448 + lane];
-  const double mke0 = me[512 + lane], mke1 = me[576 + lane];
-  const double mg0 = gainv[std::size_t(n) * kF + lane], mg1 = gainv[std::size_t(n) * kF + 64 + lane];
-  const int slot = lane < kE ? degree_slot(lane) : 7;
-  const double mge = lane < kE ? gaev[std::size_t(n) * kE + lane] : 0.0;
+  const double mq0 = me[c0], mq1 = me[c1], mk0 = me[128 + c0], mk1 = me[128 + c1];
+  const double mv0 = me[256 + c0], mv1 = me[256 + c1], mqe0 = me[384 + c0], mqe1 = me[384 + c1];
+  const double mke0 = me[512 + c0], mke1 = me[512 + c1];
+  const double mg0 = gainv[std::size_t(n) * kF + c0], mg1 = gainv[std::size_t(n) * kF + c1];
+  const double mge = evv ? gaev[std::size_t(n) * kE + m] : 0.0;
   double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
   for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
     const int e = inc[k];
@@ -1032,70 +1092,53 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     const int side = e & 1;
     const int o = pa[2 * p + 1 - side];
     const double *ot = qkv + std::size_t(o) * 640;
-    const double oq0 = ot[lane], oq1 = ot[64 + lane], ok0 = ot[128 + lane], ok1 = ot[192 + lane];
-    const double ov0 = ot[256 + lane], ov1 = ot[320 + lane], oqe0 = ot[384 + lane], oqe1 = ot[448 + lane];
-    const double oke0 = ot[512 + lane], oke1 = ot[576 + lane];
-    const double og0 = gainv[std::size_t(o) * kF + lane], og1 = gainv[std::size_t(o) * kF + 64 + lane];
-    const double oge = lane < kE ? gaev[std::size_t(o) * kE + lane] : 0.0;
+    const double oq0 = ot[c0], oq1 = ot[c1], ok0 = ot[128 + c0], ok1 = ot[128 + c1];
+    const double ov0 = ot[256 + c0], ov1 = ot[256 + c1], oqe0 = ot[384 + c0], oqe1 = ot[384 + c1];
+    const double oke0 = ot[512 + c0], oke1 = ot[512 + c1];
+    const double og0 = gainv[std::size_t(o) * kF + c0], og1 = gainv[std::size_t(o) * kF + c1];
+    const double oge = evv ? gaev[std::size_t(o) * kE + m] : 0.0;
     const double *fp = pf + 256 * std::size_t(p);
-    const double fi0 = fp[lane], fi1 = fp[64 + lane], fe0 = fp[128 + lane], fe1 = fp[192 + lane];
+    const double fi0 = fp[c0], fi1 = fp[c1], fe0 = fp[128 + c0], fe1 = fp[128 + c1];
     const double fc = pfc[p];
-    const double y = lane < kE ? pY[kE * std::size_t(p) + lane] : 0.0;
-    const double par = slot_parity(slot < 4 ? slot : 0);
-    const double y_n = side == 0 ? y : par * y;   // harmonics of edge o -> n
-    const double y_o = side == 0 ? par * y : y;   // harmonics of edge n -> o
+    const double y = evv ? pY[kE * std::size_t(p) + m] : 0.0;
+    const double y_n = side == 0 ? y : par * y;  // harmonics of edge o -> n
+    const double y_o = side == 0 ? par * y : y;  // harmonics of edge n -> o
     const double *al = palpha + 16 * std::size_t(p);
-    // incoming o -> n
-    const double ci_lo = half_sum(mg0 * ov0), ci_hi = half_sum(mg1 * ov1);  // sum g v per head
-    const double ce_m = lane < kE ? mge * y_n : 0.0;
-    double ce[4];
-    for (int l = 0; l < 4; ++l) ce[l] = wave_sum(slot == l ? ce_m : 0.0);
-    // outgoing n -> o
-    const double co_lo = half_sum(og0 * mv0), co_hi = half_sum(og1 * mv1);
-    const double cem = lane < kE ? oge * y_o : 0.0;
-    double coe[4];
-    for (int l = 0; l < 4; ++l) coe[l] = wave_sum(slot == l ? cem : 0.0);
-    const int hlo = lane >> 5, hhi = 2 + (lane >> 5);
-    const double *ain = al + 8 * side, *aout = al + 8 * (1 - side);
-    // d alpha / norm for each direction, per lane's heads
-    const double sin_lo = fc * ci_lo * inv_avg, sin_hi = fc * ci_hi * inv_avg;
-    const double sout_lo = fc * co_lo * inv_avg, sout_hi = fc * co_hi * inv_avg;
-    const double sine_lo = fc * ce[hlo] * inv_avg, sine_hi = fc * ce[hhi] * inv_avg;
-    const double soute_lo = fc * coe[hlo] * inv_avg, soute_hi = fc * coe[hhi] * inv_avg;
-    dq0 += sin_lo * ok0 * fi0; dq1 += sin_hi * ok1 * fi1;
-    dqe0 += sine_lo * oke0 * fe0; dqe1 += sine_hi * oke1 * fe1;
-    dk0 += sout_lo * oq0 * fi0; dk1 += sout_hi * oq1 * fi1;
-    dke0 += soute_lo * oqe0 * fe0; dke1 += soute_hi * oqe1 * fe1;
-    dv0 += fc * aout[hlo] * og0; dv1 += fc * aout[hhi] * og1;
+    const double ain_i = al[8 * side + h], ain_e = al[8 * side + 4 + h];
+    const double aout_i = al[8 * (1 - side) + h], aout_e = al[8 * (1 - side) + 4 + h];
+    // per-head sums for the incoming (o -> n) and outgoing (n -> o) edges
+    const double ci = group_sum(mg0 * ov0 + mg1 * ov1);
+    const double ce = group_sum(mge * y_n);
+    const double co = group_sum(og0 * mv0 + og1 * mv1);
+    const double coe = group_sum(oge * y_o);
+    const double sin_ = fc * ci * inv_avg, sine = fc * ce * inv_avg;
+    const double sout = fc * co * inv_avg, soute = fc * coe * inv_avg;
+    dq0 += sin_ * ok0 * fi0; dq1 += sin_ * ok1 * fi1;
+    dqe0 += sine * oke0 * fe0; dqe1 += sine * oke1 * fe1;
+    dk0 += sout * oq0 * fi0; dk1 += sout * oq1 * fi1;
+    dke0 += soute * oqe0 * fe0; dke1 += soute * oqe1 * fe1;
+    dv0 += fc * aout_i * og0; dv1 += fc * aout_i * og1;
     if (side == 0) {
       double *d = df + 256 * std::size_t(p);
-      d[lane] = sin_lo * mq0 * ok0 + sout_lo * oq0 * mk0;
-      d[64 + lane] = sin_hi * mq1 * ok1 + sout_hi * oq1 * mk1;
-      d[128 + lane] = sine_lo * mqe0 * oke0 + soute_lo * oqe0 * mke0;
-      d[192 + lane] = sine_hi * mqe1 * oke1 + soute_hi * oqe1 * mke1;
-      double fcg = 0.0;
-      for (int h = 0; h < 4; ++h) fcg += ain[4 + h] * ce[h] + aout[4 + h] * coe[h];
-      // invariant part: heads 0,1 from ci_lo lanes 0/32, heads 2,3 from ci_hi
-      const double c0 = __shfl(ci_lo, 0, kWave), c1 = __shfl(ci_lo, 32, kWave);
-      const double c2 = __shfl(ci_hi, 0, kWave), c3 = __shfl(ci_hi, 32, kWave);
-      const double o0 = __shfl(co_lo, 0, kWave), o1 = __shfl(co_lo, 32, kWave);
-      const double o2 = __shfl(co_hi, 0, kWave), o3 = __shfl(co_hi, 32, kWave);
-      fcg += ain[0] * c0 + ain[1] * c1 + ain[2] * c2 + ain[3] * c3;
-      fcg += aout[0] * o0 + aout[1] * o1 + aout[2] * o2 + aout[3] * o3;
+      d[c0] = sin_ * mq0 * ok0 + sout * oq0 * mk0;
+      d[c1] = sin_ * mq1 * ok1 + sout * oq1 * mk1;
+      d[128 + c0] = sine * mqe0 * oke0 + soute * oqe0 * mke0;
+      d[128 + c1] = sine * mqe1 * oke1 + soute * oqe1 * mke1;
+      // d/d fc: every head's sum appears in its 16 lanes; take one lane per head
+      const double part = ain_i * ci + ain_e * ce + aout_i * co + aout_e * coe;
+      const double fcg = __shfl(part, 0, kWave) + __shfl(part, 16, kWave) + __shfl(part, 32, kWave) +
+                         __shfl(part, 48, kWave);
       if (lane == 0) dfc[p] = fcg;
-      if (lane < kE) {
-        // dE/dY_p: edge o->n contributes via y_n, edge n->o via y_o (parity)
-        const double gin = fc * ain[4 + slot] * mge, gout = fc * aout[4 + slot] * oge;
-        dY[kE * std::size_t(p) + lane] += gin + par * gout;
-      }
+      // dE/dY_p: edge o->n via y_n (= Y_p), edge n->o via y_o (parity)
+      if (evv) dY[kE * std::size_t(p) + m] += fc * ain_e * mge + par * fc * aout_e * oge;
     }
   }
   double *g = gqkv + std::size_t(n) * 640;
-  g[lane] = dq0; g[64 + lane] = dq1;
-  g[128 + lane] = dk0; g[192 + lane] = dk1;
-  g[256 + lane] = dv0; g[320 + lane] = dv1;
-  g[384 + lane] = dqe0; g[448 + lane] = dqe1;
-  g[512 + lane] = dke0; g[576 + lane] = dke1;
+  g[c0] = dq0; g[c1] = dq1;
+  g[128 + c0] = dk0; g[128 + c1] = dk1;
+  g[256 + c0] = dv0; g[256 + c1] = dv1;
+  g[384 + c0] = dqe0; g[384 + c1] = dqe1;
+  g[512 + c0] = dke0; g[512 + c1] = dke1;
 }
 
 // g_ev_in = g_aev + sum_pairs 2 (ev_n - ev_o) cg ds[slot]
@@ -1253,7 +1296,13 @@ std::vector<double> permute_mfma(const std::vector<double> &w, std::size_t M, st
       }
     return p;
   }
-  if (K % 16 != 0) throw std::logic_error("permute_mfma: K must be 4 or a multiple of 16");
+  if (K % 16 != 0) {  // zero-pad K to the next multiple of 16
+    const std::size_t Kp = (K + 15) / 16 * 16;
+    std::vector<double> wp(M * Kp, 0.0);
+    for (std::size_t r = 0; r < M; ++r)
+      for (std::size_t c = 0; c < K; ++c) wp[r * Kp + c] = w[r * K + c];
+    return permute_mfma(wp, M, Kp);
+  }
   const std::size_t KT = K / 16;
   std::vector<double> p(MT * KT * 64 * 4, 0.0);
   for (std::size_t mt = 0; mt < MT; ++mt)
@@ -1301,6 +1350,22 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
       qkv.insert(qkv.end(), w.begin(), w.end());
     }
     B.wqkv = up(qkv);
+    {
+      std::vector<double> fwdp, bwdp;
+      for (int h = 0; h < 4; ++h) {
+        std::vector<double> Mh(160 * HW);  // [w*32 + o][k] = W[w][h][k][o]
+        for (int w = 0; w < 5; ++w)
+          for (std::size_t k = 0; k < HW; ++k)
+            for (std::size_t o = 0; o < HW; ++o)
+              Mh[(w * HW + o) * HW + k] = qkv[((std::size_t(w) * 4 + h) * HW + k) * HW + o];
+        const auto pf = permute_mfma(Mh, 160, HW);
+        const auto pb = permute_mfma(transpose(Mh, 160, HW), HW, 160);
+        fwdp.insert(fwdp.end(), pf.begin(), pf.end());
+        bwdp.insert(bwdp.end(), pb.begin(), pb.end());
+      }
+      B.qkvp = up(fwdp);
+      B.qkvtp = up(bwdp);
+    }
     for (int k = 0; k < 2; ++k) {
       // the reference evaluates the transformer-level filter nets
       // (kokkos_integrated_block0.cpp:507-512)
@@ -1337,10 +1402,14 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     const auto m1 = m.f64(p + "mlp_1.1.weight", {F, F}), m2 = m.f64(p + "mlp_1.3.weight", {F, F});
     B.m1w = up(m1); B.m1t = up(transpose(m1, F, F));
     B.m2w = up(m2); B.m2t = up(transpose(m2, F, F));
+    B.m1p = up(permute_mfma(m1, F, F)); B.m2p = up(permute_mfma(m2, F, F));
+    B.m1tp = up(permute_mfma(transpose(m1, F, F), F, F)); B.m2tp = up(permute_mfma(transpose(m2, F, F), F, F));
     B.m1b = up(m.f64(p + "mlp_1.1.bias", {F}));
     B.m2b = up(m.f64(p + "mlp_1.3.bias", {F}));
     const auto iw = m.f64(p + "interaction_block.linear_layer.weight", {NI, NI});
     B.intw = up(iw); B.intt = up(transpose(iw, NI, NI));
+    B.intp = up(permute_mfma(iw, NI, NI));
+    B.inttp = up(permute_mfma(transpose(iw, NI, NI), NI, NI));
     B.intb = up(m.f64(p + "interaction_block.linear_layer.bias", {NI}));
   }
   {
@@ -1353,6 +1422,8 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     w1.insert(w1.end(), hw1.begin(), hw1.end());
     hw_.w1 = up(w1);
     hw_.w1t = up(transpose(w1, 320, F));
+    hw_.w1p = up(permute_mfma(w1, 320, F));
+    hw_.w1tp = up(permute_mfma(transpose(w1, 320, F), F, 320));
     std::vector<double> b1 = m.f64(e + "layers.0.bias", {F});
     const auto qb1 = m.f64(q + "transform_inv_features.0.bias", {F});
     const auto hb1 = m.f64(h + "transform_features.0.bias", {std::size_t(kHH)});
@@ -1674,14 +1745,15 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   auto fill = [&](double *p, std::size_t cnt) {
     if (cnt) hipLaunchKernelGGL(k_fill, dim3(unsigned((cnt + 255) / 256)), dim3(256), 0, s, p, cnt, 0.0);
   };
-  auto linear = [&](int mode, int rows, int K, int O, const double *in, int ldin, const double *WT,
-                    const double *bias, double *out, int ldout, double *out2, const double *aux, int ldaux) {
-    const dim3 grid(unsigned(ceil_div(O, 64)), unsigned(ceil_div(rows, kLinRows)));
-    if (mode == 0) hipLaunchKernelGGL(k_linear<0>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
-    if (mode == 1) hipLaunchKernelGGL(k_linear<1>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
-    if (mode == 2) hipLaunchKernelGGL(k_linear<2>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
-    if (mode == 3) hipLaunchKernelGGL(k_linear<3>, grid, dim3(64), 0, s, rows, K, O, in, ldin, WT, bias, out, ldout, out2, aux, ldaux);
+  auto gemm = [&](int epi, int rows, int K, int O, const double *X, int ldx, const double *Wp, const double *bias,
+                  double *out, int ldo, double *out2, const double *aux, int ldaux) {
+    const dim3 grid(unsigned(ceil_div(rows, 64)));
+    if (epi == 0) hipLaunchKernelGGL(k_gemm<0>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
+    if (epi == 1) hipLaunchKernelGGL(k_gemm<1>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
+    if (epi == 2) hipLaunchKernelGGL(k_gemm<2>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
+    if (epi == 3) hipLaunchKernelGGL(k_gemm<3>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
   };
+  const unsigned gN64 = unsigned(std::max(1, ceil_div(N, 64)));
 
   // --- active short-range pairs, geometry, ZBL ---
   const double rc2 = rc_ * rc_;
@@ -1723,7 +1795,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       A.fe0[k] = B.fe0[k]; A.feb0[k] = B.feb0[k]; A.fe1t[k] = B.fe1t[k]; A.feb1[k] = B.feb1[k];
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
-    hipLaunchKernelGGL(k_qkv, dim3(ceil_div(N, 16)), dim3(128), 0, s, int(N), xb, B.wqkv, qb);
+    hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
     FilterMfma FM;
     for (int k = 0; k < 2; ++k) {
       FM.w0p[k] = B.w0p[k]; FM.b0[k] = B.fb0[k]; FM.w1p[k] = B.w1p[k]; FM.b1[k] = B.fb1[k];
@@ -1743,11 +1815,11 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     });
     hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
                        n1ib, act);
-    linear(1, int(N), kF, kF, act, kF, B.m1t, B.m1b, hpb, kF, hid, nullptr, 0);
-    // in-place: hid becomes silu(hpre); the MLP output goes to pb = n1 + W2 hid + b2
-    linear(2, int(N), kF, kF, hid, kF, B.m2t, B.m2b, pb, kF, nullptr, n1b, kF);
+    gemm(1, int(N), kF, kF, act, kF, B.m1p, B.m1b, hpb, kF, hid, nullptr, 0);
+    // the MLP output goes to pb = n1 + W2 silu(hpre) + b2
+    gemm(2, int(N), kF, kF, hid, kF, B.m2p, B.m2b, pb, kF, nullptr, n1b, kF);
     hipLaunchKernelGGL(k_concat, dim3(gN4), dim3(256), 0, s, int(N), pb, aevb, B.int_cg, cat);
-    linear(0, int(N), kNI, kNI, cat, kNI, B.intt, B.intb, tb, kNI, nullptr, nullptr, 0);
+    gemm(0, int(N), kNI, kNI, cat, kNI, B.intp, B.intb, tb, kNI, nullptr, nullptr, 0);
     hipLaunchKernelGGL(k_post2, dim3(gN4), dim3(256), 0, s, int(N), pb, tb, aevb, B.ln2w, B.ln2b, ln_eps_,
                        xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);
   }
@@ -1756,7 +1828,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hw2, hw_.hb2, hw_.hqemb, hw_.hvshift,
              hw_.eb2, hw_.qb2};
   const double *xf = xs + L * Nz * kF;
-  linear(1, int(N), kF, 320, xf, kF, hw_.w1t, hw_.b1, hhead, 320, hact, nullptr, 0);
+  gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1, hhead, 320, hact, nullptr, 0);
   hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, hkey, heff, hir);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
   timed("long_range", 1, [&] {
@@ -1769,7 +1841,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   });
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
   hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, H, ghead);
-  linear(0, int(N), 320, kF, ghead, 320, hw_.w1, nullptr, gx, kF, nullptr, nullptr, 0);
+  gemm(0, int(N), 320, kF, ghead, 320, hw_.w1tp, nullptr, gx, kF, nullptr, nullptr, 0);
   fill(gev, Nz * kE);
 
   // --- interaction blocks, reverse ---
@@ -1789,10 +1861,10 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     hipLaunchKernelGGL(k_post2_bwd, dim3(gN4), dim3(256), 0, s, int(N), gx, gev, tb, aevb, B.ln2w, p2h, p2i, gp,
                        gt, gaev);
-    linear(0, int(N), kNI, kNI, gt, kNI, B.intw, nullptr, gcat, kNI, nullptr, nullptr, 0);
+    gemm(0, int(N), kNI, kNI, gt, kNI, B.inttp, nullptr, gcat, kNI, nullptr, nullptr, 0);
     hipLaunchKernelGGL(k_post_mid_bwd, dim3(gN4), dim3(256), 0, s, int(N), gcat, aevb, B.int_cg, gp, gaev);
-    linear(3, int(N), kF, kF, gp, kF, B.m2w, nullptr, ghid, kF, nullptr, hpb, kF);
-    linear(0, int(N), kF, kF, ghid, kF, B.m1w, nullptr, gact, kF, nullptr, nullptr, 0);
+    gemm(3, int(N), kF, kF, gp, kF, B.m2tp, nullptr, ghid, kF, nullptr, hpb, kF);
+    gemm(0, int(N), kF, kF, ghid, kF, B.m1tp, nullptr, gact, kF, nullptr, nullptr, 0);
     hipLaunchKernelGGL(k_ln1_bwd, dim3(gN4), dim3(256), 0, s, int(N), gp, gact, n1b, B.ln1w, n1hb, n1ib, gainv);
     timed("attn_bwd", 1, [&] {
       hipLaunchKernelGGL(k_attn_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, qb, pfb, pY, pfc,
@@ -1811,7 +1883,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       else
         hipLaunchKernelGGL(k_filter_bwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds, dr);
     });
-    hipLaunchKernelGGL(k_qkv_bwd, dim3(ceil_div(N, 8)), dim3(128), 0, s, int(N), gqkv, B.wqkv, gainv, gx);
+    hipLaunchKernelGGL(k_qkv_bwd_mfma, dim3(gN64), dim3(256), 0, s, int(N), gqkv, B.qkvtp, gainv, gx);
     hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, evb, B.att_cg, ds,
                        gaev, gev);
   }

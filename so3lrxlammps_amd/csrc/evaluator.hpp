@@ -42,9 +42,14 @@ struct BlockWeights {
   // MFMA operand order of the filter weights (see permute_mfma in evaluator.hip)
   const double *w0p[2], *w1p[2], *e0p[2], *e1p[2];     // forward
   const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];  // reverse (transposes)
+  // MFMA operand order of the node layers: forward and reverse (transpose)
+  const double *qkvp, *qkvtp;           // per head (160 x 32) and (32 x 160)
+  const double *m1p, *m2p, *m1tp, *m2tp;
+  const double *intp, *inttp;           // 132 x 132, K padded to 144
 };
 
 struct HeadWeights {
+  const double *w1p, *w1tp;  // MFMA operand order: (320 x 128) and its transpose
   const double *w1t;    // (128, 320): energy | charge | Hirshfeld first layers, transposed
   const double *w1;     // (320, 128)
   const double *b1;     // (320)
