@@ -42,9 +42,23 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def traffic_bytes(kernel, config):
+    """HBM bytes per launch (read + written) of `kernel` from the committed
+    PMC summary (two rocprofv3 passes, FETCH_SIZE and WRITE_SIZE, scaled by a
+    plain copy of known size); None when no summary covers this workload."""
+    path = os.path.join(REPO, "profiles", "pmc_traffic_config%d.json" % config)
+    try:
+        rec = json.load(open(path))["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return rec["read_bytes"] + rec["write_bytes"]
+
+
 def cpu_baseline(z, x, box, seconds_budget):
-    """Oracle (CPU restatement of the reference math, OpenMP) on one E+F+virial
-    of a sub-box sample of the same system, scaled to atom-steps/s."""
+    """Oracle (CPU restatement of the reference math, OpenMP) timed on the
+    host cores: repeated E+F+virial calls on a periodic sub-cube of the same
+    system until about `seconds_budget` seconds of CPU work are done; reports
+    the median call as atom-steps/s."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     from oracle.oracle import Oracle, lib
     import support
@@ -55,13 +69,19 @@ def cpu_baseline(z, x, box, seconds_budget):
     sel = np.all(x < side, axis=1)
     zs, xs = z[sel], x[sel]
     sr, lr = support.build_graphs(xs, np.full(3, side))
-    t0 = time.time()
-    orc.evaluate(zs, sr, lr)
-    dt = time.time() - t0
-    return {"value": len(zs) / dt, "unit": "atom-steps/s", "cores": int(lib().orc_num_threads()),
+    orc.evaluate(zs, sr, lr)  # warm-up (page-in, thread pool)
+    times = []
+    t_start = time.time()
+    while len(times) < 3 or (time.time() - t_start < seconds_budget and len(times) < 50):
+        t0 = time.time()
+        orc.evaluate(zs, sr, lr)
+        times.append(time.time() - t0)
+    med = float(np.median(times))
+    return {"value": len(zs) / med, "unit": "atom-steps/s", "cores": int(lib().orc_num_threads()),
             "kind": "port",
-            "sample": "one E+F+virial of %d atoms (a %.0f A periodic sub-cube of the config-3 system), %.1f s"
-                      % (len(zs), side, dt)}
+            "sample": "median of %d E+F+virial calls (%.1f s of CPU work) on %d atoms: a %.0f A periodic "
+                      "sub-cube of the benchmark system, CPU fp64 oracle, OpenMP"
+                      % (len(times), sum(times), len(zs), side)}
 
 
 def main():
@@ -71,7 +91,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=30.0)
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run a plain device copy of this size first (HBM-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs one LAMMPS rank on one MI355X with no "
@@ -89,6 +111,17 @@ def main():
     # an explicit stream: handle 0 (torch's default) would leave the library on its own stream
     stream = torch.cuda.Stream(device=dev)
     torch.cuda.set_stream(stream)
+    if args.copy_probe_mib > 0:
+        # a plain copy of known size: FETCH_SIZE / WRITE_SIZE of this kernel
+        # give the counters' scale against true HBM bytes
+        with torch.cuda.stream(stream):
+            src = torch.ones(args.copy_probe_mib << 17, dtype=torch.float64, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     ctx = Context(MODEL, 0)
     ctx.set_system(z, Q, M)
     lo = np.zeros(3)
@@ -98,16 +131,21 @@ def main():
     inv_m = torch.tensor(ACC / m, dtype=torch.float64, device=dev)[:, None]
     mt = torch.tensor(m, dtype=torch.float64, device=dev)[:, None]
     ft = torch.zeros((n, 3), dtype=torch.float64, device=dev)
-    boxt = torch.tensor(box, dtype=torch.float64, device=dev)
+    lot = torch.tensor(lo, dtype=torch.float64, device=dev)
     dt, skin, tau, T0 = 0.0005, 1.0, 0.1, 300.0
-    state = {"builds": 0, "build_s": 0.0}
+    # config 4 runs NPT: Berendsen barostat at 1 bar (water compressibility)
+    npt = args.config == 4
+    P0_bar, tau_p, beta_bar = 1.0, 1.0, 4.5e-5
+    EV_A3_TO_BAR = 1.602176634e6
+    state = {"builds": 0, "build_s": 0.0, "box": np.array(box, dtype=float), "mu_total": 1.0}
 
     def rebuild():
         # HBM-resident reneighbor: wraps xt in place, builds the candidate
         # lists on the GPU (no ghost rows, no host copies)
         t0 = time.time()
-        ctx.reneighbor_device(xt, lo, box, (1, 1, 1), skin, stream=stream.cuda_stream)
+        ctx.reneighbor_device(xt, lo, lo + state["box"], (1, 1, 1), skin, stream=stream.cuda_stream)
         state["x_build"] = xt.clone()
+        state["box_build"] = state["box"].copy()
         state["builds"] += 1
         state["build_s"] += time.time() - t0
 
@@ -122,6 +160,9 @@ def main():
         vt.addcmul_(ft, inv_m, value=0.5 * dt)
         xt.add_(vt, alpha=dt)
         disp = (xt - state["x_build"]).norm(dim=1).max().item()
+        # a box change moves the far corner: LAMMPS Neighbor::check_distance
+        # charges that against the skin as well
+        disp += float(np.linalg.norm(state["box"] - state["box_build"]))
         if disp > 0.5 * skin:
             rebuild()
         e, w = force()
@@ -130,6 +171,16 @@ def main():
         temp = 2.0 * ke / (3.0 * n * KB)
         lam = torch.sqrt(1.0 + dt / tau * (T0 / temp - 1.0))
         vt.mul_(lam)
+        if npt:
+            # P = (2 KE + tr W) / (3 V); W is the LAMMPS virial (eV)
+            vol = float(np.prod(state["box"]))
+            p_bar = (2.0 * ke.item() + w[0] + w[1] + w[2]) / (3.0 * vol) * EV_A3_TO_BAR
+            mu = (1.0 - dt / tau_p * beta_bar * (P0_bar - p_bar)) ** (1.0 / 3.0)
+            xt.sub_(lot).mul_(mu).add_(lot)
+            state["box"] = state["box"] * mu
+            state["mu_total"] *= mu
+            state["pressure_bar"] = p_bar
+            ctx.set_box(lo, lo + state["box"])
         return e, w
 
     log("warmup %d steps" % args.warmup)
@@ -155,13 +206,15 @@ def main():
             timing[name] = ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched
             pass
+    free_b, total_b = torch.cuda.mem_get_info(dev)
     ms_f, launches_f, pairs_f = timing["filter_bwd"]
     avg_ms = ms_f / launches_f
     flop = FILTER_BWD_FLOP_PER_PAIR * pairs_f / launches_f
     achieved = flop / (avg_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "k_filter_bwd", "achieved": achieved, "peak": FP64_PEAK_TFS,
-                "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFS, "traffic": None,
-                "avg_launch_ms": avg_ms, "pairs_per_launch": pairs_f / launches_f}
+    roofline = {"bound": "mfma", "kernel": "k_filter_bwd_mfma", "achieved": achieved, "peak": FP64_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFS, "traffic": traffic_bytes("k_filter_bwd_mfma", args.config),
+                "avg_launch_ms": avg_ms, "pairs_per_launch": pairs_f / launches_f,
+                "flop_per_pair": FILTER_BWD_FLOP_PER_PAIR}
     kernels = {k: {"avg_ms": v[0] / v[1], "launches": v[1]} for k, v in timing.items()}
 
     cpu = None
@@ -170,18 +223,25 @@ def main():
         cpu = cpu_baseline(z, x, box, args.cpu_budget)
 
     sr_active, sr_cand, lr_cand = ctx.graph_stats()
+    if npt:
+        extra = {"ensemble": "NPT (Berendsen, 1 bar, 300 K)", "box_scale": state["mu_total"],
+                 "pressure_bar_last": state.get("pressure_bar")}
+    else:
+        extra = {"ensemble": "NVT (Berendsen, 300 K)"}
     out = {
         "metric": "atom-steps/s/GPU (fp64 E+F+virial) at 24k-atom water; max atoms per GPU",
         "value": value, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": value / A100_ATOM_STEPS, "dtype": "f64", "data": "synthetic (seeded, config 3)",
-        "config": {"workload": "config 3: " + desc, "atoms": n, "integrator": "velocity Verlet + Berendsen 300 K",
+        "vs_baseline": value / A100_ATOM_STEPS, "dtype": "f64", "data": "synthetic (seeded, config %d)" % args.config,
+        "config": {"workload": "config 3: " + desc, "atoms": n, "integrator": "velocity Verlet", **extra,
                    "timestep_fs": 0.5, "skin_A": skin, "sr_pairs_active": sr_active,
                    "sr_pair_candidates": sr_cand, "lr_pair_candidates": lr_cand,
                    "neighbor_rebuilds_timed": state["builds"] - builds0,
                    "rebuild_seconds_timed": state["build_s"] - build_s0,
                    "ns_per_day": value / n * 0.5 * 86400 / 1e6,
-                   "device_bytes": ctx.device_bytes(), "kernels": kernels},
+                   "device_bytes": ctx.device_bytes(),
+                   "hbm_used_bytes": int(total_b - free_b), "hbm_total_bytes": int(total_b),
+                   "kernels": kernels},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
