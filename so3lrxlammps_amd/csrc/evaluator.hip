@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <stdexcept>
+#include <utility>
 
 namespace so3lr_amd {
 
@@ -328,15 +329,78 @@ __device__ __forceinline__ v4d wload(const double *P, int KT, int mt, int T, int
 }
 
 struct FilterMfma {
-  const double *w0p[2], *b0[2], *w1p[2], *b1[2], *e0p[2], *eb0[2], *e1p[2], *eb1[2];
-  const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];
+  const double *w0p[2], *w1p[2], *e1p[2];              // forward operands
+  const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];  // reverse operands (transposes)
+  const double *b0p[2], *eb0p[2], *ob1p[2];             // biases in accumulator order
+  const double *e0pk[2];                                // spherical layer 0: one v4d per lane {tile 0, tile 1, 0, 0}
   const double *att_cg;
   const double *rbf_b, *rbf_k, *rbf_kr;
   double gamma;
 };
 
+// Compile-time loop: f(std::integral_constant<int, S>) for S = 0 .. N-1, so
+// every register-array index below is a constant and nothing spills.
+template <class F, int... S>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, S...>) {
+  (f(std::integral_constant<int, S>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Software-pipelined operand stream: entry S (one v4d per lane: a weight
+// fragment, a bias tile or a chunk of the incoming adjoint) is loaded PF
+// entries before step S consumes it.  The scheduling fence after each step
+// keeps the compiler from sinking the loads back next to their uses, so PF
+// L2 round trips overlap the MFMAs of the steps in between.
+template <int NS, int PF, class Load>
+struct Stream {
+  Load load;
+  v4d buf[PF];
+  __device__ __forceinline__ explicit Stream(Load l) : load(l) {}
+  __device__ __forceinline__ void prime() {
+    static_for<PF>([&](auto i) {
+      constexpr int I = decltype(i)::value;
+      if constexpr (I < NS) buf[I] = load(i);
+    });
+  }
+  template <class Step>
+  __device__ __forceinline__ void run(Step &&step) {
+    static_for<NS>([&](auto si) {
+      constexpr int S = decltype(si)::value;
+      const v4d w = buf[S % PF];
+      if constexpr (S + PF < NS) buf[S % PF] = load(std::integral_constant<int, S + PF>{});
+      step(si, w);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+};
+
+#ifndef SO3LR_FILTER_PF
+#define SO3LR_FILTER_PF 4
+#endif
+constexpr int kFilterPF = SO3LR_FILTER_PF;  // fragments in flight per wavefront
+// Two wavefronts per SIMD (<= 256 registers per lane): measured faster than
+// one wavefront with a deeper prefetch, since the second wave's MFMAs cover
+// the first one's VALU phases (RBF, SiLU).
+#ifndef SO3LR_FILTER_WAVES
+#define SO3LR_FILTER_WAVES 2
+#endif
+#define FILTER_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SO3LR_FILTER_WAVES, SO3LR_FILTER_WAVES)))
+
+__device__ __forceinline__ v4d tile_load(const double *P, int t, int lane) {
+  return reinterpret_cast<const v4d *>(P)[t * 64 + lane];
+}
+__device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
+  c = mfma(w[0], b[0], c);
+  c = mfma(w[1], b[1], c);
+  c = mfma(w[2], b[2], c);
+  return mfma(w[3], b[3], c);
+}
+
 // Bernstein basis of pair distance r at channels 16 T + g + 4 v (T < 2, v < 4).
-__device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, double *rb, double &xb) {
+__device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, v4d *rb, double &xb) {
   double x = exp(-A.gamma * r);
   x = x < 1e-6 ? 1e-6 : (x > 1.0 - 1e-6 ? 1.0 - 1e-6 : x);
   xb = x;
@@ -344,20 +408,40 @@ __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, doubl
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
-    rb[t] = exp(A.rbf_b[ch] + A.rbf_k[ch] * lx + A.rbf_kr[ch] * l1x);
+    rb[t >> 2][t & 3] = exp(A.rbf_b[ch] + A.rbf_k[ch] * lx + A.rbf_kr[ch] * l1x);
   }
 }
 
-// 16 pairs per wavefront, 4 wavefronts per block.
-__global__ __launch_bounds__(256) void k_filter_fwd_mfma(const int *n_active, const int *pa, const double *pr,
+// Both filters of one block for 16 pairs per wavefront, 4 wavefronts per block.
+// Per filter the stream holds 96 weight fragments: W0 (s < 16: tile s % 8,
+// K chunk s / 8), W1 (16 <= s < 80) and E1 (80 <= s < 96), tile-minor.
+__global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_fwd_mfma(const int *n_active, const int *pa, const double *pr,
                                                          const double *ev, FilterMfma A, double *ps, double *pf) {
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const int p = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + j;
-  if ((blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 >= nact) return;  // whole wavefront idle
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave * 16 >= nact) return;  // whole wavefront idle
+  const int p = wave * 16 + j;
   const bool valid = p < nact;
   const int pp = valid ? p : nact - 1;
-  double rb[8], xb;
+
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, which = S / 96, s = S % 96;
+    if constexpr (s < 16) return wload(A.w0p[which], 2, s % 8, s / 8, lane);
+    else if constexpr (s < 80) return wload(A.w1p[which], 8, (s - 16) % 8, (s - 16) / 8, lane);
+    else return wload(A.e1p[which], 2, (s - 80) % 8, (s - 80) / 8, lane);
+  };
+  Stream<192, kFilterPF, decltype(load)> st(load);
+  st.prime();
+
+  v4d h[8], o[8], h2[2], e0;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    h[mt] = tile_load(A.b0p[0], mt, lane);
+    o[mt] = tile_load(A.ob1p[0], mt, lane);
+  }
+  v4d rb[2];
+  double xb;
   rbf8(pr[pp], g, A, rb, xb);
   // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
   double sg = 0.0;
@@ -371,159 +455,159 @@ __global__ __launch_bounds__(256) void k_filter_fwd_mfma(const int *n_active, co
     }
     if (valid) ps[4 * std::size_t(p) + g] = sg;
   }
-  for (int which = 0; which < 2; ++which) {
-    v4d h[8];
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) h[mt] = v4d{0, 0, 0, 0};
-#pragma unroll
-    for (int T = 0; T < 2; ++T)
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const v4d w = wload(A.w0p[which], 2, mt, T, lane);
-        h[mt] = mfma(w[0], rb[4 * T + 0], h[mt]);
-        h[mt] = mfma(w[1], rb[4 * T + 1], h[mt]);
-        h[mt] = mfma(w[2], rb[4 * T + 2], h[mt]);
-        h[mt] = mfma(w[3], rb[4 * T + 3], h[mt]);
-      }
+  auto store = [&](int which) {
+    if (!valid) return;
+    double *dst = pf + 256 * std::size_t(p) + which * kF;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[mt][r] = silu(h[mt][r] + A.b0[which][16 * mt + g + 4 * r]);
-    v4d o[8];
+      for (int r = 0; r < 4; ++r) dst[16 * mt + g + 4 * r] = o[mt][r];
+  };
+
+  st.run([&](auto si, const v4d &w) {
+    constexpr int S = decltype(si)::value, which = S / 96, s = S % 96;
+    if constexpr (s == 0) {
+      // spherical layer-0 operands of this filter (h2 is free: its last use
+      // was the previous filter's E1 pass)
+      h2[0] = tile_load(A.eb0p[which], 0, lane);
+      h2[1] = tile_load(A.eb0p[which], 1, lane);
+      e0 = reinterpret_cast<const v4d *>(A.e0pk[which])[lane];
+      if constexpr (which == 1) {
+        store(0);
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) o[mt] = v4d{0, 0, 0, 0};
-#pragma unroll
-    for (int T = 0; T < 8; ++T)
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const v4d w = wload(A.w1p[which], 8, mt, T, lane);
-        o[mt] = mfma(w[0], h[T][0], o[mt]);
-        o[mt] = mfma(w[1], h[T][1], o[mt]);
-        o[mt] = mfma(w[2], h[T][2], o[mt]);
-        o[mt] = mfma(w[3], h[T][3], o[mt]);
+        for (int mt = 0; mt < 8; ++mt) o[mt] = tile_load(A.ob1p[1], mt, lane);
       }
-    // spherical branch: 4 -> 32 (silu) -> 128, added to the radial branch
-    v4d h2[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      h2[mt] = mfma(A.e0p[which][mt * 64 + lane], sg, v4d{0, 0, 0, 0});
-#pragma unroll
-      for (int r = 0; r < 4; ++r) h2[mt][r] = silu(h2[mt][r] + A.eb0[which][16 * mt + g + 4 * r]);
     }
+    if constexpr (s < 16) {
+      h[s % 8] = mfma4(w, rb[s / 8], h[s % 8]);
+    } else if constexpr (s < 80) {
+      if constexpr (s == 16) {
 #pragma unroll
-    for (int T = 0; T < 2; ++T)
+        for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const v4d w = wload(A.e1p[which], 2, mt, T, lane);
-        o[mt] = mfma(w[0], h2[T][0], o[mt]);
-        o[mt] = mfma(w[1], h2[T][1], o[mt]);
-        o[mt] = mfma(w[2], h2[T][2], o[mt]);
-        o[mt] = mfma(w[3], h2[T][3], o[mt]);
-      }
-    if (valid) {
-      double *dst = pf + 256 * std::size_t(p) + which * kF;
+          for (int r = 0; r < 4; ++r) h[mt][r] = silu(h[mt][r]);
 #pragma unroll
-      for (int mt = 0; mt < 8; ++mt)
+        for (int mt = 0; mt < 2; ++mt) {
+          h2[mt] = mfma(e0[mt], sg, h2[mt]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int c = 16 * mt + g + 4 * r;
-          dst[c] = o[mt][r] + A.b1[which][c] + A.eb1[which][c];
+          for (int r = 0; r < 4; ++r) h2[mt][r] = silu(h2[mt][r]);
         }
+      }
+      o[(s - 16) % 8] = mfma4(w, h[(s - 16) / 8], o[(s - 16) % 8]);
+    } else {
+      if constexpr (s == 80 && which == 0) {
+        // h is free after the W1 pass: the next filter's layer-0 bias
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) h[mt] = tile_load(A.b0p[1], mt, lane);
+      }
+      o[(s - 80) % 8] = mfma4(w, h2[(s - 80) / 8], o[(s - 80) % 8]);
     }
-  }
+  });
+  store(1);
 }
 
 // Reverse of both filters, the Bernstein basis and the cutoff for 16 pairs per
-// wavefront: recompute the layer-0 pre-activations, d hidden = W1^T df (.)
-// silu', d rbf = W0^T d hidden, the same for the spherical branch down to ds,
-// and dE/dr.
-__global__ __launch_bounds__(256) void k_filter_bwd_mfma(const int *n_active, const double *pr, const double *ps,
+// wavefront.  Per filter the stream holds 133 entries:
+//   s <  88  per K chunk T = s / 11: the df chunk, then W1^T tiles 0..7 and
+//            E1^T tiles 0..1 (d hidden = W^T df);
+//   s < 112  per tile mt = (s - 88) / 3: the layer-0 bias, then W0 chunks 0, 1
+//            (pre-activation recomputed tile by tile, then d hidden *= silu');
+//   s < 115  the spherical layer-0 biases and operand (same, for the 4 -> 32 layer);
+//   s < 131  W0^T (d rbf), s < 133  E0^T (ds).
+__global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const int *n_active, const double *pr, const double *ps,
                                                          const double *df, const double *dfc, FilterMfma A, double rc,
                                                          double *ds, double *dr) {
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const int p = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + j;
-  if ((blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 >= nact) return;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave * 16 >= nact) return;
+  const int p = wave * 16 + j;
   const bool valid = p < nact;
   const int pp = valid ? p : nact - 1;
+  const double *dfp = df + 256 * std::size_t(pp) + g;
+
+  constexpr int NB = 133;
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, which = S / NB, s = S % NB;
+    if constexpr (s < 88) {
+      constexpr int T = s / 11, u = s % 11;
+      if constexpr (u == 0) {
+        const double *gf = dfp + which * kF + 16 * T;
+        return v4d{gf[0], gf[4], gf[8], gf[12]};
+      } else if constexpr (u <= 8) {
+        return wload(A.w1tp[which], 8, u - 1, T, lane);
+      } else {
+        return wload(A.e1tp[which], 8, u - 9, T, lane);
+      }
+    } else if constexpr (s < 112) {
+      constexpr int mt = (s - 88) / 3, u = (s - 88) % 3;
+      if constexpr (u == 0) return tile_load(A.b0p[which], mt, lane);
+      else return wload(A.w0p[which], 2, mt, u - 1, lane);
+    } else if constexpr (s < 115) {
+      if constexpr (s < 114) return tile_load(A.eb0p[which], s - 112, lane);
+      else return reinterpret_cast<const v4d *>(A.e0pk[which])[lane];
+    } else if constexpr (s < 131) {
+      return wload(A.w0tp[which], 8, (s - 115) % 2, (s - 115) / 2, lane);
+    } else {
+      return wload(A.e0tp[which], 2, 0, s - 131, lane);
+    }
+  };
+  Stream<2 * NB, kFilterPF, decltype(load)> st(load);
+  st.prime();
+
   const double r = pr[pp];
-  double rb[8], xb;
+  v4d rb[2];
+  double xb;
   rbf8(r, g, A, rb, xb);
   const double sg = ps[4 * std::size_t(pp) + g];
-  v4d drb[2] = {v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}};
-  v4d dsa = v4d{0, 0, 0, 0};
-  for (int which = 0; which < 2; ++which) {
-    const double *gf = df + 256 * std::size_t(pp) + which * kF;
-    v4d pre[8];
+  const v4d zero = v4d{0, 0, 0, 0};
+  v4d dh[8], dh2[2], bT, pre, pre2[2];
+  v4d drb[2] = {zero, zero};
+  v4d dsa = zero;
+
+  st.run([&](auto si, const v4d &w) {
+    constexpr int S = decltype(si)::value, s = S % NB;
+    if constexpr (s == 0) {
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) pre[mt] = v4d{0, 0, 0, 0};
-#pragma unroll
-    for (int T = 0; T < 2; ++T)
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const v4d w = wload(A.w0p[which], 2, mt, T, lane);
-        pre[mt] = mfma(w[0], rb[4 * T + 0], pre[mt]);
-        pre[mt] = mfma(w[1], rb[4 * T + 1], pre[mt]);
-        pre[mt] = mfma(w[2], rb[4 * T + 2], pre[mt]);
-        pre[mt] = mfma(w[3], rb[4 * T + 3], pre[mt]);
-      }
-    v4d pre2[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) pre2[mt] = mfma(A.e0p[which][mt * 64 + lane], sg, v4d{0, 0, 0, 0});
-    v4d dh[8], dh2[2];
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) dh[mt] = v4d{0, 0, 0, 0};
-    dh2[0] = v4d{0, 0, 0, 0};
-    dh2[1] = v4d{0, 0, 0, 0};
-#pragma unroll
-    for (int T = 0; T < 8; ++T) {
-      double b[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) b[v] = gf[16 * T + g + 4 * v];
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const v4d w = wload(A.w1tp[which], 8, mt, T, lane);
-        dh[mt] = mfma(w[0], b[0], dh[mt]);
-        dh[mt] = mfma(w[1], b[1], dh[mt]);
-        dh[mt] = mfma(w[2], b[2], dh[mt]);
-        dh[mt] = mfma(w[3], b[3], dh[mt]);
-      }
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const v4d w = wload(A.e1tp[which], 8, mt, T, lane);
-        dh2[mt] = mfma(w[0], b[0], dh2[mt]);
-        dh2[mt] = mfma(w[1], b[1], dh2[mt]);
-        dh2[mt] = mfma(w[2], b[2], dh2[mt]);
-        dh2[mt] = mfma(w[3], b[3], dh2[mt]);
-      }
+      for (int mt = 0; mt < 8; ++mt) dh[mt] = zero;
+      dh2[0] = zero;
+      dh2[1] = zero;
     }
+    if constexpr (s < 88) {
+      constexpr int T = s / 11, u = s % 11;
+      if constexpr (u == 0) bT = w;
+      else if constexpr (u <= 8) dh[u - 1] = mfma4(w, bT, dh[u - 1]);
+      else dh2[u - 9] = mfma4(w, bT, dh2[u - 9]);
+      (void)T;
+    } else if constexpr (s < 112) {
+      constexpr int mt = (s - 88) / 3, u = (s - 88) % 3;
+      if constexpr (u == 0) {
+        pre = w;
+      } else {
+        pre = mfma4(w, rb[u - 1], pre);
+        if constexpr (u == 2) {
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) dh[mt][q] *= silu_prime(pre[mt][q] + A.b0[which][16 * mt + g + 4 * q]);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime(pre2[mt][q] + A.eb0[which][16 * mt + g + 4 * q]);
-#pragma unroll
-    for (int T = 0; T < 8; ++T)
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const v4d w = wload(A.w0tp[which], 8, mt, T, lane);
-        drb[mt] = mfma(w[0], dh[T][0], drb[mt]);
-        drb[mt] = mfma(w[1], dh[T][1], drb[mt]);
-        drb[mt] = mfma(w[2], dh[T][2], drb[mt]);
-        drb[mt] = mfma(w[3], dh[T][3], drb[mt]);
+          for (int q = 0; q < 4; ++q) dh[mt][q] *= silu_prime(pre[q]);
+        }
       }
+    } else if constexpr (s < 115) {
+      if constexpr (s < 114) {
+        pre2[s - 112] = w;
+      } else {
 #pragma unroll
-    for (int T = 0; T < 2; ++T) {
-      const v4d w = wload(A.e0tp[which], 2, 0, T, lane);
-      dsa = mfma(w[0], dh2[T][0], dsa);
-      dsa = mfma(w[1], dh2[T][1], dsa);
-      dsa = mfma(w[2], dh2[T][2], dsa);
-      dsa = mfma(w[3], dh2[T][3], dsa);
+        for (int mt = 0; mt < 2; ++mt) {
+          pre2[mt] = mfma(w[mt], sg, pre2[mt]);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime(pre2[mt][q]);
+        }
+      }
+    } else if constexpr (s < 131) {
+      drb[(s - 115) % 2] = mfma4(w, dh[(s - 115) / 2], drb[(s - 115) % 2]);
+    } else {
+      dsa = mfma4(w, dh2[s - 131], dsa);
     }
-  }
+  });
+
   // dE/dr: Bernstein derivative (zero where the clamp is active) + cutoff
   double part = 0.0;
   if (xb > 1e-6 && xb < 1.0 - 1e-6) {
@@ -531,7 +615,7 @@ __global__ __launch_bounds__(256) void k_filter_bwd_mfma(const int *n_active, co
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
-      part += drb[t >> 2][t & 3] * rb[t] * (-A.gamma * A.rbf_k[ch] + A.rbf_kr[ch] * q);
+      part += drb[t >> 2][t & 3] * rb[t >> 2][t & 3] * (-A.gamma * A.rbf_k[ch] + A.rbf_kr[ch] * q);
     }
   }
   part += __shfl_xor(part, 16, kWave);
@@ -1285,6 +1369,20 @@ std::vector<double> transpose(const std::vector<double> &w, std::size_t rows, st
 // P[mt][T][lane][v] = W[16 mt + lane % 16][16 T + lane / 16 + 4 v] (K a
 // multiple of 16), or P[mt][lane] = W[16 mt + lane % 16][lane / 16] for K = 4.
 // Rows beyond M (padding to a multiple of 16) are zero.
+// Bias b (length M) in MFMA accumulator order: P[mt][lane][r] = b[16 mt +
+// lane / 16 + 4 r] (zero beyond M), so a D tile starts from its bias.
+std::vector<double> bias_acc(const std::vector<double> &b, std::size_t M) {
+  const std::size_t MT = (M + 15) / 16;
+  std::vector<double> p(MT * 64 * 4, 0.0);
+  for (std::size_t mt = 0; mt < MT; ++mt)
+    for (std::size_t lane = 0; lane < 64; ++lane)
+      for (std::size_t r = 0; r < 4; ++r) {
+        const std::size_t row = 16 * mt + lane / 16 + 4 * r;
+        if (row < M) p[(mt * 64 + lane) * 4 + r] = b[row];
+      }
+  return p;
+}
+
 std::vector<double> permute_mfma(const std::vector<double> &w, std::size_t M, std::size_t K) {
   const std::size_t MT = (M + 15) / 16;
   if (K == 4) {
@@ -1392,6 +1490,21 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
       B.w0tp[k] = up(permute_mfma(transpose(w0, F, R), R, F));
       B.e1tp[k] = up(permute_mfma(transpose(e1, F, FH), FH, F));
       B.e0tp[k] = up(permute_mfma(transpose(e0, FH, 4), 4, FH));
+      const auto b0 = m.f64(f + "mlp_rbf.0.bias", {F});
+      const auto eb0 = m.f64(f + "mlp_ev.0.bias", {FH});
+      auto ob1 = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F});
+      const auto eb1 = m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F});
+      for (int c = 0; c < F; ++c) ob1[c] += eb1[c];  // both branches add into one output
+      B.b0p[k] = up(bias_acc(b0, F));
+      B.eb0p[k] = up(bias_acc(eb0, FH));
+      B.ob1p[k] = up(bias_acc(ob1, F));
+      const auto e0p = permute_mfma(e0, FH, 4);  // two tiles, one value per lane each
+      std::vector<double> e0pk(64 * 4, 0.0);
+      for (int lane = 0; lane < 64; ++lane) {
+        e0pk[lane * 4 + 0] = e0p[lane];
+        e0pk[lane * 4 + 1] = e0p[64 + lane];
+      }
+      B.e0pk[k] = up(e0pk);
     }
     B.att_cg = up(m.f64(at + "so3_conv_invariants.cg_rep", {24}));
     B.int_cg = up(m.f64(p + "interaction_block.so3_conv_invariants.cg_rep", {24}));
@@ -1644,6 +1757,19 @@ void Evaluator::compute_host(const double *x_rows, int flags, double *f, double 
   HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
+namespace {
+FilterMfma filter_mfma(const BlockWeights &B, const HeadWeights &H, double gamma) {
+  FilterMfma FM;
+  for (int k = 0; k < 2; ++k) {
+    FM.w0p[k] = B.w0p[k]; FM.w1p[k] = B.w1p[k]; FM.e1p[k] = B.e1p[k];
+    FM.w1tp[k] = B.w1tp[k]; FM.w0tp[k] = B.w0tp[k]; FM.e1tp[k] = B.e1tp[k]; FM.e0tp[k] = B.e0tp[k];
+    FM.b0p[k] = B.b0p[k]; FM.eb0p[k] = B.eb0p[k]; FM.ob1p[k] = B.ob1p[k]; FM.e0pk[k] = B.e0pk[k];
+  }
+  FM.att_cg = B.att_cg; FM.rbf_b = H.rbf_b; FM.rbf_k = H.rbf_k; FM.rbf_kr = H.rbf_kr; FM.gamma = gamma;
+  return FM;
+}
+}  // namespace
+
 void Evaluator::compute_device(const double *x, int flags, double *f_out, double *eatom_out, double *energy,
                                double *virial) {
   if (!topology_ready_) throw std::logic_error("SO3LR: compute called before set_topology");
@@ -1796,13 +1922,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
-    FilterMfma FM;
-    for (int k = 0; k < 2; ++k) {
-      FM.w0p[k] = B.w0p[k]; FM.b0[k] = B.fb0[k]; FM.w1p[k] = B.w1p[k]; FM.b1[k] = B.fb1[k];
-      FM.e0p[k] = B.e0p[k]; FM.eb0[k] = B.feb0[k]; FM.e1p[k] = B.e1p[k]; FM.eb1[k] = B.feb1[k];
-      FM.w1tp[k] = B.w1tp[k]; FM.w0tp[k] = B.w0tp[k]; FM.e1tp[k] = B.e1tp[k]; FM.e0tp[k] = B.e0tp[k];
-    }
-    FM.att_cg = B.att_cg; FM.rbf_b = hw_.rbf_b; FM.rbf_k = hw_.rbf_k; FM.rbf_kr = hw_.rbf_kr; FM.gamma = gamma_;
+    const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     timed("filter_fwd", 0, [&] {
       if (naive_filters_)
         hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
@@ -1870,13 +1990,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       hipLaunchKernelGGL(k_attn_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, qb, pfb, pY, pfc,
                          pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
     });
-    FilterMfma FM;
-    for (int k = 0; k < 2; ++k) {
-      FM.w0p[k] = B.w0p[k]; FM.b0[k] = B.fb0[k]; FM.w1p[k] = B.w1p[k]; FM.b1[k] = B.fb1[k];
-      FM.e0p[k] = B.e0p[k]; FM.eb0[k] = B.feb0[k]; FM.e1p[k] = B.e1p[k]; FM.eb1[k] = B.feb1[k];
-      FM.w1tp[k] = B.w1tp[k]; FM.w0tp[k] = B.w0tp[k]; FM.e1tp[k] = B.e1tp[k]; FM.e0tp[k] = B.e0tp[k];
-    }
-    FM.att_cg = B.att_cg; FM.rbf_b = hw_.rbf_b; FM.rbf_k = hw_.rbf_k; FM.rbf_kr = hw_.rbf_kr; FM.gamma = gamma_;
+    const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     timed("filter_bwd", 0, [&] {
       if (naive_filters_)
         hipLaunchKernelGGL(k_filter_bwd, dim3(gP), dim3(128), 0, s, nact, pr, pfc, psb, df, dfc, A, rc_, ds, dr);
