@@ -640,137 +640,188 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
 // the permuted order k = 16 T + g + 4 v (zero beyond K); W is pre-permuted
 // (permute_mfma) and zero-padded to 16-row tiles and 16-column K chunks.
 // EPI 0: out = acc + bias; 1: out = pre, out2 = silu(pre); 2: out = acc + bias
-// + aux; 3: out = acc * silu'(aux).
-template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const double *X, int ldx,
-                                              const double *Wp, const double *bias, double *out, int ldo,
-                                              double *out2, const double *aux, int ldaux) {
+// + aux; 3: out = acc * silu'(aux).  The bias comes in accumulator order
+// (bias_acc) and starts the accumulators.  Output tiles are taken MG at a
+// time; per tile group the operand stream holds, per K chunk, the X chunk and
+// the MG weight fragments.
+template <int EPI, int KT, int MT>
+__global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const double *__restrict__ X, int ldx,
+                                              const double *__restrict__ Wp, const double *__restrict__ biasp,
+                                              double *__restrict__ out, int ldo, double *__restrict__ out2,
+                                              const double *__restrict__ aux, int ldaux) {
+  constexpr int MG = MT <= 10 ? MT : 10;
+  static_assert(MT % MG == 0, "output tiles must split into equal groups");
+  constexpr int NG = MT / MG, PER_T = 1 + MG, PER_G = KT * PER_T;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w * 16 >= rows) return;
   const int n = w * 16 + j;
   const bool valid = n < rows;
   const int nn = valid ? n : rows - 1;
-  const int KT = (K + 15) / 16, MT = (O + 15) / 16;
   const double *xr = X + std::size_t(nn) * ldx;
-  for (int mt0 = 0; mt0 < MT; mt0 += 4) {
-    const int mcount = MT - mt0 < 4 ? MT - mt0 : 4;
-    v4d acc[4] = {v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}};
-    for (int T = 0; T < KT; ++T) {
-      double b[4];
+  const v4d zero = v4d{0, 0, 0, 0};
+
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, grp = S / PER_G, s = S % PER_G, T = s / PER_T, u = s % PER_T;
+    if constexpr (u == 0) {
+      v4d b;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int k = 16 * T + g + 4 * v;
-        b[v] = k < K ? xr[k] : 0.0;
+        b[v] = (16 * T + 16 <= K || k < K) ? xr[k] : 0.0;
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q >= mcount) break;
-        const v4d wv = wload(Wp, KT, mt0 + q, T, lane);
-        acc[q] = mfma(wv[0], b[0], acc[q]);
-        acc[q] = mfma(wv[1], b[1], acc[q]);
-        acc[q] = mfma(wv[2], b[2], acc[q]);
-        acc[q] = mfma(wv[3], b[3], acc[q]);
-      }
+      return b;
+    } else {
+      return wload(Wp, KT, grp * MG + u - 1, T, lane);
     }
-    if (!valid) continue;
+  };
+  Stream<NG * PER_G, kFilterPF, decltype(load)> st(load);
+  v4d acc[MG], xa[MG];
+  auto start_group = [&](int grp) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q >= mcount) break;
+    for (int q = 0; q < MG; ++q) acc[q] = biasp ? tile_load(biasp, grp * MG + q, lane) : zero;
+    if constexpr (EPI == 2 || EPI == 3) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int o = 16 * (mt0 + q) + g + 4 * r;
-        if (o >= O) continue;
-        const std::size_t io = std::size_t(n) * ldo + o;
-        const double v = acc[q][r] + (bias ? bias[o] : 0.0);
-        if (EPI == 0) out[io] = v;
-        if (EPI == 1) { out[io] = v; out2[io] = silu(v); }
-        if (EPI == 2) out[io] = v + aux[std::size_t(n) * ldaux + o];
-        if (EPI == 3) out[io] = v * silu_prime(aux[std::size_t(n) * ldaux + o]);
-      }
+      for (int q = 0; q < MG; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = 16 * (grp * MG + q) + g + 4 * r;
+          xa[q][r] = o < O ? aux[std::size_t(nn) * ldaux + o] : 0.0;
+        }
     }
-  }
+  };
+  start_group(0);
+  st.prime();
+  v4d bT = zero;
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int S = decltype(si)::value, grp = S / PER_G, s = S % PER_G, u = s % PER_T;
+    if constexpr (u == 0) {
+      bT = wv;
+    } else {
+      acc[u - 1] = mfma4(wv, bT, acc[u - 1]);
+    }
+    if constexpr (s == PER_G - 1) {
+      if (valid) {
+#pragma unroll
+        for (int q = 0; q < MG; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o = 16 * (grp * MG + q) + g + 4 * r;
+            if (o >= O) continue;
+            const std::size_t io = std::size_t(n) * ldo + o;
+            const double v = acc[q][r];
+            if constexpr (EPI == 0) out[io] = v;
+            if constexpr (EPI == 1) { out[io] = v; out2[io] = silu(v); }
+            if constexpr (EPI == 2) out[io] = v + xa[q][r];
+            if constexpr (EPI == 3) out[io] = v * silu_prime(xa[q][r]);
+          }
+      }
+      if constexpr (grp + 1 < NG) start_group(grp + 1);
+    }
+  });
 }
 
 // Block-diagonal projections: per head h, the 160 outputs (q k v q_ev k_ev,
 // 32 each) depend on x[h*32 .. h*32+32).  Wp holds, per head, the permuted
-// (160 x 32) matrix; out[n][w*128 + h*32 + o].
-__global__ __launch_bounds__(256) void k_qkv_mfma(int rows, const double *X, const double *Wp, double *out) {
+// (160 x 32) matrix; out[n][w*128 + h*32 + o].  Stream per head: the two
+// input chunks, then the 10 x 2 weight fragments (tile-major).
+__global__ __launch_bounds__(256) void k_qkv_mfma(int rows, const double *__restrict__ X,
+                                                  const double *__restrict__ Wp, double *__restrict__ out) {
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w * 16 >= rows) return;
   const int n = w * 16 + j;
   const bool valid = n < rows;
   const double *xr = X + std::size_t(valid ? n : rows - 1) * kF;
-  for (int h = 0; h < kHeads; ++h) {
-    double b[8];
+  constexpr int PER_H = 2 + 20;
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H;
+    if constexpr (s < 2) {
+      return v4d{xr[h * kHW + 16 * s + g], xr[h * kHW + 16 * s + g + 4], xr[h * kHW + 16 * s + g + 8],
+                 xr[h * kHW + 16 * s + g + 12]};
+    } else {
+      return wload(Wp + std::size_t(h) * 160 * kHW, 2, (s - 2) / 2, (s - 2) % 2, lane);
+    }
+  };
+  Stream<kHeads * PER_H, kFilterPF, decltype(load)> st(load);
+  st.prime();
+  const v4d zero = v4d{0, 0, 0, 0};
+  v4d b[2] = {zero, zero}, acc[10];
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H;
+    if constexpr (s < 2) {
+      b[s] = wv;
+      if constexpr (s == 0) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) b[t] = xr[h * kHW + 16 * (t >> 2) + g + 4 * (t & 3)];
-    const double *Wh = Wp + std::size_t(h) * 160 * kHW;
-    v4d acc[10];
+        for (int mt = 0; mt < 10; ++mt) acc[mt] = zero;
+      }
+    } else {
+      constexpr int mt = (s - 2) / 2, T = (s - 2) % 2;
+      acc[mt] = mfma4(wv, b[T], acc[mt]);
+    }
+    if constexpr (s == PER_H - 1) {
+      if (valid) {
 #pragma unroll
-    for (int mt = 0; mt < 10; ++mt) {
-      acc[mt] = v4d{0, 0, 0, 0};
+        for (int mt = 0; mt < 10; ++mt)
 #pragma unroll
-      for (int T = 0; T < 2; ++T) {
-        const v4d wv = wload(Wh, 2, mt, T, lane);
-        acc[mt] = mfma(wv[0], b[4 * T + 0], acc[mt]);
-        acc[mt] = mfma(wv[1], b[4 * T + 1], acc[mt]);
-        acc[mt] = mfma(wv[2], b[4 * T + 2], acc[mt]);
-        acc[mt] = mfma(wv[3], b[4 * T + 3], acc[mt]);
+          for (int r = 0; r < 4; ++r) {
+            const int o = 16 * mt + g + 4 * r;  // 0..159 = projection * 32 + channel
+            out[std::size_t(n) * 640 + (o >> 5) * kF + h * kHW + (o & 31)] = acc[mt][r];
+          }
       }
     }
-    if (!valid) continue;
-#pragma unroll
-    for (int mt = 0; mt < 10; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int o = 16 * mt + g + 4 * r;  // 0..159 = projection * 32 + channel
-        out[std::size_t(n) * 640 + (o >> 5) * kF + h * kHW + (o & 31)] = acc[mt][r];
-      }
-  }
+  });
 }
 
 // dx[n][h*32 + k] = base[n][.] + sum_{w,o} W[w][h][k][o] g[n][w*128 + h*32 + o];
 // per head the permuted transpose (32 x 160), K read in the permuted order
-// from the 160 gradient entries of that head.
-__global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *G, const double *Wtp,
-                                                      const double *base, double *dx) {
+// from the 160 gradient entries of that head.  Stream per head and K chunk:
+// the gradient chunk, then the two weight fragments.
+__global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *__restrict__ G,
+                                                      const double *__restrict__ Wtp, const double *__restrict__ base,
+                                                      double *__restrict__ dx) {
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w * 16 >= rows) return;
   const int n = w * 16 + j;
   const bool valid = n < rows;
   const double *gr = G + std::size_t(valid ? n : rows - 1) * 640;
-  for (int h = 0; h < kHeads; ++h) {
-    const double *Wh = Wtp + std::size_t(h) * kHW * 160;
-    v4d acc[2] = {v4d{0, 0, 0, 0}, v4d{0, 0, 0, 0}};
-#pragma unroll
-    for (int T = 0; T < 10; ++T) {
-      double b[4];
+  constexpr int PER_H = 10 * 3;
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H, T = s / 3, u = s % 3;
+    if constexpr (u == 0) {
+      v4d b;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int k = 16 * T + g + 4 * v;  // projection * 32 + channel
         b[v] = gr[(k >> 5) * kF + h * kHW + (k & 31)];
       }
+      return b;
+    } else {
+      return wload(Wtp + std::size_t(h) * kHW * 160, 10, u - 1, T, lane);
+    }
+  };
+  Stream<kHeads * PER_H, kFilterPF, decltype(load)> st(load);
+  st.prime();
+  const v4d zero = v4d{0, 0, 0, 0};
+  v4d bT = zero, acc[2];
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H, u = s % 3;
+    if constexpr (s == 0) { acc[0] = zero; acc[1] = zero; }
+    if constexpr (u == 0) bT = wv;
+    else acc[u - 1] = mfma4(wv, bT, acc[u - 1]);
+    if constexpr (s == PER_H - 1) {
+      if (valid) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const v4d wv = wload(Wh, 10, mt, T, lane);
-        acc[mt] = mfma(wv[0], b[0], acc[mt]);
-        acc[mt] = mfma(wv[1], b[1], acc[mt]);
-        acc[mt] = mfma(wv[2], b[2], acc[mt]);
-        acc[mt] = mfma(wv[3], b[3], acc[mt]);
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int c = h * kHW + 16 * mt + g + 4 * r;
+            dx[std::size_t(n) * kF + c] = base[std::size_t(n) * kF + c] + acc[mt][r];
+          }
       }
     }
-    if (!valid) continue;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int c = h * kHW + 16 * mt + g + 4 * r;
-        dx[std::size_t(n) * kF + c] = base[std::size_t(n) * kF + c] + acc[mt][r];
-      }
-  }
+  });
 }
 
 // ---------------------------------------------------------------- attention
@@ -778,6 +829,19 @@ __global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *G,
 // holds the invariant channels 32 h + t and 32 h + 16 + t (t = l % 16) and the
 // equivariant channel off[h] + t of degree h + 1 when t < 2 h + 3, so every
 // per-head sum is a 16-lane group reduction.
+// Workgroups go to the 8 XCDs round-robin (block b on XCD b % 8).  Remapped
+// so that each XCD walks one contiguous range of logical blocks: with nodes
+// in spatial order, the neighbour rows a range gathers stay in its XCD's L2.
+// A bijection of [0, gridDim.x) whatever the grid size.
+__device__ __forceinline__ int xcd_block() {
+#ifdef SO3LR_NO_XCD_MAP
+  return blockIdx.x;
+#endif
+  const int G = gridDim.x, b = blockIdx.x;
+  const int per = G >> 3, rem = G & 7, xcd = b & 7, i = b >> 3;
+  return xcd * per + (xcd < rem ? xcd : rem) + i;
+}
+
 __device__ __forceinline__ double group_sum(double v) {
   v += __shfl_xor(v, 8, kWave);
   v += __shfl_xor(v, 4, kWave);
@@ -787,48 +851,106 @@ __device__ __forceinline__ double group_sum(double v) {
 }
 __device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
 
-__global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, const int *inc,
-                                                  const int *cand2act, const int *pa,
-                                                  const double *x, const double *ev,
-                                                  const double *qkv, const double *pf,
-                                                  const double *pY, const double *pfc,
-                                                  double inv_avg, double *palpha, double *ainv,
-                                                  double *aev) {
+// Active incidence of this step: entry k of a node's list as active pair
+// index * 2 + side (-1 for a candidate beyond the cutoff) and its partner
+// node, so the node-major kernels read their pairs with one coalesced load
+// per 64 entries instead of a chain of dependent lookups.
+__global__ void k_inc_active(int E, const int *inc, const int *cand2act, const int *pa, int *iact, int *iother) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= E) return;
+  const int e = inc[k];
+  const int p = cand2act[e >> 1];
+  iact[k] = p < 0 ? -1 : (p << 1 | (e & 1));
+  iother[k] = p < 0 ? 0 : pa[2 * p + 1 - (e & 1)];
+}
+
+// Walks the active incidence entries of node rows [beg, end) two at a time:
+// body(e1, o1, e2, o2, two) with uniform (scalar) entries; when only one is
+// left, the second repeats the first and `two` is false.  Entries are visited
+// in list order, so sums keep the order of a sequential walk.
+template <class Body>
+__device__ __forceinline__ void for_active_pairs(int beg, int end, const int *iact, const int *iother, int lane,
+                                                 Body &&body) {
+  for (int k0 = beg; k0 < end; k0 += kWave) {
+    const int k = k0 + lane;
+    const int ent = k < end ? iact[k] : -1;
+    const int oth = k < end ? iother[k] : 0;
+    unsigned long long mask = __ballot(ent >= 0);
+    while (mask) {
+      const int l1 = __ffsll(mask) - 1;
+      mask &= mask - 1;
+      const bool two = mask != 0;
+      const int l2 = two ? __ffsll(mask) - 1 : l1;
+      if (two) mask &= mask - 1;
+      body(__builtin_amdgcn_readlane(ent, l1), __builtin_amdgcn_readlane(oth, l1),
+           __builtin_amdgcn_readlane(ent, l2), __builtin_amdgcn_readlane(oth, l2), two);
+    }
+  }
+}
+
+// Attention forward, node-major (kokkos_integrated_block0.cpp:330-385): for
+// node n and every incident active pair p = {n, o}, the edge o -> n gives
+// alpha = <q_n, k_o (.) f_p> / avg (per head) and the messages
+// fc alpha v_o (invariant) and fc alpha_ev Y (equivariant, (-1)^l Y when n is
+// the pair's second endpoint).  Lanes: 16 per head, two channels each.
+__global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, const int *__restrict__ iact,
+                                                  const int *__restrict__ iother, const double *__restrict__ x,
+                                                  const double *__restrict__ ev, const double *__restrict__ qkv,
+                                                  const double *__restrict__ pf, const double *__restrict__ pY,
+                                                  const double *__restrict__ pfc, double inv_avg,
+                                                  double *__restrict__ palpha, double *__restrict__ ainv,
+                                                  double *__restrict__ aev) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int h = lane >> 4, t = lane & 15;
   const int c0 = 32 * h + t, c1 = c0 + 16;
   const bool evv = t < 2 * h + 3;
-  const int m = ev_offset(h) + t;
+  const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
   const double *qn = qkv + std::size_t(n) * 640;
   const double q0 = qn[c0], q1 = qn[c1], qe0 = qn[384 + c0], qe1 = qn[384 + c1];
   double acc0 = 0.0, acc1 = 0.0, acce = 0.0;
-  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
-    const int e = inc[k];
-    const int p = cand2act[e >> 1];
-    if (p < 0) continue;
-    const int side = e & 1;
-    const int o = pa[2 * p + 1 - side];
+  struct Terms { double ai, ae, d0, d1, de; };
+  auto terms = [&](int e, int o) {
+    const int p = e >> 1, side = e & 1;
     const double *ko = qkv + std::size_t(o) * 640;
     const double *fp = pf + 256 * std::size_t(p);
-    const double ai = group_sum(q0 * ko[128 + c0] * fp[c0] + q1 * ko[128 + c1] * fp[c1]) * inv_avg;
-    const double ae = group_sum(qe0 * ko[512 + c0] * fp[128 + c0] + qe1 * ko[512 + c1] * fp[128 + c1]) * inv_avg;
+    const double k0 = ko[128 + c0], k1 = ko[128 + c1], v0 = ko[256 + c0], v1 = ko[256 + c1];
+    const double ke0 = ko[512 + c0], ke1 = ko[512 + c1];
+    const double f0 = fp[c0], f1 = fp[c1], fe0 = fp[128 + c0], fe1 = fp[128 + c1];
     const double fc = pfc[p];
-    acc0 += fc * ai * ko[256 + c0];
-    acc1 += fc * ai * ko[256 + c1];
-    if (evv) acce += fc * ae * pY[kE * std::size_t(p) + m] * (side == 0 ? 1.0 : par);
+    const double y = pY[kE * std::size_t(p) + m] * (side == 0 ? 1.0 : par);
+    Terms T;
+    T.ai = group_sum(q0 * k0 * f0 + q1 * k1 * f1) * inv_avg;
+    T.ae = group_sum(qe0 * ke0 * fe0 + qe1 * ke1 * fe1) * inv_avg;
+    T.d0 = fc * T.ai * v0;
+    T.d1 = fc * T.ai * v1;
+    T.de = fc * T.ae * y;
+    return T;
+  };
+  for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+    const Terms A = terms(e1, o1);
+    const Terms B = terms(e2, o2);
+    acc0 += A.d0; acc1 += A.d1; acce += A.de;
+    if (two) { acc0 += B.d0; acc1 += B.d1; acce += B.de; }
     if (t == 0) {
-      palpha[16 * std::size_t(p) + 8 * side + h] = ai;
-      palpha[16 * std::size_t(p) + 8 * side + 4 + h] = ae;
+      double *al = palpha + 16 * std::size_t(e1 >> 1) + 8 * (e1 & 1);
+      al[h] = A.ai;
+      al[4 + h] = A.ae;
+      if (two) {
+        double *bl = palpha + 16 * std::size_t(e2 >> 1) + 8 * (e2 & 1);
+        bl[h] = B.ai;
+        bl[4 + h] = B.ae;
+      }
     }
-  }
+  });
   const std::size_t i = std::size_t(n) * kF;
   ainv[i + c0] = x[i + c0] + acc0;
   ainv[i + c1] = x[i + c1] + acc1;
   if (evv) aev[std::size_t(n) * kE + m] = ev[std::size_t(n) * kE + m] + acce;
 }
+
 
 // LayerNorm over 128 channels held two per lane (biased variance).
 __device__ __forceinline__ void wave_layer_norm(double v0, double v1, const double *w, const double *b,
@@ -991,7 +1113,7 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
                                             double *dq, double *dhv, double *flr, double *vlr,
                                             double *parts) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int zn = z[n];
   const double qn = q[n], hn = hir[n];
@@ -1043,7 +1165,7 @@ __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, cons
                                                  const double *cref, double *elr, double *dq, double *dhv,
                                                  double *flr, double *vlr, double *parts) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int zn = z[n];
   const double qn = q[n], hn = hir[n];
@@ -1143,24 +1265,25 @@ __global__ __launch_bounds__(256) void k_ln1_bwd(int N, const double *gp, const 
 }
 
 // Attention reverse, node-major (kokkos_attention_scatter_reverse.cpp:280-500).
-// For node n and each pair p = {n, o}: the incoming edge o -> n gives dq_n,
-// the outgoing edge n -> o gives dk_n, dv_n (sender-side terms, gathered here
-// instead of scattered).  The endpoint with side 0 also writes the per-pair
-// adjoints df (both directions), dfc and accumulates dY.  Lane layout as in
-// k_attn_fwd.
-__global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, const int *inc,
-                                                  const int *cand2act, const int *pa, const double *qkv,
-                                                  const double *pf, const double *pY, const double *pfc,
-                                                  const double *palpha, const double *gainv,
-                                                  const double *gaev, double inv_avg, double *gqkv,
-                                                  double *df, double *dfc, double *dY) {
+// For node n and each active pair p = {n, o}: the incoming edge o -> n gives
+// dq_n, the outgoing edge n -> o gives dk_n, dv_n (sender-side terms,
+// gathered here instead of scattered).  The endpoint with side 0 also writes
+// the per-pair adjoints df (both directions), dfc and accumulates dY.  Lane
+// layout as in k_attn_fwd.
+__global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, const int *__restrict__ iact,
+                                                  const int *__restrict__ iother, const double *__restrict__ qkv,
+                                                  const double *__restrict__ pf, const double *__restrict__ pY,
+                                                  const double *__restrict__ pfc, const double *__restrict__ palpha,
+                                                  const double *__restrict__ gainv, const double *__restrict__ gaev,
+                                                  double inv_avg, double *__restrict__ gqkv, double *__restrict__ df,
+                                                  double *__restrict__ dfc, double *__restrict__ dY) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int h = lane >> 4, t = lane & 15;
   const int c0 = 32 * h + t, c1 = c0 + 16;
   const bool evv = t < 2 * h + 3;
-  const int m = ev_offset(h) + t;
+  const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
   const double *me = qkv + std::size_t(n) * 640;
   const double mq0 = me[c0], mq1 = me[c1], mk0 = me[128 + c0], mk1 = me[128 + c1];
@@ -1169,12 +1292,12 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   const double mg0 = gainv[std::size_t(n) * kF + c0], mg1 = gainv[std::size_t(n) * kF + c1];
   const double mge = evv ? gaev[std::size_t(n) * kE + m] : 0.0;
   double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
-  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
-    const int e = inc[k];
-    const int p = cand2act[e >> 1];
-    if (p < 0) continue;
-    const int side = e & 1;
-    const int o = pa[2 * p + 1 - side];
+  struct Terms {
+    double dq0, dq1, dqe0, dqe1, dk0, dk1, dke0, dke1, dv0, dv1;  // node-side contributions
+    double g0, g1, ge0, ge1, fcg, dy;                             // pair adjoints (side 0 only)
+  };
+  auto terms = [&](int e, int o) {
+    const int p = e >> 1, side = e & 1;
     const double *ot = qkv + std::size_t(o) * 640;
     const double oq0 = ot[c0], oq1 = ot[c1], ok0 = ot[128 + c0], ok1 = ot[128 + c1];
     const double ov0 = ot[256 + c0], ov1 = ot[256 + c1], oqe0 = ot[384 + c0], oqe1 = ot[384 + c1];
@@ -1197,26 +1320,45 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     const double coe = group_sum(oge * y_o);
     const double sin_ = fc * ci * inv_avg, sine = fc * ce * inv_avg;
     const double sout = fc * co * inv_avg, soute = fc * coe * inv_avg;
-    dq0 += sin_ * ok0 * fi0; dq1 += sin_ * ok1 * fi1;
-    dqe0 += sine * oke0 * fe0; dqe1 += sine * oke1 * fe1;
-    dk0 += sout * oq0 * fi0; dk1 += sout * oq1 * fi1;
-    dke0 += soute * oqe0 * fe0; dke1 += soute * oqe1 * fe1;
-    dv0 += fc * aout_i * og0; dv1 += fc * aout_i * og1;
-    if (side == 0) {
-      double *d = df + 256 * std::size_t(p);
-      d[c0] = sin_ * mq0 * ok0 + sout * oq0 * mk0;
-      d[c1] = sin_ * mq1 * ok1 + sout * oq1 * mk1;
-      d[128 + c0] = sine * mqe0 * oke0 + soute * oqe0 * mke0;
-      d[128 + c1] = sine * mqe1 * oke1 + soute * oqe1 * mke1;
-      // d/d fc: every head's sum appears in its 16 lanes; take one lane per head
-      const double part = ain_i * ci + ain_e * ce + aout_i * co + aout_e * coe;
-      const double fcg = __shfl(part, 0, kWave) + __shfl(part, 16, kWave) + __shfl(part, 32, kWave) +
-                         __shfl(part, 48, kWave);
-      if (lane == 0) dfc[p] = fcg;
-      // dE/dY_p: edge o->n via y_n (= Y_p), edge n->o via y_o (parity)
-      if (evv) dY[kE * std::size_t(p) + m] += fc * ain_e * mge + par * fc * aout_e * oge;
+    Terms T;
+    T.dq0 = sin_ * ok0 * fi0; T.dq1 = sin_ * ok1 * fi1;
+    T.dqe0 = sine * oke0 * fe0; T.dqe1 = sine * oke1 * fe1;
+    T.dk0 = sout * oq0 * fi0; T.dk1 = sout * oq1 * fi1;
+    T.dke0 = soute * oqe0 * fe0; T.dke1 = soute * oqe1 * fe1;
+    T.dv0 = fc * aout_i * og0; T.dv1 = fc * aout_i * og1;
+    T.g0 = sin_ * mq0 * ok0 + sout * oq0 * mk0;
+    T.g1 = sin_ * mq1 * ok1 + sout * oq1 * mk1;
+    T.ge0 = sine * mqe0 * oke0 + soute * oqe0 * mke0;
+    T.ge1 = sine * mqe1 * oke1 + soute * oqe1 * mke1;
+    // d/d fc: every head's sum appears in its 16 lanes; take one lane per head
+    const double part = ain_i * ci + ain_e * ce + aout_i * co + aout_e * coe;
+    T.fcg = __shfl(part, 0, kWave) + __shfl(part, 16, kWave) + __shfl(part, 32, kWave) + __shfl(part, 48, kWave);
+    // dE/dY_p: edge o->n via y_n (= Y_p), edge n->o via y_o (parity)
+    T.dy = fc * ain_e * mge + par * fc * aout_e * oge;
+    return T;
+  };
+  auto apply = [&](const Terms &T, int e) {
+    dq0 += T.dq0; dq1 += T.dq1;
+    dqe0 += T.dqe0; dqe1 += T.dqe1;
+    dk0 += T.dk0; dk1 += T.dk1;
+    dke0 += T.dke0; dke1 += T.dke1;
+    dv0 += T.dv0; dv1 += T.dv1;
+    if ((e & 1) == 0) {
+      const std::size_t p = std::size_t(e >> 1);
+      double *d = df + 256 * p;
+      d[c0] = T.g0;
+      d[c1] = T.g1;
+      d[128 + c0] = T.ge0;
+      d[128 + c1] = T.ge1;
+      if (lane == 0) dfc[p] = T.fcg;
+      if (evv) dY[kE * p + m] += T.dy;
     }
-  }
+  };
+  // one pair at a time: two in flight need ~190 registers and lose occupancy
+  for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+    apply(terms(e1, o1), e1);
+    if (two) apply(terms(e2, o2), e2);
+  });
   double *g = gqkv + std::size_t(n) * 640;
   g[c0] = dq0; g[c1] = dq1;
   g[128 + c0] = dk0; g[128 + c1] = dk1;
@@ -1225,24 +1367,26 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   g[512 + c0] = dke0; g[512 + c1] = dke1;
 }
 
+
 // g_ev_in = g_aev + sum_pairs 2 (ev_n - ev_o) cg ds[slot]
-__global__ __launch_bounds__(256) void k_ev_bwd(int N, const int *inc_off, const int *inc, const int *cand2act,
-                                                const int *pa, const double *ev, const double *cg,
-                                                const double *ds, const double *gaev, double *gev) {
+__global__ __launch_bounds__(256) void k_ev_bwd(int N, const int *inc_off, const int *__restrict__ iact,
+                                                const int *__restrict__ iother, const double *__restrict__ ev,
+                                                const double *__restrict__ cg, const double *__restrict__ ds,
+                                                const double *__restrict__ gaev, double *__restrict__ gev) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N || lane >= kE) return;
-  const int slot = degree_slot(lane);
-  const double en = ev[std::size_t(n) * kE + lane];
-  double acc = gaev[std::size_t(n) * kE + lane];
-  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
-    const int e = inc[k];
-    const int p = cand2act[e >> 1];
-    if (p < 0) continue;
-    const int o = pa[2 * p + 1 - (e & 1)];
-    acc += 2.0 * (en - ev[std::size_t(o) * kE + lane]) * cg[lane] * ds[4 * std::size_t(p) + slot];
-  }
-  gev[std::size_t(n) * kE + lane] = acc;
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int c = lane < kE ? lane : 0;
+  const int slot = degree_slot(c);
+  const double en = ev[std::size_t(n) * kE + c];
+  double acc = gaev[std::size_t(n) * kE + c];
+  auto term = [&](int e, int o) { return 2.0 * (en - ev[std::size_t(o) * kE + c]) * cg[c] * ds[4 * std::size_t(e >> 1) + slot]; };
+  for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+    const double a = term(e1, o1), b = term(e2, o2);
+    acc += a;
+    if (two) acc += b;
+  });
+  if (lane < kE) gev[std::size_t(n) * kE + lane] = acc;
 }
 
 // ---------------------------------------------------------------- geometry
@@ -1272,12 +1416,18 @@ __global__ __launch_bounds__(256) void k_geom_bwd(const int *n_active, const dou
 
 // forces and per-atom energies: F_a = -g, F_b = +g; each endpoint receives the
 // ZBL energy of the directed edge it receives
+// xn[n] = x[perm[n]] (positions into node order)
+__global__ void k_gather_pos(int N, const int *perm, const double *x, double *xn) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < 3 * N) xn[k] = x[3 * perm[k / 3] + k % 3];
+}
+
 __global__ __launch_bounds__(256) void k_forces(int N, const int *inc_off, const int *inc, const int *cand2act,
                                                 const double *pg, const double *pzbl, const double *flr,
-                                                const double *eatom, const double *elr, double *f,
-                                                double *ezbl, double *etot) {
+                                                const double *eatom, const double *elr, const int *perm,
+                                                double *f, double *ezbl, double *etot) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   double f0 = 0, f1 = 0, f2 = 0, ez = 0;
   for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
@@ -1290,45 +1440,65 @@ __global__ __launch_bounds__(256) void k_forces(int N, const int *inc_off, const
   }
   f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2); ez = wave_sum(ez);
   if (lane == 0) {
-    f[3 * n] = f0 + flr[3 * n];
-    f[3 * n + 1] = f1 + flr[3 * n + 1];
-    f[3 * n + 2] = f2 + flr[3 * n + 2];
+    const int a = perm ? perm[n] : n;  // caller's atom index (node order -> atom order)
+    f[3 * a] = f0 + flr[3 * n];
+    f[3 * a + 1] = f1 + flr[3 * n + 1];
+    f[3 * a + 2] = f2 + flr[3 * n + 2];
     ezbl[n] = ez;
-    etot[n] = eatom[n] + ez + elr[n];
+    etot[a] = eatom[n] + ez + elr[n];
   }
 }
 
 // energy, virial (SR pairs + LR per-node halves), electrostatic and dispersion
 // totals: red[0] E, red[1..6] W, red[7] E_el, red[8] E_disp.  One block.
-__global__ __launch_bounds__(1024) void k_reduce(int N, const int *n_active, const double *etot,
-                                                 const double *pv, const double *pg, const double *vlr,
-                                                 const double *parts, double *red) {
-  __shared__ double part[1024];
+// Energy, virial and energy parts: fixed-order two-stage reduction.  Block b
+// sums a contiguous range of nodes and of active pairs into partial[b][0..9);
+// one block then sums the partials in block order.
+constexpr int kReduceBlocks = 240;
+
+__device__ __forceinline__ void block_sum9(double *acc, double *sh, double *dst) {
+  for (int c = 0; c < 9; ++c) {
+    sh[threadIdx.x] = acc[c];
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+      if (int(threadIdx.x) < st) sh[threadIdx.x] += sh[threadIdx.x + st];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) dst[c] = sh[0];
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void k_reduce_part(int N, const int *n_active, const double *etot,
+                                                     const double *pv, const double *pg, const double *vlr,
+                                                     const double *parts, double *partial) {
+  __shared__ double sh[256];
   double acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
-  for (int i = threadIdx.x; i < N; i += 1024) {
+  const int B = gridDim.x, b = blockIdx.x;
+  const int nper = (N + B - 1) / B, n0 = b * nper, n1 = min(N, n0 + nper);
+  for (int i = n0 + threadIdx.x; i < n1; i += 256) {
     acc[0] += etot[i];
     for (int c = 0; c < 6; ++c) acc[1 + c] += vlr[6 * std::size_t(i) + c];
     acc[7] += parts[2 * i];
     acc[8] += parts[2 * i + 1];
   }
   const int P = *n_active;
-  for (int p = threadIdx.x; p < P; p += 1024) {
+  const int pper = (P + B - 1) / B, p0 = b * pper, p1 = min(P, p0 + pper);
+  for (int p = p0 + threadIdx.x; p < p1; p += 256) {
     const double *v = pv + 3 * std::size_t(p), *g = pg + 3 * std::size_t(p);
     acc[1] -= v[0] * g[0]; acc[2] -= v[1] * g[1]; acc[3] -= v[2] * g[2];
     acc[4] -= 0.5 * (v[0] * g[1] + v[1] * g[0]);
     acc[5] -= 0.5 * (v[0] * g[2] + v[2] * g[0]);
     acc[6] -= 0.5 * (v[1] * g[2] + v[2] * g[1]);
   }
-  for (int c = 0; c < 9; ++c) {
-    part[threadIdx.x] = acc[c];
-    __syncthreads();
-    for (int st = 512; st > 0; st >>= 1) {
-      if (int(threadIdx.x) < st) part[threadIdx.x] += part[threadIdx.x + st];
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) red[c] = part[0];
-    __syncthreads();
-  }
+  block_sum9(acc, sh, partial + 9 * std::size_t(b));
+}
+
+__global__ __launch_bounds__(256) void k_reduce_final(int B, const double *partial, double *red) {
+  __shared__ double sh[256];
+  double acc[9];
+  for (int c = 0; c < 9; ++c) acc[c] = int(threadIdx.x) < B ? partial[9 * threadIdx.x + c] : 0.0;
+  block_sum9(acc, sh, red);
 }
 
 int ceil_div(std::int64_t a, std::int64_t b) { return int((a + b - 1) / b); }
@@ -1519,11 +1689,14 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     B.m1tp = up(permute_mfma(transpose(m1, F, F), F, F)); B.m2tp = up(permute_mfma(transpose(m2, F, F), F, F));
     B.m1b = up(m.f64(p + "mlp_1.1.bias", {F}));
     B.m2b = up(m.f64(p + "mlp_1.3.bias", {F}));
+    B.m1bp = up(bias_acc(m.f64(p + "mlp_1.1.bias", {F}), F));
+    B.m2bp = up(bias_acc(m.f64(p + "mlp_1.3.bias", {F}), F));
     const auto iw = m.f64(p + "interaction_block.linear_layer.weight", {NI, NI});
     B.intw = up(iw); B.intt = up(transpose(iw, NI, NI));
     B.intp = up(permute_mfma(iw, NI, NI));
     B.inttp = up(permute_mfma(transpose(iw, NI, NI), NI, NI));
     B.intb = up(m.f64(p + "interaction_block.linear_layer.bias", {NI}));
+    B.intbp = up(bias_acc(m.f64(p + "interaction_block.linear_layer.bias", {NI}), NI));
   }
   {
     const std::string e = "model.atomic_energy_output_block.", q = "model.partial_charges_output_block.",
@@ -1543,6 +1716,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     b1.insert(b1.end(), qb1.begin(), qb1.end());
     b1.insert(b1.end(), hb1.begin(), hb1.end());
     hw_.b1 = up(b1);
+    hw_.b1p = up(bias_acc(b1, 320));
     hw_.ew2 = up(m.f64(e + "final_layer.weight", {1, F}));
     hw_.eb2 = m.f64(e + "final_layer.bias", {1})[0];
     hw_.escale = up(m.f64(e + "energy_scales.weight", {1, 118}));
@@ -1605,6 +1779,8 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   nb_key_ = buf("nb_key"); nb_idx_ = buf("nb_idx"); nb_skey_ = buf("nb_skey"); nb_sidx_ = buf("nb_sidx");
   nb_cstart_ = buf("nb_cstart"); nb_tmp_ = buf("nb_tmp"); nb_srcnt_ = buf("nb_srcnt"); nb_lrcnt_ = buf("nb_lrcnt");
   nb_err_ = buf("nb_err"); nb_srlist_ = buf("nb_srlist"); nb_poff_ = buf("nb_poff"); sr_code_ = buf("sr_code");
+  perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
+  iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part");
 }
 
 void Evaluator::set_box(const double lo[3], const double hi[3]) {
@@ -1731,6 +1907,7 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
   p_lr_ = std::int64_t(lr_nodes.size() / 2);
   n_rows_ = n_rows;
   shift_mode_ = false;
+  permuted_ = false;
   auto put = [&](Buffer *b, const std::vector<int> &v) {
     HIP_CHECK(hipMemcpyAsync(ensure<int>(b, v.size()), v.data(), v.size() * sizeof(int), hipMemcpyHostToDevice, stream_));
   };
@@ -1776,8 +1953,16 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   const std::int64_t N = n_, P = p_sr_, L = layers_;
   const std::size_t Nz = std::size_t(N), Pz = std::size_t(std::max<std::int64_t>(P, 1));
   hipStream_t s = stream_;
+  // --- node-order inputs (spatial order of the device reneighbor path) ---
+  const int *perm = permuted_ ? static_cast<const int *>(perm_->p) : nullptr;
+  const int *z = static_cast<const int *>((permuted_ ? nz_ : z_)->p);
+  const double *x0 = static_cast<const double *>((permuted_ ? nx0_ : x0_)->p);
+  if (permuted_) {
+    double *xn = static_cast<double *>(xn_->p);
+    hipLaunchKernelGGL(k_gather_pos, dim3(unsigned((3 * Nz + 255) / 256)), dim3(256), 0, s, int(N), perm, x, xn);
+    x = xn;
+  }
   // --- buffers (retained capacity) ---
-  const int *z = ensure<int>(z_, Nz);
   double *xs = ensure<double>(xs_, (L + 1) * Nz * kF);
   double *evs = ensure<double>(evs_, (L + 1) * Nz * kE);
   double *qkv = ensure<double>(qkv_, L * Nz * 640);
@@ -1871,13 +2056,20 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   auto fill = [&](double *p, std::size_t cnt) {
     if (cnt) hipLaunchKernelGGL(k_fill, dim3(unsigned((cnt + 255) / 256)), dim3(256), 0, s, p, cnt, 0.0);
   };
+  // node GEMM shapes (K, O) of the model: 128x128, 132x132, 128->320, 320->128
   auto gemm = [&](int epi, int rows, int K, int O, const double *X, int ldx, const double *Wp, const double *bias,
                   double *out, int ldo, double *out2, const double *aux, int ldaux) {
     const dim3 grid(unsigned(ceil_div(rows, 64)));
-    if (epi == 0) hipLaunchKernelGGL(k_gemm<0>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
-    if (epi == 1) hipLaunchKernelGGL(k_gemm<1>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
-    if (epi == 2) hipLaunchKernelGGL(k_gemm<2>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
-    if (epi == 3) hipLaunchKernelGGL(k_gemm<3>, grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, aux, ldaux);
+#define SO3LR_GEMM(E, KT, MT)                                                                                   \
+  if (epi == E && (K + 15) / 16 == KT && (O + 15) / 16 == MT) {                                                \
+    hipLaunchKernelGGL((k_gemm<E, KT, MT>), grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, \
+                       aux, ldaux);                                                                          \
+    return;                                                                                                   \
+  }
+    SO3LR_GEMM(0, 8, 8) SO3LR_GEMM(0, 9, 9) SO3LR_GEMM(0, 20, 8) SO3LR_GEMM(1, 8, 8) SO3LR_GEMM(1, 8, 20)
+    SO3LR_GEMM(2, 8, 8) SO3LR_GEMM(3, 8, 8)
+#undef SO3LR_GEMM
+    throw std::logic_error("SO3LR: internal error, no node GEMM for this shape");
   };
   const unsigned gN64 = unsigned(std::max(1, ceil_div(N, 64)));
 
@@ -1898,9 +2090,14 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   } else {
     HIP_CHECK(hipMemsetAsync(nact, 0, sizeof(int), s));
   }
+  // active incidence of this step (2 entries per candidate pair)
+  int *iact = ensure<int>(iact_, 2 * Pz), *iother = ensure<int>(iother_, 2 * Pz);
+  if (P > 0)
+    hipLaunchKernelGGL(k_inc_active, dim3(unsigned((2 * Pz + 255) / 256)), dim3(256), 0, s, int(2 * P), sr_inc, c2a,
+                       pa, iact, iother);
   fill(dY, kE * Pz);
   fill(dr, Pz);
-  HIP_CHECK(hipMemcpyAsync(xs, x0_->p, Nz * kF * sizeof(double), hipMemcpyDeviceToDevice, s));
+  HIP_CHECK(hipMemcpyAsync(xs, x0, Nz * kF * sizeof(double), hipMemcpyDeviceToDevice, s));
   fill(evs, Nz * kE);
   const double inv_avg = 1.0 / avg_;
   const unsigned gP = unsigned(std::max<std::int64_t>(P, 1));
@@ -1930,16 +2127,16 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
         hipLaunchKernelGGL(k_filter_fwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, FM, psb, pfb);
     });
     timed("attn_fwd", 1, [&] {
-      hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, xb, evb, qb,
+      hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb,
                          pfb, pY, pfc, inv_avg, pab, ainv, aevb);
     });
     hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
                        n1ib, act);
-    gemm(1, int(N), kF, kF, act, kF, B.m1p, B.m1b, hpb, kF, hid, nullptr, 0);
+    gemm(1, int(N), kF, kF, act, kF, B.m1p, B.m1bp, hpb, kF, hid, nullptr, 0);
     // the MLP output goes to pb = n1 + W2 silu(hpre) + b2
-    gemm(2, int(N), kF, kF, hid, kF, B.m2p, B.m2b, pb, kF, nullptr, n1b, kF);
+    gemm(2, int(N), kF, kF, hid, kF, B.m2p, B.m2bp, pb, kF, nullptr, n1b, kF);
     hipLaunchKernelGGL(k_concat, dim3(gN4), dim3(256), 0, s, int(N), pb, aevb, B.int_cg, cat);
-    gemm(0, int(N), kNI, kNI, cat, kNI, B.intp, B.intb, tb, kNI, nullptr, nullptr, 0);
+    gemm(0, int(N), kNI, kNI, cat, kNI, B.intp, B.intbp, tb, kNI, nullptr, nullptr, 0);
     hipLaunchKernelGGL(k_post2, dim3(gN4), dim3(256), 0, s, int(N), pb, tb, aevb, B.ln2w, B.ln2b, ln_eps_,
                        xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);
   }
@@ -1948,7 +2145,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hw2, hw_.hb2, hw_.hqemb, hw_.hvshift,
              hw_.eb2, hw_.qb2};
   const double *xf = xs + L * Nz * kF;
-  gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1, hhead, 320, hact, nullptr, 0);
+  gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1p, hhead, 320, hact, nullptr, 0);
   hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, hkey, heff, hir);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
   timed("long_range", 1, [&] {
@@ -1987,7 +2184,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     gemm(0, int(N), kF, kF, ghid, kF, B.m1tp, nullptr, gact, kF, nullptr, nullptr, 0);
     hipLaunchKernelGGL(k_ln1_bwd, dim3(gN4), dim3(256), 0, s, int(N), gp, gact, n1b, B.ln1w, n1hb, n1ib, gainv);
     timed("attn_bwd", 1, [&] {
-      hipLaunchKernelGGL(k_attn_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, qb, pfb, pY, pfc,
+      hipLaunchKernelGGL(k_attn_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY, pfc,
                          pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
     });
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
@@ -1998,7 +2195,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
         hipLaunchKernelGGL(k_filter_bwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds, dr);
     });
     hipLaunchKernelGGL(k_qkv_bwd_mfma, dim3(gN64), dim3(256), 0, s, int(N), gqkv, B.qkvtp, gainv, gx);
-    hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pa, evb, B.att_cg, ds,
+    hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, evb, B.att_cg, ds,
                        gaev, gev);
   }
 
@@ -2006,8 +2203,11 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   hipLaunchKernelGGL(k_geom_bwd, dim3(ceil_div(std::max<std::int64_t>(P, 1), 256)), dim3(256), 0, s, nact, pv, pr,
                      dr, pzbl, dY, pg);
   hipLaunchKernelGGL(k_forces, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pg, pzbl, flr, eatom, elr,
-                     fo, ezbl, etot);
-  hipLaunchKernelGGL(k_reduce, dim3(1), dim3(1024), 0, s, int(N), nact, etot, pv, pg, vlr, parts, red);
+                     perm, fo, ezbl, etot);
+  double *partial = ensure<double>(red_part_, 9 * kReduceBlocks);
+  hipLaunchKernelGGL(k_reduce_part, dim3(kReduceBlocks), dim3(256), 0, s, int(N), nact, etot, pv, pg, vlr, parts,
+                     partial);
+  hipLaunchKernelGGL(k_reduce_final, dim3(1), dim3(256), 0, s, kReduceBlocks, partial, red);
   HIP_CHECK(hipGetLastError());
   double host_red[9];
   int host_nact = 0;
@@ -2048,8 +2248,18 @@ void Evaluator::last_terms(double *learned, double *zbl, double *lr, double *cha
                            double *totals, double *image_energy) {
   if (!evaluated_) throw std::logic_error("SO3LR: no evaluation yet");
   const std::size_t Nz = std::size_t(n_);
+  // node-ordered buffers come back in the caller's atom order
+  std::vector<std::vector<double>> staged;
+  std::vector<double *> dests;
   auto get = [&](double *dst, Buffer *b) {
-    if (dst) HIP_CHECK(hipMemcpyAsync(dst, b->p, Nz * sizeof(double), hipMemcpyDeviceToHost, stream_));
+    if (!dst) return;
+    double *into = dst;
+    if (permuted_) {
+      staged.emplace_back(Nz);
+      into = staged.back().data();
+      dests.push_back(dst);
+    }
+    HIP_CHECK(hipMemcpyAsync(into, b->p, Nz * sizeof(double), hipMemcpyDeviceToHost, stream_));
   };
   get(learned, eatom_); get(zbl, ezbl_); get(lr, elr_); get(charges, q_); get(hirshfeld, hir_);
   std::vector<double> et;
@@ -2058,6 +2268,8 @@ void Evaluator::last_terms(double *learned, double *zbl, double *lr, double *cha
     HIP_CHECK(hipMemcpyAsync(et.data(), last_etot_, Nz * sizeof(double), hipMemcpyDeviceToHost, stream_));
   }
   HIP_CHECK(hipStreamSynchronize(stream_));
+  for (std::size_t k = 0; k < dests.size(); ++k)
+    for (std::size_t i = 0; i < Nz; ++i) dests[k][perm_host_[i]] = staged[k][i];
   if (totals) { totals[0] = totals_[0]; totals[1] = totals_[1]; }
   if (image_energy)
     for (std::int64_t k = 0; k < n_images_; ++k) {

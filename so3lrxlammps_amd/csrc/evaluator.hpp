@@ -48,10 +48,12 @@ struct BlockWeights {
   const double *qkvp, *qkvtp;           // per head (160 x 32) and (32 x 160)
   const double *m1p, *m2p, *m1tp, *m2tp;
   const double *intp, *inttp;           // 132 x 132, K padded to 144
+  const double *m1bp, *m2bp, *intbp;    // node-layer biases in accumulator order
 };
 
 struct HeadWeights {
   const double *w1p, *w1tp;  // MFMA operand order: (320 x 128) and its transpose
+  const double *b1p;         // first-layer bias (320) in accumulator order
   const double *w1t;    // (128, 320): energy | charge | Hirshfeld first layers, transposed
   const double *w1;     // (320, 128)
   const double *b1;     // (320)
@@ -156,16 +158,22 @@ class Evaluator {
   Buffer *hhead_, *hkey_, *heff_, *eatom_, *qraw_, *q_, *hir_, *qseed_;
   Buffer *elr_, *dq_, *dh_, *flr_, *vlr_, *elr_parts_, *ezbl_;
   Buffer *gx_, *gev_, *gp_, *gt_, *gcat_, *ghid_, *gact_, *gainv_, *gaev_, *gqkv_, *ghead_;
-  Buffer *fout_, *etot_, *red_;
+  Buffer *fout_, *etot_, *red_, *red_part_;
   // pair-sized buffers
   Buffer *owner_, *sr_rows_, *sr_nodes_, *sr_inc_off_, *sr_inc_, *lr_rows_, *lr_nodes_,
       *lr_inc_off_, *lr_inc_, *blk_count_, *n_active_, *cand2act_;
   Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
   Buffer *df_, *dfc_, *ds_, *dr_, *dY_, *pg_;
+  Buffer *iact_, *iother_;  // per step: incidence entry -> active pair * 2 + side, partner node
   Buffer *xrows_, *fhost_;
   // device reneighbor
   Buffer *nb_key_, *nb_idx_, *nb_skey_, *nb_sidx_, *nb_cstart_, *nb_tmp_, *nb_srcnt_, *nb_lrcnt_, *nb_err_,
       *nb_srlist_, *nb_poff_, *sr_code_;
+  // spatial node order of the device reneighbor path: node n holds owned atom
+  // perm[n]; node-ordered copies of the per-atom inputs
+  Buffer *perm_, *nz_, *nx0_, *xn_;
+  std::vector<int> perm_host_;
+  bool permuted_ = false;
   bool shift_mode_ = false;
   std::int64_t lr_entries_ = 0;
   double box_len_[3] = {0, 0, 0};

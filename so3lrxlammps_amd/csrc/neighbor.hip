@@ -16,6 +16,13 @@
 //      list is used as it is by the node-major LR kernel.
 // Image code c in 0..26 stands for the shift ((c/9)-1, (c/3)%3-1, c%3-1)
 // box lengths added to the neighbour's position.
+//
+// For a single system the evaluator's nodes follow a spatial (Morton) order
+// of the wrapped positions, the device analogue of LAMMPS's periodic atom
+// sort (atom_modify sort): node n is owned atom perm[n].  Neighbour gathers
+// then stay within a compact region, which one XCD's L2 can serve.  Inputs
+// are gathered into node order and forces scattered back, so callers keep
+// their own atom order.
 #include "evaluator.hpp"
 
 #include <hipcub/hipcub.hpp>
@@ -53,6 +60,44 @@ __global__ void k_wrap(int n, double *x, Grid G) {
     if (v < 0.0) v = 0.0;
     x[3 * i + d] = G.lo[d] + v;
   }
+}
+
+// 10-bit spread for a 30-bit Morton key
+__device__ __forceinline__ unsigned spread3(unsigned v) {
+  v &= 1023u;
+  v = (v | (v << 16)) & 0x030000FFu;
+  v = (v | (v << 8)) & 0x0300F00Fu;
+  v = (v | (v << 4)) & 0x030C30C3u;
+  v = (v | (v << 2)) & 0x09249249u;
+  return v;
+}
+
+__device__ __forceinline__ unsigned quantize(double v, double lo, double len) {
+  const double t = (v - lo) / len * 1024.0;
+  return t < 0.0 ? 0u : (t >= 1023.0 ? 1023u : unsigned(t));
+}
+
+__global__ void k_morton(int n, const double *x, Grid G, int *key, int *idx) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const unsigned qx = quantize(x[3 * i], G.lo[0], G.len[0]);
+  const unsigned qy = quantize(x[3 * i + 1], G.lo[1], G.len[1]);
+  const unsigned qz = quantize(x[3 * i + 2], G.lo[2], G.len[2]);
+  key[i] = int((spread3(qx) << 2) | (spread3(qy) << 1) | spread3(qz));
+  idx[i] = i;
+}
+
+__global__ void k_gather_int(int n, const int *perm, const int *src, int *dst) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[perm[i]];
+}
+
+// dst[n][c] = src[perm[n]][c] for rows of `width` doubles
+__global__ void k_gather_rows(int n, int width, const int *perm, const double *src, double *dst) {
+  const std::size_t k = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (k >= std::size_t(n) * width) return;
+  const std::size_t row = k / width, c = k % width;
+  dst[k] = src[std::size_t(perm[row]) * width + c];
 }
 
 __device__ __forceinline__ int cell_coord(double v, double lo, double len, int nc) {
@@ -241,13 +286,35 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   int *key = ensure<int>(nb_key_, n), *idx = ensure<int>(nb_idx_, n);
   int *skey = ensure<int>(nb_skey_, n), *sidx = ensure<int>(nb_sidx_, n);
   int *cstart = ensure<int>(nb_cstart_, ncell + 1);
-  hipLaunchKernelGGL(k_cell_keys, dim3((n + 255) / 256), dim3(256), 0, s, n, x, G, key, idx);
-  std::size_t tmp_bytes = 0;
+  const unsigned gb = unsigned((n + 255) / 256);
+  auto sort_pairs = [&](int *k_in, int *k_out, int *v_in, int *v_out, int bits) {
+    std::size_t tmp_bytes = 0;
+    NB_CHECK(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, k_in, k_out, v_in, v_out, n, 0, bits, s));
+    void *tmp = ensure<char>(nb_tmp_, tmp_bytes);
+    NB_CHECK(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, k_in, k_out, v_in, v_out, n, 0, bits, s));
+  };
+  // node order: Morton order of the wrapped positions (one system only: the
+  // per-image charge correction of packed images needs contiguous images)
+  const bool reorder = n_images_ == 1;
+  if (reorder) {
+    int *perm = ensure<int>(perm_, n);
+    hipLaunchKernelGGL(k_morton, dim3(gb), dim3(256), 0, s, n, x, G, key, idx);
+    sort_pairs(key, skey, idx, perm, 30);
+    double *xn = ensure<double>(xn_, 3 * std::size_t(n));
+    hipLaunchKernelGGL(k_gather_rows, dim3(unsigned((3 * std::size_t(n) + 255) / 256)), dim3(256), 0, s, n, 3, perm,
+                       x, xn);
+    hipLaunchKernelGGL(k_gather_int, dim3(gb), dim3(256), 0, s, n, perm, static_cast<const int *>(z_->p),
+                       ensure<int>(nz_, n));
+    hipLaunchKernelGGL(k_gather_rows, dim3(unsigned((std::size_t(n) * kF + 255) / 256)), dim3(256), 0, s, n, kF,
+                       perm, static_cast<const double *>(x0_->p), ensure<double>(nx0_, std::size_t(n) * kF));
+    perm_host_.resize(n);
+    NB_CHECK(hipMemcpyAsync(perm_host_.data(), perm, std::size_t(n) * sizeof(int), hipMemcpyDeviceToHost, s));
+    x = xn;  // the lists below are built in node order
+  }
+  hipLaunchKernelGGL(k_cell_keys, dim3(gb), dim3(256), 0, s, n, x, G, key, idx);
   int bits = 1;
   while ((1 << bits) < ncell + 1) ++bits;
-  NB_CHECK(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, key, skey, idx, sidx, n, 0, bits, s));
-  void *tmp = ensure<char>(nb_tmp_, tmp_bytes);
-  NB_CHECK(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, skey, idx, sidx, n, 0, bits, s));
+  sort_pairs(key, skey, idx, sidx, bits);
   hipLaunchKernelGGL(k_cell_start, dim3((n + 1 + 255) / 256), dim3(256), 0, s, n, ncell, skey, cstart);
   int *sr_cnt = ensure<int>(nb_srcnt_, n), *lr_cnt = ensure<int>(nb_lrcnt_, n);
   int *err = ensure<int>(nb_err_, 1);
@@ -290,6 +357,7 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   p_lr_ = totals[1] / 2;
   lr_entries_ = totals[1];
   for (int d = 0; d < 3; ++d) box_len_[d] = G.len[d];
+  permuted_ = reorder;
   shift_mode_ = true;
   topology_ready_ = true;
   evaluated_ = false;

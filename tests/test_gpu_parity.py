@@ -146,21 +146,30 @@ def test_device_reneighbor_matches_rows_path(orc):
     lists = Lists(np.mod(moved, box), np.zeros(3), box, (1, 1, 1))
     c.set_topology(lists)
     e1, f1, ea1, w1 = c.compute(lists.rows_positions(np.mod(moved, box)))
+    t1 = c.terms()
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(stream):
         xt = torch.tensor(moved, dtype=torch.float64, device=dev)
         ft = torch.zeros_like(xt)
+        eat = torch.zeros(len(z), dtype=torch.float64, device=dev)
         c.reneighbor_device(xt, np.zeros(3), box, (1, 1, 1), 1.0, stream=stream.cuda_stream)
-        e2, w2 = c.compute_device(xt, ft, stream=stream.cuda_stream)
+        e2, w2 = c.compute_device(xt, ft, eat, stream=stream.cuda_stream)
         stream.synchronize()
         wrapped = xt.cpu().numpy()
         f2 = ft.cpu().numpy()
+        ea2 = eat.cpu().numpy()
+    t2 = c.terms()
     assert np.all(wrapped >= 0) and np.all(wrapped < box)
     assert np.abs(wrapped - np.mod(moved, box)).max() < 1e-12
     assert abs(e1 - e2) <= 1e-12 * abs(e1)
     assert np.abs(f1 - f2).max() <= 1e-11
     assert np.abs(w1 - w2).max() <= 1e-10 * max(1.0, np.abs(w1).max())
+    # per-atom outputs come back in the caller's atom order (the device path
+    # evaluates in its own spatial node order)
+    assert np.abs(ea1 - ea2).max() <= 1e-12
+    for key in ("learned", "zbl", "long_range", "charges", "hirshfeld"):
+        assert np.abs(t1[key] - t2[key]).max() <= 1e-12, key
     sr_active, sr_cand, lr_cand = c.graph_stats()
     assert sr_cand == len(lists.lists[0][2]) // 2 and lr_cand == len(lists.lists[1][2])
     sr, lr = support.build_graphs(np.mod(moved, box), box)
