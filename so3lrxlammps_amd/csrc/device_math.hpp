@@ -15,6 +15,9 @@ namespace so3lr_amd {
 struct LrParams {
   double ke, sigma, cutoff, cuton_el, fine_factor, bohr, hartree, disp_scale, cuton_disp, full_scale;
   double shift, fshift;  // shifted-force constants at the cutoff
+  // reciprocals of the constants above: 1/sigma, 1/bohr, 2/(sqrt(pi) sigma),
+  // 1/(cutoff - cuton) of both switches
+  double inv_sigma, inv_bohr, two_over_sqrtpi_sigma, inv_w_el, inv_w_disp;
   int n_ref;
 };
 
@@ -145,27 +148,48 @@ struct LrPairTerms {
   double e_el, e_disp, pref, dh_self, radial;
 };
 
-// Coulomb + QDO dispersion for one unique pair seen from atom "i" (self).
-// dh_self = dE/dh_i; pref * q_j = dE/dq_i.  Returns false outside the cutoff.
+// bump_switch with 1 / (off - on) given, three reciprocals instead of seven
+// divisions (same function; rounding differs in the last bits).
+__device__ __forceinline__ void bump_switch_fast(double r, double on, double off, double inv_w, double &val,
+                                                 double &der) {
+  if (r >= off) { val = 0.0; der = 0.0; return; }
+  const double c = (r - on) * inv_w;
+  const double left = 1.0 - c, right = c;
+  const double isl = 1.0 / (left > 1e-12 ? left : 1e-12), isr = 1.0 / (right > 1e-12 ? right : 1e-12);
+  const double el = left > 0.0 ? exp(-isl) : 0.0;
+  const double er = right > 0.0 ? exp(-isr) : 0.0;
+  const double den = el + er + 1e-12, iden = 1.0 / den;
+  val = el * iden;
+  const double dl = left > 0.0 ? -el * isl * isl : 0.0;
+  const double dr = right > 0.0 ? er * isr * isr : 0.0;
+  der = (dl * den - el * (dl + dr)) * iden * iden * inv_w;
+}
+
+// Coulomb + QDO dispersion for one unique pair seen from atom "i" (self)
+// (kokkos_physical_long_range.cpp:62-381).  dh_self = dE/dh_i; pref * q_j =
+// dE/dq_i.  Returns false outside the cutoff.  Divisions are shared through
+// reciprocals (1/r, 1/den, 1/s_fit, 1/(7 alpha), 1/d6, 1/d8, 1/d10; 1/gamma =
+// 2 s_fit^2 exactly), alpha^(1/7) as exp(log(alpha) / 7).
 __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *__restrict__ aref,
                                               const double *__restrict__ cref, int zi_, int zj_,
                                               double qi, double qj, double hi, double hj, double r,
                                               LrPairTerms &o) {
   if (!(r > 1e-12) || r >= P.cutoff) return false;
-  const double inv_sqrt_pi = 0.56418958354775628695;
+  const double ir = 1.0 / r;
   double esw, desw;
-  bump_switch(r, P.cuton_el, P.cutoff, esw, desw);
-  const double ratio = r / P.sigma;
+  bump_switch_fast(r, P.cuton_el, P.cutoff, P.inv_w_el, esw, desw);
+  const double ratio = r * P.inv_sigma;
   const double erft = erf(ratio), expt = exp(-ratio * ratio);
-  const double pot = erft / r;
-  const double dpot = (2.0 * r * expt * inv_sqrt_pi / P.sigma - erft) / (r * r);
+  const double pot = erft * ir;
+  const double dpot = (r * expt * P.two_over_sqrtpi_sigma - erft) * ir * ir;
   const double disp = r - P.cutoff;
   const double shifted = pot - P.shift - P.fshift * disp;
   const double kern = esw * (pot - P.shift) + (1.0 - esw) * shifted;
   const double dkern = dpot - (1.0 - esw) * P.fshift + desw * P.fshift * disp;
-  o.e_el = P.full_scale * P.ke * qi * qj * kern;
-  o.pref = P.full_scale * P.ke * kern;
-  o.radial = P.full_scale * P.ke * qi * qj * dkern;
+  const double sk = P.full_scale * P.ke;
+  o.e_el = sk * qi * qj * kern;
+  o.pref = sk * kern;
+  o.radial = sk * qi * qj * dkern;
   o.e_disp = 0.0;
   o.dh_self = 0.0;
   const int zi = zi_ - 1, zj = zj_ - 1;
@@ -177,42 +201,43 @@ __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *_
   const double num = 2.0 * c6i * c6j * aj * ai;
   const double den = ai * ai * c6j + aj * aj * c6i;
   if (!(alpha > 0.0 && den > 1e-30)) return true;
-  const double c6 = num / den;
-  const double idd = 1.0 / (den * den);
+  const double iden = 1.0 / den;
+  const double c6 = num * iden;
   const double dc6i = 2.0 * ci0 * hi;
   const double dn_dhi = 2.0 * (dc6i * c6j * aj * ai + c6i * c6j * aj * ai0);
   const double dd_dhi = 2.0 * ai * ai0 * c6j + aj * aj * dc6i;
-  const double dc6_dhi = (dn_dhi * den - num * dd_dhi) * idd;
+  const double dc6_dhi = (dn_dhi * den - num * dd_dhi) * iden * iden;
   const double b0 = -0.00433008, b1 = 0.24428889, b2 = 0.04125273, b3 = -0.00078893;
-  const double a7 = pow(alpha, 1.0 / 7.0);
+  const double a7 = exp(log(alpha) * (1.0 / 7.0));
+  const double i7a = 1.0 / (7.0 * alpha);
   const double rvdw = P.fine_factor * a7;
   const double sfit = b3 * rvdw * rvdw * rvdw + b2 * rvdw * rvdw + b1 * rvdw + b0;
-  const double gam = 0.5 / (sfit * sfit);
-  const double drvdw = rvdw / (7.0 * alpha);
+  const double isfit = 1.0 / sfit;
+  const double gam = 0.5 * isfit * isfit, igam = 2.0 * sfit * sfit;
+  const double drvdw = rvdw * i7a;
   const double dsfit = (3.0 * b3 * rvdw * rvdw + 2.0 * b2 * rvdw + b1) * drvdw;
-  const double dgam = -2.0 * gam * dsfit / sfit;
-  const double c8 = 5.0 * c6 / gam, c10 = 245.0 * c6 / (8.0 * gam * gam);
+  const double dgam = -2.0 * gam * dsfit * isfit;
+  const double c8 = 5.0 * c6 * igam, c10 = (245.0 / 8.0) * c6 * igam * igam;
   const double damp = P.disp_scale * 2.0 * 2.54 * a7;
-  const double ddamp = damp / (7.0 * alpha);
-  const double ra = r / P.bohr;
+  const double ddamp = damp * i7a;
+  const double ra = r * P.inv_bohr;
   const double r2 = ra * ra, r4 = r2 * r2, r6 = r4 * r2, r8 = r4 * r4, r10 = r8 * r2;
   const double p2 = damp * damp, p4 = p2 * p2, p6 = p4 * p2, p8 = p4 * p4, p10 = p8 * p2;
-  const double d6 = r6 + p6, d8 = r8 + p8, d10 = r10 + p10;
-  const double qdo = -c6 / d6 - c8 / d8 - c10 / d10;
-  const double rad_au = 6.0 * c6 * r4 * ra / (d6 * d6) + 8.0 * c8 * r6 * ra / (d8 * d8) +
-                        10.0 * c10 * r8 * ra / (d10 * d10);
-  const double dc8 = -c8 * dgam / gam, dc10 = -2.0 * c10 * dgam / gam;
+  const double i6 = 1.0 / (r6 + p6), i8 = 1.0 / (r8 + p8), i10 = 1.0 / (r10 + p10);
+  const double qdo = -c6 * i6 - c8 * i8 - c10 * i10;
+  const double rad_au = (6.0 * c6 * r4 * i6 * i6 + 8.0 * c8 * r6 * i8 * i8 + 10.0 * c10 * r8 * i10 * i10) * ra;
+  const double dc8 = -c8 * dgam * igam, dc10 = -2.0 * c10 * dgam * igam;
   const double dd6 = 6.0 * p4 * damp * ddamp, dd8 = 8.0 * p6 * damp * ddamp,
                dd10 = 10.0 * p8 * damp * ddamp;
-  const double dqdo_da = c6 * dd6 / (d6 * d6) - dc8 / d8 + c8 * dd8 / (d8 * d8) - dc10 / d10 +
-                         c10 * dd10 / (d10 * d10);
-  const double dqdo_dc6 = -1.0 / d6 - (5.0 / gam) / d8 - (245.0 / (8.0 * gam * gam)) / d10;
+  const double dqdo_da = c6 * dd6 * i6 * i6 - dc8 * i8 + c8 * dd8 * i8 * i8 - dc10 * i10 + c10 * dd10 * i10 * i10;
+  const double dqdo_dc6 = -i6 - 5.0 * igam * i8 - (245.0 / 8.0) * igam * igam * i10;
   const double dpi = dqdo_dc6 * dc6_dhi + dqdo_da * 0.5 * ai0;
   double dsw, ddsw;
-  bump_switch(r, P.cuton_disp, P.cutoff, dsw, ddsw);
-  o.e_disp = P.full_scale * P.hartree * qdo * dsw;
-  o.radial += P.full_scale * P.hartree * (rad_au * dsw / P.bohr + qdo * ddsw);
-  o.dh_self = P.full_scale * P.hartree * dsw * dpi;
+  bump_switch_fast(r, P.cuton_disp, P.cutoff, P.inv_w_disp, dsw, ddsw);
+  const double sh = P.full_scale * P.hartree;
+  o.e_disp = sh * qdo * dsw;
+  o.radial += sh * (rad_au * dsw * P.inv_bohr + qdo * ddsw);
+  o.dh_self = sh * dsw * dpi;
   return true;
 }
 

@@ -1756,6 +1756,11 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     lr_.fshift = (2.0 * lr_.cutoff * cexp * 0.56418958354775628695 / lr_.sigma - cerf) / (lr_.cutoff * lr_.cutoff);
   }
   lr_.n_ref = hw_.n_ref;
+  lr_.inv_sigma = 1.0 / lr_.sigma;
+  lr_.inv_bohr = 1.0 / lr_.bohr;
+  lr_.two_over_sqrtpi_sigma = 2.0 * 0.56418958354775628695 / lr_.sigma;
+  lr_.inv_w_el = 1.0 / (lr_.cutoff - lr_.cuton_el);
+  lr_.inv_w_disp = 1.0 / (lr_.cutoff - lr_.cuton_disp);
 
   z_ = buf("z"); x0_ = buf("x0"); img_of_node_ = buf("img"); img_off_ = buf("img_off"); img_q_ = buf("img_q");
   xs_ = buf("xs"); evs_ = buf("evs"); qkv_ = buf("qkv"); aev_ = buf("aev"); n1_ = buf("n1");
