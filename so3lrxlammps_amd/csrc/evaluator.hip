@@ -34,18 +34,37 @@ namespace {
 constexpr int kWave = 64;
 constexpr int kCompactPerBlock = 1024;  // candidates per compaction block (256 threads x 4)
 
-__device__ __forceinline__ double half_sum(double v) {
-  // sum over the 32-lane half of the wavefront this lane belongs to
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 8, kWave);
-  v += __shfl_xor(v, 4, kWave);
-  v += __shfl_xor(v, 2, kWave);
-  v += __shfl_xor(v, 1, kWave);
+// DPP lane permute of a double within the 16-lane rows of a wavefront (two
+// 32-bit moves).  CTRL: 0xB1 quad_perm(1,0,3,2), 0x4E quad_perm(2,3,0,1),
+// 0x141 row_half_mirror, 0x140 row_mirror.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = unsigned(__builtin_amdgcn_update_dpp(0, int(unsigned(b)), CTRL, 0xF, 0xF, false));
+  const unsigned hi = unsigned(__builtin_amdgcn_update_dpp(0, int(unsigned(b >> 32)), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(double, (unsigned long long)lo | ((unsigned long long)hi << 32));
+}
+// value of v in lane l (uniform)
+__device__ __forceinline__ double lane_read(double v, int l) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = unsigned(__builtin_amdgcn_readlane(int(unsigned(b)), l));
+  const unsigned hi = unsigned(__builtin_amdgcn_readlane(int(unsigned(b >> 32)), l));
+  return __builtin_bit_cast(double, (unsigned long long)lo | ((unsigned long long)hi << 32));
+}
+// Sum over the 16-lane row this lane belongs to (quads, then half-rows, then
+// rows, each step adding the mirrored partner): every lane of the row ends
+// with the same bits.  All 64 lanes must be active.
+__device__ __forceinline__ double group_sum(double v) {
+  v += dpp_f64<0xB1>(v);
+  v += dpp_f64<0x4E>(v);
+  v += dpp_f64<0x141>(v);
+  v += dpp_f64<0x140>(v);
   return v;
 }
+// Sum over the wavefront: row sums combined in row order (uniform result).
 __device__ __forceinline__ double wave_sum(double v) {
-  v += __shfl_xor(v, 32, kWave);
-  return half_sum(v);
+  v = group_sum(v);
+  return ((lane_read(v, 0) + lane_read(v, 16)) + lane_read(v, 32)) + lane_read(v, 48);
 }
 __device__ __forceinline__ double pick4(int s, double a, double b, double c, double d) {
   return s == 0 ? a : (s == 1 ? b : (s == 2 ? c : d));
@@ -842,13 +861,6 @@ __device__ __forceinline__ int xcd_block() {
   return xcd * per + (xcd < rem ? xcd : rem) + i;
 }
 
-__device__ __forceinline__ double group_sum(double v) {
-  v += __shfl_xor(v, 8, kWave);
-  v += __shfl_xor(v, 4, kWave);
-  v += __shfl_xor(v, 2, kWave);
-  v += __shfl_xor(v, 1, kWave);
-  return v;
-}
 __device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
 
 // Active incidence of this step: entry k of a node's list as active pair
@@ -1332,7 +1344,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     T.ge1 = sine * mqe1 * oke1 + soute * oqe1 * mke1;
     // d/d fc: every head's sum appears in its 16 lanes; take one lane per head
     const double part = ain_i * ci + ain_e * ce + aout_i * co + aout_e * coe;
-    T.fcg = __shfl(part, 0, kWave) + __shfl(part, 16, kWave) + __shfl(part, 32, kWave) + __shfl(part, 48, kWave);
+    T.fcg = lane_read(part, 0) + lane_read(part, 16) + lane_read(part, 32) + lane_read(part, 48);
     // dE/dY_p: edge o->n via y_n (= Y_p), edge n->o via y_o (parity)
     T.dy = fc * ain_e * mge + par * fc * aout_e * oge;
     return T;
