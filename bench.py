@@ -54,34 +54,51 @@ def traffic_bytes(kernel, config):
     return rec["read_bytes"] + rec["write_bytes"]
 
 
-def cpu_baseline(z, x, box, seconds_budget):
+def cpu_baseline(z, x, box, periodic, images, seconds_budget):
     """Oracle (CPU restatement of the reference math, OpenMP) timed on the
-    host cores: repeated E+F+virial calls on a periodic sub-cube of the same
-    system until about `seconds_budget` seconds of CPU work are done; reports
-    the median call as atom-steps/s."""
+    host cores: repeated E+F+virial calls on a bounded sample of the same
+    workload until about `seconds_budget` seconds of CPU work are done;
+    reports the median call as atom-steps/s."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     from oracle.oracle import Oracle, lib
     import support
     orc = Oracle(MODEL)
-    # sample: every atom of a 40 A cube cut from the system, treated as
-    # periodic with that side (wider than twice the 12 A LR cutoff)
-    side = 40.0
-    sel = np.all(x < side, axis=1)
-    zs, xs = z[sel], x[sel]
-    sr, lr = support.build_graphs(xs, np.full(3, side))
-    orc.evaluate(zs, sr, lr)  # warm-up (page-in, thread pool)
+    kw = {}
+    if images is not None:
+        # the first 64 molecules of the packed batch, with their own (Q, M)
+        offs, qs, ms = images
+        k = min(64, len(qs))
+        zs, xs = z[:offs[k]], x[:offs[k]]
+        kw = dict(image=np.repeat(np.arange(k), np.diff(offs[:k + 1])), image_charge=np.asarray(qs[:k], float),
+                  image_multiplicity=ms[:k])
+        sr, lr = support.build_graphs(xs, None)
+        what = "the first %d molecules of the packed batch (open boundaries)" % k
+    elif not any(periodic):
+        zs, xs = z, x
+        sr, lr = support.build_graphs(xs, None)
+        what = "the whole molecule (open boundaries)"
+    else:
+        # every atom of a 40 A cube cut from the system, treated as periodic
+        # with that side (wider than twice the 12 A LR cutoff)
+        side = 40.0
+        sel = np.all(x < side, axis=1)
+        zs, xs = z[sel], x[sel]
+        sr, lr = support.build_graphs(xs, np.full(3, side))
+        what = "a %.0f A periodic sub-cube of the benchmark system" % side
+        if int(np.sum(zs)) % 2:
+            kw = dict(multiplicity=2.0)  # a cut that leaves an odd electron count
+    orc.evaluate(zs, sr, lr, **kw)  # warm-up (page-in, thread pool)
     times = []
     t_start = time.time()
-    while len(times) < 3 or (time.time() - t_start < seconds_budget and len(times) < 50):
+    while len(times) < 3 or (time.time() - t_start < seconds_budget and len(times) < 1000):
         t0 = time.time()
-        orc.evaluate(zs, sr, lr)
+        orc.evaluate(zs, sr, lr, **kw)
         times.append(time.time() - t0)
     med = float(np.median(times))
     return {"value": len(zs) / med, "unit": "atom-steps/s", "cores": int(lib().orc_num_threads()),
             "kind": "port",
-            "sample": "median of %d E+F+virial calls (%.1f s of CPU work) on %d atoms: a %.0f A periodic "
-                      "sub-cube of the benchmark system, CPU fp64 oracle, OpenMP"
-                      % (len(times), sum(times), len(zs), side)}
+            "sample": "median of %d E+F+virial calls (%.1f s of CPU work) on %d atoms: %s, CPU fp64 oracle, OpenMP"
+                      % (len(times), sum(times), len(zs), what)}
 
 
 def main():
@@ -104,7 +121,18 @@ def main():
     from so3lrxlammps_amd import Context, Lists, systems
 
     log("generating config %d" % args.config)
-    z, x, box, Q, M, desc = systems.config(args.config)
+    images = None
+    if args.config == 2:
+        # 512 independent molecules evaluated together (packed images)
+        z, x, offs, qs, ms, extent = systems.packed_molecules()
+        images = (offs, qs, ms)
+        box, Q, M = np.full(3, extent), None, None
+        desc = "512 molecules of 12-40 atoms (H C N O S), Q in {-1,0,1}, packed images, non-periodic"
+    else:
+        z, x, box, Q, M, desc = systems.config(args.config)
+        if box is None:  # config 0: the molecule in its 40 A box, open boundaries
+            box = np.full(3, 40.0)
+    periodic = (0, 0, 0) if args.config in (0, 2) else (1, 1, 1)
     n = len(z)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -123,7 +151,10 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
     ctx = Context(MODEL, 0)
-    ctx.set_system(z, Q, M)
+    if images is not None:
+        ctx.set_images(z, *images)
+    else:
+        ctx.set_system(z, Q, M)
     lo = np.zeros(3)
     v0, m = systems.maxwell_boltzmann(z, 300.0)
     xt = torch.tensor(x, dtype=torch.float64, device=dev)
@@ -143,7 +174,7 @@ def main():
         # HBM-resident reneighbor: wraps xt in place, builds the candidate
         # lists on the GPU (no ghost rows, no host copies)
         t0 = time.time()
-        ctx.reneighbor_device(xt, lo, lo + state["box"], (1, 1, 1), skin, stream=stream.cuda_stream)
+        ctx.reneighbor_device(xt, lo, lo + state["box"], periodic, skin, stream=stream.cuda_stream)
         state["x_build"] = xt.clone()
         state["box_build"] = state["box"].copy()
         state["builds"] += 1
@@ -156,7 +187,13 @@ def main():
     rebuild()
     e, w = force()
 
+    # config 0: repeated single points; 1 and 2: NVE; 3: NVT; 4: NPT
+    single_point = args.config == 0
+    thermostat = args.config in (3, 4)
+
     def step():
+        if single_point:
+            return force()
         vt.addcmul_(ft, inv_m, value=0.5 * dt)
         xt.add_(vt, alpha=dt)
         disp = (xt - state["x_build"]).norm(dim=1).max().item()
@@ -168,9 +205,10 @@ def main():
         e, w = force()
         vt.addcmul_(ft, inv_m, value=0.5 * dt)
         ke = 0.5 * (mt * vt * vt).sum() / ACC
-        temp = 2.0 * ke / (3.0 * n * KB)
-        lam = torch.sqrt(1.0 + dt / tau * (T0 / temp - 1.0))
-        vt.mul_(lam)
+        if thermostat:
+            temp = 2.0 * ke / (3.0 * n * KB)
+            lam = torch.sqrt(1.0 + dt / tau * (T0 / temp - 1.0))
+            vt.mul_(lam)
         if npt:
             # P = (2 KE + tr W) / (3 V); W is the LAMMPS virial (eV)
             vol = float(np.prod(state["box"]))
@@ -220,14 +258,18 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        cpu = cpu_baseline(z, x, box, args.cpu_budget)
+        cpu = cpu_baseline(z, x, box, periodic, images, args.cpu_budget)
 
     sr_active, sr_cand, lr_cand = ctx.graph_stats()
     if npt:
         extra = {"ensemble": "NPT (Berendsen, 1 bar, 300 K)", "box_scale": state["mu_total"],
                  "pressure_bar_last": state.get("pressure_bar")}
-    else:
+    elif single_point:
+        extra = {"ensemble": "single-point E+F+virial calls"}
+    elif thermostat:
         extra = {"ensemble": "NVT (Berendsen, 300 K)"}
+    else:
+        extra = {"ensemble": "NVE"}
     out = {
         "metric": "atom-steps/s/GPU (fp64 E+F+virial) at 24k-atom water; max atoms per GPU",
         "value": value, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

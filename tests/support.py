@@ -106,3 +106,26 @@ def load_golden(name):
     if box is not None:
         pos = lo + np.mod(pos - lo, box)
     return ref, z, pos, box
+
+
+def graphs_from_lists(lists, x, rc_sr=4.5, rc_lr=12.0):
+    """Oracle graphs from the LAMMPS stand-in's candidate lists (ghost rows
+    collapsed onto their owners): SR directed edges sender -> receiver with
+    v = x_receiver - x_sender, LR unique pairs (i, j) with d = x_j - x_i,
+    both cut at the model radii.  For boxes wider than twice the cutoff these
+    are the brute-force graphs of build_graphs (test_capi_cpu checks the lists
+    against brute force), in LAMMPS list order."""
+    xr = lists.rows_positions(x)
+    owner = lists.owner.astype(np.int64)
+    (il, off, nb), (il2, off2, nb2) = lists.lists
+    recv = np.repeat(il.astype(np.int64), np.diff(off))
+    v = xr[recv] - xr[nb]
+    r2 = (v * v).sum(1)
+    m = (r2 > 0.0) & (r2 < rc_sr * rc_sr)
+    sr = (owner[nb][m], recv[m], v[m])
+    i2 = np.repeat(il2.astype(np.int64), np.diff(off2))
+    d = xr[nb2] - xr[i2]
+    r2 = (d * d).sum(1)
+    m = (r2 > 0.0) & (r2 < rc_lr * rc_lr)
+    lr = (i2[m], owner[nb2][m], d[m])
+    return sr, lr
