@@ -176,3 +176,24 @@ def test_device_reneighbor_matches_rows_path(orc):
     out = orc.evaluate(z, sr, lr)
     assert abs(e2 - out["energy"]) <= 1e-10 * abs(out["energy"])
     assert np.abs(f2 - out["forces"]).max() <= 1e-9
+
+
+def test_scalar_filter_path_matches_mfma(monkeypatch):
+    """The scalar (one pair per workgroup) filter kernels, selected with
+    SO3LR_NAIVE_FILTERS=1 at context creation, against the fp64 MFMA ones: two
+    independent implementations of the filter networks and their reverse."""
+    from so3lrxlammps_amd import Context, Lists
+    ref, z, pos, box = support.load_golden("water3000")
+    results = []
+    for naive in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NAIVE_FILTERS", naive)
+        c = Context(support.MODEL, 0)
+        c.set_system(z, 0, 1)
+        lists = Lists(pos, np.zeros(3), box, (1, 1, 1))
+        c.set_topology(lists)
+        results.append(c.compute(lists.rows_positions(pos)))
+        c.close()
+    (e1, f1, ea1, w1), (e2, f2, ea2, w2) = results
+    assert abs(e1 - e2) <= 1e-12 * abs(e2)
+    assert np.abs(f1 - f2).max() <= 1e-10
+    assert np.abs(w1 - w2).max() <= 1e-10 * np.abs(w2).max()
