@@ -223,6 +223,14 @@ __device__ __forceinline__ void bernstein(double r, double gamma, const double *
   val = exp(b[ch] + k[ch] * log(xb) + kr[ch] * log(1.0 - xb));
 }
 
+// Position of filter channel c (0..127) inside its 128-wide half of a pair's
+// filter row (pf) and of its adjoint (df): a 4 x 4 transpose inside each
+// 16-channel tile, pos(c) = 16 (c / 16) + 4 (c % 4) + (c / 4) % 4.  The four
+// accumulator values an MFMA filter lane holds for one output tile (channels
+// 16 mt + g + 4 r, r = 0..3) are then adjacent, one 32-byte vector per lane,
+// and every head's 32 channels stay contiguous for the attention kernels.
+__host__ __device__ __forceinline__ int fpos(int c) { return (c & ~15) | ((c & 3) << 2) | ((c >> 2) & 3); }
+
 __global__ __launch_bounds__(128) void k_filter_fwd(const int *n_active, const int *pa, const double *pr,
                                                     const double *ev, FilterArgs A, double *ps,
                                                     double *pf) {
@@ -260,7 +268,7 @@ __global__ __launch_bounds__(128) void k_filter_fwd(const int *n_active, const i
     for (int k = 0; k < kF; ++k) f += w1t[k * kF + c] * h[k];
     const double *e1t = A.fe1t[which];
     for (int j = 0; j < kFH; ++j) f += e1t[j * kF + c] * h2[j];
-    pf[256 * std::size_t(p) + which * kF + c] = f;
+    pf[256 * std::size_t(p) + which * kF + fpos(c)] = f;
     __syncthreads();
   }
 }
@@ -278,8 +286,8 @@ __global__ __launch_bounds__(128) void k_filter_bwd(const int *n_active, const d
   const double r = pr[p];
   if (c < kR) { bernstein(r, A.gamma, A.rbf_b, A.rbf_k, A.rbf_kr, c, rbf[c]); drbf[c] = 0.0; }
   if (c < 4) { s[c] = ps[4 * std::size_t(p) + c]; dsv[c] = 0.0; }
-  g[c] = df[256 * std::size_t(p) + c];
-  g[kF + c] = df[256 * std::size_t(p) + kF + c];
+  g[c] = df[256 * std::size_t(p) + fpos(c)];
+  g[kF + c] = df[256 * std::size_t(p) + kF + fpos(c)];
   __syncthreads();
   for (int which = 0; which < 2; ++which) {
     const double *gf = g + which * kF;
@@ -474,13 +482,10 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_fwd_mfma(const 
     }
     if (valid) ps[4 * std::size_t(p) + g] = sg;
   }
-  auto store = [&](int which) {
-    if (!valid) return;
-    double *dst = pf + 256 * std::size_t(p) + which * kF;
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dst[16 * mt + g + 4 * r] = o[mt][r];
+  // tile mt of filter `which`: its four values per lane are adjacent (fpos)
+  v4d *const rowv = reinterpret_cast<v4d *>(pf + 256 * std::size_t(p) + 4 * g);
+  auto store_tile = [&](int which, int mt) {
+    if (valid) rowv[which * 32 + 4 * mt] = o[mt];
   };
 
   st.run([&](auto si, const v4d &w) {
@@ -491,11 +496,12 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_fwd_mfma(const 
       h2[0] = tile_load(A.eb0p[which], 0, lane);
       h2[1] = tile_load(A.eb0p[which], 1, lane);
       e0 = reinterpret_cast<const v4d *>(A.e0pk[which])[lane];
-      if constexpr (which == 1) {
-        store(0);
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt) o[mt] = tile_load(A.ob1p[1], mt, lane);
-      }
+    }
+    // filter 0's output leaves one tile every two steps while filter 1 runs
+    // its first layer; each tile then starts over from filter 1's bias
+    if constexpr (which == 1 && s < 16 && s % 2 == 0) {
+      store_tile(0, s / 2);
+      o[s / 2] = tile_load(A.ob1p[1], s / 2, lane);
     }
     if constexpr (s < 16) {
       h[s % 8] = mfma4(w, rb[s / 8], h[s % 8]);
@@ -522,7 +528,8 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_fwd_mfma(const 
       o[(s - 80) % 8] = mfma4(w, h2[(s - 80) / 8], o[(s - 80) % 8]);
     }
   });
-  store(1);
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) store_tile(1, mt);
 }
 
 // Reverse of both filters, the Bernstein basis and the cutoff for 16 pairs per
@@ -543,7 +550,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
   const int p = wave * 16 + j;
   const bool valid = p < nact;
   const int pp = valid ? p : nact - 1;
-  const double *dfp = df + 256 * std::size_t(pp) + g;
+  const v4d *dfv = reinterpret_cast<const v4d *>(df + 256 * std::size_t(pp) + 4 * g);
 
   constexpr int NB = 133;
   auto load = [&](auto si) -> v4d {
@@ -551,8 +558,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
     if constexpr (s < 88) {
       constexpr int T = s / 11, u = s % 11;
       if constexpr (u == 0) {
-        const double *gf = dfp + which * kF + 16 * T;
-        return v4d{gf[0], gf[4], gf[8], gf[12]};
+        return dfv[which * 32 + 4 * T];  // channels 16 T + g + 4 v, v = 0..3 (fpos)
       } else if constexpr (u <= 8) {
         return wload(A.w1tp[which], 8, u - 1, T, lane);
       } else {
@@ -917,6 +923,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
   if (n >= N) return;
   const int h = lane >> 4, t = lane & 15;
   const int c0 = 32 * h + t, c1 = c0 + 16;
+  const int p0 = fpos(c0), p1 = fpos(c1);  // their places in a filter row
   const bool evv = t < 2 * h + 3;
   const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
@@ -930,7 +937,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
     const double *fp = pf + 256 * std::size_t(p);
     const double k0 = ko[128 + c0], k1 = ko[128 + c1], v0 = ko[256 + c0], v1 = ko[256 + c1];
     const double ke0 = ko[512 + c0], ke1 = ko[512 + c1];
-    const double f0 = fp[c0], f1 = fp[c1], fe0 = fp[128 + c0], fe1 = fp[128 + c1];
+    const double f0 = fp[p0], f1 = fp[p1], fe0 = fp[128 + p0], fe1 = fp[128 + p1];
     const double fc = pfc[p];
     const double y = pY[kE * std::size_t(p) + m] * (side == 0 ? 1.0 : par);
     Terms T;
@@ -1294,6 +1301,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   if (n >= N) return;
   const int h = lane >> 4, t = lane & 15;
   const int c0 = 32 * h + t, c1 = c0 + 16;
+  const int p0 = fpos(c0), p1 = fpos(c1);  // their places in a filter row
   const bool evv = t < 2 * h + 3;
   const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
@@ -1317,7 +1325,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     const double og0 = gainv[std::size_t(o) * kF + c0], og1 = gainv[std::size_t(o) * kF + c1];
     const double oge = evv ? gaev[std::size_t(o) * kE + m] : 0.0;
     const double *fp = pf + 256 * std::size_t(p);
-    const double fi0 = fp[c0], fi1 = fp[c1], fe0 = fp[128 + c0], fe1 = fp[128 + c1];
+    const double fi0 = fp[p0], fi1 = fp[p1], fe0 = fp[128 + p0], fe1 = fp[128 + p1];
     const double fc = pfc[p];
     const double y = evv ? pY[kE * std::size_t(p) + m] : 0.0;
     const double y_n = side == 0 ? y : par * y;  // harmonics of edge o -> n
@@ -1358,10 +1366,10 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     if ((e & 1) == 0) {
       const std::size_t p = std::size_t(e >> 1);
       double *d = df + 256 * p;
-      d[c0] = T.g0;
-      d[c1] = T.g1;
-      d[128 + c0] = T.ge0;
-      d[128 + c1] = T.ge1;
+      d[p0] = T.g0;
+      d[p1] = T.g1;
+      d[128 + p0] = T.ge0;
+      d[128 + p1] = T.ge1;
       if (lane == 0) dfc[p] = T.fcg;
       if (evv) dY[kE * p + m] += T.dy;
     }
