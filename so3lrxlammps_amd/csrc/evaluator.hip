@@ -1049,7 +1049,7 @@ __global__ __launch_bounds__(256) void k_post2(int N, const double *p, const dou
 
 // ---------------------------------------------------------------- heads
 struct HeadArgs {
-  const double *ew2, *qw2, *escale, *eshift, *qemb, *hw2, *hb2, *hqemb, *hvshift;
+  const double *ew2, *qw2, *escale, *eshift, *qemb, *hw2t, *hb2, *hqemb, *hvshift, *hkey_bwd;
   double eb2, qb2;
 };
 
@@ -1065,7 +1065,7 @@ __global__ __launch_bounds__(256) void k_heads(int N, const int *z, const double
   const double e = wave_sum(H.ew2[lane] * a[lane] + H.ew2[64 + lane] * a[64 + lane]);
   const double q = wave_sum(H.qw2[lane] * a[128 + lane] + H.qw2[64 + lane] * a[192 + lane]);
   double key = H.hb2[lane];
-  for (int i = 0; i < kHH; ++i) key += H.hw2[lane * kHH + i] * a[256 + i];
+  for (int i = 0; i < kHH; ++i) key += H.hw2t[i * kHH + lane] * a[256 + i];  // coalesced rows of W2^T
   hkey[std::size_t(n) * kHH + lane] = key;
   const double qk = wave_sum(H.hqemb[zz * kHH + lane] * key);
   if (lane == 0) {
@@ -1115,10 +1115,8 @@ __global__ __launch_bounds__(256) void k_heads_bwd(int N, const int *z, const do
   const double ef = heff[n];
   const double sg = ef > 0.0 ? 1.0 : (ef < 0.0 ? -1.0 : 0.0);
   const double hs = dh[n] * sg / 8.0;
-  // ghh[i] = sum_j hw2[j][i] gk[j], gk[j] = hs * hqemb[z][j]
-  double acc = 0.0;
-  for (int j = 0; j < kHH; ++j) acc += H.hw2[j * kHH + lane] * hs * H.hqemb[zz * kHH + j];
-  g[256 + lane] = acc * silu_prime(pr[256 + lane]);
+  // ghh[i] = sum_j hw2[j][i] gk[j] with gk[j] = hs * hqemb[z][j] = hs * u[z][i]
+  g[256 + lane] = hs * H.hkey_bwd[zz * kHH + lane] * silu_prime(pr[256 + lane]);
 }
 
 // ---------------------------------------------------------------- long range
@@ -1744,9 +1742,22 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     hw_.qw2 = up(m.f64(q + "transform_inv_features.2.weight", {1, F}));
     hw_.qb2 = m.f64(q + "transform_inv_features.2.bias", {1})[0];
     hw_.qemb = up(m.f64(q + "atomic_embedding.weight", {100, 1}));
-    hw_.hw2 = up(m.f64(h + "transform_features.2.weight", {std::size_t(kHH), std::size_t(kHH)}));
+    const auto hw2 = m.f64(h + "transform_features.2.weight", {std::size_t(kHH), std::size_t(kHH)});
+    const auto hqemb = m.f64(h + "q_embedding.weight", {100, std::size_t(kHH)});
+    hw_.hw2 = up(hw2);
+    hw_.hw2t = up(transpose(hw2, kHH, kHH));
     hw_.hb2 = up(m.f64(h + "transform_features.2.bias", {std::size_t(kHH)}));
-    hw_.hqemb = up(m.f64(h + "q_embedding.weight", {100, std::size_t(kHH)}));
+    hw_.hqemb = up(hqemb);
+    // reverse of the key layer seeded by the element's query: u[z][i] =
+    // sum_j W2[j][i] q_emb[z][j] depends on the element only
+    std::vector<double> u(100 * std::size_t(kHH), 0.0);
+    for (int zz = 0; zz < 100; ++zz)
+      for (int i = 0; i < kHH; ++i) {
+        double acc = 0.0;
+        for (int j = 0; j < kHH; ++j) acc += hw2[std::size_t(j) * kHH + i] * hqemb[std::size_t(zz) * kHH + j];
+        u[std::size_t(zz) * kHH + i] = acc;
+      }
+    hw_.hkey_bwd = up(u);
     hw_.hvshift = up(m.f64(h + "v_shift_embedding.weight", {100, 1}));
     const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
     const auto kk = m.i64("model.radial_embedding.radial_basis_fn.k", {R});
@@ -2167,8 +2178,8 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   }
 
   // --- heads, charge correction, long range ---
-  HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hw2, hw_.hb2, hw_.hqemb, hw_.hvshift,
-             hw_.eb2, hw_.qb2};
+  HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hw2t, hw_.hb2, hw_.hqemb, hw_.hvshift,
+             hw_.hkey_bwd, hw_.eb2, hw_.qb2};
   const double *xf = xs + L * Nz * kF;
   gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1p, hhead, 320, hact, nullptr, 0);
   hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, hkey, heff, hir);

@@ -62,6 +62,8 @@ struct HeadWeights {
   const double *escale, *eshift;  // (118)
   const double *qemb;             // (100)
   const double *hw2, *hb2;        // (64, 64), (64)
+  const double *hw2t;             // its transpose
+  const double *hkey_bwd;         // (100, 64): u[z][i] = sum_j hw2[j][i] hqemb[z][j]
   const double *hqemb, *hvshift;  // (100, 64), (100)
   const double *rbf_b, *rbf_k, *rbf_kr;  // (32) each
   const double *alpha_ref, *c6_ref;

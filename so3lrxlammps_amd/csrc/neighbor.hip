@@ -227,33 +227,43 @@ __global__ void k_canon_count(int n, const int *off, const int *list, int *cnt) 
 }
 
 // pairs in atom-major order of their canonical entry; incidence entries
-// p * 2 + side in the same positions as the full list
-__global__ void k_pairs(int n, const int *off, const int *list, const int *poff, int *nodes, int *codes,
-                        int *inc, int *err) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+// p * 2 + side in the same positions as the full list.  One wavefront per
+// atom: canonical entries are numbered by ballot prefix in list order, and
+// each lane finds the pair of one reverse entry in its partner's list.
+__global__ __launch_bounds__(256) void k_pairs(int n, const int *off, const int *list, const int *poff, int *nodes,
+                                               int *codes, int *inc, int *err) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= n) return;
+  const int beg = off[i], end = off[i + 1];
+  const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
   int p = poff[i];
-  for (int k = off[i]; k < off[i + 1]; ++k) {
-    const int j = list[k] >> 5, code = list[k] & 31;
-    if (j > i) {
-      nodes[2 * p] = i;
-      nodes[2 * p + 1] = j;
-      codes[p] = code;
-      inc[k] = 2 * p;
-      ++p;
+  for (int k0 = beg; k0 < end; k0 += 64) {
+    const int k = k0 + lane;
+    const int e = k < end ? list[k] : 0;
+    const bool canon = k < end && (e >> 5) > i;
+    const unsigned long long mask = __ballot(canon);
+    if (canon) {
+      const int q = p + __popcll(mask & below);
+      nodes[2 * q] = i;
+      nodes[2 * q + 1] = e >> 5;
+      codes[q] = e & 31;
+      inc[k] = 2 * q;
     }
+    p += __popcll(mask);
   }
   // reverse entries: find (i, -code) in j's list, whose canonical pair index
   // is poff[j] + (number of canonical entries before it)
-  for (int k = off[i]; k < off[i + 1]; ++k) {
-    const int j = list[k] >> 5, code = list[k] & 31;
+  for (int k = beg + lane; k < end; k += 64) {
+    const int e = list[k];
+    const int j = e >> 5, code = e & 31;
     if (j > i) continue;
     const int want = i * 32 + (26 - code);  // negated image
     int q = poff[j], found = -1;
     for (int m = off[j]; m < off[j + 1]; ++m) {
-      const int e = list[m];
-      if ((e >> 5) > j) {
-        if (e == want) { found = q; break; }
+      const int f = list[m];
+      if ((f >> 5) > j) {
+        if (f == want) { found = q; break; }
         ++q;
       }
     }
@@ -346,7 +356,7 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   int *nodes = ensure<int>(sr_nodes_, 2 * std::size_t(std::max(npairs, 1)));
   int *codes = ensure<int>(sr_code_, std::max(npairs, 1));
   int *inc = ensure<int>(sr_inc_, std::max(totals[0], 1));
-  hipLaunchKernelGGL(k_pairs, dim3((n + 255) / 256), dim3(256), 0, s, n, sr_off, sr_list, poff, nodes, codes, inc, err);
+  hipLaunchKernelGGL(k_pairs, dim3(gw), dim3(256), 0, s, n, sr_off, sr_list, poff, nodes, codes, inc, err);
   NB_CHECK(hipMemcpyAsync(&herr, err, sizeof(int), hipMemcpyDeviceToHost, s));
   NB_CHECK(hipStreamSynchronize(s));
   if (herr == 1)
