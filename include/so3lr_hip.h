@@ -131,6 +131,10 @@ int so3lr_compute(so3lr_ctx *ctx, const double *x_rows, int flags, double *f_own
  * As so3lr_compute, with x_rows, f_owned and eatom in device memory (HBM
  * resident; no host copies of positions or forces).  energy and virial stay
  * host pointers.  Work is ordered on the context's stream (so3lr_set_stream).
+ * When the same call (same pointers, flags, box, stream and topology) comes
+ * twice in a row, its launch sequence is captured into a HIP graph and
+ * replayed on later identical calls; the results are bit-identical to the
+ * kernel-by-kernel launch (environment SO3LR_NO_GRAPH=1 turns replay off).
  */
 int so3lr_compute_device(so3lr_ctx *ctx, const double *x_rows_dev, int flags,
                          double *f_owned_dev, double *eatom_dev, double *energy,
@@ -178,9 +182,10 @@ int so3lr_graph_stats(const so3lr_ctx *ctx, int64_t *sr_active, int64_t *sr_cand
  * fenced host clocks, pair_so3lr_native_mpi.cpp:1681-1762): when enabled,
  * HIP events are recorded on the launch stream around the kernels
  * "filter_fwd", "filter_bwd", "attn_fwd", "attn_bwd" and "long_range".
- * Enabling clears the totals.  _read returns the summed duration, the number
- * of launches and the units processed (active pairs for the filter kernels,
- * owned atoms otherwise).
+ * Enabling clears the totals; disabling keeps them for reading.  While
+ * enabled, evaluations are launched kernel by kernel (no graph replay).
+ * _read returns the summed duration, the number of launches and the units
+ * processed (active pairs for the filter kernels, owned atoms otherwise).
  */
 int so3lr_kernel_timing(so3lr_ctx *ctx, int enable);
 int so3lr_kernel_timing_read(so3lr_ctx *ctx, const char *kernel, double *total_ms,

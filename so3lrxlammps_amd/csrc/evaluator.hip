@@ -1434,6 +1434,15 @@ __global__ __launch_bounds__(256) void k_geom_bwd(const int *n_active, const dou
 
 // forces and per-atom energies: F_a = -g, F_b = +g; each endpoint receives the
 // ZBL energy of the directed edge it receives
+__global__ void k_fill_int(int *p, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+// the active-pair count next to the reduced energy and virial, for one read-back
+__global__ void k_copy_count(const int *n_active, double *dst) {
+  if (threadIdx.x == 0) dst[0] = double(*n_active);
+}
+
 // xn[n] = x[perm[n]] (positions into node order)
 __global__ void k_gather_pos(int N, const int *perm, const double *x, double *xn) {
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1539,8 +1548,16 @@ void Evaluator::release_all() {
   weight_allocs_.clear();
 }
 
+void Evaluator::drop_graph() {
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  graph_exec_ = nullptr;
+  graph_key_ = GraphKey{};
+}
+
 Evaluator::~Evaluator() {
   if (stream_) (void)hipStreamSynchronize(stream_);
+  drop_graph();
+  if (host_out_) (void)hipHostFree(host_out_);
   release_all();
   if (own_stream_) (void)hipStreamDestroy(own_stream_);
 }
@@ -1609,6 +1626,9 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   HIP_CHECK(hipSetDevice(device));
   HIP_CHECK(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking));
   if (const char *nv = std::getenv("SO3LR_NAIVE_FILTERS")) naive_filters_ = nv[0] == '1';
+  // SO3LR_NO_GRAPH=1: always launch the kernels one by one (no graph replay)
+  if (const char *ng = std::getenv("SO3LR_NO_GRAPH")) use_graphs_ = ng[0] != '1';
+  HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_out_), 16 * sizeof(double), hipHostMallocDefault));
   stream_ = own_stream_;
   const Model &m = *model_;
   const Architecture &a = m.arch();
@@ -1870,6 +1890,7 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
   HIP_CHECK(hipStreamSynchronize(stream_));
   system_ready_ = true;
   topology_ready_ = false;
+  ++topo_version_;
   evaluated_ = false;
 }
 
@@ -1951,6 +1972,7 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
   put(lr_rows_, lr_rows); put(lr_nodes_, lr_nodes); put(lr_inc_off_, lr_off_v); put(lr_inc_, lr_inc);
   HIP_CHECK(hipStreamSynchronize(stream_));
   topology_ready_ = true;
+  ++topo_version_;
   evaluated_ = false;
 }
 
@@ -1993,12 +2015,10 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   const int *perm = permuted_ ? static_cast<const int *>(perm_->p) : nullptr;
   const int *z = static_cast<const int *>((permuted_ ? nz_ : z_)->p);
   const double *x0 = static_cast<const double *>((permuted_ ? nx0_ : x0_)->p);
-  if (permuted_) {
-    double *xn = static_cast<double *>(xn_->p);
-    hipLaunchKernelGGL(k_gather_pos, dim3(unsigned((3 * Nz + 255) / 256)), dim3(256), 0, s, int(N), perm, x, xn);
-    x = xn;
-  }
-  // --- buffers (retained capacity) ---
+  const double *x_in = x;
+  if (permuted_) x = static_cast<const double *>(xn_->p);
+  // --- buffers (retained capacity; all allocation happens before any work
+  // is enqueued, so the sequence below can be captured into a graph) ---
   double *xs = ensure<double>(xs_, (L + 1) * Nz * kF);
   double *evs = ensure<double>(evs_, (L + 1) * Nz * kE);
   double *qkv = ensure<double>(qkv_, L * Nz * 640);
@@ -2064,6 +2084,8 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   double *dr = ensure<double>(dr_, Pz);
   double *dY = ensure<double>(dY_, kE * Pz);
   double *pg = ensure<double>(pg_, 3 * Pz);
+  int *iact = ensure<int>(iact_, 2 * Pz), *iother = ensure<int>(iother_, 2 * Pz);
+  double *partial = ensure<double>(red_part_, 9 * kReduceBlocks);
   const int *sr_rows = static_cast<const int *>(sr_rows_->p);
   const int *sr_nodes = static_cast<const int *>(sr_nodes_->p);
   const int *sr_off = static_cast<const int *>(sr_inc_off_->p);
@@ -2109,6 +2131,12 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   };
   const unsigned gN64 = unsigned(std::max(1, ceil_div(N, 64)));
 
+  // Everything from here to the read-back is one sequence on stream s: run
+  // directly, or captured once into a graph and replayed.
+  auto enqueue = [&] {
+  if (permuted_)
+    hipLaunchKernelGGL(k_gather_pos, dim3(unsigned((3 * Nz + 255) / 256)), dim3(256), 0, s, int(N), perm, x_in,
+                       const_cast<double *>(x));
   // --- active short-range pairs, geometry, ZBL ---
   const double rc2 = rc_ * rc_;
   if (P > 0 && !shift_mode_) {
@@ -2124,10 +2152,9 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     hipLaunchKernelGGL(k_sr_compact<ShiftPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, sr_nodes, rc2, blk, z,
                        zbl_, c2a, pa, pv, pr, pY, pfc, pzbl);
   } else {
-    HIP_CHECK(hipMemsetAsync(nact, 0, sizeof(int), s));
+    hipLaunchKernelGGL(k_fill_int, dim3(1), dim3(64), 0, s, nact, 1, 0);  // no memset nodes in graphs
   }
   // active incidence of this step (2 entries per candidate pair)
-  int *iact = ensure<int>(iact_, 2 * Pz), *iother = ensure<int>(iother_, 2 * Pz);
   if (P > 0)
     hipLaunchKernelGGL(k_inc_active, dim3(unsigned((2 * Pz + 255) / 256)), dim3(256), 0, s, int(2 * P), sr_inc, c2a,
                        pa, iact, iother);
@@ -2240,16 +2267,42 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
                      dr, pzbl, dY, pg);
   hipLaunchKernelGGL(k_forces, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pg, pzbl, flr, eatom, elr,
                      perm, fo, ezbl, etot);
-  double *partial = ensure<double>(red_part_, 9 * kReduceBlocks);
   hipLaunchKernelGGL(k_reduce_part, dim3(kReduceBlocks), dim3(256), 0, s, int(N), nact, etot, pv, pg, vlr, parts,
                      partial);
   hipLaunchKernelGGL(k_reduce_final, dim3(1), dim3(256), 0, s, kReduceBlocks, partial, red);
+  hipLaunchKernelGGL(k_copy_count, dim3(1), dim3(64), 0, s, nact, red + 9);
   HIP_CHECK(hipGetLastError());
-  double host_red[9];
-  int host_nact = 0;
-  HIP_CHECK(hipMemcpyAsync(host_red, red, 9 * sizeof(double), hipMemcpyDeviceToHost, s));
-  HIP_CHECK(hipMemcpyAsync(&host_nact, nact, sizeof(int), hipMemcpyDeviceToHost, s));
+  HIP_CHECK(hipMemcpyAsync(host_out_, red, 10 * sizeof(double), hipMemcpyDeviceToHost, s));
+  };  // enqueue
+
+  const GraphKey key{x_in, fo, etot, flags, {box_len_[0], box_len_[1], box_len_[2]}, s, topo_version_,
+                     alloc_epoch_};
+  if (timing_ || !use_graphs_) {
+    enqueue();
+  } else if (graph_exec_ && key == graph_key_) {
+    HIP_CHECK(hipGraphLaunch(graph_exec_, s));
+  } else if (key == last_key_) {
+    // the same call twice in a row: capture it once and replay from now on
+    drop_graph();
+    hipGraph_t graph = nullptr;
+    HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    enqueue();
+    HIP_CHECK(hipStreamEndCapture(s, &graph));
+    const hipError_t ierr = hipGraphInstantiate(&graph_exec_, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ierr != hipSuccess) {
+      graph_exec_ = nullptr;
+      throw std::runtime_error(std::string("HIP error in hipGraphInstantiate: ") + hipGetErrorString(ierr));
+    }
+    graph_key_ = key;
+    HIP_CHECK(hipGraphLaunch(graph_exec_, s));
+  } else {
+    enqueue();
+  }
+  last_key_ = key;
   HIP_CHECK(hipStreamSynchronize(s));
+  const double *host_red = host_out_;
+  const std::int64_t host_nact = std::int64_t(host_out_[9]);
   last_active_ = host_nact;
   for (Pending &pd : pending) {
     float ms = 0.f;

@@ -103,7 +103,10 @@ class Evaluator {
   std::int64_t lr_candidates() const { return p_lr_; }
   std::int64_t device_bytes() const { return bytes_; }
   // Kernel timing with HIP events on the launch stream (measurement hook).
-  void set_timing(bool on) { timing_ = on; timings_.clear(); }
+  void set_timing(bool on) {  // enabling clears the totals; disabling keeps them for reading
+    if (on) timings_.clear();
+    timing_ = on;
+  }
   bool timing_read(const std::string &kernel, double &total_ms, std::int64_t &launches,
                    std::int64_t &units) const;
 
@@ -148,6 +151,7 @@ class Evaluator {
         throw std::runtime_error("HIP error in hipMalloc: out of device memory (" + std::to_string(cap) + " bytes)");
       b->bytes = cap;
       bytes_ += std::int64_t(cap);
+      ++alloc_epoch_;  // a captured graph holds the old address
     }
     return static_cast<T *>(b->p);
   }
@@ -186,6 +190,28 @@ class Evaluator {
   };
   bool timing_ = false;
   bool naive_filters_ = false;  // SO3LR_NAIVE_FILTERS=1: scalar filter kernels (cross-check)
+  // Graph replay of one evaluation: the launch sequence of compute_device is
+  // captured when the same call (inputs, outputs, flags, box, stream,
+  // topology and buffer addresses) comes twice in a row, and replayed while
+  // it keeps coming.
+  struct GraphKey {
+    const void *x = nullptr, *f = nullptr, *eatom = nullptr;
+    int flags = -1;
+    double box[3] = {0, 0, 0};
+    hipStream_t stream = nullptr;
+    std::uint64_t topology = 0, epoch = 0;
+    bool operator==(const GraphKey &o) const {
+      return x == o.x && f == o.f && eatom == o.eatom && flags == o.flags && box[0] == o.box[0] &&
+             box[1] == o.box[1] && box[2] == o.box[2] && stream == o.stream && topology == o.topology &&
+             epoch == o.epoch;
+    }
+  };
+  bool use_graphs_ = true;  // SO3LR_NO_GRAPH=1 turns replay off
+  hipGraphExec_t graph_exec_ = nullptr;
+  GraphKey graph_key_{}, last_key_{};
+  std::uint64_t topo_version_ = 1, alloc_epoch_ = 0;
+  double *host_out_ = nullptr;  // pinned: energy, virial, totals, active-pair count
+  void drop_graph();
   std::map<std::string, Timing> timings_;
   double *last_etot_ = nullptr;
 };

@@ -370,6 +370,7 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   permuted_ = reorder;
   shift_mode_ = true;
   topology_ready_ = true;
+  ++topo_version_;
   evaluated_ = false;
 }
 

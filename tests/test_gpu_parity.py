@@ -197,3 +197,43 @@ def test_scalar_filter_path_matches_mfma(monkeypatch):
     assert abs(e1 - e2) <= 1e-12 * abs(e2)
     assert np.abs(f1 - f2).max() <= 1e-10
     assert np.abs(w1 - w2).max() <= 1e-10 * np.abs(w2).max()
+
+
+def test_graph_replay_matches_eager(monkeypatch):
+    """Identical repeated calls replay a captured graph of the evaluation.
+    Every replay -- with torch work, an evaluation under a different key, moved
+    positions and a reneighbor in between -- matches an eager-only context bit
+    for bit."""
+    import torch
+    from so3lrxlammps_amd import Context
+    ref, z, pos, box = support.load_golden("water3000")
+    monkeypatch.setenv("SO3LR_NO_GRAPH", "1")
+    eager = Context(support.MODEL, 0)
+    monkeypatch.delenv("SO3LR_NO_GRAPH")
+    graph = Context(support.MODEL, 0)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    rng = np.random.default_rng(11)
+    with torch.cuda.stream(stream):
+        xt = torch.tensor(pos, dtype=torch.float64, device=dev)
+        fe = torch.zeros_like(xt)
+        fg = torch.zeros_like(xt)
+        other = torch.zeros_like(xt)
+        for c in (eager, graph):
+            c.set_system(z, 0, 1)
+            c.reneighbor_device(xt, np.zeros(3), box, (1, 1, 1), 1.0, stream=stream.cuda_stream)
+        for k in range(8):
+            if k == 5:  # new topology: the graph is dropped and captured again
+                for c in (eager, graph):
+                    c.reneighbor_device(xt, np.zeros(3), box, (1, 1, 1), 1.0, stream=stream.cuda_stream)
+            e1, w1 = eager.compute_device(xt, fe, stream=stream.cuda_stream)
+            e2, w2 = graph.compute_device(xt, fg, stream=stream.cuda_stream)
+            stream.synchronize()
+            assert e1 == e2, k
+            assert np.array_equal(w1, w2), k
+            assert torch.equal(fe, fg), k
+            # eager work between replays: torch kernels, another key, moved atoms
+            other.copy_(fg).mul_(0.5)
+            graph.compute_device(xt, other, stream=stream.cuda_stream)
+            xt.add_(torch.tensor(rng.normal(scale=1e-3, size=pos.shape), dtype=torch.float64, device=dev))
+            stream.synchronize()
