@@ -1312,7 +1312,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
   struct Terms {
     double dq0, dq1, dqe0, dqe1, dk0, dk1, dke0, dke1, dv0, dv1;  // node-side contributions
-    double g0, g1, ge0, ge1, fcg, dy;                             // pair adjoints (side 0 only)
+    double g0, g1, ge0, ge1, fcg, dy;                             // pair adjoints (side 0 only); dy: new dY
   };
   auto terms = [&](int e, int o) {
     const int p = e >> 1, side = e & 1;
@@ -1320,17 +1320,23 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     const double oq0 = ot[c0], oq1 = ot[c1], ok0 = ot[128 + c0], ok1 = ot[128 + c1];
     const double ov0 = ot[256 + c0], ov1 = ot[256 + c1], oqe0 = ot[384 + c0], oqe1 = ot[384 + c1];
     const double oke0 = ot[512 + c0], oke1 = ot[512 + c1];
+    // every load of the pair unconditional (m = 0 on lanes without an
+    // equivariant channel: a valid address, the value is masked below), so
+    // one wait covers the whole iteration
     const double og0 = gainv[std::size_t(o) * kF + c0], og1 = gainv[std::size_t(o) * kF + c1];
-    const double oge = evv ? gaev[std::size_t(o) * kE + m] : 0.0;
+    const double oge_ld = gaev[std::size_t(o) * kE + m];
     const double *fp = pf + 256 * std::size_t(p);
     const double fi0 = fp[p0], fi1 = fp[p1], fe0 = fp[128 + p0], fe1 = fp[128 + p1];
     const double fc = pfc[p];
-    const double y = evv ? pY[kE * std::size_t(p) + m] : 0.0;
-    const double y_n = side == 0 ? y : par * y;  // harmonics of edge o -> n
-    const double y_o = side == 0 ? par * y : y;  // harmonics of edge n -> o
+    const double y_ld = pY[kE * std::size_t(p) + m];
+    const double dy_old = dY[kE * std::size_t(p) + m];  // used by the side-0 endpoint only
     const double *al = palpha + 16 * std::size_t(p);
     const double ain_i = al[8 * side + h], ain_e = al[8 * side + 4 + h];
     const double aout_i = al[8 * (1 - side) + h], aout_e = al[8 * (1 - side) + 4 + h];
+    const double oge = evv ? oge_ld : 0.0;
+    const double y = evv ? y_ld : 0.0;
+    const double y_n = side == 0 ? y : par * y;  // harmonics of edge o -> n
+    const double y_o = side == 0 ? par * y : y;  // harmonics of edge n -> o
     // per-head sums for the incoming (o -> n) and outgoing (n -> o) edges
     const double ci = group_sum(mg0 * ov0 + mg1 * ov1);
     const double ce = group_sum(mge * y_n);
@@ -1352,7 +1358,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     const double part = ain_i * ci + ain_e * ce + aout_i * co + aout_e * coe;
     T.fcg = lane_read(part, 0) + lane_read(part, 16) + lane_read(part, 32) + lane_read(part, 48);
     // dE/dY_p: edge o->n via y_n (= Y_p), edge n->o via y_o (parity)
-    T.dy = fc * ain_e * mge + par * fc * aout_e * oge;
+    T.dy = dy_old + (fc * ain_e * mge + par * fc * aout_e * oge);
     return T;
   };
   auto apply = [&](const Terms &T, int e) {
@@ -1369,7 +1375,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
       d[128 + p0] = T.ge0;
       d[128 + p1] = T.ge1;
       if (lane == 0) dfc[p] = T.fcg;
-      if (evv) dY[kE * p + m] += T.dy;
+      if (evv) dY[kE * p + m] = T.dy;
     }
   };
   // one pair at a time: two in flight need ~190 registers and lose occupancy
