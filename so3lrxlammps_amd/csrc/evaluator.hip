@@ -351,8 +351,23 @@ typedef double v4d __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4d mfma(double a, double b, v4d c) {
   return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
+// Weight fragments (one v4d per lane, 2 KiB per fragment) through buffer
+// loads: the array base sits in a scalar buffer resource and the fragment
+// offset in a scalar register, so a fragment costs two loads and no vector
+// address arithmetic.  Descriptor word 3 = 0x00020000: raw 32-bit data
+// format, as gfx9-family buffer loads expect.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ double u2_to_f64(unsigned lo, unsigned hi) {
+  return __builtin_bit_cast(double, (unsigned long long)lo | ((unsigned long long)hi << 32));
+}
+__device__ __forceinline__ v4d frag_load(const double *P, int frag, int lane) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<double *>(P), 0, 0x7fffffff, 0x00020000);
+  const v4u a = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 32, frag * 2048, 0);
+  const v4u b = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 32 + 16, frag * 2048, 0);
+  return v4d{u2_to_f64(a[0], a[1]), u2_to_f64(a[2], a[3]), u2_to_f64(b[0], b[1]), u2_to_f64(b[2], b[3])};
+}
 __device__ __forceinline__ v4d wload(const double *P, int KT, int mt, int T, int lane) {
-  return reinterpret_cast<const v4d *>(P)[(mt * KT + T) * 64 + lane];
+  return frag_load(P, mt * KT + T, lane);
 }
 
 struct FilterMfma {
@@ -416,9 +431,7 @@ constexpr int kFilterPF = SO3LR_FILTER_PF;  // fragments in flight per wavefront
 #endif
 #define FILTER_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SO3LR_FILTER_WAVES, SO3LR_FILTER_WAVES)))
 
-__device__ __forceinline__ v4d tile_load(const double *P, int t, int lane) {
-  return reinterpret_cast<const v4d *>(P)[t * 64 + lane];
-}
+__device__ __forceinline__ v4d tile_load(const double *P, int t, int lane) { return frag_load(P, t, lane); }
 __device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
   c = mfma(w[0], b[0], c);
   c = mfma(w[1], b[1], c);
