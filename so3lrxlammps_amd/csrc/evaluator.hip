@@ -799,13 +799,13 @@ __global__ __launch_bounds__(256) void k_qkv_mfma(int rows, const double *__rest
     }
     if constexpr (s == PER_H - 1) {
       if (valid) {
+        // tile mt is projection mt / 2, channels 32 h + 16 (mt % 2) + [0, 16):
+        // one 16-channel tile of the row, stored in the tile-transposed order
+        // (fpos), so each lane writes its four values as one vector
+        double *row = out + std::size_t(n) * 640 + h * kHW + 4 * g;
 #pragma unroll
         for (int mt = 0; mt < 10; ++mt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 16 * mt + g + 4 * r;  // 0..159 = projection * 32 + channel
-            out[std::size_t(n) * 640 + (o >> 5) * kF + h * kHW + (o & 31)] = acc[mt][r];
-          }
+          *reinterpret_cast<v4d *>(row + (mt >> 1) * kF + 16 * (mt & 1)) = acc[mt];
       }
     }
   });
@@ -828,13 +828,9 @@ __global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *__
   auto load = [&](auto si) -> v4d {
     constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H, T = s / 3, u = s % 3;
     if constexpr (u == 0) {
-      v4d b;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int k = 16 * T + g + 4 * v;  // projection * 32 + channel
-        b[v] = gr[(k >> 5) * kF + h * kHW + (k & 31)];
-      }
-      return b;
+      // K entries 16 T + g + 4 v: projection T / 2, channels 32 h + 16 (T % 2)
+      // + g + 4 v, adjacent in the tile-transposed row order (fpos)
+      return *reinterpret_cast<const v4d *>(gr + (T >> 1) * kF + h * kHW + 16 * (T & 1) + 4 * g);
     } else {
       return wload(Wtp + std::size_t(h) * kHW * 160, 10, u - 1, T, lane);
     }
@@ -941,15 +937,15 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
   const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
   const double *qn = qkv + std::size_t(n) * 640;
-  const double q0 = qn[c0], q1 = qn[c1], qe0 = qn[384 + c0], qe1 = qn[384 + c1];
+  const double q0 = qn[p0], q1 = qn[p1], qe0 = qn[384 + p0], qe1 = qn[384 + p1];
   double acc0 = 0.0, acc1 = 0.0, acce = 0.0;
   struct Terms { double ai, ae, d0, d1, de; };
   auto terms = [&](int e, int o) {
     const int p = e >> 1, side = e & 1;
     const double *ko = qkv + std::size_t(o) * 640;
     const double *fp = pf + 256 * std::size_t(p);
-    const double k0 = ko[128 + c0], k1 = ko[128 + c1], v0 = ko[256 + c0], v1 = ko[256 + c1];
-    const double ke0 = ko[512 + c0], ke1 = ko[512 + c1];
+    const double k0 = ko[128 + p0], k1 = ko[128 + p1], v0 = ko[256 + p0], v1 = ko[256 + p1];
+    const double ke0 = ko[512 + p0], ke1 = ko[512 + p1];
     const double f0 = fp[p0], f1 = fp[p1], fe0 = fp[128 + p0], fe1 = fp[128 + p1];
     const double fc = pfc[p];
     const double y = pY[kE * std::size_t(p) + m] * (side == 0 ? 1.0 : par);
@@ -1317,9 +1313,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
   const double *me = qkv + std::size_t(n) * 640;
-  const double mq0 = me[c0], mq1 = me[c1], mk0 = me[128 + c0], mk1 = me[128 + c1];
-  const double mv0 = me[256 + c0], mv1 = me[256 + c1], mqe0 = me[384 + c0], mqe1 = me[384 + c1];
-  const double mke0 = me[512 + c0], mke1 = me[512 + c1];
+  const double mq0 = me[p0], mq1 = me[p1], mk0 = me[128 + p0], mk1 = me[128 + p1];
+  const double mv0 = me[256 + p0], mv1 = me[256 + p1], mqe0 = me[384 + p0], mqe1 = me[384 + p1];
+  const double mke0 = me[512 + p0], mke1 = me[512 + p1];
   const double mg0 = gainv[std::size_t(n) * kF + c0], mg1 = gainv[std::size_t(n) * kF + c1];
   const double mge = evv ? gaev[std::size_t(n) * kE + m] : 0.0;
   double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
@@ -1330,9 +1326,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   auto terms = [&](int e, int o) {
     const int p = e >> 1, side = e & 1;
     const double *ot = qkv + std::size_t(o) * 640;
-    const double oq0 = ot[c0], oq1 = ot[c1], ok0 = ot[128 + c0], ok1 = ot[128 + c1];
-    const double ov0 = ot[256 + c0], ov1 = ot[256 + c1], oqe0 = ot[384 + c0], oqe1 = ot[384 + c1];
-    const double oke0 = ot[512 + c0], oke1 = ot[512 + c1];
+    const double oq0 = ot[p0], oq1 = ot[p1], ok0 = ot[128 + p0], ok1 = ot[128 + p1];
+    const double ov0 = ot[256 + p0], ov1 = ot[256 + p1], oqe0 = ot[384 + p0], oqe1 = ot[384 + p1];
+    const double oke0 = ot[512 + p0], oke1 = ot[512 + p1];
     // every load of the pair unconditional (m = 0 on lanes without an
     // equivariant channel: a valid address, the value is masked below), so
     // one wait covers the whole iteration
@@ -1397,11 +1393,11 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     if (two) apply(terms(e2, o2), e2);
   });
   double *g = gqkv + std::size_t(n) * 640;
-  g[c0] = dq0; g[c1] = dq1;
-  g[128 + c0] = dk0; g[128 + c1] = dk1;
-  g[256 + c0] = dv0; g[256 + c1] = dv1;
-  g[384 + c0] = dqe0; g[384 + c1] = dqe1;
-  g[512 + c0] = dke0; g[512 + c1] = dke1;
+  g[p0] = dq0; g[p1] = dq1;
+  g[128 + p0] = dk0; g[128 + p1] = dk1;
+  g[256 + p0] = dv0; g[256 + p1] = dv1;
+  g[384 + p0] = dqe0; g[384 + p1] = dqe1;
+  g[512 + p0] = dke0; g[512 + p1] = dke1;
 }
 
 
