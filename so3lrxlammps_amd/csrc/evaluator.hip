@@ -859,6 +859,9 @@ __global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *__
 }
 
 // ---------------------------------------------------------------- attention
+// 16-byte load / store of two adjacent doubles (16-byte aligned)
+__device__ __forceinline__ double2 ld2(const double *p) { return *reinterpret_cast<const double2 *>(p); }
+__device__ __forceinline__ void st2(double *p, double a, double b) { *reinterpret_cast<double2 *>(p) = double2{a, b}; }
 // Node-major, one wavefront per node.  Lane l works for head h = l / 16: it
 // holds the invariant channels 32 h + t and 32 h + 16 + t (t = l % 16) and the
 // equivariant channel off[h] + t of degree h + 1 when t < 2 h + 3, so every
@@ -931,22 +934,27 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int h = lane >> 4, t = lane & 15;
-  const int c0 = 32 * h + t, c1 = c0 + 16;
-  const int p0 = fpos(c0), p1 = fpos(c1);  // their places in a filter row
+  // the lane's two channels sit next to each other in the tile-transposed
+  // rows (filters, q k v): positions 32 h + 2 t and + 1, read as one 16-byte
+  // vector; fpos is its own inverse, so the channels are fpos(position)
+  const int p0 = 32 * h + 2 * t, p1 = p0 + 1;
+  const int c0 = fpos(p0), c1 = fpos(p1);  // c1 = c0 + 4
   const bool evv = t < 2 * h + 3;
   const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
   const double *qn = qkv + std::size_t(n) * 640;
-  const double q0 = qn[p0], q1 = qn[p1], qe0 = qn[384 + p0], qe1 = qn[384 + p1];
+  const double2 qv = ld2(qn + p0), qev = ld2(qn + 384 + p0);
+  const double q0 = qv.x, q1 = qv.y, qe0 = qev.x, qe1 = qev.y;
   double acc0 = 0.0, acc1 = 0.0, acce = 0.0;
   struct Terms { double ai, ae, d0, d1, de; };
   auto terms = [&](int e, int o) {
     const int p = e >> 1, side = e & 1;
     const double *ko = qkv + std::size_t(o) * 640;
     const double *fp = pf + 256 * std::size_t(p);
-    const double k0 = ko[128 + p0], k1 = ko[128 + p1], v0 = ko[256 + p0], v1 = ko[256 + p1];
-    const double ke0 = ko[512 + p0], ke1 = ko[512 + p1];
-    const double f0 = fp[p0], f1 = fp[p1], fe0 = fp[128 + p0], fe1 = fp[128 + p1];
+    const double2 kv = ld2(ko + 128 + p0), vv = ld2(ko + 256 + p0), kev = ld2(ko + 512 + p0);
+    const double2 fv = ld2(fp + p0), fev = ld2(fp + 128 + p0);
+    const double k0 = kv.x, k1 = kv.y, v0 = vv.x, v1 = vv.y, ke0 = kev.x, ke1 = kev.y;
+    const double f0 = fv.x, f1 = fv.y, fe0 = fev.x, fe1 = fev.y;
     const double fc = pfc[p];
     const double y = pY[kE * std::size_t(p) + m] * (side == 0 ? 1.0 : par);
     Terms T;
@@ -1307,15 +1315,19 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int h = lane >> 4, t = lane & 15;
-  const int c0 = 32 * h + t, c1 = c0 + 16;
-  const int p0 = fpos(c0), p1 = fpos(c1);  // their places in a filter row
+  // the lane's two channels sit next to each other in the tile-transposed
+  // rows (filters, q k v): positions 32 h + 2 t and + 1, read as one 16-byte
+  // vector; fpos is its own inverse, so the channels are fpos(position)
+  const int p0 = 32 * h + 2 * t, p1 = p0 + 1;
+  const int c0 = fpos(p0), c1 = fpos(p1);  // c1 = c0 + 4
   const bool evv = t < 2 * h + 3;
   const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
   const double *me = qkv + std::size_t(n) * 640;
-  const double mq0 = me[p0], mq1 = me[p1], mk0 = me[128 + p0], mk1 = me[128 + p1];
-  const double mv0 = me[256 + p0], mv1 = me[256 + p1], mqe0 = me[384 + p0], mqe1 = me[384 + p1];
-  const double mke0 = me[512 + p0], mke1 = me[512 + p1];
+  const double2 mqv = ld2(me + p0), mkv = ld2(me + 128 + p0), mvv = ld2(me + 256 + p0);
+  const double2 mqev = ld2(me + 384 + p0), mkev = ld2(me + 512 + p0);
+  const double mq0 = mqv.x, mq1 = mqv.y, mk0 = mkv.x, mk1 = mkv.y, mv0 = mvv.x, mv1 = mvv.y;
+  const double mqe0 = mqev.x, mqe1 = mqev.y, mke0 = mkev.x, mke1 = mkev.y;
   const double mg0 = gainv[std::size_t(n) * kF + c0], mg1 = gainv[std::size_t(n) * kF + c1];
   const double mge = evv ? gaev[std::size_t(n) * kE + m] : 0.0;
   double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
@@ -1326,16 +1338,18 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   auto terms = [&](int e, int o) {
     const int p = e >> 1, side = e & 1;
     const double *ot = qkv + std::size_t(o) * 640;
-    const double oq0 = ot[p0], oq1 = ot[p1], ok0 = ot[128 + p0], ok1 = ot[128 + p1];
-    const double ov0 = ot[256 + p0], ov1 = ot[256 + p1], oqe0 = ot[384 + p0], oqe1 = ot[384 + p1];
-    const double oke0 = ot[512 + p0], oke1 = ot[512 + p1];
+    const double2 oqv = ld2(ot + p0), okv = ld2(ot + 128 + p0), ovv = ld2(ot + 256 + p0);
+    const double2 oqev = ld2(ot + 384 + p0), okev = ld2(ot + 512 + p0);
+    const double oq0 = oqv.x, oq1 = oqv.y, ok0 = okv.x, ok1 = okv.y, ov0 = ovv.x, ov1 = ovv.y;
+    const double oqe0 = oqev.x, oqe1 = oqev.y, oke0 = okev.x, oke1 = okev.y;
     // every load of the pair unconditional (m = 0 on lanes without an
     // equivariant channel: a valid address, the value is masked below), so
     // one wait covers the whole iteration
     const double og0 = gainv[std::size_t(o) * kF + c0], og1 = gainv[std::size_t(o) * kF + c1];
     const double oge_ld = gaev[std::size_t(o) * kE + m];
     const double *fp = pf + 256 * std::size_t(p);
-    const double fi0 = fp[p0], fi1 = fp[p1], fe0 = fp[128 + p0], fe1 = fp[128 + p1];
+    const double2 fiv = ld2(fp + p0), fev = ld2(fp + 128 + p0);
+    const double fi0 = fiv.x, fi1 = fiv.y, fe0 = fev.x, fe1 = fev.y;
     const double fc = pfc[p];
     const double y_ld = pY[kE * std::size_t(p) + m];
     const double dy_old = dY[kE * std::size_t(p) + m];  // used by the side-0 endpoint only
@@ -1379,10 +1393,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     if ((e & 1) == 0) {
       const std::size_t p = std::size_t(e >> 1);
       double *d = df + 256 * p;
-      d[p0] = T.g0;
-      d[p1] = T.g1;
-      d[128 + p0] = T.ge0;
-      d[128 + p1] = T.ge1;
+      st2(d + p0, T.g0, T.g1);
+      st2(d + 128 + p0, T.ge0, T.ge1);
       if (lane == 0) dfc[p] = T.fcg;
       if (evv) dY[kE * p + m] = T.dy;
     }
@@ -1393,11 +1405,11 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     if (two) apply(terms(e2, o2), e2);
   });
   double *g = gqkv + std::size_t(n) * 640;
-  g[p0] = dq0; g[p1] = dq1;
-  g[128 + p0] = dk0; g[128 + p1] = dk1;
-  g[256 + p0] = dv0; g[256 + p1] = dv1;
-  g[384 + p0] = dqe0; g[384 + p1] = dqe1;
-  g[512 + p0] = dke0; g[512 + p1] = dke1;
+  st2(g + p0, dq0, dq1);
+  st2(g + 128 + p0, dk0, dk1);
+  st2(g + 256 + p0, dv0, dv1);
+  st2(g + 384 + p0, dqe0, dqe1);
+  st2(g + 512 + p0, dke0, dke1);
 }
 
 
