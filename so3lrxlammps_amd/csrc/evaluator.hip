@@ -430,6 +430,10 @@ constexpr int kFilterPF = SO3LR_FILTER_PF;  // fragments in flight per wavefront
 #define SO3LR_FILTER_WAVES 2
 #endif
 #define FILTER_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SO3LR_FILTER_WAVES, SO3LR_FILTER_WAVES)))
+#ifndef SO3LR_FILTER_FWD_WAVES
+#define SO3LR_FILTER_FWD_WAVES SO3LR_FILTER_WAVES
+#endif
+#define FILTER_FWD_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SO3LR_FILTER_FWD_WAVES, SO3LR_FILTER_FWD_WAVES)))
 
 __device__ __forceinline__ v4d tile_load(const double *P, int t, int lane) { return frag_load(P, t, lane); }
 __device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
@@ -455,8 +459,9 @@ __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, v4d *
 // Both filters of one block for 16 pairs per wavefront, 4 wavefronts per block.
 // Per filter the stream holds 96 weight fragments: W0 (s < 16: tile s % 8,
 // K chunk s / 8), W1 (16 <= s < 80) and E1 (80 <= s < 96), tile-minor.
-__global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_fwd_mfma(const int *n_active, const int *pa, const double *pr,
-                                                         const double *ev, FilterMfma A, double *ps, double *pf) {
+__global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(const int *n_active, const int *pa,
+                                                                     const double *pr, const double *ev,
+                                                                     FilterMfma A, double *ps, double *pf) {
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -465,21 +470,28 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_fwd_mfma(const 
   const bool valid = p < nact;
   const int pp = valid ? p : nact - 1;
 
+  // Per filter the stream holds 115 entries: the layer-0 bias tiles (8), the
+  // spherical layer-0 bias tiles (2) and operand (1), W0 (16: tile s % 8, K
+  // chunk s / 8), then per output tile mt its bias, the 8 W1 chunks and the
+  // 2 E1 chunks (11 each).  The output is built one tile at a time and stored
+  // as soon as it is complete, so only one output accumulator is live.
+  constexpr int NF = 115;
   auto load = [&](auto si) -> v4d {
-    constexpr int S = decltype(si)::value, which = S / 96, s = S % 96;
-    if constexpr (s < 16) return wload(A.w0p[which], 2, s % 8, s / 8, lane);
-    else if constexpr (s < 80) return wload(A.w1p[which], 8, (s - 16) % 8, (s - 16) / 8, lane);
-    else return wload(A.e1p[which], 2, (s - 80) % 8, (s - 80) / 8, lane);
+    constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
+    if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
+    else if constexpr (s < 10) return tile_load(A.eb0p[which], s - 8, lane);
+    else if constexpr (s == 10) return tile_load(A.e0pk[which], 0, lane);
+    else if constexpr (s < 27) return wload(A.w0p[which], 2, (s - 11) % 8, (s - 11) / 8, lane);
+    else {
+      constexpr int mt = (s - 27) / 11, u = (s - 27) % 11;
+      if constexpr (u == 0) return tile_load(A.ob1p[which], mt, lane);
+      else if constexpr (u <= 8) return wload(A.w1p[which], 8, mt, u - 1, lane);
+      else return wload(A.e1p[which], 2, mt, u - 9, lane);
+    }
   };
-  Stream<192, kFilterPF, decltype(load)> st(load);
+  Stream<2 * NF, kFilterPF, decltype(load)> st(load);
   st.prime();
 
-  v4d h[8], o[8], h2[2], e0;
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt) {
-    h[mt] = tile_load(A.b0p[0], mt, lane);
-    o[mt] = tile_load(A.ob1p[0], mt, lane);
-  }
   v4d rb[2];
   double xb;
   rbf8(pr[pp], g, A, rb, xb);
@@ -497,52 +509,44 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_fwd_mfma(const 
   }
   // tile mt of filter `which`: its four values per lane are adjacent (fpos)
   v4d *const rowv = reinterpret_cast<v4d *>(pf + 256 * std::size_t(p) + 4 * g);
-  auto store_tile = [&](int which, int mt) {
-    if (valid) rowv[which * 32 + 4 * mt] = o[mt];
-  };
+  v4d h[8], h2[2], e0, o;
 
   st.run([&](auto si, const v4d &w) {
-    constexpr int S = decltype(si)::value, which = S / 96, s = S % 96;
-    if constexpr (s == 0) {
-      // spherical layer-0 operands of this filter (h2 is free: its last use
-      // was the previous filter's E1 pass)
-      h2[0] = tile_load(A.eb0p[which], 0, lane);
-      h2[1] = tile_load(A.eb0p[which], 1, lane);
-      e0 = reinterpret_cast<const v4d *>(A.e0pk[which])[lane];
-    }
-    // filter 0's output leaves one tile every two steps while filter 1 runs
-    // its first layer; each tile then starts over from filter 1's bias
-    if constexpr (which == 1 && s < 16 && s % 2 == 0) {
-      store_tile(0, s / 2);
-      o[s / 2] = tile_load(A.ob1p[1], s / 2, lane);
-    }
-    if constexpr (s < 16) {
-      h[s % 8] = mfma4(w, rb[s / 8], h[s % 8]);
-    } else if constexpr (s < 80) {
-      if constexpr (s == 16) {
+    constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
+    if constexpr (s < 8) {
+      h[s] = w;
+    } else if constexpr (s < 10) {
+      h2[s - 8] = w;
+    } else if constexpr (s == 10) {
+      e0 = w;
+    } else if constexpr (s < 27) {
+      h[(s - 11) % 8] = mfma4(w, rb[(s - 11) / 8], h[(s - 11) % 8]);
+    } else {
+      constexpr int mt = (s - 27) / 11, u = (s - 27) % 11;
+      if constexpr (s == 27) {
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt)
+        for (int t = 0; t < 8; ++t)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) h[mt][r] = silu(h[mt][r]);
+          for (int r = 0; r < 4; ++r) h[t][r] = silu(h[t][r]);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          h2[mt] = mfma(e0[mt], sg, h2[mt]);
+        for (int t = 0; t < 2; ++t) {
+          h2[t] = mfma(e0[t], sg, h2[t]);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) h2[mt][r] = silu(h2[mt][r]);
+          for (int r = 0; r < 4; ++r) h2[t][r] = silu(h2[t][r]);
         }
       }
-      o[(s - 16) % 8] = mfma4(w, h[(s - 16) / 8], o[(s - 16) % 8]);
-    } else {
-      if constexpr (s == 80 && which == 0) {
-        // h is free after the W1 pass: the next filter's layer-0 bias
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt) h[mt] = tile_load(A.b0p[1], mt, lane);
+      if constexpr (u == 0) {
+        o = w;
+      } else if constexpr (u <= 8) {
+        o = mfma4(w, h[u - 1], o);
+      } else {
+        o = mfma4(w, h2[u - 9], o);
+        if constexpr (u == 10) {
+          if (valid) rowv[which * 32 + 4 * mt] = o;
+        }
       }
-      o[(s - 80) % 8] = mfma4(w, h2[(s - 80) / 8], o[(s - 80) % 8]);
     }
   });
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt) store_tile(1, mt);
 }
 
 // Reverse of both filters, the Bernstein basis and the cutoff for 16 pairs per
