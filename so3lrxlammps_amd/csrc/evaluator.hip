@@ -686,17 +686,19 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
 // (bias_acc) and starts the accumulators.  Output tiles are taken MG at a
 // time; per tile group the operand stream holds, per K chunk, the X chunk and
 // the MG weight fragments.
-template <int EPI, int KT, int MT>
+template <int EPI, int KT, int MT, int MG>
 __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const double *__restrict__ X, int ldx,
                                               const double *__restrict__ Wp, const double *__restrict__ biasp,
                                               double *__restrict__ out, int ldo, double *__restrict__ out2,
                                               const double *__restrict__ aux, int ldaux) {
-  constexpr int MG = MT <= 10 ? MT : 10;
+  // one group of MG output tiles per wavefront (the group is blockIdx.y), so
+  // a few thousand node rows still give every SIMD several wavefronts
   static_assert(MT % MG == 0, "output tiles must split into equal groups");
-  constexpr int NG = MT / MG, PER_T = 1 + MG, PER_G = KT * PER_T;
+  constexpr int PER_T = 1 + MG, PER_G = KT * PER_T;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w * 16 >= rows) return;
+  const int grp = blockIdx.y;
   const int n = w * 16 + j;
   const bool valid = n < rows;
   const int nn = valid ? n : rows - 1;
@@ -704,7 +706,7 @@ __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const doub
   const v4d zero = v4d{0, 0, 0, 0};
 
   auto load = [&](auto si) -> v4d {
-    constexpr int S = decltype(si)::value, grp = S / PER_G, s = S % PER_G, T = s / PER_T, u = s % PER_T;
+    constexpr int s = decltype(si)::value, T = s / PER_T, u = s % PER_T;
     if constexpr (u == 0) {
       v4d b;
 #pragma unroll
@@ -717,50 +719,43 @@ __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const doub
       return wload(Wp, KT, grp * MG + u - 1, T, lane);
     }
   };
-  Stream<NG * PER_G, kFilterPF, decltype(load)> st(load);
+  Stream<PER_G, kFilterPF, decltype(load)> st(load);
   v4d acc[MG], xa[MG];
-  auto start_group = [&](int grp) {
 #pragma unroll
-    for (int q = 0; q < MG; ++q) acc[q] = biasp ? tile_load(biasp, grp * MG + q, lane) : zero;
-    if constexpr (EPI == 2 || EPI == 3) {
+  for (int q = 0; q < MG; ++q) acc[q] = biasp ? tile_load(biasp, grp * MG + q, lane) : zero;
+  if constexpr (EPI == 2 || EPI == 3) {
 #pragma unroll
-      for (int q = 0; q < MG; ++q)
+    for (int q = 0; q < MG; ++q)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int o = 16 * (grp * MG + q) + g + 4 * r;
-          xa[q][r] = o < O ? aux[std::size_t(nn) * ldaux + o] : 0.0;
-        }
-    }
-  };
-  start_group(0);
+      for (int r = 0; r < 4; ++r) {
+        const int o = 16 * (grp * MG + q) + g + 4 * r;
+        xa[q][r] = o < O ? aux[std::size_t(nn) * ldaux + o] : 0.0;
+      }
+  }
   st.prime();
   v4d bT = zero;
   st.run([&](auto si, const v4d &wv) {
-    constexpr int S = decltype(si)::value, grp = S / PER_G, s = S % PER_G, u = s % PER_T;
+    constexpr int s = decltype(si)::value, u = s % PER_T;
     if constexpr (u == 0) {
       bT = wv;
     } else {
       acc[u - 1] = mfma4(wv, bT, acc[u - 1]);
     }
-    if constexpr (s == PER_G - 1) {
-      if (valid) {
-#pragma unroll
-        for (int q = 0; q < MG; ++q)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 16 * (grp * MG + q) + g + 4 * r;
-            if (o >= O) continue;
-            const std::size_t io = std::size_t(n) * ldo + o;
-            const double v = acc[q][r];
-            if constexpr (EPI == 0) out[io] = v;
-            if constexpr (EPI == 1) { out[io] = v; out2[io] = silu(v); }
-            if constexpr (EPI == 2) out[io] = v + xa[q][r];
-            if constexpr (EPI == 3) out[io] = v * silu_prime(xa[q][r]);
-          }
-      }
-      if constexpr (grp + 1 < NG) start_group(grp + 1);
-    }
   });
+  if (!valid) return;
+#pragma unroll
+  for (int q = 0; q < MG; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = 16 * (grp * MG + q) + g + 4 * r;
+      if (o >= O) continue;
+      const std::size_t io = std::size_t(n) * ldo + o;
+      const double v = acc[q][r];
+      if constexpr (EPI == 0) out[io] = v;
+      if constexpr (EPI == 1) { out[io] = v; out2[io] = silu(v); }
+      if constexpr (EPI == 2) out[io] = v + xa[q][r];
+      if constexpr (EPI == 3) out[io] = v * silu_prime(xa[q][r]);
+    }
 }
 
 // Block-diagonal projections: per head h, the 160 outputs (q k v q_ev k_ev,
@@ -775,9 +770,10 @@ __global__ __launch_bounds__(256) void k_qkv_mfma(int rows, const double *__rest
   const int n = w * 16 + j;
   const bool valid = n < rows;
   const double *xr = X + std::size_t(valid ? n : rows - 1) * kF;
+  const int h = blockIdx.y;  // one head per wavefront
   constexpr int PER_H = 2 + 20;
   auto load = [&](auto si) -> v4d {
-    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H;
+    constexpr int s = decltype(si)::value;
     if constexpr (s < 2) {
       return v4d{xr[h * kHW + 16 * s + g], xr[h * kHW + 16 * s + g + 4], xr[h * kHW + 16 * s + g + 8],
                  xr[h * kHW + 16 * s + g + 12]};
@@ -785,12 +781,12 @@ __global__ __launch_bounds__(256) void k_qkv_mfma(int rows, const double *__rest
       return wload(Wp + std::size_t(h) * 160 * kHW, 2, (s - 2) / 2, (s - 2) % 2, lane);
     }
   };
-  Stream<kHeads * PER_H, kFilterPF, decltype(load)> st(load);
+  Stream<PER_H, kFilterPF, decltype(load)> st(load);
   st.prime();
   const v4d zero = v4d{0, 0, 0, 0};
   v4d b[2] = {zero, zero}, acc[10];
   st.run([&](auto si, const v4d &wv) {
-    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H;
+    constexpr int s = decltype(si)::value;
     if constexpr (s < 2) {
       b[s] = wv;
       if constexpr (s == 0) {
@@ -828,9 +824,10 @@ __global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *__
   const int n = w * 16 + j;
   const bool valid = n < rows;
   const double *gr = G + std::size_t(valid ? n : rows - 1) * 640;
+  const int h = blockIdx.y;  // one head per wavefront
   constexpr int PER_H = 10 * 3;
   auto load = [&](auto si) -> v4d {
-    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H, T = s / 3, u = s % 3;
+    constexpr int s = decltype(si)::value, T = s / 3, u = s % 3;
     if constexpr (u == 0) {
       // K entries 16 T + g + 4 v: projection T / 2, channels 32 h + 16 (T % 2)
       // + g + 4 v, adjacent in the tile-transposed row order (fpos)
@@ -839,12 +836,12 @@ __global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *__
       return wload(Wtp + std::size_t(h) * kHW * 160, 10, u - 1, T, lane);
     }
   };
-  Stream<kHeads * PER_H, kFilterPF, decltype(load)> st(load);
+  Stream<PER_H, kFilterPF, decltype(load)> st(load);
   st.prime();
   const v4d zero = v4d{0, 0, 0, 0};
   v4d bT = zero, acc[2];
   st.run([&](auto si, const v4d &wv) {
-    constexpr int S = decltype(si)::value, h = S / PER_H, s = S % PER_H, u = s % 3;
+    constexpr int s = decltype(si)::value, u = s % 3;
     if constexpr (s == 0) { acc[0] = zero; acc[1] = zero; }
     if constexpr (u == 0) bT = wv;
     else acc[u - 1] = mfma4(wv, bT, acc[u - 1]);
@@ -2145,18 +2142,23 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   auto fill = [&](double *p, std::size_t cnt) {
     if (cnt) hipLaunchKernelGGL(k_fill, dim3(unsigned((cnt + 255) / 256)), dim3(256), 0, s, p, cnt, 0.0);
   };
-  // node GEMM shapes (K, O) of the model: 128x128, 132x132, 128->320, 320->128
+  // node GEMM shapes (K, O) of the model: 128x128, 132x132, 128->320, 320->128;
+  // output tiles per wavefront: MT / MG groups run as separate wavefronts
+#ifndef SO3LR_MG8
+#define SO3LR_MG8 4
+#endif
   auto gemm = [&](int epi, int rows, int K, int O, const double *X, int ldx, const double *Wp, const double *bias,
                   double *out, int ldo, double *out2, const double *aux, int ldaux) {
     const dim3 grid(unsigned(ceil_div(rows, 64)));
-#define SO3LR_GEMM(E, KT, MT)                                                                                   \
-  if (epi == E && (K + 15) / 16 == KT && (O + 15) / 16 == MT) {                                                \
-    hipLaunchKernelGGL((k_gemm<E, KT, MT>), grid, dim3(256), 0, s, rows, K, O, X, ldx, Wp, bias, out, ldo, out2, \
-                       aux, ldaux);                                                                          \
+#define SO3LR_GEMM(E, KT, MT, MG)                                                                             \
+  if (epi == E && (K + 15) / 16 == KT && (O + 15) / 16 == MT) {                                              \
+    hipLaunchKernelGGL((k_gemm<E, KT, MT, MG>), dim3(grid.x, MT / MG), dim3(256), 0, s, rows, K, O, X, ldx, Wp, \
+                       bias, out, ldo, out2, aux, ldaux);                                                     \
     return;                                                                                                   \
   }
-    SO3LR_GEMM(0, 8, 8) SO3LR_GEMM(0, 9, 9) SO3LR_GEMM(0, 20, 8) SO3LR_GEMM(1, 8, 8) SO3LR_GEMM(1, 8, 20)
-    SO3LR_GEMM(2, 8, 8) SO3LR_GEMM(3, 8, 8)
+    SO3LR_GEMM(0, 8, 8, SO3LR_MG8) SO3LR_GEMM(0, 9, 9, 3) SO3LR_GEMM(0, 20, 8, SO3LR_MG8)
+    SO3LR_GEMM(1, 8, 8, SO3LR_MG8) SO3LR_GEMM(1, 8, 20, 4) SO3LR_GEMM(2, 8, 8, SO3LR_MG8)
+    SO3LR_GEMM(3, 8, 8, SO3LR_MG8)
 #undef SO3LR_GEMM
     throw std::logic_error("SO3LR: internal error, no node GEMM for this shape");
   };
@@ -2212,7 +2214,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       A.fe0[k] = B.fe0[k]; A.feb0[k] = B.feb0[k]; A.fe1t[k] = B.fe1t[k]; A.feb1[k] = B.feb1[k];
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
-    hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
+    hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     timed("filter_fwd", 0, [&] {
       if (naive_filters_)
@@ -2288,7 +2290,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       else
         hipLaunchKernelGGL(k_filter_bwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds, dr);
     });
-    hipLaunchKernelGGL(k_qkv_bwd_mfma, dim3(gN64), dim3(256), 0, s, int(N), gqkv, B.qkvtp, gainv, gx);
+    hipLaunchKernelGGL(k_qkv_bwd_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), gqkv, B.qkvtp, gainv, gx);
     hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, evb, B.att_cg, ds,
                        gaev, gev);
   }
