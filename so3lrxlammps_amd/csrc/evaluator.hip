@@ -204,6 +204,28 @@ __global__ __launch_bounds__(256) void k_sr_compact(
   }
 }
 
+// Workgroups go to the 8 XCDs round-robin (block b on XCD b % 8).  Remapped
+// so that each XCD walks one contiguous range of logical blocks: with nodes
+// in spatial order, the neighbour rows a range gathers stay in its XCD's L2.
+// A bijection of [0, gridDim.x) whatever the grid size.
+__device__ __forceinline__ int xcd_block() {
+#ifdef SO3LR_NO_XCD_MAP
+  return blockIdx.x;
+#endif
+  const int G = gridDim.x, b = blockIdx.x;
+  const int per = G >> 3, rem = G & 7, xcd = b & 7, i = b >> 3;
+  return xcd * per + (xcd < rem ? xcd : rem) + i;
+}
+// The same for a grid sized for an upper bound of the work: only the first A
+// logical blocks have work (A <= gridDim.x, known on the device only), and
+// they are spread evenly over the XCDs; -1 for a block with none.
+__device__ __forceinline__ int xcd_block_active(int A) {
+  const int b = blockIdx.x;
+  const int per = A >> 3, rem = A & 7, xcd = b & 7, i = b >> 3;
+  if (i >= per + (xcd < rem ? 1 : 0)) return -1;
+  return xcd * per + (xcd < rem ? xcd : rem) + i;
+}
+
 // ---------------------------------------------------------------- filters
 // Per active pair: Bernstein basis and PhysNet cutoff of r, the equivariant
 // invariant s_l = sum_{m in l} (ev_a - ev_b)^2 cg, and both filters
@@ -461,21 +483,33 @@ __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, v4d *
 // K chunk s / 8), W1 (16 <= s < 80) and E1 (80 <= s < 96), tile-minor.
 __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(const int *n_active, const int *pa,
                                                                      const double *pr, const double *ev,
-                                                                     FilterMfma A, double *ps, double *pf) {
+                                                                     const double *__restrict__ qkv, double inv_avg,
+                                                                     FilterMfma A, double *ps, double *pf,
+                                                                     double *palpha) {
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // consecutive pairs on one XCD: the endpoint rows they read are
+  // spatial neighbours, so they share that XCD's L2
+  const int blk = xcd_block_active((nact + 63) / 64);
+  if (blk < 0) return;
+  const int wave = blk * 4 + (threadIdx.x >> 6);
   if (wave * 16 >= nact) return;  // whole wavefront idle
   const int p = wave * 16 + j;
   const bool valid = p < nact;
   const int pp = valid ? p : nact - 1;
+  const int a = pa[2 * pp], b = pa[2 * pp + 1];
+  // q k v q_ev k_ev rows of both endpoints (tile-transposed channel order):
+  // the lane's four channels of an output tile are one 32-byte vector
+  const double *qa = qkv + std::size_t(a) * 640 + 4 * g, *qb = qkv + std::size_t(b) * 640 + 4 * g;
 
-  // Per filter the stream holds 115 entries: the layer-0 bias tiles (8), the
+  // Per filter the stream holds 147 entries: the layer-0 bias tiles (8), the
   // spherical layer-0 bias tiles (2) and operand (1), W0 (16: tile s % 8, K
-  // chunk s / 8), then per output tile mt its bias, the 8 W1 chunks and the
-  // 2 E1 chunks (11 each).  The output is built one tile at a time and stored
-  // as soon as it is complete, so only one output accumulator is live.
-  constexpr int NF = 115;
+  // chunk s / 8), then per output tile mt its bias, the 8 W1 chunks, the
+  // 2 E1 chunks and the endpoint rows q_a, k_b, q_b, k_a of its channels
+  // (15 each).  The output is built one tile at a time and stored as soon as
+  // it is complete, so only one output accumulator is live; the attention
+  // logits of both directions are reduced from it on the spot.
+  constexpr int NF = 147;
   auto load = [&](auto si) -> v4d {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
     if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
@@ -483,10 +517,15 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
     else if constexpr (s == 10) return tile_load(A.e0pk[which], 0, lane);
     else if constexpr (s < 27) return wload(A.w0p[which], 2, (s - 11) % 8, (s - 11) / 8, lane);
     else {
-      constexpr int mt = (s - 27) / 11, u = (s - 27) % 11;
+      constexpr int mt = (s - 27) / 15, u = (s - 27) % 15;
+      constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;  // q, k (invariant) or q_ev, k_ev
       if constexpr (u == 0) return tile_load(A.ob1p[which], mt, lane);
       else if constexpr (u <= 8) return wload(A.w1p[which], 8, mt, u - 1, lane);
-      else return wload(A.e1p[which], 2, mt, u - 9, lane);
+      else if constexpr (u <= 10) return wload(A.e1p[which], 2, mt, u - 9, lane);
+      else if constexpr (u == 11) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
+      else if constexpr (u == 12) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
+      else if constexpr (u == 13) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
+      else return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
     }
   };
   Stream<2 * NF, kFilterPF, decltype(load)> st(load);
@@ -498,7 +537,6 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
   double sg = 0.0;
   {
-    const int a = pa[2 * pp], b = pa[2 * pp + 1];
     const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
     const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
     for (int m = lo; m < hi; ++m) {
@@ -509,7 +547,8 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   }
   // tile mt of filter `which`: its four values per lane are adjacent (fpos)
   v4d *const rowv = reinterpret_cast<v4d *>(pf + 256 * std::size_t(p) + 4 * g);
-  v4d h[8], h2[2], e0, o;
+  v4d h[8], h2[2], e0, o, qv;
+  double t0 = 0.0, t1 = 0.0;  // per-head partial logits: a <- b (side 0), b <- a (side 1)
 
   st.run([&](auto si, const v4d &w) {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
@@ -522,7 +561,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
     } else if constexpr (s < 27) {
       h[(s - 11) % 8] = mfma4(w, rb[(s - 11) / 8], h[(s - 11) % 8]);
     } else {
-      constexpr int mt = (s - 27) / 11, u = (s - 27) % 11;
+      constexpr int mt = (s - 27) / 15, u = (s - 27) % 15;
       if constexpr (s == 27) {
 #pragma unroll
         for (int t = 0; t < 8; ++t)
@@ -539,10 +578,33 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
         o = w;
       } else if constexpr (u <= 8) {
         o = mfma4(w, h[u - 1], o);
-      } else {
+      } else if constexpr (u <= 10) {
         o = mfma4(w, h2[u - 9], o);
         if constexpr (u == 10) {
           if (valid) rowv[which * 32 + 4 * mt] = o;
+        }
+      } else if constexpr (u == 11 || u == 13) {
+        qv = w;
+      } else {
+        // <q_recv, k_send (.) f> over the lane's four channels of this tile
+        const double d = ((qv[0] * w[0] * o[0] + qv[1] * w[1] * o[1]) + qv[2] * w[2] * o[2]) + qv[3] * w[3] * o[3];
+        if constexpr (u == 12) t0 += d;
+        else t1 += d;
+        if constexpr (u == 14 && (mt & 1)) {
+          // head mt / 2 complete: sum its 32 channels over the four lane
+          // groups; the alpha of edge b -> a belongs to side 0 (a receives)
+          t0 += __shfl_xor(t0, 16, kWave);
+          t0 += __shfl_xor(t0, 32, kWave);
+          t1 += __shfl_xor(t1, 16, kWave);
+          t1 += __shfl_xor(t1, 32, kWave);
+          constexpr int hd = mt / 2;
+          if (valid && g == hd) {
+            double *al = palpha + 16 * std::size_t(p) + 4 * which + hd;
+            al[0] = t0 * inv_avg;
+            al[8] = t1 * inv_avg;
+          }
+          t0 = 0.0;
+          t1 = 0.0;
         }
       }
     }
@@ -867,18 +929,6 @@ __device__ __forceinline__ void st2(double *p, double a, double b) { *reinterpre
 // holds the invariant channels 32 h + t and 32 h + 16 + t (t = l % 16) and the
 // equivariant channel off[h] + t of degree h + 1 when t < 2 h + 3, so every
 // per-head sum is a 16-lane group reduction.
-// Workgroups go to the 8 XCDs round-robin (block b on XCD b % 8).  Remapped
-// so that each XCD walks one contiguous range of logical blocks: with nodes
-// in spatial order, the neighbour rows a range gathers stay in its XCD's L2.
-// A bijection of [0, gridDim.x) whatever the grid size.
-__device__ __forceinline__ int xcd_block() {
-#ifdef SO3LR_NO_XCD_MAP
-  return blockIdx.x;
-#endif
-  const int G = gridDim.x, b = blockIdx.x;
-  const int per = G >> 3, rem = G & 7, xcd = b & 7, i = b >> 3;
-  return xcd * per + (xcd < rem ? xcd : rem) + i;
-}
 
 __device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
 
@@ -924,6 +974,8 @@ __device__ __forceinline__ void for_active_pairs(int beg, int end, const int *ia
 // alpha = <q_n, k_o (.) f_p> / avg (per head) and the messages
 // fc alpha v_o (invariant) and fc alpha_ev Y (equivariant, (-1)^l Y when n is
 // the pair's second endpoint).  Lanes: 16 per head, two channels each.
+// This full form runs with the scalar filter kernels; the MFMA filter forms
+// alpha itself and k_attn_msg does the rest.
 __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, const int *__restrict__ iact,
                                                   const int *__restrict__ iother, const double *__restrict__ x,
                                                   const double *__restrict__ ev, const double *__restrict__ qkv,
@@ -988,6 +1040,47 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
   if (evv) aev[std::size_t(n) * kE + m] = ev[std::size_t(n) * kE + m] + acce;
 }
 
+// Attention forward messages, node-major, with the per-direction logits the
+// forward MFMA filter computed (same lane layout as k_attn_fwd): for node n
+// and every incident active pair, fc alpha v_o (invariant) and fc alpha_ev Y
+// (equivariant, (-1)^l Y when n is the pair's second endpoint).
+__global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, const int *__restrict__ iact,
+                                                  const int *__restrict__ iother, const double *__restrict__ x,
+                                                  const double *__restrict__ ev, const double *__restrict__ qkv,
+                                                  const double *__restrict__ pY, const double *__restrict__ pfc,
+                                                  const double *__restrict__ palpha, double *__restrict__ ainv,
+                                                  double *__restrict__ aev) {
+  const int lane = threadIdx.x & 63;
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int h = lane >> 4, t = lane & 15;
+  const int p0 = 32 * h + 2 * t;
+  const int c0 = fpos(p0), c1 = c0 + 4;
+  const bool evv = t < 2 * h + 3;
+  const int m = evv ? ev_offset(h) + t : 0;
+  const double par = slot_parity(h);
+  double acc0 = 0.0, acc1 = 0.0, acce = 0.0;
+  struct Terms { double d0, d1, de; };
+  auto terms = [&](int e, int o) {
+    const int p = e >> 1, side = e & 1;
+    const double2 vv = ld2(qkv + std::size_t(o) * 640 + 256 + p0);
+    const double *al = palpha + 16 * std::size_t(p) + 8 * side;
+    const double ai = al[h], ae = al[4 + h];
+    const double fc = pfc[p];
+    const double y = pY[kE * std::size_t(p) + m] * (side == 0 ? 1.0 : par);
+    return Terms{fc * ai * vv.x, fc * ai * vv.y, fc * ae * y};
+  };
+  for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+    const Terms A = terms(e1, o1);
+    const Terms B = terms(e2, o2);
+    acc0 += A.d0; acc1 += A.d1; acce += A.de;
+    if (two) { acc0 += B.d0; acc1 += B.d1; acce += B.de; }
+  });
+  const std::size_t i = std::size_t(n) * kF;
+  ainv[i + c0] = x[i + c0] + acc0;
+  ainv[i + c1] = x[i + c1] + acc1;
+  if (evv) aev[std::size_t(n) * kE + m] = ev[std::size_t(n) * kE + m] + acce;
+}
 
 // LayerNorm over 128 channels held two per lane (biased variance).
 __device__ __forceinline__ void wave_layer_norm(double v0, double v1, const double *w, const double *b,
@@ -2216,15 +2309,23 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
+    // the MFMA filter also forms the attention logits of both directions
+    // from the filter tiles it holds; the scalar cross-check path leaves them
+    // to the full attention kernel
     timed("filter_fwd", 0, [&] {
       if (naive_filters_)
         hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
       else
-        hipLaunchKernelGGL(k_filter_fwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, FM, psb, pfb);
+        hipLaunchKernelGGL(k_filter_fwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM, psb,
+                           pfb, pab);
     });
     timed("attn_fwd", 1, [&] {
-      hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb,
-                         pfb, pY, pfc, inv_avg, pab, ainv, aevb);
+      if (naive_filters_)
+        hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb,
+                           pfb, pY, pfc, inv_avg, pab, ainv, aevb);
+      else
+        hipLaunchKernelGGL(k_attn_msg, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb, pY,
+                           pfc, pab, ainv, aevb);
     });
     hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
                        n1ib, act);
