@@ -31,6 +31,50 @@ __device__ __forceinline__ double silu_prime(double x) {
   return s * (1.0 + x * (1.0 - s));
 }
 
+// Lean forms for the MFMA filter kernels.  On gfx950 every VALU instruction
+// a wavefront issues takes issue time from the fp64 MFMAs of its SIMD, so the
+// activations there are written for the fewest instructions at full fp64
+// accuracy (a few ulp), with no IEEE special-case handling beyond a clamp:
+//   e^x: Cody-Waite reduction x = n ln2 + r, |r| <= ln2 / 2, with ln2 split
+//        into a 32-bit-exact high part and a low part, then the degree-13
+//        Taylor polynomial of e^r (truncation < 4e-18 relative) and 2^n;
+//        for -745 <= x <= 708 (below that the result underflows to 0);
+//   1/d: the hardware reciprocal refined by two Newton steps
+//        r <- r + r (1 - d r), each squaring the relative error.
+__device__ __forceinline__ double exp_lean(double x) {
+  const double n = __builtin_rint(x * 1.4426950408889634074);
+  double r = fma(n, -6.93147180369123816490e-01, x);
+  r = fma(n, -1.90821492927058770002e-10, r);
+  double p = 1.0 / 6227020800.0;  // 1/13!
+  p = fma(p, r, 1.0 / 479001600.0);
+  p = fma(p, r, 1.0 / 39916800.0);
+  p = fma(p, r, 1.0 / 3628800.0);
+  p = fma(p, r, 1.0 / 362880.0);
+  p = fma(p, r, 1.0 / 40320.0);
+  p = fma(p, r, 1.0 / 5040.0);
+  p = fma(p, r, 1.0 / 720.0);
+  p = fma(p, r, 1.0 / 120.0);
+  p = fma(p, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  return __builtin_ldexp(p, int(n));
+}
+__device__ __forceinline__ double rcp_lean(double d) {
+  double r = __builtin_amdgcn_rcp(d);
+  r = fma(fma(-d, r, 1.0), r, r);
+  return fma(fma(-d, r, 1.0), r, r);
+}
+// sigmoid(x) = 1 / (1 + e^-x); x >= -708 keeps e^-x finite (below, the
+// sigmoid is < 1e-307 either way)
+__device__ __forceinline__ double sigmoid_lean(double x) { return rcp_lean(1.0 + exp_lean(-fmax(x, -708.0))); }
+__device__ __forceinline__ double silu_lean(double x) { return x * sigmoid_lean(x); }
+__device__ __forceinline__ double silu_prime_lean(double x) {
+  const double s = sigmoid_lean(x);
+  return s * (1.0 + x * (1.0 - s));
+}
+
 // degree slot (0..3 for l = 1..4) of equivariant channel m in 0..23
 __device__ __forceinline__ int degree_slot(int m) { return m < 3 ? 0 : (m < 8 ? 1 : (m < 15 ? 2 : 3)); }
 // (-1)^l for the slot: the parity of Y_l under v -> -v

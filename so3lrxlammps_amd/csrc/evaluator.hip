@@ -399,8 +399,43 @@ struct FilterMfma {
   const double *e0pk[2];                                // spherical layer 0: one v4d per lane {tile 0, tile 1, 0, 0}
   const double *att_cg;
   const double *rbf_b, *rbf_k, *rbf_kr;
+  const double *exp2_64;  // 2^(j/64), j < 64
   double gamma;
 };
+
+// Activations of the MFMA filter kernels.  On gfx950 every VALU instruction a
+// wavefront issues takes issue time from the fp64 MFMAs of its SIMD, so these
+// are written for the fewest instructions at full fp64 accuracy (a few ulp):
+// e^x = 2^m 2^(j/64) e^r with x = (64 m + j) ln2/64 + r, |r| <= ln2/128
+// (Cody-Waite, ln2/64 split into a 20-bit high part and a low part), 2^(j/64)
+// from a 64-entry table in LDS and the degree-5 Taylor polynomial of e^r
+// (truncation < 4e-17 relative).  The power 2^m is capped at 2^1000, which
+// only matters for x > 693; valid for |x| < 1e6.
+__device__ __forceinline__ double exp_tab(double x, const double *tab) {
+  const double n = __builtin_rint(x * 92.332482616893656768);  // 64 / ln2
+  double r = fma(n, -0.010830417275428772, x);
+  r = fma(n, -7.420820373486988e-09, r);
+  const int k = int(n);
+  double p = 1.0 / 120.0;
+  p = fma(p, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  return __builtin_ldexp(p * tab[k & 63], min(k >> 6, 1000));
+}
+__device__ __forceinline__ double silu_tab(double x, const double *tab) {
+  return x * rcp_lean(1.0 + exp_tab(-x, tab));
+}
+__device__ __forceinline__ double silu_prime_tab(double x, const double *tab) {
+  const double s = rcp_lean(1.0 + exp_tab(-x, tab));
+  return s * (1.0 + x * (1.0 - s));
+}
+// The table into LDS: call at kernel start, before any wavefront returns.
+#define SO3LR_EXP2_TABLE(A)                                               \
+  __shared__ double exp2_lds[64];                                         \
+  if (threadIdx.x < 64) exp2_lds[threadIdx.x] = (A).exp2_64[threadIdx.x]; \
+  __syncthreads();
 
 // Compile-time loop: f(std::integral_constant<int, S>) for S = 0 .. N-1, so
 // every register-array index below is a constant and nothing spills.
@@ -466,7 +501,8 @@ __device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
 }
 
 // Bernstein basis of pair distance r at channels 16 T + g + 4 v (T < 2, v < 4).
-__device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, v4d *rb, double &xb) {
+__device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, const double *tab, v4d *rb,
+                                     double &xb) {
   double x = exp(-A.gamma * r);
   x = x < 1e-6 ? 1e-6 : (x > 1.0 - 1e-6 ? 1.0 - 1e-6 : x);
   xb = x;
@@ -474,7 +510,7 @@ __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, v4d *
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
-    rb[t >> 2][t & 3] = exp(A.rbf_b[ch] + A.rbf_k[ch] * lx + A.rbf_kr[ch] * l1x);
+    rb[t >> 2][t & 3] = exp_tab(A.rbf_b[ch] + A.rbf_k[ch] * lx + A.rbf_kr[ch] * l1x, tab);
   }
 }
 
@@ -486,6 +522,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
                                                                      const double *__restrict__ qkv, double inv_avg,
                                                                      FilterMfma A, double *ps, double *pf,
                                                                      double *palpha) {
+  SO3LR_EXP2_TABLE(A)
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   // consecutive pairs on one XCD: the endpoint rows they read are
@@ -533,7 +570,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 
   v4d rb[2];
   double xb;
-  rbf8(pr[pp], g, A, rb, xb);
+  rbf8(pr[pp], g, A, exp2_lds, rb, xb);
   // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
   double sg = 0.0;
   {
@@ -560,24 +597,30 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
       e0 = w;
     } else if constexpr (s < 27) {
       h[(s - 11) % 8] = mfma4(w, rb[(s - 11) / 8], h[(s - 11) % 8]);
+      // each hidden tile's SiLU is taken one step before its first use,
+      // behind the MFMAs just issued (tile 0 here, tile t at W1 step t)
+      if constexpr (s == 26) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[0][r] = silu_tab(h[0][r], exp2_lds);
+      }
     } else {
       constexpr int mt = (s - 27) / 15, u = (s - 27) % 15;
-      if constexpr (s == 27) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) h[t][r] = silu(h[t][r]);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          h2[t] = mfma(e0[t], sg, h2[t]);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) h2[t][r] = silu(h2[t][r]);
-        }
-      }
       if constexpr (u == 0) {
         o = w;
       } else if constexpr (u <= 8) {
         o = mfma4(w, h[u - 1], o);
+        if constexpr (mt == 0 && u < 8) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) h[u][r] = silu_tab(h[u][r], exp2_lds);
+        }
+        if constexpr (mt == 0 && u == 8) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            h2[t] = mfma(e0[t], sg, h2[t]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab(h2[t][r], exp2_lds);
+          }
+        }
       } else if constexpr (u <= 10) {
         o = mfma4(w, h2[u - 9], o);
         if constexpr (u == 10) {
@@ -622,6 +665,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const int *n_active, const double *pr, const double *ps,
                                                          const double *df, const double *dfc, FilterMfma A, double rc,
                                                          double *ds, double *dr) {
+  SO3LR_EXP2_TABLE(A)
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -662,10 +706,10 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
   const double r = pr[pp];
   v4d rb[2];
   double xb;
-  rbf8(r, g, A, rb, xb);
+  rbf8(r, g, A, exp2_lds, rb, xb);
   const double sg = ps[4 * std::size_t(pp) + g];
   const v4d zero = v4d{0, 0, 0, 0};
-  v4d dh[8], dh2[2], bT, pre, pre2[2];
+  v4d dh[8], dh2[2], bT, pre, prev, pre2[2];
   v4d drb[2] = {zero, zero};
   v4d dsa = zero;
 
@@ -689,20 +733,27 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
         pre = w;
       } else {
         pre = mfma4(w, rb[u - 1], pre);
-        if constexpr (u == 2) {
+        // silu' of the previous tile's pre-activation (complete by now) runs
+        // while this tile's MFMAs do
+        if constexpr (u == 1 && mt > 0) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) dh[mt][q] *= silu_prime(pre[q]);
+          for (int q = 0; q < 4; ++q) dh[mt - 1][q] *= silu_prime_tab(prev[q], exp2_lds);
         }
+        if constexpr (u == 2) prev = pre;
       }
     } else if constexpr (s < 115) {
       if constexpr (s < 114) {
         pre2[s - 112] = w;
+        if constexpr (s == 112) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dh[7][q] *= silu_prime_tab(prev[q], exp2_lds);
+        }
       } else {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           pre2[mt] = mfma(w[mt], sg, pre2[mt]);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime(pre2[mt][q]);
+          for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime_tab(pre2[mt][q], exp2_lds);
         }
       }
     } else if constexpr (s < 131) {
@@ -1906,6 +1957,11 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     hw_.rbf_b = up(bb);
     hw_.rbf_k = up(std::vector<double>(kk.begin(), kk.end()));
     hw_.rbf_kr = up(std::vector<double>(kr.begin(), kr.end()));
+    {
+      std::vector<double> t(64);
+      for (int j = 0; j < 64; ++j) t[j] = double(std::exp2(static_cast<long double>(j) / 64.0L));
+      hw_.exp2_64 = up(t);
+    }
     const auto &al = m.tensor("physical.reference_alphas");
     if (al.shape.size() != 1 || al.shape[0] < 8) throw std::runtime_error("SO3LR physical reference-table contract changed");
     hw_.n_ref = int(al.shape[0]);
@@ -2122,6 +2178,7 @@ FilterMfma filter_mfma(const BlockWeights &B, const HeadWeights &H, double gamma
     FM.b0p[k] = B.b0p[k]; FM.eb0p[k] = B.eb0p[k]; FM.ob1p[k] = B.ob1p[k]; FM.e0pk[k] = B.e0pk[k];
   }
   FM.att_cg = B.att_cg; FM.rbf_b = H.rbf_b; FM.rbf_k = H.rbf_k; FM.rbf_kr = H.rbf_kr; FM.gamma = gamma;
+  FM.exp2_64 = H.exp2_64;
   return FM;
 }
 }  // namespace
