@@ -369,6 +369,7 @@ __global__ __launch_bounds__(128) void k_filter_bwd(const int *n_active, const d
 // Weights are pre-permuted on the host into that operand order, four K values
 // per lane contiguous (permute_mfma).
 typedef double v4d __attribute__((ext_vector_type(4)));
+typedef double v2d __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ v4d mfma(double a, double b, v4d c) {
   return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
@@ -624,7 +625,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
       } else if constexpr (u <= 10) {
         o = mfma4(w, h2[u - 9], o);
         if constexpr (u == 10) {
-          if (valid) rowv[which * 32 + 4 * mt] = o;
+          if (valid) __builtin_nontemporal_store(o, rowv + which * 32 + 4 * mt);
         }
       } else if constexpr (u == 11 || u == 13) {
         qv = w;
@@ -1538,8 +1539,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     if ((e & 1) == 0) {
       const std::size_t p = std::size_t(e >> 1);
       double *d = df + 256 * p;
-      st2(d + p0, T.g0, T.g1);
-      st2(d + 128 + p0, T.ge0, T.ge1);
+      __builtin_nontemporal_store(v2d{T.g0, T.g1}, reinterpret_cast<v2d *>(d + p0));
+      __builtin_nontemporal_store(v2d{T.ge0, T.ge1}, reinterpret_cast<v2d *>(d + 128 + p0));
       if (lane == 0) dfc[p] = T.fcg;
       if (evv) dY[kE * p + m] = T.dy;
     }
