@@ -1494,7 +1494,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     const double og0 = gainv[std::size_t(o) * kF + c0], og1 = gainv[std::size_t(o) * kF + c1];
     const double oge_ld = gaev[std::size_t(o) * kE + m];
     const double *fp = pf + 256 * std::size_t(p);
-    const double2 fiv = ld2(fp + p0), fev = ld2(fp + 128 + p0);
+    const v2d fiv = __builtin_nontemporal_load(reinterpret_cast<const v2d *>(fp + p0));
+    const v2d fev = __builtin_nontemporal_load(reinterpret_cast<const v2d *>(fp + 128 + p0));
     const double fi0 = fiv.x, fi1 = fiv.y, fe0 = fev.x, fe1 = fev.y;
     const double fc = pfc[p];
     const double y_ld = pY[kE * std::size_t(p) + m];
