@@ -2450,9 +2450,13 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       else
         hipLaunchKernelGGL(k_filter_bwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds, dr);
     });
-    hipLaunchKernelGGL(k_qkv_bwd_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), gqkv, B.qkvtp, gainv, gx);
-    hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, evb, B.att_cg, ds,
-                       gaev, gev);
+    // the adjoints of a block's inputs x_b, ev_b feed the block below; block
+    // 0's inputs (the embedding and ev = 0) do not depend on the positions
+    if (b > 0) {
+      hipLaunchKernelGGL(k_qkv_bwd_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), gqkv, B.qkvtp, gainv, gx);
+      hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, evb, B.att_cg, ds,
+                         gaev, gev);
+    }
   }
 
   // --- geometry reverse, forces, energies, virial ---
