@@ -1450,6 +1450,8 @@ __global__ __launch_bounds__(256) void k_ln1_bwd(int N, const double *gp, const 
 // gathered here instead of scattered).  The endpoint with side 0 also writes
 // the per-pair adjoints df (both directions), dfc and accumulates dY.  Lane
 // layout as in k_attn_fwd.
+// NODE_ADJ false (block 0): only the pair adjoints are needed, not dq, dk, dv.
+template <bool NODE_ADJ>
 __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, const int *__restrict__ iact,
                                                   const int *__restrict__ iother, const double *__restrict__ qkv,
                                                   const double *__restrict__ pf, const double *__restrict__ pY,
@@ -1532,11 +1534,13 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     return T;
   };
   auto apply = [&](const Terms &T, int e) {
-    dq0 += T.dq0; dq1 += T.dq1;
-    dqe0 += T.dqe0; dqe1 += T.dqe1;
-    dk0 += T.dk0; dk1 += T.dk1;
-    dke0 += T.dke0; dke1 += T.dke1;
-    dv0 += T.dv0; dv1 += T.dv1;
+    if constexpr (NODE_ADJ) {
+      dq0 += T.dq0; dq1 += T.dq1;
+      dqe0 += T.dqe0; dqe1 += T.dqe1;
+      dk0 += T.dk0; dk1 += T.dk1;
+      dke0 += T.dke0; dke1 += T.dke1;
+      dv0 += T.dv0; dv1 += T.dv1;
+    }
     if ((e & 1) == 0) {
       const std::size_t p = std::size_t(e >> 1);
       double *d = df + 256 * p;
@@ -1551,6 +1555,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     apply(terms(e1, o1), e1);
     if (two) apply(terms(e2, o2), e2);
   });
+  if constexpr (!NODE_ADJ) return;
   double *g = gqkv + std::size_t(n) * 640;
   st2(g + p0, dq0, dq1);
   st2(g + 128 + p0, dk0, dk1);
@@ -2440,8 +2445,12 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     gemm(0, int(N), kF, kF, ghid, kF, B.m1tp, nullptr, gact, kF, nullptr, nullptr, 0);
     hipLaunchKernelGGL(k_ln1_bwd, dim3(gN4), dim3(256), 0, s, int(N), gp, gact, n1b, B.ln1w, n1hb, n1ib, gainv);
     timed("attn_bwd", 1, [&] {
-      hipLaunchKernelGGL(k_attn_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY, pfc,
-                         pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
+      if (b > 0)
+        hipLaunchKernelGGL(k_attn_bwd<true>, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY,
+                           pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
+      else
+        hipLaunchKernelGGL(k_attn_bwd<false>, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY,
+                           pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
     });
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     timed("filter_bwd", 0, [&] {
