@@ -397,6 +397,7 @@ struct FilterMfma {
   const double *w0p[2], *w1p[2], *e1p[2];              // forward operands
   const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];  // reverse operands (transposes)
   const double *b0p[2], *eb0p[2], *ob1p[2];             // biases in accumulator order
+  const double *ob1p0[2];                               // output bias with the ev = 0 spherical branch folded in
   const double *e0pk[2];                                // spherical layer 0: one v4d per lane {tile 0, tile 1, 0, 0}
   const double *att_cg;
   const double *rbf_b, *rbf_k, *rbf_kr;
@@ -518,6 +519,7 @@ __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, const
 // Both filters of one block for 16 pairs per wavefront, 4 wavefronts per block.
 // Per filter the stream holds 96 weight fragments: W0 (s < 16: tile s % 8,
 // K chunk s / 8), W1 (16 <= s < 80) and E1 (80 <= s < 96), tile-minor.
+template <bool EV0>
 __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(const int *n_active, const int *pa,
                                                                      const double *pr, const double *ev,
                                                                      const double *__restrict__ qkv, double inv_avg,
@@ -540,29 +542,33 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   // the lane's four channels of an output tile are one 32-byte vector
   const double *qa = qkv + std::size_t(a) * 640 + 4 * g, *qb = qkv + std::size_t(b) * 640 + 4 * g;
 
-  // Per filter the stream holds 147 entries: the layer-0 bias tiles (8), the
-  // spherical layer-0 bias tiles (2) and operand (1), W0 (16: tile s % 8, K
-  // chunk s / 8), then per output tile mt its bias, the 8 W1 chunks, the
-  // 2 E1 chunks and the endpoint rows q_a, k_b, q_b, k_a of its channels
-  // (15 each).  The output is built one tile at a time and stored as soon as
-  // it is complete, so only one output accumulator is live; the attention
-  // logits of both directions are reduced from it on the spot.
-  constexpr int NF = 147;
+  // Per filter the stream holds: the layer-0 bias tiles (8), the spherical
+  // layer-0 bias tiles (2) and operand (1), W0 (16: tile s % 8, K chunk
+  // s / 8), then per output tile mt its bias, the 8 W1 chunks, the 2 E1
+  // chunks and the endpoint rows q_a, k_b, q_b, k_a of its channels (15
+  // each): 147 entries.  The output is built one tile at a time and stored as
+  // soon as it is complete, so only one output accumulator is live; the
+  // attention logits of both directions are reduced from it on the spot.
+  // EV0 (block 0, ev = 0): the spherical branch sees s = 0 for every pair,
+  // so it is the constant E1 silu(e0) + e1, folded into the output bias
+  // (ob1p0); its entries are left out (13 per tile, 128 in all).
+  constexpr int TS = EV0 ? 24 : 27, PT = EV0 ? 13 : 15, RU = EV0 ? 9 : 11;
+  constexpr int NF = TS + 8 * PT;
   auto load = [&](auto si) -> v4d {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
     if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
-    else if constexpr (s < 10) return tile_load(A.eb0p[which], s - 8, lane);
-    else if constexpr (s == 10) return tile_load(A.e0pk[which], 0, lane);
-    else if constexpr (s < 27) return wload(A.w0p[which], 2, (s - 11) % 8, (s - 11) / 8, lane);
+    else if constexpr (!EV0 && s < 10) return tile_load(A.eb0p[which], s - 8, lane);
+    else if constexpr (!EV0 && s == 10) return tile_load(A.e0pk[which], 0, lane);
+    else if constexpr (s < TS) return wload(A.w0p[which], 2, (s - TS + 16) % 8, (s - TS + 16) / 8, lane);
     else {
-      constexpr int mt = (s - 27) / 15, u = (s - 27) % 15;
+      constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
       constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;  // q, k (invariant) or q_ev, k_ev
-      if constexpr (u == 0) return tile_load(A.ob1p[which], mt, lane);
+      if constexpr (u == 0) return tile_load(EV0 ? A.ob1p0[which] : A.ob1p[which], mt, lane);
       else if constexpr (u <= 8) return wload(A.w1p[which], 8, mt, u - 1, lane);
-      else if constexpr (u <= 10) return wload(A.e1p[which], 2, mt, u - 9, lane);
-      else if constexpr (u == 11) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
-      else if constexpr (u == 12) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
-      else if constexpr (u == 13) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
+      else if constexpr (u < RU) return wload(A.e1p[which], 2, mt, u - 9, lane);
+      else if constexpr (u == RU) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
+      else if constexpr (u == RU + 1) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
+      else if constexpr (u == RU + 2) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
       else return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
     }
   };
@@ -574,7 +580,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   rbf8(pr[pp], g, A, exp2_lds, rb, xb);
   // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
   double sg = 0.0;
-  {
+  if constexpr (!EV0) {
     const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
     const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
     for (int m = lo; m < hi; ++m) {
@@ -592,20 +598,21 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
     if constexpr (s < 8) {
       h[s] = w;
-    } else if constexpr (s < 10) {
+    } else if constexpr (!EV0 && s < 10) {
       h2[s - 8] = w;
-    } else if constexpr (s == 10) {
+    } else if constexpr (!EV0 && s == 10) {
       e0 = w;
-    } else if constexpr (s < 27) {
-      h[(s - 11) % 8] = mfma4(w, rb[(s - 11) / 8], h[(s - 11) % 8]);
+    } else if constexpr (s < TS) {
+      constexpr int i = s - TS + 16;  // W0 entry 0..15
+      h[i % 8] = mfma4(w, rb[i / 8], h[i % 8]);
       // each hidden tile's SiLU is taken one step before its first use,
       // behind the MFMAs just issued (tile 0 here, tile t at W1 step t)
-      if constexpr (s == 26) {
+      if constexpr (i == 15) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) h[0][r] = silu_tab(h[0][r], exp2_lds);
       }
     } else {
-      constexpr int mt = (s - 27) / 15, u = (s - 27) % 15;
+      constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
       if constexpr (u == 0) {
         o = w;
       } else if constexpr (u <= 8) {
@@ -614,7 +621,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 #pragma unroll
           for (int r = 0; r < 4; ++r) h[u][r] = silu_tab(h[u][r], exp2_lds);
         }
-        if constexpr (mt == 0 && u == 8) {
+        if constexpr (!EV0 && mt == 0 && u == 8) {
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             h2[t] = mfma(e0[t], sg, h2[t]);
@@ -622,19 +629,22 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
             for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab(h2[t][r], exp2_lds);
           }
         }
-      } else if constexpr (u <= 10) {
-        o = mfma4(w, h2[u - 9], o);
-        if constexpr (u == 10) {
+        if constexpr (EV0 && u == 8) {
           if (valid) __builtin_nontemporal_store(o, rowv + which * 32 + 4 * mt);
         }
-      } else if constexpr (u == 11 || u == 13) {
+      } else if constexpr (u < RU) {
+        o = mfma4(w, h2[u - 9], o);
+        if constexpr (u == RU - 1) {
+          if (valid) __builtin_nontemporal_store(o, rowv + which * 32 + 4 * mt);
+        }
+      } else if constexpr (u == RU || u == RU + 2) {
         qv = w;
       } else {
         // <q_recv, k_send (.) f> over the lane's four channels of this tile
         const double d = ((qv[0] * w[0] * o[0] + qv[1] * w[1] * o[1]) + qv[2] * w[2] * o[2]) + qv[3] * w[3] * o[3];
-        if constexpr (u == 12) t0 += d;
+        if constexpr (u == RU + 1) t0 += d;
         else t1 += d;
-        if constexpr (u == 14 && (mt & 1)) {
+        if constexpr (u == RU + 3 && (mt & 1)) {
           // head mt / 2 complete: sum its 32 channels over the four lane
           // groups; the alpha of edge b -> a belongs to side 0 (a receives)
           t0 += __shfl_xor(t0, 16, kWave);
@@ -663,6 +673,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 //            (pre-activation recomputed tile by tile, then d hidden *= silu');
 //   s < 115  the spherical layer-0 biases and operand (same, for the 4 -> 32 layer);
 //   s < 131  W0^T (d rbf), s < 133  E0^T (ds).
+template <bool EV0>
 __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const int *n_active, const double *pr, const double *ps,
                                                          const double *df, const double *dfc, FilterMfma A, double rc,
                                                          double *ds, double *dr) {
@@ -676,11 +687,24 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
   const int pp = valid ? p : nact - 1;
   const v4d *dfv = reinterpret_cast<const v4d *>(df + 256 * std::size_t(pp) + 4 * g);
 
-  constexpr int NB = 133;
+  // Per filter the stream holds, in order:
+  //   per K chunk T (8): the df chunk, W1^T tiles 0..7 and E1^T tiles 0..1
+  //             (d hidden = W^T df);
+  //   per tile mt (8): the layer-0 bias, then W0 chunks 0, 1 (pre-activation
+  //             recomputed tile by tile, then d hidden *= silu');
+  //   the spherical layer-0 biases and operand (the same, 4 -> 32);
+  //   W0^T (16): d rbf = W0^T d hidden;
+  //   E0^T (2):  d s = E0^T d hidden_s.
+  // EV0 (block 0, ev = 0): the spherical branch is a constant (folded into
+  // the output bias by the forward kernel) and s has no adjoint to give, so
+  // its entries are left out.
+  constexpr int PTA = EV0 ? 9 : 11;
+  constexpr int A_END = 8 * PTA, B_END = A_END + 24, C_END = B_END + (EV0 ? 0 : 3), D_END = C_END + 16;
+  constexpr int NB = D_END + (EV0 ? 0 : 2);
   auto load = [&](auto si) -> v4d {
     constexpr int S = decltype(si)::value, which = S / NB, s = S % NB;
-    if constexpr (s < 88) {
-      constexpr int T = s / 11, u = s % 11;
+    if constexpr (s < A_END) {
+      constexpr int T = s / PTA, u = s % PTA;
       if constexpr (u == 0) {
         return dfv[which * 32 + 4 * T];  // channels 16 T + g + 4 v, v = 0..3 (fpos)
       } else if constexpr (u <= 8) {
@@ -688,17 +712,17 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
       } else {
         return wload(A.e1tp[which], 8, u - 9, T, lane);
       }
-    } else if constexpr (s < 112) {
-      constexpr int mt = (s - 88) / 3, u = (s - 88) % 3;
+    } else if constexpr (s < B_END) {
+      constexpr int mt = (s - A_END) / 3, u = (s - A_END) % 3;
       if constexpr (u == 0) return tile_load(A.b0p[which], mt, lane);
       else return wload(A.w0p[which], 2, mt, u - 1, lane);
-    } else if constexpr (s < 115) {
-      if constexpr (s < 114) return tile_load(A.eb0p[which], s - 112, lane);
+    } else if constexpr (s < C_END) {
+      if constexpr (s < C_END - 1) return tile_load(A.eb0p[which], s - B_END, lane);
       else return reinterpret_cast<const v4d *>(A.e0pk[which])[lane];
-    } else if constexpr (s < 131) {
-      return wload(A.w0tp[which], 8, (s - 115) % 2, (s - 115) / 2, lane);
+    } else if constexpr (s < D_END) {
+      return wload(A.w0tp[which], 8, (s - C_END) % 2, (s - C_END) / 2, lane);
     } else {
-      return wload(A.e0tp[which], 2, 0, s - 131, lane);
+      return wload(A.e0tp[which], 2, 0, s - D_END, lane);
     }
   };
   Stream<2 * NB, kFilterPF, decltype(load)> st(load);
@@ -708,7 +732,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
   v4d rb[2];
   double xb;
   rbf8(r, g, A, exp2_lds, rb, xb);
-  const double sg = ps[4 * std::size_t(pp) + g];
+  const double sg = EV0 ? 0.0 : ps[4 * std::size_t(pp) + g];
   const v4d zero = v4d{0, 0, 0, 0};
   v4d dh[8], dh2[2], bT, pre, prev, pre2[2];
   v4d drb[2] = {zero, zero};
@@ -722,14 +746,13 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
       dh2[0] = zero;
       dh2[1] = zero;
     }
-    if constexpr (s < 88) {
-      constexpr int T = s / 11, u = s % 11;
+    if constexpr (s < A_END) {
+      constexpr int u = s % PTA;
       if constexpr (u == 0) bT = w;
       else if constexpr (u <= 8) dh[u - 1] = mfma4(w, bT, dh[u - 1]);
       else dh2[u - 9] = mfma4(w, bT, dh2[u - 9]);
-      (void)T;
-    } else if constexpr (s < 112) {
-      constexpr int mt = (s - 88) / 3, u = (s - 88) % 3;
+    } else if constexpr (s < B_END) {
+      constexpr int mt = (s - A_END) / 3, u = (s - A_END) % 3;
       if constexpr (u == 0) {
         pre = w;
       } else {
@@ -742,13 +765,9 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
         }
         if constexpr (u == 2) prev = pre;
       }
-    } else if constexpr (s < 115) {
-      if constexpr (s < 114) {
-        pre2[s - 112] = w;
-        if constexpr (s == 112) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) dh[7][q] *= silu_prime_tab(prev[q], exp2_lds);
-        }
+    } else if constexpr (s < C_END) {
+      if constexpr (s < C_END - 1) {
+        pre2[s - B_END] = w;
       } else {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -757,10 +776,15 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
           for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime_tab(pre2[mt][q], exp2_lds);
         }
       }
-    } else if constexpr (s < 131) {
-      drb[(s - 115) % 2] = mfma4(w, dh[(s - 115) / 2], drb[(s - 115) % 2]);
+    } else if constexpr (s < D_END) {
+      drb[(s - C_END) % 2] = mfma4(w, dh[(s - C_END) / 2], drb[(s - C_END) % 2]);
     } else {
-      dsa = mfma4(w, dh2[s - 131], dsa);
+      dsa = mfma4(w, dh2[s - D_END], dsa);
+    }
+    // the last tile's silu' (it is needed from the last two W0^T steps on)
+    if constexpr (s == B_END) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dh[7][q] *= silu_prime_tab(prev[q], exp2_lds);
     }
   });
 
@@ -777,7 +801,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
   part += __shfl_xor(part, 16, kWave);
   part += __shfl_xor(part, 32, kWave);
   if (valid) {
-    ds[4 * std::size_t(p) + g] = dsa[0];  // rows 0..3 of the padded tile: lane group g, register 0
+    if constexpr (!EV0) ds[4 * std::size_t(p) + g] = dsa[0];  // rows 0..3 of the padded tile: lane group g, register 0
     if (g == 0) {
       double grad = part;
       if (r < rc) {
@@ -1885,6 +1909,15 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
       B.b0p[k] = up(bias_acc(b0, F));
       B.eb0p[k] = up(bias_acc(eb0, FH));
       B.ob1p[k] = up(bias_acc(ob1, F));
+      // with ev = 0 (block 0) the spherical branch is E1 silu(e0) + e1 for
+      // every pair: one more constant in the output bias
+      std::vector<double> ob10(ob1);
+      for (int c = 0; c < F; ++c) {
+        double acc = 0.0;
+        for (int jj = 0; jj < FH; ++jj) acc += e1[std::size_t(c) * FH + jj] * (eb0[jj] / (1.0 + std::exp(-eb0[jj])));
+        ob10[c] += acc;
+      }
+      B.ob1p0[k] = up(bias_acc(ob10, F));
       const auto e0p = permute_mfma(e0, FH, 4);  // two tiles, one value per lane each
       std::vector<double> e0pk(64 * 4, 0.0);
       for (int lane = 0; lane < 64; ++lane) {
@@ -2183,6 +2216,7 @@ FilterMfma filter_mfma(const BlockWeights &B, const HeadWeights &H, double gamma
     FM.w0p[k] = B.w0p[k]; FM.w1p[k] = B.w1p[k]; FM.e1p[k] = B.e1p[k];
     FM.w1tp[k] = B.w1tp[k]; FM.w0tp[k] = B.w0tp[k]; FM.e1tp[k] = B.e1tp[k]; FM.e0tp[k] = B.e0tp[k];
     FM.b0p[k] = B.b0p[k]; FM.eb0p[k] = B.eb0p[k]; FM.ob1p[k] = B.ob1p[k]; FM.e0pk[k] = B.e0pk[k];
+    FM.ob1p0[k] = B.ob1p0[k];
   }
   FM.att_cg = B.att_cg; FM.rbf_b = H.rbf_b; FM.rbf_k = H.rbf_k; FM.rbf_kr = H.rbf_kr; FM.gamma = gamma;
   FM.exp2_64 = H.exp2_64;
@@ -2379,9 +2413,12 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     timed("filter_fwd", 0, [&] {
       if (naive_filters_)
         hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
+      else if (b == 0)  // ev = 0: the spherical branch is a constant
+        hipLaunchKernelGGL(k_filter_fwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
+                           psb, pfb, pab);
       else
-        hipLaunchKernelGGL(k_filter_fwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM, psb,
-                           pfb, pab);
+        hipLaunchKernelGGL(k_filter_fwd_mfma<false>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
+                           psb, pfb, pab);
     });
     timed("attn_fwd", 1, [&] {
       if (naive_filters_)
@@ -2456,8 +2493,12 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     timed("filter_bwd", 0, [&] {
       if (naive_filters_)
         hipLaunchKernelGGL(k_filter_bwd, dim3(gP), dim3(128), 0, s, nact, pr, pfc, psb, df, dfc, A, rc_, ds, dr);
+      else if (b == 0)
+        hipLaunchKernelGGL(k_filter_bwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds,
+                           dr);
       else
-        hipLaunchKernelGGL(k_filter_bwd_mfma, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds, dr);
+        hipLaunchKernelGGL(k_filter_bwd_mfma<false>, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds,
+                           dr);
     });
     // the adjoints of a block's inputs x_b, ev_b feed the block below; block
     // 0's inputs (the embedding and ev = 0) do not depend on the positions

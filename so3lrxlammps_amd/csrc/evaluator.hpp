@@ -42,7 +42,8 @@ struct BlockWeights {
   // MFMA operand order of the filter weights (see permute_mfma in evaluator.hip)
   const double *w0p[2], *w1p[2], *e0p[2], *e1p[2];     // forward
   const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];  // reverse (transposes)
-  const double *b0p[2], *eb0p[2], *ob1p[2];             // biases in accumulator order (ob1 = b1 + eb1)
+  const double *b0p[2], *eb0p[2], *ob1p[2];             // biases in accumulator order
+  const double *ob1p0[2];                               // ob1p with the ev = 0 spherical branch folded in (block 0) (ob1 = b1 + eb1)
   const double *e0pk[2];                                // spherical layer 0, one v4d per lane
   // MFMA operand order of the node layers: forward and reverse (transpose)
   const double *qkvp, *qkvtp;           // per head (160 x 32) and (32 x 160)
