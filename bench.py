@@ -248,9 +248,12 @@ def main():
     torch.cuda.synchronize()
     ctx.kernel_timing(False)
 
-    # dominant kernel: the pair filters (forward + reverse) carry ~90% of the FLOPs
+    # dominant kernel: the pair filters (forward + reverse) carry ~90% of the
+    # FLOPs; the roofline is the reverse filter of blocks 1.. (block 0 runs a
+    # cheaper instantiation, ev = 0, timed under its own name)
     timing = {}
-    for name in ("filter_fwd", "filter_bwd", "attn_fwd", "attn_bwd", "long_range"):
+    for name in ("filter_fwd", "filter_fwd_block0", "filter_bwd", "filter_bwd_block0", "attn_fwd", "attn_bwd",
+                 "attn_bwd_block0", "long_range"):
         try:
             timing[name] = ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched
@@ -260,8 +263,9 @@ def main():
     avg_ms = ms_f / launches_f
     flop = FILTER_BWD_FLOP_PER_PAIR * pairs_f / launches_f
     achieved = flop / (avg_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "k_filter_bwd_mfma", "achieved": achieved, "peak": FP64_PEAK_TFS,
-                "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFS, "traffic": traffic_bytes("k_filter_bwd_mfma", args.config),
+    roofline = {"bound": "mfma", "kernel": "k_filter_bwd_mfma<false>", "achieved": achieved, "peak": FP64_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFS,
+                "traffic": traffic_bytes("k_filter_bwd_mfma<false>", args.config),
                 "avg_launch_ms": avg_ms, "pairs_per_launch": pairs_f / launches_f,
                 "flop_per_pair": FILTER_BWD_FLOP_PER_PAIR}
     kernels = {k: {"avg_ms": v[0] / v[1], "launches": v[1]} for k, v in timing.items()}

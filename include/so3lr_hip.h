@@ -182,6 +182,9 @@ int so3lr_graph_stats(const so3lr_ctx *ctx, int64_t *sr_active, int64_t *sr_cand
  * fenced host clocks, pair_so3lr_native_mpi.cpp:1681-1762): when enabled,
  * HIP events are recorded on the launch stream around the kernels
  * "filter_fwd", "filter_bwd", "attn_fwd", "attn_bwd" and "long_range".
+ * Block 0 runs cheaper instantiations of the MFMA filters and of the reverse
+ * attention (its ev input is zero); they are timed as "filter_fwd_block0",
+ * "filter_bwd_block0" and "attn_bwd_block0".
  * Enabling clears the totals; disabling keeps them for reading.  While
  * enabled, evaluations are launched kernel by kernel (no graph replay).
  * _read returns the summed duration, the number of launches and the units

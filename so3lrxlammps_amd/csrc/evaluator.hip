@@ -2410,7 +2410,9 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     // the MFMA filter also forms the attention logits of both directions
     // from the filter tiles it holds; the scalar cross-check path leaves them
     // to the full attention kernel
-    timed("filter_fwd", 0, [&] {
+    // block 0 runs cheaper instantiations (ev = 0): timed under their own names
+    const bool blk0 = b == 0 && !naive_filters_;
+    timed(blk0 ? "filter_fwd_block0" : "filter_fwd", 0, [&] {
       if (naive_filters_)
         hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
       else if (b == 0)  // ev = 0: the spherical branch is a constant
@@ -2481,7 +2483,8 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     gemm(3, int(N), kF, kF, gp, kF, B.m2tp, nullptr, ghid, kF, nullptr, hpb, kF);
     gemm(0, int(N), kF, kF, ghid, kF, B.m1tp, nullptr, gact, kF, nullptr, nullptr, 0);
     hipLaunchKernelGGL(k_ln1_bwd, dim3(gN4), dim3(256), 0, s, int(N), gp, gact, n1b, B.ln1w, n1hb, n1ib, gainv);
-    timed("attn_bwd", 1, [&] {
+    const bool blk0 = b == 0 && !naive_filters_;
+    timed(b == 0 ? "attn_bwd_block0" : "attn_bwd", 1, [&] {
       if (b > 0)
         hipLaunchKernelGGL(k_attn_bwd<true>, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY,
                            pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
@@ -2490,7 +2493,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
                            pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
     });
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
-    timed("filter_bwd", 0, [&] {
+    timed(blk0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
       if (naive_filters_)
         hipLaunchKernelGGL(k_filter_bwd, dim3(gP), dim3(128), 0, s, nact, pr, pfc, psb, df, dfc, A, rc_, ds, dr);
       else if (b == 0)
