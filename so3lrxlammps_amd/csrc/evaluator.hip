@@ -1116,6 +1116,21 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
   if (evv) aev[std::size_t(n) * kE + m] = ev[std::size_t(n) * kE + m] + acce;
 }
 
+// LayerNorm over 128 channels held two per lane (biased variance), the
+// lane's two channels having weights w0, w1 and biases b0, b1.
+__device__ __forceinline__ void wave_layer_norm_pair(double v0, double v1, double w0, double w1, double b0,
+                                                     double b1, double eps, double &y0, double &y1, double &h0,
+                                                     double &h1, double &is) {
+  const double mean = wave_sum(v0 + v1) / kF;
+  const double d0 = v0 - mean, d1 = v1 - mean;
+  const double var = wave_sum(d0 * d0 + d1 * d1) / kF;
+  is = 1.0 / sqrt(var + eps);
+  h0 = d0 * is;
+  h1 = d1 * is;
+  y0 = h0 * w0 + b0;
+  y1 = h1 * w1 + b1;
+}
+
 // Attention forward messages, node-major, with the per-direction logits the
 // forward MFMA filter computed (same lane layout as k_attn_fwd): for node n
 // and every incident active pair, fc alpha v_o (invariant) and fc alpha_ev Y
@@ -1124,8 +1139,10 @@ __global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, con
                                                   const int *__restrict__ iother, const double *__restrict__ x,
                                                   const double *__restrict__ ev, const double *__restrict__ qkv,
                                                   const double *__restrict__ pY, const double *__restrict__ pfc,
-                                                  const double *__restrict__ palpha, double *__restrict__ ainv,
-                                                  double *__restrict__ aev) {
+                                                  const double *__restrict__ palpha, const double *__restrict__ lnw,
+                                                  const double *__restrict__ lnb, double eps, double *__restrict__ n1,
+                                                  double *__restrict__ n1hat, double *__restrict__ n1is,
+                                                  double *__restrict__ act, double *__restrict__ aev) {
   const int lane = threadIdx.x & 63;
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -1152,24 +1169,27 @@ __global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, con
     acc0 += A.d0; acc1 += A.d1; acce += A.de;
     if (two) { acc0 += B.d0; acc1 += B.d1; acce += B.de; }
   });
+  // the residual, then the post-attention block's LayerNorm 1 and the silu
+  // of it (the MLP input), with the whole node row in this wavefront
   const std::size_t i = std::size_t(n) * kF;
-  ainv[i + c0] = x[i + c0] + acc0;
-  ainv[i + c1] = x[i + c1] + acc1;
+  double y0, y1, h0, h1, is;
+  wave_layer_norm_pair(x[i + c0] + acc0, x[i + c1] + acc1, lnw[c0], lnw[c1], lnb[c0], lnb[c1], eps, y0, y1, h0, h1,
+                       is);
+  n1[i + c0] = y0;
+  n1[i + c1] = y1;
+  n1hat[i + c0] = h0;
+  n1hat[i + c1] = h1;
+  if (lane == 0) n1is[n] = is;
+  act[i + c0] = silu(y0);
+  act[i + c1] = silu(y1);
   if (evv) aev[std::size_t(n) * kE + m] = ev[std::size_t(n) * kE + m] + acce;
 }
 
-// LayerNorm over 128 channels held two per lane (biased variance).
+// LayerNorm over 128 channels held two per lane: channels lane and 64 + lane.
 __device__ __forceinline__ void wave_layer_norm(double v0, double v1, const double *w, const double *b,
                                                 double eps, int lane, double &y0, double &y1,
                                                 double &h0, double &h1, double &is) {
-  const double mean = wave_sum(v0 + v1) / kF;
-  const double d0 = v0 - mean, d1 = v1 - mean;
-  const double var = wave_sum(d0 * d0 + d1 * d1) / kF;
-  is = 1.0 / sqrt(var + eps);
-  h0 = d0 * is;
-  h1 = d1 * is;
-  y0 = h0 * w[lane] + b[lane];
-  y1 = h1 * w[64 + lane] + b[64 + lane];
+  wave_layer_norm_pair(v0, v1, w[lane], w[64 + lane], b[lane], b[64 + lane], eps, y0, y1, h0, h1, is);
 }
 __device__ __forceinline__ void wave_layer_norm_bwd(double g0, double g1, const double *w, double h0,
                                                     double h1, double is, int lane, double &d0,
@@ -2428,10 +2448,11 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
                            pfb, pY, pfc, inv_avg, pab, ainv, aevb);
       else
         hipLaunchKernelGGL(k_attn_msg, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb, pY,
-                           pfc, pab, ainv, aevb);
+                           pfc, pab, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb, n1ib, act, aevb);
     });
-    hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
-                       n1ib, act);
+    if (naive_filters_)  // the MFMA path's k_attn_msg has done LayerNorm 1 already
+      hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
+                         n1ib, act);
     gemm(1, int(N), kF, kF, act, kF, B.m1p, B.m1bp, hpb, kF, hid, nullptr, 0);
     // the MLP output goes to pb = n1 + W2 silu(hpre) + b2
     gemm(2, int(N), kF, kF, hid, kF, B.m2p, B.m2bp, pb, kF, nullptr, n1b, kF);
