@@ -1256,14 +1256,13 @@ __global__ __launch_bounds__(256) void k_post2(int N, const double *p, const dou
 
 // ---------------------------------------------------------------- heads
 struct HeadArgs {
-  const double *ew2, *qw2, *escale, *eshift, *qemb, *hw2t, *hb2, *hqemb, *hvshift, *hkey_bwd;
+  const double *ew2, *qw2, *escale, *eshift, *qemb, *hqemb, *hvshift, *hkey_bwd, *hkey_c;
   double eb2, qb2;
 };
 
 // energy, raw charge, Hirshfeld key and ratio (kokkos_output_heads.cpp:137-176,341-451)
 __global__ __launch_bounds__(256) void k_heads(int N, const int *z, const double *act, HeadArgs H,
-                                               double *eatom, double *qraw, double *hkey,
-                                               double *heff, double *hir) {
+                                               double *eatom, double *qraw, double *heff, double *hir) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -1271,10 +1270,9 @@ __global__ __launch_bounds__(256) void k_heads(int N, const int *z, const double
   const int zz = z[n];
   const double e = wave_sum(H.ew2[lane] * a[lane] + H.ew2[64 + lane] * a[64 + lane]);
   const double q = wave_sum(H.qw2[lane] * a[128 + lane] + H.qw2[64 + lane] * a[192 + lane]);
-  double key = H.hb2[lane];
-  for (int i = 0; i < kHH; ++i) key += H.hw2t[i * kHH + lane] * a[256 + i];  // coalesced rows of W2^T
-  hkey[std::size_t(n) * kHH + lane] = key;
-  const double qk = wave_sum(H.hqemb[zz * kHH + lane] * key);
+  // Hirshfeld logit q_emb[z] . (W2 a + b2), contracted through the element's
+  // row u[z] = W2^T q_emb[z]
+  const double qk = H.hkey_c[zz] + wave_sum(H.hkey_bwd[zz * kHH + lane] * a[256 + lane]);
   if (lane == 0) {
     eatom[n] = (e + H.eb2) * H.escale[zz - 1] + H.eshift[zz - 1];
     qraw[n] = q + H.qb2 + H.qemb[zz];
@@ -1996,9 +1994,6 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     hw_.qemb = up(m.f64(q + "atomic_embedding.weight", {100, 1}));
     const auto hw2 = m.f64(h + "transform_features.2.weight", {std::size_t(kHH), std::size_t(kHH)});
     const auto hqemb = m.f64(h + "q_embedding.weight", {100, std::size_t(kHH)});
-    hw_.hw2 = up(hw2);
-    hw_.hw2t = up(transpose(hw2, kHH, kHH));
-    hw_.hb2 = up(m.f64(h + "transform_features.2.bias", {std::size_t(kHH)}));
     hw_.hqemb = up(hqemb);
     // reverse of the key layer seeded by the element's query: u[z][i] =
     // sum_j W2[j][i] q_emb[z][j] depends on the element only
@@ -2010,6 +2005,13 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
         u[std::size_t(zz) * kHH + i] = acc;
       }
     hw_.hkey_bwd = up(u);
+    // the Hirshfeld logit q_emb[z] . (W2 a + b2) = u[z] . a + q_emb[z] . b2:
+    // the key vector itself is never needed
+    const auto hb2 = m.f64(h + "transform_features.2.bias", {std::size_t(kHH)});
+    std::vector<double> hc(100, 0.0);
+    for (int zz = 0; zz < 100; ++zz)
+      for (int j = 0; j < kHH; ++j) hc[zz] += hqemb[std::size_t(zz) * kHH + j] * hb2[j];
+    hw_.hkey_c = up(hc);
     hw_.hvshift = up(m.f64(h + "v_shift_embedding.weight", {100, 1}));
     const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
     const auto kk = m.i64("model.radial_embedding.radial_basis_fn.k", {R});
@@ -2054,7 +2056,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   xs_ = buf("xs"); evs_ = buf("evs"); qkv_ = buf("qkv"); aev_ = buf("aev"); n1_ = buf("n1");
   n1hat_ = buf("n1hat"); n1is_ = buf("n1is"); hpre_ = buf("hpre"); tout_ = buf("tout");
   pre2hat_ = buf("pre2hat"); pre2is_ = buf("pre2is"); ainv_ = buf("ainv"); act_ = buf("act");
-  hid_ = buf("hid"); pbuf_ = buf("p"); cat_ = buf("cat"); hhead_ = buf("hhead"); hkey_ = buf("hkey");
+  hid_ = buf("hid"); pbuf_ = buf("p"); cat_ = buf("cat"); hhead_ = buf("hhead");
   heff_ = buf("heff"); eatom_ = buf("eatom"); qraw_ = buf("qraw"); q_ = buf("q"); hir_ = buf("hir");
   qseed_ = buf("qseed"); elr_ = buf("elr"); dq_ = buf("dq"); dh_ = buf("dh"); flr_ = buf("flr");
   vlr_ = buf("vlr"); elr_parts_ = buf("elr_parts"); ezbl_ = buf("ezbl"); gx_ = buf("gx");
@@ -2276,7 +2278,6 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   double *cat = ensure<double>(cat_, Nz * kNI);
   double *hhead = ensure<double>(hhead_, Nz * 320);
   double *hact = act;
-  double *hkey = ensure<double>(hkey_, Nz * kHH);
   double *heff = ensure<double>(heff_, Nz);
   double *eatom = ensure<double>(eatom_, Nz);
   double *qraw = ensure<double>(qraw_, Nz);
@@ -2463,11 +2464,11 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   }
 
   // --- heads, charge correction, long range ---
-  HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hw2t, hw_.hb2, hw_.hqemb, hw_.hvshift,
-             hw_.hkey_bwd, hw_.eb2, hw_.qb2};
+  HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hqemb, hw_.hvshift,
+             hw_.hkey_bwd, hw_.hkey_c, hw_.eb2, hw_.qb2};
   const double *xf = xs + L * Nz * kF;
   gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1p, hhead, 320, hact, nullptr, 0);
-  hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, hkey, heff, hir);
+  hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, heff, hir);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
   timed("long_range", 1, [&] {
     if (shift_mode_)

@@ -62,9 +62,8 @@ struct HeadWeights {
   double eb2, qb2;
   const double *escale, *eshift;  // (118)
   const double *qemb;             // (100)
-  const double *hw2, *hb2;        // (64, 64), (64)
-  const double *hw2t;             // its transpose
   const double *hkey_bwd;         // (100, 64): u[z][i] = sum_j hw2[j][i] hqemb[z][j]
+  const double *hkey_c;           // (100): hqemb[z] . hb2
   const double *hqemb, *hvshift;  // (100, 64), (100)
   const double *rbf_b, *rbf_k, *rbf_kr;  // (32) each
   const double *exp2_64;                 // 2^(j/64), j < 64 (lean e^x of the filter kernels)
@@ -163,7 +162,7 @@ class Evaluator {
   Buffer *z_, *x0_, *img_of_node_, *img_off_, *img_q_;
   Buffer *xs_, *evs_, *qkv_, *aev_, *n1_, *n1hat_, *n1is_, *hpre_, *tout_, *pre2hat_, *pre2is_;
   Buffer *ainv_, *act_, *hid_, *pbuf_, *cat_;
-  Buffer *hhead_, *hkey_, *heff_, *eatom_, *qraw_, *q_, *hir_, *qseed_;
+  Buffer *hhead_, *heff_, *eatom_, *qraw_, *q_, *hir_, *qseed_;
   Buffer *elr_, *dq_, *dh_, *flr_, *vlr_, *elr_parts_, *ezbl_;
   Buffer *gx_, *gev_, *gp_, *gt_, *gcat_, *ghid_, *gact_, *gainv_, *gaev_, *gqkv_, *ghead_;
   Buffer *fout_, *etot_, *red_, *red_part_;
