@@ -199,31 +199,45 @@ __device__ __forceinline__ void bump_switch_fast(double r, double on, double off
   if (r >= off) { val = 0.0; der = 0.0; return; }
   const double c = (r - on) * inv_w;
   const double left = 1.0 - c, right = c;
-  const double isl = 1.0 / (left > 1e-12 ? left : 1e-12), isr = 1.0 / (right > 1e-12 ? right : 1e-12);
-  const double el = left > 0.0 ? exp(-isl) : 0.0;
-  const double er = right > 0.0 ? exp(-isr) : 0.0;
-  const double den = el + er + 1e-12, iden = 1.0 / den;
+  const double isl = rcp_lean(left > 1e-12 ? left : 1e-12), isr = rcp_lean(right > 1e-12 ? right : 1e-12);
+  const double el = left > 0.0 ? exp_lean(-isl) : 0.0;
+  const double er = right > 0.0 ? exp_lean(-isr) : 0.0;
+  const double den = el + er + 1e-12, iden = rcp_lean(den);
   val = el * iden;
   const double dl = left > 0.0 ? -el * isl * isl : 0.0;
   const double dr = right > 0.0 ? er * isr * isr : 0.0;
   der = (dl * den - el * (dl + dr)) * iden * iden * inv_w;
 }
 
+// alpha^(1/7) for alpha > 0: a single-precision estimate refined by two
+// Newton steps on x^7 = alpha, x <- (6 x + alpha / x^6) / 7 (each squares the
+// relative error: 1e-7, 1e-13, below 1 ulp).
+__device__ __forceinline__ double root7_lean(double a) {
+  double x = double(__expf(__logf(float(a)) * (1.0f / 7.0f)));
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const double x3 = x * x * x;
+    x = (6.0 * x + a * rcp_lean(x3 * x3)) * (1.0 / 7.0);
+  }
+  return x;
+}
+
 // Coulomb + QDO dispersion for one unique pair seen from atom "i" (self)
 // (kokkos_physical_long_range.cpp:62-381).  dh_self = dE/dh_i; pref * q_j =
 // dE/dq_i.  Returns false outside the cutoff.  Divisions are shared through
 // reciprocals (1/r, 1/den, 1/s_fit, 1/(7 alpha), 1/d6, 1/d8, 1/d10; 1/gamma =
-// 2 s_fit^2 exactly), alpha^(1/7) as exp(log(alpha) / 7).
+// 2 s_fit^2 exactly).  This runs once per long-range entry (about 900 per
+// atom), so the reciprocals, e^x and alpha^(1/7) take the lean forms above.
 __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *__restrict__ aref,
                                               const double *__restrict__ cref, int zi_, int zj_,
                                               double qi, double qj, double hi, double hj, double r,
                                               LrPairTerms &o) {
   if (!(r > 1e-12) || r >= P.cutoff) return false;
-  const double ir = 1.0 / r;
+  const double ir = rcp_lean(r);
   double esw, desw;
   bump_switch_fast(r, P.cuton_el, P.cutoff, P.inv_w_el, esw, desw);
   const double ratio = r * P.inv_sigma;
-  const double erft = erf(ratio), expt = exp(-ratio * ratio);
+  const double erft = erf(ratio), expt = exp_lean(-ratio * ratio);
   const double pot = erft * ir;
   const double dpot = (r * expt * P.two_over_sqrtpi_sigma - erft) * ir * ir;
   const double disp = r - P.cutoff;
@@ -245,18 +259,18 @@ __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *_
   const double num = 2.0 * c6i * c6j * aj * ai;
   const double den = ai * ai * c6j + aj * aj * c6i;
   if (!(alpha > 0.0 && den > 1e-30)) return true;
-  const double iden = 1.0 / den;
+  const double iden = rcp_lean(den);
   const double c6 = num * iden;
   const double dc6i = 2.0 * ci0 * hi;
   const double dn_dhi = 2.0 * (dc6i * c6j * aj * ai + c6i * c6j * aj * ai0);
   const double dd_dhi = 2.0 * ai * ai0 * c6j + aj * aj * dc6i;
   const double dc6_dhi = (dn_dhi * den - num * dd_dhi) * iden * iden;
   const double b0 = -0.00433008, b1 = 0.24428889, b2 = 0.04125273, b3 = -0.00078893;
-  const double a7 = exp(log(alpha) * (1.0 / 7.0));
-  const double i7a = 1.0 / (7.0 * alpha);
+  const double a7 = root7_lean(alpha);
+  const double i7a = rcp_lean(7.0 * alpha);
   const double rvdw = P.fine_factor * a7;
   const double sfit = b3 * rvdw * rvdw * rvdw + b2 * rvdw * rvdw + b1 * rvdw + b0;
-  const double isfit = 1.0 / sfit;
+  const double isfit = rcp_lean(sfit);
   const double gam = 0.5 * isfit * isfit, igam = 2.0 * sfit * sfit;
   const double drvdw = rvdw * i7a;
   const double dsfit = (3.0 * b3 * rvdw * rvdw + 2.0 * b2 * rvdw + b1) * drvdw;
@@ -267,7 +281,7 @@ __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *_
   const double ra = r * P.inv_bohr;
   const double r2 = ra * ra, r4 = r2 * r2, r6 = r4 * r2, r8 = r4 * r4, r10 = r8 * r2;
   const double p2 = damp * damp, p4 = p2 * p2, p6 = p4 * p2, p8 = p4 * p4, p10 = p8 * p2;
-  const double i6 = 1.0 / (r6 + p6), i8 = 1.0 / (r8 + p8), i10 = 1.0 / (r10 + p10);
+  const double i6 = rcp_lean(r6 + p6), i8 = rcp_lean(r8 + p8), i10 = rcp_lean(r10 + p10);
   const double qdo = -c6 * i6 - c8 * i8 - c10 * i10;
   const double rad_au = (6.0 * c6 * r4 * i6 * i6 + 8.0 * c8 * r6 * i8 * i8 + 10.0 * c10 * r8 * i10 * i10) * ra;
   const double dc8 = -c8 * dgam * igam, dc10 = -2.0 * c10 * dgam * igam;
