@@ -222,12 +222,37 @@ __device__ __forceinline__ double root7_lean(double a) {
   return x;
 }
 
+// erfcx(x) on [0, 3] in u = 2 x / 3 - 1, highest power first (gen_erfcx_poly.py)
+// (in constant memory: read through the scalar cache, not held in registers)
+static __constant__ double kErfcxPoly[26] = {
+    -1.9285526545026629e-09, 5.7920154915414246e-09, -4.6119752723685525e-09,
+    1.2374418534053267e-08, -6.8302916092557606e-08, 1.8960282584894505e-07,
+    -4.5725982227457081e-07, 1.2076614734008636e-06, -3.1901620317342984e-06,
+    8.1102004120020287e-06, -2.0126549072150048e-05, 4.8905112127983934e-05,
+    -0.00011601010087456714, 0.00026818449435352847, -0.00060331955090763077,
+    0.0013184708553075387, -0.0027932530866193999, 0.0057231897175237054,
+    -0.011309695741544485, 0.021484255075844793, -0.039077115130126794,
+    0.06772278857525682, -0.11114180538602185, 0.17133983967481778,
+    -0.2454343765988401, 0.32158541645431754,
+};
+// erf(x) = 1 - e^{-x^2} erfcx(x) for 0 <= x <= 3 (absolute error < 4e-16),
+// given e^{-x^2}.  Used when the model's cutoff / sigma is at most 3.
+__device__ __forceinline__ double erf_lean(double x, double exp_mx2) {
+  const double u = x * (2.0 / 3.0) - 1.0;
+  double p = kErfcxPoly[0];
+#pragma unroll
+  for (int k = 1; k < 26; ++k) p = fma(p, u, kErfcxPoly[k]);
+  return fma(-exp_mx2, p, 1.0);
+}
+
 // Coulomb + QDO dispersion for one unique pair seen from atom "i" (self)
 // (kokkos_physical_long_range.cpp:62-381).  dh_self = dE/dh_i; pref * q_j =
 // dE/dq_i.  Returns false outside the cutoff.  Divisions are shared through
 // reciprocals (1/r, 1/den, 1/s_fit, 1/(7 alpha), 1/d6, 1/d8, 1/d10; 1/gamma =
 // 2 s_fit^2 exactly).  This runs once per long-range entry (about 900 per
 // atom), so the reciprocals, e^x and alpha^(1/7) take the lean forms above.
+// LEAN_ERF: erf(r / sigma) by erf_lean (the caller has checked cutoff / sigma <= 3)
+template <bool LEAN_ERF>
 __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *__restrict__ aref,
                                               const double *__restrict__ cref, int zi_, int zj_,
                                               double qi, double qj, double hi, double hj, double r,
@@ -237,7 +262,7 @@ __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *_
   double esw, desw;
   bump_switch_fast(r, P.cuton_el, P.cutoff, P.inv_w_el, esw, desw);
   const double ratio = r * P.inv_sigma;
-  const double erft = erf(ratio), expt = exp_lean(-ratio * ratio);
+  const double expt = exp_lean(-ratio * ratio), erft = LEAN_ERF ? erf_lean(ratio, expt) : erf(ratio);
   const double pot = erft * ir;
   const double dpot = (r * expt * P.two_over_sqrtpi_sigma - erft) * ir * ir;
   const double disp = r - P.cutoff;

@@ -1328,6 +1328,7 @@ __global__ __launch_bounds__(256) void k_heads_bwd(int N, const int *z, const do
 // Node-major over the LR incidence: every lane takes one pair of node n.
 // d = x_n - x_other; F_n = -dE/dr d/r; half of every pair energy and of its
 // virial goes to each endpoint.
+template <bool LEAN_ERF>
 __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int *inc, const int *rows,
                                             const int *nodes, const double *x, const int *z,
                                             const double *q, const double *hir, LrParams P,
@@ -1352,7 +1353,7 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
     const double r = sqrt(dx * dx + dy * dy + dz * dz);
     const int o = nodes[2 * c + 1 - side];
     LrPairTerms t;
-    if (!lr_pair_terms(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
+    if (!lr_pair_terms<LEAN_ERF>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
     e_el += 0.5 * t.e_el;
     e_d += 0.5 * t.e_disp;
     sdq += t.pref * q[o];
@@ -1381,6 +1382,7 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
 
 // LR over the full node-major list of the device reneighbor: entry j * 32 +
 // image code, neighbour position x_j + shift(code) * box.
+template <bool LEAN_ERF>
 __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, const int *inc, const double *x,
                                                  double lx, double ly, double lz, const int *z, const double *q,
                                                  const double *hir, LrParams P, const double *aref,
@@ -1402,7 +1404,7 @@ __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, cons
     const double dz = zn_ - x[3 * o + 2] - (code % 3 - 1) * lz;
     const double r = sqrt(dx * dx + dy * dy + dz * dz);
     LrPairTerms t;
-    if (!lr_pair_terms(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
+    if (!lr_pair_terms<LEAN_ERF>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
     e_el += 0.5 * t.e_el;
     e_d += 0.5 * t.e_disp;
     sdq += t.pref * q[o];
@@ -2470,13 +2472,23 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1p, hhead, 320, hact, nullptr, 0);
   hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, heff, hir);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
+  // erf(r / sigma) by the polynomial of erf_lean when r / sigma stays within [0, 3]
+  const bool lean_erf = lr_.cutoff * lr_.inv_sigma <= 3.0;
   timed("long_range", 1, [&] {
-    if (shift_mode_)
-      hipLaunchKernelGGL(k_lr_full, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, x, box_len_[0], box_len_[1],
-                         box_len_[2], z, q, hir, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
-    else
-      hipLaunchKernelGGL(k_lr, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x, z, q, hir,
-                         lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
+#define SO3LR_LR(FULL, LEAN)                                                                                          \
+  if (FULL)                                                                                                          \
+    hipLaunchKernelGGL(k_lr_full<LEAN>, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, x, box_len_[0],          \
+                       box_len_[1], box_len_[2], z, q, hir, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr,   \
+                       parts);                                                                                       \
+  else                                                                                                               \
+    hipLaunchKernelGGL(k_lr<LEAN>, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x, z, q,   \
+                       hir, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
+    if (lean_erf) {
+      SO3LR_LR(shift_mode_, true)
+    } else {
+      SO3LR_LR(shift_mode_, false)
+    }
+#undef SO3LR_LR
   });
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
   hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, H, ghead);
