@@ -505,10 +505,14 @@ __device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
 // Bernstein basis of pair distance r at channels 16 T + g + 4 v (T < 2, v < 4).
 __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, const double *tab, v4d *rb,
                                      double &xb) {
-  double x = exp(-A.gamma * r);
-  x = x < 1e-6 ? 1e-6 : (x > 1.0 - 1e-6 ? 1.0 - 1e-6 : x);
+  // x = e^{-gamma r} clamped to [1e-6, 1 - 1e-6]; ln x is -gamma r itself
+  // unless the clamp is active
+  const double gr = -A.gamma * r;
+  double x = exp_tab(gr, tab), lx = gr;
+  if (x < 1e-6) { x = 1e-6; lx = log(1e-6); }
+  if (x > 1.0 - 1e-6) { x = 1.0 - 1e-6; lx = log(1.0 - 1e-6); }
   xb = x;
-  const double lx = log(x), l1x = log(1.0 - x);
+  const double l1x = log(1.0 - x);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
