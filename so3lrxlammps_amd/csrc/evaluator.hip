@@ -823,8 +823,8 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
 // MFMA column block, output features as rows.  K is read from the node rows in
 // the permuted order k = 16 T + g + 4 v (zero beyond K); W is pre-permuted
 // (permute_mfma) and zero-padded to 16-row tiles and 16-column K chunks.
-// EPI 0: out = acc + bias; 1: out = pre, out2 = silu(pre); 2: out = acc + bias
-// + aux; 3: out = acc * silu'(aux).  The bias comes in accumulator order
+// EPI 0: out = acc + bias; 1: out = pre, out2 = silu(pre); 3: out = acc *
+// silu'(aux).  The bias comes in accumulator order
 // (bias_acc) and starts the accumulators.  Output tiles are taken MG at a
 // time; per tile group the operand stream holds, per K chunk, the X chunk and
 // the MG weight fragments.
@@ -865,7 +865,7 @@ __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const doub
   v4d acc[MG], xa[MG];
 #pragma unroll
   for (int q = 0; q < MG; ++q) acc[q] = biasp ? tile_load(biasp, grp * MG + q, lane) : zero;
-  if constexpr (EPI == 2 || EPI == 3) {
+  if constexpr (EPI == 3) {
 #pragma unroll
     for (int q = 0; q < MG; ++q)
 #pragma unroll
@@ -895,7 +895,6 @@ __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const doub
       const double v = acc[q][r];
       if constexpr (EPI == 0) out[io] = v;
       if constexpr (EPI == 1) { out[io] = v; out2[io] = silu(v); }
-      if constexpr (EPI == 2) out[io] = v + xa[q][r];
       if constexpr (EPI == 3) out[io] = v * silu_prime(xa[q][r]);
     }
 }
@@ -1222,40 +1221,174 @@ __global__ __launch_bounds__(256) void k_post1(int N, const double *ainv, const 
   act[i + 64 + lane] = silu(y1);
 }
 
-// cat = [p, sum_{m in l} a_ev^2 cg]  (kokkos_post_attention_block0.cpp:223-266)
-__global__ __launch_bounds__(256) void k_concat(int N, const double *p, const double *aev, const double *cg,
-                                                double *cat) {
-  const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  cat[std::size_t(n) * kNI + lane] = p[std::size_t(n) * kF + lane];
-  cat[std::size_t(n) * kNI + 64 + lane] = p[std::size_t(n) * kF + 64 + lane];
-  double v = 0.0;
-  if (lane < kE) { const double a = aev[std::size_t(n) * kE + lane]; v = a * a * cg[lane]; }
-  const int slot = lane < kE ? degree_slot(lane) : 7;
-  for (int l = 0; l < 4; ++l) {
-    const double s = wave_sum(slot == l ? v : 0.0);
-    if (lane == 0) cat[std::size_t(n) * kNI + kF + l] = s;
-  }
-}
 
-// pre2 = p + t[:128], ev_out = a_ev (1 + t[128+l]), x_out = LN2(pre2)
-__global__ __launch_bounds__(256) void k_post2(int N, const double *p, const double *t, const double *aev,
-                                               const double *w, const double *b, double eps,
-                                               double *xout, double *evout, double *pre2hat,
-                                               double *pre2is) {
-  const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  const std::size_t i = std::size_t(n) * kF, it = std::size_t(n) * kNI;
-  double y0, y1, h0, h1, is;
-  wave_layer_norm(p[i + lane] + t[it + lane], p[i + 64 + lane] + t[it + 64 + lane], w, b, eps, lane,
-                  y0, y1, h0, h1, is);
-  xout[i + lane] = y0; xout[i + 64 + lane] = y1;
-  pre2hat[i + lane] = h0; pre2hat[i + 64 + lane] = h1;
-  if (lane == 0) pre2is[n] = is;
-  if (lane < kE)
-    evout[std::size_t(n) * kE + lane] = aev[std::size_t(n) * kE + lane] * (1.0 + t[it + kF + degree_slot(lane)]);
+// The post-attention node chain of one block, 16 atoms per wavefront with
+// every activation in MFMA registers (kokkos_post_attention_block0.cpp:302-333):
+//   hpre = W1 silu(n1) + b1 (kept for the reverse), hid = silu(hpre),
+//   p = n1 + W2 hid + b2,
+//   t = Wint [p, inv(aev)] + bint (132 wide, kept), inv_l = sum_{m in l} aev_m^2 cg_m,
+//   x' = LN2(p + t[0:128]) (statistics kept), ev' = aev (1 + t[128 + slot]).
+// An MFMA output tile (rows 16 mt + 4 r + g of node j in lane j + 16 g,
+// register r) is the B operand of the next layer as it stands, so the layers
+// chain without memory round trips.  One operand stream: the MLP-1 bias
+// tiles, then per K chunk T the silu(n1) chunk and the 8 W1 fragments; the
+// MLP-2 biases, per T the 8 W2 fragments, then the 8 n1 chunks of the
+// residual; the 9 interaction biases and per T (9, the last one the
+// invariants) its 9 fragments.
+struct NodeChainArgs {
+  const double *m1p, *m1bp, *m2p, *m2bp, *intp, *intbp;  // MFMA operand order
+  const double *int_cg, *ln2w, *ln2b, *exp2_64;
+  double eps;
+};
+__global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restrict__ act,
+                                                  const double *__restrict__ n1, const double *__restrict__ aev,
+                                                  NodeChainArgs A, double *__restrict__ hpre,
+                                                  double *__restrict__ tout, double *__restrict__ xout,
+                                                  double *__restrict__ evout, double *__restrict__ pre2hat,
+                                                  double *__restrict__ pre2is) {
+  __shared__ double exp2_lds[64];
+  if (threadIdx.x < 64) exp2_lds[threadIdx.x] = A.exp2_64[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w * 16 >= N) return;
+  const int n = w * 16 + j;
+  const bool valid = n < N;
+  const std::size_t nn = std::size_t(valid ? n : N - 1);
+  // node-row chunk T in the operand order: features 16 T + g + 4 v
+  auto chunk = [&](const double *rows, int ld, int T) {
+    const double *r = rows + nn * ld + 16 * T + g;
+    return v4d{r[0], r[4], r[8], r[12]};
+  };
+  constexpr int P1 = 8 + 8 * 9, P2 = P1 + 8 + 8 * 8 + 8, NS = P2 + 9 + 9 * 9;
+  auto load = [&](auto si) -> v4d {
+    constexpr int s = decltype(si)::value;
+    if constexpr (s < 8) {
+      return tile_load(A.m1bp, s, lane);
+    } else if constexpr (s < P1) {
+      constexpr int T = (s - 8) / 9, u = (s - 8) % 9;
+      if constexpr (u == 0) return chunk(act, kF, T);
+      else return wload(A.m1p, 8, u - 1, T, lane);
+    } else if constexpr (s < P1 + 8) {
+      return tile_load(A.m2bp, s - P1, lane);
+    } else if constexpr (s < P2 - 8) {
+      constexpr int i = s - P1 - 8;
+      return wload(A.m2p, 8, i % 8, i / 8, lane);
+    } else if constexpr (s < P2) {
+      return chunk(n1, kF, s - (P2 - 8));
+    } else if constexpr (s < P2 + 9) {
+      return tile_load(A.intbp, s - P2, lane);
+    } else {
+      constexpr int i = s - P2 - 9;
+      return wload(A.intp, 9, i % 9, i / 9, lane);
+    }
+  };
+  Stream<NS, kFilterPF, decltype(load)> st(load);
+  st.prime();
+
+  // the 4 invariants of the attention's equivariant output: lane group g
+  // holds invariant g of node j, the K chunk 8 of the interaction input
+  double inv = 0.0;
+  {
+    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
+    const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
+    for (int m = lo; m < hi; ++m) {
+      const double a = aev[nn * kE + m];
+      inv += a * a * A.int_cg[m];
+    }
+  }
+  const v4d inv4 = v4d{inv, 0.0, 0.0, 0.0};
+  v4d acc[9], xb[8], xT;
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int s = decltype(si)::value;
+    if constexpr (s < 8) {
+      acc[s] = wv;
+    } else if constexpr (s < P1) {
+      constexpr int u = (s - 8) % 9;
+      if constexpr (u == 0) xT = wv;
+      else acc[u - 1] = mfma4(wv, xT, acc[u - 1]);
+      if constexpr (s == P1 - 1) {
+        // hpre kept for the reverse; silu(hpre) is the MLP-2 operand
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (valid) hpre[nn * kF + 16 * mt + 4 * r + g] = acc[mt][r];
+            xb[mt][r] = silu_tab(acc[mt][r], exp2_lds);
+          }
+        }
+      }
+    } else if constexpr (s < P1 + 8) {
+      acc[s - P1] = wv;
+    } else if constexpr (s < P2 - 8) {
+      constexpr int i = s - P1 - 8;
+      acc[i % 8] = mfma4(wv, xb[i / 8], acc[i % 8]);
+    } else if constexpr (s < P2) {
+      constexpr int mt = s - (P2 - 8);
+      xb[mt] = acc[mt] + wv;  // p = n1 + W2 hid + b2
+    } else if constexpr (s < P2 + 9) {
+      acc[s - P2] = wv;
+    } else {
+      constexpr int i = s - P2 - 9, T = i / 9;
+      if constexpr (T < 8) acc[i % 9] = mfma4(wv, xb[T], acc[i % 9]);
+      else acc[i % 9] = mfma4(wv, inv4, acc[i % 9]);
+    }
+  });
+
+  // interaction output kept for the reverse (132 wide)
+#pragma unroll
+  for (int mt = 0; mt < 9; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = 16 * mt + 4 * r + g;
+      if (valid && c < kNI) tout[nn * kNI + c] = acc[mt][r];
+    }
+  // LayerNorm 2 of p + t over the 128 features of node j: 32 per lane, the
+  // rest in the lanes of the other three lane groups
+  double sum = 0.0;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    xb[mt] += acc[mt];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sum += xb[mt][r];
+  }
+  sum += __shfl_xor(sum, 16, kWave);
+  sum += __shfl_xor(sum, 32, kWave);
+  const double mean = sum / kF;
+  double var = 0.0;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const double d = xb[mt][r] - mean;
+      var += d * d;
+    }
+  var += __shfl_xor(var, 16, kWave);
+  var += __shfl_xor(var, 32, kWave);
+  const double is = 1.0 / sqrt(var / kF + A.eps);
+  if (valid) {
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = 16 * mt + 4 * r + g;
+        const double h = (xb[mt][r] - mean) * is;
+        pre2hat[nn * kF + c] = h;
+        xout[nn * kF + c] = h * A.ln2w[c] + A.ln2b[c];
+      }
+    if (g == 0) pre2is[nn] = is;
+  }
+  // ev' = aev (1 + gate[slot]); gate l = t[128 + l] sits in lane j + 16 l, register 0
+  const double gate[4] = {__shfl(acc[8][0], j, kWave), __shfl(acc[8][0], j + 16, kWave),
+                          __shfl(acc[8][0], j + 32, kWave), __shfl(acc[8][0], j + 48, kWave)};
+  if (valid) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const int m = g + 4 * k;
+      const int sl = degree_slot(m);
+      evout[nn * kE + m] = aev[nn * kE + m] * (1.0 + pick4(sl, gate[0], gate[1], gate[2], gate[3]));
+    }
+  }
 }
 
 // ---------------------------------------------------------------- heads
@@ -2062,7 +2195,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   xs_ = buf("xs"); evs_ = buf("evs"); qkv_ = buf("qkv"); aev_ = buf("aev"); n1_ = buf("n1");
   n1hat_ = buf("n1hat"); n1is_ = buf("n1is"); hpre_ = buf("hpre"); tout_ = buf("tout");
   pre2hat_ = buf("pre2hat"); pre2is_ = buf("pre2is"); ainv_ = buf("ainv"); act_ = buf("act");
-  hid_ = buf("hid"); pbuf_ = buf("p"); cat_ = buf("cat"); hhead_ = buf("hhead");
+  hhead_ = buf("hhead");
   heff_ = buf("heff"); eatom_ = buf("eatom"); qraw_ = buf("qraw"); q_ = buf("q"); hir_ = buf("hir");
   qseed_ = buf("qseed"); elr_ = buf("elr"); dq_ = buf("dq"); dh_ = buf("dh"); flr_ = buf("flr");
   vlr_ = buf("vlr"); elr_parts_ = buf("elr_parts"); ezbl_ = buf("ezbl"); gx_ = buf("gx");
@@ -2279,9 +2412,6 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   double *pre2is = ensure<double>(pre2is_, L * Nz);
   double *ainv = ensure<double>(ainv_, Nz * kF);
   double *act = ensure<double>(act_, Nz * 320);  // MLP input (128 wide) and head activations (320)
-  double *hid = ensure<double>(hid_, Nz * kF);
-  double *pb = ensure<double>(pbuf_, Nz * kF);
-  double *cat = ensure<double>(cat_, Nz * kNI);
   double *hhead = ensure<double>(hhead_, Nz * 320);
   double *hact = act;
   double *heff = ensure<double>(heff_, Nz);
@@ -2375,7 +2505,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     return;                                                                                                   \
   }
     SO3LR_GEMM(0, 8, 8, SO3LR_MG8) SO3LR_GEMM(0, 9, 9, 3) SO3LR_GEMM(0, 20, 8, SO3LR_MG8)
-    SO3LR_GEMM(1, 8, 8, SO3LR_MG8) SO3LR_GEMM(1, 8, 20, 4) SO3LR_GEMM(2, 8, 8, SO3LR_MG8)
+    SO3LR_GEMM(1, 8, 8, SO3LR_MG8) SO3LR_GEMM(1, 8, 20, 4)
     SO3LR_GEMM(3, 8, 8, SO3LR_MG8)
 #undef SO3LR_GEMM
     throw std::logic_error("SO3LR: internal error, no node GEMM for this shape");
@@ -2460,12 +2590,10 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     if (naive_filters_)  // the MFMA path's k_attn_msg has done LayerNorm 1 already
       hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
                          n1ib, act);
-    gemm(1, int(N), kF, kF, act, kF, B.m1p, B.m1bp, hpb, kF, hid, nullptr, 0);
-    // the MLP output goes to pb = n1 + W2 silu(hpre) + b2
-    gemm(2, int(N), kF, kF, hid, kF, B.m2p, B.m2bp, pb, kF, nullptr, n1b, kF);
-    hipLaunchKernelGGL(k_concat, dim3(gN4), dim3(256), 0, s, int(N), pb, aevb, B.int_cg, cat);
-    gemm(0, int(N), kNI, kNI, cat, kNI, B.intp, B.intbp, tb, kNI, nullptr, nullptr, 0);
-    hipLaunchKernelGGL(k_post2, dim3(gN4), dim3(256), 0, s, int(N), pb, tb, aevb, B.ln2w, B.ln2b, ln_eps_,
+    // the post-attention node chain in one kernel (MLP, interaction, LayerNorm 2, ev gate)
+    const NodeChainArgs NC{B.m1p, B.m1bp, B.m2p, B.m2bp, B.intp, B.intbp, B.int_cg, B.ln2w, B.ln2b, hw_.exp2_64,
+                           ln_eps_};
+    hipLaunchKernelGGL(k_node_fwd, dim3(gN64), dim3(256), 0, s, int(N), act, n1b, aevb, NC, hpb, tb,
                        xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);
   }
 

@@ -161,7 +161,7 @@ class Evaluator {
   // node-sized device buffers (named members so the kernels' arguments read clearly)
   Buffer *z_, *x0_, *img_of_node_, *img_off_, *img_q_;
   Buffer *xs_, *evs_, *qkv_, *aev_, *n1_, *n1hat_, *n1is_, *hpre_, *tout_, *pre2hat_, *pre2is_;
-  Buffer *ainv_, *act_, *hid_, *pbuf_, *cat_;
+  Buffer *ainv_, *act_;
   Buffer *hhead_, *heff_, *eatom_, *qraw_, *q_, *hir_, *qseed_;
   Buffer *elr_, *dq_, *dh_, *flr_, *vlr_, *elr_parts_, *ezbl_;
   Buffer *gx_, *gev_, *gp_, *gt_, *gcat_, *ghid_, *gact_, *gainv_, *gaev_, *gqkv_, *ghead_;
