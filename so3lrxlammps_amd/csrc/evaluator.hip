@@ -823,16 +823,14 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
 // MFMA column block, output features as rows.  K is read from the node rows in
 // the permuted order k = 16 T + g + 4 v (zero beyond K); W is pre-permuted
 // (permute_mfma) and zero-padded to 16-row tiles and 16-column K chunks.
-// EPI 0: out = acc + bias; 1: out = pre, out2 = silu(pre); 3: out = acc *
-// silu'(aux).  The bias comes in accumulator order
+// EPI 0: out = acc + bias; 1: out = pre, out2 = silu(pre).  The bias comes in accumulator order
 // (bias_acc) and starts the accumulators.  Output tiles are taken MG at a
 // time; per tile group the operand stream holds, per K chunk, the X chunk and
 // the MG weight fragments.
 template <int EPI, int KT, int MT, int MG>
 __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const double *__restrict__ X, int ldx,
                                               const double *__restrict__ Wp, const double *__restrict__ biasp,
-                                              double *__restrict__ out, int ldo, double *__restrict__ out2,
-                                              const double *__restrict__ aux, int ldaux) {
+                                              double *__restrict__ out, int ldo, double *__restrict__ out2) {
   // one group of MG output tiles per wavefront (the group is blockIdx.y), so
   // a few thousand node rows still give every SIMD several wavefronts
   static_assert(MT % MG == 0, "output tiles must split into equal groups");
@@ -862,18 +860,9 @@ __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const doub
     }
   };
   Stream<PER_G, kFilterPF, decltype(load)> st(load);
-  v4d acc[MG], xa[MG];
+  v4d acc[MG];
 #pragma unroll
   for (int q = 0; q < MG; ++q) acc[q] = biasp ? tile_load(biasp, grp * MG + q, lane) : zero;
-  if constexpr (EPI == 3) {
-#pragma unroll
-    for (int q = 0; q < MG; ++q)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int o = 16 * (grp * MG + q) + g + 4 * r;
-        xa[q][r] = o < O ? aux[std::size_t(nn) * ldaux + o] : 0.0;
-      }
-  }
   st.prime();
   v4d bT = zero;
   st.run([&](auto si, const v4d &wv) {
@@ -895,7 +884,6 @@ __global__ __launch_bounds__(256) void k_gemm(int rows, int K, int O, const doub
       const double v = acc[q][r];
       if constexpr (EPI == 0) out[io] = v;
       if constexpr (EPI == 1) { out[io] = v; out2[io] = silu(v); }
-      if constexpr (EPI == 3) out[io] = v * silu_prime(xa[q][r]);
     }
 }
 
@@ -1194,15 +1182,6 @@ __device__ __forceinline__ void wave_layer_norm(double v0, double v1, const doub
                                                 double &h0, double &h1, double &is) {
   wave_layer_norm_pair(v0, v1, w[lane], w[64 + lane], b[lane], b[64 + lane], eps, y0, y1, h0, h1, is);
 }
-__device__ __forceinline__ void wave_layer_norm_bwd(double g0, double g1, const double *w, double h0,
-                                                    double h1, double is, int lane, double &d0,
-                                                    double &d1) {
-  const double gh0 = g0 * w[lane], gh1 = g1 * w[64 + lane];
-  const double mg = wave_sum(gh0 + gh1) / kF;
-  const double mgx = wave_sum(gh0 * h0 + gh1 * h1) / kF;
-  d0 = is * (gh0 - mg - h0 * mgx);
-  d1 = is * (gh1 - mg - h1 * mgx);
-}
 
 // LN1 of the attention residual, and silu of it for the MLP input
 __global__ __launch_bounds__(256) void k_post1(int N, const double *ainv, const double *w, const double *b,
@@ -1391,6 +1370,195 @@ __global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restric
   }
 }
 
+// Reverse of the post-attention node chain, 16 atoms per wavefront, the
+// adjoints in MFMA registers (kokkos_post_attention_reverse.cpp:328-449):
+//   LayerNorm 2 reverse: d = LN2^T gx, the adjoint of p and of t[0:128];
+//   t[128 + l] (gates): sum_{m in l} gev_m aev_m; aev: gev (1 + gate);
+//   interaction reverse: gcat = Wint^T gt; p += gcat[0:128];
+//   aev += 2 aev cg gcat[128 + slot];
+//   MLP reverse: ghid = (W2^T p) silu'(hpre), gact = W1^T ghid;
+//   LayerNorm 1 reverse of g = p + gact silu'(n1): the adjoint of the
+//   attention residual, gainv.
+// The operand stream: the gx and LN2-normalised chunks (the latter twice:
+// once for the statistics, once per K chunk of Wint^T), Wint^T (9 x 9), W2^T
+// (8 x 8) and the hpre chunks, W1^T (8 x 8), then the n1, LN1-normalised and
+// p chunks (p waits in LDS between the two halves, so that at most two
+// 8-tile register sets are live).
+struct NodeChainBwdArgs {
+  const double *inttp, *m2tp, *m1tp;  // MFMA operand order (transposes)
+  const double *int_cg, *ln1w, *ln2w;
+};
+__global__ __launch_bounds__(256) void k_node_bwd(int N, const double *__restrict__ gx,
+                                                  const double *__restrict__ gev, const double *__restrict__ t,
+                                                  const double *__restrict__ aev, const double *__restrict__ pre2hat,
+                                                  const double *__restrict__ pre2is, const double *__restrict__ hpre,
+                                                  const double *__restrict__ n1, const double *__restrict__ n1hat,
+                                                  const double *__restrict__ n1is, NodeChainBwdArgs A,
+                                                  double *__restrict__ gainv, double *__restrict__ gaev) {
+  __shared__ v4d p_lds[4][8][64];  // the p adjoint of each wavefront, operand order (64 KB)
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4, wl = threadIdx.x >> 6;
+  const int w = blockIdx.x * 4 + wl;
+  if (w * 16 >= N) return;
+  const int n = w * 16 + j;
+  const bool valid = n < N;
+  const std::size_t nn = std::size_t(valid ? n : N - 1);
+  auto chunk = [&](const double *rows, int T) {
+    const double *r = rows + nn * kF + 16 * T + g;
+    return v4d{r[0], r[4], r[8], r[12]};
+  };
+  // phase B per K chunk T < 8: the LN2-normalised chunk T, then the 9
+  // fragments; T = 8 (the gate adjoints): the 9 fragments
+  constexpr int SA = 16, SB = SA + 8 * 10 + 9, SD = SB + 64 + 8, SE = SD + 64, NS = SE + 24;
+  auto load = [&](auto si) -> v4d {
+    constexpr int s = decltype(si)::value;
+    if constexpr (s < 8) return chunk(gx, s);
+    else if constexpr (s < SA) return chunk(pre2hat, s - 8);
+    else if constexpr (s < SB) {
+      constexpr int T = (s - SA) / 10, u = (s - SA) % 10;
+      if constexpr (T < 8 && u == 0) return chunk(pre2hat, T);
+      else if constexpr (T < 8) return wload(A.inttp, 9, u - 1, T, lane);
+      else return wload(A.inttp, 9, u, 8, lane);
+    }
+    else if constexpr (s < SD - 8) return wload(A.m2tp, 8, (s - SB) % 8, (s - SB) / 8, lane);
+    else if constexpr (s < SD) return chunk(hpre, s - (SD - 8));
+    else if constexpr (s < SE) return wload(A.m1tp, 8, (s - SD) % 8, (s - SD) / 8, lane);
+    else if constexpr (s < SE + 8) return chunk(n1, s - SE);
+    else if constexpr (s < SE + 16) return chunk(n1hat, s - SE - 8);
+    else return p_lds[wl][s - SE - 16][lane];
+  };
+  Stream<NS, kFilterPF, decltype(load)> st(load);
+  st.prime();
+
+  // per-lane pieces of the equivariant part: lane group g handles channels
+  // m = g + 4 k (k < 6); the gate adjoint l = g is its slot sum
+  const double *ger = gev + nn * kE, *aer = aev + nn * kE;
+  const double gates[4] = {t[nn * kNI + kF], t[nn * kNI + kF + 1], t[nn * kNI + kF + 2], t[nn * kNI + kF + 3]};
+  double ga[6];
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    const int m = g + 4 * k;
+    ga[k] = ger[m] * (1.0 + pick4(degree_slot(m), gates[0], gates[1], gates[2], gates[3]));
+  }
+  double gsum = 0.0;
+  {
+    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
+    const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
+    for (int m = lo; m < hi; ++m) gsum += ger[m] * aer[m];
+  }
+  const v4d gt8 = v4d{gsum, 0.0, 0.0, 0.0};
+  const double is2 = pre2is[nn], is1 = n1is[nn];
+
+  v4d d[8], acc[9], hat[8];
+  double mg = 0.0, mgx = 0.0;
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int s = decltype(si)::value;
+    if constexpr (s < 8) {
+      // gh = gx * w2 (LayerNorm 2 weight of the lane's channels)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) d[s][r] = wv[r] * A.ln2w[16 * s + 4 * r + g];
+    } else if constexpr (s < SA) {
+      constexpr int mt = s - 8;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        mg += d[mt][r];
+        mgx += d[mt][r] * wv[r];
+      }
+      if constexpr (mt == 7) {
+        mg += __shfl_xor(mg, 16, kWave);
+        mg += __shfl_xor(mg, 32, kWave);
+        mgx += __shfl_xor(mgx, 16, kWave);
+        mgx += __shfl_xor(mgx, 32, kWave);
+        mg /= kF;
+        mgx /= kF;
+#pragma unroll
+        for (int q = 0; q < 9; ++q) acc[q] = v4d{0.0, 0.0, 0.0, 0.0};
+      }
+    } else if constexpr (s < SB) {
+      // gcat = Wint^T gt, gt = [d, gate adjoints]; d = LN2^T gx, chunk by chunk
+      constexpr int T = (s - SA) / 10, u = (s - SA) % 10;
+      if constexpr (T < 8 && u == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) d[T][r] = is2 * (d[T][r] - mg - wv[r] * mgx);
+      } else if constexpr (T < 8) {
+        acc[u - 1] = mfma4(wv, d[T], acc[u - 1]);
+      } else {
+        acc[u] = mfma4(wv, gt8, acc[u]);
+      }
+      if constexpr (s == SB - 1) {
+        // p += gcat[0:128] (kept in LDS until LayerNorm 1); the aev adjoint
+        // gains 2 aev cg gcat[128 + slot]
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          d[q] += acc[q];
+          p_lds[wl][q][lane] = d[q];
+          acc[q] = v4d{0.0, 0.0, 0.0, 0.0};
+        }
+        const double gc[4] = {__shfl(acc[8][0], j, kWave), __shfl(acc[8][0], j + 16, kWave),
+                              __shfl(acc[8][0], j + 32, kWave), __shfl(acc[8][0], j + 48, kWave)};
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+          const int m = g + 4 * k;
+          ga[k] += pick4(degree_slot(m), gc[0], gc[1], gc[2], gc[3]) * 2.0 * aer[m] * A.int_cg[m];
+        }
+      }
+    } else if constexpr (s < SD - 8) {
+      // W2^T p
+      constexpr int i = s - SB;
+      acc[i % 8] = mfma4(wv, d[i / 8], acc[i % 8]);
+    } else if constexpr (s < SD) {
+      // ghid = (W2^T p) silu'(hpre): the operand of W1^T
+      constexpr int mt = s - (SD - 8);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) hat[mt][r] = acc[mt][r] * silu_prime(wv[r]);
+      if constexpr (mt == 7) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] = v4d{0.0, 0.0, 0.0, 0.0};
+      }
+    } else if constexpr (s < SE) {
+      // gact = W1^T ghid
+      constexpr int i = s - SD;
+      acc[i % 8] = mfma4(wv, hat[i / 8], acc[i % 8]);
+    } else if constexpr (s < SE + 8) {
+      // gact silu'(n1)
+      constexpr int mt = s - SE;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mt][r] *= silu_prime(wv[r]);
+    } else if constexpr (s < SE + 16) {
+      hat[s - SE - 8] = wv;  // LayerNorm 1 normalised input
+    } else {
+      // g = p + gact silu'(n1), then gh = g * w1
+      constexpr int mt = s - SE - 16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mt][r] = (wv[r] + acc[mt][r]) * A.ln1w[16 * mt + 4 * r + g];
+    }
+  });
+
+  // LayerNorm 1 reverse
+  double m1 = 0.0, m1x = 0.0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      m1 += acc[q][r];
+      m1x += acc[q][r] * hat[q][r];
+    }
+  m1 += __shfl_xor(m1, 16, kWave);
+  m1 += __shfl_xor(m1, 32, kWave);
+  m1x += __shfl_xor(m1x, 16, kWave);
+  m1x += __shfl_xor(m1x, 32, kWave);
+  m1 /= kF;
+  m1x /= kF;
+  if (valid) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        gainv[nn * kF + 16 * q + 4 * r + g] = is1 * (acc[q][r] - m1 - hat[q][r] * m1x);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) gaev[nn * kE + g + 4 * k] = ga[k];
+  }
+}
+
 // ---------------------------------------------------------------- heads
 struct HeadArgs {
   const double *ew2, *qw2, *escale, *eshift, *qemb, *hqemb, *hvshift, *hkey_bwd, *hkey_c;
@@ -1569,61 +1737,10 @@ __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, cons
 
 // ---------------------------------------------------------------- block reverse
 // LN2 reverse, gate adjoint, start of the interaction reverse
-__global__ __launch_bounds__(256) void k_post2_bwd(int N, const double *gx, const double *gev, const double *t,
-                                                   const double *aev, const double *w, const double *hat,
-                                                   const double *is, double *gp, double *gt, double *gaev) {
-  const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  const std::size_t i = std::size_t(n) * kF, it = std::size_t(n) * kNI;
-  double d0, d1;
-  wave_layer_norm_bwd(gx[i + lane], gx[i + 64 + lane], w, hat[i + lane], hat[i + 64 + lane], is[n], lane,
-                      d0, d1);
-  gp[i + lane] = d0; gp[i + 64 + lane] = d1;
-  gt[it + lane] = d0; gt[it + 64 + lane] = d1;
-  const int slot = lane < kE ? degree_slot(lane) : 7;
-  double ge = 0.0, a = 0.0;
-  if (lane < kE) {
-    ge = gev[std::size_t(n) * kE + lane];
-    a = aev[std::size_t(n) * kE + lane];
-    gaev[std::size_t(n) * kE + lane] = ge * (1.0 + t[it + kF + slot]);
-  }
-  for (int l = 0; l < 4; ++l) {
-    const double s = wave_sum(slot == l ? ge * a : 0.0);
-    if (lane == 0) gt[it + kF + l] = s;
-  }
-}
 
 // gp += gcat[:128]; g_aev += gcat[128 + l] 2 a_ev cg
-__global__ __launch_bounds__(256) void k_post_mid_bwd(int N, const double *gcat, const double *aev,
-                                                      const double *cg, double *gp, double *gaev) {
-  const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  const std::size_t i = std::size_t(n) * kF, it = std::size_t(n) * kNI;
-  gp[i + lane] += gcat[it + lane];
-  gp[i + 64 + lane] += gcat[it + 64 + lane];
-  if (lane < kE) {
-    const std::size_t j = std::size_t(n) * kE + lane;
-    gaev[j] += gcat[it + kF + degree_slot(lane)] * 2.0 * aev[j] * cg[lane];
-  }
-}
 
 // g_n1 = gp + gact silu'(n1); LN1 reverse -> d/d(x + d_inv)
-__global__ __launch_bounds__(256) void k_ln1_bwd(int N, const double *gp, const double *gact, const double *n1,
-                                                 const double *w, const double *hat, const double *is,
-                                                 double *gainv) {
-  const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  const std::size_t i = std::size_t(n) * kF;
-  const double g0 = gp[i + lane] + gact[i + lane] * silu_prime(n1[i + lane]);
-  const double g1 = gp[i + 64 + lane] + gact[i + 64 + lane] * silu_prime(n1[i + 64 + lane]);
-  double d0, d1;
-  wave_layer_norm_bwd(g0, g1, w, hat[i + lane], hat[i + 64 + lane], is[n], lane, d0, d1);
-  gainv[i + lane] = d0;
-  gainv[i + 64 + lane] = d1;
-}
 
 // Attention reverse, node-major (kokkos_attention_scatter_reverse.cpp:280-500).
 // For node n and each active pair p = {n, o}: the incoming edge o -> n gives
@@ -2199,8 +2316,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   heff_ = buf("heff"); eatom_ = buf("eatom"); qraw_ = buf("qraw"); q_ = buf("q"); hir_ = buf("hir");
   qseed_ = buf("qseed"); elr_ = buf("elr"); dq_ = buf("dq"); dh_ = buf("dh"); flr_ = buf("flr");
   vlr_ = buf("vlr"); elr_parts_ = buf("elr_parts"); ezbl_ = buf("ezbl"); gx_ = buf("gx");
-  gev_ = buf("gev"); gp_ = buf("gp"); gt_ = buf("gt"); gcat_ = buf("gcat"); ghid_ = buf("ghid");
-  gact_ = buf("gact"); gainv_ = buf("gainv"); gaev_ = buf("gaev"); gqkv_ = buf("gqkv");
+  gev_ = buf("gev"); gainv_ = buf("gainv"); gaev_ = buf("gaev"); gqkv_ = buf("gqkv");
   ghead_ = buf("ghead"); fout_ = buf("fout"); etot_ = buf("etot"); red_ = buf("red");
   owner_ = buf("owner"); sr_rows_ = buf("sr_rows"); sr_nodes_ = buf("sr_nodes");
   sr_inc_off_ = buf("sr_inc_off"); sr_inc_ = buf("sr_inc"); lr_rows_ = buf("lr_rows");
@@ -2429,11 +2545,6 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   double *ezbl = ensure<double>(ezbl_, Nz);
   double *gx = ensure<double>(gx_, Nz * kF);
   double *gev = ensure<double>(gev_, Nz * kE);
-  double *gp = ensure<double>(gp_, Nz * kF);
-  double *gt = ensure<double>(gt_, Nz * kNI);
-  double *gcat = ensure<double>(gcat_, Nz * kNI);
-  double *ghid = ensure<double>(ghid_, Nz * kF);
-  double *gact = ensure<double>(gact_, Nz * kF);
   double *gainv = ensure<double>(gainv_, Nz * kF);
   double *gaev = ensure<double>(gaev_, Nz * kE);
   double *gqkv = ensure<double>(gqkv_, Nz * 640);
@@ -2490,23 +2601,21 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   auto fill = [&](double *p, std::size_t cnt) {
     if (cnt) hipLaunchKernelGGL(k_fill, dim3(unsigned((cnt + 255) / 256)), dim3(256), 0, s, p, cnt, 0.0);
   };
-  // node GEMM shapes (K, O) of the model: 128x128, 132x132, 128->320, 320->128;
+  // node GEMM shapes (K, O) of the heads: 128->320 and its reverse 320->128;
   // output tiles per wavefront: MT / MG groups run as separate wavefronts
 #ifndef SO3LR_MG8
 #define SO3LR_MG8 4
 #endif
   auto gemm = [&](int epi, int rows, int K, int O, const double *X, int ldx, const double *Wp, const double *bias,
-                  double *out, int ldo, double *out2, const double *aux, int ldaux) {
+                  double *out, int ldo, double *out2) {
     const dim3 grid(unsigned(ceil_div(rows, 64)));
 #define SO3LR_GEMM(E, KT, MT, MG)                                                                             \
   if (epi == E && (K + 15) / 16 == KT && (O + 15) / 16 == MT) {                                              \
     hipLaunchKernelGGL((k_gemm<E, KT, MT, MG>), dim3(grid.x, MT / MG), dim3(256), 0, s, rows, K, O, X, ldx, Wp, \
-                       bias, out, ldo, out2, aux, ldaux);                                                     \
+                       bias, out, ldo, out2);                                                                 \
     return;                                                                                                   \
   }
-    SO3LR_GEMM(0, 8, 8, SO3LR_MG8) SO3LR_GEMM(0, 9, 9, 3) SO3LR_GEMM(0, 20, 8, SO3LR_MG8)
-    SO3LR_GEMM(1, 8, 8, SO3LR_MG8) SO3LR_GEMM(1, 8, 20, 4)
-    SO3LR_GEMM(3, 8, 8, SO3LR_MG8)
+    SO3LR_GEMM(0, 20, 8, SO3LR_MG8) SO3LR_GEMM(1, 8, 20, 4)
 #undef SO3LR_GEMM
     throw std::logic_error("SO3LR: internal error, no node GEMM for this shape");
   };
@@ -2601,7 +2710,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hqemb, hw_.hvshift,
              hw_.hkey_bwd, hw_.hkey_c, hw_.eb2, hw_.qb2};
   const double *xf = xs + L * Nz * kF;
-  gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1p, hhead, 320, hact, nullptr, 0);
+  gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1p, hhead, 320, hact);
   hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, heff, hir);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
   // erf(r / sigma) by the polynomial of erf_lean when r / sigma stays within [0, 3]
@@ -2624,7 +2733,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   });
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
   hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, H, ghead);
-  gemm(0, int(N), 320, kF, ghead, 320, hw_.w1tp, nullptr, gx, kF, nullptr, nullptr, 0);
+  gemm(0, int(N), 320, kF, ghead, 320, hw_.w1tp, nullptr, gx, kF, nullptr);
   fill(gev, Nz * kE);
 
   // --- interaction blocks, reverse ---
@@ -2642,13 +2751,10 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       A.fe0[k] = B.fe0[k]; A.feb0[k] = B.feb0[k]; A.fe1t[k] = B.fe1t[k]; A.feb1[k] = B.feb1[k];
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
-    hipLaunchKernelGGL(k_post2_bwd, dim3(gN4), dim3(256), 0, s, int(N), gx, gev, tb, aevb, B.ln2w, p2h, p2i, gp,
-                       gt, gaev);
-    gemm(0, int(N), kNI, kNI, gt, kNI, B.inttp, nullptr, gcat, kNI, nullptr, nullptr, 0);
-    hipLaunchKernelGGL(k_post_mid_bwd, dim3(gN4), dim3(256), 0, s, int(N), gcat, aevb, B.int_cg, gp, gaev);
-    gemm(3, int(N), kF, kF, gp, kF, B.m2tp, nullptr, ghid, kF, nullptr, hpb, kF);
-    gemm(0, int(N), kF, kF, ghid, kF, B.m1tp, nullptr, gact, kF, nullptr, nullptr, 0);
-    hipLaunchKernelGGL(k_ln1_bwd, dim3(gN4), dim3(256), 0, s, int(N), gp, gact, n1b, B.ln1w, n1hb, n1ib, gainv);
+    // the post-attention node chain in reverse in one kernel: gainv, gaev
+    const NodeChainBwdArgs NB{B.inttp, B.m2tp, B.m1tp, B.int_cg, B.ln1w, B.ln2w};
+    hipLaunchKernelGGL(k_node_bwd, dim3(gN64), dim3(256), 0, s, int(N), gx, gev, tb, aevb, p2h, p2i, hpb, n1b, n1hb,
+                       n1ib, NB, gainv, gaev);
     const bool blk0 = b == 0 && !naive_filters_;
     timed(b == 0 ? "attn_bwd_block0" : "attn_bwd", 1, [&] {
       if (b > 0)

@@ -164,7 +164,7 @@ class Evaluator {
   Buffer *ainv_, *act_;
   Buffer *hhead_, *heff_, *eatom_, *qraw_, *q_, *hir_, *qseed_;
   Buffer *elr_, *dq_, *dh_, *flr_, *vlr_, *elr_parts_, *ezbl_;
-  Buffer *gx_, *gev_, *gp_, *gt_, *gcat_, *ghid_, *gact_, *gainv_, *gaev_, *gqkv_, *ghead_;
+  Buffer *gx_, *gev_, *gainv_, *gaev_, *gqkv_, *ghead_;
   Buffer *fout_, *etot_, *red_, *red_part_;
   // pair-sized buffers
   Buffer *owner_, *sr_rows_, *sr_nodes_, *sr_inc_off_, *sr_inc_, *lr_rows_, *lr_nodes_,
