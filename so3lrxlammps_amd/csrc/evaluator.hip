@@ -1370,6 +1370,182 @@ __global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restric
   }
 }
 
+// The same chain with two wavefronts per 16 atoms (four per block: two
+// 16-atom tiles), so that a 24k-atom system fills the chip: half h of a tile
+// computes the output tiles 4 h .. 4 h + 3 of each layer (and the gate tile 8
+// in half 0), and the layer inputs are exchanged through LDS in the operand
+// order (chunk T of lane l at buf[tile][T][l]).  LayerNorm 2's row sums are
+// combined across the halves through LDS as well.
+__global__ __launch_bounds__(256) void k_node_fwd2(int N, const double *__restrict__ act,
+                                                   const double *__restrict__ n1, const double *__restrict__ aev,
+                                                   NodeChainArgs A, double *__restrict__ hpre,
+                                                   double *__restrict__ tout, double *__restrict__ xout,
+                                                   double *__restrict__ evout, double *__restrict__ pre2hat,
+                                                   double *__restrict__ pre2is) {
+  __shared__ double exp2_lds[64];
+  __shared__ v4d buf[2][8][64];         // one 16-atom tile's layer input, operand order (16 KB per tile)
+  __shared__ double stat[2][2][2][64];  // [tile][half][sum, sum of squares][lane]
+  if (threadIdx.x < 64) exp2_lds[threadIdx.x] = A.exp2_64[threadIdx.x];
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int wl = threadIdx.x >> 6, tile = wl >> 1, h = wl & 1;
+  // every wavefront runs to the end (the barriers); rows beyond N are clamped
+  const int n = blockIdx.x * 32 + tile * 16 + j;
+  const bool valid = n < N;
+  const std::size_t nn = std::size_t(valid ? n : N - 1);
+  __syncthreads();
+  auto chunk = [&](const double *rows, int T) {
+    const double *r = rows + nn * kF + 16 * T + g;
+    return v4d{r[0], r[4], r[8], r[12]};
+  };
+  // stream: MLP-1 biases (4), per T the act chunk and 4 W1 fragments (40);
+  // MLP-2 biases (4), 8 x 4 W2 fragments (32), the 4 n1 chunks of the
+  // residual; the interaction biases (5: the 5th is the gate tile, used by
+  // half 0 only) and per T (9) 5 fragments
+  constexpr int P1 = 4 + 40, P2 = P1 + 4 + 32 + 4, NS = P2 + 5 + 45;
+  const int o0 = 4 * h;  // first output tile of this half
+  auto tmt = [&](int q) { return q < 4 ? o0 + q : 8; };  // interaction output tile q of this half
+  auto load = [&](auto si) -> v4d {
+    constexpr int s = decltype(si)::value;
+    if constexpr (s < 4) {
+      return tile_load(A.m1bp, o0 + s, lane);
+    } else if constexpr (s < P1) {
+      constexpr int T = (s - 4) / 5, u = (s - 4) % 5;
+      if constexpr (u == 0) return chunk(act, T);
+      else return wload(A.m1p, 8, o0 + u - 1, T, lane);
+    } else if constexpr (s < P1 + 4) {
+      return tile_load(A.m2bp, o0 + s - P1, lane);
+    } else if constexpr (s < P2 - 4) {
+      constexpr int i = s - P1 - 4;
+      return wload(A.m2p, 8, o0 + i % 4, i / 4, lane);
+    } else if constexpr (s < P2) {
+      return chunk(n1, o0 + s - (P2 - 4));
+    } else if constexpr (s < P2 + 5) {
+      return tile_load(A.intbp, tmt(s - P2), lane);
+    } else {
+      constexpr int i = s - P2 - 5;
+      return wload(A.intp, 9, tmt(i % 5), i / 5, lane);
+    }
+  };
+  Stream<NS, kFilterPF, decltype(load)> st(load);
+  st.prime();
+
+  double inv = 0.0;
+  {
+    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
+    const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
+    for (int m = lo; m < hi; ++m) {
+      const double a = aev[nn * kE + m];
+      inv += a * a * A.int_cg[m];
+    }
+  }
+  const v4d inv4 = v4d{inv, 0.0, 0.0, 0.0};
+  v4d acc[5], pb[4], xT;
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int s = decltype(si)::value;
+    if constexpr (s < 4) {
+      acc[s] = wv;
+    } else if constexpr (s < P1) {
+      constexpr int u = (s - 4) % 5;
+      if constexpr (u == 0) xT = wv;
+      else acc[u - 1] = mfma4(wv, xT, acc[u - 1]);
+      if constexpr (s == P1 - 1) {
+        // hpre (kept) and silu(hpre) into LDS for both halves
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v4d hd;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (valid) hpre[nn * kF + 16 * (o0 + q) + 4 * r + g] = acc[q][r];
+            hd[r] = silu_tab(acc[q][r], exp2_lds);
+          }
+          buf[tile][o0 + q][lane] = hd;
+        }
+        __syncthreads();
+      }
+    } else if constexpr (s < P1 + 4) {
+      acc[s - P1] = wv;
+    } else if constexpr (s < P2 - 4) {
+      constexpr int i = s - P1 - 4;
+      acc[i % 4] = mfma4(wv, buf[tile][i / 4][lane], acc[i % 4]);
+      if constexpr (s == P2 - 5) __syncthreads();  // every half has read the MLP-2 input
+    } else if constexpr (s < P2) {
+      constexpr int q = s - (P2 - 4);
+      pb[q] = acc[q] + wv;  // p = n1 + W2 hid + b2
+      buf[tile][o0 + q][lane] = pb[q];
+      if constexpr (q == 3) __syncthreads();
+    } else if constexpr (s < P2 + 5) {
+      acc[s - P2] = wv;
+    } else {
+      constexpr int i = s - P2 - 5, T = i / 5, q = i % 5;
+      if (q < 4 || h == 0) {
+        if constexpr (T < 8) acc[q] = mfma4(wv, buf[tile][T][lane], acc[q]);
+        else acc[q] = mfma4(wv, inv4, acc[q]);
+      }
+    }
+  });
+
+  // interaction output (kept); LayerNorm 2 of p + t over the row, the two
+  // halves' sums combined through LDS
+#pragma unroll
+  for (int q = 0; q < 5; ++q) {
+    if (q == 4 && h != 0) break;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = 16 * tmt(q) + 4 * r + g;
+      if (valid && c < kNI) tout[nn * kNI + c] = acc[q][r];
+    }
+  }
+  double sum = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    pb[q] += acc[q];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sum += pb[q][r];
+  }
+  sum += __shfl_xor(sum, 16, kWave);
+  sum += __shfl_xor(sum, 32, kWave);
+  stat[tile][h][0][lane] = sum;
+  __syncthreads();
+  const double mean = (stat[tile][0][0][lane] + stat[tile][1][0][lane]) / kF;
+  double var = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const double d = pb[q][r] - mean;
+      var += d * d;
+    }
+  var += __shfl_xor(var, 16, kWave);
+  var += __shfl_xor(var, 32, kWave);
+  stat[tile][h][1][lane] = var;
+  __syncthreads();
+  const double is = 1.0 / sqrt((stat[tile][0][1][lane] + stat[tile][1][1][lane]) / kF + A.eps);
+  if (valid) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = 16 * (o0 + q) + 4 * r + g;
+        const double hh = (pb[q][r] - mean) * is;
+        pre2hat[nn * kF + c] = hh;
+        xout[nn * kF + c] = hh * A.ln2w[c] + A.ln2b[c];
+      }
+    if (h == 0 && g == 0) pre2is[nn] = is;
+  }
+  if (h == 0) {
+    // ev' = aev (1 + gate[slot]); gate l = t[128 + l] in lane j + 16 l of half 0
+    const double gate[4] = {__shfl(acc[4][0], j, kWave), __shfl(acc[4][0], j + 16, kWave),
+                            __shfl(acc[4][0], j + 32, kWave), __shfl(acc[4][0], j + 48, kWave)};
+    if (valid) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) {
+        const int m = g + 4 * k;
+        evout[nn * kE + m] = aev[nn * kE + m] * (1.0 + pick4(degree_slot(m), gate[0], gate[1], gate[2], gate[3]));
+      }
+    }
+  }
+}
+
 // Reverse of the post-attention node chain, 16 atoms per wavefront, the
 // adjoints in MFMA registers (kokkos_post_attention_reverse.cpp:328-449):
 //   LayerNorm 2 reverse: d = LN2^T gx, the adjoint of p and of t[0:128];
@@ -2702,7 +2878,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     // the post-attention node chain in one kernel (MLP, interaction, LayerNorm 2, ev gate)
     const NodeChainArgs NC{B.m1p, B.m1bp, B.m2p, B.m2bp, B.intp, B.intbp, B.int_cg, B.ln2w, B.ln2b, hw_.exp2_64,
                            ln_eps_};
-    hipLaunchKernelGGL(k_node_fwd, dim3(gN64), dim3(256), 0, s, int(N), act, n1b, aevb, NC, hpb, tb,
+    hipLaunchKernelGGL(k_node_fwd2, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), act, n1b, aevb, NC, hpb, tb,
                        xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);
   }
 
