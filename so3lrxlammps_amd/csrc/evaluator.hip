@@ -1201,182 +1201,26 @@ __global__ __launch_bounds__(256) void k_post1(int N, const double *ainv, const 
 }
 
 
-// The post-attention node chain of one block, 16 atoms per wavefront with
-// every activation in MFMA registers (kokkos_post_attention_block0.cpp:302-333):
+// The post-attention node chain of one block with every activation in MFMA
+// registers (kokkos_post_attention_block0.cpp:302-333):
 //   hpre = W1 silu(n1) + b1 (kept for the reverse), hid = silu(hpre),
 //   p = n1 + W2 hid + b2,
 //   t = Wint [p, inv(aev)] + bint (132 wide, kept), inv_l = sum_{m in l} aev_m^2 cg_m,
 //   x' = LN2(p + t[0:128]) (statistics kept), ev' = aev (1 + t[128 + slot]).
 // An MFMA output tile (rows 16 mt + 4 r + g of node j in lane j + 16 g,
 // register r) is the B operand of the next layer as it stands, so the layers
-// chain without memory round trips.  One operand stream: the MLP-1 bias
-// tiles, then per K chunk T the silu(n1) chunk and the 8 W1 fragments; the
-// MLP-2 biases, per T the 8 W2 fragments, then the 8 n1 chunks of the
-// residual; the 9 interaction biases and per T (9, the last one the
-// invariants) its 9 fragments.
+// chain without memory round trips.
 struct NodeChainArgs {
   const double *m1p, *m1bp, *m2p, *m2bp, *intp, *intbp;  // MFMA operand order
   const double *int_cg, *ln2w, *ln2b, *exp2_64;
   double eps;
 };
-__global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restrict__ act,
-                                                  const double *__restrict__ n1, const double *__restrict__ aev,
-                                                  NodeChainArgs A, double *__restrict__ hpre,
-                                                  double *__restrict__ tout, double *__restrict__ xout,
-                                                  double *__restrict__ evout, double *__restrict__ pre2hat,
-                                                  double *__restrict__ pre2is) {
-  __shared__ double exp2_lds[64];
-  if (threadIdx.x < 64) exp2_lds[threadIdx.x] = A.exp2_64[threadIdx.x];
-  __syncthreads();
-  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (w * 16 >= N) return;
-  const int n = w * 16 + j;
-  const bool valid = n < N;
-  const std::size_t nn = std::size_t(valid ? n : N - 1);
-  // node-row chunk T in the operand order: features 16 T + g + 4 v
-  auto chunk = [&](const double *rows, int ld, int T) {
-    const double *r = rows + nn * ld + 16 * T + g;
-    return v4d{r[0], r[4], r[8], r[12]};
-  };
-  constexpr int P1 = 8 + 8 * 9, P2 = P1 + 8 + 8 * 8 + 8, NS = P2 + 9 + 9 * 9;
-  auto load = [&](auto si) -> v4d {
-    constexpr int s = decltype(si)::value;
-    if constexpr (s < 8) {
-      return tile_load(A.m1bp, s, lane);
-    } else if constexpr (s < P1) {
-      constexpr int T = (s - 8) / 9, u = (s - 8) % 9;
-      if constexpr (u == 0) return chunk(act, kF, T);
-      else return wload(A.m1p, 8, u - 1, T, lane);
-    } else if constexpr (s < P1 + 8) {
-      return tile_load(A.m2bp, s - P1, lane);
-    } else if constexpr (s < P2 - 8) {
-      constexpr int i = s - P1 - 8;
-      return wload(A.m2p, 8, i % 8, i / 8, lane);
-    } else if constexpr (s < P2) {
-      return chunk(n1, kF, s - (P2 - 8));
-    } else if constexpr (s < P2 + 9) {
-      return tile_load(A.intbp, s - P2, lane);
-    } else {
-      constexpr int i = s - P2 - 9;
-      return wload(A.intp, 9, i % 9, i / 9, lane);
-    }
-  };
-  Stream<NS, kFilterPF, decltype(load)> st(load);
-  st.prime();
-
-  // the 4 invariants of the attention's equivariant output: lane group g
-  // holds invariant g of node j, the K chunk 8 of the interaction input
-  double inv = 0.0;
-  {
-    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
-    const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
-    for (int m = lo; m < hi; ++m) {
-      const double a = aev[nn * kE + m];
-      inv += a * a * A.int_cg[m];
-    }
-  }
-  const v4d inv4 = v4d{inv, 0.0, 0.0, 0.0};
-  v4d acc[9], xb[8], xT;
-  st.run([&](auto si, const v4d &wv) {
-    constexpr int s = decltype(si)::value;
-    if constexpr (s < 8) {
-      acc[s] = wv;
-    } else if constexpr (s < P1) {
-      constexpr int u = (s - 8) % 9;
-      if constexpr (u == 0) xT = wv;
-      else acc[u - 1] = mfma4(wv, xT, acc[u - 1]);
-      if constexpr (s == P1 - 1) {
-        // hpre kept for the reverse; silu(hpre) is the MLP-2 operand
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (valid) hpre[nn * kF + 16 * mt + 4 * r + g] = acc[mt][r];
-            xb[mt][r] = silu_tab(acc[mt][r], exp2_lds);
-          }
-        }
-      }
-    } else if constexpr (s < P1 + 8) {
-      acc[s - P1] = wv;
-    } else if constexpr (s < P2 - 8) {
-      constexpr int i = s - P1 - 8;
-      acc[i % 8] = mfma4(wv, xb[i / 8], acc[i % 8]);
-    } else if constexpr (s < P2) {
-      constexpr int mt = s - (P2 - 8);
-      xb[mt] = acc[mt] + wv;  // p = n1 + W2 hid + b2
-    } else if constexpr (s < P2 + 9) {
-      acc[s - P2] = wv;
-    } else {
-      constexpr int i = s - P2 - 9, T = i / 9;
-      if constexpr (T < 8) acc[i % 9] = mfma4(wv, xb[T], acc[i % 9]);
-      else acc[i % 9] = mfma4(wv, inv4, acc[i % 9]);
-    }
-  });
-
-  // interaction output kept for the reverse (132 wide)
-#pragma unroll
-  for (int mt = 0; mt < 9; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = 16 * mt + 4 * r + g;
-      if (valid && c < kNI) tout[nn * kNI + c] = acc[mt][r];
-    }
-  // LayerNorm 2 of p + t over the 128 features of node j: 32 per lane, the
-  // rest in the lanes of the other three lane groups
-  double sum = 0.0;
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt) {
-    xb[mt] += acc[mt];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sum += xb[mt][r];
-  }
-  sum += __shfl_xor(sum, 16, kWave);
-  sum += __shfl_xor(sum, 32, kWave);
-  const double mean = sum / kF;
-  double var = 0.0;
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const double d = xb[mt][r] - mean;
-      var += d * d;
-    }
-  var += __shfl_xor(var, 16, kWave);
-  var += __shfl_xor(var, 32, kWave);
-  const double is = 1.0 / sqrt(var / kF + A.eps);
-  if (valid) {
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int c = 16 * mt + 4 * r + g;
-        const double h = (xb[mt][r] - mean) * is;
-        pre2hat[nn * kF + c] = h;
-        xout[nn * kF + c] = h * A.ln2w[c] + A.ln2b[c];
-      }
-    if (g == 0) pre2is[nn] = is;
-  }
-  // ev' = aev (1 + gate[slot]); gate l = t[128 + l] sits in lane j + 16 l, register 0
-  const double gate[4] = {__shfl(acc[8][0], j, kWave), __shfl(acc[8][0], j + 16, kWave),
-                          __shfl(acc[8][0], j + 32, kWave), __shfl(acc[8][0], j + 48, kWave)};
-  if (valid) {
-#pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const int m = g + 4 * k;
-      const int sl = degree_slot(m);
-      evout[nn * kE + m] = aev[nn * kE + m] * (1.0 + pick4(sl, gate[0], gate[1], gate[2], gate[3]));
-    }
-  }
-}
-
-// The same chain with two wavefronts per 16 atoms (four per block: two
-// 16-atom tiles), so that a 24k-atom system fills the chip: half h of a tile
-// computes the output tiles 4 h .. 4 h + 3 of each layer (and the gate tile 8
-// in half 0), and the layer inputs are exchanged through LDS in the operand
+// Two wavefronts per 16 atoms (four per block: two 16-atom tiles), so that a
+// 24k-atom system fills the chip: half h of a tile computes the output tiles
+// 4 h .. 4 h + 3 of each layer (and the gate tile 8 in half 0), and the layer inputs are exchanged through LDS in the operand
 // order (chunk T of lane l at buf[tile][T][l]).  LayerNorm 2's row sums are
 // combined across the halves through LDS as well.
-__global__ __launch_bounds__(256) void k_node_fwd2(int N, const double *__restrict__ act,
+__global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restrict__ act,
                                                    const double *__restrict__ n1, const double *__restrict__ aev,
                                                    NodeChainArgs A, double *__restrict__ hpre,
                                                    double *__restrict__ tout, double *__restrict__ xout,
@@ -1547,8 +1391,8 @@ __global__ __launch_bounds__(256) void k_node_fwd2(int N, const double *__restri
   }
 }
 
-// Reverse of the post-attention node chain, 16 atoms per wavefront, the
-// adjoints in MFMA registers (kokkos_post_attention_reverse.cpp:328-449):
+// Reverse of the post-attention node chain, the adjoints in MFMA registers
+// (kokkos_post_attention_reverse.cpp:328-449):
 //   LayerNorm 2 reverse: d = LN2^T gx, the adjoint of p and of t[0:128];
 //   t[128 + l] (gates): sum_{m in l} gev_m aev_m; aev: gev (1 + gate);
 //   interaction reverse: gcat = Wint^T gt; p += gcat[0:128];
@@ -1556,65 +1400,75 @@ __global__ __launch_bounds__(256) void k_node_fwd2(int N, const double *__restri
 //   MLP reverse: ghid = (W2^T p) silu'(hpre), gact = W1^T ghid;
 //   LayerNorm 1 reverse of g = p + gact silu'(n1): the adjoint of the
 //   attention residual, gainv.
-// The operand stream: the gx and LN2-normalised chunks (the latter twice:
-// once for the statistics, once per K chunk of Wint^T), Wint^T (9 x 9), W2^T
-// (8 x 8) and the hpre chunks, W1^T (8 x 8), then the n1, LN1-normalised and
-// p chunks (p waits in LDS between the two halves, so that at most two
-// 8-tile register sets are live).
 struct NodeChainBwdArgs {
   const double *inttp, *m2tp, *m1tp;  // MFMA operand order (transposes)
   const double *int_cg, *ln1w, *ln2w;
 };
+// Two wavefronts per 16 atoms (four per block: two 16-atom tiles): half h
+// owns the feature tiles 4 h .. 4 h + 3 of every 128-wide adjoint (and the
+// gate tile 8 in half 0); each layer's input adjoint is exchanged through LDS
+// in the operand order, and the LayerNorm row sums are combined across the
+// halves through LDS.
 __global__ __launch_bounds__(256) void k_node_bwd(int N, const double *__restrict__ gx,
-                                                  const double *__restrict__ gev, const double *__restrict__ t,
-                                                  const double *__restrict__ aev, const double *__restrict__ pre2hat,
-                                                  const double *__restrict__ pre2is, const double *__restrict__ hpre,
-                                                  const double *__restrict__ n1, const double *__restrict__ n1hat,
-                                                  const double *__restrict__ n1is, NodeChainBwdArgs A,
-                                                  double *__restrict__ gainv, double *__restrict__ gaev) {
-  __shared__ v4d p_lds[4][8][64];  // the p adjoint of each wavefront, operand order (64 KB)
-  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4, wl = threadIdx.x >> 6;
-  const int w = blockIdx.x * 4 + wl;
-  if (w * 16 >= N) return;
-  const int n = w * 16 + j;
+                                                   const double *__restrict__ gev, const double *__restrict__ t,
+                                                   const double *__restrict__ aev, const double *__restrict__ pre2hat,
+                                                   const double *__restrict__ pre2is, const double *__restrict__ hpre,
+                                                   const double *__restrict__ n1, const double *__restrict__ n1hat,
+                                                   const double *__restrict__ n1is, NodeChainBwdArgs A,
+                                                   double *__restrict__ gainv, double *__restrict__ gaev) {
+  __shared__ v4d buf[2][8][64];         // one tile's layer-input adjoint, operand order (16 KB per tile)
+  __shared__ double stat[2][2][2][64];  // [tile][half][two sums][lane]
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int wl = threadIdx.x >> 6, tile = wl >> 1, h = wl & 1;
+  const int n = blockIdx.x * 32 + tile * 16 + j;
   const bool valid = n < N;
   const std::size_t nn = std::size_t(valid ? n : N - 1);
+  const int o0 = 4 * h;
   auto chunk = [&](const double *rows, int T) {
     const double *r = rows + nn * kF + 16 * T + g;
     return v4d{r[0], r[4], r[8], r[12]};
   };
-  // phase B per K chunk T < 8: the LN2-normalised chunk T, then the 9
-  // fragments; T = 8 (the gate adjoints): the 9 fragments
-  constexpr int SA = 16, SB = SA + 8 * 10 + 9, SD = SB + 64 + 8, SE = SD + 64, NS = SE + 24;
+  auto tmt = [&](int q) { return q < 4 ? o0 + q : 8; };
+  // both halves' two sums of a row, combined (one barrier)
+  auto row_sums = [&](double a, double b, double &ta, double &tb) {
+    a += __shfl_xor(a, 16, kWave);
+    a += __shfl_xor(a, 32, kWave);
+    b += __shfl_xor(b, 16, kWave);
+    b += __shfl_xor(b, 32, kWave);
+    stat[tile][h][0][lane] = a;
+    stat[tile][h][1][lane] = b;
+    __syncthreads();
+    ta = stat[tile][0][0][lane] + stat[tile][1][0][lane];
+    tb = stat[tile][0][1][lane] + stat[tile][1][1][lane];
+  };
+  // stream: the 4 gx and 4 LN2-normalised chunks of this half; Wint^T for
+  // the 5 output tiles (the 5th, the gate tile, for half 0) over 9 K chunks;
+  // W2^T for 4 tiles over 8 chunks and the 4 hpre chunks; W1^T likewise and
+  // the 4 n1 and 4 LN1-normalised chunks
+  constexpr int SA = 8, SB = SA + 45, SD = SB + 32 + 4, NS = SD + 32 + 8;
   auto load = [&](auto si) -> v4d {
     constexpr int s = decltype(si)::value;
-    if constexpr (s < 8) return chunk(gx, s);
-    else if constexpr (s < SA) return chunk(pre2hat, s - 8);
-    else if constexpr (s < SB) {
-      constexpr int T = (s - SA) / 10, u = (s - SA) % 10;
-      if constexpr (T < 8 && u == 0) return chunk(pre2hat, T);
-      else if constexpr (T < 8) return wload(A.inttp, 9, u - 1, T, lane);
-      else return wload(A.inttp, 9, u, 8, lane);
-    }
-    else if constexpr (s < SD - 8) return wload(A.m2tp, 8, (s - SB) % 8, (s - SB) / 8, lane);
-    else if constexpr (s < SD) return chunk(hpre, s - (SD - 8));
-    else if constexpr (s < SE) return wload(A.m1tp, 8, (s - SD) % 8, (s - SD) / 8, lane);
-    else if constexpr (s < SE + 8) return chunk(n1, s - SE);
-    else if constexpr (s < SE + 16) return chunk(n1hat, s - SE - 8);
-    else return p_lds[wl][s - SE - 16][lane];
+    if constexpr (s < 4) return chunk(gx, o0 + s);
+    else if constexpr (s < SA) return chunk(pre2hat, o0 + s - 4);
+    else if constexpr (s < SB) return wload(A.inttp, 9, tmt((s - SA) % 5), (s - SA) / 5, lane);
+    else if constexpr (s < SD - 4) return wload(A.m2tp, 8, o0 + (s - SB) % 4, (s - SB) / 4, lane);
+    else if constexpr (s < SD) return chunk(hpre, o0 + s - (SD - 4));
+    else if constexpr (s < NS - 8) return wload(A.m1tp, 8, o0 + (s - SD) % 4, (s - SD) / 4, lane);
+    else if constexpr (s < NS - 4) return chunk(n1, o0 + s - (NS - 8));
+    else return chunk(n1hat, o0 + s - (NS - 4));
   };
   Stream<NS, kFilterPF, decltype(load)> st(load);
   st.prime();
 
-  // per-lane pieces of the equivariant part: lane group g handles channels
-  // m = g + 4 k (k < 6); the gate adjoint l = g is its slot sum
   const double *ger = gev + nn * kE, *aer = aev + nn * kE;
-  const double gates[4] = {t[nn * kNI + kF], t[nn * kNI + kF + 1], t[nn * kNI + kF + 2], t[nn * kNI + kF + 3]};
-  double ga[6];
+  double ga[6] = {0, 0, 0, 0, 0, 0};
+  if (h == 0) {
+    const double gates[4] = {t[nn * kNI + kF], t[nn * kNI + kF + 1], t[nn * kNI + kF + 2], t[nn * kNI + kF + 3]};
 #pragma unroll
-  for (int k = 0; k < 6; ++k) {
-    const int m = g + 4 * k;
-    ga[k] = ger[m] * (1.0 + pick4(degree_slot(m), gates[0], gates[1], gates[2], gates[3]));
+    for (int k = 0; k < 6; ++k) {
+      const int m = g + 4 * k;
+      ga[k] = ger[m] * (1.0 + pick4(degree_slot(m), gates[0], gates[1], gates[2], gates[3]));
+    }
   }
   double gsum = 0.0;
   {
@@ -1625,114 +1479,120 @@ __global__ __launch_bounds__(256) void k_node_bwd(int N, const double *__restric
   const v4d gt8 = v4d{gsum, 0.0, 0.0, 0.0};
   const double is2 = pre2is[nn], is1 = n1is[nn];
 
-  v4d d[8], acc[9], hat[8];
+  v4d d[4], acc[5], hat[4];
   double mg = 0.0, mgx = 0.0;
   st.run([&](auto si, const v4d &wv) {
     constexpr int s = decltype(si)::value;
-    if constexpr (s < 8) {
-      // gh = gx * w2 (LayerNorm 2 weight of the lane's channels)
+    if constexpr (s < 4) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) d[s][r] = wv[r] * A.ln2w[16 * s + 4 * r + g];
+      for (int r = 0; r < 4; ++r) d[s][r] = wv[r] * A.ln2w[16 * (o0 + s) + 4 * r + g];
     } else if constexpr (s < SA) {
-      constexpr int mt = s - 8;
+      constexpr int q = s - 4;
+      hat[q] = wv;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        mg += d[mt][r];
-        mgx += d[mt][r] * wv[r];
+        mg += d[q][r];
+        mgx += d[q][r] * wv[r];
       }
-      if constexpr (mt == 7) {
-        mg += __shfl_xor(mg, 16, kWave);
-        mg += __shfl_xor(mg, 32, kWave);
-        mgx += __shfl_xor(mgx, 16, kWave);
-        mgx += __shfl_xor(mgx, 32, kWave);
-        mg /= kF;
-        mgx /= kF;
+      if constexpr (q == 3) {
+        // LayerNorm 2 reverse; the adjoint of p and t[0:128] into LDS
+        double tm, tx;
+        row_sums(mg, mgx, tm, tx);
+        tm /= kF;
+        tx /= kF;
 #pragma unroll
-        for (int q = 0; q < 9; ++q) acc[q] = v4d{0.0, 0.0, 0.0, 0.0};
+        for (int q2 = 0; q2 < 4; ++q2) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) d[q2][r] = is2 * (d[q2][r] - tm - hat[q2][r] * tx);
+          buf[tile][o0 + q2][lane] = d[q2];
+        }
+#pragma unroll
+        for (int q2 = 0; q2 < 5; ++q2) acc[q2] = v4d{0.0, 0.0, 0.0, 0.0};
+        __syncthreads();
       }
     } else if constexpr (s < SB) {
-      // gcat = Wint^T gt, gt = [d, gate adjoints]; d = LN2^T gx, chunk by chunk
-      constexpr int T = (s - SA) / 10, u = (s - SA) % 10;
-      if constexpr (T < 8 && u == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) d[T][r] = is2 * (d[T][r] - mg - wv[r] * mgx);
-      } else if constexpr (T < 8) {
-        acc[u - 1] = mfma4(wv, d[T], acc[u - 1]);
-      } else {
-        acc[u] = mfma4(wv, gt8, acc[u]);
+      // gcat = Wint^T [d, gate adjoints]
+      constexpr int i = s - SA, T = i / 5, q = i % 5;
+      if (q < 4 || h == 0) {
+        if constexpr (T < 8) acc[q] = mfma4(wv, buf[tile][T][lane], acc[q]);
+        else acc[q] = mfma4(wv, gt8, acc[q]);
       }
       if constexpr (s == SB - 1) {
-        // p += gcat[0:128] (kept in LDS until LayerNorm 1); the aev adjoint
-        // gains 2 aev cg gcat[128 + slot]
+        // p += gcat[own]; the aev adjoint gains 2 aev cg gcat[128 + slot]
+        if (h == 0) {
+          const double gc[4] = {__shfl(acc[4][0], j, kWave), __shfl(acc[4][0], j + 16, kWave),
+                                __shfl(acc[4][0], j + 32, kWave), __shfl(acc[4][0], j + 48, kWave)};
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          d[q] += acc[q];
-          p_lds[wl][q][lane] = d[q];
-          acc[q] = v4d{0.0, 0.0, 0.0, 0.0};
+          for (int k = 0; k < 6; ++k) {
+            const int m = g + 4 * k;
+            ga[k] += pick4(degree_slot(m), gc[0], gc[1], gc[2], gc[3]) * 2.0 * aer[m] * A.int_cg[m];
+          }
         }
-        const double gc[4] = {__shfl(acc[8][0], j, kWave), __shfl(acc[8][0], j + 16, kWave),
-                              __shfl(acc[8][0], j + 32, kWave), __shfl(acc[8][0], j + 48, kWave)};
+        __syncthreads();  // every half has read d
 #pragma unroll
-        for (int k = 0; k < 6; ++k) {
-          const int m = g + 4 * k;
-          ga[k] += pick4(degree_slot(m), gc[0], gc[1], gc[2], gc[3]) * 2.0 * aer[m] * A.int_cg[m];
+        for (int q2 = 0; q2 < 4; ++q2) {
+          d[q2] += acc[q2];
+          buf[tile][o0 + q2][lane] = d[q2];
+          acc[q2] = v4d{0.0, 0.0, 0.0, 0.0};
         }
+        __syncthreads();
       }
-    } else if constexpr (s < SD - 8) {
+    } else if constexpr (s < SD - 4) {
       // W2^T p
       constexpr int i = s - SB;
-      acc[i % 8] = mfma4(wv, d[i / 8], acc[i % 8]);
+      acc[i % 4] = mfma4(wv, buf[tile][i / 4][lane], acc[i % 4]);
     } else if constexpr (s < SD) {
-      // ghid = (W2^T p) silu'(hpre): the operand of W1^T
-      constexpr int mt = s - (SD - 8);
+      // ghid = (W2^T p) silu'(hpre), own tiles
+      constexpr int q = s - (SD - 4);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) hat[mt][r] = acc[mt][r] * silu_prime(wv[r]);
-      if constexpr (mt == 7) {
+      for (int r = 0; r < 4; ++r) hat[q][r] = acc[q][r] * silu_prime(wv[r]);
+      if constexpr (q == 3) {
+        __syncthreads();  // every half has read p
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[q] = v4d{0.0, 0.0, 0.0, 0.0};
+        for (int q2 = 0; q2 < 4; ++q2) {
+          buf[tile][o0 + q2][lane] = hat[q2];
+          acc[q2] = v4d{0.0, 0.0, 0.0, 0.0};
+        }
+        __syncthreads();
       }
-    } else if constexpr (s < SE) {
+    } else if constexpr (s < NS - 8) {
       // gact = W1^T ghid
       constexpr int i = s - SD;
-      acc[i % 8] = mfma4(wv, hat[i / 8], acc[i % 8]);
-    } else if constexpr (s < SE + 8) {
-      // gact silu'(n1)
-      constexpr int mt = s - SE;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[mt][r] *= silu_prime(wv[r]);
-    } else if constexpr (s < SE + 16) {
-      hat[s - SE - 8] = wv;  // LayerNorm 1 normalised input
-    } else {
+      acc[i % 4] = mfma4(wv, buf[tile][i / 4][lane], acc[i % 4]);
+    } else if constexpr (s < NS - 4) {
       // g = p + gact silu'(n1), then gh = g * w1
-      constexpr int mt = s - SE - 16;
+      constexpr int q = s - (NS - 8);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[mt][r] = (wv[r] + acc[mt][r]) * A.ln1w[16 * mt + 4 * r + g];
+      for (int r = 0; r < 4; ++r)
+        acc[q][r] = (d[q][r] + acc[q][r] * silu_prime(wv[r])) * A.ln1w[16 * (o0 + q) + 4 * r + g];
+    } else {
+      hat[s - (NS - 4)] = wv;  // LayerNorm 1 normalised input
     }
   });
 
   // LayerNorm 1 reverse
   double m1 = 0.0, m1x = 0.0;
 #pragma unroll
-  for (int q = 0; q < 8; ++q)
+  for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       m1 += acc[q][r];
       m1x += acc[q][r] * hat[q][r];
     }
-  m1 += __shfl_xor(m1, 16, kWave);
-  m1 += __shfl_xor(m1, 32, kWave);
-  m1x += __shfl_xor(m1x, 16, kWave);
-  m1x += __shfl_xor(m1x, 32, kWave);
-  m1 /= kF;
-  m1x /= kF;
+  double tm, tx;
+  row_sums(m1, m1x, tm, tx);
+  tm /= kF;
+  tx /= kF;
   if (valid) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        gainv[nn * kF + 16 * q + 4 * r + g] = is1 * (acc[q][r] - m1 - hat[q][r] * m1x);
+        gainv[nn * kF + 16 * (o0 + q) + 4 * r + g] = is1 * (acc[q][r] - tm - hat[q][r] * tx);
+    if (h == 0) {
 #pragma unroll
-    for (int k = 0; k < 6; ++k) gaev[nn * kE + g + 4 * k] = ga[k];
+      for (int k = 0; k < 6; ++k) gaev[nn * kE + g + 4 * k] = ga[k];
+    }
   }
 }
 
@@ -2879,7 +2739,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     // the post-attention node chain in one kernel (MLP, interaction, LayerNorm 2, ev gate)
     const NodeChainArgs NC{B.m1p, B.m1bp, B.m2p, B.m2bp, B.intp, B.intbp, B.int_cg, B.ln2w, B.ln2b, hw_.exp2_64,
                            ln_eps_};
-    hipLaunchKernelGGL(k_node_fwd2, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), act, n1b, aevb, NC, hpb, tb,
+    hipLaunchKernelGGL(k_node_fwd, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), act, n1b, aevb, NC, hpb, tb,
                        xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);
   }
 
@@ -2930,8 +2790,8 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     // the post-attention node chain in reverse in one kernel: gainv, gaev
     const NodeChainBwdArgs NB{B.inttp, B.m2tp, B.m1tp, B.int_cg, B.ln1w, B.ln2w};
-    hipLaunchKernelGGL(k_node_bwd, dim3(gN64), dim3(256), 0, s, int(N), gx, gev, tb, aevb, p2h, p2i, hpb, n1b, n1hb,
-                       n1ib, NB, gainv, gaev);
+    hipLaunchKernelGGL(k_node_bwd, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), gx, gev, tb, aevb, p2h,
+                       p2i, hpb, n1b, n1hb, n1ib, NB, gainv, gaev);
     const bool blk0 = b == 0 && !naive_filters_;
     timed(b == 0 ? "attn_bwd_block0" : "attn_bwd", 1, [&] {
       if (b > 0)
