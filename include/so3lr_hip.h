@@ -58,8 +58,8 @@ int so3lr_create(const char *model_path, int device, so3lr_ctx **out);
 /* Release all device and host resources. */
 void so3lr_destroy(so3lr_ctx *ctx);
 
-/* Message of the last failure on this context (or of the last failed
- * so3lr_create when ctx is NULL). */
+/* Message of the last failure on this context (or, when ctx is NULL, of the
+ * calling thread's last failed so3lr_create or so3lr_check_system). */
 const char *so3lr_last_error(const so3lr_ctx *ctx);
 
 /* Short-range (which = 0) or long-range (which = 1) model cutoff in Angstrom;
@@ -69,6 +69,16 @@ double so3lr_cutoff(const so3lr_ctx *ctx, int which);
 /* Element token (symbol in any case, or atomic number) -> Z in 1..99, 0 when
  * unknown.  Same rule as plugins/lammps/so3lr_element_map.h:15-49. */
 int so3lr_atomic_number(const char *token);
+
+/*
+ * (Q, M) check of one composition, host only: no context and no device.
+ * Returns SO3LR_OK, SO3LR_ERR_ARGUMENT (no atoms, Z outside 1..99) or
+ * SO3LR_ERR_SYSTEM, with the reason in so3lr_last_error(NULL).  The rule of
+ * charge_multiplicity_problem (src/so3lr_charge_spin.cpp:100-141), which
+ * PairSO3LRTurbo::init_style runs for each image on its own rank
+ * (plugins/lammps/pair_so3lr_turbo.cpp:208-219).
+ */
+int so3lr_check_system(int64_t n, const int32_t *z, double total_charge, double multiplicity);
 
 /*
  * Owned atoms of the system: atomic numbers and the global (Q, M).  Validates

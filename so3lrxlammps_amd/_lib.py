@@ -19,7 +19,7 @@ LIST_FULL, LIST_HALF = 0, 1
 
 # every symbol include/so3lr_hip.h declares
 HIP_SYMBOLS = ["so3lr_create", "so3lr_destroy", "so3lr_last_error", "so3lr_cutoff",
-               "so3lr_atomic_number", "so3lr_set_system", "so3lr_set_images",
+               "so3lr_atomic_number", "so3lr_check_system", "so3lr_set_system", "so3lr_set_images",
                "so3lr_set_topology", "so3lr_compute", "so3lr_compute_device",
                "so3lr_reneighbor_device", "so3lr_set_box",
                "so3lr_set_stream", "so3lr_last_terms", "so3lr_graph_stats",
@@ -76,6 +76,7 @@ def hip():
         lib.so3lr_cutoff.argtypes = [_P, ctypes.c_int]
         lib.so3lr_cutoff.restype = _D
         lib.so3lr_atomic_number.argtypes = [ctypes.c_char_p]
+        lib.so3lr_check_system.argtypes = [_I64, _P, _D, _D]
         lib.so3lr_set_system.argtypes = [_P, _I64, _P, _D, _D]
         lib.so3lr_set_images.argtypes = [_P, _I64, _P, _I64, _P, _P, _P]
         lib.so3lr_set_topology.argtypes = [_P, _I64, _P, ctypes.c_int, _I64, _P, _P, _P, _I64, _P, _P, _P]

@@ -95,6 +95,28 @@ double so3lr_cutoff(const so3lr_ctx *ctx, int which) {
 
 int so3lr_atomic_number(const char *token) { return so3lr_amd::atomic_number_from_token(token); }
 
+int so3lr_check_system(int64_t n, const int32_t *z, double total_charge, double multiplicity) {
+  if (n <= 0 || !z) {
+    g_create_error = "SO3LR: empty system";
+    return SO3LR_ERR_ARGUMENT;
+  }
+  std::int64_t counts[119] = {0};
+  for (int64_t i = 0; i < n; ++i) {
+    if (z[i] < 1 || z[i] > 99) {
+      g_create_error = "SO3LR: atomic numbers must lie in 1..99";
+      return SO3LR_ERR_ARGUMENT;
+    }
+    ++counts[z[i]];
+  }
+  const std::string why = so3lr_amd::charge_multiplicity_problem(counts, total_charge, multiplicity);
+  if (!why.empty()) {
+    g_create_error = why;
+    return SO3LR_ERR_SYSTEM;
+  }
+  g_create_error.clear();
+  return SO3LR_OK;
+}
+
 int so3lr_set_system(so3lr_ctx *ctx, int64_t n_owned, const int32_t *z, double total_charge,
                      double multiplicity) {
   return guarded(ctx, [&] {
