@@ -14,10 +14,10 @@
  * Communicators cross this ABI as Fortran handles (MPI_Comm_c2f), so the
  * header needs no mpi.h.  The library is built against MPICH (libmpi.so.12).
  * Status codes and flags are those of so3lr_hip.h.  Every function except
- * so3lr_turbo_destroy, so3lr_turbo_last_error, so3lr_turbo_info and
- * so3lr_turbo_stats is collective over the communicator and returns the same
- * status on every rank, so that one image's problem stops every image rather
- * than leaving the others waiting.
+ * so3lr_turbo_last_error, so3lr_turbo_info and so3lr_turbo_stats is
+ * collective over the communicator, and the calls that can fail return the
+ * same status on every rank, so that one image's problem stops every image
+ * rather than leaving the others waiting.
  */
 #ifndef SO3LR_TURBO_H
 #define SO3LR_TURBO_H
@@ -62,7 +62,8 @@ int so3lr_turbo_check_images(int64_t comm_f, int64_t n, const int32_t *z, double
 int so3lr_turbo_create(int64_t comm_f, int coordinator, const char *model_path, int device,
                        so3lr_turbo **out);
 
-/* Release the broker (not collective; the coordinator's context goes with it). */
+/* Release the broker and the coordinator's context.  It frees the broker's
+ * duplicate of the communicator: call it on every rank, before MPI_Finalize. */
 void so3lr_turbo_destroy(so3lr_turbo *t);
 
 /* Message of the last failure on this broker (NULL: of the calling thread's
@@ -82,8 +83,8 @@ int so3lr_turbo_info(const so3lr_turbo *t, int *rank, int *size, int *coordinato
  *     partition has no ghost rows);
  *   total_charge, multiplicity: the image's (Q, M);
  *   lists_changed: nonzero when the lists differ from the previous call's
- *     (LAMMPS neighbor->ago == 0); the lists are gathered only on calls where
- *     some image sets it, and on the first call;
+ *     (LAMMPS neighbor->ago == 0); an image sends its lists only then, on its
+ *     first call, when its atom count changed, and after a failed call;
  *   SR list (sr_kind SO3LR_LIST_FULL as the style requests it, or
  *     SO3LR_LIST_HALF) and LR half list, CSR over receivers as in
  *     so3lr_set_topology, with NEIGHMASK already applied; every row index
@@ -108,9 +109,12 @@ int so3lr_turbo_evaluate(so3lr_turbo *t, int64_t n, const int32_t *z, const doub
 /*
  * Figures of the last evaluation on this rank (measurement, no counterpart in
  * the reference beyond its broker_ms report, pair_so3lr_turbo.cpp:281-312):
- * packed atoms and images (coordinator; 0 elsewhere), whether the lists were
- * gathered, and milliseconds spent gathering, evaluating on the GPU
- * (coordinator; 0 elsewhere), scattering, and in the whole call.
+ * packed atoms and images (coordinator; 0 elsewhere); lists_gathered: on the
+ * coordinator whether any image's lists arrived, on a worker whether this
+ * image sent its own; milliseconds: on the coordinator receiving every image
+ * (which includes waiting for the slowest), the packed GPU evaluation and
+ * sending the answers; on a worker the wait for its answer (as gather_ms);
+ * and the whole call.
  */
 int so3lr_turbo_stats(const so3lr_turbo *t, int64_t *packed_atoms, int64_t *images, int *lists_gathered,
                       double *gather_ms, double *evaluate_ms, double *scatter_ms, double *total_ms);
