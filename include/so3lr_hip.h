@@ -39,7 +39,8 @@ extern "C" {
 #define SO3LR_ENERGY 1
 #define SO3LR_EATOM 2
 #define SO3LR_VIRIAL 4
-#define SO3LR_VATOM 8 /* refused, as in pair_so3lr_native_mpi.cpp:1248-1251 */
+#define SO3LR_VATOM 8 /* accepted; values from so3lr_last_vatom (the reference refuses
+                         per-atom virial, pair_so3lr_native_mpi.cpp:1248-1251) */
 
 /* neighbour-list kinds accepted for the short-range list */
 #define SO3LR_LIST_FULL 0 /* LAMMPS full list (the reference's SR request) */
@@ -181,6 +182,19 @@ int so3lr_set_stream(so3lr_ctx *ctx, void *stream);
 int so3lr_last_terms(so3lr_ctx *ctx, double *learned, double *zbl, double *long_range,
                      double *charges, double *hirshfeld, double *totals,
                      double *image_energy);
+
+/*
+ * Per-atom virial of the last evaluation (no counterpart in the reference,
+ * which refuses vflag_atom, pair_so3lr_native_mpi.cpp:1248-1251): vatom[6 * i
+ * + c] for owned atom i, LAMMPS order xx yy zz xy xz yz.  Each pair's
+ * -v (x) dE/dv (short range: the pair vector and its energy gradient, which
+ * carries the whole network's dependence on that pair; long range: the
+ * Coulomb and dispersion pair force), symmetrised as in the global virial,
+ * goes half to each endpoint; the atoms' sum is the global virial.
+ * on_device = 0: vatom is host memory; 1: device memory, written on the
+ * context's stream.  The pair style adds it into vatom of its owned rows.
+ */
+int so3lr_last_vatom(so3lr_ctx *ctx, double *vatom, int on_device);
 
 /* Number of short-range pairs inside the cutoff at the last evaluation, and
  * the candidate counts of the current topology (SR pairs, LR pairs). */

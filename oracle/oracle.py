@@ -97,7 +97,7 @@ class _Model(ctypes.Structure):
 class _Out(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in
                 ("e_learned", "e_zbl", "e_lr", "charges", "hirshfeld", "forces", "virial",
-                 "image_energy")] + [
+                 "image_energy", "vatom")] + [
                 ("e_elec_total", ctypes.c_double), ("e_disp_total", ctypes.c_double),
                 ("e_total", ctypes.c_double)]
 
@@ -207,6 +207,7 @@ class Oracle:
         outs = {k: np.zeros(n) for k in ("e_learned", "e_zbl", "e_lr", "charges", "hirshfeld")}
         outs["forces"] = np.zeros((n, 3))
         outs["virial"] = np.zeros(6)
+        outs["vatom"] = np.zeros((n, 6))
         outs["image_energy"] = np.zeros(n_images)
         o = _Out()
         for k, v in outs.items():

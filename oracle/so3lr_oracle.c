@@ -879,6 +879,29 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     }
   }
   if (out->virial) memcpy(out->virial, W, sizeof(W));
+  if (out->vatom) {
+    /* the same terms as W, half to each endpoint of the edge or pair */
+    memset(out->vatom, 0, sizeof(double) * 6 * (size_t)n);
+    for (int64_t e = 0; e < ne; ++e) {
+      const double *v = vec + 3 * e, *g = ge + 3 * e;
+      const double w[6] = {-v[0] * g[0], -v[1] * g[1], -v[2] * g[2], -0.5 * (v[0] * g[1] + v[1] * g[0]),
+                           -0.5 * (v[0] * g[2] + v[2] * g[0]), -0.5 * (v[1] * g[2] + v[2] * g[1])};
+      for (int c = 0; c < 6; ++c) {
+        out->vatom[6 * snd[e] + c] += 0.5 * w[c];
+        out->vatom[6 * rcv[e] + c] += 0.5 * w[c];
+      }
+    }
+    for (int64_t p = 0; p < np; ++p) {
+      if (!lrp[p].valid) continue;
+      const double *v = pvec + 3 * p, *g = lr_pf + 3 * p;
+      const double w[6] = {-v[0] * g[0], -v[1] * g[1], -v[2] * g[2], -0.5 * (v[0] * g[1] + v[1] * g[0]),
+                           -0.5 * (v[0] * g[2] + v[2] * g[0]), -0.5 * (v[1] * g[2] + v[2] * g[1])};
+      for (int c = 0; c < 6; ++c) {
+        out->vatom[6 * pi[p] + c] += 0.5 * w[c];
+        out->vatom[6 * pj[p] + c] += 0.5 * w[c];
+      }
+    }
+  }
   out->e_elec_total = elec_total;
   out->e_disp_total = disp_total;
   out->e_total = etot;

@@ -107,6 +107,10 @@ typedef struct {
   double *forces;      /* n*3, total force -dE/dx */
   double *virial;      /* 6: xx yy zz xy xz yz (-sum v (x) dE/dv, symmetrised) */
   double *image_energy;/* n_images: per-image total energy (packed mode) */
+  double *vatom;       /* n*6 per-atom virial: each edge's and LR pair's
+                          -v (x) dE/dv (symmetrised, as virial) split half to
+                          each endpoint; sums to virial.  The reference has no
+                          per-atom virial (pair_so3lr_native_mpi.cpp:1248-1251). */
   double e_elec_total; /* sum of electrostatic pair energies */
   double e_disp_total; /* sum of dispersion pair energies */
   double e_total;      /* sum of all per-node energies */

@@ -22,7 +22,7 @@ HIP_SYMBOLS = ["so3lr_create", "so3lr_destroy", "so3lr_last_error", "so3lr_cutof
                "so3lr_atomic_number", "so3lr_check_system", "so3lr_set_system", "so3lr_set_images",
                "so3lr_set_topology", "so3lr_compute", "so3lr_compute_device",
                "so3lr_reneighbor_device", "so3lr_set_box",
-               "so3lr_set_stream", "so3lr_last_terms", "so3lr_graph_stats",
+               "so3lr_set_stream", "so3lr_last_terms", "so3lr_last_vatom", "so3lr_graph_stats",
                "so3lr_kernel_timing", "so3lr_kernel_timing_read", "so3lr_device_bytes"]
 EMU_SYMBOLS = ["so3lr_emu_build", "so3lr_emu_error", "so3lr_emu_free", "so3lr_emu_rows",
                "so3lr_emu_owner", "so3lr_emu_image", "so3lr_emu_inum", "so3lr_emu_ilist",
@@ -86,6 +86,7 @@ def hip():
         lib.so3lr_reneighbor_device.argtypes = [_P, _P, _P, _P, _P, _D]
         lib.so3lr_set_box.argtypes = [_P, _P, _P]
         lib.so3lr_last_terms.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P]
+        lib.so3lr_last_vatom.argtypes = [_P, _P, ctypes.c_int]
         lib.so3lr_graph_stats.argtypes = [_P, _P, _P, _P]
         lib.so3lr_kernel_timing.argtypes = [_P, ctypes.c_int]
         lib.so3lr_kernel_timing_read.argtypes = [_P, ctypes.c_char_p, _P, _P, _P]
@@ -269,6 +270,16 @@ class Context:
         out["electrostatic_total"], out["dispersion_total"] = tot
         out["image_energy"] = img
         return out
+
+    def vatom(self, out=None):
+        """Per-atom virial of the last evaluation, (n, 6) in LAMMPS order; `out`
+        may be a device tensor (written on the context's stream)."""
+        if out is not None and hasattr(out, "data_ptr") and getattr(out, "is_cuda", False):
+            self._check(self._lib.so3lr_last_vatom(self._h, ptr(out), 1))
+            return out
+        w = np.zeros((self.n, 6))
+        self._check(self._lib.so3lr_last_vatom(self._h, ptr(w), 0))
+        return w
 
     def graph_stats(self):
         a, b, c = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()

@@ -151,17 +151,14 @@ int so3lr_set_topology(so3lr_ctx *ctx, int64_t n_rows, const int32_t *owner, int
 }
 
 static int check_flags(int flags) {
-  if (flags & SO3LR_VATOM) return SO3LR_ERR_UNSUPPORTED;
-  if (flags & ~(SO3LR_ENERGY | SO3LR_EATOM | SO3LR_VIRIAL)) return SO3LR_ERR_ARGUMENT;
+  if (flags & ~(SO3LR_ENERGY | SO3LR_EATOM | SO3LR_VIRIAL | SO3LR_VATOM)) return SO3LR_ERR_ARGUMENT;
   return SO3LR_OK;
 }
 
 int so3lr_compute(so3lr_ctx *ctx, const double *x_rows, int flags, double *f, double *eatom,
                   double *energy, double *virial) {
   if (ctx && check_flags(flags) != SO3LR_OK) {
-    ctx->error = (flags & SO3LR_VATOM)
-                     ? "Pair style so3lr/native/mpi does not support per-atom virial"
-                     : "SO3LR: unknown compute flags";
+    ctx->error = "SO3LR: unknown compute flags";
     return check_flags(flags);
   }
   return guarded(ctx, [&] {
@@ -176,9 +173,7 @@ int so3lr_compute(so3lr_ctx *ctx, const double *x_rows, int flags, double *f, do
 int so3lr_compute_device(so3lr_ctx *ctx, const double *x_rows_dev, int flags, double *f_dev,
                          double *eatom_dev, double *energy, double *virial) {
   if (ctx && check_flags(flags) != SO3LR_OK) {
-    ctx->error = (flags & SO3LR_VATOM)
-                     ? "Pair style so3lr/native/mpi does not support per-atom virial"
-                     : "SO3LR: unknown compute flags";
+    ctx->error = "SO3LR: unknown compute flags";
     return check_flags(flags);
   }
   return guarded(ctx, [&] {
@@ -212,6 +207,13 @@ int so3lr_set_stream(so3lr_ctx *ctx, void *stream) {
 int so3lr_last_terms(so3lr_ctx *ctx, double *learned, double *zbl, double *lr, double *charges,
                      double *hirshfeld, double *totals, double *image_energy) {
   return guarded(ctx, [&] { ctx->ev->last_terms(learned, zbl, lr, charges, hirshfeld, totals, image_energy); });
+}
+
+int so3lr_last_vatom(so3lr_ctx *ctx, double *vatom, int on_device) {
+  return guarded(ctx, [&] {
+    if (!vatom) throw std::invalid_argument("SO3LR: per-atom virial requested without a buffer");
+    ctx->ev->last_vatom(vatom, on_device != 0);
+  });
 }
 
 int so3lr_graph_stats(const so3lr_ctx *ctx, int64_t *sr_active, int64_t *sr_cand, int64_t *lr_cand) {

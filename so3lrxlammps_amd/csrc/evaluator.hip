@@ -1990,6 +1990,37 @@ __global__ __launch_bounds__(256) void k_forces(int N, const int *inc_off, const
   }
 }
 
+// Per-atom virial (no counterpart in the reference, which refuses it): each
+// active SR pair's -v (x) dE/dv, symmetrised as in the global virial, split
+// half to each endpoint, plus the node's long-range halves.  The atoms' sum is
+// the global virial.  Node-major over the incidence lists, fixed order.
+__global__ __launch_bounds__(256) void k_vatom(int N, const int *inc_off, const int *inc, const int *cand2act,
+                                               const double *pv, const double *pg, const double *vlr,
+                                               const int *perm, double *vatom) {
+  const int lane = threadIdx.x & 63;
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  double w[6] = {0, 0, 0, 0, 0, 0};
+  for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
+    const int p = cand2act[inc[k] >> 1];
+    if (p < 0) continue;
+    const double *v = pv + 3 * std::size_t(p), *g = pg + 3 * std::size_t(p);
+    w[0] -= 0.5 * v[0] * g[0];
+    w[1] -= 0.5 * v[1] * g[1];
+    w[2] -= 0.5 * v[2] * g[2];
+    w[3] -= 0.25 * (v[0] * g[1] + v[1] * g[0]);
+    w[4] -= 0.25 * (v[0] * g[2] + v[2] * g[0]);
+    w[5] -= 0.25 * (v[1] * g[2] + v[2] * g[1]);
+  }
+#pragma unroll
+  for (int c = 0; c < 6; ++c) w[c] = wave_sum(w[c]);
+  if (lane == 0) {
+    const int a = perm ? perm[n] : n;
+#pragma unroll
+    for (int c = 0; c < 6; ++c) vatom[6 * std::size_t(a) + c] = w[c] + vlr[6 * std::size_t(n) + c];
+  }
+}
+
 // energy, virial (SR pairs + LR per-node halves), electrostatic and dispersion
 // totals: red[0] E, red[1..6] W, red[7] E_el, red[8] E_disp.  One block.
 // Energy, virial and energy parts: fixed-order two-stage reduction.  Block b
@@ -2362,7 +2393,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   pv_ = buf("pv"); pr_ = buf("pr"); pY_ = buf("pY"); pfc_ = buf("pfc"); pzbl_ = buf("pzbl");
   ps_ = buf("ps"); pf_ = buf("pf"); palpha_ = buf("palpha"); df_ = buf("df"); dfc_ = buf("dfc");
   ds_ = buf("ds"); dr_ = buf("dr"); dY_ = buf("dY"); pg_ = buf("pg"); xrows_ = buf("xrows");
-  fhost_ = buf("fhost");
+  fhost_ = buf("fhost"); vatom_ = buf("vatom");
   nb_key_ = buf("nb_key"); nb_idx_ = buf("nb_idx"); nb_skey_ = buf("nb_skey"); nb_sidx_ = buf("nb_sidx");
   nb_cstart_ = buf("nb_cstart"); nb_tmp_ = buf("nb_tmp"); nb_srcnt_ = buf("nb_srcnt"); nb_lrcnt_ = buf("nb_lrcnt");
   nb_err_ = buf("nb_err"); nb_srlist_ = buf("nb_srlist"); nb_poff_ = buf("nb_poff"); sr_code_ = buf("sr_code");
@@ -2880,6 +2911,21 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   last_etot_ = etot;
   evaluated_ = true;
   (void)flags;
+}
+
+void Evaluator::last_vatom(double *out, bool on_device) {
+  if (!evaluated_) throw std::logic_error("SO3LR: no evaluation yet");
+  const std::int64_t N = n_;
+  const std::size_t Nz = std::size_t(N), Pz = std::size_t(std::max<std::int64_t>(p_sr_, 1));
+  double *dst = on_device ? out : ensure<double>(vatom_, Nz * 6);
+  const int *perm = permuted_ ? static_cast<const int *>(perm_->p) : nullptr;
+  hipLaunchKernelGGL(k_vatom, dim3(ceil_div(N, 4)), dim3(256), 0, stream_, int(N),
+                     static_cast<const int *>(sr_inc_off_->p), static_cast<const int *>(sr_inc_->p),
+                     ensure<int>(cand2act_, Pz), ensure<double>(pv_, 3 * Pz), ensure<double>(pg_, 3 * Pz),
+                     ensure<double>(vlr_, Nz * 6), perm, dst);
+  HIP_CHECK(hipGetLastError());
+  if (!on_device) HIP_CHECK(hipMemcpyAsync(out, dst, Nz * 6 * sizeof(double), hipMemcpyDeviceToHost, stream_));
+  HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 bool Evaluator::timing_read(const std::string &kernel, double &total_ms, std::int64_t &launches,

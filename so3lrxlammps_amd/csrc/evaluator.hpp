@@ -91,6 +91,9 @@ class Evaluator {
                     double *virial);
   void last_terms(double *learned, double *zbl, double *lr, double *charges, double *hirshfeld,
                   double *totals, double *image_energy);
+  // Per-atom virial of the last evaluation (n_owned x 6, atom order), to host
+  // or device memory.
+  void last_vatom(double *out, bool on_device);
   // HBM-resident reneighbor from owned positions (wrapped in place); after it,
   // compute_device takes owned positions.  Orthogonal box [lo, hi).
   void build_topology_device(double *x_owned, const double lo[3], const double hi[3], const int per[3],
@@ -172,7 +175,7 @@ class Evaluator {
   Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
   Buffer *df_, *dfc_, *ds_, *dr_, *dY_, *pg_;
   Buffer *iact_, *iother_;  // per step: incidence entry -> active pair * 2 + side, partner node
-  Buffer *xrows_, *fhost_;
+  Buffer *xrows_, *fhost_, *vatom_;
   // device reneighbor
   Buffer *nb_key_, *nb_idx_, *nb_skey_, *nb_sidx_, *nb_cstart_, *nb_tmp_, *nb_srcnt_, *nb_lrcnt_, *nb_err_,
       *nb_srlist_, *nb_poff_, *sr_code_;

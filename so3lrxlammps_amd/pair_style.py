@@ -134,13 +134,15 @@ class PairSO3LRNativeMPI:
 
     # -- compute(eflag, vflag) (:1246-1978)
     def compute(self, atoms, eflag=True, vflag=True, eflag_atom=False, vflag_atom=False):
-        if vflag_atom:
-            raise LammpsError("Pair style so3lr/native/mpi does not support per-atom virial")
         self._neighbor(atoms)
         x_rows = self._lists.rows_positions(np.asarray(atoms.x, dtype=np.float64))
         try:
             energy, forces, eatom, virial = self.ctx.compute(x_rows, eatom=True)
         except _lib.SO3LRError as exc:
             raise LammpsError("SO3LR MPI-native LAMMPS evaluation failed: %s" % exc) from exc
+        # per-atom virial: an addition (the reference refuses vflag_atom,
+        # pair_so3lr_native_mpi.cpp:1248-1251)
+        vatom = self.ctx.vatom() if vflag_atom else None
         return {"energy": energy if eflag else None, "forces": forces,
-                "eatom": eatom if eflag_atom else None, "virial": virial if vflag else None}
+                "eatom": eatom if eflag_atom else None, "virial": virial if vflag else None,
+                "vatom": vatom}

@@ -125,11 +125,74 @@ def test_refusals(ctx):
     e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, 0, 3)
     x = np.zeros(6)
     fbuf = np.zeros(6)
-    rc = ctx.raw_compute(_lib.ptr(x), _lib.VATOM, _lib.ptr(fbuf), None, None, None)
-    assert rc == _lib.ERR_UNSUPPORTED
+    rc = ctx.raw_compute(_lib.ptr(x), 16, _lib.ptr(fbuf), None, None, None)  # an unknown flag bit
+    assert rc == _lib.ERR_ARGUMENT
     with pytest.raises(_lib.SO3LRError) as err:
         ctx.set_system(z, 0, 2)  # O2 has 16 electrons: an even count needs an odd multiplicity
     assert err.value.code == _lib.ERR_SYSTEM
+
+
+def test_per_atom_virial_matches_oracle(ctx, orc):
+    """so3lr_last_vatom (no counterpart in the reference) against the oracle's
+    per-atom virial, at the virial's bar (1e-9 of its scale), on a dimer, a
+    molecule, periodic water (rows path, and the device path into device
+    memory) and packed images; the atoms' sum is the returned global virial."""
+    import torch
+    from so3lrxlammps_amd import Context, Lists, _lib
+    for name, q, m in (("o2", 0, 3), ("acetate", -1, 1)):
+        ref, z, pos, box = support.load_golden(name)
+        e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, q, m)
+        va = ctx.vatom()
+        out = orc.evaluate(z, *support.build_graphs(pos, box), charge=q, multiplicity=m)
+        scale = max(1.0, np.abs(out["vatom"]).max())
+        assert np.abs(va - out["vatom"]).max() <= 1e-9 * scale, name
+        assert np.abs(va.sum(0) - w).max() <= 1e-12 * max(1.0, np.abs(w).max()), name
+    ref, z, pos, box = support.load_golden("water3000")
+    e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, 0, 1)
+    va = ctx.vatom()
+    out = orc.evaluate(z, *support.build_graphs(pos, box))
+    scale = max(1.0, np.abs(out["vatom"]).max())
+    assert np.abs(va - out["vatom"]).max() <= 1e-9 * scale
+    assert np.abs(va.sum(0) - w).max() <= 1e-10 * np.abs(w).max()
+    # the device path: spatial node order inside, atom order out, device memory
+    c = Context(support.MODEL, 0)
+    c.set_system(z, 0, 1)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        xt = torch.tensor(pos, dtype=torch.float64, device=dev)
+        ft = torch.zeros_like(xt)
+        vt = torch.zeros((len(z), 6), dtype=torch.float64, device=dev)
+        c.reneighbor_device(xt, np.zeros(3), box, (1, 1, 1), 1.0, stream=stream.cuda_stream)
+        e2, w2 = c.compute_device(xt, ft, stream=stream.cuda_stream)
+        c.vatom(vt)
+        stream.synchronize()
+        va2 = vt.cpu().numpy()
+    assert np.abs(va2 - out["vatom"]).max() <= 1e-9 * scale
+    c.close()
+    # packed images
+    names = [("acetate", -1, 1), ("methyl", 0, 2), ("h2o_cation", 1, 2)]
+    zs, ps, qs, ms, offs = [], [], [], [], [0]
+    for k, (name, q, m) in enumerate(names):
+        ref, zk, pk, _ = support.load_golden(name)
+        zs.append(zk); ps.append(pk + np.array([40.0 * k, 0, 0])); qs.append(q); ms.append(m)
+        offs.append(offs[-1] + len(zk))
+    zp = np.concatenate(zs); pp = np.concatenate(ps)
+    cp = Context(support.MODEL, 0)
+    cp.set_images(zp, offs, qs, ms)
+    lists = Lists(pp, pp.min(0) - 20, pp.max(0) + 20, (0, 0, 0))
+    cp.set_topology(lists)
+    # the buffers stay referenced for the whole call
+    xr = np.ascontiguousarray(lists.rows_positions(pp))
+    fr, er = np.zeros((len(zp), 3)), np.zeros(1)
+    rc = cp.raw_compute(_lib.ptr(xr), _lib.ENERGY | _lib.VATOM, _lib.ptr(fr), None, _lib.ptr(er), None)
+    assert rc == _lib.OK
+    vap = cp.vatom()
+    img = np.repeat(np.arange(len(names)), np.diff(offs))
+    outp = orc.evaluate(zp, *support.build_graphs(pp, None), image=img, image_charge=np.array(qs, float),
+                        image_multiplicity=ms)
+    assert np.abs(vap - outp["vatom"]).max() <= 1e-9 * max(1.0, np.abs(outp["vatom"]).max())
+    cp.close()
 
 
 def test_device_reneighbor_matches_rows_path(orc):

@@ -9,7 +9,9 @@ finite differences of the energy and symmetry invariants.
 * virial: finite differences of E under homogeneous strain of every edge and
   pair vector (pins the sign, the symmetrisation and the LR half-pair term);
 * rotation / translation invariance and zero net torque (pins equivariance);
-* charge/spin: the table is exactly zero for Q=0, M=1, and (Q, M) parity rules.
+* charge/spin: the table is exactly zero for Q=0, M=1, and (Q, M) parity rules;
+* per-atom virial: sum rule against the virial, dimer symmetry, permutation,
+  shift, and the f.r identity of an isolated molecule.
 """
 import numpy as np
 import pytest
@@ -171,3 +173,37 @@ def test_packed_images_match_single(orc):
         assert abs(out["image_energy"][k] - s["energy"]) < 1e-10
         assert np.abs(out["forces"][start:start + n] - s["forces"]).max() < 1e-12
         start += n
+
+
+def test_per_atom_virial(orc):
+    """Per-atom virial (an addition: the reference refuses vflag_atom).  Each
+    edge's and LR pair's -v (x) dE/dv goes half to each endpoint.  Pins: the
+    atoms' sum is the global virial, itself pinned by the strain finite
+    differences above (a dropped term, a wrong weight or a missing LR part
+    breaks it); the two atoms of a dimer get equal shares (a term given to one
+    endpoint only breaks it, since the two directed edges carry different
+    gradients); permuting the atoms permutes the rows; a rigid shift changes
+    nothing; for an isolated molecule the sum equals sym(sum_i x_i (x) f_i)."""
+    z, pos, box = _small_periodic()
+    sr, lr = support.build_graphs(pos, box)
+    out = orc.evaluate(z, sr, lr)
+    assert np.abs(out["vatom"].sum(0) - out["virial"]).max() < 1e-12 * np.abs(out["virial"]).max()
+
+    ref, z2, p2 = _molecule("o2")
+    o2 = _energy(orc, z2, p2, 0, 3)
+    assert np.abs(o2["vatom"][0] - o2["vatom"][1]).max() <= 1e-15 * np.abs(o2["vatom"]).max()
+    assert np.abs(o2["vatom"].sum(0) - o2["virial"]).max() < 1e-13 * max(1.0, np.abs(o2["virial"]).max())
+
+    ref, z3, p3 = _molecule("acetate")
+    base = _energy(orc, z3, p3, -1, 1)
+    perm = np.random.default_rng(6).permutation(len(z3))
+    out3 = _energy(orc, z3[perm], p3[perm], -1, 1)
+    assert np.abs(out3["vatom"] - base["vatom"][perm]).max() < 1e-11
+    shifted = _energy(orc, z3, p3 + np.array([5.0, -3.0, 2.5]), -1, 1)
+    assert np.abs(shifted["vatom"] - base["vatom"]).max() < 1e-11
+    x, f = p3, base["forces"]
+    fdotr = np.array([(x[:, 0] * f[:, 0]).sum(), (x[:, 1] * f[:, 1]).sum(), (x[:, 2] * f[:, 2]).sum(),
+                      0.5 * (x[:, 0] * f[:, 1] + x[:, 1] * f[:, 0]).sum(),
+                      0.5 * (x[:, 0] * f[:, 2] + x[:, 2] * f[:, 0]).sum(),
+                      0.5 * (x[:, 1] * f[:, 2] + x[:, 2] * f[:, 1]).sum()])
+    assert np.abs(base["vatom"].sum(0) - fdotr).max() < 1e-9
