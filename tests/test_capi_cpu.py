@@ -103,6 +103,11 @@ def test_missing_file_rejected():
     ("interaction_blocks", 9, "interaction_blocks"),
     ("brand_new_operator", 1, "unknown architecture key"),
     ("repulsion_type", "nlh", "repulsion other than learned ZBL"),
+    ("use_residual_scalars", True, "residual scalars"),
+    ("radial_basis_features", 64, "radial_basis_features"),
+    ("output_heads", ["atomic_energy_output_block", "partial_charges_output_block", "hirshfeld_output_block",
+                      "c6_ratios_output_block"], "output heads other than"),
+    ("layer_norm_epsilon", 1e-5, "LayerNorm epsilon"),
 ])
 def test_capability_refusal_names_the_feature(tmp_path, key, value, feature):
     """Structurally valid mutated models (re-serialised manifest, recomputed
