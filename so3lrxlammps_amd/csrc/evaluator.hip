@@ -401,42 +401,47 @@ struct FilterMfma {
   const double *e0pk[2];                                // spherical layer 0: one v4d per lane {tile 0, tile 1, 0, 0}
   const double *att_cg;
   const double *rbf_b, *rbf_k, *rbf_kr;
-  const double *exp2_64;  // 2^(j/64), j < 64
+  const double *exp2_256;  // 2^(j/256), j < 256
   double gamma;
 };
 
 // Activations of the MFMA filter kernels.  On gfx950 every VALU instruction a
 // wavefront issues takes issue time from the fp64 MFMAs of its SIMD, so these
-// are written for the fewest instructions at full fp64 accuracy (a few ulp):
-// e^x = 2^m 2^(j/64) e^r with x = (64 m + j) ln2/64 + r, |r| <= ln2/128
-// (Cody-Waite, ln2/64 split into a 20-bit high part and a low part), 2^(j/64)
-// from a 64-entry table in LDS and the degree-5 Taylor polynomial of e^r
+// are written for the fewest instructions: e^x = 2^m 2^(j/256) e^r with
+// x = (256 m + j) ln2/256 + r, |r| <= ln2/512 (Cody-Waite, ln2/256 split into
+// a 32-bit high part and a low part: exact reduction for |x| < 2800), 2^(j/256)
+// from a 256-entry table in LDS and the degree-4 Taylor polynomial of e^r
 // (truncation < 4e-17 relative).  The power 2^m is capped at 2^1000, which
-// only matters for x > 693; valid for |x| < 1e6.
+// only matters for x > 693.
 __device__ __forceinline__ double exp_tab(double x, const double *tab) {
-  const double n = __builtin_rint(x * 92.332482616893656768);  // 64 / ln2
-  double r = fma(n, -0.010830417275428772, x);
-  r = fma(n, -7.420820373486988e-09, r);
+  const double n = __builtin_rint(x * 369.3299304675746);  // 256 / ln2
+  double r = fma(n, -0.00270760617331689, x);
+  r = fma(n, -7.453964567463233e-13, r);
   const int k = int(n);
-  double p = 1.0 / 120.0;
-  p = fma(p, r, 1.0 / 24.0);
+  double p = 1.0 / 24.0;
   p = fma(p, r, 1.0 / 6.0);
   p = fma(p, r, 0.5);
   p = fma(p, r, 1.0);
   p = fma(p, r, 1.0);
-  return __builtin_ldexp(p * tab[k & 63], min(k >> 6, 1000));
+  return __builtin_ldexp(p * tab[k & 255], min(k >> 8, 1000));
+}
+// 1 / d from the hardware estimate (2^-24) and one Newton step: 2e-15
+// relative, ample inside the activations
+__device__ __forceinline__ double rcp_act(double d) {
+  const double r = __builtin_amdgcn_rcp(d);
+  return fma(fma(-d, r, 1.0), r, r);
 }
 __device__ __forceinline__ double silu_tab(double x, const double *tab) {
-  return x * rcp_lean(1.0 + exp_tab(-x, tab));
+  return x * rcp_act(1.0 + exp_tab(-x, tab));
 }
 __device__ __forceinline__ double silu_prime_tab(double x, const double *tab) {
-  const double s = rcp_lean(1.0 + exp_tab(-x, tab));
+  const double s = rcp_act(1.0 + exp_tab(-x, tab));
   return s * (1.0 + x * (1.0 - s));
 }
 // The table into LDS: call at kernel start, before any wavefront returns.
 #define SO3LR_EXP2_TABLE(A)                                               \
-  __shared__ double exp2_lds[64];                                         \
-  if (threadIdx.x < 64) exp2_lds[threadIdx.x] = (A).exp2_64[threadIdx.x]; \
+  __shared__ double exp2_lds[256];                                        \
+  if (threadIdx.x < 256) exp2_lds[threadIdx.x] = (A).exp2_256[threadIdx.x]; \
   __syncthreads();
 
 // Compile-time loop: f(std::integral_constant<int, S>) for S = 0 .. N-1, so
@@ -1212,7 +1217,7 @@ __global__ __launch_bounds__(256) void k_post1(int N, const double *ainv, const 
 // chain without memory round trips.
 struct NodeChainArgs {
   const double *m1p, *m1bp, *m2p, *m2bp, *intp, *intbp;  // MFMA operand order
-  const double *int_cg, *ln2w, *ln2b, *exp2_64;
+  const double *int_cg, *ln2w, *ln2b, *exp2_256;
   double eps;
 };
 // Two wavefronts per 16 atoms (four per block: two 16-atom tiles), so that a
@@ -1226,10 +1231,10 @@ __global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restric
                                                    double *__restrict__ tout, double *__restrict__ xout,
                                                    double *__restrict__ evout, double *__restrict__ pre2hat,
                                                    double *__restrict__ pre2is) {
-  __shared__ double exp2_lds[64];
+  __shared__ double exp2_lds[256];
   __shared__ v4d buf[2][8][64];         // one 16-atom tile's layer input, operand order (16 KB per tile)
   __shared__ double stat[2][2][2][64];  // [tile][half][sum, sum of squares][lane]
-  if (threadIdx.x < 64) exp2_lds[threadIdx.x] = A.exp2_64[threadIdx.x];
+  if (threadIdx.x < 256) exp2_lds[threadIdx.x] = A.exp2_256[threadIdx.x];
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   const int wl = threadIdx.x >> 6, tile = wl >> 1, h = wl & 1;
   // every wavefront runs to the end (the barriers); rows beyond N are clamped
@@ -2344,9 +2349,9 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     hw_.rbf_k = up(std::vector<double>(kk.begin(), kk.end()));
     hw_.rbf_kr = up(std::vector<double>(kr.begin(), kr.end()));
     {
-      std::vector<double> t(64);
-      for (int j = 0; j < 64; ++j) t[j] = double(std::exp2(static_cast<long double>(j) / 64.0L));
-      hw_.exp2_64 = up(t);
+      std::vector<double> t(256);
+      for (int j = 0; j < 256; ++j) t[j] = double(std::exp2(static_cast<long double>(j) / 256.0L));
+      hw_.exp2_256 = up(t);
     }
     const auto &al = m.tensor("physical.reference_alphas");
     if (al.shape.size() != 1 || al.shape[0] < 8) throw std::runtime_error("SO3LR physical reference-table contract changed");
@@ -2564,7 +2569,7 @@ FilterMfma filter_mfma(const BlockWeights &B, const HeadWeights &H, double gamma
     FM.ob1p0[k] = B.ob1p0[k];
   }
   FM.att_cg = B.att_cg; FM.rbf_b = H.rbf_b; FM.rbf_k = H.rbf_k; FM.rbf_kr = H.rbf_kr; FM.gamma = gamma;
-  FM.exp2_64 = H.exp2_64;
+  FM.exp2_256 = H.exp2_256;
   return FM;
 }
 }  // namespace
@@ -2768,7 +2773,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
       hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
                          n1ib, act);
     // the post-attention node chain in one kernel (MLP, interaction, LayerNorm 2, ev gate)
-    const NodeChainArgs NC{B.m1p, B.m1bp, B.m2p, B.m2bp, B.intp, B.intbp, B.int_cg, B.ln2w, B.ln2b, hw_.exp2_64,
+    const NodeChainArgs NC{B.m1p, B.m1bp, B.m2p, B.m2bp, B.intp, B.intbp, B.int_cg, B.ln2w, B.ln2b, hw_.exp2_256,
                            ln_eps_};
     hipLaunchKernelGGL(k_node_fwd, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), act, n1b, aevb, NC, hpb, tb,
                        xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);

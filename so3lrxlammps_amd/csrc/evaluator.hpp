@@ -66,7 +66,7 @@ struct HeadWeights {
   const double *hkey_c;           // (100): hqemb[z] . hb2
   const double *hqemb, *hvshift;  // (100, 64), (100)
   const double *rbf_b, *rbf_k, *rbf_kr;  // (32) each
-  const double *exp2_64;                 // 2^(j/64), j < 64 (lean e^x of the filter kernels)
+  const double *exp2_256;                // 2^(j/256), j < 256 (lean e^x of the filter kernels)
   const double *alpha_ref, *c6_ref;
   int n_ref;
 };
