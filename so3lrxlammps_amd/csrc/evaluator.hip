@@ -414,10 +414,13 @@ struct FilterMfma {
 // (truncation < 4e-17 relative).  The power 2^m is capped at 2^1000, which
 // only matters for x > 693.
 __device__ __forceinline__ double exp_tab(double x, const double *tab) {
-  const double n = __builtin_rint(x * 369.3299304675746);  // 256 / ln2
+  // t = x 256/ln2 + 1.5 2^52 rounds the product to an integer n held in the
+  // low bits of t (exact for |n| < 2^51): n = t - 1.5 2^52, k = low word of t
+  const double t = fma(x, 369.3299304675746, 6755399441055744.0);
+  const double n = t - 6755399441055744.0;
   double r = fma(n, -0.00270760617331689, x);
   r = fma(n, -7.453964567463233e-13, r);
-  const int k = int(n);
+  const int k = int(unsigned(__builtin_bit_cast(unsigned long long, t)));
   double p = 1.0 / 24.0;
   p = fma(p, r, 1.0 / 6.0);
   p = fma(p, r, 0.5);
