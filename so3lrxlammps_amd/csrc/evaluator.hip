@@ -1791,17 +1791,19 @@ __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, cons
 // For node n and each active pair p = {n, o}: the incoming edge o -> n gives
 // dq_n, the outgoing edge n -> o gives dk_n, dv_n (sender-side terms,
 // gathered here instead of scattered).  The endpoint with side 0 also writes
-// the per-pair adjoints df (both directions), dfc and accumulates dY.  Lane
+// the per-pair adjoints df (both directions), dfc and accumulates dY (the
+// first reverse block, FIRST, writes it without reading).  Lane
 // layout as in k_attn_fwd.
 // NODE_ADJ false (block 0): only the pair adjoints are needed, not dq, dk, dv.
-template <bool NODE_ADJ>
+template <bool NODE_ADJ, bool FIRST>
 __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, const int *__restrict__ iact,
                                                   const int *__restrict__ iother, const double *__restrict__ qkv,
                                                   const double *__restrict__ pf, const double *__restrict__ pY,
                                                   const double *__restrict__ pfc, const double *__restrict__ palpha,
                                                   const double *__restrict__ gainv, const double *__restrict__ gaev,
-                                                  double inv_avg, double *__restrict__ gqkv, double *__restrict__ df,
-                                                  double *__restrict__ dfc, double *__restrict__ dY) {
+                                                  double inv_avg, double *__restrict__ gqkv,
+                                                  double *__restrict__ df, double *__restrict__ dfc,
+                                                  double *__restrict__ dY) {
   const int lane = threadIdx.x & 63;
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -1844,7 +1846,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     const double fi0 = fiv.x, fi1 = fiv.y, fe0 = fev.x, fe1 = fev.y;
     const double fc = pfc[p];
     const double y_ld = pY[kE * std::size_t(p) + m];
-    const double dy_old = dY[kE * std::size_t(p) + m];  // used by the side-0 endpoint only
+    const double dy_old = FIRST ? 0.0 : dY[kE * std::size_t(p) + m];  // used by the side-0 endpoint only
     const double *al = palpha + 16 * std::size_t(p);
     const double ain_i = al[8 * side + h], ain_e = al[8 * side + 4 + h];
     const double aout_i = al[8 * (1 - side) + h], aout_e = al[8 * (1 - side) + 4 + h];
@@ -2724,7 +2726,6 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   if (P > 0)
     hipLaunchKernelGGL(k_inc_active, dim3(unsigned((2 * Pz + 255) / 256)), dim3(256), 0, s, int(2 * P), sr_inc, c2a,
                        pa, iact, iother);
-  fill(dY, kE * Pz);
   fill(dr, Pz);
   HIP_CHECK(hipMemcpyAsync(xs, x0, Nz * kF * sizeof(double), hipMemcpyDeviceToDevice, s));
   fill(evs, Nz * kE);
@@ -2833,12 +2834,15 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
                        p2i, hpb, n1b, n1hb, n1ib, NB, gainv, gaev);
     const bool blk0 = b == 0 && !naive_filters_;
     timed(b == 0 ? "attn_bwd_block0" : "attn_bwd", 1, [&] {
-      if (b > 0)
-        hipLaunchKernelGGL(k_attn_bwd<true>, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY,
-                           pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
-      else
-        hipLaunchKernelGGL(k_attn_bwd<false>, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY,
-                           pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY);
+#define SO3LR_ATTN_BWD(ADJ, FIRST)                                                                              \
+  hipLaunchKernelGGL((k_attn_bwd<ADJ, FIRST>), dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY, \
+                     pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY)
+      // the first reverse block (L - 1) writes dY, the others add to it
+      if (b > 0 && b == L - 1) SO3LR_ATTN_BWD(true, true);
+      else if (b > 0) SO3LR_ATTN_BWD(true, false);
+      else if (L == 1) SO3LR_ATTN_BWD(false, true);
+      else SO3LR_ATTN_BWD(false, false);
+#undef SO3LR_ATTN_BWD
     });
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     timed(blk0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
