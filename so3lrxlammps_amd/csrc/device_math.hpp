@@ -41,24 +41,33 @@ __device__ __forceinline__ double silu_prime(double x) {
 //        for -745 <= x <= 708 (below that the result underflows to 0);
 //   1/d: the hardware reciprocal refined by two Newton steps
 //        r <- r + r (1 - d r), each squaring the relative error.
+// a * b + c as one three-operand v_fma_f64.  Where the scalar registers are
+// full, the compiler keeps loop-invariant constants in vector registers and
+// writes fma(p, r, c) as a copy of c plus the two-address v_fmac_f64; in a
+// Horner loop that doubles the instruction count.
+__device__ __forceinline__ double fma3(double a, double b, double c) {
+  double d;
+  asm("v_fma_f64 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
 __device__ __forceinline__ double exp_lean(double x) {
   const double n = __builtin_rint(x * 1.4426950408889634074);
   double r = fma(n, -6.93147180369123816490e-01, x);
   r = fma(n, -1.90821492927058770002e-10, r);
   double p = 1.0 / 6227020800.0;  // 1/13!
-  p = fma(p, r, 1.0 / 479001600.0);
-  p = fma(p, r, 1.0 / 39916800.0);
-  p = fma(p, r, 1.0 / 3628800.0);
-  p = fma(p, r, 1.0 / 362880.0);
-  p = fma(p, r, 1.0 / 40320.0);
-  p = fma(p, r, 1.0 / 5040.0);
-  p = fma(p, r, 1.0 / 720.0);
-  p = fma(p, r, 1.0 / 120.0);
-  p = fma(p, r, 1.0 / 24.0);
-  p = fma(p, r, 1.0 / 6.0);
-  p = fma(p, r, 0.5);
-  p = fma(p, r, 1.0);
-  p = fma(p, r, 1.0);
+  p = fma3(p, r, 1.0 / 479001600.0);
+  p = fma3(p, r, 1.0 / 39916800.0);
+  p = fma3(p, r, 1.0 / 3628800.0);
+  p = fma3(p, r, 1.0 / 362880.0);
+  p = fma3(p, r, 1.0 / 40320.0);
+  p = fma3(p, r, 1.0 / 5040.0);
+  p = fma3(p, r, 1.0 / 720.0);
+  p = fma3(p, r, 1.0 / 120.0);
+  p = fma3(p, r, 1.0 / 24.0);
+  p = fma3(p, r, 1.0 / 6.0);
+  p = fma3(p, r, 0.5);
+  p = fma3(p, r, 1.0);
+  p = fma3(p, r, 1.0);
   return __builtin_ldexp(p, int(n));
 }
 __device__ __forceinline__ double rcp_lean(double d) {
