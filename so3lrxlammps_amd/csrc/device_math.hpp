@@ -250,7 +250,7 @@ __device__ __forceinline__ double erf_lean(double x, double exp_mx2) {
   const double u = x * (2.0 / 3.0) - 1.0;
   double p = kErfcxPoly[0];
 #pragma unroll
-  for (int k = 1; k < 26; ++k) p = fma(p, u, kErfcxPoly[k]);
+  for (int k = 1; k < 26; ++k) p = fma3(p, u, kErfcxPoly[k]);
   return fma(-exp_mx2, p, 1.0);
 }
 
