@@ -31,16 +31,6 @@ __device__ __forceinline__ double silu_prime(double x) {
   return s * (1.0 + x * (1.0 - s));
 }
 
-// Lean forms for the MFMA filter kernels.  On gfx950 every VALU instruction
-// a wavefront issues takes issue time from the fp64 MFMAs of its SIMD, so the
-// activations there are written for the fewest instructions at full fp64
-// accuracy (a few ulp), with no IEEE special-case handling beyond a clamp:
-//   e^x: Cody-Waite reduction x = n ln2 + r, |r| <= ln2 / 2, with ln2 split
-//        into a 32-bit-exact high part and a low part, then the degree-13
-//        Taylor polynomial of e^r (truncation < 4e-18 relative) and 2^n;
-//        for -745 <= x <= 708 (below that the result underflows to 0);
-//   1/d: the hardware reciprocal refined by two Newton steps
-//        r <- r + r (1 - d r), each squaring the relative error.
 // a * b + c as one three-operand v_fma_f64.  Where the scalar registers are
 // full, the compiler keeps loop-invariant constants in vector registers and
 // writes fma(p, r, c) as a copy of c plus the two-address v_fmac_f64; in a
@@ -50,6 +40,16 @@ __device__ __forceinline__ double fma3(double a, double b, double c) {
   asm("v_fma_f64 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
 }
+// Lean forms for the long-range pair terms and the switch functions, which run
+// once per long-range entry (about 900 per atom): the fewest VALU instructions
+// at full fp64 accuracy (a few ulp), with no IEEE special-case handling:
+//   e^x: Cody-Waite reduction x = n ln2 + r, |r| <= ln2 / 2, with ln2 split
+//        into a 32-bit-exact high part and a low part, then the degree-13
+//        Taylor polynomial of e^r (truncation < 4e-18 relative) and 2^n;
+//        for -745 <= x <= 708 (below that the result underflows to 0);
+//   1/d: the hardware reciprocal (2^-24) refined by two Newton steps
+//        r <- r + r (1 - d r), each squaring the relative error.
+// (The filter kernels' activations use a table-driven e^x in evaluator.hip.)
 __device__ __forceinline__ double exp_lean(double x) {
   const double n = __builtin_rint(x * 1.4426950408889634074);
   double r = fma(n, -6.93147180369123816490e-01, x);
@@ -74,14 +74,6 @@ __device__ __forceinline__ double rcp_lean(double d) {
   double r = __builtin_amdgcn_rcp(d);
   r = fma(fma(-d, r, 1.0), r, r);
   return fma(fma(-d, r, 1.0), r, r);
-}
-// sigmoid(x) = 1 / (1 + e^-x); x >= -708 keeps e^-x finite (below, the
-// sigmoid is < 1e-307 either way)
-__device__ __forceinline__ double sigmoid_lean(double x) { return rcp_lean(1.0 + exp_lean(-fmax(x, -708.0))); }
-__device__ __forceinline__ double silu_lean(double x) { return x * sigmoid_lean(x); }
-__device__ __forceinline__ double silu_prime_lean(double x) {
-  const double s = sigmoid_lean(x);
-  return s * (1.0 + x * (1.0 - s));
 }
 
 // degree slot (0..3 for l = 1..4) of equivariant channel m in 0..23
