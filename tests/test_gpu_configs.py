@@ -75,11 +75,11 @@ def test_config1_water(orc):
 
 
 def test_config2_packed_molecules(orc):
-    """48 of the config-2 molecules (charged, open-shell) as packed images,
+    """All 512 config-2 molecules (charged, open-shell) as packed images,
     through the LAMMPS rows path and the device path."""
     from so3lrxlammps_amd import Context, Lists, systems
-    z, x, offs, qs, ms, extent = systems.packed_molecules(n_mol=48)
-    print("config 2 subset: %d atoms in %d images" % (len(z), len(qs)), flush=True)
+    z, x, offs, qs, ms, extent = systems.packed_molecules()
+    print("config 2: %d atoms in %d images" % (len(z), len(qs)), flush=True)
     img = np.repeat(np.arange(len(qs)), np.diff(offs))
     sr, lr = support.build_graphs(x, None)
     out = orc.evaluate(z, sr, lr, image=img, image_charge=qs, image_multiplicity=ms)
