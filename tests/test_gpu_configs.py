@@ -1,11 +1,11 @@
 """The benchmark configurations on the GPU, against the CPU oracle.
 
-Configs 0-3 are checked directly against the oracle at their full size
+Every configuration is checked directly against the oracle at its full size
 (energy 1e-10 relative, forces and virial 1e-9 eV/A), the oracle's graphs
-built from the LAMMPS stand-in's lists.  Config 4 (150,000 atoms) is checked
-through size-independent properties: translation invariance, zero net force
-of a periodic cell, bitwise determinism, and agreement of a cluster cut from
-it with the oracle.
+built from the LAMMPS stand-in's lists.  Config 4 (150,000 atoms) is also
+checked through size-independent properties: translation invariance, zero net
+force of a periodic cell, bitwise determinism, and agreement of a cluster cut
+from it with the oracle.
 """
 import numpy as np
 import pytest
@@ -153,3 +153,26 @@ def test_config4_memory_ceiling_properties(orc):
     out = orc.evaluate(zs, sr, lr, charge=0.0, multiplicity=1.0)
     e4, f4, w4, _ = _device_eval(cs, xs, lo, hi, (0, 0, 0))
     _check(e4, f4, w4, out)
+
+
+def test_config4_full_size(orc):
+    """The 150,000-atom memory-ceiling water, all atoms, device path against
+    the oracle (about 60 GB of host memory for the oracle's per-edge
+    buffers and a few tens of seconds on the GPU box's cores)."""
+    import resource
+    import time
+    from so3lrxlammps_amd import Context, Lists, systems
+    z, x, box, q, m, desc = systems.config(4)
+    t0 = time.time()
+    lists = Lists(x, np.zeros(3), box, (1, 1, 1))
+    sr, lr = support.graphs_from_lists(lists, x)
+    del lists
+    out = orc.evaluate(z, sr, lr)
+    del sr, lr
+    print("config 4 oracle: %.0f s, peak host memory %.1f GB" %
+          (time.time() - t0, resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1e6), flush=True)
+    c = Context(support.MODEL, 0)
+    c.set_system(z, q, m)
+    e, f, w, ea = _device_eval(c, x, np.zeros(3), box, (1, 1, 1), eatom=True)
+    _check(e, f, w, out)
+    assert np.abs(ea - out["eatom"]).max() <= 1e-10
