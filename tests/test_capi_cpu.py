@@ -41,6 +41,32 @@ def test_element_map_known_answers():
     assert f("Es") == 99 and f("na") == 11 and f("") == 0
 
 
+def test_check_system_needs_no_device():
+    # the (Q, M) rules of src/so3lr_charge_spin.cpp:52-141 and the empty-rank
+    # refusal of src/rank_local_half_pair_graph.cpp:43, before any GPU call
+    lib = _lib.hip()
+
+    def check(z, q, m):
+        z = np.ascontiguousarray(z, dtype=np.int32)
+        rc = lib.so3lr_check_system(len(z), _lib.ptr(z), float(q), float(m))
+        return rc, (lib.so3lr_last_error(None) or b"").decode()
+
+    o2 = support.load_golden("o2")[1]
+    acetate = support.load_golden("acetate")[1]
+    assert check(o2, 0, 3)[0] == _lib.OK and check(acetate, -1, 1)[0] == _lib.OK
+    rc, msg = check(o2, 0, 2)  # 16 electrons: an even count needs an odd multiplicity
+    assert rc == _lib.ERR_SYSTEM and msg
+    assert check(acetate, 0, 2)[0] == _lib.OK  # the neutral radical: 31 electrons, a doublet
+    rc, msg = check(acetate, 0, 1)  # 31 electrons: an odd count needs an even multiplicity
+    assert rc == _lib.ERR_SYSTEM and msg
+    rc, msg = check(acetate, -1, 2)  # the anion's 32 electrons: M = 2 is refused
+    assert rc == _lib.ERR_SYSTEM and msg
+    rc, msg = check(np.zeros(0), 0, 1)
+    assert rc == _lib.ERR_ARGUMENT and "empty" in msg
+    rc, msg = check([8, 100], 0, 1)
+    assert rc == _lib.ERR_ARGUMENT and "1..99" in msg
+
+
 def _create(path):
     import ctypes
     lib = _lib.hip()

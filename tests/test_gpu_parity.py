@@ -130,6 +130,17 @@ def test_refusals(ctx):
     with pytest.raises(_lib.SO3LRError) as err:
         ctx.set_system(z, 0, 2)  # O2 has 16 electrons: an even count needs an odd multiplicity
     assert err.value.code == _lib.ERR_SYSTEM
+    # a rank that owns no atoms, and a packed image with none, are refused
+    # (src/rank_local_half_pair_graph.cpp:43)
+    with pytest.raises(_lib.SO3LRError) as err:
+        ctx.set_system(np.zeros(0, dtype=np.int32), 0, 1)
+    assert err.value.code == _lib.ERR_ARGUMENT
+    with pytest.raises(_lib.SO3LRError) as err:
+        ctx.set_images(np.array([8, 8], dtype=np.int32), [0, 2, 2], [0.0, 0.0], [3.0, 1.0])
+    assert err.value.code == _lib.ERR_ARGUMENT
+    # the context stays usable after the refusals
+    e2, f2, _, _, _ = _hip_single_point(ctx, z, pos, box, 0, 3)
+    assert e2 == e and np.array_equal(f2, f)
 
 
 def test_per_atom_virial_matches_oracle(ctx, orc):
