@@ -17,6 +17,25 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(REPO, "tests", "golden")
 MODEL = os.path.join(REPO, "models", "so3lr.so3lr")
 
+
+
+def perturbed_model(path, seed=11, scale=0.2):
+    """A copy of the shipped model in which every float64 parameter tensor is
+    scaled elementwise by 1 + scale * u, u uniform in [-1, 1] (seeded); the
+    derived and physical constants (basis, Clebsch-Gordan tables, reference
+    polarizabilities and C6) are kept. A second set of weights for parity
+    tests, written with so3lrxlammps_amd.model_file."""
+    from so3lrxlammps_amd.model_file import read_model, write_model
+    manifest, arrays = read_model(MODEL)
+    rng = np.random.default_rng(seed)
+    for rec in manifest["tensors"]:
+        if rec["role"] == "parameter" and rec["dtype"] == "float64":
+            a = arrays[rec["state_key"]]
+            arrays[rec["state_key"]] = a * (1.0 + scale * rng.uniform(-1.0, 1.0, a.shape))
+    write_model(str(path), manifest, arrays)
+    return str(path)
+
+
 SYMBOLS = ["", "H", "He", "Li", "Be", "B", "C", "N", "O", "F", "Ne", "Na", "Mg", "Al",
            "Si", "P", "S", "Cl", "Ar", "K", "Ca"]
 

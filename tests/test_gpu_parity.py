@@ -86,6 +86,25 @@ def test_water3000_periodic(ctx, orc):
     assert np.abs(f - np.asarray(ref["forces"])).max() <= 3e-6
 
 
+@pytest.fixture(scope="module")
+def perturbed(tmp_path_factory):
+    return support.perturbed_model(tmp_path_factory.mktemp("model") / "perturbed.so3lr")
+
+
+@pytest.mark.parametrize("name,q,m", [("acetate", -1, 1), ("water3000", 0, 1)])
+def test_perturbed_weights_match_oracle(perturbed, name, q, m):
+    """A second set of weights (every parameter tensor scaled elementwise by
+    1 +- 20 %, seeded), so that parity does not rest on the shipped
+    checkpoint's values alone."""
+    from so3lrxlammps_amd import Context
+    ref, z, pos, box = support.load_golden(name)
+    print("case perturbed", name, flush=True)
+    e, f, ea, w, terms = _hip_single_point(Context(perturbed, 0), z, pos, box, q, m)
+    sr, lr = support.build_graphs(pos, box)
+    out = Oracle(perturbed).evaluate(z, sr, lr, charge=q, multiplicity=m)
+    _check(out, e, f, ea, w, terms)
+
+
 def test_deterministic_bitwise(ctx):
     ref, z, pos, box = support.load_golden("alanine_cation")
     a = _hip_single_point(ctx, z, pos, box, 1, 2)
