@@ -12,11 +12,17 @@ library's loader checks (csrc/model.cpp, Model::load_bytes):
   zero padding between them; each manifest record carries its tensor's
   offset, byte count and SHA-256.
 
+`python -m so3lrxlammps_amd.model_file MODEL [--manifest OUT]` verifies a
+file and prints its summary as key=value lines, with the keys of the
+reference's check (exporter/so3lr_native_format.py:218-236), so scripts that
+read them keep working.
+
 `write_model` takes a manifest and the tensors by state key, lays the payload
 out again and recomputes every size and digest, so a manifest read from one
 file can carry new tensor values (tests use it for models with perturbed
 weights).
 """
+import argparse
 import hashlib
 import json
 import struct
@@ -83,3 +89,28 @@ def write_model(path, manifest, arrays):
                          hashlib.sha256(payload).digest(), b"\0" * 32)
     with open(path, "wb") as f:
         f.write(header + mbytes + payload)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description="Verify an SO3LR native model file and print its summary.")
+    ap.add_argument("model")
+    ap.add_argument("--manifest", help="also write the manifest here, indented")
+    args = ap.parse_args(argv)
+    manifest, arrays = read_model(args.model)
+    if args.manifest:
+        with open(args.manifest, "w") as f:
+            f.write(json.dumps(manifest, indent=2, sort_keys=True) + "\n")
+    arch = manifest.get("architecture", {})
+    with open(args.model, "rb") as f:
+        payload = HEADER.unpack(f.read(HEADER.size))[4]  # payload size, checked by read_model
+    for key, value in (("format_version", manifest["format_version"]), ("model_family", manifest.get("model_family")),
+                       ("tensor_count", manifest["tensor_count"]), ("tensor_bytes", manifest["tensor_bytes"]),
+                       ("payload_bytes", payload),
+                       ("short_range_cutoff", arch.get("short_range_cutoff_angstrom")),
+                       ("long_range_cutoff", arch.get("long_range_cutoff_angstrom"))):
+        print("%s=%s" % (key, value))
+    print("native_model_format_validation=PASS")
+
+
+if __name__ == "__main__":
+    main()

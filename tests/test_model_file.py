@@ -70,3 +70,23 @@ def test_perturbed_model_forces_are_the_energy_gradient(perturbed):
             p2 = pos.copy(); p2[i, a] -= h
             fd = -(run(orc, p1)["energy"] - run(orc, p2)["energy"]) / (2 * h)
             assert abs(fd - out["forces"][i, a]) < 2e-6, (i, a, fd, out["forces"][i, a])
+
+
+def test_verify_command_prints_the_reference_keys(tmp_path):
+    import subprocess
+    import sys
+    out = subprocess.run([sys.executable, "-m", "so3lrxlammps_amd.model_file", support.MODEL, "--manifest",
+                          str(tmp_path / "manifest.json")], cwd=support.REPO, capture_output=True, text=True,
+                         check=True).stdout
+    kv = dict(line.split("=", 1) for line in out.split())
+    assert kv["format_version"] == "1" and kv["model_family"] == "SO3LR"
+    assert kv["tensor_count"] == "213" and kv["payload_bytes"] == str(len(open(support.MODEL, "rb").read())
+                                                                     - 128 - _manifest_size())
+    assert float(kv["short_range_cutoff"]) == 4.5 and float(kv["long_range_cutoff"]) == 12.0
+    assert kv["native_model_format_validation"] == "PASS"
+    assert (tmp_path / "manifest.json").read_text().startswith("{\n")
+
+
+def _manifest_size():
+    import struct
+    return struct.unpack("<Q", open(support.MODEL, "rb").read(24)[16:24])[0]
