@@ -100,6 +100,29 @@ def test_config2_packed_molecules(orc):
     assert np.abs(t2["image_energy"] - t["image_energy"]).max() <= 1e-11 * np.abs(t["image_energy"]).max()
 
 
+def test_config2_images_perturbed_weights(tmp_path):
+    """64 config-2 molecules as packed images on a second set of weights
+    (every parameter tensor scaled elementwise by 1 +- 20 %, seeded): the
+    per-image charge correction and (Q, M) embedding with other values."""
+    from so3lrxlammps_amd import Context, Lists, systems
+    path = support.perturbed_model(tmp_path / "perturbed.so3lr")
+    z, x, offs, qs, ms, extent = systems.packed_molecules(n_mol=64)
+    print("config 2, perturbed weights: %d atoms in %d images" % (len(z), len(qs)), flush=True)
+    img = np.repeat(np.arange(len(qs)), np.diff(offs))
+    sr, lr = support.build_graphs(x, None)
+    out = Oracle(path).evaluate(z, sr, lr, image=img, image_charge=qs, image_multiplicity=ms)
+    c = Context(path, 0)
+    c.set_images(z, offs, qs, ms)
+    lists = Lists(x, np.zeros(3), np.full(3, extent), (0, 0, 0))
+    c.set_topology(lists)
+    e, f, ea, w = c.compute(lists.rows_positions(x))
+    _check(e, f, w, out)
+    t = c.terms()
+    assert np.abs(t["image_energy"] - out["image_energy"]).max() <= 1e-10 * np.abs(out["image_energy"]).max()
+    for k in range(len(qs)):
+        assert abs(t["charges"][offs[k]:offs[k + 1]].sum() - qs[k]) < 1e-12
+
+
 def test_config3_full_size(orc):
     """The headline system, all 24,000 atoms, device path against the oracle."""
     from so3lrxlammps_amd import Context, Lists, systems
