@@ -25,7 +25,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 MODEL = os.path.join(REPO, "models", "so3lr.so3lr")
-A100_ATOM_STEPS = 69706.0  # 24k-atom water, 1 A100 (examples/scaling/README.md:56-60)
+A100_ATOM_STEPS = 69706.0  # the reference's published 24k-atom water figure on 1 A100 (examples/scaling/README.md:56-60)
 HBM_PEAK_GBS = 8000.0
 FP64_PEAK_TFS = 78.6
 # algorithmic work of the dominant kernel, per active short-range pair and block
