@@ -27,7 +27,9 @@
  * Parity pins: every function here is checked in tests/test_oracle_*.py against
  * the reference's JAX golden vectors (tests/golden/refs), closed forms, finite
  * differences of the energy and invariances.  See the test files for which
- * check pins which function.
+ * check pins which function.  tests/test_model_file.py repeats the force
+ * finite differences on a second, perturbed set of weights, so that the
+ * reverse pass is not checked only on the shipped checkpoint's values.
  */
 #ifndef SO3LR_ORACLE_H
 #define SO3LR_ORACLE_H
