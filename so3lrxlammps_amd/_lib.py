@@ -128,6 +128,26 @@ def ptr(a):
     return ctypes.c_void_p(a.ctypes.data)
 
 
+def device_f64(t, count, what):
+    """Check that `t` is a contiguous float64 tensor on a GPU holding exactly
+    `count` values, and return its pointer.  The C ABI takes raw device
+    pointers and cannot see sizes, so a float32 tensor, a strided view or a
+    short buffer would become an out-of-bounds access on the device; the
+    binding refuses them here with a ValueError instead."""
+    if t is None:
+        raise ValueError("%s: a device tensor is required" % what)
+    if not getattr(t, "is_cuda", False):
+        raise ValueError("%s must be a GPU tensor (got %s)" % (what, getattr(t, "device", type(t).__name__)))
+    import torch
+    if t.dtype != torch.float64:
+        raise ValueError("%s must be float64 (got %s)" % (what, t.dtype))
+    if not t.is_contiguous():
+        raise ValueError("%s must be contiguous" % what)
+    if t.numel() != count:
+        raise ValueError("%s must hold %d values (got %d)" % (what, count, t.numel()))
+    return ptr(t)
+
+
 def _copy(p, count, dtype):
     if count == 0:
         return np.zeros(0, dtype=dtype)
@@ -208,6 +228,9 @@ class Context:
         off = np.ascontiguousarray(image_offsets, dtype=np.int64)
         q = np.ascontiguousarray(charges, dtype=np.float64)
         m = np.ascontiguousarray(multiplicities, dtype=np.float64)
+        if not (len(off) == len(q) + 1 == len(m) + 1):
+            raise ValueError("image_offsets needs one entry more than charges and multiplicities "
+                             "(%d offsets, %d charges, %d multiplicities)" % (len(off), len(q), len(m)))
         self._check(self._lib.so3lr_set_images(self._h, len(z), ptr(z), len(q), ptr(off), ptr(q), ptr(m)))
         self.n = len(z)
         self.n_images = len(q)
@@ -218,6 +241,7 @@ class Context:
         self._check(self._lib.so3lr_set_topology(
             self._h, lists.rows, ptr(lists.owner), LIST_FULL if lists.sr_full else LIST_HALF,
             len(si), ptr(si), ptr(so), ptr(sn), len(li), ptr(li), ptr(lo_), ptr(ln)))
+        self.rows = lists.rows
 
     def compute(self, x_rows, eatom=True):
         x_rows = np.ascontiguousarray(x_rows, dtype=np.float64)
@@ -231,25 +255,30 @@ class Context:
         return e.value, f, ea, w
 
     def compute_device(self, x_rows_dev, f_dev, eatom_dev=None, stream=None):
-        """Device pointers in, device forces out; returns (energy, virial)."""
+        """Device tensors in (positions of every row: owned and ghost rows after
+        set_topology, owned atoms after reneighbor_device), device forces out;
+        returns (energy, virial)."""
+        px = device_f64(x_rows_dev, 3 * self.rows, "positions")
+        pf = device_f64(f_dev, 3 * self.n, "forces")
+        pe = None if eatom_dev is None else device_f64(eatom_dev, self.n, "per-atom energies")
         if stream is not None:
             self._check(self._lib.so3lr_set_stream(self._h, ctypes.c_void_p(stream)))
         e = ctypes.c_double()
         w = np.zeros(6)
         flags = ENERGY | VIRIAL | (EATOM if eatom_dev is not None else 0)
-        self._check(self._lib.so3lr_compute_device(self._h, ptr(x_rows_dev), flags, ptr(f_dev),
-                                                   ptr(eatom_dev), ctypes.byref(e), ptr(w)))
+        self._check(self._lib.so3lr_compute_device(self._h, px, flags, pf, pe, ctypes.byref(e), ptr(w)))
         return e.value, w
 
     def reneighbor_device(self, x_owned_dev, lo, hi, periodic, skin, stream=None):
         """Device reneighbor; wraps x_owned_dev in place into [lo, hi)."""
+        px = device_f64(x_owned_dev, 3 * self.n, "owned positions")
         if stream is not None:
             self._check(self._lib.so3lr_set_stream(self._h, ctypes.c_void_p(stream)))
         lo = np.ascontiguousarray(lo, dtype=np.float64)
         hi = np.ascontiguousarray(hi, dtype=np.float64)
         per = np.ascontiguousarray(periodic, dtype=np.int32)
-        self._check(self._lib.so3lr_reneighbor_device(self._h, ptr(x_owned_dev), ptr(lo), ptr(hi), ptr(per),
-                                                      float(skin)))
+        self._check(self._lib.so3lr_reneighbor_device(self._h, px, ptr(lo), ptr(hi), ptr(per), float(skin)))
+        self.rows = self.n
 
     def set_box(self, lo, hi):
         lo = np.ascontiguousarray(lo, dtype=np.float64)
@@ -275,7 +304,7 @@ class Context:
         """Per-atom virial of the last evaluation, (n, 6) in LAMMPS order; `out`
         may be a device tensor (written on the context's stream)."""
         if out is not None and hasattr(out, "data_ptr") and getattr(out, "is_cuda", False):
-            self._check(self._lib.so3lr_last_vatom(self._h, ptr(out), 1))
+            self._check(self._lib.so3lr_last_vatom(self._h, device_f64(out, 6 * self.n, "per-atom virial"), 1))
             return out
         w = np.zeros((self.n, 6))
         self._check(self._lib.so3lr_last_vatom(self._h, ptr(w), 0))

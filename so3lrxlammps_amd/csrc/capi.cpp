@@ -37,6 +37,8 @@ int guarded(so3lr_ctx *ctx, F &&body) {
     body();
     ctx->error.clear();
     return SO3LR_OK;
+  } catch (const so3lr_amd::DeviceError &e) {
+    return fail(ctx, e, SO3LR_ERR_DEVICE);
   } catch (const std::invalid_argument &e) {
     return fail(ctx, e, SO3LR_ERR_ARGUMENT);
   } catch (const std::length_error &e) {
@@ -46,9 +48,8 @@ int guarded(so3lr_ctx *ctx, F &&body) {
   } catch (const std::logic_error &e) {
     return fail(ctx, e, SO3LR_ERR_STATE);
   } catch (const std::runtime_error &e) {
-    const std::string w = e.what();
-    return fail(ctx, e, w.rfind("HIP error", 0) == 0 ? SO3LR_ERR_DEVICE : SO3LR_ERR_MODEL);
-  } catch (const std::exception &e) {
+    return fail(ctx, e, SO3LR_ERR_MODEL);
+  } catch (const std::exception &e) {  // std::bad_alloc and the like
     return fail(ctx, e, SO3LR_ERR_DEVICE);
   }
 }
@@ -59,26 +60,30 @@ extern "C" {
 int so3lr_create(const char *model_path, int device, so3lr_ctx **out) {
   if (!out || !model_path) return SO3LR_ERR_ARGUMENT;
   *out = nullptr;
+  // the LAMMPS-visible wording of PairSO3LRNativeMPI::settings
+  // (plugins/lammps/pair_so3lr_native_mpi.cpp:1097-1137): the pair style
+  // passes this message to error->all as it stands
+  const std::string prefix = "Cannot initialize MPI-native SO3LR model: ";
+  std::shared_ptr<Model> m;
   try {
-    std::shared_ptr<Model> m = Model::load(model_path);
-    auto ctx = new so3lr_ctx();
-    try {
-      ctx->ev = std::make_unique<Evaluator>(m, device);
-    } catch (...) {
-      delete ctx;
-      throw;
-    }
-    *out = ctx;
-    return SO3LR_OK;
-  } catch (const std::runtime_error &e) {
-    const std::string w = e.what();
-    g_create_error = "Cannot initialize MPI-native SO3LR model: " + w;
-    return w.rfind("HIP error", 0) == 0 || w.find("device") != std::string::npos ? SO3LR_ERR_DEVICE
-                                                                                 : SO3LR_ERR_MODEL;
+    m = Model::load(model_path);
   } catch (const std::exception &e) {
-    g_create_error = std::string("Cannot initialize MPI-native SO3LR model: ") + e.what();
+    g_create_error = prefix + e.what();
     return SO3LR_ERR_MODEL;
   }
+  std::unique_ptr<so3lr_ctx> ctx(new so3lr_ctx());
+  try {
+    ctx->ev = std::make_unique<Evaluator>(m, device);
+  } catch (const so3lr_amd::DeviceError &e) {
+    g_create_error = prefix + e.what();
+    return SO3LR_ERR_DEVICE;
+  } catch (const std::exception &e) {  // a tensor the kernels need is missing or misshapen
+    g_create_error = prefix + e.what();
+    return SO3LR_ERR_MODEL;
+  }
+  *out = ctx.release();
+  g_create_error.clear();
+  return SO3LR_OK;
 }
 
 void so3lr_destroy(so3lr_ctx *ctx) { delete ctx; }

@@ -25,7 +25,7 @@ namespace so3lr_amd {
   do {                                                                                    \
     hipError_t err_ = (expr);                                                             \
     if (err_ != hipSuccess)                                                               \
-      throw std::runtime_error(std::string("HIP error in ") + #expr + ": " +             \
+      throw DeviceError(std::string("HIP error in ") + #expr + ": " +             \
                                hipGetErrorString(err_));                                  \
   } while (0)
 
@@ -2177,7 +2177,7 @@ std::vector<double> permute_mfma(const std::vector<double> &w, std::size_t M, st
 Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::move(model)), device_(device) {
   int count = 0;
   HIP_CHECK(hipGetDeviceCount(&count));
-  if (device < 0 || device >= count) throw std::runtime_error("SO3LR: HIP device index out of range");
+  if (device < 0 || device >= count) throw DeviceError("SO3LR: HIP device index out of range");
   HIP_CHECK(hipSetDevice(device));
   HIP_CHECK(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking));
   if (const char *nv = std::getenv("SO3LR_NAIVE_FILTERS")) naive_filters_ = nv[0] == '1';
@@ -2430,11 +2430,15 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
   if (ni < 1 || std::int64_t(multiplicities.size()) != ni || std::int64_t(image_offsets.size()) != ni + 1 ||
       image_offsets.front() != 0 || image_offsets.back() != n)
     throw std::invalid_argument("SO3LR: inconsistent image description");
+  // every offset is used as an index below: 0 = off[0] < off[1] < ... < off[ni] = n
+  for (std::int64_t k = 0; k < ni; ++k)
+    if (!(image_offsets[k + 1] > image_offsets[k]))
+      throw std::invalid_argument("SO3LR: image offsets must increase strictly from 0 to the atom count "
+                                  "(every image needs at least one atom)");
   std::vector<double> x0(std::size_t(n) * kF);
   std::vector<int> img(n);
   for (std::int64_t k = 0; k < ni; ++k) {
     const std::int64_t lo = image_offsets[k], hi = image_offsets[k + 1];
-    if (hi <= lo) throw std::invalid_argument("SO3LR: every image needs at least one atom");
     std::int64_t counts[119] = {0};
     for (std::int64_t i = lo; i < hi; ++i) ++counts[z[i]];
     const std::string why = charge_multiplicity_problem(counts, charges[k], multiplicities[k]);
@@ -2894,7 +2898,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
     (void)hipGraphDestroy(graph);
     if (ierr != hipSuccess) {
       graph_exec_ = nullptr;
-      throw std::runtime_error(std::string("HIP error in hipGraphInstantiate: ") + hipGetErrorString(ierr));
+      throw DeviceError(std::string("HIP error in hipGraphInstantiate: ") + hipGetErrorString(ierr));
     }
     graph_key_ = key;
     HIP_CHECK(hipGraphLaunch(graph_exec_, s));

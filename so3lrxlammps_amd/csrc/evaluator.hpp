@@ -25,6 +25,12 @@
 
 namespace so3lr_amd {
 
+// A failure of the HIP runtime or of the device (allocation, launch, copy,
+// device selection): reported as SO3LR_ERR_DEVICE at the C ABI.
+struct DeviceError : std::runtime_error {
+  explicit DeviceError(const std::string &what) : std::runtime_error(what) {}
+};
+
 // Device weight pointers for one interaction block.
 struct BlockWeights {
   const double *wqkv;                   // (5, 4, 32, 32): q k v q_ev k_ev, (head, in, out)
@@ -146,13 +152,13 @@ class Evaluator {
     const std::size_t need = (count ? count : 1) * sizeof(T);
     if (b->bytes < need) {
       if (b->p) {
-        if (hipFree(b->p) != hipSuccess) throw std::runtime_error("HIP error in hipFree");
+        if (hipFree(b->p) != hipSuccess) throw DeviceError("HIP error in hipFree");
         bytes_ -= std::int64_t(b->bytes);
       }
       b->p = nullptr;
       const std::size_t cap = need + need / 8;  // retained capacity with slack
       if (hipMalloc(&b->p, cap) != hipSuccess)
-        throw std::runtime_error("HIP error in hipMalloc: out of device memory (" + std::to_string(cap) + " bytes)");
+        throw DeviceError("HIP error in hipMalloc: out of device memory (" + std::to_string(cap) + " bytes)");
       b->bytes = cap;
       bytes_ += std::int64_t(cap);
       ++alloc_epoch_;  // a captured graph holds the old address

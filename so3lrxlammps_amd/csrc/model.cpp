@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <array>
+#include <charconv>
 #include <cerrno>
 #include <cctype>
 #include <cmath>
@@ -83,199 +84,315 @@ std::array<std::uint8_t, 32> sha256(const std::uint8_t *d, std::size_t n) {
   return s.digest(d, n);
 }
 
-// ---------------------------------------------------------------- JSON
-class Parser {
+// ------------------------------------------------------- canonical JSON
+// Python's repr of a finite double, the spelling the exporter's canonical
+// encoder writes (json.dumps uses float.__repr__): the shortest digits that
+// round-trip, positional notation when the decimal point position decpt
+// (value = 0.DIGITS x 10^decpt) satisfies -4 < decpt <= 16, otherwise
+// d[.ddd]e(+|-)XX with at least two exponent digits; positional values
+// always carry a fractional part ("4.0").
+std::string python_float_repr(double v) {
+  char sci[64];
+  const auto res = std::to_chars(sci, sci + sizeof sci, v, std::chars_format::scientific);
+  const std::string s(sci, res.ptr);  // [-]d[.ddd]e(+|-)XX
+  const std::size_t epos = s.find('e');
+  const bool neg = s[0] == '-';
+  std::string digits;
+  for (std::size_t i = neg ? 1 : 0; i < epos; ++i)
+    if (s[i] != '.') digits += s[i];
+  const int exp10 = std::atoi(s.c_str() + epos + 1);
+  const int decpt = exp10 + 1;
+  std::string out = neg ? "-" : "";
+  if (decpt > -4 && decpt <= 16) {
+    if (decpt <= 0) {
+      out += "0." + std::string(std::size_t(-decpt), '0') + digits;
+    } else if (std::size_t(decpt) >= digits.size()) {
+      out += digits + std::string(std::size_t(decpt) - digits.size(), '0') + ".0";
+    } else {
+      out += digits.substr(0, std::size_t(decpt)) + "." + digits.substr(std::size_t(decpt));
+    }
+  } else {
+    out += digits.substr(0, 1);
+    if (digits.size() > 1) out += "." + digits.substr(1);
+    const int a = exp10 < 0 ? -exp10 : exp10;
+    out += exp10 < 0 ? "e-" : "e+";
+    if (a < 10) out += '0';
+    out += std::to_string(a);
+  }
+  return out;
+}
+
+// Reads the whole manifest with an explicit stack of open containers (no
+// recursion, so nesting depth costs heap, not call stack).  Canonical form
+// means, byte for byte, what json.dumps(sort_keys=True, separators=(",",":"),
+// ensure_ascii=True) writes (docs/FORMAT.md:12-38 and the exporter's check
+// that re-encoding reproduces the bytes):
+//   * printable ASCII only, no whitespace between tokens;
+//   * object keys strictly increasing (sorted and unique);
+//   * in strings, a raw byte 0x20..0x7e other than '"' and '\', the short
+//     escapes \" \\ \b \f \n \r \t, or \u with four lowercase hex digits for
+//     every other code point (astral ones as a surrogate pair);
+//   * integers without leading zeros, floats spelled as Python's repr;
+//   * true, false, null.
+class CanonicalReader {
  public:
-  explicit Parser(const std::string &t) : t_(t) {}
-  Json document() {
-    Json v = value();
-    ws();
-    if (p_ != t_.size()) fail("trailing JSON data");
-    return v;
+  explicit CanonicalReader(const std::string &text) : t_(text) {}
+
+  Json run() {
+    for (std::size_t i = 0; i < t_.size(); ++i) {
+      const unsigned char c = static_cast<unsigned char>(t_[i]);
+      if (c < 0x20 || c > 0x7e) reject(i, "a byte outside printable ASCII");
+    }
+    Json done;
+    bool have_done = false;
+    for (;;) {
+      if (!have_done) {
+        // a value starts here
+        if (at_end()) reject(pos_, "input ends where a value is expected");
+        const char c = t_[pos_];
+        if (c == '{' || c == '[') {
+          Open o;
+          o.node.kind = c == '{' ? Json::Object : Json::Array;
+          ++pos_;
+          const char close = c == '{' ? '}' : ']';
+          if (!at_end() && t_[pos_] == close) {
+            ++pos_;
+            done = std::move(o.node);
+            have_done = true;
+            continue;
+          }
+          stack_.push_back(std::move(o));
+          if (c == '{') read_key();
+          continue;
+        }
+        done = scalar();
+        have_done = true;
+        continue;
+      }
+      // a value is complete: attach it to the innermost open container
+      if (stack_.empty()) {
+        if (!at_end()) reject(pos_, "text after the top-level value");
+        return done;
+      }
+      Open &top = stack_.back();
+      if (top.node.kind == Json::Array) top.node.arr.push_back(std::move(done));
+      else top.node.obj.emplace_back(std::move(top.key), std::move(done));
+      have_done = false;
+      if (at_end()) reject(pos_, "input ends inside a container");
+      const char sep = t_[pos_++];
+      if (sep == ',') {
+        if (top.node.kind == Json::Object) read_key();
+        continue;
+      }
+      if (sep != (top.node.kind == Json::Object ? '}' : ']')) reject(pos_ - 1, "expected ',' or the closing bracket");
+      done = std::move(top.node);
+      stack_.pop_back();
+      have_done = true;
+    }
   }
 
  private:
+  struct Open {
+    Json node;
+    std::string key;  // member being read (objects)
+  };
   const std::string &t_;
-  std::size_t p_ = 0;
-  void ws() {
-    while (p_ < t_.size() && (t_[p_] == ' ' || t_[p_] == '\n' || t_[p_] == '\r' || t_[p_] == '\t')) ++p_;
+  std::size_t pos_ = 0;
+  std::vector<Open> stack_;
+
+  [[noreturn]] void reject(std::size_t at, const char *why) const {
+    fail("manifest is not canonical JSON at byte " + std::to_string(at) + ": " + why);
   }
-  char next() {
-    if (p_ >= t_.size()) fail("unexpected end of JSON");
-    return t_[p_++];
+  bool at_end() const { return pos_ >= t_.size(); }
+
+  // "key": of the next member; keys must increase strictly
+  void read_key() {
+    Open &top = stack_.back();
+    if (at_end() || t_[pos_] != '"') reject(pos_, "expected a member name");
+    const std::size_t where = pos_;
+    std::string key = string_token();
+    if (!top.node.obj.empty() && !(top.node.obj.back().first < key))
+      reject(where, "member names not in strictly increasing order");
+    if (at_end() || t_[pos_] != ':') reject(pos_, "expected ':' after a member name");
+    ++pos_;
+    top.key = std::move(key);
   }
-  static void utf8(std::string &o, std::uint32_t c) {
-    if (c < 0x80) o += char(c);
-    else if (c < 0x800) { o += char(0xc0 | (c >> 6)); o += char(0x80 | (c & 0x3f)); }
-    else if (c < 0x10000) { o += char(0xe0 | (c >> 12)); o += char(0x80 | ((c >> 6) & 0x3f)); o += char(0x80 | (c & 0x3f)); }
-    else { o += char(0xf0 | (c >> 18)); o += char(0x80 | ((c >> 12) & 0x3f)); o += char(0x80 | ((c >> 6) & 0x3f)); o += char(0x80 | (c & 0x3f)); }
-  }
-  std::uint32_t hex4() {
-    std::uint32_t v = 0;
-    for (int i = 0; i < 4; ++i) {
-      const char c = next();
-      v <<= 4;
-      if (c >= '0' && c <= '9') v |= std::uint32_t(c - '0');
-      else if (c >= 'a' && c <= 'f') v |= std::uint32_t(c - 'a' + 10);
-      else if (c >= 'A' && c <= 'F') v |= std::uint32_t(c - 'A' + 10);
-      else fail("invalid JSON unicode escape");
+
+  Json scalar() {
+    Json j;
+    const char c = t_[pos_];
+    if (c == '"') {
+      j.kind = Json::String;
+      j.str = string_token();
+      return j;
     }
+    for (const char *lit : {"true", "false", "null"}) {
+      const std::size_t n = std::strlen(lit);
+      if (t_.compare(pos_, n, lit) == 0) {
+        pos_ += n;
+        if (lit[0] != 'n') {
+          j.kind = Json::Bool;
+          j.b = lit[0] == 't';
+        }
+        return j;
+      }
+    }
+    return number_token();
+  }
+
+  int hex_digit(std::size_t i) const {
+    const char c = i < t_.size() ? t_[i] : '\0';
+    if (c >= '0' && c <= '9') return c - '0';
+    if (c >= 'a' && c <= 'f') return c - 'a' + 10;
+    reject(i, "\\u needs four lowercase hexadecimal digits");
+  }
+  std::uint32_t u_escape() {  // pos_ at the 'u'
+    std::uint32_t v = 0;
+    for (int k = 1; k <= 4; ++k) v = (v << 4) | std::uint32_t(hex_digit(pos_ + k));
+    pos_ += 5;
     return v;
   }
-  std::string str() {
-    ws();
-    if (next() != '"') fail("expected JSON string");
-    std::string o;
+  static void put_utf8(std::string &o, std::uint32_t cp) {
+    int n = cp < 0x80 ? 1 : cp < 0x800 ? 2 : cp < 0x10000 ? 3 : 4;
+    static const unsigned char lead[5] = {0, 0x00, 0xc0, 0xe0, 0xf0};
+    char buf[4];
+    for (int k = n - 1; k > 0; --k) {
+      buf[k] = char(0x80 | (cp & 0x3f));
+      cp >>= 6;
+    }
+    buf[0] = char(lead[n] | cp);
+    o.append(buf, std::size_t(n));
+  }
+
+  std::string string_token() {  // pos_ at the opening quote
+    std::string out;
+    ++pos_;
     for (;;) {
-      const char c = next();
-      if (c == '"') return o;
-      if (static_cast<unsigned char>(c) < 0x20) fail("control byte in JSON string");
-      if (c != '\\') { o += c; continue; }
-      const char e = next();
-      switch (e) {
-        case '"': o += '"'; break;
-        case '\\': o += '\\'; break;
-        case '/': o += '/'; break;
-        case 'b': o += '\b'; break;
-        case 'f': o += '\f'; break;
-        case 'n': o += '\n'; break;
-        case 'r': o += '\r'; break;
-        case 't': o += '\t'; break;
-        case 'u': {
-          std::uint32_t c1 = hex4();
-          if (c1 >= 0xd800 && c1 <= 0xdbff) {
-            if (next() != '\\' || next() != 'u') fail("invalid surrogate pair");
-            const std::uint32_t c2 = hex4();
-            if (c2 < 0xdc00 || c2 > 0xdfff) fail("invalid surrogate pair");
-            c1 = 0x10000 + ((c1 - 0xd800) << 10) + (c2 - 0xdc00);
-          }
-          utf8(o, c1);
-          break;
-        }
-        default: fail("invalid JSON escape");
+      if (at_end()) reject(pos_, "unterminated string");
+      const char c = t_[pos_];
+      if (c == '"') {
+        ++pos_;
+        return out;
       }
+      if (c != '\\') {
+        out += c;
+        ++pos_;
+        continue;
+      }
+      ++pos_;
+      if (at_end()) reject(pos_, "unterminated escape");
+      const char e = t_[pos_];
+      static const char shorts[] = "\"\\bfnrt", decoded[] = "\"\\\b\f\n\r\t";
+      if (const char *s = std::strchr(shorts, e); s && e != '\0') {
+        out += decoded[s - shorts];
+        ++pos_;
+        continue;
+      }
+      if (e != 'u') reject(pos_, "an escape the canonical encoder never writes");
+      const std::size_t where = pos_;
+      std::uint32_t cp = u_escape();
+      if (cp >= 0xdc00 && cp <= 0xdfff) reject(where, "a lone low surrogate");
+      if (cp >= 0xd800 && cp <= 0xdbff) {
+        if (t_.compare(pos_, 2, "\\u") != 0) reject(pos_, "a high surrogate without its low half");
+        ++pos_;
+        const std::uint32_t lo = u_escape();
+        if (lo < 0xdc00 || lo > 0xdfff) reject(pos_, "a high surrogate without its low half");
+        cp = 0x10000 + ((cp - 0xd800) << 10) + (lo - 0xdc00);
+      }
+      const bool has_short = cp == '"' || cp == '\\' || cp == '\b' || cp == '\f' || cp == '\n' || cp == '\r' ||
+                             cp == '\t';
+      if ((cp >= 0x20 && cp <= 0x7e) || has_short) reject(where, "\\u escape of a character written literally or in short form");
+      put_utf8(out, cp);
     }
   }
-  Json num() {
-    const std::size_t b = p_;
-    auto digit = [&](std::size_t i) { return i < t_.size() && t_[i] >= '0' && t_[i] <= '9'; };
-    if (p_ < t_.size() && t_[p_] == '-') ++p_;
-    if (!digit(p_)) fail("invalid JSON number");
-    if (t_[p_] == '0') ++p_;
-    else while (digit(p_)) ++p_;
-    if (p_ < t_.size() && t_[p_] == '.') {
-      ++p_;
-      if (!digit(p_)) fail("invalid JSON fraction");
-      while (digit(p_)) ++p_;
+
+  Json number_token() {
+    const std::size_t b = pos_;
+    auto digits = [&]() {
+      const std::size_t s = pos_;
+      while (!at_end() && t_[pos_] >= '0' && t_[pos_] <= '9') ++pos_;
+      return pos_ - s;
+    };
+    if (!at_end() && t_[pos_] == '-') ++pos_;
+    const std::size_t int_begin = pos_;
+    if (digits() == 0) reject(b, "not a value");
+    const bool lead_zero = t_[int_begin] == '0' && pos_ - int_begin > 1;
+    bool is_float = false;
+    if (!at_end() && t_[pos_] == '.') {
+      ++pos_;
+      if (digits() == 0) reject(pos_, "a decimal point without digits after it");
+      is_float = true;
     }
-    if (p_ < t_.size() && (t_[p_] == 'e' || t_[p_] == 'E')) {
-      ++p_;
-      if (p_ < t_.size() && (t_[p_] == '+' || t_[p_] == '-')) ++p_;
-      if (!digit(p_)) fail("invalid JSON exponent");
-      while (digit(p_)) ++p_;
+    if (!at_end() && (t_[pos_] == 'e' || t_[pos_] == 'E')) {
+      ++pos_;
+      if (!at_end() && (t_[pos_] == '+' || t_[pos_] == '-')) ++pos_;
+      if (digits() == 0) reject(pos_, "an exponent without digits");
+      is_float = true;
     }
-    const std::string tok = t_.substr(b, p_ - b);
-    char *end = nullptr;
-    const double v = std::strtod(tok.c_str(), &end);
-    if (end != tok.c_str() + tok.size() || !std::isfinite(v)) fail("invalid JSON number");
     Json j;
     j.kind = Json::Number;
-    j.num = v;
+    j.str = t_.substr(b, pos_ - b);
+    j.num = std::strtod(j.str.c_str(), nullptr);
+    if (!std::isfinite(j.num)) reject(b, "a number outside the double range");
+    if (is_float) {
+      if (python_float_repr(j.num) != j.str) reject(b, "a float not spelled as its shortest repr");
+    } else if (lead_zero || j.str == "-0") {
+      reject(b, "an integer with a leading zero or a negative zero");
+    }
     return j;
-  }
-  void word(const char *w) {
-    const std::size_t n = std::strlen(w);
-    if (t_.compare(p_, n, w) != 0) fail("invalid JSON literal");
-    p_ += n;
-  }
-  Json value() {
-    ws();
-    if (p_ >= t_.size()) fail("unexpected end of JSON");
-    const char c = t_[p_];
-    Json j;
-    if (c == '"') { j.kind = Json::String; j.str = str(); return j; }
-    if (c == 't') { word("true"); j.kind = Json::Bool; j.b = true; return j; }
-    if (c == 'f') { word("false"); j.kind = Json::Bool; j.b = false; return j; }
-    if (c == 'n') { word("null"); return j; }
-    if (c == '[') {
-      ++p_;
-      j.kind = Json::Array;
-      ws();
-      if (p_ < t_.size() && t_[p_] == ']') { ++p_; return j; }
-      for (;;) {
-        j.arr.push_back(value());
-        ws();
-        const char d = next();
-        if (d == ']') return j;
-        if (d != ',') fail("expected comma in JSON array");
-      }
-    }
-    if (c == '{') {
-      ++p_;
-      j.kind = Json::Object;
-      ws();
-      if (p_ < t_.size() && t_[p_] == '}') { ++p_; return j; }
-      for (;;) {
-        std::string key = str();
-        ws();
-        if (next() != ':') fail("expected colon in JSON object");
-        if (!j.obj.emplace(key, value()).second) fail("duplicate JSON object key");
-        ws();
-        const char d = next();
-        if (d == '}') return j;
-        if (d != ',') fail("expected comma in JSON object");
-      }
-    }
-    return num();
   }
 };
 
-std::uint64_t le64(const std::uint8_t *p) {
-  std::uint64_t v = 0;
-  for (int i = 7; i >= 0; --i) v = (v << 8) | p[i];
+std::uint32_t get_u32(const std::uint8_t *p) {
+  std::uint32_t v = 0;
+  for (int k = 3; k >= 0; --k) v = (v << 8) | p[k];
   return v;
 }
-std::uint32_t le32(const std::uint8_t *p) {
-  return std::uint32_t(p[0]) | (std::uint32_t(p[1]) << 8) | (std::uint32_t(p[2]) << 16) |
-         (std::uint32_t(p[3]) << 24);
-}
+std::uint64_t get_u64(const std::uint8_t *p) { return std::uint64_t(get_u32(p)) | (std::uint64_t(get_u32(p + 4)) << 32); }
 
-std::size_t dtype_size(const std::string &d) {
-  if (d == "float64" || d == "int64") return 8;
-  if (d == "float32" || d == "int32") return 4;
-  if (d == "uint8" || d == "bool") return 1;
-  fail("unsupported dtype " + d);
+// Bytes per element of the dtypes of format version 1 (docs/FORMAT.md:50-62);
+// 0 for anything else.
+std::size_t element_size(const std::string &dtype) {
+  static const std::pair<const char *, std::size_t> table[] = {
+      {"float64", 8}, {"int64", 8}, {"float32", 4}, {"int32", 4}, {"uint8", 1}, {"bool", 1}};
+  for (const auto &e : table)
+    if (dtype == e.first) return e.second;
+  return 0;
 }
 
 }  // namespace
 
 // ------------------------------------------------------------------ Json API
-Json Json::parse(const std::string &text) { return Parser(text).document(); }
+Json Json::parse_canonical(const std::string &text) { return CanonicalReader(text).run(); }
 const Json *Json::find(const std::string &key) const {
   if (kind != Object) return nullptr;
-  const auto it = obj.find(key);
-  return it == obj.end() ? nullptr : &it->second;
+  const auto it = std::lower_bound(obj.begin(), obj.end(), key,
+                                   [](const std::pair<std::string, Json> &m, const std::string &k) { return m.first < k; });
+  return it != obj.end() && it->first == key ? &it->second : nullptr;
 }
 const Json &Json::at(const std::string &key) const {
   const Json *j = find(key);
-  if (!j) fail("missing JSON key " + key);
+  if (!j) fail("manifest lacks the member '" + key + "'");
   return *j;
 }
 double Json::number() const {
-  if (kind != Number) fail("JSON value is not a number");
+  if (kind != Number) fail("manifest value '" + str + "' should be a number");
   return num;
 }
 std::uint64_t Json::uint() const {
-  const double v = number();
-  if (v < 0 || std::floor(v) != v || v > 9007199254740991.0) fail("JSON value is not an exact unsigned integer");
-  return std::uint64_t(v);
+  // from the literal's digits: a float literal ("3.0", "1e3") is not a count
+  if (kind != Number || str.empty() || str.size() > 19 || str.find_first_not_of("0123456789") != std::string::npos)
+    fail("manifest value '" + str + "' should be a non-negative integer below 10^19");
+  std::uint64_t v = 0;
+  for (const char c : str) v = v * 10 + std::uint64_t(c - '0');
+  return v;
 }
 const std::string &Json::string() const {
-  if (kind != String) fail("JSON value is not a string");
+  if (kind != String) fail("manifest value should be a string");
   return str;
 }
 bool Json::boolean() const {
-  if (kind != Bool) fail("JSON value is not a boolean");
+  if (kind != Bool) fail("manifest value should be true or false");
   return b;
 }
 
@@ -303,70 +420,118 @@ std::string Architecture::summary() const {
 // --------------------------------------------------------------- loading
 std::shared_ptr<Model> Model::load(const std::string &path) {
   std::ifstream in(path, std::ios::binary);
-  if (!in) fail("cannot open " + path);
+  if (!in) fail("cannot read the model file " + path);
   std::vector<std::uint8_t> bytes((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
   return load_bytes(std::move(bytes), path);
 }
 
+// The container of docs/FORMAT.md:12-82, checked in four passes: the fixed
+// header and both digests; the manifest text (canonical JSON) and its
+// identity fields; the tensor table, record by record; then the payload as a
+// sequence of zero gaps and tensors ordered by offset, which must tile it
+// exactly.  The first failed rule ends the load.
 std::shared_ptr<Model> Model::load_bytes(std::vector<std::uint8_t> bytes, const std::string &origin) {
-  constexpr std::size_t header = 128;
-  static const std::uint8_t magic[8] = {'S', 'O', '3', 'L', 'R', 'N', '1', 0};
-  if (bytes.size() < header) fail("file is shorter than the fixed header");
-  if (std::memcmp(bytes.data(), magic, 8) != 0) fail("wrong magic");
-  if (le32(bytes.data() + 8) != 1 || le32(bytes.data() + 12) != 0) fail("unsupported version or flags");
-  const std::uint64_t msize = le64(bytes.data() + 16), psize = le64(bytes.data() + 24);
-  if (msize > bytes.size() - header || psize != bytes.size() - header - msize) fail("header length mismatch");
-  for (std::size_t i = 96; i < 128; ++i)
-    if (bytes[i] != 0) fail("nonzero reserved header bytes");
-  const std::uint8_t *mdata = bytes.data() + header, *pdata = mdata + msize;
-  const auto md = sha256(mdata, msize), pd = sha256(pdata, psize);
-  if (std::memcmp(md.data(), bytes.data() + 32, 32) != 0) fail("manifest SHA-256 mismatch");
-  if (std::memcmp(pd.data(), bytes.data() + 64, 32) != 0) fail("payload SHA-256 mismatch");
+  constexpr std::size_t kHeaderBytes = 128;
+  const std::size_t file_size = bytes.size();
+  // -- pass 1: header
+  if (file_size < kHeaderBytes)
+    fail("file of " + std::to_string(file_size) + " bytes cannot hold the 128-byte header");
+  const std::uint8_t *h = bytes.data();
+  if (std::memcmp(h, "SO3LRN1\0", 8) != 0) fail("header magic is not SO3LRN1\\0");
+  const std::uint32_t version = get_u32(h + 8), flags = get_u32(h + 12);
+  if (version != 1 || flags != 0)
+    fail("header declares version " + std::to_string(version) + ", flags " + std::to_string(flags) +
+         "; this reader takes version 1 with flags 0");
+  if (std::any_of(h + 96, h + kHeaderBytes, [](std::uint8_t c) { return c != 0; }))
+    fail("header bytes 96..127 are reserved and must be zero");
+  const std::uint64_t man_len = get_u64(h + 16), pay_len = get_u64(h + 24);
+  const std::uint64_t body = file_size - kHeaderBytes;
+  if (man_len > body || pay_len != body - man_len)
+    fail("header sizes (manifest " + std::to_string(man_len) + ", payload " + std::to_string(pay_len) +
+         ") do not add up to the " + std::to_string(body) + " bytes after the header");
+  const std::uint8_t *man = h + kHeaderBytes, *pay = man + man_len;
+  if (std::memcmp(sha256(man, man_len).data(), h + 32, 32) != 0) fail("manifest digest does not match the header");
+  if (std::memcmp(sha256(pay, pay_len).data(), h + 64, 32) != 0) fail("payload digest does not match the header");
 
+  // -- pass 2: manifest text and identity
   auto m = std::make_shared<Model>();
-  m->payload_begin_ = header + msize;
-  m->manifest_ = Json::parse(std::string(reinterpret_cast<const char *>(mdata), msize));
+  m->payload_begin_ = kHeaderBytes + man_len;
+  m->manifest_ = Json::parse_canonical(std::string(reinterpret_cast<const char *>(man), man_len));
   const Json &mf = m->manifest_;
-  if (mf.at("format").string() != "so3lr-native" || mf.at("format_version").uint() != 1)
-    fail("manifest format mismatch");
-  if (mf.at("endianness").string() != "little" || mf.at("tensor_alignment").uint() != 64)
-    fail("manifest endianness/alignment mismatch");
-  if (mf.at("model_family").string() != "SO3LR") fail("wrong model family");
-
-  std::set<std::string> names;
-  std::size_t prev_end = 0, total = 0;
-  for (const Json &rec : mf.at("tensors").arr) {
-    Tensor t;
-    const std::string name = rec.at("name").string();
-    t.state_key = rec.at("state_key").string();
-    t.dtype = rec.at("dtype").string();
-    t.offset = rec.at("offset").uint();
-    t.nbytes = rec.at("nbytes").uint();
-    std::size_t elems = 1;
-    for (const Json &e : rec.at("shape").arr) {
-      const std::size_t x = e.uint();
-      if (x != 0 && elems > (std::size_t(-1) / x)) fail("tensor shape overflow");
-      elems *= x;
-      t.shape.push_back(x);
-    }
-    if (!names.insert(name).second || m->tensors_.count(t.state_key)) fail("duplicate tensor name/state key");
-    if (t.offset % 64 != 0 || t.nbytes != elems * dtype_size(t.dtype)) fail("tensor alignment/size mismatch");
-    if (t.offset < prev_end || t.offset > psize || t.nbytes > psize - t.offset) fail("tensor overlap/range error");
-    for (std::size_t q = prev_end; q < t.offset; ++q)
-      if (pdata[q] != 0) fail("nonzero payload padding");
-    if (sha256_hex(pdata + t.offset, t.nbytes) != rec.at("sha256").string()) fail("per-tensor SHA-256 mismatch");
-    prev_end = t.offset + t.nbytes;
-    total += t.nbytes;
-    m->tensors_.emplace(t.state_key, t);
+  struct Expect {
+    const char *key, *text;
+    std::uint64_t count;  // compared when text is null
+  };
+  static const Expect identity[] = {{"format", "so3lr-native", 0},     {"format_version", nullptr, 1},
+                                    {"endianness", "little", 0},       {"tensor_alignment", nullptr, 64},
+                                    {"model_family", "SO3LR", 0}};
+  for (const Expect &e : identity) {
+    const Json &v = mf.at(e.key);
+    const bool ok = e.text ? (v.kind == Json::String && v.str == e.text) : (v.kind == Json::Number && v.uint() == e.count);
+    if (!ok)
+      fail(std::string("manifest '") + e.key + "' must be " + (e.text ? e.text : std::to_string(e.count)));
   }
-  if (prev_end != psize) fail("unreferenced trailing payload bytes");
-  if (mf.at("tensor_count").uint() != m->tensors_.size() || mf.at("tensor_bytes").uint() != total)
-    fail("tensor totals mismatch");
+
+  // -- pass 3: tensor table (names sorted and unique, as the format requires)
+  const Json &table = mf.at("tensors");
+  if (table.kind != Json::Array) fail("manifest 'tensors' must be an array");
+  std::vector<Tensor> recs;
+  std::set<std::string> keys;
+  std::string last_name;
+  std::uint64_t byte_total = 0;
+  for (const Json &rec : table.arr) {
+    const std::string name = rec.at("name").string();
+    if (!recs.empty() && !(last_name < name))
+      fail("tensor table: '" + name + "' is out of order or repeated (names must increase strictly)");
+    last_name = name;
+    Tensor t;
+    t.state_key = rec.at("state_key").string();
+    if (!keys.insert(t.state_key).second) fail("tensor table: state key '" + t.state_key + "' appears twice");
+    t.dtype = rec.at("dtype").string();
+    const std::size_t esize = element_size(t.dtype);
+    if (esize == 0) fail("tensor '" + name + "': dtype '" + t.dtype + "' is not a version-1 dtype");
+    std::uint64_t elems = 1;
+    for (const Json &dim : rec.at("shape").arr) {
+      const std::uint64_t d = dim.uint();
+      if (d != 0 && elems > (std::uint64_t(1) << 62) / d) fail("tensor '" + name + "': shape too large");
+      elems *= d;
+      t.shape.push_back(std::size_t(d));
+    }
+    t.offset = std::size_t(rec.at("offset").uint());
+    t.nbytes = std::size_t(rec.at("nbytes").uint());
+    if (t.nbytes != elems * esize)
+      fail("tensor '" + name + "': " + std::to_string(t.nbytes) + " bytes recorded, shape and dtype need " +
+           std::to_string(elems * esize));
+    if (t.offset % 64 != 0) fail("tensor '" + name + "': offset " + std::to_string(t.offset) + " is not 64-byte aligned");
+    if (t.offset > pay_len || t.nbytes > pay_len - t.offset) fail("tensor '" + name + "' reaches past the payload");
+    if (sha256_hex(pay + t.offset, t.nbytes) != rec.at("sha256").string())
+      fail("tensor '" + name + "': digest does not match its bytes");
+    byte_total += t.nbytes;
+    recs.push_back(std::move(t));
+  }
+  if (mf.at("tensor_count").uint() != recs.size() || mf.at("tensor_bytes").uint() != byte_total)
+    fail("manifest tensor_count / tensor_bytes disagree with the tensor table");
+
+  // -- pass 4: payload coverage, in offset order: zero gaps, no overlap,
+  // nothing after the last tensor
+  std::vector<const Tensor *> by_offset;
+  for (const Tensor &t : recs) by_offset.push_back(&t);
+  std::stable_sort(by_offset.begin(), by_offset.end(),
+                   [](const Tensor *a, const Tensor *b) { return a->offset < b->offset; });
+  std::size_t cursor = 0;
+  for (const Tensor *t : by_offset) {
+    if (t->offset < cursor)
+      fail("payload: tensor '" + t->state_key + "' at offset " + std::to_string(t->offset) + " overlaps the one before");
+    if (std::any_of(pay + cursor, pay + t->offset, [](std::uint8_t c) { return c != 0; }))
+      fail("payload: alignment gap before tensor '" + t->state_key + "' is not zero-filled");
+    cursor = t->offset + t->nbytes;
+  }
+  if (cursor != pay_len) fail("payload: " + std::to_string(pay_len - cursor) + " bytes after the last tensor belong to none");
+  for (Tensor &t : recs) m->tensors_.emplace(t.state_key, std::move(t));
   m->bytes_ = std::move(bytes);
   m->describe_and_negotiate(origin);
   return m;
 }
-
 const Tensor &Model::tensor(const std::string &key) const {
   const auto it = tensors_.find(key);
   if (it == tensors_.end()) fail("missing tensor " + key);
@@ -568,22 +733,38 @@ std::vector<double> ChargeSpin::table(const std::int64_t counts[119], double tot
   return out;
 }
 
+// (Q, M) against the composition.  With Z_tot the nuclear charge, the
+// system has n_e = Z_tot - Q electrons, of which M - 1 are unpaired; the rest
+// pair up, so n_e - (M - 1) must be even and non-negative, i.e. n_e + M is
+// odd and M - 1 <= n_e.  Q and M must be whole numbers; M >= 1.  (The rule
+// of src/so3lr_charge_spin.cpp:116-141.)
 std::string charge_multiplicity_problem(const std::int64_t counts[119], double q, double mult) {
-  if (!std::isfinite(q) || std::round(q) != q) return "the total charge must be an integer";
-  if (!std::isfinite(mult) || std::round(mult) != mult || mult < 1.0)
-    return "the spin multiplicity must be an integer >= 1";
-  std::int64_t protons = 0;
-  for (int zz = 1; zz <= 118; ++zz) protons += counts[zz] * zz;
-  const std::int64_t electrons = protons - std::int64_t(q);
-  const std::int64_t unpaired = std::int64_t(mult) - 1;
-  if (electrons < 0) return "the total charge leaves a negative number of electrons";
-  if (unpaired > electrons)
-    return "multiplicity " + std::to_string(std::int64_t(mult)) +
-           " needs more unpaired electrons than the system's " + std::to_string(electrons) + " electrons";
-  if ((electrons - unpaired) % 2 != 0)
-    return std::to_string(electrons) + " electrons cannot have multiplicity " +
-           std::to_string(std::int64_t(mult)) +
-           " (an even electron count needs an odd multiplicity and vice versa)";
+  constexpr double kWhole = 9007199254740992.0;  // 2^53: beyond it a double is no longer a count
+  auto whole = [&](double v) { return std::isfinite(v) && std::fabs(v) < kWhole && std::nearbyint(v) == v; };
+  std::ostringstream why;
+  if (!whole(q)) {
+    why << "total charge " << q << " is not a whole number of elementary charges";
+    return why.str();
+  }
+  if (!whole(mult) || mult < 1.0) {
+    why << "spin multiplicity " << mult << " is not a whole number of at least 1";
+    return why.str();
+  }
+  std::int64_t z_total = 0;
+  for (int zz = 1; zz <= 118; ++zz) z_total += counts[zz] * zz;
+  const std::int64_t n_e = z_total - std::int64_t(q), m = std::int64_t(mult);
+  if (n_e < 0) {
+    why << "charge " << std::int64_t(q) << " removes more electrons than the " << z_total << " the nuclei bring";
+    return why.str();
+  }
+  if (m - 1 > n_e) {
+    why << "multiplicity " << m << " means " << (m - 1) << " unpaired electrons, but the system has only " << n_e;
+    return why.str();
+  }
+  if ((n_e + m) % 2 == 0) {
+    why << "with " << n_e << " electrons the multiplicity must be " << (n_e % 2 ? "even" : "odd") << ", not " << m;
+    return why.str();
+  }
   return std::string();
 }
 

@@ -1,8 +1,9 @@
 // .so3lr model reader, architecture descriptor and capability check (host).
 //
-// Format and rejection rules: source/so3lr-lammps-native/docs/FORMAT.md:12-82,
-// enforced as in src/native_model.cpp:325-406 of the reference.  The
-// architecture fields follow src/so3lr_architecture.cpp:296-451, and the
+// Format and rejection rules: source/so3lr-lammps-native/docs/FORMAT.md:12-82
+// (the reader replaces NativeModel::load, src/native_model.cpp:325-406, and
+// also enforces the canonical manifest encoding that the format demands).
+// The architecture fields follow src/so3lr_architecture.cpp:296-451, and the
 // capability refusal follows src/so3lr_capabilities.cpp:46-289, narrowed to
 // what the gfx950 kernels of this library implement.
 #pragma once
@@ -16,16 +17,22 @@
 
 namespace so3lr_amd {
 
-// --- minimal JSON value ---------------------------------------------------
+// --- manifest JSON value --------------------------------------------------
+// The manifest is canonical JSON (docs/FORMAT.md: sorted keys, compact
+// separators, ASCII with \u escapes), so members arrive in strictly
+// increasing key order and are kept that way (lookups bisect).  A number
+// keeps its source text: integers are read from the digits exactly, never
+// through a double.
 struct Json {
   enum Kind { Null, Bool, Number, String, Array, Object } kind = Null;
   bool b = false;
   double num = 0.0;
-  std::string str;
+  std::string str;  // String: decoded UTF-8; Number: the literal as written
   std::vector<Json> arr;
-  std::map<std::string, Json> obj;
+  std::vector<std::pair<std::string, Json>> obj;  // sorted by key, keys unique
 
-  static Json parse(const std::string &text);
+  // Throws std::runtime_error unless `text` is canonical JSON.
+  static Json parse_canonical(const std::string &text);
   const Json &at(const std::string &key) const;
   const Json *find(const std::string &key) const;
   double number() const;

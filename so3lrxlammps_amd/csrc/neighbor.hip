@@ -37,7 +37,7 @@ namespace so3lr_amd {
   do {                                                                                    \
     hipError_t err_ = (expr);                                                             \
     if (err_ != hipSuccess)                                                               \
-      throw std::runtime_error(std::string("HIP error in ") + #expr + ": " +             \
+      throw DeviceError(std::string("HIP error in ") + #expr + ": " +             \
                                hipGetErrorString(err_));                                  \
   } while (0)
 

@@ -107,19 +107,19 @@ def test_corrupt_payload_rejected(tmp_path):
     def flip(b):
         b[-1] ^= 0xFF
     rc, msg = _create(_rewrite(tmp_path, mutate_bytes=flip))
-    assert rc == _lib.ERR_MODEL and "payload SHA-256 mismatch" in msg
+    assert rc == _lib.ERR_MODEL and "payload digest does not match" in msg
 
 
 def test_wrong_magic_rejected(tmp_path):
     def magic(b):
         b[0:8] = b"NOTSO3LR"
     rc, msg = _create(_rewrite(tmp_path, mutate_bytes=magic))
-    assert rc == _lib.ERR_MODEL and "wrong magic" in msg
+    assert rc == _lib.ERR_MODEL and "magic" in msg
 
 
 def test_missing_file_rejected():
     rc, msg = _create("/nonexistent/model.so3lr")
-    assert rc == _lib.ERR_MODEL and "cannot open" in msg
+    assert rc == _lib.ERR_MODEL and "cannot read" in msg
 
 
 @pytest.mark.parametrize("key,value,feature", [
@@ -154,3 +154,198 @@ def test_lammps_lists_match_brute_force():
     # every ghost row sits at its owner's position plus a lattice vector
     xr = L.rows_positions(pos)
     assert np.allclose(xr[:len(pos)], pos)
+
+
+def _with_manifest_bytes(tmp_path, edit_text=None, edit_manifest=None, edit_payload=None):
+    """The shipped model with its manifest re-encoded canonically (after
+    edit_manifest) and then edited as text (edit_text), its payload edited
+    (edit_payload), and both digests and sizes recomputed, so only the rule
+    under test is broken."""
+    data = bytes(open(support.MODEL, "rb").read())
+    msize = struct.unpack("<Q", data[16:24])[0]
+    manifest = json.loads(data[128:128 + msize])
+    payload = bytearray(data[128 + msize:])
+    if edit_manifest:
+        edit_manifest(manifest, payload)
+    if edit_payload:
+        edit_payload(manifest, payload)
+    text = json.dumps(manifest, sort_keys=True, separators=(",", ":"), ensure_ascii=True)
+    if edit_text:
+        text = edit_text(text)
+    mbytes = text.encode("utf-8")
+    header = bytearray(data[:128])
+    header[16:24] = struct.pack("<Q", len(mbytes))
+    header[24:32] = struct.pack("<Q", len(payload))
+    header[32:64] = hashlib.sha256(mbytes).digest()
+    header[64:96] = hashlib.sha256(bytes(payload)).digest()
+    p = tmp_path / "m.so3lr"
+    p.write_bytes(bytes(header) + mbytes + bytes(payload))
+    return str(p)
+
+
+def test_canonical_reencoding_loads(tmp_path):
+    rc, msg = _create(_with_manifest_bytes(tmp_path))
+    assert rc in (_lib.OK, _lib.ERR_DEVICE), msg
+
+
+@pytest.mark.parametrize("edit,why", [
+    (lambda t: t.replace('{"architecture":', '{ "architecture":', 1), "member name"),
+    (lambda t: t.replace(',"endianness"', ', "endianness"', 1), "not a value"),
+    (lambda t: t.replace('"lr_pair_scale":0.5', '"lr_pair_scale":0.50', 1), "shortest repr"),
+    (lambda t: t.replace('"lr_pair_scale":0.5', '"lr_pair_scale":5e-1', 1), "shortest repr"),
+    (lambda t: t.replace('"layer_norm_epsilon":1e-06', '"layer_norm_epsilon":1E-06', 1), "shortest repr"),
+    (lambda t: t.replace('"tensor_alignment":64', '"tensor_alignment":064', 1), "leading zero"),
+    (lambda t: t.replace('"format":"so3lr-native"', '"format":"so3lr\\u002dnative"', 1), "\\u escape"),
+    (lambda t: t.replace('"format":"so3lr-native"', '"format":"so3lr\\/native"', 1), "escape the canonical encoder"),
+    (lambda t: t.replace('"format":"so3lr-native"', '"format":"so3lr-nativé"', 1), "printable ASCII"),
+    (lambda t: t + " ", "printable ASCII"),
+    (lambda t: t + "{}", "after the top-level value"),
+    (lambda t: t[:-1], "ends inside a container"),
+])
+def test_noncanonical_manifest_rejected(tmp_path, edit, why):
+    """docs/FORMAT.md:68-82: a reader must reject noncanonical or malformed
+    JSON; canonical is the exporter's json.dumps(sort_keys=True,
+    separators=(",", ":"), ensure_ascii=True)."""
+    rc, msg = _create(_with_manifest_bytes(tmp_path, edit_text=edit))
+    assert rc == _lib.ERR_MODEL, msg
+    assert "canonical JSON" in msg or why in msg, msg
+
+
+def test_unsorted_keys_rejected(tmp_path):
+    def swap(t):
+        # move "schema" in front of "format": keys out of order, still valid JSON
+        obj = json.loads(t)
+        items = list(obj.items())
+        items.insert(0, items.pop([k for k, _ in items].index("schema")))
+        return "{" + ",".join(json.dumps(k) + ":" + json.dumps(v, sort_keys=True, separators=(",", ":"))
+                              for k, v in items) + "}"
+    rc, msg = _create(_with_manifest_bytes(tmp_path, edit_text=swap))
+    assert rc == _lib.ERR_MODEL and "strictly increasing" in msg, msg
+
+
+def _first_tensors(m):
+    return m["tensors"][0], m["tensors"][1]
+
+
+@pytest.mark.parametrize("case,expect", [
+    ("version", "version 2"),
+    ("reserved", "reserved"),
+    ("sizes", "do not add up"),
+    ("manifest_digest", "manifest digest"),
+    ("dup_name", "out of order or repeated"),
+    ("dup_key", "appears twice"),
+    ("dtype", "not a version-1 dtype"),
+    ("unaligned", "not 64-byte aligned"),
+    ("overlap", "overlaps"),
+    ("padding", "not zero-filled"),
+    ("tensor_digest", "digest does not match its bytes"),
+    ("trailing", "belong to none"),
+    ("nbytes", "bytes recorded"),
+    ("totals", "tensor_count / tensor_bytes"),
+    ("count_float", "non-negative integer"),
+    ("range", "reaches past the payload"),
+])
+def test_container_rules(tmp_path, case, expect):
+    """Each rejection rule of docs/FORMAT.md:68-82, one at a time."""
+    em = ep = et = None
+    post = None
+    if case == "version":
+        post = lambda b: b.__setitem__(slice(8, 12), struct.pack("<I", 2))
+    elif case == "reserved":
+        post = lambda b: b.__setitem__(100, 1)
+    elif case == "sizes":
+        post = lambda b: b.__setitem__(slice(24, 32), struct.pack("<Q", struct.unpack("<Q", bytes(b[24:32]))[0] + 1))
+    elif case == "manifest_digest":
+        post = lambda b: b.__setitem__(40, b[40] ^ 1)
+    elif case == "dup_name":
+        def em(m, p):
+            a, b = _first_tensors(m)
+            b["name"] = a["name"]
+    elif case == "dup_key":
+        def em(m, p):
+            a, b = _first_tensors(m)
+            b["state_key"] = a["state_key"]
+    elif case == "dtype":
+        def em(m, p):
+            m["tensors"][0]["dtype"] = "float16"
+    elif case == "unaligned":
+        def em(m, p):
+            m["tensors"][1]["offset"] += 8
+    elif case == "overlap":
+        def em(m, p):
+            a, b = _first_tensors(m)
+            b["offset"] = a["offset"]
+            b["sha256"] = hashlib.sha256(bytes(p[b["offset"]:b["offset"] + b["nbytes"]])).hexdigest()
+    elif case == "padding":
+        def ep(m, p):
+            a, b = _first_tensors(m)
+            gap = a["offset"] + a["nbytes"]
+            assert gap < b["offset"], "needs a padded gap"
+            p[gap] = 7
+    elif case == "tensor_digest":
+        def ep(m, p):
+            t = m["tensors"][0]
+            p[t["offset"]] ^= 0x40
+    elif case == "trailing":
+        def ep(m, p):
+            p.extend(b"\0" * 64)
+    elif case == "nbytes":
+        def em(m, p):
+            m["tensors"][0]["nbytes"] += 8
+    elif case == "totals":
+        def em(m, p):
+            m["tensor_bytes"] += 1
+    elif case == "count_float":
+        et = lambda t: t.replace('"tensor_alignment":64', '"tensor_alignment":64.0', 1)
+    elif case == "range":
+        def em(m, p):
+            t = m["tensors"][-1]
+            t["offset"] = (len(p) + 127) // 64 * 64
+    path = _with_manifest_bytes(tmp_path, edit_text=et, edit_manifest=em, edit_payload=ep)
+    if post:
+        b = bytearray(open(path, "rb").read())
+        post(b)
+        open(path, "wb").write(bytes(b))
+    rc, msg = _create(path)
+    assert rc == _lib.ERR_MODEL, msg
+    assert expect in msg, msg
+
+
+def test_binding_refuses_bad_device_buffers():
+    """The ctypes binding checks what the C ABI cannot see (device, dtype,
+    contiguity, size) before any pointer reaches a kernel."""
+    import torch
+    with pytest.raises(ValueError, match="GPU tensor"):
+        _lib.device_f64(torch.zeros(6, dtype=torch.float64), 6, "positions")
+    with pytest.raises(ValueError, match="GPU tensor"):
+        _lib.device_f64(np.zeros(6), 6, "positions")
+    with pytest.raises(ValueError, match="required"):
+        _lib.device_f64(None, 6, "forces")
+
+    class FakeCuda:  # the attributes a torch CUDA tensor exposes
+        def __init__(self, dtype, contiguous, n):
+            self.is_cuda, self.dtype, self._c, self._n = True, dtype, contiguous, n
+
+        def is_contiguous(self):
+            return self._c
+
+        def numel(self):
+            return self._n
+
+        def data_ptr(self):
+            return 0
+
+    with pytest.raises(ValueError, match="float64"):
+        _lib.device_f64(FakeCuda(torch.float32, True, 6), 6, "positions")
+    with pytest.raises(ValueError, match="contiguous"):
+        _lib.device_f64(FakeCuda(torch.float64, False, 6), 6, "positions")
+    with pytest.raises(ValueError, match="hold 6 values"):
+        _lib.device_f64(FakeCuda(torch.float64, True, 3), 6, "positions")
+    _lib.device_f64(FakeCuda(torch.float64, True, 6), 6, "positions")
+
+    ctx = object.__new__(_lib.Context)  # no device: the checks run before any library call
+    ctx.n, ctx.rows, ctx._h = 2, 2, None
+    with pytest.raises(ValueError, match="forces"):
+        ctx.compute_device(FakeCuda(torch.float64, True, 6), FakeCuda(torch.float64, True, 5))
+    with pytest.raises(ValueError, match="one entry more"):
+        ctx.set_images([8, 1, 1], [0, 2], [0.0, 0.0], [1.0, 1.0])

@@ -157,6 +157,13 @@ def test_refusals(ctx):
     with pytest.raises(_lib.SO3LRError) as err:
         ctx.set_images(np.array([8, 8], dtype=np.int32), [0, 2, 2], [0.0, 0.0], [3.0, 1.0])
     assert err.value.code == _lib.ERR_ARGUMENT
+    # offsets that overshoot the atom count and come back down: refused before
+    # any of them is used as an index (host-side check, no kernel runs)
+    z3 = np.array([8, 1, 1], dtype=np.int32)
+    off = np.array([0, 5, 3], dtype=np.int64)
+    qm = np.zeros(2)
+    rc = ctx._lib.so3lr_set_images(ctx._h, 3, _lib.ptr(z3), 2, _lib.ptr(off), _lib.ptr(qm), _lib.ptr(qm + 1.0))
+    assert rc == _lib.ERR_ARGUMENT, ctx._lib.so3lr_last_error(ctx._h)
     # the context stays usable after the refusals
     e2, f2, _, _, _ = _hip_single_point(ctx, z, pos, box, 0, 3)
     assert e2 == e and np.array_equal(f2, f)
