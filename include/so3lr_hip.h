@@ -152,6 +152,25 @@ int so3lr_compute_device(so3lr_ctx *ctx, const double *x_rows_dev, int flags,
                          double *virial);
 
 /*
+ * As so3lr_compute_device, allocating nothing: no counterpart in the
+ * reference; for callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc after set-up).  Every work buffer of
+ * the evaluation is a slice of one static device array of 256 MiB that the
+ * library holds on each device it runs on; a system that needs more work
+ * space is refused with SO3LR_ERR_ARGUMENT (so3lr_compute_device has no such
+ * limit).  The topology must have been set before (so3lr_set_topology or
+ * so3lr_reneighbor_device, which allocate).  No graph is captured and no
+ * event recorded; the call waits for its stream at the end (energy and
+ * virial read-back), as so3lr_compute_device does.  All contexts on one
+ * device share that device's array and the previous call's contents stay in
+ * it: calls that overlap on one device race.  so3lr_last_terms and
+ * so3lr_last_vatom refuse (SO3LR_ERR_STATE) after this call.
+ */
+int so3lr_compute_device_noalloc(so3lr_ctx *ctx, const double *x_rows_dev, int flags,
+                                 double *f_owned_dev, double *eatom_dev, double *energy,
+                                 double *virial);
+
+/*
  * HBM-resident reneighbor (no counterpart in the reference, where LAMMPS
  * builds the lists on the host): builds the same candidate sets -- every
  * periodic image within cutoff + skin, SR and LR -- on the GPU from the owned

@@ -20,7 +20,7 @@ LIST_FULL, LIST_HALF = 0, 1
 # every symbol include/so3lr_hip.h declares
 HIP_SYMBOLS = ["so3lr_create", "so3lr_destroy", "so3lr_last_error", "so3lr_cutoff",
                "so3lr_atomic_number", "so3lr_check_system", "so3lr_set_system", "so3lr_set_images",
-               "so3lr_set_topology", "so3lr_compute", "so3lr_compute_device",
+               "so3lr_set_topology", "so3lr_compute", "so3lr_compute_device", "so3lr_compute_device_noalloc",
                "so3lr_reneighbor_device", "so3lr_set_box",
                "so3lr_set_stream", "so3lr_last_terms", "so3lr_last_vatom", "so3lr_graph_stats",
                "so3lr_kernel_timing", "so3lr_kernel_timing_read", "so3lr_device_bytes"]
@@ -82,6 +82,7 @@ def hip():
         lib.so3lr_set_topology.argtypes = [_P, _I64, _P, ctypes.c_int, _I64, _P, _P, _P, _I64, _P, _P, _P]
         lib.so3lr_compute.argtypes = [_P, _P, ctypes.c_int, _P, _P, _P, _P]
         lib.so3lr_compute_device.argtypes = [_P, _P, ctypes.c_int, _P, _P, _P, _P]
+        lib.so3lr_compute_device_noalloc.argtypes = [_P, _P, ctypes.c_int, _P, _P, _P, _P]
         lib.so3lr_set_stream.argtypes = [_P, _P]
         lib.so3lr_reneighbor_device.argtypes = [_P, _P, _P, _P, _P, _D]
         lib.so3lr_set_box.argtypes = [_P, _P, _P]
@@ -267,6 +268,20 @@ class Context:
         w = np.zeros(6)
         flags = ENERGY | VIRIAL | (EATOM if eatom_dev is not None else 0)
         self._check(self._lib.so3lr_compute_device(self._h, px, flags, pf, pe, ctypes.byref(e), ptr(w)))
+        return e.value, w
+
+    def compute_device_noalloc(self, x_rows_dev, f_dev, eatom_dev=None, stream=None):
+        """As compute_device through so3lr_compute_device_noalloc: the work
+        buffers are slices of the library's static device array."""
+        px = device_f64(x_rows_dev, 3 * self.rows, "positions")
+        pf = device_f64(f_dev, 3 * self.n, "forces")
+        pe = None if eatom_dev is None else device_f64(eatom_dev, self.n, "per-atom energies")
+        if stream is not None:
+            self._check(self._lib.so3lr_set_stream(self._h, ctypes.c_void_p(stream)))
+        e = ctypes.c_double()
+        w = np.zeros(6)
+        flags = ENERGY | VIRIAL | (EATOM if eatom_dev is not None else 0)
+        self._check(self._lib.so3lr_compute_device_noalloc(self._h, px, flags, pf, pe, ctypes.byref(e), ptr(w)))
         return e.value, w
 
     def reneighbor_device(self, x_owned_dev, lo, hi, periodic, skin, stream=None):

@@ -189,6 +189,20 @@ int so3lr_compute_device(so3lr_ctx *ctx, const double *x_rows_dev, int flags, do
   });
 }
 
+int so3lr_compute_device_noalloc(so3lr_ctx *ctx, const double *x_rows_dev, int flags, double *f_dev,
+                                 double *eatom_dev, double *energy, double *virial) {
+  if (ctx && check_flags(flags) != SO3LR_OK) {
+    ctx->error = "SO3LR: unknown compute flags";
+    return check_flags(flags);
+  }
+  return guarded(ctx, [&] {
+    if (!x_rows_dev || !f_dev) throw std::invalid_argument("SO3LR: positions and forces are required");
+    if ((flags & SO3LR_EATOM) && !eatom_dev) throw std::invalid_argument("SO3LR: eatom requested without a buffer");
+    ctx->ev->compute_device_noalloc(x_rows_dev, flags, f_dev, (flags & SO3LR_EATOM) ? eatom_dev : nullptr, energy,
+                                    virial);
+  });
+}
+
 int so3lr_reneighbor_device(so3lr_ctx *ctx, double *x_owned_dev, const double *lo, const double *hi,
                             const int *periodic, double skin) {
   return guarded(ctx, [&] {

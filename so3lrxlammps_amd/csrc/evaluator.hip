@@ -16,10 +16,22 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <stdexcept>
 #include <utility>
 
 namespace so3lr_amd {
+
+// Work space of so3lr_compute_device_noalloc: one static array per device,
+// present from the module's load on that device until the process ends (256
+// MiB of its HBM).  Host code never names it as an address: the constructor
+// looks up this device's copy once with hipGetSymbolAddress and keeps the
+// pointer (scratch_dev_), which is what kernels and copies receive.  Every
+// no-allocation evaluation on a device shares that device's copy; the
+// contents of the previous call stay behind, and calls that overlap on one
+// device race.
+constexpr std::size_t kScratchBytes = std::size_t(256) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 #define HIP_CHECK(expr)                                                                   \
   do {                                                                                    \
@@ -30,6 +42,23 @@ namespace so3lr_amd {
   } while (0)
 
 namespace {
+
+// Address of `device`'s copy of the scratch array, looked up once per device
+// (the caller has made `device` current) and kept for the process.
+char *scratch_on_device(int device) {
+  static std::mutex mu;
+  static std::vector<char *> table;
+  std::lock_guard<std::mutex> lock(mu);
+  if (std::size_t(device) >= table.size()) table.resize(std::size_t(device) + 1, nullptr);
+  if (!table[device]) {
+    void *sp = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (se != hipSuccess || sp == nullptr)
+      throw DeviceError(std::string("HIP error in hipGetSymbolAddress(scratch): ") + hipGetErrorString(se));
+    table[device] = static_cast<char *>(sp);
+  }
+  return table[device];
+}
 
 constexpr int kWave = 64;
 constexpr int kCompactPerBlock = 1024;  // candidates per compaction block (256 threads x 4)
@@ -2184,6 +2213,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   // SO3LR_NO_GRAPH=1: always launch the kernels one by one (no graph replay)
   if (const char *ng = std::getenv("SO3LR_NO_GRAPH")) use_graphs_ = ng[0] != '1';
   HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_out_), 16 * sizeof(double), hipHostMallocDefault));
+  scratch_dev_ = scratch_on_device(device);
   stream_ = own_stream_;
   const Model &m = *model_;
   const Architecture &a = m.arch();
@@ -2585,6 +2615,18 @@ FilterMfma filter_mfma(const BlockWeights &B, const HeadWeights &H, double gamma
 
 void Evaluator::compute_device(const double *x, int flags, double *f_out, double *eatom_out, double *energy,
                                double *virial) {
+  compute_impl(x, flags, f_out, eatom_out, energy, virial, false);
+}
+
+void Evaluator::compute_device_noalloc(const double *x, int flags, double *f_out, double *eatom_out,
+                                       double *energy, double *virial) {
+  compute_impl(x, flags, f_out, eatom_out, energy, virial, true);
+}
+
+std::size_t Evaluator::scratch_capacity() { return kScratchBytes; }
+
+void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *eatom_out, double *energy,
+                             double *virial, bool from_scratch) {
   if (!topology_ready_) throw std::logic_error("SO3LR: compute called before set_topology");
   const std::int64_t N = n_, P = p_sr_, L = layers_;
   const std::size_t Nz = std::size_t(N), Pz = std::size_t(std::max<std::int64_t>(P, 1));
@@ -2597,64 +2639,140 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   if (permuted_) x = static_cast<const double *>(xn_->p);
   // --- buffers (retained capacity; all allocation happens before any work
   // is enqueued, so the sequence below can be captured into a graph) ---
-  double *xs = ensure<double>(xs_, (L + 1) * Nz * kF);
-  double *evs = ensure<double>(evs_, (L + 1) * Nz * kE);
-  double *qkv = ensure<double>(qkv_, L * Nz * 640);
-  double *aev = ensure<double>(aev_, L * Nz * kE);
-  double *n1 = ensure<double>(n1_, L * Nz * kF);
-  double *n1hat = ensure<double>(n1hat_, L * Nz * kF);
-  double *n1is = ensure<double>(n1is_, L * Nz);
-  double *hpre = ensure<double>(hpre_, L * Nz * kF);
-  double *tout = ensure<double>(tout_, L * Nz * kNI);
-  double *pre2hat = ensure<double>(pre2hat_, L * Nz * kF);
-  double *pre2is = ensure<double>(pre2is_, L * Nz);
-  double *ainv = ensure<double>(ainv_, Nz * kF);
-  double *act = ensure<double>(act_, Nz * 320);  // MLP input (128 wide) and head activations (320)
-  double *hhead = ensure<double>(hhead_, Nz * 320);
-  double *hact = act;
-  double *heff = ensure<double>(heff_, Nz);
-  double *eatom = ensure<double>(eatom_, Nz);
-  double *qraw = ensure<double>(qraw_, Nz);
-  double *q = ensure<double>(q_, Nz);
-  double *hir = ensure<double>(hir_, Nz);
-  double *qseed = ensure<double>(qseed_, Nz);
-  double *elr = ensure<double>(elr_, Nz);
-  double *dq = ensure<double>(dq_, Nz);
-  double *dh = ensure<double>(dh_, Nz);
-  double *flr = ensure<double>(flr_, Nz * 3);
-  double *vlr = ensure<double>(vlr_, Nz * 6);
-  double *parts = ensure<double>(elr_parts_, Nz * 2);
-  double *ezbl = ensure<double>(ezbl_, Nz);
-  double *gx = ensure<double>(gx_, Nz * kF);
-  double *gev = ensure<double>(gev_, Nz * kE);
-  double *gainv = ensure<double>(gainv_, Nz * kF);
-  double *gaev = ensure<double>(gaev_, Nz * kE);
-  double *gqkv = ensure<double>(gqkv_, Nz * 640);
-  double *ghead = ensure<double>(ghead_, Nz * 320);
-  double *fo = f_out ? f_out : ensure<double>(fout_, Nz * 3);
-  double *etot = eatom_out ? eatom_out : ensure<double>(etot_, Nz);
-  double *red = ensure<double>(red_, 16);
   const int nblk = std::max(1, ceil_div(P, kCompactPerBlock));
-  int *blk = ensure<int>(blk_count_, nblk);
-  int *nact = ensure<int>(n_active_, 1);
-  int *c2a = ensure<int>(cand2act_, Pz);
-  int *pa = ensure<int>(pa_, 2 * Pz);
-  double *pv = ensure<double>(pv_, 3 * Pz);
-  double *pr = ensure<double>(pr_, Pz);
-  double *pY = ensure<double>(pY_, kE * Pz);
-  double *pfc = ensure<double>(pfc_, Pz);
-  double *pzbl = ensure<double>(pzbl_, 2 * Pz);
-  double *ps = ensure<double>(ps_, L * 4 * Pz);
-  double *pf = ensure<double>(pf_, L * 256 * Pz);
-  double *palpha = ensure<double>(palpha_, L * 16 * Pz);
-  double *df = ensure<double>(df_, 256 * Pz);
-  double *dfc = ensure<double>(dfc_, Pz);
-  double *ds = ensure<double>(ds_, 4 * Pz);
-  double *dr = ensure<double>(dr_, Pz);
-  double *dY = ensure<double>(dY_, kE * Pz);
-  double *pg = ensure<double>(pg_, 3 * Pz);
-  int *iact = ensure<int>(iact_, 2 * Pz), *iother = ensure<int>(iother_, 2 * Pz);
-  double *partial = ensure<double>(red_part_, 9 * kReduceBlocks);
+  double *xs = nullptr;
+  double *evs = nullptr;
+  double *qkv = nullptr;
+  double *aev = nullptr;
+  double *n1 = nullptr;
+  double *n1hat = nullptr;
+  double *n1is = nullptr;
+  double *hpre = nullptr;
+  double *tout = nullptr;
+  double *pre2hat = nullptr;
+  double *pre2is = nullptr;
+  double *ainv = nullptr;
+  double *act = nullptr;
+  double *hhead = nullptr;
+  double *heff = nullptr;
+  double *eatom = nullptr;
+  double *qraw = nullptr;
+  double *q = nullptr;
+  double *hir = nullptr;
+  double *qseed = nullptr;
+  double *elr = nullptr;
+  double *dq = nullptr;
+  double *dh = nullptr;
+  double *flr = nullptr;
+  double *vlr = nullptr;
+  double *parts = nullptr;
+  double *ezbl = nullptr;
+  double *gx = nullptr;
+  double *gev = nullptr;
+  double *gainv = nullptr;
+  double *gaev = nullptr;
+  double *gqkv = nullptr;
+  double *ghead = nullptr;
+  double *fo = nullptr;
+  double *etot = nullptr;
+  double *red = nullptr;
+  int *blk = nullptr;
+  int *nact = nullptr;
+  int *c2a = nullptr;
+  int *pa = nullptr;
+  double *pv = nullptr;
+  double *pr = nullptr;
+  double *pY = nullptr;
+  double *pfc = nullptr;
+  double *pzbl = nullptr;
+  double *ps = nullptr;
+  double *pf = nullptr;
+  double *palpha = nullptr;
+  double *df = nullptr;
+  double *dfc = nullptr;
+  double *ds = nullptr;
+  double *dr = nullptr;
+  double *dY = nullptr;
+  double *pg = nullptr;
+  int *iact = nullptr, *iother = nullptr;
+  double *partial = nullptr;
+  auto carve_all = [&] {
+    xs = take<double>(xs_, (L + 1) * Nz * kF);
+    evs = take<double>(evs_, (L + 1) * Nz * kE);
+    qkv = take<double>(qkv_, L * Nz * 640);
+    aev = take<double>(aev_, L * Nz * kE);
+    n1 = take<double>(n1_, L * Nz * kF);
+    n1hat = take<double>(n1hat_, L * Nz * kF);
+    n1is = take<double>(n1is_, L * Nz);
+    hpre = take<double>(hpre_, L * Nz * kF);
+    tout = take<double>(tout_, L * Nz * kNI);
+    pre2hat = take<double>(pre2hat_, L * Nz * kF);
+    pre2is = take<double>(pre2is_, L * Nz);
+    ainv = take<double>(ainv_, Nz * kF);
+    act = take<double>(act_, Nz * 320); // MLP input (128 wide) and head activations (320)
+    hhead = take<double>(hhead_, Nz * 320);
+    heff = take<double>(heff_, Nz);
+    eatom = take<double>(eatom_, Nz);
+    qraw = take<double>(qraw_, Nz);
+    q = take<double>(q_, Nz);
+    hir = take<double>(hir_, Nz);
+    qseed = take<double>(qseed_, Nz);
+    elr = take<double>(elr_, Nz);
+    dq = take<double>(dq_, Nz);
+    dh = take<double>(dh_, Nz);
+    flr = take<double>(flr_, Nz * 3);
+    vlr = take<double>(vlr_, Nz * 6);
+    parts = take<double>(elr_parts_, Nz * 2);
+    ezbl = take<double>(ezbl_, Nz);
+    gx = take<double>(gx_, Nz * kF);
+    gev = take<double>(gev_, Nz * kE);
+    gainv = take<double>(gainv_, Nz * kF);
+    gaev = take<double>(gaev_, Nz * kE);
+    gqkv = take<double>(gqkv_, Nz * 640);
+    ghead = take<double>(ghead_, Nz * 320);
+    fo = f_out ? f_out : take<double>(fout_, Nz * 3);
+    etot = eatom_out ? eatom_out : take<double>(etot_, Nz);
+    red = take<double>(red_, 16);
+    blk = take<int>(blk_count_, nblk);
+    nact = take<int>(n_active_, 1);
+    c2a = take<int>(cand2act_, Pz);
+    pa = take<int>(pa_, 2 * Pz);
+    pv = take<double>(pv_, 3 * Pz);
+    pr = take<double>(pr_, Pz);
+    pY = take<double>(pY_, kE * Pz);
+    pfc = take<double>(pfc_, Pz);
+    pzbl = take<double>(pzbl_, 2 * Pz);
+    ps = take<double>(ps_, L * 4 * Pz);
+    pf = take<double>(pf_, L * 256 * Pz);
+    palpha = take<double>(palpha_, L * 16 * Pz);
+    df = take<double>(df_, 256 * Pz);
+    dfc = take<double>(dfc_, Pz);
+    ds = take<double>(ds_, 4 * Pz);
+    dr = take<double>(dr_, Pz);
+    dY = take<double>(dY_, kE * Pz);
+    pg = take<double>(pg_, 3 * Pz);
+    iact = take<int>(iact_, 2 * Pz);
+    iother = take<int>(iother_, 2 * Pz);
+    partial = take<double>(red_part_, 9 * kReduceBlocks);
+  };
+  struct CarveReset {  // the work-buffer source goes back to the retained buffers
+    Evaluator *e;
+    ~CarveReset() { e->carve_ = Carve::Retained; }
+  } carve_reset{this};
+  if (from_scratch) {
+    carve_ = Carve::Measure;
+    carve_used_ = 0;
+    carve_all();
+    if (carve_used_ > kScratchBytes)
+      throw std::invalid_argument("SO3LR: this system needs " + std::to_string(carve_used_) +
+                                  " bytes of work space; so3lr_compute_device_noalloc has " +
+                                  std::to_string(kScratchBytes) + " (use so3lr_compute_device)");
+    carve_ = Carve::Scratch;
+    carve_base_ = scratch_dev_;
+    carve_used_ = 0;
+  }
+  carve_all();
+  double *hact = act;
   const int *sr_rows = static_cast<const int *>(sr_rows_->p);
   const int *sr_nodes = static_cast<const int *>(sr_nodes_->p);
   const int *sr_off = static_cast<const int *>(sr_inc_off_->p);
@@ -2671,7 +2789,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   struct Pending { const char *name; hipEvent_t a, b; int unit_kind; };
   std::vector<Pending> pending;
   auto timed = [&](const char *name, int unit_kind, auto &&launch) {
-    if (!timing_) { launch(); return; }
+    if (!timing_ || from_scratch) { launch(); return; }  // events are created: not in the no-allocation call
     Pending pd{name, nullptr, nullptr, unit_kind};
     HIP_CHECK(hipEventCreate(&pd.a));
     HIP_CHECK(hipEventCreate(&pd.b));
@@ -2883,7 +3001,9 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
 
   const GraphKey key{x_in, fo, etot, flags, {box_len_[0], box_len_[1], box_len_[2]}, s, topo_version_,
                      alloc_epoch_};
-  if (timing_ || !use_graphs_) {
+  if (from_scratch) {
+    enqueue();  // instantiating a graph allocates: never here
+  } else if (timing_ || !use_graphs_) {
     enqueue();
   } else if (graph_exec_ && key == graph_key_) {
     HIP_CHECK(hipGraphLaunch(graph_exec_, s));
@@ -2905,7 +3025,7 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   } else {
     enqueue();
   }
-  last_key_ = key;
+  if (!from_scratch) last_key_ = key;
   HIP_CHECK(hipStreamSynchronize(s));
   const double *host_red = host_out_;
   const std::int64_t host_nact = std::int64_t(host_out_[9]);
@@ -2926,11 +3046,14 @@ void Evaluator::compute_device(const double *x, int flags, double *f_out, double
   totals_[1] = host_red[8];
   last_etot_ = etot;
   evaluated_ = true;
+  last_from_scratch_ = from_scratch;
   (void)flags;
 }
 
 void Evaluator::last_vatom(double *out, bool on_device) {
   if (!evaluated_) throw std::logic_error("SO3LR: no evaluation yet");
+  if (last_from_scratch_)
+    throw std::logic_error("SO3LR: so3lr_compute_device_noalloc keeps no per-atom virial; use so3lr_compute_device");
   const std::int64_t N = n_;
   const std::size_t Nz = std::size_t(N), Pz = std::size_t(std::max<std::int64_t>(p_sr_, 1));
   double *dst = on_device ? out : ensure<double>(vatom_, Nz * 6);
@@ -2957,6 +3080,8 @@ bool Evaluator::timing_read(const std::string &kernel, double &total_ms, std::in
 void Evaluator::last_terms(double *learned, double *zbl, double *lr, double *charges, double *hirshfeld,
                            double *totals, double *image_energy) {
   if (!evaluated_) throw std::logic_error("SO3LR: no evaluation yet");
+  if (last_from_scratch_)
+    throw std::logic_error("SO3LR: so3lr_compute_device_noalloc keeps no per-atom terms; use so3lr_compute_device");
   const std::size_t Nz = std::size_t(n_);
   // node-ordered buffers come back in the caller's atom order
   std::vector<std::vector<double>> staged;

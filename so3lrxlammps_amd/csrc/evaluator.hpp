@@ -95,6 +95,14 @@ class Evaluator {
                       double *energy, double *virial);
   void compute_host(const double *x_rows, int flags, double *f, double *eatom, double *energy,
                     double *virial);
+  // As compute_device, with every work buffer of the evaluation carved from
+  // the library's static device scratch array (no allocation, no graph, no
+  // events); throws std::invalid_argument when the system needs more than
+  // scratch_capacity() bytes.  Per-atom terms and the per-atom virial are not
+  // kept afterwards (last_terms / last_vatom refuse).
+  void compute_device_noalloc(const double *x_rows_dev, int flags, double *f_dev, double *eatom_dev,
+                              double *energy, double *virial);
+  static std::size_t scratch_capacity();
   void last_terms(double *learned, double *zbl, double *lr, double *charges, double *hirshfeld,
                   double *totals, double *image_energy);
   // Per-atom virial of the last evaluation (n_owned x 6, atom order), to host
@@ -166,6 +174,25 @@ class Evaluator {
     return static_cast<T *>(b->p);
   }
   void release_all();
+  // Where the work buffers of the evaluation being set up come from: the
+  // retained per-context buffers (ensure), a pass that only adds up their
+  // sizes, or consecutive 256-byte aligned slices of the static scratch array.
+  enum class Carve { Retained, Measure, Scratch };
+  Carve carve_ = Carve::Retained;
+  char *carve_base_ = nullptr;
+  std::size_t carve_used_ = 0;
+  template <class T>
+  T *take(Buffer *b, std::size_t count) {
+    if (carve_ == Carve::Retained) return ensure<T>(b, count);
+    const std::size_t bytes = ((count ? count : 1) * sizeof(T) + 255) / 256 * 256;
+    T *p = carve_ == Carve::Scratch ? reinterpret_cast<T *>(carve_base_ + carve_used_) : nullptr;
+    carve_used_ += bytes;
+    return p;
+  }
+  void compute_impl(const double *x, int flags, double *f_out, double *eatom_out, double *energy, double *virial,
+                    bool from_scratch);
+  char *scratch_dev_ = nullptr;   // this device's copy of the static scratch array
+  bool last_from_scratch_ = false;  // the last evaluation's buffers were scratch slices
 
   // node-sized device buffers (named members so the kernels' arguments read clearly)
   Buffer *z_, *x0_, *img_of_node_, *img_off_, *img_q_;

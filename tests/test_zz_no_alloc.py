@@ -1,0 +1,98 @@
+"""so3lr_compute_device_noalloc (no counterpart in the reference: the entry
+point for callers that cannot allocate device memory) against
+so3lr_compute_device on the same inputs, through the C ABI.
+
+Both run the same kernels in the same order, so the results must agree bit
+for bit.  Two no-allocation calls in a row, the second on a smaller system,
+so the second call runs on the first call's leftover contents of the shared
+static array; then a system too large for the array is refused on the host
+before any kernel runs."""
+import numpy as np
+import pytest
+
+import support
+
+pytestmark = pytest.mark.gpu
+
+
+def _evaluate(ctx, x, n, noalloc, stream, reneighbor=None):
+    import torch
+    dev = torch.device("cuda:0")
+    with torch.cuda.stream(stream):
+        xt = torch.tensor(x, dtype=torch.float64, device=dev)
+        if reneighbor is not None:
+            lo, hi, per = reneighbor
+            ctx.reneighbor_device(xt, lo, hi, per, 1.0, stream=stream.cuda_stream)
+        ft = torch.full((n, 3), float("nan"), dtype=torch.float64, device=dev)
+        et = torch.full((n,), float("nan"), dtype=torch.float64, device=dev)
+        fn = ctx.compute_device_noalloc if noalloc else ctx.compute_device
+        e, w = fn(xt, ft, et, stream=stream.cuda_stream)
+        stream.synchronize()
+        return e, np.asarray(w), ft.cpu().numpy(), et.cpu().numpy()
+
+
+def _same(a, b, what):
+    ea, wa, fa, eta = a
+    eb, wb, fb, etb = b
+    assert ea == eb, (what, ea, eb)
+    assert np.array_equal(wa, wb), (what, wa, wb)
+    assert np.array_equal(fa, fb), (what, np.abs(fa - fb).max())
+    assert np.array_equal(eta, etb), (what, np.abs(eta - etb).max())
+    assert np.isfinite(fa).all() and np.isfinite(eta).all(), what
+
+
+def test_noalloc_matches_compute_device():
+    import torch
+    from so3lrxlammps_amd import Context, Lists, _lib, systems
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+
+    # call 1: 16 packed config-2 molecules (rows path, each with its own (Q, M))
+    z, x, offs, qs, ms, _ = systems.packed_molecules(n_mol=16)
+    print("noalloc call 1: %d atoms, 16 packed molecules, rows path" % len(z), flush=True)
+    c1 = Context(support.MODEL, 0)
+    c1.set_images(z, offs, qs, ms)
+    lists = Lists(x, x.min(0) - 20.0, x.max(0) + 20.0, (0, 0, 0))
+    c1.set_topology(lists)
+    xr = lists.rows_positions(x)
+    ref1 = _evaluate(c1, xr, len(z), False, stream)
+    got1 = _evaluate(c1, xr, len(z), True, stream)
+    _same(got1, ref1, "packed molecules")
+    # per-atom terms are not kept by the no-allocation call
+    with pytest.raises(_lib.SO3LRError) as err:
+        c1.terms()
+    assert err.value.code == _lib.ERR_STATE
+
+    # call 2, smaller: the acetate anion on the device-reneighbor path (spatial
+    # node order inside), in a second context on the same device
+    ref, za, pa, _ = support.load_golden("acetate")
+    print("noalloc call 2: %d atoms, acetate, device reneighbor path" % len(za), flush=True)
+    c2 = Context(support.MODEL, 0)
+    c2.set_system(za, -1, 1)
+    box = (pa.min(0) - 20.0, pa.max(0) + 20.0, (0, 0, 0))
+    got2 = _evaluate(c2, pa, len(za), True, stream, reneighbor=box)
+    ref2 = _evaluate(c2, pa, len(za), False, stream, reneighbor=box)
+    _same(got2, ref2, "acetate")
+
+    # the first context again: its retained path still agrees after both
+    # no-allocation calls wrote the shared array
+    again = _evaluate(c1, xr, len(z), False, stream)
+    _same(again, ref1, "packed molecules, retained path after the no-allocation calls")
+
+    # a system larger than the static array: refused before any kernel runs
+    _, zw, pw, bw = support.load_golden("water3000")
+    print("noalloc oversize: %d atoms, expect a refusal" % len(zw), flush=True)
+    c3 = Context(support.MODEL, 0)
+    c3.set_system(zw, 0, 1)
+    lw = Lists(pw, np.zeros(3), bw, (1, 1, 1))
+    c3.set_topology(lw)
+    with torch.cuda.stream(stream):
+        xt = torch.tensor(lw.rows_positions(pw), dtype=torch.float64, device=dev)
+        ft = torch.zeros((len(zw), 3), dtype=torch.float64, device=dev)
+        with pytest.raises(_lib.SO3LRError) as err:
+            c3.compute_device_noalloc(xt, ft, stream=stream.cuda_stream)
+        stream.synchronize()
+    assert err.value.code == _lib.ERR_ARGUMENT and "bytes of work space" in str(err.value)
+    for c in (c1, c2, c3):
+        c.close()
