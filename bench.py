@@ -1,21 +1,33 @@
 #!/usr/bin/env python3
 """SO3LR MD throughput on one MI355X: atom-steps/s at the 24,000-atom NaCl
-solution, fp64 E + F + virial every step.
+solution, fp64 E + F + virial every step; and the
+metric's second half, max atoms per GPU, from the 150,000-atom water box
+(configs[4]) run in the same process.
 
-One step = velocity Verlet with a Berendsen thermostat at 300 K (0.5 fs),
-ghost-row update, neighbour-list rebuild when an atom moved more than half the
+Headline (`value`): one step = velocity Verlet with a Berendsen thermostat at
+300 K (0.5 fs), a neighbour-list rebuild when an atom moved more than half the
 1 A skin (LAMMPS `neigh_modify every 1 delay 0 check yes`), and one
 so3lr_compute_device call.  Positions, velocities and forces stay in HBM
 (torch tensors as plumbing); the rebuild wraps the positions and builds the
 candidate lists on the GPU (so3lr_reneighbor_device).
 
-Prints one JSON line (the driver's contract), with the dominant kernel's
-roofline from HIP events recorded on its launch stream, and the CPU oracle
-timed on the same host on a bounded sample.
+`rows_path`: the drop-in route a LAMMPS pair style takes, timed on the same
+system: host positions, the LAMMPS stand-in's ghost rows and candidate lists
+at every rebuild (LAMMPS's own work, reported apart), so3lr_set_topology with
+those lists, then so3lr_compute with host arrays every step.
+
+`capacity`: config 4 (150,000 atoms) NPT steps with hipMemGetInfo before and
+after, the library's device bytes and bytes per atom.
+
+`roofline`: the kernel with the most GPU time per step among the timed ones,
+its algorithmic work per unit (no recompute) / its HIP-event average on the
+launch stream.  `cpu_baseline`: the CPU oracle on a bounded sample.
+Prints one JSON line (the driver's contract).
 """
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 
@@ -28,30 +40,71 @@ MODEL = os.path.join(REPO, "models", "so3lr.so3lr")
 A100_ATOM_STEPS = 69706.0  # the reference's published 24k-atom water figure on 1 A100 (examples/scaling/README.md:56-60)
 HBM_PEAK_GBS = 8000.0
 FP64_PEAK_TFS = 78.6
-# algorithmic work of the dominant kernel, per active short-range pair and block
-# (filters: 2 x (32x128 + 128x128 + 4x32 + 32x128) MAC, forward)
-FILTER_FWD_FLOP_PER_PAIR = 2.0 * 2.0 * (32 * 128 + 128 * 128 + 4 * 32 + 32 * 128)
-# reverse: dgrad of W1 (128x128), E1 (128x32), W0 (128x32), E0 (32x4) plus the
-# layer-0 recompute (32x128 + 4x32), both filters
-FILTER_BWD_FLOP_PER_PAIR = 2.0 * 2.0 * (128 * 128 + 128 * 32 + 128 * 32 + 32 * 4 + 32 * 128 + 4 * 32)
 KB = 8.617333262e-5
 ACC = 9648.533212  # eV / (A amu) -> A / ps^2
+
+
+def _mac(*shapes):
+    return sum(a * b for a, b in shapes)
+
+
+# Algorithmic work per unit of each timed kernel: minimal forward and
+# input-gradient work, no recompute (units: active SR pairs for the filters,
+# owned atoms otherwise).  "issued" is what the kernel executes when that
+# differs (the reverse filters recompute the layer-0 pre-activations).
+# Filters, per pair and block, both filters (F = 128, R = 32, F/4 = 32):
+#   forward  radial W0 (128x32) + W1 (128x128), spherical E0 (32x4) + E1 (128x32);
+#   reverse  the transposes of the same four layers (input gradients only).
+_FILTER = 2 * 2 * _mac((128, 32), (128, 128), (32, 4), (128, 32))   # 98,816 flop
+_FILTER_B0 = 2 * 2 * _mac((128, 32), (128, 128))                     # 81,920: ev = 0 in block 0
+_FILTER_BWD_ISSUED = _FILTER + 2 * 2 * _mac((128, 32), (32, 4))      # + layer-0 recompute: 115,712
+_FILTER_BWD_B0_ISSUED = _FILTER_B0 + 2 * 2 * _mac((128, 32))         # 98,304
+KERNEL_WORK = {
+    # name: (kernel symbol, bound, algorithmic per unit, issued per unit, unit)
+    "filter_fwd": ("k_filter_fwd_mfma<false>", "mfma", _FILTER, _FILTER, "pair"),
+    "filter_fwd_block0": ("k_filter_fwd_mfma<true>", "mfma", _FILTER_B0, _FILTER_B0, "pair"),
+    "filter_bwd": ("k_filter_bwd_mfma<false>", "mfma", _FILTER, _FILTER_BWD_ISSUED, "pair"),
+    "filter_bwd_block0": ("k_filter_bwd_mfma<true>", "mfma", _FILTER_B0, _FILTER_BWD_B0_ISSUED, "pair"),
+}
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def traffic_bytes(kernel, config):
-    """HBM bytes per launch (read + written) of `kernel` from the committed
-    PMC summary (two rocprofv3 passes, FETCH_SIZE and WRITE_SIZE, scaled by a
-    plain copy of known size); None when no summary covers this workload."""
+def cpu_info():
+    model = platform.processor() or "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"cpu_model": model, "nproc": affinity, "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS")}
+
+
+def traffic_per_launch(kernel, config, units_per_launch):
+    """HBM bytes per launch of `kernel` from the committed PMC summary (two
+    rocprofv3 passes, FETCH_SIZE and WRITE_SIZE, scaled by a plain copy of
+    known size), rescaled to this run's units per launch; None when the
+    summary does not cover this kernel and workload."""
     path = os.path.join(REPO, "profiles", "pmc_traffic_config%d.json" % config)
     try:
-        rec = json.load(open(path))["kernels"][kernel]
-    except (OSError, KeyError, ValueError):
-        return None
-    return rec["read_bytes"] + rec["write_bytes"]
+        doc = json.load(open(path))
+        rec = doc["kernels"][kernel]
+        per_unit = (rec["read_bytes"] + rec["write_bytes"]) / rec.get("units_per_launch", doc["pairs_per_launch"])
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None, None
+    return per_unit * units_per_launch, "profiles/pmc_traffic_config%d.json: %.0f B per %s, x this run's count" % (
+        config, per_unit, KERNEL_WORK_UNIT.get(kernel, "unit"))
+
+
+KERNEL_WORK_UNIT = {v[0]: v[4] for v in KERNEL_WORK.values()}
 
 
 def cpu_baseline(z, x, box, periodic, images, seconds_budget):
@@ -95,10 +148,242 @@ def cpu_baseline(z, x, box, periodic, images, seconds_budget):
         orc.evaluate(zs, sr, lr, **kw)
         times.append(time.time() - t0)
     med = float(np.median(times))
-    return {"value": len(zs) / med, "unit": "atom-steps/s", "cores": int(lib().orc_num_threads()),
-            "kind": "port",
-            "sample": "median of %d E+F+virial calls (%.1f s of CPU work) on %d atoms: %s, CPU fp64 oracle, OpenMP"
-                      % (len(times), sum(times), len(zs), what)}
+    out = {"value": len(zs) / med, "unit": "atom-steps/s", "cores": int(lib().orc_num_threads()),
+           "kind": "port",
+           "sample": "median of %d E+F+virial calls (%.1f s of CPU work) on %d atoms: %s, CPU fp64 oracle, OpenMP"
+                     % (len(times), sum(times), len(zs), what)}
+    out.update(cpu_info())
+    return out
+
+
+def load_config(index):
+    from so3lrxlammps_amd import systems
+    images = None
+    if index == 2:
+        z, x, offs, qs, ms, extent = systems.packed_molecules()
+        images = (offs, qs, ms)
+        box, Q, M = np.full(3, extent), None, None
+        desc = "512 molecules of 12-40 atoms (H C N O S), Q in {-1,0,1}, packed images, non-periodic"
+    else:
+        z, x, box, Q, M, desc = systems.config(index)
+        if box is None:  # config 0: the molecule in its 40 A box, open boundaries
+            box = np.full(3, 40.0)
+    periodic = (0, 0, 0) if index in (0, 2) else (1, 1, 1)
+    return z, x, np.asarray(box, float), Q, M, images, periodic, desc
+
+
+class DeviceMD:
+    """The HBM-resident MD loop on one context (config 0: repeated single
+    points; 1 and 2: NVE; 3: NVT; 4: NPT with a Berendsen barostat)."""
+
+    def __init__(self, index, z, x, box, Q, M, images, periodic, stream):
+        import torch
+        from so3lrxlammps_amd import Context, systems
+        self.torch = torch
+        self.index = index
+        self.stream = stream
+        dev = torch.device("cuda:0")
+        self.ctx = Context(MODEL, 0)
+        if images is not None:
+            self.ctx.set_images(z, *images)
+        else:
+            self.ctx.set_system(z, Q, M)
+        self.n = len(z)
+        self.periodic = periodic
+        self.lo = np.zeros(3)
+        v0, m = systems.maxwell_boltzmann(z, 300.0)
+        self.xt = torch.tensor(x, dtype=torch.float64, device=dev)
+        self.vt = torch.tensor(v0, dtype=torch.float64, device=dev)
+        self.inv_m = torch.tensor(ACC / m, dtype=torch.float64, device=dev)[:, None]
+        self.mt = torch.tensor(m, dtype=torch.float64, device=dev)[:, None]
+        self.ft = torch.zeros((self.n, 3), dtype=torch.float64, device=dev)
+        self.lot = torch.tensor(self.lo, dtype=torch.float64, device=dev)
+        self.dt, self.skin, self.tau, self.T0 = 0.0005, 1.0, 0.1, 300.0
+        self.npt = index == 4
+        self.single_point = index == 0
+        self.thermostat = index in (3, 4)
+        self.P0_bar, self.tau_p, self.beta_bar = 1.0, 1.0, 4.5e-5
+        self.state = {"builds": 0, "build_s": 0.0, "box": np.array(box, dtype=float), "mu_total": 1.0}
+        self.rebuild()
+        self.force()
+
+    def rebuild(self):
+        # HBM-resident reneighbor: wraps xt in place, builds the candidate
+        # lists on the GPU (no ghost rows, no host copies)
+        st = self.state
+        t0 = time.time()
+        self.ctx.reneighbor_device(self.xt, self.lo, self.lo + st["box"], self.periodic, self.skin,
+                                   stream=self.stream.cuda_stream)
+        st["x_build"] = self.xt.clone()
+        st["box_build"] = st["box"].copy()
+        st["builds"] += 1
+        st["build_s"] += time.time() - t0
+
+    def force(self):
+        return self.ctx.compute_device(self.xt, self.ft, stream=self.stream.cuda_stream)
+
+    def step(self):
+        torch, st, dt = self.torch, self.state, self.dt
+        if self.single_point:
+            return self.force()
+        self.vt.addcmul_(self.ft, self.inv_m, value=0.5 * dt)
+        self.xt.add_(self.vt, alpha=dt)
+        disp = (self.xt - st["x_build"]).norm(dim=1).max().item()
+        # a box change moves the far corner: LAMMPS Neighbor::check_distance
+        # charges that against the skin as well
+        disp += float(np.linalg.norm(st["box"] - st["box_build"]))
+        if disp > 0.5 * self.skin:
+            self.rebuild()
+        e, w = self.force()
+        self.vt.addcmul_(self.ft, self.inv_m, value=0.5 * dt)
+        ke = 0.5 * (self.mt * self.vt * self.vt).sum() / ACC
+        if self.thermostat:
+            temp = 2.0 * ke / (3.0 * self.n * KB)
+            self.vt.mul_(torch.sqrt(1.0 + dt / self.tau * (self.T0 / temp - 1.0)))
+        if self.npt:
+            # P = (2 KE + tr W) / (3 V); W is the LAMMPS virial (eV)
+            vol = float(np.prod(st["box"]))
+            p_bar = (2.0 * ke.item() + w[0] + w[1] + w[2]) / (3.0 * vol) * 1.602176634e6
+            mu = (1.0 - dt / self.tau_p * self.beta_bar * (self.P0_bar - p_bar)) ** (1.0 / 3.0)
+            self.xt.sub_(self.lot).mul_(mu).add_(self.lot)
+            st["box"] = st["box"] * mu
+            st["mu_total"] *= mu
+            st["pressure_bar"] = p_bar
+            self.ctx.set_box(self.lo, self.lo + st["box"])
+        return e, w
+
+    def run(self, warmup, steps, report_every=25):
+        for _ in range(warmup):
+            self.step()
+        self.torch.cuda.synchronize()
+        b0, s0 = self.state["builds"], self.state["build_s"]
+        t0 = time.perf_counter()
+        for k in range(steps):
+            e, w = self.step()
+            if (k + 1) % report_every == 0:
+                log("  step %d E=%.6f eV" % (k + 1, e))
+        self.torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        return elapsed, self.state["builds"] - b0, self.state["build_s"] - s0
+
+    def ensemble(self):
+        if self.npt:
+            return {"ensemble": "NPT (Berendsen, 1 bar, 300 K)", "box_scale": self.state["mu_total"],
+                    "pressure_bar_last": self.state.get("pressure_bar")}
+        if self.single_point:
+            return {"ensemble": "single-point E+F+virial calls"}
+        return {"ensemble": "NVT (Berendsen, 300 K)" if self.thermostat else "NVE"}
+
+
+def rows_path(z, x, box, Q, M, periodic, steps, warmup):
+    """The LAMMPS pair-style route on host arrays: NVT velocity Verlet in
+    numpy; at every rebuild the stand-in wraps the owned atoms, makes the ghost
+    rows and the full SR / half LR candidate lists (LAMMPS's work, timed
+    apart), then so3lr_set_topology; every step the ghost rows' positions
+    (LAMMPS forward communication) and so3lr_compute with host arrays."""
+    from so3lrxlammps_amd import Context, Lists, systems
+    ctx = Context(MODEL, 0)
+    ctx.set_system(z, Q, M)
+    n = len(z)
+    lo, hi = np.zeros(3), np.asarray(box, float)
+    v, m = systems.maxwell_boltzmann(z, 300.0)
+    inv_m = (ACC / m)[:, None]
+    x = np.array(x, dtype=float)
+    dt, skin, tau, T0 = 0.0005, 1.0, 0.1, 300.0
+    t = {"lammps_lists": 0.0, "set_topology": 0.0, "forward_comm": 0.0, "compute": 0.0, "rebuilds": 0}
+    st = {}
+
+    def rebuild():
+        t0 = time.perf_counter()
+        np.copyto(x, lo + np.mod(x - lo, hi - lo))  # LAMMPS Domain::pbc at reneighbor
+        lists = Lists(x, lo, hi, periodic)
+        t1 = time.perf_counter()
+        ctx.set_topology(lists)
+        t2 = time.perf_counter()
+        t["lammps_lists"] += t1 - t0
+        t["set_topology"] += t2 - t1
+        t["rebuilds"] += 1
+        st["lists"], st["x_build"] = lists, x.copy()
+
+    def force():
+        t0 = time.perf_counter()
+        xr = st["lists"].rows_positions(x)
+        t1 = time.perf_counter()
+        e, f, _, w = ctx.compute(xr, eatom=False)
+        t2 = time.perf_counter()
+        t["forward_comm"] += t1 - t0
+        t["compute"] += t2 - t1
+        return e, f, w
+
+    rebuild()
+    e, f, w = force()
+
+    def step(f):
+        v[:] += 0.5 * dt * f * inv_m
+        x[:] += dt * v
+        if np.sqrt(((x - st["x_build"]) ** 2).sum(1)).max() > 0.5 * skin:
+            rebuild()
+        e, f, w = force()
+        v[:] += 0.5 * dt * f * inv_m
+        temp = (m[:, None] * v * v).sum() / ACC / (3.0 * n * KB)
+        v[:] *= np.sqrt(1.0 + dt / tau * (T0 / temp - 1.0))
+        return f
+
+    for _ in range(warmup):
+        f = step(f)
+    for k in t:
+        t[k] = 0 if k == "rebuilds" else 0.0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        f = step(f)
+    elapsed = time.perf_counter() - t0
+    lib_s = t["set_topology"] + t["compute"]
+    rb = max(1, t["rebuilds"])
+    out = {
+        "value": n * steps / elapsed, "unit": "atom-steps/s", "steps": steps, "ms_per_step": 1e3 * elapsed / steps,
+        "library_value": n * steps / lib_s,
+        "library_ms_per_step": 1e3 * lib_s / steps,
+        "set_topology_ms": 1e3 * t["set_topology"] / rb,
+        "compute_ms": 1e3 * t["compute"] / steps,
+        "rebuilds": t["rebuilds"],
+        "lammps_stand_in_lists_ms_per_rebuild": 1e3 * t["lammps_lists"] / rb,
+        "forward_comm_ms_per_step": 1e3 * t["forward_comm"] / steps,
+        "note": "value: whole loop on host arrays including the LAMMPS stand-in's list builds and ghost-row "
+                "positions (LAMMPS's own work); library_value: so3lr_set_topology + so3lr_compute only",
+    }
+    ctx.close()
+    return out
+
+
+def capacity(steps, warmup, stream):
+    """Config 4 (150,000 atoms) NPT on the device path: throughput, HBM in use
+    (hipMemGetInfo) and the library's bytes per atom."""
+    import torch
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    free0, total = torch.cuda.mem_get_info()
+    z, x, box, Q, M, images, periodic, desc = load_config(4)
+    md = DeviceMD(4, z, x, box, Q, M, images, periodic, stream)
+    elapsed, builds, _ = md.run(warmup, steps)
+    free1, _ = torch.cuda.mem_get_info()
+    n = md.n
+    dev_bytes = md.ctx.device_bytes()
+    used = total - free1
+    used_by_run = free0 - free1
+    out = {"workload": "config 4: " + desc, "atoms": n, "steps": steps,
+           "ms_per_step": 1e3 * elapsed / steps, "atom_steps_per_s": n * steps / elapsed,
+           "hbm_used_bytes": int(used), "hbm_used_by_this_run_bytes": int(used_by_run),
+           "hbm_total_bytes": int(total), "device_bytes": int(dev_bytes),
+           "device_bytes_per_atom": dev_bytes / n,
+           "max_atoms_estimate": int((total - (used - used_by_run)) / (used_by_run / n)),
+           "note": "max_atoms_estimate: HBM not in use before this run / (HBM this run took per atom); "
+                   "water at 1 g/cm^3, linear in the candidate pair count"}
+    out.update(md.ensemble())
+    md.ctx.close()
+    del md
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -109,6 +394,10 @@ def main():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-rows-path", action="store_true")
+    ap.add_argument("--rows-steps", type=int, default=0, help="rows-path steps (default: --steps)")
+    ap.add_argument("--no-capacity", action="store_true")
+    ap.add_argument("--capacity-steps", type=int, default=5)
     ap.add_argument("--roofline-steps", type=int, default=10,
                     help="steps after the timed ones with per-kernel HIP events")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -120,21 +409,9 @@ def main():
         sys.exit(2)
 
     import torch
-    from so3lrxlammps_amd import Context, Lists, systems
 
     log("generating config %d" % args.config)
-    images = None
-    if args.config == 2:
-        # 512 independent molecules evaluated together (packed images)
-        z, x, offs, qs, ms, extent = systems.packed_molecules()
-        images = (offs, qs, ms)
-        box, Q, M = np.full(3, extent), None, None
-        desc = "512 molecules of 12-40 atoms (H C N O S), Q in {-1,0,1}, packed images, non-periodic"
-    else:
-        z, x, box, Q, M, desc = systems.config(args.config)
-        if box is None:  # config 0: the molecule in its 40 A box, open boundaries
-            box = np.full(3, 40.0)
-    periodic = (0, 0, 0) if args.config in (0, 2) else (1, 1, 1)
+    z, x, box, Q, M, images, periodic, desc = load_config(args.config)
     n = len(z)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -152,154 +429,93 @@ def main():
         torch.cuda.synchronize()
         del src, dst
         torch.cuda.empty_cache()
-    ctx = Context(MODEL, 0)
-    if images is not None:
-        ctx.set_images(z, *images)
-    else:
-        ctx.set_system(z, Q, M)
-    lo = np.zeros(3)
-    v0, m = systems.maxwell_boltzmann(z, 300.0)
-    xt = torch.tensor(x, dtype=torch.float64, device=dev)
-    vt = torch.tensor(v0, dtype=torch.float64, device=dev)
-    inv_m = torch.tensor(ACC / m, dtype=torch.float64, device=dev)[:, None]
-    mt = torch.tensor(m, dtype=torch.float64, device=dev)[:, None]
-    ft = torch.zeros((n, 3), dtype=torch.float64, device=dev)
-    lot = torch.tensor(lo, dtype=torch.float64, device=dev)
-    dt, skin, tau, T0 = 0.0005, 1.0, 0.1, 300.0
-    # config 4 runs NPT: Berendsen barostat at 1 bar (water compressibility)
-    npt = args.config == 4
-    P0_bar, tau_p, beta_bar = 1.0, 1.0, 4.5e-5
-    EV_A3_TO_BAR = 1.602176634e6
-    state = {"builds": 0, "build_s": 0.0, "box": np.array(box, dtype=float), "mu_total": 1.0}
 
-    def rebuild():
-        # HBM-resident reneighbor: wraps xt in place, builds the candidate
-        # lists on the GPU (no ghost rows, no host copies)
-        t0 = time.time()
-        ctx.reneighbor_device(xt, lo, lo + state["box"], periodic, skin, stream=stream.cuda_stream)
-        state["x_build"] = xt.clone()
-        state["box_build"] = state["box"].copy()
-        state["builds"] += 1
-        state["build_s"] += time.time() - t0
-
-    def force():
-        e, w = ctx.compute_device(xt, ft, stream=stream.cuda_stream)
-        return e, w
-
-    rebuild()
-    e, w = force()
-
-    # config 0: repeated single points; 1 and 2: NVE; 3: NVT; 4: NPT
-    single_point = args.config == 0
-    thermostat = args.config in (3, 4)
-
-    def step():
-        if single_point:
-            return force()
-        vt.addcmul_(ft, inv_m, value=0.5 * dt)
-        xt.add_(vt, alpha=dt)
-        disp = (xt - state["x_build"]).norm(dim=1).max().item()
-        # a box change moves the far corner: LAMMPS Neighbor::check_distance
-        # charges that against the skin as well
-        disp += float(np.linalg.norm(state["box"] - state["box_build"]))
-        if disp > 0.5 * skin:
-            rebuild()
-        e, w = force()
-        vt.addcmul_(ft, inv_m, value=0.5 * dt)
-        ke = 0.5 * (mt * vt * vt).sum() / ACC
-        if thermostat:
-            temp = 2.0 * ke / (3.0 * n * KB)
-            lam = torch.sqrt(1.0 + dt / tau * (T0 / temp - 1.0))
-            vt.mul_(lam)
-        if npt:
-            # P = (2 KE + tr W) / (3 V); W is the LAMMPS virial (eV)
-            vol = float(np.prod(state["box"]))
-            p_bar = (2.0 * ke.item() + w[0] + w[1] + w[2]) / (3.0 * vol) * EV_A3_TO_BAR
-            mu = (1.0 - dt / tau_p * beta_bar * (P0_bar - p_bar)) ** (1.0 / 3.0)
-            xt.sub_(lot).mul_(mu).add_(lot)
-            state["box"] = state["box"] * mu
-            state["mu_total"] *= mu
-            state["pressure_bar"] = p_bar
-            ctx.set_box(lo, lo + state["box"])
-        return e, w
-
-    log("warmup %d steps" % args.warmup)
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    builds0, build_s0 = state["builds"], state["build_s"]
-    log("timing %d steps" % args.steps)
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        e, w = step()
-        if (k + 1) % 25 == 0:
-            log("  step %d E=%.6f eV" % (k + 1, e))
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    md = DeviceMD(args.config, z, x, box, Q, M, images, periodic, stream)
+    log("warmup %d steps, timing %d steps" % (args.warmup, args.steps))
+    elapsed, builds_timed, build_s_timed = md.run(args.warmup, args.steps)
     value = n * args.steps / elapsed
-    builds_timed, build_s_timed = state["builds"] - builds0, state["build_s"] - build_s0
 
     # kernel durations for the roofline: HIP events on the launch stream over
     # further steps of the same run (events keep the evaluation out of graph
     # replay, so they are not recorded during the timed steps above)
-    ctx.kernel_timing(True)
+    md.ctx.kernel_timing(True)
     for _ in range(args.roofline_steps):
-        step()
+        md.step()
     torch.cuda.synchronize()
-    ctx.kernel_timing(False)
-
-    # dominant kernel: the pair filters (forward + reverse) carry ~90% of the
-    # FLOPs; the roofline is the reverse filter of blocks 1.. (block 0 runs a
-    # cheaper instantiation, ev = 0, timed under its own name)
+    md.ctx.kernel_timing(False)
     timing = {}
     for name in ("filter_fwd", "filter_fwd_block0", "filter_bwd", "filter_bwd_block0", "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range"):
         try:
-            timing[name] = ctx.kernel_timing_read(name)
+            timing[name] = md.ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched
             pass
+    steps_timed = max(1, args.roofline_steps)
+    kernels = {}
+    for k, (ms, launches, units) in timing.items():
+        row = {"avg_ms": ms / launches, "launches": launches, "ms_per_step": ms / steps_timed}
+        if k in KERNEL_WORK:
+            sym, bound, alg, issued, unit = KERNEL_WORK[k]
+            per_launch = units / launches
+            row.update({"kernel": sym, "units_per_launch": per_launch,
+                        "tflops_algorithmic": alg * per_launch / (ms / launches * 1e-3) / 1e12,
+                        "frac": alg * per_launch / (ms / launches * 1e-3) / 1e12 / FP64_PEAK_TFS})
+        kernels[k] = row
+    # the roofline kernel: most GPU time per step among those with a work model
+    dom = max((k for k in kernels if k in KERNEL_WORK), key=lambda k: kernels[k]["ms_per_step"])
+    sym, bound, alg, issued, unit = KERNEL_WORK[dom]
+    ms, launches, units = timing[dom]
+    avg_ms = ms / launches
+    per_launch = units / launches
+    achieved = alg * per_launch / (avg_ms * 1e-3) / 1e12
+    traffic, traffic_src = traffic_per_launch(sym, args.config, per_launch)
+    roofline = {"bound": bound, "kernel": sym, "achieved": achieved, "peak": FP64_PEAK_TFS, "unit": "TFLOP/s",
+                "frac": achieved / FP64_PEAK_TFS, "traffic": traffic, "traffic_source": traffic_src,
+                "avg_launch_ms": avg_ms, "pairs_per_launch": per_launch,
+                "flop_per_pair_algorithmic": alg, "flop_per_pair_issued": issued,
+                "achieved_issued": issued * per_launch / (avg_ms * 1e-3) / 1e12,
+                "selection": "the timed kernel with the most GPU time per step (%.3f ms of %d steps' HIP events)"
+                             % (kernels[dom]["ms_per_step"], steps_timed)}
     free_b, total_b = torch.cuda.mem_get_info(dev)
-    ms_f, launches_f, pairs_f = timing["filter_bwd"]
-    avg_ms = ms_f / launches_f
-    flop = FILTER_BWD_FLOP_PER_PAIR * pairs_f / launches_f
-    achieved = flop / (avg_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "k_filter_bwd_mfma<false>", "achieved": achieved, "peak": FP64_PEAK_TFS,
-                "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFS,
-                "traffic": traffic_bytes("k_filter_bwd_mfma<false>", args.config),
-                "avg_launch_ms": avg_ms, "pairs_per_launch": pairs_f / launches_f,
-                "flop_per_pair": FILTER_BWD_FLOP_PER_PAIR}
-    kernels = {k: {"avg_ms": v[0] / v[1], "launches": v[1]} for k, v in timing.items()}
+    sr_active, sr_cand, lr_cand = md.ctx.graph_stats()
+    config = {"workload": "config %d: %s" % (args.config, desc), "atoms": n, "integrator": "velocity Verlet",
+              **md.ensemble(), "timestep_fs": 0.5, "skin_A": md.skin, "sr_pairs_active": sr_active,
+              "sr_pair_candidates": sr_cand, "lr_pair_candidates": lr_cand,
+              "neighbor_rebuilds_timed": builds_timed, "rebuild_seconds_timed": build_s_timed,
+              "ns_per_day": value / n * 0.5 * 86400 / 1e6, "device_bytes": md.ctx.device_bytes(),
+              "device_bytes_per_atom": md.ctx.device_bytes() / n,
+              "hbm_used_bytes": int(total_b - free_b), "hbm_total_bytes": int(total_b), "kernels": kernels}
+    md.ctx.close()
+    del md
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    rows = None
+    if not args.no_rows_path and args.config in (1, 3) and Q is not None:
+        log("rows path (LAMMPS pair-style route, host arrays)")
+        rows = rows_path(z, x, box, Q, M, periodic, args.rows_steps or args.steps, max(2, args.warmup // 2))
+        rows["fraction_of_device_path"] = rows["value"] / value
+        rows["library_fraction_of_device_path"] = rows["library_value"] / value
+    cap = None
+    if not args.no_capacity and args.config != 4:
+        log("capacity: config 4")
+        cap = capacity(args.capacity_steps, 2, stream)
 
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
         cpu = cpu_baseline(z, x, box, periodic, images, args.cpu_budget)
 
-    sr_active, sr_cand, lr_cand = ctx.graph_stats()
-    if npt:
-        extra = {"ensemble": "NPT (Berendsen, 1 bar, 300 K)", "box_scale": state["mu_total"],
-                 "pressure_bar_last": state.get("pressure_bar")}
-    elif single_point:
-        extra = {"ensemble": "single-point E+F+virial calls"}
-    elif thermostat:
-        extra = {"ensemble": "NVT (Berendsen, 300 K)"}
-    else:
-        extra = {"ensemble": "NVE"}
     out = {
         "metric": "atom-steps/s/GPU (fp64 E+F+virial) at 24k-atom water; max atoms per GPU",
         "value": value, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": value / A100_ATOM_STEPS, "dtype": "f64", "data": "synthetic (seeded, config %d)" % args.config,
-        "config": {"workload": "config 3: " + desc, "atoms": n, "integrator": "velocity Verlet", **extra,
-                   "timestep_fs": 0.5, "skin_A": skin, "sr_pairs_active": sr_active,
-                   "sr_pair_candidates": sr_cand, "lr_pair_candidates": lr_cand,
-                   "neighbor_rebuilds_timed": builds_timed,
-                   "rebuild_seconds_timed": build_s_timed,
-                   "ns_per_day": value / n * 0.5 * 86400 / 1e6,
-                   "device_bytes": ctx.device_bytes(),
-                   "hbm_used_bytes": int(total_b - free_b), "hbm_total_bytes": int(total_b),
-                   "kernels": kernels},
+        "vs_baseline": value / A100_ATOM_STEPS if args.config == 3 else None, "dtype": "f64",
+        "data": "synthetic (seeded, config %d)" % args.config,
+        "config": config,
         "roofline": roofline,
+        "rows_path": rows,
+        "capacity": cap,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

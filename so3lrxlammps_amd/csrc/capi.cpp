@@ -39,6 +39,8 @@ int guarded(so3lr_ctx *ctx, F &&body) {
     return SO3LR_OK;
   } catch (const so3lr_amd::DeviceError &e) {
     return fail(ctx, e, SO3LR_ERR_DEVICE);
+  } catch (const so3lr_amd::TopologyError &e) {
+    return fail(ctx, e, SO3LR_ERR_TOPOLOGY);
   } catch (const std::invalid_argument &e) {
     return fail(ctx, e, SO3LR_ERR_ARGUMENT);
   } catch (const std::length_error &e) {

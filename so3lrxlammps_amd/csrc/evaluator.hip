@@ -2439,6 +2439,12 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   nb_err_ = buf("nb_err"); nb_srlist_ = buf("nb_srlist"); nb_poff_ = buf("nb_poff"); sr_code_ = buf("sr_code");
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
   iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part");
+  top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
+  top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp");
+  for (int w = 0; w < 2; ++w) {
+    top_ilist_[w] = buf("top_ilist"); top_off_[w] = buf("top_off"); top_neigh_[w] = buf("top_neigh");
+    top_cnt_[w] = buf("top_cnt"); top_poff_[w] = buf("top_poff");
+  }
 }
 
 void Evaluator::set_box(const double lo[3], const double hi[3]) {
@@ -2496,88 +2502,6 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
   HIP_CHECK(hipStreamSynchronize(stream_));
   system_ready_ = true;
   topology_ready_ = false;
-  ++topo_version_;
-  evaluated_ = false;
-}
-
-namespace {
-// half pairs -> node-major incidence CSR (stable: pairs in increasing order)
-void incidence(std::int64_t n, const std::vector<int> &nodes, std::vector<int> &off, std::vector<int> &inc) {
-  const std::int64_t P = std::int64_t(nodes.size() / 2);
-  if (2 * P >= (std::int64_t(1) << 31)) throw std::length_error("SO3LR: neighbour list exceeds 2^30 pairs");
-  off.assign(n + 1, 0);
-  for (std::int64_t p = 0; p < P; ++p) { ++off[nodes[2 * p] + 1]; ++off[nodes[2 * p + 1] + 1]; }
-  for (std::int64_t i = 0; i < n; ++i) off[i + 1] += off[i];
-  inc.resize(2 * P);
-  std::vector<int> fill(off.begin(), off.end() - 1);
-  for (std::int64_t p = 0; p < P; ++p) {
-    inc[fill[nodes[2 * p]]++] = int(2 * p);
-    inc[fill[nodes[2 * p + 1]]++] = int(2 * p + 1);
-  }
-}
-}  // namespace
-
-void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int sr_kind, std::int64_t sr_inum,
-                             const std::int32_t *sr_ilist, const std::int64_t *sr_off,
-                             const std::int32_t *sr_neigh, std::int64_t lr_inum,
-                             const std::int32_t *lr_ilist, const std::int64_t *lr_off,
-                             const std::int32_t *lr_neigh) {
-  if (!system_ready_) throw std::logic_error("SO3LR: set the system before the topology");
-  const std::int64_t n = n_;
-  if (n_rows < n || !owner) throw std::invalid_argument("SO3LR: fewer rows than owned atoms");
-  for (std::int64_t r = 0; r < n_rows; ++r) {
-    const std::int32_t o = owner[r];
-    if (o < 0 || o >= n || (r < n && o != r))
-      throw std::invalid_argument("SO3LR: owner_of_row must be the identity on owned rows and map ghosts to owned atoms");
-  }
-  auto collect = [&](const char *what, bool full, std::int64_t inum, const std::int32_t *ilist,
-                     const std::int64_t *off, const std::int32_t *neigh, std::vector<int> &rows,
-                     std::vector<int> &nodes) {
-    if (inum < 0 || (inum > 0 && (!ilist || !off || !neigh)))
-      throw std::invalid_argument(std::string("SO3LR: invalid ") + what + " neighbour list");
-    if (inum > 0 && off[0] != 0) throw std::invalid_argument(std::string("SO3LR: ") + what + " offsets must start at 0");
-    std::int64_t kept = 0, dropped = 0;
-    rows.clear();
-    nodes.clear();
-    for (std::int64_t k = 0; k < inum; ++k) {
-      const std::int32_t i = ilist[k];
-      if (i < 0 || i >= n) throw std::invalid_argument(std::string("SO3LR: ") + what + " receiver is not an owned row");
-      if (off[k + 1] < off[k]) throw std::invalid_argument(std::string("SO3LR: decreasing ") + what + " offsets");
-      for (std::int64_t e = off[k]; e < off[k + 1]; ++e) {
-        const std::int32_t j = neigh[e];
-        if (j < 0 || j >= n_rows) throw std::invalid_argument(std::string("SO3LR: ") + what + " neighbour row out of range");
-        if (j == i) continue;
-        const std::int32_t oj = owner[j];
-        if (oj == i)
-          throw std::invalid_argument(std::string("SO3LR: ") + what +
-                                      " list pairs an atom with its own periodic image; the box is too small for the cutoff");
-        if (full && oj < i) { ++dropped; continue; }
-        ++kept;
-        rows.push_back(i); rows.push_back(j);
-        nodes.push_back(i); nodes.push_back(oj);
-      }
-    }
-    if (full && kept != dropped)
-      throw std::invalid_argument("SO3LR: the full short-range list is not symmetric (an edge lacks its reverse)");
-  };
-  std::vector<int> sr_rows, sr_nodes, lr_rows, lr_nodes;
-  collect("short-range", sr_kind == 0, sr_inum, sr_ilist, sr_off, sr_neigh, sr_rows, sr_nodes);
-  collect("long-range", false, lr_inum, lr_ilist, lr_off, lr_neigh, lr_rows, lr_nodes);
-  std::vector<int> sr_off_v, sr_inc, lr_off_v, lr_inc;
-  incidence(n, sr_nodes, sr_off_v, sr_inc);
-  incidence(n, lr_nodes, lr_off_v, lr_inc);
-  p_sr_ = std::int64_t(sr_nodes.size() / 2);
-  p_lr_ = std::int64_t(lr_nodes.size() / 2);
-  n_rows_ = n_rows;
-  shift_mode_ = false;
-  permuted_ = false;
-  auto put = [&](Buffer *b, const std::vector<int> &v) {
-    HIP_CHECK(hipMemcpyAsync(ensure<int>(b, v.size()), v.data(), v.size() * sizeof(int), hipMemcpyHostToDevice, stream_));
-  };
-  put(sr_rows_, sr_rows); put(sr_nodes_, sr_nodes); put(sr_inc_off_, sr_off_v); put(sr_inc_, sr_inc);
-  put(lr_rows_, lr_rows); put(lr_nodes_, lr_nodes); put(lr_inc_off_, lr_off_v); put(lr_inc_, lr_inc);
-  HIP_CHECK(hipStreamSynchronize(stream_));
-  topology_ready_ = true;
   ++topo_version_;
   evaluated_ = false;
 }

@@ -31,6 +31,12 @@ struct DeviceError : std::runtime_error {
   explicit DeviceError(const std::string &what) : std::runtime_error(what) {}
 };
 
+// Neighbour lists inconsistent with the rows or with each other: reported as
+// SO3LR_ERR_TOPOLOGY at the C ABI.
+struct TopologyError : std::runtime_error {
+  explicit TopologyError(const std::string &what) : std::runtime_error(what) {}
+};
+
 // Device weight pointers for one interaction block.
 struct BlockWeights {
   const double *wqkv;                   // (5, 4, 32, 32): q k v q_ev k_ev, (head, in, out)
@@ -215,6 +221,10 @@ class Evaluator {
   // spatial node order of the device reneighbor path: node n holds owned atom
   // perm[n]; node-ordered copies of the per-atom inputs
   Buffer *perm_, *nz_, *nx0_, *xn_;
+  // LAMMPS lists on the device (set_topology): the raw upload and the build's
+  // work buffers; [0] short range, [1] long range
+  Buffer *top_owner_, *top_ilist_[2], *top_off_[2], *top_neigh_[2], *top_cnt_[2], *top_poff_[2], *top_stat_,
+      *top_slots_, *top_skeys_, *top_tmp_;
   std::vector<int> perm_host_;
   bool permuted_ = false;
   bool shift_mode_ = false;

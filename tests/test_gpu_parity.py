@@ -337,3 +337,55 @@ def test_graph_replay_matches_eager(monkeypatch):
             graph.compute_device(xt, other, stream=stream.cuda_stream)
             xt.add_(torch.tensor(rng.normal(scale=1e-3, size=pos.shape), dtype=torch.float64, device=dev))
             stream.synchronize()
+
+
+def test_topology_faults_are_refused():
+    """so3lr_set_topology builds the pair tables on the GPU; malformed LAMMPS
+    lists come back as SO3LR_ERR_TOPOLOGY (owner map, a row out of range, an
+    atom paired with its own image, a full list missing a reverse edge), and
+    the context stays usable."""
+    from so3lrxlammps_amd import Context, Lists, _lib
+    ref, z, pos, box = support.load_golden("water3000")
+    c = Context(support.MODEL, 0)
+    c.set_system(z, 0, 1)
+    lists = Lists(pos, np.zeros(3), box, (1, 1, 1))
+    (si, so, sn), (li, lo_, ln) = lists.lists
+    n = len(z)
+
+    def submit(owner=lists.owner, sneigh=sn, lneigh=ln):
+        owner = np.ascontiguousarray(owner, dtype=np.int32)
+        sneigh = np.ascontiguousarray(sneigh, dtype=np.int32)
+        lneigh = np.ascontiguousarray(lneigh, dtype=np.int32)
+        rc = c._lib.so3lr_set_topology(c._h, lists.rows, _lib.ptr(owner), _lib.LIST_FULL, len(si), _lib.ptr(si),
+                                       _lib.ptr(so), _lib.ptr(sneigh), len(li), _lib.ptr(li), _lib.ptr(lo_),
+                                       _lib.ptr(lneigh))
+        return rc, c._lib.so3lr_last_error(c._h).decode()
+
+    bad_owner = lists.owner.copy()
+    bad_owner[n + 3] = n + 7  # a ghost mapped outside the owned atoms
+    rc, msg = submit(owner=bad_owner)
+    assert rc == _lib.ERR_TOPOLOGY and "owner_of_row" in msg, msg
+    bad = sn.copy()
+    bad[5] = lists.rows + 2  # a row that does not exist
+    rc, msg = submit(sneigh=bad)
+    assert rc == _lib.ERR_TOPOLOGY and "out of range" in msg, msg
+    ghost = n + 10
+    i = int(lists.owner[ghost])
+    bad = ln.copy()
+    bad[lo_[i]] = ghost  # atom i paired with its own image
+    rc, msg = submit(lneigh=bad)
+    assert rc == _lib.ERR_TOPOLOGY and "own periodic image" in msg, msg
+    bad = sn.copy()
+    bad[so[0]] = si[0]  # the receiver itself (skipped): its partner's reverse edge is now unmatched
+    rc, msg = submit(sneigh=bad)
+    assert rc == _lib.ERR_TOPOLOGY and "not symmetric" in msg, msg
+    # still usable: the good lists give the rows-path result of a fresh context
+    c.set_topology(lists)
+    e1, f1, _, w1 = c.compute(lists.rows_positions(pos))
+    c2 = Context(support.MODEL, 0)
+    c2.set_system(z, 0, 1)
+    c2.set_topology(lists)
+    e2, f2, _, w2 = c2.compute(lists.rows_positions(pos))
+    assert e1 == e2 and np.array_equal(f1, f2) and np.array_equal(w1, w2)
+    c.close()
+    c2.close()
