@@ -13,6 +13,7 @@
 #include "evaluator.hpp"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -519,6 +520,9 @@ struct Stream {
 #define SO3LR_FILTER_PF 4
 #endif
 constexpr int kFilterPF = SO3LR_FILTER_PF;  // fragments in flight per wavefront
+#ifndef SO3LR_FILTER_BWD_PF
+#define SO3LR_FILTER_BWD_PF SO3LR_FILTER_PF
+#endif
 // Two wavefronts per SIMD (<= 256 registers per lane): measured faster than
 // one wavefront with a deeper prefetch, since the second wave's MFMAs cover
 // the first one's VALU phases (RBF, SiLU).
@@ -537,6 +541,30 @@ __device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
   c = mfma(w[1], b[1], c);
   c = mfma(w[2], b[2], c);
   return mfma(w[3], b[3], c);
+}
+
+// first equivariant channel of degree slot h (l = h + 1): 0, 3, 8, 15
+__device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
+
+// The same basis and, in db, d rbf / dr at those channels (zero where the
+// clamp of x is active): rbf (-gamma k + gamma k' x / (1 - x)).
+__device__ __forceinline__ void rbf8_with_grad(double r, int g, const FilterMfma &A, const double *tab, v4d *rb,
+                                               v4d *db) {
+  const double gr = -A.gamma * r;
+  double x = exp_tab(gr, tab), lx = gr;
+  bool clamped = false;
+  if (x < 1e-6) { x = 1e-6; lx = log(1e-6); clamped = true; }
+  if (x > 1.0 - 1e-6) { x = 1.0 - 1e-6; lx = log(1.0 - 1e-6); clamped = true; }
+  const double l1x = log(1.0 - x);
+  const double q = clamped ? 0.0 : A.gamma * x / (1.0 - x), gk = clamped ? 0.0 : -A.gamma;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
+    const double k = A.rbf_k[ch], kr = A.rbf_kr[ch];
+    const double v = exp_tab(A.rbf_b[ch] + k * lx + kr * l1x, tab);
+    rb[t >> 2][t & 3] = v;
+    db[t >> 2][t & 3] = v * (gk * k + kr * q);
+  }
 }
 
 // Bernstein basis of pair distance r at channels 16 T + g + 4 v (T < 2, v < 4).
@@ -706,81 +734,231 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   });
 }
 
-// Reverse of both filters, the Bernstein basis and the cutoff for 16 pairs per
-// wavefront.  Per filter the stream holds 133 entries:
-//   s <  88  per K chunk T = s / 11: the df chunk, then W1^T tiles 0..7 and
-//            E1^T tiles 0..1 (d hidden = W^T df);
-//   s < 112  per tile mt = (s - 88) / 3: the layer-0 bias, then W0 chunks 0, 1
-//            (pre-activation recomputed tile by tile, then d hidden *= silu');
-//   s < 115  the spherical layer-0 biases and operand (same, for the 4 -> 32 layer);
-//   s < 131  W0^T (d rbf), s < 133  E0^T (ds).
-template <bool EV0>
-__global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const int *n_active, const double *pr, const double *ps,
-                                                         const double *df, const double *dfc, FilterMfma A, double rc,
-                                                         double *ds, double *dr) {
+// Operand schedule of the reverse filter's first section (per filter).
+// Entry kinds: P, a term of the invariant head scalars (q = 0..3: gainv_a,
+// v_b, gainv_b, v_a of chunk T, head h; `last` completes the head); R, a row
+// chunk of the df of chunk T (u = 0..3: q_a, k_b, q_b, k_a); M, the MFMA
+// entry `tile` of chunk T (W1^T tiles 0..7, then E1^T tiles 8..9).  The
+// loads that carry no MFMA work (P and R) ride between the M entries of the
+// previous chunk, so every one of them is covered by MFMA time: chunk T's
+// rows arrive during chunk T - 1, and head h + 1's scalars during head h's
+// chunks (P riders before R riders, so a head's scalars are complete before
+// its first df is formed).
+struct BwdEntry {
+  int kind, q, T, h, last;
+};
+template <bool EV0, int WHICH>
+constexpr int bwd_section_len() {
+  constexpr int NM = EV0 ? 8 : 10;
+  return (WHICH == 0 ? 8 + 24 : 0) + 4 + 8 * NM + 28;
+}
+template <bool EV0, int WHICH>
+constexpr std::array<BwdEntry, bwd_section_len<EV0, WHICH>()> bwd_schedule() {
+  constexpr int NM = EV0 ? 8 : 10;
+  std::array<BwdEntry, bwd_section_len<EV0, WHICH>()> out{};
+  int n = 0;
+  auto put = [&](int kind, int q, int T, int h, int last) { out[n++] = BwdEntry{kind, q, T, h, last}; };
+  if (WHICH == 0)  // lead-in: head 0's scalars
+    for (int T = 0; T < 2; ++T)
+      for (int q = 0; q < 4; ++q) put(0, q, T, 0, T == 1 && q == 3);
+  for (int u = 0; u < 4; ++u) put(1, u, 0, 0, 0);  // lead-in: chunk 0's rows
+  for (int T = 0; T < 8; ++T) {
+    BwdEntry riders[8] = {};
+    int nr = 0;
+    const int h = T / 2;
+    if (WHICH == 0 && h + 1 < 4)
+      for (int q = 0; q < 4; ++q)
+        riders[nr++] = BwdEntry{0, q, 2 * (h + 1) + (T & 1), h + 1, (T & 1) == 1 && q == 3};
+    if (T + 1 < 8)
+      for (int u = 0; u < 4; ++u) riders[nr++] = BwdEntry{1, u, T + 1, (T + 1) / 2, 0};
+    for (int m = 0; m < NM; ++m) {
+      put(2, m, T, h, 0);
+      if (m < nr) out[n++] = riders[m];
+    }
+  }
+  return out;
+}
+template <bool EV0, int WHICH>
+constexpr BwdEntry bwd_entry(int s) {
+  return bwd_schedule<EV0, WHICH>()[s];
+}
+// Compile-time check of a schedule: every slot filled (one M entry per MFMA
+// tile of each chunk), the four row entries of chunk T before its first M
+// entry, each head's scalars complete (`last`) before the first row entry
+// that uses them.
+template <bool EV0, int WHICH>
+constexpr bool bwd_schedule_ok() {
+  constexpr int NM = EV0 ? 8 : 10;
+  const auto sc = bwd_schedule<EV0, WHICH>();
+  int rows_seen[8] = {}, m_seen[8] = {}, head_done = WHICH == 0 ? -1 : 3;
+  for (const BwdEntry &e : sc) {
+    if (e.kind == 0 && e.last) head_done = e.h;
+    if (e.kind == 1) {
+      if (e.q == 1 && e.h > head_done) return false;
+      if (m_seen[e.T]) return false;
+      ++rows_seen[e.T];
+    }
+    if (e.kind == 2) {
+      if (rows_seen[e.T] != 4) return false;
+      ++m_seen[e.T];
+    }
+  }
+  for (int T = 0; T < 8; ++T)
+    if (m_seen[T] != NM || rows_seen[T] != 4) return false;
+  return true;
+}
+static_assert(bwd_schedule_ok<false, 0>() && bwd_schedule_ok<false, 1>() && bwd_schedule_ok<true, 0>() &&
+                  bwd_schedule_ok<true, 1>(),
+              "reverse-filter operand schedule out of order");
+
+// Reverse of the attention's pair terms, of both filters, of the Bernstein
+// basis and of the cutoff, for 16 pairs per wavefront
+// (kokkos_attention_scatter_reverse.cpp:280-500 for the pair adjoints;
+// kokkos_block2_attention_input_reverse.cpp:198-240,301-336 for the rest).
+//
+// The adjoint of the filter outputs, df, is formed here in registers and
+// never stored.  For pair {a, b} (a receives along b -> a, b along a -> b)
+// and head h, with g the attention-residual adjoints (gainv, gaev) of the
+// block and fc the cutoff:
+//   ci_h = <g_a, v_b>_h,  co_h = <g_b, v_a>_h        (invariant channels of h)
+//   ce_h = <gev_a, Y>_h,  coe_h = (-1)^(h+1) <gev_b, Y>_h   (degree h + 1)
+//   df_inv[c] = fc/avg (ci_h q_a[c] k_b[c] + co_h q_b[c] k_a[c])
+//   df_ev[c]  = fc/avg (ce_h qe_a[c] ke_b[c] + coe_h qe_b[c] ke_a[c])
+//   dE/dfc    = sum_h alpha(a<-b)_h ci_h + alpha_ev(a<-b)_h ce_h
+//                     + alpha(b<-a)_h co_h + alpha_ev(b<-a)_h coe_h
+//   dE/dY[m] += fc (alpha_ev(a<-b) gev_a[m] + (-1)^l alpha_ev(b<-a) gev_b[m])
+// (FIRST, the first block of the reverse pass, writes dE/dY without reading
+// it).  The node rows (q, k, v, q_ev, k_ev of both endpoints and their
+// gainv) arrive through the operand stream in the tile-transposed channel
+// order, so a lane's four channels of a tile are one 32-byte vector.
+//
+// Per filter the stream holds the first section (bwd_schedule: the head
+// scalars, the df rows and d hidden = W^T df over W1^T and E1^T), then:
+//   per tile mt (8): the layer-0 bias, then W0 chunks 0, 1 (pre-activation
+//             recomputed tile by tile, then d hidden *= silu');
+//   the spherical layer-0 biases and operand (the same, 4 -> 32);
+//   W0^T (16): d rbf = W0^T d hidden;
+//   E0^T (2):  d s = E0^T d hidden_s.
+// EV0 (block 0, ev = 0): the spherical branch is a constant (folded into the
+// output bias by the forward kernel) and s has no adjoint to give, so its
+// entries are left out.
+template <bool EV0, bool FIRST>
+__global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
+    const int *n_active, const int *pa, const double *pr, const double *ps, const double *pfc, const double *pY,
+    const double *palpha, const double *__restrict__ qkv, const double *__restrict__ gainv,
+    const double *__restrict__ gaev, double inv_avg, FilterMfma A, double rc, double *ds, double *dr, double *dY) {
   SO3LR_EXP2_TABLE(A)
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // consecutive pairs on one XCD: the node rows they gather are spatial
+  // neighbours, so they share that XCD's L2
+  const int blk = xcd_block_active((nact + 63) / 64);
+  if (blk < 0) return;
+  const int wave = blk * 4 + (threadIdx.x >> 6);
   if (wave * 16 >= nact) return;
   const int p = wave * 16 + j;
   const bool valid = p < nact;
   const int pp = valid ? p : nact - 1;
-  const v4d *dfv = reinterpret_cast<const v4d *>(df + 256 * std::size_t(pp) + 4 * g);
+  const int a = pa[2 * pp], b = pa[2 * pp + 1];
+  // node rows, tile-transposed: chunk T of this lane at +16 T
+  const double *ra = qkv + std::size_t(a) * 640 + 4 * g, *rb = qkv + std::size_t(b) * 640 + 4 * g;
+  const double *gaa = gainv + std::size_t(a) * kF + 4 * g, *gab = gainv + std::size_t(b) * kF + 4 * g;
+  auto row = [](const double *r, int off) { return *reinterpret_cast<const v4d *>(r + off); };
 
-  // Per filter the stream holds, in order:
-  //   per K chunk T (8): the df chunk, W1^T tiles 0..7 and E1^T tiles 0..1
-  //             (d hidden = W^T df);
-  //   per tile mt (8): the layer-0 bias, then W0 chunks 0, 1 (pre-activation
-  //             recomputed tile by tile, then d hidden *= silu');
-  //   the spherical layer-0 biases and operand (the same, 4 -> 32);
-  //   W0^T (16): d rbf = W0^T d hidden;
-  //   E0^T (2):  d s = E0^T d hidden_s.
-  // EV0 (block 0, ev = 0): the spherical branch is a constant (folded into
-  // the output bias by the forward kernel) and s has no adjoint to give, so
-  // its entries are left out.
-  constexpr int PTA = EV0 ? 9 : 11;
-  constexpr int A_END = 8 * PTA, B_END = A_END + 24, C_END = B_END + (EV0 ? 0 : 3), D_END = C_END + 16;
-  constexpr int NB = D_END + (EV0 ? 0 : 2);
+  constexpr int A_END0 = bwd_section_len<EV0, 0>(), A_END1 = bwd_section_len<EV0, 1>();
+  constexpr int B_LEN = 24, C_LEN = EV0 ? 0 : 3, D_LEN = 16, E_LEN = EV0 ? 0 : 2;
+  constexpr int TAIL = B_LEN + C_LEN + D_LEN + E_LEN;
+  constexpr int NB0 = A_END0 + TAIL, NB1 = A_END1 + TAIL;
   auto load = [&](auto si) -> v4d {
-    constexpr int S = decltype(si)::value, which = S / NB, s = S % NB;
+    constexpr int S = decltype(si)::value, which = S < NB0 ? 0 : 1, s = which ? S - NB0 : S;
+    constexpr int A_END = which ? A_END1 : A_END0;
+    constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;
     if constexpr (s < A_END) {
-      constexpr int T = s / PTA, u = s % PTA;
-      if constexpr (u == 0) {
-        return dfv[which * 32 + 4 * T];  // channels 16 T + g + 4 v, v = 0..3 (fpos)
-      } else if constexpr (u <= 8) {
-        return wload(A.w1tp[which], 8, u - 1, T, lane);
+      constexpr BwdEntry e = bwd_entry<EV0, which>(s);
+      if constexpr (e.kind == 0) {
+        if constexpr (e.q == 0) return row(gaa, 16 * e.T);
+        else if constexpr (e.q == 1) return row(rb, 256 + 16 * e.T);
+        else if constexpr (e.q == 2) return row(gab, 16 * e.T);
+        else return row(ra, 256 + 16 * e.T);
+      } else if constexpr (e.kind == 1) {
+        if constexpr (e.q == 0) return row(ra, qoff + 16 * e.T);
+        else if constexpr (e.q == 1) return row(rb, koff + 16 * e.T);
+        else if constexpr (e.q == 2) return row(rb, qoff + 16 * e.T);
+        else return row(ra, koff + 16 * e.T);
       } else {
-        return wload(A.e1tp[which], 8, u - 9, T, lane);
+        if constexpr (e.q < 8) return wload(A.w1tp[which], 8, e.q, e.T, lane);
+        else return wload(A.e1tp[which], 8, e.q - 8, e.T, lane);
       }
-    } else if constexpr (s < B_END) {
+    } else if constexpr (s < A_END + B_LEN) {
       constexpr int mt = (s - A_END) / 3, u = (s - A_END) % 3;
       if constexpr (u == 0) return tile_load(A.b0p[which], mt, lane);
       else return wload(A.w0p[which], 2, mt, u - 1, lane);
-    } else if constexpr (s < C_END) {
-      if constexpr (s < C_END - 1) return tile_load(A.eb0p[which], s - B_END, lane);
+    } else if constexpr (s < A_END + B_LEN + C_LEN) {
+      constexpr int c = s - A_END - B_LEN;
+      if constexpr (c < 2) return tile_load(A.eb0p[which], c, lane);
       else return reinterpret_cast<const v4d *>(A.e0pk[which])[lane];
-    } else if constexpr (s < D_END) {
-      return wload(A.w0tp[which], 8, (s - C_END) % 2, (s - C_END) / 2, lane);
+    } else if constexpr (s < A_END + B_LEN + C_LEN + D_LEN) {
+      constexpr int d = s - A_END - B_LEN - C_LEN;
+      return wload(A.w0tp[which], 8, d % 2, d / 2, lane);
     } else {
-      return wload(A.e0tp[which], 2, 0, s - D_END, lane);
+      return wload(A.e0tp[which], 2, 0, s - A_END - B_LEN - C_LEN - D_LEN, lane);
     }
   };
-  Stream<2 * NB, kFilterPF, decltype(load)> st(load);
+  Stream<NB0 + NB1, SO3LR_FILTER_BWD_PF, decltype(load)> st(load);
   st.prime();
 
   const double r = pr[pp];
-  v4d rb[2];
-  double xb;
-  rbf8(r, g, A, exp2_lds, rb, xb);
-  const double sg = EV0 ? 0.0 : ps[4 * std::size_t(pp) + g];
+  const double fcs = pfc[pp] * inv_avg;  // fc / avg
+  const double *al = palpha + 16 * std::size_t(pp);
+  // Equivariant pair terms: lane group g takes degree slot g (channels
+  // off(g) .. off(g) + 2g + 2, contiguous in the natural ev order): its
+  // <gev_a, Y>, <gev_b, Y> and its share of dE/dY.
+  double ce_mine = 0.0, coe_mine = 0.0;
+  {
+    const int lo = ev_offset(g), n_m = 2 * g + 3;
+    const double par = slot_parity(g);
+    const double ain_e = al[4 + g], aout_e = al[12 + g];
+    const double *gea = gaev + std::size_t(a) * kE, *geb = gaev + std::size_t(b) * kE;
+    const double *y = pY + kE * std::size_t(pp);
+    double *dy = dY + kE * std::size_t(pp);
+    const double fc = pfc[pp];
+    for (int k = 0; k < n_m; ++k) {
+      const int m = lo + k;
+      const double ea = gea[m], eb = geb[m], ym = y[m];
+      ce_mine += ea * ym;
+      coe_mine += eb * ym;
+      if (valid) dy[m] = (FIRST ? 0.0 : dy[m]) + fc * (ain_e * ea + par * aout_e * eb);
+    }
+    coe_mine *= par;
+  }
+  // dE/dfc: the equivariant terms of this lane group's slot now, the
+  // invariant ones head by head below (every lane ends with the whole sum)
+  double dfc = al[4 + g] * ce_mine + al[12 + g] * coe_mine;
+  dfc += __shfl_xor(dfc, 16, kWave);
+  dfc += __shfl_xor(dfc, 32, kWave);
+  // The running sums (dfc, part, ds_acc) are needed only at the end; an empty
+  // asm on each update keeps the compiler from sinking the updates to that
+  // use, which would hold every head's terms in registers until then.
+  auto pin = [](double &v) { asm volatile("" : "+v"(v)); };
+  pin(dfc);
+
   const v4d zero = v4d{0, 0, 0, 0};
-  v4d dh[8], dh2[2], bT, pre, prev, pre2[2];
-  v4d drb[2] = {zero, zero};
-  v4d dsa = zero;
+  const double sg = EV0 ? 0.0 : ps[4 * std::size_t(pp) + g];
+  // the Bernstein basis is formed where the layer-0 recompute starts (once
+  // per filter), not held through the df / W^T section
+  v4d rb8[2], db8[2];
+  v4d dh[8], dh2[2], bT, bTn, t2, hold, pre, prev, pre2[2];
+  // d rbf and d s of one filter, folded into scalars at the end of their
+  // sections (dE/dr is linear in d rbf), so neither is held through the next
+  // filter's df section
+  v4d drb[2], dsa;
+  double part = 0.0, ds_acc = 0.0;
+  double ci = 0.0, co = 0.0, s_in = 0.0, s_out = 0.0;
 
   st.run([&](auto si, const v4d &w) {
-    constexpr int S = decltype(si)::value, s = S % NB;
+    constexpr int S = decltype(si)::value, which = S < NB0 ? 0 : 1, s = which ? S - NB0 : S;
+    constexpr int A_END = which ? A_END1 : A_END0;
+    constexpr int B_END = A_END + B_LEN, C_END = B_END + C_LEN, D_END = C_END + D_LEN;
     if constexpr (s == 0) {
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) dh[mt] = zero;
@@ -788,16 +966,65 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
       dh2[1] = zero;
     }
     if constexpr (s < A_END) {
-      constexpr int u = s % PTA;
-      if constexpr (u == 0) bT = w;
-      else if constexpr (u <= 8) dh[u - 1] = mfma4(w, bT, dh[u - 1]);
-      else dh2[u - 9] = mfma4(w, bT, dh2[u - 9]);
+      constexpr BwdEntry e = bwd_entry<EV0, which>(s);
+      if constexpr (e.kind == 0) {
+        // <gainv_a, v_b> and <gainv_b, v_a> over the lane's channels of head e.h
+        if constexpr (e.q == 0 || e.q == 2) {
+          hold = w;
+        } else {
+          const double d = ((hold[0] * w[0] + hold[1] * w[1]) + hold[2] * w[2]) + hold[3] * w[3];
+          if constexpr (e.q == 1) ci += d;
+          else co += d;
+        }
+        if constexpr (e.last) {
+          // the head is complete: sum over the four lane groups
+          ci += __shfl_xor(ci, 16, kWave);
+          ci += __shfl_xor(ci, 32, kWave);
+          co += __shfl_xor(co, 16, kWave);
+          co += __shfl_xor(co, 32, kWave);
+          dfc += al[e.h] * ci + al[8 + e.h] * co;
+          pin(dfc);
+          s_in = fcs * ci;
+          s_out = fcs * co;
+          ci = 0.0;
+          co = 0.0;
+        }
+      } else if constexpr (e.kind == 1) {
+        // the df of chunk e.T, built while the previous chunk's MFMAs run
+        if constexpr (which == 1 && e.q == 0 && (e.T & 1) == 0) {
+          // the slot-h sums live in lane group h
+          s_in = fcs * __shfl(ce_mine, j + 16 * e.h, kWave);
+          s_out = fcs * __shfl(coe_mine, j + 16 * e.h, kWave);
+        }
+        if constexpr (e.q == 0) {
+          bTn = w;  // q_a
+        } else if constexpr (e.q == 1) {
+          bTn = s_in * (bTn * w);  // (a <- b): q_a k_b
+        } else if constexpr (e.q == 2) {
+          t2 = w;  // q_b
+        } else {
+          bTn += s_out * (t2 * w);  // (b <- a): q_b k_a
+        }
+      } else {
+        if constexpr (e.q == 0) bT = bTn;
+        if constexpr (e.q < 8) dh[e.q] = mfma4(w, bT, dh[e.q]);
+        else dh2[e.q - 8] = mfma4(w, bT, dh2[e.q - 8]);
+      }
     } else if constexpr (s < B_END) {
       constexpr int mt = (s - A_END) / 3, u = (s - A_END) % 3;
+      if constexpr (s == A_END) {
+        // each filter forms its own copy: an opaque copy of the inputs keeps
+        // the compiler from merging the two computations into one that stays
+        // live across the second filter's df section
+        double rr = r;
+        int gg = g;
+        asm volatile("" : "+v"(rr), "+v"(gg));
+        rbf8_with_grad(rr, gg, A, exp2_lds, rb8, db8);
+      }
       if constexpr (u == 0) {
         pre = w;
       } else {
-        pre = mfma4(w, rb[u - 1], pre);
+        pre = mfma4(w, rb8[u - 1], pre);
         // silu' of the previous tile's pre-activation (complete by now) runs
         // while this tile's MFMAs do
         if constexpr (u == 1 && mt > 0) {
@@ -818,9 +1045,24 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
         }
       }
     } else if constexpr (s < D_END) {
+      if constexpr (s == C_END) {
+        drb[0] = zero;
+        drb[1] = zero;
+      }
       drb[(s - C_END) % 2] = mfma4(w, dh[(s - C_END) / 2], drb[(s - C_END) % 2]);
+      if constexpr (s == D_END - 1) {
+        // dE/dr through the Bernstein basis
+#pragma unroll
+        for (int t = 0; t < 8; ++t) part += drb[t >> 2][t & 3] * db8[t >> 2][t & 3];
+        pin(part);
+      }
     } else {
+      if constexpr (s == D_END) dsa = zero;
       dsa = mfma4(w, dh2[s - D_END], dsa);
+      if constexpr (s == D_END + E_LEN - 1) {
+        ds_acc += dsa[0];  // rows 0..3 of the padded tile: lane group g, register 0
+        pin(ds_acc);
+      }
     }
     // the last tile's silu' (it is needed from the last two W0^T steps on)
     if constexpr (s == B_END) {
@@ -829,31 +1071,21 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(const 
     }
   });
 
-  // dE/dr: Bernstein derivative (zero where the clamp is active) + cutoff
-  double part = 0.0;
-  if (xb > 1e-6 && xb < 1.0 - 1e-6) {
-    const double q = A.gamma * xb / (1.0 - xb);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
-      part += drb[t >> 2][t & 3] * rb[t >> 2][t & 3] * (-A.gamma * A.rbf_k[ch] + A.rbf_kr[ch] * q);
-    }
-  }
+  // dE/dr: the Bernstein part of both filters + the cutoff
   part += __shfl_xor(part, 16, kWave);
   part += __shfl_xor(part, 32, kWave);
   if (valid) {
-    if constexpr (!EV0) ds[4 * std::size_t(p) + g] = dsa[0];  // rows 0..3 of the padded tile: lane group g, register 0
+    if constexpr (!EV0) ds[4 * std::size_t(p) + g] = ds_acc;
     if (g == 0) {
       double grad = part;
       if (r < rc) {
         const double t = r / rc;
-        grad += dfc[p] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
+        grad += dfc * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
       }
       dr[p] += grad;
     }
   }
 }
-
 
 // ---------------------------------------------------------------- MFMA node GEMMs
 // out[n][o] = sum_k W[o][k] X[n][k] (+ epilogue), 16 nodes per wavefront as the
@@ -1013,13 +1245,17 @@ __global__ __launch_bounds__(256) void k_qkv_bwd_mfma(int rows, const double *__
     else acc[u - 1] = mfma4(wv, bT, acc[u - 1]);
     if constexpr (s == PER_H - 1) {
       if (valid) {
+        // base (the attention-residual adjoint) is stored in the
+        // tile-transposed order: channels 16 mt + g + 4 r at 16 mt + 4 g + r
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 2; ++mt) {
+          const v4d bv = *reinterpret_cast<const v4d *>(base + std::size_t(n) * kF + h * kHW + 16 * mt + 4 * g);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int c = h * kHW + 16 * mt + g + 4 * r;
-            dx[std::size_t(n) * kF + c] = base[std::size_t(n) * kF + c] + acc[mt][r];
+            dx[std::size_t(n) * kF + c] = bv[r] + acc[mt][r];
           }
+        }
       }
     }
   });
@@ -1034,7 +1270,6 @@ __device__ __forceinline__ void st2(double *p, double a, double b) { *reinterpre
 // equivariant channel off[h] + t of degree h + 1 when t < 2 h + 3, so every
 // per-head sum is a 16-lane group reduction.
 
-__device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
 
 // Active incidence of this step: entry k of a node's list as active pair
 // index * 2 + side (-1 for a candidate beyond the cutoff) and its partner
@@ -1621,11 +1856,15 @@ __global__ __launch_bounds__(256) void k_node_bwd(int N, const double *__restric
   tm /= kF;
   tx /= kF;
   if (valid) {
+    // tile-transposed channel order (fpos): channels 16 T + g + 4 r, r = 0..3,
+    // of this lane are one 32-byte vector at 16 T + 4 g
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < 4; ++q) {
+      v4d out;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        gainv[nn * kF + 16 * (o0 + q) + 4 * r + g] = is1 * (acc[q][r] - tm - hat[q][r] * tx);
+      for (int r = 0; r < 4; ++r) out[r] = is1 * (acc[q][r] - tm - hat[q][r] * tx);
+      *reinterpret_cast<v4d *>(gainv + nn * kF + 16 * (o0 + q) + 4 * g) = out;
+    }
     if (h == 0) {
 #pragma unroll
       for (int k = 0; k < 6; ++k) gaev[nn * kE + g + 4 * k] = ga[k];
@@ -1850,7 +2089,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   const double2 mqev = ld2(me + 384 + p0), mkev = ld2(me + 512 + p0);
   const double mq0 = mqv.x, mq1 = mqv.y, mk0 = mkv.x, mk1 = mkv.y, mv0 = mvv.x, mv1 = mvv.y;
   const double mqe0 = mqev.x, mqe1 = mqev.y, mke0 = mkev.x, mke1 = mkev.y;
-  const double mg0 = gainv[std::size_t(n) * kF + c0], mg1 = gainv[std::size_t(n) * kF + c1];
+  const double2 mgv = ld2(gainv + std::size_t(n) * kF + p0);  // fpos rows: channels c0, c1
+  const double mg0 = mgv.x, mg1 = mgv.y;
   const double mge = evv ? gaev[std::size_t(n) * kE + m] : 0.0;
   double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
   struct Terms {
@@ -1867,7 +2107,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
     // every load of the pair unconditional (m = 0 on lanes without an
     // equivariant channel: a valid address, the value is masked below), so
     // one wait covers the whole iteration
-    const double og0 = gainv[std::size_t(o) * kF + c0], og1 = gainv[std::size_t(o) * kF + c1];
+    const double2 ogv = ld2(gainv + std::size_t(o) * kF + p0);
+    const double og0 = ogv.x, og1 = ogv.y;
     const double oge_ld = gaev[std::size_t(o) * kE + m];
     const double *fp = pf + 256 * std::size_t(p);
     const v2d fiv = __builtin_nontemporal_load(reinterpret_cast<const v2d *>(fp + p0));
@@ -1938,6 +2179,75 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   st2(g + 512 + p0, dke0, dke1);
 }
 
+
+// Attention reverse, node adjoints only (kokkos_attention_scatter_reverse.cpp:
+// 280-500): for node n and each active pair p = {n, o}, the incoming edge
+// o -> n gives dq_n, dq_ev_n and the outgoing edge n -> o gives dk_n,
+// dk_ev_n, dv_n (sender-side terms gathered, not scattered).  The pair
+// adjoints (df, dE/dfc, dE/dY) are formed by the reverse filter kernel, so
+// nothing is written per pair.  Lane layout as in k_attn_fwd; gainv in the
+// tile-transposed order.
+__global__ __launch_bounds__(256) void k_attn_bwd_nodes(int N, const int *inc_off, const int *__restrict__ iact,
+                                                        const int *__restrict__ iother, const double *__restrict__ qkv,
+                                                        const double *__restrict__ pf, const double *__restrict__ pY,
+                                                        const double *__restrict__ pfc,
+                                                        const double *__restrict__ palpha,
+                                                        const double *__restrict__ gainv,
+                                                        const double *__restrict__ gaev, double inv_avg,
+                                                        double *__restrict__ gqkv) {
+  const int lane = threadIdx.x & 63;
+  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int h = lane >> 4, t = lane & 15;
+  const int p0 = 32 * h + 2 * t;
+  const bool evv = t < 2 * h + 3;
+  const int m = evv ? ev_offset(h) + t : 0;
+  const double par = slot_parity(h);
+  const double *me = qkv + std::size_t(n) * 640;
+  const double2 mvv = ld2(me + 256 + p0);
+  const double2 mgv = ld2(gainv + std::size_t(n) * kF + p0);
+  const double mge = evv ? gaev[std::size_t(n) * kE + m] : 0.0;
+  double dq0 = 0, dq1 = 0, dk0 = 0, dk1 = 0, dv0 = 0, dv1 = 0, dqe0 = 0, dqe1 = 0, dke0 = 0, dke1 = 0;
+  auto visit = [&](int e, int o) {
+    const int p = e >> 1, side = e & 1;
+    const double *ot = qkv + std::size_t(o) * 640;
+    const double2 oqv = ld2(ot + p0), okv = ld2(ot + 128 + p0), ovv = ld2(ot + 256 + p0);
+    const double2 oqev = ld2(ot + 384 + p0), okev = ld2(ot + 512 + p0);
+    const double2 ogv = ld2(gainv + std::size_t(o) * kF + p0);
+    const double oge_ld = gaev[std::size_t(o) * kE + m];  // m = 0 off the ev lanes: valid, masked below
+    const double *fp = pf + 256 * std::size_t(p);
+    const v2d fiv = __builtin_nontemporal_load(reinterpret_cast<const v2d *>(fp + p0));
+    const v2d fev = __builtin_nontemporal_load(reinterpret_cast<const v2d *>(fp + 128 + p0));
+    const double fc = pfc[p];
+    const double y_ld = pY[kE * std::size_t(p) + m];
+    const double aout_i = palpha[16 * std::size_t(p) + 8 * (1 - side) + h];
+    const double oge = evv ? oge_ld : 0.0;
+    const double y = evv ? y_ld : 0.0;
+    const double y_n = side == 0 ? y : par * y;  // harmonics of edge o -> n
+    const double y_o = side == 0 ? par * y : y;  // harmonics of edge n -> o
+    const double ci = group_sum(mgv.x * ovv.x + mgv.y * ovv.y);
+    const double ce = group_sum(mge * y_n);
+    const double co = group_sum(ogv.x * mvv.x + ogv.y * mvv.y);
+    const double coe = group_sum(oge * y_o);
+    const double sin_ = fc * ci * inv_avg, sine = fc * ce * inv_avg;
+    const double sout = fc * co * inv_avg, soute = fc * coe * inv_avg;
+    dq0 += sin_ * okv.x * fiv.x; dq1 += sin_ * okv.y * fiv.y;
+    dqe0 += sine * okev.x * fev.x; dqe1 += sine * okev.y * fev.y;
+    dk0 += sout * oqv.x * fiv.x; dk1 += sout * oqv.y * fiv.y;
+    dke0 += soute * oqev.x * fev.x; dke1 += soute * oqev.y * fev.y;
+    dv0 += fc * aout_i * ogv.x; dv1 += fc * aout_i * ogv.y;
+  };
+  for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+    visit(e1, o1);
+    if (two) visit(e2, o2);
+  });
+  double *gq = gqkv + std::size_t(n) * 640;
+  st2(gq + p0, dq0, dq1);
+  st2(gq + 128 + p0, dk0, dk1);
+  st2(gq + 256 + p0, dv0, dv1);
+  st2(gq + 384 + p0, dqe0, dqe1);
+  st2(gq + 512 + p0, dke0, dke1);
+}
 
 // g_ev_in = g_aev + sum_pairs 2 (ev_n - ev_o) cg ds[slot]
 __global__ __launch_bounds__(256) void k_ev_bwd(int N, const int *inc_off, const int *__restrict__ iact,
@@ -2669,8 +2979,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     ps = take<double>(ps_, L * 4 * Pz);
     pf = take<double>(pf_, L * 256 * Pz);
     palpha = take<double>(palpha_, L * 16 * Pz);
-    df = take<double>(df_, 256 * Pz);
-    dfc = take<double>(dfc_, Pz);
+    // the pair adjoints of the filters stay in registers on the MFMA path
+    df = naive_filters_ ? take<double>(df_, 256 * Pz) : nullptr;
+    dfc = naive_filters_ ? take<double>(dfc_, Pz) : nullptr;
     ds = take<double>(ds_, 4 * Pz);
     dr = take<double>(dr_, Pz);
     dY = take<double>(dY_, kE * Pz);
@@ -2878,29 +3189,45 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     const NodeChainBwdArgs NB{B.inttp, B.m2tp, B.m1tp, B.int_cg, B.ln1w, B.ln2w};
     hipLaunchKernelGGL(k_node_bwd, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), gx, gev, tb, aevb, p2h,
                        p2i, hpb, n1b, n1hb, n1ib, NB, gainv, gaev);
-    const bool blk0 = b == 0 && !naive_filters_;
-    timed(b == 0 ? "attn_bwd_block0" : "attn_bwd", 1, [&] {
+    if (naive_filters_) {
+      // scalar cross-check path: the attention reverse writes the pair
+      // adjoints (df, dE/dfc, dE/dY) and the scalar filter reverse reads them
+      timed(b == 0 ? "attn_bwd_block0" : "attn_bwd", 1, [&] {
 #define SO3LR_ATTN_BWD(ADJ, FIRST)                                                                              \
   hipLaunchKernelGGL((k_attn_bwd<ADJ, FIRST>), dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY, \
                      pfc, pab, gainv, gaev, inv_avg, gqkv, df, dfc, dY)
-      // the first reverse block (L - 1) writes dY, the others add to it
-      if (b > 0 && b == L - 1) SO3LR_ATTN_BWD(true, true);
-      else if (b > 0) SO3LR_ATTN_BWD(true, false);
-      else if (L == 1) SO3LR_ATTN_BWD(false, true);
-      else SO3LR_ATTN_BWD(false, false);
+        // the first reverse block (L - 1) writes dY, the others add to it
+        if (b > 0 && b == L - 1) SO3LR_ATTN_BWD(true, true);
+        else if (b > 0) SO3LR_ATTN_BWD(true, false);
+        else if (L == 1) SO3LR_ATTN_BWD(false, true);
+        else SO3LR_ATTN_BWD(false, false);
 #undef SO3LR_ATTN_BWD
-    });
-    const FilterMfma FM = filter_mfma(B, hw_, gamma_);
-    timed(blk0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
-      if (naive_filters_)
+      });
+      timed(b == 0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
         hipLaunchKernelGGL(k_filter_bwd, dim3(gP), dim3(128), 0, s, nact, pr, pfc, psb, df, dfc, A, rc_, ds, dr);
-      else if (b == 0)
-        hipLaunchKernelGGL(k_filter_bwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds,
-                           dr);
-      else
-        hipLaunchKernelGGL(k_filter_bwd_mfma<false>, dim3(gP64), dim3(256), 0, s, nact, pr, psb, df, dfc, FM, rc_, ds,
-                           dr);
-    });
+      });
+    } else {
+      // node adjoints (dq, dk, dv; not needed in block 0, whose inputs do not
+      // depend on the positions), then the pair adjoints and the filter
+      // reverse in one pair-major kernel
+      if (b > 0)
+        timed("attn_bwd", 1, [&] {
+          hipLaunchKernelGGL(k_attn_bwd_nodes, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY,
+                             pfc, pab, gainv, gaev, inv_avg, gqkv);
+        });
+      const FilterMfma FM = filter_mfma(B, hw_, gamma_);
+      timed(b == 0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
+#define SO3LR_FILTER_BWD(E0, FIRST)                                                                                \
+  hipLaunchKernelGGL((k_filter_bwd_mfma<E0, FIRST>), dim3(gP64), dim3(256), 0, s, nact, pa, pr, psb, pfc, pY, pab,  \
+                     qb, gainv, gaev, inv_avg, FM, rc_, ds, dr, dY)
+        const bool first = b == L - 1;
+        if (b == 0 && first) SO3LR_FILTER_BWD(true, true);
+        else if (b == 0) SO3LR_FILTER_BWD(true, false);
+        else if (first) SO3LR_FILTER_BWD(false, true);
+        else SO3LR_FILTER_BWD(false, false);
+#undef SO3LR_FILTER_BWD
+      });
+    }
     // the adjoints of a block's inputs x_b, ev_b feed the block below; block
     // 0's inputs (the embedding and ev = 0) do not depend on the positions
     if (b > 0) {
