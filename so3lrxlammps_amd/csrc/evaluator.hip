@@ -738,67 +738,71 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 // Entry kinds: P, a term of the invariant head scalars (q = 0..3: gainv_a,
 // v_b, gainv_b, v_a of chunk T, head h; `last` completes the head); R, a row
 // chunk of the df of chunk T (u = 0..3: q_a, k_b, q_b, k_a); M, the MFMA
-// entry `tile` of chunk T (W1^T tiles 0..7, then E1^T tiles 8..9).  The
-// loads that carry no MFMA work (P and R) ride between the M entries of the
-// previous chunk, so every one of them is covered by MFMA time: chunk T's
-// rows arrive during chunk T - 1, and head h + 1's scalars during head h's
-// chunks (P riders before R riders, so a head's scalars are complete before
-// its first df is formed).
+// entry `tile` of chunk T (W1^T tiles 0..7, then E1^T tiles 8..9); S, the
+// head-h scalar record written by the node-major attention reverse.  The
+// loads that carry no MFMA work (P, S and R) ride between the M entries of
+// the previous chunk, so every one of them is covered by MFMA time: chunk
+// T's rows arrive during chunk T - 1, and head h + 1's scalars during head
+// h's chunks (scalar riders before row riders, so a head's scalars are
+// complete before its first df is formed).
+// SRC: 0 = P entries (block 0, invariant filter), 1 = S entries (blocks
+// after 0, whose node-major reverse wrote the scalars), 2 = neither (block 0,
+// equivariant filter: the scalars are lane shuffles).
 struct BwdEntry {
   int kind, q, T, h, last;
 };
-template <bool EV0, int WHICH>
+constexpr int kBwdP = 0, kBwdR = 1, kBwdM = 2, kBwdS = 3;
+template <int NM, int SRC>
 constexpr int bwd_section_len() {
-  constexpr int NM = EV0 ? 8 : 10;
-  return (WHICH == 0 ? 8 + 24 : 0) + 4 + 8 * NM + 28;
+  return (SRC == 0 ? 8 + 24 : SRC == 1 ? 4 : 0) + 4 + 8 * NM + 28;
 }
-template <bool EV0, int WHICH>
-constexpr std::array<BwdEntry, bwd_section_len<EV0, WHICH>()> bwd_schedule() {
-  constexpr int NM = EV0 ? 8 : 10;
-  std::array<BwdEntry, bwd_section_len<EV0, WHICH>()> out{};
+template <int NM, int SRC>
+constexpr std::array<BwdEntry, bwd_section_len<NM, SRC>()> bwd_schedule() {
+  std::array<BwdEntry, bwd_section_len<NM, SRC>()> out{};
   int n = 0;
   auto put = [&](int kind, int q, int T, int h, int last) { out[n++] = BwdEntry{kind, q, T, h, last}; };
-  if (WHICH == 0)  // lead-in: head 0's scalars
+  if (SRC == 0)  // lead-in: head 0's scalars
     for (int T = 0; T < 2; ++T)
-      for (int q = 0; q < 4; ++q) put(0, q, T, 0, T == 1 && q == 3);
-  for (int u = 0; u < 4; ++u) put(1, u, 0, 0, 0);  // lead-in: chunk 0's rows
+      for (int q = 0; q < 4; ++q) put(kBwdP, q, T, 0, T == 1 && q == 3);
+  if (SRC == 1) put(kBwdS, 0, 0, 0, 1);
+  for (int u = 0; u < 4; ++u) put(kBwdR, u, 0, 0, 0);  // lead-in: chunk 0's rows
   for (int T = 0; T < 8; ++T) {
-    BwdEntry riders[8] = {};
+    BwdEntry riders[9] = {};
     int nr = 0;
     const int h = T / 2;
-    if (WHICH == 0 && h + 1 < 4)
+    if (SRC == 0 && h + 1 < 4)
       for (int q = 0; q < 4; ++q)
-        riders[nr++] = BwdEntry{0, q, 2 * (h + 1) + (T & 1), h + 1, (T & 1) == 1 && q == 3};
+        riders[nr++] = BwdEntry{kBwdP, q, 2 * (h + 1) + (T & 1), h + 1, (T & 1) == 1 && q == 3};
+    if (SRC == 1 && T + 1 < 8 && ((T + 1) & 1) == 0) riders[nr++] = BwdEntry{kBwdS, 0, T + 1, (T + 1) / 2, 1};
     if (T + 1 < 8)
-      for (int u = 0; u < 4; ++u) riders[nr++] = BwdEntry{1, u, T + 1, (T + 1) / 2, 0};
+      for (int u = 0; u < 4; ++u) riders[nr++] = BwdEntry{kBwdR, u, T + 1, (T + 1) / 2, 0};
     for (int m = 0; m < NM; ++m) {
-      put(2, m, T, h, 0);
+      put(kBwdM, m, T, h, 0);
       if (m < nr) out[n++] = riders[m];
     }
   }
   return out;
 }
-template <bool EV0, int WHICH>
+template <int NM, int SRC>
 constexpr BwdEntry bwd_entry(int s) {
-  return bwd_schedule<EV0, WHICH>()[s];
+  return bwd_schedule<NM, SRC>()[s];
 }
 // Compile-time check of a schedule: every slot filled (one M entry per MFMA
 // tile of each chunk), the four row entries of chunk T before its first M
-// entry, each head's scalars complete (`last`) before the first row entry
-// that uses them.
-template <bool EV0, int WHICH>
+// entry, each head's scalars complete before the first row entry that uses
+// them.
+template <int NM, int SRC>
 constexpr bool bwd_schedule_ok() {
-  constexpr int NM = EV0 ? 8 : 10;
-  const auto sc = bwd_schedule<EV0, WHICH>();
-  int rows_seen[8] = {}, m_seen[8] = {}, head_done = WHICH == 0 ? -1 : 3;
+  const auto sc = bwd_schedule<NM, SRC>();
+  int rows_seen[8] = {}, m_seen[8] = {}, head_done = SRC == 2 ? 3 : -1;
   for (const BwdEntry &e : sc) {
-    if (e.kind == 0 && e.last) head_done = e.h;
-    if (e.kind == 1) {
+    if ((e.kind == kBwdP || e.kind == kBwdS) && e.last) head_done = e.h;
+    if (e.kind == kBwdR) {
       if (e.q == 1 && e.h > head_done) return false;
       if (m_seen[e.T]) return false;
       ++rows_seen[e.T];
     }
-    if (e.kind == 2) {
+    if (e.kind == kBwdM) {
       if (rows_seen[e.T] != 4) return false;
       ++m_seen[e.T];
     }
@@ -807,8 +811,7 @@ constexpr bool bwd_schedule_ok() {
     if (m_seen[T] != NM || rows_seen[T] != 4) return false;
   return true;
 }
-static_assert(bwd_schedule_ok<false, 0>() && bwd_schedule_ok<false, 1>() && bwd_schedule_ok<true, 0>() &&
-                  bwd_schedule_ok<true, 1>(),
+static_assert(bwd_schedule_ok<10, 1>() && bwd_schedule_ok<8, 0>() && bwd_schedule_ok<8, 2>(),
               "reverse-filter operand schedule out of order");
 
 // Reverse of the attention's pair terms, of both filters, of the Bernstein
@@ -827,10 +830,14 @@ static_assert(bwd_schedule_ok<false, 0>() && bwd_schedule_ok<false, 1>() && bwd_
 //   dE/dfc    = sum_h alpha(a<-b)_h ci_h + alpha_ev(a<-b)_h ce_h
 //                     + alpha(b<-a)_h co_h + alpha_ev(b<-a)_h coe_h
 //   dE/dY[m] += fc (alpha_ev(a<-b) gev_a[m] + (-1)^l alpha_ev(b<-a) gev_b[m])
-// (FIRST, the first block of the reverse pass, writes dE/dY without reading
-// it).  The node rows (q, k, v, q_ev, k_ev of both endpoints and their
-// gainv) arrive through the operand stream in the tile-transposed channel
-// order, so a lane's four channels of a tile are one 32-byte vector.
+// For blocks after 0 the node-major reverse (k_attn_bwd_nodes) has formed
+// the head sums, dE/dfc and dE/dY already, and this kernel reads the sums'
+// record; block 0 has no node-major reverse (its inputs do not depend on the
+// positions), so its instantiation (EV0) forms all three here (FIRST, when
+// block 0 is also the first block of the reverse pass, writes dE/dY without
+// reading it).  The node rows (q, k, v, q_ev, k_ev of both endpoints and
+// their gainv) arrive through the operand stream in the tile-transposed
+// channel order, so a lane's four channels of a tile are one 32-byte vector.
 //
 // Per filter the stream holds the first section (bwd_schedule: the head
 // scalars, the df rows and d hidden = W^T df over W1^T and E1^T), then:
@@ -846,7 +853,8 @@ template <bool EV0, bool FIRST>
 __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
     const int *n_active, const int *pa, const double *pr, const double *ps, const double *pfc, const double *pY,
     const double *palpha, const double *__restrict__ qkv, const double *__restrict__ gainv,
-    const double *__restrict__ gaev, double inv_avg, FilterMfma A, double rc, double *ds, double *dr, double *dY) {
+    const double *__restrict__ gaev, const double *__restrict__ psc, const double *__restrict__ pdfc, double inv_avg,
+    FilterMfma A, double rc, double *ds, double *dr, double *dY) {
   SO3LR_EXP2_TABLE(A)
   const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
@@ -865,7 +873,11 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
   const double *gaa = gainv + std::size_t(a) * kF + 4 * g, *gab = gainv + std::size_t(b) * kF + 4 * g;
   auto row = [](const double *r, int off) { return *reinterpret_cast<const v4d *>(r + off); };
 
-  constexpr int A_END0 = bwd_section_len<EV0, 0>(), A_END1 = bwd_section_len<EV0, 1>();
+  // head scalars: block 0 forms them here (SRC 0 and 2), later blocks read
+  // the node-major reverse's record (SRC 1)
+  constexpr int NM = EV0 ? 8 : 10, SRC0 = EV0 ? 0 : 1, SRC1 = EV0 ? 2 : 1;
+  constexpr int A_END0 = bwd_section_len<NM, SRC0>(), A_END1 = bwd_section_len<NM, SRC1>();
+  const double *rec = psc + 16 * std::size_t(pp);
   constexpr int B_LEN = 24, C_LEN = EV0 ? 0 : 3, D_LEN = 16, E_LEN = EV0 ? 0 : 2;
   constexpr int TAIL = B_LEN + C_LEN + D_LEN + E_LEN;
   constexpr int NB0 = A_END0 + TAIL, NB1 = A_END1 + TAIL;
@@ -874,13 +886,15 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
     constexpr int A_END = which ? A_END1 : A_END0;
     constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;
     if constexpr (s < A_END) {
-      constexpr BwdEntry e = bwd_entry<EV0, which>(s);
-      if constexpr (e.kind == 0) {
+      constexpr BwdEntry e = bwd_entry<NM, which ? SRC1 : SRC0>(s);
+      if constexpr (e.kind == kBwdS) {
+        return *reinterpret_cast<const v4d *>(rec + 4 * e.h);
+      } else if constexpr (e.kind == kBwdP) {
         if constexpr (e.q == 0) return row(gaa, 16 * e.T);
         else if constexpr (e.q == 1) return row(rb, 256 + 16 * e.T);
         else if constexpr (e.q == 2) return row(gab, 16 * e.T);
         else return row(ra, 256 + 16 * e.T);
-      } else if constexpr (e.kind == 1) {
+      } else if constexpr (e.kind == kBwdR) {
         if constexpr (e.q == 0) return row(ra, qoff + 16 * e.T);
         else if constexpr (e.q == 1) return row(rb, koff + 16 * e.T);
         else if constexpr (e.q == 2) return row(rb, qoff + 16 * e.T);
@@ -914,7 +928,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
   // off(g) .. off(g) + 2g + 2, contiguous in the natural ev order): its
   // <gev_a, Y>, <gev_b, Y> and its share of dE/dY.
   double ce_mine = 0.0, coe_mine = 0.0;
-  {
+  if constexpr (EV0) {
     const int lo = ev_offset(g), n_m = 2 * g + 3;
     const double par = slot_parity(g);
     const double ain_e = al[4 + g], aout_e = al[12 + g];
@@ -933,9 +947,12 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
   }
   // dE/dfc: the equivariant terms of this lane group's slot now, the
   // invariant ones head by head below (every lane ends with the whole sum)
-  double dfc = al[4 + g] * ce_mine + al[12 + g] * coe_mine;
-  dfc += __shfl_xor(dfc, 16, kWave);
-  dfc += __shfl_xor(dfc, 32, kWave);
+  double dfc = 0.0;
+  if constexpr (EV0) {
+    dfc = al[4 + g] * ce_mine + al[12 + g] * coe_mine;
+    dfc += __shfl_xor(dfc, 16, kWave);
+    dfc += __shfl_xor(dfc, 32, kWave);
+  }
   // The running sums (dfc, part, ds_acc) are needed only at the end; an empty
   // asm on each update keeps the compiler from sinking the updates to that
   // use, which would hold every head's terms in registers until then.
@@ -966,8 +983,12 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
       dh2[1] = zero;
     }
     if constexpr (s < A_END) {
-      constexpr BwdEntry e = bwd_entry<EV0, which>(s);
-      if constexpr (e.kind == 0) {
+      constexpr BwdEntry e = bwd_entry<NM, which ? SRC1 : SRC0>(s);
+      if constexpr (e.kind == kBwdS) {
+        // fc/avg-scaled head scalars of this pair: {in, out, in_ev, out_ev}
+        s_in = which ? w[2] : w[0];
+        s_out = which ? w[3] : w[1];
+      } else if constexpr (e.kind == kBwdP) {
         // <gainv_a, v_b> and <gainv_b, v_a> over the lane's channels of head e.h
         if constexpr (e.q == 0 || e.q == 2) {
           hold = w;
@@ -989,9 +1010,9 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
           ci = 0.0;
           co = 0.0;
         }
-      } else if constexpr (e.kind == 1) {
+      } else if constexpr (e.kind == kBwdR) {
         // the df of chunk e.T, built while the previous chunk's MFMAs run
-        if constexpr (which == 1 && e.q == 0 && (e.T & 1) == 0) {
+        if constexpr (EV0 && which == 1 && e.q == 0 && (e.T & 1) == 0) {
           // the slot-h sums live in lane group h
           s_in = fcs * __shfl(ce_mine, j + 16 * e.h, kWave);
           s_out = fcs * __shfl(coe_mine, j + 16 * e.h, kWave);
@@ -1077,6 +1098,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
   if (valid) {
     if constexpr (!EV0) ds[4 * std::size_t(p) + g] = ds_acc;
     if (g == 0) {
+      if constexpr (!EV0) dfc = pdfc[pp];
       double grad = part;
       if (r < rc) {
         const double t = r / rc;
@@ -2180,13 +2202,17 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
 }
 
 
-// Attention reverse, node adjoints only (kokkos_attention_scatter_reverse.cpp:
+// Attention reverse, node-major (kokkos_attention_scatter_reverse.cpp:
 // 280-500): for node n and each active pair p = {n, o}, the incoming edge
 // o -> n gives dq_n, dq_ev_n and the outgoing edge n -> o gives dk_n,
-// dk_ev_n, dv_n (sender-side terms gathered, not scattered).  The pair
-// adjoints (df, dE/dfc, dE/dY) are formed by the reverse filter kernel, so
-// nothing is written per pair.  Lane layout as in k_attn_fwd; gainv in the
-// tile-transposed order.
+// dk_ev_n, dv_n (sender-side terms gathered, not scattered).  The endpoint
+// with side 0 also writes the pair's terms for the reverse filter, which
+// forms df from them and the node rows: per head h the record
+//   {fc/avg ci_h, fc/avg co_h, fc/avg ce_h, fc/avg coe_h}
+// (32 bytes, psc + 16 p + 4 h), dE/dfc and dE/dY (FIRST, the first block of
+// the reverse pass, writes dE/dY without reading it).  Lane layout as in
+// k_attn_fwd; gainv in the tile-transposed order.
+template <bool FIRST>
 __global__ __launch_bounds__(256) void k_attn_bwd_nodes(int N, const int *inc_off, const int *__restrict__ iact,
                                                         const int *__restrict__ iother, const double *__restrict__ qkv,
                                                         const double *__restrict__ pf, const double *__restrict__ pY,
@@ -2194,7 +2220,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_nodes(int N, const int *inc_of
                                                         const double *__restrict__ palpha,
                                                         const double *__restrict__ gainv,
                                                         const double *__restrict__ gaev, double inv_avg,
-                                                        double *__restrict__ gqkv) {
+                                                        double *__restrict__ gqkv, double *__restrict__ psc,
+                                                        double *__restrict__ pdfc, double *__restrict__ dY) {
   const int lane = threadIdx.x & 63;
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -2220,7 +2247,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_nodes(int N, const int *inc_of
     const v2d fev = __builtin_nontemporal_load(reinterpret_cast<const v2d *>(fp + 128 + p0));
     const double fc = pfc[p];
     const double y_ld = pY[kE * std::size_t(p) + m];
-    const double aout_i = palpha[16 * std::size_t(p) + 8 * (1 - side) + h];
+    const double *al = palpha + 16 * std::size_t(p);
+    const double aout_i = al[8 * (1 - side) + h];
     const double oge = evv ? oge_ld : 0.0;
     const double y = evv ? y_ld : 0.0;
     const double y_n = side == 0 ? y : par * y;  // harmonics of edge o -> n
@@ -2236,6 +2264,19 @@ __global__ __launch_bounds__(256) void k_attn_bwd_nodes(int N, const int *inc_of
     dk0 += sout * oqv.x * fiv.x; dk1 += sout * oqv.y * fiv.y;
     dke0 += soute * oqev.x * fev.x; dke1 += soute * oqev.y * fev.y;
     dv0 += fc * aout_i * ogv.x; dv1 += fc * aout_i * ogv.y;
+    // the pair's terms, once per pair (its side-0 endpoint; side is uniform
+    // across the wavefront): every head's sums appear in that head's 16 lanes
+    if (side == 0) {
+      const double ain_i = al[h], ain_e = al[4 + h], aout_e = al[12 + h];
+      const double part = ain_i * ci + ain_e * ce + aout_i * co + aout_e * coe;
+      const double fcg = lane_read(part, 0) + lane_read(part, 16) + lane_read(part, 32) + lane_read(part, 48);
+      if (t == 0) *reinterpret_cast<v4d *>(psc + 16 * std::size_t(p) + 4 * h) = v4d{sin_, sout, sine, soute};
+      if (lane == 0) pdfc[p] = fcg;
+      if (evv) {
+        double *dy = dY + kE * std::size_t(p) + m;
+        *dy = (FIRST ? 0.0 : *dy) + fc * (ain_e * mge + par * aout_e * oge);
+      }
+    }
   };
   for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
     visit(e1, o1);
@@ -2740,7 +2781,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   sr_inc_off_ = buf("sr_inc_off"); sr_inc_ = buf("sr_inc"); lr_rows_ = buf("lr_rows");
   lr_nodes_ = buf("lr_nodes"); lr_inc_off_ = buf("lr_inc_off"); lr_inc_ = buf("lr_inc");
   blk_count_ = buf("blk"); n_active_ = buf("nact"); cand2act_ = buf("c2a"); pa_ = buf("pa");
-  pv_ = buf("pv"); pr_ = buf("pr"); pY_ = buf("pY"); pfc_ = buf("pfc"); pzbl_ = buf("pzbl");
+  psc_ = buf("psc"); pv_ = buf("pv"); pr_ = buf("pr"); pY_ = buf("pY"); pfc_ = buf("pfc"); pzbl_ = buf("pzbl");
   ps_ = buf("ps"); pf_ = buf("pf"); palpha_ = buf("palpha"); df_ = buf("df"); dfc_ = buf("dfc");
   ds_ = buf("ds"); dr_ = buf("dr"); dY_ = buf("dY"); pg_ = buf("pg"); xrows_ = buf("xrows");
   fhost_ = buf("fhost"); vatom_ = buf("vatom");
@@ -2924,6 +2965,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   double *palpha = nullptr;
   double *df = nullptr;
   double *dfc = nullptr;
+  double *psc = nullptr;
   double *ds = nullptr;
   double *dr = nullptr;
   double *dY = nullptr;
@@ -2979,9 +3021,11 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     ps = take<double>(ps_, L * 4 * Pz);
     pf = take<double>(pf_, L * 256 * Pz);
     palpha = take<double>(palpha_, L * 16 * Pz);
-    // the pair adjoints of the filters stay in registers on the MFMA path
+    // the pair adjoints of the filters stay in registers on the MFMA path;
+    // it passes the head scalars (16 per pair) and dE/dfc between its kernels
     df = naive_filters_ ? take<double>(df_, 256 * Pz) : nullptr;
-    dfc = naive_filters_ ? take<double>(dfc_, Pz) : nullptr;
+    dfc = take<double>(dfc_, Pz);
+    psc = naive_filters_ ? nullptr : take<double>(psc_, 16 * Pz);
     ds = take<double>(ds_, 4 * Pz);
     dr = take<double>(dr_, Pz);
     dY = take<double>(dY_, kE * Pz);
@@ -3210,21 +3254,24 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       // node adjoints (dq, dk, dv; not needed in block 0, whose inputs do not
       // depend on the positions), then the pair adjoints and the filter
       // reverse in one pair-major kernel
+      const bool first = b == L - 1;
       if (b > 0)
         timed("attn_bwd", 1, [&] {
-          hipLaunchKernelGGL(k_attn_bwd_nodes, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb, pfb, pY,
-                             pfc, pab, gainv, gaev, inv_avg, gqkv);
+          if (first)
+            hipLaunchKernelGGL(k_attn_bwd_nodes<true>, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb,
+                               pfb, pY, pfc, pab, gainv, gaev, inv_avg, gqkv, psc, dfc, dY);
+          else
+            hipLaunchKernelGGL(k_attn_bwd_nodes<false>, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, qb,
+                               pfb, pY, pfc, pab, gainv, gaev, inv_avg, gqkv, psc, dfc, dY);
         });
       const FilterMfma FM = filter_mfma(B, hw_, gamma_);
       timed(b == 0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
 #define SO3LR_FILTER_BWD(E0, FIRST)                                                                                \
   hipLaunchKernelGGL((k_filter_bwd_mfma<E0, FIRST>), dim3(gP64), dim3(256), 0, s, nact, pa, pr, psb, pfc, pY, pab,  \
-                     qb, gainv, gaev, inv_avg, FM, rc_, ds, dr, dY)
-        const bool first = b == L - 1;
+                     qb, gainv, gaev, psc, dfc, inv_avg, FM, rc_, ds, dr, dY)
         if (b == 0 && first) SO3LR_FILTER_BWD(true, true);
         else if (b == 0) SO3LR_FILTER_BWD(true, false);
-        else if (first) SO3LR_FILTER_BWD(false, true);
-        else SO3LR_FILTER_BWD(false, false);
+        else SO3LR_FILTER_BWD(false, false);  // dE/dY of blocks after 0: the node-major reverse
 #undef SO3LR_FILTER_BWD
       });
     }

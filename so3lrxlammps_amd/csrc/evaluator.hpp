@@ -212,7 +212,7 @@ class Evaluator {
   Buffer *owner_, *sr_rows_, *sr_nodes_, *sr_inc_off_, *sr_inc_, *lr_rows_, *lr_nodes_,
       *lr_inc_off_, *lr_inc_, *blk_count_, *n_active_, *cand2act_;
   Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
-  Buffer *df_, *dfc_, *ds_, *dr_, *dY_, *pg_;
+  Buffer *df_, *dfc_, *psc_, *ds_, *dr_, *dY_, *pg_;
   Buffer *iact_, *iother_;  // per step: incidence entry -> active pair * 2 + side, partner node
   Buffer *xrows_, *fhost_, *vatom_;
   // device reneighbor
