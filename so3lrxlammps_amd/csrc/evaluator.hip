@@ -160,8 +160,9 @@ __global__ __launch_bounds__(256) void k_sr_count(int P, Pos pos, double rc2, in
   if (threadIdx.x == 0) blk_count[blockIdx.x] = part[0];
 }
 
-// exclusive scan of per-block counts in place; total to *n_active
-__global__ __launch_bounds__(1024) void k_scan_counts(int nblk, int *cnt, int *n_active) {
+// exclusive scan of per-block counts in place; the total to *n_total and,
+// clamped to the capacity of the active-pair buffers, to *n_active
+__global__ __launch_bounds__(1024) void k_scan_counts(int nblk, int *cnt, int *n_active, int cap, int *n_total) {
   __shared__ int buf[1024];
   __shared__ int carry;
   if (threadIdx.x == 0) carry = 0;
@@ -182,12 +183,15 @@ __global__ __launch_bounds__(1024) void k_scan_counts(int nblk, int *cnt, int *n
     if (threadIdx.x == 1023) carry += buf[1023];
     __syncthreads();
   }
-  if (threadIdx.x == 0) *n_active = carry;
+  if (threadIdx.x == 0) {
+    *n_active = carry < cap ? carry : cap;
+    if (n_total) *n_total = carry;
+  }
 }
 
 template <class Pos>
 __global__ __launch_bounds__(256) void k_sr_compact(
-    int P, Pos pos, const int *nodes, double rc2, const int *blk_off,
+    int P, Pos pos, const int *nodes, double rc2, const int *blk_off, int cap,
     const int *z, ZblParams zp, int *cand2act, int *pa, double *pv, double *pr, double *pY,
     double *pfc, double *pzbl) {
   __shared__ int part[256];
@@ -215,6 +219,10 @@ __global__ __launch_bounds__(256) void k_sr_compact(
     double dx, dy, dz;
     sr_active(pos, c, rc2, dx, dy, dz);
     const int p = at++;
+    if (p >= cap) {  // beyond the active-pair buffers: the host grows them and evaluates again
+      cand2act[c] = -1;
+      continue;
+    }
     cand2act[c] = p;
     const int na = nodes[2 * c], nb = nodes[2 * c + 1];
     pa[2 * p] = na;
@@ -659,7 +667,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
     if (valid) ps[4 * std::size_t(p) + g] = sg;
   }
   // tile mt of filter `which`: its four values per lane are adjacent (fpos)
-  v4d *const rowv = reinterpret_cast<v4d *>(pf + 256 * std::size_t(p) + 4 * g);
+  v4d *const rowv = EV0 ? nullptr : reinterpret_cast<v4d *>(pf + 256 * std::size_t(p) + 4 * g);
   v4d h[8], h2[2], e0, o, qv;
   double t0 = 0.0, t1 = 0.0;  // per-head partial logits: a <- b (side 0), b <- a (side 1)
 
@@ -698,9 +706,8 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
             for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab(h2[t][r], exp2_lds);
           }
         }
-        if constexpr (EV0 && u == 8) {
-          if (valid) __builtin_nontemporal_store(o, rowv + which * 32 + 4 * mt);
-        }
+        // (block 0, EV0: the rows are not stored; its reverse has no node-major
+        // attention kernel to read them, and the messages use alpha)
       } else if constexpr (u < RU) {
         o = mfma4(w, h2[u - 9], o);
         if constexpr (u == RU - 1) {
@@ -2101,8 +2108,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd(int N, const int *inc_off, con
   // the lane's two channels sit next to each other in the tile-transposed
   // rows (filters, q k v): positions 32 h + 2 t and + 1, read as one 16-byte
   // vector; fpos is its own inverse, so the channels are fpos(position)
-  const int p0 = 32 * h + 2 * t, p1 = p0 + 1;
-  const int c0 = fpos(p0), c1 = fpos(p1);  // c1 = c0 + 4
+  const int p0 = 32 * h + 2 * t;
   const bool evv = t < 2 * h + 3;
   const int m = evv ? ev_offset(h) + t : 0;
   const double par = slot_parity(h);
@@ -2789,7 +2795,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   nb_cstart_ = buf("nb_cstart"); nb_tmp_ = buf("nb_tmp"); nb_srcnt_ = buf("nb_srcnt"); nb_lrcnt_ = buf("nb_lrcnt");
   nb_err_ = buf("nb_err"); nb_srlist_ = buf("nb_srlist"); nb_poff_ = buf("nb_poff"); sr_code_ = buf("sr_code");
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
-  iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part");
+  iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part"); probe_ = buf("probe");
   top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
   top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp");
   for (int w = 0; w < 2; ++w) {
@@ -2906,15 +2912,41 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const std::int64_t N = n_, P = p_sr_, L = layers_;
   const std::size_t Nz = std::size_t(N), Pz = std::size_t(std::max<std::int64_t>(P, 1));
   hipStream_t s = stream_;
+  const double rc2 = rc_ * rc_;
+  const int nblk = std::max(1, ceil_div(P, kCompactPerBlock));
   // --- node-order inputs (spatial order of the device reneighbor path) ---
   const int *perm = permuted_ ? static_cast<const int *>(perm_->p) : nullptr;
   const int *z = static_cast<const int *>((permuted_ ? nz_ : z_)->p);
   const double *x0 = static_cast<const double *>((permuted_ ? nx0_ : x0_)->p);
   const double *x_in = x;
   if (permuted_) x = static_cast<const double *>(xn_->p);
+  // --- capacity of the active-pair buffers: the pairs inside the cutoff
+  // (about 60% of the candidates with a 1 A skin), counted once per topology
+  // and given 1/8 of margin; an evaluation that finds more grows it and runs
+  // again (see the end of this function) ---
+  if (act_cap_ == 0 && P > 0) {
+    int *cnt = from_scratch ? reinterpret_cast<int *>(scratch_dev_) : ensure<int>(probe_, std::size_t(nblk) + 2);
+    if (permuted_)
+      hipLaunchKernelGGL(k_gather_pos, dim3(unsigned((3 * Nz + 255) / 256)), dim3(256), 0, s, int(N), perm, x_in,
+                         const_cast<double *>(x));
+    if (shift_mode_) {
+      const ShiftPos pos{x, static_cast<const int *>(sr_nodes_->p), static_cast<const int *>(sr_code_->p),
+                         box_len_[0], box_len_[1], box_len_[2]};
+      hipLaunchKernelGGL(k_sr_count<ShiftPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, rc2, cnt);
+    } else {
+      const RowsPos pos{x, static_cast<const int *>(sr_rows_->p)};
+      hipLaunchKernelGGL(k_sr_count<RowsPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, rc2, cnt);
+    }
+    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, cnt, cnt + nblk, 0x7fffffff, cnt + nblk + 1);
+    int total = 0;
+    HIP_CHECK(hipMemcpyAsync(&total, cnt + nblk + 1, sizeof(int), hipMemcpyDeviceToHost, s));
+    HIP_CHECK(hipStreamSynchronize(s));
+    act_cap_ = std::min<std::int64_t>(P, std::int64_t(total) + total / 8 + 256);
+  }
+  const std::int64_t PA = std::max<std::int64_t>(std::min(act_cap_, P), 1);
+  const std::size_t Pa = std::size_t(PA);
   // --- buffers (retained capacity; all allocation happens before any work
   // is enqueued, so the sequence below can be captured into a graph) ---
-  const int nblk = std::max(1, ceil_div(P, kCompactPerBlock));
   double *xs = nullptr;
   double *evs = nullptr;
   double *qkv = nullptr;
@@ -3010,26 +3042,30 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     etot = eatom_out ? eatom_out : take<double>(etot_, Nz);
     red = take<double>(red_, 16);
     blk = take<int>(blk_count_, nblk);
-    nact = take<int>(n_active_, 1);
+    nact = take<int>(n_active_, 2);  // [0] active pairs kept, [1] active pairs found
     c2a = take<int>(cand2act_, Pz);
-    pa = take<int>(pa_, 2 * Pz);
-    pv = take<double>(pv_, 3 * Pz);
-    pr = take<double>(pr_, Pz);
-    pY = take<double>(pY_, kE * Pz);
-    pfc = take<double>(pfc_, Pz);
-    pzbl = take<double>(pzbl_, 2 * Pz);
-    ps = take<double>(ps_, L * 4 * Pz);
-    pf = take<double>(pf_, L * 256 * Pz);
-    palpha = take<double>(palpha_, L * 16 * Pz);
+    // per active pair (the candidate-indexed map c2a and the incidence stay
+    // sized by candidates)
+    pa = take<int>(pa_, 2 * Pa);
+    pv = take<double>(pv_, 3 * Pa);
+    pr = take<double>(pr_, Pa);
+    pY = take<double>(pY_, kE * Pa);
+    pfc = take<double>(pfc_, Pa);
+    pzbl = take<double>(pzbl_, 2 * Pa);
+    ps = take<double>(ps_, L * 4 * Pa);
+    // filter rows of every block for the scalar cross-check path; of blocks
+    // after 0 only on the MFMA path (block 0's are never read there)
+    pf = take<double>(pf_, std::size_t(naive_filters_ ? L : L - 1) * 256 * Pa);
+    palpha = take<double>(palpha_, L * 16 * Pa);
     // the pair adjoints of the filters stay in registers on the MFMA path;
     // it passes the head scalars (16 per pair) and dE/dfc between its kernels
-    df = naive_filters_ ? take<double>(df_, 256 * Pz) : nullptr;
-    dfc = take<double>(dfc_, Pz);
-    psc = naive_filters_ ? nullptr : take<double>(psc_, 16 * Pz);
-    ds = take<double>(ds_, 4 * Pz);
-    dr = take<double>(dr_, Pz);
-    dY = take<double>(dY_, kE * Pz);
-    pg = take<double>(pg_, 3 * Pz);
+    df = naive_filters_ ? take<double>(df_, 256 * Pa) : nullptr;
+    dfc = take<double>(dfc_, Pa);
+    psc = naive_filters_ ? nullptr : take<double>(psc_, 16 * Pa);
+    ds = take<double>(ds_, 4 * Pa);
+    dr = take<double>(dr_, Pa);
+    dY = take<double>(dY_, kE * Pa);
+    pg = take<double>(pg_, 3 * Pa);
     iact = take<int>(iact_, 2 * Pz);
     iother = take<int>(iother_, 2 * Pz);
     partial = take<double>(red_part_, 9 * kReduceBlocks);
@@ -3107,32 +3143,32 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     hipLaunchKernelGGL(k_gather_pos, dim3(unsigned((3 * Nz + 255) / 256)), dim3(256), 0, s, int(N), perm, x_in,
                        const_cast<double *>(x));
   // --- active short-range pairs, geometry, ZBL ---
-  const double rc2 = rc_ * rc_;
+  const int cap = int(PA);
   if (P > 0 && !shift_mode_) {
     const RowsPos pos{x, sr_rows};
     hipLaunchKernelGGL(k_sr_count<RowsPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, rc2, blk);
-    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, blk, nact);
-    hipLaunchKernelGGL(k_sr_compact<RowsPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, sr_nodes, rc2, blk, z,
+    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, blk, nact, cap, nact + 1);
+    hipLaunchKernelGGL(k_sr_compact<RowsPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, sr_nodes, rc2, blk, cap, z,
                        zbl_, c2a, pa, pv, pr, pY, pfc, pzbl);
   } else if (P > 0) {
     const ShiftPos pos{x, sr_nodes, static_cast<const int *>(sr_code_->p), box_len_[0], box_len_[1], box_len_[2]};
     hipLaunchKernelGGL(k_sr_count<ShiftPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, rc2, blk);
-    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, blk, nact);
-    hipLaunchKernelGGL(k_sr_compact<ShiftPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, sr_nodes, rc2, blk, z,
+    hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, s, nblk, blk, nact, cap, nact + 1);
+    hipLaunchKernelGGL(k_sr_compact<ShiftPos>, dim3(nblk), dim3(256), 0, s, int(P), pos, sr_nodes, rc2, blk, cap, z,
                        zbl_, c2a, pa, pv, pr, pY, pfc, pzbl);
   } else {
-    hipLaunchKernelGGL(k_fill_int, dim3(1), dim3(64), 0, s, nact, 1, 0);  // no memset nodes in graphs
+    hipLaunchKernelGGL(k_fill_int, dim3(1), dim3(64), 0, s, nact, 2, 0);  // no memset nodes in graphs
   }
   // active incidence of this step (2 entries per candidate pair)
   if (P > 0)
     hipLaunchKernelGGL(k_inc_active, dim3(unsigned((2 * Pz + 255) / 256)), dim3(256), 0, s, int(2 * P), sr_inc, c2a,
                        pa, iact, iother);
-  fill(dr, Pz);
+  fill(dr, Pa);
   HIP_CHECK(hipMemcpyAsync(xs, x0, Nz * kF * sizeof(double), hipMemcpyDeviceToDevice, s));
   fill(evs, Nz * kE);
   const double inv_avg = 1.0 / avg_;
-  const unsigned gP = unsigned(std::max<std::int64_t>(P, 1));
-  const unsigned gP64 = unsigned(std::max(1, ceil_div(P, 64)));  // 64 pairs per MFMA block
+  const unsigned gP = unsigned(PA);
+  const unsigned gP64 = unsigned(std::max(1, ceil_div(PA, 64)));  // 64 pairs per MFMA block
 
   // --- interaction blocks, forward ---
   for (int b = 0; b < L; ++b) {
@@ -3142,7 +3178,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     double *n1b = n1 + b * Nz * kF, *n1hb = n1hat + b * Nz * kF, *n1ib = n1is + b * Nz;
     double *hpb = hpre + b * Nz * kF, *tb = tout + b * Nz * kNI;
     double *p2h = pre2hat + b * Nz * kF, *p2i = pre2is + b * Nz;
-    double *psb = ps + b * 4 * Pz, *pfb = pf + b * 256 * Pz, *pab = palpha + b * 16 * Pz;
+    double *psb = ps + b * 4 * Pa, *pab = palpha + b * 16 * Pa;
+    double *pfb = naive_filters_ ? pf + b * 256 * Pa : (b > 0 ? pf + (b - 1) * 256 * Pa : nullptr);
     FilterArgs A;
     for (int k = 0; k < 2; ++k) {
       A.fw0[k] = B.fw0[k]; A.fb0[k] = B.fb0[k]; A.fw1t[k] = B.fw1t[k]; A.fb1[k] = B.fb1[k];
@@ -3222,7 +3259,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     double *n1b = n1 + b * Nz * kF, *n1hb = n1hat + b * Nz * kF, *n1ib = n1is + b * Nz;
     double *hpb = hpre + b * Nz * kF, *tb = tout + b * Nz * kNI;
     double *p2h = pre2hat + b * Nz * kF, *p2i = pre2is + b * Nz;
-    double *psb = ps + b * 4 * Pz, *pfb = pf + b * 256 * Pz, *pab = palpha + b * 16 * Pz;
+    double *psb = ps + b * 4 * Pa, *pab = palpha + b * 16 * Pa;
+    double *pfb = naive_filters_ ? pf + b * 256 * Pa : (b > 0 ? pf + (b - 1) * 256 * Pa : nullptr);
     FilterArgs A;
     for (int k = 0; k < 2; ++k) {
       A.fw0[k] = B.fw0[k]; A.fb0[k] = B.fb0[k]; A.fw1t[k] = B.fw1t[k]; A.fb1[k] = B.fb1[k];
@@ -3285,14 +3323,14 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   }
 
   // --- geometry reverse, forces, energies, virial ---
-  hipLaunchKernelGGL(k_geom_bwd, dim3(ceil_div(std::max<std::int64_t>(P, 1), 256)), dim3(256), 0, s, nact, pv, pr,
+  hipLaunchKernelGGL(k_geom_bwd, dim3(ceil_div(PA, 256)), dim3(256), 0, s, nact, pv, pr,
                      dr, pzbl, dY, pg);
   hipLaunchKernelGGL(k_forces, dim3(gN4), dim3(256), 0, s, int(N), sr_off, sr_inc, c2a, pg, pzbl, flr, eatom, elr,
                      perm, fo, ezbl, etot);
   hipLaunchKernelGGL(k_reduce_part, dim3(kReduceBlocks), dim3(256), 0, s, int(N), nact, etot, pv, pg, vlr, parts,
                      partial);
   hipLaunchKernelGGL(k_reduce_final, dim3(1), dim3(256), 0, s, kReduceBlocks, partial, red);
-  hipLaunchKernelGGL(k_copy_count, dim3(1), dim3(64), 0, s, nact, red + 9);
+  hipLaunchKernelGGL(k_copy_count, dim3(1), dim3(64), 0, s, nact + 1, red + 9);  // the pairs found
   HIP_CHECK(hipGetLastError());
   HIP_CHECK(hipMemcpyAsync(host_out_, red, 10 * sizeof(double), hipMemcpyDeviceToHost, s));
   };  // enqueue
@@ -3328,6 +3366,17 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const double *host_red = host_out_;
   const std::int64_t host_nact = std::int64_t(host_out_[9]);
   last_active_ = host_nact;
+  if (host_nact > PA) {
+    // more active pairs than the buffers hold (atoms moved closer since the
+    // count): nothing beyond the capacity was written; grow and evaluate again
+    for (Pending &pd : pending) {
+      (void)hipEventDestroy(pd.a);
+      (void)hipEventDestroy(pd.b);
+    }
+    act_cap_ = std::min<std::int64_t>(P, host_nact + host_nact / 8 + 256);
+    compute_impl(x_in, flags, f_out, eatom_out, energy, virial, from_scratch);
+    return;
+  }
   for (Pending &pd : pending) {
     float ms = 0.f;
     HIP_CHECK(hipEventElapsedTime(&ms, pd.a, pd.b));
@@ -3353,13 +3402,14 @@ void Evaluator::last_vatom(double *out, bool on_device) {
   if (last_from_scratch_)
     throw std::logic_error("SO3LR: so3lr_compute_device_noalloc keeps no per-atom virial; use so3lr_compute_device");
   const std::int64_t N = n_;
-  const std::size_t Nz = std::size_t(N), Pz = std::size_t(std::max<std::int64_t>(p_sr_, 1));
+  const std::size_t Nz = std::size_t(N);
   double *dst = on_device ? out : ensure<double>(vatom_, Nz * 6);
   const int *perm = permuted_ ? static_cast<const int *>(perm_->p) : nullptr;
+  // the evaluation's own buffers, as it left them
   hipLaunchKernelGGL(k_vatom, dim3(ceil_div(N, 4)), dim3(256), 0, stream_, int(N),
                      static_cast<const int *>(sr_inc_off_->p), static_cast<const int *>(sr_inc_->p),
-                     ensure<int>(cand2act_, Pz), ensure<double>(pv_, 3 * Pz), ensure<double>(pg_, 3 * Pz),
-                     ensure<double>(vlr_, Nz * 6), perm, dst);
+                     static_cast<const int *>(cand2act_->p), static_cast<const double *>(pv_->p),
+                     static_cast<const double *>(pg_->p), static_cast<const double *>(vlr_->p), perm, dst);
   HIP_CHECK(hipGetLastError());
   if (!on_device) HIP_CHECK(hipMemcpyAsync(out, dst, Nz * 6 * sizeof(double), hipMemcpyDeviceToHost, stream_));
   HIP_CHECK(hipStreamSynchronize(stream_));

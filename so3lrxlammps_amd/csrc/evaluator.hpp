@@ -214,6 +214,10 @@ class Evaluator {
   Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
   Buffer *df_, *dfc_, *psc_, *ds_, *dr_, *dY_, *pg_;
   Buffer *iact_, *iother_;  // per step: incidence entry -> active pair * 2 + side, partner node
+  Buffer *probe_;           // the active-pair count of a new topology
+  // capacity (pairs) of the active-pair buffers for the current topology; 0
+  // until the first evaluation on it counts the active pairs
+  std::int64_t act_cap_ = 0;
   Buffer *xrows_, *fhost_, *vatom_;
   // device reneighbor
   Buffer *nb_key_, *nb_idx_, *nb_skey_, *nb_sidx_, *nb_cstart_, *nb_tmp_, *nb_srcnt_, *nb_lrcnt_, *nb_err_,

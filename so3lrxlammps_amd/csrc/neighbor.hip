@@ -372,6 +372,7 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   topology_ready_ = true;
   ++topo_version_;
   evaluated_ = false;
+  act_cap_ = 0;  // counted again by the next evaluation
 }
 
 }  // namespace so3lr_amd

@@ -312,6 +312,7 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
   topology_ready_ = true;
   ++topo_version_;
   evaluated_ = false;
+  act_cap_ = 0;  // counted again by the next evaluation
 }
 
 }  // namespace so3lr_amd

@@ -389,3 +389,30 @@ def test_topology_faults_are_refused():
     assert e1 == e2 and np.array_equal(f1, f2) and np.array_equal(w1, w2)
     c.close()
     c2.close()
+
+
+def test_active_pair_capacity_overflow_reevaluates():
+    """The per-pair buffers hold the active pairs counted at the first
+    evaluation of a topology plus 1/8; a geometry with more pairs inside the
+    cutoff (here the positions compressed by 6 %) makes the evaluation grow
+    them and run again.  Its result must be bit-identical to a context that
+    counted at that geometry in the first place."""
+    from so3lrxlammps_amd import Context, Lists
+    ref, z, pos, box = support.load_golden("water3000")
+    lists = Lists(pos, np.zeros(3), box, (1, 1, 1))
+    rows0 = lists.rows_positions(pos)
+    rows1 = np.ascontiguousarray(rows0 * 0.94)
+    a = Context(support.MODEL, 0)
+    a.set_system(z, 0, 1)
+    a.set_topology(lists)
+    a.compute(rows0)
+    n0 = a.graph_stats()[0]
+    e1, f1, ea1, w1 = a.compute(rows1)
+    assert a.graph_stats()[0] > n0 + n0 // 8 + 256  # the compressed geometry overflowed the capacity
+    b = Context(support.MODEL, 0)
+    b.set_system(z, 0, 1)
+    b.set_topology(lists)
+    e2, f2, ea2, w2 = b.compute(rows1)
+    assert e1 == e2 and np.array_equal(f1, f2) and np.array_equal(ea1, ea2) and np.array_equal(w1, w2)
+    a.close()
+    b.close()
