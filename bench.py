@@ -63,8 +63,8 @@ KERNEL_WORK = {
     # name: (kernel symbol, bound, algorithmic per unit, issued per unit, unit)
     "filter_fwd": ("k_filter_fwd_mfma<false>", "mfma", _FILTER, _FILTER, "pair"),
     "filter_fwd_block0": ("k_filter_fwd_mfma<true>", "mfma", _FILTER_B0, _FILTER_B0, "pair"),
-    "filter_bwd": ("k_filter_bwd_mfma<false>", "mfma", _FILTER, _FILTER_BWD_ISSUED, "pair"),
-    "filter_bwd_block0": ("k_filter_bwd_mfma<true>", "mfma", _FILTER_B0, _FILTER_BWD_B0_ISSUED, "pair"),
+    "filter_bwd": ("k_filter_bwd_mfma<false, false>", "mfma", _FILTER, _FILTER_BWD_ISSUED, "pair"),
+    "filter_bwd_block0": ("k_filter_bwd_mfma<true, false>", "mfma", _FILTER_B0, _FILTER_BWD_B0_ISSUED, "pair"),
 }
 
 
