@@ -15,7 +15,9 @@ from . import model_io
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
 
-F, NH, HW, E, R, L = 128, 4, 32, 24, 32, 3
+F, NH, HW, E, R, MAXL = 128, 4, 32, 24, 32, 8
+NORM_LAYER, NORM_RMS, NORM_NONE = 0, 1, 2
+REP_ZBL, REP_NLH = 0, 1
 
 GLOBAL_KEYS = [
     "model.inv_feature_embedding.embedding.weight",
@@ -49,6 +51,13 @@ GLOBAL_KEYS = [
     "model.spin_embedding.mlp.3.weight",
     "physical.reference_alphas",
     "physical.reference_c6",
+    # the optional C6 ratio head (absent from v1 models)
+    "model.c6_ratios_output_block.q_embedding.weight",
+    "model.c6_ratios_output_block.transform_features.0.weight",
+    "model.c6_ratios_output_block.transform_features.0.bias",
+    "model.c6_ratios_output_block.transform_features.2.weight",
+    "model.c6_ratios_output_block.transform_features.2.bias",
+    "model.c6_ratios_output_block.v_shift_embedding.weight",
 ]
 
 _FILTER = ["mlp_rbf.0.weight", "mlp_rbf.0.bias", "mlp_rbf.mlp_rbf_layer_1.0.weight",
@@ -83,7 +92,7 @@ SCALAR_KEYS = [
     "lr_hartree_ev", "lr_dispersion_scale", "lr_dispersion_cuton_angstrom", "lr_pair_scale",
 ]
 
-NTENSOR = len(GLOBAL_KEYS) + L * len(block_keys(0))
+NTENSOR = len(GLOBAL_KEYS) + MAXL * len(block_keys(0))
 
 
 class _Model(ctypes.Structure):
@@ -91,13 +100,23 @@ class _Model(ctypes.Structure):
                 ("rbf_k", ctypes.c_void_p),
                 ("rbf_krev", ctypes.c_void_p),
                 ("n_alpha_ref", ctypes.c_int64),
-                ("s", ctypes.c_double * len(SCALAR_KEYS))]
+                ("s", ctypes.c_double * len(SCALAR_KEYS)),
+                ("n_blocks", ctypes.c_int64),
+                ("norm1", ctypes.c_int64),
+                ("norm2", ctypes.c_int64),
+                ("qk_norm", ctypes.c_int64),
+                ("repulsion", ctypes.c_int64),
+                ("nlh_cap", ctypes.c_int64),
+                ("nlh_a", ctypes.c_void_p),
+                ("nlh_b", ctypes.c_void_p),
+                ("resid", ctypes.c_void_p),
+                ("x0l", ctypes.c_void_p)]
 
 
 class _Out(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in
                 ("e_learned", "e_zbl", "e_lr", "charges", "hirshfeld", "forces", "virial",
-                 "image_energy", "vatom")] + [
+                 "image_energy", "vatom", "c6_ratios")] + [
                 ("e_elec_total", ctypes.c_double), ("e_disp_total", ctypes.c_double),
                 ("e_total", ctypes.c_double)]
 
@@ -120,6 +139,7 @@ def lib():
         _lib.orc_charge_spin_table.restype = ctypes.c_int
         _lib.orc_charge_multiplicity_problem.restype = ctypes.c_int
         _lib.orc_num_threads.restype = ctypes.c_int
+        _lib.orc_rms_rows.restype = None
     return _lib
 
 
@@ -133,29 +153,60 @@ class Oracle:
     def __init__(self, model_path):
         self.model = model_io.load(model_path)
         m = self.model
+        arch = m.arch
         self._keep = []
         st = _Model()
+        nb = int(arch["interaction_blocks"])
+        if not 1 <= nb <= MAXL:
+            raise ValueError("interaction_blocks outside 1..%d" % MAXL)
         keys = list(GLOBAL_KEYS)
-        for b in range(L):
-            keys += block_keys(b)
+        for b in range(MAXL):
+            keys += block_keys(b) if b < nb else [None] * len(block_keys(0))
         assert len(keys) == NTENSOR
         for i, k in enumerate(keys):
-            arr = np.ascontiguousarray(m[k], dtype=np.float64)
-            self._keep.append(arr)
-            st.t[i] = arr.ctypes.data
+            if k is None or k not in m.tensors:
+                st.t[i] = None  # absent: the C6 head of a v1 model, parameter-free norms
+                continue
+            st.t[i] = self._hold(m[k], np.float64)
         k = np.ascontiguousarray(m["model.radial_embedding.radial_basis_fn.k"], dtype=np.int64)
         kr = np.ascontiguousarray(m["model.radial_embedding.radial_basis_fn.k_rev"], dtype=np.int64)
         self._keep += [k, kr]
         st.rbf_k = k.ctypes.data
         st.rbf_krev = kr.ctypes.data
         st.n_alpha_ref = m["physical.reference_alphas"].shape[0]
-        arch = m.arch
         for i, key in enumerate(SCALAR_KEYS):
             if key is None:
                 st.s[i] = float(m["model.radial_embedding.radial_basis_fn.gamma"])
-            else:
+            elif key == "avg_num_neighbors":
+                st.s[i] = attention_norm(arch)
+            elif key in arch:
                 st.s[i] = float(arch[key])
+            elif key.startswith("zbl_") and arch.get("repulsion_type") == "nlh":
+                st.s[i] = 0.0  # learned-ZBL parameters: not part of an NLH model
+            else:
+                raise KeyError(key)
+        # architecture options (so3lr_architecture.cpp:356-392)
+        st.n_blocks = nb
+        enabled = NORM_RMS if arch.get("use_rms_norm", False) else NORM_LAYER
+        st.norm1 = enabled if arch.get("layer_normalization_1", True) else NORM_NONE
+        st.norm2 = enabled if arch.get("layer_normalization_2", True) else NORM_NONE
+        st.qk_norm = 1 if arch.get("qk_norm", False) else 0
+        if arch.get("repulsion_type", "zbl_learned") == "nlh":
+            st.repulsion = REP_NLH
+            a = m["physical.nlh_a"]
+            st.nlh_cap = a.shape[0]
+            st.nlh_a = self._hold(a, np.float64)
+            st.nlh_b = self._hold(m["physical.nlh_b"], np.float64)
+        if arch.get("use_residual_scalars", False):
+            st.resid = self._hold(m["model.resid_lambdas"], np.float64)
+            st.x0l = self._hold(m["model.x0_lambdas"], np.float64)
+        self.has_c6 = "model.c6_ratios_output_block.transform_features.0.weight" in m.tensors
         self._st = st
+
+    def _hold(self, a, dtype):
+        arr = np.ascontiguousarray(a, dtype=dtype)
+        self._keep.append(arr)
+        return arr.ctypes.data
 
     def charge_spin_table(self, counts, charge, multiplicity):
         counts = np.ascontiguousarray(counts, dtype=np.int64)
@@ -209,6 +260,8 @@ class Oracle:
         outs["virial"] = np.zeros(6)
         outs["vatom"] = np.zeros((n, 6))
         outs["image_energy"] = np.zeros(n_images)
+        if self.has_c6:
+            outs["c6_ratios"] = np.zeros(n)
         o = _Out()
         for k, v in outs.items():
             setattr(o, k, v.ctypes.data)
@@ -224,6 +277,30 @@ class Oracle:
         outs["energy"] = o.e_total
         outs["eatom"] = outs["e_learned"] + outs["e_zbl"] + outs["e_lr"]
         return outs
+
+
+def attention_norm(arch):
+    """The divisor of the attention logits (so3lr_architecture.cpp:340-355):
+    1, sqrt(attention_head_width) or avg_num_neighbors, by
+    message_normalization (avg_num_neighbors when the key is absent)."""
+    kind = arch.get("message_normalization", "avg_num_neighbors")
+    if kind == "identity":
+        return 1.0
+    if kind == "sqrt_num_features":
+        return float(np.sqrt(float(arch["attention_head_width"])))
+    if kind == "avg_num_neighbors":
+        return float(arch["avg_num_neighbors"])
+    raise ValueError("unknown message_normalization %r" % kind)
+
+
+def rms_rows(x, eps):
+    """orc_rms_rows over the rows of x (2-D): (y, 1 / rms per row)."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.zeros_like(x)
+    r = np.zeros(x.shape[0])
+    lib().orc_rms_rows(ctypes.c_int64(x.shape[0]), ctypes.c_int64(x.shape[1]), _ptr(x), ctypes.c_double(eps),
+                       _ptr(y), _ptr(r))
+    return y, r
 
 
 def spherical_harmonics(u):

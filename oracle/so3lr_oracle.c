@@ -20,7 +20,6 @@
 #define HW ORC_HW
 #define E ORC_E
 #define R ORC_R
-#define L ORC_L
 #define NI ORC_NI
 #define FH ORC_FH
 #define HH ORC_HH
@@ -213,7 +212,9 @@ static void smooth_switch(double r, double on, double off, double *val, double *
   *der = ((dl * den - el * (dl + dr)) / (den * den)) / w;
 }
 
-/* ZBL for one directed edge (kokkos_physical_zbl.cpp:81-177). */
+/* Repulsion for one directed edge (kokkos_physical_zbl.cpp:81-177): learned
+ * ZBL, or the NLH pair tables indexed (min Z, max Z) from 1, whose pairs
+ * outside the tables get no screening term. */
 static void zbl_edge(const orc_model *m, double zi, double zj, double r,
                      double *energy, double *grad) {
   const double rc = m->s[ORC_S_RMAX];
@@ -242,27 +243,42 @@ static void zbl_edge(const orc_model *m, double zi, double zj, double r,
   const double ke = m->s[ORC_S_ZBL_KE];
   const double X = ke * fc * zz * inv;
   const double dX = ke * zz * (dfc * inv + fc * dinv);
-  const double rate = (pow(zi, m->s[ORC_S_ZBL_P]) + pow(zj, m->s[ORC_S_ZBL_P])) * m->s[ORC_S_ZBL_D];
   double Yv = 0.0, dY = 0.0;
-  for (int k = 0; k < 4; ++k) {
-    const double a = m->s[ORC_S_ZBL_A1 + k], c = m->s[ORC_S_ZBL_C1 + k];
-    const double ex = exp(-a * r * rate);
-    Yv += c * ex;
-    dY -= c * a * rate * ex;
+  if (m->repulsion == ORC_REP_NLH) {
+    const int64_t za = (int64_t)(zi < zj ? zi : zj), zb = (int64_t)(zi < zj ? zj : zi);
+    if (za >= 1 && zb <= m->nlh_cap) {
+      const size_t base = ((size_t)(za - 1) * (size_t)m->nlh_cap + (size_t)(zb - 1)) * 3;
+      for (int k = 0; k < 3; ++k) {
+        const double amp = m->nlh_a[base + k], rate = m->nlh_b[base + k];
+        const double ex = exp(-rate * r);
+        Yv += amp * ex;
+        dY -= rate * amp * ex;
+      }
+    }
+  } else {
+    const double rate = (pow(zi, m->s[ORC_S_ZBL_P]) + pow(zj, m->s[ORC_S_ZBL_P])) * m->s[ORC_S_ZBL_D];
+    for (int k = 0; k < 4; ++k) {
+      const double a = m->s[ORC_S_ZBL_A1 + k], c = m->s[ORC_S_ZBL_C1 + k];
+      const double ex = exp(-a * r * rate);
+      Yv += c * ex;
+      dY -= c * a * rate * ex;
+    }
   }
   *energy = 0.5 * sw * X * Yv;
   *grad = 0.5 * (dsw * X * Yv + sw * dX * Yv + sw * X * dY);
 }
 
-/* One LR half pair (kokkos_physical_long_range.cpp:147-380, v1: C6 from h). */
+/* One LR half pair (kokkos_physical_long_range.cpp:147-380).  C6 of an atom
+ * is C6_ref h^2 (v1) or, with a C6 head (sep), C6_ref c with c its C6 ratio;
+ * the polarisability is alpha_ref h either way.  dci, dcj: dE/dc (sep only). */
 typedef struct {
-  double e_elec, e_disp, charge_pref, dhi, dhj, radial;
+  double e_elec, e_disp, charge_pref, dhi, dhj, dci, dcj, radial;
   int valid;
 } lr_pair_t;
 
 static lr_pair_t lr_pair(const orc_model *m, int64_t zi_, int64_t zj_, double qi, double qj,
-                         double hi, double hj, double r) {
-  lr_pair_t o = {0, 0, 0, 0, 0, 0, 0};
+                         double hi, double hj, int sep, double cri, double crj, double r) {
+  lr_pair_t o = {0, 0, 0, 0, 0, 0, 0, 0, 0};
   const double cutoff = m->s[ORC_S_LR_CUTOFF], sigma = m->s[ORC_S_LR_SIGMA];
   const double ke = m->s[ORC_S_LR_KE];
   if (!(r > 1e-12) || r >= cutoff) return o;
@@ -292,20 +308,29 @@ static lr_pair_t lr_pair(const orc_model *m, int64_t zi_, int64_t zj_, double qi
     const double *aref = m->t[ORC_ALPHA_REF], *cref = m->t[ORC_C6_REF];
     const double ai0 = aref[zi], aj0 = aref[zj], ci0 = cref[zi], cj0 = cref[zj];
     const double ai = ai0 * hi, aj = aj0 * hj;
-    const double c6i = ci0 * hi * hi, c6j = cj0 * hj * hj;
+    const double c6i = sep ? ci0 * cri : ci0 * hi * hi, c6j = sep ? cj0 * crj : cj0 * hj * hj;
     const double alpha = 0.5 * (ai + aj);
     const double num = 2.0 * c6i * c6j * aj * ai;
     const double den = ai * ai * c6j + aj * aj * c6i;
     if (alpha > 0.0 && den > 1e-30) {
       const double c6 = num / den;
       const double idd = 1.0 / (den * den);
-      const double dc6i = 2.0 * ci0 * hi, dc6j = 2.0 * cj0 * hj;
-      const double dn_dhi = 2.0 * (dc6i * c6j * aj * ai + c6i * c6j * aj * ai0);
-      const double dn_dhj = 2.0 * (c6i * dc6j * aj * ai + c6i * c6j * aj0 * ai);
-      const double dd_dhi = 2.0 * ai * ai0 * c6j + aj * aj * dc6i;
-      const double dd_dhj = ai * ai * dc6j + 2.0 * aj * aj0 * c6i;
-      const double dc6_dhi = (dn_dhi * den - num * dd_dhi) * idd;
-      const double dc6_dhj = (dn_dhj * den - num * dd_dhj) * idd;
+      double dc6_dhi, dc6_dhj, dc6_dci = 0.0, dc6_dcj = 0.0;
+      if (!sep) {
+        const double dc6i = 2.0 * ci0 * hi, dc6j = 2.0 * cj0 * hj;
+        const double dn_dhi = 2.0 * (dc6i * c6j * aj * ai + c6i * c6j * aj * ai0);
+        const double dn_dhj = 2.0 * (c6i * dc6j * aj * ai + c6i * c6j * aj0 * ai);
+        const double dd_dhi = 2.0 * ai * ai0 * c6j + aj * aj * dc6i;
+        const double dd_dhj = ai * ai * dc6j + 2.0 * aj * aj0 * c6i;
+        dc6_dhi = (dn_dhi * den - num * dd_dhi) * idd;
+        dc6_dhj = (dn_dhj * den - num * dd_dhj) * idd;
+      } else {
+        /* h reaches C6 through the polarisabilities only, c through C6_i */
+        dc6_dhi = (2.0 * c6i * c6j * aj * ai0 * den - num * 2.0 * ai * ai0 * c6j) * idd;
+        dc6_dhj = (2.0 * c6i * c6j * aj0 * ai * den - num * 2.0 * aj * aj0 * c6i) * idd;
+        dc6_dci = (2.0 * ci0 * c6j * aj * ai * den - num * aj * aj * ci0) * idd;
+        dc6_dcj = (2.0 * c6i * cj0 * aj * ai * den - num * ai * ai * cj0) * idd;
+      }
       const double b0 = -0.00433008, b1 = 0.24428889, b2 = 0.04125273, b3 = -0.00078893;
       const double a7 = pow(alpha, 1.0 / 7.0);
       const double rvdw = pow(m->s[ORC_S_LR_FINE], -4.0 / 21.0) * a7;
@@ -339,6 +364,8 @@ static lr_pair_t lr_pair(const orc_model *m, int64_t zi_, int64_t zj_, double qi
       radial += full * hart * (rad_au * dsw / m->s[ORC_S_LR_BOHR] + qdo * ddsw);
       o.dhi = full * hart * dsw * dpi;
       o.dhj = full * hart * dsw * dpj;
+      o.dci = full * hart * dsw * dqdo_dc6 * dc6_dci;
+      o.dcj = full * hart * dsw * dqdo_dc6 * dc6_dcj;
     }
   }
   o.radial = radial;
@@ -356,9 +383,42 @@ static void build_csr(int64_t n, int64_t ne, const int64_t *key, int64_t *off, i
   free(fill);
 }
 
-/* LayerNorm with biased variance (kokkos_post_attention_block0.cpp:97-122) */
-static void layer_norm(const double *x, const double *w, const double *b, double eps,
+void orc_rms_rows(int64_t rows, int64_t width, const double *x, double eps, double *y,
+                  double *inv_rms) {
+  for (int64_t i = 0; i < rows; ++i) {
+    const double *xi = x + i * width;
+    double ms = 0.0;
+    for (int64_t c = 0; c < width; ++c) ms += xi[c] * xi[c];
+    ms /= (double)width;
+    const double r = 1.0 / sqrt(ms + eps);
+    for (int64_t c = 0; c < width; ++c) y[i * width + c] = xi[c] * r;
+    if (inv_rms) inv_rms[i] = r;
+  }
+}
+/* d/dx of y = x * r(x), r = 1 / sqrt(mean(x^2) + eps), given gy and y:
+ * r (gy - y mean(gy y)) */
+static void rms_rows_bwd(int width, const double *gy, const double *y, double r, double *gx) {
+  double m = 0.0;
+  for (int c = 0; c < width; ++c) m += gy[c] * y[c];
+  m /= (double)width;
+  for (int c = 0; c < width; ++c) gx[c] = r * (gy[c] - y[c] * m);
+}
+
+/* The normalisation of one node row (kokkos_post_attention_block0.cpp:97-162):
+ * affine LayerNorm with biased variance, RMSNorm without scale (xhat = y),
+ * or none (xhat = y = x, is = 1). */
+static void layer_norm(int mode, const double *x, const double *w, const double *b, double eps,
                        double *y, double *xhat, double *inv_sigma) {
+  if (mode == ORC_NORM_NONE) {
+    *inv_sigma = 1.0;
+    for (int c = 0; c < F; ++c) { xhat[c] = x[c]; y[c] = x[c]; }
+    return;
+  }
+  if (mode == ORC_NORM_RMS) {
+    orc_rms_rows(1, F, x, eps, xhat, inv_sigma);
+    for (int c = 0; c < F; ++c) y[c] = xhat[c];
+    return;
+  }
   double mean = 0.0;
   for (int c = 0; c < F; ++c) mean += x[c];
   mean /= F;
@@ -369,9 +429,17 @@ static void layer_norm(const double *x, const double *w, const double *b, double
   *inv_sigma = is;
   for (int c = 0; c < F; ++c) { xhat[c] = (x[c] - mean) * is; y[c] = xhat[c] * w[c] + b[c]; }
 }
-/* gx = dL/dx given gy, for y = xhat*w + b */
-static void layer_norm_bwd(const double *gy, const double *w, const double *xhat, double is,
+/* gx = dL/dx given gy, for the normalisation above */
+static void layer_norm_bwd(int mode, const double *gy, const double *w, const double *xhat, double is,
                            double *gx) {
+  if (mode == ORC_NORM_NONE) {
+    for (int c = 0; c < F; ++c) gx[c] = gy[c];
+    return;
+  }
+  if (mode == ORC_NORM_RMS) {
+    rms_rows_bwd(F, gy, xhat, is, gx);
+    return;
+  }
   double mg = 0.0, mgx = 0.0;
   double gh[F];
   for (int c = 0; c < F; ++c) { gh[c] = gy[c] * w[c]; mg += gh[c]; mgx += gh[c] * xhat[c]; }
@@ -382,7 +450,9 @@ static void layer_norm_bwd(const double *gy, const double *w, const double *xhat
 /* per-block saved state for the reverse pass */
 typedef struct {
   double *x_in, *ev_in;           /* n*F, n*E  block inputs */
-  double *qkv;                    /* n*5F: q k v qe ke */
+  double *qkv;                    /* n*5F: q k v qe ke (q, k, qe, ke RMS-normalised per
+                                     head with the QK normalisation) */
+  double *qkis;                   /* n*16: their 1/rms per (row, head), QK normalisation */
   double *s;                      /* ne*4 edge invariants */
   double *finv, *fev;             /* ne*F filters */
   double *ainv_alpha, *aev_alpha; /* ne*4 */
@@ -414,12 +484,16 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   const double gamma = m->s[ORC_S_GAMMA], rmax = m->s[ORC_S_RMAX];
   const double avg = m->s[ORC_S_AVG_NN], emb_scale = m->s[ORC_S_EMB_SCALE];
   const double eps = m->s[ORC_S_LN_EPS];
+  const int L = m->n_blocks > 0 ? (int)m->n_blocks : 3;
+  if (L > ORC_MAXL) return 6;
+  const int has_c6 = m->t[ORC_C6_W1] != NULL;
 
   double *r = NULL, *Y = NULL, *fc = NULL, *rbf = NULL, *zbl_e = NULL, *zbl_g = NULL;
   double *x = NULL, *ev = NULL, *dinv = NULL, *dev = NULL;
   double *gx = NULL, *gev = NULL, *gr = NULL, *gY = NULL, *ge = NULL;
   double *he_pre = NULL, *hq_pre = NULL, *hh_pre = NULL, *hkey = NULL, *heff = NULL;
   double *eatom = NULL, *qraw = NULL, *q = NULL, *hir = NULL;
+  double *x_emb = NULL, *c6_pre = NULL, *c6_key = NULL, *c6_eff = NULL, *c6r = NULL, *lr_dc = NULL;
   double *lr_e = NULL, *lr_dq = NULL, *lr_dh = NULL, *lr_f = NULL, *lr_pf = NULL;
   double *sr_f = NULL, *gqkv = NULL, *gfinv = NULL, *gfev = NULL, *gfc = NULL;
   double *img_sum = NULL, *img_cnt = NULL, *img_seed = NULL;
@@ -427,7 +501,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   double *gs = NULL, *gainv = NULL, *gaev = NULL;
   int64_t *roff = NULL, *ridx = NULL, *soff = NULL, *sidx = NULL;
   lr_pair_t *lrp = NULL;
-  block_state bs[L];
+  block_state bs[ORC_MAXL];
   memset(bs, 0, sizeof(bs));
 
   ALLOC(r, ne); ALLOC(Y, ne * E); ALLOC(fc, ne); ALLOC(rbf, ne * R);
@@ -469,16 +543,25 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   for (int64_t i = 0; i < n; ++i)
     for (int c = 0; c < F; ++c)
       x[i * F + c] = (m->t[ORC_EMB_W][c * 118 + (z[i] - 1)] + (emb_offset ? emb_offset[i * F + c] : 0.0)) / emb_scale;
+  if (m->resid) {
+    ALLOC(x_emb, n * F);
+    memcpy(x_emb, x, sizeof(double) * (size_t)(n * F));
+  }
 
   /* ---- interaction blocks, forward ---- */
   for (int b = 0; b < L; ++b) {
     const double *const *T = m->t + ORC_NGLOBAL + b * ORC_NBLOCK;
     block_state *S = &bs[b];
-    ALLOC(S->x_in, n * F); ALLOC(S->ev_in, n * E); ALLOC(S->qkv, n * 5 * F);
+    ALLOC(S->x_in, n * F); ALLOC(S->ev_in, n * E); ALLOC(S->qkv, n * 5 * F); ALLOC(S->qkis, n * 16);
     ALLOC(S->s, ne * 4); ALLOC(S->finv, ne * F); ALLOC(S->fev, ne * F);
     ALLOC(S->ainv_alpha, ne * 4); ALLOC(S->aev_alpha, ne * 4); ALLOC(S->a_ev, n * E);
     ALLOC(S->n1, n * F); ALLOC(S->n1hat, n * F); ALLOC(S->n1is, n); ALLOC(S->hpre, n * F);
     ALLOC(S->tout, n * NI); ALLOC(S->pre2hat, n * F); ALLOC(S->pre2is, n);
+    /* residual scalars (kokkos_local_energy_reverse.cpp:143-158): the block
+     * input is resid[b] x + x0[b] x_emb, x the previous block's output (the
+     * embedding itself for block 0) */
+    if (m->resid)
+      for (int64_t k = 0; k < n * F; ++k) x[k] = m->resid[b] * x[k] + m->x0l[b] * x_emb[k];
     memcpy(S->x_in, x, sizeof(double) * (size_t)(n * F));
     memcpy(S->ev_in, ev, sizeof(double) * (size_t)(n * E));
     const double *acg = T[ORC_B_ATT_CG], *icg = T[ORC_B_INT_CG];
@@ -516,6 +599,18 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
             for (int k = 0; k < HW; ++k) s += x[i * F + h * HW + k] * T[wid[w]][(h * HW + k) * HW + o];
             S->qkv[i * 5 * F + w * F + h * HW + o] = s;
           }
+    /* QK normalisation per (node, head) row of q, k, q_ev, k_ev, eps 1e-6
+     * (kokkos_integrated_block0.cpp:288-328); v is left as it is */
+    if (m->qk_norm) {
+      const int rows[4] = {0, 1, 3, 4};
+#pragma omp parallel for schedule(static)
+      for (int64_t i = 0; i < n; ++i)
+        for (int k = 0; k < 4; ++k)
+          for (int h = 0; h < NH; ++h) {
+            double *row = S->qkv + i * 5 * F + rows[k] * F + h * HW;
+            orc_rms_rows(1, HW, row, 1e-6, row, S->qkis + i * 16 + k * 4 + h);
+          }
+    }
     /* attention coefficients per (edge, head) */
 #pragma omp parallel for schedule(static)
     for (int64_t e = 0; e < ne; ++e) {
@@ -550,7 +645,8 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
       double ainv[F], act[F], hid[F], mlp[F], p[F], cat[NI], pre2[F], y2[F];
       for (int c = 0; c < F; ++c) ainv[c] = x[i * F + c] + dinv[i * F + c];
       for (int c = 0; c < E; ++c) S->a_ev[i * E + c] = ev[i * E + c] + dev[i * E + c];
-      layer_norm(ainv, T[ORC_B_LN1_W], T[ORC_B_LN1_B], eps, S->n1 + i * F, S->n1hat + i * F, &S->n1is[i]);
+      layer_norm((int)m->norm1, ainv, T[ORC_B_LN1_W], T[ORC_B_LN1_B], eps, S->n1 + i * F, S->n1hat + i * F,
+                 &S->n1is[i]);
       const double *n1 = S->n1 + i * F;
       for (int c = 0; c < F; ++c) act[c] = silu(n1[c]);
       matvec(T[ORC_B_M1_W], T[ORC_B_M1_B], F, F, act, S->hpre + i * F);
@@ -564,7 +660,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
       const double *t = S->tout + i * NI;
       for (int c = 0; c < F; ++c) pre2[c] = p[c] + t[c];
       for (int c = 0; c < E; ++c) ev[i * E + c] = S->a_ev[i * E + c] * (1.0 + t[F + degree_of(c)]);
-      layer_norm(pre2, T[ORC_B_LN2_W], T[ORC_B_LN2_B], eps, y2, S->pre2hat + i * F, &S->pre2is[i]);
+      layer_norm((int)m->norm2, pre2, T[ORC_B_LN2_W], T[ORC_B_LN2_B], eps, y2, S->pre2hat + i * F, &S->pre2is[i]);
       memcpy(x + i * F, y2, sizeof(y2));
     }
   }
@@ -572,6 +668,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   /* ---- output heads (kokkos_output_heads.cpp:137-176,341-451) ---- */
   ALLOC(he_pre, n * F); ALLOC(hq_pre, n * F); ALLOC(hh_pre, n * HH); ALLOC(hkey, n * HH);
   ALLOC(heff, n); ALLOC(eatom, n); ALLOC(qraw, n); ALLOC(q, n); ALLOC(hir, n);
+  if (has_c6) { ALLOC(c6_pre, n * HH); ALLOC(c6_key, n * HH); ALLOC(c6_eff, n); ALLOC(c6r, n); }
 #pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < n; ++i) {
     double t[F], hh[HH];
@@ -593,6 +690,17 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     for (int c = 0; c < HH; ++c) qk += m->t[ORC_H_QEMB][zi * HH + c] * hkey[i * HH + c];
     heff[i] = m->t[ORC_H_VSHIFT][zi] + qk / sqrt((double)HH);
     hir[i] = fabs(heff[i]);
+    if (has_c6) {
+      /* the C6 ratio head: a second ratio head of the Hirshfeld form
+       * (kokkos_output_heads.cpp:108-180) */
+      matvec(m->t[ORC_C6_W1], m->t[ORC_C6_B1], HH, F, x + i * F, c6_pre + i * HH);
+      for (int c = 0; c < HH; ++c) hh[c] = silu(c6_pre[i * HH + c]);
+      matvec(m->t[ORC_C6_W2], m->t[ORC_C6_B2], HH, HH, hh, c6_key + i * HH);
+      double ck = 0.0;
+      for (int c = 0; c < HH; ++c) ck += m->t[ORC_C6_QEMB][zi * HH + c] * c6_key[i * HH + c];
+      c6_eff[i] = m->t[ORC_C6_VSHIFT][zi] + ck / sqrt((double)HH);
+      c6r[i] = fabs(c6_eff[i]);
+    }
   }
   /* per-image charge conservation (kokkos_image_segments.cpp) */
   ALLOC(img_sum, n_images); ALLOC(img_cnt, n_images); ALLOC(img_seed, n_images);
@@ -608,7 +716,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   }
 
   /* ---- long range per unique half pair ---- */
-  ALLOC(lr_e, n); ALLOC(lr_dq, n); ALLOC(lr_dh, n); ALLOC(lr_f, n * 3); ALLOC(lr_pf, (np > 0 ? np : 1) * 3);
+  ALLOC(lr_e, n); ALLOC(lr_dq, n); ALLOC(lr_dh, n); ALLOC(lr_dc, n); ALLOC(lr_f, n * 3); ALLOC(lr_pf, (np > 0 ? np : 1) * 3);
   lrp = (lr_pair_t *)calloc((size_t)(np > 0 ? np : 1), sizeof(lr_pair_t));
   if (!lrp) goto fail;
 #pragma omp parallel for schedule(static)
@@ -617,7 +725,8 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     if (i == j) continue;
     const double dx = pvec[3 * p], dy = pvec[3 * p + 1], dz = pvec[3 * p + 2];
     const double rr = sqrt(dx * dx + dy * dy + dz * dz);
-    lrp[p] = lr_pair(m, z[i], z[j], q[i], q[j], hir[i], hir[j], rr);
+    lrp[p] = lr_pair(m, z[i], z[j], q[i], q[j], hir[i], hir[j], has_c6, has_c6 ? c6r[i] : 0.0,
+                     has_c6 ? c6r[j] : 0.0, rr);
     if (lrp[p].valid) {
       const double inv = 1.0 / rr;
       lr_pf[3 * p] = lrp[p].radial * dx * inv;
@@ -633,6 +742,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     lr_e[i] += 0.5 * pe; lr_e[j] += 0.5 * pe;
     lr_dq[i] += lrp[p].charge_pref * q[j]; lr_dq[j] += lrp[p].charge_pref * q[i];
     lr_dh[i] += lrp[p].dhi; lr_dh[j] += lrp[p].dhj;
+    lr_dc[i] += lrp[p].dci; lr_dc[j] += lrp[p].dcj;
     for (int a = 0; a < 3; ++a) { lr_f[3 * i + a] += lr_pf[3 * p + a]; lr_f[3 * j + a] -= lr_pf[3 * p + a]; }
   }
 
@@ -659,6 +769,15 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     matvecT_acc(m->t[ORC_H_W2], HH, HH, gk, ghh);
     for (int c = 0; c < HH; ++c) ghh[c] *= silu_prime(hh_pre[i * HH + c]);
     matvecT_acc(m->t[ORC_H_W1], HH, F, ghh, g);
+    if (has_c6) {
+      const double sc = c6_eff[i] > 0.0 ? 1.0 : (c6_eff[i] < 0.0 ? -1.0 : 0.0);
+      const double cs = lr_dc[i] * sc / sqrt((double)HH);
+      for (int c = 0; c < HH; ++c) gk[c] = cs * m->t[ORC_C6_QEMB][zi * HH + c];
+      memset(ghh, 0, sizeof(ghh));
+      matvecT_acc(m->t[ORC_C6_W2], HH, HH, gk, ghh);
+      for (int c = 0; c < HH; ++c) ghh[c] *= silu_prime(c6_pre[i * HH + c]);
+      matvecT_acc(m->t[ORC_C6_W1], HH, F, ghh, g);
+    }
   }
 
   /* ---- interaction blocks, reverse ---- */
@@ -673,7 +792,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     for (int64_t i = 0; i < n; ++i) {
       double gpre2[F], gt[NI], gcat[NI], gp[F], ghid[F], gact[F], gn1[F];
       const double *t = S->tout + i * NI, *aev = S->a_ev + i * E;
-      layer_norm_bwd(gx + i * F, T[ORC_B_LN2_W], S->pre2hat + i * F, S->pre2is[i], gpre2);
+      layer_norm_bwd((int)m->norm2, gx + i * F, T[ORC_B_LN2_W], S->pre2hat + i * F, S->pre2is[i], gpre2);
       for (int c = 0; c < F; ++c) { gt[c] = gpre2[c]; gp[c] = gpre2[c]; }
       for (int l = 0; l < 4; ++l) gt[F + l] = 0.0;
       double *ga = gaev + i * E;
@@ -692,7 +811,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
       memset(gact, 0, sizeof(gact));
       matvecT_acc(T[ORC_B_M1_W], F, F, ghid, gact);
       for (int c = 0; c < F; ++c) gn1[c] = gp[c] + gact[c] * silu_prime(S->n1[i * F + c]);
-      layer_norm_bwd(gn1, T[ORC_B_LN1_W], S->n1hat + i * F, S->n1is[i], gainv + i * F);
+      layer_norm_bwd((int)m->norm1, gn1, T[ORC_B_LN1_W], S->n1hat + i * F, S->n1is[i], gainv + i * F);
     }
     /* attention reverse per edge (kokkos_attention_scatter_reverse.cpp:280-500) */
 #pragma omp parallel for schedule(static)
@@ -796,6 +915,17 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     for (int64_t i = 0; i < n; ++i) {
       double *g = gx + i * F;
       for (int c = 0; c < F; ++c) g[c] = gainv[i * F + c];
+      if (m->qk_norm) {
+        /* through the QK normalisation: the adjoints of the raw rows */
+        const int rows[4] = {0, 1, 3, 4};
+        for (int k = 0; k < 4; ++k)
+          for (int h = 0; h < NH; ++h) {
+            double *gr_ = gqkv + i * 5 * F + rows[k] * F + h * HW;
+            double tmp[HW];
+            rms_rows_bwd(HW, gr_, S->qkv + i * 5 * F + rows[k] * F + h * HW, S->qkis[i * 16 + k * 4 + h], tmp);
+            memcpy(gr_, tmp, sizeof(tmp));
+          }
+      }
       for (int w = 0; w < 5; ++w)
         for (int h = 0; h < NH; ++h)
           for (int k = 0; k < HW; ++k) {
@@ -816,6 +946,10 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
         for (int c = 0; c < E; ++c)
           ge_[c] -= gs[e * 4 + degree_of(c)] * 2.0 * (S->ev_in[snd[e] * E + c] - evi[c]) * acg[c];
       }
+      /* residual scalars: d/d(previous output) = resid[b] d/d(input); the
+       * embedding term does not depend on the positions */
+      if (m->resid)
+        for (int c = 0; c < F; ++c) g[c] *= m->resid[b];
     }
   }
 
@@ -871,6 +1005,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     if (out->e_lr) out->e_lr[i] = lr_e[i];
     if (out->charges) out->charges[i] = q[i];
     if (out->hirshfeld) out->hirshfeld[i] = hir[i];
+    if (out->c6_ratios && has_c6) out->c6_ratios[i] = c6r[i];
     if (out->forces)
       for (int a = 0; a < 3; ++a) out->forces[3 * i + a] = sr_f[3 * i + a] + lr_f[3 * i + a];
     if (out->image_energy) {
@@ -913,12 +1048,13 @@ fail:
   free(x); free(ev); free(dinv); free(dev); free(gx); free(gev); free(gr); free(gY); free(ge);
   free(he_pre); free(hq_pre); free(hh_pre); free(hkey); free(heff);
   free(eatom); free(qraw); free(q); free(hir);
+  free(x_emb); free(c6_pre); free(c6_key); free(c6_eff); free(c6r); free(lr_dc);
   free(lr_e); free(lr_dq); free(lr_dh); free(lr_f); free(lr_pf); free(lrp);
   free(sr_f); free(gqkv); free(gfinv); free(gfev); free(gfc); free(gs); free(gainv); free(gaev);
   free(roff); free(ridx); free(soff); free(sidx);
   for (int b = 0; b < L; ++b) {
     block_state *S = &bs[b];
-    free(S->x_in); free(S->ev_in); free(S->qkv); free(S->s); free(S->finv); free(S->fev);
+    free(S->x_in); free(S->ev_in); free(S->qkv); free(S->qkis); free(S->s); free(S->finv); free(S->fev);
     free(S->ainv_alpha); free(S->aev_alpha); free(S->a_ev); free(S->n1); free(S->n1hat);
     free(S->n1is); free(S->hpre); free(S->tout); free(S->pre2hat); free(S->pre2is);
   }

@@ -23,6 +23,13 @@
  *   orchestration, charge
  *   correction, virial              plugins/lammps/pair_so3lr_native_mpi.cpp:944-990,1596-1878
  *   per-image charge correction     src/kokkos_image_segments.cpp
+ *   architecture options            src/so3lr_architecture.cpp:300-392
+ *     RMSNorm, norm positions       src/kokkos_post_attention_block0.cpp:126-162
+ *     QK normalisation              src/kokkos_integrated_block0.cpp:288-328
+ *     residual scalars              src/kokkos_local_energy_reverse.cpp:85-170
+ *     NLH repulsion                 src/kokkos_physical_zbl.cpp:145-162
+ *     C6 ratio head, C6 mixing      src/kokkos_output_heads.cpp:108-180,405-415,
+ *                                   src/kokkos_physical_long_range.cpp:120-360
  *
  * Parity pins: every function here is checked in tests/test_oracle_*.py against
  * the reference's JAX golden vectors (tests/golden/refs), closed forms, finite
@@ -40,13 +47,14 @@
 extern "C" {
 #endif
 
-/* v1 widths (the only architecture the shipped model uses). */
+/* Widths of the models the oracle evaluates (those of every released F = 128
+ * checkpoint); the block count is a model field (1..ORC_MAXL). */
 #define ORC_F 128   /* invariant features */
 #define ORC_NH 4    /* heads (invariant == equivariant head count) */
 #define ORC_HW 32   /* head width */
 #define ORC_E 24    /* equivariant channels, degrees 1..4 */
 #define ORC_R 32    /* radial basis */
-#define ORC_L 3     /* interaction blocks */
+#define ORC_MAXL 8  /* interaction blocks, at most */
 #define ORC_NI 132  /* interaction width F + 4 */
 #define ORC_FH 32   /* spherical filter hidden width F/4 */
 #define ORC_HH 64   /* Hirshfeld head width */
@@ -61,6 +69,9 @@ enum {
   ORC_CE_WQ, ORC_CE_WK, ORC_CE_WV, ORC_CE_M1, ORC_CE_M3,
   ORC_SE_WQ, ORC_SE_WK, ORC_SE_WV, ORC_SE_M1, ORC_SE_M3,
   ORC_ALPHA_REF, ORC_C6_REF,
+  /* optional C6 ratio head (NULL when the model has none), laid out as the
+   * Hirshfeld head: (100,64) (64,128) (64) (64,64) (64) (100,1) */
+  ORC_C6_QEMB, ORC_C6_W1, ORC_C6_B1, ORC_C6_W2, ORC_C6_B2, ORC_C6_VSHIFT,
   ORC_NGLOBAL
 };
 
@@ -77,7 +88,14 @@ enum {
   ORC_NBLOCK
 };
 
-#define ORC_NTENSOR (ORC_NGLOBAL + ORC_L * ORC_NBLOCK)
+#define ORC_NTENSOR (ORC_NGLOBAL + ORC_MAXL * ORC_NBLOCK)
+
+/* Normalisation at the two positions of the post-attention block
+ * (kokkos_post_attention_block0.cpp:97-162): affine LayerNorm, RMSNorm
+ * without scale, or none (the second position only). */
+enum { ORC_NORM_LAYER = 0, ORC_NORM_RMS = 1, ORC_NORM_NONE = 2 };
+/* Short-range repulsion (kokkos_physical_zbl.cpp:81-177). */
+enum { ORC_REP_ZBL = 0, ORC_REP_NLH = 1 };
 
 /* Scalar slots. */
 enum {
@@ -97,6 +115,15 @@ typedef struct {
   const int64_t *rbf_krev;  /* (32) */
   int64_t n_alpha_ref;      /* extent of the reference alpha/C6 tables */
   double s[ORC_NSCALAR];
+  /* Architecture options; all zero/NULL is the v1 model with 3 blocks. */
+  int64_t n_blocks;         /* interaction blocks (0 means 3) */
+  int64_t norm1, norm2;     /* ORC_NORM_* of the two positions */
+  int64_t qk_norm;          /* RMS-normalise the q, k, q_ev, k_ev head rows */
+  int64_t repulsion;        /* ORC_REP_* */
+  int64_t nlh_cap;          /* NLH tables: (cap, cap, 3) amplitudes and rates */
+  const double *nlh_a, *nlh_b;
+  const double *resid;      /* residual scalars per block (NULL: none) */
+  const double *x0l;
 } orc_model;
 
 typedef struct {
@@ -113,6 +140,7 @@ typedef struct {
                           -v (x) dE/dv (symmetrised, as virial) split half to
                           each endpoint; sums to virial.  The reference has no
                           per-atom virial (pair_so3lr_native_mpi.cpp:1248-1251). */
+  double *c6_ratios;   /* C6 head output (models with that head) */
   double e_elec_total; /* sum of electrostatic pair energies */
   double e_disp_total; /* sum of dispersion pair energies */
   double e_total;      /* sum of all per-node energies */
@@ -152,6 +180,15 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
                  int64_t ne, const int64_t *senders, const int64_t *receivers,
                  const double *vectors, int64_t np, const int64_t *pi,
                  const int64_t *pj, const double *pvectors, orc_out *out);
+
+/* RMS normalisation of `rows` rows of `width` values:
+ * y = x / sqrt(mean(x^2) + eps), inv_rms[row] = 1 / sqrt(mean(x^2) + eps)
+ * (inv_rms may be NULL).  RMSNorm without scale
+ * (kokkos_post_attention_block0.cpp:126-143, width 128, eps of the model) and
+ * the QK normalisation (kokkos_integrated_block0.cpp:288-328, width 32,
+ * eps 1e-6) are this function. */
+void orc_rms_rows(int64_t rows, int64_t width, const double *x, double eps, double *y,
+                  double *inv_rms);
 
 /* Real spherical harmonics l=1..4 at a unit vector (24 values). */
 void orc_spherical_harmonics(double x, double y, double z, double *value);

@@ -23,6 +23,10 @@ struct LrParams {
 
 struct ZblParams {
   double ke, rc, switch_off, p, d, a[4], c[4];
+  // NLH repulsion (nlh_cap > 0): per element pair (min Z, max Z, from 1)
+  // three amplitudes and rates in place of the screening sum
+  const double *nlh_a, *nlh_b;
+  int nlh_cap;
 };
 
 __device__ __forceinline__ double silu(double x) { return x / (1.0 + exp(-x)); }
@@ -161,7 +165,8 @@ __device__ __forceinline__ void bump_switch(double r, double on, double off, dou
   der = ((dl * den - el * (dl + dr)) / (den * den)) / w;
 }
 
-// ZBL energy and d/dr of ONE directed edge (the value is symmetric in i, j).
+// Repulsion energy and d/dr of ONE directed edge (the value is symmetric in
+// i, j): learned ZBL, or NLH tables (kokkos_physical_zbl.cpp:81-177).
 __device__ __forceinline__ void zbl_directed(const ZblParams &P, double zi, double zj, double r,
                                              double &energy, double &grad) {
   energy = 0.0;
@@ -177,13 +182,27 @@ __device__ __forceinline__ void zbl_directed(const ZblParams &P, double zi, doub
   const double inv = 1.0 / rs, dinv = r > 1e-6 ? -1.0 / (r * r) : 0.0;
   const double X = P.ke * fc * zz * inv;
   const double dX = P.ke * zz * (dfc * inv + fc * dinv);
-  const double rate = (pow(zi, P.p) + pow(zj, P.p)) * P.d;
   double Yv = 0.0, dY = 0.0;
+  if (P.nlh_cap > 0) {
+    const int za = int(zi < zj ? zi : zj), zb = int(zi < zj ? zj : zi);
+    if (za >= 1 && zb <= P.nlh_cap) {
+      const int base = ((za - 1) * P.nlh_cap + (zb - 1)) * 3;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const double ex = exp(-P.a[k] * r * rate);
-    Yv += P.c[k] * ex;
-    dY -= P.c[k] * P.a[k] * rate * ex;
+      for (int k = 0; k < 3; ++k) {
+        const double amp = P.nlh_a[base + k], rt = P.nlh_b[base + k];
+        const double ex = exp(-rt * r);
+        Yv += amp * ex;
+        dY -= rt * amp * ex;
+      }
+    }
+  } else {
+    const double rate = (pow(zi, P.p) + pow(zj, P.p)) * P.d;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const double ex = exp(-P.a[k] * r * rate);
+      Yv += P.c[k] * ex;
+      dY -= P.c[k] * P.a[k] * rate * ex;
+    }
   }
   energy = 0.5 * sw * X * Yv;
   grad = 0.5 * (dsw * X * Yv + sw * dX * Yv + sw * X * dY);
@@ -191,6 +210,7 @@ __device__ __forceinline__ void zbl_directed(const ZblParams &P, double zi, doub
 
 struct LrPairTerms {
   double e_el, e_disp, pref, dh_self, radial;
+  double dc_self;  // dE/dc_i of the C6 ratio (SEP_C6 only)
 };
 
 // bump_switch with 1 / (off - on) given, three reciprocals instead of seven
@@ -253,11 +273,14 @@ __device__ __forceinline__ double erf_lean(double x, double exp_mx2) {
 // 2 s_fit^2 exactly).  This runs once per long-range entry (about 900 per
 // atom), so the reciprocals, e^x and alpha^(1/7) take the lean forms above.
 // LEAN_ERF: erf(r / sigma) by erf_lean (the caller has checked cutoff / sigma <= 3)
-template <bool LEAN_ERF>
+// SEP_C6: the model's C6 head gives C6_i = C6_ref c_i (ci, cj); h then
+// enters through the polarisabilities only (kokkos_physical_long_range.cpp:
+// 217-285), and dc_self = dE/dc_i
+template <bool LEAN_ERF, bool SEP_C6 = false>
 __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *__restrict__ aref,
                                               const double *__restrict__ cref, int zi_, int zj_,
                                               double qi, double qj, double hi, double hj, double r,
-                                              LrPairTerms &o) {
+                                              LrPairTerms &o, double ci = 0.0, double cj = 0.0) {
   if (!(r > 1e-12) || r >= P.cutoff) return false;
   const double ir = rcp_lean(r);
   double esw, desw;
@@ -276,21 +299,28 @@ __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *_
   o.radial = sk * qi * qj * dkern;
   o.e_disp = 0.0;
   o.dh_self = 0.0;
+  o.dc_self = 0.0;
   const int zi = zi_ - 1, zj = zj_ - 1;
   if (zi < 0 || zj < 0 || zi >= P.n_ref || zj >= P.n_ref) return true;
   const double ai0 = aref[zi], aj0 = aref[zj], ci0 = cref[zi], cj0 = cref[zj];
   const double ai = ai0 * hi, aj = aj0 * hj;
-  const double c6i = ci0 * hi * hi, c6j = cj0 * hj * hj;
+  const double c6i = SEP_C6 ? ci0 * ci : ci0 * hi * hi, c6j = SEP_C6 ? cj0 * cj : cj0 * hj * hj;
   const double alpha = 0.5 * (ai + aj);
   const double num = 2.0 * c6i * c6j * aj * ai;
   const double den = ai * ai * c6j + aj * aj * c6i;
   if (!(alpha > 0.0 && den > 1e-30)) return true;
   const double iden = rcp_lean(den);
   const double c6 = num * iden;
-  const double dc6i = 2.0 * ci0 * hi;
-  const double dn_dhi = 2.0 * (dc6i * c6j * aj * ai + c6i * c6j * aj * ai0);
-  const double dd_dhi = 2.0 * ai * ai0 * c6j + aj * aj * dc6i;
-  const double dc6_dhi = (dn_dhi * den - num * dd_dhi) * iden * iden;
+  double dc6_dhi, dc6_dci = 0.0;
+  if constexpr (SEP_C6) {
+    dc6_dhi = (2.0 * c6i * c6j * aj * ai0 * den - num * 2.0 * ai * ai0 * c6j) * iden * iden;
+    dc6_dci = (2.0 * ci0 * c6j * aj * ai * den - num * aj * aj * ci0) * iden * iden;
+  } else {
+    const double dc6i = 2.0 * ci0 * hi;
+    const double dn_dhi = 2.0 * (dc6i * c6j * aj * ai + c6i * c6j * aj * ai0);
+    const double dd_dhi = 2.0 * ai * ai0 * c6j + aj * aj * dc6i;
+    dc6_dhi = (dn_dhi * den - num * dd_dhi) * iden * iden;
+  }
   const double b0 = -0.00433008, b1 = 0.24428889, b2 = 0.04125273, b3 = -0.00078893;
   const double a7 = root7_lean(alpha);
   const double i7a = rcp_lean(7.0 * alpha);
@@ -322,6 +352,7 @@ __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *_
   o.e_disp = sh * qdo * dsw;
   o.radial += sh * (rad_au * dsw * P.inv_bohr + qdo * ddsw);
   o.dh_self = sh * dsw * dpi;
+  if constexpr (SEP_C6) o.dc_self = sh * dsw * dqdo_dc6 * dc6_dci;
   return true;
 }
 

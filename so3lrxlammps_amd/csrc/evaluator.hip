@@ -105,6 +105,52 @@ __global__ void k_fill(double *p, std::size_t n, double v) {
   if (i < n) p[i] = v;
 }
 
+// Residual scalars (kokkos_local_energy_reverse.cpp:124-170): a block's input
+// x <- a x + c x0 (x0 the embedding), and the adjoint of the previous block's
+// output g <- a g.
+__global__ void k_axpby(std::size_t n, double a, double *x, double c, const double *x0) {
+  const std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = a * x[i] + c * x0[i];
+}
+__global__ void k_scale(std::size_t n, double a, double *g) {
+  const std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) g[i] *= a;
+}
+
+// QK normalisation (kokkos_integrated_block0.cpp:288-328): each head row
+// (32 channels) of q, k, q_ev, k_ev of a node divided by its RMS, eps 1e-6;
+// v untouched.  One thread per (node, row); row r = 4 w + h, w = q, k, q_ev,
+// k_ev at 0, 128, 384, 512 of the 640-wide node row (a head's 32 channels stay
+// together in the tile-transposed order).  1/rms kept for the reverse.
+__device__ __forceinline__ int qk_row(int r) { return (r < 8 ? 128 * (r >> 2) : 128 * ((r >> 2) + 1)) + 32 * (r & 3); }
+__global__ __launch_bounds__(256) void k_qk_norm(int N, double *qkv, double *qkis) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= N * 16) return;
+  double *row = qkv + std::size_t(t >> 4) * 640 + qk_row(t & 15);
+  double ms = 0.0;
+#pragma unroll 8
+  for (int c = 0; c < 32; ++c) ms += row[c] * row[c];
+  const double r = 1.0 / sqrt(ms / 32.0 + 1e-6);
+#pragma unroll 8
+  for (int c = 0; c < 32; ++c) row[c] *= r;
+  qkis[t] = r;
+}
+// its reverse on the row adjoints: g <- r (g - y mean(g y)), y the normalised row
+__global__ __launch_bounds__(256) void k_qk_norm_bwd(int N, const double *qkv, const double *qkis, double *gqkv) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= N * 16) return;
+  const std::size_t o = std::size_t(t >> 4) * 640 + qk_row(t & 15);
+  const double *y = qkv + o;
+  double *g = gqkv + o;
+  double m = 0.0;
+#pragma unroll 8
+  for (int c = 0; c < 32; ++c) m += g[c] * y[c];
+  m /= 32.0;
+  const double r = qkis[t];
+#pragma unroll 8
+  for (int c = 0; c < 32; ++c) g[c] = r * (g[c] - y[c] * m);
+}
+
 // ---------------------------------------------------------------- compaction
 // Active short-range pairs are those with 0 < r^2 < rc^2, kept in candidate
 // order (pair_so3lr_native_mpi.cpp:258-291,306-373 count + stable scan).
@@ -479,6 +525,18 @@ __device__ __forceinline__ double silu_prime_tab(double x, const double *tab) {
   const double s = rcp_act(1.0 + exp_tab(-x, tab));
   return s * (1.0 + x * (1.0 - s));
 }
+// The same for arguments of any size: the exponent is clamped to [-1000,
+// 1000], where e^-x has long underflowed to 0 or reached the 2^1000 cap, so
+// silu(x) = x (x > 1000) or 0 to within 1e-290 (x < -1000).  exp_tab's range
+// ends near |x| = 5.8e6; the spherical filter branch takes the edge
+// invariants of the equivariant features, whose size no weight bounds.
+__device__ __forceinline__ double silu_tab_wide(double x, const double *tab) {
+  return x * rcp_act(1.0 + exp_tab(-fmin(fmax(x, -1000.0), 1000.0), tab));
+}
+__device__ __forceinline__ double silu_prime_tab_wide(double x, const double *tab) {
+  const double s = rcp_act(1.0 + exp_tab(-fmin(fmax(x, -1000.0), 1000.0), tab));
+  return s * (1.0 + x * (1.0 - s));
+}
 // The table into LDS: call at kernel start, before any wavefront returns.
 #define SO3LR_EXP2_TABLE(A)                                               \
   __shared__ double exp2_lds[256];                                        \
@@ -703,7 +761,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
           for (int t = 0; t < 2; ++t) {
             h2[t] = mfma(e0[t], sg, h2[t]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab(h2[t][r], exp2_lds);
+            for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
           }
         }
         // (block 0, EV0: the rows are not stored; its reverse has no node-major
@@ -1069,7 +1127,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
         for (int mt = 0; mt < 2; ++mt) {
           pre2[mt] = mfma(w[mt], sg, pre2[mt]);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime_tab(pre2[mt][q], exp2_lds);
+          for (int q = 0; q < 4; ++q) dh2[mt][q] *= silu_prime_tab_wide(pre2[mt][q], exp2_lds);
         }
       }
     } else if constexpr (s < D_END) {
@@ -1410,13 +1468,14 @@ __global__ __launch_bounds__(256) void k_attn_fwd(int N, const int *inc_off, con
 
 // LayerNorm over 128 channels held two per lane (biased variance), the
 // lane's two channels having weights w0, w1 and biases b0, b1.
+// mode (NormMode): 0 affine LayerNorm; 1 RMSNorm without scale (no mean
+// removed; the caller passes w = 1, b = 0); 2 none (h = y = v, is = 1)
 __device__ __forceinline__ void wave_layer_norm_pair(double v0, double v1, double w0, double w1, double b0,
-                                                     double b1, double eps, double &y0, double &y1, double &h0,
-                                                     double &h1, double &is) {
-  const double mean = wave_sum(v0 + v1) / kF;
+                                                     double b1, double eps, int mode, double &y0, double &y1,
+                                                     double &h0, double &h1, double &is) {
+  const double mean = mode == 0 ? wave_sum(v0 + v1) / kF : 0.0;
   const double d0 = v0 - mean, d1 = v1 - mean;
-  const double var = wave_sum(d0 * d0 + d1 * d1) / kF;
-  is = 1.0 / sqrt(var + eps);
+  is = mode == 2 ? 1.0 : 1.0 / sqrt(wave_sum(d0 * d0 + d1 * d1) / kF + eps);
   h0 = d0 * is;
   h1 = d1 * is;
   y0 = h0 * w0 + b0;
@@ -1432,9 +1491,10 @@ __global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, con
                                                   const double *__restrict__ ev, const double *__restrict__ qkv,
                                                   const double *__restrict__ pY, const double *__restrict__ pfc,
                                                   const double *__restrict__ palpha, const double *__restrict__ lnw,
-                                                  const double *__restrict__ lnb, double eps, double *__restrict__ n1,
-                                                  double *__restrict__ n1hat, double *__restrict__ n1is,
-                                                  double *__restrict__ act, double *__restrict__ aev) {
+                                                  const double *__restrict__ lnb, double eps, int lnmode,
+                                                  double *__restrict__ n1, double *__restrict__ n1hat,
+                                                  double *__restrict__ n1is, double *__restrict__ act,
+                                                  double *__restrict__ aev) {
   const int lane = threadIdx.x & 63;
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -1465,8 +1525,8 @@ __global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, con
   // of it (the MLP input), with the whole node row in this wavefront
   const std::size_t i = std::size_t(n) * kF;
   double y0, y1, h0, h1, is;
-  wave_layer_norm_pair(x[i + c0] + acc0, x[i + c1] + acc1, lnw[c0], lnw[c1], lnb[c0], lnb[c1], eps, y0, y1, h0, h1,
-                       is);
+  wave_layer_norm_pair(x[i + c0] + acc0, x[i + c1] + acc1, lnw[c0], lnw[c1], lnb[c0], lnb[c1], eps, lnmode, y0, y1,
+                       h0, h1, is);
   n1[i + c0] = y0;
   n1[i + c1] = y1;
   n1hat[i + c0] = h0;
@@ -1479,21 +1539,21 @@ __global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, con
 
 // LayerNorm over 128 channels held two per lane: channels lane and 64 + lane.
 __device__ __forceinline__ void wave_layer_norm(double v0, double v1, const double *w, const double *b,
-                                                double eps, int lane, double &y0, double &y1,
+                                                double eps, int mode, int lane, double &y0, double &y1,
                                                 double &h0, double &h1, double &is) {
-  wave_layer_norm_pair(v0, v1, w[lane], w[64 + lane], b[lane], b[64 + lane], eps, y0, y1, h0, h1, is);
+  wave_layer_norm_pair(v0, v1, w[lane], w[64 + lane], b[lane], b[64 + lane], eps, mode, y0, y1, h0, h1, is);
 }
 
 // LN1 of the attention residual, and silu of it for the MLP input
 __global__ __launch_bounds__(256) void k_post1(int N, const double *ainv, const double *w, const double *b,
-                                               double eps, double *n1, double *n1hat, double *n1is,
+                                               double eps, int mode, double *n1, double *n1hat, double *n1is,
                                                double *act) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const std::size_t i = std::size_t(n) * kF;
   double y0, y1, h0, h1, is;
-  wave_layer_norm(ainv[i + lane], ainv[i + 64 + lane], w, b, eps, lane, y0, y1, h0, h1, is);
+  wave_layer_norm(ainv[i + lane], ainv[i + 64 + lane], w, b, eps, mode, lane, y0, y1, h0, h1, is);
   n1[i + lane] = y0; n1[i + 64 + lane] = y1;
   n1hat[i + lane] = h0; n1hat[i + 64 + lane] = h1;
   if (lane == 0) n1is[n] = is;
@@ -1515,6 +1575,7 @@ struct NodeChainArgs {
   const double *m1p, *m1bp, *m2p, *m2bp, *intp, *intbp;  // MFMA operand order
   const double *int_cg, *ln2w, *ln2b, *exp2_256;
   double eps;
+  int mode2;  // NormMode of the second position (RMSNorm, none: w = 1, b = 0 given)
 };
 // Two wavefronts per 16 atoms (four per block: two 16-atom tiles), so that a
 // 24k-atom system fills the chip: half h of a tile computes the output tiles
@@ -1652,7 +1713,7 @@ __global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restric
   sum += __shfl_xor(sum, 32, kWave);
   stat[tile][h][0][lane] = sum;
   __syncthreads();
-  const double mean = (stat[tile][0][0][lane] + stat[tile][1][0][lane]) / kF;
+  const double mean = A.mode2 == 0 ? (stat[tile][0][0][lane] + stat[tile][1][0][lane]) / kF : 0.0;
   double var = 0.0;
 #pragma unroll
   for (int q = 0; q < 4; ++q)
@@ -1665,7 +1726,7 @@ __global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restric
   var += __shfl_xor(var, 32, kWave);
   stat[tile][h][1][lane] = var;
   __syncthreads();
-  const double is = 1.0 / sqrt((stat[tile][0][1][lane] + stat[tile][1][1][lane]) / kF + A.eps);
+  const double is = A.mode2 == 2 ? 1.0 : 1.0 / sqrt((stat[tile][0][1][lane] + stat[tile][1][1][lane]) / kF + A.eps);
   if (valid) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -1704,6 +1765,7 @@ __global__ __launch_bounds__(256) void k_node_fwd(int N, const double *__restric
 struct NodeChainBwdArgs {
   const double *inttp, *m2tp, *m1tp;  // MFMA operand order (transposes)
   const double *int_cg, *ln1w, *ln2w;
+  int mode1, mode2;  // NormMode of the two positions: RMSNorm drops the mean term, none both
 };
 // Two wavefronts per 16 atoms (four per block: two 16-atom tiles): half h
 // owns the feature tiles 4 h .. 4 h + 3 of every 128-wide adjoint (and the
@@ -1799,8 +1861,8 @@ __global__ __launch_bounds__(256) void k_node_bwd(int N, const double *__restric
         // LayerNorm 2 reverse; the adjoint of p and t[0:128] into LDS
         double tm, tx;
         row_sums(mg, mgx, tm, tx);
-        tm /= kF;
-        tx /= kF;
+        tm = A.mode2 == 0 ? tm / kF : 0.0;
+        tx = A.mode2 == 2 ? 0.0 : tx / kF;
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) {
 #pragma unroll
@@ -1882,8 +1944,8 @@ __global__ __launch_bounds__(256) void k_node_bwd(int N, const double *__restric
     }
   double tm, tx;
   row_sums(m1, m1x, tm, tx);
-  tm /= kF;
-  tx /= kF;
+  tm = A.mode1 == 0 ? tm / kF : 0.0;
+  tx = A.mode1 == 2 ? 0.0 : tx / kF;
   if (valid) {
     // tile-transposed channel order (fpos): channels 16 T + g + 4 r, r = 0..3,
     // of this lane are one 32-byte vector at 16 T + 4 g
@@ -1905,27 +1967,38 @@ __global__ __launch_bounds__(256) void k_node_bwd(int N, const double *__restric
 struct HeadArgs {
   const double *ew2, *qw2, *escale, *eshift, *qemb, *hqemb, *hvshift, *hkey_bwd, *hkey_c;
   double eb2, qb2;
+  const double *ckey_bwd, *ckey_c, *cvshift;  // C6 ratio head (null: none); its hidden units at 320
+  int ho;                                     // head activation row width (320, or 384 with the C6 head)
 };
 
 // energy, raw charge, Hirshfeld key and ratio (kokkos_output_heads.cpp:137-176,341-451)
+// (and, with the C6 head, its logit and ratio: the same form as Hirshfeld's,
+// kokkos_output_heads.cpp:108-180)
 __global__ __launch_bounds__(256) void k_heads(int N, const int *z, const double *act, HeadArgs H,
-                                               double *eatom, double *qraw, double *heff, double *hir) {
+                                               double *eatom, double *qraw, double *heff, double *hir,
+                                               double *c6eff, double *c6r) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
-  const double *a = act + std::size_t(n) * 320;
+  const double *a = act + std::size_t(n) * H.ho;
   const int zz = z[n];
   const double e = wave_sum(H.ew2[lane] * a[lane] + H.ew2[64 + lane] * a[64 + lane]);
   const double q = wave_sum(H.qw2[lane] * a[128 + lane] + H.qw2[64 + lane] * a[192 + lane]);
   // Hirshfeld logit q_emb[z] . (W2 a + b2), contracted through the element's
   // row u[z] = W2^T q_emb[z]
   const double qk = H.hkey_c[zz] + wave_sum(H.hkey_bwd[zz * kHH + lane] * a[256 + lane]);
+  const double ck = H.ckey_bwd ? H.ckey_c[zz] + wave_sum(H.ckey_bwd[zz * kHH + lane] * a[320 + lane]) : 0.0;
   if (lane == 0) {
     eatom[n] = (e + H.eb2) * H.escale[zz - 1] + H.eshift[zz - 1];
     qraw[n] = q + H.qb2 + H.qemb[zz];
     const double ef = H.hvshift[zz] + qk / 8.0;  // sqrt(64)
     heff[n] = ef;
     hir[n] = fabs(ef);
+    if (H.ckey_bwd) {
+      const double ce = H.cvshift[zz] + ck / 8.0;
+      c6eff[n] = ce;
+      c6r[n] = fabs(ce);
+    }
   }
 }
 
@@ -1949,14 +2022,15 @@ __global__ __launch_bounds__(1024) void k_image_center(const std::int64_t *img_o
 }
 
 // seeds -> d/d(x_final): energy 1, charge (dE/dq - mean), Hirshfeld dE/dh
+// (and dE/dc of the C6 head into its hidden units)
 __global__ __launch_bounds__(256) void k_heads_bwd(int N, const int *z, const double *pre, const double *qseed,
-                                                   const double *dh, const double *heff, HeadArgs H,
-                                                   double *ghead) {
+                                                   const double *dh, const double *heff, const double *dc,
+                                                   const double *c6eff, HeadArgs H, double *ghead) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
-  const double *pr = pre + std::size_t(n) * 320;
-  double *g = ghead + std::size_t(n) * 320;
+  const double *pr = pre + std::size_t(n) * H.ho;
+  double *g = ghead + std::size_t(n) * H.ho;
   const int zz = z[n];
   const double sc = H.escale[zz - 1];
   g[lane] = sc * H.ew2[lane] * silu_prime(pr[lane]);
@@ -1969,25 +2043,31 @@ __global__ __launch_bounds__(256) void k_heads_bwd(int N, const int *z, const do
   const double hs = dh[n] * sg / 8.0;
   // ghh[i] = sum_j hw2[j][i] gk[j] with gk[j] = hs * hqemb[z][j] = hs * u[z][i]
   g[256 + lane] = hs * H.hkey_bwd[zz * kHH + lane] * silu_prime(pr[256 + lane]);
+  if (H.ckey_bwd) {
+    const double ce = c6eff[n];
+    const double cs = dc[n] * (ce > 0.0 ? 1.0 : (ce < 0.0 ? -1.0 : 0.0)) / 8.0;
+    g[320 + lane] = cs * H.ckey_bwd[zz * kHH + lane] * silu_prime(pr[320 + lane]);
+  }
 }
 
 // ---------------------------------------------------------------- long range
 // Node-major over the LR incidence: every lane takes one pair of node n.
 // d = x_n - x_other; F_n = -dE/dr d/r; half of every pair energy and of its
-// virial goes to each endpoint.
-template <bool LEAN_ERF>
+// virial goes to each endpoint.  SEP: the C6 ratios c6r of the model's C6
+// head set C6 (dE/dc into dcv).
+template <bool LEAN_ERF, bool SEP>
 __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int *inc, const int *rows,
                                             const int *nodes, const double *x, const int *z,
-                                            const double *q, const double *hir, LrParams P,
+                                            const double *q, const double *hir, const double *c6r, LrParams P,
                                             const double *aref, const double *cref, double *elr,
-                                            double *dq, double *dhv, double *flr, double *vlr,
+                                            double *dq, double *dhv, double *dcv, double *flr, double *vlr,
                                             double *parts) {
   const int lane = threadIdx.x & 63;
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int zn = z[n];
-  const double qn = q[n], hn = hir[n];
-  double e_el = 0, e_d = 0, sdq = 0, sdh = 0, f0 = 0, f1 = 0, f2 = 0;
+  const double qn = q[n], hn = hir[n], cn = SEP ? c6r[n] : 0.0;
+  double e_el = 0, e_d = 0, sdq = 0, sdh = 0, sdc = 0, f0 = 0, f1 = 0, f2 = 0;
   double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
   for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
     const int e = inc[k];
@@ -2000,11 +2080,14 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
     const double r = sqrt(dx * dx + dy * dy + dz * dz);
     const int o = nodes[2 * c + 1 - side];
     LrPairTerms t;
-    if (!lr_pair_terms<LEAN_ERF>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
+    if (!lr_pair_terms<LEAN_ERF, SEP>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t, cn,
+                                      SEP ? c6r[o] : 0.0))
+      continue;
     e_el += 0.5 * t.e_el;
     e_d += 0.5 * t.e_disp;
     sdq += t.pref * q[o];
     sdh += t.dh_self;
+    if constexpr (SEP) sdc += t.dc_self;
     const double s = t.radial / r;
     f0 -= s * dx; f1 -= s * dy; f2 -= s * dz;
     // W = -sum_pairs d (x) f_pair, f_pair = radial d / r; half per endpoint
@@ -2012,6 +2095,7 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
     w3 -= 0.5 * s * dx * dy; w4 -= 0.5 * s * dx * dz; w5 -= 0.5 * s * dy * dz;
   }
   e_el = wave_sum(e_el); e_d = wave_sum(e_d); sdq = wave_sum(sdq); sdh = wave_sum(sdh);
+  if constexpr (SEP) sdc = wave_sum(sdc);
   f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2);
   w0 = wave_sum(w0); w1 = wave_sum(w1); w2 = wave_sum(w2);
   w3 = wave_sum(w3); w4 = wave_sum(w4); w5 = wave_sum(w5);
@@ -2019,6 +2103,7 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
     elr[n] = e_el + e_d;
     dq[n] = sdq;
     dhv[n] = sdh;
+    if constexpr (SEP) dcv[n] = sdc;
     flr[3 * n] = f0; flr[3 * n + 1] = f1; flr[3 * n + 2] = f2;
     double *v = vlr + 6 * std::size_t(n);
     v[0] = w0; v[1] = w1; v[2] = w2; v[3] = w3; v[4] = w4; v[5] = w5;
@@ -2029,19 +2114,20 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
 
 // LR over the full node-major list of the device reneighbor: entry j * 32 +
 // image code, neighbour position x_j + shift(code) * box.
-template <bool LEAN_ERF>
+template <bool LEAN_ERF, bool SEP>
 __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, const int *inc, const double *x,
                                                  double lx, double ly, double lz, const int *z, const double *q,
-                                                 const double *hir, LrParams P, const double *aref,
-                                                 const double *cref, double *elr, double *dq, double *dhv,
-                                                 double *flr, double *vlr, double *parts) {
+                                                 const double *hir, const double *c6r, LrParams P,
+                                                 const double *aref, const double *cref, double *elr, double *dq,
+                                                 double *dhv, double *dcv, double *flr, double *vlr,
+                                                 double *parts) {
   const int lane = threadIdx.x & 63;
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int zn = z[n];
-  const double qn = q[n], hn = hir[n];
+  const double qn = q[n], hn = hir[n], cn = SEP ? c6r[n] : 0.0;
   const double xn = x[3 * n], yn = x[3 * n + 1], zn_ = x[3 * n + 2];
-  double e_el = 0, e_d = 0, sdq = 0, sdh = 0, f0 = 0, f1 = 0, f2 = 0;
+  double e_el = 0, e_d = 0, sdq = 0, sdh = 0, sdc = 0, f0 = 0, f1 = 0, f2 = 0;
   double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
   for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
     const int e = inc[k];
@@ -2051,17 +2137,21 @@ __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, cons
     const double dz = zn_ - x[3 * o + 2] - (code % 3 - 1) * lz;
     const double r = sqrt(dx * dx + dy * dy + dz * dz);
     LrPairTerms t;
-    if (!lr_pair_terms<LEAN_ERF>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t)) continue;
+    if (!lr_pair_terms<LEAN_ERF, SEP>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t, cn,
+                                      SEP ? c6r[o] : 0.0))
+      continue;
     e_el += 0.5 * t.e_el;
     e_d += 0.5 * t.e_disp;
     sdq += t.pref * q[o];
     sdh += t.dh_self;
+    if constexpr (SEP) sdc += t.dc_self;
     const double s = t.radial / r;
     f0 -= s * dx; f1 -= s * dy; f2 -= s * dz;
     w0 -= 0.5 * s * dx * dx; w1 -= 0.5 * s * dy * dy; w2 -= 0.5 * s * dz * dz;
     w3 -= 0.5 * s * dx * dy; w4 -= 0.5 * s * dx * dz; w5 -= 0.5 * s * dy * dz;
   }
   e_el = wave_sum(e_el); e_d = wave_sum(e_d); sdq = wave_sum(sdq); sdh = wave_sum(sdh);
+  if constexpr (SEP) sdc = wave_sum(sdc);
   f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2);
   w0 = wave_sum(w0); w1 = wave_sum(w1); w2 = wave_sum(w2);
   w3 = wave_sum(w3); w4 = wave_sum(w4); w5 = wave_sum(w5);
@@ -2069,6 +2159,7 @@ __global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, cons
     elr[n] = e_el + e_d;
     dq[n] = sdq;
     dhv[n] = sdh;
+    if constexpr (SEP) dcv[n] = sdc;
     flr[3 * n] = f0; flr[3 * n + 1] = f1; flr[3 * n + 2] = f2;
     double *v = vlr + 6 * std::size_t(n);
     v[0] = w0; v[1] = w1; v[2] = w2; v[3] = w3; v[4] = w4; v[5] = w5;
@@ -2579,6 +2670,14 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   rc_ = a.sr_cutoff;
   avg_ = a.attention_norm;
   ln_eps_ = a.ln_eps;
+  norm1_ = int(a.norm1);
+  norm2_ = int(a.norm2);
+  qk_norm_ = a.qk_norm;
+  c6_ = a.c6_head;
+  if (a.residual_scalars) {
+    resid_ = m.f64("model.resid_lambdas", {std::size_t(a.layers)});
+    x0l_ = m.f64("model.x0_lambdas", {std::size_t(a.layers)});
+  }
   auto up = [&](const std::vector<double> &v) -> const double * {
     void *p = nullptr;
     HIP_CHECK(hipMalloc(&p, v.size() * sizeof(double)));
@@ -2667,10 +2766,14 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     }
     B.att_cg = up(m.f64(at + "so3_conv_invariants.cg_rep", {24}));
     B.int_cg = up(m.f64(p + "interaction_block.so3_conv_invariants.cg_rep", {24}));
-    B.ln1w = up(m.f64(p + "layer_norm_inv_1.weight", {F}));
-    B.ln1b = up(m.f64(p + "layer_norm_inv_1.bias", {F}));
-    B.ln2w = up(m.f64(p + "layer_norm_inv_2.weight", {F}));
-    B.ln2b = up(m.f64(p + "layer_norm_inv_2.bias", {F}));
+    // an affine LayerNorm has parameters; RMSNorm and no normalisation run
+    // the same kernels with w = 1, b = 0
+    const std::vector<double> ones(F, 1.0), zeros(F, 0.0);
+    const bool ln1 = a.norm1 == NormMode::Layer, ln2 = a.norm2 == NormMode::Layer;
+    B.ln1w = up(ln1 ? m.f64(p + "layer_norm_inv_1.weight", {F}) : ones);
+    B.ln1b = up(ln1 ? m.f64(p + "layer_norm_inv_1.bias", {F}) : zeros);
+    B.ln2w = up(ln2 ? m.f64(p + "layer_norm_inv_2.weight", {F}) : ones);
+    B.ln2b = up(ln2 ? m.f64(p + "layer_norm_inv_2.bias", {F}) : zeros);
     const auto m1 = m.f64(p + "mlp_1.1.weight", {F, F}), m2 = m.f64(p + "mlp_1.3.weight", {F, F});
     B.m1w = up(m1); B.m1t = up(transpose(m1, F, F));
     B.m2w = up(m2); B.m2t = up(transpose(m2, F, F));
@@ -2690,22 +2793,32 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   {
     const std::string e = "model.atomic_energy_output_block.", q = "model.partial_charges_output_block.",
                       h = "model.hirshfeld_output_block.";
+    const std::string c6h = "model.c6_ratios_output_block.";
+    const std::size_t HH = kHH;
     std::vector<double> w1 = m.f64(e + "layers.0.weight", {F, F});
     const auto qw1 = m.f64(q + "transform_inv_features.0.weight", {F, F});
-    const auto hw1 = m.f64(h + "transform_features.0.weight", {std::size_t(kHH), F});
+    const auto hw1 = m.f64(h + "transform_features.0.weight", {HH, F});
     w1.insert(w1.end(), qw1.begin(), qw1.end());
     w1.insert(w1.end(), hw1.begin(), hw1.end());
-    hw_.w1 = up(w1);
-    hw_.w1t = up(transpose(w1, 320, F));
-    hw_.w1p = up(permute_mfma(w1, 320, F));
-    hw_.w1tp = up(permute_mfma(transpose(w1, 320, F), F, 320));
     std::vector<double> b1 = m.f64(e + "layers.0.bias", {F});
     const auto qb1 = m.f64(q + "transform_inv_features.0.bias", {F});
-    const auto hb1 = m.f64(h + "transform_features.0.bias", {std::size_t(kHH)});
+    const auto hb1 = m.f64(h + "transform_features.0.bias", {HH});
     b1.insert(b1.end(), qb1.begin(), qb1.end());
     b1.insert(b1.end(), hb1.begin(), hb1.end());
+    if (c6_) {  // the C6 head's first layer: 64 more hidden units at 320
+      const auto cw1 = m.f64(c6h + "transform_features.0.weight", {HH, F});
+      const auto cb1 = m.f64(c6h + "transform_features.0.bias", {HH});
+      w1.insert(w1.end(), cw1.begin(), cw1.end());
+      b1.insert(b1.end(), cb1.begin(), cb1.end());
+    }
+    const int HO = c6_ ? 384 : 320;
+    hw_.ho = HO;
+    hw_.w1 = up(w1);
+    hw_.w1t = up(transpose(w1, HO, F));
+    hw_.w1p = up(permute_mfma(w1, HO, F));
+    hw_.w1tp = up(permute_mfma(transpose(w1, HO, F), F, HO));
     hw_.b1 = up(b1);
-    hw_.b1p = up(bias_acc(b1, 320));
+    hw_.b1p = up(bias_acc(b1, HO));
     hw_.ew2 = up(m.f64(e + "final_layer.weight", {1, F}));
     hw_.eb2 = m.f64(e + "final_layer.bias", {1})[0];
     hw_.escale = up(m.f64(e + "energy_scales.weight", {1, 118}));
@@ -2713,27 +2826,31 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     hw_.qw2 = up(m.f64(q + "transform_inv_features.2.weight", {1, F}));
     hw_.qb2 = m.f64(q + "transform_inv_features.2.bias", {1})[0];
     hw_.qemb = up(m.f64(q + "atomic_embedding.weight", {100, 1}));
-    const auto hw2 = m.f64(h + "transform_features.2.weight", {std::size_t(kHH), std::size_t(kHH)});
-    const auto hqemb = m.f64(h + "q_embedding.weight", {100, std::size_t(kHH)});
-    hw_.hqemb = up(hqemb);
-    // reverse of the key layer seeded by the element's query: u[z][i] =
-    // sum_j W2[j][i] q_emb[z][j] depends on the element only
-    std::vector<double> u(100 * std::size_t(kHH), 0.0);
-    for (int zz = 0; zz < 100; ++zz)
-      for (int i = 0; i < kHH; ++i) {
-        double acc = 0.0;
-        for (int j = 0; j < kHH; ++j) acc += hw2[std::size_t(j) * kHH + i] * hqemb[std::size_t(zz) * kHH + j];
-        u[std::size_t(zz) * kHH + i] = acc;
+    // reverse of a ratio head's key layer seeded by the element's query:
+    // u[z][i] = sum_j W2[j][i] q_emb[z][j] depends on the element only, and
+    // the logit q_emb[z] . (W2 a + b2) = u[z] . a + q_emb[z] . b2, so the key
+    // vector itself is never needed
+    auto ratio_head = [&](const std::string &pre, const double *&kbwd, const double *&kc, const double *&vsh) {
+      const auto w2 = m.f64(pre + "transform_features.2.weight", {HH, HH});
+      const auto qe = m.f64(pre + "q_embedding.weight", {100, HH});
+      const auto b2 = m.f64(pre + "transform_features.2.bias", {HH});
+      std::vector<double> u(100 * HH, 0.0), c(100, 0.0);
+      for (std::size_t zz = 0; zz < 100; ++zz) {
+        for (std::size_t i = 0; i < HH; ++i) {
+          double acc = 0.0;
+          for (std::size_t j = 0; j < HH; ++j) acc += w2[j * HH + i] * qe[zz * HH + j];
+          u[zz * HH + i] = acc;
+        }
+        for (std::size_t j = 0; j < HH; ++j) c[zz] += qe[zz * HH + j] * b2[j];
       }
-    hw_.hkey_bwd = up(u);
-    // the Hirshfeld logit q_emb[z] . (W2 a + b2) = u[z] . a + q_emb[z] . b2:
-    // the key vector itself is never needed
-    const auto hb2 = m.f64(h + "transform_features.2.bias", {std::size_t(kHH)});
-    std::vector<double> hc(100, 0.0);
-    for (int zz = 0; zz < 100; ++zz)
-      for (int j = 0; j < kHH; ++j) hc[zz] += hqemb[std::size_t(zz) * kHH + j] * hb2[j];
-    hw_.hkey_c = up(hc);
-    hw_.hvshift = up(m.f64(h + "v_shift_embedding.weight", {100, 1}));
+      kbwd = up(u);
+      kc = up(c);
+      vsh = up(m.f64(pre + "v_shift_embedding.weight", {100, 1}));
+      return qe;
+    };
+    hw_.hqemb = up(ratio_head(h, hw_.hkey_bwd, hw_.hkey_c, hw_.hvshift));
+    hw_.ckey_bwd = hw_.ckey_c = hw_.cvshift = nullptr;
+    if (c6_) ratio_head(c6h, hw_.ckey_bwd, hw_.ckey_c, hw_.cvshift);
     const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
     const auto kk = m.i64("model.radial_embedding.radial_basis_fn.k", {R});
     const auto kr = m.i64("model.radial_embedding.radial_basis_fn.k_rev", {R});
@@ -2756,6 +2873,14 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   zbl_.ke = a.zbl_ke; zbl_.rc = a.sr_cutoff; zbl_.switch_off = a.zbl_switch_off;
   zbl_.p = a.zbl_p; zbl_.d = a.zbl_d;
   for (int k = 0; k < 4; ++k) { zbl_.a[k] = a.zbl_a[k]; zbl_.c[k] = a.zbl_c[k]; }
+  zbl_.nlh_a = zbl_.nlh_b = nullptr;
+  zbl_.nlh_cap = 0;
+  if (a.nlh) {
+    const auto &ta = m.tensor("physical.nlh_a");
+    zbl_.nlh_a = up(m.f64("physical.nlh_a", ta.shape));
+    zbl_.nlh_b = up(m.f64("physical.nlh_b", ta.shape));
+    zbl_.nlh_cap = int(ta.shape[0]);
+  }
   lr_.ke = a.lr_ke; lr_.sigma = a.lr_sigma; lr_.cutoff = a.lr_cutoff; lr_.cuton_el = a.lr_cuton_el;
   lr_.fine_factor = std::pow(a.lr_fine, -4.0 / 21.0);
   lr_.bohr = a.lr_bohr; lr_.hartree = a.lr_hartree; lr_.disp_scale = a.lr_disp_scale;
@@ -2783,6 +2908,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   vlr_ = buf("vlr"); elr_parts_ = buf("elr_parts"); ezbl_ = buf("ezbl"); gx_ = buf("gx");
   gev_ = buf("gev"); gainv_ = buf("gainv"); gaev_ = buf("gaev"); gqkv_ = buf("gqkv");
   ghead_ = buf("ghead"); fout_ = buf("fout"); etot_ = buf("etot"); red_ = buf("red");
+  qkis_ = buf("qkis"); c6eff_ = buf("c6eff"); c6r_ = buf("c6r"); dc_ = buf("dc");
   owner_ = buf("owner"); sr_rows_ = buf("sr_rows"); sr_nodes_ = buf("sr_nodes");
   sr_inc_off_ = buf("sr_inc_off"); sr_inc_ = buf("sr_inc"); lr_rows_ = buf("lr_rows");
   lr_nodes_ = buf("lr_nodes"); lr_inc_off_ = buf("lr_inc_off"); lr_inc_ = buf("lr_inc");
@@ -2947,6 +3073,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const std::size_t Pa = std::size_t(PA);
   // --- buffers (retained capacity; all allocation happens before any work
   // is enqueued, so the sequence below can be captured into a graph) ---
+  const std::size_t HO = std::size_t(hw_.ho);
+  double *qkis = nullptr, *c6eff = nullptr, *c6r = nullptr, *dc = nullptr;
   double *xs = nullptr;
   double *evs = nullptr;
   double *qkv = nullptr;
@@ -3017,8 +3145,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     pre2hat = take<double>(pre2hat_, L * Nz * kF);
     pre2is = take<double>(pre2is_, L * Nz);
     ainv = take<double>(ainv_, Nz * kF);
-    act = take<double>(act_, Nz * 320); // MLP input (128 wide) and head activations (320)
-    hhead = take<double>(hhead_, Nz * 320);
+    act = take<double>(act_, Nz * HO); // MLP input (128 wide) and head activations (HO)
+    hhead = take<double>(hhead_, Nz * HO);
     heff = take<double>(heff_, Nz);
     eatom = take<double>(eatom_, Nz);
     qraw = take<double>(qraw_, Nz);
@@ -3037,7 +3165,11 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     gainv = take<double>(gainv_, Nz * kF);
     gaev = take<double>(gaev_, Nz * kE);
     gqkv = take<double>(gqkv_, Nz * 640);
-    ghead = take<double>(ghead_, Nz * 320);
+    ghead = take<double>(ghead_, Nz * HO);
+    qkis = qk_norm_ ? take<double>(qkis_, L * Nz * 16) : nullptr;
+    c6eff = c6_ ? take<double>(c6eff_, Nz) : nullptr;
+    c6r = c6_ ? take<double>(c6r_, Nz) : nullptr;
+    dc = c6_ ? take<double>(dc_, Nz) : nullptr;
     fo = f_out ? f_out : take<double>(fout_, Nz * 3);
     etot = eatom_out ? eatom_out : take<double>(etot_, Nz);
     red = take<double>(red_, 16);
@@ -3131,6 +3263,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     return;                                                                                                   \
   }
     SO3LR_GEMM(0, 20, 8, SO3LR_MG8) SO3LR_GEMM(1, 8, 20, 4)
+    SO3LR_GEMM(0, 24, 8, SO3LR_MG8) SO3LR_GEMM(1, 8, 24, 4)  // with the C6 head (384 hidden units)
 #undef SO3LR_GEMM
     throw std::logic_error("SO3LR: internal error, no node GEMM for this shape");
   };
@@ -3165,6 +3298,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                        pa, iact, iother);
   fill(dr, Pa);
   HIP_CHECK(hipMemcpyAsync(xs, x0, Nz * kF * sizeof(double), hipMemcpyDeviceToDevice, s));
+  const unsigned gNF = unsigned((Nz * kF + 255) / 256);
+  // residual scalars: block b's input is resid[b] x + x0[b] x0, x the block
+  // below's output (block 0: the embedding itself)
+  if (!resid_.empty()) hipLaunchKernelGGL(k_axpby, dim3(gNF), dim3(256), 0, s, Nz * kF, resid_[0], xs, x0l_[0], x0);
   fill(evs, Nz * kE);
   const double inv_avg = 1.0 / avg_;
   const unsigned gP = unsigned(PA);
@@ -3187,6 +3324,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
+    if (qk_norm_)
+      hipLaunchKernelGGL(k_qk_norm, dim3(unsigned(ceil_div(16 * N, 256))), dim3(256), 0, s, int(N), qb,
+                         qkis + b * Nz * 16);
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     // the MFMA filter also forms the attention logits of both directions
     // from the filter tiles it holds; the scalar cross-check path leaves them
@@ -3209,46 +3349,50 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                            pfb, pY, pfc, inv_avg, pab, ainv, aevb);
       else
         hipLaunchKernelGGL(k_attn_msg, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb, pY,
-                           pfc, pab, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb, n1ib, act, aevb);
+                           pfc, pab, B.ln1w, B.ln1b, ln_eps_, norm1_, n1b, n1hb, n1ib, act, aevb);
     });
     if (naive_filters_)  // the MFMA path's k_attn_msg has done LayerNorm 1 already
-      hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, n1b, n1hb,
-                         n1ib, act);
+      hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, norm1_, n1b,
+                         n1hb, n1ib, act);
     // the post-attention node chain in one kernel (MLP, interaction, LayerNorm 2, ev gate)
     const NodeChainArgs NC{B.m1p, B.m1bp, B.m2p, B.m2bp, B.intp, B.intbp, B.int_cg, B.ln2w, B.ln2b, hw_.exp2_256,
-                           ln_eps_};
+                           ln_eps_, norm2_};
     hipLaunchKernelGGL(k_node_fwd, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), act, n1b, aevb, NC, hpb, tb,
                        xs + (b + 1) * Nz * kF, evs + (b + 1) * Nz * kE, p2h, p2i);
+    if (!resid_.empty() && b + 1 < L)
+      hipLaunchKernelGGL(k_axpby, dim3(gNF), dim3(256), 0, s, Nz * kF, resid_[b + 1], xs + (b + 1) * Nz * kF,
+                         x0l_[b + 1], x0);
   }
 
   // --- heads, charge correction, long range ---
   HeadArgs H{hw_.ew2, hw_.qw2, hw_.escale, hw_.eshift, hw_.qemb, hw_.hqemb, hw_.hvshift,
-             hw_.hkey_bwd, hw_.hkey_c, hw_.eb2, hw_.qb2};
+             hw_.hkey_bwd, hw_.hkey_c, hw_.eb2, hw_.qb2, hw_.ckey_bwd, hw_.ckey_c, hw_.cvshift, hw_.ho};
   const double *xf = xs + L * Nz * kF;
-  gemm(1, int(N), kF, 320, xf, kF, hw_.w1p, hw_.b1p, hhead, 320, hact);
-  hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, heff, hir);
+  gemm(1, int(N), kF, int(HO), xf, kF, hw_.w1p, hw_.b1p, hhead, int(HO), hact);
+  hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, heff, hir, c6eff, c6r);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
   // erf(r / sigma) by the polynomial of erf_lean when r / sigma stays within [0, 3]
   const bool lean_erf = lr_.cutoff * lr_.inv_sigma <= 3.0;
   timed("long_range", 1, [&] {
-#define SO3LR_LR(FULL, LEAN)                                                                                          \
+#define SO3LR_LR(FULL, LEAN, SEP)                                                                                     \
   if (FULL)                                                                                                          \
-    hipLaunchKernelGGL(k_lr_full<LEAN>, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, x, box_len_[0],          \
-                       box_len_[1], box_len_[2], z, q, hir, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr,   \
-                       parts);                                                                                       \
+    hipLaunchKernelGGL((k_lr_full<LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, x, box_len_[0],   \
+                       box_len_[1], box_len_[2], z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc,    \
+                       flr, vlr, parts);                                                                             \
   else                                                                                                               \
-    hipLaunchKernelGGL(k_lr<LEAN>, dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x, z, q,   \
-                       hir, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, flr, vlr, parts);
-    if (lean_erf) {
-      SO3LR_LR(shift_mode_, true)
+    hipLaunchKernelGGL((k_lr<LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x,  \
+                       z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc, flr, vlr, parts);
+    if (c6_) {
+      if (lean_erf) { SO3LR_LR(shift_mode_, true, true) } else { SO3LR_LR(shift_mode_, false, true) }
     } else {
-      SO3LR_LR(shift_mode_, false)
+      if (lean_erf) { SO3LR_LR(shift_mode_, true, false) } else { SO3LR_LR(shift_mode_, false, false) }
     }
 #undef SO3LR_LR
   });
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
-  hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, H, ghead);
-  gemm(0, int(N), 320, kF, ghead, 320, hw_.w1tp, nullptr, gx, kF, nullptr);
+  hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, dc, c6eff, H,
+                     ghead);
+  gemm(0, int(N), int(HO), kF, ghead, int(HO), hw_.w1tp, nullptr, gx, kF, nullptr);
   fill(gev, Nz * kE);
 
   // --- interaction blocks, reverse ---
@@ -3268,7 +3412,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     // the post-attention node chain in reverse in one kernel: gainv, gaev
-    const NodeChainBwdArgs NB{B.inttp, B.m2tp, B.m1tp, B.int_cg, B.ln1w, B.ln2w};
+    const NodeChainBwdArgs NB{B.inttp, B.m2tp, B.m1tp, B.int_cg, B.ln1w, B.ln2w, norm1_, norm2_};
     hipLaunchKernelGGL(k_node_bwd, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), gx, gev, tb, aevb, p2h,
                        p2i, hpb, n1b, n1hb, n1ib, NB, gainv, gaev);
     if (naive_filters_) {
@@ -3316,7 +3460,12 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     // the adjoints of a block's inputs x_b, ev_b feed the block below; block
     // 0's inputs (the embedding and ev = 0) do not depend on the positions
     if (b > 0) {
+      if (qk_norm_)  // through the QK normalisation to the raw projections
+        hipLaunchKernelGGL(k_qk_norm_bwd, dim3(unsigned(ceil_div(16 * N, 256))), dim3(256), 0, s, int(N), qb,
+                           qkis + b * Nz * 16, gqkv);
       hipLaunchKernelGGL(k_qkv_bwd_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), gqkv, B.qkvtp, gainv, gx);
+      // residual scalars: the adjoint of the block below's output
+      if (!resid_.empty()) hipLaunchKernelGGL(k_scale, dim3(gNF), dim3(256), 0, s, Nz * kF, resid_[b], gx);
       hipLaunchKernelGGL(k_ev_bwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, evb, B.att_cg, ds,
                          gaev, gev);
     }

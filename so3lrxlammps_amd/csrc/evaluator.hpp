@@ -65,8 +65,9 @@ struct BlockWeights {
 };
 
 struct HeadWeights {
-  const double *w1p, *w1tp;  // MFMA operand order: (320 x 128) and its transpose
-  const double *b1p;         // first-layer bias (320) in accumulator order
+  int ho = 320;              // first-layer width: energy 128 | charge 128 | Hirshfeld 64 (| C6 64)
+  const double *w1p, *w1tp;  // MFMA operand order: (ho x 128) and its transpose
+  const double *b1p;         // first-layer bias (ho) in accumulator order
   const double *w1t;    // (128, 320): energy | charge | Hirshfeld first layers, transposed
   const double *w1;     // (320, 128)
   const double *b1;     // (320)
@@ -77,6 +78,7 @@ struct HeadWeights {
   const double *hkey_bwd;         // (100, 64): u[z][i] = sum_j hw2[j][i] hqemb[z][j]
   const double *hkey_c;           // (100): hqemb[z] . hb2
   const double *hqemb, *hvshift;  // (100, 64), (100)
+  const double *ckey_bwd, *ckey_c, *cvshift;  // the C6 ratio head's, as hkey_bwd, hkey_c, hvshift (or null)
   const double *rbf_b, *rbf_k, *rbf_kr;  // (32) each
   const double *exp2_256;                // 2^(j/256), j < 256 (lean e^x of the filter kernels)
   const double *alpha_ref, *c6_ref;
@@ -146,6 +148,10 @@ class Evaluator {
   LrParams lr_{};
   double gamma_ = 0, rc_ = 0, avg_ = 1, ln_eps_ = 1e-6;
   int layers_ = 0;
+  // architecture options (Architecture in model.hpp)
+  int norm1_ = 0, norm2_ = 0;   // NormMode of the two normalisation positions
+  bool qk_norm_ = false, c6_ = false;
+  std::vector<double> resid_, x0l_;  // residual scalars per block (empty: none)
   ChargeSpin charge_spin_;
   std::vector<double> emb_w_;  // (128, 118)
 
@@ -207,6 +213,7 @@ class Evaluator {
   Buffer *hhead_, *heff_, *eatom_, *qraw_, *q_, *hir_, *qseed_;
   Buffer *elr_, *dq_, *dh_, *flr_, *vlr_, *elr_parts_, *ezbl_;
   Buffer *gx_, *gev_, *gainv_, *gaev_, *gqkv_, *ghead_;
+  Buffer *qkis_, *c6eff_, *c6r_, *dc_;  // QK normalisation 1/rms; C6 head logit, ratio, dE/dratio
   Buffer *fout_, *etot_, *red_, *red_part_;
   // pair-sized buffers
   Buffer *owner_, *sr_rows_, *sr_nodes_, *sr_inc_off_, *sr_inc_, *lr_rows_, *lr_nodes_,

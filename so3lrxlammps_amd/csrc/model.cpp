@@ -414,6 +414,10 @@ std::string Architecture::summary() const {
   std::ostringstream o;
   o << "layers=" << layers << " features=" << kF << " heads=" << kHeads << "x" << kHW
     << " degrees=[1,2,3,4] rbf=" << kR << " r_cut=" << sr_cutoff << " r_cut_lr=" << lr_cutoff;
+  static const char *norms[3] = {"layer", "rms", "none"};
+  o << " norm=" << norms[int(norm1)] << "/" << norms[int(norm2)] << " attention_norm=" << attention_norm
+    << " repulsion=" << (nlh ? "nlh" : "zbl") << (qk_norm ? " qk_norm" : "")
+    << (residual_scalars ? " residual_scalars" : "") << (c6_head ? " c6_head" : "");
   return o.str();
 }
 
@@ -592,21 +596,42 @@ void Model::describe_and_negotiate(const std::string &origin) {
   need(a.at("attention_heads").uint() == 4 && a.at("attention_head_width").uint() == 32, "attention heads other than 4 x 32");
   need(a.at("euclidean_degree_channels").uint() == 4, "euclidean_degree_channels != 4");
   need(a.at("radial_basis_features").uint() == std::uint64_t(kR), "radial_basis_features != 32");
-  need(!flag("use_rms_norm", false), "RMSNorm (use_rms_norm)");
-  need(!flag("qk_norm", false), "QK normalisation (qk_norm)");
-  need(!flag("use_residual_scalars", false), "residual scalars (use_residual_scalars)");
-  need(flag("layer_normalization_1", true) && flag("layer_normalization_2", true), "disabled LayerNorm positions");
+  // normalisation: one module choice for both positions, each position
+  // switchable; the reference's post-attention block requires the first
+  // (kokkos_post_attention_block0.cpp:386-390)
+  const NormMode enabled = flag("use_rms_norm", false) ? NormMode::Rms : NormMode::Layer;
+  arch_.norm1 = flag("layer_normalization_1", true) ? enabled : NormMode::None;
+  arch_.norm2 = flag("layer_normalization_2", true) ? enabled : NormMode::None;
+  need(arch_.norm1 != NormMode::None, "no normalisation at the first position (layer_normalization_1 = false)");
+  arch_.qk_norm = flag("qk_norm", false);
+  arch_.residual_scalars = flag("use_residual_scalars", false);
   need(flag("residual_mlp_1", true) && !flag("residual_mlp_2", false), "residual MLP layout other than mlp_1 only");
   if (const Json *q = a.find("qk_nonlinearity")) need(q->string() == "identity", "QK nonlinearity other than identity");
-  if (const Json *r = a.find("repulsion_type")) need(r->string() == "zbl_learned", "repulsion other than learned ZBL");
-  else need(a.find("zbl_enabled") && a.at("zbl_enabled").number() == 1.0, "missing ZBL repulsion");
+  // repulsion: explicit repulsion_type, else zbl_enabled (so3lr_architecture.cpp:356-368)
+  if (const Json *r = a.find("repulsion_type")) {
+    need(r->string() == "zbl_learned" || r->string() == "nlh", "repulsion other than learned ZBL or NLH tables");
+    arch_.nlh = r->string() == "nlh";
+  } else {
+    need(a.find("zbl_enabled") && a.at("zbl_enabled").number() == 1.0, "missing ZBL repulsion");
+  }
   if (const Json *zc = a.find("zbl_cutoff_function")) need(zc->string() == "phys", "ZBL cutoff function other than phys");
-  if (const Json *mn = a.find("message_normalization")) need(mn->string() == "avg_num_neighbors", "message normalisation other than avg_num_neighbors");
+  // attention normalisation (so3lr_architecture.cpp:126-156, 340-355)
+  std::string norm_kind = "avg_num_neighbors";
+  if (const Json *mn = a.find("message_normalization")) norm_kind = mn->string();
+  need(norm_kind == "identity" || norm_kind == "sqrt_num_features" || norm_kind == "avg_num_neighbors",
+       "message normalisation '" + norm_kind + "'");
+  need(norm_kind != "avg_num_neighbors" || a.find("avg_num_neighbors") != nullptr,
+       "message normalisation avg_num_neighbors without an avg_num_neighbors value");
+  // heads: energy, charges, Hirshfeld ratios, optionally the C6 ratios
+  // (kokkos_output_heads.cpp:271-283)
   const Json &heads = a.at("output_heads");
-  need(heads.arr.size() == 3 && heads.arr[0].string() == "atomic_energy_output_block" &&
+  const bool three = heads.arr.size() == 3;
+  const bool four = heads.arr.size() == 4 && heads.arr[3].string() == "c6_ratios_output_block";
+  need((three || four) && heads.arr[0].string() == "atomic_energy_output_block" &&
            heads.arr[1].string() == "partial_charges_output_block" &&
            heads.arr[2].string() == "hirshfeld_output_block",
-       "output heads other than energy, partial charges and Hirshfeld ratios");
+       "output heads other than energy, partial charges, Hirshfeld ratios and optionally C6 ratios");
+  arch_.c6_head = four;
   if (misses.empty()) {
     // degree layout {3,5,7,9} in every block
     for (int b = 0; b < arch_.layers; ++b) {
@@ -626,22 +651,92 @@ void Model::describe_and_negotiate(const std::string &origin) {
   arch_.sr_cutoff = num("short_range_cutoff_angstrom");
   arch_.lr_cutoff = num("long_range_cutoff_angstrom");
   arch_.embedding_scale = num("embedding_scale");
-  arch_.attention_norm = num("avg_num_neighbors");
+  if (norm_kind == "identity") arch_.attention_norm = 1.0;
+  else if (norm_kind == "sqrt_num_features") arch_.attention_norm = std::sqrt(double(kHW));
+  else arch_.attention_norm = num("avg_num_neighbors");
+  if (!(arch_.attention_norm > 0) || !std::isfinite(arch_.attention_norm)) fail("attention normalisation must be positive");
   if (!(arch_.sr_cutoff > 0) || !(arch_.lr_cutoff >= arch_.sr_cutoff)) fail("invalid native model cutoffs");
   if (!(arch_.embedding_scale > 0) || !std::isfinite(arch_.embedding_scale)) fail("embedding scale must be positive");
   arch_.gamma = f64("model.radial_embedding.radial_basis_fn.gamma", {})[0];
+  // the repulsion prefactor and switch are shared by both kinds; the
+  // screening parameters are learned ZBL's (so3lr_repulsion_setup.cpp:9-34)
   arch_.zbl_ke = num("zbl_ke");
   arch_.zbl_switch_off = num("zbl_switch_off_angstrom");
-  arch_.zbl_p = num("zbl_p");
-  arch_.zbl_d = num("zbl_d");
-  double csum = 0;
-  for (int k = 0; k < 4; ++k) {
-    arch_.zbl_a[k] = num(("zbl_a" + std::to_string(k + 1)).c_str());
-    arch_.zbl_c[k] = num(("zbl_c" + std::to_string(k + 1)).c_str());
-    if (!(arch_.zbl_a[k] > 0) || !(arch_.zbl_c[k] > 0)) fail("invalid ZBL parameter");
-    csum += arch_.zbl_c[k];
+  if (!(arch_.zbl_ke > 0) || !(arch_.zbl_switch_off > 0)) fail("invalid repulsion prefactor or switch");
+  if (arch_.nlh) {
+    const Tensor &ta = tensor("physical.nlh_a");
+    const std::size_t cap = ta.shape.empty() ? 0 : ta.shape[0];
+    if (cap == 0 || cap > 118 || ta.shape != std::vector<std::size_t>({cap, cap, 3}) ||
+        tensor("physical.nlh_b").shape != ta.shape || ta.dtype != "float64" || tensor("physical.nlh_b").dtype != "float64")
+      fail("NLH repulsion tables physical.nlh_a / physical.nlh_b must be float64 (cap, cap, 3)");
+  } else {
+    arch_.zbl_p = num("zbl_p");
+    arch_.zbl_d = num("zbl_d");
+    double csum = 0;
+    for (int k = 0; k < 4; ++k) {
+      arch_.zbl_a[k] = num(("zbl_a" + std::to_string(k + 1)).c_str());
+      arch_.zbl_c[k] = num(("zbl_c" + std::to_string(k + 1)).c_str());
+      if (!(arch_.zbl_a[k] > 0) || !(arch_.zbl_c[k] > 0)) fail("invalid ZBL parameter");
+      csum += arch_.zbl_c[k];
+    }
+    if (std::abs(csum - 1.0) > 2e-12) fail("normalized ZBL coefficients changed");
   }
-  if (std::abs(csum - 1.0) > 2e-12) fail("normalized ZBL coefficients changed");
+  // The filter kernels evaluate SiLU through a table-based e^x whose argument
+  // reduction is exact for |x| < 2800.  The radial hidden layer sees
+  // W0 rbf + b0 with every Bernstein value in [0, 1], and the node MLP sees
+  // W1 silu(n1) + b1 with |n1_k| <= sqrt(F) |w_k| + |b_k| after either
+  // normalisation: both are bounded by the weights, checked here.
+  {
+    double worst = 0.0;
+    const double sf = std::sqrt(double(kF));
+    for (int b = 0; b < arch_.layers; ++b) {
+      const std::string p = "model.euclidean_transformers." + std::to_string(b) + ".";
+      for (const char *fn : {"filter_net_inv.", "filter_net_ev."}) {
+        const auto w0 = f64(p + fn + "mlp_rbf.0.weight", {std::size_t(kF), std::size_t(kR)});
+        const auto b0 = f64(p + fn + "mlp_rbf.0.bias", {std::size_t(kF)});
+        for (int c = 0; c < kF; ++c) {
+          double acc = std::abs(b0[c]);
+          for (int k = 0; k < kR; ++k) acc += std::abs(w0[std::size_t(c) * kR + k]);
+          worst = std::max(worst, acc);
+        }
+      }
+      std::vector<double> lnw(kF, 1.0), lnb(kF, 0.0);
+      if (arch_.norm1 == NormMode::Layer) {
+        lnw = f64(p + "layer_norm_inv_1.weight", {std::size_t(kF)});
+        lnb = f64(p + "layer_norm_inv_1.bias", {std::size_t(kF)});
+      }
+      const auto w1 = f64(p + "mlp_1.1.weight", {std::size_t(kF), std::size_t(kF)});
+      const auto b1 = f64(p + "mlp_1.1.bias", {std::size_t(kF)});
+      for (int c = 0; c < kF; ++c) {
+        double acc = std::abs(b1[c]);
+        for (int k = 0; k < kF; ++k)
+          acc += std::abs(w1[std::size_t(c) * kF + k]) * (sf * std::abs(lnw[k]) + std::abs(lnb[k]));
+        worst = std::max(worst, acc);
+      }
+    }
+    if (!(worst < 2000.0))
+      fail("weights allow SiLU arguments up to " + std::to_string(worst) +
+           " in the filter or node MLP hidden layers; this build's activations take |x| < 2000");
+  }
+  if (arch_.c6_head) {
+    // a ratio head of the Hirshfeld head's widths (kokkos_output_heads.cpp:108-132;
+    // the kernels here take hidden and key width 64)
+    const std::string c = "model.c6_ratios_output_block.";
+    const std::size_t HH = kHH, F = kF;
+    const std::pair<const char *, std::vector<std::size_t>> parts[] = {
+        {"transform_features.0.weight", {HH, F}}, {"transform_features.0.bias", {HH}},
+        {"transform_features.2.weight", {HH, HH}}, {"transform_features.2.bias", {HH}},
+        {"q_embedding.weight", {100, HH}},       {"v_shift_embedding.weight", {100, 1}}};
+    for (const auto &pt : parts)
+      if (tensor(c + pt.first).dtype != "float64" || tensor(c + pt.first).shape != pt.second)
+        fail("C6 ratio head tensor " + c + pt.first + " is not float64 of the Hirshfeld head's shape");
+  }
+  if (arch_.residual_scalars) {
+    const std::vector<std::size_t> shp{std::size_t(arch_.layers)};
+    for (const char *k : {"model.resid_lambdas", "model.x0_lambdas"})
+      if (tensor(k).dtype != "float64" || tensor(k).shape != shp)
+        fail(std::string("residual scalars ") + k + " must be float64 of length interaction_blocks");
+  }
   arch_.lr_ke = num("lr_electrostatic_ke");
   arch_.lr_sigma = num("lr_electrostatic_sigma");
   arch_.lr_cuton_el = num("lr_electrostatic_cuton_angstrom");

@@ -62,12 +62,24 @@ constexpr int kFH = 32;   // spherical filter hidden width F / 4
 constexpr int kHH = 64;   // Hirshfeld head width
 constexpr int kMaxBlocks = 8;
 
+// Normalisation at the two positions of the post-attention block
+// (src/so3lr_architecture.cpp:376-392): affine LayerNorm, RMSNorm without
+// scale, or none (the second position only).
+enum class NormMode : int { Layer = 0, Rms = 1, None = 2 };
+
 struct Architecture {
   int layers = 0;
-  double sr_cutoff = 0, lr_cutoff = 0, embedding_scale = 1, attention_norm = 1;
+  double sr_cutoff = 0, lr_cutoff = 0, embedding_scale = 1;
+  double attention_norm = 1;  // divisor of the attention logits (message_normalization)
   double ln_eps = 1e-6;
   double gamma = 0;
-  // ZBL
+  // options; the defaults are the v1 model
+  NormMode norm1 = NormMode::Layer, norm2 = NormMode::Layer;
+  bool qk_norm = false;           // RMS-normalised q, k, q_ev, k_ev head rows
+  bool residual_scalars = false;  // block input = resid[b] x + x0[b] x_embedding
+  bool nlh = false;               // NLH pair-table repulsion instead of learned ZBL
+  bool c6_head = false;           // C6 ratio head feeding the dispersion C6
+  // repulsion (ZBL screening parameters: learned ZBL only)
   double zbl_ke = 0, zbl_switch_off = 0, zbl_p = 0, zbl_d = 0, zbl_a[4] = {}, zbl_c[4] = {};
   // long range
   double lr_ke = 0, lr_sigma = 0, lr_cuton_el = 0, lr_fine = 0, lr_bohr = 0, lr_hartree = 0,

@@ -36,6 +36,135 @@ def perturbed_model(path, seed=11, scale=0.2):
     return str(path)
 
 
+def variant_model(path, blocks=None, rms_norm=False, norm2=True, qk_norm=False, resid=None, x0=None,
+                  nlh=None, c6=None, message_normalization=None, edit=None, seed=5, base=MODEL):
+    """A model file with the reference's optional operators switched on
+    (so3lr_architecture.cpp:300-392), written from the shipped model:
+
+    blocks: interaction block count (new blocks copy block b % 3 with weights
+      scaled by 1 + 0.2 u, u uniform in [-1, 1]);
+    rms_norm: RMSNorm without scale at the enabled positions (the LayerNorm
+      tensors are dropped: RMSNorm has none); norm2=False: no second norm;
+    qk_norm: RMS-normalised q, k, q_ev, k_ev head rows;
+    resid, x0: residual scalars per block (model.resid_lambdas, x0_lambdas);
+    nlh: (a, b) NLH tables of shape (cap, cap, 3) (physical.nlh_a, nlh_b);
+      the learned-ZBL screening keys are removed;
+    c6: "copy" (the C6 head is the Hirshfeld head), "perturb" (a copy with
+      weights scaled by 1 + 0.2 u) or a dict of its six tensors by suffix;
+    message_normalization: "identity", "sqrt_num_features" or
+      "avg_num_neighbors";
+    edit: called as edit(manifest, arrays) last, for anything else.
+    Records are re-sorted by name, sizes and digests recomputed on writing."""
+    from so3lrxlammps_amd.model_file import read_model, write_model
+    manifest, arrays = read_model(base)
+    arch = manifest["architecture"]
+    rng = np.random.default_rng(seed)
+    recs = {r["state_key"]: r for r in manifest["tensors"]}
+
+    def add(key, a, role="parameter"):
+        a = np.asarray(a, dtype=np.float64)
+        arrays[key] = a
+        recs[key] = {"dtype": "float64", "name": "wrapper.model." + key, "nbytes": 0, "offset": 0,
+                     "role": role, "sha256": "", "shape": list(a.shape), "state_key": key}
+
+    def drop(key):
+        recs.pop(key)
+        arrays.pop(key)
+
+    def perturbed(a):
+        return a * (1.0 + 0.2 * rng.uniform(-1.0, 1.0, a.shape))
+
+    L0 = int(arch["interaction_blocks"])
+    if blocks is not None and blocks != L0:
+        prefix = "model.euclidean_transformers.%d."
+        for b in range(blocks, L0):
+            for k in [k for k in recs if k.startswith(prefix % b)]:
+                drop(k)
+        for b in range(L0, blocks):
+            src = prefix % (b % L0)
+            for k in [k for k in list(recs) if k.startswith(src)]:
+                r = dict(recs[k])
+                nk = (prefix % b) + k[len(src):]
+                r["state_key"] = nk
+                r["name"] = r["name"].replace(src, prefix % b)
+                a = arrays[k]
+                if r["role"] == "parameter" and r["dtype"] == "float64":
+                    a = perturbed(a)
+                arrays[nk] = a
+                recs[nk] = r
+        arch["interaction_blocks"] = blocks
+    L = int(arch["interaction_blocks"])
+    if rms_norm:
+        arch["use_rms_norm"] = True
+        for b in range(L):
+            for pos in (1, 2):
+                for w in ("weight", "bias"):
+                    drop("model.euclidean_transformers.%d.layer_norm_inv_%d.%s" % (b, pos, w))
+    if not norm2:
+        arch["layer_normalization_2"] = False
+        for b in range(L):
+            for w in ("weight", "bias"):
+                k = "model.euclidean_transformers.%d.layer_norm_inv_2.%s" % (b, w)
+                if k in recs:
+                    drop(k)
+    if qk_norm:
+        arch["qk_norm"] = True
+    if resid is not None:
+        arch["use_residual_scalars"] = True
+        add("model.resid_lambdas", np.asarray(resid, dtype=np.float64))
+        add("model.x0_lambdas", np.asarray(x0 if x0 is not None else np.zeros(L), dtype=np.float64))
+    if nlh is not None:
+        arch["repulsion_type"] = "nlh"
+        for k in ("zbl_p", "zbl_d", "zbl_a1", "zbl_a2", "zbl_a3", "zbl_a4", "zbl_c1", "zbl_c2", "zbl_c3",
+                  "zbl_c4", "zbl_enabled"):
+            arch.pop(k, None)
+        add("physical.nlh_a", nlh[0], role="physical_constant")
+        add("physical.nlh_b", nlh[1], role="physical_constant")
+    if c6 is not None:
+        arch["output_heads"] = list(arch["output_heads"]) + ["c6_ratios_output_block"]
+        for suffix in ("q_embedding.weight", "transform_features.0.weight", "transform_features.0.bias",
+                       "transform_features.2.weight", "transform_features.2.bias", "v_shift_embedding.weight"):
+            h = arrays["model.hirshfeld_output_block." + suffix]
+            if isinstance(c6, dict):
+                a = c6[suffix]
+            else:
+                a = h.copy() if c6 == "copy" else perturbed(h)
+            add("model.c6_ratios_output_block." + suffix, a)
+    if message_normalization is not None:
+        arch["message_normalization"] = message_normalization
+    if edit is not None:
+        edit(manifest, arrays)
+    manifest["tensors"] = sorted(recs.values(), key=lambda r: r["name"])
+    arch["state_tensor_count"] = len(manifest["tensors"])
+    arch["parameter_elements"] = int(sum(np.asarray(arrays[r["state_key"]]).size for r in manifest["tensors"]
+                                         if r["role"] == "parameter"))
+    write_model(str(path), manifest, arrays)
+    return str(path)
+
+
+def zbl_as_nlh(arch, cap=20, terms=(0, 1, 2), garbage_lower=True, seed=3):
+    """NLH tables (cap, cap, 3) holding, for every pair (za <= zb), the learned
+    ZBL screening terms `terms` (amplitude c_k, rate a_k (za^p + zb^p) d;
+    kokkos_physical_zbl.cpp:163-172), zero in unused slots; the unused lower
+    triangle (za > zb) holds large random values, so a transposed lookup
+    shows."""
+    a = np.zeros((cap, cap, 3))
+    b = np.zeros((cap, cap, 3))
+    rng = np.random.default_rng(seed)
+    if garbage_lower:
+        lo = np.tril_indices(cap, -1)
+        a[lo] = rng.uniform(5, 50, (len(lo[0]), 3))
+        b[lo] = rng.uniform(0.1, 1, (len(lo[0]), 3))
+    p, d = arch["zbl_p"], arch["zbl_d"]
+    for za in range(1, cap + 1):
+        for zb in range(za, cap + 1):
+            rate = (za ** p + zb ** p) * d
+            for slot, k in enumerate(terms):
+                a[za - 1, zb - 1, slot] = arch["zbl_c%d" % (k + 1)]
+                b[za - 1, zb - 1, slot] = arch["zbl_a%d" % (k + 1)] * rate
+    return a, b
+
+
 SYMBOLS = ["", "H", "He", "Li", "Be", "B", "C", "N", "O", "F", "Ne", "Na", "Mg", "Al",
            "Si", "P", "S", "Cl", "Ar", "K", "Ca"]
 

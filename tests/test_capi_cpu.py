@@ -123,17 +123,26 @@ def test_missing_file_rejected():
 
 
 @pytest.mark.parametrize("key,value,feature", [
-    ("use_rms_norm", True, "RMSNorm"),
-    ("qk_norm", True, "QK normalisation"),
     ("invariant_features", 256, "invariant_features"),
     ("interaction_blocks", 9, "interaction_blocks"),
     ("brand_new_operator", 1, "unknown architecture key"),
-    ("repulsion_type", "nlh", "repulsion other than learned ZBL"),
-    ("use_residual_scalars", True, "residual scalars"),
+    ("repulsion_type", "none", "repulsion other than"),
     ("radial_basis_features", 64, "radial_basis_features"),
     ("output_heads", ["atomic_energy_output_block", "partial_charges_output_block", "hirshfeld_output_block",
-                      "c6_ratios_output_block"], "output heads other than"),
+                      "dipole_vec_output_block"], "output heads other than"),
     ("layer_norm_epsilon", 1e-5, "LayerNorm epsilon"),
+    # refused by the reference's post-attention block as well
+    # (kokkos_post_attention_block0.cpp:386-390)
+    ("layer_normalization_1", False, "first position"),
+    ("residual_mlp_2", True, "residual MLP layout"),
+    ("message_normalization", "sum", "message normalisation"),
+    ("qk_nonlinearity", "silu", "QK nonlinearity"),
+    # accepted options whose tensors the mutated manifest lacks: the load
+    # names the missing tensor
+    ("repulsion_type", "nlh", "physical.nlh_a"),
+    ("use_residual_scalars", True, "model.resid_lambdas"),
+    ("output_heads", ["atomic_energy_output_block", "partial_charges_output_block", "hirshfeld_output_block",
+                      "c6_ratios_output_block"], "c6_ratios_output_block"),
 ])
 def test_capability_refusal_names_the_feature(tmp_path, key, value, feature):
     """Structurally valid mutated models (re-serialised manifest, recomputed
@@ -143,6 +152,30 @@ def test_capability_refusal_names_the_feature(tmp_path, key, value, feature):
     rc, msg = _create(_rewrite(tmp_path, mutate_manifest=mutate))
     assert rc == _lib.ERR_MODEL, msg
     assert feature in msg, msg
+
+
+def test_weights_beyond_the_activation_range_are_refused(tmp_path):
+    """A radial filter weight large enough to take a SiLU argument past the
+    table exponential's range is refused at load, not evaluated wrongly."""
+    def big(manifest, arrays):
+        arrays["model.euclidean_transformers.1.filter_net_ev.mlp_rbf.0.weight"][3, 5] = 5000.0
+    path = support.variant_model(tmp_path / "big.so3lr", edit=big)
+    rc, msg = _create(path)
+    assert rc == _lib.ERR_MODEL and "SiLU arguments" in msg, msg
+
+
+@pytest.mark.parametrize("key,value", [
+    ("use_rms_norm", True), ("qk_norm", True), ("layer_normalization_2", False),
+    ("message_normalization", "identity"), ("message_normalization", "sqrt_num_features"),
+])
+def test_architecture_options_are_accepted(tmp_path, key, value):
+    """Options the reference runs and this build implements load (up to the
+    device step on a machine without a GPU); RMSNorm needs no tensors, so the
+    shipped LayerNorm parameters are simply not read."""
+    def mutate(m):
+        m["architecture"][key] = value
+    rc, msg = _create(_rewrite(tmp_path, mutate_manifest=mutate))
+    assert rc in (_lib.OK, _lib.ERR_DEVICE), msg
 
 
 def test_lammps_lists_match_brute_force():

@@ -43,6 +43,10 @@ def _hip_single_point(ctx, z, pos, box, charge, mult):
 
 
 def _check(out, e, f, ea, w, terms, ftol=1e-9):
+    # the achieved margins, printed so the logs show them against the bars
+    print("  |dE|/|E| %.2e  max|dF| %.2e eV/A  max|dW| %.2e eV (max|W| %.2e)" % (
+        abs(e - out["energy"]) / abs(out["energy"]), np.abs(f - out["forces"]).max(),
+        np.abs(w - out["virial"]).max(), np.abs(out["virial"]).max()), flush=True)
     assert abs(e - out["energy"]) <= 1e-10 * abs(out["energy"]), (e, out["energy"])
     assert np.abs(f - out["forces"]).max() <= ftol
     wscale = max(1.0, np.abs(out["virial"]).max())
