@@ -19,6 +19,7 @@
 #include <cstring>
 #include <mutex>
 #include <stdexcept>
+#include <type_traits>
 #include <utility>
 
 namespace so3lr_amd {
@@ -485,6 +486,7 @@ struct FilterMfma {
   const double *e0pk[2];                                // spherical layer 0: one v4d per lane {tile 0, tile 1, 0, 0}
   const double *att_cg;
   const double *rbf_b, *rbf_k, *rbf_kr;
+  const double *rbf_e;     // Bernstein factors: e^{b_c} (c < 4), e^{b_c - b_{c-4}} (c >= 4)
   const double *exp2_256;  // 2^(j/256), j < 256
   double gamma;
 };
@@ -612,43 +614,58 @@ __device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
 // first equivariant channel of degree slot h (l = h + 1): 0, 3, 8, 15
 __device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
 
-// The same basis and, in db, d rbf / dr at those channels (zero where the
-// clamp of x is active): rbf (-gamma k + gamma k' x / (1 - x)).
-__device__ __forceinline__ void rbf8_with_grad(double r, int g, const FilterMfma &A, const double *tab, v4d *rb,
-                                               v4d *db) {
-  const double gr = -A.gamma * r;
-  double x = exp_tab(gr, tab), lx = gr;
-  bool clamped = false;
-  if (x < 1e-6) { x = 1e-6; lx = log(1e-6); clamped = true; }
-  if (x > 1.0 - 1e-6) { x = 1.0 - 1e-6; lx = log(1.0 - 1e-6); clamped = true; }
-  const double l1x = log(1.0 - x);
-  const double q = clamped ? 0.0 : A.gamma * x / (1.0 - x), gk = clamped ? 0.0 : -A.gamma;
+// Bernstein basis b_c(x) = e^{b_c} x^c (1 - x)^(31 - c), x = e^{-gamma r}
+// clamped to [1e-6, 1 - 1e-6] (kokkos_integrated_block0.cpp:117-160; the
+// exponents k_c = c, 31 - c are checked at load), at the lane's channels
+// c = g + 4 t, t < 8 (register t & 3 of tile t >> 2).  The first from powers
+// of x and y = 1 - x, each next one by the ratio b_{c+4} / b_c =
+// e^{b_{c+4} - b_c} (x / y)^4: no logarithm and one exponential (x itself)
+// per lane instead of eight.  rbf_e holds e^{b_c} for c < 4 and
+// e^{b_c - b_{c-4}} for c >= 4.  rho = x / y.
+__device__ __forceinline__ void bernstein8(double x, int g, const double *__restrict__ rbf_e, v4d *rb,
+                                           double &rho) {
+  const double y = 1.0 - x;
+  const double y2 = y * y, y4 = y2 * y2, y8 = y4 * y4;
+  const double y28 = (y8 * y8) * (y8 * y4);
+  const double x2 = x * x;
+  // x^g y^(3 - g)
+  const double lead = g == 0 ? y2 * y : (g == 1 ? x * y2 : (g == 2 ? x2 * y : x2 * x));
+  double v = rbf_e[g] * lead * y28;
+  rho = x * rcp_act(y);
+  const double r2 = rho * rho, r4 = r2 * r2;
+  rb[0][0] = v;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
-    const double k = A.rbf_k[ch], kr = A.rbf_kr[ch];
-    const double v = exp_tab(A.rbf_b[ch] + k * lx + kr * l1x, tab);
+  for (int t = 1; t < 8; ++t) {
+    v = v * r4 * rbf_e[g + 4 * t];
     rb[t >> 2][t & 3] = v;
-    db[t >> 2][t & 3] = v * (gk * k + kr * q);
   }
 }
 
-// Bernstein basis of pair distance r at channels 16 T + g + 4 v (T < 2, v < 4).
-__device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, const double *tab, v4d *rb,
-                                     double &xb) {
-  // x = e^{-gamma r} clamped to [1e-6, 1 - 1e-6]; ln x is -gamma r itself
-  // unless the clamp is active
-  const double gr = -A.gamma * r;
-  double x = exp_tab(gr, tab), lx = gr;
-  if (x < 1e-6) { x = 1e-6; lx = log(1e-6); }
-  if (x > 1.0 - 1e-6) { x = 1.0 - 1e-6; lx = log(1.0 - 1e-6); }
-  xb = x;
-  const double l1x = log(1.0 - x);
+// The basis and, in db, d b_c / dr at those channels (zero where the clamp of
+// x is active): b_c (-gamma c + gamma (31 - c) x / (1 - x)).
+__device__ __forceinline__ void rbf8_with_grad(double r, int g, const FilterMfma &A, const double *tab, v4d *rb,
+                                               v4d *db) {
+  double x = exp_tab(-A.gamma * r, tab);
+  bool clamped = false;
+  if (x < 1e-6) { x = 1e-6; clamped = true; }
+  if (x > 1.0 - 1e-6) { x = 1.0 - 1e-6; clamped = true; }
+  double rho;
+  bernstein8(x, g, A.rbf_e, rb, rho);
+  const double q = clamped ? 0.0 : A.gamma * rho, gk = clamped ? 0.0 : -A.gamma;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const int ch = 16 * (t >> 2) + g + 4 * (t & 3);
-    rb[t >> 2][t & 3] = exp_tab(A.rbf_b[ch] + A.rbf_k[ch] * lx + A.rbf_kr[ch] * l1x, tab);
+    const double k = double(g + 4 * t);
+    db[t >> 2][t & 3] = rb[t >> 2][t & 3] * (gk * k + (31.0 - k) * q);
   }
+}
+
+// The basis alone (forward filter).
+__device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, const double *tab, v4d *rb) {
+  double x = exp_tab(-A.gamma * r, tab);
+  if (x < 1e-6) x = 1e-6;
+  if (x > 1.0 - 1e-6) x = 1.0 - 1e-6;
+  double rho;
+  bernstein8(x, g, A.rbf_e, rb, rho);
 }
 
 // Both filters of one block for 16 pairs per wavefront, 4 wavefronts per block.
@@ -711,8 +728,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   st.prime();
 
   v4d rb[2];
-  double xb;
-  rbf8(pr[pp], g, A, exp2_lds, rb, xb);
+  rbf8(pr[pp], g, A, exp2_lds, rb);
   // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
   double sg = 0.0;
   if constexpr (!EV0) {
@@ -2051,41 +2067,93 @@ __global__ __launch_bounds__(256) void k_heads_bwd(int N, const int *z, const do
 }
 
 // ---------------------------------------------------------------- long range
-// Node-major over the LR incidence: every lane takes one pair of node n.
-// d = x_n - x_other; F_n = -dE/dr d/r; half of every pair energy and of its
-// virial goes to each endpoint.  SEP: the C6 ratios c6r of the model's C6
-// head set C6 (dE/dc into dcv).
-template <bool LEAN_ERF, bool SEP>
-__global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int *inc, const int *rows,
-                                            const int *nodes, const double *x, const int *z,
-                                            const double *q, const double *hir, const double *c6r, LrParams P,
-                                            const double *aref, const double *cref, double *elr,
-                                            double *dq, double *dhv, double *dcv, double *flr, double *vlr,
-                                            double *parts) {
-  const int lane = threadIdx.x & 63;
-  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
+// Node-major over the node's long-range entries (kokkos_physical_long_range.cpp:
+// 147-380, each pair seen from both endpoints): d = x_n - x_other; F_n =
+// -dE/dr d/r; half of every pair energy and of its virial goes to each
+// endpoint.  SEP: the C6 ratios c6r of the model's C6 head set C6 (dE/dc into
+// dcv).  The lists carry a skin (about a fifth of the entries lie beyond the
+// cutoff), so the wavefront first finds the entries inside it, 64 at a time,
+// queues them in LDS, and evaluates only full wavefronts of them (and one
+// partial at the end): the pair terms are the kernel's whole cost.
+// Src gives an entry's partner node and displacement:
+//   LrRows: LAMMPS half pairs through the incidence (entry = pair * 2 + side);
+//   LrImages: the device reneighbor's full list (entry = node * 32 + image code).
+struct LrRows {
+  const int *rows, *nodes;
+  const double *x;
+  __device__ __forceinline__ int other(int e) const { return nodes[2 * (e >> 1) + 1 - (e & 1)]; }
+  __device__ __forceinline__ void disp(int e, int, double &dx, double &dy, double &dz) const {
+    const int c = e >> 1;
+    const double sgn = (e & 1) == 0 ? 1.0 : -1.0;
+    const int ra = rows[2 * c], rb = rows[2 * c + 1];
+    dx = sgn * (x[3 * ra] - x[3 * rb]);
+    dy = sgn * (x[3 * ra + 1] - x[3 * rb + 1]);
+    dz = sgn * (x[3 * ra + 2] - x[3 * rb + 2]);
+  }
+};
+struct LrImages {
+  const double *x;
+  const double *shift;  // LDS: 27 x 4 image shifts (box multiples)
+  __device__ __forceinline__ int other(int e) const { return e >> 5; }
+  __device__ __forceinline__ void disp(int e, int n, double &dx, double &dy, double &dz) const {
+    const int o = e >> 5, code = e & 31;
+    const double *sh = shift + 4 * code;
+    dx = x[3 * n] - x[3 * o] - sh[0];
+    dy = x[3 * n + 1] - x[3 * o + 1] - sh[1];
+    dz = x[3 * n + 2] - x[3 * o + 2] - sh[2];
+  }
+};
+#ifndef SO3LR_LR_WAVES
+#define SO3LR_LR_WAVES 2
+#endif
+#define LR_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SO3LR_LR_WAVES)))
+template <class Src, bool LEAN_ERF, bool SEP>
+__global__ __launch_bounds__(256) LR_OCCUPANCY void k_lr(int N, const int *inc_off, const int *inc, Src S,
+                                                         double lx, double ly, double lz, const int *z,
+                                                         const double *q, const double *hir, const double *c6r,
+                                                         LrParams P, const double *aref, const double *cref,
+                                                         double *elr, double *dq, double *dhv, double *dcv,
+                                                         double *flr, double *vlr, double *parts) {
+  // per wavefront, up to 127 queued entries inside the cutoff: displacement,
+  // partner charge, Hirshfeld ratio, C6 ratio and element (all gathered in
+  // the scan, so the evaluation reads LDS only)
+  struct Queue {
+    double dx[128], dy[128], dz[128], qo[128], ho[128], co[SEP ? 128 : 1];
+    int zo[128];
+  };
+  __shared__ double shift[27 * 4];
+  __shared__ Queue queue[4];
+  if (threadIdx.x < 27) {  // the image shift of code c: ((c/9) - 1, (c/3)%3 - 1, c%3 - 1) box lengths
+    const int c = threadIdx.x;
+    shift[4 * c] = (c / 9 - 1) * lx;
+    shift[4 * c + 1] = ((c / 3) % 3 - 1) * ly;
+    shift[4 * c + 2] = (c % 3 - 1) * lz;
+    shift[4 * c + 3] = 0.0;
+  }
+  __syncthreads();
+  if constexpr (std::is_same<Src, LrImages>::value) S.shift = shift;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n = xcd_block() * 4 + wv;
   if (n >= N) return;
+  Queue &Q = queue[wv];
+  const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
   const int zn = z[n];
   const double qn = q[n], hn = hir[n], cn = SEP ? c6r[n] : 0.0;
+  // the cutoff test of lr_pair_terms, widened by a relative 1e-12 so that no
+  // entry it would evaluate is dropped here (it tests r < cutoff itself)
+  const double rc2 = P.cutoff * P.cutoff * (1.0 + 1e-12);
   double e_el = 0, e_d = 0, sdq = 0, sdh = 0, sdc = 0, f0 = 0, f1 = 0, f2 = 0;
   double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
-  for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
-    const int e = inc[k];
-    const int c = e >> 1, side = e & 1;
-    const int ra = rows[2 * c], rb = rows[2 * c + 1];
-    const double sgn = side == 0 ? 1.0 : -1.0;
-    const double dx = sgn * (x[3 * ra] - x[3 * rb]);
-    const double dy = sgn * (x[3 * ra + 1] - x[3 * rb + 1]);
-    const double dz = sgn * (x[3 * ra + 2] - x[3 * rb + 2]);
+  auto evaluate = [&](int i) {
+    const double dx = Q.dx[i], dy = Q.dy[i], dz = Q.dz[i], qo = Q.qo[i];
     const double r = sqrt(dx * dx + dy * dy + dz * dz);
-    const int o = nodes[2 * c + 1 - side];
     LrPairTerms t;
-    if (!lr_pair_terms<LEAN_ERF, SEP>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t, cn,
-                                      SEP ? c6r[o] : 0.0))
-      continue;
+    if (!lr_pair_terms<LEAN_ERF, SEP>(P, aref, cref, zn, Q.zo[i], qn, qo, hn, Q.ho[i], r, t, cn,
+                                      SEP ? Q.co[SEP ? i : 0] : 0.0))
+      return;
     e_el += 0.5 * t.e_el;
     e_d += 0.5 * t.e_disp;
-    sdq += t.pref * q[o];
+    sdq += t.pref * qo;
     sdh += t.dh_self;
     if constexpr (SEP) sdc += t.dc_self;
     const double s = t.radial / r;
@@ -2093,63 +2161,49 @@ __global__ __launch_bounds__(256) void k_lr(int N, const int *inc_off, const int
     // W = -sum_pairs d (x) f_pair, f_pair = radial d / r; half per endpoint
     w0 -= 0.5 * s * dx * dx; w1 -= 0.5 * s * dy * dy; w2 -= 0.5 * s * dz * dz;
     w3 -= 0.5 * s * dx * dy; w4 -= 0.5 * s * dx * dz; w5 -= 0.5 * s * dy * dz;
+  };
+  int pending = 0;  // queued entries, the same in every lane (< 64 between scans)
+  const int beg = inc_off[n], end = inc_off[n + 1];
+  for (int k0 = beg; k0 < end; k0 += kWave) {
+    const int k = k0 + lane;
+    bool in = false;
+    int e = 0;
+    double dx = 0, dy = 0, dz = 0;
+    if (k < end) {
+      e = inc[k];
+      S.disp(e, n, dx, dy, dz);
+      const double r2 = dx * dx + dy * dy + dz * dz;
+      in = r2 > 1e-24 && r2 < rc2;
+    }
+    const unsigned long long m = __ballot(in);
+    if (in) {
+      const int i = pending + __popcll(m & below);  // at most 126
+      const int o = S.other(e);
+      Q.dx[i] = dx; Q.dy[i] = dy; Q.dz[i] = dz;
+      Q.qo[i] = q[o]; Q.ho[i] = hir[o]; Q.zo[i] = z[o];
+      if constexpr (SEP) Q.co[i] = c6r[o];
+    }
+    pending += __popcll(m);
+    // the wavefront's LDS writes are complete before any lane reads them
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    if (pending >= kWave) {
+      evaluate(lane);
+      // move the overflow (pending - 64 < 64 entries) to the front
+      const int rest = pending - kWave;
+      const int src = kWave + (lane < rest ? lane : 0);
+      const double mx = Q.dx[src], my = Q.dy[src], mz = Q.dz[src], mq = Q.qo[src], mh = Q.ho[src];
+      const double mc = SEP ? Q.co[SEP ? src : 0] : 0.0;
+      const int mzo = Q.zo[src];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      if (lane < rest) {
+        Q.dx[lane] = mx; Q.dy[lane] = my; Q.dz[lane] = mz; Q.qo[lane] = mq; Q.ho[lane] = mh; Q.zo[lane] = mzo;
+        if constexpr (SEP) Q.co[lane] = mc;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      pending = rest;
+    }
   }
-  e_el = wave_sum(e_el); e_d = wave_sum(e_d); sdq = wave_sum(sdq); sdh = wave_sum(sdh);
-  if constexpr (SEP) sdc = wave_sum(sdc);
-  f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2);
-  w0 = wave_sum(w0); w1 = wave_sum(w1); w2 = wave_sum(w2);
-  w3 = wave_sum(w3); w4 = wave_sum(w4); w5 = wave_sum(w5);
-  if (lane == 0) {
-    elr[n] = e_el + e_d;
-    dq[n] = sdq;
-    dhv[n] = sdh;
-    if constexpr (SEP) dcv[n] = sdc;
-    flr[3 * n] = f0; flr[3 * n + 1] = f1; flr[3 * n + 2] = f2;
-    double *v = vlr + 6 * std::size_t(n);
-    v[0] = w0; v[1] = w1; v[2] = w2; v[3] = w3; v[4] = w4; v[5] = w5;
-    parts[2 * n] = e_el;
-    parts[2 * n + 1] = e_d;
-  }
-}
-
-// LR over the full node-major list of the device reneighbor: entry j * 32 +
-// image code, neighbour position x_j + shift(code) * box.
-template <bool LEAN_ERF, bool SEP>
-__global__ __launch_bounds__(256) void k_lr_full(int N, const int *inc_off, const int *inc, const double *x,
-                                                 double lx, double ly, double lz, const int *z, const double *q,
-                                                 const double *hir, const double *c6r, LrParams P,
-                                                 const double *aref, const double *cref, double *elr, double *dq,
-                                                 double *dhv, double *dcv, double *flr, double *vlr,
-                                                 double *parts) {
-  const int lane = threadIdx.x & 63;
-  const int n = xcd_block() * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  const int zn = z[n];
-  const double qn = q[n], hn = hir[n], cn = SEP ? c6r[n] : 0.0;
-  const double xn = x[3 * n], yn = x[3 * n + 1], zn_ = x[3 * n + 2];
-  double e_el = 0, e_d = 0, sdq = 0, sdh = 0, sdc = 0, f0 = 0, f1 = 0, f2 = 0;
-  double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
-  for (int k = inc_off[n] + lane; k < inc_off[n + 1]; k += kWave) {
-    const int e = inc[k];
-    const int o = e >> 5, code = e & 31;
-    const double dx = xn - x[3 * o] - (code / 9 - 1) * lx;
-    const double dy = yn - x[3 * o + 1] - ((code / 3) % 3 - 1) * ly;
-    const double dz = zn_ - x[3 * o + 2] - (code % 3 - 1) * lz;
-    const double r = sqrt(dx * dx + dy * dy + dz * dz);
-    LrPairTerms t;
-    if (!lr_pair_terms<LEAN_ERF, SEP>(P, aref, cref, zn, z[o], qn, q[o], hn, hir[o], r, t, cn,
-                                      SEP ? c6r[o] : 0.0))
-      continue;
-    e_el += 0.5 * t.e_el;
-    e_d += 0.5 * t.e_disp;
-    sdq += t.pref * q[o];
-    sdh += t.dh_self;
-    if constexpr (SEP) sdc += t.dc_self;
-    const double s = t.radial / r;
-    f0 -= s * dx; f1 -= s * dy; f2 -= s * dz;
-    w0 -= 0.5 * s * dx * dx; w1 -= 0.5 * s * dy * dy; w2 -= 0.5 * s * dz * dz;
-    w3 -= 0.5 * s * dx * dy; w4 -= 0.5 * s * dx * dz; w5 -= 0.5 * s * dy * dz;
-  }
+  if (lane < pending) evaluate(lane);
   e_el = wave_sum(e_el); e_d = wave_sum(e_d); sdq = wave_sum(sdq); sdh = wave_sum(sdh);
   if constexpr (SEP) sdc = wave_sum(sdc);
   f0 = wave_sum(f0); f1 = wave_sum(f1); f2 = wave_sum(f2);
@@ -2858,6 +2912,12 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     hw_.rbf_k = up(std::vector<double>(kk.begin(), kk.end()));
     hw_.rbf_kr = up(std::vector<double>(kr.begin(), kr.end()));
     {
+      std::vector<double> e(R);
+      for (std::size_t c = 0; c < R; ++c)
+        e[c] = double(std::exp(static_cast<long double>(bb[c]) - (c >= 4 ? static_cast<long double>(bb[c - 4]) : 0.0L)));
+      hw_.rbf_e = up(e);
+    }
+    {
       std::vector<double> t(256);
       for (int j = 0; j < 256; ++j) t[j] = double(std::exp2(static_cast<long double>(j) / 256.0L));
       hw_.exp2_256 = up(t);
@@ -3015,6 +3075,7 @@ FilterMfma filter_mfma(const BlockWeights &B, const HeadWeights &H, double gamma
     FM.ob1p0[k] = B.ob1p0[k];
   }
   FM.att_cg = B.att_cg; FM.rbf_b = H.rbf_b; FM.rbf_k = H.rbf_k; FM.rbf_kr = H.rbf_kr; FM.gamma = gamma;
+  FM.rbf_e = H.rbf_e;
   FM.exp2_256 = H.exp2_256;
   return FM;
 }
@@ -3376,12 +3437,13 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   timed("long_range", 1, [&] {
 #define SO3LR_LR(FULL, LEAN, SEP)                                                                                     \
   if (FULL)                                                                                                          \
-    hipLaunchKernelGGL((k_lr_full<LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, x, box_len_[0],   \
-                       box_len_[1], box_len_[2], z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc,    \
-                       flr, vlr, parts);                                                                             \
+    hipLaunchKernelGGL((k_lr<LrImages, LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc,              \
+                       LrImages{x, nullptr}, box_len_[0], box_len_[1], box_len_[2], z, q, hir, c6r, lr_,             \
+                       hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc, flr, vlr, parts);                                 \
   else                                                                                                               \
-    hipLaunchKernelGGL((k_lr<LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc, lr_rows, lr_nodes, x,  \
-                       z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc, flr, vlr, parts);
+    hipLaunchKernelGGL((k_lr<LrRows, LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc,                \
+                       LrRows{lr_rows, lr_nodes, x}, 0.0, 0.0, 0.0, z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref,  \
+                       elr, dq, dh, dc, flr, vlr, parts);
     if (c6_) {
       if (lean_erf) { SO3LR_LR(shift_mode_, true, true) } else { SO3LR_LR(shift_mode_, false, true) }
     } else {

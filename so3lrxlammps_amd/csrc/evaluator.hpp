@@ -80,6 +80,7 @@ struct HeadWeights {
   const double *hqemb, *hvshift;  // (100, 64), (100)
   const double *ckey_bwd, *ckey_c, *cvshift;  // the C6 ratio head's, as hkey_bwd, hkey_c, hvshift (or null)
   const double *rbf_b, *rbf_k, *rbf_kr;  // (32) each
+  const double *rbf_e;                   // (32) Bernstein recurrence factors (FilterMfma::rbf_e)
   const double *exp2_256;                // 2^(j/256), j < 256 (lean e^x of the filter kernels)
   const double *alpha_ref, *c6_ref;
   int n_ref;

@@ -718,6 +718,14 @@ void Model::describe_and_negotiate(const std::string &origin) {
       fail("weights allow SiLU arguments up to " + std::to_string(worst) +
            " in the filter or node MLP hidden layers; this build's activations take |x| < 2000");
   }
+  {
+    // the Bernstein exponents k = 0..R-1 and R-1-k (the filter kernels step
+    // the basis through them)
+    const auto k = i64("model.radial_embedding.radial_basis_fn.k", {std::size_t(kR)});
+    const auto kr = i64("model.radial_embedding.radial_basis_fn.k_rev", {std::size_t(kR)});
+    for (int c = 0; c < kR; ++c)
+      if (k[c] != c || kr[c] != kR - 1 - c) fail("Bernstein basis exponents other than k = 0..31, k_rev = 31 - k");
+  }
   if (arch_.c6_head) {
     // a ratio head of the Hirshfeld head's widths (kokkos_output_heads.cpp:108-132;
     // the kernels here take hidden and key width 64)
