@@ -696,15 +696,19 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 
   // Per filter the stream holds: the layer-0 bias tiles (8), the spherical
   // layer-0 bias tiles (2) and operand (1), W0 (16: tile s % 8, K chunk
-  // s / 8), then per output tile mt its bias, the 8 W1 chunks, the 2 E1
-  // chunks and the endpoint rows q_a, k_b, q_b, k_a of its channels (15
-  // each): 147 entries.  The output is built one tile at a time and stored as
+  // s / 8), then per output tile mt its bias, the endpoint rows q_a, k_b,
+  // q_b, k_a of its channels, the 8 W1 chunks and the 2 E1 chunks (15
+  // each): 147 entries.  The rows come first so that their loads (from L2,
+  // or HBM where a partner's row has left it) are issued a whole tile of
+  // MFMAs before the logits need them; q_a k_b and q_b k_a are multiplied as
+  // they arrive.  The output is built one tile at a time and stored as
   // soon as it is complete, so only one output accumulator is live; the
   // attention logits of both directions are reduced from it on the spot.
   // EV0 (block 0, ev = 0): the spherical branch sees s = 0 for every pair,
   // so it is the constant E1 silu(e0) + e1, folded into the output bias
   // (ob1p0); its entries are left out (13 per tile, 128 in all).
-  constexpr int TS = EV0 ? 24 : 27, PT = EV0 ? 13 : 15, RU = EV0 ? 9 : 11;
+  constexpr int TS = EV0 ? 24 : 27, PT = EV0 ? 13 : 15;
+  constexpr int UW = 5, UE = 13;  // first W1 and first E1 entry of a tile
   constexpr int NF = TS + 8 * PT;
   auto load = [&](auto si) -> v4d {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
@@ -716,12 +720,12 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
       constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
       constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;  // q, k (invariant) or q_ev, k_ev
       if constexpr (u == 0) return tile_load(EV0 ? A.ob1p0[which] : A.ob1p[which], mt, lane);
-      else if constexpr (u <= 8) return wload(A.w1p[which], 8, mt, u - 1, lane);
-      else if constexpr (u < RU) return wload(A.e1p[which], 2, mt, u - 9, lane);
-      else if constexpr (u == RU) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
-      else if constexpr (u == RU + 1) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
-      else if constexpr (u == RU + 2) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
-      else return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
+      else if constexpr (u == 1) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
+      else if constexpr (u == 2) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
+      else if constexpr (u == 3) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
+      else if constexpr (u == 4) return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
+      else if constexpr (u < UE) return wload(A.w1p[which], 8, mt, u - UW, lane);
+      else return wload(A.e1p[which], 2, mt, u - UE, lane);
     }
   };
   Stream<2 * NF, kFilterPF, decltype(load)> st(load);
@@ -742,7 +746,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   }
   // tile mt of filter `which`: its four values per lane are adjacent (fpos)
   v4d *const rowv = EV0 ? nullptr : reinterpret_cast<v4d *>(pf + 256 * std::size_t(p) + 4 * g);
-  v4d h[8], h2[2], e0, o, qv;
+  v4d h[8], h2[2], e0, o, qv, qk0, qk1;
   double t0 = 0.0, t1 = 0.0;  // per-head partial logits: a <- b (side 0), b <- a (side 1)
 
   st.run([&](auto si, const v4d &w) {
@@ -766,49 +770,57 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
       constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
       if constexpr (u == 0) {
         o = w;
-      } else if constexpr (u <= 8) {
-        o = mfma4(w, h[u - 1], o);
-        if constexpr (mt == 0 && u < 8) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) h[u][r] = silu_tab(h[u][r], exp2_lds);
-        }
-        if constexpr (!EV0 && mt == 0 && u == 8) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            h2[t] = mfma(e0[t], sg, h2[t]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
-          }
-        }
-        // (block 0, EV0: the rows are not stored; its reverse has no node-major
-        // attention kernel to read them, and the messages use alpha)
-      } else if constexpr (u < RU) {
-        o = mfma4(w, h2[u - 9], o);
-        if constexpr (u == RU - 1) {
-          if (valid) __builtin_nontemporal_store(o, rowv + which * 32 + 4 * mt);
-        }
-      } else if constexpr (u == RU || u == RU + 2) {
+      } else if constexpr (u == 1 || u == 3) {
         qv = w;
+      } else if constexpr (u == 2) {
+        qk0 = qv * w;  // q_a k_b: edge b -> a
+      } else if constexpr (u == 4) {
+        qk1 = qv * w;  // q_b k_a: edge a -> b
       } else {
-        // <q_recv, k_send (.) f> over the lane's four channels of this tile
-        const double d = ((qv[0] * w[0] * o[0] + qv[1] * w[1] * o[1]) + qv[2] * w[2] * o[2]) + qv[3] * w[3] * o[3];
-        if constexpr (u == RU + 1) t0 += d;
-        else t1 += d;
-        if constexpr (u == RU + 3 && (mt & 1)) {
-          // head mt / 2 complete: sum its 32 channels over the four lane
-          // groups; the alpha of edge b -> a belongs to side 0 (a receives)
-          t0 += __shfl_xor(t0, 16, kWave);
-          t0 += __shfl_xor(t0, 32, kWave);
-          t1 += __shfl_xor(t1, 16, kWave);
-          t1 += __shfl_xor(t1, 32, kWave);
-          constexpr int hd = mt / 2;
-          if (valid && g == hd) {
-            double *al = palpha + 16 * std::size_t(p) + 4 * which + hd;
-            al[0] = t0 * inv_avg;
-            al[8] = t1 * inv_avg;
+        if constexpr (u < UE) {
+          constexpr int i = u - UW;  // W1 chunk
+          o = mfma4(w, h[i], o);
+          if constexpr (mt == 0 && i < 7) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) h[i + 1][r] = silu_tab(h[i + 1][r], exp2_lds);
           }
-          t0 = 0.0;
-          t1 = 0.0;
+          if constexpr (!EV0 && mt == 0 && i == 7) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              h2[t] = mfma(e0[t], sg, h2[t]);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
+            }
+          }
+          // (block 0, EV0: the rows are not stored; its reverse has no
+          // node-major attention kernel to read them, and the messages use alpha)
+        } else {
+          o = mfma4(w, h2[u - UE], o);
+        }
+        if constexpr (u == PT - 1) {
+          // the output tile is complete
+          if constexpr (!EV0) {
+            if (valid) __builtin_nontemporal_store(o, rowv + which * 32 + 4 * mt);
+          }
+          // <q_recv, k_send (.) f> over the lane's four channels of this tile
+          t0 += ((qk0[0] * o[0] + qk0[1] * o[1]) + qk0[2] * o[2]) + qk0[3] * o[3];
+          t1 += ((qk1[0] * o[0] + qk1[1] * o[1]) + qk1[2] * o[2]) + qk1[3] * o[3];
+          if constexpr (mt & 1) {
+            // head mt / 2 complete: sum its 32 channels over the four lane
+            // groups; the alpha of edge b -> a belongs to side 0 (a receives)
+            t0 += __shfl_xor(t0, 16, kWave);
+            t0 += __shfl_xor(t0, 32, kWave);
+            t1 += __shfl_xor(t1, 16, kWave);
+            t1 += __shfl_xor(t1, 32, kWave);
+            constexpr int hd = mt / 2;
+            if (valid && g == hd) {
+              double *al = palpha + 16 * std::size_t(p) + 4 * which + hd;
+              al[0] = t0 * inv_avg;
+              al[8] = t1 * inv_avg;
+            }
+            t0 = 0.0;
+            t1 = 0.0;
+          }
         }
       }
     }
