@@ -15,7 +15,7 @@ from . import model_io
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
 
-F, NH, HW, E, R, MAXL = 128, 4, 32, 24, 32, 8
+HW, MAXL, MAXS = 32, 8, 8
 NORM_LAYER, NORM_RMS, NORM_NONE = 0, 1, 2
 REP_ZBL, REP_NLH = 0, 1
 
@@ -110,7 +110,12 @@ class _Model(ctypes.Structure):
                 ("nlh_a", ctypes.c_void_p),
                 ("nlh_b", ctypes.c_void_p),
                 ("resid", ctypes.c_void_p),
-                ("x0l", ctypes.c_void_p)]
+                ("x0l", ctypes.c_void_p),
+                ("F", ctypes.c_int64),
+                ("R", ctypes.c_int64),
+                ("n_slots", ctypes.c_int64),
+                ("degrees", ctypes.c_int64 * MAXS),
+                ("head_hidden", ctypes.c_int64)]
 
 
 class _Out(ctypes.Structure):
@@ -201,6 +206,17 @@ class Oracle:
             st.resid = self._hold(m["model.resid_lambdas"], np.float64)
             st.x0l = self._hold(m["model.x0_lambdas"], np.float64)
         self.has_c6 = "model.c6_ratios_output_block.transform_features.0.weight" in m.tensors
+        # widths (so3lr_architecture.cpp:197-212, 246-293, 444-446)
+        self.F = int(arch["invariant_features"])
+        st.F = self.F
+        st.R = int(arch["radial_basis_features"])
+        rep = [int(v) for v in m["model.euclidean_transformers.0.euclidean_attention_block.degree_repeats"]]
+        if len(rep) > MAXS:
+            raise ValueError("more than %d degree slots" % MAXS)
+        st.n_slots = len(rep)
+        for s, v in enumerate(rep):
+            st.degrees[s] = (v - 1) // 2
+        st.head_hidden = m["model.atomic_energy_output_block.layers.0.weight"].shape[0]
         self._st = st
 
     def _hold(self, a, dtype):
@@ -210,7 +226,7 @@ class Oracle:
 
     def charge_spin_table(self, counts, charge, multiplicity):
         counts = np.ascontiguousarray(counts, dtype=np.int64)
-        table = np.zeros((118, F))
+        table = np.zeros((118, self.F))
         rc = lib().orc_charge_spin_table(ctypes.byref(self._st), _ptr(counts),
                                          ctypes.c_double(charge),
                                          ctypes.c_double(multiplicity - 1.0), _ptr(table))
@@ -245,7 +261,7 @@ class Oracle:
             img = np.ascontiguousarray(image, dtype=np.int64)
             n_images = int(img.max()) + 1
             img_q = np.ascontiguousarray(image_charge, dtype=np.float64)
-            offset = np.zeros((n, F))
+            offset = np.zeros((n, self.F))
             for k in range(n_images):
                 sel = img == k
                 counts = np.bincount(z[sel], minlength=119).astype(np.int64)

@@ -15,13 +15,7 @@
 #include <omp.h>
 #endif
 
-#define F ORC_F
-#define NH ORC_NH
 #define HW ORC_HW
-#define E ORC_E
-#define R ORC_R
-#define NI ORC_NI
-#define FH ORC_FH
 #define HH ORC_HH
 
 int orc_num_threads(void) {
@@ -34,10 +28,44 @@ int orc_num_threads(void) {
 
 static const double PI = 3.141592653589793238462643383279502884;
 
-/* degree slot of equivariant channel m (channels 0-2 l=1, 3-7 l=2, 8-14 l=3,
- * 15-23 l=4): so3_conv_invariants.segment_ids in the model. */
-static int degree_of(int m) { return m < 3 ? 0 : (m < 8 ? 1 : (m < 15 ? 2 : 3)); }
-static const int deg_off[5] = {0, 3, 8, 15, 24};
+/* The widths of one model (so3lr_architecture.cpp:197-212, 246-293).  Slot s
+ * (one equivariant head) holds channels off[s] .. off[s+1]-1, all of degree
+ * deg[s]; channel c replicates the unique harmonic sh[c] (the unique
+ * harmonics are l = 1..4 in order, 2l+1 each, so with degrees 1,2,3,4 the
+ * map is the identity and slot_of is so3_conv_invariants.segment_ids). */
+typedef struct {
+  int F, NH, E, R, NI, FH, HK;
+  int deg[ORC_MAXS], off[ORC_MAXS + 1];
+  int slot_of[ORC_MAXE], sh[ORC_MAXE];
+} dims_t;
+
+/* 0, or a nonzero code for widths outside what the oracle takes. */
+static int model_dims(const orc_model *m, dims_t *d) {
+  d->F = m->F > 0 ? (int)m->F : 128;
+  d->R = m->R > 0 ? (int)m->R : 32;
+  if (d->F % HW != 0 || d->F > ORC_MAXF || d->R > ORC_MAXR) return 1;
+  d->NH = d->F / HW;
+  if (d->NH > ORC_MAXS) return 1;
+  const int slots = m->n_slots > 0 ? (int)m->n_slots : 4;
+  if (slots != d->NH) return 1;
+  d->off[0] = 0;
+  for (int s = 0; s < d->NH; ++s) {
+    d->deg[s] = m->n_slots > 0 ? (int)m->degrees[s] : s + 1;
+    if (d->deg[s] < 1 || d->deg[s] > 4 || (s > 0 && d->deg[s] < d->deg[s - 1])) return 1;
+    d->off[s + 1] = d->off[s] + 2 * d->deg[s] + 1;
+    const int base = d->deg[s] * d->deg[s] - 1; /* unique harmonics of l below: l^2 - 1 */
+    for (int k = 0; k < 2 * d->deg[s] + 1; ++k) {
+      d->slot_of[d->off[s] + k] = s;
+      d->sh[d->off[s] + k] = base + k;
+    }
+  }
+  d->E = d->off[d->NH];
+  d->NI = d->F + d->NH;
+  d->FH = d->F / 4;
+  d->HK = m->head_hidden > 0 ? (int)m->head_hidden : d->F;
+  if (d->HK > ORC_MAXK) return 1;
+  return 0;
+}
 
 static double silu(double x) { return x / (1.0 + exp(-x)); }
 static double silu_prime(double x) {
@@ -142,7 +170,7 @@ static void sh_vjp(double x, double y, double z, const double *g, double *gu) {
 /* ---------------------------------------------------------------------- */
 /* Charge/spin embedding (so3lr_charge_spin.cpp:52-114)                   */
 /* ---------------------------------------------------------------------- */
-static void charge_spin_module(const double *wq, const double *wk, const double *wv,
+static void charge_spin_module(int F, const double *wq, const double *wk, const double *wv,
                                const double *m1, const double *m3,
                                const int64_t counts[119], double psi, double *table) {
   if (psi == 0.0) return;
@@ -157,7 +185,7 @@ static void charge_spin_module(const double *wq, const double *wk, const double 
     y[zz] = softplus(qk / sqrt((double)F));
     denom += (double)counts[zz] * y[zz];
   }
-  double x[F], sx[F], h[F], sh[F], g[F];
+  double x[ORC_MAXF], sx[ORC_MAXF], h[ORC_MAXF], sh[ORC_MAXF], g[ORC_MAXF];
   for (int zz = 1; zz <= 118; ++zz) {
     if (counts[zz] <= 0) continue;
     const double a = psi * y[zz] / denom;
@@ -171,10 +199,13 @@ static void charge_spin_module(const double *wq, const double *wk, const double 
 
 int orc_charge_spin_table(const orc_model *m, const int64_t counts[119],
                           double total_charge, double unpaired, double *table) {
+  dims_t d;
+  if (model_dims(m, &d) != 0) return 1;
+  const int F = d.F;
   memset(table, 0, sizeof(double) * 118 * F);
-  charge_spin_module(m->t[ORC_CE_WQ], m->t[ORC_CE_WK], m->t[ORC_CE_WV], m->t[ORC_CE_M1],
+  charge_spin_module(F, m->t[ORC_CE_WQ], m->t[ORC_CE_WK], m->t[ORC_CE_WV], m->t[ORC_CE_M1],
                      m->t[ORC_CE_M3], counts, total_charge, table);
-  charge_spin_module(m->t[ORC_SE_WQ], m->t[ORC_SE_WK], m->t[ORC_SE_WV], m->t[ORC_SE_M1],
+  charge_spin_module(F, m->t[ORC_SE_WQ], m->t[ORC_SE_WK], m->t[ORC_SE_WV], m->t[ORC_SE_M1],
                      m->t[ORC_SE_M3], counts, unpaired, table);
   return 0;
 }
@@ -407,7 +438,7 @@ static void rms_rows_bwd(int width, const double *gy, const double *y, double r,
 /* The normalisation of one node row (kokkos_post_attention_block0.cpp:97-162):
  * affine LayerNorm with biased variance, RMSNorm without scale (xhat = y),
  * or none (xhat = y = x, is = 1). */
-static void layer_norm(int mode, const double *x, const double *w, const double *b, double eps,
+static void layer_norm(int mode, int F, const double *x, const double *w, const double *b, double eps,
                        double *y, double *xhat, double *inv_sigma) {
   if (mode == ORC_NORM_NONE) {
     *inv_sigma = 1.0;
@@ -430,7 +461,7 @@ static void layer_norm(int mode, const double *x, const double *w, const double 
   for (int c = 0; c < F; ++c) { xhat[c] = (x[c] - mean) * is; y[c] = xhat[c] * w[c] + b[c]; }
 }
 /* gx = dL/dx given gy, for the normalisation above */
-static void layer_norm_bwd(int mode, const double *gy, const double *w, const double *xhat, double is,
+static void layer_norm_bwd(int mode, int F, const double *gy, const double *w, const double *xhat, double is,
                            double *gx) {
   if (mode == ORC_NORM_NONE) {
     for (int c = 0; c < F; ++c) gx[c] = gy[c];
@@ -441,7 +472,7 @@ static void layer_norm_bwd(int mode, const double *gy, const double *w, const do
     return;
   }
   double mg = 0.0, mgx = 0.0;
-  double gh[F];
+  double gh[ORC_MAXF];
   for (int c = 0; c < F; ++c) { gh[c] = gy[c] * w[c]; mg += gh[c]; mgx += gh[c] * xhat[c]; }
   mg /= F; mgx /= F;
   for (int c = 0; c < F; ++c) gx[c] = is * (gh[c] - mg - xhat[c] * mgx);
@@ -452,10 +483,10 @@ typedef struct {
   double *x_in, *ev_in;           /* n*F, n*E  block inputs */
   double *qkv;                    /* n*5F: q k v qe ke (q, k, qe, ke RMS-normalised per
                                      head with the QK normalisation) */
-  double *qkis;                   /* n*16: their 1/rms per (row, head), QK normalisation */
-  double *s;                      /* ne*4 edge invariants */
+  double *qkis;                   /* n*4*NH: their 1/rms per (row, head), QK normalisation */
+  double *s;                      /* ne*NH edge invariants, one per degree slot */
   double *finv, *fev;             /* ne*F filters */
-  double *ainv_alpha, *aev_alpha; /* ne*4 */
+  double *ainv_alpha, *aev_alpha; /* ne*NH */
   double *a_ev;                   /* n*E  ev + d_ev */
   double *n1, *n1hat, *n1is;      /* LN1 */
   double *hpre;                   /* n*F  MLP hidden preact */
@@ -480,6 +511,10 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   for (int64_t p = 0; p < np; ++p)
     if (pi[p] < 0 || pi[p] >= n || pj[p] < 0 || pj[p] >= n) return 4;
   if (n_images <= 0) return 5;
+  dims_t D;
+  if (model_dims(m, &D) != 0) return 7;
+  /* ev heads are the degree slots: NH of each */
+  const int F = D.F, NH = D.NH, E = D.E, R = D.R, NI = D.NI, FH = D.FH, HK = D.HK;
 
   const double gamma = m->s[ORC_S_GAMMA], rmax = m->s[ORC_S_RMAX];
   const double avg = m->s[ORC_S_AVG_NN], emb_scale = m->s[ORC_S_EMB_SCALE];
@@ -524,7 +559,9 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     const double rr = sqrt(vx * vx + vy * vy + vz * vz);
     r[e] = rr;
     const double inv = rr > 1e-14 ? 1.0 / rr : 0.0;
-    orc_spherical_harmonics(vx * inv, vy * inv, vz * inv, Y + E * e);
+    double ysh[24];
+    orc_spherical_harmonics(vx * inv, vy * inv, vz * inv, ysh);
+    for (int c = 0; c < E; ++c) Y[E * e + c] = ysh[D.sh[c]];
     if (rr < rmax) {
       const double t = rr / rmax, t3 = t * t * t;
       fc[e] = 1.0 - 10.0 * t3 + 15.0 * t3 * t - 6.0 * t3 * t * t;
@@ -552,9 +589,9 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   for (int b = 0; b < L; ++b) {
     const double *const *T = m->t + ORC_NGLOBAL + b * ORC_NBLOCK;
     block_state *S = &bs[b];
-    ALLOC(S->x_in, n * F); ALLOC(S->ev_in, n * E); ALLOC(S->qkv, n * 5 * F); ALLOC(S->qkis, n * 16);
-    ALLOC(S->s, ne * 4); ALLOC(S->finv, ne * F); ALLOC(S->fev, ne * F);
-    ALLOC(S->ainv_alpha, ne * 4); ALLOC(S->aev_alpha, ne * 4); ALLOC(S->a_ev, n * E);
+    ALLOC(S->x_in, n * F); ALLOC(S->ev_in, n * E); ALLOC(S->qkv, n * 5 * F); ALLOC(S->qkis, n * 4 * NH);
+    ALLOC(S->s, ne * NH); ALLOC(S->finv, ne * F); ALLOC(S->fev, ne * F);
+    ALLOC(S->ainv_alpha, ne * NH); ALLOC(S->aev_alpha, ne * NH); ALLOC(S->a_ev, n * E);
     ALLOC(S->n1, n * F); ALLOC(S->n1hat, n * F); ALLOC(S->n1is, n); ALLOC(S->hpre, n * F);
     ALLOC(S->tout, n * NI); ALLOC(S->pre2hat, n * F); ALLOC(S->pre2is, n);
     /* residual scalars (kokkos_local_energy_reverse.cpp:143-158): the block
@@ -569,19 +606,19 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     /* edge invariants + both filters (kokkos_integrated_block0.cpp:166-255) */
 #pragma omp parallel for schedule(static)
     for (int64_t e = 0; e < ne; ++e) {
-      double sv[4] = {0, 0, 0, 0};
+      double sv[ORC_MAXS] = {0};
       for (int c = 0; c < E; ++c) {
         const double d = ev[snd[e] * E + c] - ev[rcv[e] * E + c];
-        sv[degree_of(c)] += d * d * acg[c];
+        sv[D.slot_of[c]] += d * d * acg[c];
       }
-      for (int l = 0; l < 4; ++l) S->s[e * 4 + l] = sv[l];
+      for (int l = 0; l < NH; ++l) S->s[e * NH + l] = sv[l];
       for (int which = 0; which < 2; ++which) {
         const int base = which == 0 ? ORC_B_FI_RW0 : ORC_B_FE_RW0;
-        double h[F], h2[FH], t1[F], t2[F];
+        double h[ORC_MAXF], h2[ORC_MAXF / 4], t1[ORC_MAXF], t2[ORC_MAXF];
         matvec(T[base + 0], T[base + 1], F, R, rbf + e * R, h);
         for (int c = 0; c < F; ++c) h[c] = silu(h[c]);
         matvec(T[base + 2], T[base + 3], F, F, h, t1);
-        matvec(T[base + 4], T[base + 5], FH, 4, sv, h2);
+        matvec(T[base + 4], T[base + 5], FH, NH, sv, h2);
         for (int c = 0; c < FH; ++c) h2[c] = silu(h2[c]);
         matvec(T[base + 6], T[base + 7], F, FH, h2, t2);
         double *dst = which == 0 ? S->finv + e * F : S->fev + e * F;
@@ -608,7 +645,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
         for (int k = 0; k < 4; ++k)
           for (int h = 0; h < NH; ++h) {
             double *row = S->qkv + i * 5 * F + rows[k] * F + h * HW;
-            orc_rms_rows(1, HW, row, 1e-6, row, S->qkis + i * 16 + k * 4 + h);
+            orc_rms_rows(1, HW, row, 1e-6, row, S->qkis + (i * 4 + k) * NH + h);
           }
     }
     /* attention coefficients per (edge, head) */
@@ -621,31 +658,31 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
           ai += qr[c] * ks[F + c] * S->finv[e * F + c];
           ae += qr[3 * F + c] * ks[4 * F + c] * S->fev[e * F + c];
         }
-        S->ainv_alpha[e * 4 + h] = ai / avg;
-        S->aev_alpha[e * 4 + h] = ae / avg;
+        S->ainv_alpha[e * NH + h] = ai / avg;
+        S->aev_alpha[e * NH + h] = ae / avg;
       }
     }
     /* receiver-side scatter, as a gather over the receiver CSR */
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
-      double di[F], de[E];
-      memset(di, 0, sizeof(di)); memset(de, 0, sizeof(de));
+      double di[ORC_MAXF] = {0}, de[ORC_MAXE] = {0};
       for (int64_t k = roff[i]; k < roff[i + 1]; ++k) {
         const int64_t e = ridx[k];
         const double *vs = S->qkv + snd[e] * 5 * F + 2 * F;
-        for (int c = 0; c < F; ++c) di[c] += fc[e] * S->ainv_alpha[e * 4 + c / HW] * vs[c];
-        for (int c = 0; c < E; ++c) de[c] += fc[e] * S->aev_alpha[e * 4 + degree_of(c)] * Y[e * E + c];
+        for (int c = 0; c < F; ++c) di[c] += fc[e] * S->ainv_alpha[e * NH + c / HW] * vs[c];
+        for (int c = 0; c < E; ++c) de[c] += fc[e] * S->aev_alpha[e * NH + D.slot_of[c]] * Y[e * E + c];
       }
-      memcpy(dinv + i * F, di, sizeof(di));
-      memcpy(dev + i * E, de, sizeof(de));
+      memcpy(dinv + i * F, di, sizeof(double) * (size_t)F);
+      memcpy(dev + i * E, de, sizeof(double) * (size_t)E);
     }
     /* post-attention (kokkos_post_attention_block0.cpp:165-300) */
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
-      double ainv[F], act[F], hid[F], mlp[F], p[F], cat[NI], pre2[F], y2[F];
+      double ainv[ORC_MAXF], act[ORC_MAXF], hid[ORC_MAXF], mlp[ORC_MAXF], p[ORC_MAXF];
+      double cat[ORC_MAXF + ORC_MAXS], pre2[ORC_MAXF], y2[ORC_MAXF];
       for (int c = 0; c < F; ++c) ainv[c] = x[i * F + c] + dinv[i * F + c];
       for (int c = 0; c < E; ++c) S->a_ev[i * E + c] = ev[i * E + c] + dev[i * E + c];
-      layer_norm((int)m->norm1, ainv, T[ORC_B_LN1_W], T[ORC_B_LN1_B], eps, S->n1 + i * F, S->n1hat + i * F,
+      layer_norm((int)m->norm1, F, ainv, T[ORC_B_LN1_W], T[ORC_B_LN1_B], eps, S->n1 + i * F, S->n1hat + i * F,
                  &S->n1is[i]);
       const double *n1 = S->n1 + i * F;
       for (int c = 0; c < F; ++c) act[c] = silu(n1[c]);
@@ -654,34 +691,34 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
       matvec(T[ORC_B_M2_W], T[ORC_B_M2_B], F, F, hid, mlp);
       for (int c = 0; c < F; ++c) p[c] = n1[c] + mlp[c];
       for (int c = 0; c < F; ++c) cat[c] = p[c];
-      for (int l = 0; l < 4; ++l) cat[F + l] = 0.0;
-      for (int c = 0; c < E; ++c) cat[F + degree_of(c)] += S->a_ev[i * E + c] * S->a_ev[i * E + c] * icg[c];
+      for (int l = 0; l < NH; ++l) cat[F + l] = 0.0;
+      for (int c = 0; c < E; ++c) cat[F + D.slot_of[c]] += S->a_ev[i * E + c] * S->a_ev[i * E + c] * icg[c];
       matvec(T[ORC_B_INT_W], T[ORC_B_INT_B], NI, NI, cat, S->tout + i * NI);
       const double *t = S->tout + i * NI;
       for (int c = 0; c < F; ++c) pre2[c] = p[c] + t[c];
-      for (int c = 0; c < E; ++c) ev[i * E + c] = S->a_ev[i * E + c] * (1.0 + t[F + degree_of(c)]);
-      layer_norm((int)m->norm2, pre2, T[ORC_B_LN2_W], T[ORC_B_LN2_B], eps, y2, S->pre2hat + i * F, &S->pre2is[i]);
-      memcpy(x + i * F, y2, sizeof(y2));
+      for (int c = 0; c < E; ++c) ev[i * E + c] = S->a_ev[i * E + c] * (1.0 + t[F + D.slot_of[c]]);
+      layer_norm((int)m->norm2, F, pre2, T[ORC_B_LN2_W], T[ORC_B_LN2_B], eps, y2, S->pre2hat + i * F, &S->pre2is[i]);
+      memcpy(x + i * F, y2, sizeof(double) * (size_t)F);
     }
   }
 
   /* ---- output heads (kokkos_output_heads.cpp:137-176,341-451) ---- */
-  ALLOC(he_pre, n * F); ALLOC(hq_pre, n * F); ALLOC(hh_pre, n * HH); ALLOC(hkey, n * HH);
+  ALLOC(he_pre, n * HK); ALLOC(hq_pre, n * HK); ALLOC(hh_pre, n * HH); ALLOC(hkey, n * HH);
   ALLOC(heff, n); ALLOC(eatom, n); ALLOC(qraw, n); ALLOC(q, n); ALLOC(hir, n);
   if (has_c6) { ALLOC(c6_pre, n * HH); ALLOC(c6_key, n * HH); ALLOC(c6_eff, n); ALLOC(c6r, n); }
 #pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < n; ++i) {
-    double t[F], hh[HH];
+    double t[ORC_MAXK], hh[HH];
     const int64_t zi = z[i];
-    matvec(m->t[ORC_E_W1], m->t[ORC_E_B1], F, F, x + i * F, he_pre + i * F);
-    for (int c = 0; c < F; ++c) t[c] = silu(he_pre[i * F + c]);
+    matvec(m->t[ORC_E_W1], m->t[ORC_E_B1], HK, F, x + i * F, he_pre + i * HK);
+    for (int c = 0; c < HK; ++c) t[c] = silu(he_pre[i * HK + c]);
     double er = 0.0;
-    for (int c = 0; c < F; ++c) er += m->t[ORC_E_W2][c] * t[c];
+    for (int c = 0; c < HK; ++c) er += m->t[ORC_E_W2][c] * t[c];
     eatom[i] = (er + m->t[ORC_E_B2][0]) * m->t[ORC_E_SCALE][zi - 1] + m->t[ORC_E_SHIFT][zi - 1];
-    matvec(m->t[ORC_Q_W1], m->t[ORC_Q_B1], F, F, x + i * F, hq_pre + i * F);
-    for (int c = 0; c < F; ++c) t[c] = silu(hq_pre[i * F + c]);
+    matvec(m->t[ORC_Q_W1], m->t[ORC_Q_B1], HK, F, x + i * F, hq_pre + i * HK);
+    for (int c = 0; c < HK; ++c) t[c] = silu(hq_pre[i * HK + c]);
     double qr = 0.0;
-    for (int c = 0; c < F; ++c) qr += m->t[ORC_Q_W2][c] * t[c];
+    for (int c = 0; c < HK; ++c) qr += m->t[ORC_Q_W2][c] * t[c];
     qraw[i] = qr + m->t[ORC_Q_B2][0] + m->t[ORC_Q_EMB][zi];
     matvec(m->t[ORC_H_W1], m->t[ORC_H_B1], HH, F, x + i * F, hh_pre + i * HH);
     for (int c = 0; c < HH; ++c) hh[c] = silu(hh_pre[i * HH + c]);
@@ -753,15 +790,15 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   for (int64_t i = 0; i < n; ++i) {
     const int64_t zi = z[i];
     const int64_t im = image ? image[i] : 0;
-    double gh[F], ghh[HH], gk[HH];
+    double gh[ORC_MAXK], ghh[HH], gk[HH];
     double *g = gx + i * F;
     memset(g, 0, sizeof(double) * F);
-    for (int c = 0; c < F; ++c)
-      gh[c] = m->t[ORC_E_SCALE][zi - 1] * m->t[ORC_E_W2][c] * silu_prime(he_pre[i * F + c]);
-    matvecT_acc(m->t[ORC_E_W1], F, F, gh, g);
+    for (int c = 0; c < HK; ++c)
+      gh[c] = m->t[ORC_E_SCALE][zi - 1] * m->t[ORC_E_W2][c] * silu_prime(he_pre[i * HK + c]);
+    matvecT_acc(m->t[ORC_E_W1], HK, F, gh, g);
     const double qseed = lr_dq[i] - img_seed[im] / img_cnt[im];
-    for (int c = 0; c < F; ++c) gh[c] = qseed * m->t[ORC_Q_W2][c] * silu_prime(hq_pre[i * F + c]);
-    matvecT_acc(m->t[ORC_Q_W1], F, F, gh, g);
+    for (int c = 0; c < HK; ++c) gh[c] = qseed * m->t[ORC_Q_W2][c] * silu_prime(hq_pre[i * HK + c]);
+    matvecT_acc(m->t[ORC_Q_W1], HK, F, gh, g);
     const double sg = heff[i] > 0.0 ? 1.0 : (heff[i] < 0.0 ? -1.0 : 0.0);
     const double hs = lr_dh[i] * sg / sqrt((double)HH);
     for (int c = 0; c < HH; ++c) gk[c] = hs * m->t[ORC_H_QEMB][zi * HH + c];
@@ -782,7 +819,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
 
   /* ---- interaction blocks, reverse ---- */
   ALLOC(gr, ne); ALLOC(gY, ne * E); ALLOC(gqkv, n * 5 * F); ALLOC(gfinv, ne * F);
-  ALLOC(gfev, ne * F); ALLOC(gfc, ne); ALLOC(gs, ne * 4); ALLOC(gainv, n * F); ALLOC(gaev, n * E);
+  ALLOC(gfev, ne * F); ALLOC(gfc, ne); ALLOC(gs, ne * NH); ALLOC(gainv, n * F); ALLOC(gaev, n * E);
   for (int b = L - 1; b >= 0; --b) {
     const double *const *T = m->t + ORC_NGLOBAL + b * ORC_NBLOCK;
     block_state *S = &bs[b];
@@ -790,28 +827,29 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     /* post-attention reverse (kokkos_post_attention_reverse.cpp) */
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) {
-      double gpre2[F], gt[NI], gcat[NI], gp[F], ghid[F], gact[F], gn1[F];
+      double gpre2[ORC_MAXF], gt[ORC_MAXF + ORC_MAXS], gcat[ORC_MAXF + ORC_MAXS], gp[ORC_MAXF];
+      double ghid[ORC_MAXF], gact[ORC_MAXF], gn1[ORC_MAXF];
       const double *t = S->tout + i * NI, *aev = S->a_ev + i * E;
-      layer_norm_bwd((int)m->norm2, gx + i * F, T[ORC_B_LN2_W], S->pre2hat + i * F, S->pre2is[i], gpre2);
+      layer_norm_bwd((int)m->norm2, F, gx + i * F, T[ORC_B_LN2_W], S->pre2hat + i * F, S->pre2is[i], gpre2);
       for (int c = 0; c < F; ++c) { gt[c] = gpre2[c]; gp[c] = gpre2[c]; }
-      for (int l = 0; l < 4; ++l) gt[F + l] = 0.0;
+      for (int l = 0; l < NH; ++l) gt[F + l] = 0.0;
       double *ga = gaev + i * E;
       for (int c = 0; c < E; ++c) {
-        gt[F + degree_of(c)] += gev[i * E + c] * aev[c];
-        ga[c] = gev[i * E + c] * (1.0 + t[F + degree_of(c)]);
+        gt[F + D.slot_of[c]] += gev[i * E + c] * aev[c];
+        ga[c] = gev[i * E + c] * (1.0 + t[F + D.slot_of[c]]);
       }
-      memset(gcat, 0, sizeof(gcat));
+      memset(gcat, 0, sizeof(double) * (size_t)NI);
       matvecT_acc(T[ORC_B_INT_W], NI, NI, gt, gcat);
       for (int c = 0; c < F; ++c) gp[c] += gcat[c];
-      for (int c = 0; c < E; ++c) ga[c] += gcat[F + degree_of(c)] * 2.0 * aev[c] * icg[c];
+      for (int c = 0; c < E; ++c) ga[c] += gcat[F + D.slot_of[c]] * 2.0 * aev[c] * icg[c];
       /* p = n1 + W2 silu(hpre) + b2,  hpre = W1 silu(n1) + b1 */
-      memset(ghid, 0, sizeof(ghid));
+      memset(ghid, 0, sizeof(double) * (size_t)F);
       matvecT_acc(T[ORC_B_M2_W], F, F, gp, ghid);
       for (int c = 0; c < F; ++c) ghid[c] *= silu_prime(S->hpre[i * F + c]);
-      memset(gact, 0, sizeof(gact));
+      memset(gact, 0, sizeof(double) * (size_t)F);
       matvecT_acc(T[ORC_B_M1_W], F, F, ghid, gact);
       for (int c = 0; c < F; ++c) gn1[c] = gp[c] + gact[c] * silu_prime(S->n1[i * F + c]);
-      layer_norm_bwd((int)m->norm1, gn1, T[ORC_B_LN1_W], S->n1hat + i * F, S->n1is[i], gainv + i * F);
+      layer_norm_bwd((int)m->norm1, F, gn1, T[ORC_B_LN1_W], S->n1hat + i * F, S->n1is[i], gainv + i * F);
     }
     /* attention reverse per edge (kokkos_attention_scatter_reverse.cpp:280-500) */
 #pragma omp parallel for schedule(static)
@@ -826,12 +864,12 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
           dai += gdi[c] * fc[e] * ks[2 * F + c];
           ci += gdi[c] * ks[2 * F + c];
         }
-        for (int c = deg_off[h]; c < deg_off[h + 1]; ++c) {
+        for (int c = D.off[h]; c < D.off[h + 1]; ++c) {
           dae += gde[c] * fc[e] * Y[e * E + c];
           ce += gde[c] * Y[e * E + c];
-          gY[e * E + c] += gde[c] * fc[e] * S->aev_alpha[e * 4 + h];
+          gY[e * E + c] += gde[c] * fc[e] * S->aev_alpha[e * NH + h];
         }
-        dfc += ci * S->ainv_alpha[e * 4 + h] + ce * S->aev_alpha[e * 4 + h];
+        dfc += ci * S->ainv_alpha[e * NH + h] + ce * S->aev_alpha[e * NH + h];
         const double si_ = dai / avg, se_ = dae / avg;
         for (int c = h * HW; c < (h + 1) * HW; ++c) {
           gfinv[e * F + c] = si_ * qr[c] * ks[F + c];
@@ -853,7 +891,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
         for (int h = 0; h < NH; ++h) {
           double dai = 0.0, dae = 0.0;
           for (int c = h * HW; c < (h + 1) * HW; ++c) dai += gdi[c] * fc[e] * ks[2 * F + c];
-          for (int c = deg_off[h]; c < deg_off[h + 1]; ++c) dae += gde[c] * fc[e] * Y[e * E + c];
+          for (int c = D.off[h]; c < D.off[h + 1]; ++c) dae += gde[c] * fc[e] * Y[e * E + c];
           for (int c = h * HW; c < (h + 1) * HW; ++c) {
             g[c] += dai / avg * ks[F + c] * S->finv[e * F + c];
             g[3 * F + c] += dae / avg * ks[4 * F + c] * S->fev[e * F + c];
@@ -867,10 +905,10 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
         for (int h = 0; h < NH; ++h) {
           double dai = 0.0, dae = 0.0;
           for (int c = h * HW; c < (h + 1) * HW; ++c) dai += gdi[c] * fc[e] * qi[2 * F + c];
-          for (int c = deg_off[h]; c < deg_off[h + 1]; ++c) dae += gde[c] * fc[e] * Y[e * E + c];
+          for (int c = D.off[h]; c < D.off[h + 1]; ++c) dae += gde[c] * fc[e] * Y[e * E + c];
           for (int c = h * HW; c < (h + 1) * HW; ++c) {
             g[F + c] += dai / avg * qr[c] * S->finv[e * F + c];
-            g[2 * F + c] += fc[e] * S->ainv_alpha[e * 4 + h] * gdi[c];
+            g[2 * F + c] += fc[e] * S->ainv_alpha[e * NH + h] * gdi[c];
             g[4 * F + c] += dae / avg * qr[3 * F + c] * S->fev[e * F + c];
           }
         }
@@ -879,24 +917,23 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     /* filter dgrad per edge (kokkos_block2_attention_input_reverse.cpp:198-240,301-336) */
 #pragma omp parallel for schedule(static)
     for (int64_t e = 0; e < ne; ++e) {
-      double grbf[R], gsv[4];
-      memset(grbf, 0, sizeof(grbf)); memset(gsv, 0, sizeof(gsv));
+      double grbf[ORC_MAXR] = {0}, gsv[ORC_MAXS] = {0};
       for (int which = 0; which < 2; ++which) {
         const int base = which == 0 ? ORC_B_FI_RW0 : ORC_B_FE_RW0;
         const double *gf = which == 0 ? gfinv + e * F : gfev + e * F;
-        double pre[F], gh[F], pre2[FH], gh2[FH];
+        double pre[ORC_MAXF], gh[ORC_MAXF], pre2[ORC_MAXF / 4], gh2[ORC_MAXF / 4];
         matvec(T[base + 0], T[base + 1], F, R, rbf + e * R, pre);
-        memset(gh, 0, sizeof(gh));
+        memset(gh, 0, sizeof(double) * (size_t)F);
         matvecT_acc(T[base + 2], F, F, gf, gh);
         for (int c = 0; c < F; ++c) gh[c] *= silu_prime(pre[c]);
         matvecT_acc(T[base + 0], F, R, gh, grbf);
-        matvec(T[base + 4], T[base + 5], FH, 4, S->s + e * 4, pre2);
-        memset(gh2, 0, sizeof(gh2));
+        matvec(T[base + 4], T[base + 5], FH, NH, S->s + e * NH, pre2);
+        memset(gh2, 0, sizeof(double) * (size_t)FH);
         matvecT_acc(T[base + 6], F, FH, gf, gh2);
         for (int c = 0; c < FH; ++c) gh2[c] *= silu_prime(pre2[c]);
-        matvecT_acc(T[base + 4], FH, 4, gh2, gsv);
+        matvecT_acc(T[base + 4], FH, NH, gh2, gsv);
       }
-      for (int l = 0; l < 4; ++l) gs[e * 4 + l] = gsv[l];
+      for (int l = 0; l < NH; ++l) gs[e * NH + l] = gsv[l];
       const double rr = r[e];
       double grad = 0.0;
       if (rr < rmax) {
@@ -922,7 +959,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
           for (int h = 0; h < NH; ++h) {
             double *gr_ = gqkv + i * 5 * F + rows[k] * F + h * HW;
             double tmp[HW];
-            rms_rows_bwd(HW, gr_, S->qkv + i * 5 * F + rows[k] * F + h * HW, S->qkis[i * 16 + k * 4 + h], tmp);
+            rms_rows_bwd(HW, gr_, S->qkv + i * 5 * F + rows[k] * F + h * HW, S->qkis[(i * 4 + k) * NH + h], tmp);
             memcpy(gr_, tmp, sizeof(tmp));
           }
       }
@@ -939,12 +976,12 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
       for (int64_t k = soff[i]; k < soff[i + 1]; ++k) {
         const int64_t e = sidx[k];
         for (int c = 0; c < E; ++c)
-          ge_[c] += gs[e * 4 + degree_of(c)] * 2.0 * (evi[c] - S->ev_in[rcv[e] * E + c]) * acg[c];
+          ge_[c] += gs[e * NH + D.slot_of[c]] * 2.0 * (evi[c] - S->ev_in[rcv[e] * E + c]) * acg[c];
       }
       for (int64_t k = roff[i]; k < roff[i + 1]; ++k) {
         const int64_t e = ridx[k];
         for (int c = 0; c < E; ++c)
-          ge_[c] -= gs[e * 4 + degree_of(c)] * 2.0 * (S->ev_in[snd[e] * E + c] - evi[c]) * acg[c];
+          ge_[c] -= gs[e * NH + D.slot_of[c]] * 2.0 * (S->ev_in[snd[e] * E + c] - evi[c]) * acg[c];
       }
       /* residual scalars: d/d(previous output) = resid[b] d/d(input); the
        * embedding term does not depend on the positions */
@@ -961,8 +998,11 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     const double rr = r[e];
     if (rr <= 1e-14) { ge[3 * e] = ge[3 * e + 1] = ge[3 * e + 2] = 0.0; continue; }
     const double u[3] = {vx / rr, vy / rr, vz / rr};
-    double gu[3];
-    sh_vjp(u[0], u[1], u[2], gY + e * E, gu);
+    /* the feature channels' adjoints summed onto the unique harmonics they
+     * replicate (kokkos_local_cartesian_forces.cpp) */
+    double gu[3], gsh[24] = {0};
+    for (int c = 0; c < E; ++c) gsh[D.sh[c]] += gY[e * E + c];
+    sh_vjp(u[0], u[1], u[2], gsh, gu);
     const double radial = u[0] * gu[0] + u[1] * gu[1] + u[2] * gu[2];
     const double dr = gr[e] + zbl_g[e];
     for (int a = 0; a < 3; ++a) ge[3 * e + a] = dr * u[a] + (gu[a] - u[a] * radial) / rr;

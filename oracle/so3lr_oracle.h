@@ -47,22 +47,28 @@
 extern "C" {
 #endif
 
-/* Widths of the models the oracle evaluates (those of every released F = 128
- * checkpoint); the block count is a model field (1..ORC_MAXL). */
-#define ORC_F 128   /* invariant features */
-#define ORC_NH 4    /* heads (invariant == equivariant head count) */
-#define ORC_HW 32   /* head width */
-#define ORC_E 24    /* equivariant channels, degrees 1..4 */
-#define ORC_R 32    /* radial basis */
-#define ORC_MAXL 8  /* interaction blocks, at most */
-#define ORC_NI 132  /* interaction width F + 4 */
-#define ORC_FH 32   /* spherical filter hidden width F/4 */
-#define ORC_HH 64   /* Hirshfeld head width */
+/* Widths.  The invariant width F, the radial basis R, the degree slots and
+ * the energy/charge head width are model fields (so3lr_architecture.cpp:
+ * 246-330, 420-450); the rest are fixed by the architecture:
+ *   heads = F / 32, each 32 wide, one equivariant head per degree slot
+ *   (so3lr_capabilities.cpp:62-69); slot s carries 2 l_s + 1 channels, the
+ *   slots' degrees sorted, l in 1..4, a degree may repeat; equivariant width
+ *   E = sum_s (2 l_s + 1); interaction width F + slots; spherical filter
+ *   hidden width F / 4; Hirshfeld and C6 ratio heads 64 wide
+ *   (kokkos_output_heads.cpp:16-20). */
+#define ORC_HW 32    /* head width */
+#define ORC_HH 64    /* Hirshfeld head width */
+#define ORC_MAXL 8   /* interaction blocks, at most */
+#define ORC_MAXF 256 /* invariant width, at most */
+#define ORC_MAXR 64  /* radial basis, at most */
+#define ORC_MAXS 8   /* degree slots (= heads), at most */
+#define ORC_MAXE 72  /* equivariant channels, at most (8 slots of l = 4) */
+#define ORC_MAXK 256 /* energy/charge head hidden width, at most */
 
 /* Global tensors (pointer slots, filled by the caller from the .so3lr file). */
 enum {
-  ORC_EMB_W = 0,    /* (128,118) model.inv_feature_embedding.embedding.weight */
-  ORC_RBF_B,        /* (32)      model.radial_embedding.radial_basis_fn.b */
+  ORC_EMB_W = 0,    /* (F,118) model.inv_feature_embedding.embedding.weight */
+  ORC_RBF_B,        /* (R)       model.radial_embedding.radial_basis_fn.b */
   ORC_E_W1, ORC_E_B1, ORC_E_W2, ORC_E_B2, ORC_E_SCALE, ORC_E_SHIFT,
   ORC_Q_EMB, ORC_Q_W1, ORC_Q_B1, ORC_Q_W2, ORC_Q_B2,
   ORC_H_QEMB, ORC_H_W1, ORC_H_B1, ORC_H_W2, ORC_H_B2, ORC_H_VSHIFT,
@@ -70,14 +76,14 @@ enum {
   ORC_SE_WQ, ORC_SE_WK, ORC_SE_WV, ORC_SE_M1, ORC_SE_M3,
   ORC_ALPHA_REF, ORC_C6_REF,
   /* optional C6 ratio head (NULL when the model has none), laid out as the
-   * Hirshfeld head: (100,64) (64,128) (64) (64,64) (64) (100,1) */
+   * Hirshfeld head: (100,64) (64,F) (64) (64,64) (64) (100,1) */
   ORC_C6_QEMB, ORC_C6_W1, ORC_C6_B1, ORC_C6_W2, ORC_C6_B2, ORC_C6_VSHIFT,
   ORC_NGLOBAL
 };
 
 /* Per-block tensors: slot ORC_NGLOBAL + block * ORC_NBLOCK + id. */
 enum {
-  ORC_B_WQ = 0, ORC_B_WK, ORC_B_WV, ORC_B_WQE, ORC_B_WKE, /* (4,32,32) */
+  ORC_B_WQ = 0, ORC_B_WK, ORC_B_WV, ORC_B_WQE, ORC_B_WKE, /* (F/32,32,32) */
   ORC_B_FI_RW0, ORC_B_FI_RB0, ORC_B_FI_RW1, ORC_B_FI_RB1,
   ORC_B_FI_EW0, ORC_B_FI_EB0, ORC_B_FI_EW1, ORC_B_FI_EB1,
   ORC_B_FE_RW0, ORC_B_FE_RB0, ORC_B_FE_RW1, ORC_B_FE_RB1,
@@ -111,8 +117,8 @@ enum {
 
 typedef struct {
   const double *t[ORC_NTENSOR];
-  const int64_t *rbf_k;     /* (32) */
-  const int64_t *rbf_krev;  /* (32) */
+  const int64_t *rbf_k;     /* (R) */
+  const int64_t *rbf_krev;  /* (R) */
   int64_t n_alpha_ref;      /* extent of the reference alpha/C6 tables */
   double s[ORC_NSCALAR];
   /* Architecture options; all zero/NULL is the v1 model with 3 blocks. */
@@ -124,6 +130,12 @@ typedef struct {
   const double *nlh_a, *nlh_b;
   const double *resid;      /* residual scalars per block (NULL: none) */
   const double *x0l;
+  /* Widths; all zero is F = 128, R = 32, degrees 1,2,3,4, head width F. */
+  int64_t F;                /* invariant features: a multiple of 32 up to ORC_MAXF */
+  int64_t R;                /* radial basis, up to ORC_MAXR */
+  int64_t n_slots;          /* degree slots = F / 32 */
+  int64_t degrees[ORC_MAXS];/* degree of each slot, sorted, 1..4 */
+  int64_t head_hidden;      /* energy and charge head hidden width */
 } orc_model;
 
 typedef struct {
@@ -147,7 +159,7 @@ typedef struct {
 } orc_out;
 
 /*
- * Charge/spin offset table (118 x 128, row Z-1), to be added to the element
+ * Charge/spin offset table (118 x F, row Z-1), to be added to the element
  * embedding before the embedding scale.  counts[z] is the number of atoms of
  * element z (index 0 unused).  psi is the total charge for the charge module
  * and multiplicity-1 for the spin module.  Follows so3lr_charge_spin.cpp:52-114.
@@ -164,7 +176,7 @@ int orc_charge_multiplicity_problem(const int64_t counts[119],
 /*
  * Full E + F + virial evaluation of one packed set of images.
  *   n nodes (all owned), atomic numbers z.
- *   emb_offset: n*128 per-node charge/spin offsets (NULL = zero).
+ *   emb_offset: n*F per-node charge/spin offsets (NULL = zero).
  *   image: n image ids in [0, n_images) (NULL = one image), image_charge:
  *   requested total charge per image.
  *   SR graph: ne directed edges, senders/receivers node indices, vectors
@@ -184,7 +196,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
 /* RMS normalisation of `rows` rows of `width` values:
  * y = x / sqrt(mean(x^2) + eps), inv_rms[row] = 1 / sqrt(mean(x^2) + eps)
  * (inv_rms may be NULL).  RMSNorm without scale
- * (kokkos_post_attention_block0.cpp:126-143, width 128, eps of the model) and
+ * (kokkos_post_attention_block0.cpp:126-143, width F, eps of the model) and
  * the QK normalisation (kokkos_integrated_block0.cpp:288-328, width 32,
  * eps 1e-6) are this function. */
 void orc_rms_rows(int64_t rows, int64_t width, const double *x, double eps, double *y,

@@ -19,14 +19,14 @@ MODEL = os.path.join(REPO, "models", "so3lr.so3lr")
 
 
 
-def perturbed_model(path, seed=11, scale=0.2):
-    """A copy of the shipped model in which every float64 parameter tensor is
+def perturbed_model(path, seed=11, scale=0.2, base=MODEL):
+    """A copy of the model `base` (the shipped model by default) in which every float64 parameter tensor is
     scaled elementwise by 1 + scale * u, u uniform in [-1, 1] (seeded); the
     derived and physical constants (basis, Clebsch-Gordan tables, reference
     polarizabilities and C6) are kept. A second set of weights for parity
     tests, written with so3lrxlammps_amd.model_file."""
     from so3lrxlammps_amd.model_file import read_model, write_model
-    manifest, arrays = read_model(MODEL)
+    manifest, arrays = read_model(base)
     rng = np.random.default_rng(seed)
     for rec in manifest["tensors"]:
         if rec["role"] == "parameter" and rec["dtype"] == "float64":
@@ -138,6 +138,161 @@ def variant_model(path, blocks=None, rms_norm=False, norm2=True, qk_norm=False, 
     arch["state_tensor_count"] = len(manifest["tensors"])
     arch["parameter_elements"] = int(sum(np.asarray(arrays[r["state_key"]]).size for r in manifest["tensors"]
                                          if r["role"] == "parameter"))
+    write_model(str(path), manifest, arrays)
+    return str(path)
+
+
+def _bernstein_elevation(n, m):
+    """M (n+1, n+m+1) with B^n_k = sum_j M[k, j] B^(n+m)_j: degree elevation of
+    the Bernstein basis, M[k, j] = C(n, k) C(m, j - k) / C(n + m, j)."""
+    from math import comb
+    M = np.zeros((n + 1, n + m + 1))
+    for k in range(n + 1):
+        for j in range(k, k + m + 1):
+            M[k, j] = comb(n, k) * comb(m, j - k) / comb(n + m, j)
+    return M
+
+
+def lifted_model(path, base=MODEL, R=64, split=0.3):
+    """The F = 256 model with R = 64 radial functions and the duplicated degree
+    slots 1,1,2,2,3,3,4,4 (the "l" widths the reference runs,
+    so3lr_capabilities.cpp:54-85) that computes exactly the same function as
+    the F = 128 model `base`: a two-copy lift.
+
+    Invariant head h' (8 heads of 32) is a copy of head h'//2 of `base` and
+    degree slot s' a copy of slot s'//2; copy = h' % 2 (s' % 2).  Every weight
+    that sums over a lifted input takes the base weight times `split` on copy
+    0 and 1 - `split` on copy 1, so both copies of every hidden value equal the
+    base value (the forward pass is the base pass twice over) while the
+    adjoints of the two copies differ, and a reverse pass that mixes them up
+    is caught.  The charge/spin query weights carry sqrt(2) for the
+    1/sqrt(F) of their logits, and the radial layer reads the degree-31
+    Bernstein basis re-expressed in the degree-R-1 basis (exact degree
+    elevation).  The energy and charge heads keep their hidden width 128, so
+    it differs from F (the "256 -> 128" heads, kokkos_output_heads.cpp:16-19).
+    Energies, forces and the virial equal those of `base` up to rounding."""
+    from so3lrxlammps_amd.model_file import read_model, write_model
+    manifest, arrays = read_model(base)
+    arch = manifest["architecture"]
+    F, R0 = int(arch["invariant_features"]), int(arch["radial_basis_features"])
+    assert F == 128 and int(arch["attention_heads"]) == 4 and int(arch["euclidean_degree_channels"]) == 4
+    F2, S2 = 2 * F, 8
+    h2 = np.arange(F2) // 32
+    cmap = (h2 // 2) * 32 + np.arange(F2) % 32
+    csplit = np.where(h2 % 2 == 0, split, 1.0 - split)
+    smap = np.arange(S2) // 2
+    ssplit = np.where(np.arange(S2) % 2 == 0, split, 1.0 - split)
+    hmap = np.arange(F2 // 4) // 2
+    hsplit = np.where(np.arange(F2 // 4) % 2 == 0, split, 1.0 - split)
+    reps0 = [3, 5, 7, 9]
+    off0 = np.concatenate([[0], np.cumsum(reps0)])
+    reps = [reps0[s // 2] for s in range(S2)]
+    chmap = np.concatenate([off0[s // 2] + np.arange(reps[s]) for s in range(S2)])
+    seg = np.concatenate([np.full(reps[s], s) for s in range(S2)])
+    elev = _bernstein_elevation(R0 - 1, R - R0)
+    rowmap = np.concatenate([cmap, F + smap])
+    colsplit = np.concatenate([csplit, ssplit])
+
+    def lift_rows_cols(w):  # (F, F) with the input split
+        return w[cmap][:, cmap] * csplit[None, :]
+
+    def lift_cols(w):  # (out, F): a head reading the lifted features
+        return w[:, cmap] * csplit[None, :]
+
+    out = {}
+    for k, a in arrays.items():
+        t = k.split(".")
+        if k == "model.inv_feature_embedding.embedding.weight":
+            out[k] = a[cmap]
+        elif k.startswith(("model.charge_embedding.", "model.spin_embedding.")):
+            if t[-2] == "Wq":
+                out[k] = a[cmap] * np.sqrt(2.0) * csplit[:, None]
+            elif t[-1] in ("Wk", "Wv"):
+                out[k] = a[:, cmap]
+            else:
+                out[k] = lift_rows_cols(a)
+        elif k == "model.radial_embedding.radial_basis_fn.b":
+            from math import lgamma
+            out[k] = np.array([lgamma(R) - lgamma(j + 1) - lgamma(R - j) for j in range(R)])
+        elif k == "model.radial_embedding.radial_basis_fn.k":
+            out[k] = np.arange(R, dtype=np.int64)
+        elif k == "model.radial_embedding.radial_basis_fn.k_rev":
+            out[k] = (R - 1 - np.arange(R)).astype(np.int64)
+        elif k.startswith("model.euclidean_transformers."):
+            if t[-1] in ("W_q_inv", "W_k_inv", "W_v_inv", "W_q_ev", "W_k_ev"):
+                out[k] = a[np.arange(F2 // 32) // 2]
+            elif t[-1] == "degree_repeats":
+                out[k] = np.array(reps, dtype=np.int64)
+            elif t[-1] == "cg_rep":
+                out[k] = a[chmap]
+            elif t[-1] == "segment_ids":
+                out[k] = seg.astype(a.dtype)
+            elif t[-1] == "segment_sum_matrix":
+                out[k] = np.eye(S2)[seg]
+            elif "mlp_rbf" in t:
+                if ".mlp_rbf.0." in k:
+                    out[k] = (a @ elev)[cmap] if t[-1] == "weight" else a[cmap]
+                else:
+                    out[k] = lift_rows_cols(a) if t[-1] == "weight" else a[cmap]
+            elif "mlp_ev" in t:
+                if ".mlp_ev.0." in k:
+                    out[k] = a[hmap][:, smap] * ssplit[None, :] if t[-1] == "weight" else a[hmap]
+                else:
+                    out[k] = a[cmap][:, hmap] * hsplit[None, :] if t[-1] == "weight" else a[cmap]
+            elif t[-2] in ("layer_norm_inv_1", "layer_norm_inv_2"):
+                out[k] = a[cmap]
+            elif t[-3] == "mlp_1":
+                out[k] = lift_rows_cols(a) if t[-1] == "weight" else a[cmap]
+            elif t[-2] == "linear_layer":
+                out[k] = a[rowmap][:, rowmap] * colsplit[None, :] if t[-1] == "weight" else a[rowmap]
+            else:
+                raise KeyError("lifted_model: no rule for " + k)
+        elif k in ("model.atomic_energy_output_block.layers.0.weight",
+                   "model.partial_charges_output_block.transform_inv_features.0.weight",
+                   "model.hirshfeld_output_block.transform_features.0.weight",
+                   "model.c6_ratios_output_block.transform_features.0.weight"):
+            out[k] = lift_cols(a)
+        else:
+            out[k] = a  # per-element tables, head outputs, physical constants
+    for rec in manifest["tensors"]:
+        rec["shape"] = list(np.shape(out[rec["state_key"]]))
+    arch["invariant_features"] = F2
+    arch["attention_heads"] = F2 // 32
+    arch["euclidean_degree_channels"] = S2
+    arch["radial_basis_features"] = R
+    arch["parameter_elements"] = int(sum(np.asarray(out[r["state_key"]]).size for r in manifest["tensors"]
+                                         if r["role"] == "parameter"))
+    write_model(str(path), manifest, out)
+    return str(path)
+
+
+def degrees_model(path, degrees, base=MODEL):
+    """`base` (4 degree slots) with the slots' degrees set to `degrees` (four,
+    sorted, 1..4, repeats allowed: so3lr_architecture.cpp:246-293), e.g.
+    (1, 1, 2, 3) or (1, 2, 3, 3).  Every weight keeps its shape (the slot count
+    is unchanged); the equivariant width becomes sum(2l + 1), and the
+    Clebsch-Gordan weights, degree repeats and segment tables are those of
+    the new degrees (cg = 1/sqrt(2l + 1), as in the shipped model)."""
+    from so3lrxlammps_amd.model_file import read_model, write_model
+    manifest, arrays = read_model(base)
+    assert int(manifest["architecture"]["euclidean_degree_channels"]) == len(degrees) == 4
+    reps = [2 * l + 1 for l in degrees]
+    seg = np.concatenate([np.full(r, s) for s, r in enumerate(reps)])
+    cg = np.concatenate([np.full(r, 1.0 / np.sqrt(r)) for r in reps])
+    for k in list(arrays):
+        t = k.split(".")
+        if not k.startswith("model.euclidean_transformers."):
+            continue
+        if t[-1] == "degree_repeats":
+            arrays[k] = np.array(reps, dtype=np.int64)
+        elif t[-1] == "cg_rep":
+            arrays[k] = cg.copy()
+        elif t[-1] == "segment_ids":
+            arrays[k] = seg.astype(arrays[k].dtype)
+        elif t[-1] == "segment_sum_matrix":
+            arrays[k] = np.eye(len(degrees))[seg]
+    for rec in manifest["tensors"]:
+        rec["shape"] = list(np.shape(arrays[rec["state_key"]]))
     write_model(str(path), manifest, arrays)
     return str(path)
 
