@@ -2752,8 +2752,12 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     bytes_ += std::int64_t(v.size() * sizeof(double));
     return static_cast<const double *>(p);
   };
+  // models of other widths than v1's run on the generic kernels, which hold
+  // their own weights; the fused v1 kernels' weights are laid out below
+  if (a.generic) gen_ = std::make_unique<GenericPath>(m, up);
+  F_ = a.F;
   const std::size_t F = kF, R = kR, FH = kFH, NI = kNI, HW = kHW;
-  for (int b = 0; b < layers_; ++b) {
+  for (int b = 0; b < (a.generic ? 0 : layers_); ++b) {
     const std::string p = "model.euclidean_transformers." + std::to_string(b) + ".";
     const std::string at = p + "euclidean_attention_block.";
     BlockWeights &B = bw_[b];
@@ -2856,7 +2860,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     B.intb = up(m.f64(p + "interaction_block.linear_layer.bias", {NI}));
     B.intbp = up(bias_acc(m.f64(p + "interaction_block.linear_layer.bias", {NI}), NI));
   }
-  {
+  if (!a.generic) {
     const std::string e = "model.atomic_energy_output_block.", q = "model.partial_charges_output_block.",
                       h = "model.hirshfeld_output_block.";
     const std::string c6h = "model.c6_ratios_output_block.";
@@ -2934,13 +2938,15 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
       for (int j = 0; j < 256; ++j) t[j] = double(std::exp2(static_cast<long double>(j) / 256.0L));
       hw_.exp2_256 = up(t);
     }
+  }
+  {
     const auto &al = m.tensor("physical.reference_alphas");
     if (al.shape.size() != 1 || al.shape[0] < 8) throw std::runtime_error("SO3LR physical reference-table contract changed");
     hw_.n_ref = int(al.shape[0]);
     hw_.alpha_ref = up(m.f64("physical.reference_alphas", al.shape));
     hw_.c6_ref = up(m.f64("physical.reference_c6", al.shape));
   }
-  emb_w_ = m.f64("model.inv_feature_embedding.embedding.weight", {F, 118});
+  emb_w_ = m.f64("model.inv_feature_embedding.embedding.weight", {std::size_t(F_), 118});
   charge_spin_.load(m);
   zbl_.ke = a.zbl_ke; zbl_.rc = a.sr_cutoff; zbl_.switch_off = a.zbl_switch_off;
   zbl_.p = a.zbl_p; zbl_.d = a.zbl_d;
@@ -3000,6 +3006,8 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     top_ilist_[w] = buf("top_ilist"); top_off_[w] = buf("top_off"); top_neigh_[w] = buf("top_neigh");
     top_cnt_[w] = buf("top_cnt"); top_poff_[w] = buf("top_poff");
   }
+  if (gen_)
+    for (int i = 0; i < GenericPath::kBuffers; ++i) gbuf_[i] = buf("generic");
 }
 
 void Evaluator::set_box(const double lo[3], const double hi[3]) {
@@ -3026,7 +3034,8 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
     if (!(image_offsets[k + 1] > image_offsets[k]))
       throw std::invalid_argument("SO3LR: image offsets must increase strictly from 0 to the atom count "
                                   "(every image needs at least one atom)");
-  std::vector<double> x0(std::size_t(n) * kF);
+  const int F = F_;
+  std::vector<double> x0(std::size_t(n) * F);
   std::vector<int> img(n);
   for (std::int64_t k = 0; k < ni; ++k) {
     const std::int64_t lo = image_offsets[k], hi = image_offsets[k + 1];
@@ -3040,8 +3049,8 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
     const double inv = 1.0 / model_->arch().embedding_scale;
     for (std::int64_t i = lo; i < hi; ++i) {
       img[i] = int(k);
-      for (int c = 0; c < kF; ++c)
-        x0[std::size_t(i) * kF + c] = (emb_w_[c * 118 + (z[i] - 1)] + tab[(z[i] - 1) * kF + c]) * inv;
+      for (int c = 0; c < F; ++c)
+        x0[std::size_t(i) * F + c] = (emb_w_[c * 118 + (z[i] - 1)] + tab[(z[i] - 1) * F + c]) * inv;
     }
   }
   n_ = n;
@@ -3206,6 +3215,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   int *iact = nullptr, *iother = nullptr;
   double *partial = nullptr;
   auto carve_all = [&] {
+    if (!gen_) {
     xs = take<double>(xs_, (L + 1) * Nz * kF);
     evs = take<double>(evs_, (L + 1) * Nz * kE);
     qkv = take<double>(qkv_, L * Nz * 640);
@@ -3220,6 +3230,27 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     ainv = take<double>(ainv_, Nz * kF);
     act = take<double>(act_, Nz * HO); // MLP input (128 wide) and head activations (HO)
     hhead = take<double>(hhead_, Nz * HO);
+    gx = take<double>(gx_, Nz * kF);
+    gev = take<double>(gev_, Nz * kE);
+    gainv = take<double>(gainv_, Nz * kF);
+    gaev = take<double>(gaev_, Nz * kE);
+    gqkv = take<double>(gqkv_, Nz * 640);
+    ghead = take<double>(ghead_, Nz * HO);
+    qkis = qk_norm_ ? take<double>(qkis_, L * Nz * 16) : nullptr;
+    ps = take<double>(ps_, L * 4 * Pa);
+    // filter rows of every block for the scalar cross-check path; of blocks
+    // after 0 only on the MFMA path (block 0's are never read there)
+    pf = take<double>(pf_, std::size_t(naive_filters_ ? L : L - 1) * 256 * Pa);
+    palpha = take<double>(palpha_, L * 16 * Pa);
+    // the pair adjoints of the filters stay in registers on the MFMA path;
+    // it passes the head scalars (16 per pair) and dE/dfc between its kernels
+    df = naive_filters_ ? take<double>(df_, 256 * Pa) : nullptr;
+    dfc = take<double>(dfc_, Pa);
+    psc = naive_filters_ ? nullptr : take<double>(psc_, 16 * Pa);
+    ds = take<double>(ds_, 4 * Pa);
+    } else {
+      gen_->carve(int(N), int(PA), [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
+    }
     heff = take<double>(heff_, Nz);
     eatom = take<double>(eatom_, Nz);
     qraw = take<double>(qraw_, Nz);
@@ -3233,13 +3264,6 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     vlr = take<double>(vlr_, Nz * 6);
     parts = take<double>(elr_parts_, Nz * 2);
     ezbl = take<double>(ezbl_, Nz);
-    gx = take<double>(gx_, Nz * kF);
-    gev = take<double>(gev_, Nz * kE);
-    gainv = take<double>(gainv_, Nz * kF);
-    gaev = take<double>(gaev_, Nz * kE);
-    gqkv = take<double>(gqkv_, Nz * 640);
-    ghead = take<double>(ghead_, Nz * HO);
-    qkis = qk_norm_ ? take<double>(qkis_, L * Nz * 16) : nullptr;
     c6eff = c6_ ? take<double>(c6eff_, Nz) : nullptr;
     c6r = c6_ ? take<double>(c6r_, Nz) : nullptr;
     dc = c6_ ? take<double>(dc_, Nz) : nullptr;
@@ -3257,17 +3281,6 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     pY = take<double>(pY_, kE * Pa);
     pfc = take<double>(pfc_, Pa);
     pzbl = take<double>(pzbl_, 2 * Pa);
-    ps = take<double>(ps_, L * 4 * Pa);
-    // filter rows of every block for the scalar cross-check path; of blocks
-    // after 0 only on the MFMA path (block 0's are never read there)
-    pf = take<double>(pf_, std::size_t(naive_filters_ ? L : L - 1) * 256 * Pa);
-    palpha = take<double>(palpha_, L * 16 * Pa);
-    // the pair adjoints of the filters stay in registers on the MFMA path;
-    // it passes the head scalars (16 per pair) and dE/dfc between its kernels
-    df = naive_filters_ ? take<double>(df_, 256 * Pa) : nullptr;
-    dfc = take<double>(dfc_, Pa);
-    psc = naive_filters_ ? nullptr : take<double>(psc_, 16 * Pa);
-    ds = take<double>(ds_, 4 * Pa);
     dr = take<double>(dr_, Pa);
     dY = take<double>(dY_, kE * Pa);
     pg = take<double>(pg_, 3 * Pa);
@@ -3370,6 +3383,37 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     hipLaunchKernelGGL(k_inc_active, dim3(unsigned((2 * Pz + 255) / 256)), dim3(256), 0, s, int(2 * P), sr_inc, c2a,
                        pa, iact, iother);
   fill(dr, Pa);
+  // erf(r / sigma) by the polynomial of erf_lean when r / sigma stays within [0, 3]
+  const bool lean_erf = lr_.cutoff * lr_.inv_sigma <= 3.0;
+  auto long_range = [&] { timed("long_range", 1, [&] {
+#define SO3LR_LR(FULL, LEAN, SEP)                                                                                     \
+  if (FULL)                                                                                                          \
+    hipLaunchKernelGGL((k_lr<LrImages, LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc,              \
+                       LrImages{x, nullptr}, box_len_[0], box_len_[1], box_len_[2], z, q, hir, c6r, lr_,             \
+                       hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc, flr, vlr, parts);                                 \
+  else                                                                                                               \
+    hipLaunchKernelGGL((k_lr<LrRows, LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc,                \
+                       LrRows{lr_rows, lr_nodes, x}, 0.0, 0.0, 0.0, z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref,  \
+                       elr, dq, dh, dc, flr, vlr, parts);
+    if (c6_) {
+      if (lean_erf) { SO3LR_LR(shift_mode_, true, true) } else { SO3LR_LR(shift_mode_, false, true) }
+    } else {
+      if (lean_erf) { SO3LR_LR(shift_mode_, true, false) } else { SO3LR_LR(shift_mode_, false, false) }
+    }
+#undef SO3LR_LR
+  }); };
+  if (gen_) {
+    // generic widths: blocks and heads forward, the long range and the charge
+    // seeds as below, then heads and blocks in reverse to dE/dY, dE/dr
+    GContext G{s, int(N), int(PA), nact, pa, pr, pY, pfc, sr_off, iact, iother, z, x0, 1.0 / avg_, ln_eps_,
+               gamma_, rc_, norm1_, norm2_, qk_norm_ ? 1 : 0, &resid_, &x0l_, eatom, qraw, heff, hir, c6eff, c6r,
+               qseed, dh, dc, dY, dr};
+    gen_->forward(G);
+    hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
+    long_range();
+    hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
+    gen_->reverse(G);
+  } else {
   HIP_CHECK(hipMemcpyAsync(xs, x0, Nz * kF * sizeof(double), hipMemcpyDeviceToDevice, s));
   const unsigned gNF = unsigned((Nz * kF + 255) / 256);
   // residual scalars: block b's input is resid[b] x + x0[b] x0, x the block
@@ -3444,25 +3488,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   gemm(1, int(N), kF, int(HO), xf, kF, hw_.w1p, hw_.b1p, hhead, int(HO), hact);
   hipLaunchKernelGGL(k_heads, dim3(gN4), dim3(256), 0, s, int(N), z, hact, H, eatom, qraw, heff, hir, c6eff, c6r);
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
-  // erf(r / sigma) by the polynomial of erf_lean when r / sigma stays within [0, 3]
-  const bool lean_erf = lr_.cutoff * lr_.inv_sigma <= 3.0;
-  timed("long_range", 1, [&] {
-#define SO3LR_LR(FULL, LEAN, SEP)                                                                                     \
-  if (FULL)                                                                                                          \
-    hipLaunchKernelGGL((k_lr<LrImages, LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc,              \
-                       LrImages{x, nullptr}, box_len_[0], box_len_[1], box_len_[2], z, q, hir, c6r, lr_,             \
-                       hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc, flr, vlr, parts);                                 \
-  else                                                                                                               \
-    hipLaunchKernelGGL((k_lr<LrRows, LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc,                \
-                       LrRows{lr_rows, lr_nodes, x}, 0.0, 0.0, 0.0, z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref,  \
-                       elr, dq, dh, dc, flr, vlr, parts);
-    if (c6_) {
-      if (lean_erf) { SO3LR_LR(shift_mode_, true, true) } else { SO3LR_LR(shift_mode_, false, true) }
-    } else {
-      if (lean_erf) { SO3LR_LR(shift_mode_, true, false) } else { SO3LR_LR(shift_mode_, false, false) }
-    }
-#undef SO3LR_LR
-  });
+  long_range();
   hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, dq, qseed, 1);
   hipLaunchKernelGGL(k_heads_bwd, dim3(gN4), dim3(256), 0, s, int(N), z, hhead, qseed, dh, heff, dc, c6eff, H,
                      ghead);
@@ -3544,6 +3570,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                          gaev, gev);
     }
   }
+
+  }  // v1 widths
 
   // --- geometry reverse, forces, energies, virial ---
   hipLaunchKernelGGL(k_geom_bwd, dim3(ceil_div(PA, 256)), dim3(256), 0, s, nact, pv, pr,

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "device_math.hpp"
+#include "generic.hpp"
 #include "model.hpp"
 
 namespace so3lr_amd {
@@ -154,7 +155,10 @@ class Evaluator {
   bool qk_norm_ = false, c6_ = false;
   std::vector<double> resid_, x0l_;  // residual scalars per block (empty: none)
   ChargeSpin charge_spin_;
-  std::vector<double> emb_w_;  // (128, 118)
+  std::vector<double> emb_w_;  // (F, 118)
+  int F_ = kF;                 // invariant features
+  // the generic-width path (models other than the v1 widths) and its buffers
+  std::unique_ptr<GenericPath> gen_;
 
   // system
   std::int64_t n_ = 0, n_images_ = 0, n_rows_ = 0;
@@ -222,6 +226,7 @@ class Evaluator {
   Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
   Buffer *df_, *dfc_, *psc_, *ds_, *dr_, *dY_, *pg_;
   Buffer *iact_, *iother_;  // per step: incidence entry -> active pair * 2 + side, partner node
+  Buffer *gbuf_[GenericPath::kBuffers] = {};
   Buffer *probe_;           // the active-pair count of a new topology
   // capacity (pairs) of the active-pair buffers for the current topology; 0
   // until the first evaluation on it counts the active pairs

@@ -1,0 +1,980 @@
+// The generic-width evaluation (see generic.hpp): kernels and host side.
+//
+// Data layout in HBM (N nodes, P active-pair capacity, L blocks), natural
+// channel order throughout:
+//   node state per block b:  x[b] N x F, ev[b] N x E, qkv[b] N x 5F
+//                            (q | k | v | q_ev | k_ev, head-major inside each)
+//   pair state per block b:  s (NH slot invariants), f (F inv | F ev filters),
+//                            alpha (2 directions x (NH inv + NH ev))
+//   per evaluation:          rbf (R), and the reverse's df (2F), ds (NH),
+//                            dE/dr and dE/dY (24)
+// Pair p = {a, b}, v = x_a - x_b: direction 0 is the edge b -> a (receiver a,
+// harmonics Y(v/r)), direction 1 the edge a -> b ((-1)^l Y(v/r)).
+#include "generic.hpp"
+#include "evaluator.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <stdexcept>
+#include <string>
+
+namespace so3lr_amd {
+
+#define G_CHECK(expr)                                                                                    \
+  do {                                                                                                   \
+    hipError_t err_ = (expr);                                                                            \
+    if (err_ != hipSuccess) throw DeviceError(std::string("HIP error in ") + #expr + ": " + hipGetErrorString(err_)); \
+  } while (0)
+
+namespace {
+
+__device__ __forceinline__ double gsilu(double x) { return x / (1.0 + exp(-x)); }
+__device__ __forceinline__ double gsilu_prime(double x) {
+  const double s = 1.0 / (1.0 + exp(-x));
+  return s * (1.0 + x * (1.0 - s));
+}
+// Sum over the 64 lanes of a wavefront, the same value in every lane (lane
+// 0's butterfly result, broadcast).  All lanes must be active.
+__device__ __forceinline__ double wsum(double v) {
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return __shfl(v, 0, 64);
+}
+
+// ------------------------------------------------------------------ GEMM
+// Y (rows x O, leading dimension ldy) = epilogue(X (rows x K, ldx) op(W) + bias)
+// with op(W) = W^T for W (O x K) row-major (the model file's (out, in)
+// layout) or, WKO, W itself for W (K x O) row-major (the adjoint of a layer:
+// X W).  rows = min(*rows_dev, rows) when rows_dev is given (the active-pair
+// count on the device).  64 x 64 output tiles, 256 threads of 4 x 4 outputs,
+// K in steps of 16 through LDS.
+enum { EPI_STORE = 0, EPI_SILU, EPI_ACCUM, EPI_ADD, EPI_DSILU, EPI_DSILU_ADD };
+struct GemmArgs {
+  int rows;
+  const int *rows_dev;
+  int K, O;
+  const double *X;
+  int ldx;
+  const double *W;
+  const double *bias;
+  double *Y;
+  int ldy;
+  double *Y2;         // EPI_SILU: the pre-activation as well (may be null)
+  int ldy2;
+  const double *aux;  // EPI_DSILU*: silu' of aux
+  int ldaux;
+  const double *res;  // EPI_ADD, EPI_DSILU_ADD: added
+  int ldres;
+};
+
+template <int EPI, bool WKO>
+__global__ __launch_bounds__(256) void g_gemm(GemmArgs A) {
+  __shared__ double xs[16][65];
+  __shared__ double ws[16][65];
+  const int rows = A.rows_dev ? min(*A.rows_dev, A.rows) : A.rows;
+  const int row0 = blockIdx.x * 64, col0 = blockIdx.y * 64;
+  if (row0 >= rows) return;  // uniform over the block
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  double acc[4][4];
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+  for (int k0 = 0; k0 < A.K; k0 += 16) {
+    for (int q = 0; q < 4; ++q) {
+      const int idx = tid + 256 * q;
+      const int kk = idx & 15, rr = idx >> 4;
+      const int row = row0 + rr, k = k0 + kk;
+      xs[kk][rr] = (row < rows && k < A.K) ? A.X[std::size_t(row) * A.ldx + k] : 0.0;
+      if (WKO) {
+        const int cc = idx & 63, kw = idx >> 6;
+        const int col = col0 + cc, k2 = k0 + kw;
+        ws[kw][cc] = (col < A.O && k2 < A.K) ? A.W[std::size_t(k2) * A.O + col] : 0.0;
+      } else {
+        const int col = col0 + rr;
+        ws[kk][rr] = (col < A.O && k < A.K) ? A.W[std::size_t(col) * A.K + k] : 0.0;
+      }
+    }
+    __syncthreads();
+    for (int kk = 0; kk < 16; ++kk) {
+      double xv[4], wv[4];
+      for (int i = 0; i < 4; ++i) xv[i] = xs[kk][ty + 16 * i];
+      for (int j = 0; j < 4; ++j) wv[j] = ws[kk][tx + 16 * j];
+      for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) acc[i][j] = fma(xv[i], wv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + ty + 16 * i;
+    if (row >= rows) continue;
+    for (int j = 0; j < 4; ++j) {
+      const int col = col0 + tx + 16 * j;
+      if (col >= A.O) continue;
+      const double pre = acc[i][j] + (A.bias ? A.bias[col] : 0.0);
+      double *y = A.Y + std::size_t(row) * A.ldy + col;
+      if (EPI == EPI_STORE) {
+        *y = pre;
+      } else if (EPI == EPI_SILU) {
+        if (A.Y2) A.Y2[std::size_t(row) * A.ldy2 + col] = pre;
+        *y = gsilu(pre);
+      } else if (EPI == EPI_ACCUM) {
+        *y += pre;
+      } else if (EPI == EPI_ADD) {
+        *y = pre + A.res[std::size_t(row) * A.ldres + col];
+      } else if (EPI == EPI_DSILU) {
+        *y = acc[i][j] * gsilu_prime(A.aux[std::size_t(row) * A.ldaux + col]);
+      } else {
+        *y = A.res[std::size_t(row) * A.ldres + col] + acc[i][j] * gsilu_prime(A.aux[std::size_t(row) * A.ldaux + col]);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- node kernels
+// q, k, v, q_ev, k_ev per head: out[w][h*32 + o] = sum_k x[h*32 + k] W[w][h][k][o]
+// (kokkos_integrated_block0.cpp:257-287).  One thread per output.
+__global__ __launch_bounds__(256) void g_qkv(int N, int F, int NH, const double *__restrict__ x,
+                                             const double *__restrict__ w, double *__restrict__ qkv) {
+  const std::size_t t = std::size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= std::size_t(N) * 5 * F) return;
+  const int n = int(t / (5 * F)), r = int(t % (5 * F));
+  const int ws = r / F, c = r % F, h = c >> 5, o = c & 31;
+  const double *xr = x + std::size_t(n) * F + 32 * h;
+  const double *wm = w + (std::size_t(ws) * NH + h) * 1024 + o;
+  double s = 0.0;
+  for (int k = 0; k < 32; ++k) s += xr[k] * wm[32 * k];
+  qkv[t] = s;
+}
+
+// gx = gainv + sum_w W[w] gqkv[w] per head (the adjoint of g_qkv).
+__global__ __launch_bounds__(256) void g_qkv_bwd(int N, int F, int NH, const double *__restrict__ gqkv,
+                                                 const double *__restrict__ w, const double *__restrict__ gainv,
+                                                 double *__restrict__ gx) {
+  const std::size_t t = std::size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= std::size_t(N) * F) return;
+  const int n = int(t / F), c = int(t % F), h = c >> 5, k = c & 31;
+  double g = gainv[t];
+  for (int ws = 0; ws < 5; ++ws) {
+    const double *gr = gqkv + std::size_t(n) * 5 * F + std::size_t(ws) * F + 32 * h;
+    const double *wm = w + (std::size_t(ws) * NH + h) * 1024 + 32 * k;
+    double s = 0.0;
+    for (int o = 0; o < 32; ++o) s += wm[o] * gr[o];
+    g += s;
+  }
+  gx[t] = g;
+}
+
+// QK normalisation: each 32-wide head row of q, k, q_ev, k_ev scaled to unit
+// RMS (eps 1e-6; kokkos_integrated_block0.cpp:288-328), 1/rms kept.
+__device__ __forceinline__ int qk_row(int k) { return k < 2 ? k : k + 1; }  // q k (v) qe ke
+__global__ __launch_bounds__(256) void g_qk_norm(int N, int F, int NH, double *__restrict__ qkv,
+                                                 double *__restrict__ qkis) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= N * 4 * NH) return;
+  const int n = t / (4 * NH), k = (t / NH) % 4, h = t % NH;
+  double *row = qkv + std::size_t(n) * 5 * F + std::size_t(qk_row(k)) * F + 32 * h;
+  double ms = 0.0;
+  for (int c = 0; c < 32; ++c) ms += row[c] * row[c];
+  const double r = 1.0 / sqrt(ms / 32.0 + 1e-6);
+  for (int c = 0; c < 32; ++c) row[c] *= r;
+  qkis[t] = r;
+}
+// Through the normalisation: g <- r (g - y mean(g y)), y the normalised row.
+__global__ __launch_bounds__(256) void g_qk_norm_bwd(int N, int F, int NH, const double *__restrict__ qkv,
+                                                     const double *__restrict__ qkis, double *__restrict__ gqkv) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= N * 4 * NH) return;
+  const int n = t / (4 * NH), k = (t / NH) % 4, h = t % NH;
+  const std::size_t o = std::size_t(n) * 5 * F + std::size_t(qk_row(k)) * F + 32 * h;
+  double m = 0.0;
+  for (int c = 0; c < 32; ++c) m += gqkv[o + c] * qkv[o + c];
+  m /= 32.0;
+  const double r = qkis[t];
+  for (int c = 0; c < 32; ++c) gqkv[o + c] = r * (gqkv[o + c] - qkv[o + c] * m);
+}
+
+__global__ void g_axpby(std::size_t n, double a, double *x, double c, const double *x0) {
+  const std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = a * x[i] + c * x0[i];
+}
+__global__ void g_scale(std::size_t n, double a, double *g) {
+  const std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) g[i] *= a;
+}
+__global__ void g_fill(double *p, std::size_t n) {
+  const std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0;
+}
+
+// The normalisation of one node row held 4 channels per lane (c = lane + 64 j,
+// j < F / 64; kokkos_post_attention_block0.cpp:97-162): mode 0 affine
+// LayerNorm (biased variance), 1 RMSNorm without scale (w = 1, b = 0
+// given), 2 none.  h = normalised row, y = h w + b, is = 1 / sigma.
+__device__ __forceinline__ void g_norm_row(int F, int mode, const double *v, const double *w, const double *b,
+                                           double eps, int lane, double *y, double *h, double &is) {
+  const int J = F >> 6;
+  double s = 0.0;
+  for (int j = 0; j < J; ++j) s += v[j];
+  const double mean = mode == 0 ? wsum(s) / F : 0.0;
+  double q = 0.0;
+  for (int j = 0; j < J; ++j) q += (v[j] - mean) * (v[j] - mean);
+  is = mode == 2 ? 1.0 : 1.0 / sqrt(wsum(q) / F + eps);
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    h[j] = (v[j] - mean) * is;
+    y[j] = mode == 2 ? v[j] : h[j] * w[c] + b[c];
+  }
+}
+// Its adjoint: gx given gy, the normalised row h and 1 / sigma.
+__device__ __forceinline__ void g_norm_row_bwd(int F, int mode, const double *gy, const double *w,
+                                               const double *h, double is, int lane, double *gx) {
+  const int J = F >> 6;
+  if (mode == 2) {
+    for (int j = 0; j < J; ++j) gx[j] = gy[j];
+    return;
+  }
+  double gh[4], a = 0.0, bsum = 0.0;
+  for (int j = 0; j < J; ++j) {
+    gh[j] = mode == 0 ? gy[j] * w[lane + 64 * j] : gy[j];
+    a += gh[j];
+    bsum += gh[j] * h[j];
+  }
+  const double mg = mode == 0 ? wsum(a) / F : 0.0, mgx = wsum(bsum) / F;
+  for (int j = 0; j < J; ++j) gx[j] = is * (gh[j] - mg - h[j] * mgx);
+}
+
+// Attention messages, node-major (kokkos_integrated_block0.cpp:330-385):
+// node n receives from each incident pair's partner o the invariant message
+// fc alpha v_o and the equivariant fc alpha_ev Y (parity of the direction),
+// then the residual and the first normalisation (and silu of it, the MLP
+// input).  One wavefront per node.
+__global__ __launch_bounds__(256) void g_attn_msg(GDims d, int N, const int *__restrict__ inc_off,
+                                                  const int *__restrict__ iact, const int *__restrict__ iother,
+                                                  const double *__restrict__ x, const double *__restrict__ ev,
+                                                  const double *__restrict__ qkv, const double *__restrict__ pY,
+                                                  const double *__restrict__ pfc, const double *__restrict__ palpha,
+                                                  const double *__restrict__ lnw, const double *__restrict__ lnb,
+                                                  double eps, int mode, double *__restrict__ n1,
+                                                  double *__restrict__ n1hat, double *__restrict__ n1is,
+                                                  double *__restrict__ act, double *__restrict__ aev) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int F = d.F, NH = d.NH, E = d.E, J = F >> 6;
+  double di[4] = {0, 0, 0, 0}, de[2] = {0, 0};
+  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
+    const int e = iact[k];
+    if (e < 0) continue;
+    const int o = iother[k], p = e >> 1, side = e & 1;
+    const double fc = pfc[p];
+    const double *al = palpha + std::size_t(p) * 4 * NH + side * 2 * NH;
+    const double *vo = qkv + std::size_t(o) * 5 * F + 2 * F;
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      di[j] += fc * al[c >> 5] * vo[c];
+    }
+    for (int j = 0; j < 2; ++j) {
+      const int c = lane + 64 * j;
+      if (c < E) {
+        const int sl = d.slot[c];
+        const double y = pY[std::size_t(p) * 24 + d.sh[c]] * (side ? d.par[sl] : 1.0);
+        de[j] += fc * al[NH + sl] * y;
+      }
+    }
+  }
+  double v[4], y[4], h[4], is;
+  for (int j = 0; j < J; ++j) v[j] = x[std::size_t(n) * F + lane + 64 * j] + di[j];
+  g_norm_row(F, mode, v, lnw, lnb, eps, lane, y, h, is);
+  for (int j = 0; j < J; ++j) {
+    const std::size_t i = std::size_t(n) * F + lane + 64 * j;
+    n1[i] = y[j];
+    n1hat[i] = h[j];
+    act[i] = gsilu(y[j]);
+  }
+  if (lane == 0) n1is[n] = is;
+  for (int j = 0; j < 2; ++j) {
+    const int c = lane + 64 * j;
+    if (c < E) aev[std::size_t(n) * E + c] = ev[std::size_t(n) * E + c] + de[j];
+  }
+}
+
+// Interaction input: cat[n][F + s] = sum_{c in slot s} aev_c^2 cg_c
+// (kokkos_post_attention_block0.cpp:302-333).
+__global__ void g_cat_inv(GDims d, int N, const double *__restrict__ aev, const double *__restrict__ cg,
+                          double *__restrict__ cat) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * d.NH) return;
+  const int n = t / d.NH, s = t % d.NH;
+  double acc = 0.0;
+  for (int c = d.off[s]; c < d.off[s + 1]; ++c) {
+    const double a = aev[std::size_t(n) * d.E + c];
+    acc += a * a * cg[c];
+  }
+  cat[std::size_t(n) * d.NI + d.F + s] = acc;
+}
+
+// Block output: x' = norm2(p + t[0:F]), ev' = aev (1 + t[F + slot]).
+__global__ __launch_bounds__(256) void g_node_post(GDims d, int N, const double *__restrict__ cat,
+                                                   const double *__restrict__ tout, const double *__restrict__ aev,
+                                                   const double *__restrict__ lnw, const double *__restrict__ lnb,
+                                                   double eps, int mode, double *__restrict__ xout,
+                                                   double *__restrict__ evout, double *__restrict__ pre2hat,
+                                                   double *__restrict__ pre2is) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int F = d.F, J = F >> 6;
+  const std::size_t r = std::size_t(n) * d.NI;
+  double v[4], y[4], h[4], is;
+  for (int j = 0; j < J; ++j) v[j] = cat[r + lane + 64 * j] + tout[r + lane + 64 * j];
+  g_norm_row(F, mode, v, lnw, lnb, eps, lane, y, h, is);
+  for (int j = 0; j < J; ++j) {
+    const std::size_t i = std::size_t(n) * F + lane + 64 * j;
+    xout[i] = y[j];
+    pre2hat[i] = h[j];
+  }
+  if (lane == 0) pre2is[n] = is;
+  for (int j = 0; j < 2; ++j) {
+    const int c = lane + 64 * j;
+    if (c < d.E) evout[std::size_t(n) * d.E + c] = aev[std::size_t(n) * d.E + c] * (1.0 + tout[r + F + d.slot[c]]);
+  }
+}
+
+// Output heads from their hidden activations (kokkos_output_heads.cpp:137-176):
+// energy (HK), charge (HK), Hirshfeld and C6 ratio keys (64 each).
+__global__ __launch_bounds__(256) void g_heads(GDims d, int N, const int *__restrict__ z, const double *__restrict__ hact,
+                                               const double *__restrict__ hkey, GHeads H, double *__restrict__ eatom,
+                                               double *__restrict__ qraw, double *__restrict__ heff,
+                                               double *__restrict__ hir, double *__restrict__ c6eff,
+                                               double *__restrict__ c6r) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const double *a = hact + std::size_t(n) * d.HO;
+  double e = 0.0, q = 0.0;
+  for (int c = lane; c < d.HK; c += 64) {
+    e += H.ew2[c] * a[c];
+    q += H.qw2[c] * a[d.HK + c];
+  }
+  e = wsum(e);
+  q = wsum(q);
+  const int zz = z[n];
+  const double hk = wsum(H.hqemb[zz * 64 + lane] * hkey[std::size_t(n) * 128 + lane]);
+  const double ck = d.c6 ? wsum(H.cqemb[zz * 64 + lane] * hkey[std::size_t(n) * 128 + 64 + lane]) : 0.0;
+  if (lane == 0) {
+    eatom[n] = (e + H.eb2) * H.escale[zz - 1] + H.eshift[zz - 1];
+    qraw[n] = q + H.qb2 + H.qemb[zz];
+    const double hv = H.hvshift[zz] + hk / 8.0;  // q . k / sqrt(64)
+    heff[n] = hv;
+    hir[n] = fabs(hv);
+    if (d.c6) {
+      const double cv = H.cvshift[zz] + ck / 8.0;
+      c6eff[n] = cv;
+      c6r[n] = fabs(cv);
+    }
+  }
+}
+
+// Heads in reverse to the adjoint of their hidden pre-activations
+// (kokkos_output_heads.cpp:182-220): energy seed 1, charge seed qseed,
+// Hirshfeld dE/dh, C6 dE/dc.
+__global__ __launch_bounds__(256) void g_heads_bwd(GDims d, int N, const int *__restrict__ z,
+                                                   const double *__restrict__ hpre, const double *__restrict__ qseed,
+                                                   const double *__restrict__ dh, const double *__restrict__ heff,
+                                                   const double *__restrict__ dc, const double *__restrict__ c6eff,
+                                                   GHeads H, double *__restrict__ ghead) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int zz = z[n], HK = d.HK;
+  const double *pre = hpre + std::size_t(n) * d.HO;
+  double *g = ghead + std::size_t(n) * d.HO;
+  const double es = H.escale[zz - 1], qs = qseed[n];
+  for (int c = lane; c < HK; c += 64) {
+    g[c] = es * H.ew2[c] * gsilu_prime(pre[c]);
+    g[HK + c] = qs * H.qw2[c] * gsilu_prime(pre[HK + c]);
+  }
+  auto ratio = [&](double seed, double logit, const double *qemb, const double *w2, int at) {
+    const double sg = logit > 0.0 ? 1.0 : (logit < 0.0 ? -1.0 : 0.0);
+    const double s = seed * sg / 8.0;
+    double acc = 0.0;  // sum_j W2[j][lane] q_emb[z][j] s
+    for (int j = 0; j < 64; ++j) acc += w2[j * 64 + lane] * (s * qemb[zz * 64 + j]);
+    g[at + lane] = acc * gsilu_prime(pre[at + lane]);
+  };
+  ratio(dh[n], heff[n], H.hqemb, H.hw2, 2 * HK);
+  if (d.c6) ratio(dc[n], c6eff[n], H.cqemb, H.cw2, 2 * HK + 64);
+}
+
+// Reverse of the second normalisation and the ev gate (kokkos_post_attention_reverse.cpp):
+// gt[0:F] = dnorm2, gt[F + s] = sum_{c in s} gev_c aev_c, ga = gev (1 + t[F + slot]).
+__global__ __launch_bounds__(256) void g_ln2_bwd(GDims d, int N, const double *__restrict__ gx,
+                                                 const double *__restrict__ gev, const double *__restrict__ tout,
+                                                 const double *__restrict__ aev, const double *__restrict__ pre2hat,
+                                                 const double *__restrict__ pre2is, const double *__restrict__ lnw,
+                                                 int mode, double *__restrict__ gt, double *__restrict__ ga) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int F = d.F, J = F >> 6;
+  double gy[4], h[4], gxo[4];
+  for (int j = 0; j < J; ++j) {
+    gy[j] = gx[std::size_t(n) * F + lane + 64 * j];
+    h[j] = pre2hat[std::size_t(n) * F + lane + 64 * j];
+  }
+  g_norm_row_bwd(F, mode, gy, lnw, h, pre2is[n], lane, gxo);
+  const std::size_t r = std::size_t(n) * d.NI;
+  for (int j = 0; j < J; ++j) gt[r + lane + 64 * j] = gxo[j];
+  if (lane < d.NH) {
+    double acc = 0.0;
+    for (int c = d.off[lane]; c < d.off[lane + 1]; ++c) acc += gev[std::size_t(n) * d.E + c] * aev[std::size_t(n) * d.E + c];
+    gt[r + F + lane] = acc;
+  }
+  for (int j = 0; j < 2; ++j) {
+    const int c = lane + 64 * j;
+    if (c < d.E) ga[std::size_t(n) * d.E + c] = gev[std::size_t(n) * d.E + c] * (1.0 + tout[r + F + d.slot[c]]);
+  }
+}
+
+// gp = gt[0:F] + gcat[0:F]; ga += gcat[F + slot] 2 aev cg.
+__global__ void g_cat_bwd(GDims d, int N, const double *__restrict__ gt, const double *__restrict__ gcat,
+                          const double *__restrict__ aev, const double *__restrict__ cg, double *__restrict__ gp,
+                          double *__restrict__ ga) {
+  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int W = d.F + d.E;
+  if (t >= std::size_t(N) * W) return;
+  const int n = int(t / W), c = int(t % W);
+  const std::size_t r = std::size_t(n) * d.NI;
+  if (c < d.F) {
+    gp[std::size_t(n) * d.F + c] = gt[r + c] + gcat[r + c];
+  } else {
+    const int m = c - d.F;
+    const std::size_t i = std::size_t(n) * d.E + m;
+    ga[i] += gcat[r + d.F + d.slot[m]] * 2.0 * aev[i] * cg[m];
+  }
+}
+
+__global__ __launch_bounds__(256) void g_ln1_bwd(int F, int N, const double *__restrict__ gn1,
+                                                 const double *__restrict__ lnw, const double *__restrict__ n1hat,
+                                                 const double *__restrict__ n1is, int mode, double *__restrict__ gainv) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int J = F >> 6;
+  double gy[4], h[4], go[4];
+  for (int j = 0; j < J; ++j) {
+    gy[j] = gn1[std::size_t(n) * F + lane + 64 * j];
+    h[j] = n1hat[std::size_t(n) * F + lane + 64 * j];
+  }
+  g_norm_row_bwd(F, mode, gy, lnw, h, n1is[n], lane, go);
+  for (int j = 0; j < J; ++j) gainv[std::size_t(n) * F + lane + 64 * j] = go[j];
+}
+
+// The attention reverse's node gathers (kokkos_attention_scatter_reverse.cpp:280-500):
+// dq at the receiver, dk and dv at the sender of each direction.
+__global__ __launch_bounds__(256) void g_attn_bwd_node(GDims d, int N, const int *__restrict__ inc_off,
+                                                       const int *__restrict__ iact, const int *__restrict__ iother,
+                                                       const double *__restrict__ qkv, const double *__restrict__ pf,
+                                                       const double *__restrict__ pfc,
+                                                       const double *__restrict__ palpha,
+                                                       const double *__restrict__ psc,
+                                                       const double *__restrict__ gainv, double *__restrict__ gqkv) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int F = d.F, NH = d.NH, J = F >> 6;
+  double gq[4] = {0, 0, 0, 0}, gk[4] = {0, 0, 0, 0}, gv[4] = {0, 0, 0, 0}, gqe[4] = {0, 0, 0, 0},
+         gke[4] = {0, 0, 0, 0};
+  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
+    const int e = iact[k];
+    if (e < 0) continue;
+    const int o = iother[k], p = e >> 1, sn = e & 1, so = 1 - sn;
+    const double fc = pfc[p];
+    const double *sc = psc + std::size_t(p) * 4 * NH;
+    const double *al = palpha + std::size_t(p) * 4 * NH;
+    const double *fi = pf + std::size_t(p) * 2 * F, *fe = fi + F;
+    const double *qo = qkv + std::size_t(o) * 5 * F;
+    const double *go = gainv + std::size_t(o) * F;
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j, h = c >> 5;
+      // n receives (direction sn) from o
+      gq[j] += sc[sn * 2 * NH + h] * qo[F + c] * fi[c];
+      gqe[j] += sc[sn * 2 * NH + NH + h] * qo[4 * F + c] * fe[c];
+      // n sends (direction so) to o
+      gk[j] += sc[so * 2 * NH + h] * qo[c] * fi[c];
+      gv[j] += fc * al[so * 2 * NH + h] * go[c];
+      gke[j] += sc[so * 2 * NH + NH + h] * qo[3 * F + c] * fe[c];
+    }
+  }
+  double *g = gqkv + std::size_t(n) * 5 * F;
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    g[c] = gq[j];
+    g[F + c] = gk[j];
+    g[2 * F + c] = gv[j];
+    g[3 * F + c] = gqe[j];
+    g[4 * F + c] = gke[j];
+  }
+}
+
+// gev = ga + sum over incident pairs of 2 (ev_n - ev_o) cg ds[slot]: the
+// edge invariants' adjoint (kokkos_block2_attention_input_reverse.cpp:144-196).
+__global__ __launch_bounds__(256) void g_ev_bwd(GDims d, int N, const int *__restrict__ inc_off,
+                                                const int *__restrict__ iact, const int *__restrict__ iother,
+                                                const double *__restrict__ ev, const double *__restrict__ cg,
+                                                const double *__restrict__ ds, const double *__restrict__ ga,
+                                                double *__restrict__ gev) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int E = d.E;
+  for (int j = 0; j < 2; ++j) {
+    const int c = lane + 64 * j;
+    if (c >= E) continue;
+    const int sl = d.slot[c];
+    const double en = ev[std::size_t(n) * E + c];
+    double acc = ga[std::size_t(n) * E + c];
+    for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
+      const int e = iact[k];
+      if (e < 0) continue;
+      acc += 2.0 * (en - ev[std::size_t(iother[k]) * E + c]) * cg[c] * ds[std::size_t(e >> 1) * d.NH + sl];
+    }
+    gev[std::size_t(n) * E + c] = acc;
+  }
+}
+
+// ------------------------------------------------------------- pair kernels
+// Bernstein basis of the distance (kokkos_integrated_block0.cpp:117-164), one
+// thread per active pair.
+__global__ void g_rbf(int R, const int *nact, int cap, const double *__restrict__ pr, double gamma,
+                      const double *__restrict__ b, const double *__restrict__ kk, const double *__restrict__ kr,
+                      double *__restrict__ rbf) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= min(*nact, cap)) return;
+  double xb = exp(-gamma * pr[p]);
+  xb = xb < 1e-6 ? 1e-6 : (xb > 1.0 - 1e-6 ? 1.0 - 1e-6 : xb);
+  const double lx = log(xb), l1x = log(1.0 - xb);
+  for (int k = 0; k < R; ++k) rbf[std::size_t(p) * R + k] = exp(b[k] + kk[k] * lx + kr[k] * l1x);
+}
+
+// Equivariant invariants per slot: s = sum_{c in slot} (ev_a - ev_b)^2 cg
+// (kokkos_integrated_block0.cpp:166-195).
+__global__ void g_pair_inv(GDims d, const int *nact, int cap, const int *__restrict__ pa,
+                           const double *__restrict__ ev, const double *__restrict__ cg, double *__restrict__ ps) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int p = t / d.NH, s = t % d.NH;
+  if (p >= min(*nact, cap)) return;
+  const double *ea = ev + std::size_t(pa[2 * p]) * d.E, *eb = ev + std::size_t(pa[2 * p + 1]) * d.E;
+  double acc = 0.0;
+  for (int c = d.off[s]; c < d.off[s + 1]; ++c) {
+    const double x = ea[c] - eb[c];
+    acc += x * x * cg[c];
+  }
+  ps[std::size_t(p) * d.NH + s] = acc;
+}
+
+// Attention logits per pair, direction and head (kokkos_integrated_block0.cpp:330-360):
+// alpha = <q_receiver, k_sender (.) f> / norm (inv: q k f_inv, ev: q_ev k_ev f_ev).
+__global__ void g_alpha(GDims d, const int *nact, int cap, const int *__restrict__ pa,
+                        const double *__restrict__ qkv, const double *__restrict__ pf, double inv_avg,
+                        double *__restrict__ palpha) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int NH = d.NH, F = d.F;
+  const int p = t / (4 * NH), r = t % (4 * NH);
+  if (p >= min(*nact, cap)) return;
+  const int side = r / (2 * NH), which = (r / NH) & 1, h = r % NH;
+  const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
+  const double *qr = qkv + std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + 32 * h;
+  const double *ks = qkv + std::size_t(snd) * 5 * F + (which ? 4 * F : F) + 32 * h;
+  const double *f = pf + std::size_t(p) * 2 * F + (which ? F : 0) + 32 * h;
+  double acc = 0.0;
+  for (int c = 0; c < 32; ++c) acc += qr[c] * ks[c] * f[c];
+  palpha[t] = acc * inv_avg;
+}
+
+// Attention reverse per pair, direction and head: ci = <gainv_r, v_s>_h,
+// ce = <gaev_r, Y'>_slot h; psc = fc c norm (the logits' adjoints).
+__global__ void g_attn_bwd_scal(GDims d, const int *nact, int cap, const int *__restrict__ pa,
+                                const double *__restrict__ qkv, const double *__restrict__ pY,
+                                const double *__restrict__ pfc, const double *__restrict__ gainv,
+                                const double *__restrict__ ga, double inv_avg, double *__restrict__ cpart,
+                                double *__restrict__ psc) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int NH = d.NH, F = d.F;
+  const int p = t / (2 * NH), r = t % (2 * NH);
+  if (p >= min(*nact, cap)) return;
+  const int side = r / NH, h = r % NH;
+  const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
+  const double *g = gainv + std::size_t(rcv) * F + 32 * h;
+  const double *v = qkv + std::size_t(snd) * 5 * F + 2 * F + 32 * h;
+  double ci = 0.0;
+  for (int c = 0; c < 32; ++c) ci += g[c] * v[c];
+  const double pr = side ? d.par[h] : 1.0;
+  double ce = 0.0;
+  for (int c = d.off[h]; c < d.off[h + 1]; ++c) ce += ga[std::size_t(rcv) * d.E + c] * pY[std::size_t(p) * 24 + d.sh[c]] * pr;
+  const double fc = pfc[p];
+  const std::size_t o = std::size_t(p) * 4 * NH + side * 2 * NH;
+  cpart[o + h] = ci;
+  cpart[o + NH + h] = ce;
+  psc[o + h] = fc * ci * inv_avg;
+  psc[o + NH + h] = fc * ce * inv_avg;
+}
+
+// Per pair: dE/dY of the 24 harmonics (side-0 orientation; m = 0..23) and
+// dE/dfc (m = 24).  The first reverse block writes dY, the others add.
+__global__ void g_attn_bwd_pair(GDims d, const int *nact, int cap, const int *__restrict__ pa,
+                                const double *__restrict__ pfc, const double *__restrict__ palpha,
+                                const double *__restrict__ cpart, const double *__restrict__ ga, int first,
+                                double *__restrict__ dY, double *__restrict__ dfc) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int p = t / 25, m = t % 25, NH = d.NH;
+  if (p >= min(*nact, cap)) return;
+  const double *al = palpha + std::size_t(p) * 4 * NH;
+  if (m == 24) {
+    const double *cp = cpart + std::size_t(p) * 4 * NH;
+    double acc = 0.0;
+    for (int side = 0; side < 2; ++side)
+      for (int h = 0; h < NH; ++h)
+        acc += cp[side * 2 * NH + h] * al[side * 2 * NH + h] + cp[side * 2 * NH + NH + h] * al[side * 2 * NH + NH + h];
+    dfc[p] = acc;
+    return;
+  }
+  const double fc = pfc[p];
+  double acc = 0.0;
+  for (int side = 0; side < 2; ++side) {
+    const int rcv = pa[2 * p + side];
+    for (int c = 0; c < d.E; ++c) {
+      if (d.sh[c] != m) continue;
+      const int sl = d.slot[c];
+      acc += ga[std::size_t(rcv) * d.E + c] * fc * al[side * 2 * NH + NH + sl] * (side ? d.par[sl] : 1.0);
+    }
+  }
+  double *y = dY + std::size_t(p) * 24 + m;
+  *y = first ? acc : *y + acc;
+}
+
+// The filters' adjoints per pair, both directions summed (the filter is
+// shared): df_inv = sum_side psc_inv q_r k_s, df_ev = sum_side psc_ev q_ev k_ev.
+__global__ void g_attn_bwd_df(GDims d, const int *nact, int cap, const int *__restrict__ pa,
+                              const double *__restrict__ qkv, const double *__restrict__ psc,
+                              double *__restrict__ df) {
+  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int F = d.F, NH = d.NH;
+  const std::size_t p = t / (2 * F);
+  const int c = int(t % (2 * F));
+  if (p >= std::size_t(min(*nact, cap))) return;
+  const int which = c / F, cc = c % F, h = cc >> 5;
+  double acc = 0.0;
+  for (int side = 0; side < 2; ++side) {
+    const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
+    const double qv = qkv[std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + cc];
+    const double kv = qkv[std::size_t(snd) * 5 * F + (which ? 4 * F : F) + cc];
+    acc += psc[p * 4 * NH + side * 2 * NH + which * NH + h] * qv * kv;
+  }
+  df[t] = acc;
+}
+
+// dE/dr of the pair from the cutoff and the radial basis.
+__global__ void g_pair_radial_bwd(int R, const int *nact, int cap, const double *__restrict__ pr,
+                                  const double *__restrict__ dfc, const double *__restrict__ grbf,
+                                  const double *__restrict__ rbf, const double *__restrict__ kk,
+                                  const double *__restrict__ kr, double gamma, double rc, double *__restrict__ dr) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= min(*nact, cap)) return;
+  const double r = pr[p];
+  double grad = 0.0;
+  if (r < rc) {
+    const double t = r / rc;
+    grad += dfc[p] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
+  }
+  const double xb = exp(-gamma * r);
+  if (xb > 1e-6 && xb < 1.0 - 1e-6) {
+    const double a = gamma * xb / (1.0 - xb);
+    for (int k = 0; k < R; ++k)
+      grad += grbf[std::size_t(p) * R + k] * rbf[std::size_t(p) * R + k] * (-gamma * kk[k] + a * kr[k]);
+  }
+  dr[p] += grad;
+}
+
+unsigned blocks_for(std::size_t n, int per) { return unsigned((n + std::size_t(per) - 1) / std::size_t(per)); }
+
+}  // namespace
+
+// ------------------------------------------------------------------ host side
+namespace {
+enum Buf {
+  XS = 0, EVS, QKV, QKIS, AEV, N1, N1HAT, N1IS, HPRE, TOUT, PRE2HAT, PRE2IS,
+  ACT, HID, CAT, HACT, HHPRE, HKEY, GHEAD,
+  GX, GEV, GT, GCAT, GA, GP, GHID, GN1, GAINV, GQKV,
+  RBF, PS, PF, PALPHA, HT, H2T, GH, GH2, DF, PSC, CPART, DFC, DS, GRBF,
+  NBUF
+};
+static_assert(NBUF <= GenericPath::kBuffers, "generic path buffer table");
+
+template <int EPI, bool WKO>
+void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const double *X, int ldx, const double *W,
+          const double *bias, double *Y, int ldy, const double *aux = nullptr, int ldaux = 0,
+          const double *res = nullptr, int ldres = 0, double *Y2 = nullptr, int ldy2 = 0) {
+  if (rows <= 0) return;
+  GemmArgs A{rows, rows_dev, K, O, X, ldx, W, bias, Y, ldy, Y2, ldy2, aux, ldaux, res, ldres};
+  hipLaunchKernelGGL((g_gemm<EPI, WKO>), dim3(blocks_for(std::size_t(rows), 64), blocks_for(std::size_t(O), 64)),
+                     dim3(256), 0, s, A);
+}
+}  // namespace
+
+GenericPath::GenericPath(const Model &m, const std::function<const double *(const std::vector<double> &)> &up) {
+  const Architecture &a = m.arch();
+  GDims &d = d_;
+  d.F = a.F;
+  d.NH = a.heads;
+  d.R = a.R;
+  d.FH = a.F / 4;
+  d.HK = a.head_hidden;
+  d.NI = a.F + a.heads;
+  d.c6 = a.c6_head ? 1 : 0;
+  d.HO = 2 * d.HK + 64 + (d.c6 ? 64 : 0);
+  if (d.F % 64 != 0 || d.F > 256 || d.NH > 8 || d.NH * 32 != d.F)
+    throw std::logic_error("SO3LR: generic path given widths outside F = 64..256 in heads of 32");
+  int off = 0;
+  d.off[0] = 0;
+  for (int s = 0; s < d.NH; ++s) {
+    const int l = a.degrees[std::size_t(s)];
+    for (int k = 0; k < 2 * l + 1; ++k) {
+      d.slot[off + k] = static_cast<signed char>(s);
+      d.sh[off + k] = static_cast<signed char>(l * l - 1 + k);  // unique harmonics of l start at l^2 - 1
+    }
+    off += 2 * l + 1;
+    d.off[s + 1] = static_cast<signed char>(off);
+    d.par[s] = (l & 1) ? -1.0 : 1.0;
+  }
+  d.E = off;
+  layers_ = a.layers;
+  const std::size_t F = std::size_t(d.F), R = std::size_t(d.R), FH = std::size_t(d.FH), NH = std::size_t(d.NH),
+                    NI = std::size_t(d.NI), E = std::size_t(d.E), HK = std::size_t(d.HK), HH = 64;
+  for (int b = 0; b < layers_; ++b) {
+    const std::string p = "model.euclidean_transformers." + std::to_string(b) + ".";
+    const std::string at = p + "euclidean_attention_block.";
+    GBlock &B = bw_[b];
+    std::vector<double> qkv;
+    for (const char *nm : {"W_q_inv", "W_k_inv", "W_v_inv", "W_q_ev", "W_k_ev"}) {
+      const auto w = m.f64(at + nm, {NH, 32, 32});
+      qkv.insert(qkv.end(), w.begin(), w.end());
+    }
+    B.wqkv = up(qkv);
+    for (int k = 0; k < 2; ++k) {
+      // the transformer-level filter nets (kokkos_integrated_block0.cpp:507-512)
+      const std::string f = p + (k == 0 ? "filter_net_inv." : "filter_net_ev.");
+      B.w0[k] = up(m.f64(f + "mlp_rbf.0.weight", {F, R}));
+      B.b0[k] = up(m.f64(f + "mlp_rbf.0.bias", {F}));
+      B.w1[k] = up(m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.weight", {F, F}));
+      B.b1[k] = up(m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F}));
+      B.e0[k] = up(m.f64(f + "mlp_ev.0.weight", {FH, NH}));
+      B.eb0[k] = up(m.f64(f + "mlp_ev.0.bias", {FH}));
+      B.e1[k] = up(m.f64(f + "mlp_ev.mlp_ev_layer_1.0.weight", {F, FH}));
+      B.eb1[k] = up(m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F}));
+    }
+    B.att_cg = up(m.f64(at + "so3_conv_invariants.cg_rep", {E}));
+    B.int_cg = up(m.f64(p + "interaction_block.so3_conv_invariants.cg_rep", {E}));
+    const std::vector<double> ones(F, 1.0), zeros(F, 0.0);
+    const bool ln1 = a.norm1 == NormMode::Layer, ln2 = a.norm2 == NormMode::Layer;
+    B.ln1w = up(ln1 ? m.f64(p + "layer_norm_inv_1.weight", {F}) : ones);
+    B.ln1b = up(ln1 ? m.f64(p + "layer_norm_inv_1.bias", {F}) : zeros);
+    B.ln2w = up(ln2 ? m.f64(p + "layer_norm_inv_2.weight", {F}) : ones);
+    B.ln2b = up(ln2 ? m.f64(p + "layer_norm_inv_2.bias", {F}) : zeros);
+    B.m1 = up(m.f64(p + "mlp_1.1.weight", {F, F}));
+    B.m1b = up(m.f64(p + "mlp_1.1.bias", {F}));
+    B.m2 = up(m.f64(p + "mlp_1.3.weight", {F, F}));
+    B.m2b = up(m.f64(p + "mlp_1.3.bias", {F}));
+    B.wi = up(m.f64(p + "interaction_block.linear_layer.weight", {NI, NI}));
+    B.bi = up(m.f64(p + "interaction_block.linear_layer.bias", {NI}));
+  }
+  const std::string e = "model.atomic_energy_output_block.", q = "model.partial_charges_output_block.",
+                    h = "model.hirshfeld_output_block.", c6h = "model.c6_ratios_output_block.";
+  std::vector<double> w1 = m.f64(e + "layers.0.weight", {HK, F});
+  std::vector<double> b1 = m.f64(e + "layers.0.bias", {HK});
+  auto append = [](std::vector<double> &dst, const std::vector<double> &src) { dst.insert(dst.end(), src.begin(), src.end()); };
+  append(w1, m.f64(q + "transform_inv_features.0.weight", {HK, F}));
+  append(b1, m.f64(q + "transform_inv_features.0.bias", {HK}));
+  append(w1, m.f64(h + "transform_features.0.weight", {HH, F}));
+  append(b1, m.f64(h + "transform_features.0.bias", {HH}));
+  if (d.c6) {
+    append(w1, m.f64(c6h + "transform_features.0.weight", {HH, F}));
+    append(b1, m.f64(c6h + "transform_features.0.bias", {HH}));
+  }
+  hw_.w1 = up(w1);
+  hw_.b1 = up(b1);
+  hw_.hw2 = up(m.f64(h + "transform_features.2.weight", {HH, HH}));
+  hw_.hb2 = up(m.f64(h + "transform_features.2.bias", {HH}));
+  hw_.hqemb = up(m.f64(h + "q_embedding.weight", {100, HH}));
+  hw_.hvshift = up(m.f64(h + "v_shift_embedding.weight", {100, 1}));
+  hw_.cw2 = hw_.cb2 = hw_.cqemb = hw_.cvshift = nullptr;
+  if (d.c6) {
+    hw_.cw2 = up(m.f64(c6h + "transform_features.2.weight", {HH, HH}));
+    hw_.cb2 = up(m.f64(c6h + "transform_features.2.bias", {HH}));
+    hw_.cqemb = up(m.f64(c6h + "q_embedding.weight", {100, HH}));
+    hw_.cvshift = up(m.f64(c6h + "v_shift_embedding.weight", {100, 1}));
+  }
+  hw_.ew2 = up(m.f64(e + "final_layer.weight", {1, HK}));
+  hw_.eb2 = m.f64(e + "final_layer.bias", {1})[0];
+  hw_.qw2 = up(m.f64(q + "transform_inv_features.2.weight", {1, HK}));
+  hw_.qb2 = m.f64(q + "transform_inv_features.2.bias", {1})[0];
+  hw_.escale = up(m.f64(e + "energy_scales.weight", {1, 118}));
+  hw_.eshift = up(m.f64(e + "energy_shifts", {118}));
+  hw_.qemb = up(m.f64(q + "atomic_embedding.weight", {100, 1}));
+  hw_.rbf_b = up(m.f64("model.radial_embedding.radial_basis_fn.b", {R}));
+  const auto kk = m.i64("model.radial_embedding.radial_basis_fn.k", {R});
+  const auto kr = m.i64("model.radial_embedding.radial_basis_fn.k_rev", {R});
+  hw_.rbf_k = up(std::vector<double>(kk.begin(), kk.end()));
+  hw_.rbf_kr = up(std::vector<double>(kr.begin(), kr.end()));
+}
+
+void GenericPath::carve(int N, int cap, const std::function<double *(int, std::size_t)> &take) {
+  const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1)), L = std::size_t(layers_);
+  const std::size_t F = std::size_t(d_.F), E = std::size_t(d_.E), NH = std::size_t(d_.NH), NI = std::size_t(d_.NI),
+                    R = std::size_t(d_.R), FH = std::size_t(d_.FH), HO = std::size_t(d_.HO);
+  const std::size_t sizes[NBUF] = {
+      (L + 1) * n * F, (L + 1) * n * E, L * n * 5 * F, L * n * 4 * NH, L * n * E, L * n * F, L * n * F, L * n,
+      L * n * F, L * n * NI, L * n * F, L * n,
+      n * F, n * F, n * NI, n * HO, n * HO, n * 128, n * HO,
+      n * F, n * E, n * NI, n * NI, n * E, n * F, n * F, n * F, n * F, n * 5 * F,
+      P * R, L * P * NH, L * P * 2 * F, L * P * 4 * NH, P * F, P * FH, P * F, P * FH, P * 2 * F, P * 4 * NH,
+      P * 4 * NH, P, P * NH, P * R};
+  for (int i = 0; i < NBUF; ++i) b_[i] = take(i, sizes[i]);
+}
+
+void GenericPath::forward(const GContext &c) {
+  const GDims &d = d_;
+  const hipStream_t s = c.s;
+  const int N = c.N, cap = c.cap, F = d.F, E = d.E, NH = d.NH, NI = d.NI, R = d.R, FH = d.FH;
+  const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1));
+  const unsigned g4 = blocks_for(n, 4);
+  const unsigned gP = blocks_for(P, 256);
+  double *xs = b_[XS], *evs = b_[EVS];
+  G_CHECK(hipMemcpyAsync(xs, c.x0, n * F * sizeof(double), hipMemcpyDeviceToDevice, s));
+  if (!c.resid->empty())
+    hipLaunchKernelGGL(g_axpby, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, n * F, (*c.resid)[0], xs,
+                       (*c.x0l)[0], c.x0);
+  hipLaunchKernelGGL(g_fill, dim3(blocks_for(n * E, 256)), dim3(256), 0, s, evs, n * E);
+  hipLaunchKernelGGL(g_rbf, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, c.gamma, hw_.rbf_b, hw_.rbf_k,
+                     hw_.rbf_kr, b_[RBF]);
+  for (int b = 0; b < layers_; ++b) {
+    const GBlock &B = bw_[b];
+    double *xb = xs + b * n * F, *evb = evs + b * n * E;
+    double *qb = b_[QKV] + b * n * 5 * F, *aevb = b_[AEV] + b * n * E;
+    double *n1b = b_[N1] + b * n * F, *n1hb = b_[N1HAT] + b * n * F, *n1ib = b_[N1IS] + b * n;
+    double *hpb = b_[HPRE] + b * n * F, *tb = b_[TOUT] + b * n * NI;
+    double *p2h = b_[PRE2HAT] + b * n * F, *p2i = b_[PRE2IS] + b * n;
+    double *psb = b_[PS] + b * P * NH, *pfb = b_[PF] + b * P * 2 * F, *pab = b_[PALPHA] + b * P * 4 * NH;
+    hipLaunchKernelGGL(g_qkv, dim3(blocks_for(n * 5 * F, 256)), dim3(256), 0, s, N, F, NH, xb, B.wqkv, qb);
+    if (c.qk_norm)
+      hipLaunchKernelGGL(g_qk_norm, dim3(blocks_for(n * 4 * NH, 256)), dim3(256), 0, s, N, F, NH, qb,
+                         b_[QKIS] + b * n * 4 * NH);
+    // pair invariants and both filters (kokkos_integrated_block0.cpp:166-255)
+    hipLaunchKernelGGL(g_pair_inv, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, evb,
+                       B.att_cg, psb);
+    for (int w = 0; w < 2; ++w) {
+      gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], F);
+      gemm<EPI_STORE, false>(s, cap, c.nact, F, F, b_[HT], F, B.w1[w], B.b1[w], pfb + w * F, 2 * F);
+      gemm<EPI_SILU, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[H2T], FH);
+      gemm<EPI_ACCUM, false>(s, cap, c.nact, FH, F, b_[H2T], FH, B.e1[w], B.eb1[w], pfb + w * F, 2 * F);
+    }
+    hipLaunchKernelGGL(g_alpha, dim3(blocks_for(P * 4 * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, pfb,
+                       c.inv_avg, pab);
+    hipLaunchKernelGGL(g_attn_msg, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
+                       c.pfc, pab, B.ln1w, B.ln1b, c.ln_eps, c.norm1, n1b, n1hb, n1ib, b_[ACT], aevb);
+    // post-attention node chain (kokkos_post_attention_block0.cpp:165-300)
+    gemm<EPI_SILU, false>(s, N, nullptr, F, F, b_[ACT], F, B.m1, B.m1b, b_[HID], F, nullptr, 0, nullptr, 0, hpb, F);
+    gemm<EPI_ADD, false>(s, N, nullptr, F, F, b_[HID], F, B.m2, B.m2b, b_[CAT], NI, nullptr, 0, n1b, F);
+    hipLaunchKernelGGL(g_cat_inv, dim3(blocks_for(n * NH, 256)), dim3(256), 0, s, d, N, aevb, B.int_cg, b_[CAT]);
+    gemm<EPI_STORE, false>(s, N, nullptr, NI, NI, b_[CAT], NI, B.wi, B.bi, tb, NI);
+    hipLaunchKernelGGL(g_node_post, dim3(g4), dim3(256), 0, s, d, N, b_[CAT], tb, aevb, B.ln2w, B.ln2b, c.ln_eps,
+                       c.norm2, xs + (b + 1) * n * F, evs + (b + 1) * n * E, p2h, p2i);
+    if (!c.resid->empty() && b + 1 < layers_)
+      hipLaunchKernelGGL(g_axpby, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, n * F, (*c.resid)[b + 1],
+                         xs + (b + 1) * n * F, (*c.x0l)[b + 1], c.x0);
+  }
+  // output heads (kokkos_output_heads.cpp:137-176)
+  const double *xf = xs + std::size_t(layers_) * n * F;
+  gemm<EPI_SILU, false>(s, N, nullptr, F, d.HO, xf, F, hw_.w1, hw_.b1, b_[HACT], d.HO, nullptr, 0, nullptr, 0,
+                        b_[HHPRE], d.HO);
+  gemm<EPI_STORE, false>(s, N, nullptr, 64, 64, b_[HACT] + 2 * d.HK, d.HO, hw_.hw2, hw_.hb2, b_[HKEY], 128);
+  if (d.c6)
+    gemm<EPI_STORE, false>(s, N, nullptr, 64, 64, b_[HACT] + 2 * d.HK + 64, d.HO, hw_.cw2, hw_.cb2, b_[HKEY] + 64,
+                           128);
+  hipLaunchKernelGGL(g_heads, dim3(g4), dim3(256), 0, s, d, N, c.z, b_[HACT], b_[HKEY], hw_, c.eatom, c.qraw,
+                     c.heff, c.hir, c.c6eff, c.c6r);
+  G_CHECK(hipGetLastError());
+}
+
+void GenericPath::reverse(const GContext &c) {
+  const GDims &d = d_;
+  const hipStream_t s = c.s;
+  const int N = c.N, cap = c.cap, F = d.F, E = d.E, NH = d.NH, NI = d.NI, R = d.R, FH = d.FH;
+  const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1));
+  const unsigned g4 = blocks_for(n, 4);
+  const unsigned gP = blocks_for(P, 256);
+  // heads in reverse to dE/dx of the last block's output
+  hipLaunchKernelGGL(g_heads_bwd, dim3(g4), dim3(256), 0, s, d, N, c.z, b_[HHPRE], c.qseed, c.dh, c.heff, c.dc,
+                     c.c6eff, hw_, b_[GHEAD]);
+  gemm<EPI_STORE, true>(s, N, nullptr, d.HO, F, b_[GHEAD], d.HO, hw_.w1, nullptr, b_[GX], F);
+  hipLaunchKernelGGL(g_fill, dim3(blocks_for(n * E, 256)), dim3(256), 0, s, b_[GEV], n * E);
+  double *gx = b_[GX], *gev = b_[GEV];
+  for (int b = layers_ - 1; b >= 0; --b) {
+    const GBlock &B = bw_[b];
+    const double *evb = b_[EVS] + b * n * E;
+    double *qb = b_[QKV] + b * n * 5 * F, *aevb = b_[AEV] + b * n * E;
+    double *n1b = b_[N1] + b * n * F, *n1hb = b_[N1HAT] + b * n * F, *n1ib = b_[N1IS] + b * n;
+    double *hpb = b_[HPRE] + b * n * F, *tb = b_[TOUT] + b * n * NI;
+    double *p2h = b_[PRE2HAT] + b * n * F, *p2i = b_[PRE2IS] + b * n;
+    double *psb = b_[PS] + b * P * NH, *pfb = b_[PF] + b * P * 2 * F, *pab = b_[PALPHA] + b * P * 4 * NH;
+    // post-attention chain in reverse (kokkos_post_attention_reverse.cpp:107-449)
+    hipLaunchKernelGGL(g_ln2_bwd, dim3(g4), dim3(256), 0, s, d, N, gx, gev, tb, aevb, p2h, p2i, B.ln2w, c.norm2,
+                       b_[GT], b_[GA]);
+    gemm<EPI_STORE, true>(s, N, nullptr, NI, NI, b_[GT], NI, B.wi, nullptr, b_[GCAT], NI);
+    hipLaunchKernelGGL(g_cat_bwd, dim3(blocks_for(n * (F + E), 256)), dim3(256), 0, s, d, N, b_[GT], b_[GCAT], aevb,
+                       B.int_cg, b_[GP], b_[GA]);
+    gemm<EPI_DSILU, true>(s, N, nullptr, F, F, b_[GP], F, B.m2, nullptr, b_[GHID], F, hpb, F);
+    gemm<EPI_DSILU_ADD, true>(s, N, nullptr, F, F, b_[GHID], F, B.m1, nullptr, b_[GN1], F, n1b, F, b_[GP], F);
+    hipLaunchKernelGGL(g_ln1_bwd, dim3(g4), dim3(256), 0, s, F, N, b_[GN1], B.ln1w, n1hb, n1ib, c.norm1, b_[GAINV]);
+    // attention reverse per pair (kokkos_attention_scatter_reverse.cpp:280-500)
+    hipLaunchKernelGGL(g_attn_bwd_scal, dim3(blocks_for(P * 2 * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb,
+                       c.pY, c.pfc, b_[GAINV], b_[GA], c.inv_avg, b_[CPART], b_[PSC]);
+    hipLaunchKernelGGL(g_attn_bwd_pair, dim3(blocks_for(P * 25, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, c.pfc,
+                       pab, b_[CPART], b_[GA], b == layers_ - 1 ? 1 : 0, c.dY, b_[DFC]);
+    hipLaunchKernelGGL(g_attn_bwd_df, dim3(blocks_for(P * 2 * F, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb,
+                       b_[PSC], b_[DF]);
+    if (b > 0)
+      hipLaunchKernelGGL(g_attn_bwd_node, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
+                         c.pfc, pab, b_[PSC], b_[GAINV], b_[GQKV]);
+    // filter reverse (kokkos_block2_attention_input_reverse.cpp:198-336)
+    for (int w = 0; w < 2; ++w) {
+      gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], F);
+      gemm<EPI_DSILU, true>(s, cap, c.nact, F, F, b_[DF] + w * F, 2 * F, B.w1[w], nullptr, b_[GH], F, b_[HT], F);
+      if (w == 0)
+        gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], F, B.w0[w], nullptr, b_[GRBF], R);
+      else
+        gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], F, B.w0[w], nullptr, b_[GRBF], R);
+      gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[H2T], FH);
+      gemm<EPI_DSILU, true>(s, cap, c.nact, F, FH, b_[DF] + w * F, 2 * F, B.e1[w], nullptr, b_[GH2], FH, b_[H2T], FH);
+      if (w == 0)
+        gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH2], FH, B.e0[w], nullptr, b_[DS], NH);
+      else
+        gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH2], FH, B.e0[w], nullptr, b_[DS], NH);
+    }
+    hipLaunchKernelGGL(g_pair_radial_bwd, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC], b_[GRBF],
+                       b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
+    // the adjoints of the block's inputs feed the block below; block 0's
+    // inputs (embedding, ev = 0) do not depend on the positions
+    if (b > 0) {
+      if (c.qk_norm)
+        hipLaunchKernelGGL(g_qk_norm_bwd, dim3(blocks_for(n * 4 * NH, 256)), dim3(256), 0, s, N, F, NH, qb,
+                           b_[QKIS] + b * n * 4 * NH, b_[GQKV]);
+      hipLaunchKernelGGL(g_qkv_bwd, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, N, F, NH, b_[GQKV], B.wqkv,
+                         b_[GAINV], gx);
+      if (!c.resid->empty())
+        hipLaunchKernelGGL(g_scale, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, n * F, (*c.resid)[b], gx);
+      hipLaunchKernelGGL(g_ev_bwd, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, evb, B.att_cg,
+                         b_[DS], b_[GA], gev);
+    }
+  }
+  G_CHECK(hipGetLastError());
+}
+
+}  // namespace so3lr_amd

@@ -1,0 +1,111 @@
+// The evaluation at any of the widths the reference's MPI path accepts
+// (src/so3lr_capabilities.cpp:54-85): F = 128 or 256 invariant features in
+// F / 32 heads of 32, one equivariant head per degree slot, slots of any
+// sorted degrees 1..4 (a degree may repeat), R = 32 or 64 radial functions,
+// an energy/charge head width of its own.  The v1 widths (F = 128, R = 32,
+// degrees 1,2,3,4, head width 128) run on the fused kernels of evaluator.hip;
+// every other model runs here.
+//
+// Same pair-based, deterministic design as the v1 path (and the same
+// geometry, long-range, force and virial kernels around it): unique pairs
+// {a, b} with both directions carried per pair, node sums as gathers over the
+// node-major incidence, no atomics.  The dense layers are one LDS-tiled fp64
+// GEMM with fused epilogues, over pairs (filters) or nodes; the rest are
+// node- or pair-major kernels in natural channel order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <functional>
+#include <vector>
+
+#include "model.hpp"
+
+namespace so3lr_amd {
+
+constexpr int kGMaxE = 72;  // equivariant channels, at most (8 slots of l = 4)
+
+// The widths of one model.  Slot s (equivariant head s) holds channels
+// off[s] .. off[s+1]-1 of degree deg[s]; channel c replicates the unique
+// harmonic sh[c] (l = 1..4 in order, 2l + 1 each: the 24 values of a pair's
+// harmonics row) and belongs to slot slot[c].
+struct GDims {
+  int F, NH, E, R, FH, HK, NI, HO;  // HO: energy HK | charge HK | Hirshfeld 64 (| C6 64)
+  int c6;
+  signed char slot[kGMaxE], sh[kGMaxE];
+  signed char off[9];
+  double par[8];  // (-1)^l of each slot: the harmonics of the reversed direction
+};
+
+// Device weights of one interaction block, in the model file's layouts.
+struct GBlock {
+  const double *wqkv;  // (5, NH, 32, 32): q k v q_ev k_ev, (head, in, out)
+  const double *w0[2], *b0[2], *w1[2], *b1[2];    // radial layers (F, R) (F) (F, F) (F)
+  const double *e0[2], *eb0[2], *e1[2], *eb1[2];  // spherical layers (FH, NH) (FH) (F, FH) (F)
+  const double *att_cg, *int_cg;                  // (E)
+  const double *ln1w, *ln1b, *ln2w, *ln2b;        // (F); RMSNorm and none: 1 and 0
+  const double *m1, *m1b, *m2, *m2b;              // (F, F) (F)
+  const double *wi, *bi;                          // (NI, NI) (NI)
+};
+
+struct GHeads {
+  const double *w1, *b1;      // (HO, F) (HO): the first layers of all heads
+  const double *hw2, *hb2;    // Hirshfeld key layer (64, 64) (64)
+  const double *cw2, *cb2;    // C6 ratio head key layer (or null)
+  const double *ew2, *qw2;    // (HK)
+  double eb2, qb2;
+  const double *escale, *eshift;  // (118)
+  const double *qemb;             // (100)
+  const double *hqemb, *hvshift;  // (100, 64) (100)
+  const double *cqemb, *cvshift;  // C6 head's (or null)
+  const double *rbf_b, *rbf_k, *rbf_kr;  // (R)
+};
+
+// What one evaluation hands the generic path: the shared inputs (active
+// pairs, incidence, embedding) and where its outputs go.
+struct GContext {
+  hipStream_t s;
+  int N, cap;              // nodes; capacity of the active-pair buffers
+  const int *nact;         // active pairs found (device)
+  const int *pa;           // (cap, 2) endpoints a, b; v = x_a - x_b
+  const double *pr, *pY, *pfc;  // distance, 24 harmonics of v / r, cutoff
+  const int *inc_off, *iact, *iother;  // node-major incidence: pair * 2 + side, partner
+  const int *z;
+  const double *x0;        // (N, F) embedding
+  double inv_avg, ln_eps, gamma, rc;
+  int norm1, norm2, qk_norm;
+  const std::vector<double> *resid, *x0l;
+  // heads forward (outputs)
+  double *eatom, *qraw, *heff, *hir, *c6eff, *c6r;
+  // heads reverse (inputs): charge seed after the image mean, dE/dh, dE/dc
+  const double *qseed, *dh, *dc;
+  // reverse (outputs): dE/dY of the 24 harmonics per pair (side-0
+  // orientation), dE/dr per pair (added to)
+  double *dY, *dr;
+};
+
+class GenericPath {
+ public:
+  // upload: copies a host vector to device memory the evaluator owns.
+  GenericPath(const Model &m, const std::function<const double *(const std::vector<double> &)> &upload);
+  const GDims &dims() const { return d_; }
+  int F() const { return d_.F; }
+  // The work buffers of one evaluation: take(id, doubles) returns buffer id's
+  // memory (the evaluator's retained buffers or scratch slices).
+  static constexpr int kBuffers = 48;
+  void carve(int N, int cap, const std::function<double *(int, std::size_t)> &take);
+  // Blocks and heads forward (to the heads' outputs), then, after the
+  // evaluator's long-range step, heads and blocks in reverse.
+  void forward(const GContext &c);
+  void reverse(const GContext &c);
+
+ private:
+  GDims d_{};
+  int layers_ = 0;
+  GBlock bw_[kMaxBlocks];
+  GHeads hw_{};
+  double *b_[kBuffers] = {};
+};
+
+}  // namespace so3lr_amd

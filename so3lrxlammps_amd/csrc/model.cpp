@@ -412,8 +412,9 @@ std::size_t Tensor::count() const {
 
 std::string Architecture::summary() const {
   std::ostringstream o;
-  o << "layers=" << layers << " features=" << kF << " heads=" << kHeads << "x" << kHW
-    << " degrees=[1,2,3,4] rbf=" << kR << " r_cut=" << sr_cutoff << " r_cut_lr=" << lr_cutoff;
+  o << "layers=" << layers << " features=" << F << " heads=" << heads << "x" << kHW << " degrees=[";
+  for (std::size_t s = 0; s < degrees.size(); ++s) o << (s ? "," : "") << degrees[s];
+  o << "] rbf=" << R << " head_width=" << head_hidden << " r_cut=" << sr_cutoff << " r_cut_lr=" << lr_cutoff;
   static const char *norms[3] = {"layer", "rms", "none"};
   o << " norm=" << norms[int(norm1)] << "/" << norms[int(norm2)] << " attention_norm=" << attention_norm
     << " repulsion=" << (nlh ? "nlh" : "zbl") << (qk_norm ? " qk_norm" : "")
@@ -592,10 +593,17 @@ void Model::describe_and_negotiate(const std::string &origin) {
   };
   arch_.layers = int(a.at("interaction_blocks").uint());
   need(arch_.layers >= 1 && arch_.layers <= kMaxBlocks, "interaction_blocks outside 1..8");
-  need(a.at("invariant_features").uint() == std::uint64_t(kF), "invariant_features != 128 (gfx950 kernels are built for F=128)");
-  need(a.at("attention_heads").uint() == 4 && a.at("attention_head_width").uint() == 32, "attention heads other than 4 x 32");
-  need(a.at("euclidean_degree_channels").uint() == 4, "euclidean_degree_channels != 4");
-  need(a.at("radial_basis_features").uint() == std::uint64_t(kR), "radial_basis_features != 32");
+  // widths: those of the released models (so3lr_capabilities.cpp:54-69):
+  // F = 128 or 256 in heads of 32, one degree slot per head, R = 32 or 64
+  arch_.F = int(a.at("invariant_features").uint());
+  arch_.R = int(a.at("radial_basis_features").uint());
+  arch_.heads = int(a.at("attention_heads").uint());
+  need(arch_.F == 128 || arch_.F == 256, "invariant_features other than 128 or 256");
+  need(a.at("attention_head_width").uint() == 32 && arch_.heads * 32 == arch_.F,
+       "attention heads other than invariant_features / 32 heads of width 32");
+  need(a.at("euclidean_degree_channels").uint() == std::uint64_t(arch_.heads),
+       "euclidean_degree_channels other than attention_heads (one equivariant head per degree slot)");
+  need(arch_.R == 32 || arch_.R == 64, "radial_basis_features other than 32 or 64");
   // normalisation: one module choice for both positions, each position
   // switchable; the reference's post-attention block requires the first
   // (kokkos_post_attention_block0.cpp:386-390)
@@ -633,12 +641,31 @@ void Model::describe_and_negotiate(const std::string &origin) {
        "output heads other than energy, partial charges, Hirshfeld ratios and optionally C6 ratios");
   arch_.c6_head = four;
   if (misses.empty()) {
-    // degree layout {3,5,7,9} in every block
+    // degree slots (so3lr_architecture.cpp:246-293): block 0's repeats, each
+    // 2l + 1 with l in 1..4, sorted; every block carries the same layout
+    const std::size_t S = std::size_t(arch_.heads);
+    const auto rep = i64("model.euclidean_transformers.0.euclidean_attention_block.degree_repeats", {S});
+    arch_.degrees.clear();
+    arch_.E = 0;
+    for (std::size_t s = 0; s < S; ++s) {
+      const std::int64_t r = rep[s];
+      if (r < 3 || r > 9 || r % 2 == 0) fail("degree_repeats entries must be 2l + 1 with l in 1..4");
+      arch_.degrees.push_back(int((r - 1) / 2));
+      arch_.E += int(r);
+      if (s > 0 && arch_.degrees[s] < arch_.degrees[s - 1]) fail("degree slots must be sorted by degree");
+    }
     for (int b = 0; b < arch_.layers; ++b) {
       const std::string p = "model.euclidean_transformers." + std::to_string(b);
-      const auto rep = i64(p + ".euclidean_attention_block.degree_repeats", {4});
-      need(rep == std::vector<std::int64_t>({3, 5, 7, 9}), "degree layout other than l = 1,2,3,4");
+      for (const char *blk : {".euclidean_attention_block.degree_repeats", ".interaction_block.degree_repeats"})
+        if (i64(p + blk, {S}) != rep) fail("block " + std::to_string(b) + " has another degree layout than block 0");
     }
+    // the energy and charge heads' hidden width (so3lr_architecture.cpp:444-446)
+    const Tensor &ew = tensor("model.atomic_energy_output_block.layers.0.weight");
+    if (ew.shape.size() != 2 || ew.shape[1] != std::size_t(arch_.F) || ew.shape[0] == 0 || ew.shape[0] > 1024)
+      fail("energy head first layer must be (hidden, invariant_features)");
+    arch_.head_hidden = int(ew.shape[0]);
+    arch_.generic = !(arch_.F == kF && arch_.R == kR && arch_.degrees == std::vector<int>({1, 2, 3, 4}) &&
+                      arch_.head_hidden == kF);
     const double eps = a.find("layer_norm_epsilon") ? num("layer_norm_epsilon") : 1e-6;
     need(std::abs(eps - 1e-6) < 1e-15, "LayerNorm epsilon other than 1e-6");
     arch_.ln_eps = eps;
@@ -681,12 +708,12 @@ void Model::describe_and_negotiate(const std::string &origin) {
     }
     if (std::abs(csum - 1.0) > 2e-12) fail("normalized ZBL coefficients changed");
   }
-  // The filter kernels evaluate SiLU through a table-based e^x whose argument
-  // reduction is exact for |x| < 2800.  The radial hidden layer sees
+  // The v1 filter kernels evaluate SiLU through a table-based e^x whose argument
+  // reduction is exact for |x| < 2800 (the generic kernels call exp).  The radial hidden layer sees
   // W0 rbf + b0 with every Bernstein value in [0, 1], and the node MLP sees
   // W1 silu(n1) + b1 with |n1_k| <= sqrt(F) |w_k| + |b_k| after either
   // normalisation: both are bounded by the weights, checked here.
-  {
+  if (!arch_.generic) {
     double worst = 0.0;
     const double sf = std::sqrt(double(kF));
     for (int b = 0; b < arch_.layers; ++b) {
@@ -719,18 +746,19 @@ void Model::describe_and_negotiate(const std::string &origin) {
            " in the filter or node MLP hidden layers; this build's activations take |x| < 2000");
   }
   {
-    // the Bernstein exponents k = 0..R-1 and R-1-k (the filter kernels step
-    // the basis through them)
-    const auto k = i64("model.radial_embedding.radial_basis_fn.k", {std::size_t(kR)});
-    const auto kr = i64("model.radial_embedding.radial_basis_fn.k_rev", {std::size_t(kR)});
-    for (int c = 0; c < kR; ++c)
-      if (k[c] != c || kr[c] != kR - 1 - c) fail("Bernstein basis exponents other than k = 0..31, k_rev = 31 - k");
+    // the Bernstein exponents k = 0..R-1 and R-1-k (the v1 filter kernels
+    // step the basis through them)
+    const int R = arch_.R;
+    const auto k = i64("model.radial_embedding.radial_basis_fn.k", {std::size_t(R)});
+    const auto kr = i64("model.radial_embedding.radial_basis_fn.k_rev", {std::size_t(R)});
+    for (int c = 0; c < R; ++c)
+      if (k[c] != c || kr[c] != R - 1 - c) fail("Bernstein basis exponents other than k = 0..R-1, k_rev = R-1-k");
   }
   if (arch_.c6_head) {
     // a ratio head of the Hirshfeld head's widths (kokkos_output_heads.cpp:108-132;
     // the kernels here take hidden and key width 64)
     const std::string c = "model.c6_ratios_output_block.";
-    const std::size_t HH = kHH, F = kF;
+    const std::size_t HH = kHH, F = std::size_t(arch_.F);
     const std::pair<const char *, std::vector<std::size_t>> parts[] = {
         {"transform_features.0.weight", {HH, F}}, {"transform_features.0.bias", {HH}},
         {"transform_features.2.weight", {HH, HH}}, {"transform_features.2.bias", {HH}},
@@ -785,51 +813,52 @@ int atomic_number_from_token(const char *token) {
 // ------------------------------------------------------------ charge/spin
 void ChargeSpin::load(const Model &model) {
   static const char *names[2] = {"model.charge_embedding.", "model.spin_embedding."};
+  F = model.arch().F;
   for (int k = 0; k < 2; ++k) {
     const std::string b = names[k];
-    wq[k] = model.f64(b + "Wq.weight", {std::size_t(kF), 118});
-    wk[k] = model.f64(b + "Wk", {2, std::size_t(kF)});
-    wv[k] = model.f64(b + "Wv", {2, std::size_t(kF)});
-    m1[k] = model.f64(b + "mlp.1.weight", {std::size_t(kF), std::size_t(kF)});
-    m3[k] = model.f64(b + "mlp.3.weight", {std::size_t(kF), std::size_t(kF)});
+    wq[k] = model.f64(b + "Wq.weight", {std::size_t(F), 118});
+    wk[k] = model.f64(b + "Wk", {2, std::size_t(F)});
+    wv[k] = model.f64(b + "Wv", {2, std::size_t(F)});
+    m1[k] = model.f64(b + "mlp.1.weight", {std::size_t(F), std::size_t(F)});
+    m3[k] = model.f64(b + "mlp.3.weight", {std::size_t(F), std::size_t(F)});
   }
 }
 
 std::vector<double> ChargeSpin::table(const std::int64_t counts[119], double total_charge,
                                       double unpaired) const {
-  std::vector<double> out(118 * kF, 0.0);
+  std::vector<double> out(118 * F, 0.0);
   auto silu = [](double x) { return x / (1.0 + std::exp(-x)); };
   const double psis[2] = {total_charge, unpaired};
   for (int k = 0; k < 2; ++k) {
     const double psi = psis[k];
     if (psi == 0.0) continue;  // the module's output is exactly zero
     const int row = psi < 0.0 ? 1 : 0;
-    const double *key = wk[k].data() + row * kF, *val = wv[k].data() + row * kF;
+    const double *key = wk[k].data() + row * F, *val = wv[k].data() + row * F;
     double y[119] = {0};
     double den = 0.0;
     for (int zz = 1; zz <= 118; ++zz) {
       if (counts[zz] <= 0) continue;
       double qk = 0.0;
-      for (int c = 0; c < kF; ++c) qk += wq[k][c * 118 + (zz - 1)] * key[c];
-      const double x = qk / std::sqrt(double(kF));
+      for (int c = 0; c < F; ++c) qk += wq[k][c * 118 + (zz - 1)] * key[c];
+      const double x = qk / std::sqrt(double(F));
       y[zz] = std::max(x, 0.0) + std::log1p(std::exp(-std::abs(x)));  // softplus
       den += double(counts[zz]) * y[zz];
     }
-    std::vector<double> x(kF), sx(kF), h(kF), sh(kF);
+    std::vector<double> x(F), sx(F), h(F), sh(F);
     for (int zz = 1; zz <= 118; ++zz) {
       if (counts[zz] <= 0) continue;
       const double w = psi * y[zz] / den;
-      for (int c = 0; c < kF; ++c) { x[c] = w * val[c]; sx[c] = silu(x[c]); }
-      for (int o = 0; o < kF; ++o) {
+      for (int c = 0; c < F; ++c) { x[c] = w * val[c]; sx[c] = silu(x[c]); }
+      for (int o = 0; o < F; ++o) {
         double s = 0.0;
-        for (int i = 0; i < kF; ++i) s += m1[k][o * kF + i] * sx[i];
+        for (int i = 0; i < F; ++i) s += m1[k][o * F + i] * sx[i];
         h[o] = s;
         sh[o] = silu(s);
       }
-      for (int o = 0; o < kF; ++o) {
+      for (int o = 0; o < F; ++o) {
         double s = 0.0;
-        for (int i = 0; i < kF; ++i) s += m3[k][o * kF + i] * sh[i];
-        out[(zz - 1) * kF + o] += x[o] + s;
+        for (int i = 0; i < F; ++i) s += m3[k][o * F + i] * sh[i];
+        out[(zz - 1) * F + o] += x[o] + s;
       }
     }
   }

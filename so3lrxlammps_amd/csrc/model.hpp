@@ -51,7 +51,8 @@ struct Tensor {
   std::size_t count() const;
 };
 
-// The v1 widths every kernel of this library is written for.
+// The v1 widths the fused kernels of evaluator.hip are written for; models of
+// other widths run on the generic kernels (generic.hip).
 constexpr int kF = 128;   // invariant features
 constexpr int kHeads = 4; // attention heads == degree slots
 constexpr int kHW = 32;   // head width
@@ -79,6 +80,12 @@ struct Architecture {
   bool residual_scalars = false;  // block input = resid[b] x + x0[b] x_embedding
   bool nlh = false;               // NLH pair-table repulsion instead of learned ZBL
   bool c6_head = false;           // C6 ratio head feeding the dispersion C6
+  // widths (so3lr_architecture.cpp:197-212, 246-293, 444-446): F features in
+  // F / 32 heads of 32, one equivariant head per degree slot, R radial
+  // functions, the energy/charge head width; generic = not the v1 widths
+  int F = kF, R = kR, heads = kHeads, E = kE, head_hidden = kF;
+  std::vector<int> degrees{1, 2, 3, 4};
+  bool generic = false;
   // repulsion (ZBL screening parameters: learned ZBL only)
   double zbl_ke = 0, zbl_switch_off = 0, zbl_p = 0, zbl_d = 0, zbl_a[4] = {}, zbl_c[4] = {};
   // long range
@@ -120,6 +127,7 @@ int atomic_number_from_token(const char *token);
 
 // Charge/spin embedding (src/so3lr_charge_spin.cpp:52-141).
 struct ChargeSpin {
+  int F = kF;
   std::vector<double> wq[2], wk[2], wv[2], m1[2], m3[2];  // [0] charge, [1] spin
   void load(const Model &model);
   // 118 x F table (row Z-1) added to the element embedding before the scale.

@@ -315,8 +315,8 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
                        x, xn);
     hipLaunchKernelGGL(k_gather_int, dim3(gb), dim3(256), 0, s, n, perm, static_cast<const int *>(z_->p),
                        ensure<int>(nz_, n));
-    hipLaunchKernelGGL(k_gather_rows, dim3(unsigned((std::size_t(n) * kF + 255) / 256)), dim3(256), 0, s, n, kF,
-                       perm, static_cast<const double *>(x0_->p), ensure<double>(nx0_, std::size_t(n) * kF));
+    hipLaunchKernelGGL(k_gather_rows, dim3(unsigned((std::size_t(n) * F_ + 255) / 256)), dim3(256), 0, s, n, F_,
+                       perm, static_cast<const double *>(x0_->p), ensure<double>(nx0_, std::size_t(n) * F_));
     perm_host_.resize(n);
     NB_CHECK(hipMemcpyAsync(perm_host_.data(), perm, std::size_t(n) * sizeof(int), hipMemcpyDeviceToHost, s));
     x = xn;  // the lists below are built in node order

@@ -123,11 +123,16 @@ def test_missing_file_rejected():
 
 
 @pytest.mark.parametrize("key,value,feature", [
-    ("invariant_features", 256, "invariant_features"),
+    ("invariant_features", 512, "invariant_features"),
+    # the released widths F = 256 and R = 64 load; these manifests keep the
+    # v1 tensors, so the contract names what disagrees
+    ("invariant_features", 256, "invariant_features / 32 heads"),
     ("interaction_blocks", 9, "interaction_blocks"),
     ("brand_new_operator", 1, "unknown architecture key"),
     ("repulsion_type", "none", "repulsion other than"),
-    ("radial_basis_features", 64, "radial_basis_features"),
+    ("radial_basis_features", 48, "radial_basis_features"),
+    ("radial_basis_features", 64, "radial_basis_fn.k"),
+    ("euclidean_degree_channels", 3, "euclidean_degree_channels"),
     ("output_heads", ["atomic_energy_output_block", "partial_charges_output_block", "hirshfeld_output_block",
                       "dipole_vec_output_block"], "output heads other than"),
     ("layer_norm_epsilon", 1e-5, "LayerNorm epsilon"),
@@ -162,6 +167,38 @@ def test_weights_beyond_the_activation_range_are_refused(tmp_path):
     path = support.variant_model(tmp_path / "big.so3lr", edit=big)
     rc, msg = _create(path)
     assert rc == _lib.ERR_MODEL and "SiLU arguments" in msg, msg
+
+
+def test_released_widths_are_accepted(tmp_path):
+    """F = 256 with R = 64, duplicated degree slots and an energy/charge head
+    narrower than F (support.lifted_model), and duplicated or missing degrees
+    at F = 128 (support.degrees_model) load up to the device step."""
+    for path in (support.lifted_model(tmp_path / "wide.so3lr"),
+                 support.degrees_model(tmp_path / "d1123.so3lr", (1, 1, 2, 3)),
+                 support.degrees_model(tmp_path / "d1233.so3lr", (1, 2, 3, 3))):
+        rc, msg = _create(path)
+        assert rc in (_lib.OK, _lib.ERR_DEVICE), msg
+
+
+@pytest.mark.parametrize("repeats,feature", [
+    ([3, 5, 9, 7], "sorted"), ([3, 5, 7, 11], "2l + 1"), ([3, 4, 7, 9], "2l + 1")])
+def test_degree_layout_rules(tmp_path, repeats, feature):
+    """Degree slots must be 2l + 1 wide with l in 1..4 and sorted
+    (so3lr_architecture.cpp:246-268); a later block with another layout than
+    block 0 is refused too."""
+    def edit(manifest, arrays):
+        for b in range(3):
+            for blk in ("euclidean_attention_block", "interaction_block"):
+                arrays["model.euclidean_transformers.%d.%s.degree_repeats" % (b, blk)] = np.array(repeats, dtype=np.int64)
+    rc, msg = _create(support.variant_model(tmp_path / "deg.so3lr", edit=edit))
+    assert rc == _lib.ERR_MODEL and feature in msg, msg
+
+
+def test_degree_layout_must_agree_across_blocks(tmp_path):
+    def edit(manifest, arrays):
+        arrays["model.euclidean_transformers.2.interaction_block.degree_repeats"] = np.array([3, 3, 7, 9], dtype=np.int64)
+    rc, msg = _create(support.variant_model(tmp_path / "deg2.so3lr", edit=edit))
+    assert rc == _lib.ERR_MODEL and "another degree layout" in msg, msg
 
 
 @pytest.mark.parametrize("key,value", [

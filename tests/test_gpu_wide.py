@@ -1,0 +1,97 @@
+"""HIP path vs the CPU oracle at the widths beyond v1 that the reference runs
+(so3lr_capabilities.cpp:54-85): F = 256 (8 heads, 8 degree slots), R = 64,
+duplicated degree slots, energy/charge heads narrower than F, and duplicated
+or missing degrees at F = 128.  These models run on the generic kernels
+(csrc/generic.hip).  The oracle at these widths is pinned by
+tests/test_oracle_wide.py.  Same tolerances as test_gpu_parity.py.
+"""
+import numpy as np
+import pytest
+
+import support
+from oracle.oracle import Oracle
+from test_gpu_parity import _check, _hip_single_point
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def models(tmp_path_factory):
+    d = tmp_path_factory.mktemp("wide")
+    from test_gpu_arch import _variants
+    # every option on, filters quietened as in test_gpu_arch (the untrained
+    # model's attention logits otherwise give forces of 10^4 eV/A on water)
+    options = support.variant_model(d / "options.so3lr", **_variants()["all"])
+    lift = support.lifted_model(d / "lift.so3lr")
+    return {
+        "lift": lift,
+        # the lift with every weight perturbed: the two copies no longer agree
+        "lift_perturbed": support.perturbed_model(d / "lift_p.so3lr", seed=23, scale=0.2, base=lift),
+        "lift_options": support.lifted_model(d / "lift_opt.so3lr", base=options),
+        "deg1123": support.degrees_model(d / "d1123.so3lr", (1, 1, 2, 3)),
+        "deg1233": support.degrees_model(d / "d1233.so3lr", (1, 2, 3, 3)),
+    }
+
+
+CASES = [(m, n) for m in ("lift", "lift_perturbed", "lift_options", "deg1123", "deg1233")
+         for n in ("acetate", "alanine_cation", "water3000")]
+
+
+@pytest.mark.parametrize("model,name", CASES)
+def test_wide_model_matches_oracle(models, model, name):
+    from so3lrxlammps_amd import Context
+    ref, z, pos, box = support.load_golden(name)
+    q, m = ref.get("charge", 0), ref.get("multiplicity", 1)
+    print("case", model, name, flush=True)
+    ctx = Context(models[model], 0)
+    e, f, ea, w, terms = _hip_single_point(ctx, z, pos, box, q, m)
+    ctx.close()
+    out = Oracle(models[model]).evaluate(z, *support.build_graphs(pos, box), charge=q, multiplicity=m)
+    _check(out, e, f, ea, w, terms, ftol=1e-9 * max(1.0, np.abs(out["forces"]).max() / 10.0))
+
+
+def test_lift_on_the_gpu_equals_the_v1_model(models):
+    """The lift computes the v1 model's function: the generic kernels on it
+    agree with the fused v1 kernels on the shipped model."""
+    from so3lrxlammps_amd import Context
+    ref, z, pos, box = support.load_golden("water3000")
+    res = []
+    for path in (models["lift"], support.MODEL):
+        ctx = Context(path, 0)
+        res.append(_hip_single_point(ctx, z, pos, box, 0, 1))
+        ctx.close()
+    (e1, f1, _, w1, _), (e0, f0, _, w0, _) = res
+    assert abs(e1 - e0) <= 1e-11 * abs(e0)
+    assert np.abs(f1 - f0).max() <= 1e-9
+    assert np.abs(w1 - w0).max() <= 1e-9 * max(1.0, np.abs(w0).max())
+
+
+def test_wide_device_path_and_replay(models):
+    """so3lr_reneighbor_device + so3lr_compute_device on the perturbed lift:
+    bitwise equal across graph replays and equal to the rows path."""
+    import torch
+    from so3lrxlammps_amd import Context, Lists
+    ref, z, pos, box = support.load_golden("water3000")
+    print("case lift_perturbed device path", flush=True)
+    ctx = Context(models["lift_perturbed"], 0)
+    ctx.set_system(z, 0, 1)
+    lists = Lists(pos, np.zeros(3), box, (1, 1, 1))
+    ctx.set_topology(lists)
+    e0, f0, _, w0 = ctx.compute(lists.rows_positions(pos))
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    runs = []
+    with torch.cuda.stream(stream):
+        x = torch.tensor(pos, dtype=torch.float64, device=dev)
+        f = torch.zeros_like(x)
+        ctx.reneighbor_device(x, np.zeros(3), box, (1, 1, 1), 1.0, stream=stream.cuda_stream)
+        for _ in range(3):
+            e, w = ctx.compute_device(x, f, stream=stream.cuda_stream)
+            stream.synchronize()
+            runs.append((e, w.copy(), f.cpu().numpy().copy()))
+    ctx.close()
+    for e, w, ff in runs[1:]:
+        assert e == runs[0][0] and np.array_equal(w, runs[0][1]) and np.array_equal(ff, runs[0][2])
+    assert abs(runs[0][0] - e0) <= 1e-11 * abs(e0)
+    assert np.abs(runs[0][2] - f0).max() <= 1e-10
+    assert np.abs(runs[0][1] - w0).max() <= 1e-10 * max(1.0, np.abs(w0).max())
