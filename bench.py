@@ -386,7 +386,24 @@ def capacity(steps, warmup, stream):
     return out
 
 
+def model_widths(path):
+    """The model's file name and widths, and which kernels evaluate it (the
+    fused ones at the v1 widths, the generic ones otherwise)."""
+    from so3lrxlammps_amd.model_file import read_model
+    manifest, arrays = read_model(path)
+    a = manifest["architecture"]
+    rep = [int(v) for v in arrays["model.euclidean_transformers.0.euclidean_attention_block.degree_repeats"]]
+    degrees = [(r - 1) // 2 for r in rep]
+    head = int(arrays["model.atomic_energy_output_block.layers.0.weight"].shape[0])
+    F, R = int(a["invariant_features"]), int(a["radial_basis_features"])
+    v1 = F == 128 and R == 32 and degrees == [1, 2, 3, 4] and head == 128
+    return {"file": os.path.basename(path), "invariant_features": F, "radial_basis_features": R,
+            "degree_slots": degrees, "head_width": head, "blocks": int(a["interaction_blocks"]),
+            "kernels": "fused v1" if v1 else "generic"}
+
+
 def main():
+    global MODEL
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -402,7 +419,12 @@ def main():
                     help="steps after the timed ones with per-kernel HIP events")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run a plain device copy of this size first (HBM-counter calibration)")
+    ap.add_argument("--model", default=MODEL,
+                    help="model file (default: the shipped v1 model; models of other widths run on the "
+                         "generic kernels and are reported without a roofline or baseline ratio)")
     args = ap.parse_args()
+    default_model = os.path.abspath(args.model) == os.path.abspath(MODEL)
+    MODEL = args.model
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs one LAMMPS rank on one MI355X with no "
               "GPU-to-GPU exchange (--gpus %d is not supported)" % args.gpus, file=sys.stderr)
@@ -462,20 +484,24 @@ def main():
                         "frac": alg * per_launch / (ms / launches * 1e-3) / 1e12 / FP64_PEAK_TFS})
         kernels[k] = row
     # the roofline kernel: most GPU time per step among those with a work model
-    dom = max((k for k in kernels if k in KERNEL_WORK), key=lambda k: kernels[k]["ms_per_step"])
-    sym, bound, alg, issued, unit = KERNEL_WORK[dom]
-    ms, launches, units = timing[dom]
-    avg_ms = ms / launches
-    per_launch = units / launches
-    achieved = alg * per_launch / (avg_ms * 1e-3) / 1e12
-    traffic, traffic_src = traffic_per_launch(sym, args.config, per_launch)
-    roofline = {"bound": bound, "kernel": sym, "achieved": achieved, "peak": FP64_PEAK_TFS, "unit": "TFLOP/s",
-                "frac": achieved / FP64_PEAK_TFS, "traffic": traffic, "traffic_source": traffic_src,
-                "avg_launch_ms": avg_ms, "pairs_per_launch": per_launch,
-                "flop_per_pair_algorithmic": alg, "flop_per_pair_issued": issued,
-                "achieved_issued": issued * per_launch / (avg_ms * 1e-3) / 1e12,
-                "selection": "the timed kernel with the most GPU time per step (%.3f ms of %d steps' HIP events)"
-                             % (kernels[dom]["ms_per_step"], steps_timed)}
+    # (the fused v1 kernels; a model on the generic kernels has none timed)
+    roofline = None
+    timed_with_model = [k for k in kernels if k in KERNEL_WORK]
+    if timed_with_model:
+        dom = max(timed_with_model, key=lambda k: kernels[k]["ms_per_step"])
+        sym, bound, alg, issued, unit = KERNEL_WORK[dom]
+        ms, launches, units = timing[dom]
+        avg_ms = ms / launches
+        per_launch = units / launches
+        achieved = alg * per_launch / (avg_ms * 1e-3) / 1e12
+        traffic, traffic_src = traffic_per_launch(sym, args.config, per_launch)
+        roofline = {"bound": bound, "kernel": sym, "achieved": achieved, "peak": FP64_PEAK_TFS, "unit": "TFLOP/s",
+                    "frac": achieved / FP64_PEAK_TFS, "traffic": traffic, "traffic_source": traffic_src,
+                    "avg_launch_ms": avg_ms, "pairs_per_launch": per_launch,
+                    "flop_per_pair_algorithmic": alg, "flop_per_pair_issued": issued,
+                    "achieved_issued": issued * per_launch / (avg_ms * 1e-3) / 1e12,
+                    "selection": "the timed kernel with the most GPU time per step (%.3f ms of %d steps' HIP events)"
+                                 % (kernels[dom]["ms_per_step"], steps_timed)}
     free_b, total_b = torch.cuda.mem_get_info(dev)
     sr_active, sr_cand, lr_cand = md.ctx.graph_stats()
     config = {"workload": "config %d: %s" % (args.config, desc), "atoms": n, "integrator": "velocity Verlet",
@@ -510,13 +536,14 @@ def main():
         "metric": "atom-steps/s/GPU (fp64 E+F+virial) at 24k-atom water; max atoms per GPU",
         "value": value, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": 1000.0 * elapsed / args.steps, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": value / A100_ATOM_STEPS if args.config == 3 else None, "dtype": "f64",
+        "vs_baseline": value / A100_ATOM_STEPS if args.config == 3 and default_model else None, "dtype": "f64",
         "data": "synthetic (seeded, config %d)" % args.config,
         "config": config,
         "roofline": roofline,
         "rows_path": rows,
         "capacity": cap,
         "cpu_baseline": cpu,
+        "model": model_widths(MODEL),
     }
     print(json.dumps(out))
 

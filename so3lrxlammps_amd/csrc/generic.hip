@@ -45,8 +45,7 @@ __device__ __forceinline__ double wsum(double v) {
 // with op(W) = W^T for W (O x K) row-major (the model file's (out, in)
 // layout) or, WKO, W itself for W (K x O) row-major (the adjoint of a layer:
 // X W).  rows = min(*rows_dev, rows) when rows_dev is given (the active-pair
-// count on the device).  64 x 64 output tiles, 256 threads of 4 x 4 outputs,
-// K in steps of 16 through LDS.
+// count on the device).
 enum { EPI_STORE = 0, EPI_SILU, EPI_ACCUM, EPI_ADD, EPI_DSILU, EPI_DSILU_ADD };
 struct GemmArgs {
   int rows;
@@ -64,104 +63,134 @@ struct GemmArgs {
   int ldaux;
   const double *res;  // EPI_ADD, EPI_DSILU_ADD: added
   int ldres;
+  // batches (grid z = nby * nbx, z = zy * nbx + zx): X, Y and res move by
+  // zy * (..)0 + zx * (..)1 elements, W by z * wbs
+  int nbx;
+  long xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs;
 };
 
-template <int EPI, bool WKO>
+typedef double gv4d __attribute__((ext_vector_type(4)));
+
+// 64 x BN output tiles (BN = 64 or 128) on fp64 MFMA 16x16x4: four
+// wavefronts in 2 x 2, each 32 rows x BN/2 columns (2 x BN/32 MFMA tiles).
+// D[i][j] += sum_k A[i][k] B[k][j] with A[i][k] = X[row i][k] (lane l gives
+// i = l % 16, k = l / 16) and B[k][j] = op(W)[k][col j] (lane l gives
+// k = l / 16, j = l % 16); lane l holds D[l / 16 + 4 r][l % 16] in register
+// r, so sixteen lanes write sixteen adjacent columns of one row.  K runs in
+// chunks of 16 through LDS; the next chunk's global loads are issued before
+// the current chunk's MFMAs.
+template <int EPI, bool WKO, int BN>
 __global__ __launch_bounds__(256) void g_gemm(GemmArgs A) {
-  __shared__ double xs[16][65];
-  __shared__ double ws[16][65];
+  constexpr int NT = BN / 32;      // MFMA column tiles per wavefront
+  constexpr int WPT = BN / 16;     // W chunk values per thread (BN x 16 / 256)
+  __shared__ double xs[64][17];
+  __shared__ double ws[BN][17];
   const int rows = A.rows_dev ? min(*A.rows_dev, A.rows) : A.rows;
-  const int row0 = blockIdx.x * 64, col0 = blockIdx.y * 64;
+  const int row0 = blockIdx.x * 64, col0 = blockIdx.y * BN;
   if (row0 >= rows) return;  // uniform over the block
-  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  double acc[4][4];
-  for (int i = 0; i < 4; ++i)
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
-  for (int k0 = 0; k0 < A.K; k0 += 16) {
+  {
+    const long zx = long(blockIdx.z) % A.nbx, zy = long(blockIdx.z) / A.nbx;
+    A.X += zy * A.xbs0 + zx * A.xbs1;
+    A.Y += zy * A.ybs0 + zx * A.ybs1;
+    if (A.res) A.res += zy * A.rbs0 + zx * A.rbs1;
+    A.W += long(blockIdx.z) * A.wbs;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wr0 = (wv >> 1) * 32, wc0 = (wv & 1) * (BN / 2);
+  const int li = lane & 15, lk = lane >> 4;
+  double xreg[4], wreg[WPT];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int idx = tid + 256 * q, kk = idx & 15, rr = idx >> 4;
+      const int row = row0 + rr, k = k0 + kk;
+      xreg[q] = (row < rows && k < A.K) ? A.X[std::size_t(row) * A.ldx + k] : 0.0;
+    }
+#pragma unroll
+    for (int q = 0; q < WPT; ++q) {
+      const int idx = tid + 256 * q;
+      if (WKO) {
+        const int cc = idx % BN, kk = idx / BN, col = col0 + cc, k = k0 + kk;
+        wreg[q] = (col < A.O && k < A.K) ? A.W[std::size_t(k) * A.O + col] : 0.0;
+      } else {
+        const int kk = idx & 15, cc = idx >> 4, col = col0 + cc, k = k0 + kk;
+        wreg[q] = (col < A.O && k < A.K) ? A.W[std::size_t(col) * A.K + k] : 0.0;
+      }
+    }
+  };
+  auto stash = [&] {
+#pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int idx = tid + 256 * q;
-      const int kk = idx & 15, rr = idx >> 4;
-      const int row = row0 + rr, k = k0 + kk;
-      xs[kk][rr] = (row < rows && k < A.K) ? A.X[std::size_t(row) * A.ldx + k] : 0.0;
-      if (WKO) {
-        const int cc = idx & 63, kw = idx >> 6;
-        const int col = col0 + cc, k2 = k0 + kw;
-        ws[kw][cc] = (col < A.O && k2 < A.K) ? A.W[std::size_t(k2) * A.O + col] : 0.0;
-      } else {
-        const int col = col0 + rr;
-        ws[kk][rr] = (col < A.O && k < A.K) ? A.W[std::size_t(col) * A.K + k] : 0.0;
-      }
+      xs[idx >> 4][idx & 15] = xreg[q];
+    }
+#pragma unroll
+    for (int q = 0; q < WPT; ++q) {
+      const int idx = tid + 256 * q;
+      if (WKO) ws[idx % BN][idx / BN] = wreg[q];
+      else ws[idx >> 4][idx & 15] = wreg[q];
+    }
+  };
+  gv4d acc[2][NT];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b) acc[a][b] = gv4d{0.0, 0.0, 0.0, 0.0};
+  fetch(0);
+  stash();
+  __syncthreads();
+  for (int k0 = 0; k0 < A.K; k0 += 16) {
+    const bool more = k0 + 16 < A.K;
+    if (more) fetch(k0 + 16);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int kk = lk + 4 * v;
+      double av[2], bv[NT];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) av[a] = xs[wr0 + 16 * a + li][kk];
+#pragma unroll
+      for (int b = 0; b < NT; ++b) bv[b] = ws[wc0 + 16 * b + li][kk];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < NT; ++b) acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
     }
     __syncthreads();
-    for (int kk = 0; kk < 16; ++kk) {
-      double xv[4], wv[4];
-      for (int i = 0; i < 4; ++i) xv[i] = xs[kk][ty + 16 * i];
-      for (int j = 0; j < 4; ++j) wv[j] = ws[kk][tx + 16 * j];
-      for (int i = 0; i < 4; ++i)
-        for (int j = 0; j < 4; ++j) acc[i][j] = fma(xv[i], wv[j], acc[i][j]);
+    if (more) {
+      stash();
+      __syncthreads();
     }
-    __syncthreads();
   }
-  for (int i = 0; i < 4; ++i) {
-    const int row = row0 + ty + 16 * i;
-    if (row >= rows) continue;
-    for (int j = 0; j < 4; ++j) {
-      const int col = col0 + tx + 16 * j;
-      if (col >= A.O) continue;
-      const double pre = acc[i][j] + (A.bias ? A.bias[col] : 0.0);
-      double *y = A.Y + std::size_t(row) * A.ldy + col;
-      if (EPI == EPI_STORE) {
-        *y = pre;
-      } else if (EPI == EPI_SILU) {
-        if (A.Y2) A.Y2[std::size_t(row) * A.ldy2 + col] = pre;
-        *y = gsilu(pre);
-      } else if (EPI == EPI_ACCUM) {
-        *y += pre;
-      } else if (EPI == EPI_ADD) {
-        *y = pre + A.res[std::size_t(row) * A.ldres + col];
-      } else if (EPI == EPI_DSILU) {
-        *y = acc[i][j] * gsilu_prime(A.aux[std::size_t(row) * A.ldaux + col]);
-      } else {
-        *y = A.res[std::size_t(row) * A.ldres + col] + acc[i][j] * gsilu_prime(A.aux[std::size_t(row) * A.ldaux + col]);
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + wr0 + 16 * a + lk + 4 * r;
+        const int col = col0 + wc0 + 16 * b + li;
+        if (row >= rows || col >= A.O) continue;
+        const double dot = acc[a][b][r];
+        const double pre = dot + (A.bias ? A.bias[col] : 0.0);
+        double *y = A.Y + std::size_t(row) * A.ldy + col;
+        if (EPI == EPI_STORE) {
+          *y = pre;
+        } else if (EPI == EPI_SILU) {
+          if (A.Y2) A.Y2[std::size_t(row) * A.ldy2 + col] = pre;
+          *y = gsilu(pre);
+        } else if (EPI == EPI_ACCUM) {
+          *y += pre;
+        } else if (EPI == EPI_ADD) {
+          *y = pre + A.res[std::size_t(row) * A.ldres + col];
+        } else if (EPI == EPI_DSILU) {
+          *y = dot * gsilu_prime(A.aux[std::size_t(row) * A.ldaux + col]);
+        } else {
+          *y = A.res[std::size_t(row) * A.ldres + col] + dot * gsilu_prime(A.aux[std::size_t(row) * A.ldaux + col]);
+        }
       }
-    }
-  }
 }
 
 // ------------------------------------------------------------- node kernels
-// q, k, v, q_ev, k_ev per head: out[w][h*32 + o] = sum_k x[h*32 + k] W[w][h][k][o]
-// (kokkos_integrated_block0.cpp:257-287).  One thread per output.
-__global__ __launch_bounds__(256) void g_qkv(int N, int F, int NH, const double *__restrict__ x,
-                                             const double *__restrict__ w, double *__restrict__ qkv) {
-  const std::size_t t = std::size_t(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= std::size_t(N) * 5 * F) return;
-  const int n = int(t / (5 * F)), r = int(t % (5 * F));
-  const int ws = r / F, c = r % F, h = c >> 5, o = c & 31;
-  const double *xr = x + std::size_t(n) * F + 32 * h;
-  const double *wm = w + (std::size_t(ws) * NH + h) * 1024 + o;
-  double s = 0.0;
-  for (int k = 0; k < 32; ++k) s += xr[k] * wm[32 * k];
-  qkv[t] = s;
-}
-
-// gx = gainv + sum_w W[w] gqkv[w] per head (the adjoint of g_qkv).
-__global__ __launch_bounds__(256) void g_qkv_bwd(int N, int F, int NH, const double *__restrict__ gqkv,
-                                                 const double *__restrict__ w, const double *__restrict__ gainv,
-                                                 double *__restrict__ gx) {
-  const std::size_t t = std::size_t(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= std::size_t(N) * F) return;
-  const int n = int(t / F), c = int(t % F), h = c >> 5, k = c & 31;
-  double g = gainv[t];
-  for (int ws = 0; ws < 5; ++ws) {
-    const double *gr = gqkv + std::size_t(n) * 5 * F + std::size_t(ws) * F + 32 * h;
-    const double *wm = w + (std::size_t(ws) * NH + h) * 1024 + 32 * k;
-    double s = 0.0;
-    for (int o = 0; o < 32; ++o) s += wm[o] * gr[o];
-    g += s;
-  }
-  gx[t] = g;
-}
-
 // QK normalisation: each 32-wide head row of q, k, q_ev, k_ev scaled to unit
 // RMS (eps 1e-6; kokkos_integrated_block0.cpp:288-328), 1/rms kept.
 __device__ __forceinline__ int qk_row(int k) { return k < 2 ? k : k + 1; }  // q k (v) qe ke
@@ -570,127 +599,151 @@ __global__ void g_pair_inv(GDims d, const int *nact, int cap, const int *__restr
   ps[std::size_t(p) * d.NH + s] = acc;
 }
 
+// Sum over each 32-lane half of a wavefront (lanes 0-31 and 32-63 apart).
+__device__ __forceinline__ double half_sum(double v) {
+  for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, 32);
+  return v;
+}
+
 // Attention logits per pair, direction and head (kokkos_integrated_block0.cpp:330-360):
-// alpha = <q_receiver, k_sender (.) f> / norm (inv: q k f_inv, ev: q_ev k_ev f_ev).
-__global__ void g_alpha(GDims d, const int *nact, int cap, const int *__restrict__ pa,
-                        const double *__restrict__ qkv, const double *__restrict__ pf, double inv_avg,
-                        double *__restrict__ palpha) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  const int NH = d.NH, F = d.F;
-  const int p = t / (4 * NH), r = t % (4 * NH);
+// alpha = <q_receiver, k_sender (.) f> / norm (inv: q k f_inv, ev: q_ev k_ev
+// f_ev).  One wavefront per pair, lanes over channels (channel lane + 64 j is
+// in head 2 j + lane / 32).
+__global__ __launch_bounds__(256) void g_alpha(GDims d, const int *nact, int cap, const int *__restrict__ pa,
+                                               const double *__restrict__ qkv, const double *__restrict__ pf,
+                                               double inv_avg, double *__restrict__ palpha) {
+  const int lane = threadIdx.x & 63;
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (p >= min(*nact, cap)) return;
-  const int side = r / (2 * NH), which = (r / NH) & 1, h = r % NH;
-  const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
-  const double *qr = qkv + std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + 32 * h;
-  const double *ks = qkv + std::size_t(snd) * 5 * F + (which ? 4 * F : F) + 32 * h;
-  const double *f = pf + std::size_t(p) * 2 * F + (which ? F : 0) + 32 * h;
-  double acc = 0.0;
-  for (int c = 0; c < 32; ++c) acc += qr[c] * ks[c] * f[c];
-  palpha[t] = acc * inv_avg;
-}
-
-// Attention reverse per pair, direction and head: ci = <gainv_r, v_s>_h,
-// ce = <gaev_r, Y'>_slot h; psc = fc c norm (the logits' adjoints).
-__global__ void g_attn_bwd_scal(GDims d, const int *nact, int cap, const int *__restrict__ pa,
-                                const double *__restrict__ qkv, const double *__restrict__ pY,
-                                const double *__restrict__ pfc, const double *__restrict__ gainv,
-                                const double *__restrict__ ga, double inv_avg, double *__restrict__ cpart,
-                                double *__restrict__ psc) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  const int NH = d.NH, F = d.F;
-  const int p = t / (2 * NH), r = t % (2 * NH);
-  if (p >= min(*nact, cap)) return;
-  const int side = r / NH, h = r % NH;
-  const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
-  const double *g = gainv + std::size_t(rcv) * F + 32 * h;
-  const double *v = qkv + std::size_t(snd) * 5 * F + 2 * F + 32 * h;
-  double ci = 0.0;
-  for (int c = 0; c < 32; ++c) ci += g[c] * v[c];
-  const double pr = side ? d.par[h] : 1.0;
-  double ce = 0.0;
-  for (int c = d.off[h]; c < d.off[h + 1]; ++c) ce += ga[std::size_t(rcv) * d.E + c] * pY[std::size_t(p) * 24 + d.sh[c]] * pr;
-  const double fc = pfc[p];
-  const std::size_t o = std::size_t(p) * 4 * NH + side * 2 * NH;
-  cpart[o + h] = ci;
-  cpart[o + NH + h] = ce;
-  psc[o + h] = fc * ci * inv_avg;
-  psc[o + NH + h] = fc * ce * inv_avg;
-}
-
-// Per pair: dE/dY of the 24 harmonics (side-0 orientation; m = 0..23) and
-// dE/dfc (m = 24).  The first reverse block writes dY, the others add.
-__global__ void g_attn_bwd_pair(GDims d, const int *nact, int cap, const int *__restrict__ pa,
-                                const double *__restrict__ pfc, const double *__restrict__ palpha,
-                                const double *__restrict__ cpart, const double *__restrict__ ga, int first,
-                                double *__restrict__ dY, double *__restrict__ dfc) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  const int p = t / 25, m = t % 25, NH = d.NH;
-  if (p >= min(*nact, cap)) return;
-  const double *al = palpha + std::size_t(p) * 4 * NH;
-  if (m == 24) {
-    const double *cp = cpart + std::size_t(p) * 4 * NH;
-    double acc = 0.0;
-    for (int side = 0; side < 2; ++side)
-      for (int h = 0; h < NH; ++h)
-        acc += cp[side * 2 * NH + h] * al[side * 2 * NH + h] + cp[side * 2 * NH + NH + h] * al[side * 2 * NH + NH + h];
-    dfc[p] = acc;
-    return;
-  }
-  const double fc = pfc[p];
-  double acc = 0.0;
+  const int NH = d.NH, F = d.F, J = F >> 6;
   for (int side = 0; side < 2; ++side) {
-    const int rcv = pa[2 * p + side];
-    for (int c = 0; c < d.E; ++c) {
-      if (d.sh[c] != m) continue;
-      const int sl = d.slot[c];
-      acc += ga[std::size_t(rcv) * d.E + c] * fc * al[side * 2 * NH + NH + sl] * (side ? d.par[sl] : 1.0);
+    const double *qr = qkv + std::size_t(pa[2 * p + side]) * 5 * F;
+    const double *ks = qkv + std::size_t(pa[2 * p + 1 - side]) * 5 * F;
+    for (int which = 0; which < 2; ++which) {
+      const double *q = qr + (which ? 3 * F : 0), *k = ks + (which ? 4 * F : F);
+      const double *f = pf + std::size_t(p) * 2 * F + (which ? F : 0);
+      for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        const double t = half_sum(q[c] * k[c] * f[c]);
+        if ((lane & 31) == 0) palpha[std::size_t(p) * 4 * NH + side * 2 * NH + which * NH + 2 * j + (lane >> 5)] = t * inv_avg;
+      }
     }
   }
-  double *y = dY + std::size_t(p) * 24 + m;
-  *y = first ? acc : *y + acc;
 }
 
-// The filters' adjoints per pair, both directions summed (the filter is
-// shared): df_inv = sum_side psc_inv q_r k_s, df_ev = sum_side psc_ev q_ev k_ev.
-__global__ void g_attn_bwd_df(GDims d, const int *nact, int cap, const int *__restrict__ pa,
-                              const double *__restrict__ qkv, const double *__restrict__ psc,
-                              double *__restrict__ df) {
-  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int F = d.F, NH = d.NH;
-  const std::size_t p = t / (2 * F);
-  const int c = int(t % (2 * F));
-  if (p >= std::size_t(min(*nact, cap))) return;
-  const int which = c / F, cc = c % F, h = cc >> 5;
-  double acc = 0.0;
-  for (int side = 0; side < 2; ++side) {
-    const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
-    const double qv = qkv[std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + cc];
-    const double kv = qkv[std::size_t(snd) * 5 * F + (which ? 4 * F : F) + cc];
-    acc += psc[p * 4 * NH + side * 2 * NH + which * NH + h] * qv * kv;
+// Attention reverse, pair side (kokkos_attention_scatter_reverse.cpp:280-500),
+// one wavefront per pair, both directions: with r the receiver and s the
+// sender of a direction,
+//   ci_h = <gainv_r, v_s>_head h,  ce_h = <gaev_r, Y'>_slot h  (Y' the
+//   direction's harmonics), psc = fc c norm (the logits' adjoints, kept for
+//   the node gathers), dE/dfc = sum ci alpha + ce alpha_ev,
+//   df = sum_dir psc q_r k_s (inv) and psc_ev q_ev_r k_ev_s (ev): the shared
+//   filter's adjoint,
+//   dE/dY_m = sum_dir sum_{c: sh(c) = m} gaev_r,c fc alpha_ev par (side-0
+//   orientation); the first reverse block writes dY, the others add.
+// Every wavefront reaches the barriers (inactive ones skip the work).
+__global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact, int cap, const int *__restrict__ pa,
+                                                        const double *__restrict__ qkv, const double *__restrict__ pY,
+                                                        const double *__restrict__ pfc,
+                                                        const double *__restrict__ palpha,
+                                                        const double *__restrict__ gainv,
+                                                        const double *__restrict__ ga, double inv_avg, int first,
+                                                        double *__restrict__ psc, double *__restrict__ df,
+                                                        double *__restrict__ dY, double *__restrict__ dfc) {
+  __shared__ double lt[4][2][kGMaxE];  // per wavefront: dE/dY terms per direction and channel
+  __shared__ double lps[4][32];        // per wavefront: psc of the pair
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int p = blockIdx.x * 4 + wv;
+  const bool on = p < min(*nact, cap);
+  const int NH = d.NH, F = d.F, E = d.E, J = F >> 6;
+  if (on) {
+    const double fc = pfc[p];
+    const double *al = palpha + std::size_t(p) * 4 * NH;
+    double dsum = 0.0;  // dE/dfc (uniform over the wavefront)
+    for (int side = 0; side < 2; ++side) {
+      const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
+      const double *g = gainv + std::size_t(rcv) * F, *v = qkv + std::size_t(snd) * 5 * F + 2 * F;
+      for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        const double ci = half_sum(g[c] * v[c]);
+        const int h = 2 * j + (lane >> 5);
+        dsum += __shfl(ci * al[side * 2 * NH + h], 0, 64) + __shfl(ci * al[side * 2 * NH + h], 32, 64);
+        if ((lane & 31) == 0) lps[wv][side * 2 * NH + h] = fc * ci * inv_avg;
+      }
+      double te[2] = {0.0, 0.0};
+      for (int jj = 0; jj < 2; ++jj) {
+        const int c = lane + 64 * jj;
+        if (c < E) {
+          const int sl = d.slot[c];
+          const double pr = side ? d.par[sl] : 1.0;
+          const double gr = ga[std::size_t(rcv) * E + c];
+          te[jj] = gr * pY[std::size_t(p) * 24 + d.sh[c]] * pr;
+          lt[wv][side][c] = gr * fc * al[side * 2 * NH + NH + sl] * pr;
+        }
+      }
+      for (int sl = 0; sl < NH; ++sl) {
+        double part = 0.0;
+        for (int jj = 0; jj < 2; ++jj) {
+          const int c = lane + 64 * jj;
+          if (c >= d.off[sl] && c < d.off[sl + 1]) part += te[jj];
+        }
+        const double ce = wsum(part);
+        dsum += ce * al[side * 2 * NH + NH + sl];
+        if (lane == 0) lps[wv][side * 2 * NH + NH + sl] = fc * ce * inv_avg;
+      }
+    }
+    if (lane == 0) dfc[p] = dsum;
   }
-  df[t] = acc;
+  __syncthreads();
+  if (on) {
+    if (lane < 4 * NH) psc[std::size_t(p) * 4 * NH + lane] = lps[wv][lane];
+    for (int c = lane; c < 2 * F; c += 64) {
+      const int which = c / F, cc = c % F, h = cc >> 5;
+      double acc = 0.0;
+      for (int side = 0; side < 2; ++side) {
+        const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
+        const double qv = qkv[std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + cc];
+        const double kv = qkv[std::size_t(snd) * 5 * F + (which ? 4 * F : F) + cc];
+        acc += lps[wv][side * 2 * NH + which * NH + h] * qv * kv;
+      }
+      df[std::size_t(p) * 2 * F + c] = acc;
+    }
+    if (lane < 24) {
+      double acc = 0.0;
+      for (int side = 0; side < 2; ++side)
+        for (int t = 0; t < d.shn[lane]; ++t) acc += lt[wv][side][d.shc[lane][t]];
+      double *y = dY + std::size_t(p) * 24 + lane;
+      *y = first ? acc : *y + acc;
+    }
+  }
 }
 
-// dE/dr of the pair from the cutoff and the radial basis.
-__global__ void g_pair_radial_bwd(int R, const int *nact, int cap, const double *__restrict__ pr,
-                                  const double *__restrict__ dfc, const double *__restrict__ grbf,
-                                  const double *__restrict__ rbf, const double *__restrict__ kk,
-                                  const double *__restrict__ kr, double gamma, double rc, double *__restrict__ dr) {
-  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+// dE/dr of the pair from the cutoff and the radial basis; one wavefront per
+// pair, lanes over the basis (R <= 64).
+__global__ __launch_bounds__(256) void g_pair_radial_bwd(int R, const int *nact, int cap, const double *__restrict__ pr,
+                                                         const double *__restrict__ dfc, const double *__restrict__ grbf,
+                                                         const double *__restrict__ rbf, const double *__restrict__ kk,
+                                                         const double *__restrict__ kr, double gamma, double rc,
+                                                         double *__restrict__ dr) {
+  const int lane = threadIdx.x & 63;
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (p >= min(*nact, cap)) return;
   const double r = pr[p];
-  double grad = 0.0;
-  if (r < rc) {
-    const double t = r / rc;
-    grad += dfc[p] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
-  }
   const double xb = exp(-gamma * r);
-  if (xb > 1e-6 && xb < 1.0 - 1e-6) {
-    const double a = gamma * xb / (1.0 - xb);
-    for (int k = 0; k < R; ++k)
-      grad += grbf[std::size_t(p) * R + k] * rbf[std::size_t(p) * R + k] * (-gamma * kk[k] + a * kr[k]);
+  double t = 0.0;
+  if (lane < R && xb > 1e-6 && xb < 1.0 - 1e-6) {
+    const std::size_t i = std::size_t(p) * R + lane;
+    t = grbf[i] * rbf[i] * (-gamma * kk[lane] + gamma * xb / (1.0 - xb) * kr[lane]);
   }
-  dr[p] += grad;
+  t = wsum(t);
+  if (lane == 0) {
+    double grad = t;
+    if (r < rc) {
+      const double u = r / rc;
+      grad += dfc[p] * (-30.0 * u * u * (1.0 - u) * (1.0 - u) / rc);
+    }
+    dr[p] += grad;
+  }
 }
 
 unsigned blocks_for(std::size_t n, int per) { return unsigned((n + std::size_t(per) - 1) / std::size_t(per)); }
@@ -703,7 +756,7 @@ enum Buf {
   XS = 0, EVS, QKV, QKIS, AEV, N1, N1HAT, N1IS, HPRE, TOUT, PRE2HAT, PRE2IS,
   ACT, HID, CAT, HACT, HHPRE, HKEY, GHEAD,
   GX, GEV, GT, GCAT, GA, GP, GHID, GN1, GAINV, GQKV,
-  RBF, PS, PF, PALPHA, HT, H2T, GH, GH2, DF, PSC, CPART, DFC, DS, GRBF,
+  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF,
   NBUF
 };
 static_assert(NBUF <= GenericPath::kBuffers, "generic path buffer table");
@@ -713,8 +766,23 @@ void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const doub
           const double *bias, double *Y, int ldy, const double *aux = nullptr, int ldaux = 0,
           const double *res = nullptr, int ldres = 0, double *Y2 = nullptr, int ldy2 = 0) {
   if (rows <= 0) return;
-  GemmArgs A{rows, rows_dev, K, O, X, ldx, W, bias, Y, ldy, Y2, ldy2, aux, ldaux, res, ldres};
-  hipLaunchKernelGGL((g_gemm<EPI, WKO>), dim3(blocks_for(std::size_t(rows), 64), blocks_for(std::size_t(O), 64)),
+  GemmArgs A{rows, rows_dev, K, O, X, ldx, W, bias, Y, ldy, Y2, ldy2, aux, ldaux, res, ldres,
+             1, 0, 0, 0, 0, 0, 0, 0};
+  if (O > 64)
+    hipLaunchKernelGGL((g_gemm<EPI, WKO, 128>), dim3(blocks_for(std::size_t(rows), 64), blocks_for(std::size_t(O), 128)),
+                       dim3(256), 0, s, A);
+  else
+    hipLaunchKernelGGL((g_gemm<EPI, WKO, 64>), dim3(blocks_for(std::size_t(rows), 64), 1), dim3(256), 0, s, A);
+}
+// Per-head 32 x 32 projections as one batched launch (O = K = 32).
+template <int EPI, bool WKO>
+void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int ldx, long xbs0, long xbs1,
+                const double *W, long wbs, double *Y, int ldy, long ybs0, long ybs1, const double *res = nullptr,
+                int ldres = 0, long rbs0 = 0, long rbs1 = 0) {
+  if (rows <= 0) return;
+  GemmArgs A{rows, nullptr, 32, 32, X, ldx, W, nullptr, Y, ldy, nullptr, 0, nullptr, 0, res, ldres,
+             nbx, xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs};
+  hipLaunchKernelGGL((g_gemm<EPI, WKO, 64>), dim3(blocks_for(std::size_t(rows), 64), 1, unsigned(nby * nbx)),
                      dim3(256), 0, s, A);
 }
 }  // namespace
@@ -745,6 +813,12 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
     d.par[s] = (l & 1) ? -1.0 : 1.0;
   }
   d.E = off;
+  for (int m = 0; m < 24; ++m) d.shn[m] = 0;
+  for (int c = 0; c < d.E; ++c) {
+    const int m = d.sh[c];
+    d.shc[m][int(d.shn[m])] = static_cast<signed char>(c);
+    d.shn[m] = static_cast<signed char>(d.shn[m] + 1);
+  }
   layers_ = a.layers;
   const std::size_t F = std::size_t(d.F), R = std::size_t(d.R), FH = std::size_t(d.FH), NH = std::size_t(d.NH),
                     NI = std::size_t(d.NI), E = std::size_t(d.E), HK = std::size_t(d.HK), HH = 64;
@@ -769,6 +843,20 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
       B.eb0[k] = up(m.f64(f + "mlp_ev.0.bias", {FH}));
       B.e1[k] = up(m.f64(f + "mlp_ev.mlp_ev_layer_1.0.weight", {F, FH}));
       B.eb1[k] = up(m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F}));
+      {
+        const auto w1 = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.weight", {F, F});
+        const auto e1 = m.f64(f + "mlp_ev.mlp_ev_layer_1.0.weight", {F, FH});
+        auto bc = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F});
+        const auto eb1 = m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F});
+        std::vector<double> wc(F * (F + FH));
+        for (std::size_t o = 0; o < F; ++o) {
+          for (std::size_t i = 0; i < F; ++i) wc[o * (F + FH) + i] = w1[o * F + i];
+          for (std::size_t i = 0; i < FH; ++i) wc[o * (F + FH) + F + i] = e1[o * FH + i];
+          bc[o] += eb1[o];
+        }
+        B.wcat[k] = up(wc);
+        B.bcat[k] = up(bc);
+      }
     }
     B.att_cg = up(m.f64(at + "so3_conv_invariants.cg_rep", {E}));
     B.int_cg = up(m.f64(p + "interaction_block.so3_conv_invariants.cg_rep", {E}));
@@ -834,8 +922,8 @@ void GenericPath::carve(int N, int cap, const std::function<double *(int, std::s
       L * n * F, L * n * NI, L * n * F, L * n,
       n * F, n * F, n * NI, n * HO, n * HO, n * 128, n * HO,
       n * F, n * E, n * NI, n * NI, n * E, n * F, n * F, n * F, n * F, n * 5 * F,
-      P * R, L * P * NH, L * P * 2 * F, L * P * 4 * NH, P * F, P * FH, P * F, P * FH, P * 2 * F, P * 4 * NH,
-      P * 4 * NH, P, P * NH, P * R};
+      P * R, L * P * NH, L * P * 2 * F, L * P * 4 * NH, P * (F + FH), P * (F + FH), P * 2 * F, P * 4 * NH,
+      P, P * NH, P * R};
   for (int i = 0; i < NBUF; ++i) b_[i] = take(i, sizes[i]);
 }
 
@@ -862,21 +950,25 @@ void GenericPath::forward(const GContext &c) {
     double *hpb = b_[HPRE] + b * n * F, *tb = b_[TOUT] + b * n * NI;
     double *p2h = b_[PRE2HAT] + b * n * F, *p2i = b_[PRE2IS] + b * n;
     double *psb = b_[PS] + b * P * NH, *pfb = b_[PF] + b * P * 2 * F, *pab = b_[PALPHA] + b * P * 4 * NH;
-    hipLaunchKernelGGL(g_qkv, dim3(blocks_for(n * 5 * F, 256)), dim3(256), 0, s, N, F, NH, xb, B.wqkv, qb);
+    // q k v q_ev k_ev per head: out[w][h*32 + o] = sum_k x[h*32 + k] W[w][h][k][o]
+    // (kokkos_integrated_block0.cpp:257-287), batch z = w NH + h
+    gemm_heads<EPI_STORE, true>(s, N, 5, NH, xb, F, 0, 32, B.wqkv, 1024, qb, 5 * F, F, 32);
     if (c.qk_norm)
       hipLaunchKernelGGL(g_qk_norm, dim3(blocks_for(n * 4 * NH, 256)), dim3(256), 0, s, N, F, NH, qb,
                          b_[QKIS] + b * n * 4 * NH);
     // pair invariants and both filters (kokkos_integrated_block0.cpp:166-255)
     hipLaunchKernelGGL(g_pair_inv, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, evb,
                        B.att_cg, psb);
+    // per filter: the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)] (F + FH
+    // wide), then f = [W1 | E1] row + b1 + e1 in one GEMM
+    const int HW = F + FH;
     for (int w = 0; w < 2; ++w) {
-      gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], F);
-      gemm<EPI_STORE, false>(s, cap, c.nact, F, F, b_[HT], F, B.w1[w], B.b1[w], pfb + w * F, 2 * F);
-      gemm<EPI_SILU, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[H2T], FH);
-      gemm<EPI_ACCUM, false>(s, cap, c.nact, FH, F, b_[H2T], FH, B.e1[w], B.eb1[w], pfb + w * F, 2 * F);
+      gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
+      gemm<EPI_SILU, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
+      gemm<EPI_STORE, false>(s, cap, c.nact, HW, F, b_[HT], HW, B.wcat[w], B.bcat[w], pfb + w * F, 2 * F);
     }
-    hipLaunchKernelGGL(g_alpha, dim3(blocks_for(P * 4 * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, pfb,
-                       c.inv_avg, pab);
+    hipLaunchKernelGGL(g_alpha, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, pfb, c.inv_avg,
+                       pab);
     hipLaunchKernelGGL(g_attn_msg, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
                        c.pfc, pab, B.ln1w, B.ln1b, c.ln_eps, c.norm1, n1b, n1hb, n1ib, b_[ACT], aevb);
     // post-attention node chain (kokkos_post_attention_block0.cpp:165-300)
@@ -909,7 +1001,6 @@ void GenericPath::reverse(const GContext &c) {
   const int N = c.N, cap = c.cap, F = d.F, E = d.E, NH = d.NH, NI = d.NI, R = d.R, FH = d.FH;
   const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1));
   const unsigned g4 = blocks_for(n, 4);
-  const unsigned gP = blocks_for(P, 256);
   // heads in reverse to dE/dx of the last block's output
   hipLaunchKernelGGL(g_heads_bwd, dim3(g4), dim3(256), 0, s, d, N, c.z, b_[HHPRE], c.qseed, c.dh, c.heff, c.dc,
                      c.c6eff, hw_, b_[GHEAD]);
@@ -934,40 +1025,45 @@ void GenericPath::reverse(const GContext &c) {
     gemm<EPI_DSILU_ADD, true>(s, N, nullptr, F, F, b_[GHID], F, B.m1, nullptr, b_[GN1], F, n1b, F, b_[GP], F);
     hipLaunchKernelGGL(g_ln1_bwd, dim3(g4), dim3(256), 0, s, F, N, b_[GN1], B.ln1w, n1hb, n1ib, c.norm1, b_[GAINV]);
     // attention reverse per pair (kokkos_attention_scatter_reverse.cpp:280-500)
-    hipLaunchKernelGGL(g_attn_bwd_scal, dim3(blocks_for(P * 2 * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb,
-                       c.pY, c.pfc, b_[GAINV], b_[GA], c.inv_avg, b_[CPART], b_[PSC]);
-    hipLaunchKernelGGL(g_attn_bwd_pair, dim3(blocks_for(P * 25, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, c.pfc,
-                       pab, b_[CPART], b_[GA], b == layers_ - 1 ? 1 : 0, c.dY, b_[DFC]);
-    hipLaunchKernelGGL(g_attn_bwd_df, dim3(blocks_for(P * 2 * F, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb,
-                       b_[PSC], b_[DF]);
+    hipLaunchKernelGGL(g_attn_bwd_pairs, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, c.pY,
+                       c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg, b == layers_ - 1 ? 1 : 0, b_[PSC], b_[DF], c.dY,
+                       b_[DFC]);
     if (b > 0)
       hipLaunchKernelGGL(g_attn_bwd_node, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
                          c.pfc, pab, b_[PSC], b_[GAINV], b_[GQKV]);
     // filter reverse (kokkos_block2_attention_input_reverse.cpp:198-336)
+    // per filter: the hidden row's pre-activations again, its adjoint
+    // (df [W1 | E1]) (.) silu'(pre) in one GEMM, then through W0 and E0
+    const int HW = F + FH;
     for (int w = 0; w < 2; ++w) {
-      gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], F);
-      gemm<EPI_DSILU, true>(s, cap, c.nact, F, F, b_[DF] + w * F, 2 * F, B.w1[w], nullptr, b_[GH], F, b_[HT], F);
-      if (w == 0)
-        gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], F, B.w0[w], nullptr, b_[GRBF], R);
-      else
-        gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], F, B.w0[w], nullptr, b_[GRBF], R);
-      gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[H2T], FH);
-      gemm<EPI_DSILU, true>(s, cap, c.nact, F, FH, b_[DF] + w * F, 2 * F, B.e1[w], nullptr, b_[GH2], FH, b_[H2T], FH);
-      if (w == 0)
-        gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH2], FH, B.e0[w], nullptr, b_[DS], NH);
-      else
-        gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH2], FH, B.e0[w], nullptr, b_[DS], NH);
+      gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
+      gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
+      gemm<EPI_DSILU, true>(s, cap, c.nact, F, HW, b_[DF] + w * F, 2 * F, B.wcat[w], nullptr, b_[GH], HW, b_[HT], HW);
+      if (w == 0) {
+        gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
+        gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+      } else {
+        gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
+        gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+      }
     }
-    hipLaunchKernelGGL(g_pair_radial_bwd, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC], b_[GRBF],
-                       b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
+    hipLaunchKernelGGL(g_pair_radial_bwd, dim3(blocks_for(P, 4)), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC],
+                       b_[GRBF], b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
     // the adjoints of the block's inputs feed the block below; block 0's
     // inputs (embedding, ev = 0) do not depend on the positions
     if (b > 0) {
       if (c.qk_norm)
         hipLaunchKernelGGL(g_qk_norm_bwd, dim3(blocks_for(n * 4 * NH, 256)), dim3(256), 0, s, N, F, NH, qb,
                            b_[QKIS] + b * n * 4 * NH, b_[GQKV]);
-      hipLaunchKernelGGL(g_qkv_bwd, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, N, F, NH, b_[GQKV], B.wqkv,
-                         b_[GAINV], gx);
+      // gx = gainv + sum_w gqkv[w] W[w]^T per head, batch z = h
+      for (int w = 0; w < 5; ++w) {
+        if (w == 0)
+          gemm_heads<EPI_ADD, false>(s, N, 1, NH, b_[GQKV], 5 * F, 0, 32, B.wqkv, 1024, gx, F, 0, 32, b_[GAINV], F,
+                                     0, 32);
+        else
+          gemm_heads<EPI_ACCUM, false>(s, N, 1, NH, b_[GQKV] + w * F, 5 * F, 0, 32, B.wqkv + std::size_t(w) * NH * 1024,
+                                       1024, gx, F, 0, 32);
+      }
       if (!c.resid->empty())
         hipLaunchKernelGGL(g_scale, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, n * F, (*c.resid)[b], gx);
       hipLaunchKernelGGL(g_ev_bwd, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, evb, B.att_cg,

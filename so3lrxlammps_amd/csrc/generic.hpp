@@ -36,6 +36,8 @@ struct GDims {
   signed char slot[kGMaxE], sh[kGMaxE];
   signed char off[9];
   double par[8];  // (-1)^l of each slot: the harmonics of the reversed direction
+  // the channels replicating unique harmonic m: shc[m][0 .. shn[m])
+  signed char shn[24], shc[24][8];
 };
 
 // Device weights of one interaction block, in the model file's layouts.
@@ -43,6 +45,9 @@ struct GBlock {
   const double *wqkv;  // (5, NH, 32, 32): q k v q_ev k_ev, (head, in, out)
   const double *w0[2], *b0[2], *w1[2], *b1[2];    // radial layers (F, R) (F) (F, F) (F)
   const double *e0[2], *eb0[2], *e1[2], *eb1[2];  // spherical layers (FH, NH) (FH) (F, FH) (F)
+  // both output layers side by side, (F, F + FH): [W1 | E1], and b1 + eb1,
+  // so one GEMM over the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)]
+  const double *wcat[2], *bcat[2];
   const double *att_cg, *int_cg;                  // (E)
   const double *ln1w, *ln1b, *ln2w, *ln2b;        // (F); RMSNorm and none: 1 and 0
   const double *m1, *m1b, *m2, *m2b;              // (F, F) (F)
