@@ -95,3 +95,27 @@ def test_wide_device_path_and_replay(models):
     assert abs(runs[0][0] - e0) <= 1e-11 * abs(e0)
     assert np.abs(runs[0][2] - f0).max() <= 1e-10
     assert np.abs(runs[0][1] - w0).max() <= 1e-10 * max(1.0, np.abs(w0).max())
+
+
+def test_wide_packed_images(models):
+    """64 config-2 molecules as packed images (each with its own (Q, M)) on
+    the perturbed lift: per-image charge correction and embedding on the
+    generic kernels, rows path against the oracle."""
+    from so3lrxlammps_amd import Context, Lists, systems
+    from test_gpu_configs import _check as check_config
+    z, x, offs, qs, ms, extent = systems.packed_molecules(n_mol=64)
+    print("case lift_perturbed packed images: %d atoms in %d images" % (len(z), len(qs)), flush=True)
+    img = np.repeat(np.arange(len(qs)), np.diff(offs))
+    sr, lr = support.build_graphs(x, None)
+    out = Oracle(models["lift_perturbed"]).evaluate(z, sr, lr, image=img, image_charge=qs, image_multiplicity=ms)
+    c = Context(models["lift_perturbed"], 0)
+    c.set_images(z, offs, qs, ms)
+    lists = Lists(x, np.zeros(3), np.full(3, extent), (0, 0, 0))
+    c.set_topology(lists)
+    e, f, ea, w = c.compute(lists.rows_positions(x))
+    check_config(e, f, w, out)
+    t = c.terms()
+    c.close()
+    assert np.abs(t["image_energy"] - out["image_energy"]).max() <= 1e-10 * np.abs(out["image_energy"]).max()
+    for k in range(len(qs)):
+        assert abs(t["charges"][offs[k]:offs[k + 1]].sum() - qs[k]) < 1e-12

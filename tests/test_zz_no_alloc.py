@@ -96,3 +96,28 @@ def test_noalloc_matches_compute_device():
     assert err.value.code == _lib.ERR_ARGUMENT and "bytes of work space" in str(err.value)
     for c in (c1, c2, c3):
         c.close()
+
+
+def test_noalloc_generic_widths(tmp_path):
+    """The same agreement for a model on the generic kernels (F = 256, R = 64,
+    duplicated degrees: support.lifted_model, weights perturbed), two calls
+    in a row, the second smaller."""
+    import torch
+    from so3lrxlammps_amd import Context, Lists
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+    path = support.perturbed_model(tmp_path / "wide_p.so3lr", seed=23, scale=0.2,
+                                   base=support.lifted_model(tmp_path / "wide.so3lr"))
+    ctx = Context(path, 0)
+    for name in ("alanine_cation", "acetate"):
+        ref, z, pos, _ = support.load_golden(name)
+        print("noalloc generic widths: %s, %d atoms" % (name, len(z)), flush=True)
+        ctx.set_system(z, ref.get("charge", 0), ref.get("multiplicity", 1))
+        lists = Lists(pos, pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0))
+        ctx.set_topology(lists)
+        xr = lists.rows_positions(pos)
+        got = _evaluate(ctx, xr, len(z), True, stream)
+        want = _evaluate(ctx, xr, len(z), False, stream)
+        _same(got, want, name)
+    ctx.close()
