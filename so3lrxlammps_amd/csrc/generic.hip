@@ -71,17 +71,22 @@ struct GemmArgs {
 
 typedef double gv4d __attribute__((ext_vector_type(4)));
 
-// 64 x BN output tiles (BN = 64 or 128) on fp64 MFMA 16x16x4: four
-// wavefronts in 2 x 2, each 32 rows x BN/2 columns (2 x BN/32 MFMA tiles).
+// 64 x BN output tiles (BN = 32 NT, up to 320 columns: a filter or node
+// layer's whole output row in one workgroup, so X is read once) on fp64 MFMA
+// 16x16x4: four wavefronts in 2 x 2, each 32 rows x BN/2 columns (2 x NT
+// MFMA tiles).
 // D[i][j] += sum_k A[i][k] B[k][j] with A[i][k] = X[row i][k] (lane l gives
 // i = l % 16, k = l / 16) and B[k][j] = op(W)[k][col j] (lane l gives
 // k = l / 16, j = l % 16); lane l holds D[l / 16 + 4 r][l % 16] in register
 // r, so sixteen lanes write sixteen adjacent columns of one row.  K runs in
 // chunks of 16 through LDS; the next chunk's global loads are issued before
 // the current chunk's MFMAs.
-template <int EPI, bool WKO, int BN>
-__global__ __launch_bounds__(256) void g_gemm(GemmArgs A) {
-  constexpr int NT = BN / 32;      // MFMA column tiles per wavefront
+#ifndef SO3LR_GEMM_WAVES
+#define SO3LR_GEMM_WAVES 3
+#endif
+template <int EPI, bool WKO, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_GEMM_WAVES))) void g_gemm(GemmArgs A) {
+  constexpr int BN = 32 * NT;      // output columns per workgroup (NT MFMA column tiles per wavefront)
   constexpr int WPT = BN / 16;     // W chunk values per thread (BN x 16 / 256)
   __shared__ double xs[64][17];
   __shared__ double ws[BN][17];
@@ -761,6 +766,11 @@ enum Buf {
 };
 static_assert(NBUF <= GenericPath::kBuffers, "generic path buffer table");
 
+#ifndef SO3LR_GEMM_MAX_NT
+#define SO3LR_GEMM_MAX_NT 4
+#endif
+constexpr int kGemmMaxNT = SO3LR_GEMM_MAX_NT;
+
 template <int EPI, bool WKO>
 void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const double *X, int ldx, const double *W,
           const double *bias, double *Y, int ldy, const double *aux = nullptr, int ldaux = 0,
@@ -768,11 +778,19 @@ void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const doub
   if (rows <= 0) return;
   GemmArgs A{rows, rows_dev, K, O, X, ldx, W, bias, Y, ldy, Y2, ldy2, aux, ldaux, res, ldres,
              1, 0, 0, 0, 0, 0, 0, 0};
-  if (O > 64)
-    hipLaunchKernelGGL((g_gemm<EPI, WKO, 128>), dim3(blocks_for(std::size_t(rows), 64), blocks_for(std::size_t(O), 128)),
-                       dim3(256), 0, s, A);
-  else
-    hipLaunchKernelGGL((g_gemm<EPI, WKO, 64>), dim3(blocks_for(std::size_t(rows), 64), 1), dim3(256), 0, s, A);
+  // column blocks of at most 32 kGemmMaxNT columns; NT = 32-column tiles per wavefront
+  const int cmax = 32 * kGemmMaxNT;
+  const int nb = (O + cmax - 1) / cmax, cols = (O + nb - 1) / nb, tiles = (cols + 31) / 32;
+  const dim3 grid(blocks_for(std::size_t(rows), 64), unsigned(nb));
+#define G_GEMM_NT(NT)                                                              \
+  if (tiles <= NT) {                                                               \
+    A.O = O;                                                                       \
+    hipLaunchKernelGGL((g_gemm<EPI, WKO, NT>), grid, dim3(256), 0, s, A);          \
+    return;                                                                        \
+  }
+  G_GEMM_NT(2) G_GEMM_NT(4) G_GEMM_NT(6) G_GEMM_NT(8) G_GEMM_NT(10)
+#undef G_GEMM_NT
+  throw std::logic_error("SO3LR: generic GEMM with more than 320 columns per block");
 }
 // Per-head 32 x 32 projections as one batched launch (O = K = 32).
 template <int EPI, bool WKO>
@@ -782,7 +800,7 @@ void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int 
   if (rows <= 0) return;
   GemmArgs A{rows, nullptr, 32, 32, X, ldx, W, nullptr, Y, ldy, nullptr, 0, nullptr, 0, res, ldres,
              nbx, xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs};
-  hipLaunchKernelGGL((g_gemm<EPI, WKO, 64>), dim3(blocks_for(std::size_t(rows), 64), 1, unsigned(nby * nbx)),
+  hipLaunchKernelGGL((g_gemm<EPI, WKO, 2>), dim3(blocks_for(std::size_t(rows), 64), 1, unsigned(nby * nbx)),
                      dim3(256), 0, s, A);
 }
 }  // namespace
