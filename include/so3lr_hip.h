@@ -52,7 +52,11 @@ typedef struct so3lr_ctx so3lr_ctx;
  * Read and validate a .so3lr model, negotiate capabilities, upload weights to
  * HIP device `device`.  Replaces PairSO3LRNativeMPI::settings model loading
  * (plugins/lammps/pair_so3lr_native_mpi.cpp:1097-1137) and NativeModel::load
- * (src/native_model.cpp:325-406).
+ * (src/native_model.cpp:325-406).  Accepts what the reference's MPI path
+ * accepts (src/so3lr_capabilities.cpp:54-85): F = 128 or 256 features in
+ * heads of 32, R = 32 or 64, sorted degree slots (repeats allowed), any
+ * energy/charge head width and the optional operators; refusals return
+ * SO3LR_ERR_MODEL with the rule in so3lr_last_error(NULL).
  */
 int so3lr_create(const char *model_path, int device, so3lr_ctx **out);
 
