@@ -153,7 +153,7 @@ def _bernstein_elevation(n, m):
     return M
 
 
-def lifted_model(path, base=MODEL, R=64, split=0.3):
+def lifted_model(path, base=MODEL, R=64, split=0.3, copies=2):
     """The F = 256 model with R = 64 radial functions and the duplicated degree
     slots 1,1,2,2,3,3,4,4 (the "l" widths the reference runs,
     so3lr_capabilities.cpp:54-85) that computes exactly the same function as
@@ -170,24 +170,32 @@ def lifted_model(path, base=MODEL, R=64, split=0.3):
     Bernstein basis re-expressed in the degree-R-1 basis (exact degree
     elevation).  The energy and charge heads keep their hidden width 128, so
     it differs from F (the "256 -> 128" heads, kokkos_output_heads.cpp:16-19).
-    Energies, forces and the virial equal those of `base` up to rounding."""
+    Energies, forces and the virial equal those of `base` up to rounding.
+    copies=1 keeps F = 128 and the degrees and changes only the radial basis
+    (to R functions by the same degree elevation)."""
     from so3lrxlammps_amd.model_file import read_model, write_model
     manifest, arrays = read_model(base)
     arch = manifest["architecture"]
     F, R0 = int(arch["invariant_features"]), int(arch["radial_basis_features"])
     assert F == 128 and int(arch["attention_heads"]) == 4 and int(arch["euclidean_degree_channels"]) == 4
-    F2, S2 = 2 * F, 8
+    assert copies in (1, 2)
+    c = copies
+    F2, S2 = c * F, 4 * c
+
+    def part(n):  # weight of copy k of n lifted entries: split, 1 - split (1 unlifted)
+        k = np.arange(n) % c if c == 2 else np.zeros(n, dtype=int)
+        return np.where(k == 0, split, 1.0 - split) if c == 2 else np.ones(n)
     h2 = np.arange(F2) // 32
-    cmap = (h2 // 2) * 32 + np.arange(F2) % 32
-    csplit = np.where(h2 % 2 == 0, split, 1.0 - split)
-    smap = np.arange(S2) // 2
-    ssplit = np.where(np.arange(S2) % 2 == 0, split, 1.0 - split)
-    hmap = np.arange(F2 // 4) // 2
-    hsplit = np.where(np.arange(F2 // 4) % 2 == 0, split, 1.0 - split)
+    cmap = (h2 // c) * 32 + np.arange(F2) % 32
+    csplit = part(F2 // 32)[h2]
+    smap = np.arange(S2) // c
+    ssplit = part(S2)
+    hmap = np.arange(F2 // 4) // c
+    hsplit = part(F2 // 4)
     reps0 = [3, 5, 7, 9]
     off0 = np.concatenate([[0], np.cumsum(reps0)])
-    reps = [reps0[s // 2] for s in range(S2)]
-    chmap = np.concatenate([off0[s // 2] + np.arange(reps[s]) for s in range(S2)])
+    reps = [reps0[s // c] for s in range(S2)]
+    chmap = np.concatenate([off0[s // c] + np.arange(reps[s]) for s in range(S2)])
     seg = np.concatenate([np.full(reps[s], s) for s in range(S2)])
     elev = _bernstein_elevation(R0 - 1, R - R0)
     rowmap = np.concatenate([cmap, F + smap])
@@ -206,7 +214,7 @@ def lifted_model(path, base=MODEL, R=64, split=0.3):
             out[k] = a[cmap]
         elif k.startswith(("model.charge_embedding.", "model.spin_embedding.")):
             if t[-2] == "Wq":
-                out[k] = a[cmap] * np.sqrt(2.0) * csplit[:, None]
+                out[k] = a[cmap] * np.sqrt(float(c)) * csplit[:, None]
             elif t[-1] in ("Wk", "Wv"):
                 out[k] = a[:, cmap]
             else:
@@ -220,7 +228,7 @@ def lifted_model(path, base=MODEL, R=64, split=0.3):
             out[k] = (R - 1 - np.arange(R)).astype(np.int64)
         elif k.startswith("model.euclidean_transformers."):
             if t[-1] in ("W_q_inv", "W_k_inv", "W_v_inv", "W_q_ev", "W_k_ev"):
-                out[k] = a[np.arange(F2 // 32) // 2]
+                out[k] = a[np.arange(F2 // 32) // c]
             elif t[-1] == "degree_repeats":
                 out[k] = np.array(reps, dtype=np.int64)
             elif t[-1] == "cg_rep":
@@ -263,6 +271,31 @@ def lifted_model(path, base=MODEL, R=64, split=0.3):
     arch["parameter_elements"] = int(sum(np.asarray(out[r["state_key"]]).size for r in manifest["tensors"]
                                          if r["role"] == "parameter"))
     write_model(str(path), manifest, out)
+    return str(path)
+
+
+def head_width_model(path, width, base=MODEL, live=False):
+    """`base` with the energy and charge heads' hidden layer widened to
+    `width` units (> F): with the new units' output weights zero (live=False)
+    the same function with a head width other than F
+    (so3lr_architecture.cpp:444-446); live=True gives them small random output
+    weights (another function)."""
+    from so3lrxlammps_amd.model_file import read_model, write_model
+    manifest, arrays = read_model(base)
+    rng = np.random.default_rng(29)
+    for pre, w1, b1, w2 in (("model.atomic_energy_output_block.", "layers.0.weight", "layers.0.bias",
+                             "final_layer.weight"),
+                            ("model.partial_charges_output_block.", "transform_inv_features.0.weight",
+                             "transform_inv_features.0.bias", "transform_inv_features.2.weight")):
+        W, bb, W2 = arrays[pre + w1], arrays[pre + b1], arrays[pre + w2]
+        extra = width - W.shape[0]
+        arrays[pre + w1] = np.concatenate([W, 0.1 * rng.standard_normal((extra, W.shape[1]))])
+        arrays[pre + b1] = np.concatenate([bb, 0.1 * rng.standard_normal(extra)])
+        new = 0.05 * rng.standard_normal((1, extra)) if live else np.zeros((1, extra))
+        arrays[pre + w2] = np.concatenate([W2, new], axis=1)
+    for rec in manifest["tensors"]:
+        rec["shape"] = list(np.shape(arrays[rec["state_key"]]))
+    write_model(str(path), manifest, arrays)
     return str(path)
 
 

@@ -30,11 +30,16 @@ def models(tmp_path_factory):
         "lift_options": support.lifted_model(d / "lift_opt.so3lr", base=options),
         "deg1123": support.degrees_model(d / "d1123.so3lr", (1, 1, 2, 3)),
         "deg1233": support.degrees_model(d / "d1233.so3lr", (1, 2, 3, 3)),
+        # the other accepted width combinations (tests/test_oracle_wide.py)
+        "f128_r64": support.lifted_model(d / "r64.so3lr", copies=1, R=64),
+        "f256_r32": support.lifted_model(d / "f256r32.so3lr", copies=2, R=32),
+        "head_width_192": support.head_width_model(d / "hk192_live.so3lr", 192, live=True),
     }
 
 
 CASES = [(m, n) for m in ("lift", "lift_perturbed", "lift_options", "deg1123", "deg1233")
          for n in ("acetate", "alanine_cation", "water3000")]
+CASES += [(m, n) for m in ("f128_r64", "f256_r32", "head_width_192") for n in ("acetate", "water3000")]
 
 
 @pytest.mark.parametrize("model,name", CASES)

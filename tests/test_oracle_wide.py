@@ -15,7 +15,10 @@ mathematics fixes:
 * duplicated and missing degrees at F = 128 (slots 1,1,2,3 and 1,2,3,3): the
   energy is invariant under rotations (which fails if a slot's channels are
   not the harmonics of its degree) and the forces are finite differences of
-  the energy.
+  the energy;
+* the other width combinations (F = 128 with R = 64, F = 256 with R = 32,
+  heads 192 wide at F = 128), each built to equal the shipped model; heads
+  whose new units feed the outputs, by finite differences.
 """
 import numpy as np
 import pytest
@@ -129,6 +132,32 @@ def test_wide_virial_finite_difference(wide_perturbed):
             es.append(wide_perturbed.evaluate(z, (sr[0], sr[1], sr[2] @ M.T), (lr[0], lr[1], lr[2] @ M.T))["energy"])
         dEdt = (es[0] - es[1]) / (2 * h)
         assert abs(-dEdt - out["virial"][k]) < 2e-6 * max(1.0, abs(out["virial"][k])), (k, -dEdt, out["virial"][k])
+
+
+@pytest.mark.parametrize("kind", ["f128_r64", "f256_r32", "head_width_192"])
+def test_other_width_combinations_equal_base(tmp, v1, kind):
+    """The other combinations of the accepted widths, each built to compute
+    the shipped model's function: F = 128 with R = 64 (degree elevation
+    only), F = 256 with R = 32 (the lift without elevation), and energy/charge
+    heads 192 wide at F = 128 (64 new units with zero output weights)."""
+    path = {"f128_r64": lambda: support.lifted_model(tmp / "r64.so3lr", copies=1, R=64),
+            "f256_r32": lambda: support.lifted_model(tmp / "f256r32.so3lr", copies=2, R=32),
+            "head_width_192": lambda: support.head_width_model(tmp / "hk192.so3lr", 192)}[kind]()
+    orc = Oracle(path)
+    widths = {"f128_r64": (128, 64, 128), "f256_r32": (256, 32, 128), "head_width_192": (128, 32, 192)}[kind]
+    assert (orc._st.F, orc._st.R, orc._st.head_hidden) == widths
+    for name in ("acetate", "alanine_cation"):
+        z, pos, q, m = _golden(name)
+        _same(_run(orc, z, pos, q, m), _run(v1, z, pos, q, m))
+
+
+def test_live_head_width_forces_finite_difference(tmp, v1):
+    """Heads 192 wide whose new units feed the outputs: another function
+    (checked), forces = -dE/dx."""
+    orc = Oracle(support.head_width_model(tmp / "hk192_live.so3lr", 192, live=True))
+    z, pos, q, m = _golden("acetate")
+    assert abs(_run(orc, z, pos, q, m)["energy"] - _run(v1, z, pos, q, m)["energy"]) > 1e-3
+    _fd_forces(orc, z, pos, q, m, (1, 5))
 
 
 @pytest.mark.parametrize("degrees", [(1, 1, 2, 3), (1, 2, 3, 3)])
