@@ -6,7 +6,8 @@ the 4.5 A cutoff, and packed images down to one atom each, with their own
 charge and multiplicity (a bare proton, an open-shell H atom, triplet O).
 Both the LAMMPS-rows path and the HBM-resident device path are checked at the
 bars of the other parity tests: energy 1e-10 relative, forces and virial
-1e-9 eV/A.
+1e-9 eV/A; each case runs on the shipped model (fused kernels) and on an
+F = 256 model (generic kernels).
 """
 import numpy as np
 import pytest
@@ -17,9 +18,20 @@ from oracle.oracle import Oracle
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(scope="module", params=["v1", "generic"])
+def model(request, tmp_path_factory):
+    """The shipped model (fused v1 kernels) and a perturbed F = 256, R = 64
+    lift with duplicated degrees (generic kernels)."""
+    if request.param == "v1":
+        return support.MODEL
+    d = tmp_path_factory.mktemp("edges")
+    return support.perturbed_model(d / "wide_p.so3lr", seed=23, scale=0.2,
+                                   base=support.lifted_model(d / "wide.so3lr"))
+
+
 @pytest.fixture(scope="module")
-def orc():
-    return Oracle(support.MODEL)
+def orc(model):
+    return Oracle(model)
 
 
 def _check(e, f, w, out):
@@ -28,14 +40,14 @@ def _check(e, f, w, out):
     assert np.abs(w - out["virial"]).max() <= 1e-9 * max(1.0, np.abs(out["virial"]).max())
 
 
-def _both_paths(z, x, q, m, orc):
+def _both_paths(z, x, q, m, orc, model):
     """Rows path and device path of one open (non-periodic) system vs the oracle."""
     import torch
     from so3lrxlammps_amd import Context, Lists
     sr, lr = support.build_graphs(x, None)
     out = orc.evaluate(z, sr, lr, charge=q, multiplicity=m)
     lo, hi = x.min(0) - 20.0, x.max(0) + 20.0
-    c = Context(support.MODEL, 0)
+    c = Context(model, 0)
     c.set_system(z, q, m)
     lists = Lists(x, lo, hi, (0, 0, 0))
     c.set_topology(lists)
@@ -55,24 +67,24 @@ def _both_paths(z, x, q, m, orc):
     return out
 
 
-def test_single_atom(orc):
+def test_single_atom(orc, model):
     """One O atom (triplet): no pair of any kind, energy from the heads alone."""
     z = np.array([8])
     x = np.array([[1.0, 2.0, 3.0]])
-    out = _both_paths(z, x, 0.0, 3.0, orc)
+    out = _both_paths(z, x, 0.0, 3.0, orc, model)
     assert np.abs(out["forces"]).max() == 0.0
 
 
-def test_long_range_pair_only(orc):
+def test_long_range_pair_only(orc, model):
     """Na+ and Cl- 8 A apart: no short-range candidate, one long-range pair."""
     z = np.array([11, 17])
     x = np.array([[0.0, 0.0, 0.0], [8.0, 0.0, 0.0]])
-    out = _both_paths(z, x, 0.0, 1.0, orc)
+    out = _both_paths(z, x, 0.0, 1.0, orc, model)
     assert np.abs(out["forces"]).max() > 0.0
 
 
 @pytest.mark.parametrize("r", [4.5 - 1e-7, 4.5 + 1e-7])
-def test_pair_at_short_range_cutoff(orc, r):
+def test_pair_at_short_range_cutoff(orc, model, r):
     """Two water molecules with one O-O distance just inside / just outside
     the 4.5 A short-range cutoff."""
     oh, ang = 0.9572, np.deg2rad(104.52)
@@ -82,10 +94,10 @@ def test_pair_at_short_range_cutoff(orc, r):
     x = np.vstack([w1, w2])
     d = np.linalg.norm(x[:, None] - x[None], axis=-1)
     assert abs(d[0, 3] - r) < 1e-12
-    _both_paths(z, x, 0.0, 1.0, orc)
+    _both_paths(z, x, 0.0, 1.0, orc, model)
 
 
-def test_packed_tiny_images(orc):
+def test_packed_tiny_images(orc, model):
     """Packed images of 1-3 atoms, each with its own (Q, M), through the rows
     path: H2, a bare proton, an H atom (doublet), a triplet O atom, OH-."""
     from so3lrxlammps_amd import Context, Lists
@@ -105,7 +117,7 @@ def test_packed_tiny_images(orc):
     img = np.repeat(np.arange(len(qs)), np.diff(offs))
     sr, lr = support.build_graphs(x, None)
     out = orc.evaluate(z, sr, lr, image=img, image_charge=np.array(qs), image_multiplicity=np.array(ms))
-    c = Context(support.MODEL, 0)
+    c = Context(model, 0)
     c.set_images(z, offs, qs, ms)
     lo, hi = x.min(0) - 20.0, x.max(0) + 20.0
     lists = Lists(x, lo, hi, (0, 0, 0))
