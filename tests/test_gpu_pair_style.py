@@ -15,17 +15,27 @@ from so3lrxlammps_amd.pair_style import Atoms, LammpsError, PairSO3LRNativeMPI
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(scope="module", params=["v1", "generic"])
+def model(request, tmp_path_factory):
+    """The shipped model and a perturbed F = 256, R = 64 lift (generic kernels)."""
+    if request.param == "v1":
+        return support.MODEL
+    d = tmp_path_factory.mktemp("pair_style")
+    return support.perturbed_model(d / "wide_p.so3lr", seed=23, scale=0.2,
+                                   base=support.lifted_model(d / "wide.so3lr"))
+
+
 @pytest.fixture(scope="module")
-def orc():
-    return Oracle(support.MODEL)
+def orc(model):
+    return Oracle(model)
 
 
-def _setup(name, q, m):
+def _setup(name, q, m, model=support.MODEL):
     ref, z, pos, box = support.load_golden(name)
     symbols = ref["types"]
     types = np.array([symbols.index(support.SYMBOLS[int(zz)]) + 1 for zz in z])
     p = PairSO3LRNativeMPI()
-    p.settings([support.MODEL, repr(float(q)), repr(float(m))])
+    p.settings([model, repr(float(q)), repr(float(m))])
     p.coeff(["*", "*"] + list(symbols), len(symbols))
     assert p.init_one(1, 1) == p.short_range_cutoff
     if box is None:
@@ -46,8 +56,8 @@ def _check(res, out):
 
 
 @pytest.mark.parametrize("name,q,m", [("acetate", -1, 1), ("water3000", 0, 1)])
-def test_pair_style_matches_oracle(orc, name, q, m):
-    p, atoms, z, box = _setup(name, q, m)
+def test_pair_style_matches_oracle(orc, model, name, q, m):
+    p, atoms, z, box = _setup(name, q, m, model)
     rng = np.random.default_rng(4)
     for step in range(3):
         if step == 1:  # within half the 1 A skin: the lists are reused
