@@ -107,6 +107,21 @@ def traffic_per_launch(kernel, config, units_per_launch):
 KERNEL_WORK_UNIT = {v[0]: v[4] for v in KERNEL_WORK.values()}
 
 
+def kernel_work(widths):
+    """KERNEL_WORK plus the generic-width filter sections of a model on the
+    generic kernels: per active pair and block, both filters, algorithmic
+    2 (R F + NH F/4 + (F + F/4) F) MAC each way; the reverse also issues the
+    hidden row's recompute (R F + NH F/4)."""
+    work = dict(KERNEL_WORK)
+    F, R = widths["invariant_features"], widths["radial_basis_features"]
+    NH, FH = len(widths["degree_slots"]), widths["invariant_features"] // 4
+    alg = 2 * 2 * (R * F + NH * FH + (F + FH) * F)
+    work["generic_filter_fwd"] = ("g_gemm: filter forward (6 launches)", "mfma", alg, alg, "pair")
+    work["generic_filter_bwd"] = ("g_gemm: filter reverse (10 launches)", "mfma", alg,
+                                  alg + 2 * 2 * (R * F + NH * FH), "pair")
+    return work
+
+
 def cpu_baseline(z, x, box, periodic, images, seconds_budget):
     """Oracle (CPU restatement of the reference math, OpenMP) timed on the
     host cores: repeated E+F+virial calls on a bounded sample of the same
@@ -421,7 +436,8 @@ def main():
                     help="run a plain device copy of this size first (HBM-counter calibration)")
     ap.add_argument("--model", default=MODEL,
                     help="model file (default: the shipped v1 model; models of other widths run on the "
-                         "generic kernels and are reported without a roofline or baseline ratio)")
+                         "generic kernels, whose roofline is that of their filter GEMM sections, and are "
+                         "reported without a baseline ratio)")
     args = ap.parse_args()
     default_model = os.path.abspath(args.model) == os.path.abspath(MODEL)
     MODEL = args.model
@@ -466,8 +482,10 @@ def main():
     torch.cuda.synchronize()
     md.ctx.kernel_timing(False)
     timing = {}
+    work = kernel_work(model_widths(MODEL))
     for name in ("filter_fwd", "filter_fwd_block0", "filter_bwd", "filter_bwd_block0", "attn_fwd", "attn_bwd",
-                 "attn_bwd_block0", "long_range"):
+                 "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd", "generic_alpha",
+                 "generic_attn_bwd_pairs"):
         try:
             timing[name] = md.ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched
@@ -476,20 +494,19 @@ def main():
     kernels = {}
     for k, (ms, launches, units) in timing.items():
         row = {"avg_ms": ms / launches, "launches": launches, "ms_per_step": ms / steps_timed}
-        if k in KERNEL_WORK:
-            sym, bound, alg, issued, unit = KERNEL_WORK[k]
+        if k in work:
+            sym, bound, alg, issued, unit = work[k]
             per_launch = units / launches
             row.update({"kernel": sym, "units_per_launch": per_launch,
                         "tflops_algorithmic": alg * per_launch / (ms / launches * 1e-3) / 1e12,
                         "frac": alg * per_launch / (ms / launches * 1e-3) / 1e12 / FP64_PEAK_TFS})
         kernels[k] = row
     # the roofline kernel: most GPU time per step among those with a work model
-    # (the fused v1 kernels; a model on the generic kernels has none timed)
     roofline = None
-    timed_with_model = [k for k in kernels if k in KERNEL_WORK]
+    timed_with_model = [k for k in kernels if k in work]
     if timed_with_model:
         dom = max(timed_with_model, key=lambda k: kernels[k]["ms_per_step"])
-        sym, bound, alg, issued, unit = KERNEL_WORK[dom]
+        sym, bound, alg, issued, unit = work[dom]
         ms, launches, units = timing[dom]
         avg_ms = ms / launches
         per_launch = units / launches

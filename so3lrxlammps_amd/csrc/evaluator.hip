@@ -3407,7 +3407,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     // seeds as below, then heads and blocks in reverse to dE/dY, dE/dr
     GContext G{s, int(N), int(PA), nact, pa, pr, pY, pfc, sr_off, iact, iother, z, x0, 1.0 / avg_, ln_eps_,
                gamma_, rc_, norm1_, norm2_, qk_norm_ ? 1 : 0, &resid_, &x0l_, eatom, qraw, heff, hir, c6eff, c6r,
-               qseed, dh, dc, dY, dr};
+               qseed, dh, dc, dY, dr, nullptr};
+    if (timing_ && !from_scratch)
+      G.timed = [&](const char *name, const std::function<void()> &f) { timed(name, 0, f); };
     gen_->forward(G);
     hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
     long_range();

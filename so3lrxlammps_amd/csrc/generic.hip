@@ -805,6 +805,14 @@ void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int 
 }
 }  // namespace
 
+namespace {
+// run f, under c.timed when the evaluator is timing kernels
+void section(const GContext &c, const char *name, const std::function<void()> &f) {
+  if (c.timed) c.timed(name, f);
+  else f();
+}
+}  // namespace
+
 GenericPath::GenericPath(const Model &m, const std::function<const double *(const std::vector<double> &)> &up) {
   const Architecture &a = m.arch();
   GDims &d = d_;
@@ -980,13 +988,17 @@ void GenericPath::forward(const GContext &c) {
     // per filter: the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)] (F + FH
     // wide), then f = [W1 | E1] row + b1 + e1 in one GEMM
     const int HW = F + FH;
-    for (int w = 0; w < 2; ++w) {
-      gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
-      gemm<EPI_SILU, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
-      gemm<EPI_STORE, false>(s, cap, c.nact, HW, F, b_[HT], HW, B.wcat[w], B.bcat[w], pfb + w * F, 2 * F);
-    }
-    hipLaunchKernelGGL(g_alpha, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, pfb, c.inv_avg,
-                       pab);
+    section(c, "generic_filter_fwd", [&] {
+      for (int w = 0; w < 2; ++w) {
+        gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
+        gemm<EPI_SILU, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
+        gemm<EPI_STORE, false>(s, cap, c.nact, HW, F, b_[HT], HW, B.wcat[w], B.bcat[w], pfb + w * F, 2 * F);
+      }
+    });
+    section(c, "generic_alpha", [&] {
+      hipLaunchKernelGGL(g_alpha, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, pfb, c.inv_avg,
+                         pab);
+    });
     hipLaunchKernelGGL(g_attn_msg, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
                        c.pfc, pab, B.ln1w, B.ln1b, c.ln_eps, c.norm1, n1b, n1hb, n1ib, b_[ACT], aevb);
     // post-attention node chain (kokkos_post_attention_block0.cpp:165-300)
@@ -1043,9 +1055,11 @@ void GenericPath::reverse(const GContext &c) {
     gemm<EPI_DSILU_ADD, true>(s, N, nullptr, F, F, b_[GHID], F, B.m1, nullptr, b_[GN1], F, n1b, F, b_[GP], F);
     hipLaunchKernelGGL(g_ln1_bwd, dim3(g4), dim3(256), 0, s, F, N, b_[GN1], B.ln1w, n1hb, n1ib, c.norm1, b_[GAINV]);
     // attention reverse per pair (kokkos_attention_scatter_reverse.cpp:280-500)
-    hipLaunchKernelGGL(g_attn_bwd_pairs, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, c.pY,
-                       c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg, b == layers_ - 1 ? 1 : 0, b_[PSC], b_[DF], c.dY,
-                       b_[DFC]);
+    section(c, "generic_attn_bwd_pairs", [&] {
+      hipLaunchKernelGGL(g_attn_bwd_pairs, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, c.pY,
+                         c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg, b == layers_ - 1 ? 1 : 0, b_[PSC], b_[DF], c.dY,
+                         b_[DFC]);
+    });
     if (b > 0)
       hipLaunchKernelGGL(g_attn_bwd_node, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
                          c.pfc, pab, b_[PSC], b_[GAINV], b_[GQKV]);
@@ -1053,18 +1067,20 @@ void GenericPath::reverse(const GContext &c) {
     // per filter: the hidden row's pre-activations again, its adjoint
     // (df [W1 | E1]) (.) silu'(pre) in one GEMM, then through W0 and E0
     const int HW = F + FH;
-    for (int w = 0; w < 2; ++w) {
-      gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
-      gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
-      gemm<EPI_DSILU, true>(s, cap, c.nact, F, HW, b_[DF] + w * F, 2 * F, B.wcat[w], nullptr, b_[GH], HW, b_[HT], HW);
-      if (w == 0) {
-        gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-        gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
-      } else {
-        gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-        gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+    section(c, "generic_filter_bwd", [&] {
+      for (int w = 0; w < 2; ++w) {
+        gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
+        gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
+        gemm<EPI_DSILU, true>(s, cap, c.nact, F, HW, b_[DF] + w * F, 2 * F, B.wcat[w], nullptr, b_[GH], HW, b_[HT], HW);
+        if (w == 0) {
+          gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
+          gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+        } else {
+          gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
+          gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+        }
       }
-    }
+    });
     hipLaunchKernelGGL(g_pair_radial_bwd, dim3(blocks_for(P, 4)), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC],
                        b_[GRBF], b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
     // the adjoints of the block's inputs feed the block below; block 0's

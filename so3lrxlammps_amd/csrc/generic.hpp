@@ -88,6 +88,9 @@ struct GContext {
   // reverse (outputs): dE/dY of the 24 harmonics per pair (side-0
   // orientation), dE/dr per pair (added to)
   double *dY, *dr;
+  // when set, runs a launch sequence under a name for the evaluator's
+  // per-kernel timing (HIP events around it; units: active pairs)
+  std::function<void(const char *, const std::function<void()> &)> timed;
 };
 
 class GenericPath {
