@@ -3001,7 +3001,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
   iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part"); probe_ = buf("probe");
   top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
-  top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp");
+  top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp"); top_box_ = buf("top_box");
   for (int w = 0; w < 2; ++w) {
     top_ilist_[w] = buf("top_ilist"); top_off_[w] = buf("top_off"); top_neigh_[w] = buf("top_neigh");
     top_cnt_[w] = buf("top_cnt"); top_poff_[w] = buf("top_poff");
@@ -3122,19 +3122,23 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   hipStream_t s = stream_;
   const double rc2 = rc_ * rc_;
   const int nblk = std::max(1, ceil_div(P, kCompactPerBlock));
-  // --- node-order inputs (spatial order of the device reneighbor path) ---
+  // --- node-order inputs: the spatial order of the device reneighbor path
+  // (positions gathered into node order as well), or of a LAMMPS-list
+  // topology, set at its first evaluation (positions stay in row order) ---
+  if (rows_order_pending_ && !shift_mode_) order_rows_nodes(x);
   const int *perm = permuted_ ? static_cast<const int *>(perm_->p) : nullptr;
   const int *z = static_cast<const int *>((permuted_ ? nz_ : z_)->p);
   const double *x0 = static_cast<const double *>((permuted_ ? nx0_ : x0_)->p);
   const double *x_in = x;
-  if (permuted_) x = static_cast<const double *>(xn_->p);
+  const bool gather_pos = permuted_ && shift_mode_;
+  if (gather_pos) x = static_cast<const double *>(xn_->p);
   // --- capacity of the active-pair buffers: the pairs inside the cutoff
   // (about 60% of the candidates with a 1 A skin), counted once per topology
   // and given 1/8 of margin; an evaluation that finds more grows it and runs
   // again (see the end of this function) ---
   if (act_cap_ == 0 && P > 0) {
     int *cnt = from_scratch ? reinterpret_cast<int *>(scratch_dev_) : ensure<int>(probe_, std::size_t(nblk) + 2);
-    if (permuted_)
+    if (gather_pos)
       hipLaunchKernelGGL(k_gather_pos, dim3(unsigned((3 * Nz + 255) / 256)), dim3(256), 0, s, int(N), perm, x_in,
                          const_cast<double *>(x));
     if (shift_mode_) {
@@ -3358,7 +3362,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   // Everything from here to the read-back is one sequence on stream s: run
   // directly, or captured once into a graph and replayed.
   auto enqueue = [&] {
-  if (permuted_)
+  if (gather_pos)
     hipLaunchKernelGGL(k_gather_pos, dim3(unsigned((3 * Nz + 255) / 256)), dim3(256), 0, s, int(N), perm, x_in,
                        const_cast<double *>(x));
   // --- active short-range pairs, geometry, ZBL ---

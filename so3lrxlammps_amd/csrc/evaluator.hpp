@@ -208,6 +208,11 @@ class Evaluator {
   }
   void compute_impl(const double *x, int flags, double *f_out, double *eatom_out, double *energy, double *virial,
                     bool from_scratch);
+  // LAMMPS-list path: the nodes are put in the spatial order of the owned
+  // rows' positions at the first evaluation after set_topology (the lists
+  // carry no positions); rows_order_pending_ until then
+  void order_rows_nodes(const double *x_rows);
+  bool rows_order_pending_ = false;
   char *scratch_dev_ = nullptr;   // this device's copy of the static scratch array
   bool last_from_scratch_ = false;  // the last evaluation's buffers were scratch slices
 
@@ -235,13 +240,14 @@ class Evaluator {
   // device reneighbor
   Buffer *nb_key_, *nb_idx_, *nb_skey_, *nb_sidx_, *nb_cstart_, *nb_tmp_, *nb_srcnt_, *nb_lrcnt_, *nb_err_,
       *nb_srlist_, *nb_poff_, *sr_code_;
-  // spatial node order of the device reneighbor path: node n holds owned atom
-  // perm[n]; node-ordered copies of the per-atom inputs
+  // spatial node order (device reneighbor, or the LAMMPS-list path after its
+  // first evaluation): node n holds owned atom perm[n]; node-ordered copies
+  // of the per-atom inputs (xn_: positions, device reneighbor path only)
   Buffer *perm_, *nz_, *nx0_, *xn_;
   // LAMMPS lists on the device (set_topology): the raw upload and the build's
   // work buffers; [0] short range, [1] long range
   Buffer *top_owner_, *top_ilist_[2], *top_off_[2], *top_neigh_[2], *top_cnt_[2], *top_poff_[2], *top_stat_,
-      *top_slots_, *top_skeys_, *top_tmp_;
+      *top_slots_, *top_skeys_, *top_tmp_, *top_box_;
   std::vector<int> perm_host_;
   bool permuted_ = false;
   bool shift_mode_ = false;

@@ -24,6 +24,7 @@
 // are gathered into node order and forces scattered back, so callers keep
 // their own atom order.
 #include "evaluator.hpp"
+#include "spatial_order.hpp"
 
 #include <hipcub/hipcub.hpp>
 
@@ -60,44 +61,6 @@ __global__ void k_wrap(int n, double *x, Grid G) {
     if (v < 0.0) v = 0.0;
     x[3 * i + d] = G.lo[d] + v;
   }
-}
-
-// 10-bit spread for a 30-bit Morton key
-__device__ __forceinline__ unsigned spread3(unsigned v) {
-  v &= 1023u;
-  v = (v | (v << 16)) & 0x030000FFu;
-  v = (v | (v << 8)) & 0x0300F00Fu;
-  v = (v | (v << 4)) & 0x030C30C3u;
-  v = (v | (v << 2)) & 0x09249249u;
-  return v;
-}
-
-__device__ __forceinline__ unsigned quantize(double v, double lo, double len) {
-  const double t = (v - lo) / len * 1024.0;
-  return t < 0.0 ? 0u : (t >= 1023.0 ? 1023u : unsigned(t));
-}
-
-__global__ void k_morton(int n, const double *x, Grid G, int *key, int *idx) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const unsigned qx = quantize(x[3 * i], G.lo[0], G.len[0]);
-  const unsigned qy = quantize(x[3 * i + 1], G.lo[1], G.len[1]);
-  const unsigned qz = quantize(x[3 * i + 2], G.lo[2], G.len[2]);
-  key[i] = int((spread3(qx) << 2) | (spread3(qy) << 1) | spread3(qz));
-  idx[i] = i;
-}
-
-__global__ void k_gather_int(int n, const int *perm, const int *src, int *dst) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) dst[i] = src[perm[i]];
-}
-
-// dst[n][c] = src[perm[n]][c] for rows of `width` doubles
-__global__ void k_gather_rows(int n, int width, const int *perm, const double *src, double *dst) {
-  const std::size_t k = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (k >= std::size_t(n) * width) return;
-  const std::size_t row = k / width, c = k % width;
-  dst[k] = src[std::size_t(perm[row]) * width + c];
 }
 
 __device__ __forceinline__ int cell_coord(double v, double lo, double len, int nc) {
@@ -308,7 +271,12 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   const bool reorder = n_images_ == 1;
   if (reorder) {
     int *perm = ensure<int>(perm_, n);
-    hipLaunchKernelGGL(k_morton, dim3(gb), dim3(256), 0, s, n, x, G, key, idx);
+    MortonBox B;
+    for (int d = 0; d < 3; ++d) {
+      B.lo[d] = G.lo[d];
+      B.len[d] = G.len[d];
+    }
+    hipLaunchKernelGGL(k_morton, dim3(gb), dim3(256), 0, s, n, x, B, key, idx);
     sort_pairs(key, skey, idx, perm, 30);
     double *xn = ensure<double>(xn_, 3 * std::size_t(n));
     hipLaunchKernelGGL(k_gather_rows, dim3(unsigned((3 * std::size_t(n) + 255) / 256)), dim3(256), 0, s, n, 3, perm,
@@ -368,6 +336,7 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   lr_entries_ = totals[1];
   for (int d = 0; d < 3; ++d) box_len_[d] = G.len[d];
   permuted_ = reorder;
+  rows_order_pending_ = false;
   shift_mode_ = true;
   topology_ready_ = true;
   ++topo_version_;

@@ -20,10 +20,12 @@
 //      increasing pair order, and the node offsets from the sorted keys.
 // Results are identical to a sequential host walk of the lists.
 #include "evaluator.hpp"
+#include "spatial_order.hpp"
 
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -149,6 +151,43 @@ __global__ void k_segment_starts(int m, int n, const int *skey, int *off) {
   for (int v = prev + 1; v <= cur; ++v) off[v] = t;
 }
 
+// Bounding box of the first n rows: out = {min x, y, z, max x, y, z}.  One
+// block; the reduction order is fixed.
+__global__ __launch_bounds__(1024) void k_bbox(int n, const double *x, double *out) {
+  __shared__ double sh[6][1024];
+  const int t = threadIdx.x;
+  double lo[3] = {HUGE_VAL, HUGE_VAL, HUGE_VAL}, hi[3] = {-HUGE_VAL, -HUGE_VAL, -HUGE_VAL};
+  for (int i = t; i < n; i += 1024)
+    for (int d = 0; d < 3; ++d) {
+      lo[d] = fmin(lo[d], x[3 * i + d]);
+      hi[d] = fmax(hi[d], x[3 * i + d]);
+    }
+  for (int d = 0; d < 3; ++d) {
+    sh[d][t] = lo[d];
+    sh[3 + d][t] = hi[d];
+  }
+  __syncthreads();
+  for (int st = 512; st > 0; st >>= 1) {
+    if (t < st)
+      for (int d = 0; d < 3; ++d) {
+        sh[d][t] = fmin(sh[d][t], sh[d][t + st]);
+        sh[3 + d][t] = fmax(sh[3 + d][t], sh[3 + d][t + st]);
+      }
+    __syncthreads();
+  }
+  if (t < 6) out[t] = sh[t][0];
+}
+
+__global__ void k_invert(int n, const int *perm, int *inv) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) inv[perm[i]] = i;
+}
+
+__global__ void k_relabel(int m, const int *inv, int *nodes) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < m) nodes[t] = inv[nodes[t]];
+}
+
 }  // namespace
 
 void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int sr_kind, std::int64_t sr_inum,
@@ -263,6 +302,22 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
     m_max = std::max(m_max, std::size_t(m));
     tmp_max = std::max(tmp_max, tmp_bytes);
   }
+  // the spatial node order of the first evaluation (order_rows_nodes) runs
+  // on buffers sized here, so that evaluation allocates nothing: a single
+  // system only (packed images keep their nodes contiguous per image)
+  const bool reorder = n_images_ == 1 && n >= 2;
+  if (reorder) {
+    std::size_t tmp_bytes = 0;
+    TOPO_CHECK(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, static_cast<const int *>(nullptr),
+                                                  static_cast<int *>(nullptr), static_cast<const int *>(nullptr),
+                                                  static_cast<int *>(nullptr), int(n), 0, 30, s));
+    tmp_max = std::max(tmp_max, tmp_bytes);
+    const std::size_t nz = std::size_t(n);
+    ensure<int>(nb_key_, nz); ensure<int>(nb_idx_, nz); ensure<int>(nb_skey_, nz); ensure<int>(nb_sidx_, nz);
+    ensure<int>(perm_, nz); ensure<int>(nz_, nz); ensure<double>(nx0_, nz * std::size_t(F_));
+    ensure<double>(top_box_, 6);
+    perm_host_.resize(nz);
+  }
   int *slots = ensure<int>(top_slots_, m_max), *skeys = ensure<int>(top_skeys_, m_max);
   void *tmp = ensure<char>(top_tmp_, tmp_max);
   for (int w = 0; w < 2; ++w) {
@@ -309,10 +364,78 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
   n_rows_ = n_rows;
   shift_mode_ = false;
   permuted_ = false;
+  rows_order_pending_ = reorder;
   topology_ready_ = true;
   ++topo_version_;
   evaluated_ = false;
   act_cap_ = 0;  // counted again by the next evaluation
+}
+
+// The nodes of a LAMMPS-list topology in the Morton order of the owned rows'
+// positions (the first n rows), the analogue of LAMMPS's own periodic atom
+// sort: the node-major gathers (attention, long range) then read partner rows
+// from a compact region that one XCD's L2 serves, whatever order the caller
+// keeps its atoms in.  The pairs keep their list order; their endpoint nodes
+// are relabelled and each incidence list sorted again by node (stable, so a
+// node's entries stay in increasing pair order).  Runs once per topology, at
+// its first evaluation, on buffers set_topology sized.
+void Evaluator::order_rows_nodes(const double *x) {
+  rows_order_pending_ = false;
+  const int n = int(n_);
+  hipStream_t s = stream_;
+  double *box = ensure<double>(top_box_, 6);
+  hipLaunchKernelGGL(k_bbox, dim3(1), dim3(1024), 0, s, n, x, box);
+  double hb[6];
+  TOPO_CHECK(hipMemcpyAsync(hb, box, sizeof(hb), hipMemcpyDeviceToHost, s));
+  TOPO_CHECK(hipStreamSynchronize(s));
+  MortonBox B;
+  for (int d = 0; d < 3; ++d) {
+    if (!std::isfinite(hb[d]) || !std::isfinite(hb[3 + d]))
+      throw std::invalid_argument("SO3LR: non-finite positions");
+    B.lo[d] = hb[d];
+    B.len[d] = std::max(hb[3 + d] - hb[d], 1e-6);
+  }
+  const std::size_t nz = std::size_t(n);
+  int *key = ensure<int>(nb_key_, nz), *idx = ensure<int>(nb_idx_, nz), *skey = ensure<int>(nb_skey_, nz);
+  int *inv = ensure<int>(nb_sidx_, nz), *perm = ensure<int>(perm_, nz);
+  const unsigned gn = unsigned((n + 255) / 256);
+  hipLaunchKernelGGL(k_morton, dim3(gn), dim3(256), 0, s, n, x, B, key, idx);
+  void *tmp = top_tmp_->p;
+  std::size_t tmp_bytes = top_tmp_->bytes;
+  TOPO_CHECK(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, static_cast<const int *>(key), skey,
+                                                static_cast<const int *>(idx), perm, n, 0, 30, s));
+  hipLaunchKernelGGL(k_invert, dim3(gn), dim3(256), 0, s, n, perm, inv);
+  int bits = 1;
+  while ((std::int64_t(1) << bits) < n) ++bits;
+  struct Inc {
+    Buffer *nodes, *inc_off, *inc;
+    std::int64_t pairs;
+  };
+  const Inc lists[2] = {{sr_nodes_, sr_inc_off_, sr_inc_, p_sr_}, {lr_nodes_, lr_inc_off_, lr_inc_, p_lr_}};
+  for (const Inc &L : lists) {
+    const int m = int(2 * L.pairs);
+    if (m == 0) continue;  // its node offsets are all zero already
+    int *nodes = static_cast<int *>(L.nodes->p), *slots = static_cast<int *>(top_slots_->p),
+        *skeys = static_cast<int *>(top_skeys_->p);
+    const unsigned gm = unsigned((m + 255) / 256);
+    hipLaunchKernelGGL(k_relabel, dim3(gm), dim3(256), 0, s, m, inv, nodes);
+    hipLaunchKernelGGL(k_iota, dim3(gm), dim3(256), 0, s, m, slots);
+    tmp_bytes = top_tmp_->bytes;
+    TOPO_CHECK(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, static_cast<const int *>(nodes), skeys,
+                                                  static_cast<const int *>(slots), static_cast<int *>(L.inc->p), m,
+                                                  0, bits, s));
+    hipLaunchKernelGGL(k_segment_starts, dim3(unsigned((m + 1 + 255) / 256)), dim3(256), 0, s, m, n, skeys,
+                       static_cast<int *>(L.inc_off->p));
+  }
+  hipLaunchKernelGGL(k_gather_int, dim3(gn), dim3(256), 0, s, n, perm, static_cast<const int *>(z_->p),
+                     static_cast<int *>(nz_->p));
+  hipLaunchKernelGGL(k_gather_rows, dim3(unsigned((nz * std::size_t(F_) + 255) / 256)), dim3(256), 0, s, n, F_, perm,
+                     static_cast<const double *>(x0_->p), static_cast<double *>(nx0_->p));
+  TOPO_CHECK(hipMemcpyAsync(perm_host_.data(), perm, nz * sizeof(int), hipMemcpyDeviceToHost, s));
+  TOPO_CHECK(hipGetLastError());
+  TOPO_CHECK(hipStreamSynchronize(s));
+  permuted_ = true;
+  ++topo_version_;
 }
 
 }  // namespace so3lr_amd
