@@ -173,6 +173,30 @@ def test_refusals(ctx):
     assert e2 == e and np.array_equal(f2, f)
 
 
+def test_rows_path_atom_order(ctx):
+    """The LAMMPS-list path puts its nodes in a spatial order of its own at
+    the first evaluation of a topology, so the caller's atom order must not
+    matter: water3000 with its atoms shuffled gives the same energy, virial,
+    forces, per-atom energies, per-atom virials and per-atom terms, each in
+    the shuffled order (to rounding: the node-major sums meet the pairs in
+    another order)."""
+    ref, z, pos, box = support.load_golden("water3000")
+    p = np.random.default_rng(7).permutation(len(z))
+    runs = []
+    for zz, xx in ((z, pos), (z[p], pos[p])):
+        e, f, ea, w, terms = _hip_single_point(ctx, zz, xx, box, 0, 1)
+        runs.append((e, f, ea, w, terms, ctx.vatom()))
+    (e0, f0, ea0, w0, t0, v0), (e1, f1, ea1, w1, t1, v1) = runs
+    print("  |dE| %.2e  max|dF| %.2e" % (abs(e1 - e0), np.abs(f1 - f0[p]).max()), flush=True)
+    assert abs(e1 - e0) <= 1e-12 * abs(e0)
+    assert np.abs(w1 - w0).max() <= 1e-11 * np.abs(w0).max()
+    assert np.abs(f1 - f0[p]).max() <= 1e-11
+    assert np.abs(ea1 - ea0[p]).max() <= 1e-12 * np.abs(ea0).max()
+    assert np.abs(v1 - v0[p]).max() <= 1e-11 * np.abs(v0).max()
+    for k in ("charges", "hirshfeld", "learned", "zbl", "long_range"):
+        assert np.abs(t1[k] - t0[k][p]).max() <= 1e-11 * max(1.0, np.abs(t0[k]).max()), k
+
+
 def test_per_atom_virial_matches_oracle(ctx, orc):
     """so3lr_last_vatom (no counterpart in the reference) against the oracle's
     per-atom virial, at the virial's bar (1e-9 of its scale), on a dimer, a
