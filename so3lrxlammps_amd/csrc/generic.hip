@@ -275,6 +275,32 @@ __device__ __forceinline__ void g_norm_row_bwd(int F, int mode, const double *gy
   for (int j = 0; j < J; ++j) gx[j] = is * (gh[j] - mg - h[j] * mgx);
 }
 
+// Walks the active incidence entries of a node, [beg, end), in list order:
+// 64 entries per coalesced load of iact / iother, then the active ones two at
+// a time as uniform values, body(e1, o1, e2, o2, two) (when one is left the
+// second repeats the first and `two` is false), so a body can issue both
+// entries' loads before it sums either, and the sums keep the order of a
+// sequential walk.
+template <class Body>
+__device__ __forceinline__ void g_walk(int beg, int end, const int *__restrict__ iact, const int *__restrict__ iother,
+                                       int lane, Body &&body) {
+  for (int k0 = beg; k0 < end; k0 += 64) {
+    const int k = k0 + lane;
+    const int ent = k < end ? iact[k] : -1;
+    const int oth = k < end ? iother[k] : 0;
+    unsigned long long mask = __ballot(ent >= 0);
+    while (mask) {
+      const int l1 = __ffsll(mask) - 1;
+      mask &= mask - 1;
+      const bool two = mask != 0;
+      const int l2 = two ? __ffsll(mask) - 1 : l1;
+      if (two) mask &= mask - 1;
+      body(__builtin_amdgcn_readlane(ent, l1), __builtin_amdgcn_readlane(oth, l1),
+           __builtin_amdgcn_readlane(ent, l2), __builtin_amdgcn_readlane(oth, l2), two);
+    }
+  }
+}
+
 // Attention messages, node-major (kokkos_integrated_block0.cpp:330-385):
 // node n receives from each incident pair's partner o the invariant message
 // fc alpha v_o and the equivariant fc alpha_ev Y (parity of the direction),
@@ -294,26 +320,56 @@ __global__ __launch_bounds__(256) void g_attn_msg(GDims d, int N, const int *__r
   if (n >= N) return;
   const int F = d.F, NH = d.NH, E = d.E, J = F >> 6;
   double di[4] = {0, 0, 0, 0}, de[2] = {0, 0};
-  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
-    const int e = iact[k];
-    if (e < 0) continue;
-    const int o = iother[k], p = e >> 1, side = e & 1;
-    const double fc = pfc[p];
-    const double *al = palpha + std::size_t(p) * 4 * NH + side * 2 * NH;
-    const double *vo = qkv + std::size_t(o) * 5 * F + 2 * F;
-    for (int j = 0; j < J; ++j) {
-      const int c = lane + 64 * j;
-      di[j] += fc * al[c >> 5] * vo[c];
-    }
-    for (int j = 0; j < 2; ++j) {
-      const int c = lane + 64 * j;
-      if (c < E) {
-        const int sl = d.slot[c];
-        const double y = pY[std::size_t(p) * 24 + d.sh[c]] * (side ? d.par[sl] : 1.0);
-        de[j] += fc * al[NH + sl] * y;
-      }
+  // this lane's channels: invariant c = lane + 64 j (head c / 32), and
+  // equivariant c = lane + 64 j below E (slot, harmonic, parity)
+  int sl[2] = {0, 0}, sh[2] = {0, 0};
+  double par[2] = {1.0, 1.0};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = lane + 64 * j;
+    if (c < E) {
+      sl[j] = d.slot[c];
+      sh[j] = d.sh[c];
+      par[j] = d.par[sl[j]];
     }
   }
+  struct Terms {
+    double v[4], a[4], y[2], ae[2], fc;
+  };
+  auto load = [&](int e, int o) {
+    Terms T;
+    const int p = e >> 1, side = e & 1;
+    T.fc = pfc[p];
+    const double *al = palpha + std::size_t(p) * 4 * NH + side * 2 * NH;
+    const double *vo = qkv + std::size_t(o) * 5 * F + 2 * F;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + 64 * (j < J ? j : 0);
+      T.v[j] = vo[c];
+      T.a[j] = al[c >> 5];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = lane + 64 * j;
+      const bool on = c < E;
+      T.y[j] = on ? pY[std::size_t(p) * 24 + sh[j]] * (side ? par[j] : 1.0) : 0.0;
+      T.ae[j] = on ? al[NH + sl[j]] : 0.0;
+    }
+    return T;
+  };
+  auto add = [&](const Terms &T) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < J) di[j] += T.fc * T.a[j] * T.v[j];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      if (lane + 64 * j < E) de[j] += T.fc * T.ae[j] * T.y[j];
+  };
+  g_walk(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+    const Terms A = load(e1, o1), B = load(e2, o2);
+    add(A);
+    if (two) add(B);
+  });
   double v[4], y[4], h[4], is;
   for (int j = 0; j < J; ++j) v[j] = x[std::size_t(n) * F + lane + 64 * j] + di[j];
   g_norm_row(F, mode, v, lnw, lnb, eps, lane, y, h, is);
@@ -516,27 +572,55 @@ __global__ __launch_bounds__(256) void g_attn_bwd_node(GDims d, int N, const int
   const int F = d.F, NH = d.NH, J = F >> 6;
   double gq[4] = {0, 0, 0, 0}, gk[4] = {0, 0, 0, 0}, gv[4] = {0, 0, 0, 0}, gqe[4] = {0, 0, 0, 0},
          gke[4] = {0, 0, 0, 0};
-  for (int k = inc_off[n]; k < inc_off[n + 1]; ++k) {
-    const int e = iact[k];
-    if (e < 0) continue;
-    const int o = iother[k], p = e >> 1, sn = e & 1, so = 1 - sn;
-    const double fc = pfc[p];
+  // per entry and lane channel c = lane + 64 j (head h = c / 32): n receives
+  // along direction sn from o and sends along so = 1 - sn to o
+  struct Terms {
+    double si[4], sie[4], so[4], soe[4], ao[4], fi[4], fe[4], qo[4], ko[4], qeo[4], keo[4], go[4], fc;
+  };
+  auto load = [&](int e, int o) {
+    Terms T;
+    const int p = e >> 1, sn = e & 1, so = 1 - sn;
+    T.fc = pfc[p];
     const double *sc = psc + std::size_t(p) * 4 * NH;
     const double *al = palpha + std::size_t(p) * 4 * NH;
     const double *fi = pf + std::size_t(p) * 2 * F, *fe = fi + F;
     const double *qo = qkv + std::size_t(o) * 5 * F;
     const double *go = gainv + std::size_t(o) * F;
-    for (int j = 0; j < J; ++j) {
-      const int c = lane + 64 * j, h = c >> 5;
-      // n receives (direction sn) from o
-      gq[j] += sc[sn * 2 * NH + h] * qo[F + c] * fi[c];
-      gqe[j] += sc[sn * 2 * NH + NH + h] * qo[4 * F + c] * fe[c];
-      // n sends (direction so) to o
-      gk[j] += sc[so * 2 * NH + h] * qo[c] * fi[c];
-      gv[j] += fc * al[so * 2 * NH + h] * go[c];
-      gke[j] += sc[so * 2 * NH + NH + h] * qo[3 * F + c] * fe[c];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + 64 * (j < J ? j : 0), h = c >> 5;
+      T.si[j] = sc[sn * 2 * NH + h];
+      T.sie[j] = sc[sn * 2 * NH + NH + h];
+      T.so[j] = sc[so * 2 * NH + h];
+      T.soe[j] = sc[so * 2 * NH + NH + h];
+      T.ao[j] = al[so * 2 * NH + h];
+      T.fi[j] = fi[c];
+      T.fe[j] = fe[c];
+      T.qo[j] = qo[c];
+      T.ko[j] = qo[F + c];
+      T.qeo[j] = qo[3 * F + c];
+      T.keo[j] = qo[4 * F + c];
+      T.go[j] = go[c];
     }
-  }
+    return T;
+  };
+  auto add = [&](const Terms &T) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j >= J) continue;
+      gq[j] += T.si[j] * T.ko[j] * T.fi[j];
+      gqe[j] += T.sie[j] * T.keo[j] * T.fe[j];
+      gk[j] += T.so[j] * T.qo[j] * T.fi[j];
+      gv[j] += T.fc * T.ao[j] * T.go[j];
+      gke[j] += T.soe[j] * T.qeo[j] * T.fe[j];
+    }
+  };
+  // one entry's loads at a time here (174 registers; both entries' loads
+  // first took 256 and ran no faster)
+  g_walk(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+    add(load(e1, o1));
+    if (two) add(load(e2, o2));
+  });
   double *g = gqkv + std::size_t(n) * 5 * F;
   for (int j = 0; j < J; ++j) {
     const int c = lane + 64 * j;
@@ -604,35 +688,72 @@ __global__ void g_pair_inv(GDims d, const int *nact, int cap, const int *__restr
   ps[std::size_t(p) * d.NH + s] = acc;
 }
 
-// Sum over each 32-lane half of a wavefront (lanes 0-31 and 32-63 apart).
-__device__ __forceinline__ double half_sum(double v) {
-  for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, 32);
-  return v;
+// M sums over each 32-lane half of a wavefront at once (M = 2, 4, 8 or 16
+// values per lane, v[0..M)): at each of the first log2 M butterfly steps a
+// lane keeps half of its values, sends the other half to its partner and adds
+// the partner's copy of the half it kept (lane bit 4, then 3, ...: a set bit
+// keeps the upper half); the remaining steps add the single value left.
+// Lane l of half H = l / 32 ends with the sum of value index
+// (l % 32) >> (5 - log2 M) of its half, the same in each run of 32 / M lanes;
+// M - 1 + 5 - log2 M exchanges instead of 5 M.
+template <int W, int MASK, int M>
+__device__ __forceinline__ void half_sums_step(double (&v)[M], int lane) {
+  if constexpr (W > 1) {
+    constexpr int H = W / 2;
+    const bool up = (lane & MASK) != 0;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const double send = up ? v[i] : v[H + i];
+      const double keep = up ? v[H + i] : v[i];
+      v[i] = keep + __shfl_xor(send, MASK, 64);
+    }
+    half_sums_step<H, MASK / 2, M>(v, lane);
+  } else if constexpr (MASK > 0) {
+    v[0] += __shfl_xor(v[0], MASK, 64);
+    half_sums_step<1, MASK / 2, M>(v, lane);
+  }
+}
+template <int M>
+__device__ __forceinline__ double half_sums(double (&v)[M], int lane) {
+  static_assert(M == 2 || M == 4 || M == 8 || M == 16, "half_sums takes 2, 4, 8 or 16 values");
+  half_sums_step<M, 16, M>(v, lane);
+  return v[0];
 }
 
 // Attention logits per pair, direction and head (kokkos_integrated_block0.cpp:330-360):
 // alpha = <q_receiver, k_sender (.) f> / norm (inv: q k f_inv, ev: q_ev k_ev
 // f_ev).  One wavefront per pair, lanes over channels (channel lane + 64 j is
-// in head 2 j + lane / 32).
+// in head 2 j + lane / 32, J = F / 64 channels per lane); the 4 J products
+// of a lane (direction, filter, j) are summed per head by half_sums.
+template <int J>
 __global__ __launch_bounds__(256) void g_alpha(GDims d, const int *nact, int cap, const int *__restrict__ pa,
                                                const double *__restrict__ qkv, const double *__restrict__ pf,
                                                double inv_avg, double *__restrict__ palpha) {
   const int lane = threadIdx.x & 63;
   const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (p >= min(*nact, cap)) return;
-  const int NH = d.NH, F = d.F, J = F >> 6;
-  for (int side = 0; side < 2; ++side) {
-    const double *qr = qkv + std::size_t(pa[2 * p + side]) * 5 * F;
-    const double *ks = qkv + std::size_t(pa[2 * p + 1 - side]) * 5 * F;
-    for (int which = 0; which < 2; ++which) {
-      const double *q = qr + (which ? 3 * F : 0), *k = ks + (which ? 4 * F : F);
-      const double *f = pf + std::size_t(p) * 2 * F + (which ? F : 0);
-      for (int j = 0; j < J; ++j) {
-        const int c = lane + 64 * j;
-        const double t = half_sum(q[c] * k[c] * f[c]);
-        if ((lane & 31) == 0) palpha[std::size_t(p) * 4 * NH + side * 2 * NH + which * NH + 2 * j + (lane >> 5)] = t * inv_avg;
-      }
+  const int NH = d.NH, F = d.F;
+  const double *ra = qkv + std::size_t(pa[2 * p]) * 5 * F, *rb = qkv + std::size_t(pa[2 * p + 1]) * 5 * F;
+  const double *f = pf + std::size_t(p) * 2 * F;
+  constexpr int M = 4 * J;
+  double v[M];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const int qo = w ? 3 * F : 0, ko = w ? 4 * F : F;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = lane + 64 * j;
+      const double fc = f[w * F + c];
+      v[(0 * 2 + w) * J + j] = ra[qo + c] * rb[ko + c] * fc;  // direction 0: a receives from b
+      v[(1 * 2 + w) * J + j] = rb[qo + c] * ra[ko + c] * fc;  // direction 1: b receives from a
     }
+  }
+  const double t = half_sums<M>(v, lane);
+  constexpr int LOG = J == 2 ? 3 : 4, RUN = 32 >> LOG;
+  if ((lane % RUN) == 0) {
+    const int m = (lane & 31) / RUN, j = m % J, w = (m / J) % 2, side = m / (2 * J);
+    const int h = 2 * j + (lane >> 5);
+    palpha[std::size_t(p) * 4 * NH + side * 2 * NH + w * NH + h] = t * inv_avg;
   }
 }
 
@@ -646,7 +767,11 @@ __global__ __launch_bounds__(256) void g_alpha(GDims d, const int *nact, int cap
 //   filter's adjoint,
 //   dE/dY_m = sum_dir sum_{c: sh(c) = m} gaev_r,c fc alpha_ev par (side-0
 //   orientation); the first reverse block writes dY, the others add.
-// Every wavefront reaches the barriers (inactive ones skip the work).
+// The head sums ci come from half_sums over the 2 J products of a lane
+// (direction, j); the slot sums ce from the wavefront's own LDS rows, one
+// lane per direction and slot.  Each wavefront uses only its own LDS rows, so
+// a wavefront-level fence orders them and an idle wavefront leaves at once.
+template <int J>
 __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact, int cap, const int *__restrict__ pa,
                                                         const double *__restrict__ qkv, const double *__restrict__ pY,
                                                         const double *__restrict__ pfc,
@@ -655,71 +780,71 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
                                                         const double *__restrict__ ga, double inv_avg, int first,
                                                         double *__restrict__ psc, double *__restrict__ df,
                                                         double *__restrict__ dY, double *__restrict__ dfc) {
-  __shared__ double lt[4][2][kGMaxE];  // per wavefront: dE/dY terms per direction and channel
-  __shared__ double lps[4][32];        // per wavefront: psc of the pair
+  __shared__ double lt[4][2][kGMaxE];   // per wavefront: dE/dY terms per direction and channel
+  __shared__ double lte[4][2][kGMaxE];  // per wavefront: gaev_r Y' per direction and channel
+  __shared__ double lps[4][32];         // per wavefront: psc of the pair
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int p = blockIdx.x * 4 + wv;
-  const bool on = p < min(*nact, cap);
-  const int NH = d.NH, F = d.F, E = d.E, J = F >> 6;
-  if (on) {
-    const double fc = pfc[p];
-    const double *al = palpha + std::size_t(p) * 4 * NH;
-    double dsum = 0.0;  // dE/dfc (uniform over the wavefront)
+  if (p >= min(*nact, cap)) return;
+  const int NH = d.NH, F = d.F, E = d.E;
+  const double fc = pfc[p];
+  const double *al = palpha + std::size_t(p) * 4 * NH;
+  double v[2 * J];
+#pragma unroll
+  for (int side = 0; side < 2; ++side) {
+    const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
+    const double *g = gainv + std::size_t(rcv) * F, *vs = qkv + std::size_t(snd) * 5 * F + 2 * F;
+#pragma unroll
+    for (int j = 0; j < J; ++j) v[side * J + j] = g[lane + 64 * j] * vs[lane + 64 * j];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int c = lane + 64 * jj;
+      if (c < E) {
+        const int sl = d.slot[c];
+        const double pr = side ? d.par[sl] : 1.0;
+        const double gr = ga[std::size_t(rcv) * E + c];
+        lte[wv][side][c] = gr * pY[std::size_t(p) * 24 + d.sh[c]] * pr;
+        lt[wv][side][c] = gr * fc * al[side * 2 * NH + NH + sl] * pr;
+      }
+    }
+  }
+  const double ci = half_sums<2 * J>(v, lane);
+  constexpr int RUN = 32 >> (J == 2 ? 2 : 3);
+  double part = 0.0;  // this lane's terms of dE/dfc
+  if (lane % RUN == 0) {
+    const int m = (lane & 31) / RUN, j = m % J, side = m / J, h = 2 * j + (lane >> 5);
+    part = ci * al[side * 2 * NH + h];
+    lps[wv][side * 2 * NH + h] = fc * ci * inv_avg;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  if (lane < 2 * NH) {
+    const int side = lane / NH, sl = lane % NH;
+    double ce = 0.0;
+    for (int c = d.off[sl]; c < d.off[sl + 1]; ++c) ce += lte[wv][side][c];
+    part += ce * al[side * 2 * NH + NH + sl];
+    lps[wv][side * 2 * NH + NH + sl] = fc * ce * inv_avg;
+  }
+  const double dsum = wsum(part);
+  if (lane == 0) dfc[p] = dsum;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  if (lane < 4 * NH) psc[std::size_t(p) * 4 * NH + lane] = lps[wv][lane];
+  for (int c = lane; c < 2 * F; c += 64) {
+    const int which = c / F, cc = c % F, h = cc >> 5;
+    double acc = 0.0;
     for (int side = 0; side < 2; ++side) {
       const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
-      const double *g = gainv + std::size_t(rcv) * F, *v = qkv + std::size_t(snd) * 5 * F + 2 * F;
-      for (int j = 0; j < J; ++j) {
-        const int c = lane + 64 * j;
-        const double ci = half_sum(g[c] * v[c]);
-        const int h = 2 * j + (lane >> 5);
-        dsum += __shfl(ci * al[side * 2 * NH + h], 0, 64) + __shfl(ci * al[side * 2 * NH + h], 32, 64);
-        if ((lane & 31) == 0) lps[wv][side * 2 * NH + h] = fc * ci * inv_avg;
-      }
-      double te[2] = {0.0, 0.0};
-      for (int jj = 0; jj < 2; ++jj) {
-        const int c = lane + 64 * jj;
-        if (c < E) {
-          const int sl = d.slot[c];
-          const double pr = side ? d.par[sl] : 1.0;
-          const double gr = ga[std::size_t(rcv) * E + c];
-          te[jj] = gr * pY[std::size_t(p) * 24 + d.sh[c]] * pr;
-          lt[wv][side][c] = gr * fc * al[side * 2 * NH + NH + sl] * pr;
-        }
-      }
-      for (int sl = 0; sl < NH; ++sl) {
-        double part = 0.0;
-        for (int jj = 0; jj < 2; ++jj) {
-          const int c = lane + 64 * jj;
-          if (c >= d.off[sl] && c < d.off[sl + 1]) part += te[jj];
-        }
-        const double ce = wsum(part);
-        dsum += ce * al[side * 2 * NH + NH + sl];
-        if (lane == 0) lps[wv][side * 2 * NH + NH + sl] = fc * ce * inv_avg;
-      }
+      const double qv = qkv[std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + cc];
+      const double kv = qkv[std::size_t(snd) * 5 * F + (which ? 4 * F : F) + cc];
+      acc += lps[wv][side * 2 * NH + which * NH + h] * qv * kv;
     }
-    if (lane == 0) dfc[p] = dsum;
+    df[std::size_t(p) * 2 * F + c] = acc;
   }
-  __syncthreads();
-  if (on) {
-    if (lane < 4 * NH) psc[std::size_t(p) * 4 * NH + lane] = lps[wv][lane];
-    for (int c = lane; c < 2 * F; c += 64) {
-      const int which = c / F, cc = c % F, h = cc >> 5;
-      double acc = 0.0;
-      for (int side = 0; side < 2; ++side) {
-        const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
-        const double qv = qkv[std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + cc];
-        const double kv = qkv[std::size_t(snd) * 5 * F + (which ? 4 * F : F) + cc];
-        acc += lps[wv][side * 2 * NH + which * NH + h] * qv * kv;
-      }
-      df[std::size_t(p) * 2 * F + c] = acc;
-    }
-    if (lane < 24) {
-      double acc = 0.0;
-      for (int side = 0; side < 2; ++side)
-        for (int t = 0; t < d.shn[lane]; ++t) acc += lt[wv][side][d.shc[lane][t]];
-      double *y = dY + std::size_t(p) * 24 + lane;
-      *y = first ? acc : *y + acc;
-    }
+  if (lane < 24) {
+    double acc = 0.0;
+    for (int side = 0; side < 2; ++side)
+      for (int t = 0; t < d.shn[lane]; ++t) acc += lt[wv][side][d.shc[lane][t]];
+    double *y = dY + std::size_t(p) * 24 + lane;
+    *y = first ? acc : *y + acc;
   }
 }
 
@@ -824,8 +949,8 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
   d.NI = a.F + a.heads;
   d.c6 = a.c6_head ? 1 : 0;
   d.HO = 2 * d.HK + 64 + (d.c6 ? 64 : 0);
-  if (d.F % 64 != 0 || d.F > 256 || d.NH > 8 || d.NH * 32 != d.F)
-    throw std::logic_error("SO3LR: generic path given widths outside F = 64..256 in heads of 32");
+  if ((d.F != 128 && d.F != 256) || d.NH * 32 != d.F)
+    throw std::logic_error("SO3LR: generic path given widths other than F = 128 or 256 in heads of 32");
   int off = 0;
   d.off[0] = 0;
   for (int s = 0; s < d.NH; ++s) {
@@ -996,7 +1121,8 @@ void GenericPath::forward(const GContext &c) {
       }
     });
     section(c, "generic_alpha", [&] {
-      hipLaunchKernelGGL(g_alpha, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, pfb, c.inv_avg,
+      hipLaunchKernelGGL(F == 256 ? g_alpha<4> : g_alpha<2>, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact,
+                         cap, c.pa, qb, pfb, c.inv_avg,
                          pab);
     });
     hipLaunchKernelGGL(g_attn_msg, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
@@ -1056,9 +1182,9 @@ void GenericPath::reverse(const GContext &c) {
     hipLaunchKernelGGL(g_ln1_bwd, dim3(g4), dim3(256), 0, s, F, N, b_[GN1], B.ln1w, n1hb, n1ib, c.norm1, b_[GAINV]);
     // attention reverse per pair (kokkos_attention_scatter_reverse.cpp:280-500)
     section(c, "generic_attn_bwd_pairs", [&] {
-      hipLaunchKernelGGL(g_attn_bwd_pairs, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact, cap, c.pa, qb, c.pY,
-                         c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg, b == layers_ - 1 ? 1 : 0, b_[PSC], b_[DF], c.dY,
-                         b_[DFC]);
+      hipLaunchKernelGGL(F == 256 ? g_attn_bwd_pairs<4> : g_attn_bwd_pairs<2>, dim3(blocks_for(P, 4)), dim3(256), 0,
+                         s, d, c.nact, cap, c.pa, qb, c.pY, c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg,
+                         b == layers_ - 1 ? 1 : 0, b_[PSC], b_[DF], c.dY, b_[DFC]);
     });
     if (b > 0)
       hipLaunchKernelGGL(g_attn_bwd_node, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
