@@ -2088,22 +2088,25 @@ __global__ __launch_bounds__(256) void k_heads_bwd(int N, const int *z, const do
 // queues them in LDS, and evaluates only full wavefronts of them (and one
 // partial at the end): the pair terms are the kernel's whole cost.
 // Src gives an entry's partner node and displacement:
-//   LrRows: LAMMPS half pairs through the incidence (entry = pair * 2 + side);
+//   LrRows: LAMMPS half pairs, one record per incidence entry k (the entry is
+//   k itself): the partner node, this endpoint's row and the partner's row,
+//   three arrays of the incidence's length (lr_rec, built with the incidence),
+//   so the scan reads them in order instead of through the pair table;
 //   LrImages: the device reneighbor's full list (entry = node * 32 + image code).
 struct LrRows {
-  const int *rows, *nodes;
+  static constexpr bool kByIndex = true;
+  const int *o, *row_self, *row_other;
   const double *x;
-  __device__ __forceinline__ int other(int e) const { return nodes[2 * (e >> 1) + 1 - (e & 1)]; }
+  __device__ __forceinline__ int other(int e) const { return o[e]; }
   __device__ __forceinline__ void disp(int e, int, double &dx, double &dy, double &dz) const {
-    const int c = e >> 1;
-    const double sgn = (e & 1) == 0 ? 1.0 : -1.0;
-    const int ra = rows[2 * c], rb = rows[2 * c + 1];
-    dx = sgn * (x[3 * ra] - x[3 * rb]);
-    dy = sgn * (x[3 * ra + 1] - x[3 * rb + 1]);
-    dz = sgn * (x[3 * ra + 2] - x[3 * rb + 2]);
+    const int ra = row_self[e], rb = row_other[e];
+    dx = x[3 * ra] - x[3 * rb];
+    dy = x[3 * ra + 1] - x[3 * rb + 1];
+    dz = x[3 * ra + 2] - x[3 * rb + 2];
   }
 };
 struct LrImages {
+  static constexpr bool kByIndex = false;
   const double *x;
   const double *shift;  // LDS: 27 x 4 image shifts (box multiples)
   __device__ __forceinline__ int other(int e) const { return e >> 5; }
@@ -2182,7 +2185,7 @@ __global__ __launch_bounds__(256) LR_OCCUPANCY void k_lr(int N, const int *inc_o
     int e = 0;
     double dx = 0, dy = 0, dz = 0;
     if (k < end) {
-      e = inc[k];
+      e = Src::kByIndex ? k : inc[k];
       S.disp(e, n, dx, dy, dz);
       const double r2 = dx * dx + dy * dy + dz * dz;
       in = r2 > 1e-24 && r2 < rc2;
@@ -2990,6 +2993,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   owner_ = buf("owner"); sr_rows_ = buf("sr_rows"); sr_nodes_ = buf("sr_nodes");
   sr_inc_off_ = buf("sr_inc_off"); sr_inc_ = buf("sr_inc"); lr_rows_ = buf("lr_rows");
   lr_nodes_ = buf("lr_nodes"); lr_inc_off_ = buf("lr_inc_off"); lr_inc_ = buf("lr_inc");
+  lr_rec_ = buf("lr_rec");
   blk_count_ = buf("blk"); n_active_ = buf("nact"); cand2act_ = buf("c2a"); pa_ = buf("pa");
   psc_ = buf("psc"); pv_ = buf("pv"); pr_ = buf("pr"); pY_ = buf("pY"); pfc_ = buf("pfc"); pzbl_ = buf("pzbl");
   ps_ = buf("ps"); pf_ = buf("pf"); palpha_ = buf("palpha"); df_ = buf("df"); dfc_ = buf("dfc");
@@ -3314,8 +3318,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const int *sr_nodes = static_cast<const int *>(sr_nodes_->p);
   const int *sr_off = static_cast<const int *>(sr_inc_off_->p);
   const int *sr_inc = static_cast<const int *>(sr_inc_->p);
-  const int *lr_rows = static_cast<const int *>(lr_rows_->p);
-  const int *lr_nodes = static_cast<const int *>(lr_nodes_->p);
+  // LAMMPS-list long range: per incidence entry the partner node, own row and
+  // partner row (lr_rec_, three arrays of lr_rec_len_ entries)
+  const int *lr_rec = static_cast<const int *>(lr_rec_->p);
+  const std::size_t lr_m = std::size_t(lr_rec_len_);
   const int *lr_off = static_cast<const int *>(lr_inc_off_->p);
   const int *lr_inc = static_cast<const int *>(lr_inc_->p);
   const std::int64_t *img_off = static_cast<const std::int64_t *>(img_off_->p);
@@ -3397,7 +3403,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                        hw_.alpha_ref, hw_.c6_ref, elr, dq, dh, dc, flr, vlr, parts);                                 \
   else                                                                                                               \
     hipLaunchKernelGGL((k_lr<LrRows, LEAN, SEP>), dim3(gN4), dim3(256), 0, s, int(N), lr_off, lr_inc,                \
-                       LrRows{lr_rows, lr_nodes, x}, 0.0, 0.0, 0.0, z, q, hir, c6r, lr_, hw_.alpha_ref, hw_.c6_ref,  \
+                       LrRows{lr_rec, lr_rec + lr_m, lr_rec + 2 * lr_m, x}, 0.0, 0.0, 0.0, z, q, hir, c6r, lr_,     \
+                       hw_.alpha_ref, hw_.c6_ref,                                                                    \
                        elr, dq, dh, dc, flr, vlr, parts);
     if (c6_) {
       if (lean_erf) { SO3LR_LR(shift_mode_, true, true) } else { SO3LR_LR(shift_mode_, false, true) }

@@ -228,6 +228,11 @@ class Evaluator {
   // pair-sized buffers
   Buffer *owner_, *sr_rows_, *sr_nodes_, *sr_inc_off_, *sr_inc_, *lr_rows_, *lr_nodes_,
       *lr_inc_off_, *lr_inc_, *blk_count_, *n_active_, *cand2act_;
+  // LAMMPS-list long range, per incidence entry: partner node, own row,
+  // partner row (three arrays of lr_rec_len_ entries; build_lr_records)
+  Buffer *lr_rec_;
+  std::int64_t lr_rec_len_ = 0;
+  void build_lr_records();
   Buffer *pa_, *pv_, *pr_, *pY_, *pfc_, *pzbl_, *ps_, *pf_, *palpha_;
   Buffer *df_, *dfc_, *psc_, *ds_, *dr_, *dY_, *pg_;
   Buffer *iact_, *iother_;  // per step: incidence entry -> active pair * 2 + side, partner node

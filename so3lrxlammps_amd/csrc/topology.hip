@@ -183,6 +183,17 @@ __global__ void k_invert(int n, const int *perm, int *inv) {
   if (i < n) inv[perm[i]] = i;
 }
 
+// Per long-range incidence entry k (pair slot e = 2 c + side): the partner
+// node, this endpoint's row and the partner's row, in three arrays of m.
+__global__ void k_lr_records(int m, const int *inc, const int *rows, const int *nodes, int *rec) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= m) return;
+  const int e = inc[k], c = e >> 1, side = e & 1;
+  rec[k] = nodes[2 * c + 1 - side];
+  rec[std::size_t(m) + k] = rows[2 * c + side];
+  rec[2 * std::size_t(m) + k] = rows[2 * c + 1 - side];
+}
+
 __global__ void k_relabel(int m, const int *inv, int *nodes) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t < m) nodes[t] = inv[nodes[t]];
@@ -357,10 +368,11 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
     hipLaunchKernelGGL(k_segment_starts, dim3(unsigned((m + 1 + 255) / 256)), dim3(256), 0, s, m, int(n), skeys,
                        inc_off);
   }
-  TOPO_CHECK(hipGetLastError());
-  TOPO_CHECK(hipStreamSynchronize(s));
   p_sr_ = lists[0].pairs;
   p_lr_ = lists[1].pairs;
+  build_lr_records();
+  TOPO_CHECK(hipGetLastError());
+  TOPO_CHECK(hipStreamSynchronize(s));
   n_rows_ = n_rows;
   shift_mode_ = false;
   permuted_ = false;
@@ -427,6 +439,7 @@ void Evaluator::order_rows_nodes(const double *x) {
     hipLaunchKernelGGL(k_segment_starts, dim3(unsigned((m + 1 + 255) / 256)), dim3(256), 0, s, m, n, skeys,
                        static_cast<int *>(L.inc_off->p));
   }
+  build_lr_records();
   hipLaunchKernelGGL(k_gather_int, dim3(gn), dim3(256), 0, s, n, perm, static_cast<const int *>(z_->p),
                      static_cast<int *>(nz_->p));
   hipLaunchKernelGGL(k_gather_rows, dim3(unsigned((nz * std::size_t(F_) + 255) / 256)), dim3(256), 0, s, n, F_, perm,
@@ -436,6 +449,18 @@ void Evaluator::order_rows_nodes(const double *x) {
   TOPO_CHECK(hipStreamSynchronize(s));
   permuted_ = true;
   ++topo_version_;
+}
+
+// The long-range records of the current LAMMPS-list incidence (its pairs,
+// rows and nodes); after set_topology and after the nodes are relabelled.
+void Evaluator::build_lr_records() {
+  const int m = int(2 * p_lr_);
+  lr_rec_len_ = m;
+  int *rec = ensure<int>(lr_rec_, 3 * std::size_t(std::max(m, 1)));
+  if (m == 0) return;
+  hipLaunchKernelGGL(k_lr_records, dim3(unsigned((m + 255) / 256)), dim3(256), 0, stream_, m,
+                     static_cast<const int *>(lr_inc_->p), static_cast<const int *>(lr_rows_->p),
+                     static_cast<const int *>(lr_nodes_->p), rec);
 }
 
 }  // namespace so3lr_amd
