@@ -122,7 +122,10 @@ int so3lr_set_images(so3lr_ctx *ctx, int64_t n_owned, const int32_t *z,
  * Replaces snapshot_neighbor_list + build_lammps_native_candidate_topologies +
  * upload_device_candidate_graph (pair_so3lr_native_mpi.cpp:76-105,1297-1334;
  * src/lammps_neighbor_adapter.cpp:190-280).  A pair of an atom with its own
- * periodic image is refused, as the one-rank collapse refuses it.
+ * periodic image is refused, as the one-rank collapse refuses it.  For one
+ * system (not packed images) the first evaluation on a new topology also puts
+ * the owned atoms in a spatial order of its positions, inside the library;
+ * results still come back in the caller's atom order.
  */
 int so3lr_set_topology(so3lr_ctx *ctx, int64_t n_rows, const int32_t *owner_of_row,
                        int sr_kind, int64_t sr_inum, const int32_t *sr_ilist,
