@@ -584,12 +584,18 @@ struct Stream {
   }
 };
 
+// Stream entries in flight per wavefront (measured at config 3: 4 for the
+// forward filter of blocks after 0, which 3, 5 or 6 slow by 3-18%; 6 for
+// block 0's forward and for the reverse filters, 1-2% faster than 4 there).
 #ifndef SO3LR_FILTER_PF
 #define SO3LR_FILTER_PF 4
 #endif
-constexpr int kFilterPF = SO3LR_FILTER_PF;  // fragments in flight per wavefront
+constexpr int kFilterPF = SO3LR_FILTER_PF;
+#ifndef SO3LR_FILTER_FWD0_PF
+#define SO3LR_FILTER_FWD0_PF 6
+#endif
 #ifndef SO3LR_FILTER_BWD_PF
-#define SO3LR_FILTER_BWD_PF SO3LR_FILTER_PF
+#define SO3LR_FILTER_BWD_PF 6
 #endif
 // Two wavefronts per SIMD (<= 256 registers per lane): measured faster than
 // one wavefront with a deeper prefetch, since the second wave's MFMAs cover
@@ -728,7 +734,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
       else return wload(A.e1p[which], 2, mt, u - UE, lane);
     }
   };
-  Stream<2 * NF, kFilterPF, decltype(load)> st(load);
+  Stream<2 * NF, EV0 ? SO3LR_FILTER_FWD0_PF : kFilterPF, decltype(load)> st(load);
   st.prime();
 
   v4d rb[2];
