@@ -101,7 +101,7 @@ def test_noalloc_matches_compute_device():
 def test_noalloc_generic_widths(tmp_path):
     """The same agreement for a model on the generic kernels (F = 256, R = 64,
     duplicated degrees: support.lifted_model, weights perturbed), two calls
-    in a row, the second smaller."""
+    in a row, the second smaller, each the first evaluation of its topology."""
     import torch
     from so3lrxlammps_amd import Context, Lists
     dev = torch.device("cuda:0")
@@ -117,7 +117,12 @@ def test_noalloc_generic_widths(tmp_path):
         lists = Lists(pos, pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0))
         ctx.set_topology(lists)
         xr = lists.rows_positions(pos)
+        # the first evaluation of the topology (it also sets the spatial node
+        # order) is the no-allocation one: the library's device memory does
+        # not grow
+        held = ctx.device_bytes()
         got = _evaluate(ctx, xr, len(z), True, stream)
+        assert ctx.device_bytes() == held, name
         want = _evaluate(ctx, xr, len(z), False, stream)
         _same(got, want, name)
     ctx.close()
