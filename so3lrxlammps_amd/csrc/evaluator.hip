@@ -2733,6 +2733,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   HIP_CHECK(hipSetDevice(device));
   HIP_CHECK(hipStreamCreateWithFlags(&own_stream_, hipStreamNonBlocking));
   if (const char *nv = std::getenv("SO3LR_NAIVE_FILTERS")) naive_filters_ = nv[0] == '1';
+  if (const char *sp = std::getenv("SO3LR_SCALAR_FILTER_PAIRS")) scalar_pairs_max_ = std::atoll(sp);
   // SO3LR_NO_GRAPH=1: always launch the kernels one by one (no graph replay)
   if (const char *ng = std::getenv("SO3LR_NO_GRAPH")) use_graphs_ = ng[0] != '1';
   HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_out_), 16 * sizeof(double), hipHostMallocDefault));
@@ -3164,7 +3165,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     HIP_CHECK(hipMemcpyAsync(&total, cnt + nblk + 1, sizeof(int), hipMemcpyDeviceToHost, s));
     HIP_CHECK(hipStreamSynchronize(s));
     act_cap_ = std::min<std::int64_t>(P, std::int64_t(total) + total / 8 + 256);
+    scalar_now_ = std::int64_t(total) <= scalar_pairs_max_;
   }
+  if (P == 0) scalar_now_ = false;
+  const bool scalar = naive_filters_ || scalar_now_;
   const std::int64_t PA = std::max<std::int64_t>(std::min(act_cap_, P), 1);
   const std::size_t Pa = std::size_t(PA);
   // --- buffers (retained capacity; all allocation happens before any work
@@ -3254,13 +3258,13 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     ps = take<double>(ps_, L * 4 * Pa);
     // filter rows of every block for the scalar cross-check path; of blocks
     // after 0 only on the MFMA path (block 0's are never read there)
-    pf = take<double>(pf_, std::size_t(naive_filters_ ? L : L - 1) * 256 * Pa);
+    pf = take<double>(pf_, std::size_t(scalar ? L : L - 1) * 256 * Pa);
     palpha = take<double>(palpha_, L * 16 * Pa);
     // the pair adjoints of the filters stay in registers on the MFMA path;
     // it passes the head scalars (16 per pair) and dE/dfc between its kernels
-    df = naive_filters_ ? take<double>(df_, 256 * Pa) : nullptr;
+    df = scalar ? take<double>(df_, 256 * Pa) : nullptr;
     dfc = take<double>(dfc_, Pa);
-    psc = naive_filters_ ? nullptr : take<double>(psc_, 16 * Pa);
+    psc = scalar ? nullptr : take<double>(psc_, 16 * Pa);
     ds = take<double>(ds_, 4 * Pa);
     } else {
       gen_->carve(int(N), int(PA), [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
@@ -3452,7 +3456,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     double *hpb = hpre + b * Nz * kF, *tb = tout + b * Nz * kNI;
     double *p2h = pre2hat + b * Nz * kF, *p2i = pre2is + b * Nz;
     double *psb = ps + b * 4 * Pa, *pab = palpha + b * 16 * Pa;
-    double *pfb = naive_filters_ ? pf + b * 256 * Pa : (b > 0 ? pf + (b - 1) * 256 * Pa : nullptr);
+    double *pfb = scalar ? pf + b * 256 * Pa : (b > 0 ? pf + (b - 1) * 256 * Pa : nullptr);
     FilterArgs A;
     for (int k = 0; k < 2; ++k) {
       A.fw0[k] = B.fw0[k]; A.fb0[k] = B.fb0[k]; A.fw1t[k] = B.fw1t[k]; A.fb1[k] = B.fb1[k];
@@ -3468,9 +3472,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     // from the filter tiles it holds; the scalar cross-check path leaves them
     // to the full attention kernel
     // block 0 runs cheaper instantiations (ev = 0): timed under their own names
-    const bool blk0 = b == 0 && !naive_filters_;
+    const bool blk0 = b == 0 && !scalar;
     timed(blk0 ? "filter_fwd_block0" : "filter_fwd", 0, [&] {
-      if (naive_filters_)
+      if (scalar)
         hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
       else if (b == 0)  // ev = 0: the spherical branch is a constant
         hipLaunchKernelGGL(k_filter_fwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
@@ -3480,14 +3484,14 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                            psb, pfb, pab);
     });
     timed("attn_fwd", 1, [&] {
-      if (naive_filters_)
+      if (scalar)
         hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb,
                            pfb, pY, pfc, inv_avg, pab, ainv, aevb);
       else
         hipLaunchKernelGGL(k_attn_msg, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb, pY,
                            pfc, pab, B.ln1w, B.ln1b, ln_eps_, norm1_, n1b, n1hb, n1ib, act, aevb);
     });
-    if (naive_filters_)  // the MFMA path's k_attn_msg has done LayerNorm 1 already
+    if (scalar)  // the MFMA path's k_attn_msg has done LayerNorm 1 already
       hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, norm1_, n1b,
                          n1hb, n1ib, act);
     // the post-attention node chain in one kernel (MLP, interaction, LayerNorm 2, ev gate)
@@ -3523,7 +3527,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     double *hpb = hpre + b * Nz * kF, *tb = tout + b * Nz * kNI;
     double *p2h = pre2hat + b * Nz * kF, *p2i = pre2is + b * Nz;
     double *psb = ps + b * 4 * Pa, *pab = palpha + b * 16 * Pa;
-    double *pfb = naive_filters_ ? pf + b * 256 * Pa : (b > 0 ? pf + (b - 1) * 256 * Pa : nullptr);
+    double *pfb = scalar ? pf + b * 256 * Pa : (b > 0 ? pf + (b - 1) * 256 * Pa : nullptr);
     FilterArgs A;
     for (int k = 0; k < 2; ++k) {
       A.fw0[k] = B.fw0[k]; A.fb0[k] = B.fb0[k]; A.fw1t[k] = B.fw1t[k]; A.fb1[k] = B.fb1[k];
@@ -3534,7 +3538,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     const NodeChainBwdArgs NB{B.inttp, B.m2tp, B.m1tp, B.int_cg, B.ln1w, B.ln2w, norm1_, norm2_};
     hipLaunchKernelGGL(k_node_bwd, dim3(unsigned(ceil_div(N, 32))), dim3(256), 0, s, int(N), gx, gev, tb, aevb, p2h,
                        p2i, hpb, n1b, n1hb, n1ib, NB, gainv, gaev);
-    if (naive_filters_) {
+    if (scalar) {
       // scalar cross-check path: the attention reverse writes the pair
       // adjoints (df, dE/dfc, dE/dY) and the scalar filter reverse reads them
       timed(b == 0 ? "attn_bwd_block0" : "attn_bwd", 1, [&] {

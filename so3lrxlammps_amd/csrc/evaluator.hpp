@@ -265,6 +265,13 @@ class Evaluator {
   };
   bool timing_ = false;
   bool naive_filters_ = false;  // SO3LR_NAIVE_FILTERS=1: scalar filter kernels (cross-check)
+  // Small systems run the scalar filter kernels: with a few hundred active
+  // pairs the fully unrolled MFMA filters are bound by fetching their code
+  // into a cold instruction cache (30-40 us per launch).  Decided when a
+  // topology's active pairs are counted: at most scalar_pairs_max_ of them
+  // (SO3LR_SCALAR_FILTER_PAIRS; 0 never).
+  std::int64_t scalar_pairs_max_ = 256;
+  bool scalar_now_ = false;
   // Graph replay of one evaluation: the launch sequence of compute_device is
   // captured when the same call (inputs, outputs, flags, box, stream,
   // topology and buffer addresses) comes twice in a row, and replayed while

@@ -6,9 +6,12 @@ the 4.5 A cutoff, and packed images down to one atom each, with their own
 charge and multiplicity (a bare proton, an open-shell H atom, triplet O).
 Both the LAMMPS-rows path and the HBM-resident device path are checked at the
 bars of the other parity tests: energy 1e-10 relative, forces and virial
-1e-9 eV/A; each case runs on the shipped model (fused kernels) and on an
-F = 256 model (generic kernels).
+1e-9 eV/A; each case runs on the shipped model (with the filter kernels
+the library picks for these sizes, and with the fused MFMA ones forced) and
+on an F = 256 model (generic kernels).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -18,15 +21,27 @@ from oracle.oracle import Oracle
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module", params=["v1", "generic"])
+@pytest.fixture(scope="module", params=["v1", "v1_mfma", "generic"])
 def model(request, tmp_path_factory):
-    """The shipped model (fused v1 kernels) and a perturbed F = 256, R = 64
-    lift with duplicated degrees (generic kernels)."""
+    """The shipped model (v1 kernels: these systems are small enough for the
+    scalar filter kernels), the same with the fused MFMA filters forced
+    (SO3LR_SCALAR_FILTER_PAIRS=0 while its tests create their contexts), and
+    a perturbed F = 256, R = 64 lift with duplicated degrees (generic
+    kernels)."""
     if request.param == "v1":
-        return support.MODEL
-    d = tmp_path_factory.mktemp("edges")
-    return support.perturbed_model(d / "wide_p.so3lr", seed=23, scale=0.2,
-                                   base=support.lifted_model(d / "wide.so3lr"))
+        yield support.MODEL
+    elif request.param == "v1_mfma":
+        old = os.environ.get("SO3LR_SCALAR_FILTER_PAIRS")
+        os.environ["SO3LR_SCALAR_FILTER_PAIRS"] = "0"
+        yield support.MODEL
+        if old is None:
+            del os.environ["SO3LR_SCALAR_FILTER_PAIRS"]
+        else:
+            os.environ["SO3LR_SCALAR_FILTER_PAIRS"] = old
+    else:
+        d = tmp_path_factory.mktemp("edges")
+        yield support.perturbed_model(d / "wide_p.so3lr", seed=23, scale=0.2,
+                                      base=support.lifted_model(d / "wide.so3lr"))
 
 
 @pytest.fixture(scope="module")

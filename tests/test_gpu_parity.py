@@ -70,6 +70,41 @@ def test_molecule_matches_oracle(ctx, orc, name):
     _check(out, e, f, ea, w, terms)
 
 
+def test_molecules_mfma_filters_match_oracle(orc, monkeypatch):
+    """Molecules this small run the scalar filter kernels by default (at most
+    SO3LR_SCALAR_FILTER_PAIRS active pairs); the same molecules with the fused
+    MFMA filters forced, against the oracle at the same bars."""
+    from so3lrxlammps_amd import Context
+    monkeypatch.setenv("SO3LR_SCALAR_FILTER_PAIRS", "0")
+    c = Context(support.MODEL, 0)
+    for name in MOLECULES:
+        ref, z, pos, box = support.load_golden(name)
+        q, m = ref.get("charge", 0), ref.get("multiplicity", 1)
+        print("case", name, "(MFMA filters)", flush=True)
+        e, f, ea, w, terms = _hip_single_point(c, z, pos, box, q, m)
+        out = orc.evaluate(z, *support.build_graphs(pos, box), charge=q, multiplicity=m)
+        _check(out, e, f, ea, w, terms)
+    c.close()
+
+
+def test_small_system_filter_paths_agree(monkeypatch):
+    """The filter path switches with the active-pair count; both paths on the
+    same molecule agree to rounding (the scalar kernels use the library exp
+    and division, the MFMA ones the lean activations)."""
+    from so3lrxlammps_amd import Context
+    ref, z, pos, box = support.load_golden("alanine_cation")
+    res = []
+    for limit in ("0", "1000000"):
+        monkeypatch.setenv("SO3LR_SCALAR_FILTER_PAIRS", limit)
+        c = Context(support.MODEL, 0)
+        res.append(_hip_single_point(c, z, pos, box, 1, 2))
+        c.close()
+    (e0, f0, _, w0, _), (e1, f1, _, w1, _) = res
+    assert abs(e1 - e0) <= 1e-12 * abs(e0)
+    assert np.abs(f1 - f0).max() <= 1e-10
+    assert np.abs(w1 - w0).max() <= 1e-10 * max(1.0, np.abs(w0).max())
+
+
 def test_molecule_matches_golden_reference(ctx):
     """The HIP path against the reference's JAX vectors directly (float64 refs)."""
     for name in ["acetate", "alanine_cation", "methylammonium"]:
