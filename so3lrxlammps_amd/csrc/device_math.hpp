@@ -356,4 +356,30 @@ __device__ __forceinline__ bool lr_pair_terms(const LrParams &P, const double *_
   return true;
 }
 
+// Walks the active incidence entries of a node, [beg, end), in list order:
+// 64 entries per coalesced load of iact / iother, then the active ones two at
+// a time as uniform values, body(e1, o1, e2, o2, two) (when one is left the
+// second repeats the first and `two` is false), so a body may issue both
+// entries' loads before it sums either and still keep the order of a
+// sequential walk.  All 64 lanes of the wavefront take part.
+template <class Body>
+__device__ __forceinline__ void for_active_pairs(int beg, int end, const int *__restrict__ iact,
+                                                 const int *__restrict__ iother, int lane, Body &&body) {
+  for (int k0 = beg; k0 < end; k0 += 64) {
+    const int k = k0 + lane;
+    const int ent = k < end ? iact[k] : -1;
+    const int oth = k < end ? iother[k] : 0;
+    unsigned long long mask = __ballot(ent >= 0);
+    while (mask) {
+      const int l1 = __ffsll(mask) - 1;
+      mask &= mask - 1;
+      const bool two = mask != 0;
+      const int l2 = two ? __ffsll(mask) - 1 : l1;
+      if (two) mask &= mask - 1;
+      body(__builtin_amdgcn_readlane(ent, l1), __builtin_amdgcn_readlane(oth, l1),
+           __builtin_amdgcn_readlane(ent, l2), __builtin_amdgcn_readlane(oth, l2), two);
+    }
+  }
+}
+
 }  // namespace so3lr_amd

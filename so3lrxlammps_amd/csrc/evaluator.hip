@@ -1405,30 +1405,6 @@ __global__ void k_inc_active(int E, const int *inc, const int *cand2act, const i
   iother[k] = p < 0 ? 0 : pa[2 * p + 1 - (e & 1)];
 }
 
-// Walks the active incidence entries of node rows [beg, end) two at a time:
-// body(e1, o1, e2, o2, two) with uniform (scalar) entries; when only one is
-// left, the second repeats the first and `two` is false.  Entries are visited
-// in list order, so sums keep the order of a sequential walk.
-template <class Body>
-__device__ __forceinline__ void for_active_pairs(int beg, int end, const int *iact, const int *iother, int lane,
-                                                 Body &&body) {
-  for (int k0 = beg; k0 < end; k0 += kWave) {
-    const int k = k0 + lane;
-    const int ent = k < end ? iact[k] : -1;
-    const int oth = k < end ? iother[k] : 0;
-    unsigned long long mask = __ballot(ent >= 0);
-    while (mask) {
-      const int l1 = __ffsll(mask) - 1;
-      mask &= mask - 1;
-      const bool two = mask != 0;
-      const int l2 = two ? __ffsll(mask) - 1 : l1;
-      if (two) mask &= mask - 1;
-      body(__builtin_amdgcn_readlane(ent, l1), __builtin_amdgcn_readlane(oth, l1),
-           __builtin_amdgcn_readlane(ent, l2), __builtin_amdgcn_readlane(oth, l2), two);
-    }
-  }
-}
-
 // Attention forward, node-major (kokkos_integrated_block0.cpp:330-385): for
 // node n and every incident active pair p = {n, o}, the edge o -> n gives
 // alpha = <q_n, k_o (.) f_p> / avg (per head) and the messages

@@ -275,32 +275,6 @@ __device__ __forceinline__ void g_norm_row_bwd(int F, int mode, const double *gy
   for (int j = 0; j < J; ++j) gx[j] = is * (gh[j] - mg - h[j] * mgx);
 }
 
-// Walks the active incidence entries of a node, [beg, end), in list order:
-// 64 entries per coalesced load of iact / iother, then the active ones two at
-// a time as uniform values, body(e1, o1, e2, o2, two) (when one is left the
-// second repeats the first and `two` is false), so a body can issue both
-// entries' loads before it sums either, and the sums keep the order of a
-// sequential walk.
-template <class Body>
-__device__ __forceinline__ void g_walk(int beg, int end, const int *__restrict__ iact, const int *__restrict__ iother,
-                                       int lane, Body &&body) {
-  for (int k0 = beg; k0 < end; k0 += 64) {
-    const int k = k0 + lane;
-    const int ent = k < end ? iact[k] : -1;
-    const int oth = k < end ? iother[k] : 0;
-    unsigned long long mask = __ballot(ent >= 0);
-    while (mask) {
-      const int l1 = __ffsll(mask) - 1;
-      mask &= mask - 1;
-      const bool two = mask != 0;
-      const int l2 = two ? __ffsll(mask) - 1 : l1;
-      if (two) mask &= mask - 1;
-      body(__builtin_amdgcn_readlane(ent, l1), __builtin_amdgcn_readlane(oth, l1),
-           __builtin_amdgcn_readlane(ent, l2), __builtin_amdgcn_readlane(oth, l2), two);
-    }
-  }
-}
-
 // Attention messages, node-major (kokkos_integrated_block0.cpp:330-385):
 // node n receives from each incident pair's partner o the invariant message
 // fc alpha v_o and the equivariant fc alpha_ev Y (parity of the direction),
@@ -365,7 +339,7 @@ __global__ __launch_bounds__(256) void g_attn_msg(GDims d, int N, const int *__r
     for (int j = 0; j < 2; ++j)
       if (lane + 64 * j < E) de[j] += T.fc * T.ae[j] * T.y[j];
   };
-  g_walk(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+  for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
     const Terms A = load(e1, o1), B = load(e2, o2);
     add(A);
     if (two) add(B);
@@ -617,7 +591,7 @@ __global__ __launch_bounds__(256) void g_attn_bwd_node(GDims d, int N, const int
   };
   // one entry's loads at a time here (174 registers; both entries' loads
   // first took 256 and ran no faster)
-  g_walk(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
+  for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
     add(load(e1, o1));
     if (two) add(load(e2, o2));
   });
