@@ -67,6 +67,7 @@ struct GemmArgs {
   // zy * (..)0 + zx * (..)1 elements, W by z * wbs
   int nbx;
   long xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs;
+  int ldw;  // WKO: the weight's row length (its full output width); 0: O
 };
 
 typedef double gv4d __attribute__((ext_vector_type(4)));
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_GEMM_
       const int idx = tid + 256 * q;
       if (WKO) {
         const int cc = idx % BN, kk = idx / BN, col = col0 + cc, k = k0 + kk;
-        wreg[q] = (col < A.O && k < A.K) ? A.W[std::size_t(k) * A.O + col] : 0.0;
+        wreg[q] = (col < A.O && k < A.K) ? A.W[std::size_t(k) * (A.ldw ? A.ldw : A.O) + col] : 0.0;
       } else {
         const int kk = idx & 15, cc = idx >> 4, col = col0 + cc, k = k0 + kk;
         wreg[q] = (col < A.O && k < A.K) ? A.W[std::size_t(col) * A.K + k] : 0.0;
@@ -876,20 +877,49 @@ void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const doub
           const double *res = nullptr, int ldres = 0, double *Y2 = nullptr, int ldy2 = 0) {
   if (rows <= 0) return;
   GemmArgs A{rows, rows_dev, K, O, X, ldx, W, bias, Y, ldy, Y2, ldy2, aux, ldaux, res, ldres,
-             1, 0, 0, 0, 0, 0, 0, 0};
-  // column blocks of at most 32 kGemmMaxNT columns; NT = 32-column tiles per wavefront
+             1, 0, 0, 0, 0, 0, 0, 0, 0};
+  // column blocks of 32 kGemmMaxNT columns, and the rest (O not a multiple
+  // of that, e.g. 320 = 2 x 128 + 64) as a launch of its own on the columns
+  // left, so no block computes padded columns; NT = 32-column tiles per
+  // wavefront
   const int cmax = 32 * kGemmMaxNT;
-  const int nb = (O + cmax - 1) / cmax, cols = (O + nb - 1) / nb, tiles = (cols + 31) / 32;
-  const dim3 grid(blocks_for(std::size_t(rows), 64), unsigned(nb));
+  const dim3 gr(blocks_for(std::size_t(rows), 64));
+  auto launch = [&](GemmArgs B, int nb, int tiles) {
+    const dim3 grid(gr.x, unsigned(nb));
 #define G_GEMM_NT(NT)                                                              \
   if (tiles <= NT) {                                                               \
-    A.O = O;                                                                       \
-    hipLaunchKernelGGL((g_gemm<EPI, WKO, NT>), grid, dim3(256), 0, s, A);          \
+    hipLaunchKernelGGL((g_gemm<EPI, WKO, NT>), grid, dim3(256), 0, s, B);          \
     return;                                                                        \
   }
-  G_GEMM_NT(2) G_GEMM_NT(4) G_GEMM_NT(6) G_GEMM_NT(8) G_GEMM_NT(10)
+    G_GEMM_NT(2) G_GEMM_NT(4) G_GEMM_NT(6) G_GEMM_NT(8) G_GEMM_NT(10)
 #undef G_GEMM_NT
-  throw std::logic_error("SO3LR: generic GEMM with more than 320 columns per block");
+    throw std::logic_error("SO3LR: generic GEMM with more than 320 columns per block");
+  };
+  const int full = O / cmax, rest = O - full * cmax;
+  if (full == 0 || rest == 0) {
+    const int nb = (O + cmax - 1) / cmax, cols = (O + nb - 1) / nb;
+    launch(A, nb, (cols + 31) / 32);
+    return;
+  }
+  GemmArgs M = A;
+  M.O = full * cmax;
+  if (WKO) M.ldw = O;
+  launch(M, full, kGemmMaxNT);
+  GemmArgs R = A;
+  const int c0 = full * cmax;
+  R.O = rest;
+  if (WKO) {
+    R.W = W + c0;
+    R.ldw = O;
+  } else {
+    R.W = W + std::size_t(c0) * K;
+  }
+  if (bias) R.bias = bias + c0;
+  R.Y = Y + c0;
+  if (Y2) R.Y2 = Y2 + c0;
+  if (aux) R.aux = aux + c0;
+  if (res) R.res = res + c0;
+  launch(R, 1, (rest + 31) / 32);
 }
 // Per-head 32 x 32 projections as one batched launch (O = K = 32).
 template <int EPI, bool WKO>
@@ -898,7 +928,7 @@ void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int 
                 int ldres = 0, long rbs0 = 0, long rbs1 = 0) {
   if (rows <= 0) return;
   GemmArgs A{rows, nullptr, 32, 32, X, ldx, W, nullptr, Y, ldy, nullptr, 0, nullptr, 0, res, ldres,
-             nbx, xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs};
+             nbx, xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs, 0};
   hipLaunchKernelGGL((g_gemm<EPI, WKO, 2>), dim3(blocks_for(std::size_t(rows), 64), 1, unsigned(nby * nbx)),
                      dim3(256), 0, s, A);
 }
