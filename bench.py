@@ -116,8 +116,8 @@ def kernel_work(widths):
     F, R = widths["invariant_features"], widths["radial_basis_features"]
     NH, FH = len(widths["degree_slots"]), widths["invariant_features"] // 4
     alg = 2 * 2 * (R * F + NH * FH + (F + FH) * F)
-    work["generic_filter_fwd"] = ("g_gemm: filter forward (6 launches)", "mfma", alg, alg, "pair")
-    work["generic_filter_bwd"] = ("g_gemm: filter reverse (10 launches)", "mfma", alg,
+    work["generic_filter_fwd"] = ("g_gemm: filter forward section (both filters)", "mfma", alg, alg, "pair")
+    work["generic_filter_bwd"] = ("g_gemm: filter reverse section (both filters)", "mfma", alg,
                                   alg + 2 * 2 * (R * F + NH * FH), "pair")
     return work
 
