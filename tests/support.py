@@ -36,6 +36,48 @@ def perturbed_model(path, seed=11, scale=0.2, base=MODEL):
     return str(path)
 
 
+def relabelled_model(path, swaps=((1, 11), (7, 17)), base=MODEL):
+    """A copy of the model `base` in which the element rows of each pair of
+    atomic numbers in `swaps` trade places in every per-element table, at the
+    reference's indexing of each: the learned one-hot tables 118 wide at
+    class Z - 1 (embedding, charge/spin queries, energy scales and shifts;
+    kokkos_output_heads.cpp:424-436, kokkos_local_energy_reverse.cpp:190-214),
+    the 100-row head tables at row Z (atomic charge embedding, Hirshfeld
+    queries and shifts; kokkos_output_heads.cpp:157-174,424-439) and the
+    reference polarisabilities and C6 at Z - 1
+    (kokkos_physical_long_range.cpp:201-211).  A molecule evaluated with this
+    model and its atoms relabelled by the same swaps has the learned energy,
+    charges, Hirshfeld ratios and long-range energy of the original
+    (everything but the ZBL repulsion, which sees the nuclear charge)."""
+    from so3lrxlammps_amd.model_file import read_model, write_model
+    manifest, arrays = read_model(base)
+    learned = {"model.inv_feature_embedding.embedding.weight", "model.charge_embedding.Wq.weight",
+               "model.spin_embedding.Wq.weight", "model.atomic_energy_output_block.energy_scales.weight",
+               "model.atomic_energy_output_block.energy_shifts"}
+    by_z = {"model.partial_charges_output_block.atomic_embedding.weight",
+            "model.hirshfeld_output_block.q_embedding.weight", "model.hirshfeld_output_block.v_shift_embedding.weight"}
+    physical = {"physical.reference_alphas", "physical.reference_c6"}
+    for key in learned | by_z | physical:
+        a = arrays[key].copy()
+        for za, zb in swaps:
+            if key in learned:
+                assert a.shape[-1] == 118, key
+                a[..., [za - 1, zb - 1]] = a[..., [zb - 1, za - 1]]
+            elif key in by_z:
+                assert a.shape[0] == 100, key
+                a[[za, zb]] = a[[zb, za]]
+            else:
+                a[[za - 1, zb - 1]] = a[[zb - 1, za - 1]]
+        arrays[key] = a
+    # no other tensor may carry a per-element axis
+    for rec in manifest["tensors"]:
+        k = rec["state_key"]
+        if k not in learned | by_z | physical and k != "atomic_numbers_map":
+            assert not any(d in (100, 102, 118) for d in arrays[k].shape), k
+    write_model(str(path), manifest, arrays)
+    return str(path)
+
+
 def variant_model(path, blocks=None, rms_norm=False, norm2=True, qk_norm=False, resid=None, x0=None,
                   nlh=None, c6=None, message_normalization=None, edit=None, seed=5, base=MODEL):
     """A model file with the reference's optional operators switched on

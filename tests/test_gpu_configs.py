@@ -38,6 +38,11 @@ def _device_eval(ctx, x, lo, hi, per, eatom=False):
 
 
 def _check(e, f, w, out, wtol=1e-9):
+    # the achieved margins, printed so the logs show them against the bars
+    print("  |dE|/|E| %.2e  max|dF| %.2e eV/A  max|dW| %.2e eV (max|W| %.2e, bar %.2e eV)" % (
+        abs(e - out["energy"]) / abs(out["energy"]), np.abs(f - out["forces"]).max(),
+        np.abs(w - out["virial"]).max(), np.abs(out["virial"]).max(),
+        wtol * max(1.0, np.abs(out["virial"]).max())), flush=True)
     assert abs(e - out["energy"]) <= 1e-10 * abs(out["energy"]), (e, out["energy"])
     assert np.abs(f - out["forces"]).max() <= 1e-9
     assert np.abs(w - out["virial"]).max() <= wtol * max(1.0, np.abs(out["virial"]).max())

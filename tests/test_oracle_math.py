@@ -11,7 +11,11 @@ finite differences of the energy and symmetry invariants.
 * rotation / translation invariance and zero net torque (pins equivariance);
 * charge/spin: the table is exactly zero for Q=0, M=1, and (Q, M) parity rules;
 * per-atom virial: sum rule against the virial, dimer symmetry, permutation,
-  shift, and the f.r identity of an isolated molecule.
+  shift, and the f.r identity of an isolated molecule;
+* Na and Cl rows (no golden vector holds an ion): relabelling H -> Na and
+  N -> Cl together with a model whose element tables trade those rows leaves
+  every term but ZBL unchanged (ZBL reads no table: it is one function of
+  the nuclear charges for every element, pinned by the molecules' goldens).
 """
 import numpy as np
 import pytest
@@ -207,3 +211,27 @@ def test_per_atom_virial(orc):
                       0.5 * (x[:, 0] * f[:, 2] + x[:, 2] * f[:, 0]).sum(),
                       0.5 * (x[:, 1] * f[:, 2] + x[:, 2] * f[:, 1]).sum()])
     assert np.abs(base["vatom"].sum(0) - fdotr).max() < 1e-9
+
+
+def test_ion_rows_by_relabelling(orc, tmp_path):
+    """Na (Z = 11) and Cl (Z = 17) through every per-element table: alanine
+    with H relabelled Na and N relabelled Cl, evaluated with a model whose
+    tables trade the rows of those elements (support.relabelled_model, at
+    the reference's own indexing of each table), gives the original learned
+    energies, charges, Hirshfeld ratios and long-range energies atom by atom.
+    A table read at the wrong row for Z > 10 only (an 8- or 10-element table,
+    an index off by one past neon) changes one of them.  The electron parity
+    is unchanged (+10 per relabelled atom), so (Q, M) stays valid."""
+    ref, z, pos, box = support.load_golden("alanine_cation")
+    q, m = ref["charge"], ref["multiplicity"]
+    sr, lr = support.build_graphs(pos, box)
+    base = orc.evaluate(z, sr, lr, charge=q, multiplicity=m)
+    z2 = np.asarray(z).copy()
+    z2[z2 == 1] = 11
+    z2[z2 == 7] = 17
+    assert (z2 == 11).any() and (z2 == 17).any()
+    relab = Oracle(support.relabelled_model(tmp_path / "relabelled.so3lr")).evaluate(
+        z2, sr, lr, charge=q, multiplicity=m)
+    for key in ("e_learned", "charges", "hirshfeld", "e_lr"):
+        np.testing.assert_allclose(relab[key], base[key], rtol=1e-13, atol=1e-14, err_msg=key)
+    assert not np.allclose(relab["e_zbl"], base["e_zbl"])
