@@ -359,7 +359,11 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
     else
       hipLaunchKernelGGL((k_list_walk<false, false>), grid, dim3(256), 0, s, int(L.inum), int(n_rows), il, of, ng,
                          d_owner, nullptr, nullptr, nullptr, poff, rows, nodes);
-    // incidence: endpoint slots 2p + side sorted by their node (stable)
+    // incidence: endpoint slots 2p + side sorted by their node (stable).
+    // A topology that the first evaluation puts in spatial node order
+    // (order_rows_nodes) gets its incidence there, from the relabelled nodes,
+    // and no evaluation runs before that: it is not sorted twice.
+    if (reorder) continue;
     const int m = int(2 * L.pairs);
     hipLaunchKernelGGL(k_iota, dim3(unsigned((m + 255) / 256)), dim3(256), 0, s, m, slots);
     std::size_t tmp_bytes = tmp_max;
@@ -370,7 +374,10 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
   }
   p_sr_ = lists[0].pairs;
   p_lr_ = lists[1].pairs;
-  build_lr_records();
+  if (reorder)  // built by order_rows_nodes, on a buffer sized here
+    ensure<int>(lr_rec_, 3 * std::size_t(std::max<std::int64_t>(2 * p_lr_, 1)));
+  else
+    build_lr_records();
   TOPO_CHECK(hipGetLastError());
   TOPO_CHECK(hipStreamSynchronize(s));
   n_rows_ = n_rows;
