@@ -223,6 +223,7 @@ class Context:
         z = np.ascontiguousarray(z, dtype=np.int32)
         self._check(self._lib.so3lr_set_system(self._h, len(z), ptr(z), float(charge), float(multiplicity)))
         self.n = len(z)
+        self.rows = None  # a new system needs a new topology
 
     def set_images(self, z, image_offsets, charges, multiplicities):
         z = np.ascontiguousarray(z, dtype=np.int32)
@@ -235,6 +236,7 @@ class Context:
         self._check(self._lib.so3lr_set_images(self._h, len(z), ptr(z), len(q), ptr(off), ptr(q), ptr(m)))
         self.n = len(z)
         self.n_images = len(q)
+        self.rows = None  # a new system needs a new topology
 
     def set_topology(self, lists):
         (si, so, sn), (li, lo_, ln) = lists.lists
@@ -244,10 +246,19 @@ class Context:
             len(si), ptr(si), ptr(so), ptr(sn), len(li), ptr(li), ptr(lo_), ptr(ln)))
         self.rows = lists.rows
 
-    def compute(self, x_rows, eatom=True):
+    def compute(self, x_rows, eatom=True, out=None):
+        """so3lr_compute on host arrays: (energy, forces, eatom, virial).
+        `out` = (forces (n, 3), eatom (n,)) reuses the caller's arrays, as a
+        pair style reuses its own from step to step."""
         x_rows = np.ascontiguousarray(x_rows, dtype=np.float64)
-        f = np.zeros((self.n, 3))
-        ea = np.zeros(self.n)
+        if out is None:
+            f = np.zeros((self.n, 3))
+            ea = np.zeros(self.n)
+        else:
+            f, ea = out
+            if f.shape != (self.n, 3) or ea.shape != (self.n,) or f.dtype != np.float64 or ea.dtype != np.float64 \
+                    or not (f.flags.c_contiguous and ea.flags.c_contiguous):
+                raise ValueError("out must be C-contiguous float64 arrays of shape (%d, 3) and (%d,)" % (self.n, self.n))
         e = ctypes.c_double()
         w = np.zeros(6)
         flags = ENERGY | VIRIAL | (EATOM if eatom else 0)
@@ -255,11 +266,19 @@ class Context:
                                             ctypes.byref(e), ptr(w)))
         return e.value, f, ea, w
 
+    def _rows(self):
+        """Rows the positions must cover; refused like the library's own
+        ERR_STATE when no topology follows the current system."""
+        rows = getattr(self, "rows", None)
+        if rows is None:
+            raise SO3LRError(ERR_STATE, "SO3LR: compute called before set_topology")
+        return rows
+
     def compute_device(self, x_rows_dev, f_dev, eatom_dev=None, stream=None):
         """Device tensors in (positions of every row: owned and ghost rows after
         set_topology, owned atoms after reneighbor_device), device forces out;
         returns (energy, virial)."""
-        px = device_f64(x_rows_dev, 3 * self.rows, "positions")
+        px = device_f64(x_rows_dev, 3 * self._rows(), "positions")
         pf = device_f64(f_dev, 3 * self.n, "forces")
         pe = None if eatom_dev is None else device_f64(eatom_dev, self.n, "per-atom energies")
         if stream is not None:
@@ -273,7 +292,7 @@ class Context:
     def compute_device_noalloc(self, x_rows_dev, f_dev, eatom_dev=None, stream=None):
         """As compute_device through so3lr_compute_device_noalloc: the work
         buffers are slices of the library's static device array."""
-        px = device_f64(x_rows_dev, 3 * self.rows, "positions")
+        px = device_f64(x_rows_dev, 3 * self._rows(), "positions")
         pf = device_f64(f_dev, 3 * self.n, "forces")
         pe = None if eatom_dev is None else device_f64(eatom_dev, self.n, "per-atom energies")
         if stream is not None:

@@ -112,7 +112,10 @@ __global__ __launch_bounds__(256) void k_list_walk(int inum, int n_rows, const i
   }
 }
 
-// exclusive scan of cnt[0..n) into out[0..n] (one block; fixed order)
+// Exclusive scan of cnt[0..n) into out[0..n] (one block; fixed order): the
+// per-receiver pair counts.  The sum is at most
+// the list's entry count, which set_topology refuses above 2^30 on the host
+// before any upload, so every partial sum fits an int.
 __global__ __launch_bounds__(1024) void k_scan_rows(int n, const int *cnt, int *out) {
   __shared__ int part[1024];
   __shared__ int base;
@@ -153,14 +156,19 @@ __global__ void k_segment_starts(int m, int n, const int *skey, int *off) {
 
 // Bounding box of the first n rows: out = {min x, y, z, max x, y, z}.  One
 // block; the reduction order is fixed.
+// min and max that keep a NaN once they have seen one (fmin/fmax drop it),
+// so that a NaN coordinate reaches the host's finiteness check
+__device__ __forceinline__ double min_keep_nan(double a, double b) { return (b < a || b != b) ? b : a; }
+__device__ __forceinline__ double max_keep_nan(double a, double b) { return (b > a || b != b) ? b : a; }
+
 __global__ __launch_bounds__(1024) void k_bbox(int n, const double *x, double *out) {
   __shared__ double sh[6][1024];
   const int t = threadIdx.x;
   double lo[3] = {HUGE_VAL, HUGE_VAL, HUGE_VAL}, hi[3] = {-HUGE_VAL, -HUGE_VAL, -HUGE_VAL};
   for (int i = t; i < n; i += 1024)
     for (int d = 0; d < 3; ++d) {
-      lo[d] = fmin(lo[d], x[3 * i + d]);
-      hi[d] = fmax(hi[d], x[3 * i + d]);
+      lo[d] = min_keep_nan(lo[d], x[3 * i + d]);
+      hi[d] = max_keep_nan(hi[d], x[3 * i + d]);
     }
   for (int d = 0; d < 3; ++d) {
     sh[d][t] = lo[d];
@@ -170,8 +178,8 @@ __global__ __launch_bounds__(1024) void k_bbox(int n, const double *x, double *o
   for (int st = 512; st > 0; st >>= 1) {
     if (t < st)
       for (int d = 0; d < 3; ++d) {
-        sh[d][t] = fmin(sh[d][t], sh[d][t + st]);
-        sh[3 + d][t] = fmax(sh[3 + d][t], sh[3 + d][t + st]);
+        sh[d][t] = min_keep_nan(sh[d][t], sh[d][t + st]);
+        sh[3 + d][t] = max_keep_nan(sh[3 + d][t], sh[3 + d][t + st]);
       }
     __syncthreads();
   }
@@ -399,7 +407,9 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
 // node's entries stay in increasing pair order).  Runs once per topology, at
 // its first evaluation, on buffers set_topology sized.
 void Evaluator::order_rows_nodes(const double *x) {
-  rows_order_pending_ = false;
+  // rows_order_pending_ stays set until the order is built: a refusal below
+  // (non-finite positions) leaves the topology exactly as set_topology left
+  // it, unsorted incidence and all, and the next evaluation orders it again
   const int n = int(n_);
   hipStream_t s = stream_;
   double *box = ensure<double>(top_box_, 6);
@@ -455,6 +465,7 @@ void Evaluator::order_rows_nodes(const double *x) {
   TOPO_CHECK(hipGetLastError());
   TOPO_CHECK(hipStreamSynchronize(s));
   permuted_ = true;
+  rows_order_pending_ = false;
   ++topo_version_;
 }
 

@@ -1,8 +1,9 @@
 """HIP path vs the CPU oracle, through the C ABI (libso3lr_hip.so).
 
 Tolerances are the ones BASELINE.json states for this path: energies within
-1e-10 relative, forces and virial within 1e-9 eV/A (virial components in eV,
-compared at 1e-9 relative to their scale).  The oracle's graph is built by
+1e-10 relative, forces within 1e-9 eV/A and the virial within 1e-9 eV
+(absolute: the oracle sums its totals with compensation, so its own rounding
+stays far below that at every size).  The oracle's graph is built by
 brute force with the minimum-image convention (tests/support.py), the HIP
 path's by the LAMMPS stand-in (ghost rows, full SR + half LR lists with a
 1 A skin), so the neighbour handling is checked too.
@@ -44,13 +45,13 @@ def _hip_single_point(ctx, z, pos, box, charge, mult):
 
 def _check(out, e, f, ea, w, terms, ftol=1e-9):
     # the achieved margins, printed so the logs show them against the bars
+    support.record_margin(e, f, w, out)
     print("  |dE|/|E| %.2e  max|dF| %.2e eV/A  max|dW| %.2e eV (max|W| %.2e)" % (
         abs(e - out["energy"]) / abs(out["energy"]), np.abs(f - out["forces"]).max(),
         np.abs(w - out["virial"]).max(), np.abs(out["virial"]).max()), flush=True)
     assert abs(e - out["energy"]) <= 1e-10 * abs(out["energy"]), (e, out["energy"])
     assert np.abs(f - out["forces"]).max() <= ftol
-    wscale = max(1.0, np.abs(out["virial"]).max())
-    assert np.abs(w - out["virial"]).max() <= 1e-9 * wscale
+    assert np.abs(w - out["virial"]).max() <= 1e-9  # eV, absolute
     assert np.abs(ea - out["eatom"]).max() <= 1e-10 * max(1.0, np.abs(out["eatom"]).max())
     assert np.abs(terms["charges"] - out["charges"]).max() <= 1e-12
     assert np.abs(terms["hirshfeld"] - out["hirshfeld"]).max() <= 1e-12
@@ -477,5 +478,36 @@ def test_active_pair_capacity_overflow_reevaluates():
     b.set_topology(lists)
     e2, f2, ea2, w2 = b.compute(rows1)
     assert e1 == e2 and np.array_equal(f1, f2) and np.array_equal(ea1, ea2) and np.array_equal(w1, w2)
+    a.close()
+    b.close()
+
+
+def test_refused_first_evaluation_leaves_context_usable():
+    """The first evaluation of a single system's LAMMPS-list topology puts its
+    nodes in spatial order and sorts the incidence there.  A first evaluation
+    with a non-finite owned position is refused before any of that; the next
+    finite evaluation on the same context must order the topology itself and
+    equal, bit for bit, a fresh context's first evaluation."""
+    from so3lrxlammps_amd import Context, Lists, _lib
+    ref, z, pos, box = support.load_golden("alanine")
+    lists = Lists(pos, pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0))
+    rows = lists.rows_positions(pos)
+    bad = rows.copy()
+    bad[3, 1] = np.nan
+    a = Context(support.MODEL, 0)
+    a.set_system(z, 0, 1)
+    a.set_topology(lists)
+    print("case alanine, NaN first evaluation", flush=True)
+    with pytest.raises(_lib.SO3LRError) as err:
+        a.compute(bad)
+    assert err.value.code == _lib.ERR_ARGUMENT and "non-finite" in str(err.value)
+    got = a.compute(rows)
+    b = Context(support.MODEL, 0)
+    b.set_system(z, 0, 1)
+    b.set_topology(lists)
+    want = b.compute(rows)
+    assert got[0] == want[0]
+    for g, w in zip(got[1:], want[1:]):
+        assert np.array_equal(g, w)
     a.close()
     b.close()
