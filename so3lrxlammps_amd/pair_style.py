@@ -44,10 +44,12 @@ class PairSO3LRNativeMPI:
     single_enable = 0
     no_virial_fdotr_compute = 1
 
-    def __init__(self, device=0, skin=1.0, comm_cutoff=13.0):
+    def __init__(self, device=0, skin=1.0, comm_cutoff=13.0, nprocs=1):
         self.device = device
         self.skin = skin
         self.comm_cutoff = comm_cutoff
+        self.nprocs = nprocs  # MPI ranks of this LAMMPS run
+        self.warnings = []    # what error->warning would print
         self.ctx = None
         self.type_to_z = None
         self.total_charge = 0.0
@@ -100,11 +102,22 @@ class PairSO3LRNativeMPI:
             raise LammpsError("Pair style so3lr/native/mpi model was not initialized")
         if self.type_to_z is None:
             raise LammpsError("Pair style so3lr/native/mpi coefficients are missing")
+        # one rank drives one GPU: ghosts come from LAMMPS's own communication
+        if self.nprocs != 1:
+            raise LammpsError("Pair style so3lr/native/mpi on libso3lr_hip runs one MPI rank per GPU "
+                              "(got %d ranks)" % self.nprocs)
+        if self.comm_cutoff < self.long_range_cutoff + self.skin:
+            raise LammpsError("Pair style so3lr/native/mpi needs comm_modify cutoff >= %g "
+                              "(long-range cutoff + skin)" % (self.long_range_cutoff + self.skin))
         z = self.type_to_z[np.asarray(atoms.types)]
         try:
             self.ctx.set_system(z, self.total_charge, self.multiplicity)
         except _lib.SO3LRError as exc:
             raise LammpsError("Pair style so3lr/native/mpi: %s" % exc) from exc
+        if self.total_charge != 0.0 and any(atoms.periodic):
+            self.warnings.append("SO3LR: net charge %g in a periodic cell. SO3LR's long range is "
+                                 "truncated real-space Coulomb, so the energy is defined, but there is "
+                                 "no neutralizing background" % self.total_charge)
         self._lists = None
 
     def _neighbor(self, atoms):
