@@ -67,6 +67,24 @@ static int model_dims(const orc_model *m, dims_t *d) {
   return 0;
 }
 
+/* Compensated (Kahan-Babuska-Neumaier) accumulation of the extensive totals:
+ * energy and virial of a 150,000-atom cell sum tens of millions of terms, and
+ * a plain running sum carries a rounding error of order 1e-12 relative that
+ * would be the checker's own.  sum_add keeps the lost low part in c; the
+ * total is s + c. */
+typedef struct {
+  double s, c;
+} csum_t;
+static void sum_add(csum_t *a, double x) {
+  const double t = a->s + x;
+  if (fabs(a->s) >= fabs(x))
+    a->c += (a->s - t) + x;
+  else
+    a->c += (x - t) + a->s;
+  a->s = t;
+}
+static double sum_value(const csum_t *a) { return a->s + a->c; }
+
 static double silu(double x) { return x / (1.0 + exp(-x)); }
 static double silu_prime(double x) {
   const double s = 1.0 / (1.0 + exp(-x));
@@ -532,7 +550,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   double *lr_e = NULL, *lr_dq = NULL, *lr_dh = NULL, *lr_f = NULL, *lr_pf = NULL;
   double *sr_f = NULL, *gqkv = NULL, *gfinv = NULL, *gfev = NULL, *gfc = NULL;
   double *img_sum = NULL, *img_cnt = NULL, *img_seed = NULL;
-  double elec_total = 0.0, disp_total = 0.0;
+  csum_t elec_total = {0, 0}, disp_total = {0, 0};
   double *gs = NULL, *gainv = NULL, *gaev = NULL;
   int64_t *roff = NULL, *ridx = NULL, *soff = NULL, *sidx = NULL;
   lr_pair_t *lrp = NULL;
@@ -775,7 +793,7 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
     if (!lrp[p].valid) continue;
     const int64_t i = pi[p], j = pj[p];
     const double pe = lrp[p].e_elec + lrp[p].e_disp;
-    elec_total += lrp[p].e_elec; disp_total += lrp[p].e_disp;
+    sum_add(&elec_total, lrp[p].e_elec); sum_add(&disp_total, lrp[p].e_disp);
     lr_e[i] += 0.5 * pe; lr_e[j] += 0.5 * pe;
     lr_dq[i] += lrp[p].charge_pref * q[j]; lr_dq[j] += lrp[p].charge_pref * q[i];
     lr_dh[i] += lrp[p].dhi; lr_dh[j] += lrp[p].dhj;
@@ -1018,28 +1036,32 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
   }
 
   /* ---- outputs ---- */
-  double W[6] = {0, 0, 0, 0, 0, 0};
+  /* W = -sum v (x) g over SR edges and LR pairs, symmetrised
+   * (pair_so3lr_native_mpi.cpp:944-990), compensated */
+  csum_t Wc[6] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}, {0, 0}};
   for (int64_t e = 0; e < ne; ++e) {
     const double *v = vec + 3 * e, *g = ge + 3 * e;
-    W[0] -= v[0] * g[0]; W[1] -= v[1] * g[1]; W[2] -= v[2] * g[2];
-    W[3] -= 0.5 * (v[0] * g[1] + v[1] * g[0]);
-    W[4] -= 0.5 * (v[0] * g[2] + v[2] * g[0]);
-    W[5] -= 0.5 * (v[1] * g[2] + v[2] * g[1]);
+    sum_add(&Wc[0], -v[0] * g[0]); sum_add(&Wc[1], -v[1] * g[1]); sum_add(&Wc[2], -v[2] * g[2]);
+    sum_add(&Wc[3], -0.5 * (v[0] * g[1] + v[1] * g[0]));
+    sum_add(&Wc[4], -0.5 * (v[0] * g[2] + v[2] * g[0]));
+    sum_add(&Wc[5], -0.5 * (v[1] * g[2] + v[2] * g[1]));
   }
   for (int64_t p = 0; p < np; ++p) {
     if (!lrp[p].valid) continue;
     const double *v = pvec + 3 * p, *g = lr_pf + 3 * p;
-    W[0] -= v[0] * g[0]; W[1] -= v[1] * g[1]; W[2] -= v[2] * g[2];
-    W[3] -= 0.5 * (v[0] * g[1] + v[1] * g[0]);
-    W[4] -= 0.5 * (v[0] * g[2] + v[2] * g[0]);
-    W[5] -= 0.5 * (v[1] * g[2] + v[2] * g[1]);
+    sum_add(&Wc[0], -v[0] * g[0]); sum_add(&Wc[1], -v[1] * g[1]); sum_add(&Wc[2], -v[2] * g[2]);
+    sum_add(&Wc[3], -0.5 * (v[0] * g[1] + v[1] * g[0]));
+    sum_add(&Wc[4], -0.5 * (v[0] * g[2] + v[2] * g[0]));
+    sum_add(&Wc[5], -0.5 * (v[1] * g[2] + v[2] * g[1]));
   }
-  double etot = 0.0;
+  double W[6];
+  for (int c = 0; c < 6; ++c) W[c] = sum_value(&Wc[c]);
+  csum_t etot_c = {0, 0};
   for (int64_t i = 0; i < n; ++i) {
     double ez = 0.0;
     for (int64_t k = roff[i]; k < roff[i + 1]; ++k) ez += zbl_e[ridx[k]];
     const double ei = eatom[i] + ez + lr_e[i];
-    etot += ei;
+    sum_add(&etot_c, ei);
     if (out->e_learned) out->e_learned[i] = eatom[i];
     if (out->e_zbl) out->e_zbl[i] = ez;
     if (out->e_lr) out->e_lr[i] = lr_e[i];
@@ -1077,9 +1099,9 @@ int orc_evaluate(const orc_model *m, int64_t n, const int64_t *z,
       }
     }
   }
-  out->e_elec_total = elec_total;
-  out->e_disp_total = disp_total;
-  out->e_total = etot;
+  out->e_elec_total = sum_value(&elec_total);
+  out->e_disp_total = sum_value(&disp_total);
+  out->e_total = sum_value(&etot_c);
   status = 0;
 
 fail:

@@ -17,6 +17,26 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = os.path.join(REPO, "tests", "golden")
 MODEL = os.path.join(REPO, "models", "so3lr.so3lr")
 
+# achieved parity margins of the GPU tests, printed at the end of the pytest
+# run by tests/conftest.py (pytest keeps the stdout of passing tests to itself)
+MARGINS = []
+# trajectory comparisons: (case, max|dx| in A, energy difference, its unit)
+TRAJECTORY = []
+
+
+def record_margin(e, f, w, out, what=""):
+    """Record one comparison of a HIP result (energy e, forces f, virial w)
+    with the oracle's `out`: |dE|/|E|, max|dF| and the absolute max|dW|,
+    under the current test's name."""
+    case = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0].split("::")[-1]
+    row = (case + (" " + what if what else ""),
+           abs(e - out["energy"]) / max(abs(out["energy"]), 1e-300),
+           float(np.abs(np.asarray(f) - out["forces"]).max()) if len(out["forces"]) else 0.0,
+           float(np.abs(np.asarray(w) - out["virial"]).max()),
+           float(np.abs(out["virial"]).max()))
+    MARGINS.append(row)
+    return row
+
 
 
 def perturbed_model(path, seed=11, scale=0.2, base=MODEL):
@@ -434,6 +454,24 @@ def read_lammps_data(path):
     pos = np.array([[a[2], a[3], a[4]] for a in atoms])
     types = np.array([a[1] for a in atoms])
     return pos, types, lo, hi
+
+
+def read_molecule(name):
+    """(z, positions) of tests/golden/molecules/<name>.data, the element of
+    each type read from its mass in the Masses section."""
+    from so3lrxlammps_amd.systems import MASS
+    path = os.path.join(GOLDEN, "molecules", name + ".data")
+    lines = [l.split("#")[0].strip() for l in open(path)]
+    k = lines.index("Masses") + 1
+    while not lines[k]:
+        k += 1
+    type_z = {}
+    while lines[k]:
+        t, mass = lines[k].split()[:2]
+        type_z[int(t)] = min(MASS, key=lambda zz: abs(MASS[zz] - float(mass)))
+        k += 1
+    pos, types, _, _ = read_lammps_data(path)
+    return np.array([type_z[int(t)] for t in types], dtype=np.int64), pos
 
 
 def build_graphs(pos, box=None, rc_sr=4.5, rc_lr=12.0):
