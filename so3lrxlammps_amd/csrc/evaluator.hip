@@ -2641,6 +2641,8 @@ Evaluator::~Evaluator() {
   if (stream_) (void)hipStreamSynchronize(stream_);
   drop_graph();
   if (host_out_) (void)hipHostFree(host_out_);
+  for (Pinned *b : {&pin_x_, &pin_f_})
+    if (b->p) (void)hipHostFree(b->p);
   release_all();
   if (own_stream_) (void)hipStreamDestroy(own_stream_);
 }
@@ -2985,6 +2987,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   nb_key_ = buf("nb_key"); nb_idx_ = buf("nb_idx"); nb_skey_ = buf("nb_skey"); nb_sidx_ = buf("nb_sidx");
   nb_cstart_ = buf("nb_cstart"); nb_tmp_ = buf("nb_tmp"); nb_srcnt_ = buf("nb_srcnt"); nb_lrcnt_ = buf("nb_lrcnt");
   nb_err_ = buf("nb_err"); nb_srlist_ = buf("nb_srlist"); nb_poff_ = buf("nb_poff"); sr_code_ = buf("sr_code");
+  nb_tot_ = buf("nb_tot");
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
   iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part"); probe_ = buf("probe");
   top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
@@ -3057,20 +3060,49 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
   evaluated_ = false;
 }
 
+double *Evaluator::pinned(Pinned &b, std::size_t count) {
+  if (b.count < count) {
+    if (b.p) HIP_CHECK(hipHostFree(b.p));
+    b.p = nullptr;
+    b.count = 0;
+    const std::size_t cap = count + count / 8;
+    HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&b.p), cap * sizeof(double), hipHostMallocDefault));
+    b.count = cap;
+  }
+  return b.p;
+}
+
 void Evaluator::compute_host(const double *x_rows, int flags, double *f, double *eatom, double *energy,
                              double *virial) {
   if (!topology_ready_) throw std::logic_error("SO3LR: compute called before set_topology");
   if (shift_mode_)
     throw std::logic_error("SO3LR: the topology came from so3lr_reneighbor_device; call so3lr_compute_device "
                            "with owned positions");
-  double *xd = ensure<double>(xrows_, std::size_t(n_rows_) * 3);
-  HIP_CHECK(hipMemcpyAsync(xd, x_rows, std::size_t(n_rows_) * 3 * sizeof(double), hipMemcpyHostToDevice, stream_));
-  double *fd = ensure<double>(fhost_, std::size_t(n_) * 4);
+  const std::size_t nx = std::size_t(n_rows_) * 3, n = std::size_t(n_);
+  double *xd = ensure<double>(xrows_, nx);
+  double *fd = ensure<double>(fhost_, n * 4);
+  double *px = pinned(pin_x_, nx), *pf = pinned(pin_f_, n * 4);
+  // positions in: copied into pinned memory slice by slice, each slice's DMA
+  // running while the next slice is copied (the stream is idle here: every
+  // evaluation ends waiting for it)
+  constexpr std::size_t kSlice = std::size_t(1) << 16;  // doubles, 512 KiB
+  for (std::size_t a = 0; a < nx; a += kSlice) {
+    const std::size_t c = std::min(kSlice, nx - a);
+    std::memcpy(px + a, x_rows + a, c * sizeof(double));
+    HIP_CHECK(hipMemcpyAsync(xd + a, px + a, c * sizeof(double), hipMemcpyHostToDevice, stream_));
+  }
+  // forces (and per-atom energies, which follow them in fd) out: one copy to
+  // pinned memory, enqueued by the evaluation ahead of its one wait
+  struct StageReset {
+    Evaluator *e;
+    ~StageReset() { e->stage_count_ = 0; }
+  } stage_reset{this};
+  stage_src_ = fd;
+  stage_dst_ = pf;
+  stage_count_ = n * ((flags & 2) ? 4 : 3);
   compute_device(xd, flags, fd, (flags & 2) ? fd + 3 * n_ : nullptr, energy, virial);
-  if (f) HIP_CHECK(hipMemcpyAsync(f, fd, std::size_t(n_) * 3 * sizeof(double), hipMemcpyDeviceToHost, stream_));
-  if (eatom && (flags & 2))
-    HIP_CHECK(hipMemcpyAsync(eatom, fd + 3 * n_, std::size_t(n_) * sizeof(double), hipMemcpyDeviceToHost, stream_));
-  HIP_CHECK(hipStreamSynchronize(stream_));
+  if (f) std::memcpy(f, pf, n * 3 * sizeof(double));
+  if (eatom && (flags & 2)) std::memcpy(eatom, pf + 3 * n, n * sizeof(double));
 }
 
 namespace {
@@ -3612,6 +3644,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     enqueue();
   }
   if (!from_scratch) last_key_ = key;
+  if (stage_count_)  // compute_host's read-back, ahead of the one wait
+    HIP_CHECK(hipMemcpyAsync(stage_dst_, stage_src_, stage_count_ * sizeof(double), hipMemcpyDeviceToHost, s));
   HIP_CHECK(hipStreamSynchronize(s));
   const double *host_red = host_out_;
   const std::int64_t host_nact = std::int64_t(host_out_[9]);

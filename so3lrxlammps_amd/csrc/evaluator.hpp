@@ -244,7 +244,7 @@ class Evaluator {
   Buffer *xrows_, *fhost_, *vatom_;
   // device reneighbor
   Buffer *nb_key_, *nb_idx_, *nb_skey_, *nb_sidx_, *nb_cstart_, *nb_tmp_, *nb_srcnt_, *nb_lrcnt_, *nb_err_,
-      *nb_srlist_, *nb_poff_, *sr_code_;
+      *nb_srlist_, *nb_poff_, *sr_code_, *nb_tot_;
   // spatial node order (device reneighbor, or the LAMMPS-list path after its
   // first evaluation): node n holds owned atom perm[n]; node-ordered copies
   // of the per-atom inputs (xn_: positions, device reneighbor path only)
@@ -293,6 +293,19 @@ class Evaluator {
   GraphKey graph_key_{}, last_key_{};
   std::uint64_t topo_version_ = 1, alloc_epoch_ = 0;
   double *host_out_ = nullptr;  // pinned: energy, virial, totals, active-pair count
+  // compute_host's staging: pinned host buffers the library owns (positions
+  // in; forces and per-atom energies out), grown as needed
+  struct Pinned {
+    double *p = nullptr;
+    std::size_t count = 0;
+  };
+  Pinned pin_x_, pin_f_;
+  double *pinned(Pinned &b, std::size_t count);
+  // a device -> pinned copy that compute_impl enqueues after the evaluation's
+  // kernels and before its one wait (compute_host's forces and energies)
+  const double *stage_src_ = nullptr;
+  double *stage_dst_ = nullptr;
+  std::size_t stage_count_ = 0;
   void drop_graph();
   std::map<std::string, Timing> timings_;
   double *last_etot_ = nullptr;
