@@ -124,9 +124,10 @@ def kernel_work(widths):
 
 def cpu_baseline(z, x, box, periodic, images, seconds_budget):
     """Oracle (CPU restatement of the reference math, OpenMP) timed on the
-    host cores: repeated E+F+virial calls on a bounded sample of the same
-    workload until about `seconds_budget` seconds of CPU work are done;
-    reports the median call as atom-steps/s."""
+    host cores: for a periodic configuration the whole system, the median of
+    5 E+F+virial calls after 2 warm-ups; otherwise repeated calls on a
+    bounded sample until about `seconds_budget` seconds of CPU work are
+    done.  Reports the median call as atom-steps/s."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
     from oracle.oracle import Oracle, lib
     import support
@@ -146,22 +147,26 @@ def cpu_baseline(z, x, box, periodic, images, seconds_budget):
         sr, lr = support.build_graphs(xs, None)
         what = "the whole molecule (open boundaries)"
     else:
-        # every atom of a 40 A cube cut from the system, treated as periodic
-        # with that side (wider than twice the 12 A LR cutoff)
-        side = 40.0
-        sel = np.all(x < side, axis=1)
-        zs, xs = z[sel], x[sel]
-        sr, lr = support.build_graphs(xs, np.full(3, side))
-        what = "a %.0f A periodic sub-cube of the benchmark system" % side
-        if int(np.sum(zs)) % 2:
-            kw = dict(multiplicity=2.0)  # a cut that leaves an odd electron count
-    orc.evaluate(zs, sr, lr, **kw)  # warm-up (page-in, thread pool)
+        # the whole periodic system, its graphs from the LAMMPS stand-in's
+        # lists: the median of 5 calls after 2 warm-ups
+        from so3lrxlammps_amd import Lists
+        zs, xs = z, x
+        sr, lr = support.graphs_from_lists(Lists(xs, np.zeros(3), box, periodic), xs)
+        what = "the whole periodic benchmark system"
     times = []
-    t_start = time.time()
-    while len(times) < 3 or (time.time() - t_start < seconds_budget and len(times) < 1000):
-        t0 = time.time()
-        orc.evaluate(zs, sr, lr, **kw)
-        times.append(time.time() - t0)
+    if any(periodic):
+        for k in range(7):
+            t0 = time.time()
+            orc.evaluate(zs, sr, lr, **kw)
+            if k >= 2:
+                times.append(time.time() - t0)
+    else:
+        orc.evaluate(zs, sr, lr, **kw)  # warm-up (page-in, thread pool)
+        t_start = time.time()
+        while len(times) < 3 or (time.time() - t_start < seconds_budget and len(times) < 1000):
+            t0 = time.time()
+            orc.evaluate(zs, sr, lr, **kw)
+            times.append(time.time() - t0)
     med = float(np.median(times))
     out = {"value": len(zs) / med, "unit": "atom-steps/s", "cores": int(lib().orc_num_threads()),
            "kind": "port",
@@ -373,14 +378,28 @@ def rows_path(z, x, box, Q, M, periodic, steps, warmup):
     return out
 
 
-def capacity(steps, warmup, stream):
-    """Config 4 (150,000 atoms) NPT on the device path: throughput, HBM in use
-    (hipMemGetInfo) and the library's bytes per atom."""
+def tiled(z, x, box, tile):
+    """The periodic cell repeated tile = (a, b, c) times along its axes: a
+    larger periodic system with the same local structure."""
+    a, b, c = tile
+    shifts = np.array([[i, j, k] for i in range(a) for j in range(b) for k in range(c)], float) * box
+    xs = (x[None, :, :] + shifts[:, None, :]).reshape(-1, 3)
+    return np.tile(z, len(shifts)), xs, box * np.array(tile, float)
+
+
+def capacity(steps, warmup, stream, tile=(1, 1, 1)):
+    """Config 4 (150,000 atoms; with `tile`, that cell repeated) NPT on the
+    device path: throughput, HBM in use (hipMemGetInfo) and the library's
+    bytes per atom."""
     import torch
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     free0, total = torch.cuda.mem_get_info()
     z, x, box, Q, M, images, periodic, desc = load_config(4)
+    if tuple(tile) != (1, 1, 1):
+        z, x, box = tiled(z, x, box, tile)
+        desc = "config 4 cell repeated %dx%dx%d: %d H2O, %.1f x %.1f x %.1f A, periodic" % (
+            tuple(tile) + (len(z) // 3,) + tuple(box))
     md = DeviceMD(4, z, x, box, Q, M, images, periodic, stream)
     elapsed, builds, _ = md.run(warmup, steps)
     free1, _ = torch.cuda.mem_get_info()
@@ -388,7 +407,7 @@ def capacity(steps, warmup, stream):
     dev_bytes = md.ctx.device_bytes()
     used = total - free1
     used_by_run = free0 - free1
-    out = {"workload": "config 4: " + desc, "atoms": n, "steps": steps,
+    out = {"workload": ("config 4: " if tuple(tile) == (1, 1, 1) else "") + desc, "atoms": n, "steps": steps,
            "ms_per_step": 1e3 * elapsed / steps, "atom_steps_per_s": n * steps / elapsed,
            "hbm_used_bytes": int(used), "hbm_used_by_this_run_bytes": int(used_by_run),
            "hbm_total_bytes": int(total), "device_bytes": int(dev_bytes),
@@ -433,6 +452,9 @@ def main():
     ap.add_argument("--rows-steps", type=int, default=0, help="rows-path steps (default: --steps)")
     ap.add_argument("--no-capacity", action="store_true")
     ap.add_argument("--capacity-steps", type=int, default=5)
+    ap.add_argument("--capacity-tiles", default="1x1x1",
+                    help="comma-separated repeats of the config-4 cell for the capacity block, e.g. "
+                         "1x1x1,1x2x2,2x2x2 (a memory-vs-size curve; the first is the reported block)")
     ap.add_argument("--roofline-steps", type=int, default=10,
                     help="steps after the timed ones with per-kernel HIP events")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -544,8 +566,16 @@ def main():
         rows["library_fraction_of_device_path"] = rows["library_value"] / value
     cap = None
     if not args.no_capacity and args.config != 4:
-        log("capacity: config 4")
-        cap = capacity(args.capacity_steps, 2, stream)
+        tiles = [tuple(int(v) for v in t.split("x")) for t in args.capacity_tiles.split(",")]
+        curve = []
+        for tile in tiles:
+            log("capacity: config 4 cell x %s" % "x".join(map(str, tile)))
+            curve.append(capacity(args.capacity_steps, 2, stream, tile))
+        cap = curve[0]
+        if len(curve) > 1:
+            cap["curve"] = [{k: c[k] for k in ("workload", "atoms", "ms_per_step", "atom_steps_per_s",
+                                               "hbm_used_bytes", "hbm_used_by_this_run_bytes", "device_bytes",
+                                               "device_bytes_per_atom")} for c in curve]
 
     cpu = None
     if not args.no_cpu_baseline:

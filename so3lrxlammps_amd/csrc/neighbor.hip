@@ -44,6 +44,13 @@ namespace so3lr_amd {
 
 namespace {
 
+// Entries of both candidate lists together (short and long range, each pair
+// in both directions) that a device reneighbor accepts: list entries,
+// incidence slots and their offsets are ints.  Water at 1 g/cm^3 with a 1 A
+// skin holds about 990 entries per atom, so the limit is near 2.1 million
+// atoms, above what 288 GB of HBM holds at the evaluation's ~200 KB per atom.
+constexpr long long kMaxListEntries = (1LL << 31) - 2;
+
 struct Grid {
   double lo[3], len[3];
   int nc[3];
@@ -154,10 +161,14 @@ __global__ __launch_bounds__(256) void k_nbr(int n, const double *x, Grid G, con
   }
 }
 
-// exclusive scan of counts[0..n) into off[0..n] (one block, deterministic)
-__global__ __launch_bounds__(1024) void k_scan_int(int n, const int *cnt, int *off) {
+// exclusive scan of counts[0..n) into off[0..n] (one block, deterministic).
+// The running total is carried in 64 bits and written to *total: the int
+// offsets are valid only while it stays below 2^31, which the host checks
+// before it reads or uses them.  A 1024-count tile sums in int (each count
+// is one atom's neighbours: far below 2^21).
+__global__ __launch_bounds__(1024) void k_scan_int(int n, const int *cnt, int *off, long long *total) {
   __shared__ int buf[1024];
-  __shared__ int carry;
+  __shared__ long long carry;
   if (threadIdx.x == 0) carry = 0;
   __syncthreads();
   for (int start = 0; start < n; start += 1024) {
@@ -171,12 +182,15 @@ __global__ __launch_bounds__(1024) void k_scan_int(int n, const int *cnt, int *o
       buf[threadIdx.x] += t;
       __syncthreads();
     }
-    if (i < n) off[i] = carry + buf[threadIdx.x] - v;
+    if (i < n) off[i] = int(carry + buf[threadIdx.x] - v);
     __syncthreads();
     if (threadIdx.x == 1023) carry += buf[1023];
     __syncthreads();
   }
-  if (threadIdx.x == 0) off[n] = carry;
+  if (threadIdx.x == 0) {
+    off[n] = int(carry);
+    *total = carry;
+  }
 }
 
 // canonical SR entries (i < j) per atom
@@ -302,14 +316,19 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   hipLaunchKernelGGL(k_nbr<false>, dim3(gw), dim3(256), 0, s, n, x, G, cstart, sidx, sr2, lr2, sr_cnt, lr_cnt,
                      nullptr, nullptr, nullptr, nullptr, err);
   int *sr_off = ensure<int>(sr_inc_off_, n + 1), *lr_off = ensure<int>(lr_inc_off_, n + 1);
-  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, sr_cnt, sr_off);
-  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, lr_cnt, lr_off);
-  int totals[2];
-  NB_CHECK(hipMemcpyAsync(&totals[0], sr_off + n, sizeof(int), hipMemcpyDeviceToHost, s));
-  NB_CHECK(hipMemcpyAsync(&totals[1], lr_off + n, sizeof(int), hipMemcpyDeviceToHost, s));
+  long long *tot = ensure<long long>(nb_tot_, 4);
+  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, sr_cnt, sr_off, tot);
+  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, lr_cnt, lr_off, tot + 1);
+  long long tot64[2] = {0, 0};
+  NB_CHECK(hipMemcpyAsync(tot64, tot, sizeof(tot64), hipMemcpyDeviceToHost, s));
   NB_CHECK(hipStreamSynchronize(s));
-  if (std::int64_t(totals[0]) + totals[1] >= (std::int64_t(1) << 31) - 1)
-    throw std::length_error("SO3LR: neighbour lists exceed 2^31 entries");
+  // the 64-bit totals decide before any int offset is read: every list entry
+  // and incidence slot is addressed by an int
+  if (tot64[0] + tot64[1] > kMaxListEntries)
+    throw std::length_error("SO3LR: the neighbour lists of " + std::to_string(n) + " atoms hold " +
+                            std::to_string(tot64[0] + tot64[1]) + " entries (short + long range); the limit is " +
+                            std::to_string(kMaxListEntries) + " (about 2.1 million atoms of water)");
+  const int totals[2] = {int(tot64[0]), int(tot64[1])};
   int *sr_list = ensure<int>(nb_srlist_, totals[0]);
   int *lr_list = ensure<int>(lr_inc_, totals[1]);
   hipLaunchKernelGGL(k_nbr<true>, dim3(gw), dim3(256), 0, s, n, x, G, cstart, sidx, sr2, lr2, nullptr, nullptr,
@@ -317,7 +336,7 @@ void Evaluator::build_topology_device(double *x, const double lo[3], const doubl
   // half-pair table of the SR list
   hipLaunchKernelGGL(k_canon_count, dim3((n + 255) / 256), dim3(256), 0, s, n, sr_off, sr_list, sr_cnt);
   int *poff = ensure<int>(nb_poff_, n + 1);
-  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, sr_cnt, poff);
+  hipLaunchKernelGGL(k_scan_int, dim3(1), dim3(1024), 0, s, n, sr_cnt, poff, tot + 2);  // at most totals[0]
   int npairs = 0, herr = 0;
   NB_CHECK(hipMemcpyAsync(&npairs, poff + n, sizeof(int), hipMemcpyDeviceToHost, s));
   NB_CHECK(hipStreamSynchronize(s));

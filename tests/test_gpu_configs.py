@@ -204,3 +204,30 @@ def test_config4_full_size(orc):
     e, f, w, ea = _device_eval(c, x, np.zeros(3), box, (1, 1, 1), eatom=True)
     _check(e, f, w, out)
     assert np.abs(ea - out["eatom"]).max() <= 1e-10
+
+
+def test_device_reneighbor_refuses_lists_past_int_range():
+    """The device reneighbor counts each atom's candidates, scans the counts
+    into int offsets and carries the total in 64 bits; past 2^31 - 2 entries
+    (short and long range together) it refuses before any int offset is
+    read.  40,000 hydrogen atoms in an 8 A cube: every pair is a long-range
+    candidate (1.6e9 entries, both directions) and most are short-range ones,
+    together above 2^31."""
+    import torch
+    from so3lrxlammps_amd import Context, _lib
+    n = 40000
+    rng = np.random.default_rng(7)
+    x = rng.uniform(0.0, 8.0, (n, 3))
+    c = Context(support.MODEL, 0)
+    c.set_system(np.ones(n, dtype=np.int64), 0, 1)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    print("capacity: %d atoms in an 8 A cube, expect a refusal" % n, flush=True)
+    with torch.cuda.stream(stream):
+        xt = torch.tensor(x, dtype=torch.float64, device=dev)
+        with pytest.raises(_lib.SO3LRError) as err:
+            c.reneighbor_device(xt, np.full(3, -10.0), np.full(3, 20.0), (0, 0, 0), 1.0, stream=stream.cuda_stream)
+        stream.synchronize()
+    print("  refused:", err.value, flush=True)
+    assert err.value.code == _lib.ERR_TOPOLOGY and "the limit is 2147483646" in str(err.value)
+    c.close()
