@@ -59,12 +59,19 @@ _FILTER = 2 * 2 * _mac((128, 32), (128, 128), (32, 4), (128, 32))   # 98,816 flo
 _FILTER_B0 = 2 * 2 * _mac((128, 32), (128, 128))                     # 81,920: ev = 0 in block 0
 _FILTER_BWD_ISSUED = _FILTER + 2 * 2 * _mac((128, 32), (32, 4))      # + layer-0 recompute: 115,712
 _FILTER_BWD_B0_ISSUED = _FILTER_B0 + 2 * 2 * _mac((128, 32))         # 98,304
+# block 0 through element-pair tables: W0 (128x32) and 8 table rows of 128
+# (4 heads x 2 directions) per filter; the reverse recomputes W0's output
+_FILTER_B0_TAB = 2 * 2 * _mac((128, 32), (8, 128))                    # 20,480
+_FILTER_BWD_B0_TAB_ISSUED = _FILTER_B0_TAB + 2 * 2 * _mac((128, 32))  # 36,864
 KERNEL_WORK = {
     # name: (kernel symbol, bound, algorithmic per unit, issued per unit, unit)
     "filter_fwd": ("k_filter_fwd_mfma<false>", "mfma", _FILTER, _FILTER, "pair"),
     "filter_fwd_block0": ("k_filter_fwd_mfma<true>", "mfma", _FILTER_B0, _FILTER_B0, "pair"),
     "filter_bwd": ("k_filter_bwd_mfma<false, false>", "mfma", _FILTER, _FILTER_BWD_ISSUED, "pair"),
     "filter_bwd_block0": ("k_filter_bwd_mfma<true, false>", "mfma", _FILTER_B0, _FILTER_BWD_B0_ISSUED, "pair"),
+    "filter_fwd_block0_tables": ("k_filter_fwd_class", "mfma", _FILTER_B0_TAB, _FILTER_B0_TAB, "pair"),
+    "filter_bwd_block0_tables": ("k_filter_bwd_class<false>", "mfma", _FILTER_B0_TAB, _FILTER_BWD_B0_TAB_ISSUED,
+                                 "pair"),
 }
 
 
@@ -508,7 +515,8 @@ def main():
     md.ctx.kernel_timing(False)
     timing = {}
     work = kernel_work(model_widths(MODEL))
-    for name in ("filter_fwd", "filter_fwd_block0", "filter_bwd", "filter_bwd_block0", "attn_fwd", "attn_bwd",
+    for name in ("filter_fwd", "filter_fwd_block0", "filter_fwd_block0_tables", "filter_bwd", "filter_bwd_block0",
+                 "filter_bwd_block0_tables", "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd", "generic_alpha",
                  "generic_attn_bwd_pairs"):
         try:

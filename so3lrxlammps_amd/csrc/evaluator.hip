@@ -1208,6 +1208,398 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
   }
 }
 
+// ---------------------------------------------------------------- block 0 through element-pair tables
+// Block 0's node rows (q, k, v, q_ev, k_ev) are projections of the embedding
+// x0, which in a one-image system is a function of the atomic number alone
+// (x0[i] = (emb[z_i] + charge/spin table[z_i]) / scale): the rows take one
+// value per element present, its class.  Block 0 uses its filter outputs f
+// only inside the attention logits <q_a (.) k_b, f>_h, with
+// f = W1 silu(W0 rbf + b0) + ob1 (the ev = 0 spherical branch folded into
+// ob1).  With the element-pair tables, for filter w, classes A, B, head h,
+//   M[w][A][B][h] = W1_w^T (q_A (.) k_B on the 32 channels of head h)   (128)
+//   c0[w][A][B][h] = <q_A (.) k_B, ob1_w>_h
+// a logit is <M[w][A][B][h], hidden> + c0[w][A][B][h], and the reverse's
+// W1^T df is sum_h s_in_h M[w][A][B][h] + s_out_h M[w][B][A][h]; the head
+// sums <gainv_a, v_b>_h are Gv[a][class(b)][h] (k_class_gv).  The W1 and E1
+// products (two thirds of block 0's filter MFMAs) and the node-row gathers
+// drop out.  Same algebra as k_filter_fwd_mfma<true> / k_filter_bwd_mfma<true,
+// .>, different rounding.
+//
+// Table rows hold the 128 hidden features in the MFMA register order: the
+// coefficient of feature f at tpos(f), so that a lane's four features of
+// tile t (16 t + g + 4 r) are the 32-byte vector at 16 t + 4 g.  The node
+// rows use the same order for their channels.
+constexpr int kMaxClasses = 16;
+__host__ __device__ constexpr int tpos(int c) { return 16 * (c / 16) + 4 * (c % 4) + (c % 16) / 4; }
+
+// rep[c] = the node that holds class c's first atom (rep0[c], caller's order);
+// also clears the class-pair histogram of k_cls_count (nkeys entries)
+__global__ void k_class_reps(int n, const int *z, const int *cls, const int *perm, const int *rep0, int *rep,
+                             int nkeys, int *hist) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nkeys) hist[i] = 0;
+  if (i >= n) return;
+  const int c = cls[z[i]];
+  if ((perm ? perm[i] : i) == rep0[c]) rep[c] = i;
+}
+
+// One block per (A, B) and (w, h); thread f = hidden feature.
+__global__ __launch_bounds__(128) void k_class_tables(int C, const double *__restrict__ qkv, const int *rep,
+                                                      const double *__restrict__ w1_0,
+                                                      const double *__restrict__ w1_1,
+                                                      const double *__restrict__ ob_0,
+                                                      const double *__restrict__ ob_1, double *Mt, double *c0) {
+  const int A = blockIdx.x / C, B = blockIdx.x % C, w = blockIdx.y / 4, h = blockIdx.y % 4;
+  const int f = threadIdx.x;
+  const double *W1 = w ? w1_1 : w1_0;  // (out, in)
+  const double *qa = qkv + std::size_t(rep[A]) * 640 + (w ? 384 : 0);
+  const double *kb = qkv + std::size_t(rep[B]) * 640 + (w ? 512 : 128);
+  __shared__ double qk[32];
+  if (f < 32) {
+    const int pc = tpos(32 * h + f);
+    qk[f] = qa[pc] * kb[pc];
+  }
+  __syncthreads();
+  const std::size_t row = ((std::size_t(w) * C + A) * C + B) * 4 + h;
+  double acc = 0.0;
+  for (int k = 0; k < 32; ++k) acc += W1[std::size_t(32 * h + k) * kF + f] * qk[k];
+  Mt[row * kF + tpos(f)] = acc;
+  if (f == 0) {
+    const double *ob = w ? ob_1 : ob_0;
+    double s = 0.0;
+    for (int k = 0; k < 32; ++k) s += ob[32 * h + k] * qk[k];
+    c0[row] = s;
+  }
+}
+
+// Gv[a][B][h] = <gainv_a, v_B>_h: positions 32 h .. 32 h + 31 of both rows
+// (one head's two tiles).  One thread per (a, B, h).
+__global__ void k_class_gv(int n, int C, const double *__restrict__ gainv, const double *__restrict__ qkv,
+                           const int *rep, double *Gv) {
+  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= std::size_t(n) * C * 4) return;
+  const int h = int(t % 4), B = int((t / 4) % C);
+  const std::size_t a = t / (4 * std::size_t(C));
+  const double *ga = gainv + a * kF + 32 * h;
+  const double *v = qkv + std::size_t(rep[B]) * 640 + 256 + 32 * h;
+  double s = 0.0;
+#pragma unroll 8
+  for (int k = 0; k < 32; ++k) s += ga[k] * v[k];
+  Gv[t] = s;
+}
+
+// A lane's 32 bytes of a table row through buffer loads: the lane's row
+// start in a vector offset, the row and tile part (the same for every lane)
+// in a scalar offset, so the 64 rows of a filter need no vector addresses.
+// The offset passes through an empty asm, which keeps the compiler from
+// hoisting every row's load to the start of the section (the rows' uses
+// carry no MFMA dependence that would hold them in their stream slots).
+__device__ __forceinline__ v4d table_load(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  asm volatile("" : "+v"(voff));
+  const v4u x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+  const v4u y = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16, soff, 0);
+  return v4d{u2_to_f64(x[0], x[1]), u2_to_f64(x[2], x[3]), u2_to_f64(y[0], y[1]), u2_to_f64(y[2], y[3])};
+}
+
+// The active pairs in order of their element pair {min, max} (key
+// min * C + max), for the table kernels: a wavefront's 16 pairs then read the
+// same table rows, which the vector L1 serves once.  A counting sort: counts
+// (k_cls_count), bucket starts (k_cls_scan), placement (k_cls_place).  Within
+// a bucket the order depends on the atomics' timing; every pair's results go
+// to its own slots, so the kernels' outputs do not.
+__device__ __forceinline__ int cls_key(int ca, int cb, int C) { return ca < cb ? ca * C + cb : cb * C + ca; }
+
+__global__ __launch_bounds__(256) void k_cls_count(const int *n_active, const int *pa, const int *z, const int *cls,
+                                                   int C, int *hist) {
+  __shared__ int lc[kMaxClasses * kMaxClasses];
+  const int nact = *n_active;
+  if (int(blockIdx.x) * 256 >= nact) return;  // the whole block
+  for (int t = threadIdx.x; t < C * C; t += 256) lc[t] = 0;
+  __syncthreads();
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p < nact) atomicAdd(&lc[cls_key(cls[z[pa[2 * p]]], cls[z[pa[2 * p + 1]]], C)], 1);
+  __syncthreads();
+  for (int t = threadIdx.x; t < C * C; t += 256)
+    if (lc[t]) atomicAdd(&hist[t], lc[t]);
+}
+
+__global__ void k_cls_scan(int nkeys, const int *hist, int *cursor) {
+  if (threadIdx.x != 0) return;
+  int run = 0;
+  for (int t = 0; t < nkeys; ++t) {
+    cursor[t] = run;
+    run += hist[t];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_cls_place(const int *n_active, const int *pa, const int *z, const int *cls,
+                                                   int C, int *cursor, int *order) {
+  __shared__ int lc[kMaxClasses * kMaxClasses], lb[kMaxClasses * kMaxClasses];
+  const int nact = *n_active;
+  if (int(blockIdx.x) * 256 >= nact) return;
+  for (int t = threadIdx.x; t < C * C; t += 256) lc[t] = 0;
+  __syncthreads();
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  int key = 0, rank = 0;
+  if (p < nact) {
+    key = cls_key(cls[z[pa[2 * p]]], cls[z[pa[2 * p + 1]]], C);
+    rank = atomicAdd(&lc[key], 1);
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < C * C; t += 256) lb[t] = lc[t] ? atomicAdd(&cursor[t], lc[t]) : 0;
+  __syncthreads();
+  if (p < nact) order[lb[key] + rank] = p;
+}
+
+__device__ __forceinline__ double pick4(double a0, double a1, double a2, double a3, int g) {
+  return g == 0 ? a0 : (g == 1 ? a1 : (g == 2 ? a2 : a3));
+}
+
+// Block 0's forward filter through the tables: per filter the stream holds
+// the layer-0 bias tiles (8), W0 (16: tile s % 8, K chunk s / 8), the table
+// rows of both directions (64: direction, head, tile; the lane's four
+// features of each) and the two c0 vectors (heads 0..3).  Writes the logits
+// (palpha) of both directions and filters, as k_filter_fwd_mfma<true>.
+__global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_class(
+    const int *n_active, const int *order, const int *pa, const double *pr, const int *__restrict__ z,
+    const int *__restrict__ cls, int C, const double *__restrict__ Mt, const double *__restrict__ c0, double inv_avg,
+    FilterMfma A, double *palpha) {
+  SO3LR_EXP2_TABLE(A)
+  const int nact = *n_active;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int blk = xcd_block_active((nact + 63) / 64);
+  if (blk < 0) return;
+  const int wave = blk * 4 + (threadIdx.x >> 6);
+  if (wave * 16 >= nact) return;
+  // slot q of the element-pair order holds pair p
+  const int q = wave * 16 + j;
+  const bool valid = q < nact;
+  const int p = order[valid ? q : nact - 1];
+  const int ca = cls[z[pa[2 * p]]], cb = cls[z[pa[2 * p + 1]]];
+  const int tw = C * C * 4 * kF * 8, cw = C * C * 4;  // one filter's tables (bytes; entries)
+  // direction 0 reads the rows of (lo, hi), direction 1 those of (hi, lo),
+  // the same in every lane of a bucket; with ca > cb direction 0 is b <- a
+  const bool sw = ca > cb;
+  const int lo = sw ? cb : ca, hi = sw ? ca : cb;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<double *>(Mt), 0, 0x7fffffff, 0x00020000);
+  const int vab = ((lo * C + hi) * 4 * kF + 4 * g) * 8, vba = ((hi * C + lo) * 4 * kF + 4 * g) * 8;
+  const double *cab = c0 + std::size_t(lo * C + hi) * 4, *cba = c0 + std::size_t(hi * C + lo) * 4;
+  constexpr int NF = 24 + 64 + 2;
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
+    if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
+    else if constexpr (s < 24) return wload(A.w0p[which], 2, (s - 8) % 8, (s - 8) / 8, lane);
+    else if constexpr (s < 88) {
+      constexpr int k = s - 24, dir = k / 32, hd = (k / 8) % 4, t = k % 8;
+      return table_load(rs, dir ? vba : vab, which * tw + (hd * kF + 16 * t) * 8);
+    } else {
+      return *reinterpret_cast<const v4d *>((s == 88 ? cab : cba) + which * cw);
+    }
+  };
+  Stream<2 * NF, SO3LR_FILTER_FWD0_PF, decltype(load)> st(load);
+  st.prime();
+
+  v4d rb[2];
+  rbf8(pr[p], g, A, exp2_lds, rb);
+  v4d h[8], cv0;
+  double acc[8];  // [direction * 4 + head]: this lane's part of the logits
+  st.run([&](auto si, const v4d &w) {
+    constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
+    if constexpr (s < 8) {
+      h[s] = w;
+    } else if constexpr (s < 24) {
+      constexpr int i = s - 8;
+      h[i % 8] = mfma4(w, rb[i / 8], h[i % 8]);
+    } else if constexpr (s < 88) {
+      constexpr int k = s - 24, dir = k / 32, hd = (k / 8) % 4, t = k % 8;
+      if constexpr (k < 8) {  // each hidden tile's SiLU at its first use
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[t][r] = silu_tab(h[t][r], exp2_lds);
+      }
+      const double d = ((w[0] * h[t][0] + w[1] * h[t][1]) + w[2] * h[t][2]) + w[3] * h[t][3];
+      if constexpr (t == 0) acc[dir * 4 + hd] = d;
+      else acc[dir * 4 + hd] += d;
+    } else if constexpr (s == 88) {
+      cv0 = w;
+    } else {
+      // sums over the four lane groups; lane group g writes head g
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        acc[q] += __shfl_xor(acc[q], 16, kWave);
+        acc[q] += __shfl_xor(acc[q], 32, kWave);
+      }
+      if (valid) {
+        const double d0 = (pick4(acc[0], acc[1], acc[2], acc[3], g) + pick4(cv0[0], cv0[1], cv0[2], cv0[3], g)) * inv_avg;
+        const double d1 = (pick4(acc[4], acc[5], acc[6], acc[7], g) + pick4(w[0], w[1], w[2], w[3], g)) * inv_avg;
+        double *al = palpha + 16 * std::size_t(p) + 4 * which;
+        al[g] = sw ? d1 : d0;  // a <- b
+        al[8 + g] = sw ? d0 : d1;  // b <- a
+      }
+    }
+  });
+}
+
+// Block 0's reverse filter through the tables (k_filter_bwd_mfma<true, FIRST>
+// with the df section replaced): per filter the stream holds the table rows
+// (64: direction, head, tile), then per tile the layer-0 bias and W0 chunks
+// (24: the pre-activation recomputed, d hidden *= silu'), then W0^T (16:
+// d rbf = W0^T d hidden).  The head sums of the invariant filter come from
+// Gv, those of the equivariant filter from <gev, Y> as in the full kernel.
+template <bool FIRST>
+__global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_class(
+    const int *n_active, const int *order, const int *pa, const double *pr, const double *pfc, const double *pY,
+    const double *palpha, const double *__restrict__ gaev, const int *__restrict__ z,
+    const int *__restrict__ cls, int C, const double *__restrict__ Mt, const double *__restrict__ Gv,
+    double inv_avg, FilterMfma A, double rc, double *dr, double *dY) {
+  SO3LR_EXP2_TABLE(A)
+  const int nact = *n_active;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int blk = xcd_block_active((nact + 63) / 64);
+  if (blk < 0) return;
+  const int wave = blk * 4 + (threadIdx.x >> 6);
+  if (wave * 16 >= nact) return;
+  // slot q of the element-pair order holds pair pp
+  const int q = wave * 16 + j;
+  const bool valid = q < nact;
+  const int pp = order[valid ? q : nact - 1];
+  const int a = pa[2 * pp], b = pa[2 * pp + 1];
+  const int ca = cls[z[a]], cb = cls[z[b]];
+  const int tw = C * C * 4 * kF * 8;  // one filter's tables, bytes
+  // direction 0 reads (lo, hi), direction 1 (hi, lo); with ca > cb direction
+  // 0 carries the b <- a coefficients
+  const bool sw = ca > cb;
+  const int lo = sw ? cb : ca, hi = sw ? ca : cb;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<double *>(Mt), 0, 0x7fffffff, 0x00020000);
+  const int vab = ((lo * C + hi) * 4 * kF + 4 * g) * 8, vba = ((hi * C + lo) * 4 * kF + 4 * g) * 8;
+  constexpr int NB = 64 + 24 + 16;
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, which = S / NB, s = S % NB;
+    if constexpr (s < 64) {
+      constexpr int dir = s / 32, hd = (s / 8) % 4, t = s % 8;
+      return table_load(rs, dir ? vba : vab, which * tw + (hd * kF + 16 * t) * 8);
+    } else if constexpr (s < 88) {
+      constexpr int mt = (s - 64) / 3, u = (s - 64) % 3;
+      if constexpr (u == 0) return tile_load(A.b0p[which], mt, lane);
+      else return wload(A.w0p[which], 2, mt, u - 1, lane);
+    } else {
+      constexpr int d = s - 88;
+      return wload(A.w0tp[which], 8, d % 2, d / 2, lane);
+    }
+  };
+  Stream<2 * NB, SO3LR_FILTER_BWD_PF, decltype(load)> st(load);
+  st.prime();
+
+  // the invariant filter's head sums: <gainv_a, v_b>_h and <gainv_b, v_a>_h
+  const v4d gin = *reinterpret_cast<const v4d *>(Gv + (std::size_t(a) * C + cb) * 4);
+  const v4d gout = *reinterpret_cast<const v4d *>(Gv + (std::size_t(b) * C + ca) * 4);
+  const double r = pr[pp];
+  const double fcs = pfc[pp] * inv_avg;  // fc / avg
+  const double *al = palpha + 16 * std::size_t(pp);
+  // equivariant pair terms: lane group g takes degree slot g, as in
+  // k_filter_bwd_mfma: its <gev_a, Y>, <gev_b, Y> and its share of dE/dY
+  double ce_mine = 0.0, coe_mine = 0.0;
+  {
+    const int lo = ev_offset(g), n_m = 2 * g + 3;
+    const double par = slot_parity(g);
+    const double ain_e = al[4 + g], aout_e = al[12 + g];
+    const double *gea = gaev + std::size_t(a) * kE, *geb = gaev + std::size_t(b) * kE;
+    const double *y = pY + kE * std::size_t(pp);
+    double *dy = dY + kE * std::size_t(pp);
+    const double fc = pfc[pp];
+    for (int k = 0; k < n_m; ++k) {
+      const int m = lo + k;
+      const double ea = gea[m], eb = geb[m], ym = y[m];
+      ce_mine += ea * ym;
+      coe_mine += eb * ym;
+      if (valid) dy[m] = (FIRST ? 0.0 : dy[m]) + fc * (ain_e * ea + par * aout_e * eb);
+    }
+    coe_mine *= par;
+  }
+  double dfc = al[4 + g] * ce_mine + al[12 + g] * coe_mine;
+  dfc += __shfl_xor(dfc, 16, kWave);
+  dfc += __shfl_xor(dfc, 32, kWave);
+#pragma unroll
+  for (int hd = 0; hd < 4; ++hd) dfc += al[hd] * gin[hd] + al[8 + hd] * gout[hd];
+  auto pin = [](double &v) { asm volatile("" : "+v"(v)); };
+  pin(dfc);
+
+  const v4d zero = v4d{0, 0, 0, 0};
+  // coefficients of the direction-0 and direction-1 rows
+  double s_in[4], s_out[4];
+#pragma unroll
+  for (int hd = 0; hd < 4; ++hd) {
+    s_in[hd] = fcs * (sw ? gout[hd] : gin[hd]);
+    s_out[hd] = fcs * (sw ? gin[hd] : gout[hd]);
+  }
+  v4d rb8[2], db8[2], dh[8], pre, prev, drb[2];
+  double part = 0.0;
+  st.run([&](auto si, const v4d &w) {
+    constexpr int S = decltype(si)::value, which = S / NB, s = S % NB;
+    if constexpr (which == 1 && s == 0) {
+      // the equivariant filter's head sums: slot h lives in lane group h
+#pragma unroll
+      for (int hd = 0; hd < 4; ++hd) {
+        const double ci = fcs * __shfl(ce_mine, j + 16 * hd, kWave);
+        const double co = fcs * __shfl(coe_mine, j + 16 * hd, kWave);
+        s_in[hd] = sw ? co : ci;
+        s_out[hd] = sw ? ci : co;
+      }
+    }
+    if constexpr (s < 64) {
+      constexpr int dir = s / 32, hd = (s / 8) % 4, t = s % 8;
+      const double c = dir ? s_out[hd] : s_in[hd];
+      if constexpr (s < 8) dh[t] = c * w;
+      else dh[t] += c * w;
+      // held here: sunk to its use, every row would stay live until then
+      asm volatile("" : "+v"(dh[t]));
+    } else if constexpr (s < 88) {
+      constexpr int mt = (s - 64) / 3, u = (s - 64) % 3;
+      if constexpr (s == 64) {
+        // an opaque copy per filter, as in k_filter_bwd_mfma
+        double rr = r;
+        int gg = g;
+        asm volatile("" : "+v"(rr), "+v"(gg));
+        rbf8_with_grad(rr, gg, A, exp2_lds, rb8, db8);
+      }
+      if constexpr (u == 0) {
+        pre = w;
+      } else {
+        pre = mfma4(w, rb8[u - 1], pre);
+        if constexpr (u == 1 && mt > 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dh[mt - 1][q] *= silu_prime_tab(prev[q], exp2_lds);
+        }
+        if constexpr (u == 2) prev = pre;
+      }
+    } else {
+      constexpr int d = s - 88;
+      if constexpr (d == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dh[7][q] *= silu_prime_tab(prev[q], exp2_lds);
+        drb[0] = zero;
+        drb[1] = zero;
+      }
+      drb[d % 2] = mfma4(w, dh[d / 2], drb[d % 2]);
+      if constexpr (d == 15) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) part += drb[t >> 2][t & 3] * db8[t >> 2][t & 3];
+        pin(part);
+      }
+    }
+  });
+
+  part += __shfl_xor(part, 16, kWave);
+  part += __shfl_xor(part, 32, kWave);
+  if (valid && g == 0) {
+    double grad = part;
+    if (r < rc) {
+      const double t = r / rc;
+      grad += dfc * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
+    }
+    dr[pp] += grad;
+  }
+}
+
 // ---------------------------------------------------------------- MFMA node GEMMs
 // out[n][o] = sum_k W[o][k] X[n][k] (+ epilogue), 16 nodes per wavefront as the
 // MFMA column block, output features as rows.  K is read from the node rows in
@@ -2714,6 +3106,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   if (const char *sp = std::getenv("SO3LR_SCALAR_FILTER_PAIRS")) scalar_pairs_max_ = std::atoll(sp);
   // SO3LR_NO_GRAPH=1: always launch the kernels one by one (no graph replay)
   if (const char *ng = std::getenv("SO3LR_NO_GRAPH")) use_graphs_ = ng[0] != '1';
+  if (const char *nc = std::getenv("SO3LR_NO_CLASS_TABLES")) class_tables_ = nc[0] != '1';
   HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_out_), 16 * sizeof(double), hipHostMallocDefault));
   scratch_dev_ = scratch_on_device(device);
   stream_ = own_stream_;
@@ -2814,6 +3207,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
         ob10[c] += acc;
       }
       B.ob1p0[k] = up(bias_acc(ob10, F));
+      B.ob10[k] = up(ob10);
       const auto e0p = permute_mfma(e0, FH, 4);  // two tiles, one value per lane each
       std::vector<double> e0pk(64 * 4, 0.0);
       for (int lane = 0; lane < 64; ++lane) {
@@ -2989,6 +3383,8 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   nb_err_ = buf("nb_err"); nb_srlist_ = buf("nb_srlist"); nb_poff_ = buf("nb_poff"); sr_code_ = buf("sr_code");
   nb_tot_ = buf("nb_tot");
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
+  cls_lut_ = buf("cls_lut"); cls_rep0_ = buf("cls_rep0"); cls_rep_ = buf("cls_rep"); cls_mt_ = buf("cls_mt");
+  cls_c0_ = buf("cls_c0"); cls_gv_ = buf("cls_gv"); cls_hist_ = buf("cls_hist"); cls_order_ = buf("cls_order");
   iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part"); probe_ = buf("probe");
   top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
   top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp"); top_box_ = buf("top_box");
@@ -3053,6 +3449,26 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
                            (ni + 1) * sizeof(std::int64_t), hipMemcpyHostToDevice, stream_));
   HIP_CHECK(hipMemcpyAsync(ensure<double>(img_q_, ni), charges.data(), ni * sizeof(double),
                            hipMemcpyHostToDevice, stream_));
+  // block 0's element classes: with one image x0 depends on z alone
+  n_cls_ = 0;
+  std::vector<int> lut(128, 0), rep0;
+  if (ni == 1) {
+    std::vector<int> seen(128, -1);
+    for (std::int64_t i = 0; i < n; ++i)
+      if (seen[z[i]] < 0) {
+        seen[z[i]] = int(rep0.size());
+        rep0.push_back(int(i));
+      }
+    if (int(rep0.size()) <= kMaxClasses) {
+      for (int zz = 0; zz < 128; ++zz) lut[zz] = std::max(seen[zz], 0);
+      rep0.resize(kMaxClasses, 0);
+      HIP_CHECK(hipMemcpyAsync(ensure<int>(cls_lut_, 128), lut.data(), 128 * sizeof(int), hipMemcpyHostToDevice,
+                               stream_));
+      HIP_CHECK(hipMemcpyAsync(ensure<int>(cls_rep0_, kMaxClasses), rep0.data(), kMaxClasses * sizeof(int),
+                               hipMemcpyHostToDevice, stream_));
+      n_cls_ = int(std::count_if(seen.begin(), seen.end(), [](int c) { return c >= 0; }));
+    }
+  }
   HIP_CHECK(hipStreamSynchronize(stream_));
   system_ready_ = true;
   topology_ready_ = false;
@@ -3240,6 +3656,11 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   double *pg = nullptr;
   int *iact = nullptr, *iother = nullptr;
   double *partial = nullptr;
+  // block 0 through element-pair tables (k_filter_fwd_class, k_filter_bwd_class)
+  const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
+  const int C = use_cls ? n_cls_ : 0;
+  int *crep = nullptr, *chist = nullptr, *ccur = nullptr, *cord = nullptr;
+  double *cmt = nullptr, *cc0 = nullptr, *cgv = nullptr;
   auto carve_all = [&] {
     if (!gen_) {
     xs = take<double>(xs_, (L + 1) * Nz * kF);
@@ -3274,6 +3695,15 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     dfc = take<double>(dfc_, Pa);
     psc = scalar ? nullptr : take<double>(psc_, 16 * Pa);
     ds = take<double>(ds_, 4 * Pa);
+    if (use_cls) {
+      crep = take<int>(cls_rep_, kMaxClasses);
+      chist = take<int>(cls_hist_, 2 * kMaxClasses * kMaxClasses);  // counts, then bucket cursors
+      ccur = chist + kMaxClasses * kMaxClasses;
+      cord = take<int>(cls_order_, Pa);
+      cmt = take<double>(cls_mt_, 2 * std::size_t(C) * C * 4 * kF);
+      cc0 = take<double>(cls_c0_, 2 * std::size_t(C) * C * 4);
+      cgv = take<double>(cls_gv_, Nz * C * 4);
+    }
     } else {
       gen_->carve(int(N), int(PA), [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
     }
@@ -3481,8 +3911,24 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     // to the full attention kernel
     // block 0 runs cheaper instantiations (ev = 0): timed under their own names
     const bool blk0 = b == 0 && !scalar;
-    timed(blk0 ? "filter_fwd_block0" : "filter_fwd", 0, [&] {
-      if (scalar)
+    if (blk0 && use_cls) {
+      // the element-pair tables of this evaluation's block-0 rows
+      // and the active pairs in element-pair order (used again by the reverse)
+      const int *lut = static_cast<const int *>(cls_lut_->p);
+      hipLaunchKernelGGL(k_class_reps, dim3(unsigned(ceil_div(std::max<std::int64_t>(N, C * C), 256))), dim3(256), 0, s,
+                         int(N), z, lut, perm, static_cast<const int *>(cls_rep0_->p), crep, C * C, chist);
+      hipLaunchKernelGGL(k_class_tables, dim3(unsigned(C * C), 8), dim3(128), 0, s, C, qb, crep, B.fw1[0], B.fw1[1],
+                         B.ob10[0], B.ob10[1], cmt, cc0);
+      const dim3 gsort(unsigned(ceil_div(PA, 256)));
+      hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, lut, C, chist);
+      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur);
+      hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, lut, C, ccur, cord);
+    }
+    timed(blk0 ? (use_cls ? "filter_fwd_block0_tables" : "filter_fwd_block0") : "filter_fwd", 0, [&] {
+      if (blk0 && use_cls)
+        hipLaunchKernelGGL(k_filter_fwd_class, dim3(gP64), dim3(256), 0, s, nact, cord, pa, pr, z,
+                           static_cast<const int *>(cls_lut_->p), C, cmt, cc0, inv_avg, FM, pab);
+      else if (scalar)
         hipLaunchKernelGGL(k_filter_fwd, dim3(gP), dim3(128), 0, s, nact, pa, pr, evb, A, psb, pfb);
       else if (b == 0)  // ev = 0: the spherical branch is a constant
         hipLaunchKernelGGL(k_filter_fwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
@@ -3578,15 +4024,29 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                                pfb, pY, pfc, pab, gainv, gaev, inv_avg, gqkv, psc, dfc, dY);
         });
       const FilterMfma FM = filter_mfma(B, hw_, gamma_);
-      timed(b == 0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
+      if (b == 0 && use_cls) {
+        hipLaunchKernelGGL(k_class_gv, dim3(unsigned((Nz * C * 4 + 255) / 256)), dim3(256), 0, s, int(N), C, gainv, qb,
+                           crep, cgv);
+        timed("filter_bwd_block0_tables", 0, [&] {
+          const int *lut = static_cast<const int *>(cls_lut_->p);
+          if (first)
+            hipLaunchKernelGGL(k_filter_bwd_class<true>, dim3(gP64), dim3(256), 0, s, nact, cord, pa, pr, pfc, pY, pab,
+                               gaev, z, lut, C, cmt, cgv, inv_avg, FM, rc_, dr, dY);
+          else
+            hipLaunchKernelGGL(k_filter_bwd_class<false>, dim3(gP64), dim3(256), 0, s, nact, cord, pa, pr, pfc, pY,
+                               pab, gaev, z, lut, C, cmt, cgv, inv_avg, FM, rc_, dr, dY);
+        });
+      } else {
+        timed(b == 0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
 #define SO3LR_FILTER_BWD(E0, FIRST)                                                                                \
   hipLaunchKernelGGL((k_filter_bwd_mfma<E0, FIRST>), dim3(gP64), dim3(256), 0, s, nact, pa, pr, psb, pfc, pY, pab,  \
                      qb, gainv, gaev, psc, dfc, inv_avg, FM, rc_, ds, dr, dY)
-        if (b == 0 && first) SO3LR_FILTER_BWD(true, true);
-        else if (b == 0) SO3LR_FILTER_BWD(true, false);
-        else SO3LR_FILTER_BWD(false, false);  // dE/dY of blocks after 0: the node-major reverse
+          if (b == 0 && first) SO3LR_FILTER_BWD(true, true);
+          else if (b == 0) SO3LR_FILTER_BWD(true, false);
+          else SO3LR_FILTER_BWD(false, false);  // dE/dY of blocks after 0: the node-major reverse
 #undef SO3LR_FILTER_BWD
-      });
+        });
+      }
     }
     // the adjoints of a block's inputs x_b, ev_b feed the block below; block
     // 0's inputs (the embedding and ev = 0) do not depend on the positions

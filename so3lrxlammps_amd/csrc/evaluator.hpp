@@ -57,6 +57,7 @@ struct BlockWeights {
   const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];  // reverse (transposes)
   const double *b0p[2], *eb0p[2], *ob1p[2];             // biases in accumulator order
   const double *ob1p0[2];                               // ob1p with the ev = 0 spherical branch folded in (block 0) (ob1 = b1 + eb1)
+  const double *ob10[2];                                // the same output bias in natural order (block 0's tables)
   const double *e0pk[2];                                // spherical layer 0, one v4d per lane
   // MFMA operand order of the node layers: forward and reverse (transpose)
   const double *qkvp, *qkvtp;           // per head (160 x 32) and (32 x 160)
@@ -272,6 +273,15 @@ class Evaluator {
   // (SO3LR_SCALAR_FILTER_PAIRS; 0 never).
   std::int64_t scalar_pairs_max_ = 256;
   bool scalar_now_ = false;
+  // Block 0 through element-pair tables (k_filter_fwd_class and
+  // k_filter_bwd_class): a one-image system of at most 16 elements, whose
+  // block-0 node rows depend on the element alone.  n_cls_ classes (0: the
+  // full block-0 kernels); cls_lut_[z] = class of atomic number z; cls_rep0_[c]
+  // = first atom of class c in the caller's order.  SO3LR_NO_CLASS_TABLES=1
+  // runs the full kernels.
+  int n_cls_ = 0;
+  bool class_tables_ = true;
+  Buffer *cls_lut_, *cls_rep0_, *cls_rep_, *cls_mt_, *cls_c0_, *cls_gv_, *cls_hist_, *cls_order_;
   // Graph replay of one evaluation: the launch sequence of compute_device is
   // captured when the same call (inputs, outputs, flags, box, stream,
   // topology and buffer addresses) comes twice in a row, and replayed while

@@ -363,6 +363,40 @@ def test_scalar_filter_path_matches_mfma(monkeypatch):
     assert np.abs(w1 - w2).max() <= 1e-10 * np.abs(w2).max()
 
 
+@pytest.mark.parametrize("name,q,m", [("water3000", 0, 1), ("alanine", 0, 1), ("acetate", -1, 1)])
+def test_block0_element_tables_match_full_kernels(monkeypatch, name, q, m):
+    """Block 0 through element-pair tables (the default for a one-image
+    system) against the full block-0 filter kernels (SO3LR_NO_CLASS_TABLES=1):
+    the same algebra summed in another order, so equal to rounding.  The
+    molecules take the MFMA path too (SO3LR_SCALAR_FILTER_PAIRS=0): 2, 4 and
+    3 elements."""
+    from so3lrxlammps_amd import Context, Lists
+    ref, z, pos, box = support.load_golden(name)
+    monkeypatch.setenv("SO3LR_SCALAR_FILTER_PAIRS", "0")
+    if box is None:
+        lo, hi, per = pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0)
+    else:
+        lo, hi, per = np.zeros(3), box, (1, 1, 1)
+    results = []
+    for off in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NO_CLASS_TABLES", off)
+        c = Context(support.MODEL, 0)
+        c.set_system(z, q, m)
+        lists = Lists(pos, lo, hi, per)
+        c.set_topology(lists)
+        e, f, ea, w = c.compute(lists.rows_positions(pos))
+        results.append((e, f.copy(), ea.copy(), w.copy(), c.vatom()))
+        c.close()
+    (e1, f1, ea1, w1, va1), (e2, f2, ea2, w2, va2) = results
+    print("%s: |dE| %.2e max|dF| %.2e max|dW| %.2e" % (name, abs(e1 - e2), np.abs(f1 - f2).max(),
+                                                       np.abs(w1 - w2).max()), flush=True)
+    assert abs(e1 - e2) <= 1e-13 * abs(e2)
+    assert np.abs(f1 - f2).max() <= 1e-11
+    assert np.abs(w1 - w2).max() <= 1e-11 * max(1.0, np.abs(w2).max())
+    assert np.abs(ea1 - ea2).max() <= 1e-12 * max(1.0, np.abs(ea2).max())
+    assert np.abs(va1 - va2).max() <= 1e-11 * max(1.0, np.abs(va2).max())
+
+
 def test_graph_replay_matches_eager(monkeypatch):
     """Identical repeated calls replay a captured graph of the evaluation.
     Every replay -- with torch work, an evaluation under a different key, moved
