@@ -1243,8 +1243,17 @@ __global__ void k_class_reps(int n, const int *z, const int *cls, const int *per
   if ((perm ? perm[i] : i) == rep0[c]) rep[c] = i;
 }
 
-// One block per (A, B) and (w, h); thread f = hidden feature.
-__global__ __launch_bounds__(128) void k_class_tables(int C, const double *__restrict__ qkv, const int *rep,
+// Block 0's input rows of the classes (rep[c]'s row of x), for their q k v
+// rows (k_qkv_mfma on C rows): the only block-0 node rows the table path reads.
+__global__ void k_class_rows(int C, const int *rep, const double *__restrict__ x, double *__restrict__ xc) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= C * kF) return;
+  xc[t] = x[std::size_t(rep[t / kF]) * kF + t % kF];
+}
+
+// One block per (A, B) and (w, h); thread f = hidden feature.  qkv: the
+// classes' rows (k_class_rows).
+__global__ __launch_bounds__(128) void k_class_tables(int C, const double *__restrict__ qkv,
                                                       const double *__restrict__ w1_0,
                                                       const double *__restrict__ w1_1,
                                                       const double *__restrict__ ob_0,
@@ -1252,8 +1261,8 @@ __global__ __launch_bounds__(128) void k_class_tables(int C, const double *__res
   const int A = blockIdx.x / C, B = blockIdx.x % C, w = blockIdx.y / 4, h = blockIdx.y % 4;
   const int f = threadIdx.x;
   const double *W1 = w ? w1_1 : w1_0;  // (out, in)
-  const double *qa = qkv + std::size_t(rep[A]) * 640 + (w ? 384 : 0);
-  const double *kb = qkv + std::size_t(rep[B]) * 640 + (w ? 512 : 128);
+  const double *qa = qkv + std::size_t(A) * 640 + (w ? 384 : 0);
+  const double *kb = qkv + std::size_t(B) * 640 + (w ? 512 : 128);
   __shared__ double qk[32];
   if (f < 32) {
     const int pc = tpos(32 * h + f);
@@ -1273,15 +1282,15 @@ __global__ __launch_bounds__(128) void k_class_tables(int C, const double *__res
 }
 
 // Gv[a][B][h] = <gainv_a, v_B>_h: positions 32 h .. 32 h + 31 of both rows
-// (one head's two tiles).  One thread per (a, B, h).
+// (one head's two tiles).  One thread per (a, B, h); qkv: the classes' rows.
 __global__ void k_class_gv(int n, int C, const double *__restrict__ gainv, const double *__restrict__ qkv,
-                           const int *rep, double *Gv) {
+                           double *Gv) {
   const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= std::size_t(n) * C * 4) return;
   const int h = int(t % 4), B = int((t / 4) % C);
   const std::size_t a = t / (4 * std::size_t(C));
   const double *ga = gainv + a * kF + 32 * h;
-  const double *v = qkv + std::size_t(rep[B]) * 640 + 256 + 32 * h;
+  const double *v = qkv + std::size_t(B) * 640 + 256 + 32 * h;
   double s = 0.0;
 #pragma unroll 8
   for (int k = 0; k < 32; ++k) s += ga[k] * v[k];
@@ -1896,7 +1905,8 @@ __global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, con
                                                   const double *__restrict__ lnb, double eps, int lnmode,
                                                   double *__restrict__ n1, double *__restrict__ n1hat,
                                                   double *__restrict__ n1is, double *__restrict__ act,
-                                                  double *__restrict__ aev) {
+                                                  double *__restrict__ aev, const int *__restrict__ z,
+                                                  const int *__restrict__ cls) {
   const int lane = threadIdx.x & 63;
   const int n = xcd_block() * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -1910,7 +1920,8 @@ __global__ __launch_bounds__(256) void k_attn_msg(int N, const int *inc_off, con
   struct Terms { double d0, d1, de; };
   auto terms = [&](int e, int o) {
     const int p = e >> 1, side = e & 1;
-    const double2 vv = ld2(qkv + std::size_t(o) * 640 + 256 + p0);
+    // block 0 on the table path: qkv holds one row per element class
+    const double2 vv = ld2(qkv + std::size_t(cls ? cls[z[o]] : o) * 640 + 256 + p0);
     const double *al = palpha + 16 * std::size_t(p) + 8 * side;
     const double ai = al[h], ae = al[4 + h];
     const double fc = pfc[p];
@@ -3385,6 +3396,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
   cls_lut_ = buf("cls_lut"); cls_rep0_ = buf("cls_rep0"); cls_rep_ = buf("cls_rep"); cls_mt_ = buf("cls_mt");
   cls_c0_ = buf("cls_c0"); cls_gv_ = buf("cls_gv"); cls_hist_ = buf("cls_hist"); cls_order_ = buf("cls_order");
+  cls_rows_ = buf("cls_rows");
   iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part"); probe_ = buf("probe");
   top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
   top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp"); top_box_ = buf("top_box");
@@ -3660,7 +3672,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
   const int C = use_cls ? n_cls_ : 0;
   int *crep = nullptr, *chist = nullptr, *ccur = nullptr, *cord = nullptr;
-  double *cmt = nullptr, *cc0 = nullptr, *cgv = nullptr;
+  double *cmt = nullptr, *cc0 = nullptr, *cgv = nullptr, *cxr = nullptr, *cqkv = nullptr, *cqis = nullptr;
   auto carve_all = [&] {
     if (!gen_) {
     xs = take<double>(xs_, (L + 1) * Nz * kF);
@@ -3700,6 +3712,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       chist = take<int>(cls_hist_, 2 * kMaxClasses * kMaxClasses);  // counts, then bucket cursors
       ccur = chist + kMaxClasses * kMaxClasses;
       cord = take<int>(cls_order_, Pa);
+      // the classes' block-0 input rows, q k v rows and QK-norm factors
+      cxr = take<double>(cls_rows_, kMaxClasses * std::size_t(kF + 640 + 16));
+      cqkv = cxr + kMaxClasses * kF;
+      cqis = cqkv + kMaxClasses * 640;
       cmt = take<double>(cls_mt_, 2 * std::size_t(C) * C * 4 * kF);
       cc0 = take<double>(cls_c0_, 2 * std::size_t(C) * C * 4);
       cgv = take<double>(cls_gv_, Nz * C * 4);
@@ -3901,10 +3917,6 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       A.fe0[k] = B.fe0[k]; A.feb0[k] = B.feb0[k]; A.fe1t[k] = B.fe1t[k]; A.feb1[k] = B.feb1[k];
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
-    hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
-    if (qk_norm_)
-      hipLaunchKernelGGL(k_qk_norm, dim3(unsigned(ceil_div(16 * N, 256))), dim3(256), 0, s, int(N), qb,
-                         qkis + b * Nz * 16);
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     // the MFMA filter also forms the attention logits of both directions
     // from the filter tiles it holds; the scalar cross-check path leaves them
@@ -3912,17 +3924,27 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     // block 0 runs cheaper instantiations (ev = 0): timed under their own names
     const bool blk0 = b == 0 && !scalar;
     if (blk0 && use_cls) {
-      // the element-pair tables of this evaluation's block-0 rows
-      // and the active pairs in element-pair order (used again by the reverse)
+      // block 0's q k v rows of the element classes only, the element-pair
+      // tables from them, and the active pairs in element-pair order (used
+      // again by the reverse)
       const int *lut = static_cast<const int *>(cls_lut_->p);
       hipLaunchKernelGGL(k_class_reps, dim3(unsigned(ceil_div(std::max<std::int64_t>(N, C * C), 256))), dim3(256), 0, s,
                          int(N), z, lut, perm, static_cast<const int *>(cls_rep0_->p), crep, C * C, chist);
-      hipLaunchKernelGGL(k_class_tables, dim3(unsigned(C * C), 8), dim3(128), 0, s, C, qb, crep, B.fw1[0], B.fw1[1],
+      hipLaunchKernelGGL(k_class_rows, dim3(unsigned(ceil_div(C * kF, 256))), dim3(256), 0, s, C, crep, xb, cxr);
+      hipLaunchKernelGGL(k_qkv_mfma, dim3(1, kHeads), dim3(256), 0, s, C, cxr, B.qkvp, cqkv);
+      if (qk_norm_)
+        hipLaunchKernelGGL(k_qk_norm, dim3(unsigned(ceil_div(16 * C, 256))), dim3(256), 0, s, C, cqkv, cqis);
+      hipLaunchKernelGGL(k_class_tables, dim3(unsigned(C * C), 8), dim3(128), 0, s, C, cqkv, B.fw1[0], B.fw1[1],
                          B.ob10[0], B.ob10[1], cmt, cc0);
       const dim3 gsort(unsigned(ceil_div(PA, 256)));
       hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, lut, C, chist);
       hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur);
       hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, lut, C, ccur, cord);
+    } else {
+      hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
+      if (qk_norm_)
+        hipLaunchKernelGGL(k_qk_norm, dim3(unsigned(ceil_div(16 * N, 256))), dim3(256), 0, s, int(N), qb,
+                           qkis + b * Nz * 16);
     }
     timed(blk0 ? (use_cls ? "filter_fwd_block0_tables" : "filter_fwd_block0") : "filter_fwd", 0, [&] {
       if (blk0 && use_cls)
@@ -3942,8 +3964,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
         hipLaunchKernelGGL(k_attn_fwd, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb,
                            pfb, pY, pfc, inv_avg, pab, ainv, aevb);
       else
-        hipLaunchKernelGGL(k_attn_msg, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb, qb, pY,
-                           pfc, pab, B.ln1w, B.ln1b, ln_eps_, norm1_, n1b, n1hb, n1ib, act, aevb);
+        hipLaunchKernelGGL(k_attn_msg, dim3(gN4), dim3(256), 0, s, int(N), sr_off, iact, iother, xb, evb,
+                           blk0 && use_cls ? cqkv : qb, pY, pfc, pab, B.ln1w, B.ln1b, ln_eps_, norm1_, n1b, n1hb,
+                           n1ib, act, aevb, z, blk0 && use_cls ? static_cast<const int *>(cls_lut_->p) : nullptr);
     });
     if (scalar)  // the MFMA path's k_attn_msg has done LayerNorm 1 already
       hipLaunchKernelGGL(k_post1, dim3(gN4), dim3(256), 0, s, int(N), ainv, B.ln1w, B.ln1b, ln_eps_, norm1_, n1b,
@@ -4025,8 +4048,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
         });
       const FilterMfma FM = filter_mfma(B, hw_, gamma_);
       if (b == 0 && use_cls) {
-        hipLaunchKernelGGL(k_class_gv, dim3(unsigned((Nz * C * 4 + 255) / 256)), dim3(256), 0, s, int(N), C, gainv, qb,
-                           crep, cgv);
+        hipLaunchKernelGGL(k_class_gv, dim3(unsigned((Nz * C * 4 + 255) / 256)), dim3(256), 0, s, int(N), C, gainv,
+                           cqkv, cgv);
         timed("filter_bwd_block0_tables", 0, [&] {
           const int *lut = static_cast<const int *>(cls_lut_->p);
           if (first)

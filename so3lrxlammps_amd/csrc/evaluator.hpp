@@ -281,7 +281,7 @@ class Evaluator {
   // runs the full kernels.
   int n_cls_ = 0;
   bool class_tables_ = true;
-  Buffer *cls_lut_, *cls_rep0_, *cls_rep_, *cls_mt_, *cls_c0_, *cls_gv_, *cls_hist_, *cls_order_;
+  Buffer *cls_lut_, *cls_rep0_, *cls_rep_, *cls_mt_, *cls_c0_, *cls_gv_, *cls_hist_, *cls_order_, *cls_rows_;
   // Graph replay of one evaluation: the launch sequence of compute_device is
   // captured when the same call (inputs, outputs, flags, box, stream,
   // topology and buffer addresses) comes twice in a row, and replayed while
