@@ -1281,20 +1281,21 @@ __global__ __launch_bounds__(128) void k_class_tables(int C, const double *__res
   }
 }
 
-// Gv[a][B][h] = <gainv_a, v_B>_h: positions 32 h .. 32 h + 31 of both rows
-// (one head's two tiles).  One thread per (a, B, h); qkv: the classes' rows.
-__global__ void k_class_gv(int n, int C, const double *__restrict__ gainv, const double *__restrict__ qkv,
-                           double *Gv) {
-  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= std::size_t(n) * C * 4) return;
-  const int h = int(t % 4), B = int((t / 4) % C);
-  const std::size_t a = t / (4 * std::size_t(C));
-  const double *ga = gainv + a * kF + 32 * h;
-  const double *v = qkv + std::size_t(B) * 640 + 256 + 32 * h;
-  double s = 0.0;
-#pragma unroll 8
-  for (int k = 0; k < 32; ++k) s += ga[k] * v[k];
-  Gv[t] = s;
+// Gv[a][B][h] = <gainv_a, v_B>_h over positions 32 h .. 32 h + 31 (one
+// head's two tiles) of both rows: one wavefront per node, lane l holding
+// positions 2 l and 2 l + 1, so its 16-lane row is head l / 16; qkv: the
+// classes' rows.
+__global__ __launch_bounds__(256) void k_class_gv(int n, int C, const double *__restrict__ gainv,
+                                                  const double *__restrict__ qkv, double *Gv) {
+  const int lane = threadIdx.x & 63;
+  const int a = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (a >= n) return;  // the whole wavefront
+  const double2 ga = *reinterpret_cast<const double2 *>(gainv + std::size_t(a) * kF + 2 * lane);
+  for (int B = 0; B < C; ++B) {
+    const double2 v = *reinterpret_cast<const double2 *>(qkv + std::size_t(B) * 640 + 256 + 2 * lane);
+    const double sum = group_sum(ga.x * v.x + ga.y * v.y);
+    if ((lane & 15) == 0) Gv[(std::size_t(a) * C + B) * 4 + (lane >> 4)] = sum;
+  }
 }
 
 // A lane's 32 bytes of a table row through buffer loads: the lane's row
@@ -4066,8 +4067,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
         });
       const FilterMfma FM = filter_mfma(B, hw_, gamma_);
       if (b == 0 && use_cls) {
-        hipLaunchKernelGGL(k_class_gv, dim3(unsigned((Nz * C * 4 + 255) / 256)), dim3(256), 0, s, int(N), C, gainv,
-                           cqkv, cgv);
+        hipLaunchKernelGGL(k_class_gv, dim3(unsigned(ceil_div(N, 4))), dim3(256), 0, s, int(N), C, gainv, cqkv, cgv);
         timed("filter_bwd_block0_tables", 0, [&] {
           const int *lut = static_cast<const int *>(cls_lut_->p);
           if (first)
