@@ -1341,16 +1341,23 @@ __device__ __forceinline__ int wave_key_add(int key, int *counters) {
   return out;
 }
 
+// Each block takes kClsChunk consecutive pairs (16 per thread), so the
+// global counters see one atomic per key and block.
+constexpr int kClsPer = 16, kClsChunk = 256 * kClsPer;
+
 __global__ __launch_bounds__(256) void k_cls_count(const int *n_active, const int *pa, const int *z, const int *cls,
                                                    int C, int *hist) {
   __shared__ int lc[kMaxClasses * kMaxClasses];
   const int nact = *n_active;
-  if (int(blockIdx.x) * 256 >= nact) return;  // the whole block
+  const int p0 = blockIdx.x * kClsChunk;
+  if (p0 >= nact) return;  // the whole block
   for (int t = threadIdx.x; t < C * C; t += 256) lc[t] = 0;
   __syncthreads();
-  const int p = blockIdx.x * 256 + threadIdx.x;
-  const int key = p < nact ? cls_key(cls[z[pa[2 * p]]], cls[z[pa[2 * p + 1]]], C) : -1;
-  (void)wave_key_add(key, lc);
+  for (int it = 0; it < kClsPer; ++it) {
+    const int p = p0 + it * 256 + threadIdx.x;
+    const int key = p < nact ? cls_key(cls[z[pa[2 * p]]], cls[z[pa[2 * p + 1]]], C) : -1;
+    (void)wave_key_add(key, lc);
+  }
   __syncthreads();
   for (int t = threadIdx.x; t < C * C; t += 256)
     if (lc[t]) atomicAdd(&hist[t], lc[t]);
@@ -1369,16 +1376,23 @@ __global__ __launch_bounds__(256) void k_cls_place(const int *n_active, const in
                                                    int C, int *cursor, int *order) {
   __shared__ int lc[kMaxClasses * kMaxClasses], lb[kMaxClasses * kMaxClasses];
   const int nact = *n_active;
-  if (int(blockIdx.x) * 256 >= nact) return;
+  const int p0 = blockIdx.x * kClsChunk;
+  if (p0 >= nact) return;
   for (int t = threadIdx.x; t < C * C; t += 256) lc[t] = 0;
   __syncthreads();
-  const int p = blockIdx.x * 256 + threadIdx.x;
-  const int key = p < nact ? cls_key(cls[z[pa[2 * p]]], cls[z[pa[2 * p + 1]]], C) : -1;
-  const int rank = wave_key_add(key, lc);
+  int key[kClsPer], rank[kClsPer];
+#pragma unroll
+  for (int it = 0; it < kClsPer; ++it) {
+    const int p = p0 + it * 256 + threadIdx.x;
+    key[it] = p < nact ? cls_key(cls[z[pa[2 * p]]], cls[z[pa[2 * p + 1]]], C) : -1;
+    rank[it] = wave_key_add(key[it], lc);
+  }
   __syncthreads();
   for (int t = threadIdx.x; t < C * C; t += 256) lb[t] = lc[t] ? atomicAdd(&cursor[t], lc[t]) : 0;
   __syncthreads();
-  if (key >= 0) order[lb[key] + rank] = p;
+#pragma unroll
+  for (int it = 0; it < kClsPer; ++it)
+    if (key[it] >= 0) order[lb[key[it]] + rank[it]] = p0 + it * 256 + threadIdx.x;
 }
 
 // Block 0's forward filter through the tables: per filter the stream holds
@@ -3955,7 +3969,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
         hipLaunchKernelGGL(k_qk_norm, dim3(unsigned(ceil_div(16 * C, 256))), dim3(256), 0, s, C, cqkv, cqis);
       hipLaunchKernelGGL(k_class_tables, dim3(unsigned(C * C), 8), dim3(128), 0, s, C, cqkv, B.fw1[0], B.fw1[1],
                          B.ob10[0], B.ob10[1], cmt, cc0);
-      const dim3 gsort(unsigned(ceil_div(PA, 256)));
+      const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
       hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, lut, C, chist);
       hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur);
       hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, lut, C, ccur, cord);
