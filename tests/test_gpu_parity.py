@@ -154,6 +154,30 @@ def test_deterministic_bitwise(ctx):
     assert np.array_equal(a[3], b[3])
 
 
+def test_deterministic_bitwise_table_path(monkeypatch):
+    """Periodic water on block 0's table path, whose element-pair sort places
+    pairs with integer atomics: two contexts (one eager, one replaying a
+    graph), three calls each, all bit for bit equal."""
+    from so3lrxlammps_amd import Context, Lists
+    ref, z, pos, box = support.load_golden("water3000")
+    lists = Lists(pos, np.zeros(3), box, (1, 1, 1))
+    xr = lists.rows_positions(pos)
+    outs = []
+    for no_graph in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NO_GRAPH", no_graph)
+        c = Context(support.MODEL, 0)
+        c.set_system(z, 0, 1)
+        c.set_topology(lists)
+        for _ in range(3):
+            e, f, ea, w = c.compute(xr)
+            outs.append((e, f.copy(), w.copy()))
+        c.close()
+    for e, f, w in outs[1:]:
+        assert e == outs[0][0]
+        assert np.array_equal(f, outs[0][1])
+        assert np.array_equal(w, outs[0][2])
+
+
 def test_packed_images_match_oracle(orc):
     from so3lrxlammps_amd import Context, Lists
     names = [("acetate", -1, 1), ("methyl", 0, 2), ("h2o_cation", 1, 2), ("alanine", 0, 1)]
