@@ -202,6 +202,22 @@ __global__ void k_lr_records(int m, const int *inc, const int *rows, const int *
   rec[2 * std::size_t(m) + k] = rows[2 * c + 1 - side];
 }
 
+// key = the first endpoint's node of pair c, value = c (the short-range
+// pairs' spatial order)
+__global__ void k_pair_keys(int np, const int *nodes, int *key, int *val) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= np) return;
+  key[c] = nodes[2 * c];
+  val[c] = c;
+}
+
+// dst[2 i + side] = src[2 order[i] + side]
+__global__ void k_gather_pairs(int np, const int *order, const int *src, int *dst) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= 2 * np) return;
+  dst[t] = src[2 * order[t >> 1] + (t & 1)];
+}
+
 __global__ void k_relabel(int m, const int *inv, int *nodes) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t < m) nodes[t] = inv[nodes[t]];
@@ -402,10 +418,14 @@ void Evaluator::set_topology(std::int64_t n_rows, const std::int32_t *owner, int
 // positions (the first n rows), the analogue of LAMMPS's own periodic atom
 // sort: the node-major gathers (attention, long range) then read partner rows
 // from a compact region that one XCD's L2 serves, whatever order the caller
-// keeps its atoms in.  The pairs keep their list order; their endpoint nodes
-// are relabelled and each incidence list sorted again by node (stable, so a
-// node's entries stay in increasing pair order).  Runs once per topology, at
-// its first evaluation, on buffers set_topology sized.
+// keeps its atoms in.  The endpoint nodes are relabelled; the short-range
+// pairs are put in the order of their first endpoint's new node (stable), so
+// the pair-major filter kernels read endpoint rows of spatial neighbours as
+// on the device reneighbor path (the long-range pairs, read node-major
+// through their records, keep their list order); each incidence list is
+// sorted again by node (stable, so a node's entries stay in increasing pair
+// order).  Runs once per topology, at its first evaluation, on buffers
+// set_topology sized.
 void Evaluator::order_rows_nodes(const double *x) {
   // rows_order_pending_ stays set until the order is built: a refusal below
   // (non-finite positions) leaves the topology exactly as set_topology left
@@ -437,10 +457,12 @@ void Evaluator::order_rows_nodes(const double *x) {
   int bits = 1;
   while ((std::int64_t(1) << bits) < n) ++bits;
   struct Inc {
-    Buffer *nodes, *inc_off, *inc;
+    Buffer *rows, *nodes, *inc_off, *inc;
     std::int64_t pairs;
+    bool reorder_pairs;
   };
-  const Inc lists[2] = {{sr_nodes_, sr_inc_off_, sr_inc_, p_sr_}, {lr_nodes_, lr_inc_off_, lr_inc_, p_lr_}};
+  const Inc lists[2] = {{sr_rows_, sr_nodes_, sr_inc_off_, sr_inc_, p_sr_, true},
+                        {lr_rows_, lr_nodes_, lr_inc_off_, lr_inc_, p_lr_, false}};
   for (const Inc &L : lists) {
     const int m = int(2 * L.pairs);
     if (m == 0) continue;  // its node offsets are all zero already
@@ -448,6 +470,23 @@ void Evaluator::order_rows_nodes(const double *x) {
         *skeys = static_cast<int *>(top_skeys_->p);
     const unsigned gm = unsigned((m + 255) / 256);
     hipLaunchKernelGGL(k_relabel, dim3(gm), dim3(256), 0, s, m, inv, nodes);
+    if (L.reorder_pairs) {
+      // the pairs in the order of their first node: keys and values in the
+      // two halves of slots, sorted into those of skeys (both hold 2 P),
+      // then rows and nodes gathered through slots
+      const int np = m / 2;
+      int *rows = static_cast<int *>(L.rows->p);
+      const unsigned gp = unsigned((np + 255) / 256);
+      hipLaunchKernelGGL(k_pair_keys, dim3(gp), dim3(256), 0, s, np, nodes, slots, slots + np);
+      tmp_bytes = top_tmp_->bytes;
+      TOPO_CHECK(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, static_cast<const int *>(slots), skeys,
+                                                    static_cast<const int *>(slots + np), skeys + np, np, 0, bits,
+                                                    s));
+      for (int *arr : {rows, nodes}) {
+        hipLaunchKernelGGL(k_gather_pairs, dim3(gm), dim3(256), 0, s, np, skeys + np, arr, slots);
+        TOPO_CHECK(hipMemcpyAsync(arr, slots, std::size_t(m) * sizeof(int), hipMemcpyDeviceToDevice, s));
+      }
+    }
     hipLaunchKernelGGL(k_iota, dim3(gm), dim3(256), 0, s, m, slots);
     tmp_bytes = top_tmp_->bytes;
     TOPO_CHECK(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, static_cast<const int *>(nodes), skeys,

@@ -154,6 +154,53 @@ def test_deterministic_bitwise(ctx):
     assert np.array_equal(a[3], b[3])
 
 
+_ELEMENTS17 = [1, 6, 7, 8, 9, 11, 12, 13, 14, 15, 16, 17, 19, 20, 35, 53, 3]
+
+
+def _cluster(elements, n=240, seed=5):
+    """n atoms of the given elements (each at least once) at random sites of
+    a sphere, no two closer than 1.8 A; multiplicity by electron parity."""
+    rng = np.random.default_rng(seed)
+    pts = []
+    while len(pts) < n:
+        p = rng.uniform(-13.0, 13.0, 3)
+        if np.linalg.norm(p) < 13.0 and all(np.linalg.norm(p - q) >= 1.8 for q in pts):
+            pts.append(p)
+    z = np.array(list(elements) + list(rng.choice(elements, n - len(elements))), dtype=np.int64)
+    return z, np.array(pts), 1 + int(z.sum()) % 2
+
+
+@pytest.mark.parametrize("count", [16, 17])
+def test_element_table_limit(monkeypatch, orc, count):
+    """At the table path's limit: 16 elements run block 0 through the tables
+    (equal to the full kernels to rounding), 17 fall back to the full kernels
+    (bit for bit the SO3LR_NO_CLASS_TABLES=1 result); both against the oracle."""
+    from so3lrxlammps_amd import Context, Lists
+    z, pos, mult = _cluster(_ELEMENTS17[:count])
+    monkeypatch.setenv("SO3LR_SCALAR_FILTER_PAIRS", "0")
+    lists = Lists(pos, pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0))
+    res = []
+    for off in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NO_CLASS_TABLES", off)
+        c = Context(support.MODEL, 0)
+        c.set_system(z, 0, mult)
+        c.set_topology(lists)
+        e, f, ea, w = c.compute(lists.rows_positions(pos))
+        res.append((e, f.copy(), w.copy()))
+        c.close()
+    (e1, f1, w1), (e2, f2, w2) = res
+    print("%d elements: |dE| %.2e max|dF| %.2e" % (count, abs(e1 - e2), np.abs(f1 - f2).max()), flush=True)
+    if count == 17:
+        assert e1 == e2 and np.array_equal(f1, f2) and np.array_equal(w1, w2)
+    else:
+        assert abs(e1 - e2) <= 1e-13 * abs(e2)
+        assert np.abs(f1 - f2).max() <= 1e-11
+    out = orc.evaluate(z, *support.build_graphs(pos, None), charge=0, multiplicity=mult)
+    assert abs(e2 - out["energy"]) <= 1e-10 * abs(out["energy"])
+    assert np.abs(f2 - out["forces"]).max() <= 1e-9
+    assert np.abs(w2 - out["virial"]).max() <= 1e-9
+
+
 def test_deterministic_bitwise_table_path(monkeypatch):
     """Periodic water on block 0's table path, whose element-pair sort places
     pairs with integer atomics: two contexts (one eager, one replaying a
