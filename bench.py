@@ -114,11 +114,13 @@ def traffic_per_launch(kernel, config, units_per_launch):
 KERNEL_WORK_UNIT = {v[0]: v[4] for v in KERNEL_WORK.values()}
 
 
-def kernel_work(widths):
+def kernel_work(widths, elements=0):
     """KERNEL_WORK plus the generic-width filter sections of a model on the
     generic kernels: per active pair and block, both filters, algorithmic
     2 (R F + NH F/4 + (F + F/4) F) MAC each way; the reverse also issues the
-    hidden row's recompute (R F + NH F/4)."""
+    hidden row's recompute (R F + NH F/4).  Block 0 through the element-pair
+    tables (`elements` = C classes): 2 (R F + C^2 NH F) MAC each way, the
+    reverse issuing R F more."""
     work = dict(KERNEL_WORK)
     F, R = widths["invariant_features"], widths["radial_basis_features"]
     NH, FH = len(widths["degree_slots"]), widths["invariant_features"] // 4
@@ -126,6 +128,12 @@ def kernel_work(widths):
     work["generic_filter_fwd"] = ("g_gemm: filter forward section (both filters)", "mfma", alg, alg, "pair")
     work["generic_filter_bwd"] = ("g_gemm: filter reverse section (both filters)", "mfma", alg,
                                   alg + 2 * 2 * (R * F + NH * FH), "pair")
+    if elements:
+        tab = 2 * 2 * (R * F + elements * elements * NH * F)
+        work["generic_filter_fwd_block0_tables"] = ("g_gemm: block 0's table forward section", "mfma", tab, tab,
+                                                    "pair")
+        work["generic_filter_bwd_block0_tables"] = ("g_gemm: block 0's table reverse section", "mfma", tab,
+                                                    tab + 2 * 2 * R * F, "pair")
     return work
 
 
@@ -525,11 +533,11 @@ def main():
     torch.cuda.synchronize()
     md.ctx.kernel_timing(False)
     timing = {}
-    work = kernel_work(model_widths(MODEL))
+    work = kernel_work(model_widths(MODEL), elements=len(set(int(v) for v in z)))
     for name in ("filter_fwd", "filter_fwd_block0", "filter_fwd_block0_tables", "filter_bwd", "filter_bwd_block0",
                  "filter_bwd_block0_tables", "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd", "generic_alpha",
-                 "generic_attn_bwd_pairs"):
+                 "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables"):
         try:
             timing[name] = md.ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched

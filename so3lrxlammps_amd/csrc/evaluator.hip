@@ -3703,6 +3703,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   double *partial = nullptr;
   // block 0 through element-pair tables (k_filter_fwd_class, k_filter_bwd_class)
   const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
+  // the generic path's block 0 takes the tables where their GEMMs are the
+  // smaller ones
+  const bool gen_cls = gen_ && class_tables_ && n_cls_ > 0 && gen_->class_tables_pay(n_cls_, PA);
   const int C = use_cls ? n_cls_ : 0;
   int *crep = nullptr, *chist = nullptr, *ccur = nullptr, *cord = nullptr;
   double *cmt = nullptr, *cc0 = nullptr, *cgv = nullptr, *cxr = nullptr, *cqkv = nullptr, *cqis = nullptr;
@@ -3755,6 +3758,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     }
     } else {
       gen_->carve(int(N), int(PA), [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
+      if (gen_cls) crep = take<int>(cls_rep_, kMaxClasses);
     }
     heff = take<double>(heff_, Nz);
     eatom = take<double>(eatom_, Nz);
@@ -3918,6 +3922,13 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                qseed, dh, dc, dY, dr, nullptr};
     if (timing_ && !from_scratch)
       G.timed = [&](const char *name, const std::function<void()> &f) { timed(name, 0, f); };
+    if (gen_cls) {
+      G.cls_C = n_cls_;
+      G.cls_lut = static_cast<const int *>(cls_lut_->p);
+      G.cls_rep = crep;
+      hipLaunchKernelGGL(k_class_reps, dim3(unsigned(ceil_div(N, 256))), dim3(256), 0, s, int(N), z, G.cls_lut, perm,
+                         static_cast<const int *>(cls_rep0_->p), crep, 0, nullptr);
+    }
     gen_->forward(G);
     hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
     long_range();

@@ -803,7 +803,8 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
   if (lane == 0) dfc[p] = dsum;
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   if (lane < 4 * NH) psc[std::size_t(p) * 4 * NH + lane] = lps[wv][lane];
-  for (int c = lane; c < 2 * F; c += 64) {
+  // (block 0 on the element-table path needs psc only: no df)
+  for (int c = lane; df && c < 2 * F; c += 64) {
     const int which = c / F, cc = c % F, h = cc >> 5;
     double acc = 0.0;
     for (int side = 0; side < 2; ++side) {
@@ -821,6 +822,98 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
     double *y = dY + std::size_t(p) * 24 + lane;
     *y = first ? acc : *y + acc;
   }
+}
+
+// Block 0 through element-pair tables (the algebra of evaluator.hip's
+// k_class_tables, at generic widths): block 0's q, k rows depend on the
+// element alone in a one-image system, and its filter outputs enter only the
+// logits <q_a (.) k_b, f>_h, f = W1 hidden + bias with s = 0 (the spherical
+// hidden row is silu(eb0) for every pair).  Per filter w the table rows
+//   M[w][(A C + B) NH + h][f] = sum_{c in head h} W1_w[c][f] q_A[c] k_B[c]
+//   cb[w][(A C + B) NH + h]  = sum_{c in head h} (b1 + e1 + E1 silu(e0))[c] q_A[c] k_B[c]
+// make the logits one GEMM of the hidden rows against M (C^2 NH columns, cb
+// as its bias), and the reverse's W1^T df one GEMM of a sparse coefficient
+// row per pair against M.  One block per (A, B, h) and filter; thread f.
+__global__ __launch_bounds__(256) void g_cls_tables(int F, int NH, int FH, int C, const double *__restrict__ qkv,
+                                                    const int *__restrict__ rep, const double *__restrict__ wcat0,
+                                                    const double *__restrict__ wcat1,
+                                                    const double *__restrict__ bcat0,
+                                                    const double *__restrict__ bcat1,
+                                                    const double *__restrict__ eb00,
+                                                    const double *__restrict__ eb01, double *__restrict__ M,
+                                                    double *__restrict__ cb) {
+  const int w = blockIdx.y, col = blockIdx.x, h = col % NH, AB = col / NH, A = AB / C, B = AB % C;
+  const int f = threadIdx.x, HW = F + FH;
+  const double *wc = w ? wcat1 : wcat0;
+  const double *qa = qkv + std::size_t(rep[A]) * 5 * F + (w ? 3 * F : 0);
+  const double *kb = qkv + std::size_t(rep[B]) * 5 * F + (w ? 4 * F : F);
+  __shared__ double qk[32], tb[32];
+  if (f < 32) {
+    const int c = 32 * h + f;
+    qk[f] = qa[c] * kb[c];
+    // the output bias of channel c with the spherical branch at s = 0
+    const double *eb0 = w ? eb01 : eb00;
+    double bias = (w ? bcat1 : bcat0)[c];
+    for (int j = 0; j < FH; ++j) bias += wc[std::size_t(c) * HW + F + j] * gsilu(eb0[j]);
+    tb[f] = bias * qk[f];
+  }
+  __syncthreads();
+  const std::size_t row = std::size_t(w) * C * C * NH + col;
+  if (f < F) {
+    double acc = 0.0;
+    for (int k = 0; k < 32; ++k) acc += wc[std::size_t(32 * h + k) * HW + f] * qk[k];
+    M[row * F + f] = acc;
+  }
+  if (f == 0) {
+    double sum = 0.0;
+    for (int k = 0; k < 32; ++k) sum += tb[k];
+    cb[row] = sum;
+  }
+}
+
+// The logits of filter w from the table GEMM's output Y (P x C^2 NH): side 0
+// (a receives from b) is column (c_a C + c_b) NH + h, side 1 (c_b C + c_a) NH + h.
+// Also keeps each pair's two first columns, (c_a C + c_b) NH and
+// (c_b C + c_a) NH, for the reverse (pkey).
+__global__ void g_alpha_cls(int NH, int C, const int *nact, int cap, const int *__restrict__ pa,
+                            const int *__restrict__ z, const int *__restrict__ cls, const double *__restrict__ Y,
+                            int w, double inv_avg, double *__restrict__ palpha, int2 *__restrict__ pkey) {
+  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::size_t p = t / NH;
+  const int h = int(t % NH);
+  if (p >= std::size_t(min(*nact, cap))) return;
+  const int ca = cls[z[pa[2 * p]]], cb = cls[z[pa[2 * p + 1]]];
+  const int k0 = (ca * C + cb) * NH, k1 = (cb * C + ca) * NH;
+  const double *y = Y + p * C * C * NH;
+  double *al = palpha + p * 4 * NH + w * NH + h;
+  al[0] = y[k0 + h] * inv_avg;
+  al[2 * NH] = y[k1 + h] * inv_avg;
+  if (h == 0) pkey[p] = make_int2(k0, k1);
+}
+
+// The reverse's coefficient rows for filter w (P x K, K = C^2 NH, a multiple
+// of 4): the logits' adjoints psc of side 0 in columns pkey.x + h, of side 1
+// in pkey.y + h (both in one column when c_a = c_b), zero elsewhere.  One
+// thread per four entries of a row (32-byte stores; P K / 4 < 2^31).
+__global__ void g_cls_coef(int NH, int K, const int *nact, int cap, const int2 *__restrict__ pkey,
+                           const double *__restrict__ psc, int w, double *__restrict__ S) {
+  const unsigned t = blockIdx.x * blockDim.x + threadIdx.x, K4 = unsigned(K) / 4u;
+  const unsigned p = t / K4;
+  if (p >= unsigned(min(*nact, cap))) return;
+  const int col0 = int(t - p * K4) * 4;
+  const int2 k = pkey[p];
+  const double *ps = psc + std::size_t(p) * 4 * NH + w * NH;
+  double v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int col = col0 + q;
+    v[q] = 0.0;
+    if (col >= k.x && col < k.x + NH) v[q] += ps[col - k.x];
+    if (col >= k.y && col < k.y + NH) v[q] += ps[2 * NH + col - k.y];
+  }
+  double2 *dst = reinterpret_cast<double2 *>(S + std::size_t(p) * K + col0);
+  dst[0] = make_double2(v[0], v[1]);
+  dst[1] = make_double2(v[2], v[3]);
 }
 
 // dE/dr of the pair from the cutoff and the radial basis; one wavefront per
@@ -861,7 +954,7 @@ enum Buf {
   XS = 0, EVS, QKV, QKIS, AEV, N1, N1HAT, N1IS, HPRE, TOUT, PRE2HAT, PRE2IS,
   ACT, HID, CAT, HACT, HHPRE, HKEY, GHEAD,
   GX, GEV, GT, GCAT, GA, GP, GHID, GN1, GAINV, GQKV,
-  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF,
+  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF, CLS_M, CLS_B, CLS_K,
   NBUF
 };
 static_assert(NBUF <= GenericPath::kBuffers, "generic path buffer table");
@@ -936,6 +1029,8 @@ void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int 
 
 namespace {
 // run f, under c.timed when the evaluator is timing kernels
+bool cls_on(const GContext &c) { return c.cls_C > 0; }
+
 void section(const GContext &c, const char *name, const std::function<void()> &f) {
   if (c.timed) c.timed(name, f);
   else f();
@@ -1078,7 +1173,11 @@ void GenericPath::carve(int N, int cap, const std::function<double *(int, std::s
       n * F, n * F, n * NI, n * HO, n * HO, n * 128, n * HO,
       n * F, n * E, n * NI, n * NI, n * E, n * F, n * F, n * F, n * F, n * 5 * F,
       P * R, L * P * NH, L * P * 2 * F, L * P * 4 * NH, P * (F + FH), P * (F + FH), P * 2 * F, P * 4 * NH,
-      P, P * NH, P * R};
+      P, P * NH, P * R,
+      // block 0's element-pair tables: at most F columns per filter
+      // (class_tables_pay), F deep
+      2 * F * F, 2 * F,
+      P};  // each pair's two table columns (two ints in a double's place)
   for (int i = 0; i < NBUF; ++i) b_[i] = take(i, sizes[i]);
 }
 
@@ -1111,12 +1210,30 @@ void GenericPath::forward(const GContext &c) {
     if (c.qk_norm)
       hipLaunchKernelGGL(g_qk_norm, dim3(blocks_for(n * 4 * NH, 256)), dim3(256), 0, s, N, F, NH, qb,
                          b_[QKIS] + b * n * 4 * NH);
+    const int HW = F + FH;
+    if (b == 0 && cls_on(c)) {
+      // block 0 through the element-pair tables: per filter the hidden row
+      // silu(W0 rbf + b0), its products with the table rows (one GEMM, the
+      // logits' constants as its bias) into block 0's filter-row buffer,
+      // and the logits picked from them
+      const int C = c.cls_C, K = C * C * NH;
+      hipLaunchKernelGGL(g_cls_tables, dim3(unsigned(K), 2), dim3(unsigned(F)), 0, s, F, NH, FH, C, qb, c.cls_rep,
+                         B.wcat[0], B.wcat[1], B.bcat[0], B.bcat[1], B.eb0[0], B.eb0[1], b_[CLS_M], b_[CLS_B]);
+      section(c, "generic_filter_fwd_block0_tables", [&] {
+        for (int w = 0; w < 2; ++w) {
+          gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
+          gemm<EPI_STORE, false>(s, cap, c.nact, F, K, b_[HT], HW, b_[CLS_M] + std::size_t(w) * K * F,
+                                 b_[CLS_B] + std::size_t(w) * K, pfb, K);
+          hipLaunchKernelGGL(g_alpha_cls, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, NH, C, c.nact, cap, c.pa,
+                             c.z, c.cls_lut, pfb, w, c.inv_avg, pab, reinterpret_cast<int2 *>(b_[CLS_K]));
+        }
+      });
+    } else {
     // pair invariants and both filters (kokkos_integrated_block0.cpp:166-255)
     hipLaunchKernelGGL(g_pair_inv, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, evb,
                        B.att_cg, psb);
     // per filter: the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)] (F + FH
     // wide), then f = [W1 | E1] row + b1 + e1 in one GEMM
-    const int HW = F + FH;
     section(c, "generic_filter_fwd", [&] {
       for (int w = 0; w < 2; ++w) {
         gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
@@ -1129,6 +1246,7 @@ void GenericPath::forward(const GContext &c) {
                          cap, c.pa, qb, pfb, c.inv_avg,
                          pab);
     });
+    }
     hipLaunchKernelGGL(g_attn_msg, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
                        c.pfc, pab, B.ln1w, B.ln1b, c.ln_eps, c.norm1, n1b, n1hb, n1ib, b_[ACT], aevb);
     // post-attention node chain (kokkos_post_attention_block0.cpp:165-300)
@@ -1185,10 +1303,11 @@ void GenericPath::reverse(const GContext &c) {
     gemm<EPI_DSILU_ADD, true>(s, N, nullptr, F, F, b_[GHID], F, B.m1, nullptr, b_[GN1], F, n1b, F, b_[GP], F);
     hipLaunchKernelGGL(g_ln1_bwd, dim3(g4), dim3(256), 0, s, F, N, b_[GN1], B.ln1w, n1hb, n1ib, c.norm1, b_[GAINV]);
     // attention reverse per pair (kokkos_attention_scatter_reverse.cpp:280-500)
+    const bool tables = b == 0 && cls_on(c);
     section(c, "generic_attn_bwd_pairs", [&] {
       hipLaunchKernelGGL(F == 256 ? g_attn_bwd_pairs<4> : g_attn_bwd_pairs<2>, dim3(blocks_for(P, 4)), dim3(256), 0,
                          s, d, c.nact, cap, c.pa, qb, c.pY, c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg,
-                         b == layers_ - 1 ? 1 : 0, b_[PSC], b_[DF], c.dY, b_[DFC]);
+                         b == layers_ - 1 ? 1 : 0, b_[PSC], tables ? nullptr : b_[DF], c.dY, b_[DFC]);
     });
     if (b > 0)
       hipLaunchKernelGGL(g_attn_bwd_node, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
@@ -1197,20 +1316,41 @@ void GenericPath::reverse(const GContext &c) {
     // per filter: the hidden row's pre-activations again, its adjoint
     // (df [W1 | E1]) (.) silu'(pre) in one GEMM, then through W0 and E0
     const int HW = F + FH;
-    section(c, "generic_filter_bwd", [&] {
-      for (int w = 0; w < 2; ++w) {
-        gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
-        gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
-        gemm<EPI_DSILU, true>(s, cap, c.nact, F, HW, b_[DF] + w * F, 2 * F, B.wcat[w], nullptr, b_[GH], HW, b_[HT], HW);
-        if (w == 0) {
-          gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-          gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
-        } else {
-          gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-          gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+    if (tables) {
+      // block 0 through the element-pair tables: per filter the
+      // pre-activation again, d hidden = (coefficients x table rows) (.)
+      // silu'(pre) in one GEMM, then through W0 (s has no adjoint in block 0)
+      const int C = c.cls_C, K = C * C * NH;
+      section(c, "generic_filter_bwd_block0_tables", [&] {
+        for (int w = 0; w < 2; ++w) {
+          gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
+          hipLaunchKernelGGL(g_cls_coef, dim3(blocks_for(P * K / 4, 256)), dim3(256), 0, s, NH, K, c.nact, cap,
+                             reinterpret_cast<const int2 *>(b_[CLS_K]), b_[PSC], w, b_[DF]);
+          gemm<EPI_DSILU, true>(s, cap, c.nact, K, F, b_[DF], K, b_[CLS_M] + std::size_t(w) * K * F, nullptr, b_[GH],
+                                HW, b_[HT], HW);
+          if (w == 0)
+            gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
+          else
+            gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
         }
-      }
-    });
+      });
+    } else {
+      section(c, "generic_filter_bwd", [&] {
+        for (int w = 0; w < 2; ++w) {
+          gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
+          gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
+          gemm<EPI_DSILU, true>(s, cap, c.nact, F, HW, b_[DF] + w * F, 2 * F, B.wcat[w], nullptr, b_[GH], HW, b_[HT],
+                                HW);
+          if (w == 0) {
+            gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
+            gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+          } else {
+            gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
+            gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
+          }
+        }
+      });
+    }
     hipLaunchKernelGGL(g_pair_radial_bwd, dim3(blocks_for(P, 4)), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC],
                        b_[GRBF], b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
     // the adjoints of the block's inputs feed the block below; block 0's

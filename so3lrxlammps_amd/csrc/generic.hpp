@@ -91,6 +91,12 @@ struct GContext {
   // when set, runs a launch sequence under a name for the evaluator's
   // per-kernel timing (HIP events around it; units: active pairs)
   std::function<void(const char *, const std::function<void()> &)> timed;
+  // block 0 through element-pair tables (a one-image system, whose block-0
+  // rows depend on the element alone): cls_C classes (0: the full filters),
+  // the class of each atomic number, and the node that holds each class's
+  // first atom (device)
+  int cls_C = 0;
+  const int *cls_lut = nullptr, *cls_rep = nullptr;
 };
 
 class GenericPath {
@@ -107,6 +113,12 @@ class GenericPath {
   // evaluator's long-range step, heads and blocks in reverse.
   void forward(const GContext &c);
   void reverse(const GContext &c);
+  // Whether block 0 can take the element-pair tables for C classes and cap
+  // active pairs: their GEMMs have C^2 NH columns, the filters' output GEMM F
+  // (and F + F/4 deep); the coefficient rows are indexed in 32 bits
+  bool class_tables_pay(int C, std::int64_t cap) const {
+    return C > 0 && C * C * d_.NH <= d_.F && cap * C * C * d_.NH / 4 < (std::int64_t(1) << 31);
+  }
 
  private:
   GDims d_{};

@@ -71,6 +71,28 @@ def test_lift_on_the_gpu_equals_the_v1_model(models):
     assert np.abs(w1 - w0).max() <= 1e-9 * max(1.0, np.abs(w0).max())
 
 
+@pytest.mark.parametrize("model,name", [("lift_perturbed", "water3000"), ("lift_options", "alanine_cation"),
+                                        ("deg1123", "acetate")])
+def test_wide_block0_element_tables_match_full_filters(monkeypatch, models, model, name):
+    """Block 0 through the element-pair tables on the generic kernels (one
+    image, C^2 NH <= F: 2, 4 and 3 elements here) against the full filter
+    GEMMs (SO3LR_NO_CLASS_TABLES=1): equal to rounding."""
+    from so3lrxlammps_amd import Context
+    ref, z, pos, box = support.load_golden(name)
+    q, m = ref.get("charge", 0), ref.get("multiplicity", 1)
+    res = []
+    for off in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NO_CLASS_TABLES", off)
+        ctx = Context(models[model], 0)
+        res.append(_hip_single_point(ctx, z, pos, box, q, m))
+        ctx.close()
+    (e1, f1, ea1, w1, _), (e2, f2, ea2, w2, _) = res
+    print("%s %s: |dE| %.2e max|dF| %.2e" % (model, name, abs(e1 - e2), np.abs(f1 - f2).max()), flush=True)
+    assert abs(e1 - e2) <= 1e-12 * abs(e2)
+    assert np.abs(f1 - f2).max() <= 1e-10 * max(1.0, np.abs(f2).max() / 10.0)
+    assert np.abs(w1 - w2).max() <= 1e-10 * max(1.0, np.abs(w2).max())
+
+
 def test_wide_device_path_and_replay(models):
     """so3lr_reneighbor_device + so3lr_compute_device on the perturbed lift:
     bitwise equal across graph replays and equal to the rows path."""
