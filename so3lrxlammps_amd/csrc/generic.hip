@@ -92,7 +92,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_GEMM_
   __shared__ double xs[64][17];
   __shared__ double ws[BN][17];
   const int rows = A.rows_dev ? min(*A.rows_dev, A.rows) : A.rows;
-  const int row0 = blockIdx.x * 64, col0 = blockIdx.y * BN;
+  // With several column blocks the grid's x is a multiple of 8 and the
+  // blocks are taken in dispatch order, (row block, column block) such that
+  // the column blocks of one row block run one after another on one XCD
+  // (dispatch goes round-robin over the 8 XCDs): the later ones read that
+  // row block's X from the XCD's L2, not HBM.
+  int rb = blockIdx.x, cb = blockIdx.y;
+  if (gridDim.y > 1) {
+    const unsigned lin = blockIdx.y * gridDim.x + blockIdx.x, k = lin >> 3;
+    rb = int((k / gridDim.y) * 8 + (lin & 7));
+    cb = int(k % gridDim.y);
+  }
+  const int row0 = rb * 64, col0 = cb * BN;
   if (row0 >= rows) return;  // uniform over the block
   {
     const long zx = long(blockIdx.z) % A.nbx, zy = long(blockIdx.z) / A.nbx;
@@ -978,7 +989,7 @@ void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const doub
   const int cmax = 32 * kGemmMaxNT;
   const dim3 gr(blocks_for(std::size_t(rows), 64));
   auto launch = [&](GemmArgs B, int nb, int tiles) {
-    const dim3 grid(gr.x, unsigned(nb));
+    const dim3 grid(nb > 1 ? (gr.x + 7) / 8 * 8 : gr.x, unsigned(nb));
 #define G_GEMM_NT(NT)                                                              \
   if (tiles <= NT) {                                                               \
     hipLaunchKernelGGL((g_gemm<EPI, WKO, NT>), grid, dim3(256), 0, s, B);          \
