@@ -1363,11 +1363,14 @@ __global__ __launch_bounds__(256) void k_cls_count(const int *n_active, const in
     if (lc[t]) atomicAdd(&hist[t], lc[t]);
 }
 
-__global__ void k_cls_scan(int nkeys, const int *hist, int *cursor) {
+// bucket starts into cursor (advanced by the placement) and, when given,
+// start (kept)
+__global__ void k_cls_scan(int nkeys, const int *hist, int *cursor, int *start) {
   if (threadIdx.x != 0) return;
   int run = 0;
   for (int t = 0; t < nkeys; ++t) {
     cursor[t] = run;
+    if (start) start[t] = run;
     run += hist[t];
   }
 }
@@ -3758,7 +3761,13 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     }
     } else {
       gen_->carve(int(N), int(PA), [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
-      if (gen_cls) crep = take<int>(cls_rep_, kMaxClasses);
+      if (gen_cls) {
+        crep = take<int>(cls_rep_, kMaxClasses);
+        // class-pair counts, cursors and starts; the pairs in element-pair order
+        chist = take<int>(cls_hist_, 3 * kMaxClasses * kMaxClasses);
+        ccur = chist + kMaxClasses * kMaxClasses;
+        cord = take<int>(cls_order_, Pa);
+      }
     }
     heff = take<double>(heff_, Nz);
     eatom = take<double>(eatom_, Nz);
@@ -3923,11 +3932,20 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     if (timing_ && !from_scratch)
       G.timed = [&](const char *name, const std::function<void()> &f) { timed(name, 0, f); };
     if (gen_cls) {
-      G.cls_C = n_cls_;
+      const int C = n_cls_;
+      int *cstart = ccur + kMaxClasses * kMaxClasses;
+      G.cls_C = C;
       G.cls_lut = static_cast<const int *>(cls_lut_->p);
       G.cls_rep = crep;
-      hipLaunchKernelGGL(k_class_reps, dim3(unsigned(ceil_div(N, 256))), dim3(256), 0, s, int(N), z, G.cls_lut, perm,
-                         static_cast<const int *>(cls_rep0_->p), crep, 0, nullptr);
+      G.cls_order = cord;
+      G.cls_count = chist;
+      G.cls_start = cstart;
+      hipLaunchKernelGGL(k_class_reps, dim3(unsigned(ceil_div(std::max<std::int64_t>(N, C * C), 256))), dim3(256), 0, s,
+                         int(N), z, G.cls_lut, perm, static_cast<const int *>(cls_rep0_->p), crep, C * C, chist);
+      const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
+      hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, chist);
+      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, cstart);
+      hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, ccur, cord);
     }
     gen_->forward(G);
     hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);
@@ -3982,7 +4000,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                          B.ob10[0], B.ob10[1], cmt, cc0);
       const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
       hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, lut, C, chist);
-      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur);
+      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, nullptr);
       hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, lut, C, ccur, cord);
     } else {
       hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);

@@ -68,6 +68,11 @@ struct GemmArgs {
   int nbx;
   long xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs;
   int ldw;  // WKO: the weight's row length (its full output width); 0: O
+  // ragged batches (grid z): batch z takes zcount[z] rows from row zstart[z]
+  // of X, Y, Y2, aux and res (device counts; rows caps them), its weight at
+  // z wbs and its bias at z bbs
+  const int *zcount = nullptr, *zstart = nullptr;
+  long bbs = 0;
 };
 
 typedef double gv4d __attribute__((ext_vector_type(4)));
@@ -91,7 +96,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_GEMM_
   constexpr int WPT = BN / 16;     // W chunk values per thread (BN x 16 / 256)
   __shared__ double xs[64][17];
   __shared__ double ws[BN][17];
-  const int rows = A.rows_dev ? min(*A.rows_dev, A.rows) : A.rows;
+  int rows = A.rows_dev ? min(*A.rows_dev, A.rows) : A.rows;
+  if (A.zcount) {
+    const int z = blockIdx.z;
+    rows = min(A.zcount[z], A.rows);
+    const long st = A.zstart[z];
+    A.X += st * A.ldx;
+    A.Y += st * A.ldy;
+    if (A.Y2) A.Y2 += st * A.ldy2;
+    if (A.aux) A.aux += st * A.ldaux;
+    if (A.res) A.res += st * A.ldres;
+    if (A.bias) A.bias += long(z) * A.bbs;
+  }
   // With several column blocks the grid's x is a multiple of 8 and the
   // blocks are taken in dispatch order, (row block, column block) such that
   // the column blocks of one row block run one after another on one XCD
@@ -647,12 +663,13 @@ __global__ __launch_bounds__(256) void g_ev_bwd(GDims d, int N, const int *__res
 // ------------------------------------------------------------- pair kernels
 // Bernstein basis of the distance (kokkos_integrated_block0.cpp:117-164), one
 // thread per active pair.
+// (order: slot p holds pair order[p]; null: pair p)
 __global__ void g_rbf(int R, const int *nact, int cap, const double *__restrict__ pr, double gamma,
                       const double *__restrict__ b, const double *__restrict__ kk, const double *__restrict__ kr,
-                      double *__restrict__ rbf) {
+                      double *__restrict__ rbf, const int *__restrict__ order) {
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= min(*nact, cap)) return;
-  double xb = exp(-gamma * pr[p]);
+  double xb = exp(-gamma * pr[order ? order[p] : p]);
   xb = xb < 1e-6 ? 1e-6 : (xb > 1.0 - 1e-6 ? 1.0 - 1e-6 : xb);
   const double lx = log(xb), l1x = log(1.0 - xb);
   for (int k = 0; k < R; ++k) rbf[std::size_t(p) * R + k] = exp(b[k] + kk[k] * lx + kr[k] * l1x);
@@ -839,21 +856,26 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
 // k_class_tables, at generic widths): block 0's q, k rows depend on the
 // element alone in a one-image system, and its filter outputs enter only the
 // logits <q_a (.) k_b, f>_h, f = W1 hidden + bias with s = 0 (the spherical
-// hidden row is silu(eb0) for every pair).  Per filter w the table rows
-//   M[w][(A C + B) NH + h][f] = sum_{c in head h} W1_w[c][f] q_A[c] k_B[c]
-//   cb[w][(A C + B) NH + h]  = sum_{c in head h} (b1 + e1 + E1 silu(e0))[c] q_A[c] k_B[c]
-// make the logits one GEMM of the hidden rows against M (C^2 NH columns, cb
-// as its bias), and the reverse's W1^T df one GEMM of a sparse coefficient
-// row per pair against M.  One block per (A, B, h) and filter; thread f.
+// hidden row is silu(eb0) for every pair).  The pairs run in element-pair
+// order (key lo C + hi, lo <= hi the two classes), and per filter w and key
+// the 2 NH table rows
+//   Mb[w][key][r][f]  = sum_{c in head h} W1_w[c][f] q_A[c] k_B[c]
+//   cbb[w][key][r]    = sum_{c in head h} (b1 + e1 + E1 silu(e0))[c] q_A[c] k_B[c]
+// with (A, B, h) = (lo, hi, r) for r < NH and (hi, lo, r - NH) after make a
+// bucket's logits one GEMM of its hidden rows against its 2 NH rows (cbb the
+// bias), and its W1^T df one GEMM of its 2 NH coefficients per pair against
+// the same rows.  One block per (key, r) and filter; thread f.
 __global__ __launch_bounds__(256) void g_cls_tables(int F, int NH, int FH, int C, const double *__restrict__ qkv,
                                                     const int *__restrict__ rep, const double *__restrict__ wcat0,
                                                     const double *__restrict__ wcat1,
                                                     const double *__restrict__ bcat0,
                                                     const double *__restrict__ bcat1,
                                                     const double *__restrict__ eb00,
-                                                    const double *__restrict__ eb01, double *__restrict__ M,
-                                                    double *__restrict__ cb) {
-  const int w = blockIdx.y, col = blockIdx.x, h = col % NH, AB = col / NH, A = AB / C, B = AB % C;
+                                                    const double *__restrict__ eb01, double *__restrict__ Mb,
+                                                    double *__restrict__ cbb) {
+  const int w = blockIdx.y, key = blockIdx.x / (2 * NH), r = blockIdx.x % (2 * NH);
+  const int lo = key / C, hi = key % C, h = r % NH;
+  const int A = r < NH ? lo : hi, B = r < NH ? hi : lo;
   const int f = threadIdx.x, HW = F + FH;
   const double *wc = w ? wcat1 : wcat0;
   const double *qa = qkv + std::size_t(rep[A]) * 5 * F + (w ? 3 * F : 0);
@@ -869,79 +891,72 @@ __global__ __launch_bounds__(256) void g_cls_tables(int F, int NH, int FH, int C
     tb[f] = bias * qk[f];
   }
   __syncthreads();
-  const std::size_t row = std::size_t(w) * C * C * NH + col;
+  const std::size_t row = (std::size_t(w) * C * C + key) * 2 * NH + r;
   if (f < F) {
     double acc = 0.0;
     for (int k = 0; k < 32; ++k) acc += wc[std::size_t(32 * h + k) * HW + f] * qk[k];
-    M[row * F + f] = acc;
+    Mb[row * F + f] = acc;
   }
   if (f == 0) {
     double sum = 0.0;
     for (int k = 0; k < 32; ++k) sum += tb[k];
-    cb[row] = sum;
+    cbb[row] = sum;
   }
 }
 
-// The logits of filter w from the table GEMM's output Y (P x C^2 NH): side 0
-// (a receives from b) is column (c_a C + c_b) NH + h, side 1 (c_b C + c_a) NH + h.
-// Also keeps each pair's two first columns, (c_a C + c_b) NH and
-// (c_b C + c_a) NH, for the reverse (pkey).
-__global__ void g_alpha_cls(int NH, int C, const int *nact, int cap, const int *__restrict__ pa,
-                            const int *__restrict__ z, const int *__restrict__ cls, const double *__restrict__ Y,
-                            int w, double inv_avg, double *__restrict__ palpha, int2 *__restrict__ pkey) {
+// The logits of filter w from the bucket GEMMs' output Y (slot q's 2 NH
+// values: the (lo, hi) rows, then the (hi, lo) rows): side 0 (a receives
+// from b) reads the (c_a, c_b) half.
+__global__ void g_alpha_cls(int NH, const int *nact, int cap, const int *__restrict__ order,
+                            const int *__restrict__ pa, const int *__restrict__ z, const int *__restrict__ cls,
+                            const double *__restrict__ Y, int w, double inv_avg, double *__restrict__ palpha) {
   const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const std::size_t p = t / NH;
+  const std::size_t q = t / NH;
   const int h = int(t % NH);
-  if (p >= std::size_t(min(*nact, cap))) return;
-  const int ca = cls[z[pa[2 * p]]], cb = cls[z[pa[2 * p + 1]]];
-  const int k0 = (ca * C + cb) * NH, k1 = (cb * C + ca) * NH;
-  const double *y = Y + p * C * C * NH;
-  double *al = palpha + p * 4 * NH + w * NH + h;
-  al[0] = y[k0 + h] * inv_avg;
-  al[2 * NH] = y[k1 + h] * inv_avg;
-  if (h == 0) pkey[p] = make_int2(k0, k1);
+  if (q >= std::size_t(min(*nact, cap))) return;
+  const int p = order[q];
+  const bool sw = cls[z[pa[2 * p]]] > cls[z[pa[2 * p + 1]]];
+  const double *y = Y + q * 2 * NH;
+  const double d0 = y[h] * inv_avg, d1 = y[NH + h] * inv_avg;
+  double *al = palpha + std::size_t(p) * 4 * NH + w * NH + h;
+  al[0] = sw ? d1 : d0;
+  al[2 * NH] = sw ? d0 : d1;
 }
 
-// The reverse's coefficient rows for filter w (P x K, K = C^2 NH, a multiple
-// of 4): the logits' adjoints psc of side 0 in columns pkey.x + h, of side 1
-// in pkey.y + h (both in one column when c_a = c_b), zero elsewhere.  One
-// thread per four entries of a row (32-byte stores; P K / 4 < 2^31).
-__global__ void g_cls_coef(int NH, int K, const int *nact, int cap, const int2 *__restrict__ pkey,
+// The reverse's coefficients of filter w, slot q (2 NH values: of the
+// (lo, hi) rows, then of the (hi, lo) rows): the logits' adjoints psc of the
+// side whose (receiver, sender) classes each half stands for.
+__global__ void g_cls_coef(int NH, const int *nact, int cap, const int *__restrict__ order,
+                           const int *__restrict__ pa, const int *__restrict__ z, const int *__restrict__ cls,
                            const double *__restrict__ psc, int w, double *__restrict__ S) {
-  const unsigned t = blockIdx.x * blockDim.x + threadIdx.x, K4 = unsigned(K) / 4u;
-  const unsigned p = t / K4;
-  if (p >= unsigned(min(*nact, cap))) return;
-  const int col0 = int(t - p * K4) * 4;
-  const int2 k = pkey[p];
+  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::size_t q = t / (2 * NH);
+  const int j = int(t % (2 * NH));
+  if (q >= std::size_t(min(*nact, cap))) return;
+  const int p = order[q];
+  const bool sw = cls[z[pa[2 * p]]] > cls[z[pa[2 * p + 1]]];
   const double *ps = psc + std::size_t(p) * 4 * NH + w * NH;
-  double v[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int col = col0 + q;
-    v[q] = 0.0;
-    if (col >= k.x && col < k.x + NH) v[q] += ps[col - k.x];
-    if (col >= k.y && col < k.y + NH) v[q] += ps[2 * NH + col - k.y];
-  }
-  double2 *dst = reinterpret_cast<double2 *>(S + std::size_t(p) * K + col0);
-  dst[0] = make_double2(v[0], v[1]);
-  dst[1] = make_double2(v[2], v[3]);
+  const int side = (j >= NH) != sw ? 1 : 0;  // the (lo, hi) half is side 0 unless swapped
+  S[t] = ps[side * 2 * NH + j % NH];
 }
 
 // dE/dr of the pair from the cutoff and the radial basis; one wavefront per
 // pair, lanes over the basis (R <= 64).
+// (order: the basis rows in element-pair order, row q of pair order[q])
 __global__ __launch_bounds__(256) void g_pair_radial_bwd(int R, const int *nact, int cap, const double *__restrict__ pr,
                                                          const double *__restrict__ dfc, const double *__restrict__ grbf,
                                                          const double *__restrict__ rbf, const double *__restrict__ kk,
                                                          const double *__restrict__ kr, double gamma, double rc,
-                                                         double *__restrict__ dr) {
+                                                         double *__restrict__ dr, const int *__restrict__ order) {
   const int lane = threadIdx.x & 63;
-  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (p >= min(*nact, cap)) return;
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= min(*nact, cap)) return;
+  const int p = order ? order[q] : q;
   const double r = pr[p];
   const double xb = exp(-gamma * r);
   double t = 0.0;
   if (lane < R && xb > 1e-6 && xb < 1.0 - 1e-6) {
-    const std::size_t i = std::size_t(p) * R + lane;
+    const std::size_t i = std::size_t(q) * R + lane;
     t = grbf[i] * rbf[i] * (-gamma * kk[lane] + gamma * xb / (1.0 - xb) * kr[lane]);
   }
   t = wsum(t);
@@ -965,7 +980,7 @@ enum Buf {
   XS = 0, EVS, QKV, QKIS, AEV, N1, N1HAT, N1IS, HPRE, TOUT, PRE2HAT, PRE2IS,
   ACT, HID, CAT, HACT, HHPRE, HKEY, GHEAD,
   GX, GEV, GT, GCAT, GA, GP, GHID, GN1, GAINV, GQKV,
-  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF, CLS_M, CLS_B, CLS_K,
+  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF, CLS_M, CLS_B, RBF_S,
   NBUF
 };
 static_assert(NBUF <= GenericPath::kBuffers, "generic path buffer table");
@@ -1025,6 +1040,34 @@ void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const doub
   if (res) R.res = res + c0;
   launch(R, 1, (rest + 31) / 32);
 }
+// One GEMM per element-pair bucket (grid z over the C^2 keys, the empty
+// ones exiting at once): rows of bucket z from row start[z], count[z] of
+// them; the weight of bucket z at z wbs, its bias at z bbs.  O a multiple of
+// 32 kGemmMaxNT or at most that.
+template <int EPI, bool WKO>
+void gemm_buckets(hipStream_t s, int nz, int cap, const int *count, const int *start, int K, int O, const double *X,
+                  int ldx, const double *W, long wbs, const double *bias, long bbs, double *Y, int ldy,
+                  const double *aux = nullptr, int ldaux = 0) {
+  if (cap <= 0) return;
+  GemmArgs A{cap, nullptr, K, O, X, ldx, W, bias, Y, ldy, nullptr, 0, aux, ldaux, nullptr, 0,
+             1, 0, 0, 0, 0, 0, 0, wbs, 0};
+  A.zcount = count;
+  A.zstart = start;
+  A.bbs = bbs;
+  const int cmax = 32 * kGemmMaxNT, nb = (O + cmax - 1) / cmax, cols = (O + nb - 1) / nb;
+  const unsigned gx = blocks_for(std::size_t(cap), 64);
+  const dim3 grid(nb > 1 ? (gx + 7) / 8 * 8 : gx, unsigned(nb), unsigned(nz));
+  const int tiles = (cols + 31) / 32;
+#define G_GEMM_NT(NT)                                                              \
+  if (tiles <= NT) {                                                               \
+    hipLaunchKernelGGL((g_gemm<EPI, WKO, NT>), grid, dim3(256), 0, s, A);          \
+    return;                                                                        \
+  }
+  G_GEMM_NT(2) G_GEMM_NT(4)
+#undef G_GEMM_NT
+  throw std::logic_error("SO3LR: generic bucket GEMM wider than one column block");
+}
+
 // Per-head 32 x 32 projections as one batched launch (O = K = 32).
 template <int EPI, bool WKO>
 void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int ldx, long xbs0, long xbs1,
@@ -1185,10 +1228,10 @@ void GenericPath::carve(int N, int cap, const std::function<double *(int, std::s
       n * F, n * E, n * NI, n * NI, n * E, n * F, n * F, n * F, n * F, n * 5 * F,
       P * R, L * P * NH, L * P * 2 * F, L * P * 4 * NH, P * (F + FH), P * (F + FH), P * 2 * F, P * 4 * NH,
       P, P * NH, P * R,
-      // block 0's element-pair tables: at most F columns per filter
-      // (class_tables_pay), F deep
-      2 * F * F, 2 * F,
-      P};  // each pair's two table columns (two ints in a double's place)
+      // block 0's element-pair tables: 2 filters x C^2 keys x 2 NH rows
+      // (C^2 NH <= F: class_tables_pay) of F, their biases, and block 0's
+      // basis rows in element-pair order
+      4 * F * F, 4 * F, P * R};
   for (int i = 0; i < NBUF; ++i) b_[i] = take(i, sizes[i]);
 }
 
@@ -1206,7 +1249,10 @@ void GenericPath::forward(const GContext &c) {
                        (*c.x0l)[0], c.x0);
   hipLaunchKernelGGL(g_fill, dim3(blocks_for(n * E, 256)), dim3(256), 0, s, evs, n * E);
   hipLaunchKernelGGL(g_rbf, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, c.gamma, hw_.rbf_b, hw_.rbf_k,
-                     hw_.rbf_kr, b_[RBF]);
+                     hw_.rbf_kr, b_[RBF], nullptr);
+  if (cls_on(c))  // block 0's, in element-pair order
+    hipLaunchKernelGGL(g_rbf, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, c.gamma, hw_.rbf_b, hw_.rbf_k,
+                       hw_.rbf_kr, b_[RBF_S], c.cls_order);
   for (int b = 0; b < layers_; ++b) {
     const GBlock &B = bw_[b];
     double *xb = xs + b * n * F, *evb = evs + b * n * E;
@@ -1227,16 +1273,20 @@ void GenericPath::forward(const GContext &c) {
       // silu(W0 rbf + b0), its products with the table rows (one GEMM, the
       // logits' constants as its bias) into block 0's filter-row buffer,
       // and the logits picked from them
-      const int C = c.cls_C, K = C * C * NH;
-      hipLaunchKernelGGL(g_cls_tables, dim3(unsigned(K), 2), dim3(unsigned(F)), 0, s, F, NH, FH, C, qb, c.cls_rep,
-                         B.wcat[0], B.wcat[1], B.bcat[0], B.bcat[1], B.eb0[0], B.eb0[1], b_[CLS_M], b_[CLS_B]);
+      // (in element-pair order: the basis rows RBF_S, the hidden rows, one
+      // GEMM per bucket against its 2 NH table rows)
+      const int C = c.cls_C, NK = C * C, K2 = 2 * NH;
+      hipLaunchKernelGGL(g_cls_tables, dim3(unsigned(NK * K2), 2), dim3(unsigned(F)), 0, s, F, NH, FH, C, qb,
+                         c.cls_rep, B.wcat[0], B.wcat[1], B.bcat[0], B.bcat[1], B.eb0[0], B.eb0[1], b_[CLS_M],
+                         b_[CLS_B]);
       section(c, "generic_filter_fwd_block0_tables", [&] {
         for (int w = 0; w < 2; ++w) {
-          gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
-          gemm<EPI_STORE, false>(s, cap, c.nact, F, K, b_[HT], HW, b_[CLS_M] + std::size_t(w) * K * F,
-                                 b_[CLS_B] + std::size_t(w) * K, pfb, K);
-          hipLaunchKernelGGL(g_alpha_cls, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, NH, C, c.nact, cap, c.pa,
-                             c.z, c.cls_lut, pfb, w, c.inv_avg, pab, reinterpret_cast<int2 *>(b_[CLS_K]));
+          gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF_S], R, B.w0[w], B.b0[w], b_[HT], HW);
+          gemm_buckets<EPI_STORE, false>(s, NK, cap, c.cls_count, c.cls_start, F, K2, b_[HT], HW,
+                                         b_[CLS_M] + std::size_t(w) * NK * K2 * F, long(K2) * F,
+                                         b_[CLS_B] + std::size_t(w) * NK * K2, K2, pfb, K2);
+          hipLaunchKernelGGL(g_alpha_cls, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, NH, c.nact, cap,
+                             c.cls_order, c.pa, c.z, c.cls_lut, pfb, w, c.inv_avg, pab);
         }
       });
     } else {
@@ -1331,14 +1381,17 @@ void GenericPath::reverse(const GContext &c) {
       // block 0 through the element-pair tables: per filter the
       // pre-activation again, d hidden = (coefficients x table rows) (.)
       // silu'(pre) in one GEMM, then through W0 (s has no adjoint in block 0)
-      const int C = c.cls_C, K = C * C * NH;
+      // (in element-pair order, as the forward; dE/dr through the basis
+      // rows of that order)
+      const int C = c.cls_C, NK = C * C, K2 = 2 * NH;
       section(c, "generic_filter_bwd_block0_tables", [&] {
         for (int w = 0; w < 2; ++w) {
-          gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
-          hipLaunchKernelGGL(g_cls_coef, dim3(blocks_for(P * K / 4, 256)), dim3(256), 0, s, NH, K, c.nact, cap,
-                             reinterpret_cast<const int2 *>(b_[CLS_K]), b_[PSC], w, b_[DF]);
-          gemm<EPI_DSILU, true>(s, cap, c.nact, K, F, b_[DF], K, b_[CLS_M] + std::size_t(w) * K * F, nullptr, b_[GH],
-                                HW, b_[HT], HW);
+          gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF_S], R, B.w0[w], B.b0[w], b_[HT], HW);
+          hipLaunchKernelGGL(g_cls_coef, dim3(blocks_for(P * K2, 256)), dim3(256), 0, s, NH, c.nact, cap,
+                             c.cls_order, c.pa, c.z, c.cls_lut, b_[PSC], w, b_[DF]);
+          gemm_buckets<EPI_DSILU, true>(s, NK, cap, c.cls_count, c.cls_start, K2, F, b_[DF], K2,
+                                        b_[CLS_M] + std::size_t(w) * NK * K2 * F, long(K2) * F, nullptr, 0, b_[GH],
+                                        HW, b_[HT], HW);
           if (w == 0)
             gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
           else
@@ -1363,7 +1416,8 @@ void GenericPath::reverse(const GContext &c) {
       });
     }
     hipLaunchKernelGGL(g_pair_radial_bwd, dim3(blocks_for(P, 4)), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC],
-                       b_[GRBF], b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
+                       b_[GRBF], tables ? b_[RBF_S] : b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr,
+                       tables ? c.cls_order : nullptr);
     // the adjoints of the block's inputs feed the block below; block 0's
     // inputs (embedding, ev = 0) do not depend on the positions
     if (b > 0) {

@@ -97,6 +97,9 @@ struct GContext {
   // first atom (device)
   int cls_C = 0;
   const int *cls_lut = nullptr, *cls_rep = nullptr;
+  // the active pairs in element-pair order (slot q holds pair cls_order[q])
+  // and each element-pair bucket's count and first slot (key min C + max)
+  const int *cls_order = nullptr, *cls_count = nullptr, *cls_start = nullptr;
 };
 
 class GenericPath {
