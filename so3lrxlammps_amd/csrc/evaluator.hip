@@ -11,6 +11,7 @@
 // The directed edge "b -> a" (receiver a) uses Y(v/r); "a -> b" uses
 // (-1)^l Y(v/r).  Node sums are gathers over a CSR incidence list.
 #include "evaluator.hpp"
+#include "mfma_ops.hpp"
 
 #include <algorithm>
 #include <array>
@@ -443,41 +444,6 @@ __global__ __launch_bounds__(128) void k_filter_bwd(const int *n_active, const d
 
 
 // ---------------------------------------------------------------- MFMA filters
-// fp64 MFMA V_MFMA_F64_16X16X4F64: D(16x16) += A(16x4) B(4x16) with
-//   A[i][k] in lane i + 16k, B[k][j] in lane j + 16k,
-//   D[i][j] in lane j + 16 (i % 4), register i / 4          (probed on gfx950).
-// The filters run transposed: rows = features, columns = 16 pairs per
-// wavefront.  A D tile then holds, in lane group g = lane / 16 and register r,
-// feature 16 T + g + 4 r of pair lane % 16.  Taking the K index of the next
-// layer in the same order (k = 16 T + g + 4 v) makes every layer's B operand
-// the previous layer's D register, so activations never leave registers.
-// Weights are pre-permuted on the host into that operand order, four K values
-// per lane contiguous (permute_mfma).
-typedef double v4d __attribute__((ext_vector_type(4)));
-typedef double v2d __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ v4d mfma(double a, double b, v4d c) {
-  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
-}
-// Weight fragments (one v4d per lane, 2 KiB per fragment) through buffer
-// loads: the array base sits in a scalar buffer resource and the fragment
-// offset in a scalar register, so a fragment costs two loads and no vector
-// address arithmetic.  Descriptor word 3 = 0x00020000: raw 32-bit data
-// format, as gfx9-family buffer loads expect.
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ double u2_to_f64(unsigned lo, unsigned hi) {
-  return __builtin_bit_cast(double, (unsigned long long)lo | ((unsigned long long)hi << 32));
-}
-__device__ __forceinline__ v4d frag_load(const double *P, int frag, int lane) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<double *>(P), 0, 0x7fffffff, 0x00020000);
-  const v4u a = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 32, frag * 2048, 0);
-  const v4u b = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 32 + 16, frag * 2048, 0);
-  return v4d{u2_to_f64(a[0], a[1]), u2_to_f64(a[2], a[3]), u2_to_f64(b[0], b[1]), u2_to_f64(b[2], b[3])};
-}
-__device__ __forceinline__ v4d wload(const double *P, int KT, int mt, int T, int lane) {
-  return frag_load(P, mt * KT + T, lane);
-}
-
 struct FilterMfma {
   const double *w0p[2], *w1p[2], *e1p[2];              // forward operands
   const double *w1tp[2], *w0tp[2], *e1tp[2], *e0tp[2];  // reverse operands (transposes)
@@ -491,98 +457,11 @@ struct FilterMfma {
   double gamma;
 };
 
-// Activations of the MFMA filter kernels.  On gfx950 every VALU instruction a
-// wavefront issues takes issue time from the fp64 MFMAs of its SIMD, so these
-// are written for the fewest instructions: e^x = 2^m 2^(j/256) e^r with
-// x = (256 m + j) ln2/256 + r, |r| <= ln2/512 (Cody-Waite, ln2/256 split into
-// a 32-bit high part and a low part: exact reduction for |x| < 2800), 2^(j/256)
-// from a 256-entry table in LDS and the degree-4 Taylor polynomial of e^r
-// (truncation < 4e-17 relative).  The power 2^m is capped at 2^1000, which
-// only matters for x > 693.
-__device__ __forceinline__ double exp_tab(double x, const double *tab) {
-  // t = x 256/ln2 + 1.5 2^52 rounds the product to an integer n held in the
-  // low bits of t (exact for |n| < 2^51): n = t - 1.5 2^52, k = low word of t
-  const double t = fma(x, 369.3299304675746, 6755399441055744.0);
-  const double n = t - 6755399441055744.0;
-  double r = fma(n, -0.00270760617331689, x);
-  r = fma(n, -7.453964567463233e-13, r);
-  const int k = int(unsigned(__builtin_bit_cast(unsigned long long, t)));
-  double p = 1.0 / 24.0;
-  p = fma(p, r, 1.0 / 6.0);
-  p = fma(p, r, 0.5);
-  p = fma(p, r, 1.0);
-  p = fma(p, r, 1.0);
-  return __builtin_ldexp(p * tab[k & 255], min(k >> 8, 1000));
-}
-// 1 / d from the hardware estimate (2^-24) and one Newton step: 2e-15
-// relative, ample inside the activations
-__device__ __forceinline__ double rcp_act(double d) {
-  const double r = __builtin_amdgcn_rcp(d);
-  return fma(fma(-d, r, 1.0), r, r);
-}
-__device__ __forceinline__ double silu_tab(double x, const double *tab) {
-  return x * rcp_act(1.0 + exp_tab(-x, tab));
-}
-__device__ __forceinline__ double silu_prime_tab(double x, const double *tab) {
-  const double s = rcp_act(1.0 + exp_tab(-x, tab));
-  return s * (1.0 + x * (1.0 - s));
-}
-// The same for arguments of any size: the exponent is clamped to [-1000,
-// 1000], where e^-x has long underflowed to 0 or reached the 2^1000 cap, so
-// silu(x) = x (x > 1000) or 0 to within 1e-290 (x < -1000).  exp_tab's range
-// ends near |x| = 5.8e6; the spherical filter branch takes the edge
-// invariants of the equivariant features, whose size no weight bounds.
-__device__ __forceinline__ double silu_tab_wide(double x, const double *tab) {
-  return x * rcp_act(1.0 + exp_tab(-fmin(fmax(x, -1000.0), 1000.0), tab));
-}
-__device__ __forceinline__ double silu_prime_tab_wide(double x, const double *tab) {
-  const double s = rcp_act(1.0 + exp_tab(-fmin(fmax(x, -1000.0), 1000.0), tab));
-  return s * (1.0 + x * (1.0 - s));
-}
 // The table into LDS: call at kernel start, before any wavefront returns.
 #define SO3LR_EXP2_TABLE(A)                                               \
   __shared__ double exp2_lds[256];                                        \
   if (threadIdx.x < 256) exp2_lds[threadIdx.x] = (A).exp2_256[threadIdx.x]; \
   __syncthreads();
-
-// Compile-time loop: f(std::integral_constant<int, S>) for S = 0 .. N-1, so
-// every register-array index below is a constant and nothing spills.
-template <class F, int... S>
-__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, S...>) {
-  (f(std::integral_constant<int, S>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-// Software-pipelined operand stream: entry S (one v4d per lane: a weight
-// fragment, a bias tile or a chunk of the incoming adjoint) is loaded PF
-// entries before step S consumes it.  The scheduling fence after each step
-// keeps the compiler from sinking the loads back next to their uses, so PF
-// L2 round trips overlap the MFMAs of the steps in between.
-template <int NS, int PF, class Load>
-struct Stream {
-  Load load;
-  v4d buf[PF];
-  __device__ __forceinline__ explicit Stream(Load l) : load(l) {}
-  __device__ __forceinline__ void prime() {
-    static_for<PF>([&](auto i) {
-      constexpr int I = decltype(i)::value;
-      if constexpr (I < NS) buf[I] = load(i);
-    });
-  }
-  template <class Step>
-  __device__ __forceinline__ void run(Step &&step) {
-    static_for<NS>([&](auto si) {
-      constexpr int S = decltype(si)::value;
-      const v4d w = buf[S % PF];
-      if constexpr (S + PF < NS) buf[S % PF] = load(std::integral_constant<int, S + PF>{});
-      step(si, w);
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  }
-};
 
 // Stream entries in flight per wavefront (measured at config 3: 4 for the
 // forward filter of blocks after 0, which 3, 5 or 6 slow by 3-18%; 6 for
@@ -610,12 +489,6 @@ constexpr int kFilterPF = SO3LR_FILTER_PF;
 #define FILTER_FWD_OCCUPANCY __attribute__((amdgpu_waves_per_eu(SO3LR_FILTER_FWD_WAVES, SO3LR_FILTER_FWD_WAVES)))
 
 __device__ __forceinline__ v4d tile_load(const double *P, int t, int lane) { return frag_load(P, t, lane); }
-__device__ __forceinline__ v4d mfma4(const v4d &w, const v4d &b, v4d c) {
-  c = mfma(w[0], b[0], c);
-  c = mfma(w[1], b[1], c);
-  c = mfma(w[2], b[2], c);
-  return mfma(w[3], b[3], c);
-}
 
 // first equivariant channel of degree slot h (l = h + 1): 0, 3, 8, 15
 __device__ __forceinline__ int ev_offset(int h) { return h == 0 ? 0 : (h == 1 ? 3 : (h == 2 ? 8 : 15)); }
@@ -1363,16 +1236,16 @@ __global__ __launch_bounds__(256) void k_cls_count(const int *n_active, const in
     if (lc[t]) atomicAdd(&hist[t], lc[t]);
 }
 
-// bucket starts into cursor (advanced by the placement) and, when given,
-// start (kept)
-__global__ void k_cls_scan(int nkeys, const int *hist, int *cursor, int *start) {
+// bucket starts into cursor (advanced by the placement), each bucket padded
+// to a multiple of pad slots; the slots' end into *total when given
+__global__ void k_cls_scan(int nkeys, const int *hist, int *cursor, int pad, int *total) {
   if (threadIdx.x != 0) return;
   int run = 0;
   for (int t = 0; t < nkeys; ++t) {
     cursor[t] = run;
-    if (start) start[t] = run;
-    run += hist[t];
+    run += (hist[t] + pad - 1) / pad * pad;
   }
+  if (total) *total = run;
 }
 
 __global__ __launch_bounds__(256) void k_cls_place(const int *n_active, const int *pa, const int *z, const int *cls,
@@ -3086,7 +2959,7 @@ Evaluator::~Evaluator() {
   if (own_stream_) (void)hipStreamDestroy(own_stream_);
 }
 
-namespace {
+// (declared in evaluator.hpp: the generic path uses them too)
 std::vector<double> transpose(const std::vector<double> &w, std::size_t rows, std::size_t cols) {
   std::vector<double> t(w.size());
   for (std::size_t r = 0; r < rows; ++r)
@@ -3141,7 +3014,7 @@ std::vector<double> permute_mfma(const std::vector<double> &w, std::size_t M, st
         }
   return p;
 }
-}  // namespace
+
 
 Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::move(model)), device_(device) {
   int count = 0;
@@ -3706,9 +3579,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   double *partial = nullptr;
   // block 0 through element-pair tables (k_filter_fwd_class, k_filter_bwd_class)
   const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
-  // the generic path's block 0 takes the tables where their GEMMs are the
-  // smaller ones
-  const bool gen_cls = gen_ && class_tables_ && n_cls_ > 0 && gen_->class_tables_pay(n_cls_, PA);
+  // (the generic path's: g_cls_tables, g_b0_fwd, g_b0_bwd)
+  const bool gen_cls = gen_ && class_tables_ && n_cls_ > 0;
   const int C = use_cls ? n_cls_ : 0;
   int *crep = nullptr, *chist = nullptr, *ccur = nullptr, *cord = nullptr;
   double *cmt = nullptr, *cc0 = nullptr, *cgv = nullptr, *cxr = nullptr, *cqkv = nullptr, *cqis = nullptr;
@@ -3760,13 +3632,15 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       cgv = take<double>(cls_gv_, Nz * C * 4);
     }
     } else {
-      gen_->carve(int(N), int(PA), [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
+      gen_->carve(int(N), int(PA), gen_cls ? n_cls_ : 0,
+                  [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
       if (gen_cls) {
         crep = take<int>(cls_rep_, kMaxClasses);
-        // class-pair counts, cursors and starts; the pairs in element-pair order
-        chist = take<int>(cls_hist_, 3 * kMaxClasses * kMaxClasses);
+        // class-pair counts and cursors, then the slot count; the pairs in
+        // element-pair order, each bucket padded with -1
+        chist = take<int>(cls_hist_, 2 * kMaxClasses * kMaxClasses + 1);
         ccur = chist + kMaxClasses * kMaxClasses;
-        cord = take<int>(cls_order_, Pa);
+        cord = take<int>(cls_order_, Pa + std::size_t(GContext::kB0Pad) * n_cls_ * n_cls_);
       }
     }
     heff = take<double>(heff_, Nz);
@@ -3933,18 +3807,19 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       G.timed = [&](const char *name, const std::function<void()> &f) { timed(name, 0, f); };
     if (gen_cls) {
       const int C = n_cls_;
-      int *cstart = ccur + kMaxClasses * kMaxClasses;
+      const int slots_max = int(Pa) + GContext::kB0Pad * C * C;
+      int *cslots = ccur + kMaxClasses * kMaxClasses;
       G.cls_C = C;
       G.cls_lut = static_cast<const int *>(cls_lut_->p);
       G.cls_rep = crep;
       G.cls_order = cord;
-      G.cls_count = chist;
-      G.cls_start = cstart;
+      G.cls_slots = cslots;
       hipLaunchKernelGGL(k_class_reps, dim3(unsigned(ceil_div(std::max<std::int64_t>(N, C * C), 256))), dim3(256), 0, s,
                          int(N), z, G.cls_lut, perm, static_cast<const int *>(cls_rep0_->p), crep, C * C, chist);
+      hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(slots_max, 256))), dim3(256), 0, s, cord, slots_max, -1);
       const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
       hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, chist);
-      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, cstart);
+      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, GContext::kB0Pad, cslots);
       hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, ccur, cord);
     }
     gen_->forward(G);
@@ -4000,7 +3875,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                          B.ob10[0], B.ob10[1], cmt, cc0);
       const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
       hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, lut, C, chist);
-      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, nullptr);
+      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, 1, nullptr);
       hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, lut, C, ccur, cord);
     } else {
       hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);

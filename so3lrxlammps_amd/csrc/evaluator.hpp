@@ -38,6 +38,14 @@ struct TopologyError : std::runtime_error {
   explicit TopologyError(const std::string &what) : std::runtime_error(what) {}
 };
 
+// Host-side weight layouts of the fp64 MFMA kernels (evaluator.hip): the
+// transpose of a rows x cols row-major matrix; a bias of length M in MFMA
+// accumulator order (a D tile starts from it); an M x K row-major matrix in
+// MFMA A-operand order, 16-row tiles by 16-wide K chunks.
+std::vector<double> transpose(const std::vector<double> &w, std::size_t rows, std::size_t cols);
+std::vector<double> bias_acc(const std::vector<double> &b, std::size_t M);
+std::vector<double> permute_mfma(const std::vector<double> &w, std::size_t M, std::size_t K);
+
 // Device weight pointers for one interaction block.
 struct BlockWeights {
   const double *wqkv;                   // (5, 4, 32, 32): q k v q_ev k_ev, (head, in, out)

@@ -12,6 +12,7 @@
 // harmonics Y(v/r)), direction 1 the edge a -> b ((-1)^l Y(v/r)).
 #include "generic.hpp"
 #include "evaluator.hpp"
+#include "mfma_ops.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -663,13 +664,12 @@ __global__ __launch_bounds__(256) void g_ev_bwd(GDims d, int N, const int *__res
 // ------------------------------------------------------------- pair kernels
 // Bernstein basis of the distance (kokkos_integrated_block0.cpp:117-164), one
 // thread per active pair.
-// (order: slot p holds pair order[p]; null: pair p)
 __global__ void g_rbf(int R, const int *nact, int cap, const double *__restrict__ pr, double gamma,
                       const double *__restrict__ b, const double *__restrict__ kk, const double *__restrict__ kr,
-                      double *__restrict__ rbf, const int *__restrict__ order) {
+                      double *__restrict__ rbf) {
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= min(*nact, cap)) return;
-  double xb = exp(-gamma * pr[order ? order[p] : p]);
+  double xb = exp(-gamma * pr[p]);
   xb = xb < 1e-6 ? 1e-6 : (xb > 1.0 - 1e-6 ? 1.0 - 1e-6 : xb);
   const double lx = log(xb), l1x = log(1.0 - xb);
   for (int k = 0; k < R; ++k) rbf[std::size_t(p) * R + k] = exp(b[k] + kk[k] * lx + kr[k] * l1x);
@@ -856,32 +856,35 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
 // k_class_tables, at generic widths): block 0's q, k rows depend on the
 // element alone in a one-image system, and its filter outputs enter only the
 // logits <q_a (.) k_b, f>_h, f = W1 hidden + bias with s = 0 (the spherical
-// hidden row is silu(eb0) for every pair).  The pairs run in element-pair
-// order (key lo C + hi, lo <= hi the two classes), and per filter w and key
-// the 2 NH table rows
-//   Mb[w][key][r][f]  = sum_{c in head h} W1_w[c][f] q_A[c] k_B[c]
-//   cbb[w][key][r]    = sum_{c in head h} (b1 + e1 + E1 silu(e0))[c] q_A[c] k_B[c]
-// with (A, B, h) = (lo, hi, r) for r < NH and (hi, lo, r - NH) after make a
-// bucket's logits one GEMM of its hidden rows against its 2 NH rows (cbb the
-// bias), and its W1^T df one GEMM of its 2 NH coefficients per pair against
-// the same rows.  One block per (key, r) and filter; thread f.
+// hidden row is silu(eb0) for every pair).  Per filter w and key (lo, hi)
+// (key lo C + hi; the keys with lo > hi go unused) the 2 NH table rows
+//   M[r][f] = sum_{c in head h} W1_w[c][f] q_A[c] k_B[c]
+//   cb[r]   = sum_{c in head h} (b1 + e1 + E1 silu(e0))[c] q_A[c] k_B[c]
+// with (A, B, h) = (lo, hi, r) for r < NH and (hi, lo, r - NH) after make
+// the logits of a pair M hidden + cb, and its hidden adjoint M^T times the
+// logits' adjoints.  The rows go out as MFMA A operands, zero-padded to 16
+// rows (2 NH = F / 16 <= 16):
+//   tf[w][key][T][lane][v] = M[lane % 16][16 T + lane / 16 + 4 v]  (rows r)
+//   tr[w][key][T][lane][v] = M[lane / 16 + 4 v][16 T + lane % 16]  (rows f)
+// and cb[w][key][r].  One block per (key, r < 16) and filter; thread f.
 __global__ __launch_bounds__(256) void g_cls_tables(int F, int NH, int FH, int C, const double *__restrict__ qkv,
                                                     const int *__restrict__ rep, const double *__restrict__ wcat0,
                                                     const double *__restrict__ wcat1,
                                                     const double *__restrict__ bcat0,
                                                     const double *__restrict__ bcat1,
                                                     const double *__restrict__ eb00,
-                                                    const double *__restrict__ eb01, double *__restrict__ Mb,
-                                                    double *__restrict__ cbb) {
-  const int w = blockIdx.y, key = blockIdx.x / (2 * NH), r = blockIdx.x % (2 * NH);
+                                                    const double *__restrict__ eb01, double *__restrict__ tf,
+                                                    double *__restrict__ tr, double *__restrict__ cb) {
+  const int w = blockIdx.y, key = blockIdx.x / 16, r = blockIdx.x % 16;
   const int lo = key / C, hi = key % C, h = r % NH;
   const int A = r < NH ? lo : hi, B = r < NH ? hi : lo;
-  const int f = threadIdx.x, HW = F + FH;
+  const bool live = r < 2 * NH;
+  const int f = threadIdx.x, HW = F + FH, FT = F / 16;
   const double *wc = w ? wcat1 : wcat0;
-  const double *qa = qkv + std::size_t(rep[A]) * 5 * F + (w ? 3 * F : 0);
-  const double *kb = qkv + std::size_t(rep[B]) * 5 * F + (w ? 4 * F : F);
   __shared__ double qk[32], tb[32];
-  if (f < 32) {
+  if (live && f < 32) {
+    const double *qa = qkv + std::size_t(rep[A]) * 5 * F + (w ? 3 * F : 0);
+    const double *kb = qkv + std::size_t(rep[B]) * 5 * F + (w ? 4 * F : F);
     const int c = 32 * h + f;
     qk[f] = qa[c] * kb[c];
     // the output bias of channel c with the spherical branch at s = 0
@@ -891,72 +894,298 @@ __global__ __launch_bounds__(256) void g_cls_tables(int F, int NH, int FH, int C
     tb[f] = bias * qk[f];
   }
   __syncthreads();
-  const std::size_t row = (std::size_t(w) * C * C + key) * 2 * NH + r;
+  const std::size_t wk = std::size_t(w) * C * C + key;
   if (f < F) {
     double acc = 0.0;
-    for (int k = 0; k < 32; ++k) acc += wc[std::size_t(32 * h + k) * HW + f] * qk[k];
-    Mb[row * F + f] = acc;
+    if (live)
+      for (int k = 0; k < 32; ++k) acc += wc[std::size_t(32 * h + k) * HW + f] * qk[k];
+    const int T = f / 16, fi = f % 16;
+    tf[((wk * FT + T) * 64 + r + 16 * (fi % 4)) * 4 + fi / 4] = acc;
+    tr[((wk * FT + T) * 64 + fi + 16 * (r % 4)) * 4 + r / 4] = acc;
   }
-  if (f == 0) {
+  if (live && f == 0) {
     double sum = 0.0;
     for (int k = 0; k < 32; ++k) sum += tb[k];
-    cbb[row] = sum;
+    cb[wk * 2 * NH + r] = sum;
   }
 }
 
-// The logits of filter w from the bucket GEMMs' output Y (slot q's 2 NH
-// values: the (lo, hi) rows, then the (hi, lo) rows): side 0 (a receives
-// from b) reads the (c_a, c_b) half.
-__global__ void g_alpha_cls(int NH, const int *nact, int cap, const int *__restrict__ order,
-                            const int *__restrict__ pa, const int *__restrict__ z, const int *__restrict__ cls,
-                            const double *__restrict__ Y, int w, double inv_avg, double *__restrict__ palpha) {
-  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const std::size_t q = t / NH;
-  const int h = int(t % NH);
-  if (q >= std::size_t(min(*nact, cap))) return;
-  const int p = order[q];
-  const bool sw = cls[z[pa[2 * p]]] > cls[z[pa[2 * p + 1]]];
-  const double *y = Y + q * 2 * NH;
-  const double d0 = y[h] * inv_avg, d1 = y[NH + h] * inv_avg;
-  double *al = palpha + std::size_t(p) * 4 * NH + w * NH + h;
-  al[0] = sw ? d1 : d0;
-  al[2 * NH] = sw ? d0 : d1;
+// Block 0's filters through the tables, fused: per pair and filter the
+// hidden row silu(W0 rbf + b0) stays in registers, its logits are one MFMA
+// chain per hidden tile against the table rows; in reverse the hidden
+// adjoint is the table rows times the logits' adjoints, then through
+// silu'(pre) (pre recomputed) and W0^T to the basis adjoint, and dE/dr as
+// g_pair_radial_bwd.  The layout of evaluator.hip's MFMA filters: features
+// as rows, 16 pairs per column tile, a tile's D registers the next layer's B
+// operand (feature 16 T + g + 4 r of pair lane % 16 in lane group g,
+// register r).  FT = F / 16 hidden tiles, RT = R / 16 basis chunks, NH =
+// FT / 2 heads (F = 32 NH), so the 2 NH table rows fit one MFMA tile.
+// The slots run in element-pair order, each bucket padded with -1 to a
+// multiple of 32: a wavefront's CT column tiles (16 CT <= 32 slots) are of
+// one key, whose table rows every lane reads, and its first slot holds a
+// pair unless the whole wavefront is padding.
+struct B0Args {
+  const int *slots, *order, *pa, *z, *cls;
+  int C;
+  const double *pr, *rbf;               // distance; basis rows (R per pair)
+  const double *w0p[2], *w0tp[2], *b0a[2];
+  const double *tf, *tr, *cb;           // g_cls_tables
+  const double *exp2_256, *kk, *kr;
+  double gamma, rc, inv_avg;
+  double *palpha;                       // forward: the logits (4 NH per pair)
+  const double *psc, *dfc;              // reverse: the logits' and the cutoff's adjoints
+  double *dr;                           // reverse: dE/dr (added to)
+};
+
+// The wavefront's slots: pair p[ct] of column tile ct (padding: the first
+// slot's pair, with ok false), its orientation sw[ct] (classes (hi, lo)),
+// the key, and the lane's basis values rb[ct][Kc][v] = rbf_k,
+// k = 16 Kc + g + 4 v.  False: no pair in the wavefront.
+template <int RT, int CT>
+__device__ __forceinline__ bool b0_slots(const B0Args &A, int wave, int j, int g, int *p, bool *ok, bool *sw,
+                                         int &key, v4d (*rb)[RT]) {
+  const int q0 = wave * 16 * CT;
+  if (q0 >= *A.slots) return false;
+  const int p0 = __builtin_amdgcn_readfirstlane(A.order[q0]);
+  if (p0 < 0) return false;
+  const int ca = A.cls[A.z[A.pa[2 * p0]]], cbb = A.cls[A.z[A.pa[2 * p0 + 1]]];
+  key = __builtin_amdgcn_readfirstlane(ca < cbb ? ca * A.C + cbb : cbb * A.C + ca);
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int e = A.order[q0 + 16 * ct + j];
+    ok[ct] = e >= 0;
+    p[ct] = ok[ct] ? e : p0;
+    sw[ct] = A.cls[A.z[A.pa[2 * p[ct]]]] > A.cls[A.z[A.pa[2 * p[ct] + 1]]];
+    const double *row = A.rbf + std::size_t(p[ct]) * 16 * RT + g;
+#pragma unroll
+    for (int Kc = 0; Kc < RT; ++Kc)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) rb[ct][Kc][v] = row[16 * Kc + 4 * v];
+  }
+  return true;
 }
 
-// The reverse's coefficients of filter w, slot q (2 NH values: of the
-// (lo, hi) rows, then of the (hi, lo) rows): the logits' adjoints psc of the
-// side whose (receiver, sender) classes each half stands for.
-__global__ void g_cls_coef(int NH, const int *nact, int cap, const int *__restrict__ order,
-                           const int *__restrict__ pa, const int *__restrict__ z, const int *__restrict__ cls,
-                           const double *__restrict__ psc, int w, double *__restrict__ S) {
-  const std::size_t t = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const std::size_t q = t / (2 * NH);
-  const int j = int(t % (2 * NH));
-  if (q >= std::size_t(min(*nact, cap))) return;
-  const int p = order[q];
-  const bool sw = cls[z[pa[2 * p]]] > cls[z[pa[2 * p + 1]]];
-  const double *ps = psc + std::size_t(p) * 4 * NH + w * NH;
-  const int side = (j >= NH) != sw ? 1 : 0;  // the (lo, hi) half is side 0 unless swapped
-  S[t] = ps[side * 2 * NH + j % NH];
+#ifndef SO3LR_B0_FWD_CT
+#define SO3LR_B0_FWD_CT 2
+#endif
+#ifndef SO3LR_B0_BWD_CT
+#define SO3LR_B0_BWD_CT 1
+#endif
+#ifndef SO3LR_B0_PF
+#define SO3LR_B0_PF 6
+#endif
+
+// Forward: per filter the stream holds, per hidden tile T, the bias tile,
+// the RT W0 chunks and the table rows of tile T - 1 (whose SiLU runs after
+// tile T's first MFMA, off the critical path), then the last tile's rows.
+template <int FT, int RT, int CT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void g_b0_fwd(B0Args A) {
+  constexpr int NH = FT / 2, NT = FT * (RT + 2);
+  __shared__ double tab[256];
+  tab[threadIdx.x] = A.exp2_256[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + int(threadIdx.x >> 6));
+  int p[CT], key = 0;
+  bool ok[CT], sw[CT];
+  v4d rb[CT][RT];
+  if (!b0_slots<RT, CT>(A, wave, j, g, p, ok, sw, key, rb)) return;
+  const std::size_t NK = std::size_t(A.C) * A.C;
+  const double *tfw[2] = {A.tf + std::size_t(key) * FT * 256, A.tf + (NK + key) * FT * 256};
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, w = S / NT, s = S % NT;
+    constexpr int T = s < RT + 1 ? 0 : 1 + (s - RT - 1) / (RT + 2);
+    constexpr int u = s < RT + 1 ? s : (s - RT - 1) % (RT + 2);
+    if constexpr (T == FT) return frag_load(tfw[w], FT - 1, lane);
+    else if constexpr (u == 0) return frag_load(A.b0a[w], T, lane);
+    else if constexpr (u <= RT) return frag_load(A.w0p[w], T * RT + u - 1, lane);
+    else return frag_load(tfw[w], T - 1, lane);
+  };
+  Stream<2 * NT, SO3LR_B0_PF, decltype(load)> st(load);
+  st.prime();
+  v4d pre[2][CT], h[CT], lg[CT];
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int S = decltype(si)::value, w = S / NT, s = S % NT;
+    constexpr int T = s < RT + 1 ? 0 : 1 + (s - RT - 1) / (RT + 2);
+    constexpr int u = s < RT + 1 ? s : (s - RT - 1) % (RT + 2);
+    if constexpr (s == 0) {
+      // the logits start from the table biases (rows r = g + 4 rr)
+      const double *cbw = A.cb + (w * NK + key) * 2 * NH;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) lg[ct][rr] = g + 4 * rr < 2 * NH ? cbw[g + 4 * rr] : 0.0;
+    }
+    if constexpr (T == FT) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) h[ct][rr] = silu_tab(pre[(FT - 1) % 2][ct][rr], tab);
+        lg[ct] = mfma4(wv, h[ct], lg[ct]);
+      }
+      // row r < NH: the logit of (lo, hi) head r, the receiver's side unless
+      // the pair runs (hi, lo)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int r = g + 4 * rr;
+          if (r < 2 * NH && ok[ct]) {
+            const int side = (r >= NH) != sw[ct] ? 1 : 0;
+            A.palpha[std::size_t(p[ct]) * 4 * NH + side * 2 * NH + w * NH + r % NH] = lg[ct][rr] * A.inv_avg;
+          }
+        }
+    } else if constexpr (u == 0) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) pre[T % 2][ct] = wv;
+    } else if constexpr (u <= RT) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) pre[T % 2][ct] = mfma4(wv, rb[ct][u - 1], pre[T % 2][ct]);
+      if constexpr (u == 1 && T > 0) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) h[ct][rr] = silu_tab(pre[(T - 1) % 2][ct][rr], tab);
+      }
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) lg[ct] = mfma4(wv, h[ct], lg[ct]);
+    }
+  });
+}
+
+// Reverse: per filter the stream holds, per hidden tile T, the bias tile,
+// the table rows (d hidden = rows^T coefficients), the RT W0 chunks (pre
+// again; silu' of tile T - 1 after the first) and the RT W0^T chunks of tile
+// T - 1 (d rbf += W0^T d hidden), then the last tile's W0^T chunks.
+template <int FT, int RT, int CT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void g_b0_bwd(B0Args A) {
+  constexpr int NH = FT / 2, NB = FT * (2 + 2 * RT);
+  __shared__ double tab[256];
+  tab[threadIdx.x] = A.exp2_256[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * 4 + int(threadIdx.x >> 6));
+  int p[CT], key = 0;
+  bool ok[CT], sw[CT];
+  v4d rb[CT][RT];
+  if (!b0_slots<RT, CT>(A, wave, j, g, p, ok, sw, key, rb)) return;
+  const std::size_t NK = std::size_t(A.C) * A.C;
+  const double *trw[2] = {A.tr + std::size_t(key) * FT * 256, A.tr + (NK + key) * FT * 256};
+  // the B operand of the table product: row r = g + 4 v's logit adjoint
+  v4d cf[2][CT];
+#pragma unroll
+  for (int w = 0; w < 2; ++w)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = g + 4 * v;
+        const int side = (r >= NH) != sw[ct] ? 1 : 0;
+        cf[w][ct][v] = r < 2 * NH ? A.psc[std::size_t(p[ct]) * 4 * NH + side * 2 * NH + w * NH + r % NH] : 0.0;
+      }
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, w = S / NB, s = S % NB;
+    constexpr int T = s < RT + 2 ? 0 : 1 + (s - RT - 2) / (2 * RT + 2);
+    constexpr int u = s < RT + 2 ? s : (s - RT - 2) % (2 * RT + 2);
+    if constexpr (T == FT) return frag_load(A.w0tp[w], u * FT + FT - 1, lane);
+    else if constexpr (u == 0) return frag_load(A.b0a[w], T, lane);
+    else if constexpr (u == 1) return frag_load(trw[w], T, lane);
+    else if constexpr (u < RT + 2) return frag_load(A.w0p[w], T * RT + u - 2, lane);
+    else return frag_load(A.w0tp[w], (u - RT - 2) * FT + T - 1, lane);
+  };
+  Stream<2 * NB, SO3LR_B0_PF, decltype(load)> st(load);
+  st.prime();
+  const v4d zero = v4d{0.0, 0.0, 0.0, 0.0};
+  v4d pre[2][CT], gh[2][CT], drb[CT][RT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int Kc = 0; Kc < RT; ++Kc) drb[ct][Kc] = zero;
+  auto dsilu = [&](int t) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) gh[t][ct][rr] *= silu_prime_tab(pre[t][ct][rr], tab);
+  };
+  st.run([&](auto si, const v4d &wv) {
+    constexpr int S = decltype(si)::value, w = S / NB, s = S % NB;
+    constexpr int T = s < RT + 2 ? 0 : 1 + (s - RT - 2) / (2 * RT + 2);
+    constexpr int u = s < RT + 2 ? s : (s - RT - 2) % (2 * RT + 2);
+    if constexpr (T == FT) {
+      if constexpr (u == 0) dsilu((FT - 1) % 2);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) drb[ct][u] = mfma4(wv, gh[(FT - 1) % 2][ct], drb[ct][u]);
+    } else if constexpr (u == 0) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) pre[T % 2][ct] = wv;
+    } else if constexpr (u == 1) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        // rows r >= 2 NH are zero: two MFMAs cover the 8 rows of NH = 4
+        v4d acc = mfma(wv[0], cf[w][ct][0], zero);
+        acc = mfma(wv[1], cf[w][ct][1], acc);
+        if constexpr (2 * NH > 8) {
+          acc = mfma(wv[2], cf[w][ct][2], acc);
+          acc = mfma(wv[3], cf[w][ct][3], acc);
+        }
+        gh[T % 2][ct] = acc;
+      }
+    } else if constexpr (u < RT + 2) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) pre[T % 2][ct] = mfma4(wv, rb[ct][u - 2], pre[T % 2][ct]);
+      if constexpr (u == 2 && T > 0) dsilu((T - 1) % 2);
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        drb[ct][u - RT - 2] = mfma4(wv, gh[(T - 1) % 2][ct], drb[ct][u - RT - 2]);
+    }
+  });
+  // dE/dr: the basis adjoint against d rbf / dr (zero where the basis
+  // variable is clamped), plus the cutoff's
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const double r = A.pr[p[ct]];
+    const double xb = exp(-A.gamma * r);
+    double part = 0.0;
+    if (xb > 1e-6 && xb < 1.0 - 1e-6) {
+      const double ratio = xb / (1.0 - xb);
+#pragma unroll
+      for (int Kc = 0; Kc < RT; ++Kc)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int k = 16 * Kc + g + 4 * rr;
+          part += drb[ct][Kc][rr] * rb[ct][Kc][rr] * (-A.gamma * A.kk[k] + A.gamma * ratio * A.kr[k]);
+        }
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    if (ok[ct] && g == 0) {
+      double grad = part;
+      if (r < A.rc) {
+        const double t = r / A.rc;
+        grad += A.dfc[p[ct]] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / A.rc);
+      }
+      A.dr[p[ct]] += grad;
+    }
+  }
 }
 
 // dE/dr of the pair from the cutoff and the radial basis; one wavefront per
 // pair, lanes over the basis (R <= 64).
-// (order: the basis rows in element-pair order, row q of pair order[q])
 __global__ __launch_bounds__(256) void g_pair_radial_bwd(int R, const int *nact, int cap, const double *__restrict__ pr,
                                                          const double *__restrict__ dfc, const double *__restrict__ grbf,
                                                          const double *__restrict__ rbf, const double *__restrict__ kk,
                                                          const double *__restrict__ kr, double gamma, double rc,
-                                                         double *__restrict__ dr, const int *__restrict__ order) {
+                                                         double *__restrict__ dr) {
   const int lane = threadIdx.x & 63;
-  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (q >= min(*nact, cap)) return;
-  const int p = order ? order[q] : q;
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (p >= min(*nact, cap)) return;
   const double r = pr[p];
   const double xb = exp(-gamma * r);
   double t = 0.0;
   if (lane < R && xb > 1e-6 && xb < 1.0 - 1e-6) {
-    const std::size_t i = std::size_t(q) * R + lane;
+    const std::size_t i = std::size_t(p) * R + lane;
     t = grbf[i] * rbf[i] * (-gamma * kk[lane] + gamma * xb / (1.0 - xb) * kr[lane]);
   }
   t = wsum(t);
@@ -980,7 +1209,7 @@ enum Buf {
   XS = 0, EVS, QKV, QKIS, AEV, N1, N1HAT, N1IS, HPRE, TOUT, PRE2HAT, PRE2IS,
   ACT, HID, CAT, HACT, HHPRE, HKEY, GHEAD,
   GX, GEV, GT, GCAT, GA, GP, GHID, GN1, GAINV, GQKV,
-  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF, CLS_M, CLS_B, RBF_S,
+  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF, CLS_M, CLS_B,
   NBUF
 };
 static_assert(NBUF <= GenericPath::kBuffers, "generic path buffer table");
@@ -1040,34 +1269,6 @@ void gemm(hipStream_t s, int rows, const int *rows_dev, int K, int O, const doub
   if (res) R.res = res + c0;
   launch(R, 1, (rest + 31) / 32);
 }
-// One GEMM per element-pair bucket (grid z over the C^2 keys, the empty
-// ones exiting at once): rows of bucket z from row start[z], count[z] of
-// them; the weight of bucket z at z wbs, its bias at z bbs.  O a multiple of
-// 32 kGemmMaxNT or at most that.
-template <int EPI, bool WKO>
-void gemm_buckets(hipStream_t s, int nz, int cap, const int *count, const int *start, int K, int O, const double *X,
-                  int ldx, const double *W, long wbs, const double *bias, long bbs, double *Y, int ldy,
-                  const double *aux = nullptr, int ldaux = 0) {
-  if (cap <= 0) return;
-  GemmArgs A{cap, nullptr, K, O, X, ldx, W, bias, Y, ldy, nullptr, 0, aux, ldaux, nullptr, 0,
-             1, 0, 0, 0, 0, 0, 0, wbs, 0};
-  A.zcount = count;
-  A.zstart = start;
-  A.bbs = bbs;
-  const int cmax = 32 * kGemmMaxNT, nb = (O + cmax - 1) / cmax, cols = (O + nb - 1) / nb;
-  const unsigned gx = blocks_for(std::size_t(cap), 64);
-  const dim3 grid(nb > 1 ? (gx + 7) / 8 * 8 : gx, unsigned(nb), unsigned(nz));
-  const int tiles = (cols + 31) / 32;
-#define G_GEMM_NT(NT)                                                              \
-  if (tiles <= NT) {                                                               \
-    hipLaunchKernelGGL((g_gemm<EPI, WKO, NT>), grid, dim3(256), 0, s, A);          \
-    return;                                                                        \
-  }
-  G_GEMM_NT(2) G_GEMM_NT(4)
-#undef G_GEMM_NT
-  throw std::logic_error("SO3LR: generic bucket GEMM wider than one column block");
-}
-
 // Per-head 32 x 32 projections as one batched launch (O = K = 32).
 template <int EPI, bool WKO>
 void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int ldx, long xbs0, long xbs1,
@@ -1082,9 +1283,64 @@ void gemm_heads(hipStream_t s, int rows, int nby, int nbx, const double *X, int 
 }  // namespace
 
 namespace {
-// run f, under c.timed when the evaluator is timing kernels
 bool cls_on(const GContext &c) { return c.cls_C > 0; }
 
+// Slots of block 0's element-pair order, at most: every nonempty bucket
+// padded by fewer than kB0Pad
+std::size_t b0_slot_bound(const GContext &c) {
+  return std::size_t(std::max(c.cap, 1)) + std::size_t(GContext::kB0Pad) * c.cls_C * c.cls_C;
+}
+
+// g_b0_fwd / g_b0_bwd at F = 16 FT, R = 16 RT over `slots` slots (one
+// wavefront per 16 CT)
+template <bool FWD>
+void launch_b0(hipStream_t s, int F, int R, std::size_t slots, const B0Args &A) {
+  constexpr int CT = FWD ? SO3LR_B0_FWD_CT : SO3LR_B0_BWD_CT;
+  static_assert(GContext::kB0Pad % (16 * CT) == 0, "a wavefront's slots lie in one bucket");
+  const dim3 grid(blocks_for(slots, 64 * CT));
+#define G_B0(FT, RT)                                                                        \
+  if (F == 16 * FT && R == 16 * RT) {                                                       \
+    if constexpr (FWD) hipLaunchKernelGGL((g_b0_fwd<FT, RT, CT>), grid, dim3(256), 0, s, A); \
+    else hipLaunchKernelGGL((g_b0_bwd<FT, RT, CT>), grid, dim3(256), 0, s, A);              \
+    return;                                                                                 \
+  }
+  G_B0(8, 2) G_B0(8, 4) G_B0(16, 2) G_B0(16, 4)
+#undef G_B0
+  throw std::logic_error("SO3LR: block 0's table kernels at widths other than F = 128, 256 and R = 32, 64");
+}
+
+// block 0's table kernels' arguments (the reverse adds its inputs and dr)
+B0Args b0_args(const GContext &c, const GBlock &B, const GHeads &H, const double *rbf, const double *tables,
+               const double *cb, int F, double *palpha) {
+  const std::size_t NK = std::size_t(c.cls_C) * c.cls_C;
+  B0Args A{};
+  A.slots = c.cls_slots;
+  A.order = c.cls_order;
+  A.pa = c.pa;
+  A.z = c.z;
+  A.cls = c.cls_lut;
+  A.C = c.cls_C;
+  A.pr = c.pr;
+  A.rbf = rbf;
+  for (int w = 0; w < 2; ++w) {
+    A.w0p[w] = B.w0p[w];
+    A.w0tp[w] = B.w0tp[w];
+    A.b0a[w] = B.b0a[w];
+  }
+  A.tf = tables;
+  A.tr = tables + NK * 32 * std::size_t(F);
+  A.cb = cb;
+  A.exp2_256 = H.exp2_256;
+  A.kk = H.rbf_k;
+  A.kr = H.rbf_kr;
+  A.gamma = c.gamma;
+  A.rc = c.rc;
+  A.inv_avg = c.inv_avg;
+  A.palpha = palpha;
+  return A;
+}
+
+// run f, under c.timed when the evaluator is timing kernels
 void section(const GContext &c, const char *name, const std::function<void()> &f) {
   if (c.timed) c.timed(name, f);
   else f();
@@ -1141,6 +1397,13 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
       const std::string f = p + (k == 0 ? "filter_net_inv." : "filter_net_ev.");
       B.w0[k] = up(m.f64(f + "mlp_rbf.0.weight", {F, R}));
       B.b0[k] = up(m.f64(f + "mlp_rbf.0.bias", {F}));
+      B.w0p[k] = B.w0tp[k] = B.b0a[k] = nullptr;
+      if (b == 0) {  // g_b0_fwd, g_b0_bwd
+        const auto w0 = m.f64(f + "mlp_rbf.0.weight", {F, R});
+        B.w0p[k] = up(permute_mfma(w0, F, R));
+        B.w0tp[k] = up(permute_mfma(transpose(w0, F, R), R, F));
+        B.b0a[k] = up(bias_acc(m.f64(f + "mlp_rbf.0.bias", {F}), F));
+      }
       B.w1[k] = up(m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.weight", {F, F}));
       B.b1[k] = up(m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F}));
       B.e0[k] = up(m.f64(f + "mlp_ev.0.weight", {FH, NH}));
@@ -1215,9 +1478,12 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
   const auto kr = m.i64("model.radial_embedding.radial_basis_fn.k_rev", {R});
   hw_.rbf_k = up(std::vector<double>(kk.begin(), kk.end()));
   hw_.rbf_kr = up(std::vector<double>(kr.begin(), kr.end()));
+  std::vector<double> t(256);
+  for (int j = 0; j < 256; ++j) t[std::size_t(j)] = double(std::exp2(static_cast<long double>(j) / 256.0L));
+  hw_.exp2_256 = up(t);
 }
 
-void GenericPath::carve(int N, int cap, const std::function<double *(int, std::size_t)> &take) {
+void GenericPath::carve(int N, int cap, int C, const std::function<double *(int, std::size_t)> &take) {
   const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1)), L = std::size_t(layers_);
   const std::size_t F = std::size_t(d_.F), E = std::size_t(d_.E), NH = std::size_t(d_.NH), NI = std::size_t(d_.NI),
                     R = std::size_t(d_.R), FH = std::size_t(d_.FH), HO = std::size_t(d_.HO);
@@ -1228,10 +1494,9 @@ void GenericPath::carve(int N, int cap, const std::function<double *(int, std::s
       n * F, n * E, n * NI, n * NI, n * E, n * F, n * F, n * F, n * F, n * 5 * F,
       P * R, L * P * NH, L * P * 2 * F, L * P * 4 * NH, P * (F + FH), P * (F + FH), P * 2 * F, P * 4 * NH,
       P, P * NH, P * R,
-      // block 0's element-pair tables: 2 filters x C^2 keys x 2 NH rows
-      // (C^2 NH <= F: class_tables_pay) of F, their biases, and block 0's
-      // basis rows in element-pair order
-      4 * F * F, 4 * F, P * R};
+      // block 0's element-pair tables (g_cls_tables): per filter and key the
+      // rows as 16 x F operands of both orientations, and their biases
+      std::size_t(C) * C * 64 * F, std::size_t(C) * C * 4 * NH};
   for (int i = 0; i < NBUF; ++i) b_[i] = take(i, sizes[i]);
 }
 
@@ -1249,10 +1514,7 @@ void GenericPath::forward(const GContext &c) {
                        (*c.x0l)[0], c.x0);
   hipLaunchKernelGGL(g_fill, dim3(blocks_for(n * E, 256)), dim3(256), 0, s, evs, n * E);
   hipLaunchKernelGGL(g_rbf, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, c.gamma, hw_.rbf_b, hw_.rbf_k,
-                     hw_.rbf_kr, b_[RBF], nullptr);
-  if (cls_on(c))  // block 0's, in element-pair order
-    hipLaunchKernelGGL(g_rbf, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, c.gamma, hw_.rbf_b, hw_.rbf_k,
-                       hw_.rbf_kr, b_[RBF_S], c.cls_order);
+                     hw_.rbf_kr, b_[RBF]);
   for (int b = 0; b < layers_; ++b) {
     const GBlock &B = bw_[b];
     double *xb = xs + b * n * F, *evb = evs + b * n * E;
@@ -1269,26 +1531,14 @@ void GenericPath::forward(const GContext &c) {
                          b_[QKIS] + b * n * 4 * NH);
     const int HW = F + FH;
     if (b == 0 && cls_on(c)) {
-      // block 0 through the element-pair tables: per filter the hidden row
-      // silu(W0 rbf + b0), its products with the table rows (one GEMM, the
-      // logits' constants as its bias) into block 0's filter-row buffer,
-      // and the logits picked from them
-      // (in element-pair order: the basis rows RBF_S, the hidden rows, one
-      // GEMM per bucket against its 2 NH table rows)
-      const int C = c.cls_C, NK = C * C, K2 = 2 * NH;
-      hipLaunchKernelGGL(g_cls_tables, dim3(unsigned(NK * K2), 2), dim3(unsigned(F)), 0, s, F, NH, FH, C, qb,
+      // block 0 through the element-pair tables: their rows as MFMA
+      // operands, then both filters to the logits in one fused kernel
+      const std::size_t NK = std::size_t(c.cls_C) * c.cls_C;
+      hipLaunchKernelGGL(g_cls_tables, dim3(unsigned(NK * 16), 2), dim3(unsigned(F)), 0, s, F, NH, FH, c.cls_C, qb,
                          c.cls_rep, B.wcat[0], B.wcat[1], B.bcat[0], B.bcat[1], B.eb0[0], B.eb0[1], b_[CLS_M],
-                         b_[CLS_B]);
-      section(c, "generic_filter_fwd_block0_tables", [&] {
-        for (int w = 0; w < 2; ++w) {
-          gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF_S], R, B.w0[w], B.b0[w], b_[HT], HW);
-          gemm_buckets<EPI_STORE, false>(s, NK, cap, c.cls_count, c.cls_start, F, K2, b_[HT], HW,
-                                         b_[CLS_M] + std::size_t(w) * NK * K2 * F, long(K2) * F,
-                                         b_[CLS_B] + std::size_t(w) * NK * K2, K2, pfb, K2);
-          hipLaunchKernelGGL(g_alpha_cls, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, NH, c.nact, cap,
-                             c.cls_order, c.pa, c.z, c.cls_lut, pfb, w, c.inv_avg, pab);
-        }
-      });
+                         b_[CLS_M] + NK * 32 * F, b_[CLS_B]);
+      section(c, "generic_filter_fwd_block0_tables",
+              [&] { launch_b0<true>(s, F, R, b0_slot_bound(c), b0_args(c, B, hw_, b_[RBF], b_[CLS_M], b_[CLS_B], F, pab)); });
     } else {
     // pair invariants and both filters (kokkos_integrated_block0.cpp:166-255)
     hipLaunchKernelGGL(g_pair_inv, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, evb,
@@ -1378,26 +1628,15 @@ void GenericPath::reverse(const GContext &c) {
     // (df [W1 | E1]) (.) silu'(pre) in one GEMM, then through W0 and E0
     const int HW = F + FH;
     if (tables) {
-      // block 0 through the element-pair tables: per filter the
-      // pre-activation again, d hidden = (coefficients x table rows) (.)
-      // silu'(pre) in one GEMM, then through W0 (s has no adjoint in block 0)
-      // (in element-pair order, as the forward; dE/dr through the basis
-      // rows of that order)
-      const int C = c.cls_C, NK = C * C, K2 = 2 * NH;
-      section(c, "generic_filter_bwd_block0_tables", [&] {
-        for (int w = 0; w < 2; ++w) {
-          gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF_S], R, B.w0[w], B.b0[w], b_[HT], HW);
-          hipLaunchKernelGGL(g_cls_coef, dim3(blocks_for(P * K2, 256)), dim3(256), 0, s, NH, c.nact, cap,
-                             c.cls_order, c.pa, c.z, c.cls_lut, b_[PSC], w, b_[DF]);
-          gemm_buckets<EPI_DSILU, true>(s, NK, cap, c.cls_count, c.cls_start, K2, F, b_[DF], K2,
-                                        b_[CLS_M] + std::size_t(w) * NK * K2 * F, long(K2) * F, nullptr, 0, b_[GH],
-                                        HW, b_[HT], HW);
-          if (w == 0)
-            gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-          else
-            gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-        }
-      });
+      // block 0 through the element-pair tables, fused: the hidden rows'
+      // adjoints from the table rows, through W0 to dE/dr (the spherical
+      // input s has no adjoint in block 0)
+      B0Args A = b0_args(c, B, hw_, b_[RBF], b_[CLS_M], b_[CLS_B], F, pab);
+      A.psc = b_[PSC];
+      A.dfc = b_[DFC];
+      A.dr = c.dr;
+      section(c, "generic_filter_bwd_block0_tables",
+              [&] { launch_b0<false>(s, F, R, b0_slot_bound(c), A); });
     } else {
       section(c, "generic_filter_bwd", [&] {
         for (int w = 0; w < 2; ++w) {
@@ -1414,10 +1653,9 @@ void GenericPath::reverse(const GContext &c) {
           }
         }
       });
+      hipLaunchKernelGGL(g_pair_radial_bwd, dim3(blocks_for(P, 4)), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC],
+                         b_[GRBF], b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
     }
-    hipLaunchKernelGGL(g_pair_radial_bwd, dim3(blocks_for(P, 4)), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC],
-                       b_[GRBF], tables ? b_[RBF_S] : b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr,
-                       tables ? c.cls_order : nullptr);
     // the adjoints of the block's inputs feed the block below; block 0's
     // inputs (embedding, ev = 0) do not depend on the positions
     if (b > 0) {

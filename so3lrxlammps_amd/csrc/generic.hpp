@@ -48,6 +48,9 @@ struct GBlock {
   // both output layers side by side, (F, F + FH): [W1 | E1], and b1 + eb1,
   // so one GEMM over the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)]
   const double *wcat[2], *bcat[2];
+  // block 0's radial layer as MFMA operands (permute_mfma): W0 (F x R), W0^T
+  // (R x F), b0 in accumulator order (bias_acc); null in later blocks
+  const double *w0p[2], *w0tp[2], *b0a[2];
   const double *att_cg, *int_cg;                  // (E)
   const double *ln1w, *ln1b, *ln2w, *ln2b;        // (F); RMSNorm and none: 1 and 0
   const double *m1, *m1b, *m2, *m2b;              // (F, F) (F)
@@ -65,6 +68,7 @@ struct GHeads {
   const double *hqemb, *hvshift;  // (100, 64) (100)
   const double *cqemb, *cvshift;  // C6 head's (or null)
   const double *rbf_b, *rbf_k, *rbf_kr;  // (R)
+  const double *exp2_256;                // 2^(j/256), j < 256 (exp_tab)
 };
 
 // What one evaluation hands the generic path: the shared inputs (active
@@ -97,9 +101,11 @@ struct GContext {
   // first atom (device)
   int cls_C = 0;
   const int *cls_lut = nullptr, *cls_rep = nullptr;
-  // the active pairs in element-pair order (slot q holds pair cls_order[q])
-  // and each element-pair bucket's count and first slot (key min C + max)
-  const int *cls_order = nullptr, *cls_count = nullptr, *cls_start = nullptr;
+  // the active pairs in element-pair order (key min C + max), each bucket
+  // padded with -1 to a multiple of kB0Pad slots: slot q holds pair
+  // cls_order[q], the slots end at *cls_slots (device)
+  const int *cls_order = nullptr, *cls_slots = nullptr;
+  static constexpr int kB0Pad = 32;
 };
 
 class GenericPath {
@@ -110,18 +116,13 @@ class GenericPath {
   int F() const { return d_.F; }
   // The work buffers of one evaluation: take(id, doubles) returns buffer id's
   // memory (the evaluator's retained buffers or scratch slices).
+  // C: the element classes of block 0's tables (0: none)
   static constexpr int kBuffers = 48;
-  void carve(int N, int cap, const std::function<double *(int, std::size_t)> &take);
+  void carve(int N, int cap, int C, const std::function<double *(int, std::size_t)> &take);
   // Blocks and heads forward (to the heads' outputs), then, after the
   // evaluator's long-range step, heads and blocks in reverse.
   void forward(const GContext &c);
   void reverse(const GContext &c);
-  // Whether block 0 can take the element-pair tables for C classes and cap
-  // active pairs: their GEMMs have C^2 NH columns, the filters' output GEMM F
-  // (and F + F/4 deep); the coefficient rows are indexed in 32 bits
-  bool class_tables_pay(int C, std::int64_t cap) const {
-    return C > 0 && C * C * d_.NH <= d_.F && cap * C * C * d_.NH / 4 < (std::int64_t(1) << 31);
-  }
 
  private:
   GDims d_{};

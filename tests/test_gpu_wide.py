@@ -75,8 +75,8 @@ def test_lift_on_the_gpu_equals_the_v1_model(models):
                                         ("deg1123", "acetate")])
 def test_wide_block0_element_tables_match_full_filters(monkeypatch, models, model, name):
     """Block 0 through the element-pair tables on the generic kernels (one
-    image, C^2 NH <= F: 2, 4 and 3 elements here) against the full filter
-    GEMMs (SO3LR_NO_CLASS_TABLES=1): equal to rounding."""
+    image: 2, 4 and 3 elements here) against the full filter GEMMs
+    (SO3LR_NO_CLASS_TABLES=1): equal to rounding."""
     from so3lrxlammps_amd import Context
     ref, z, pos, box = support.load_golden(name)
     q, m = ref.get("charge", 0), ref.get("multiplicity", 1)
@@ -91,6 +91,42 @@ def test_wide_block0_element_tables_match_full_filters(monkeypatch, models, mode
     assert abs(e1 - e2) <= 1e-12 * abs(e2)
     assert np.abs(f1 - f2).max() <= 1e-10 * max(1.0, np.abs(f2).max() / 10.0)
     assert np.abs(w1 - w2).max() <= 1e-10 * max(1.0, np.abs(w2).max())
+
+
+@pytest.mark.parametrize("count", [16, 17])
+def test_wide_element_table_limit(monkeypatch, models, count):
+    """The generic kernels at the table path's limit (perturbed lift, a
+    240-atom cluster): 16 elements (136 element pairs) run block 0 through
+    the tables, equal to the full filters to rounding; 17 fall back to the
+    full filters, bit for bit the SO3LR_NO_CLASS_TABLES=1 result; both
+    against the oracle."""
+    from so3lrxlammps_amd import Context, Lists
+    from test_gpu_parity import _ELEMENTS17, _cluster
+    z, pos, mult = _cluster(_ELEMENTS17[:count])
+    print("case lift_perturbed cluster of %d elements" % count, flush=True)
+    lists = Lists(pos, pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0))
+    res = []
+    for off in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NO_CLASS_TABLES", off)
+        c = Context(models["lift_perturbed"], 0)
+        c.set_system(z, 0, mult)
+        c.set_topology(lists)
+        e, f, ea, w = c.compute(lists.rows_positions(pos))
+        res.append((e, f.copy(), w.copy()))
+        c.close()
+    (e1, f1, w1), (e2, f2, w2) = res
+    print("%d elements: |dE| %.2e max|dF| %.2e" % (count, abs(e1 - e2), np.abs(f1 - f2).max()), flush=True)
+    if count == 17:
+        assert e1 == e2 and np.array_equal(f1, f2) and np.array_equal(w1, w2)
+    else:
+        assert abs(e1 - e2) <= 1e-12 * abs(e2)
+        assert np.abs(f1 - f2).max() <= 1e-10 * max(1.0, np.abs(f2).max() / 10.0)
+    out = Oracle(models["lift_perturbed"]).evaluate(z, *support.build_graphs(pos, None), charge=0,
+                                                    multiplicity=mult)
+    ftol = 1e-9 * max(1.0, np.abs(out["forces"]).max() / 10.0)
+    assert abs(e2 - out["energy"]) <= 1e-10 * abs(out["energy"])
+    assert np.abs(f2 - out["forces"]).max() <= ftol
+    assert np.abs(w2 - out["virial"]).max() <= 1e-9 * max(1.0, np.abs(out["virial"]).max())
 
 
 def test_wide_device_path_and_replay(models):
