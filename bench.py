@@ -119,8 +119,9 @@ def kernel_work(widths, elements=0):
     generic kernels: per active pair and block, both filters, algorithmic
     2 (R F + NH F/4 + (F + F/4) F) MAC each way; the reverse also issues the
     hidden row's recompute (R F + NH F/4).  Block 0 through the element-pair
-    tables (`elements` = C classes): 2 (R F + C^2 NH F) MAC each way, the
-    reverse issuing R F more."""
+    tables (`elements` > 0: g_b0_fwd, g_b0_bwd): 2 (R F + 2 NH F) MAC each
+    way; the forward issues the table rows padded to 16 (16 F), the reverse
+    R F more for the recompute."""
     work = dict(KERNEL_WORK)
     F, R = widths["invariant_features"], widths["radial_basis_features"]
     NH, FH = len(widths["degree_slots"]), widths["invariant_features"] // 4
@@ -129,10 +130,10 @@ def kernel_work(widths, elements=0):
     work["generic_filter_bwd"] = ("g_gemm: filter reverse section (both filters)", "mfma", alg,
                                   alg + 2 * 2 * (R * F + NH * FH), "pair")
     if elements:
-        tab = 2 * 2 * (R * F + elements * elements * NH * F)
-        work["generic_filter_fwd_block0_tables"] = ("g_gemm: block 0's table forward section", "mfma", tab, tab,
-                                                    "pair")
-        work["generic_filter_bwd_block0_tables"] = ("g_gemm: block 0's table reverse section", "mfma", tab,
+        tab = 2 * 2 * (R * F + 2 * NH * F)
+        work["generic_filter_fwd_block0_tables"] = ("g_b0_fwd: block 0's fused table filters", "mfma", tab,
+                                                    2 * 2 * (R * F + 16 * F), "pair")
+        work["generic_filter_bwd_block0_tables"] = ("g_b0_bwd: block 0's fused table filters, reverse", "mfma", tab,
                                                     tab + 2 * 2 * R * F, "pair")
     return work
 

@@ -69,11 +69,6 @@ struct GemmArgs {
   int nbx;
   long xbs0, xbs1, ybs0, ybs1, rbs0, rbs1, wbs;
   int ldw;  // WKO: the weight's row length (its full output width); 0: O
-  // ragged batches (grid z): batch z takes zcount[z] rows from row zstart[z]
-  // of X, Y, Y2, aux and res (device counts; rows caps them), its weight at
-  // z wbs and its bias at z bbs
-  const int *zcount = nullptr, *zstart = nullptr;
-  long bbs = 0;
 };
 
 typedef double gv4d __attribute__((ext_vector_type(4)));
@@ -97,18 +92,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_GEMM_
   constexpr int WPT = BN / 16;     // W chunk values per thread (BN x 16 / 256)
   __shared__ double xs[64][17];
   __shared__ double ws[BN][17];
-  int rows = A.rows_dev ? min(*A.rows_dev, A.rows) : A.rows;
-  if (A.zcount) {
-    const int z = blockIdx.z;
-    rows = min(A.zcount[z], A.rows);
-    const long st = A.zstart[z];
-    A.X += st * A.ldx;
-    A.Y += st * A.ldy;
-    if (A.Y2) A.Y2 += st * A.ldy2;
-    if (A.aux) A.aux += st * A.ldaux;
-    if (A.res) A.res += st * A.ldres;
-    if (A.bias) A.bias += long(z) * A.bbs;
-  }
+  const int rows = A.rows_dev ? min(*A.rows_dev, A.rows) : A.rows;
   // With several column blocks the grid's x is a multiple of 8 and the
   // blocks are taken in dispatch order, (row block, column block) such that
   // the column blocks of one row block run one after another on one XCD
