@@ -126,8 +126,8 @@ def kernel_work(widths, elements=0):
     F, R = widths["invariant_features"], widths["radial_basis_features"]
     NH, FH = len(widths["degree_slots"]), widths["invariant_features"] // 4
     alg = 2 * 2 * (R * F + NH * FH + (F + FH) * F)
-    work["generic_filter_fwd"] = ("g_gemm: filter forward section (both filters)", "mfma", alg, alg, "pair")
-    work["generic_filter_bwd"] = ("g_gemm: filter reverse section (both filters)", "mfma", alg,
+    work["generic_filter_fwd"] = ("g_filt_fwd: both filters and the logits, fused", "mfma", alg, alg, "pair")
+    work["generic_filter_bwd"] = ("g_filt_bwd: both filters' reverse, fused", "mfma", alg,
                                   alg + 2 * 2 * (R * F + NH * FH), "pair")
     if elements:
         tab = 2 * 2 * (R * F + 2 * NH * F)
@@ -537,7 +537,7 @@ def main():
     work = kernel_work(model_widths(MODEL), elements=len(set(int(v) for v in z)))
     for name in ("filter_fwd", "filter_fwd_block0", "filter_fwd_block0_tables", "filter_bwd", "filter_bwd_block0",
                  "filter_bwd_block0_tables", "attn_fwd", "attn_bwd",
-                 "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd", "generic_alpha",
+                 "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd",
                  "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables"):
         try:
             timing[name] = md.ctx.kernel_timing_read(name)

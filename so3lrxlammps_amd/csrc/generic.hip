@@ -15,6 +15,7 @@
 #include "mfma_ops.hpp"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <stdexcept>
 #include <string>
@@ -707,51 +708,14 @@ __device__ __forceinline__ double half_sums(double (&v)[M], int lane) {
   return v[0];
 }
 
-// Attention logits per pair, direction and head (kokkos_integrated_block0.cpp:330-360):
-// alpha = <q_receiver, k_sender (.) f> / norm (inv: q k f_inv, ev: q_ev k_ev
-// f_ev).  One wavefront per pair, lanes over channels (channel lane + 64 j is
-// in head 2 j + lane / 32, J = F / 64 channels per lane); the 4 J products
-// of a lane (direction, filter, j) are summed per head by half_sums.
-template <int J>
-__global__ __launch_bounds__(256) void g_alpha(GDims d, const int *nact, int cap, const int *__restrict__ pa,
-                                               const double *__restrict__ qkv, const double *__restrict__ pf,
-                                               double inv_avg, double *__restrict__ palpha) {
-  const int lane = threadIdx.x & 63;
-  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (p >= min(*nact, cap)) return;
-  const int NH = d.NH, F = d.F;
-  const double *ra = qkv + std::size_t(pa[2 * p]) * 5 * F, *rb = qkv + std::size_t(pa[2 * p + 1]) * 5 * F;
-  const double *f = pf + std::size_t(p) * 2 * F;
-  constexpr int M = 4 * J;
-  double v[M];
-#pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const int qo = w ? 3 * F : 0, ko = w ? 4 * F : F;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int c = lane + 64 * j;
-      const double fc = f[w * F + c];
-      v[(0 * 2 + w) * J + j] = ra[qo + c] * rb[ko + c] * fc;  // direction 0: a receives from b
-      v[(1 * 2 + w) * J + j] = rb[qo + c] * ra[ko + c] * fc;  // direction 1: b receives from a
-    }
-  }
-  const double t = half_sums<M>(v, lane);
-  constexpr int LOG = J == 2 ? 3 : 4, RUN = 32 >> LOG;
-  if ((lane % RUN) == 0) {
-    const int m = (lane & 31) / RUN, j = m % J, w = (m / J) % 2, side = m / (2 * J);
-    const int h = 2 * j + (lane >> 5);
-    palpha[std::size_t(p) * 4 * NH + side * 2 * NH + w * NH + h] = t * inv_avg;
-  }
-}
-
 // Attention reverse, pair side (kokkos_attention_scatter_reverse.cpp:280-500),
 // one wavefront per pair, both directions: with r the receiver and s the
 // sender of a direction,
 //   ci_h = <gainv_r, v_s>_head h,  ce_h = <gaev_r, Y'>_slot h  (Y' the
 //   direction's harmonics), psc = fc c norm (the logits' adjoints, kept for
-//   the node gathers), dE/dfc = sum ci alpha + ce alpha_ev,
-//   df = sum_dir psc q_r k_s (inv) and psc_ev q_ev_r k_ev_s (ev): the shared
-//   filter's adjoint,
+//   the node gathers and the filters' reverse, which forms the filter
+//   adjoint df = sum_dir psc q_r k_s (inv) and psc_ev q_ev_r k_ev_s (ev)),
+//   dE/dfc = sum ci alpha + ce alpha_ev,
 //   dE/dY_m = sum_dir sum_{c: sh(c) = m} gaev_r,c fc alpha_ev par (side-0
 //   orientation); the first reverse block writes dY, the others add.
 // The head sums ci come from half_sums over the 2 J products of a lane
@@ -765,8 +729,8 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
                                                         const double *__restrict__ palpha,
                                                         const double *__restrict__ gainv,
                                                         const double *__restrict__ ga, double inv_avg, int first,
-                                                        double *__restrict__ psc, double *__restrict__ df,
-                                                        double *__restrict__ dY, double *__restrict__ dfc) {
+                                                        double *__restrict__ psc, double *__restrict__ dY,
+                                                        double *__restrict__ dfc) {
   __shared__ double lt[4][2][kGMaxE];   // per wavefront: dE/dY terms per direction and channel
   __shared__ double lte[4][2][kGMaxE];  // per wavefront: gaev_r Y' per direction and channel
   __shared__ double lps[4][32];         // per wavefront: psc of the pair
@@ -815,18 +779,6 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
   if (lane == 0) dfc[p] = dsum;
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   if (lane < 4 * NH) psc[std::size_t(p) * 4 * NH + lane] = lps[wv][lane];
-  // (block 0 on the element-table path needs psc only: no df)
-  for (int c = lane; df && c < 2 * F; c += 64) {
-    const int which = c / F, cc = c % F, h = cc >> 5;
-    double acc = 0.0;
-    for (int side = 0; side < 2; ++side) {
-      const int rcv = pa[2 * p + side], snd = pa[2 * p + 1 - side];
-      const double qv = qkv[std::size_t(rcv) * 5 * F + (which ? 3 * F : 0) + cc];
-      const double kv = qkv[std::size_t(snd) * 5 * F + (which ? 4 * F : F) + cc];
-      acc += lps[wv][side * 2 * NH + which * NH + h] * qv * kv;
-    }
-    df[std::size_t(p) * 2 * F + c] = acc;
-  }
   if (lane < 24) {
     double acc = 0.0;
     for (int side = 0; side < 2; ++side)
@@ -1155,31 +1107,399 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
-// dE/dr of the pair from the cutoff and the radial basis; one wavefront per
-// pair, lanes over the basis (R <= 64).
-__global__ __launch_bounds__(256) void g_pair_radial_bwd(int R, const int *nact, int cap, const double *__restrict__ pr,
-                                                         const double *__restrict__ dfc, const double *__restrict__ grbf,
-                                                         const double *__restrict__ rbf, const double *__restrict__ kk,
-                                                         const double *__restrict__ kr, double gamma, double rc,
-                                                         double *__restrict__ dr) {
-  const int lane = threadIdx.x & 63;
-  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (p >= min(*nact, cap)) return;
-  const double r = pr[p];
-  const double xb = exp(-gamma * r);
-  double t = 0.0;
-  if (lane < R && xb > 1e-6 && xb < 1.0 - 1e-6) {
-    const std::size_t i = std::size_t(p) * R + lane;
-    t = grbf[i] * rbf[i] * (-gamma * kk[lane] + gamma * xb / (1.0 - xb) * kr[lane]);
+// ------------------------------------------------------ fused filters
+// Both filters of a block for 16 pairs per wavefront, on fp64 MFMA in the
+// layout of the table kernels above (features as rows, the pairs as the 16
+// columns, a tile's D registers the next layer's B operand)
+// (kokkos_integrated_block0.cpp:198-255 forward,
+// kokkos_block2_attention_input_reverse.cpp:198-336 reverse).  FT = F / 16
+// hidden tiles of the radial branch and FT / 4 of the spherical one (FH =
+// F / 4), RT = R / 16 basis chunks, NH = FT / 2 slots.
+//   forward: the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)] (HT = FT +
+//            FT / 4 tiles) in registers, then f = [W1 | E1] hidden + b1 + e1
+//            one output tile at a time, stored as the pair's filter row;
+//   reverse: d hidden = [W1 | E1]^T df, df formed from the logits' adjoints
+//            and the endpoint rows as g_attn_bwd_pairs forms it, TG hidden
+//            tiles at a time; each group then times silu'(pre) (pre again)
+//            and through W0^T to the basis adjoint or E0^T to dE/ds; last
+//            dE/dr as g_pair_radial_bwd.
+struct FiltArgs {
+  const int *nact;
+  int cap;
+  const int *pa;
+  const double *pr, *rbf, *ps, *qkv;                                   // distance, basis rows, s, node rows
+  const double *w0p[2], *b0a[2], *e0p[2], *eb0a[2], *wcp[2], *bca[2];  // forward operands
+  const double *w0tp[2], *e0tp[2], *wctp[2];                           // reverse operands
+  const double *exp2_256, *kk, *kr;
+  double gamma, rc, inv_avg;
+  double *pf, *palpha;      // forward: filter rows (2 F per pair), logits (4 NH)
+  const double *psc, *dfc;  // reverse: the logits' and the cutoff's adjoints
+  double *ds, *dr;          // reverse: dE/ds (NH per pair), dE/dr (added to)
+};
+
+// Dispatch block b (round-robin over the 8 XCDs) to logical block: each XCD
+// takes a contiguous run of the `active` blocks, so consecutive pairs, which
+// share endpoints, share that XCD's L2.  -1: beyond the active blocks.  The
+// grid is a multiple of 8 and holds at least `active` blocks.
+__device__ __forceinline__ int g_xcd_block(int active) {
+  const int b = blockIdx.x;
+  const int per = active >> 3, rem = active & 7, xcd = b & 7, i = b >> 3;
+  if (i >= per + (xcd < rem ? 1 : 0)) return -1;
+  return xcd * per + (xcd < rem ? xcd : rem) + i;
+}
+
+#ifndef SO3LR_FILT_PF
+#define SO3LR_FILT_PF 6
+#endif
+
+// the lane's pair (padding lanes: the last active pair, valid false);
+// false: the wavefront has no pair
+__device__ __forceinline__ bool filt_pair(const FiltArgs &A, int j, int &pp, bool &valid) {
+  const int nact = min(*A.nact, A.cap);
+  const int blk = g_xcd_block((nact + 63) / 64);
+  if (blk < 0) return false;
+  const int wave = blk * 4 + int(threadIdx.x >> 6);
+  if (wave * 16 >= nact) return false;
+  const int p = wave * 16 + j;
+  valid = p < nact;
+  pp = valid ? p : nact - 1;
+  return true;
+}
+// the pair's basis values rb[Kc][v] = rbf_k (k = 16 Kc + g + 4 v) and
+// invariants sv[v] = s_{g + 4 v} (0 beyond NH), the B operands of the
+// hidden row's layer 0; loaded where each pass over the hidden row starts
+// (from L2 after the first), so they hold no registers in between
+template <int RT, int NH>
+__device__ __forceinline__ void filt_inputs(const FiltArgs &A, int pp, int g, v4d *rb, v4d &sv) {
+  // an opaque copy of the pair index: the loads of one pass are not merged
+  // with those of another (which would keep the values live throughout)
+  asm volatile("" : "+v"(pp));
+  const double *row = A.rbf + std::size_t(pp) * 16 * RT + g;
+#pragma unroll
+  for (int Kc = 0; Kc < RT; ++Kc)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) rb[Kc][v] = row[16 * Kc + 4 * v];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) sv[v] = g + 4 * v < NH ? A.ps[std::size_t(pp) * NH + g + 4 * v] : 0.0;
+}
+
+// One wavefront per SIMD: at two, F = 256 overflows the registers (the
+// hidden row alone takes 160); measured at config 3, F = 256: 3.56 ms per
+// block (logits included) against 5.11 ms at two wavefronts with spills.
+#ifndef SO3LR_FILT_FWD_WAVES
+#define SO3LR_FILT_FWD_WAVES 1
+#endif
+#ifndef SO3LR_FILT_PFB
+#define SO3LR_FILT_PFB 10
+#endif
+template <int FT, int RT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_FILT_FWD_WAVES, SO3LR_FILT_FWD_WAVES))) void
+g_filt_fwd(FiltArgs A) {
+  constexpr int FHT = FT / 4, NH = FT / 2, HT = FT + FHT, F = 16 * FT;
+  constexpr int NA = FT * (1 + RT) + 2 * FHT;  // hidden row: per tile the bias and its weight chunks
+  constexpr int NB = HT;                       // output tile: its HT weight chunks
+  constexpr int PFB = NB % SO3LR_FILT_PFB == 0 ? SO3LR_FILT_PFB : NB;
+  __shared__ double tab[256];
+  tab[threadIdx.x] = A.exp2_256[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  int pp = 0;
+  bool valid = false;
+  if (!filt_pair(A, j, pp, valid)) return;
+  const int a = A.pa[2 * pp], b = A.pa[2 * pp + 1];
+  // the output rows of [W1 | E1] come permuted within each tile (row 16 mt +
+  // i is channel 16 mt + 4 (i % 4) + i / 4), so register r of lane group g
+  // holds channel 16 mt + 4 g + r: a lane's four channels are contiguous
+  const double *ra = A.qkv + std::size_t(a) * 5 * F + 4 * g, *rr = A.qkv + std::size_t(b) * 5 * F + 4 * g;
+  double *frow = A.pf + std::size_t(pp) * 2 * F + 4 * g;
+  double *al = A.palpha + std::size_t(pp) * 4 * NH;
+  v4d h[HT];
+  static_for<2>([&](auto wi) {
+    constexpr int w = decltype(wi)::value;
+    const double *b0a = A.b0a[w], *w0p = A.w0p[w], *eb0a = A.eb0a[w], *e0p = A.e0p[w], *bca = A.bca[w],
+                 *wcp = A.wcp[w];
+    v4d rb[RT], sv;
+    filt_inputs<RT, NH>(A, pp, g, rb, sv);
+    auto la = [&](auto si) -> v4d {
+      constexpr int S = decltype(si)::value;
+      if constexpr (S < FT * (1 + RT)) {
+        constexpr int T = S / (1 + RT), u = S % (1 + RT);
+        if constexpr (u == 0) return frag_load(b0a, T, lane);
+        else return frag_load(w0p, T * RT + u - 1, lane);
+      } else {
+        constexpr int t = (S - FT * (1 + RT)) / 2, u = (S - FT * (1 + RT)) % 2;
+        if constexpr (u == 0) return frag_load(eb0a, t, lane);
+        else return frag_load(e0p, t, lane);
+      }
+    };
+    Stream<NA, SO3LR_FILT_PF, decltype(la)> sa(la);
+    sa.prime();
+    sa.run([&](auto si, const v4d &wv) {
+      constexpr int S = decltype(si)::value;
+      constexpr bool RAD = S < FT * (1 + RT);
+      constexpr int T = RAD ? S / (1 + RT) : FT + (S - FT * (1 + RT)) / 2;
+      constexpr int u = RAD ? S % (1 + RT) : (S - FT * (1 + RT)) % 2;
+      if constexpr (u == 0) {
+        h[T] = wv;
+      } else {
+        if constexpr (RAD) {
+          h[T] = mfma4(wv, rb[u - 1], h[T]);
+        } else {
+          h[T] = mfma(wv[0], sv[0], h[T]);
+          if constexpr (NH > 4) h[T] = mfma(wv[1], sv[1], h[T]);
+        }
+        // the tile before: its SiLU behind the MFMA just issued
+        if constexpr (u == 1 && T > 0) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (T - 1 < FT) h[T - 1][r] = silu_tab(h[T - 1][r], tab);
+            else h[T - 1][r] = silu_tab_wide(h[T - 1][r], tab);
+          }
+        }
+      }
+    });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) h[HT - 1][r] = silu_tab_wide(h[HT - 1][r], tab);
+    auto lb = [&](auto si, int mt) -> v4d { return frag_load(wcp, mt * HT + decltype(si)::value, lane); };
+    LoopStream<NB, PFB, decltype(lb)> sb(lb);
+    sb.prime();
+    constexpr int qo = w ? 3 * F : 0, ko = w ? 4 * F : F;  // q, k or q_ev, k_ev
+    v4d o, qa, kb, qb, ka, bn = frag_load(bca, 0, lane);  // bn: the next tile's bias
+    double t0 = 0.0, t1 = 0.0;  // the lane's part of the head's logits: a <- b, b <- a
+    sb.run(FT, [&](auto si, int mt, const v4d &wv) {
+      constexpr int u = decltype(si)::value;
+      if constexpr (u == 0) {
+        o = mfma4(wv, h[0], bn);
+        bn = frag_load(bca, min(mt + 1, FT - 1), lane);
+        // the endpoint rows at the tile's channels, used when it is complete
+        qa = *reinterpret_cast<const v4d *>(ra + qo + 16 * mt);
+        kb = *reinterpret_cast<const v4d *>(rr + ko + 16 * mt);
+        qb = *reinterpret_cast<const v4d *>(rr + qo + 16 * mt);
+        ka = *reinterpret_cast<const v4d *>(ra + ko + 16 * mt);
+      } else {
+        o = mfma4(wv, h[u], o);
+      }
+      if constexpr (u == NB - 1) {
+        if (valid) *reinterpret_cast<v4d *>(frow + w * F + 16 * mt) = o;
+        // alpha = <q_receiver, k_sender (.) f>_h / avg (kokkos_integrated_block0.cpp:330-360)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          t0 += qa[r] * kb[r] * o[r];
+          t1 += qb[r] * ka[r] * o[r];
+        }
+        if (mt & 1) {  // head mt / 2 complete: sum over the lane groups
+          t0 += __shfl_xor(t0, 16, 64);
+          t0 += __shfl_xor(t0, 32, 64);
+          t1 += __shfl_xor(t1, 16, 64);
+          t1 += __shfl_xor(t1, 32, 64);
+          if (valid && g == 0) {
+            al[w * NH + (mt >> 1)] = t0 * A.inv_avg;
+            al[2 * NH + w * NH + (mt >> 1)] = t1 * A.inv_avg;
+          }
+          t0 = 0.0;
+          t1 = 0.0;
+        }
+      }
+    });
+  });
+}
+
+// The reverse's second part for hidden tiles T0 .. T0 + TG - 1: per tile
+// its bias (kind 0), forward chunks (kind 1: W0 K chunks or E0) and, one
+// tile behind, the previous tile's transposed chunks (kind 2: W0^T row tiles
+// or E0^T), then the last tile's transposed chunks.
+struct FEntry {
+  int kind, T, k;
+};
+template <int FT, int RT>
+constexpr int filt_chunks(int T) { return T < FT ? RT : 1; }
+template <int FT, int RT, int T0, int TG>
+constexpr int filt_sched_len() {
+  int n = 0;
+  for (int T = T0; T < T0 + TG; ++T) n += 1 + filt_chunks<FT, RT>(T) + (T > T0 ? filt_chunks<FT, RT>(T - 1) : 0);
+  return n + filt_chunks<FT, RT>(T0 + TG - 1);
+}
+template <int FT, int RT, int T0, int TG>
+constexpr std::array<FEntry, filt_sched_len<FT, RT, T0, TG>()> filt_sched() {
+  std::array<FEntry, filt_sched_len<FT, RT, T0, TG>()> out{};
+  int n = 0;
+  for (int T = T0; T < T0 + TG; ++T) {
+    out[n++] = FEntry{0, T, 0};
+    for (int k = 0; k < filt_chunks<FT, RT>(T); ++k) out[n++] = FEntry{1, T, k};
+    if (T > T0)
+      for (int k = 0; k < filt_chunks<FT, RT>(T - 1); ++k) out[n++] = FEntry{2, T - 1, k};
   }
-  t = wsum(t);
-  if (lane == 0) {
-    double grad = t;
-    if (r < rc) {
-      const double u = r / rc;
-      grad += dfc[p] * (-30.0 * u * u * (1.0 - u) * (1.0 - u) / rc);
+  for (int k = 0; k < filt_chunks<FT, RT>(T0 + TG - 1); ++k) out[n++] = FEntry{2, T0 + TG - 1, k};
+  return out;
+}
+template <int FT, int RT, int T0, int TG>
+constexpr FEntry filt_entry(int s) {
+  return filt_sched<FT, RT, T0, TG>()[s];
+}
+
+// The whole hidden row's adjoint in one group (TG = HT, its accumulators in
+// the accumulation registers) at one wavefront per SIMD: measured at F = 256
+// (config 3) 4.59 ms per block against 5.72 for groups of 5 at two
+// wavefronts per SIMD, whose endpoint rows are read once per group.
+#ifndef SO3LR_FILT_TG
+#define SO3LR_FILT_TG 20
+#endif
+
+#ifndef SO3LR_FILT_BWD_WAVES
+#define SO3LR_FILT_BWD_WAVES 1
+#endif
+template <int FT, int RT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_FILT_BWD_WAVES, SO3LR_FILT_BWD_WAVES))) void
+g_filt_bwd(FiltArgs A) {
+  constexpr int FHT = FT / 4, NH = FT / 2, HT = FT + FHT, F = 16 * FT;
+  constexpr int TG = HT % SO3LR_FILT_TG == 0 ? SO3LR_FILT_TG : HT, NG = HT / TG;  // hidden tiles per group
+  constexpr int N1 = 4 + TG;  // per output tile: four endpoint rows, then TG weight chunks
+#ifndef SO3LR_FILT_PF1
+#define SO3LR_FILT_PF1 6
+#endif
+  constexpr int PF1 = N1 % SO3LR_FILT_PF1 == 0 ? SO3LR_FILT_PF1 : (N1 % 4 == 0 ? 4 : N1);
+  __shared__ double tab[256];
+  tab[threadIdx.x] = A.exp2_256[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  int pp = 0;
+  bool valid = false;
+  if (!filt_pair(A, j, pp, valid)) return;
+  const int a = A.pa[2 * pp], b = A.pa[2 * pp + 1];
+  const double *ra = A.qkv + std::size_t(a) * 5 * F + 4 * g, *rr = A.qkv + std::size_t(b) * 5 * F + 4 * g;
+  const double *ps = A.psc + std::size_t(pp) * 4 * NH;
+  const v4d zero = v4d{0.0, 0.0, 0.0, 0.0};
+  v4d drb[RT], dsa = zero;
+#pragma unroll
+  for (int Kc = 0; Kc < RT; ++Kc) drb[Kc] = zero;
+  // one filter at a time, a loop: unrolled, the two filters' code overflows
+  // the registers
+#pragma unroll 1
+  for (int w = 0; w < 2; ++w) {
+    const int qo = w ? 3 * F : 0, ko = w ? 4 * F : F;
+    const double *b0a = w ? A.b0a[1] : A.b0a[0], *w0p = w ? A.w0p[1] : A.w0p[0], *w0tp = w ? A.w0tp[1] : A.w0tp[0];
+    const double *eb0a = w ? A.eb0a[1] : A.eb0a[0], *e0p = w ? A.e0p[1] : A.e0p[0], *e0tp = w ? A.e0tp[1] : A.e0tp[0];
+    const double *wctp = w ? A.wctp[1] : A.wctp[0];
+    static_for<NG>([&](auto gi) {
+      constexpr int T0 = decltype(gi)::value * TG;
+      v4d dh[TG];
+#pragma unroll
+      for (int t = 0; t < TG; ++t) dh[t] = zero;
+      // d hidden (tiles T0..) = sum over output tiles mt of [W1 | E1]^T df_mt,
+      // df_mt = psc_0 q_a k_b + psc_1 q_b k_a at the lane's channels
+      // 16 mt + 4 g + v (side 0: a receives from b): [W1 | E1]^T comes with
+      // its K chunks in that order (permute_mfma_kc), so a lane's four
+      // channels of a row are one 32-byte load
+      auto l1 = [&](auto si, int mt) -> v4d {
+        constexpr int u = decltype(si)::value;
+        if constexpr (u < 4) {
+          const double *row = (u == 0 ? ra + qo : (u == 1 ? rr + ko : (u == 2 ? rr + qo : ra + ko))) + 16 * mt;
+          return *reinterpret_cast<const v4d *>(row);
+        } else {
+          return frag_load(wctp, (T0 + u - 4) * FT + mt, lane);
+        }
+      };
+      LoopStream<N1, PF1, decltype(l1)> s1(l1);
+      s1.prime();
+      double c0 = ps[w * NH], c1 = ps[2 * NH + w * NH];  // head 0
+      v4d qv, df;
+      s1.run(FT, [&](auto si, int mt, const v4d &wv) {
+        constexpr int u = decltype(si)::value;
+        if constexpr (u == 0 || u == 2) {
+          qv = wv;
+        } else if constexpr (u == 1) {
+          df = c0 * (qv * wv);
+        } else if constexpr (u == 3) {
+          df += c1 * (qv * wv);
+          // the coefficients of the next tile's head (a tile lies in one head)
+          const int hn = min(mt + 1, FT - 1) >> 1;
+          c0 = ps[w * NH + hn];
+          c1 = ps[2 * NH + w * NH + hn];
+        } else {
+          dh[u - 4] = mfma4(wv, df, dh[u - 4]);
+        }
+      });
+      // per tile: pre again, d hidden *= silu'(pre), then through W0^T / E0^T
+      v4d rb[RT], sv;
+      filt_inputs<RT, NH>(A, pp, g, rb, sv);
+      auto l2 = [&](auto si) -> v4d {
+        constexpr FEntry e = filt_entry<FT, RT, T0, TG>(decltype(si)::value);
+        if constexpr (e.kind == 0) {
+          if constexpr (e.T < FT) return frag_load(b0a, e.T, lane);
+          else return frag_load(eb0a, e.T - FT, lane);
+        } else if constexpr (e.kind == 1) {
+          if constexpr (e.T < FT) return frag_load(w0p, e.T * RT + e.k, lane);
+          else return frag_load(e0p, e.T - FT, lane);
+        } else {
+          if constexpr (e.T < FT) return frag_load(w0tp, e.k * FT + e.T, lane);
+          else return frag_load(e0tp, e.T - FT, lane);
+        }
+      };
+      constexpr int N2 = filt_sched_len<FT, RT, T0, TG>();
+      Stream<N2, SO3LR_FILT_PF, decltype(l2)> s2(l2);
+      s2.prime();
+      v4d pre[2];
+      auto dsilu = [&](auto ti) {
+        constexpr int T = decltype(ti)::value;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (T < FT) dh[T - T0][r] *= silu_prime_tab(pre[T % 2][r], tab);
+          else dh[T - T0][r] *= silu_prime_tab_wide(pre[T % 2][r], tab);
+        }
+      };
+      s2.run([&](auto si, const v4d &wv) {
+        constexpr FEntry e = filt_entry<FT, RT, T0, TG>(decltype(si)::value);
+        constexpr int T = e.T;
+        if constexpr (e.kind == 0) {
+          pre[T % 2] = wv;
+        } else if constexpr (e.kind == 1) {
+          if constexpr (T < FT) {
+            pre[T % 2] = mfma4(wv, rb[e.k], pre[T % 2]);
+          } else {
+            pre[T % 2] = mfma(wv[0], sv[0], pre[T % 2]);
+            if constexpr (NH > 4) pre[T % 2] = mfma(wv[1], sv[1], pre[T % 2]);
+          }
+          if constexpr (e.k == 0 && T > T0) dsilu(std::integral_constant<int, T - 1>{});
+        } else {
+          if constexpr (e.k == 0 && T == T0 + TG - 1) dsilu(std::integral_constant<int, T>{});
+          if constexpr (T < FT) drb[e.k] = mfma4(wv, dh[T - T0], drb[e.k]);
+          else dsa = mfma4(wv, dh[T - T0], dsa);
+        }
+      });
+    });
+  }
+  // dE/ds of the pair's slots (rows g + 4 r of the E0^T tile), summed over
+  // both filters
+  if (valid) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (g + 4 * r < NH) A.ds[std::size_t(pp) * NH + g + 4 * r] = dsa[r];
+  }
+  // dE/dr: the basis adjoint against d rbf / dr (zero where the basis
+  // variable is clamped), plus the cutoff's
+  const double r = A.pr[pp];
+  const double xb = exp(-A.gamma * r);
+  double part = 0.0;
+  if (xb > 1e-6 && xb < 1.0 - 1e-6) {
+    const double ratio = xb / (1.0 - xb);
+    const double *row = A.rbf + std::size_t(pp) * 16 * RT + g;
+#pragma unroll
+    for (int Kc = 0; Kc < RT; ++Kc)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int k = 16 * Kc + g + 4 * q;
+        part += drb[Kc][q] * row[k - g] * (-A.gamma * A.kk[k] + A.gamma * ratio * A.kr[k]);
+      }
+  }
+  part += __shfl_xor(part, 16, 64);
+  part += __shfl_xor(part, 32, 64);
+  if (valid && g == 0) {
+    double grad = part;
+    if (r < A.rc) {
+      const double t = r / A.rc;
+      grad += A.dfc[pp] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / A.rc);
     }
-    dr[p] += grad;
+    A.dr[pp] += grad;
   }
 }
 
@@ -1193,7 +1513,7 @@ enum Buf {
   XS = 0, EVS, QKV, QKIS, AEV, N1, N1HAT, N1IS, HPRE, TOUT, PRE2HAT, PRE2IS,
   ACT, HID, CAT, HACT, HHPRE, HKEY, GHEAD,
   GX, GEV, GT, GCAT, GA, GP, GHID, GN1, GAINV, GQKV,
-  RBF, PS, PF, PALPHA, HT, GH, DF, PSC, DFC, DS, GRBF, CLS_M, CLS_B,
+  RBF, PS, PF, PALPHA, PSC, DFC, DS, CLS_M, CLS_B,
   NBUF
 };
 static_assert(NBUF <= GenericPath::kBuffers, "generic path buffer table");
@@ -1293,6 +1613,54 @@ void launch_b0(hipStream_t s, int F, int R, std::size_t slots, const B0Args &A) 
   throw std::logic_error("SO3LR: block 0's table kernels at widths other than F = 128, 256 and R = 32, 64");
 }
 
+// g_filt_fwd / g_filt_bwd at F = 16 FT, R = 16 RT over cap pairs (one
+// wavefront per 16, the grid a multiple of 8: g_xcd_block)
+template <bool FWD>
+void launch_filt(hipStream_t s, int F, int R, std::size_t cap, const FiltArgs &A) {
+  const dim3 grid((blocks_for(cap, 64) + 7) / 8 * 8);
+#define G_FILT(FT, RT)                                                                \
+  if (F == 16 * FT && R == 16 * RT) {                                                 \
+    if constexpr (FWD) hipLaunchKernelGGL((g_filt_fwd<FT, RT>), grid, dim3(256), 0, s, A); \
+    else hipLaunchKernelGGL((g_filt_bwd<FT, RT>), grid, dim3(256), 0, s, A);          \
+    return;                                                                           \
+  }
+  G_FILT(8, 2) G_FILT(8, 4) G_FILT(16, 2) G_FILT(16, 4)
+#undef G_FILT
+  throw std::logic_error("SO3LR: fused filters at widths other than F = 128, 256 and R = 32, 64");
+}
+
+// the fused filters' arguments (the reverse adds its inputs and outputs)
+FiltArgs filt_args(const GContext &c, const GBlock &B, const GHeads &H, const double *rbf, const double *ps,
+                   const double *qkv, double *pf) {
+  FiltArgs A{};
+  A.nact = c.nact;
+  A.cap = c.cap;
+  A.pa = c.pa;
+  A.pr = c.pr;
+  A.rbf = rbf;
+  A.ps = ps;
+  A.qkv = qkv;
+  for (int w = 0; w < 2; ++w) {
+    A.w0p[w] = B.w0p[w];
+    A.b0a[w] = B.b0a[w];
+    A.e0p[w] = B.e0p[w];
+    A.eb0a[w] = B.eb0a[w];
+    A.wcp[w] = B.wcp[w];
+    A.bca[w] = B.bca[w];
+    A.w0tp[w] = B.w0tp[w];
+    A.e0tp[w] = B.e0tp[w];
+    A.wctp[w] = B.wctp[w];
+  }
+  A.exp2_256 = H.exp2_256;
+  A.kk = H.rbf_k;
+  A.kr = H.rbf_kr;
+  A.gamma = c.gamma;
+  A.rc = c.rc;
+  A.inv_avg = c.inv_avg;
+  A.pf = pf;
+  return A;
+}
+
 // block 0's table kernels' arguments (the reverse adds its inputs and dr)
 B0Args b0_args(const GContext &c, const GBlock &B, const GHeads &H, const double *rbf, const double *tables,
                const double *cb, int F, double *palpha) {
@@ -1322,6 +1690,23 @@ B0Args b0_args(const GContext &c, const GBlock &B, const GHeads &H, const double
   A.inv_avg = c.inv_avg;
   A.palpha = palpha;
   return A;
+}
+
+// permute_mfma with each K chunk's columns in the order k = 16 T + 4 (lane
+// / 16) + v: the B operand of MFMA v then holds, in lane group g, channel
+// 16 T + 4 g + v, so a lane's four values of a chunk are contiguous in a row
+// (K a multiple of 16)
+std::vector<double> permute_mfma_kc(const std::vector<double> &w, std::size_t M, std::size_t K) {
+  const std::size_t MT = (M + 15) / 16, KT = K / 16;
+  std::vector<double> p(MT * KT * 64 * 4, 0.0);
+  for (std::size_t mt = 0; mt < MT; ++mt)
+    for (std::size_t T = 0; T < KT; ++T)
+      for (std::size_t lane = 0; lane < 64; ++lane)
+        for (std::size_t v = 0; v < 4; ++v) {
+          const std::size_t row = 16 * mt + lane % 16, col = 16 * T + 4 * (lane / 16) + v;
+          if (row < M) p[((mt * KT + T) * 64 + lane) * 4 + v] = w[row * K + col];
+        }
+  return p;
 }
 
 // run f, under c.timed when the evaluator is timing kernels
@@ -1381,12 +1766,19 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
       const std::string f = p + (k == 0 ? "filter_net_inv." : "filter_net_ev.");
       B.w0[k] = up(m.f64(f + "mlp_rbf.0.weight", {F, R}));
       B.b0[k] = up(m.f64(f + "mlp_rbf.0.bias", {F}));
-      B.w0p[k] = B.w0tp[k] = B.b0a[k] = nullptr;
-      if (b == 0) {  // g_b0_fwd, g_b0_bwd
+      {
+        // the fused kernels' operands (g_filt_fwd, g_filt_bwd, g_b0_fwd, g_b0_bwd)
         const auto w0 = m.f64(f + "mlp_rbf.0.weight", {F, R});
+        const auto e0 = m.f64(f + "mlp_ev.0.weight", {FH, NH});
+        std::vector<double> e0k(FH * 16, 0.0);  // K (the NH slots) padded to 16
+        for (std::size_t o = 0; o < FH; ++o)
+          for (std::size_t i = 0; i < NH; ++i) e0k[o * 16 + i] = e0[o * NH + i];
         B.w0p[k] = up(permute_mfma(w0, F, R));
         B.w0tp[k] = up(permute_mfma(transpose(w0, F, R), R, F));
+        B.e0p[k] = up(permute_mfma(e0k, FH, 16));
+        B.e0tp[k] = up(permute_mfma(transpose(e0, FH, NH), NH, FH));
         B.b0a[k] = up(bias_acc(m.f64(f + "mlp_rbf.0.bias", {F}), F));
+        B.eb0a[k] = up(bias_acc(m.f64(f + "mlp_ev.0.bias", {FH}), FH));
       }
       B.w1[k] = up(m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.weight", {F, F}));
       B.b1[k] = up(m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F}));
@@ -1407,6 +1799,17 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
         }
         B.wcat[k] = up(wc);
         B.bcat[k] = up(bc);
+        // the forward's output rows permuted within each tile (g_filt_fwd)
+        std::vector<double> wcr(wc.size()), bcr(F);
+        for (std::size_t o = 0; o < F; ++o) {
+          const std::size_t src = 16 * (o / 16) + 4 * (o % 4) + (o % 16) / 4;
+          std::copy(wc.begin() + std::ptrdiff_t(src * (F + FH)), wc.begin() + std::ptrdiff_t((src + 1) * (F + FH)),
+                    wcr.begin() + std::ptrdiff_t(o * (F + FH)));
+          bcr[o] = bc[src];
+        }
+        B.wcp[k] = up(permute_mfma(wcr, F, F + FH));
+        B.bca[k] = up(bias_acc(bcr, F));
+        B.wctp[k] = up(permute_mfma_kc(transpose(wc, F, F + FH), F + FH, F));
       }
     }
     B.att_cg = up(m.f64(at + "so3_conv_invariants.cg_rep", {E}));
@@ -1470,18 +1873,26 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
 void GenericPath::carve(int N, int cap, int C, const std::function<double *(int, std::size_t)> &take) {
   const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1)), L = std::size_t(layers_);
   const std::size_t F = std::size_t(d_.F), E = std::size_t(d_.E), NH = std::size_t(d_.NH), NI = std::size_t(d_.NI),
-                    R = std::size_t(d_.R), FH = std::size_t(d_.FH), HO = std::size_t(d_.HO);
+                    R = std::size_t(d_.R), HO = std::size_t(d_.HO);
   const std::size_t sizes[NBUF] = {
       (L + 1) * n * F, (L + 1) * n * E, L * n * 5 * F, L * n * 4 * NH, L * n * E, L * n * F, L * n * F, L * n,
       L * n * F, L * n * NI, L * n * F, L * n,
       n * F, n * F, n * NI, n * HO, n * HO, n * 128, n * HO,
       n * F, n * E, n * NI, n * NI, n * E, n * F, n * F, n * F, n * F, n * 5 * F,
-      P * R, L * P * NH, L * P * 2 * F, L * P * 4 * NH, P * (F + FH), P * (F + FH), P * 2 * F, P * 4 * NH,
-      P, P * NH, P * R,
+      // the pairs' basis rows, s, filter rows (none for block 0 on the
+      // element-pair tables), logits, the logits' adjoints, dE/dfc, dE/ds
+      P * R, L * P * NH, (L - (C > 0 ? 1 : 0)) * P * 2 * F, L * P * 4 * NH, P * 4 * NH, P, P * NH,
       // block 0's element-pair tables (g_cls_tables): per filter and key the
       // rows as 16 x F operands of both orientations, and their biases
       std::size_t(C) * C * 64 * F, std::size_t(C) * C * 4 * NH};
   for (int i = 0; i < NBUF; ++i) b_[i] = take(i, sizes[i]);
+}
+
+// block b's filter rows (2 F per pair); block 0 on the element-pair tables
+// has none
+double *GenericPath::pf_rows(const GContext &c, int b) const {
+  const int first = cls_on(c) ? 1 : 0;
+  return b < first ? nullptr : b_[PF] + std::size_t(b - first) * std::size_t(std::max(c.cap, 1)) * 2 * d_.F;
 }
 
 void GenericPath::forward(const GContext &c) {
@@ -1506,14 +1917,13 @@ void GenericPath::forward(const GContext &c) {
     double *n1b = b_[N1] + b * n * F, *n1hb = b_[N1HAT] + b * n * F, *n1ib = b_[N1IS] + b * n;
     double *hpb = b_[HPRE] + b * n * F, *tb = b_[TOUT] + b * n * NI;
     double *p2h = b_[PRE2HAT] + b * n * F, *p2i = b_[PRE2IS] + b * n;
-    double *psb = b_[PS] + b * P * NH, *pfb = b_[PF] + b * P * 2 * F, *pab = b_[PALPHA] + b * P * 4 * NH;
+    double *psb = b_[PS] + b * P * NH, *pfb = pf_rows(c, b), *pab = b_[PALPHA] + b * P * 4 * NH;
     // q k v q_ev k_ev per head: out[w][h*32 + o] = sum_k x[h*32 + k] W[w][h][k][o]
     // (kokkos_integrated_block0.cpp:257-287), batch z = w NH + h
     gemm_heads<EPI_STORE, true>(s, N, 5, NH, xb, F, 0, 32, B.wqkv, 1024, qb, 5 * F, F, 32);
     if (c.qk_norm)
       hipLaunchKernelGGL(g_qk_norm, dim3(blocks_for(n * 4 * NH, 256)), dim3(256), 0, s, N, F, NH, qb,
                          b_[QKIS] + b * n * 4 * NH);
-    const int HW = F + FH;
     if (b == 0 && cls_on(c)) {
       // block 0 through the element-pair tables: their rows as MFMA
       // operands, then both filters to the logits in one fused kernel
@@ -1527,19 +1937,12 @@ void GenericPath::forward(const GContext &c) {
     // pair invariants and both filters (kokkos_integrated_block0.cpp:166-255)
     hipLaunchKernelGGL(g_pair_inv, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, evb,
                        B.att_cg, psb);
-    // per filter: the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)] (F + FH
-    // wide), then f = [W1 | E1] row + b1 + e1 in one GEMM
+    // both filters' rows f = [W1 | E1] [silu(W0 rbf + b0) | silu(E0 s + e0)]
+    // + b1 + e1 and the attention logits from them, fused
     section(c, "generic_filter_fwd", [&] {
-      for (int w = 0; w < 2; ++w) {
-        gemm<EPI_SILU, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
-        gemm<EPI_SILU, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
-        gemm<EPI_STORE, false>(s, cap, c.nact, HW, F, b_[HT], HW, B.wcat[w], B.bcat[w], pfb + w * F, 2 * F);
-      }
-    });
-    section(c, "generic_alpha", [&] {
-      hipLaunchKernelGGL(F == 256 ? g_alpha<4> : g_alpha<2>, dim3(blocks_for(P, 4)), dim3(256), 0, s, d, c.nact,
-                         cap, c.pa, qb, pfb, c.inv_avg,
-                         pab);
+      FiltArgs A = filt_args(c, B, hw_, b_[RBF], psb, qb, pfb);
+      A.palpha = pab;
+      launch_filt<true>(s, F, R, P, A);
     });
     }
     hipLaunchKernelGGL(g_attn_msg, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
@@ -1571,7 +1974,7 @@ void GenericPath::forward(const GContext &c) {
 void GenericPath::reverse(const GContext &c) {
   const GDims &d = d_;
   const hipStream_t s = c.s;
-  const int N = c.N, cap = c.cap, F = d.F, E = d.E, NH = d.NH, NI = d.NI, R = d.R, FH = d.FH;
+  const int N = c.N, cap = c.cap, F = d.F, E = d.E, NH = d.NH, NI = d.NI, R = d.R;
   const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1));
   const unsigned g4 = blocks_for(n, 4);
   // heads in reverse to dE/dx of the last block's output
@@ -1587,7 +1990,7 @@ void GenericPath::reverse(const GContext &c) {
     double *n1b = b_[N1] + b * n * F, *n1hb = b_[N1HAT] + b * n * F, *n1ib = b_[N1IS] + b * n;
     double *hpb = b_[HPRE] + b * n * F, *tb = b_[TOUT] + b * n * NI;
     double *p2h = b_[PRE2HAT] + b * n * F, *p2i = b_[PRE2IS] + b * n;
-    double *psb = b_[PS] + b * P * NH, *pfb = b_[PF] + b * P * 2 * F, *pab = b_[PALPHA] + b * P * 4 * NH;
+    double *psb = b_[PS] + b * P * NH, *pfb = pf_rows(c, b), *pab = b_[PALPHA] + b * P * 4 * NH;
     // post-attention chain in reverse (kokkos_post_attention_reverse.cpp:107-449)
     hipLaunchKernelGGL(g_ln2_bwd, dim3(g4), dim3(256), 0, s, d, N, gx, gev, tb, aevb, p2h, p2i, B.ln2w, c.norm2,
                        b_[GT], b_[GA]);
@@ -1602,15 +2005,12 @@ void GenericPath::reverse(const GContext &c) {
     section(c, "generic_attn_bwd_pairs", [&] {
       hipLaunchKernelGGL(F == 256 ? g_attn_bwd_pairs<4> : g_attn_bwd_pairs<2>, dim3(blocks_for(P, 4)), dim3(256), 0,
                          s, d, c.nact, cap, c.pa, qb, c.pY, c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg,
-                         b == layers_ - 1 ? 1 : 0, b_[PSC], tables ? nullptr : b_[DF], c.dY, b_[DFC]);
+                         b == layers_ - 1 ? 1 : 0, b_[PSC], c.dY, b_[DFC]);
     });
     if (b > 0)
       hipLaunchKernelGGL(g_attn_bwd_node, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
                          c.pfc, pab, b_[PSC], b_[GAINV], b_[GQKV]);
     // filter reverse (kokkos_block2_attention_input_reverse.cpp:198-336)
-    // per filter: the hidden row's pre-activations again, its adjoint
-    // (df [W1 | E1]) (.) silu'(pre) in one GEMM, then through W0 and E0
-    const int HW = F + FH;
     if (tables) {
       // block 0 through the element-pair tables, fused: the hidden rows'
       // adjoints from the table rows, through W0 to dE/dr (the spherical
@@ -1622,23 +2022,15 @@ void GenericPath::reverse(const GContext &c) {
       section(c, "generic_filter_bwd_block0_tables",
               [&] { launch_b0<false>(s, F, R, b0_slot_bound(c), A); });
     } else {
-      section(c, "generic_filter_bwd", [&] {
-        for (int w = 0; w < 2; ++w) {
-          gemm<EPI_STORE, false>(s, cap, c.nact, R, F, b_[RBF], R, B.w0[w], B.b0[w], b_[HT], HW);
-          gemm<EPI_STORE, false>(s, cap, c.nact, NH, FH, psb, NH, B.e0[w], B.eb0[w], b_[HT] + F, HW);
-          gemm<EPI_DSILU, true>(s, cap, c.nact, F, HW, b_[DF] + w * F, 2 * F, B.wcat[w], nullptr, b_[GH], HW, b_[HT],
-                                HW);
-          if (w == 0) {
-            gemm<EPI_STORE, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-            gemm<EPI_STORE, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
-          } else {
-            gemm<EPI_ACCUM, true>(s, cap, c.nact, F, R, b_[GH], HW, B.w0[w], nullptr, b_[GRBF], R);
-            gemm<EPI_ACCUM, true>(s, cap, c.nact, FH, NH, b_[GH] + F, HW, B.e0[w], nullptr, b_[DS], NH);
-          }
-        }
-      });
-      hipLaunchKernelGGL(g_pair_radial_bwd, dim3(blocks_for(P, 4)), dim3(256), 0, s, R, c.nact, cap, c.pr, b_[DFC],
-                         b_[GRBF], b_[RBF], hw_.rbf_k, hw_.rbf_kr, c.gamma, c.rc, c.dr);
+      // both filters fused: d hidden = [W1 | E1]^T df (df from the logits'
+      // adjoints psc), (.) silu'(pre), through W0^T and E0^T to dE/dr and
+      // dE/ds
+      FiltArgs A = filt_args(c, B, hw_, b_[RBF], psb, qb, nullptr);
+      A.psc = b_[PSC];
+      A.dfc = b_[DFC];
+      A.ds = b_[DS];
+      A.dr = c.dr;
+      section(c, "generic_filter_bwd", [&] { launch_filt<false>(s, F, R, P, A); });
     }
     // the adjoints of the block's inputs feed the block below; block 0's
     // inputs (embedding, ev = 0) do not depend on the positions

@@ -48,9 +48,11 @@ struct GBlock {
   // both output layers side by side, (F, F + FH): [W1 | E1], and b1 + eb1,
   // so one GEMM over the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)]
   const double *wcat[2], *bcat[2];
-  // block 0's radial layer as MFMA operands (permute_mfma): W0 (F x R), W0^T
-  // (R x F), b0 in accumulator order (bias_acc); null in later blocks
-  const double *w0p[2], *w0tp[2], *b0a[2];
+  // the filters as MFMA operands (permute_mfma; biases in accumulator order,
+  // bias_acc): W0 (F x R), E0 (FH x NH, K padded to 16), [W1 | E1], and their
+  // transposes; b0, e0, b1 + e1
+  const double *w0p[2], *e0p[2], *wcp[2], *w0tp[2], *e0tp[2], *wctp[2];
+  const double *b0a[2], *eb0a[2], *bca[2];
   const double *att_cg, *int_cg;                  // (E)
   const double *ln1w, *ln1b, *ln2w, *ln2b;        // (F); RMSNorm and none: 1 and 0
   const double *m1, *m1b, *m2, *m2b;              // (F, F) (F)
@@ -123,6 +125,7 @@ class GenericPath {
   // evaluator's long-range step, heads and blocks in reverse.
   void forward(const GContext &c);
   void reverse(const GContext &c);
+  double *pf_rows(const GContext &c, int b) const;
 
  private:
   GDims d_{};

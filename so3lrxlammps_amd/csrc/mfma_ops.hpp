@@ -93,6 +93,35 @@ struct Stream {
 };
 
 
+// The same over a runtime loop of n iterations of NS entries each: entry S
+// of iteration `it` (its kind and buffer slot fixed by S, its address by
+// it) is loaded PF entries ahead, the last PF entries of an iteration
+// loading the next iteration's first ones.  PF divides NS, so every buffer
+// slot is a compile-time index.
+template <int NS, int PF, class Load>
+struct LoopStream {
+  static_assert(NS % PF == 0 && PF <= NS, "stream depth must divide the loop body");
+  Load load;  // load(std::integral_constant<int, S>, int it) -> v4d
+  v4d buf[PF];
+  __device__ __forceinline__ explicit LoopStream(Load l) : load(l) {}
+  __device__ __forceinline__ void prime() {
+    static_for<PF>([&](auto i) { buf[decltype(i)::value] = load(i, 0); });
+  }
+  template <class Step>
+  __device__ __forceinline__ void run(int n, Step &&step) {
+    for (int it = 0; it < n; ++it) {
+      static_for<NS>([&](auto si) {
+        constexpr int S = decltype(si)::value, N2 = S + PF;
+        const v4d w = buf[S % PF];
+        if constexpr (N2 < NS) buf[S % PF] = load(std::integral_constant<int, N2>{}, it);
+        else if (it + 1 < n) buf[S % PF] = load(std::integral_constant<int, N2 - NS>{}, it + 1);
+        step(si, it, w);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    }
+  }
+};
+
 // Activations of the MFMA filter kernels.  On gfx950 every VALU instruction a
 // wavefront issues takes issue time from the fp64 MFMAs of its SIMD, so these
 // are written for the fewest instructions: e^x = 2^m 2^(j/256) e^r with
