@@ -289,6 +289,18 @@ __device__ __forceinline__ void g_norm_row_bwd(int F, int mode, const double *gy
   for (int j = 0; j < J; ++j) gx[j] = is * (gh[j] - mg - h[j] * mgx);
 }
 
+// Dispatch block b (round-robin over the 8 XCDs) to logical block: each XCD
+// takes a contiguous run of the `active` blocks, so consecutive pairs or
+// nodes (spatially sorted: they share endpoints and partners) share that
+// XCD's L2.  -1: beyond the active blocks.  The grid is a multiple of 8 and
+// holds at least `active` blocks.
+__device__ __forceinline__ int g_xcd_block(int active) {
+  const int b = blockIdx.x;
+  const int per = active >> 3, rem = active & 7, xcd = b & 7, i = b >> 3;
+  if (i >= per + (xcd < rem ? 1 : 0)) return -1;
+  return xcd * per + (xcd < rem ? xcd : rem) + i;
+}
+
 // Attention messages, node-major (kokkos_integrated_block0.cpp:330-385):
 // node n receives from each incident pair's partner o the invariant message
 // fc alpha v_o and the equivariant fc alpha_ev Y (parity of the direction),
@@ -304,7 +316,9 @@ __global__ __launch_bounds__(256) void g_attn_msg(GDims d, int N, const int *__r
                                                   double *__restrict__ n1hat, double *__restrict__ n1is,
                                                   double *__restrict__ act, double *__restrict__ aev) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int blk = g_xcd_block((N + 3) / 4);
+  if (blk < 0) return;
+  const int n = blk * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int F = d.F, NH = d.NH, E = d.E, J = F >> 6;
   double di[4] = {0, 0, 0, 0}, de[2] = {0, 0};
@@ -546,7 +560,10 @@ __global__ __launch_bounds__(256) void g_ln1_bwd(int F, int N, const double *__r
 }
 
 // The attention reverse's node gathers (kokkos_attention_scatter_reverse.cpp:280-500):
-// dq at the receiver, dk and dv at the sender of each direction.
+// dq at the receiver, dk and dv at the sender of each direction.  One
+// wavefront per node and 64 channels (F / 64 wavefronts per node, in one
+// workgroup): a lane holds one channel's five sums, so a wavefront needs
+// few registers and many are in flight to cover the entries' loads.
 __global__ __launch_bounds__(256) void g_attn_bwd_node(GDims d, int N, const int *__restrict__ inc_off,
                                                        const int *__restrict__ iact, const int *__restrict__ iother,
                                                        const double *__restrict__ qkv, const double *__restrict__ pf,
@@ -555,15 +572,17 @@ __global__ __launch_bounds__(256) void g_attn_bwd_node(GDims d, int N, const int
                                                        const double *__restrict__ psc,
                                                        const double *__restrict__ gainv, double *__restrict__ gqkv) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int F = d.F, NH = d.NH, NQ = F >> 6;
+  const int blk = g_xcd_block((N * NQ + 3) / 4);
+  if (blk < 0) return;
+  const int wq = blk * 4 + (threadIdx.x >> 6), n = wq / NQ;
   if (n >= N) return;
-  const int F = d.F, NH = d.NH, J = F >> 6;
-  double gq[4] = {0, 0, 0, 0}, gk[4] = {0, 0, 0, 0}, gv[4] = {0, 0, 0, 0}, gqe[4] = {0, 0, 0, 0},
-         gke[4] = {0, 0, 0, 0};
-  // per entry and lane channel c = lane + 64 j (head h = c / 32): n receives
-  // along direction sn from o and sends along so = 1 - sn to o
+  const int c = 64 * (wq % NQ) + lane, h = c >> 5;
+  double gq = 0.0, gk = 0.0, gv = 0.0, gqe = 0.0, gke = 0.0;
+  // per entry: n receives along direction sn from o and sends along
+  // so = 1 - sn to o
   struct Terms {
-    double si[4], sie[4], so[4], soe[4], ao[4], fi[4], fe[4], qo[4], ko[4], qeo[4], keo[4], go[4], fc;
+    double si, sie, so, soe, ao, fi, fe, qo, ko, qeo, keo, go, fc;
   };
   auto load = [&](int e, int o) {
     Terms T;
@@ -571,53 +590,40 @@ __global__ __launch_bounds__(256) void g_attn_bwd_node(GDims d, int N, const int
     T.fc = pfc[p];
     const double *sc = psc + std::size_t(p) * 4 * NH;
     const double *al = palpha + std::size_t(p) * 4 * NH;
-    const double *fi = pf + std::size_t(p) * 2 * F, *fe = fi + F;
+    const double *fi = pf + std::size_t(p) * 2 * F;
     const double *qo = qkv + std::size_t(o) * 5 * F;
-    const double *go = gainv + std::size_t(o) * F;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = lane + 64 * (j < J ? j : 0), h = c >> 5;
-      T.si[j] = sc[sn * 2 * NH + h];
-      T.sie[j] = sc[sn * 2 * NH + NH + h];
-      T.so[j] = sc[so * 2 * NH + h];
-      T.soe[j] = sc[so * 2 * NH + NH + h];
-      T.ao[j] = al[so * 2 * NH + h];
-      T.fi[j] = fi[c];
-      T.fe[j] = fe[c];
-      T.qo[j] = qo[c];
-      T.ko[j] = qo[F + c];
-      T.qeo[j] = qo[3 * F + c];
-      T.keo[j] = qo[4 * F + c];
-      T.go[j] = go[c];
-    }
+    T.si = sc[sn * 2 * NH + h];
+    T.sie = sc[sn * 2 * NH + NH + h];
+    T.so = sc[so * 2 * NH + h];
+    T.soe = sc[so * 2 * NH + NH + h];
+    T.ao = al[so * 2 * NH + h];
+    T.fi = fi[c];
+    T.fe = fi[F + c];
+    T.qo = qo[c];
+    T.ko = qo[F + c];
+    T.qeo = qo[3 * F + c];
+    T.keo = qo[4 * F + c];
+    T.go = gainv[std::size_t(o) * F + c];
     return T;
   };
   auto add = [&](const Terms &T) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j >= J) continue;
-      gq[j] += T.si[j] * T.ko[j] * T.fi[j];
-      gqe[j] += T.sie[j] * T.keo[j] * T.fe[j];
-      gk[j] += T.so[j] * T.qo[j] * T.fi[j];
-      gv[j] += T.fc * T.ao[j] * T.go[j];
-      gke[j] += T.soe[j] * T.qeo[j] * T.fe[j];
-    }
+    gq += T.si * T.ko * T.fi;
+    gqe += T.sie * T.keo * T.fe;
+    gk += T.so * T.qo * T.fi;
+    gv += T.fc * T.ao * T.go;
+    gke += T.soe * T.qeo * T.fe;
   };
-  // one entry's loads at a time here (174 registers; both entries' loads
-  // first took 256 and ran no faster)
   for_active_pairs(inc_off[n], inc_off[n + 1], iact, iother, lane, [&](int e1, int o1, int e2, int o2, bool two) {
-    add(load(e1, o1));
-    if (two) add(load(e2, o2));
+    const Terms A = load(e1, o1), B = load(e2, o2);
+    add(A);
+    if (two) add(B);
   });
-  double *g = gqkv + std::size_t(n) * 5 * F;
-  for (int j = 0; j < J; ++j) {
-    const int c = lane + 64 * j;
-    g[c] = gq[j];
-    g[F + c] = gk[j];
-    g[2 * F + c] = gv[j];
-    g[3 * F + c] = gqe[j];
-    g[4 * F + c] = gke[j];
-  }
+  double *g = gqkv + std::size_t(n) * 5 * F + c;
+  g[0] = gq;
+  g[F] = gk;
+  g[2 * F] = gv;
+  g[3 * F] = gqe;
+  g[4 * F] = gke;
 }
 
 // gev = ga + sum over incident pairs of 2 (ev_n - ev_o) cg ds[slot]: the
@@ -628,7 +634,9 @@ __global__ __launch_bounds__(256) void g_ev_bwd(GDims d, int N, const int *__res
                                                 const double *__restrict__ ds, const double *__restrict__ ga,
                                                 double *__restrict__ gev) {
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int blk = g_xcd_block((N + 3) / 4);
+  if (blk < 0) return;
+  const int n = blk * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int E = d.E;
   for (int j = 0; j < 2; ++j) {
@@ -735,7 +743,9 @@ __global__ __launch_bounds__(256) void g_attn_bwd_pairs(GDims d, const int *nact
   __shared__ double lte[4][2][kGMaxE];  // per wavefront: gaev_r Y' per direction and channel
   __shared__ double lps[4][32];         // per wavefront: psc of the pair
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int p = blockIdx.x * 4 + wv;
+  const int blk = g_xcd_block((min(*nact, cap) + 3) / 4);
+  if (blk < 0) return;
+  const int p = blk * 4 + wv;
   if (p >= min(*nact, cap)) return;
   const int NH = d.NH, F = d.F, E = d.E;
   const double fc = pfc[p];
@@ -1136,17 +1146,6 @@ struct FiltArgs {
   const double *psc, *dfc;  // reverse: the logits' and the cutoff's adjoints
   double *ds, *dr;          // reverse: dE/ds (NH per pair), dE/dr (added to)
 };
-
-// Dispatch block b (round-robin over the 8 XCDs) to logical block: each XCD
-// takes a contiguous run of the `active` blocks, so consecutive pairs, which
-// share endpoints, share that XCD's L2.  -1: beyond the active blocks.  The
-// grid is a multiple of 8 and holds at least `active` blocks.
-__device__ __forceinline__ int g_xcd_block(int active) {
-  const int b = blockIdx.x;
-  const int per = active >> 3, rem = active & 7, xcd = b & 7, i = b >> 3;
-  if (i >= per + (xcd < rem ? 1 : 0)) return -1;
-  return xcd * per + (xcd < rem ? xcd : rem) + i;
-}
 
 #ifndef SO3LR_FILT_PF
 #define SO3LR_FILT_PF 6
@@ -1900,7 +1899,7 @@ void GenericPath::forward(const GContext &c) {
   const hipStream_t s = c.s;
   const int N = c.N, cap = c.cap, F = d.F, E = d.E, NH = d.NH, NI = d.NI, R = d.R, FH = d.FH;
   const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1));
-  const unsigned g4 = blocks_for(n, 4);
+  const unsigned g4 = blocks_for(n, 4), g4x = (g4 + 7) / 8 * 8;  // g4x: g_xcd_block's grids
   const unsigned gP = blocks_for(P, 256);
   double *xs = b_[XS], *evs = b_[EVS];
   G_CHECK(hipMemcpyAsync(xs, c.x0, n * F * sizeof(double), hipMemcpyDeviceToDevice, s));
@@ -1945,7 +1944,7 @@ void GenericPath::forward(const GContext &c) {
       launch_filt<true>(s, F, R, P, A);
     });
     }
-    hipLaunchKernelGGL(g_attn_msg, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
+    hipLaunchKernelGGL(g_attn_msg, dim3(g4x), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
                        c.pfc, pab, B.ln1w, B.ln1b, c.ln_eps, c.norm1, n1b, n1hb, n1ib, b_[ACT], aevb);
     // post-attention node chain (kokkos_post_attention_block0.cpp:165-300)
     gemm<EPI_SILU, false>(s, N, nullptr, F, F, b_[ACT], F, B.m1, B.m1b, b_[HID], F, nullptr, 0, nullptr, 0, hpb, F);
@@ -1976,7 +1975,7 @@ void GenericPath::reverse(const GContext &c) {
   const hipStream_t s = c.s;
   const int N = c.N, cap = c.cap, F = d.F, E = d.E, NH = d.NH, NI = d.NI, R = d.R;
   const std::size_t n = std::size_t(N), P = std::size_t(std::max(cap, 1));
-  const unsigned g4 = blocks_for(n, 4);
+  const unsigned g4 = blocks_for(n, 4), g4x = (g4 + 7) / 8 * 8;  // g4x: g_xcd_block's grids
   // heads in reverse to dE/dx of the last block's output
   hipLaunchKernelGGL(g_heads_bwd, dim3(g4), dim3(256), 0, s, d, N, c.z, b_[HHPRE], c.qseed, c.dh, c.heff, c.dc,
                      c.c6eff, hw_, b_[GHEAD]);
@@ -2003,12 +2002,13 @@ void GenericPath::reverse(const GContext &c) {
     // attention reverse per pair (kokkos_attention_scatter_reverse.cpp:280-500)
     const bool tables = b == 0 && cls_on(c);
     section(c, "generic_attn_bwd_pairs", [&] {
-      hipLaunchKernelGGL(F == 256 ? g_attn_bwd_pairs<4> : g_attn_bwd_pairs<2>, dim3(blocks_for(P, 4)), dim3(256), 0,
+      hipLaunchKernelGGL(F == 256 ? g_attn_bwd_pairs<4> : g_attn_bwd_pairs<2>, dim3((blocks_for(P, 4) + 7) / 8 * 8),
+                         dim3(256), 0,
                          s, d, c.nact, cap, c.pa, qb, c.pY, c.pfc, pab, b_[GAINV], b_[GA], c.inv_avg,
                          b == layers_ - 1 ? 1 : 0, b_[PSC], c.dY, b_[DFC]);
     });
     if (b > 0)
-      hipLaunchKernelGGL(g_attn_bwd_node, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
+      hipLaunchKernelGGL(g_attn_bwd_node, dim3((blocks_for(n * (F / 64), 4) + 7) / 8 * 8), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
                          c.pfc, pab, b_[PSC], b_[GAINV], b_[GQKV]);
     // filter reverse (kokkos_block2_attention_input_reverse.cpp:198-336)
     if (tables) {
@@ -2049,7 +2049,7 @@ void GenericPath::reverse(const GContext &c) {
       }
       if (!c.resid->empty())
         hipLaunchKernelGGL(g_scale, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, n * F, (*c.resid)[b], gx);
-      hipLaunchKernelGGL(g_ev_bwd, dim3(g4), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, evb, B.att_cg,
+      hipLaunchKernelGGL(g_ev_bwd, dim3(g4x), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, evb, B.att_cg,
                          b_[DS], b_[GA], gev);
     }
   }
