@@ -98,7 +98,9 @@ def test_noalloc_matches_compute_device():
     again = _evaluate(c1, xr, len(z), False, stream)
     _same(again, ref1, "packed molecules, retained path after the no-allocation calls")
 
-    # a system larger than the static array: refused before any kernel runs
+    # a system larger than the static array: refused at the work-space size
+    # check, after the node order and the pair count that size it and before
+    # the evaluation's own kernels
     _, zw, pw, bw = support.load_golden("water3000")
     print("noalloc oversize: %d atoms, expect a refusal" % len(zw), flush=True)
     c3 = Context(support.MODEL, 0)
