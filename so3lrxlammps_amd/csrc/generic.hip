@@ -1005,7 +1005,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // again; silu' of tile T - 1 after the first) and the RT W0^T chunks of tile
 // T - 1 (d rbf += W0^T d hidden), then the last tile's W0^T chunks.
 template <int FT, int RT, int CT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void g_b0_bwd(B0Args A) {
+// Two wavefronts per SIMD, 16 pairs each: at F = 256, R = 64 (config 3)
+// 1.25 ms, against 1.38 for 32 pairs at one wavefront per SIMD.
+#ifndef SO3LR_B0_BWD_WAVES
+#define SO3LR_B0_BWD_WAVES 2
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_B0_BWD_WAVES, SO3LR_B0_BWD_WAVES))) void
+g_b0_bwd(B0Args A) {
   constexpr int NH = FT / 2, NB = FT * (2 + 2 * RT);
   __shared__ double tab[256];
   tab[threadIdx.x] = A.exp2_256[threadIdx.x];
