@@ -1354,7 +1354,14 @@ constexpr FEntry filt_entry(int s) {
 #define SO3LR_FILT_BWD_WAVES 1
 #endif
 template <int FT, int RT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_FILT_BWD_WAVES, SO3LR_FILT_BWD_WAVES))) void
+// At F = 128 the hidden row's adjoint (10 tiles) leaves room for two
+// wavefronts per SIMD: 1.07 against 1.25 ms per block (slots 1,1,2,3, R =
+// 32, config 3), 1.40 against 1.61 at R = 64.
+#ifndef SO3LR_FILT_BWD_WAVES_F128
+#define SO3LR_FILT_BWD_WAVES_F128 2
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
+    FT == 8 ? SO3LR_FILT_BWD_WAVES_F128 : SO3LR_FILT_BWD_WAVES, FT == 8 ? SO3LR_FILT_BWD_WAVES_F128 : SO3LR_FILT_BWD_WAVES))) void
 g_filt_bwd(FiltArgs A) {
   constexpr int FHT = FT / 4, NH = FT / 2, HT = FT + FHT, F = 16 * FT;
   constexpr int TG = HT % SO3LR_FILT_TG == 0 ? SO3LR_FILT_TG : HT, NG = HT / TG;  // hidden tiles per group
