@@ -1198,12 +1198,23 @@ __device__ __forceinline__ void filt_inputs(const FiltArgs &A, int pp, int g, v4
 #define SO3LR_FILT_PFB 10
 #endif
 template <int FT, int RT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SO3LR_FILT_FWD_WAVES, SO3LR_FILT_FWD_WAVES))) void
+// At F = 128 (a 10-tile hidden row) two wavefronts per SIMD fit with five
+// chunks in flight: 1.10 against 1.17 ms per block at one wavefront (slots
+// 1,1,2,3, R = 32, config 3).
+#ifndef SO3LR_FILT_FWD_WAVES_F128
+#define SO3LR_FILT_FWD_WAVES_F128 2
+#endif
+#ifndef SO3LR_FILT_PFB_F128
+#define SO3LR_FILT_PFB_F128 5
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
+    FT == 8 ? SO3LR_FILT_FWD_WAVES_F128 : SO3LR_FILT_FWD_WAVES, FT == 8 ? SO3LR_FILT_FWD_WAVES_F128 : SO3LR_FILT_FWD_WAVES))) void
 g_filt_fwd(FiltArgs A) {
   constexpr int FHT = FT / 4, NH = FT / 2, HT = FT + FHT, F = 16 * FT;
   constexpr int NA = FT * (1 + RT) + 2 * FHT;  // hidden row: per tile the bias and its weight chunks
   constexpr int NB = HT;                       // output tile: its HT weight chunks
-  constexpr int PFB = NB % SO3LR_FILT_PFB == 0 ? SO3LR_FILT_PFB : NB;
+  constexpr int PFS = FT == 8 ? SO3LR_FILT_PFB_F128 : SO3LR_FILT_PFB;
+  constexpr int PFB = NB % PFS == 0 ? PFS : NB;
   __shared__ double tab[256];
   tab[threadIdx.x] = A.exp2_256[threadIdx.x];
   __syncthreads();
