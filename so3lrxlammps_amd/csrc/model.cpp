@@ -708,12 +708,40 @@ void Model::describe_and_negotiate(const std::string &origin) {
     }
     if (std::abs(csum - 1.0) > 2e-12) fail("normalized ZBL coefficients changed");
   }
-  // The v1 filter kernels evaluate SiLU through a table-based e^x whose argument
-  // reduction is exact for |x| < 2800 (the generic kernels call exp).  The radial hidden layer sees
-  // W0 rbf + b0 with every Bernstein value in [0, 1], and the node MLP sees
-  // W1 silu(n1) + b1 with |n1_k| <= sqrt(F) |w_k| + |b_k| after either
-  // normalisation: both are bounded by the weights, checked here.
-  if (!arch_.generic) {
+  {
+    // the Bernstein exponents k = 0..R-1 and R-1-k (the v1 filter kernels
+    // step the basis through them)
+    const int R = arch_.R;
+    const auto k = i64("model.radial_embedding.radial_basis_fn.k", {std::size_t(R)});
+    const auto kr = i64("model.radial_embedding.radial_basis_fn.k_rev", {std::size_t(R)});
+    for (int c = 0; c < R; ++c)
+      if (k[c] != c || kr[c] != R - 1 - c) fail("Bernstein basis exponents other than k = 0..R-1, k_rev = R-1-k");
+  }
+  // The filter kernels evaluate SiLU through a table-based e^x whose argument
+  // reduction is exact for |x| < 2800 (the generic node layers call exp).  The
+  // radial hidden layer sees W0 rbf + b0 with every Bernstein value in [0, 1],
+  // and the v1 node MLP sees W1 silu(n1) + b1 with |n1_k| <= sqrt(F) |w_k| +
+  // |b_k| after either normalisation: both are bounded by the weights, checked
+  // here (the spherical branch clamps its argument instead).
+  if (arch_.generic) {
+    const std::size_t F = std::size_t(arch_.F), R = std::size_t(arch_.R);
+    double worst = 0.0;
+    for (int b = 0; b < arch_.layers; ++b) {
+      const std::string p = "model.euclidean_transformers." + std::to_string(b) + ".";
+      for (const char *fn : {"filter_net_inv.", "filter_net_ev."}) {
+        const auto w0 = f64(p + fn + "mlp_rbf.0.weight", {F, R});
+        const auto b0 = f64(p + fn + "mlp_rbf.0.bias", {F});
+        for (std::size_t c = 0; c < F; ++c) {
+          double acc = std::abs(b0[c]);
+          for (std::size_t k = 0; k < R; ++k) acc += std::abs(w0[c * R + k]);
+          worst = std::max(worst, acc);
+        }
+      }
+    }
+    if (!(worst < 2000.0))
+      fail("weights allow SiLU arguments up to " + std::to_string(worst) +
+           " in the filters' radial hidden layers; this build's activations take |x| < 2000");
+  } else {
     double worst = 0.0;
     const double sf = std::sqrt(double(kF));
     for (int b = 0; b < arch_.layers; ++b) {
@@ -744,15 +772,6 @@ void Model::describe_and_negotiate(const std::string &origin) {
     if (!(worst < 2000.0))
       fail("weights allow SiLU arguments up to " + std::to_string(worst) +
            " in the filter or node MLP hidden layers; this build's activations take |x| < 2000");
-  }
-  {
-    // the Bernstein exponents k = 0..R-1 and R-1-k (the v1 filter kernels
-    // step the basis through them)
-    const int R = arch_.R;
-    const auto k = i64("model.radial_embedding.radial_basis_fn.k", {std::size_t(R)});
-    const auto kr = i64("model.radial_embedding.radial_basis_fn.k_rev", {std::size_t(R)});
-    for (int c = 0; c < R; ++c)
-      if (k[c] != c || kr[c] != R - 1 - c) fail("Bernstein basis exponents other than k = 0..R-1, k_rev = R-1-k");
   }
   if (arch_.c6_head) {
     // a ratio head of the Hirshfeld head's widths (kokkos_output_heads.cpp:108-132;

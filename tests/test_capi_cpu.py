@@ -169,6 +169,17 @@ def test_weights_beyond_the_activation_range_are_refused(tmp_path):
     assert rc == _lib.ERR_MODEL and "SiLU arguments" in msg, msg
 
 
+def test_generic_weights_beyond_the_activation_range_are_refused(tmp_path):
+    """The same bound for a model on the generic kernels, whose fused filters
+    take the radial hidden layer through the table exponential too."""
+    def big(manifest, arrays):
+        arrays["model.euclidean_transformers.2.filter_net_inv.mlp_rbf.0.weight"][7, 40] = 5000.0
+    base = support.lifted_model(tmp_path / "wide.so3lr")
+    path = support.variant_model(tmp_path / "wide_big.so3lr", edit=big, base=base)
+    rc, msg = _create(path)
+    assert rc == _lib.ERR_MODEL and "SiLU arguments" in msg and "radial" in msg, msg
+
+
 def test_released_widths_are_accepted(tmp_path):
     """F = 256 with R = 64, duplicated degree slots and an energy/charge head
     narrower than F (support.lifted_model), and duplicated or missing degrees
