@@ -860,8 +860,8 @@ __global__ __launch_bounds__(256) void g_cls_tables(int F, int NH, int FH, int C
 // hidden row silu(W0 rbf + b0) stays in registers, its logits are one MFMA
 // chain per hidden tile against the table rows; in reverse the hidden
 // adjoint is the table rows times the logits' adjoints, then through
-// silu'(pre) (pre recomputed) and W0^T to the basis adjoint, and dE/dr as
-// g_pair_radial_bwd.  The layout of evaluator.hip's MFMA filters: features
+// silu'(pre) (pre recomputed) and W0^T to the basis adjoint, and dE/dr from
+// it and the cutoff's adjoint.  The layout of evaluator.hip's MFMA filters: features
 // as rows, 16 pairs per column tile, a tile's D registers the next layer's B
 // operand (feature 16 T + g + 4 r of pair lane % 16 in lane group g,
 // register r).  FT = F / 16 hidden tiles, RT = R / 16 basis chunks, NH =
@@ -1133,12 +1133,14 @@ g_b0_bwd(B0Args A) {
 // F / 4), RT = R / 16 basis chunks, NH = FT / 2 slots.
 //   forward: the hidden row [silu(W0 rbf + b0) | silu(E0 s + e0)] (HT = FT +
 //            FT / 4 tiles) in registers, then f = [W1 | E1] hidden + b1 + e1
-//            one output tile at a time, stored as the pair's filter row;
-//   reverse: d hidden = [W1 | E1]^T df, df formed from the logits' adjoints
-//            and the endpoint rows as g_attn_bwd_pairs forms it, TG hidden
-//            tiles at a time; each group then times silu'(pre) (pre again)
-//            and through W0^T to the basis adjoint or E0^T to dE/ds; last
-//            dE/dr as g_pair_radial_bwd.
+//            one output tile at a time, stored as the pair's filter row, and
+//            the attention logits <q_r, k_s (.) f>_h / avg from each tile;
+//   reverse: d hidden = [W1 | E1]^T df, df = psc_0 q_a k_b + psc_1 q_b k_a
+//            formed from the logits' adjoints psc (g_attn_bwd_pairs) and the
+//            endpoint rows, TG hidden tiles at a time (all of them unless
+//            set lower); each group then times silu'(pre) (pre again) and
+//            through W0^T to the basis adjoint or E0^T to dE/ds; last dE/dr
+//            from the basis adjoint and the cutoff's.
 struct FiltArgs {
   const int *nact;
   int cap;
