@@ -4,10 +4,11 @@
 // channel order throughout:
 //   node state per block b:  x[b] N x F, ev[b] N x E, qkv[b] N x 5F
 //                            (q | k | v | q_ev | k_ev, head-major inside each)
-//   pair state per block b:  s (NH slot invariants), f (F inv | F ev filters),
+//   pair state per block b:  s (NH slot invariants), f (F inv | F ev filters;
+//                            none for block 0 on the element-pair tables),
 //                            alpha (2 directions x (NH inv + NH ev))
-//   per evaluation:          rbf (R), and the reverse's df (2F), ds (NH),
-//                            dE/dr and dE/dY (24)
+//   per evaluation:          rbf (R), and the reverse's logit adjoints psc
+//                            (4 NH), dE/dfc, ds (NH), dE/dr and dE/dY (24)
 // Pair p = {a, b}, v = x_a - x_b: direction 0 is the edge b -> a (receiver a,
 // harmonics Y(v/r)), direction 1 the edge a -> b ((-1)^l Y(v/r)).
 #include "generic.hpp"

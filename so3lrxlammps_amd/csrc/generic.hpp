@@ -9,8 +9,10 @@
 // Same pair-based, deterministic design as the v1 path (and the same
 // geometry, long-range, force and virial kernels around it): unique pairs
 // {a, b} with both directions carried per pair, node sums as gathers over the
-// node-major incidence, no atomics.  The dense layers are one LDS-tiled fp64
-// GEMM with fused epilogues, over pairs (filters) or nodes; the rest are
+// node-major incidence, no atomics.  The filters over pairs are fused fp64
+// MFMA kernels that keep each pair's hidden row in registers (block 0 of a
+// one-image system through its element-pair tables); the node-side dense
+// layers are one LDS-tiled fp64 GEMM with fused epilogues; the rest are
 // node- or pair-major kernels in natural channel order.
 #pragma once
 
