@@ -535,8 +535,9 @@ def main():
     md.ctx.kernel_timing(False)
     timing = {}
     work = kernel_work(model_widths(MODEL), elements=len(set(int(v) for v in z)))
-    for name in ("filter_fwd", "filter_fwd_block0", "filter_fwd_block0_tables", "filter_bwd", "filter_bwd_block0",
-                 "filter_bwd_block0_tables", "attn_fwd", "attn_bwd",
+    for name in ("filter_fwd", "filter_fwd_block0", "filter_fwd_block0_tables", "filter_fwd_block0_radial",
+                 "filter_bwd", "filter_bwd_block0", "filter_bwd_block0_tables", "filter_bwd_block0_radial",
+                 "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd",
                  "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables"):
         try:

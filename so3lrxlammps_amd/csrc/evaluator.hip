@@ -12,6 +12,7 @@
 // (-1)^l Y(v/r).  Node sums are gathers over a CSR incidence list.
 #include "evaluator.hpp"
 #include "mfma_ops.hpp"
+#include "radial_table.hpp"
 
 #include <algorithm>
 #include <array>
@@ -1515,6 +1516,190 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_class(
       grad += dfc * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / rc);
     }
     dr[pp] += grad;
+  }
+}
+
+// ---------------------------------------------------------------- block 0, radial tables
+// With the element-pair tables, each of block 0's logits is a fixed function
+// of r per element pair: <M[w][A][B][h], h_w(r)> + c0[w][A][B][h], h_w the
+// filter's radial hidden layer.  fit_radial_hidden (radial_table.cpp) fits
+// h_w and dh_w/dr per interval of [r0, rc] as polynomials of degree 13 in
+// t in [-1, 1] (monomial coefficients, [w][interval][power][feature]);
+// k_radial_tables contracts them with the element pairs' M rows into one
+// polynomial per logit and its r-derivative.  The forward then evaluates 16
+// polynomials per pair instead of both filters' MFMA chains, the reverse 16
+// derivatives instead of recomputing the pre-activations.
+//
+// Table record of (element pair {lo <= hi}, interval): 7 coefficient pairs x
+// 16 logits x 2: the lane of logit l = 8 w + 4 dir + h (dir 0: lo <- hi, the
+// M rows of (lo, hi)) reads coefficients 2 kp and 2 kp + 1 at
+// kp * 32 + 2 l, so that the 16 lanes of a pair read 256 contiguous bytes per
+// load.  Element pairs in triangular order (tri_key).
+constexpr int kRadCoefs = kRadialDegree + 1, kRadRecord = kRadCoefs * 16;
+static_assert(kRadCoefs % 2 == 0, "the table records hold coefficient pairs");
+
+__device__ __forceinline__ int tri_key(int lo, int hi, int C) { return lo * C - lo * (lo - 1) / 2 + (hi - lo); }
+
+// One block per (element pair, interval), thread (power k, logit l):
+// coefficient k of logit l's polynomial and of its derivative.  c0 joins
+// the constant coefficient of the value.
+__global__ __launch_bounds__(256) void k_radial_tables(int C, const double *__restrict__ Mt,
+                                                       const double *__restrict__ c0,
+                                                       const double *__restrict__ gval,
+                                                       const double *__restrict__ gslope, RadialDomain d,
+                                                       double *tval, double *tslope) {
+  const int key = blockIdx.x / d.intervals, i = blockIdx.x % d.intervals;
+  const int t = threadIdx.x;
+  if (t >= 16 * kRadCoefs) return;
+  int lo = 0, start = 0;
+  while (start + (C - lo) <= key) start += C - lo++;
+  const int hi = lo + (key - start);
+  const int l = t & 15, k = t >> 4;
+  const int w = l >> 3, dir = (l >> 2) & 1, h = l & 3;
+  const int A = dir ? hi : lo, B = dir ? lo : hi;
+  const std::size_t row = ((std::size_t(w) * C + A) * C + B) * 4 + h;
+  const double *m = Mt + row * kF;
+  const std::size_t g = ((std::size_t(w) * d.intervals + i) * kRadCoefs + k) * kF;
+  double av = 0.0, as = 0.0;
+  for (int f = 0; f < kF; ++f) {
+    const double mf = m[tpos(f)];
+    av += mf * gval[g + f];
+    as += mf * gslope[g + f];
+  }
+  if (k == 0) av += c0[row];
+  const std::size_t o = (std::size_t(key) * d.intervals + i) * kRadRecord + (k >> 1) * 32 + 2 * l + (k & 1);
+  tval[o] = av;
+  tslope[o] = as;
+}
+
+// Interval and local coordinate of r; below r0 the basis is clamped: the
+// value at r0, slope 0 (inside = false).
+__device__ __forceinline__ int radial_locate(double r, const RadialDomain &d, double &t, bool &inside) {
+  inside = r >= d.r0;
+  if (!inside) {
+    t = -1.0;
+    return 0;
+  }
+  const int i = int(fmin((r - d.r0) * (0.5 * d.scale), double(d.intervals - 1)));
+  t = fma(r - fma(double(i), d.step, d.r0), d.scale, -1.0);
+  return i;
+}
+
+// Polynomial of lane l's logit at t (Horner from the highest power).
+__device__ __forceinline__ double radial_eval(const double *__restrict__ rec, int l, double t) {
+  double2 c[kRadCoefs / 2];
+#pragma unroll
+  for (int kp = 0; kp < kRadCoefs / 2; ++kp) c[kp] = *reinterpret_cast<const double2 *>(rec + kp * 32 + 2 * l);
+  double v = c[kRadCoefs / 2 - 1].y;
+#pragma unroll
+  for (int k = kRadCoefs - 2; k >= 0; --k) v = fma(v, t, (k & 1) ? c[k >> 1].y : c[k >> 1].x);
+  return v;
+}
+
+// Block 0's forward through the radial tables: 16 lanes per pair (lane l =
+// logit 8 w + 4 dir + h), 16 pairs per block in pair order (no element-pair
+// sort: the tables of a few elements stay in L2).  Writes the logits as
+// k_filter_fwd_class.
+__global__ __launch_bounds__(256) void k_radial_fwd(const int *n_active, const int *pa,
+                                                    const double *pr, const int *__restrict__ z,
+                                                    const int *__restrict__ cls, int C,
+                                                    const double *__restrict__ tval, RadialDomain d, double inv_avg,
+                                                    double *palpha) {
+  const int nact = *n_active;
+  const int blk = xcd_block_active((nact + 15) / 16);
+  if (blk < 0) return;
+  const int q = blk * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
+  if (q >= nact) return;  // the pair's 16 lanes
+  const int p = q;
+  const int ca = cls[z[pa[2 * p]]], cb = cls[z[pa[2 * p + 1]]];
+  const bool sw = ca > cb;
+  const int lo = sw ? cb : ca, hi = sw ? ca : cb;
+  double t;
+  bool inside;
+  const int i = radial_locate(pr[p], d, t, inside);
+  const double *rec = tval + (std::size_t(tri_key(lo, hi, C)) * d.intervals + i) * kRadRecord;
+  const double v = radial_eval(rec, l, t);
+  // lo <- hi is a <- b unless the classes are swapped
+  const int dir = (l >> 2) & 1;
+  palpha[16 * std::size_t(p) + (((dir ^ int(sw)) << 3) | ((l >> 3) << 2) | (l & 3))] = v * inv_avg;
+}
+
+// Block 0's reverse through the radial tables (k_filter_bwd_class's result):
+// lane l of a pair holds logit l's head sum S (invariant filter: Gv; the
+// equivariant filter's degree slot h: <gev, Y>), adds al * S to dE/dfc and
+// fc/avg * S * d logit/dr to dE/dr; the pair's lanes share its 24 channels of
+// dE/dY.
+template <bool FIRST>
+__global__ __launch_bounds__(256) void k_radial_bwd(const int *n_active, const int *pa,
+                                                    const double *pr, const double *pfc, const double *pY,
+                                                    const double *palpha, const double *__restrict__ gaev,
+                                                    const int *__restrict__ z, const int *__restrict__ cls, int C,
+                                                    const double *__restrict__ tslope, const double *__restrict__ Gv,
+                                                    RadialDomain d, double inv_avg, double rc, double *dr,
+                                                    double *dY) {
+  const int nact = *n_active;
+  const int blk = xcd_block_active((nact + 15) / 16);
+  if (blk < 0) return;
+  const int q = blk * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
+  if (q >= nact) return;  // the pair's 16 lanes
+  const int p = q;
+  const int a = pa[2 * p], b = pa[2 * p + 1];
+  const int ca = cls[z[a]], cb = cls[z[b]];
+  const bool sw = ca > cb;
+  const int lo = sw ? cb : ca, hi = sw ? ca : cb;
+  const double r = pr[p];
+  double t;
+  bool inside;
+  const int i = radial_locate(r, d, t, inside);
+  const double *rec = tslope + (std::size_t(tri_key(lo, hi, C)) * d.intervals + i) * kRadRecord;
+  const double slope = inside ? radial_eval(rec, l, t) : 0.0;
+  const int w = l >> 3, h = l & 3, dd = ((l >> 2) & 1) ^ int(sw);  // dd 0: a <- b
+  const double *al = palpha + 16 * std::size_t(p);
+  const double al_m = al[(dd << 3) | (w << 2) | h];
+  const double fc = pfc[p];
+  // the equivariant pair terms channel by channel: lane l takes channels l
+  // and 16 + l (l < 8) of dE/dY and of the slot sums <gev_a, Y>_s (es[s])
+  // and <gev_b, Y>_s (es[4 + s]), summed over the pair's lanes below
+  const double *gea = gaev + std::size_t(a) * kE, *geb = gaev + std::size_t(b) * kE;
+  const double *y = pY + kE * std::size_t(p);
+  double *dy = dY + kE * std::size_t(p);
+  double es[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int m = l + 16 * c;
+    if (m < kE) {
+      const int hs = m < 3 ? 0 : (m < 8 ? 1 : (m < 15 ? 2 : 3));
+      const double ea = gea[m], eb = geb[m], ym = y[m];
+      dy[m] = (FIRST ? 0.0 : dy[m]) + fc * (al[4 + hs] * ea + slot_parity(hs) * al[12 + hs] * eb);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        es[s] += hs == s ? ea * ym : 0.0;
+        es[4 + s] += hs == s ? eb * ym : 0.0;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) es[k] += __shfl_xor(es[k], o, 16);
+  // head sum of this lane's logit: invariant filter from Gv, equivariant
+  // filter (slot h) from the slot sums
+  double S;
+  if (w == 0) S = Gv[(std::size_t(dd ? b : a) * C + (dd ? ca : cb)) * 4 + h];
+  else S = dd ? slot_parity(h) * pick4(h, es[4], es[5], es[6], es[7]) : pick4(h, es[0], es[1], es[2], es[3]);
+  double part = fc * inv_avg * S * slope, dfc = al_m * S;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    part += __shfl_xor(part, o, 16);
+    dfc += __shfl_xor(dfc, o, 16);
+  }
+  if (l == 0) {
+    double grad = part;
+    if (r < rc) {
+      const double u = r / rc;
+      grad += dfc * (-30.0 * u * u * (1.0 - u) * (1.0 - u) / rc);
+    }
+    dr[p] += grad;
   }
 }
 
@@ -3162,6 +3347,33 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     B.intb = up(m.f64(p + "interaction_block.linear_layer.bias", {NI}));
     B.intbp = up(bias_acc(m.f64(p + "interaction_block.linear_layer.bias", {NI}), NI));
   }
+  // block 0's radial hidden layers as piecewise polynomials (radial tables),
+  // used when both filters fit to within 1e-14 (values) and 1e-13 (slopes)
+  // of their largest magnitudes at the check points
+  if (const char *nr = std::getenv("SO3LR_NO_RADIAL_TABLES")) radial_tables_ = nr[0] != '1';
+  if (!a.generic && radial_tables_ && class_tables_) {
+    const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
+    std::vector<double> val, slope;
+    bool ok = true;
+    for (int k = 0; k < 2 && ok; ++k) {
+      const std::string f = std::string("model.euclidean_transformers.0.") + (k ? "filter_net_ev." : "filter_net_inv.");
+      try {
+        const RadialFit fit = fit_radial_hidden(m.f64(f + "mlp_rbf.0.weight", {F, R}), m.f64(f + "mlp_rbf.0.bias", {F}),
+                                                int(F), int(R), bb, gamma_, rc_, kRadialIntervals, kRadialDegree);
+        ok = fit.value_error <= 1e-14 && fit.slope_error <= 1e-13;
+        val.insert(val.end(), fit.value.begin(), fit.value.end());
+        slope.insert(slope.end(), fit.slope.begin(), fit.slope.end());
+        rad_dom_ = RadialDomain{fit.r0, fit.step, fit.scale, fit.intervals};
+      } catch (const std::invalid_argument &) {
+        ok = false;
+      }
+    }
+    if (ok) {
+      rad_val_ = up(val);
+      rad_slope_ = up(slope);
+      radial_ok_ = true;
+    }
+  }
   if (!a.generic) {
     const std::string e = "model.atomic_energy_output_block.", q = "model.partial_charges_output_block.",
                       h = "model.hirshfeld_output_block.";
@@ -3305,7 +3517,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
   cls_lut_ = buf("cls_lut"); cls_rep0_ = buf("cls_rep0"); cls_rep_ = buf("cls_rep"); cls_mt_ = buf("cls_mt");
   cls_c0_ = buf("cls_c0"); cls_gv_ = buf("cls_gv"); cls_hist_ = buf("cls_hist"); cls_order_ = buf("cls_order");
-  cls_rows_ = buf("cls_rows");
+  cls_rows_ = buf("cls_rows"); rad_tab_ = buf("rad_tab");
   iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part"); probe_ = buf("probe");
   top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
   top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp"); top_box_ = buf("top_box");
@@ -3390,6 +3602,11 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
       n_cls_ = int(std::count_if(seen.begin(), seen.end(), [](int c) { return c >= 0; }));
     }
   }
+  // block 0's radial tables: sized here (no allocation in the evaluation),
+  // filled by the next evaluation
+  rad_stale_ = true;
+  if (radial_ok_ && !gen_ && n_cls_ > 0)
+    (void)ensure<double>(rad_tab_, 2 * std::size_t(n_cls_) * (n_cls_ + 1) / 2 * kRadialIntervals * kRadRecord);
   HIP_CHECK(hipStreamSynchronize(stream_));
   system_ready_ = true;
   topology_ready_ = false;
@@ -3579,6 +3796,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   double *partial = nullptr;
   // block 0 through element-pair tables (k_filter_fwd_class, k_filter_bwd_class)
   const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
+  // and with the radial tables (k_radial_fwd, k_radial_bwd)
+  const bool use_rad = use_cls && radial_ok_;
   // (the generic path's: g_cls_tables, g_b0_fwd, g_b0_bwd)
   const bool gen_cls = gen_ && class_tables_ && n_cls_ > 0;
   const int C = use_cls ? n_cls_ : 0;
@@ -3837,6 +4056,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const double inv_avg = 1.0 / avg_;
   const unsigned gP = unsigned(PA);
   const unsigned gP64 = unsigned(std::max(1, ceil_div(PA, 64)));  // 64 pairs per MFMA block
+  const unsigned gP16 = unsigned(std::max(1, ceil_div(PA, 16)));  // 16 pairs per radial-table block
 
   // --- interaction blocks, forward ---
   for (int b = 0; b < L; ++b) {
@@ -3871,20 +4091,36 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       hipLaunchKernelGGL(k_qkv_mfma, dim3(1, kHeads), dim3(256), 0, s, C, cxr, B.qkvp, cqkv);
       if (qk_norm_)
         hipLaunchKernelGGL(k_qk_norm, dim3(unsigned(ceil_div(16 * C, 256))), dim3(256), 0, s, C, cqkv, cqis);
-      hipLaunchKernelGGL(k_class_tables, dim3(unsigned(C * C), 8), dim3(128), 0, s, C, cqkv, B.fw1[0], B.fw1[1],
-                         B.ob10[0], B.ob10[1], cmt, cc0);
-      const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
-      hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, lut, C, chist);
-      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, 1, nullptr);
-      hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, lut, C, ccur, cord);
+      if (!use_rad || rad_stale_)  // with the radial tables filled, nothing reads these
+        hipLaunchKernelGGL(k_class_tables, dim3(unsigned(C * C), 8), dim3(128), 0, s, C, cqkv, B.fw1[0], B.fw1[1],
+                           B.ob10[0], B.ob10[1], cmt, cc0);
+      if (use_rad && rad_stale_) {  // the classes' rows are those of the system: once after set_system
+        const std::size_t keys = std::size_t(C) * (C + 1) / 2, half = keys * kRadialIntervals * kRadRecord;
+        double *tab = static_cast<double *>(rad_tab_->p);
+        hipLaunchKernelGGL(k_radial_tables, dim3(unsigned(keys * kRadialIntervals)), dim3(256), 0, s, C, cmt, cc0,
+                           rad_val_, rad_slope_, rad_dom_, tab, tab + half);
+        rad_stale_ = false;
+      }
+      if (!use_rad) {  // the element-pair kernels' pair order
+        const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
+        hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, lut, C, chist);
+        hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, 1, nullptr);
+        hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, lut, C, ccur, cord);
+      }
     } else {
       hipLaunchKernelGGL(k_qkv_mfma, dim3(gN64, kHeads), dim3(256), 0, s, int(N), xb, B.qkvp, qb);
       if (qk_norm_)
         hipLaunchKernelGGL(k_qk_norm, dim3(unsigned(ceil_div(16 * N, 256))), dim3(256), 0, s, int(N), qb,
                            qkis + b * Nz * 16);
     }
-    timed(blk0 ? (use_cls ? "filter_fwd_block0_tables" : "filter_fwd_block0") : "filter_fwd", 0, [&] {
-      if (blk0 && use_cls)
+    timed(blk0 ? (use_rad ? "filter_fwd_block0_radial" : use_cls ? "filter_fwd_block0_tables" : "filter_fwd_block0")
+               : "filter_fwd",
+          0, [&] {
+      if (blk0 && use_rad)
+        hipLaunchKernelGGL(k_radial_fwd, dim3(gP16), dim3(256), 0, s, nact, pa, pr, z,
+                           static_cast<const int *>(cls_lut_->p), C, static_cast<const double *>(rad_tab_->p),
+                           rad_dom_, inv_avg, pab);
+      else if (blk0 && use_cls)
         hipLaunchKernelGGL(k_filter_fwd_class, dim3(gP64), dim3(256), 0, s, nact, cord, pa, pr, z,
                            static_cast<const int *>(cls_lut_->p), C, cmt, cc0, inv_avg, FM, pab);
       else if (scalar)
@@ -3986,9 +4222,19 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       const FilterMfma FM = filter_mfma(B, hw_, gamma_);
       if (b == 0 && use_cls) {
         hipLaunchKernelGGL(k_class_gv, dim3(unsigned(ceil_div(N, 4))), dim3(256), 0, s, int(N), C, gainv, cqkv, cgv);
-        timed("filter_bwd_block0_tables", 0, [&] {
+        timed(use_rad ? "filter_bwd_block0_radial" : "filter_bwd_block0_tables", 0, [&] {
           const int *lut = static_cast<const int *>(cls_lut_->p);
-          if (first)
+          const double *slope =
+              use_rad ? static_cast<const double *>(rad_tab_->p) +
+                            std::size_t(C) * (C + 1) / 2 * kRadialIntervals * kRadRecord
+                      : nullptr;
+          if (use_rad && first)
+            hipLaunchKernelGGL(k_radial_bwd<true>, dim3(gP16), dim3(256), 0, s, nact, pa, pr, pfc, pY, pab, gaev, z,
+                               lut, C, slope, cgv, rad_dom_, inv_avg, rc_, dr, dY);
+          else if (use_rad)
+            hipLaunchKernelGGL(k_radial_bwd<false>, dim3(gP16), dim3(256), 0, s, nact, pa, pr, pfc, pY, pab, gaev,
+                               z, lut, C, slope, cgv, rad_dom_, inv_avg, rc_, dr, dY);
+          else if (first)
             hipLaunchKernelGGL(k_filter_bwd_class<true>, dim3(gP64), dim3(256), 0, s, nact, cord, pa, pr, pfc, pY, pab,
                                gaev, z, lut, C, cmt, cgv, inv_avg, FM, rc_, dr, dY);
           else

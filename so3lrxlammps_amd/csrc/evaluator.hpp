@@ -74,6 +74,15 @@ struct BlockWeights {
   const double *m1bp, *m2bp, *intbp;    // node-layer biases in accumulator order
 };
 
+// Block 0's radial tables (k_radial_* in evaluator.hip): the domain of the
+// fits (fit_radial_hidden) as the kernels read it; intervals of width step
+// from r0, t = (r - left edge) * scale - 1.
+struct RadialDomain {
+  double r0, step, scale;
+  int intervals;
+};
+constexpr int kRadialIntervals = 256, kRadialDegree = 13;
+
 struct HeadWeights {
   int ho = 320;              // first-layer width: energy 128 | charge 128 | Hirshfeld 64 (| C6 64)
   const double *w1p, *w1tp;  // MFMA operand order: (ho x 128) and its transpose
@@ -290,6 +299,17 @@ class Evaluator {
   int n_cls_ = 0;
   bool class_tables_ = true;
   Buffer *cls_lut_, *cls_rep0_, *cls_rep_, *cls_mt_, *cls_c0_, *cls_gv_, *cls_hist_, *cls_order_, *cls_rows_;
+  // Block 0's radial tables (k_radial_tables, k_radial_fwd, k_radial_bwd): on
+  // the element-pair path, every block-0 logit as a polynomial of r per
+  // interval.  radial_ok_: both filters' radial hidden layers fit to the
+  // bound (constructor); SO3LR_NO_RADIAL_TABLES=1 keeps the element-pair
+  // MFMA kernels.  rad_tab_ holds the element pairs' value and slope tables,
+  // sized by set_system and filled by the first evaluation after it
+  // (rad_stale_).
+  bool radial_tables_ = true, radial_ok_ = false, rad_stale_ = true;
+  RadialDomain rad_dom_{};
+  const double *rad_val_ = nullptr, *rad_slope_ = nullptr;  // [filter][interval][power][feature]
+  Buffer *rad_tab_;
   // Graph replay of one evaluation: the launch sequence of compute_device is
   // captured when the same call (inputs, outputs, flags, box, stream,
   // topology and buffer addresses) comes twice in a row, and replayed while

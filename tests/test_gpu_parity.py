@@ -201,11 +201,15 @@ def test_element_table_limit(monkeypatch, orc, count):
     assert np.abs(w2 - out["virial"]).max() <= 1e-9
 
 
-def test_deterministic_bitwise_table_path(monkeypatch):
-    """Periodic water on block 0's table path, whose element-pair sort places
-    pairs with integer atomics: two contexts (one eager, one replaying a
-    graph), three calls each, all bit for bit equal."""
+@pytest.mark.parametrize("radial_off", ["0", "1"])
+def test_deterministic_bitwise_table_path(monkeypatch, radial_off):
+    """Periodic water on block 0's table paths: the radial tables (built by
+    the first call) and the element-pair kernels, whose element-pair sort
+    places pairs with integer atomics (SO3LR_NO_RADIAL_TABLES=1).  Two
+    contexts (one eager, one replaying a graph), three calls each, all bit
+    for bit equal."""
     from so3lrxlammps_amd import Context, Lists
+    monkeypatch.setenv("SO3LR_NO_RADIAL_TABLES", radial_off)
     ref, z, pos, box = support.load_golden("water3000")
     lists = Lists(pos, np.zeros(3), box, (1, 1, 1))
     xr = lists.rows_positions(pos)
@@ -466,6 +470,54 @@ def test_block0_element_tables_match_full_kernels(monkeypatch, name, q, m):
     assert np.abs(w1 - w2).max() <= 1e-11 * max(1.0, np.abs(w2).max())
     assert np.abs(ea1 - ea2).max() <= 1e-12 * max(1.0, np.abs(ea2).max())
     assert np.abs(va1 - va2).max() <= 1e-11 * max(1.0, np.abs(va2).max())
+
+
+def _launches(ctx, kernel):
+    """Launches of a timed kernel name (0 when it never ran)."""
+    from so3lrxlammps_amd import SO3LRError
+    try:
+        return ctx.kernel_timing_read(kernel)[1]
+    except SO3LRError:
+        return 0
+
+
+@pytest.mark.parametrize("name,q,m", [("water3000", 0, 1), ("alanine", 0, 1), ("acetate", -1, 1)])
+def test_block0_radial_tables_match_element_tables(monkeypatch, name, q, m):
+    """Block 0's logits from the radial tables (piecewise polynomials of r per
+    element pair, the default) against the element-pair MFMA kernels
+    (SO3LR_NO_RADIAL_TABLES=1).  The fits of the radial hidden layers hold to
+    about 1e-16 (values) and 4e-15 (slopes) of their largest magnitudes, so
+    the two agree to rounding; the kernel timings show which path ran."""
+    from so3lrxlammps_amd import Context, Lists
+    ref, z, pos, box = support.load_golden(name)
+    monkeypatch.setenv("SO3LR_SCALAR_FILTER_PAIRS", "0")
+    if box is None:
+        lo, hi, per = pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0)
+    else:
+        lo, hi, per = np.zeros(3), box, (1, 1, 1)
+    results = []
+    for off in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NO_RADIAL_TABLES", off)
+        c = Context(support.MODEL, 0)
+        c.kernel_timing(True)
+        c.set_system(z, q, m)
+        lists = Lists(pos, lo, hi, per)
+        c.set_topology(lists)
+        e, f, ea, w = c.compute(lists.rows_positions(pos))
+        ran = {k: _launches(c, k) for k in ("filter_fwd_block0_radial", "filter_bwd_block0_radial",
+                                             "filter_fwd_block0_tables", "filter_bwd_block0_tables")}
+        results.append((e, f.copy(), ea.copy(), w.copy(), ran))
+        c.close()
+    (e1, f1, ea1, w1, ran1), (e2, f2, ea2, w2, ran2) = results
+    print("%s: |dE| %.2e max|dF| %.2e max|dW| %.2e" % (name, abs(e1 - e2), np.abs(f1 - f2).max(),
+                                                       np.abs(w1 - w2).max()), flush=True)
+    assert ran1["filter_fwd_block0_tables"] == 1 and ran1["filter_fwd_block0_radial"] == 0
+    assert ran2["filter_fwd_block0_radial"] == 1 and ran2["filter_bwd_block0_radial"] == 1
+    assert ran2["filter_fwd_block0_tables"] == 0 and ran2["filter_bwd_block0_tables"] == 0
+    assert abs(e1 - e2) <= 1e-13 * abs(e2)
+    assert np.abs(f1 - f2).max() <= 1e-11
+    assert np.abs(w1 - w2).max() <= 1e-11 * max(1.0, np.abs(w2).max())
+    assert np.abs(ea1 - ea2).max() <= 1e-12 * max(1.0, np.abs(ea2).max())
 
 
 def test_graph_replay_matches_eager(monkeypatch):
