@@ -539,7 +539,8 @@ def main():
                  "filter_bwd", "filter_bwd_block0", "filter_bwd_block0_tables", "filter_bwd_block0_radial",
                  "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd",
-                 "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables"):
+                 "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables",
+                 "generic_filter_fwd_block0_radial", "generic_filter_bwd_block0_radial"):
         try:
             timing[name] = md.ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched

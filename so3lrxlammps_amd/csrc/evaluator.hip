@@ -1530,15 +1530,9 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_class(
 // polynomials per pair instead of both filters' MFMA chains, the reverse 16
 // derivatives instead of recomputing the pre-activations.
 //
-// Table record of (element pair {lo <= hi}, interval): 7 coefficient pairs x
-// 16 logits x 2: the lane of logit l = 8 w + 4 dir + h (dir 0: lo <- hi, the
-// M rows of (lo, hi)) reads coefficients 2 kp and 2 kp + 1 at
-// kp * 32 + 2 l, so that the 16 lanes of a pair read 256 contiguous bytes per
-// load.  Element pairs in triangular order (tri_key).
-constexpr int kRadCoefs = kRadialDegree + 1, kRadRecord = kRadCoefs * 16;
-static_assert(kRadCoefs % 2 == 0, "the table records hold coefficient pairs");
-
-__device__ __forceinline__ int tri_key(int lo, int hi, int C) { return lo * C - lo * (lo - 1) / 2 + (hi - lo); }
+// Table records (mfma_ops.hpp) of 16 logits: l = 8 w + 4 dir + h, dir 0:
+// lo <- hi, the M rows of (lo, hi).
+constexpr int kRadRecord = kRadialCoefs * 16;
 
 // One block per (element pair, interval), thread (power k, logit l):
 // coefficient k of logit l's polynomial and of its derivative.  c0 joins
@@ -1550,7 +1544,7 @@ __global__ __launch_bounds__(256) void k_radial_tables(int C, const double *__re
                                                        double *tval, double *tslope) {
   const int key = blockIdx.x / d.intervals, i = blockIdx.x % d.intervals;
   const int t = threadIdx.x;
-  if (t >= 16 * kRadCoefs) return;
+  if (t >= 16 * kRadialCoefs) return;
   int lo = 0, start = 0;
   while (start + (C - lo) <= key) start += C - lo++;
   const int hi = lo + (key - start);
@@ -1559,7 +1553,7 @@ __global__ __launch_bounds__(256) void k_radial_tables(int C, const double *__re
   const int A = dir ? hi : lo, B = dir ? lo : hi;
   const std::size_t row = ((std::size_t(w) * C + A) * C + B) * 4 + h;
   const double *m = Mt + row * kF;
-  const std::size_t g = ((std::size_t(w) * d.intervals + i) * kRadCoefs + k) * kF;
+  const std::size_t g = ((std::size_t(w) * d.intervals + i) * kRadialCoefs + k) * kF;
   double av = 0.0, as = 0.0;
   for (int f = 0; f < kF; ++f) {
     const double mf = m[tpos(f)];
@@ -1570,30 +1564,6 @@ __global__ __launch_bounds__(256) void k_radial_tables(int C, const double *__re
   const std::size_t o = (std::size_t(key) * d.intervals + i) * kRadRecord + (k >> 1) * 32 + 2 * l + (k & 1);
   tval[o] = av;
   tslope[o] = as;
-}
-
-// Interval and local coordinate of r; below r0 the basis is clamped: the
-// value at r0, slope 0 (inside = false).
-__device__ __forceinline__ int radial_locate(double r, const RadialDomain &d, double &t, bool &inside) {
-  inside = r >= d.r0;
-  if (!inside) {
-    t = -1.0;
-    return 0;
-  }
-  const int i = int(fmin((r - d.r0) * (0.5 * d.scale), double(d.intervals - 1)));
-  t = fma(r - fma(double(i), d.step, d.r0), d.scale, -1.0);
-  return i;
-}
-
-// Polynomial of lane l's logit at t (Horner from the highest power).
-__device__ __forceinline__ double radial_eval(const double *__restrict__ rec, int l, double t) {
-  double2 c[kRadCoefs / 2];
-#pragma unroll
-  for (int kp = 0; kp < kRadCoefs / 2; ++kp) c[kp] = *reinterpret_cast<const double2 *>(rec + kp * 32 + 2 * l);
-  double v = c[kRadCoefs / 2 - 1].y;
-#pragma unroll
-  for (int k = kRadCoefs - 2; k >= 0; --k) v = fma(v, t, (k & 1) ? c[k >> 1].y : c[k >> 1].x);
-  return v;
 }
 
 // Block 0's forward through the radial tables: 16 lanes per pair (lane l =
@@ -1618,7 +1588,7 @@ __global__ __launch_bounds__(256) void k_radial_fwd(const int *n_active, const i
   bool inside;
   const int i = radial_locate(pr[p], d, t, inside);
   const double *rec = tval + (std::size_t(tri_key(lo, hi, C)) * d.intervals + i) * kRadRecord;
-  const double v = radial_eval(rec, l, t);
+  const double v = radial_eval<16>(rec, l, t);
   // lo <- hi is a <- b unless the classes are swapped
   const int dir = (l >> 2) & 1;
   palpha[16 * std::size_t(p) + (((dir ^ int(sw)) << 3) | ((l >> 3) << 2) | (l & 3))] = v * inv_avg;
@@ -1652,7 +1622,7 @@ __global__ __launch_bounds__(256) void k_radial_bwd(const int *n_active, const i
   bool inside;
   const int i = radial_locate(r, d, t, inside);
   const double *rec = tslope + (std::size_t(tri_key(lo, hi, C)) * d.intervals + i) * kRadRecord;
-  const double slope = inside ? radial_eval(rec, l, t) : 0.0;
+  const double slope = inside ? radial_eval<16>(rec, l, t) : 0.0;
   const int w = l >> 3, h = l & 3, dd = ((l >> 2) & 1) ^ int(sw);  // dd 0: a <- b
   const double *al = palpha + 16 * std::size_t(p);
   const double al_m = al[(dd << 3) | (w << 2) | h];
@@ -3212,6 +3182,8 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   // SO3LR_NO_GRAPH=1: always launch the kernels one by one (no graph replay)
   if (const char *ng = std::getenv("SO3LR_NO_GRAPH")) use_graphs_ = ng[0] != '1';
   if (const char *nc = std::getenv("SO3LR_NO_CLASS_TABLES")) class_tables_ = nc[0] != '1';
+  // SO3LR_NO_RADIAL_TABLES=1: block 0 on the element-pair MFMA kernels
+  if (const char *nr = std::getenv("SO3LR_NO_RADIAL_TABLES")) radial_tables_ = nr[0] != '1';
   HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_out_), 16 * sizeof(double), hipHostMallocDefault));
   scratch_dev_ = scratch_on_device(device);
   stream_ = own_stream_;
@@ -3240,7 +3212,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   };
   // models of other widths than v1's run on the generic kernels, which hold
   // their own weights; the fused v1 kernels' weights are laid out below
-  if (a.generic) gen_ = std::make_unique<GenericPath>(m, up);
+  if (a.generic) gen_ = std::make_unique<GenericPath>(m, up, radial_tables_ && class_tables_);
   F_ = a.F;
   const std::size_t F = kF, R = kR, FH = kFH, NI = kNI, HW = kHW;
   for (int b = 0; b < (a.generic ? 0 : layers_); ++b) {
@@ -3350,7 +3322,6 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   // block 0's radial hidden layers as piecewise polynomials (radial tables),
   // used when both filters fit to within 1e-14 (values) and 1e-13 (slopes)
   // of their largest magnitudes at the check points
-  if (const char *nr = std::getenv("SO3LR_NO_RADIAL_TABLES")) radial_tables_ = nr[0] != '1';
   if (!a.generic && radial_tables_ && class_tables_) {
     const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
     std::vector<double> val, slope;
@@ -3605,8 +3576,9 @@ void Evaluator::set_system(const std::vector<std::int32_t> &z, const std::vector
   // block 0's radial tables: sized here (no allocation in the evaluation),
   // filled by the next evaluation
   rad_stale_ = true;
-  if (radial_ok_ && !gen_ && n_cls_ > 0)
-    (void)ensure<double>(rad_tab_, 2 * std::size_t(n_cls_) * (n_cls_ + 1) / 2 * kRadialIntervals * kRadRecord);
+  const std::size_t rad_rec = gen_ ? (gen_->radial_ok() ? gen_->radial_record() : 0) : (radial_ok_ ? kRadRecord : 0);
+  if (rad_rec && n_cls_ > 0)
+    (void)ensure<double>(rad_tab_, 2 * std::size_t(n_cls_) * (n_cls_ + 1) / 2 * kRadialIntervals * rad_rec);
   HIP_CHECK(hipStreamSynchronize(stream_));
   system_ready_ = true;
   topology_ready_ = false;
@@ -4035,11 +4007,19 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       G.cls_slots = cslots;
       hipLaunchKernelGGL(k_class_reps, dim3(unsigned(ceil_div(std::max<std::int64_t>(N, C * C), 256))), dim3(256), 0, s,
                          int(N), z, G.cls_lut, perm, static_cast<const int *>(cls_rep0_->p), crep, C * C, chist);
-      hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(slots_max, 256))), dim3(256), 0, s, cord, slots_max, -1);
-      const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
-      hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, chist);
-      hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, GContext::kB0Pad, cslots);
-      hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, ccur, cord);
+      if (gen_->radial_ok()) {
+        // block 0 through the radial tables (filled once after set_system), in pair order
+        G.rad_tab = static_cast<double *>(rad_tab_->p);
+        G.rad_build = rad_stale_;
+        rad_stale_ = false;
+      } else {
+        // the element-pair kernels' slot order
+        hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(slots_max, 256))), dim3(256), 0, s, cord, slots_max, -1);
+        const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
+        hipLaunchKernelGGL(k_cls_count, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, chist);
+        hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, GContext::kB0Pad, cslots);
+        hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, ccur, cord);
+      }
     }
     gen_->forward(G);
     hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);

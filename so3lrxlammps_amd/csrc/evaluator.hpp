@@ -74,15 +74,6 @@ struct BlockWeights {
   const double *m1bp, *m2bp, *intbp;    // node-layer biases in accumulator order
 };
 
-// Block 0's radial tables (k_radial_* in evaluator.hip): the domain of the
-// fits (fit_radial_hidden) as the kernels read it; intervals of width step
-// from r0, t = (r - left edge) * scale - 1.
-struct RadialDomain {
-  double r0, step, scale;
-  int intervals;
-};
-constexpr int kRadialIntervals = 256, kRadialDegree = 13;
-
 struct HeadWeights {
   int ho = 320;              // first-layer width: energy 128 | charge 128 | Hirshfeld 64 (| C6 64)
   const double *w1p, *w1tp;  // MFMA operand order: (ho x 128) and its transpose

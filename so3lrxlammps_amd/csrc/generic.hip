@@ -1124,6 +1124,106 @@ g_b0_bwd(B0Args A) {
   }
 }
 
+// ------------------------------------------------------ block 0, radial tables
+// Block 0's logits as polynomials of r per element pair (the algebra of
+// evaluator.hip's k_radial_* at generic widths): each filter's radial hidden
+// layer h_w(r) is fitted per interval of r (fit_radial_hidden), and the
+// 4 NH logits of a pair are <M row, h_w(r)> + cb with g_cls_tables' rows and
+// biases.  Table records (mfma_ops.hpp) of L = 4 NH logits, l = 2 NH w + r
+// with g_cls_tables' row r (r < NH: lo <- hi, head r; else hi <- lo, head
+// r - NH); the value table, then the slope table.
+
+// One block per (element pair {lo <= hi}, interval); threads over (power k,
+// logit l): coefficient k of logit l's value and slope polynomials.
+__global__ __launch_bounds__(256) void g_radial_tables(int F, int NH, int C, const double *__restrict__ tf,
+                                                       const double *__restrict__ cb,
+                                                       const double *__restrict__ gval,
+                                                       const double *__restrict__ gslope, RadialDomain d,
+                                                       double *tval, double *tslope) {
+  const int key = int(blockIdx.x) / d.intervals, i = int(blockIdx.x) % d.intervals;
+  int lo = 0, start = 0;
+  while (start + (C - lo) <= key) start += C - lo++;
+  const int hi = lo + (key - start);
+  const int L = 4 * NH, FT = F / 16;
+  const std::size_t rec = std::size_t(kRadialCoefs) * L;
+  for (int t = threadIdx.x; t < kRadialCoefs * L; t += blockDim.x) {
+    const int l = t % L, k = t / L;
+    const int w = l / (2 * NH), r = l % (2 * NH);
+    const std::size_t wk = std::size_t(w) * C * C + std::size_t(lo) * C + hi;
+    const double *m = tf + wk * FT * 256;  // row r of (lo, hi) in g_cls_tables' tf order
+    const std::size_t g = ((std::size_t(w) * d.intervals + i) * kRadialCoefs + k) * F;
+    double av = 0.0, as = 0.0;
+    for (int f = 0; f < F; ++f) {
+      const int T = f / 16, fi = f % 16;
+      const double mf = m[(T * 64 + r + 16 * (fi % 4)) * 4 + fi / 4];
+      av += mf * gval[g + f];
+      as += mf * gslope[g + f];
+    }
+    if (k == 0) av += cb[wk * 2 * NH + r];
+    const std::size_t o = (std::size_t(key) * d.intervals + i) * rec + (k >> 1) * 2 * L + 2 * l + (k & 1);
+    tval[o] = av;
+    tslope[o] = as;
+  }
+}
+
+// Forward: L = 4 NH lanes per pair (logit l), 256 / L pairs per block in
+// pair order; the logits (times 1 / avg) where g_b0_fwd writes them.
+template <int L>
+__global__ __launch_bounds__(256) void g_radial_fwd(const int *n_active, const int *pa, const double *pr,
+                                                    const int *__restrict__ z, const int *__restrict__ cls, int C,
+                                                    const double *__restrict__ tval, RadialDomain d, double inv_avg,
+                                                    double *palpha) {
+  constexpr int NH = L / 4, PB = 256 / L;
+  const int q = int(blockIdx.x) * PB + int(threadIdx.x) / L, l = int(threadIdx.x) % L;
+  if (q >= *n_active) return;  // the pair's L lanes
+  const int ca = cls[z[pa[2 * q]]], cb = cls[z[pa[2 * q + 1]]];
+  const bool sw = ca > cb;
+  double t;
+  bool inside;
+  const int i = radial_locate(pr[q], d, t, inside);
+  const double *rec = tval + (std::size_t(tri_key(sw ? cb : ca, sw ? ca : cb, C)) * d.intervals + i) *
+                                 (std::size_t(kRadialCoefs) * L);
+  const double v = radial_eval<L>(rec, l, t);
+  const int w = l / (2 * NH), r = l % (2 * NH);
+  const int side = (r >= NH) != sw ? 1 : 0;  // 0: a <- b
+  palpha[std::size_t(q) * 4 * NH + side * 2 * NH + w * NH + r % NH] = v * inv_avg;
+}
+
+// Reverse: dE/dr += sum over the pair's logits of their adjoints (psc) times
+// the slopes, plus the cutoff's adjoint (dfc) times fc'(r).
+template <int L>
+__global__ __launch_bounds__(256) void g_radial_bwd(const int *n_active, const int *pa, const double *pr,
+                                                    const int *__restrict__ z, const int *__restrict__ cls, int C,
+                                                    const double *__restrict__ tslope, RadialDomain d,
+                                                    const double *__restrict__ psc, const double *__restrict__ dfc,
+                                                    double rc, double *dr) {
+  constexpr int NH = L / 4, PB = 256 / L;
+  const int q = int(blockIdx.x) * PB + int(threadIdx.x) / L, l = int(threadIdx.x) % L;
+  if (q >= *n_active) return;  // the pair's L lanes
+  const int ca = cls[z[pa[2 * q]]], cb = cls[z[pa[2 * q + 1]]];
+  const bool sw = ca > cb;
+  const double r = pr[q];
+  double t;
+  bool inside;
+  const int i = radial_locate(r, d, t, inside);
+  const double *rec = tslope + (std::size_t(tri_key(sw ? cb : ca, sw ? ca : cb, C)) * d.intervals + i) *
+                                   (std::size_t(kRadialCoefs) * L);
+  const double slope = inside ? radial_eval<L>(rec, l, t) : 0.0;
+  const int w = l / (2 * NH), row = l % (2 * NH);
+  const int side = (row >= NH) != sw ? 1 : 0;
+  double part = psc[std::size_t(q) * 4 * NH + side * 2 * NH + w * NH + row % NH] * slope;
+#pragma unroll
+  for (int o = 1; o < L; o <<= 1) part += __shfl_xor(part, o, L);
+  if (l == 0) {
+    double grad = part;
+    if (r < rc) {
+      const double u = r / rc;
+      grad += dfc[q] * (-30.0 * u * u * (1.0 - u) * (1.0 - u) / rc);
+    }
+    dr[q] += grad;
+  }
+}
+
 // ------------------------------------------------------ fused filters
 // Both filters of a block for 16 pairs per wavefront, on fp64 MFMA in the
 // layout of the table kernels above (features as rows, the pairs as the 16
@@ -1641,6 +1741,26 @@ void launch_b0(hipStream_t s, int F, int R, std::size_t slots, const B0Args &A) 
   throw std::logic_error("SO3LR: block 0's table kernels at widths other than F = 128, 256 and R = 32, 64");
 }
 
+// g_radial_fwd / g_radial_bwd at NH = 4 or 8 heads over cap pairs
+template <bool FWD>
+void launch_radial(hipStream_t s, int NH, const GContext &c, const double *tab, RadialDomain d, double *palpha,
+                   const double *psc, const double *dfc) {
+#define G_RAD(L)                                                                                                    \
+  if (4 * NH == L) {                                                                                                \
+    const dim3 grid(blocks_for(std::size_t(std::max(c.cap, 1)), 256 / L));                                         \
+    if constexpr (FWD)                                                                                              \
+      hipLaunchKernelGGL(g_radial_fwd<L>, grid, dim3(256), 0, s, c.nact, c.pa, c.pr, c.z, c.cls_lut, c.cls_C, tab, \
+                         d, c.inv_avg, palpha);                                                                     \
+    else                                                                                                            \
+      hipLaunchKernelGGL(g_radial_bwd<L>, grid, dim3(256), 0, s, c.nact, c.pa, c.pr, c.z, c.cls_lut, c.cls_C, tab, \
+                         d, psc, dfc, c.rc, c.dr);                                                                  \
+    return;                                                                                                         \
+  }
+  G_RAD(16) G_RAD(32)
+#undef G_RAD
+  throw std::logic_error("SO3LR: block 0's radial tables at other than 4 or 8 heads");
+}
+
 // g_filt_fwd / g_filt_bwd at F = 16 FT, R = 16 RT over cap pairs (one
 // wavefront per 16, the grid a multiple of 8: g_xcd_block)
 template <bool FWD>
@@ -1744,7 +1864,8 @@ void section(const GContext &c, const char *name, const std::function<void()> &f
 }
 }  // namespace
 
-GenericPath::GenericPath(const Model &m, const std::function<const double *(const std::vector<double> &)> &up) {
+GenericPath::GenericPath(const Model &m, const std::function<const double *(const std::vector<double> &)> &up,
+                         bool fit_radial) {
   const Architecture &a = m.arch();
   GDims &d = d_;
   d.F = a.F;
@@ -1896,6 +2017,33 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
   std::vector<double> t(256);
   for (int j = 0; j < 256; ++j) t[std::size_t(j)] = double(std::exp2(static_cast<long double>(j) / 256.0L));
   hw_.exp2_256 = up(t);
+  // block 0's radial hidden layers as piecewise polynomials (radial tables),
+  // used when both filters fit to within 1e-14 (values) and 1e-13 (slopes)
+  // of their largest magnitudes at the check points
+  if (fit_radial) {
+    const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
+    std::vector<double> val, slope;
+    bool ok = true;
+    for (int k = 0; k < 2 && ok; ++k) {
+      const std::string f = std::string("model.euclidean_transformers.0.") + (k ? "filter_net_ev." : "filter_net_inv.");
+      try {
+        const RadialFit fit = fit_radial_hidden(m.f64(f + "mlp_rbf.0.weight", {F, R}), m.f64(f + "mlp_rbf.0.bias", {F}),
+                                                int(F), int(R), bb, a.gamma, a.sr_cutoff, kRadialIntervals,
+                                                kRadialDegree);
+        ok = fit.value_error <= 1e-14 && fit.slope_error <= 1e-13;
+        val.insert(val.end(), fit.value.begin(), fit.value.end());
+        slope.insert(slope.end(), fit.slope.begin(), fit.slope.end());
+        rad_dom_ = RadialDomain{fit.r0, fit.step, fit.scale, fit.intervals};
+      } catch (const std::invalid_argument &) {
+        ok = false;
+      }
+    }
+    if (ok) {
+      rad_val_ = up(val);
+      rad_slope_ = up(slope);
+      radial_ok_ = true;
+    }
+  }
 }
 
 void GenericPath::carve(int N, int cap, int C, const std::function<double *(int, std::size_t)> &take) {
@@ -1956,11 +2104,24 @@ void GenericPath::forward(const GContext &c) {
       // block 0 through the element-pair tables: their rows as MFMA
       // operands, then both filters to the logits in one fused kernel
       const std::size_t NK = std::size_t(c.cls_C) * c.cls_C;
-      hipLaunchKernelGGL(g_cls_tables, dim3(unsigned(NK * 16), 2), dim3(unsigned(F)), 0, s, F, NH, FH, c.cls_C, qb,
-                         c.cls_rep, B.wcat[0], B.wcat[1], B.bcat[0], B.bcat[1], B.eb0[0], B.eb0[1], b_[CLS_M],
-                         b_[CLS_M] + NK * 32 * F, b_[CLS_B]);
-      section(c, "generic_filter_fwd_block0_tables",
-              [&] { launch_b0<true>(s, F, R, b0_slot_bound(c), b0_args(c, B, hw_, b_[RBF], b_[CLS_M], b_[CLS_B], F, pab)); });
+      if (!c.rad_tab || c.rad_build)  // with the radial tables filled, nothing reads these
+        hipLaunchKernelGGL(g_cls_tables, dim3(unsigned(NK * 16), 2), dim3(unsigned(F)), 0, s, F, NH, FH, c.cls_C, qb,
+                           c.cls_rep, B.wcat[0], B.wcat[1], B.bcat[0], B.bcat[1], B.eb0[0], B.eb0[1], b_[CLS_M],
+                           b_[CLS_M] + NK * 32 * F, b_[CLS_B]);
+      if (c.rad_tab) {
+        // the logits from the radial tables (filled once after set_system)
+        const std::size_t keys = std::size_t(c.cls_C) * (c.cls_C + 1) / 2;
+        if (c.rad_build)
+          hipLaunchKernelGGL(g_radial_tables, dim3(unsigned(keys * kRadialIntervals)), dim3(256), 0, s, F, NH, c.cls_C,
+                             b_[CLS_M], b_[CLS_B], rad_val_, rad_slope_, rad_dom_, c.rad_tab,
+                             c.rad_tab + keys * kRadialIntervals * radial_record());
+        section(c, "generic_filter_fwd_block0_radial",
+                [&] { launch_radial<true>(s, NH, c, c.rad_tab, rad_dom_, pab, nullptr, nullptr); });
+      } else {
+        section(c, "generic_filter_fwd_block0_tables", [&] {
+          launch_b0<true>(s, F, R, b0_slot_bound(c), b0_args(c, B, hw_, b_[RBF], b_[CLS_M], b_[CLS_B], F, pab));
+        });
+      }
     } else {
     // pair invariants and both filters (kokkos_integrated_block0.cpp:166-255)
     hipLaunchKernelGGL(g_pair_inv, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, evb,
@@ -2040,7 +2201,15 @@ void GenericPath::reverse(const GContext &c) {
       hipLaunchKernelGGL(g_attn_bwd_node, dim3((blocks_for(n * (F / 64), 4) + 7) / 8 * 8), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, qb, pfb,
                          c.pfc, pab, b_[PSC], b_[GAINV], b_[GQKV]);
     // filter reverse (kokkos_block2_attention_input_reverse.cpp:198-336)
-    if (tables) {
+    if (tables && c.rad_tab) {
+      // block 0 through the radial tables: the logits' adjoints times the
+      // slopes to dE/dr
+      const std::size_t keys = std::size_t(c.cls_C) * (c.cls_C + 1) / 2;
+      section(c, "generic_filter_bwd_block0_radial", [&] {
+        launch_radial<false>(s, NH, c, c.rad_tab + keys * kRadialIntervals * radial_record(), rad_dom_, nullptr,
+                             b_[PSC], b_[DFC]);
+      });
+    } else if (tables) {
       // block 0 through the element-pair tables, fused: the hidden rows'
       // adjoints from the table rows, through W0 to dE/dr (the spherical
       // input s has no adjoint in block 0)

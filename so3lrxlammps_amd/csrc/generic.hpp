@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "model.hpp"
+#include "radial_table.hpp"
 
 namespace so3lr_amd {
 
@@ -110,12 +111,24 @@ struct GContext {
   // cls_order[q], the slots end at *cls_slots (device)
   const int *cls_order = nullptr, *cls_slots = nullptr;
   static constexpr int kB0Pad = 32;
+  // block 0's radial tables (with the element-pair tables, when the model's
+  // fits hold): the element pairs' value and slope tables (GenericPath::
+  // radial_record() doubles per element pair and interval each), filled by
+  // this evaluation when rad_build; null: the element-pair MFMA kernels
+  double *rad_tab = nullptr;
+  bool rad_build = false;
 };
 
 class GenericPath {
  public:
   // upload: copies a host vector to device memory the evaluator owns.
-  GenericPath(const Model &m, const std::function<const double *(const std::vector<double> &)> &upload);
+  // fit_radial: fit block 0's radial hidden layers for the radial tables.
+  GenericPath(const Model &m, const std::function<const double *(const std::vector<double> &)> &upload,
+              bool fit_radial);
+  // block 0's radial tables: whether the fits hold, and the doubles of one
+  // table record (element pair and interval: kRadialCoefs x 4 NH logits)
+  bool radial_ok() const { return radial_ok_; }
+  std::size_t radial_record() const { return std::size_t(kRadialCoefs) * 4 * d_.NH; }
   const GDims &dims() const { return d_; }
   int F() const { return d_.F; }
   // The work buffers of one evaluation: take(id, doubles) returns buffer id's
@@ -135,6 +148,10 @@ class GenericPath {
   GBlock bw_[kMaxBlocks];
   GHeads hw_{};
   double *b_[kBuffers] = {};
+  // block 0's radial fits, [filter][interval][power][feature] (radial_table.hpp)
+  bool radial_ok_ = false;
+  RadialDomain rad_dom_{};
+  const double *rad_val_ = nullptr, *rad_slope_ = nullptr;
 };
 
 }  // namespace so3lr_amd

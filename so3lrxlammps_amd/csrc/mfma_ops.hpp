@@ -6,8 +6,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <type_traits>
 #include <utility>
+
+#include "radial_table.hpp"
 
 namespace so3lr_amd {
 namespace {
@@ -169,6 +172,43 @@ __device__ __forceinline__ double silu_tab_wide(double x, const double *tab) {
 __device__ __forceinline__ double silu_prime_tab_wide(double x, const double *tab) {
   const double s = rcp_act(1.0 + exp_tab(-fmin(fmax(x, -1000.0), 1000.0), tab));
   return s * (1.0 + x * (1.0 - s));
+}
+
+// ---------------------------------------------------------------- radial tables
+// Block 0's radial tables (evaluator.hip, generic.hip): per element pair
+// {lo <= hi} (triangular index tri_key) and interval of r, one polynomial of
+// degree kRadialDegree in t per logit, stored as kRadialCoefs / 2 coefficient
+// pairs x L logits x 2: logit l's coefficients 2 kp and 2 kp + 1 at
+// kp * 2 L + 2 l, so that the L lanes of a pair read 16 L contiguous bytes
+// per load.
+__device__ __forceinline__ int tri_key(int lo, int hi, int C) { return lo * C - lo * (lo - 1) / 2 + (hi - lo); }
+
+// Interval and local coordinate t of r; below r0 the basis variable is
+// clamped: the value at r0, slope 0 (inside = false).
+__device__ __forceinline__ int radial_locate(double r, const RadialDomain &d, double &t, bool &inside) {
+  inside = r >= d.r0;
+  if (!inside) {
+    t = -1.0;
+    return 0;
+  }
+  const int i = int(fmin((r - d.r0) * (0.5 * d.scale), double(d.intervals - 1)));
+  t = fma(r - fma(double(i), d.step, d.r0), d.scale, -1.0);
+  return i;
+}
+
+// Logit l's polynomial at t from its record (L logits), Horner from the
+// highest power.
+template <int L>
+__device__ __forceinline__ double radial_eval(const double *__restrict__ rec, int l, double t) {
+  static_assert(kRadialCoefs % 2 == 0, "the table records hold coefficient pairs");
+  double2 c[kRadialCoefs / 2];
+#pragma unroll
+  for (int kp = 0; kp < kRadialCoefs / 2; ++kp)
+    c[kp] = *reinterpret_cast<const double2 *>(rec + kp * 2 * L + 2 * l);
+  double v = c[kRadialCoefs / 2 - 1].y;
+#pragma unroll
+  for (int k = kRadialCoefs - 2; k >= 0; --k) v = fma(v, t, (k & 1) ? c[k >> 1].y : c[k >> 1].x);
+  return v;
 }
 
 }  // namespace

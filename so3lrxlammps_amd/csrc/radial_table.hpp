@@ -17,6 +17,15 @@
 
 namespace so3lr_amd {
 
+// Block 0's radial tables: intervals and polynomial degree of the fits, and
+// their domain as the kernels read it (intervals of width step from r0,
+// t = (r - left edge) * scale - 1)
+constexpr int kRadialIntervals = 256, kRadialDegree = 13, kRadialCoefs = kRadialDegree + 1;
+struct RadialDomain {
+  double r0, step, scale;
+  int intervals;
+};
+
 struct RadialFit {
   int intervals = 0, degree = 0, width = 0;
   double r0 = 0.0, r1 = 0.0, step = 0.0, scale = 0.0;  // domain, interval width, 2 / width

@@ -93,6 +93,45 @@ def test_wide_block0_element_tables_match_full_filters(monkeypatch, models, mode
     assert np.abs(w1 - w2).max() <= 1e-10 * max(1.0, np.abs(w2).max())
 
 
+@pytest.mark.parametrize("model,name", [("lift", "water3000"), ("lift_perturbed", "alanine_cation"),
+                                        ("f128_r64", "acetate"), ("deg1123", "water3000")])
+def test_wide_block0_radial_tables_match_element_tables(monkeypatch, models, model, name):
+    """Block 0's logits from the radial tables (the default) against the
+    element-pair MFMA kernels (SO3LR_NO_RADIAL_TABLES=1) on the generic
+    kernels, 8 and 4 heads: equal to rounding, and the kernel timings show
+    which path ran."""
+    from so3lrxlammps_amd import Context, Lists
+    from test_gpu_parity import _launches
+    ref, z, pos, box = support.load_golden(name)
+    q, m = ref.get("charge", 0), ref.get("multiplicity", 1)
+    if box is None:
+        lo, hi, per = pos.min(0) - 20.0, pos.max(0) + 20.0, (0, 0, 0)
+    else:
+        lo, hi, per = np.zeros(3), box, (1, 1, 1)
+    res = []
+    for off in ("1", "0"):
+        monkeypatch.setenv("SO3LR_NO_RADIAL_TABLES", off)
+        c = Context(models[model], 0)
+        c.kernel_timing(True)
+        c.set_system(z, q, m)
+        lists = Lists(pos, lo, hi, per)
+        c.set_topology(lists)
+        e, f, ea, w = c.compute(lists.rows_positions(pos))
+        ran = {k: _launches(c, "generic_filter_%s_block0_%s" % (k[0], k[1]))
+               for k in (("fwd", "radial"), ("bwd", "radial"), ("fwd", "tables"), ("bwd", "tables"))}
+        res.append((e, f.copy(), w.copy(), ran))
+        c.close()
+    (e1, f1, w1, ran1), (e2, f2, w2, ran2) = res
+    print("%s %s: |dE| %.2e max|dF| %.2e max|dW| %.2e" % (model, name, abs(e1 - e2), np.abs(f1 - f2).max(),
+                                                          np.abs(w1 - w2).max()), flush=True)
+    assert ran1[("fwd", "tables")] == 1 and ran1[("fwd", "radial")] == 0
+    assert ran2[("fwd", "radial")] == 1 and ran2[("bwd", "radial")] == 1
+    assert ran2[("fwd", "tables")] == 0 and ran2[("bwd", "tables")] == 0
+    assert abs(e1 - e2) <= 1e-12 * abs(e2)
+    assert np.abs(f1 - f2).max() <= 1e-10 * max(1.0, np.abs(f2).max() / 10.0)
+    assert np.abs(w1 - w2).max() <= 1e-10 * max(1.0, np.abs(w2).max())
+
+
 @pytest.mark.parametrize("count", [16, 17])
 def test_wide_element_table_limit(monkeypatch, models, count):
     """The generic kernels at the table path's limit (perturbed lift, a
