@@ -551,24 +551,47 @@ __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, const
 // Both filters of one block for 16 pairs per wavefront, 4 wavefronts per block.
 // Per filter the stream holds 96 weight fragments: W0 (s < 16: tile s % 8,
 // K chunk s / 8), W1 (16 <= s < 80) and E1 (80 <= s < 96), tile-minor.
-template <bool EV0>
-__global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(const int *n_active, const int *pa,
-                                                                     const double *pr, const double *ev,
-                                                                     const double *__restrict__ qkv, double inv_avg,
-                                                                     FilterMfma A, double *ps, double *pf,
-                                                                     double *palpha) {
+// RT (blocks after 0 on their radial tables): the pairs run in interval
+// order (16 slots of one interval per wavefront, -1 in the padding), and
+// each filter's radial branch W1 silu(W0 rbf + b0) + ob1 is, per output
+// tile, one MFMA product of the interval's coefficient tile (rtab) with the
+// pairs' powers of t instead of the W0 and W1 chains.
+#ifndef SO3LR_RT_FWD_WAVES
+#define SO3LR_RT_FWD_WAVES 2
+#endif
+#ifndef SO3LR_RT_BWD_WAVES
+#define SO3LR_RT_BWD_WAVES 2
+#endif
+template <bool EV0, bool RT = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT ? SO3LR_RT_FWD_WAVES : SO3LR_FILTER_FWD_WAVES,
+                                                                     RT ? SO3LR_RT_FWD_WAVES : SO3LR_FILTER_FWD_WAVES))) void
+k_filter_fwd_mfma(
+    const int *n_active, const int *pa, const double *pr, const double *ev, const double *__restrict__ qkv,
+    double inv_avg, FilterMfma A, double *ps, double *pf, double *palpha, const int *n_slots = nullptr,
+    const int *order = nullptr, const double *__restrict__ rtab = nullptr, RadialDomain rd = {}) {
   SO3LR_EXP2_TABLE(A)
-  const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  // consecutive pairs on one XCD: the endpoint rows they read are
-  // spatial neighbours, so they share that XCD's L2
-  const int blk = xcd_block_active((nact + 63) / 64);
-  if (blk < 0) return;
-  const int wave = blk * 4 + (threadIdx.x >> 6);
-  if (wave * 16 >= nact) return;  // whole wavefront idle
-  const int p = wave * 16 + j;
-  const bool valid = p < nact;
-  const int pp = valid ? p : nact - 1;
+  int p, pp, ri = 0;
+  bool valid;
+  v4d tp;
+  if constexpr (RT) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    bool inside;
+    if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
+    valid = p >= 0;
+    pp = valid ? p : order[wave * 16];
+  } else {
+    const int nact = *n_active;
+    // consecutive pairs on one XCD: the endpoint rows they read are
+    // spatial neighbours, so they share that XCD's L2
+    const int blk = xcd_block_active((nact + 63) / 64);
+    if (blk < 0) return;
+    const int wave = blk * 4 + (threadIdx.x >> 6);
+    if (wave * 16 >= nact) return;  // whole wavefront idle
+    p = wave * 16 + j;
+    valid = p < nact;
+    pp = valid ? p : nact - 1;
+  }
   const int a = pa[2 * pp], b = pa[2 * pp + 1];
   // q k v q_ev k_ev rows of both endpoints (tile-transposed channel order):
   // the lane's four channels of an output tile are one 32-byte vector
@@ -587,12 +610,27 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   // EV0 (block 0, ev = 0): the spherical branch sees s = 0 for every pair,
   // so it is the constant E1 silu(e0) + e1, folded into the output bias
   // (ob1p0); its entries are left out (13 per tile, 128 in all).
-  constexpr int TS = EV0 ? 24 : 27, PT = EV0 ? 13 : 15;
-  constexpr int UW = 5, UE = 13;  // first W1 and first E1 entry of a tile
+  // RT: the spherical layer-0 biases and operand (3), then per output tile
+  // the interval's coefficient tile (in place of the bias), the endpoint
+  // rows and the 2 E1 chunks (7 each): 59 entries.
+  static_assert(!(EV0 && RT), "block 0 has its own tables");
+  constexpr int TS = RT ? 3 : (EV0 ? 24 : 27), PT = RT ? 7 : (EV0 ? 13 : 15);
+  constexpr int UW = 5, UE = RT ? 5 : 13;  // first W1 and first E1 entry of a tile
   constexpr int NF = TS + 8 * PT;
   auto load = [&](auto si) -> v4d {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
-    if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
+    if constexpr (RT && s < 2) return tile_load(A.eb0p[which], s, lane);
+    else if constexpr (RT && s == 2) return tile_load(A.e0pk[which], 0, lane);
+    else if constexpr (RT) {
+      constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
+      constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;
+      if constexpr (u == 0) return frag_load(rtab + (std::size_t(ri) * 2 + which) * 8 * 256, mt, lane);
+      else if constexpr (u == 1) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
+      else if constexpr (u == 2) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
+      else if constexpr (u == 3) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
+      else if constexpr (u == 4) return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
+      else return wload(A.e1p[which], 2, mt, u - UE, lane);
+    } else if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
     else if constexpr (!EV0 && s < 10) return tile_load(A.eb0p[which], s - 8, lane);
     else if constexpr (!EV0 && s == 10) return tile_load(A.e0pk[which], 0, lane);
     else if constexpr (s < TS) return wload(A.w0p[which], 2, (s - TS + 16) % 8, (s - TS + 16) / 8, lane);
@@ -612,7 +650,7 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   st.prime();
 
   v4d rb[2];
-  rbf8(pr[pp], g, A, exp2_lds, rb);
+  if constexpr (!RT) rbf8(pr[pp], g, A, exp2_lds, rb);
   // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
   double sg = 0.0;
   if constexpr (!EV0) {
@@ -631,13 +669,23 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 
   st.run([&](auto si, const v4d &w) {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
-    if constexpr (s < 8) {
+    if constexpr (RT && s < 2) {
+      h2[s] = w;
+    } else if constexpr (RT && s == 2) {
+      // the spherical hidden row, before the first output tile
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        h2[t] = mfma(w[t], sg, h2[t]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
+      }
+    } else if constexpr (!RT && s < 8) {
       h[s] = w;
-    } else if constexpr (!EV0 && s < 10) {
+    } else if constexpr (!RT && !EV0 && s < 10) {
       h2[s - 8] = w;
-    } else if constexpr (!EV0 && s == 10) {
+    } else if constexpr (!RT && !EV0 && s == 10) {
       e0 = w;
-    } else if constexpr (s < TS) {
+    } else if constexpr (!RT && s < TS) {
       constexpr int i = s - TS + 16;  // W0 entry 0..15
       h[i % 8] = mfma4(w, rb[i / 8], h[i % 8]);
       // each hidden tile's SiLU is taken one step before its first use,
@@ -649,7 +697,8 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
     } else {
       constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
       if constexpr (u == 0) {
-        o = w;
+        if constexpr (RT) o = mfma4(w, tp, v4d{0.0, 0.0, 0.0, 0.0});  // the radial branch of tile mt
+        else o = w;
       } else if constexpr (u == 1 || u == 3) {
         qv = w;
       } else if constexpr (u == 2) {
@@ -749,8 +798,9 @@ constexpr std::array<BwdEntry, bwd_section_len<NM, SRC>()> bwd_schedule() {
     if (SRC == 1 && T + 1 < 8 && ((T + 1) & 1) == 0) riders[nr++] = BwdEntry{kBwdS, 0, T + 1, (T + 1) / 2, 1};
     if (T + 1 < 8)
       for (int u = 0; u < 4; ++u) riders[nr++] = BwdEntry{kBwdR, u, T + 1, (T + 1) / 2, 0};
-    for (int m = 0; m < NM; ++m) {
-      put(kBwdM, m, T, h, 0);
+    // one rider after each M entry; riders beyond the M entries follow them
+    for (int m = 0; m < (NM > nr ? NM : nr); ++m) {
+      if (m < NM) put(kBwdM, m, T, h, 0);
       if (m < nr) out[n++] = riders[m];
     }
   }
@@ -784,7 +834,8 @@ constexpr bool bwd_schedule_ok() {
     if (m_seen[T] != NM || rows_seen[T] != 4) return false;
   return true;
 }
-static_assert(bwd_schedule_ok<10, 1>() && bwd_schedule_ok<8, 0>() && bwd_schedule_ok<8, 2>(),
+static_assert(bwd_schedule_ok<10, 1>() && bwd_schedule_ok<8, 0>() && bwd_schedule_ok<8, 2>() &&
+                  bwd_schedule_ok<3, 1>(),
               "reverse-filter operand schedule out of order");
 
 // Reverse of the attention's pair terms, of both filters, of the Bernstein
@@ -822,24 +873,43 @@ static_assert(bwd_schedule_ok<10, 1>() && bwd_schedule_ok<8, 0>() && bwd_schedul
 // EV0 (block 0, ev = 0): the spherical branch is a constant (folded into the
 // output bias by the forward kernel) and s has no adjoint to give, so its
 // entries are left out.
-template <bool EV0, bool FIRST>
-__global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
+// RT (blocks after 0 on their radial tables): pairs in interval order as in
+// the forward; the first section keeps E1^T (2 entries per chunk) and takes
+// the interval's slope tile against each chunk's df (third entry), whose
+// sum over the powers of t is the radial branches' dE/dr; the layer-0
+// recompute, W0^T and the Bernstein basis are left out.
+template <bool EV0, bool FIRST, bool RT = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT ? SO3LR_RT_BWD_WAVES : SO3LR_FILTER_WAVES,
+                                                                     RT ? SO3LR_RT_BWD_WAVES : SO3LR_FILTER_WAVES))) void
+k_filter_bwd_mfma(
     const int *n_active, const int *pa, const double *pr, const double *ps, const double *pfc, const double *pY,
     const double *palpha, const double *__restrict__ qkv, const double *__restrict__ gainv,
     const double *__restrict__ gaev, const double *__restrict__ psc, const double *__restrict__ pdfc, double inv_avg,
-    FilterMfma A, double rc, double *ds, double *dr, double *dY) {
+    FilterMfma A, double rc, double *ds, double *dr, double *dY, const int *n_slots = nullptr,
+    const int *order = nullptr, const double *__restrict__ rtab = nullptr, RadialDomain rd = {}) {
+  static_assert(!(EV0 && RT), "block 0 has its own tables");
   SO3LR_EXP2_TABLE(A)
-  const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  // consecutive pairs on one XCD: the node rows they gather are spatial
-  // neighbours, so they share that XCD's L2
-  const int blk = xcd_block_active((nact + 63) / 64);
-  if (blk < 0) return;
-  const int wave = blk * 4 + (threadIdx.x >> 6);
-  if (wave * 16 >= nact) return;
-  const int p = wave * 16 + j;
-  const bool valid = p < nact;
-  const int pp = valid ? p : nact - 1;
+  int p, pp, ri = 0;
+  bool valid, inside = false;
+  v4d tp;
+  if constexpr (RT) {
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
+    valid = p >= 0;
+    pp = valid ? p : order[wave * 16];
+  } else {
+    const int nact = *n_active;
+    // consecutive pairs on one XCD: the node rows they gather are spatial
+    // neighbours, so they share that XCD's L2
+    const int blk = xcd_block_active((nact + 63) / 64);
+    if (blk < 0) return;
+    const int wave = blk * 4 + (threadIdx.x >> 6);
+    if (wave * 16 >= nact) return;
+    p = wave * 16 + j;
+    valid = p < nact;
+    pp = valid ? p : nact - 1;
+  }
   const int a = pa[2 * pp], b = pa[2 * pp + 1];
   // node rows, tile-transposed: chunk T of this lane at +16 T
   const double *ra = qkv + std::size_t(a) * 640 + 4 * g, *rb = qkv + std::size_t(b) * 640 + 4 * g;
@@ -848,10 +918,10 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
 
   // head scalars: block 0 forms them here (SRC 0 and 2), later blocks read
   // the node-major reverse's record (SRC 1)
-  constexpr int NM = EV0 ? 8 : 10, SRC0 = EV0 ? 0 : 1, SRC1 = EV0 ? 2 : 1;
+  constexpr int NM = RT ? 3 : (EV0 ? 8 : 10), SRC0 = EV0 ? 0 : 1, SRC1 = EV0 ? 2 : 1;
   constexpr int A_END0 = bwd_section_len<NM, SRC0>(), A_END1 = bwd_section_len<NM, SRC1>();
   const double *rec = psc + 16 * std::size_t(pp);
-  constexpr int B_LEN = 24, C_LEN = EV0 ? 0 : 3, D_LEN = 16, E_LEN = EV0 ? 0 : 2;
+  constexpr int B_LEN = RT ? 0 : 24, C_LEN = EV0 ? 0 : 3, D_LEN = RT ? 0 : 16, E_LEN = EV0 ? 0 : 2;
   constexpr int TAIL = B_LEN + C_LEN + D_LEN + E_LEN;
   constexpr int NB0 = A_END0 + TAIL, NB1 = A_END1 + TAIL;
   auto load = [&](auto si) -> v4d {
@@ -873,7 +943,9 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
         else if constexpr (e.q == 2) return row(rb, qoff + 16 * e.T);
         else return row(ra, koff + 16 * e.T);
       } else {
-        if constexpr (e.q < 8) return wload(A.w1tp[which], 8, e.q, e.T, lane);
+        if constexpr (RT && e.q == 2) return frag_load(rtab + (std::size_t(ri) * 2 + which) * 8 * 256, e.T, lane);
+        else if constexpr (RT) return wload(A.e1tp[which], 8, e.q, e.T, lane);
+        else if constexpr (e.q < 8) return wload(A.w1tp[which], 8, e.q, e.T, lane);
         else return wload(A.e1tp[which], 8, e.q - 8, e.T, lane);
       }
     } else if constexpr (s < A_END + B_LEN) {
@@ -941,7 +1013,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
   // d rbf and d s of one filter, folded into scalars at the end of their
   // sections (dE/dr is linear in d rbf), so neither is held through the next
   // filter's df section
-  v4d drb[2], dsa;
+  v4d drb[2], dsa, accdr;
   double part = 0.0, ds_acc = 0.0;
   double ci = 0.0, co = 0.0, s_in = 0.0, s_out = 0.0;
 
@@ -954,6 +1026,7 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
       for (int mt = 0; mt < 8; ++mt) dh[mt] = zero;
       dh2[0] = zero;
       dh2[1] = zero;
+      if constexpr (RT && which == 0) accdr = zero;
     }
     if constexpr (s < A_END) {
       constexpr BwdEntry e = bwd_entry<NM, which ? SRC1 : SRC0>(s);
@@ -1001,8 +1074,14 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
         }
       } else {
         if constexpr (e.q == 0) bT = bTn;
-        if constexpr (e.q < 8) dh[e.q] = mfma4(w, bT, dh[e.q]);
-        else dh2[e.q - 8] = mfma4(w, bT, dh2[e.q - 8]);
+        if constexpr (RT) {
+          if constexpr (e.q < 2) dh2[e.q] = mfma4(w, bT, dh2[e.q]);
+          else accdr = mfma4(w, bT, accdr);  // slopes . df, rows = powers of t
+        } else if constexpr (e.q < 8) {
+          dh[e.q] = mfma4(w, bT, dh[e.q]);
+        } else {
+          dh2[e.q - 8] = mfma4(w, bT, dh2[e.q - 8]);
+        }
       }
     } else if constexpr (s < B_END) {
       constexpr int mt = (s - A_END) / 3, u = (s - A_END) % 3;
@@ -1059,12 +1138,15 @@ __global__ __launch_bounds__(256) FILTER_OCCUPANCY void k_filter_bwd_mfma(
       }
     }
     // the last tile's silu' (it is needed from the last two W0^T steps on)
-    if constexpr (s == B_END) {
+    if constexpr (!RT && s == B_END) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) dh[7][q] *= silu_prime_tab(prev[q], exp2_lds);
     }
   });
 
+  // RT: the radial branches' dE/dr, sum over the powers of t (rows g + 4 r)
+  if constexpr (RT)
+    part = inside ? ((accdr[0] * tp[0] + accdr[1] * tp[1]) + accdr[2] * tp[2]) + accdr[3] * tp[3] : 0.0;
   // dE/dr: the Bernstein part of both filters + the cutoff
   part += __shfl_xor(part, 16, kWave);
   part += __shfl_xor(part, 32, kWave);
@@ -1671,6 +1753,80 @@ __global__ __launch_bounds__(256) void k_radial_bwd(const int *n_active, const i
     }
     dr[p] += grad;
   }
+}
+
+// ---------------------------------------------------------------- blocks after 0, radial tables
+// A filter's radial branch W1 silu(W0 rbf + b0) + ob1 (the whole output bias
+// included) depends on r alone in every block: fit_radial_hidden fits its
+// 128 outputs and their r-derivatives per interval of r, and the blocks
+// after 0 evaluate the fits as MFMA products over a wavefront's 16 pairs,
+// which therefore lie in one interval: the active pairs in interval order,
+// each interval's bucket padded to 16 slots (-1 in the padding): counts
+// (k_rint_count), bucket starts (k_rint_scan), placement (k_rint_place).  Within a bucket the order depends on the atomics'
+// timing; each pair's results go to its own rows, so the results do not.
+__device__ __forceinline__ int rint_key(double r, const RadialDomain &d) {
+  double t;
+  bool inside;
+  return radial_locate(r, d, t, inside);
+}
+
+__global__ __launch_bounds__(256) void k_rint_count(const int *n_active, const double *pr, RadialDomain d,
+                                                    int *hist) {
+  __shared__ int lc[kRadialIntervals];
+  const int nact = *n_active;
+  const int p0 = blockIdx.x * kClsChunk;
+  if (p0 >= nact) return;  // the whole block
+  for (int t = threadIdx.x; t < kRadialIntervals; t += 256) lc[t] = 0;
+  __syncthreads();
+  for (int it = 0; it < kClsPer; ++it) {
+    const int p = p0 + it * 256 + threadIdx.x;
+    if (p < nact) atomicAdd(&lc[rint_key(pr[p], d)], 1);
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < kRadialIntervals; t += 256)
+    if (lc[t]) atomicAdd(&hist[t], lc[t]);
+}
+
+// bucket starts of the 256 intervals, each bucket padded to 16 slots, into
+// cursor; the slots' end into *total (one block of 256 threads)
+static_assert(kRadialIntervals == 256, "k_rint_scan: one thread per interval");
+__global__ __launch_bounds__(256) void k_rint_scan(const int *hist, int *cursor, int *total) {
+  __shared__ int v[kRadialIntervals];
+  const int t = threadIdx.x;
+  const int own = (hist[t] + 15) / 16 * 16;
+  v[t] = own;
+  __syncthreads();
+  for (int o = 1; o < kRadialIntervals; o <<= 1) {
+    const int add = t >= o ? v[t - o] : 0;
+    __syncthreads();
+    v[t] += add;
+    __syncthreads();
+  }
+  cursor[t] = v[t] - own;
+  if (t == kRadialIntervals - 1) *total = v[t];
+}
+
+__global__ __launch_bounds__(256) void k_rint_place(const int *n_active, const double *pr, RadialDomain d,
+                                                    int *cursor, int *order) {
+  __shared__ int lc[kRadialIntervals], lb[kRadialIntervals];
+  const int nact = *n_active;
+  const int p0 = blockIdx.x * kClsChunk;
+  if (p0 >= nact) return;
+  for (int t = threadIdx.x; t < kRadialIntervals; t += 256) lc[t] = 0;
+  __syncthreads();
+  int key[kClsPer], rank[kClsPer];
+#pragma unroll
+  for (int it = 0; it < kClsPer; ++it) {
+    const int p = p0 + it * 256 + threadIdx.x;
+    key[it] = p < nact ? rint_key(pr[p], d) : -1;
+    rank[it] = key[it] >= 0 ? atomicAdd(&lc[key[it]], 1) : 0;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < kRadialIntervals; t += 256) lb[t] = lc[t] ? atomicAdd(&cursor[t], lc[t]) : 0;
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kClsPer; ++it)
+    if (key[it] >= 0) order[lb[key[it]] + rank[it]] = p0 + it * 256 + threadIdx.x;
 }
 
 // ---------------------------------------------------------------- MFMA node GEMMs
@@ -3345,6 +3501,57 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
       radial_ok_ = true;
     }
   }
+  // the blocks after 0: each filter's whole radial branch W1 h(r) + ob1 as
+  // piecewise polynomials (the same bound), laid out as MFMA operands: per
+  // interval and filter the coefficients (128 x 16 powers, zero beyond the
+  // degree) and the slope coefficients transposed (16 x 128)
+  if (!a.generic && radial_tables_ && layers_ > 1) {
+    const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
+    bool ok = true;
+    std::vector<std::vector<double>> rows(layers_), drs(layers_);
+    for (int b = 1; b < layers_ && ok; ++b) {
+      std::vector<RadialFit> fits;
+      for (int k = 0; k < 2 && ok; ++k) {
+        const std::string f = "model.euclidean_transformers." + std::to_string(b) + "." +
+                              (k ? "filter_net_ev." : "filter_net_inv.");
+        const auto w1 = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.weight", {F, F});
+        auto ob1 = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F});
+        const auto eb1 = m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F});
+        for (std::size_t c = 0; c < F; ++c) ob1[c] += eb1[c];
+        try {
+          fits.push_back(fit_radial_hidden(m.f64(f + "mlp_rbf.0.weight", {F, R}), m.f64(f + "mlp_rbf.0.bias", {F}),
+                                           int(F), int(R), bb, gamma_, rc_, kRadialIntervals, kRadialDegree, &w1,
+                                           &ob1, int(F)));
+          ok = fits.back().value_error <= 1e-14 && fits.back().slope_error <= 1e-13;
+        } catch (const std::invalid_argument &) {
+          ok = false;
+        }
+      }
+      if (!ok) break;
+      const std::size_t n = kRadialCoefs;
+      for (int i = 0; i < kRadialIntervals; ++i)
+        for (int k = 0; k < 2; ++k) {
+          const RadialFit &ft = fits[std::size_t(k)];
+          std::vector<double> cv(F * n), st(n * F);
+          for (std::size_t c = 0; c < F; ++c)
+            for (std::size_t kk = 0; kk < n; ++kk) {
+              cv[c * n + kk] = ft.value[(std::size_t(i) * n + kk) * F + c];
+              st[kk * F + c] = ft.slope[(std::size_t(i) * n + kk) * F + c];
+            }
+          const auto pr = permute_mfma(cv, F, n), pd = permute_mfma(st, n, F);
+          rows[std::size_t(b)].insert(rows[std::size_t(b)].end(), pr.begin(), pr.end());
+          drs[std::size_t(b)].insert(drs[std::size_t(b)].end(), pd.begin(), pd.end());
+        }
+      rbl_dom_ = RadialDomain{fits[0].r0, fits[0].step, fits[0].scale, fits[0].intervals};
+    }
+    if (ok) {
+      for (int b = 1; b < layers_; ++b) {
+        bw_[b].rrow = up(rows[std::size_t(b)]);
+        bw_[b].rdr = up(drs[std::size_t(b)]);
+      }
+      radial_blocks_ = true;
+    }
+  }
   if (!a.generic) {
     const std::string e = "model.atomic_energy_output_block.", q = "model.partial_charges_output_block.",
                       h = "model.hirshfeld_output_block.";
@@ -3488,7 +3695,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
   perm_ = buf("perm"); nz_ = buf("nz"); nx0_ = buf("nx0"); xn_ = buf("xn");
   cls_lut_ = buf("cls_lut"); cls_rep0_ = buf("cls_rep0"); cls_rep_ = buf("cls_rep"); cls_mt_ = buf("cls_mt");
   cls_c0_ = buf("cls_c0"); cls_gv_ = buf("cls_gv"); cls_hist_ = buf("cls_hist"); cls_order_ = buf("cls_order");
-  cls_rows_ = buf("cls_rows"); rad_tab_ = buf("rad_tab");
+  cls_rows_ = buf("cls_rows"); rad_tab_ = buf("rad_tab"); rint_order_ = buf("rint_order"); rint_hist_ = buf("rint_hist");
   iact_ = buf("iact"); iother_ = buf("iother"); red_part_ = buf("red_part"); probe_ = buf("probe");
   top_owner_ = buf("top_owner"); top_stat_ = buf("top_stat"); top_slots_ = buf("top_slots");
   top_skeys_ = buf("top_skeys"); top_tmp_ = buf("top_tmp"); top_box_ = buf("top_box");
@@ -3770,6 +3977,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
   // and with the radial tables (k_radial_fwd, k_radial_bwd)
   const bool use_rad = use_cls && radial_ok_;
+  // the blocks after 0 on their radial tables (k_filter_fwd_mfma<false, true>,
+  // k_filter_bwd_mfma<false, false, true>, in interval order)
+  const bool use_rt = !gen_ && !scalar && radial_blocks_ && L > 1;
+  int *rord = nullptr, *rhist = nullptr;
   // (the generic path's: g_cls_tables, g_b0_fwd, g_b0_bwd)
   const bool gen_cls = gen_ && class_tables_ && n_cls_ > 0;
   const int C = use_cls ? n_cls_ : 0;
@@ -3809,6 +4020,11 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     dfc = take<double>(dfc_, Pa);
     psc = scalar ? nullptr : take<double>(psc_, 16 * Pa);
     ds = take<double>(ds_, 4 * Pa);
+    if (use_rt) {
+      // counts, bucket cursors and the slots' end; the interval order
+      rhist = take<int>(rint_hist_, 2 * kRadialIntervals + 1);
+      rord = take<int>(rint_order_, Pa + 16 * std::size_t(kRadialIntervals));
+    }
     if (use_cls) {
       crep = take<int>(cls_rep_, kMaxClasses);
       chist = take<int>(cls_hist_, 2 * kMaxClasses * kMaxClasses);  // counts, then bucket cursors
@@ -4037,6 +4253,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const unsigned gP = unsigned(PA);
   const unsigned gP64 = unsigned(std::max(1, ceil_div(PA, 64)));  // 64 pairs per MFMA block
   const unsigned gP16 = unsigned(std::max(1, ceil_div(PA, 16)));  // 16 pairs per radial-table block
+  // slots of the interval order: every bucket padded by fewer than 16
+  const int rslots_max = PA + 16 * kRadialIntervals;
+  const unsigned gR = unsigned(ceil_div(rslots_max, 64));  // 16 slots per wavefront
+  const int *rslots = rhist ? rhist + 2 * kRadialIntervals : nullptr;
 
   // --- interaction blocks, forward ---
   for (int b = 0; b < L; ++b) {
@@ -4055,6 +4275,16 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     }
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
+    if (use_rt && b == 1) {
+      // the active pairs in interval order, for every block after 0 and the reverse
+      const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
+      hipLaunchKernelGGL(k_fill_int, dim3(1), dim3(256), 0, s, rhist, kRadialIntervals, 0);
+      hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(rslots_max, 256))), dim3(256), 0, s, rord, rslots_max, -1);
+      hipLaunchKernelGGL(k_rint_count, gsort, dim3(256), 0, s, nact, pr, rbl_dom_, rhist);
+      hipLaunchKernelGGL(k_rint_scan, dim3(1), dim3(kRadialIntervals), 0, s, rhist, rhist + kRadialIntervals,
+                         rhist + 2 * kRadialIntervals);
+      hipLaunchKernelGGL(k_rint_place, gsort, dim3(256), 0, s, nact, pr, rbl_dom_, rhist + kRadialIntervals, rord);
+    }
     // the MFMA filter also forms the attention logits of both directions
     // from the filter tiles it holds; the scalar cross-check path leaves them
     // to the full attention kernel
@@ -4108,6 +4338,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       else if (b == 0)  // ev = 0: the spherical branch is a constant
         hipLaunchKernelGGL(k_filter_fwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
                            psb, pfb, pab);
+      else if (use_rt)  // in interval order, the radial branches from the tables
+        hipLaunchKernelGGL((k_filter_fwd_mfma<false, true>), dim3(gR), dim3(256), 0, s, nact, pa, pr, evb, qb,
+                           inv_avg, FM, psb, pfb, pab, rslots, rord, B.rrow, rbl_dom_);
       else
         hipLaunchKernelGGL(k_filter_fwd_mfma<false>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
                            psb, pfb, pab);
@@ -4228,6 +4461,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                      qb, gainv, gaev, psc, dfc, inv_avg, FM, rc_, ds, dr, dY)
           if (b == 0 && first) SO3LR_FILTER_BWD(true, true);
           else if (b == 0) SO3LR_FILTER_BWD(true, false);
+          else if (use_rt)  // in interval order, the radial branches' dE/dr from the slope tables
+            hipLaunchKernelGGL((k_filter_bwd_mfma<false, false, true>), dim3(gR), dim3(256), 0, s, nact, pa, pr, psb,
+                               pfc, pY, pab, qb, gainv, gaev, psc, dfc, inv_avg, FM, rc_, ds, dr, dY, rslots, rord,
+                               B.rdr, rbl_dom_);
           else SO3LR_FILTER_BWD(false, false);  // dE/dY of blocks after 0: the node-major reverse
 #undef SO3LR_FILTER_BWD
         });

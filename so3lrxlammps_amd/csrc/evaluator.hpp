@@ -67,6 +67,11 @@ struct BlockWeights {
   const double *ob1p0[2];                               // ob1p with the ev = 0 spherical branch folded in (block 0) (ob1 = b1 + eb1)
   const double *ob10[2];                                // the same output bias in natural order (block 0's tables)
   const double *e0pk[2];                                // spherical layer 0, one v4d per lane
+  // radial tables of the blocks after 0 (the RT filter kernels): per
+  // interval and filter, the radial branch W1 silu(W0 rbf + b0) + ob1 as
+  // 16 powers of t (an MFMA A operand of 128 x 16) and its r-derivative
+  // (16 x 128); null without the tables
+  const double *rrow, *rdr;
   // MFMA operand order of the node layers: forward and reverse (transpose)
   const double *qkvp, *qkvtp;           // per head (160 x 32) and (32 x 160)
   const double *m1p, *m2p, *m1tp, *m2tp;
@@ -298,6 +303,13 @@ class Evaluator {
   // sized by set_system and filled by the first evaluation after it
   // (rad_stale_).
   bool radial_tables_ = true, radial_ok_ = false, rad_stale_ = true;
+  // the blocks after 0 on their radial tables (BlockWeights::rrow, rdr): every
+  // such block's both radial branches fit to the bound; their pairs in
+  // interval order, each interval's bucket padded to 16 slots (rint_order_,
+  // -1 in the padding), counted and placed per evaluation (rint_hist_)
+  bool radial_blocks_ = false;
+  RadialDomain rbl_dom_{};
+  Buffer *rint_order_, *rint_hist_;
   RadialDomain rad_dom_{};
   const double *rad_val_ = nullptr, *rad_slope_ = nullptr;  // [filter][interval][power][feature]
   Buffer *rad_tab_;

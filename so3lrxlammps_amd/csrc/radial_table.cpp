@@ -17,9 +17,33 @@ struct Net {
   const std::vector<double> &w0, &b0, &bb;
   int F, R;
   LD gamma;
+  const std::vector<double> *w1, *bias;  // optional output layer (O, F), (O)
+  int O;                                 // outputs: O with w1, F without
 };
 
 // h and dh/dr of every feature at r >= r0 (x below its clamp)
+void hidden_at(const Net &n, LD r, LD *h, LD *dh, std::vector<LD> &bas, std::vector<LD> &dbas);
+
+// the fitted function at r: h, or w1 h + bias with the output layer;
+// hs, dhs: work rows of F
+void output_at(const Net &n, LD r, LD *y, LD *dy, std::vector<LD> &bas, std::vector<LD> &dbas, LD *hs, LD *dhs) {
+  if (!n.w1) {
+    hidden_at(n, r, y, dy, bas, dbas);
+    return;
+  }
+  hidden_at(n, r, hs, dhs, bas, dbas);
+  for (int c = 0; c < n.O; ++c) {
+    const double *w = n.w1->data() + std::size_t(c) * n.F;
+    LD v = (*n.bias)[c], dv = 0.0L;
+    for (int f = 0; f < n.F; ++f) {
+      v += LD(w[f]) * hs[f];
+      dv += LD(w[f]) * dhs[f];
+    }
+    y[c] = v;
+    dy[c] = dv;
+  }
+}
+
 void hidden_at(const Net &n, LD r, LD *h, LD *dh, std::vector<LD> &bas, std::vector<LD> &dbas) {
   const LD lx = -n.gamma * r, x = std::exp(lx), l1x = std::log1p(-x), q = x / (1.0L - x);
   for (int c = 0; c < n.R; ++c) {
@@ -44,10 +68,12 @@ void hidden_at(const Net &n, LD r, LD *h, LD *dh, std::vector<LD> &bas, std::vec
 
 RadialFit fit_radial_hidden(const std::vector<double> &w0, const std::vector<double> &b0, int width, int nbasis,
                             const std::vector<double> &basis_b, double gamma, double r_cut, int intervals,
-                            int degree) {
+                            int degree, const std::vector<double> *w1, const std::vector<double> *bias,
+                            int outputs) {
   if (width < 1 || nbasis < 2 || intervals < 1 || degree < 1 || gamma <= 0.0 || r_cut <= 0.0 ||
       w0.size() != std::size_t(width) * nbasis || b0.size() != std::size_t(width) ||
-      basis_b.size() != std::size_t(nbasis))
+      basis_b.size() != std::size_t(nbasis) || (w1 != nullptr) != (bias != nullptr) ||
+      (w1 && (outputs < 1 || w1->size() != std::size_t(outputs) * width || bias->size() != std::size_t(outputs))))
     throw std::invalid_argument("SO3LR: radial fit: inconsistent arguments");
   const LD g = gamma;
   // x = e^{-gamma r} stays at or above 1e-6 up to the cutoff
@@ -56,16 +82,16 @@ RadialFit fit_radial_hidden(const std::vector<double> &w0, const std::vector<dou
   RadialFit fit;
   fit.intervals = intervals;
   fit.degree = degree;
-  fit.width = width;
+  fit.width = w1 ? outputs : width;
   fit.r0 = double(-std::log1p(-1e-6L) / g);
   fit.r1 = r_cut;
   if (!(fit.r0 < fit.r1)) throw std::invalid_argument("SO3LR: radial fit: empty domain");
   fit.step = (fit.r1 - fit.r0) / intervals;
   fit.scale = 2.0 / fit.step;
-  const int n = degree + 1, F = width;
+  const int n = degree + 1, F = fit.width;  // F: the fitted functions
   fit.value.assign(std::size_t(intervals) * n * F, 0.0);
   fit.slope.assign(std::size_t(intervals) * n * F, 0.0);
-  const Net net{w0, b0, basis_b, width, nbasis, g};
+  const Net net{w0, b0, basis_b, width, nbasis, g, w1, bias, F};
 
   // Chebyshev nodes, cos(pi k (j + 1/2) / n), and the monomial coefficients of T_k
   std::vector<LD> tn(n), ck(std::size_t(n) * n), tm(std::size_t(n) * n, 0.0L);
@@ -87,13 +113,14 @@ RadialFit fit_radial_hidden(const std::vector<double> &w0, const std::vector<dou
   };
   auto run = [&](int i0, int i1, Part &pt) {
     std::vector<LD> bas(nbasis), dbas(nbasis), hv(std::size_t(n) * F), dv(std::size_t(n) * F),
-        cc(std::size_t(n) * F), he(F), de(F);
+        cc(std::size_t(n) * F), he(F), de(F), hs(width), dhs(width);
     constexpr int kChecks = 9;  // t = -1, -0.75, ..., 1
     for (int i = i0; i < i1; ++i) {
       const double e = std::fma(double(i), fit.step, fit.r0);
       auto r_at = [&](LD t) { return LD(e) + (t + 1.0L) / LD(fit.scale); };
       for (int j = 0; j < n; ++j)
-        hidden_at(net, r_at(tn[j]), &hv[std::size_t(j) * F], &dv[std::size_t(j) * F], bas, dbas);
+        output_at(net, r_at(tn[j]), &hv[std::size_t(j) * F], &dv[std::size_t(j) * F], bas, dbas, hs.data(),
+                  dhs.data());
       for (int which = 0; which < 2; ++which) {
         const std::vector<LD> &y = which ? dv : hv;
         std::vector<double> &out = which ? fit.slope : fit.value;
@@ -113,7 +140,7 @@ RadialFit fit_radial_hidden(const std::vector<double> &w0, const std::vector<dou
       // the stored (double) coefficients by Horner in double, as on the device
       for (int c = 0; c < kChecks; ++c) {
         const LD t = -1.0L + 2.0L * c / (kChecks - 1);
-        hidden_at(net, r_at(t), he.data(), de.data(), bas, dbas);
+        output_at(net, r_at(t), he.data(), de.data(), bas, dbas, hs.data(), dhs.data());
         const double td = double(t);
         for (int f = 0; f < F; ++f) {
           double pv = fit.value[(std::size_t(i) * n + degree) * F + f];

@@ -1,5 +1,6 @@
 // Piecewise polynomial fits of a filter's radial hidden layer, for block 0's
-// radial tables (host side; the kernels are in evaluator.hip and generic.hip).
+// radial tables (host side; the kernels are in evaluator.hip and generic.hip),
+// and of a whole radial branch W1 h(r) + bias for the blocks after 0.
 //
 // The radial branch of a filter is h(r) = silu(W0 b(r) + b0), b the Bernstein
 // basis of x = e^{-gamma r} (kokkos_integrated_block0.cpp:117-160, 194-255).
@@ -37,11 +38,14 @@ struct RadialFit {
 };
 
 // w0: (width, nbasis) row-major; b0: (width); basis_b: (nbasis) log prefactors
-// of the Bernstein basis, exponents c and nbasis - 1 - c.  Throws
+// of the Bernstein basis, exponents c and nbasis - 1 - c.  With w1 (outputs,
+// width) row-major and bias (outputs) given, the fit is of the filter's
+// radial branch w1 h(r) + bias instead (RadialFit::width = outputs).  Throws
 // std::invalid_argument when the far clamp of x (x >= 1e-6) falls inside
 // the domain.
 RadialFit fit_radial_hidden(const std::vector<double> &w0, const std::vector<double> &b0, int width, int nbasis,
                             const std::vector<double> &basis_b, double gamma, double r_cut, int intervals,
-                            int degree);
+                            int degree, const std::vector<double> *w1 = nullptr,
+                            const std::vector<double> *bias = nullptr, int outputs = 0);
 
 }  // namespace so3lr_amd
