@@ -63,8 +63,23 @@ _FILTER_BWD_B0_ISSUED = _FILTER_B0 + 2 * 2 * _mac((128, 32))         # 98,304
 # (4 heads x 2 directions) per filter; the reverse recomputes W0's output
 _FILTER_B0_TAB = 2 * 2 * _mac((128, 32), (8, 128))                    # 20,480
 _FILTER_BWD_B0_TAB_ISSUED = _FILTER_B0_TAB + 2 * 2 * _mac((128, 32))  # 36,864
+# Blocks after 0 on their radial tables: the radial branch W1 silu(W0 rbf +
+# b0) + ob1 of each filter is a fitted polynomial of r (14 coefficients per
+# channel), so the forward is bound by its rows: per pair it must write the
+# filter rows (2 x 128 doubles), the logits (16) and s (4), and read r and
+# the endpoints (algorithmic bytes; the row read back by the logits pass is
+# the design's, not the algorithm's).  The reverse contracts df with the
+# slope polynomials (14 x 128 per filter) and runs the spherical branch's
+# transposes: E1^T (32x128), E0^T (4x32).
+_FILTER_RT_BYTES = 8 * (256 + 16 + 4) + 8 + 8                        # 2,224 B
+_FILTER_BWD_RT = 2 * 2 * _mac((14, 128), (32, 128), (4, 32))          # 24,064 flop
+_FILTER_BWD_RT_ISSUED = 2 * 2 * _mac((16, 128), (32, 128), (4, 32))   # 25,088: powers padded to 16
 KERNEL_WORK = {
     # name: (kernel symbol, bound, algorithmic per unit, issued per unit, unit)
+    # (bound "hbm": bytes per unit; "mfma": flop per unit)
+    "filter_fwd_radial": ("k_radial_frows + k_filter_logits", "hbm", _FILTER_RT_BYTES, _FILTER_RT_BYTES, "pair"),
+    "filter_bwd_radial": ("k_filter_bwd_mfma<false, false, true>", "mfma", _FILTER_BWD_RT, _FILTER_BWD_RT_ISSUED,
+                          "pair"),
     "filter_fwd": ("k_filter_fwd_mfma<false>", "mfma", _FILTER, _FILTER, "pair"),
     "filter_fwd_block0": ("k_filter_fwd_mfma<true>", "mfma", _FILTER_B0, _FILTER_B0, "pair"),
     "filter_bwd": ("k_filter_bwd_mfma<false, false>", "mfma", _FILTER, _FILTER_BWD_ISSUED, "pair"),
@@ -535,8 +550,9 @@ def main():
     md.ctx.kernel_timing(False)
     timing = {}
     work = kernel_work(model_widths(MODEL), elements=len(set(int(v) for v in z)))
-    for name in ("filter_fwd", "filter_fwd_block0", "filter_fwd_block0_tables", "filter_fwd_block0_radial",
-                 "filter_bwd", "filter_bwd_block0", "filter_bwd_block0_tables", "filter_bwd_block0_radial",
+    for name in ("filter_fwd", "filter_fwd_radial", "filter_fwd_block0", "filter_fwd_block0_tables",
+                 "filter_fwd_block0_radial", "filter_bwd", "filter_bwd_radial", "filter_bwd_block0",
+                 "filter_bwd_block0_tables", "filter_bwd_block0_radial",
                  "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd",
                  "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables",
@@ -552,9 +568,13 @@ def main():
         if k in work:
             sym, bound, alg, issued, unit = work[k]
             per_launch = units / launches
-            row.update({"kernel": sym, "units_per_launch": per_launch,
-                        "tflops_algorithmic": alg * per_launch / (ms / launches * 1e-3) / 1e12,
-                        "frac": alg * per_launch / (ms / launches * 1e-3) / 1e12 / FP64_PEAK_TFS})
+            rate = alg * per_launch / (ms / launches * 1e-3)  # flop/s or B/s
+            if bound == "hbm":
+                row.update({"kernel": sym, "units_per_launch": per_launch, "gbs_algorithmic": rate / 1e9,
+                            "frac": rate / 1e9 / HBM_PEAK_GBS})
+            else:
+                row.update({"kernel": sym, "units_per_launch": per_launch, "tflops_algorithmic": rate / 1e12,
+                            "frac": rate / 1e12 / FP64_PEAK_TFS})
         kernels[k] = row
     # the roofline kernel: most GPU time per step among those with a work model
     roofline = None
@@ -565,13 +585,17 @@ def main():
         ms, launches, units = timing[dom]
         avg_ms = ms / launches
         per_launch = units / launches
-        achieved = alg * per_launch / (avg_ms * 1e-3) / 1e12
+        hbm = bound == "hbm"
+        scale, peak = (1e9, HBM_PEAK_GBS) if hbm else (1e12, FP64_PEAK_TFS)
+        achieved = alg * per_launch / (avg_ms * 1e-3) / scale
         traffic, traffic_src = traffic_per_launch(sym, args.config, per_launch)
-        roofline = {"bound": bound, "kernel": sym, "achieved": achieved, "peak": FP64_PEAK_TFS, "unit": "TFLOP/s",
-                    "frac": achieved / FP64_PEAK_TFS, "traffic": traffic, "traffic_source": traffic_src,
+        roofline = {"bound": bound, "kernel": sym, "achieved": achieved, "peak": peak,
+                    "unit": "GB/s" if hbm else "TFLOP/s",
+                    "frac": achieved / peak, "traffic": traffic, "traffic_source": traffic_src,
                     "avg_launch_ms": avg_ms, "pairs_per_launch": per_launch,
-                    "flop_per_pair_algorithmic": alg, "flop_per_pair_issued": issued,
-                    "achieved_issued": issued * per_launch / (avg_ms * 1e-3) / 1e12,
+                    ("bytes_per_pair_algorithmic" if hbm else "flop_per_pair_algorithmic"): alg,
+                    ("bytes_per_pair_issued" if hbm else "flop_per_pair_issued"): issued,
+                    "achieved_issued": issued * per_launch / (avg_ms * 1e-3) / scale,
                     "selection": "the timed kernel with the most GPU time per step (%.3f ms of %d steps' HIP events)"
                                  % (kernels[dom]["ms_per_step"], steps_timed)}
     free_b, total_b = torch.cuda.mem_get_info(dev)

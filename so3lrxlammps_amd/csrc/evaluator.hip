@@ -551,47 +551,32 @@ __device__ __forceinline__ void rbf8(double r, int g, const FilterMfma &A, const
 // Both filters of one block for 16 pairs per wavefront, 4 wavefronts per block.
 // Per filter the stream holds 96 weight fragments: W0 (s < 16: tile s % 8,
 // K chunk s / 8), W1 (16 <= s < 80) and E1 (80 <= s < 96), tile-minor.
-// RT (blocks after 0 on their radial tables): the pairs run in interval
-// order (16 slots of one interval per wavefront, -1 in the padding), and
-// each filter's radial branch W1 silu(W0 rbf + b0) + ob1 is, per output
-// tile, one MFMA product of the interval's coefficient tile (rtab) with the
-// pairs' powers of t instead of the W0 and W1 chains.
-#ifndef SO3LR_RT_FWD_WAVES
-#define SO3LR_RT_FWD_WAVES 2
+// The RT reverse (blocks after 0 on their radial tables, in interval order):
+// operand-stream depth and wavefronts per SIMD.
+#ifndef SO3LR_RT_BWD_PF
+#define SO3LR_RT_BWD_PF 6
 #endif
 #ifndef SO3LR_RT_BWD_WAVES
 #define SO3LR_RT_BWD_WAVES 2
 #endif
-template <bool EV0, bool RT = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RT ? SO3LR_RT_FWD_WAVES : SO3LR_FILTER_FWD_WAVES,
-                                                                     RT ? SO3LR_RT_FWD_WAVES : SO3LR_FILTER_FWD_WAVES))) void
-k_filter_fwd_mfma(
-    const int *n_active, const int *pa, const double *pr, const double *ev, const double *__restrict__ qkv,
-    double inv_avg, FilterMfma A, double *ps, double *pf, double *palpha, const int *n_slots = nullptr,
-    const int *order = nullptr, const double *__restrict__ rtab = nullptr, RadialDomain rd = {}) {
+template <bool EV0>
+__global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(const int *n_active, const int *pa,
+                                                                     const double *pr, const double *ev,
+                                                                     const double *__restrict__ qkv, double inv_avg,
+                                                                     FilterMfma A, double *ps, double *pf,
+                                                                     double *palpha) {
   SO3LR_EXP2_TABLE(A)
+  const int nact = *n_active;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  int p, pp, ri = 0;
-  bool valid;
-  v4d tp;
-  if constexpr (RT) {
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    bool inside;
-    if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
-    valid = p >= 0;
-    pp = valid ? p : order[wave * 16];
-  } else {
-    const int nact = *n_active;
-    // consecutive pairs on one XCD: the endpoint rows they read are
-    // spatial neighbours, so they share that XCD's L2
-    const int blk = xcd_block_active((nact + 63) / 64);
-    if (blk < 0) return;
-    const int wave = blk * 4 + (threadIdx.x >> 6);
-    if (wave * 16 >= nact) return;  // whole wavefront idle
-    p = wave * 16 + j;
-    valid = p < nact;
-    pp = valid ? p : nact - 1;
-  }
+  // consecutive pairs on one XCD: the endpoint rows they read are
+  // spatial neighbours, so they share that XCD's L2
+  const int blk = xcd_block_active((nact + 63) / 64);
+  if (blk < 0) return;
+  const int wave = blk * 4 + (threadIdx.x >> 6);
+  if (wave * 16 >= nact) return;  // whole wavefront idle
+  const int p = wave * 16 + j;
+  const bool valid = p < nact;
+  const int pp = valid ? p : nact - 1;
   const int a = pa[2 * pp], b = pa[2 * pp + 1];
   // q k v q_ev k_ev rows of both endpoints (tile-transposed channel order):
   // the lane's four channels of an output tile are one 32-byte vector
@@ -610,27 +595,12 @@ k_filter_fwd_mfma(
   // EV0 (block 0, ev = 0): the spherical branch sees s = 0 for every pair,
   // so it is the constant E1 silu(e0) + e1, folded into the output bias
   // (ob1p0); its entries are left out (13 per tile, 128 in all).
-  // RT: the spherical layer-0 biases and operand (3), then per output tile
-  // the interval's coefficient tile (in place of the bias), the endpoint
-  // rows and the 2 E1 chunks (7 each): 59 entries.
-  static_assert(!(EV0 && RT), "block 0 has its own tables");
-  constexpr int TS = RT ? 3 : (EV0 ? 24 : 27), PT = RT ? 7 : (EV0 ? 13 : 15);
-  constexpr int UW = 5, UE = RT ? 5 : 13;  // first W1 and first E1 entry of a tile
+  constexpr int TS = EV0 ? 24 : 27, PT = EV0 ? 13 : 15;
+  constexpr int UW = 5, UE = 13;  // first W1 and first E1 entry of a tile
   constexpr int NF = TS + 8 * PT;
   auto load = [&](auto si) -> v4d {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
-    if constexpr (RT && s < 2) return tile_load(A.eb0p[which], s, lane);
-    else if constexpr (RT && s == 2) return tile_load(A.e0pk[which], 0, lane);
-    else if constexpr (RT) {
-      constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
-      constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;
-      if constexpr (u == 0) return frag_load(rtab + (std::size_t(ri) * 2 + which) * 8 * 256, mt, lane);
-      else if constexpr (u == 1) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
-      else if constexpr (u == 2) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
-      else if constexpr (u == 3) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
-      else if constexpr (u == 4) return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
-      else return wload(A.e1p[which], 2, mt, u - UE, lane);
-    } else if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
+    if constexpr (s < 8) return tile_load(A.b0p[which], s, lane);
     else if constexpr (!EV0 && s < 10) return tile_load(A.eb0p[which], s - 8, lane);
     else if constexpr (!EV0 && s == 10) return tile_load(A.e0pk[which], 0, lane);
     else if constexpr (s < TS) return wload(A.w0p[which], 2, (s - TS + 16) % 8, (s - TS + 16) / 8, lane);
@@ -650,15 +620,26 @@ k_filter_fwd_mfma(
   st.prime();
 
   v4d rb[2];
-  if constexpr (!RT) rbf8(pr[pp], g, A, exp2_lds, rb);
+  rbf8(pr[pp], g, A, exp2_lds, rb);
   // equivariant invariant of degree slot g (K = 4 operand of the spherical filter)
   double sg = 0.0;
   if constexpr (!EV0) {
-    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15));
-    const int hi = g == 0 ? 3 : (g == 1 ? 8 : (g == 2 ? 15 : 24));
-    for (int m = lo; m < hi; ++m) {
-      const double d = ev[std::size_t(a) * kE + m] - ev[std::size_t(b) * kE + m];
-      sg += d * d * A.att_cg[m];
+    // slot g's 2 g + 3 channels, as nine loads per endpoint with the channels
+    // past the slot weighted by zero, so that all of them are in flight at
+    // once (the endpoints' rows are far apart in interval order)
+    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15)), n = 2 * g + 3;
+    const double *ea = ev + std::size_t(a) * kE, *eb = ev + std::size_t(b) * kE;
+    double va[9], vb[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      const int m = min(lo + k, kE - 1);
+      va[k] = ea[m];
+      vb[k] = eb[m];
+    }
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      const double d = va[k] - vb[k];
+      sg += k < n ? d * d * A.att_cg[lo + k] : 0.0;
     }
     if (valid) ps[4 * std::size_t(p) + g] = sg;
   }
@@ -669,23 +650,13 @@ k_filter_fwd_mfma(
 
   st.run([&](auto si, const v4d &w) {
     constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
-    if constexpr (RT && s < 2) {
-      h2[s] = w;
-    } else if constexpr (RT && s == 2) {
-      // the spherical hidden row, before the first output tile
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        h2[t] = mfma(w[t], sg, h2[t]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
-      }
-    } else if constexpr (!RT && s < 8) {
+    if constexpr (s < 8) {
       h[s] = w;
-    } else if constexpr (!RT && !EV0 && s < 10) {
+    } else if constexpr (!EV0 && s < 10) {
       h2[s - 8] = w;
-    } else if constexpr (!RT && !EV0 && s == 10) {
+    } else if constexpr (!EV0 && s == 10) {
       e0 = w;
-    } else if constexpr (!RT && s < TS) {
+    } else if constexpr (s < TS) {
       constexpr int i = s - TS + 16;  // W0 entry 0..15
       h[i % 8] = mfma4(w, rb[i / 8], h[i % 8]);
       // each hidden tile's SiLU is taken one step before its first use,
@@ -697,8 +668,7 @@ k_filter_fwd_mfma(
     } else {
       constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
       if constexpr (u == 0) {
-        if constexpr (RT) o = mfma4(w, tp, v4d{0.0, 0.0, 0.0, 0.0});  // the radial branch of tile mt
-        else o = w;
+        o = w;
       } else if constexpr (u == 1 || u == 3) {
         qv = w;
       } else if constexpr (u == 2) {
@@ -751,6 +721,134 @@ k_filter_fwd_mfma(
             t1 = 0.0;
           }
         }
+      }
+    }
+  });
+}
+
+// The forward filters of the blocks after 0 on their radial tables, in two
+// passes.  k_radial_frows runs the pairs in interval order (16 slots of one
+// interval per wavefront, -1 in the padding): per filter and output tile T
+// the radial branch W1 silu(W0 rbf + b0) + ob1 is one MFMA product of the
+// interval's coefficient tile with the pairs' powers of t, and E1 silu(E0 s
+// + e0) is added as in k_filter_fwd_mfma; the rows go to pf and s to ps.
+// k_filter_logits then forms the attention logits from the rows and the
+// endpoints' q, k rows in pair order, where consecutive pairs share their
+// endpoints' rows in L2 (interval order scatters them).
+__global__ __launch_bounds__(256) void k_radial_frows(const int *n_slots, const int *order, const int *pa,
+                                                      const double *pr, const double *__restrict__ ev,
+                                                      const double *__restrict__ rtab, RadialDomain rd, FilterMfma A,
+                                                      double *ps, double *pf) {
+  SO3LR_EXP2_TABLE(A)
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  int p, ri;
+  bool inside;
+  v4d tp;
+  if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
+  const bool valid = p >= 0;
+  const int pp = valid ? p : order[wave * 16];
+  const int a = pa[2 * pp], b = pa[2 * pp + 1];
+  // equivariant invariant of degree slot g, all loads in flight at once
+  const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15)), n = 2 * g + 3;
+  const double *ea = ev + std::size_t(a) * kE, *eb = ev + std::size_t(b) * kE;
+  double va[9], vb[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) {
+    const int m = min(lo + k, kE - 1);
+    va[k] = ea[m];
+    vb[k] = eb[m];
+  }
+  double sg = 0.0;
+#pragma unroll
+  for (int k = 0; k < 9; ++k) {
+    const double d = va[k] - vb[k];
+    sg += k < n ? d * d * A.att_cg[lo + k] : 0.0;
+  }
+  if (valid) ps[4 * std::size_t(p) + g] = sg;
+  v4d *row = reinterpret_cast<v4d *>(pf + 256 * std::size_t(pp) + 4 * g);
+  const v4d zero = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const v4d e0 = tile_load(A.e0pk[w], 0, lane);
+    v4d h2[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      h2[t] = mfma(e0[t], sg, tile_load(A.eb0p[w], t, lane));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
+    }
+    const double *c = rtab + (std::size_t(ri) * 2 + w) * 8 * 256;
+#pragma unroll
+    for (int T = 0; T < 8; ++T) {
+      v4d o = mfma4(frag_load(c, T, lane), tp, zero);
+      o = mfma4(wload(A.e1p[w], 2, T, 0, lane), h2[0], o);
+      o = mfma4(wload(A.e1p[w], 2, T, 1, lane), h2[1], o);
+      if (valid) __builtin_nontemporal_store(o, row + 32 * w + 4 * T);
+    }
+  }
+}
+
+#ifndef SO3LR_LOGITS_PF
+#define SO3LR_LOGITS_PF 8
+#endif
+// 16 pairs per wavefront in pair order: per filter and tile the row and the
+// four endpoint rows q_a, k_b, q_b, k_a of its channels through the operand
+// stream; the logits of both directions as k_filter_fwd_mfma forms them.
+__global__ __launch_bounds__(256) void k_filter_logits(const int *n_active, const int *pa,
+                                                       const double *__restrict__ qkv, const double *__restrict__ pf,
+                                                       double inv_avg, double *palpha) {
+  const int nact = *n_active;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int blk = xcd_block_active((nact + 63) / 64);
+  if (blk < 0) return;
+  const int wave = blk * 4 + (threadIdx.x >> 6);
+  if (wave * 16 >= nact) return;
+  const int p = wave * 16 + j;
+  const bool valid = p < nact;
+  const int pp = valid ? p : nact - 1;
+  const int a = pa[2 * pp], b = pa[2 * pp + 1];
+  const double *qa = qkv + std::size_t(a) * 640 + 4 * g, *qb = qkv + std::size_t(b) * 640 + 4 * g;
+  const double *row = pf + 256 * std::size_t(pp) + 4 * g;
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, which = S / 40, mt = (S % 40) / 5, u = S % 5;
+    constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;
+    if constexpr (u == 0) return *reinterpret_cast<const v4d *>(row + 128 * which + 16 * mt);
+    else if constexpr (u == 1) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
+    else if constexpr (u == 2) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
+    else if constexpr (u == 3) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
+    else return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
+  };
+  Stream<80, SO3LR_LOGITS_PF, decltype(load)> st(load);
+  st.prime();
+  v4d o, qv;
+  double t0 = 0.0, t1 = 0.0;
+  st.run([&](auto si, const v4d &w) {
+    constexpr int S = decltype(si)::value, which = S / 40, mt = (S % 40) / 5, u = S % 5;
+    if constexpr (u == 0) {
+      o = w;
+    } else if constexpr (u == 1 || u == 3) {
+      qv = w;
+    } else if constexpr (u == 2) {
+      const v4d qk = qv * w;  // q_a k_b: edge b -> a
+      t0 += ((qk[0] * o[0] + qk[1] * o[1]) + qk[2] * o[2]) + qk[3] * o[3];
+    } else {
+      const v4d qk = qv * w;  // q_b k_a: edge a -> b
+      t1 += ((qk[0] * o[0] + qk[1] * o[1]) + qk[2] * o[2]) + qk[3] * o[3];
+      if constexpr (mt & 1) {
+        // head mt / 2 complete: sum over the four lane groups
+        t0 += __shfl_xor(t0, 16, kWave);
+        t0 += __shfl_xor(t0, 32, kWave);
+        t1 += __shfl_xor(t1, 16, kWave);
+        t1 += __shfl_xor(t1, 32, kWave);
+        constexpr int hd = mt / 2;
+        if (valid && g == hd) {
+          double *al = palpha + 16 * std::size_t(p) + 4 * which + hd;
+          al[0] = t0 * inv_avg;
+          al[8] = t1 * inv_avg;
+        }
+        t0 = 0.0;
+        t1 = 0.0;
       }
     }
   });
@@ -874,7 +972,7 @@ static_assert(bwd_schedule_ok<10, 1>() && bwd_schedule_ok<8, 0>() && bwd_schedul
 // output bias by the forward kernel) and s has no adjoint to give, so its
 // entries are left out.
 // RT (blocks after 0 on their radial tables): pairs in interval order as in
-// the forward; the first section keeps E1^T (2 entries per chunk) and takes
+// k_radial_frows; the first section keeps E1^T (2 entries per chunk) and takes
 // the interval's slope tile against each chunk's df (third entry), whose
 // sum over the powers of t is the radial branches' dE/dr; the layer-0
 // recompute, W0^T and the Bernstein basis are left out.
@@ -963,7 +1061,7 @@ k_filter_bwd_mfma(
       return wload(A.e0tp[which], 2, 0, s - A_END - B_LEN - C_LEN - D_LEN, lane);
     }
   };
-  Stream<NB0 + NB1, SO3LR_FILTER_BWD_PF, decltype(load)> st(load);
+  Stream<NB0 + NB1, RT ? SO3LR_RT_BWD_PF : SO3LR_FILTER_BWD_PF, decltype(load)> st(load);
   st.prime();
 
   const double r = pr[pp];
@@ -3977,8 +4075,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
   // and with the radial tables (k_radial_fwd, k_radial_bwd)
   const bool use_rad = use_cls && radial_ok_;
-  // the blocks after 0 on their radial tables (k_filter_fwd_mfma<false, true>,
-  // k_filter_bwd_mfma<false, false, true>, in interval order)
+  // the blocks after 0 on their radial tables (k_radial_frows, k_filter_logits,
+  // k_filter_bwd_mfma<false, false, true>)
   const bool use_rt = !gen_ && !scalar && radial_blocks_ && L > 1;
   int *rord = nullptr, *rhist = nullptr;
   // (the generic path's: g_cls_tables, g_b0_fwd, g_b0_bwd)
@@ -4324,7 +4422,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                            qkis + b * Nz * 16);
     }
     timed(blk0 ? (use_rad ? "filter_fwd_block0_radial" : use_cls ? "filter_fwd_block0_tables" : "filter_fwd_block0")
-               : "filter_fwd",
+               : (use_rt ? "filter_fwd_radial" : "filter_fwd"),
           0, [&] {
       if (blk0 && use_rad)
         hipLaunchKernelGGL(k_radial_fwd, dim3(gP16), dim3(256), 0, s, nact, pa, pr, z,
@@ -4338,10 +4436,11 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       else if (b == 0)  // ev = 0: the spherical branch is a constant
         hipLaunchKernelGGL(k_filter_fwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
                            psb, pfb, pab);
-      else if (use_rt)  // in interval order, the radial branches from the tables
-        hipLaunchKernelGGL((k_filter_fwd_mfma<false, true>), dim3(gR), dim3(256), 0, s, nact, pa, pr, evb, qb,
-                           inv_avg, FM, psb, pfb, pab, rslots, rord, B.rrow, rbl_dom_);
-      else
+      else if (use_rt) {  // the rows in interval order from the tables, then the logits in pair order
+        hipLaunchKernelGGL(k_radial_frows, dim3(gR), dim3(256), 0, s, rslots, rord, pa, pr, evb, B.rrow, rbl_dom_, FM,
+                           psb, pfb);
+        hipLaunchKernelGGL(k_filter_logits, dim3(gP64), dim3(256), 0, s, nact, pa, qb, pfb, inv_avg, pab);
+      } else
         hipLaunchKernelGGL(k_filter_fwd_mfma<false>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
                            psb, pfb, pab);
     });
@@ -4455,7 +4554,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
                                pab, gaev, z, lut, C, cmt, cgv, inv_avg, FM, rc_, dr, dY);
         });
       } else {
-        timed(b == 0 ? "filter_bwd_block0" : "filter_bwd", 0, [&] {
+        timed(b == 0 ? "filter_bwd_block0" : (use_rt ? "filter_bwd_radial" : "filter_bwd"), 0, [&] {
 #define SO3LR_FILTER_BWD(E0, FIRST)                                                                                \
   hipLaunchKernelGGL((k_filter_bwd_mfma<E0, FIRST>), dim3(gP64), dim3(256), 0, s, nact, pa, pr, psb, pfc, pY, pab,  \
                      qb, gainv, gaev, psc, dfc, inv_avg, FM, rc_, ds, dr, dY)
