@@ -727,11 +727,12 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
 }
 
 // The forward filters of the blocks after 0 on their radial tables, in two
-// passes.  k_radial_frows runs the pairs in interval order (16 slots of one
-// interval per wavefront, -1 in the padding): per filter and output tile T
-// the radial branch W1 silu(W0 rbf + b0) + ob1 is one MFMA product of the
-// interval's coefficient tile with the pairs' powers of t, and E1 silu(E0 s
-// + e0) is added as in k_filter_fwd_mfma; the rows go to pf and s to ps.
+// passes.  k_radial_frows runs the pairs in bucket order (16 slots of one
+// bucket, spatial block and interval, per wavefront; -1 in the padding): per
+// filter and output tile T the radial branch W1 silu(W0 rbf + b0) + ob1 is
+// one MFMA product of the interval's coefficient tile (128 channels x 32
+// powers) with the pairs' powers of t, and E1 silu(E0 s + e0) is added as in
+// k_filter_fwd_mfma; the rows go to pf and s to ps.
 // k_filter_logits then forms the attention logits from the rows and the
 // endpoints' q, k rows in pair order, where consecutive pairs share their
 // endpoints' rows in L2 (interval order scatters them).
@@ -741,10 +742,12 @@ __global__ __launch_bounds__(256) void k_radial_frows(const int *n_slots, const 
                                                       double *ps, double *pf) {
   SO3LR_EXP2_TABLE(A)
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // consecutive slots on one XCD: a spatial block's buckets share its L2
+  const int blk = xcd_block_active((*n_slots + 63) / 64);
+  const int wave = blk < 0 ? -1 : blk * 4 + (threadIdx.x >> 6);
   int p, ri;
   bool inside;
-  v4d tp;
+  v4d tp[2];
   if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
   const bool valid = p >= 0;
   const int pp = valid ? p : order[wave * 16];
@@ -778,10 +781,11 @@ __global__ __launch_bounds__(256) void k_radial_frows(const int *n_slots, const 
 #pragma unroll
       for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
     }
-    const double *c = rtab + (std::size_t(ri) * 2 + w) * 8 * 256;
+    const double *c = rtab + (std::size_t(ri) * 2 + w) * 16 * 256;
 #pragma unroll
     for (int T = 0; T < 8; ++T) {
-      v4d o = mfma4(frag_load(c, T, lane), tp, zero);
+      v4d o = mfma4(wload(c, 2, T, 0, lane), tp[0], zero);
+      o = mfma4(wload(c, 2, T, 1, lane), tp[1], o);
       o = mfma4(wload(A.e1p[w], 2, T, 0, lane), h2[0], o);
       o = mfma4(wload(A.e1p[w], 2, T, 1, lane), h2[1], o);
       if (valid) __builtin_nontemporal_store(o, row + 32 * w + 4 * T);
@@ -933,7 +937,7 @@ constexpr bool bwd_schedule_ok() {
   return true;
 }
 static_assert(bwd_schedule_ok<10, 1>() && bwd_schedule_ok<8, 0>() && bwd_schedule_ok<8, 2>() &&
-                  bwd_schedule_ok<3, 1>(),
+                  bwd_schedule_ok<4, 1>(),
               "reverse-filter operand schedule out of order");
 
 // Reverse of the attention's pair terms, of both filters, of the Bernstein
@@ -990,9 +994,11 @@ k_filter_bwd_mfma(
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
   int p, pp, ri = 0;
   bool valid, inside = false;
-  v4d tp;
+  v4d tp[2];
   if constexpr (RT) {
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // consecutive slots on one XCD: a spatial block's buckets share its L2
+    const int blk = xcd_block_active((*n_slots + 63) / 64);
+    const int wave = blk < 0 ? -1 : blk * 4 + (threadIdx.x >> 6);
     if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
     valid = p >= 0;
     pp = valid ? p : order[wave * 16];
@@ -1016,7 +1022,7 @@ k_filter_bwd_mfma(
 
   // head scalars: block 0 forms them here (SRC 0 and 2), later blocks read
   // the node-major reverse's record (SRC 1)
-  constexpr int NM = RT ? 3 : (EV0 ? 8 : 10), SRC0 = EV0 ? 0 : 1, SRC1 = EV0 ? 2 : 1;
+  constexpr int NM = RT ? 4 : (EV0 ? 8 : 10), SRC0 = EV0 ? 0 : 1, SRC1 = EV0 ? 2 : 1;
   constexpr int A_END0 = bwd_section_len<NM, SRC0>(), A_END1 = bwd_section_len<NM, SRC1>();
   const double *rec = psc + 16 * std::size_t(pp);
   constexpr int B_LEN = RT ? 0 : 24, C_LEN = EV0 ? 0 : 3, D_LEN = RT ? 0 : 16, E_LEN = EV0 ? 0 : 2;
@@ -1041,7 +1047,7 @@ k_filter_bwd_mfma(
         else if constexpr (e.q == 2) return row(rb, qoff + 16 * e.T);
         else return row(ra, koff + 16 * e.T);
       } else {
-        if constexpr (RT && e.q == 2) return frag_load(rtab + (std::size_t(ri) * 2 + which) * 8 * 256, e.T, lane);
+        if constexpr (RT && e.q >= 2) return wload(rtab + (std::size_t(ri) * 2 + which) * 16 * 256, 8, e.q - 2, e.T, lane);
         else if constexpr (RT) return wload(A.e1tp[which], 8, e.q, e.T, lane);
         else if constexpr (e.q < 8) return wload(A.w1tp[which], 8, e.q, e.T, lane);
         else return wload(A.e1tp[which], 8, e.q - 8, e.T, lane);
@@ -1111,7 +1117,7 @@ k_filter_bwd_mfma(
   // d rbf and d s of one filter, folded into scalars at the end of their
   // sections (dE/dr is linear in d rbf), so neither is held through the next
   // filter's df section
-  v4d drb[2], dsa, accdr;
+  v4d drb[2], dsa, accdr[2];
   double part = 0.0, ds_acc = 0.0;
   double ci = 0.0, co = 0.0, s_in = 0.0, s_out = 0.0;
 
@@ -1124,7 +1130,10 @@ k_filter_bwd_mfma(
       for (int mt = 0; mt < 8; ++mt) dh[mt] = zero;
       dh2[0] = zero;
       dh2[1] = zero;
-      if constexpr (RT && which == 0) accdr = zero;
+      if constexpr (RT && which == 0) {
+        accdr[0] = zero;
+        accdr[1] = zero;
+      }
     }
     if constexpr (s < A_END) {
       constexpr BwdEntry e = bwd_entry<NM, which ? SRC1 : SRC0>(s);
@@ -1174,7 +1183,7 @@ k_filter_bwd_mfma(
         if constexpr (e.q == 0) bT = bTn;
         if constexpr (RT) {
           if constexpr (e.q < 2) dh2[e.q] = mfma4(w, bT, dh2[e.q]);
-          else accdr = mfma4(w, bT, accdr);  // slopes . df, rows = powers of t
+          else accdr[e.q - 2] = mfma4(w, bT, accdr[e.q - 2]);  // slopes . df, rows = powers of t
         } else if constexpr (e.q < 8) {
           dh[e.q] = mfma4(w, bT, dh[e.q]);
         } else {
@@ -1242,9 +1251,16 @@ k_filter_bwd_mfma(
     }
   });
 
-  // RT: the radial branches' dE/dr, sum over the powers of t (rows g + 4 r)
-  if constexpr (RT)
-    part = inside ? ((accdr[0] * tp[0] + accdr[1] * tp[1]) + accdr[2] * tp[2]) + accdr[3] * tp[3] : 0.0;
+  // RT: the radial branches' dE/dr, sum over the powers of t (tile m, row
+  // g + 4 r: power 16 m + g + 4 r)
+  if constexpr (RT) {
+    double sum = 0.0;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sum += accdr[m][r] * tp[m][r];
+    part = inside ? sum : 0.0;
+  }
   // dE/dr: the Bernstein part of both filters + the cutoff
   part += __shfl_xor(part, 16, kWave);
   part += __shfl_xor(part, 32, kWave);
@@ -1856,75 +1872,57 @@ __global__ __launch_bounds__(256) void k_radial_bwd(const int *n_active, const i
 // ---------------------------------------------------------------- blocks after 0, radial tables
 // A filter's radial branch W1 silu(W0 rbf + b0) + ob1 (the whole output bias
 // included) depends on r alone in every block: fit_radial_hidden fits its
-// 128 outputs and their r-derivatives per interval of r, and the blocks
-// after 0 evaluate the fits as MFMA products over a wavefront's 16 pairs,
-// which therefore lie in one interval: the active pairs in interval order,
-// each interval's bucket padded to 16 slots (-1 in the padding): counts
-// (k_rint_count), bucket starts (k_rint_scan), placement (k_rint_place).  Within a bucket the order depends on the atomics'
-// timing; each pair's results go to its own rows, so the results do not.
-__device__ __forceinline__ int rint_key(double r, const RadialDomain &d) {
+// 128 outputs and their r-derivatives per interval of r (32 intervals of
+// degree 31 for the blocks after 0), and those blocks evaluate the fits as
+// MFMA products over a wavefront's 16 pairs, which therefore lie in one
+// interval.  The active pairs are bucketed by (spatial block of kRintAtoms
+// nodes of their first endpoint, interval), each bucket padded to 16 slots
+// (-1 in the padding): counts (k_rint_count), bucket starts (k_rint_scan),
+// placement (k_rint_place).  The nodes are in spatial order, so a block's
+// buckets, run one after another on one XCD, read one region's node rows
+// from L2.  Within a bucket the order depends on the atomics' timing; each
+// pair's results go to its own rows, so the results do not.
+__device__ __forceinline__ int rint_key(int a, double r, const RadialDomain &d) {
   double t;
   bool inside;
-  return radial_locate(r, d, t, inside);
+  return (a / kRintAtoms) * kBlockIntervals + radial_locate(r, d, t, inside);
 }
 
-__global__ __launch_bounds__(256) void k_rint_count(const int *n_active, const double *pr, RadialDomain d,
-                                                    int *hist) {
-  __shared__ int lc[kRadialIntervals];
-  const int nact = *n_active;
-  const int p0 = blockIdx.x * kClsChunk;
-  if (p0 >= nact) return;  // the whole block
-  for (int t = threadIdx.x; t < kRadialIntervals; t += 256) lc[t] = 0;
-  __syncthreads();
-  for (int it = 0; it < kClsPer; ++it) {
-    const int p = p0 + it * 256 + threadIdx.x;
-    if (p < nact) atomicAdd(&lc[rint_key(pr[p], d)], 1);
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < kRadialIntervals; t += 256)
-    if (lc[t]) atomicAdd(&hist[t], lc[t]);
+// one active pair per thread: hist[key] += 1
+__global__ __launch_bounds__(256) void k_rint_count(const int *n_active, const int *pa, const double *pr,
+                                                    RadialDomain d, int *hist) {
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p < *n_active) atomicAdd(&hist[rint_key(pa[2 * p], pr[p], d)], 1);
 }
 
-// bucket starts of the 256 intervals, each bucket padded to 16 slots, into
-// cursor; the slots' end into *total (one block of 256 threads)
-static_assert(kRadialIntervals == 256, "k_rint_scan: one thread per interval");
-__global__ __launch_bounds__(256) void k_rint_scan(const int *hist, int *cursor, int *total) {
-  __shared__ int v[kRadialIntervals];
-  const int t = threadIdx.x;
-  const int own = (hist[t] + 15) / 16 * 16;
+// bucket starts, each bucket padded to 16 slots, into cursor; the slots' end
+// into *total (one block: a contiguous run of keys per thread)
+__global__ __launch_bounds__(1024) void k_rint_scan(int nkeys, const int *hist, int *cursor, int *total) {
+  __shared__ int v[1024];
+  const int t = threadIdx.x, per = (nkeys + 1023) / 1024, k0 = t * per, k1 = min(nkeys, k0 + per);
+  int own = 0;
+  for (int k = k0; k < k1; ++k) own += (hist[k] + 15) / 16 * 16;
   v[t] = own;
   __syncthreads();
-  for (int o = 1; o < kRadialIntervals; o <<= 1) {
+  for (int o = 1; o < 1024; o <<= 1) {
     const int add = t >= o ? v[t - o] : 0;
     __syncthreads();
     v[t] += add;
     __syncthreads();
   }
-  cursor[t] = v[t] - own;
-  if (t == kRadialIntervals - 1) *total = v[t];
+  int run = v[t] - own;
+  for (int k = k0; k < k1; ++k) {
+    cursor[k] = run;
+    run += (hist[k] + 15) / 16 * 16;
+  }
+  if (t == 1023) *total = v[t];
 }
 
-__global__ __launch_bounds__(256) void k_rint_place(const int *n_active, const double *pr, RadialDomain d,
-                                                    int *cursor, int *order) {
-  __shared__ int lc[kRadialIntervals], lb[kRadialIntervals];
-  const int nact = *n_active;
-  const int p0 = blockIdx.x * kClsChunk;
-  if (p0 >= nact) return;
-  for (int t = threadIdx.x; t < kRadialIntervals; t += 256) lc[t] = 0;
-  __syncthreads();
-  int key[kClsPer], rank[kClsPer];
-#pragma unroll
-  for (int it = 0; it < kClsPer; ++it) {
-    const int p = p0 + it * 256 + threadIdx.x;
-    key[it] = p < nact ? rint_key(pr[p], d) : -1;
-    rank[it] = key[it] >= 0 ? atomicAdd(&lc[key[it]], 1) : 0;
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < kRadialIntervals; t += 256) lb[t] = lc[t] ? atomicAdd(&cursor[t], lc[t]) : 0;
-  __syncthreads();
-#pragma unroll
-  for (int it = 0; it < kClsPer; ++it)
-    if (key[it] >= 0) order[lb[key[it]] + rank[it]] = p0 + it * 256 + threadIdx.x;
+// one active pair per thread: its slot from its bucket's cursor
+__global__ __launch_bounds__(256) void k_rint_place(const int *n_active, const int *pa, const double *pr,
+                                                    RadialDomain d, int *cursor, int *order) {
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p < *n_active) order[atomicAdd(&cursor[rint_key(pa[2 * p], pr[p], d)], 1)] = p;
 }
 
 // ---------------------------------------------------------------- MFMA node GEMMs
@@ -3600,9 +3598,9 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
     }
   }
   // the blocks after 0: each filter's whole radial branch W1 h(r) + ob1 as
-  // piecewise polynomials (the same bound), laid out as MFMA operands: per
-  // interval and filter the coefficients (128 x 16 powers, zero beyond the
-  // degree) and the slope coefficients transposed (16 x 128)
+  // piecewise polynomials (32 intervals of degree 31, the same bound), laid
+  // out as MFMA operands: per interval and filter the coefficients (128 x 32
+  // powers) and the slope coefficients transposed (32 x 128)
   if (!a.generic && radial_tables_ && layers_ > 1) {
     const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
     bool ok = true;
@@ -3618,7 +3616,7 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
         for (std::size_t c = 0; c < F; ++c) ob1[c] += eb1[c];
         try {
           fits.push_back(fit_radial_hidden(m.f64(f + "mlp_rbf.0.weight", {F, R}), m.f64(f + "mlp_rbf.0.bias", {F}),
-                                           int(F), int(R), bb, gamma_, rc_, kRadialIntervals, kRadialDegree, &w1,
+                                           int(F), int(R), bb, gamma_, rc_, kBlockIntervals, kBlockDegree, &w1,
                                            &ob1, int(F)));
           ok = fits.back().value_error <= 1e-14 && fits.back().slope_error <= 1e-13;
         } catch (const std::invalid_argument &) {
@@ -3626,8 +3624,8 @@ Evaluator::Evaluator(std::shared_ptr<Model> model, int device) : model_(std::mov
         }
       }
       if (!ok) break;
-      const std::size_t n = kRadialCoefs;
-      for (int i = 0; i < kRadialIntervals; ++i)
+      const std::size_t n = kBlockPowers;
+      for (int i = 0; i < kBlockIntervals; ++i)
         for (int k = 0; k < 2; ++k) {
           const RadialFit &ft = fits[std::size_t(k)];
           std::vector<double> cv(F * n), st(n * F);
@@ -4079,6 +4077,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   // k_filter_bwd_mfma<false, false, true>)
   const bool use_rt = !gen_ && !scalar && radial_blocks_ && L > 1;
   int *rord = nullptr, *rhist = nullptr;
+  // buckets of the blocks after 0: (spatial block of kRintAtoms nodes, interval)
+  const int rkeys = int(ceil_div(N, kRintAtoms)) * kBlockIntervals;
   // (the generic path's: g_cls_tables, g_b0_fwd, g_b0_bwd)
   const bool gen_cls = gen_ && class_tables_ && n_cls_ > 0;
   const int C = use_cls ? n_cls_ : 0;
@@ -4119,9 +4119,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     psc = scalar ? nullptr : take<double>(psc_, 16 * Pa);
     ds = take<double>(ds_, 4 * Pa);
     if (use_rt) {
-      // counts, bucket cursors and the slots' end; the interval order
-      rhist = take<int>(rint_hist_, 2 * kRadialIntervals + 1);
-      rord = take<int>(rint_order_, Pa + 16 * std::size_t(kRadialIntervals));
+      // counts, bucket cursors and the slots' end; the bucket order
+      rhist = take<int>(rint_hist_, 2 * std::size_t(rkeys) + 1);
+      rord = take<int>(rint_order_, Pa + 16 * std::size_t(rkeys));
     }
     if (use_cls) {
       crep = take<int>(cls_rep_, kMaxClasses);
@@ -4351,10 +4351,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const unsigned gP = unsigned(PA);
   const unsigned gP64 = unsigned(std::max(1, ceil_div(PA, 64)));  // 64 pairs per MFMA block
   const unsigned gP16 = unsigned(std::max(1, ceil_div(PA, 16)));  // 16 pairs per radial-table block
-  // slots of the interval order: every bucket padded by fewer than 16
-  const int rslots_max = PA + 16 * kRadialIntervals;
+  // slots of the bucket order: every bucket padded by fewer than 16
+  const int rslots_max = PA + 16 * rkeys;
   const unsigned gR = unsigned(ceil_div(rslots_max, 64));  // 16 slots per wavefront
-  const int *rslots = rhist ? rhist + 2 * kRadialIntervals : nullptr;
+  const int *rslots = rhist ? rhist + 2 * rkeys : nullptr;
 
   // --- interaction blocks, forward ---
   for (int b = 0; b < L; ++b) {
@@ -4374,14 +4374,13 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     A.att_cg = B.att_cg; A.rbf_b = hw_.rbf_b; A.rbf_k = hw_.rbf_k; A.rbf_kr = hw_.rbf_kr; A.gamma = gamma_;
     const FilterMfma FM = filter_mfma(B, hw_, gamma_);
     if (use_rt && b == 1) {
-      // the active pairs in interval order, for every block after 0 and the reverse
-      const dim3 gsort(unsigned(ceil_div(PA, kClsChunk)));
-      hipLaunchKernelGGL(k_fill_int, dim3(1), dim3(256), 0, s, rhist, kRadialIntervals, 0);
+      // the active pairs in bucket order, for every block after 0 and the reverse
+      const dim3 gpair(unsigned(std::max(1, ceil_div(PA, 256))));
+      hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(rkeys, 256))), dim3(256), 0, s, rhist, rkeys, 0);
       hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(rslots_max, 256))), dim3(256), 0, s, rord, rslots_max, -1);
-      hipLaunchKernelGGL(k_rint_count, gsort, dim3(256), 0, s, nact, pr, rbl_dom_, rhist);
-      hipLaunchKernelGGL(k_rint_scan, dim3(1), dim3(kRadialIntervals), 0, s, rhist, rhist + kRadialIntervals,
-                         rhist + 2 * kRadialIntervals);
-      hipLaunchKernelGGL(k_rint_place, gsort, dim3(256), 0, s, nact, pr, rbl_dom_, rhist + kRadialIntervals, rord);
+      hipLaunchKernelGGL(k_rint_count, gpair, dim3(256), 0, s, nact, pa, pr, rbl_dom_, rhist);
+      hipLaunchKernelGGL(k_rint_scan, dim3(1), dim3(1024), 0, s, rkeys, rhist, rhist + rkeys, rhist + 2 * rkeys);
+      hipLaunchKernelGGL(k_rint_place, gpair, dim3(256), 0, s, nact, pa, pr, rbl_dom_, rhist + rkeys, rord);
     }
     // the MFMA filter also forms the attention logits of both directions
     // from the filter tiles it holds; the scalar cross-check path leaves them

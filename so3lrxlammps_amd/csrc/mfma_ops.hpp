@@ -211,26 +211,29 @@ __device__ __forceinline__ double radial_eval(const double *__restrict__ rec, in
   return v;
 }
 
-// A wavefront's 16 slots of an interval order (pairs by interval of r, each
-// interval's bucket padded to 16 slots with -1): the lane's pair p (-1:
+// A wavefront's 16 slots of an interval order (pairs bucketed by interval of
+// r, each bucket padded to 16 slots with -1): the lane's pair p (-1:
 // padding, whose lane works on the bucket's first pair and writes nothing),
-// the interval i (the same in every lane), t and the powers t^(g + 4 v) in
-// MFMA B-operand order (K index g + 4 v).  False: the wavefront holds no pair.
+// the interval i (the same in every lane), and the powers t^(16 c + g + 4 v)
+// of chunk c in MFMA B-operand order (K index 16 c + g + 4 v).  False: the
+// wavefront holds no pair.
 __device__ __forceinline__ bool rint_slots(const int *n_slots, const int *order, const double *pr,
                                            const RadialDomain &d, int wave, int j, int g, int &p, int &i,
-                                           bool &inside, v4d &tp) {
+                                           bool &inside, v4d *tp) {
   const int q0 = wave * 16;
-  if (q0 >= *n_slots) return false;
+  if (wave < 0 || q0 >= *n_slots) return false;
   const int p0 = order[q0];
   if (p0 < 0) return false;  // a bucket's slots start with its pairs
   p = order[q0 + j];
   double t;
   i = __builtin_amdgcn_readfirstlane(radial_locate(pr[p >= 0 ? p : p0], d, t, inside));
-  const double t2 = t * t, t4 = t2 * t2;
-  tp[0] = g == 0 ? 1.0 : (g == 1 ? t : (g == 2 ? t2 : t2 * t));
-  tp[1] = tp[0] * t4;
-  tp[2] = tp[1] * t4;
-  tp[3] = tp[2] * t4;
+  const double t2 = t * t, t4 = t2 * t2, t8 = t4 * t4, t16 = t8 * t8;
+  tp[0][0] = g == 0 ? 1.0 : (g == 1 ? t : (g == 2 ? t2 : t2 * t));
+  tp[0][1] = tp[0][0] * t4;
+  tp[0][2] = tp[0][1] * t4;
+  tp[0][3] = tp[0][2] * t4;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) tp[1][v] = tp[0][v] * t16;
   return true;
 }
 

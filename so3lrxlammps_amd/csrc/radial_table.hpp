@@ -22,6 +22,10 @@ namespace so3lr_amd {
 // their domain as the kernels read it (intervals of width step from r0,
 // t = (r - left edge) * scale - 1)
 constexpr int kRadialIntervals = 256, kRadialDegree = 13, kRadialCoefs = kRadialDegree + 1;
+// The blocks after 0: coarser intervals of higher degree (32 powers: two
+// MFMA K chunks), so that their pairs, bucketed by (spatial block of
+// kRintAtoms nodes, interval), keep a block's endpoint rows in L2
+constexpr int kBlockIntervals = 32, kBlockDegree = 31, kBlockPowers = kBlockDegree + 1, kRintAtoms = 256;
 struct RadialDomain {
   double r0, step, scale;
   int intervals;
