@@ -742,53 +742,76 @@ __global__ __launch_bounds__(256) void k_radial_frows(const int *n_slots, const 
                                                       double *ps, double *pf) {
   SO3LR_EXP2_TABLE(A)
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  // consecutive slots on one XCD: a spatial block's buckets share its L2
-  const int blk = xcd_block_active((*n_slots + 63) / 64);
+  // 32 slots (two column tiles of one bucket) per wavefront, so that every
+  // coefficient and E1 fragment feeds both; consecutive slots on one XCD: a
+  // spatial block's buckets share its L2
+  const int blk = xcd_block_active((*n_slots + 127) / 128);
   const int wave = blk < 0 ? -1 : blk * 4 + (threadIdx.x >> 6);
-  int p, ri;
-  bool inside;
-  v4d tp[2];
-  if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
-  const bool valid = p >= 0;
-  const int pp = valid ? p : order[wave * 16];
-  const int a = pa[2 * pp], b = pa[2 * pp + 1];
-  // equivariant invariant of degree slot g, all loads in flight at once
-  const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15)), n = 2 * g + 3;
-  const double *ea = ev + std::size_t(a) * kE, *eb = ev + std::size_t(b) * kE;
-  double va[9], vb[9];
-#pragma unroll
-  for (int k = 0; k < 9; ++k) {
-    const int m = min(lo + k, kE - 1);
-    va[k] = ea[m];
-    vb[k] = eb[m];
+  int p[2], ri[2];
+  bool inside[2];
+  v4d tp[2][2];
+  if (wave < 0 || !rint_slots(n_slots, order, pr, rd, 2 * wave, j, g, p[0], ri[0], inside[0], tp[0])) return;
+  if (!rint_slots(n_slots, order, pr, rd, 2 * wave + 1, j, g, p[1], ri[1], inside[1], tp[1])) {
+    p[1] = -1;  // the bucket's padding: the column computes on the first one's values and writes nothing
+    tp[1][0] = tp[0][0];
+    tp[1][1] = tp[0][1];
   }
-  double sg = 0.0;
+  const int i = ri[0];
+  const int p0 = order[wave * 32];
+  double sg[2];
+  v4d *row[2];
 #pragma unroll
-  for (int k = 0; k < 9; ++k) {
-    const double d = va[k] - vb[k];
-    sg += k < n ? d * d * A.att_cg[lo + k] : 0.0;
+  for (int ct = 0; ct < 2; ++ct) {
+    const int pp = p[ct] >= 0 ? p[ct] : p0;
+    const int a = pa[2 * pp], b = pa[2 * pp + 1];
+    // equivariant invariant of degree slot g, all loads in flight at once
+    const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15)), n = 2 * g + 3;
+    const double *ea = ev + std::size_t(a) * kE, *eb = ev + std::size_t(b) * kE;
+    double va[9], vb[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      const int m = min(lo + k, kE - 1);
+      va[k] = ea[m];
+      vb[k] = eb[m];
+    }
+    double s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      const double d = va[k] - vb[k];
+      s2 += k < n ? d * d * A.att_cg[lo + k] : 0.0;
+    }
+    sg[ct] = s2;
+    if (p[ct] >= 0) ps[4 * std::size_t(p[ct]) + g] = s2;
+    row[ct] = reinterpret_cast<v4d *>(pf + 256 * std::size_t(pp) + 4 * g);
   }
-  if (valid) ps[4 * std::size_t(p) + g] = sg;
-  v4d *row = reinterpret_cast<v4d *>(pf + 256 * std::size_t(pp) + 4 * g);
   const v4d zero = v4d{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
   for (int w = 0; w < 2; ++w) {
     const v4d e0 = tile_load(A.e0pk[w], 0, lane);
-    v4d h2[2];
+    v4d h2[2][2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      h2[t] = mfma(e0[t], sg, tile_load(A.eb0p[w], t, lane));
+      const v4d eb0 = tile_load(A.eb0p[w], t, lane);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
+      for (int ct = 0; ct < 2; ++ct) {
+        h2[ct][t] = mfma(e0[t], sg[ct], eb0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h2[ct][t][r] = silu_tab_wide(h2[ct][t][r], exp2_lds);
+      }
     }
-    const double *c = rtab + (std::size_t(ri) * 2 + w) * 16 * 256;
+    const double *c = rtab + (std::size_t(i) * 2 + w) * 16 * 256;
 #pragma unroll
     for (int T = 0; T < 8; ++T) {
-      v4d o = mfma4(wload(c, 2, T, 0, lane), tp[0], zero);
-      o = mfma4(wload(c, 2, T, 1, lane), tp[1], o);
-      o = mfma4(wload(A.e1p[w], 2, T, 0, lane), h2[0], o);
-      o = mfma4(wload(A.e1p[w], 2, T, 1, lane), h2[1], o);
-      if (valid) __builtin_nontemporal_store(o, row + 32 * w + 4 * T);
+      const v4d c0 = wload(c, 2, T, 0, lane), c1 = wload(c, 2, T, 1, lane);
+      const v4d e10 = wload(A.e1p[w], 2, T, 0, lane), e11 = wload(A.e1p[w], 2, T, 1, lane);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        v4d o = mfma4(c0, tp[ct][0], zero);
+        o = mfma4(c1, tp[ct][1], o);
+        o = mfma4(e10, h2[ct][0], o);
+        o = mfma4(e11, h2[ct][1], o);
+        if (p[ct] >= 0) __builtin_nontemporal_store(o, row[ct] + 32 * w + 4 * T);
+      }
     }
   }
 }
@@ -1876,8 +1899,8 @@ __global__ __launch_bounds__(256) void k_radial_bwd(const int *n_active, const i
 // degree 31 for the blocks after 0), and those blocks evaluate the fits as
 // MFMA products over a wavefront's 16 pairs, which therefore lie in one
 // interval.  The active pairs are bucketed by (spatial block of kRintAtoms
-// nodes of their first endpoint, interval), each bucket padded to 16 slots
-// (-1 in the padding): counts (k_rint_count), bucket starts (k_rint_scan),
+// nodes of their first endpoint, interval), each bucket padded to a multiple
+// of 32 slots (-1 in the padding): counts (k_rint_count), bucket starts (k_rint_scan),
 // placement (k_rint_place).  The nodes are in spatial order, so a block's
 // buckets, run one after another on one XCD, read one region's node rows
 // from L2.  Within a bucket the order depends on the atomics' timing; each
@@ -1895,13 +1918,13 @@ __global__ __launch_bounds__(256) void k_rint_count(const int *n_active, const i
   if (p < *n_active) atomicAdd(&hist[rint_key(pa[2 * p], pr[p], d)], 1);
 }
 
-// bucket starts, each bucket padded to 16 slots, into cursor; the slots' end
-// into *total (one block: a contiguous run of keys per thread)
+// bucket starts, each bucket padded to 32 slots (two 16-slot groups), into
+// cursor; the slots' end into *total (one block: a run of keys per thread)
 __global__ __launch_bounds__(1024) void k_rint_scan(int nkeys, const int *hist, int *cursor, int *total) {
   __shared__ int v[1024];
   const int t = threadIdx.x, per = (nkeys + 1023) / 1024, k0 = t * per, k1 = min(nkeys, k0 + per);
   int own = 0;
-  for (int k = k0; k < k1; ++k) own += (hist[k] + 15) / 16 * 16;
+  for (int k = k0; k < k1; ++k) own += (hist[k] + 31) / 32 * 32;
   v[t] = own;
   __syncthreads();
   for (int o = 1; o < 1024; o <<= 1) {
@@ -1913,7 +1936,7 @@ __global__ __launch_bounds__(1024) void k_rint_scan(int nkeys, const int *hist, 
   int run = v[t] - own;
   for (int k = k0; k < k1; ++k) {
     cursor[k] = run;
-    run += (hist[k] + 15) / 16 * 16;
+    run += (hist[k] + 31) / 32 * 32;
   }
   if (t == 1023) *total = v[t];
 }
@@ -4121,7 +4144,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     if (use_rt) {
       // counts, bucket cursors and the slots' end; the bucket order
       rhist = take<int>(rint_hist_, 2 * std::size_t(rkeys) + 1);
-      rord = take<int>(rint_order_, Pa + 16 * std::size_t(rkeys));
+      rord = take<int>(rint_order_, Pa + 32 * std::size_t(rkeys));
     }
     if (use_cls) {
       crep = take<int>(cls_rep_, kMaxClasses);
@@ -4351,9 +4374,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const unsigned gP = unsigned(PA);
   const unsigned gP64 = unsigned(std::max(1, ceil_div(PA, 64)));  // 64 pairs per MFMA block
   const unsigned gP16 = unsigned(std::max(1, ceil_div(PA, 16)));  // 16 pairs per radial-table block
-  // slots of the bucket order: every bucket padded by fewer than 16
-  const int rslots_max = PA + 16 * rkeys;
-  const unsigned gR = unsigned(ceil_div(rslots_max, 64));  // 16 slots per wavefront
+  // slots of the bucket order: every bucket padded by fewer than 32
+  const int rslots_max = PA + 32 * rkeys;
+  const unsigned gR = unsigned(ceil_div(rslots_max, 64));    // 16 slots per wavefront
+  const unsigned gR32 = unsigned(ceil_div(rslots_max, 128));  // 32 slots per wavefront
   const int *rslots = rhist ? rhist + 2 * rkeys : nullptr;
 
   // --- interaction blocks, forward ---
@@ -4436,8 +4460,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
         hipLaunchKernelGGL(k_filter_fwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
                            psb, pfb, pab);
       else if (use_rt) {  // the rows in interval order from the tables, then the logits in pair order
-        hipLaunchKernelGGL(k_radial_frows, dim3(gR), dim3(256), 0, s, rslots, rord, pa, pr, evb, B.rrow, rbl_dom_, FM,
-                           psb, pfb);
+        hipLaunchKernelGGL(k_radial_frows, dim3(gR32), dim3(256), 0, s, rslots, rord, pa, pr, evb, B.rrow, rbl_dom_,
+                           FM, psb, pfb);
         hipLaunchKernelGGL(k_filter_logits, dim3(gP64), dim3(256), 0, s, nact, pa, qb, pfb, inv_avg, pab);
       } else
         hipLaunchKernelGGL(k_filter_fwd_mfma<false>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,

@@ -305,8 +305,9 @@ class Evaluator {
   bool radial_tables_ = true, radial_ok_ = false, rad_stale_ = true;
   // the blocks after 0 on their radial tables (BlockWeights::rrow, rdr): every
   // such block's both radial branches fit to the bound; their pairs in
-  // interval order, each interval's bucket padded to 16 slots (rint_order_,
-  // -1 in the padding), counted and placed per evaluation (rint_hist_)
+  // buckets of (spatial block, interval), each padded to a multiple of 32
+  // slots (rint_order_, -1 in the padding), counted and placed per
+  // evaluation (rint_hist_)
   bool radial_blocks_ = false;
   RadialDomain rbl_dom_{};
   Buffer *rint_order_, *rint_hist_;

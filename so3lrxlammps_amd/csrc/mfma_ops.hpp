@@ -212,7 +212,7 @@ __device__ __forceinline__ double radial_eval(const double *__restrict__ rec, in
 }
 
 // A wavefront's 16 slots of an interval order (pairs bucketed by interval of
-// r, each bucket padded to 16 slots with -1): the lane's pair p (-1:
+// r, each bucket padded with -1 to a multiple of 16 slots): the lane's pair p (-1:
 // padding, whose lane works on the bucket's first pair and writes nothing),
 // the interval i (the same in every lane), and the powers t^(16 c + g + 4 v)
 // of chunk c in MFMA B-operand order (K index 16 c + g + 4 v).  False: the
