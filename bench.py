@@ -64,20 +64,19 @@ _FILTER_BWD_B0_ISSUED = _FILTER_B0 + 2 * 2 * _mac((128, 32))         # 98,304
 _FILTER_B0_TAB = 2 * 2 * _mac((128, 32), (8, 128))                    # 20,480
 _FILTER_BWD_B0_TAB_ISSUED = _FILTER_B0_TAB + 2 * 2 * _mac((128, 32))  # 36,864
 # Blocks after 0 on their radial tables: the radial branch W1 silu(W0 rbf +
-# b0) + ob1 of each filter is a fitted polynomial of r (14 coefficients per
+# b0) + ob1 of each filter is a fitted polynomial of r (32 coefficients per
 # channel), so the forward is bound by its rows: per pair it must write the
 # filter rows (2 x 128 doubles), the logits (16) and s (4), and read r and
-# the endpoints (algorithmic bytes; the row read back by the logits pass is
-# the design's, not the algorithm's).  The reverse contracts df with the
-# slope polynomials (14 x 128 per filter) and runs the spherical branch's
-# transposes: E1^T (32x128), E0^T (4x32).
+# the endpoints (algorithmic bytes).  The reverse contracts df with the slope
+# polynomials (14 x 128 per filter at the accuracy of degree 13; 32 x 128
+# issued) and runs the spherical branch's transposes: E1^T (32x128), E0^T (4x32).
 _FILTER_RT_BYTES = 8 * (256 + 16 + 4) + 8 + 8                        # 2,224 B
 _FILTER_BWD_RT = 2 * 2 * _mac((14, 128), (32, 128), (4, 32))          # 24,064 flop
-_FILTER_BWD_RT_ISSUED = 2 * 2 * _mac((16, 128), (32, 128), (4, 32))   # 25,088: powers padded to 16
+_FILTER_BWD_RT_ISSUED = 2 * 2 * _mac((32, 128), (32, 128), (4, 32))   # 33,280: 32 powers
 KERNEL_WORK = {
     # name: (kernel symbol, bound, algorithmic per unit, issued per unit, unit)
     # (bound "hbm": bytes per unit; "mfma": flop per unit)
-    "filter_fwd_radial": ("k_radial_frows + k_filter_logits", "hbm", _FILTER_RT_BYTES, _FILTER_RT_BYTES, "pair"),
+    "filter_fwd_radial": ("k_radial_fwd_rows", "hbm", _FILTER_RT_BYTES, _FILTER_RT_BYTES, "pair"),
     "filter_bwd_radial": ("k_filter_bwd_mfma<false, false, true>", "mfma", _FILTER_BWD_RT, _FILTER_BWD_RT_ISSUED,
                           "pair"),
     "filter_fwd": ("k_filter_fwd_mfma<false>", "mfma", _FILTER, _FILTER, "pair"),

@@ -726,45 +726,58 @@ __global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_filter_fwd_mfma(co
   });
 }
 
-// The forward filters of the blocks after 0 on their radial tables, in two
-// passes.  k_radial_frows runs the pairs in bucket order (16 slots of one
-// bucket, spatial block and interval, per wavefront; -1 in the padding): per
-// filter and output tile T the radial branch W1 silu(W0 rbf + b0) + ob1 is
-// one MFMA product of the interval's coefficient tile (128 channels x 32
-// powers) with the pairs' powers of t, and E1 silu(E0 s + e0) is added as in
-// k_filter_fwd_mfma; the rows go to pf and s to ps.
-// k_filter_logits then forms the attention logits from the rows and the
-// endpoints' q, k rows in pair order, where consecutive pairs share their
-// endpoints' rows in L2 (interval order scatters them).
-__global__ __launch_bounds__(256) void k_radial_frows(const int *n_slots, const int *order, const int *pa,
-                                                      const double *pr, const double *__restrict__ ev,
-                                                      const double *__restrict__ rtab, RadialDomain rd, FilterMfma A,
-                                                      double *ps, double *pf) {
+// The forward filters of the blocks after 0 on their radial tables, in
+// bucket order (16 slots of one bucket, spatial block and interval, per
+// wavefront; -1 in the padding).  Per filter the stream holds the spherical
+// layer-0 biases and operand (3), then per output tile the interval's
+// coefficient tile (128 channels x 32 powers: two K chunks, against the
+// pairs' powers of t in place of the W0 and W1 chains), the endpoint rows
+// q_a, k_b, q_b, k_a of its channels (from L2: a spatial block's buckets
+// run together on one XCD) and the 2 E1 chunks.  The rows go to pf and the
+// logits of both directions to palpha as in k_filter_fwd_mfma.  Measured
+// as two passes (the rows in bucket order, the logits in pair order) it
+// took 0.79 against 0.70 ms.
+#ifndef SO3LR_RT_FWD_PF
+#define SO3LR_RT_FWD_PF 6
+#endif
+__global__ __launch_bounds__(256) FILTER_FWD_OCCUPANCY void k_radial_fwd_rows(
+    const int *n_slots, const int *order, const int *pa, const double *pr, const double *__restrict__ ev,
+    const double *__restrict__ qkv, const double *__restrict__ rtab, RadialDomain rd, double inv_avg, FilterMfma A,
+    double *ps, double *pf, double *palpha) {
   SO3LR_EXP2_TABLE(A)
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  // 32 slots (two column tiles of one bucket) per wavefront, so that every
-  // coefficient and E1 fragment feeds both; consecutive slots on one XCD: a
-  // spatial block's buckets share its L2
-  const int blk = xcd_block_active((*n_slots + 127) / 128);
+  const int blk = xcd_block_active((*n_slots + 63) / 64);
   const int wave = blk < 0 ? -1 : blk * 4 + (threadIdx.x >> 6);
-  int p[2], ri[2];
-  bool inside[2];
-  v4d tp[2][2];
-  if (wave < 0 || !rint_slots(n_slots, order, pr, rd, 2 * wave, j, g, p[0], ri[0], inside[0], tp[0])) return;
-  if (!rint_slots(n_slots, order, pr, rd, 2 * wave + 1, j, g, p[1], ri[1], inside[1], tp[1])) {
-    p[1] = -1;  // the bucket's padding: the column computes on the first one's values and writes nothing
-    tp[1][0] = tp[0][0];
-    tp[1][1] = tp[0][1];
-  }
-  const int i = ri[0];
-  const int p0 = order[wave * 32];
-  double sg[2];
-  v4d *row[2];
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct) {
-    const int pp = p[ct] >= 0 ? p[ct] : p0;
-    const int a = pa[2 * pp], b = pa[2 * pp + 1];
-    // equivariant invariant of degree slot g, all loads in flight at once
+  int p, ri;
+  bool inside;
+  v4d tp[2];
+  if (!rint_slots(n_slots, order, pr, rd, wave, j, g, p, ri, inside, tp)) return;
+  const bool valid = p >= 0;
+  const int pp = valid ? p : order[wave * 16];
+  const int a = pa[2 * pp], b = pa[2 * pp + 1];
+  const double *qa = qkv + std::size_t(a) * 640 + 4 * g, *qb = qkv + std::size_t(b) * 640 + 4 * g;
+  const double *coef = rtab + std::size_t(ri) * 2 * 16 * 256;
+  constexpr int TS = 3, PT = 8, NF = TS + 8 * PT;
+  auto load = [&](auto si) -> v4d {
+    constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
+    if constexpr (s < 2) return tile_load(A.eb0p[which], s, lane);
+    else if constexpr (s == 2) return tile_load(A.e0pk[which], 0, lane);
+    else {
+      constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
+      constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;
+      if constexpr (u < 2) return wload(coef + which * 16 * 256, 2, mt, u, lane);
+      else if constexpr (u == 2) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
+      else if constexpr (u == 3) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
+      else if constexpr (u == 4) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
+      else if constexpr (u == 5) return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
+      else return wload(A.e1p[which], 2, mt, u - 6, lane);
+    }
+  };
+  Stream<2 * NF, SO3LR_RT_FWD_PF, decltype(load)> st(load);
+  st.prime();
+  // equivariant invariant of degree slot g, all loads in flight at once
+  double sg = 0.0;
+  {
     const int lo = g == 0 ? 0 : (g == 1 ? 3 : (g == 2 ? 8 : 15)), n = 2 * g + 3;
     const double *ea = ev + std::size_t(a) * kE, *eb = ev + std::size_t(b) * kE;
     double va[9], vb[9];
@@ -774,108 +787,61 @@ __global__ __launch_bounds__(256) void k_radial_frows(const int *n_slots, const 
       va[k] = ea[m];
       vb[k] = eb[m];
     }
-    double s2 = 0.0;
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
       const double d = va[k] - vb[k];
-      s2 += k < n ? d * d * A.att_cg[lo + k] : 0.0;
+      sg += k < n ? d * d * A.att_cg[lo + k] : 0.0;
     }
-    sg[ct] = s2;
-    if (p[ct] >= 0) ps[4 * std::size_t(p[ct]) + g] = s2;
-    row[ct] = reinterpret_cast<v4d *>(pf + 256 * std::size_t(pp) + 4 * g);
+    if (valid) ps[4 * std::size_t(p) + g] = sg;
   }
+  v4d *const rowv = reinterpret_cast<v4d *>(pf + 256 * std::size_t(pp) + 4 * g);
   const v4d zero = v4d{0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const v4d e0 = tile_load(A.e0pk[w], 0, lane);
-    v4d h2[2][2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const v4d eb0 = tile_load(A.eb0p[w], t, lane);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        h2[ct][t] = mfma(e0[t], sg[ct], eb0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) h2[ct][t][r] = silu_tab_wide(h2[ct][t][r], exp2_lds);
-      }
-    }
-    const double *c = rtab + (std::size_t(i) * 2 + w) * 16 * 256;
-#pragma unroll
-    for (int T = 0; T < 8; ++T) {
-      const v4d c0 = wload(c, 2, T, 0, lane), c1 = wload(c, 2, T, 1, lane);
-      const v4d e10 = wload(A.e1p[w], 2, T, 0, lane), e11 = wload(A.e1p[w], 2, T, 1, lane);
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        v4d o = mfma4(c0, tp[ct][0], zero);
-        o = mfma4(c1, tp[ct][1], o);
-        o = mfma4(e10, h2[ct][0], o);
-        o = mfma4(e11, h2[ct][1], o);
-        if (p[ct] >= 0) __builtin_nontemporal_store(o, row[ct] + 32 * w + 4 * T);
-      }
-    }
-  }
-}
-
-#ifndef SO3LR_LOGITS_PF
-#define SO3LR_LOGITS_PF 8
-#endif
-// 16 pairs per wavefront in pair order: per filter and tile the row and the
-// four endpoint rows q_a, k_b, q_b, k_a of its channels through the operand
-// stream; the logits of both directions as k_filter_fwd_mfma forms them.
-__global__ __launch_bounds__(256) void k_filter_logits(const int *n_active, const int *pa,
-                                                       const double *__restrict__ qkv, const double *__restrict__ pf,
-                                                       double inv_avg, double *palpha) {
-  const int nact = *n_active;
-  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const int blk = xcd_block_active((nact + 63) / 64);
-  if (blk < 0) return;
-  const int wave = blk * 4 + (threadIdx.x >> 6);
-  if (wave * 16 >= nact) return;
-  const int p = wave * 16 + j;
-  const bool valid = p < nact;
-  const int pp = valid ? p : nact - 1;
-  const int a = pa[2 * pp], b = pa[2 * pp + 1];
-  const double *qa = qkv + std::size_t(a) * 640 + 4 * g, *qb = qkv + std::size_t(b) * 640 + 4 * g;
-  const double *row = pf + 256 * std::size_t(pp) + 4 * g;
-  auto load = [&](auto si) -> v4d {
-    constexpr int S = decltype(si)::value, which = S / 40, mt = (S % 40) / 5, u = S % 5;
-    constexpr int qoff = which ? 384 : 0, koff = which ? 512 : 128;
-    if constexpr (u == 0) return *reinterpret_cast<const v4d *>(row + 128 * which + 16 * mt);
-    else if constexpr (u == 1) return *reinterpret_cast<const v4d *>(qa + qoff + 16 * mt);
-    else if constexpr (u == 2) return *reinterpret_cast<const v4d *>(qb + koff + 16 * mt);
-    else if constexpr (u == 3) return *reinterpret_cast<const v4d *>(qb + qoff + 16 * mt);
-    else return *reinterpret_cast<const v4d *>(qa + koff + 16 * mt);
-  };
-  Stream<80, SO3LR_LOGITS_PF, decltype(load)> st(load);
-  st.prime();
-  v4d o, qv;
+  v4d h2[2], o, qv, qk0, qk1;
   double t0 = 0.0, t1 = 0.0;
   st.run([&](auto si, const v4d &w) {
-    constexpr int S = decltype(si)::value, which = S / 40, mt = (S % 40) / 5, u = S % 5;
-    if constexpr (u == 0) {
-      o = w;
-    } else if constexpr (u == 1 || u == 3) {
-      qv = w;
-    } else if constexpr (u == 2) {
-      const v4d qk = qv * w;  // q_a k_b: edge b -> a
-      t0 += ((qk[0] * o[0] + qk[1] * o[1]) + qk[2] * o[2]) + qk[3] * o[3];
+    constexpr int S = decltype(si)::value, which = S / NF, s = S % NF;
+    if constexpr (s < 2) {
+      h2[s] = w;
+    } else if constexpr (s == 2) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        h2[t] = mfma(w[t], sg, h2[t]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h2[t][r] = silu_tab_wide(h2[t][r], exp2_lds);
+      }
     } else {
-      const v4d qk = qv * w;  // q_b k_a: edge a -> b
-      t1 += ((qk[0] * o[0] + qk[1] * o[1]) + qk[2] * o[2]) + qk[3] * o[3];
-      if constexpr (mt & 1) {
-        // head mt / 2 complete: sum over the four lane groups
-        t0 += __shfl_xor(t0, 16, kWave);
-        t0 += __shfl_xor(t0, 32, kWave);
-        t1 += __shfl_xor(t1, 16, kWave);
-        t1 += __shfl_xor(t1, 32, kWave);
-        constexpr int hd = mt / 2;
-        if (valid && g == hd) {
-          double *al = palpha + 16 * std::size_t(p) + 4 * which + hd;
-          al[0] = t0 * inv_avg;
-          al[8] = t1 * inv_avg;
+      constexpr int mt = (s - TS) / PT, u = (s - TS) % PT;
+      if constexpr (u == 0) {
+        o = mfma4(w, tp[0], zero);
+      } else if constexpr (u == 1) {
+        o = mfma4(w, tp[1], o);
+      } else if constexpr (u == 2 || u == 4) {
+        qv = w;
+      } else if constexpr (u == 3) {
+        qk0 = qv * w;  // q_a k_b: edge b -> a
+      } else if constexpr (u == 5) {
+        qk1 = qv * w;  // q_b k_a: edge a -> b
+      } else {
+        o = mfma4(w, h2[u - 6], o);
+        if constexpr (u == PT - 1) {
+          if (valid) __builtin_nontemporal_store(o, rowv + which * 32 + 4 * mt);
+          t0 += ((qk0[0] * o[0] + qk0[1] * o[1]) + qk0[2] * o[2]) + qk0[3] * o[3];
+          t1 += ((qk1[0] * o[0] + qk1[1] * o[1]) + qk1[2] * o[2]) + qk1[3] * o[3];
+          if constexpr (mt & 1) {
+            t0 += __shfl_xor(t0, 16, kWave);
+            t0 += __shfl_xor(t0, 32, kWave);
+            t1 += __shfl_xor(t1, 16, kWave);
+            t1 += __shfl_xor(t1, 32, kWave);
+            constexpr int hd = mt / 2;
+            if (valid && g == hd) {
+              double *al = palpha + 16 * std::size_t(p) + 4 * which + hd;
+              al[0] = t0 * inv_avg;
+              al[8] = t1 * inv_avg;
+            }
+            t0 = 0.0;
+            t1 = 0.0;
+          }
         }
-        t0 = 0.0;
-        t1 = 0.0;
       }
     }
   });
@@ -998,8 +964,8 @@ static_assert(bwd_schedule_ok<10, 1>() && bwd_schedule_ok<8, 0>() && bwd_schedul
 // EV0 (block 0, ev = 0): the spherical branch is a constant (folded into the
 // output bias by the forward kernel) and s has no adjoint to give, so its
 // entries are left out.
-// RT (blocks after 0 on their radial tables): pairs in interval order as in
-// k_radial_frows; the first section keeps E1^T (2 entries per chunk) and takes
+// RT (blocks after 0 on their radial tables): pairs in bucket order as in
+// k_radial_fwd_rows; the first section keeps E1^T (2 entries per chunk) and takes
 // the interval's slope tile against each chunk's df (third entry), whose
 // sum over the powers of t is the radial branches' dE/dr; the layer-0
 // recompute, W0^T and the Bernstein basis are left out.
@@ -1900,7 +1866,7 @@ __global__ __launch_bounds__(256) void k_radial_bwd(const int *n_active, const i
 // MFMA products over a wavefront's 16 pairs, which therefore lie in one
 // interval.  The active pairs are bucketed by (spatial block of kRintAtoms
 // nodes of their first endpoint, interval), each bucket padded to a multiple
-// of 32 slots (-1 in the padding): counts (k_rint_count), bucket starts (k_rint_scan),
+// of 16 slots (-1 in the padding): counts (k_rint_count), bucket starts (k_rint_scan),
 // placement (k_rint_place).  The nodes are in spatial order, so a block's
 // buckets, run one after another on one XCD, read one region's node rows
 // from L2.  Within a bucket the order depends on the atomics' timing; each
@@ -1918,13 +1884,13 @@ __global__ __launch_bounds__(256) void k_rint_count(const int *n_active, const i
   if (p < *n_active) atomicAdd(&hist[rint_key(pa[2 * p], pr[p], d)], 1);
 }
 
-// bucket starts, each bucket padded to 32 slots (two 16-slot groups), into
-// cursor; the slots' end into *total (one block: a run of keys per thread)
+// bucket starts, each bucket padded to a multiple of 16 slots, into cursor;
+// the slots' end into *total (one block: a run of keys per thread)
 __global__ __launch_bounds__(1024) void k_rint_scan(int nkeys, const int *hist, int *cursor, int *total) {
   __shared__ int v[1024];
   const int t = threadIdx.x, per = (nkeys + 1023) / 1024, k0 = t * per, k1 = min(nkeys, k0 + per);
   int own = 0;
-  for (int k = k0; k < k1; ++k) own += (hist[k] + 31) / 32 * 32;
+  for (int k = k0; k < k1; ++k) own += (hist[k] + 15) / 16 * 16;
   v[t] = own;
   __syncthreads();
   for (int o = 1; o < 1024; o <<= 1) {
@@ -1936,7 +1902,7 @@ __global__ __launch_bounds__(1024) void k_rint_scan(int nkeys, const int *hist, 
   int run = v[t] - own;
   for (int k = k0; k < k1; ++k) {
     cursor[k] = run;
-    run += (hist[k] + 31) / 32 * 32;
+    run += (hist[k] + 15) / 16 * 16;
   }
   if (t == 1023) *total = v[t];
 }
@@ -4096,7 +4062,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const bool use_cls = !gen_ && !scalar && class_tables_ && n_cls_ > 0;
   // and with the radial tables (k_radial_fwd, k_radial_bwd)
   const bool use_rad = use_cls && radial_ok_;
-  // the blocks after 0 on their radial tables (k_radial_frows, k_filter_logits,
+  // the blocks after 0 on their radial tables (k_radial_fwd_rows,
   // k_filter_bwd_mfma<false, false, true>)
   const bool use_rt = !gen_ && !scalar && radial_blocks_ && L > 1;
   int *rord = nullptr, *rhist = nullptr;
@@ -4144,7 +4110,7 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     if (use_rt) {
       // counts, bucket cursors and the slots' end; the bucket order
       rhist = take<int>(rint_hist_, 2 * std::size_t(rkeys) + 1);
-      rord = take<int>(rint_order_, Pa + 32 * std::size_t(rkeys));
+      rord = take<int>(rint_order_, Pa + 16 * std::size_t(rkeys));
     }
     if (use_cls) {
       crep = take<int>(cls_rep_, kMaxClasses);
@@ -4374,10 +4340,9 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   const unsigned gP = unsigned(PA);
   const unsigned gP64 = unsigned(std::max(1, ceil_div(PA, 64)));  // 64 pairs per MFMA block
   const unsigned gP16 = unsigned(std::max(1, ceil_div(PA, 16)));  // 16 pairs per radial-table block
-  // slots of the bucket order: every bucket padded by fewer than 32
-  const int rslots_max = PA + 32 * rkeys;
-  const unsigned gR = unsigned(ceil_div(rslots_max, 64));    // 16 slots per wavefront
-  const unsigned gR32 = unsigned(ceil_div(rslots_max, 128));  // 32 slots per wavefront
+  // slots of the bucket order: every bucket padded by fewer than 16
+  const int rslots_max = PA + 16 * rkeys;
+  const unsigned gR = unsigned(ceil_div(rslots_max, 64));  // 16 slots per wavefront
   const int *rslots = rhist ? rhist + 2 * rkeys : nullptr;
 
   // --- interaction blocks, forward ---
@@ -4459,11 +4424,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
       else if (b == 0)  // ev = 0: the spherical branch is a constant
         hipLaunchKernelGGL(k_filter_fwd_mfma<true>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
                            psb, pfb, pab);
-      else if (use_rt) {  // the rows in interval order from the tables, then the logits in pair order
-        hipLaunchKernelGGL(k_radial_frows, dim3(gR32), dim3(256), 0, s, rslots, rord, pa, pr, evb, B.rrow, rbl_dom_,
-                           FM, psb, pfb);
-        hipLaunchKernelGGL(k_filter_logits, dim3(gP64), dim3(256), 0, s, nact, pa, qb, pfb, inv_avg, pab);
-      } else
+      else if (use_rt)  // rows and logits in bucket order, the radial branches from the tables
+        hipLaunchKernelGGL(k_radial_fwd_rows, dim3(gR), dim3(256), 0, s, rslots, rord, pa, pr, evb, qb, B.rrow,
+                           rbl_dom_, inv_avg, FM, psb, pfb, pab);
+      else
         hipLaunchKernelGGL(k_filter_fwd_mfma<false>, dim3(gP64), dim3(256), 0, s, nact, pa, pr, evb, qb, inv_avg, FM,
                            psb, pfb, pab);
     });

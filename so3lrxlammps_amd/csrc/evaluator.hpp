@@ -305,7 +305,7 @@ class Evaluator {
   bool radial_tables_ = true, radial_ok_ = false, rad_stale_ = true;
   // the blocks after 0 on their radial tables (BlockWeights::rrow, rdr): every
   // such block's both radial branches fit to the bound; their pairs in
-  // buckets of (spatial block, interval), each padded to a multiple of 32
+  // buckets of (spatial block, interval), each padded to a multiple of 16
   // slots (rint_order_, -1 in the padding), counted and placed per
   // evaluation (rint_hist_)
   bool radial_blocks_ = false;
