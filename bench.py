@@ -143,6 +143,11 @@ def kernel_work(widths, elements=0):
     work["generic_filter_fwd"] = ("g_filt_fwd: both filters and the logits, fused", "mfma", alg, alg, "pair")
     work["generic_filter_bwd"] = ("g_filt_bwd: both filters' reverse, fused", "mfma", alg,
                                   alg + 2 * 2 * (R * F + NH * FH), "pair")
+    # the blocks after 0 on their radial tables: bound by the rows, 2 F
+    # doubles written per pair with the 4 NH logits and NH invariants (the
+    # invariants are read back), r and the endpoints read
+    rt_bytes = 8 * (2 * F + 4 * NH + NH) + 16
+    work["generic_filter_fwd_radial"] = ("g_radial_fwd_rows", "hbm", rt_bytes, rt_bytes, "pair")
     if elements:
         tab = 2 * 2 * (R * F + 2 * NH * F)
         work["generic_filter_fwd_block0_tables"] = ("g_b0_fwd: block 0's fused table filters", "mfma", tab,
@@ -555,7 +560,7 @@ def main():
                  "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd",
                  "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables",
-                 "generic_filter_fwd_block0_radial", "generic_filter_bwd_block0_radial"):
+                 "generic_filter_fwd_block0_radial", "generic_filter_bwd_block0_radial", "generic_filter_fwd_radial"):
         try:
             timing[name] = md.ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched

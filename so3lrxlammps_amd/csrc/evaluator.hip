@@ -4065,6 +4065,8 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
   // the blocks after 0 on their radial tables (k_radial_fwd_rows,
   // k_filter_bwd_mfma<false, false, true>)
   const bool use_rt = !gen_ && !scalar && radial_blocks_ && L > 1;
+  // and the generic path's (g_radial_fwd_rows)
+  const bool use_grt = gen_ && gen_->radial_blocks_ok() && L > 1;
   int *rord = nullptr, *rhist = nullptr;
   // buckets of the blocks after 0: (spatial block of kRintAtoms nodes, interval)
   const int rkeys = int(ceil_div(N, kRintAtoms)) * kBlockIntervals;
@@ -4128,6 +4130,10 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
     } else {
       gen_->carve(int(N), int(PA), gen_cls ? n_cls_ : 0,
                   [&](int i, std::size_t cnt) { return take<double>(gbuf_[i], cnt); });
+      if (use_grt) {
+        rhist = take<int>(rint_hist_, 2 * std::size_t(rkeys) + 1);
+        rord = take<int>(rint_order_, Pa + 16 * std::size_t(rkeys));
+      }
       if (gen_cls) {
         crep = take<int>(cls_rep_, kMaxClasses);
         // class-pair counts and cursors, then the slot count; the pairs in
@@ -4323,6 +4329,20 @@ void Evaluator::compute_impl(const double *x, int flags, double *f_out, double *
         hipLaunchKernelGGL(k_cls_scan, dim3(1), dim3(64), 0, s, C * C, chist, ccur, GContext::kB0Pad, cslots);
         hipLaunchKernelGGL(k_cls_place, gsort, dim3(256), 0, s, nact, pa, z, G.cls_lut, C, ccur, cord);
       }
+    }
+    if (use_grt) {
+      // the blocks after 0 on their radial tables: the active pairs in bucket order
+      const int slots_max = PA + 16 * rkeys;
+      const RadialDomain &dom = gen_->rbl_domain();
+      const dim3 gpair(unsigned(std::max(1, ceil_div(PA, 256))));
+      hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(rkeys, 256))), dim3(256), 0, s, rhist, rkeys, 0);
+      hipLaunchKernelGGL(k_fill_int, dim3(unsigned(ceil_div(slots_max, 256))), dim3(256), 0, s, rord, slots_max, -1);
+      hipLaunchKernelGGL(k_rint_count, gpair, dim3(256), 0, s, nact, pa, pr, dom, rhist);
+      hipLaunchKernelGGL(k_rint_scan, dim3(1), dim3(1024), 0, s, rkeys, rhist, rhist + rkeys, rhist + 2 * rkeys);
+      hipLaunchKernelGGL(k_rint_place, gpair, dim3(256), 0, s, nact, pa, pr, dom, rhist + rkeys, rord);
+      G.rint_order = rord;
+      G.rint_slots = rhist + 2 * rkeys;
+      G.rint_max = slots_max;
     }
     gen_->forward(G);
     hipLaunchKernelGGL(k_image_center, dim3(unsigned(n_images_)), dim3(1024), 0, s, img_off, img_q, qraw, q, 0);

@@ -1741,6 +1741,110 @@ void launch_b0(hipStream_t s, int F, int R, std::size_t slots, const B0Args &A) 
   throw std::logic_error("SO3LR: block 0's table kernels at widths other than F = 128, 256 and R = 32, 64");
 }
 
+// The forward filters of the blocks after 0 on their radial tables (the
+// algebra of evaluator.hip's k_radial_fwd_rows at generic widths): the pairs
+// in bucket order (16 slots of one bucket, spatial block and interval, per
+// wavefront), per filter the spherical hidden tiles silu(E0 s + e0), then
+// per output tile the interval's coefficient tile (two K chunks against the
+// pairs' powers of t, in place of the W0 and W1 chains), the E1 chunks and
+// the endpoint rows; the rows go to pf and the logits to palpha as in
+// g_filt_fwd.
+struct GRadArgs {
+  const int *slots, *order, *pa;
+  const double *pr, *ps, *qkv, *rtab;
+  RadialDomain d;
+  const double *eb0a[2], *e0p[2], *wcp[2];
+  const double *exp2_256;
+  double inv_avg;
+  double *pf, *palpha;
+};
+
+template <int FT>
+__global__ __launch_bounds__(256) void g_radial_fwd_rows(GRadArgs A) {
+  constexpr int FHT = FT / 4, NH = FT / 2, HT = FT + FHT, F = 16 * FT, NE = 6 + FHT;
+  __shared__ double tab[256];
+  tab[threadIdx.x] = A.exp2_256[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int blk = g_xcd_block((*A.slots + 63) / 64);
+  const int wave = blk < 0 ? -1 : blk * 4 + int(threadIdx.x >> 6);
+  int p, ri;
+  bool inside;
+  v4d tp[2];
+  if (!rint_slots(A.slots, A.order, A.pr, A.d, wave, j, g, p, ri, inside, tp)) return;
+  const bool valid = p >= 0;
+  const int pp = valid ? p : A.order[wave * 16];
+  const int a = A.pa[2 * pp], b = A.pa[2 * pp + 1];
+  const double *ra = A.qkv + std::size_t(a) * 5 * F + 4 * g, *rr = A.qkv + std::size_t(b) * 5 * F + 4 * g;
+  double *frow = A.pf + std::size_t(pp) * 2 * F + 4 * g;
+  double *al = A.palpha + std::size_t(pp) * 4 * NH;
+  v4d sv;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) sv[v] = g + 4 * v < NH ? A.ps[std::size_t(pp) * NH + g + 4 * v] : 0.0;
+  const v4d zero = v4d{0.0, 0.0, 0.0, 0.0};
+  static_for<2>([&](auto wi) {
+    constexpr int w = decltype(wi)::value;
+    v4d he[FHT];
+#pragma unroll
+    for (int t = 0; t < FHT; ++t) {
+      const v4d e0 = frag_load(A.e0p[w], t, lane);
+      he[t] = mfma(e0[0], sv[0], frag_load(A.eb0a[w], t, lane));
+      if constexpr (NH > 4) he[t] = mfma(e0[1], sv[1], he[t]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) he[t][r] = silu_tab_wide(he[t][r], tab);
+    }
+    const double *coef = A.rtab + (std::size_t(ri) * 2 + w) * FT * 2 * 256;
+    constexpr int qo = w ? 3 * F : 0, ko = w ? 4 * F : F;  // q, k or q_ev, k_ev
+    auto ld = [&](auto si) -> v4d {
+      constexpr int S = decltype(si)::value, mt = S / NE, u = S % NE;
+      if constexpr (u < 2) return frag_load(coef, mt * 2 + u, lane);
+      else if constexpr (u < 2 + FHT) return frag_load(A.wcp[w], mt * HT + FT + u - 2, lane);
+      else if constexpr (u == 2 + FHT) return *reinterpret_cast<const v4d *>(ra + qo + 16 * mt);
+      else if constexpr (u == 3 + FHT) return *reinterpret_cast<const v4d *>(rr + ko + 16 * mt);
+      else if constexpr (u == 4 + FHT) return *reinterpret_cast<const v4d *>(rr + qo + 16 * mt);
+      else return *reinterpret_cast<const v4d *>(ra + ko + 16 * mt);
+    };
+    Stream<FT * NE, 6, decltype(ld)> st(ld);
+    st.prime();
+    v4d o, qv, qk0, qk1;
+    double t0 = 0.0, t1 = 0.0;
+    st.run([&](auto si, const v4d &wv) {
+      constexpr int S = decltype(si)::value, mt = S / NE, u = S % NE;
+      if constexpr (u == 0) {
+        o = mfma4(wv, tp[0], zero);
+      } else if constexpr (u == 1) {
+        o = mfma4(wv, tp[1], o);
+      } else if constexpr (u < 2 + FHT) {
+        o = mfma4(wv, he[u - 2], o);
+      } else if constexpr (u == 2 + FHT || u == 4 + FHT) {
+        qv = wv;
+      } else if constexpr (u == 3 + FHT) {
+        qk0 = qv * wv;  // q_a k_b: edge b -> a
+      } else {
+        qk1 = qv * wv;  // q_b k_a: edge a -> b
+        if (valid) *reinterpret_cast<v4d *>(frow + w * F + 16 * mt) = o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          t0 += qk0[r] * o[r];
+          t1 += qk1[r] * o[r];
+        }
+        if constexpr (mt & 1) {  // head mt / 2 complete: sum over the lane groups
+          t0 += __shfl_xor(t0, 16, 64);
+          t0 += __shfl_xor(t0, 32, 64);
+          t1 += __shfl_xor(t1, 16, 64);
+          t1 += __shfl_xor(t1, 32, 64);
+          if (valid && g == 0) {
+            al[w * NH + (mt >> 1)] = t0 * A.inv_avg;
+            al[2 * NH + w * NH + (mt >> 1)] = t1 * A.inv_avg;
+          }
+          t0 = 0.0;
+          t1 = 0.0;
+        }
+      }
+    });
+  });
+}
+
 // g_radial_fwd / g_radial_bwd at NH = 4 or 8 heads over cap pairs
 template <bool FWD>
 void launch_radial(hipStream_t s, int NH, const GContext &c, const double *tab, RadialDomain d, double *palpha,
@@ -2044,6 +2148,54 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
       radial_ok_ = true;
     }
   }
+  // the blocks after 0: each filter's radial branch W1 h(r) + b1 + e1 as
+  // piecewise polynomials (32 intervals of degree 31, the same bound), per
+  // interval and filter an F x 32 coefficient tile with the output rows
+  // permuted within each tile as wcp's (g_filt_fwd's channel order)
+  if (fit_radial && layers_ > 1) {
+    const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
+    bool ok = true;
+    std::vector<std::vector<double>> rows(static_cast<std::size_t>(layers_));
+    RadialDomain dom{};
+    for (int b = 1; b < layers_ && ok; ++b) {
+      std::vector<RadialFit> fits;
+      for (int k = 0; k < 2 && ok; ++k) {
+        const std::string f = "model.euclidean_transformers." + std::to_string(b) + "." +
+                              (k ? "filter_net_ev." : "filter_net_inv.");
+        const auto w1 = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.weight", {F, F});
+        auto bc = m.f64(f + "mlp_rbf.mlp_rbf_layer_1.0.bias", {F});
+        const auto eb1 = m.f64(f + "mlp_ev.mlp_ev_layer_1.0.bias", {F});
+        for (std::size_t c = 0; c < F; ++c) bc[c] += eb1[c];
+        try {
+          fits.push_back(fit_radial_hidden(m.f64(f + "mlp_rbf.0.weight", {F, R}), m.f64(f + "mlp_rbf.0.bias", {F}),
+                                           int(F), int(R), bb, a.gamma, a.sr_cutoff, kBlockIntervals, kBlockDegree,
+                                           &w1, &bc, int(F)));
+          ok = fits.back().value_error <= 1e-14 && fits.back().slope_error <= 1e-13;
+        } catch (const std::invalid_argument &) {
+          ok = false;
+        }
+      }
+      if (!ok) break;
+      const std::size_t n = kBlockPowers;
+      for (int i = 0; i < kBlockIntervals; ++i)
+        for (int k = 0; k < 2; ++k) {
+          const RadialFit &ft = fits[std::size_t(k)];
+          std::vector<double> cv(F * n);
+          for (std::size_t o = 0; o < F; ++o) {
+            const std::size_t src = 16 * (o / 16) + 4 * (o % 4) + (o % 16) / 4;
+            for (std::size_t kk = 0; kk < n; ++kk) cv[o * n + kk] = ft.value[(std::size_t(i) * n + kk) * F + src];
+          }
+          const auto pr = permute_mfma(cv, F, n);
+          rows[std::size_t(b)].insert(rows[std::size_t(b)].end(), pr.begin(), pr.end());
+        }
+      dom = RadialDomain{fits[0].r0, fits[0].step, fits[0].scale, fits[0].intervals};
+    }
+    if (ok) {
+      for (int b = 1; b < layers_; ++b) bw_[b].rrow = up(rows[std::size_t(b)]);
+      rbl_dom_ = dom;
+      radial_blocks_ok_ = true;
+    }
+  }
 }
 
 void GenericPath::carve(int N, int cap, int C, const std::function<double *(int, std::size_t)> &take) {
@@ -2126,6 +2278,16 @@ void GenericPath::forward(const GContext &c) {
     // pair invariants and both filters (kokkos_integrated_block0.cpp:166-255)
     hipLaunchKernelGGL(g_pair_inv, dim3(blocks_for(P * NH, 256)), dim3(256), 0, s, d, c.nact, cap, c.pa, evb,
                        B.att_cg, psb);
+    if (b > 0 && c.rint_order) {
+      // the radial tables, in bucket order
+      GRadArgs R{c.rint_slots, c.rint_order, c.pa, c.pr, psb, qb, B.rrow, rbl_dom_, {B.eb0a[0], B.eb0a[1]},
+                 {B.e0p[0], B.e0p[1]}, {B.wcp[0], B.wcp[1]}, hw_.exp2_256, c.inv_avg, pfb, pab};
+      const dim3 grid(blocks_for(std::size_t(std::max(c.rint_max, 1)), 64));
+      section(c, "generic_filter_fwd_radial", [&] {
+        if (F == 128) hipLaunchKernelGGL(g_radial_fwd_rows<8>, grid, dim3(256), 0, s, R);
+        else hipLaunchKernelGGL(g_radial_fwd_rows<16>, grid, dim3(256), 0, s, R);
+      });
+    } else {
     // both filters' rows f = [W1 | E1] [silu(W0 rbf + b0) | silu(E0 s + e0)]
     // + b1 + e1 and the attention logits from them, fused
     section(c, "generic_filter_fwd", [&] {
@@ -2133,6 +2295,7 @@ void GenericPath::forward(const GContext &c) {
       A.palpha = pab;
       launch_filt<true>(s, F, R, P, A);
     });
+    }
     }
     hipLaunchKernelGGL(g_attn_msg, dim3(g4x), dim3(256), 0, s, d, N, c.inc_off, c.iact, c.iother, xb, evb, qb, c.pY,
                        c.pfc, pab, B.ln1w, B.ln1b, c.ln_eps, c.norm1, n1b, n1hb, n1ib, b_[ACT], aevb);

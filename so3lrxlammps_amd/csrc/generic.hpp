@@ -56,6 +56,10 @@ struct GBlock {
   // transposes; b0, e0, b1 + e1
   const double *w0p[2], *e0p[2], *wcp[2], *w0tp[2], *e0tp[2], *wctp[2];
   const double *b0a[2], *eb0a[2], *bca[2];
+  // blocks after 0 on their radial tables: per interval and filter the radial
+  // branch W1 silu(W0 rbf + b0) + b1 + e1 as F x 32 powers of t (rows
+  // permuted within each tile as wcp's), MFMA A operands; null without them
+  const double *rrow;
   const double *att_cg, *int_cg;                  // (E)
   const double *ln1w, *ln1b, *ln2w, *ln2b;        // (F); RMSNorm and none: 1 and 0
   const double *m1, *m1b, *m2, *m2b;              // (F, F) (F)
@@ -117,6 +121,11 @@ struct GContext {
   // this evaluation when rad_build; null: the element-pair MFMA kernels
   double *rad_tab = nullptr;
   bool rad_build = false;
+  // the blocks after 0 on their radial tables: the active pairs in buckets
+  // of (spatial block, interval), padded with -1 to multiples of 16 slots;
+  // the slots end at *rint_slots (device); null: the full forward filters
+  const int *rint_order = nullptr, *rint_slots = nullptr;
+  int rint_max = 0;  // slots at most
 };
 
 class GenericPath {
@@ -128,6 +137,9 @@ class GenericPath {
   // block 0's radial tables: whether the fits hold, and the doubles of one
   // table record (element pair and interval: kRadialCoefs x 4 NH logits)
   bool radial_ok() const { return radial_ok_; }
+  // the blocks after 0's radial tables: whether every fit holds, their domain
+  bool radial_blocks_ok() const { return radial_blocks_ok_; }
+  const RadialDomain &rbl_domain() const { return rbl_dom_; }
   std::size_t radial_record() const { return std::size_t(kRadialCoefs) * 4 * d_.NH; }
   const GDims &dims() const { return d_; }
   int F() const { return d_.F; }
@@ -149,8 +161,8 @@ class GenericPath {
   GHeads hw_{};
   double *b_[kBuffers] = {};
   // block 0's radial fits, [filter][interval][power][feature] (radial_table.hpp)
-  bool radial_ok_ = false;
-  RadialDomain rad_dom_{};
+  bool radial_ok_ = false, radial_blocks_ok_ = false;
+  RadialDomain rad_dom_{}, rbl_dom_{};
   const double *rad_val_ = nullptr, *rad_slope_ = nullptr;
 };
 

@@ -2,7 +2,10 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
+#include <cstring>
 #include <functional>
+#include <mutex>
 #include <stdexcept>
 #include <thread>
 
@@ -66,10 +69,64 @@ void hidden_at(const Net &n, LD r, LD *h, LD *dh, std::vector<LD> &bas, std::vec
 
 }  // namespace
 
+namespace {
+
+// Fits already made in this process, by the exact bytes of their inputs
+// (contexts of one model fit the same layers again): at most kCacheSize.
+struct CacheEntry {
+  std::vector<double> key;
+  RadialFit fit;
+};
+constexpr std::size_t kCacheSize = 16;
+std::mutex cache_mutex;
+std::vector<CacheEntry> cache;
+
+std::vector<double> cache_key(const std::vector<double> &w0, const std::vector<double> &b0, int width, int nbasis,
+                              const std::vector<double> &basis_b, double gamma, double r_cut, int intervals,
+                              int degree, const std::vector<double> *w1, const std::vector<double> *bias,
+                              int outputs) {
+  std::vector<double> k{double(width), double(nbasis), gamma, r_cut, double(intervals), double(degree),
+                        double(outputs), w1 ? 1.0 : 0.0};
+  for (const std::vector<double> *v : {&w0, &b0, &basis_b}) k.insert(k.end(), v->begin(), v->end());
+  if (w1) {
+    k.insert(k.end(), w1->begin(), w1->end());
+    k.insert(k.end(), bias->begin(), bias->end());
+  }
+  return k;
+}
+
+bool same_bytes(const std::vector<double> &a, const std::vector<double> &b) {
+  return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * sizeof(double)) == 0;
+}
+
+RadialFit fit_uncached(const std::vector<double> &w0, const std::vector<double> &b0, int width, int nbasis,
+                       const std::vector<double> &basis_b, double gamma, double r_cut, int intervals, int degree,
+                       const std::vector<double> *w1, const std::vector<double> *bias, int outputs);
+
+}  // namespace
+
 RadialFit fit_radial_hidden(const std::vector<double> &w0, const std::vector<double> &b0, int width, int nbasis,
                             const std::vector<double> &basis_b, double gamma, double r_cut, int intervals,
                             int degree, const std::vector<double> *w1, const std::vector<double> *bias,
                             int outputs) {
+  std::vector<double> key = cache_key(w0, b0, width, nbasis, basis_b, gamma, r_cut, intervals, degree, w1, bias, outputs);
+  {
+    std::lock_guard<std::mutex> lock(cache_mutex);
+    for (const CacheEntry &e : cache)
+      if (same_bytes(e.key, key)) return e.fit;
+  }
+  RadialFit fit = fit_uncached(w0, b0, width, nbasis, basis_b, gamma, r_cut, intervals, degree, w1, bias, outputs);
+  std::lock_guard<std::mutex> lock(cache_mutex);
+  if (cache.size() >= kCacheSize) cache.erase(cache.begin());
+  cache.push_back(CacheEntry{std::move(key), fit});
+  return fit;
+}
+
+namespace {
+
+RadialFit fit_uncached(const std::vector<double> &w0, const std::vector<double> &b0, int width, int nbasis,
+                       const std::vector<double> &basis_b, double gamma, double r_cut, int intervals, int degree,
+                       const std::vector<double> *w1, const std::vector<double> *bias, int outputs) {
   if (width < 1 || nbasis < 2 || intervals < 1 || degree < 1 || gamma <= 0.0 || r_cut <= 0.0 ||
       w0.size() != std::size_t(width) * nbasis || b0.size() != std::size_t(width) ||
       basis_b.size() != std::size_t(nbasis) || (w1 != nullptr) != (bias != nullptr) ||
@@ -175,5 +232,7 @@ RadialFit fit_radial_hidden(const std::vector<double> &w0, const std::vector<dou
   fit.slope_error = double(err_d / std::max(max_d, LD(1e-300)));
   return fit;
 }
+
+}  // namespace
 
 }  // namespace so3lr_amd
