@@ -148,6 +148,11 @@ def kernel_work(widths, elements=0):
     # invariants are read back), r and the endpoints read
     rt_bytes = 8 * (2 * F + 4 * NH + NH) + 16
     work["generic_filter_fwd_radial"] = ("g_radial_fwd_rows", "hbm", rt_bytes, rt_bytes, "pair")
+    # and the reverse: df against the slope polynomials (14 powers per
+    # channel at the accuracy of degree 13; 32 issued), E1^T, E0^T
+    rt_bwd = 2 * 2 * (14 * F + FH * F + NH * FH)
+    work["generic_filter_bwd_radial"] = ("g_radial_bwd_rows", "mfma", rt_bwd, 2 * 2 * (32 * F + FH * F + NH * FH),
+                                         "pair")
     if elements:
         tab = 2 * 2 * (R * F + 2 * NH * F)
         work["generic_filter_fwd_block0_tables"] = ("g_b0_fwd: block 0's fused table filters", "mfma", tab,
@@ -560,7 +565,8 @@ def main():
                  "attn_fwd", "attn_bwd",
                  "attn_bwd_block0", "long_range", "generic_filter_fwd", "generic_filter_bwd",
                  "generic_attn_bwd_pairs", "generic_filter_fwd_block0_tables", "generic_filter_bwd_block0_tables",
-                 "generic_filter_fwd_block0_radial", "generic_filter_bwd_block0_radial", "generic_filter_fwd_radial"):
+                 "generic_filter_fwd_block0_radial", "generic_filter_bwd_block0_radial", "generic_filter_fwd_radial",
+                 "generic_filter_bwd_radial"):
         try:
             timing[name] = md.ctx.kernel_timing_read(name)
         except Exception:  # kernel not launched

@@ -1757,6 +1757,10 @@ struct GRadArgs {
   const double *exp2_256;
   double inv_avg;
   double *pf, *palpha;
+  // reverse (g_radial_bwd_rows): rtab holds the slope tiles
+  const double *e0tp[2], *wctp[2], *psc, *dfc;
+  double rc;
+  double *ds, *dr;
 };
 
 template <int FT>
@@ -1843,6 +1847,110 @@ __global__ __launch_bounds__(256) void g_radial_fwd_rows(GRadArgs A) {
       }
     });
   });
+}
+
+// The reverse filters of the blocks after 0 on their radial tables, in
+// bucket order: per filter and output tile mt, df from the logits' adjoints
+// and the endpoint rows as in g_filt_bwd, then the spherical hidden row's
+// adjoint (E1^T chunks) and the slope tiles against df, whose sum over the
+// powers of t is the radial branches' dE/dr; the spherical branch goes on
+// through silu' and E0^T to dE/ds.  No W1^T, no layer-0 recompute.
+template <int FT>
+__global__ __launch_bounds__(256) void g_radial_bwd_rows(GRadArgs A) {
+  constexpr int FHT = FT / 4, NH = FT / 2, F = 16 * FT, NE = 4 + FHT + 2;
+  __shared__ double tab[256];
+  tab[threadIdx.x] = A.exp2_256[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const int blk = g_xcd_block((*A.slots + 63) / 64);
+  const int wave = blk < 0 ? -1 : blk * 4 + int(threadIdx.x >> 6);
+  int p, ri;
+  bool inside;
+  v4d tp[2];
+  if (!rint_slots(A.slots, A.order, A.pr, A.d, wave, j, g, p, ri, inside, tp)) return;
+  const bool valid = p >= 0;
+  const int pp = valid ? p : A.order[wave * 16];
+  const int a = A.pa[2 * pp], b = A.pa[2 * pp + 1];
+  const double *ra = A.qkv + std::size_t(a) * 5 * F + 4 * g, *rr = A.qkv + std::size_t(b) * 5 * F + 4 * g;
+  const double *ps = A.psc + std::size_t(pp) * 4 * NH;
+  v4d sv;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) sv[v] = g + 4 * v < NH ? A.ps[std::size_t(pp) * NH + g + 4 * v] : 0.0;
+  const v4d zero = v4d{0.0, 0.0, 0.0, 0.0};
+  v4d dsa = zero, accdr[2] = {zero, zero};
+  static_for<2>([&](auto wi) {
+    constexpr int w = decltype(wi)::value;
+    constexpr int qo = w ? 3 * F : 0, ko = w ? 4 * F : F;
+    const double *slope = A.rtab + (std::size_t(ri) * 2 + w) * 2 * FT * 256;
+    v4d dh[FHT];
+#pragma unroll
+    for (int t = 0; t < FHT; ++t) dh[t] = zero;
+    auto ld = [&](auto si) -> v4d {
+      constexpr int S = decltype(si)::value, mt = S / NE, u = S % NE;
+      if constexpr (u < 4) {
+        const double *row = (u == 0 ? ra + qo : (u == 1 ? rr + ko : (u == 2 ? rr + qo : ra + ko))) + 16 * mt;
+        return *reinterpret_cast<const v4d *>(row);
+      } else if constexpr (u < 4 + FHT) {
+        return frag_load(A.wctp[w], (FT + u - 4) * FT + mt, lane);
+      } else {
+        return frag_load(slope, (u - 4 - FHT) * FT + mt, lane);
+      }
+    };
+    double c0 = ps[w * NH], c1 = ps[2 * NH + w * NH];  // head 0
+    v4d qv, df;
+    Stream<NE * FT, 6, decltype(ld)> st(ld);
+    st.prime();
+    st.run([&](auto si, const v4d &wv) {
+      constexpr int S = decltype(si)::value, mt = S / NE, u = S % NE;
+      if constexpr (u == 0 || u == 2) {
+        qv = wv;
+      } else if constexpr (u == 1) {
+        df = c0 * (qv * wv);
+      } else if constexpr (u == 3) {
+        df += c1 * (qv * wv);
+        const int hn = min(mt + 1, FT - 1) >> 1;  // the next tile's head
+        c0 = ps[w * NH + hn];
+        c1 = ps[2 * NH + w * NH + hn];
+      } else if constexpr (u < 4 + FHT) {
+        dh[u - 4] = mfma4(wv, df, dh[u - 4]);
+      } else {
+        accdr[u - 4 - FHT] = mfma4(wv, df, accdr[u - 4 - FHT]);
+      }
+    });
+    // the spherical branch: pre again, d hidden *= silu'(pre), E0^T
+#pragma unroll
+    for (int t = 0; t < FHT; ++t) {
+      const v4d e0 = frag_load(A.e0p[w], t, lane);
+      v4d pre = mfma(e0[0], sv[0], frag_load(A.eb0a[w], t, lane));
+      if constexpr (NH > 4) pre = mfma(e0[1], sv[1], pre);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dh[t][r] *= silu_prime_tab_wide(pre[r], tab);
+      dsa = mfma4(frag_load(A.e0tp[w], t, lane), dh[t], dsa);
+    }
+  });
+  if (valid) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (g + 4 * r < NH) A.ds[std::size_t(pp) * NH + g + 4 * r] = dsa[r];
+  }
+  // dE/dr: the radial branches' (powers 16 m + g + 4 r), plus the cutoff's
+  double part = 0.0;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part += accdr[m][r] * tp[m][r];
+  if (!inside) part = 0.0;
+  part += __shfl_xor(part, 16, 64);
+  part += __shfl_xor(part, 32, 64);
+  if (valid && g == 0) {
+    const double r = A.pr[pp];
+    double grad = part;
+    if (r < A.rc) {
+      const double t = r / A.rc;
+      grad += A.dfc[pp] * (-30.0 * t * t * (1.0 - t) * (1.0 - t) / A.rc);
+    }
+    A.dr[pp] += grad;
+  }
 }
 
 // g_radial_fwd / g_radial_bwd at NH = 4 or 8 heads over cap pairs
@@ -2155,7 +2263,7 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
   if (fit_radial && layers_ > 1) {
     const auto bb = m.f64("model.radial_embedding.radial_basis_fn.b", {R});
     bool ok = true;
-    std::vector<std::vector<double>> rows(static_cast<std::size_t>(layers_));
+    std::vector<std::vector<double>> rows(static_cast<std::size_t>(layers_)), drs(static_cast<std::size_t>(layers_));
     RadialDomain dom{};
     for (int b = 1; b < layers_ && ok; ++b) {
       std::vector<RadialFit> fits;
@@ -2187,11 +2295,20 @@ GenericPath::GenericPath(const Model &m, const std::function<const double *(cons
           }
           const auto pr = permute_mfma(cv, F, n);
           rows[std::size_t(b)].insert(rows[std::size_t(b)].end(), pr.begin(), pr.end());
+          // the slopes transposed, channels in natural order (the reverse's df)
+          std::vector<double> st(n * F);
+          for (std::size_t kk = 0; kk < n; ++kk)
+            for (std::size_t o = 0; o < F; ++o) st[kk * F + o] = ft.slope[(std::size_t(i) * n + kk) * F + o];
+          const auto pd = permute_mfma_kc(st, n, F);
+          drs[std::size_t(b)].insert(drs[std::size_t(b)].end(), pd.begin(), pd.end());
         }
       dom = RadialDomain{fits[0].r0, fits[0].step, fits[0].scale, fits[0].intervals};
     }
     if (ok) {
-      for (int b = 1; b < layers_; ++b) bw_[b].rrow = up(rows[std::size_t(b)]);
+      for (int b = 1; b < layers_; ++b) {
+        bw_[b].rrow = up(rows[std::size_t(b)]);
+        bw_[b].rdr = up(drs[std::size_t(b)]);
+      }
       rbl_dom_ = dom;
       radial_blocks_ok_ = true;
     }
@@ -2382,6 +2499,17 @@ void GenericPath::reverse(const GContext &c) {
       A.dr = c.dr;
       section(c, "generic_filter_bwd_block0_tables",
               [&] { launch_b0<false>(s, F, R, b0_slot_bound(c), A); });
+    } else if (b > 0 && c.rint_order) {
+      // the radial tables, in bucket order: df against the slope tiles to
+      // dE/dr, the spherical branch to dE/ds
+      GRadArgs Rg{c.rint_slots, c.rint_order, c.pa, c.pr, psb, qb, B.rdr, rbl_dom_, {B.eb0a[0], B.eb0a[1]},
+                  {B.e0p[0], B.e0p[1]}, {nullptr, nullptr}, hw_.exp2_256, c.inv_avg, nullptr, nullptr,
+                  {B.e0tp[0], B.e0tp[1]}, {B.wctp[0], B.wctp[1]}, b_[PSC], b_[DFC], c.rc, b_[DS], c.dr};
+      const dim3 grid(blocks_for(std::size_t(std::max(c.rint_max, 1)), 64));
+      section(c, "generic_filter_bwd_radial", [&] {
+        if (F == 128) hipLaunchKernelGGL(g_radial_bwd_rows<8>, grid, dim3(256), 0, s, Rg);
+        else hipLaunchKernelGGL(g_radial_bwd_rows<16>, grid, dim3(256), 0, s, Rg);
+      });
     } else {
       // both filters fused: d hidden = [W1 | E1]^T df (df from the logits'
       // adjoints psc), (.) silu'(pre), through W0^T and E0^T to dE/dr and

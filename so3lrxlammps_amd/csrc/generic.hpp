@@ -60,6 +60,8 @@ struct GBlock {
   // branch W1 silu(W0 rbf + b0) + b1 + e1 as F x 32 powers of t (rows
   // permuted within each tile as wcp's), MFMA A operands; null without them
   const double *rrow;
+  // and their slopes transposed, 32 powers x F (permute_mfma_kc, as wctp)
+  const double *rdr;
   const double *att_cg, *int_cg;                  // (E)
   const double *ln1w, *ln1b, *ln2w, *ln2b;        // (F); RMSNorm and none: 1 and 0
   const double *m1, *m1b, *m2, *m2b;              // (F, F) (F)
