@@ -2353,8 +2353,11 @@ void GenericPath::forward(const GContext &c) {
     hipLaunchKernelGGL(g_axpby, dim3(blocks_for(n * F, 256)), dim3(256), 0, s, n * F, (*c.resid)[0], xs,
                        (*c.x0l)[0], c.x0);
   hipLaunchKernelGGL(g_fill, dim3(blocks_for(n * E, 256)), dim3(256), 0, s, evs, n * E);
-  hipLaunchKernelGGL(g_rbf, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, c.gamma, hw_.rbf_b, hw_.rbf_k,
-                     hw_.rbf_kr, b_[RBF]);
+  // the basis rows, read by the full filter chains only: not when every
+  // block runs on its radial tables
+  if (!(c.rint_order && cls_on(c) && c.rad_tab))
+    hipLaunchKernelGGL(g_rbf, dim3(gP), dim3(256), 0, s, R, c.nact, cap, c.pr, c.gamma, hw_.rbf_b, hw_.rbf_k,
+                       hw_.rbf_kr, b_[RBF]);
   for (int b = 0; b < layers_; ++b) {
     const GBlock &B = bw_[b];
     double *xb = xs + b * n * F, *evb = evs + b * n * E;
