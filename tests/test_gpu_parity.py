@@ -483,11 +483,13 @@ def _launches(ctx, kernel):
 
 @pytest.mark.parametrize("name,q,m", [("water3000", 0, 1), ("alanine", 0, 1), ("acetate", -1, 1)])
 def test_block0_radial_tables_match_element_tables(monkeypatch, name, q, m):
-    """Block 0's logits from the radial tables (piecewise polynomials of r per
-    element pair, the default) against the element-pair MFMA kernels
-    (SO3LR_NO_RADIAL_TABLES=1).  The fits of the radial hidden layers hold to
-    about 1e-16 (values) and 4e-15 (slopes) of their largest magnitudes, so
-    the two agree to rounding; the kernel timings show which path ran."""
+    """Every block on its radial tables (the default): block 0's logits as
+    piecewise polynomials of r per element pair, the later blocks' radial
+    branches as fitted polynomials evaluated in bucket order; against the
+    element-pair MFMA kernels and the full filter chains
+    (SO3LR_NO_RADIAL_TABLES=1).  The fits hold to about 1e-16 (values) and
+    4e-15 (slopes) of their largest magnitudes, so the two agree to
+    rounding; the kernel timings show which path ran."""
     from so3lrxlammps_amd import Context, Lists
     ref, z, pos, box = support.load_golden(name)
     monkeypatch.setenv("SO3LR_SCALAR_FILTER_PAIRS", "0")
@@ -505,7 +507,8 @@ def test_block0_radial_tables_match_element_tables(monkeypatch, name, q, m):
         c.set_topology(lists)
         e, f, ea, w = c.compute(lists.rows_positions(pos))
         ran = {k: _launches(c, k) for k in ("filter_fwd_block0_radial", "filter_bwd_block0_radial",
-                                             "filter_fwd_block0_tables", "filter_bwd_block0_tables")}
+                                             "filter_fwd_block0_tables", "filter_bwd_block0_tables",
+                                             "filter_fwd_radial", "filter_bwd_radial", "filter_fwd", "filter_bwd")}
         results.append((e, f.copy(), ea.copy(), w.copy(), ran))
         c.close()
     (e1, f1, ea1, w1, ran1), (e2, f2, ea2, w2, ran2) = results
@@ -514,6 +517,9 @@ def test_block0_radial_tables_match_element_tables(monkeypatch, name, q, m):
     assert ran1["filter_fwd_block0_tables"] == 1 and ran1["filter_fwd_block0_radial"] == 0
     assert ran2["filter_fwd_block0_radial"] == 1 and ran2["filter_bwd_block0_radial"] == 1
     assert ran2["filter_fwd_block0_tables"] == 0 and ran2["filter_bwd_block0_tables"] == 0
+    # the blocks after 0: their radial tables (two blocks), or the full chains
+    assert ran2["filter_fwd_radial"] == 2 and ran2["filter_bwd_radial"] == 2 and ran2["filter_fwd"] == 0
+    assert ran1["filter_fwd"] == 2 and ran1["filter_bwd"] == 2 and ran1["filter_fwd_radial"] == 0
     assert abs(e1 - e2) <= 1e-13 * abs(e2)
     assert np.abs(f1 - f2).max() <= 1e-11
     assert np.abs(w1 - w2).max() <= 1e-11 * max(1.0, np.abs(w2).max())

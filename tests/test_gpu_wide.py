@@ -96,10 +96,10 @@ def test_wide_block0_element_tables_match_full_filters(monkeypatch, models, mode
 @pytest.mark.parametrize("model,name", [("lift", "water3000"), ("lift_perturbed", "alanine_cation"),
                                         ("f128_r64", "acetate"), ("deg1123", "water3000")])
 def test_wide_block0_radial_tables_match_element_tables(monkeypatch, models, model, name):
-    """Block 0's logits from the radial tables (the default) against the
-    element-pair MFMA kernels (SO3LR_NO_RADIAL_TABLES=1) on the generic
-    kernels, 8 and 4 heads: equal to rounding, and the kernel timings show
-    which path ran."""
+    """Every block on its radial tables (the default) against the
+    element-pair MFMA kernels and the full fused filter chains
+    (SO3LR_NO_RADIAL_TABLES=1) on the generic kernels, 8 and 4 heads: equal
+    to rounding, and the kernel timings show which path ran."""
     from so3lrxlammps_amd import Context, Lists
     from test_gpu_parity import _launches
     ref, z, pos, box = support.load_golden(name)
@@ -119,6 +119,7 @@ def test_wide_block0_radial_tables_match_element_tables(monkeypatch, models, mod
         e, f, ea, w = c.compute(lists.rows_positions(pos))
         ran = {k: _launches(c, "generic_filter_%s_block0_%s" % (k[0], k[1]))
                for k in (("fwd", "radial"), ("bwd", "radial"), ("fwd", "tables"), ("bwd", "tables"))}
+        ran.update({k: _launches(c, "generic_filter_" + k) for k in ("fwd_radial", "bwd_radial", "fwd", "bwd")})
         res.append((e, f.copy(), w.copy(), ran))
         c.close()
     (e1, f1, w1, ran1), (e2, f2, w2, ran2) = res
@@ -127,6 +128,14 @@ def test_wide_block0_radial_tables_match_element_tables(monkeypatch, models, mod
     assert ran1[("fwd", "tables")] == 1 and ran1[("fwd", "radial")] == 0
     assert ran2[("fwd", "radial")] == 1 and ran2[("bwd", "radial")] == 1
     assert ran2[("fwd", "tables")] == 0 and ran2[("bwd", "tables")] == 0
+    # the blocks after 0 (two): their radial tables where every fit holds its
+    # bound (the perturbed lift's need not: then the full fused chains), or
+    # the full chains
+    assert ran2["fwd_radial"] + ran2["fwd"] == 2 and ran2["bwd_radial"] + ran2["bwd"] == 2
+    assert ran2["fwd_radial"] in (0, 2) and ran2["fwd_radial"] == ran2["bwd_radial"]
+    if model != "lift_perturbed":
+        assert ran2["fwd_radial"] == 2
+    assert ran1["fwd"] == 2 and ran1["bwd"] == 2 and ran1["fwd_radial"] == 0
     assert abs(e1 - e2) <= 1e-12 * abs(e2)
     assert np.abs(f1 - f2).max() <= 1e-10 * max(1.0, np.abs(f2).max() / 10.0)
     assert np.abs(w1 - w2).max() <= 1e-10 * max(1.0, np.abs(w2).max())
